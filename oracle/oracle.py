@@ -1,0 +1,333 @@
+"""ctypes front of the CPU oracle (liboracle.so, built from oracle.c).
+
+TEST INFRASTRUCTURE ONLY: tests/, the smoke check in __graft_entry__.py and
+bench.py's CPU-baseline leg use it as the checker. The product package
+(webgllm_amd) never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def _load():
+    if not os.path.exists(_LIB_PATH):
+        build()
+    return C.CDLL(_LIB_PATH)
+
+
+_lib = _load()
+
+_P = C.c_void_p
+_I = C.c_int
+
+
+class _QM(C.Structure):
+    _fields_ = [("N", _I), ("K", _I), ("quants", _P), ("scales", _P), ("zeros", _P),
+                ("zero_halves", _P), ("raw", _P)]
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(_P)
+
+
+_lib.orc_to_half.restype = C.c_uint16
+_lib.orc_to_half.argtypes = [C.c_double]
+_lib.orc_from_half.restype = C.c_float
+_lib.orc_from_half.argtypes = [C.c_uint16]
+for name in ("orc_pack_q4_0", "orc_pack_q4_k"):
+    getattr(_lib, name).argtypes = [C.POINTER(_QM), _I, _P, C.c_size_t, _I, _P]
+_lib.orc_pack_nbits.argtypes = [C.POINTER(_QM), _I, _P, _P, _P, _I, _P]
+_lib.orc_pack_nbits_scales.argtypes = [C.POINTER(_QM), _I, _P, _P, _I]
+_lib.orc_quants_from_raw.argtypes = [_P, _I, _I, _P]
+_lib.orc_matrix_row.argtypes = [C.POINTER(_QM), _I, _P]
+_lib.orc_dequantize_q4_k.argtypes = [_P, _I, _I, _P]
+_lib.orc_dequantize_nbits_row.argtypes = [_I, _P, _P, _P, _I, _P]
+_lib.orc_quantize_q4_0.argtypes = [_P, _I, _I, _P]
+_lib.orc_quantize_nbits.argtypes = [_P, _I, _I, _P, _P, _P, _P]
+_lib.orc_gemv_f64.argtypes = [C.POINTER(_QM), _P, _I, _P, _I]
+_lib.orc_matmul_split.argtypes = [C.POINTER(_QM), _P, _I, _P, _I, _I, _I]
+_lib.orc_f32_to_h2.argtypes = [_P, C.c_size_t, _P]
+_lib.orc_rms_norm.argtypes = [_P, _P, _I, _I, C.c_float, _P]
+_lib.orc_swiglu.argtypes = [_P, _I, _I, _P]
+_lib.orc_rope_table.argtypes = [C.c_double, _I, _I, _I, _I, _P]
+_lib.orc_rope_rows.argtypes = [_I]
+_lib.orc_head_prep.argtypes = [_P, _P, _P, _I, _I, _I, C.c_float, C.c_float, _I, _P]
+_lib.orc_attention_f64.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _P]
+_lib.orc_short_conv.argtypes = [_P, _I, _I, _I, _P, _P, _P, _P, _P]
+_lib.orc_argmax.restype = _I
+_lib.orc_argmax.argtypes = [_P, _I, C.POINTER(C.c_float)]
+_lib.orc_now.restype = C.c_double
+
+
+def to_half(v: float) -> int:
+    return int(_lib.orc_to_half(float(v)))
+
+
+def from_half(h: int) -> float:
+    return float(_lib.orc_from_half(int(h) & 0xFFFF))
+
+
+def halves_to_f32(h: np.ndarray) -> np.ndarray:
+    """Half bits to float32 through the oracle's own table (half.ts:37-55)."""
+    table = np.array([_lib.orc_from_half(i) for i in range(65536)], dtype=np.float32) \
+        if not hasattr(halves_to_f32, "_t") else halves_to_f32._t
+    halves_to_f32._t = table
+    return table[np.asarray(h, dtype=np.uint16)]
+
+
+def f32_to_h2(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    _lib.orc_f32_to_h2(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+class QuantMatrix:
+    """src/weights.ts:153-178 as numpy arrays (4-bit only)."""
+
+    def __init__(self, N: int, K: int, zeros: bool | str = False):
+        if N % 4:
+            raise ValueError(f"matrix rows ({N}) must be a multiple of 4")
+        if K % 32:
+            raise ValueError(f"matrix columns ({K}) must be a multiple of 32")
+        self.N, self.K = N, K
+        blocks = K // 32
+        self.quants = np.zeros(N * blocks * 4, dtype=np.uint32)
+        self.scales = np.zeros(N * blocks, dtype=np.uint16)
+        self.zeros = np.full(N * blocks, 8, dtype=np.uint8) if zeros is True else None
+        self.zero_halves = np.zeros(N * blocks, dtype=np.uint16) if zeros == "halves" else None
+        self.raw = None
+
+    def _c(self):
+        return _QM(self.N, self.K, _ptr(self.quants), _ptr(self.scales), _ptr(self.zeros),
+                   _ptr(self.zero_halves), _ptr(self.raw))
+
+    def row(self, n: int) -> np.ndarray:
+        out = np.empty(self.K, dtype=np.float32)
+        _lib.orc_matrix_row(C.byref(self._c()), n, _ptr(out))
+        return out
+
+    def dense(self) -> np.ndarray:
+        return np.stack([self.row(n) for n in range(self.N)])
+
+
+def _rows(src_rows):
+    return None if src_rows is None else np.ascontiguousarray(src_rows, dtype=np.int32)
+
+
+def pack_q4_0(m: QuantMatrix, row0: int, src: np.ndarray, rows: int, src_rows=None) -> None:
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    sr = _rows(src_rows)
+    rc = _lib.orc_pack_q4_0(C.byref(m._c()), row0, _ptr(src), src.size, rows, _ptr(sr))
+    if rc:
+        raise ValueError(f"packQ4_0 failed ({rc})")
+
+
+def pack_q4_k(m: QuantMatrix, row0: int, src: np.ndarray, rows: int, src_rows=None) -> None:
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    sr = _rows(src_rows)
+    rc = _lib.orc_pack_q4_k(C.byref(m._c()), row0, _ptr(src), src.size, rows, _ptr(sr))
+    if rc == -3:
+        raise ValueError("Q4_K rows go into a matrix with fractional zero points")
+    if rc:
+        raise ValueError(f"packQ4_K failed ({rc})")
+
+
+def pack_nbits(m: QuantMatrix, row0: int, quant, scale_bytes, zp, rows: int, src_rows=None):
+    quant = np.ascontiguousarray(quant, dtype=np.uint8)
+    scale_bytes = np.ascontiguousarray(scale_bytes).view(np.uint8)
+    zp = None if zp is None else np.ascontiguousarray(zp, dtype=np.uint8)
+    sr = _rows(src_rows)
+    rc = _lib.orc_pack_nbits(C.byref(m._c()), row0, _ptr(quant), _ptr(scale_bytes), _ptr(zp),
+                             rows, _ptr(sr))
+    if rc:
+        raise ValueError(f"packMatMulNBits failed ({rc})")
+
+
+def pack_nbits_scales(m: QuantMatrix, row0: int, scale_bytes, zp, rows: int):
+    scale_bytes = np.ascontiguousarray(scale_bytes).view(np.uint8)
+    zp = None if zp is None else np.ascontiguousarray(zp, dtype=np.uint8)
+    rc = _lib.orc_pack_nbits_scales(C.byref(m._c()), row0, _ptr(scale_bytes), _ptr(zp), rows)
+    if rc:
+        raise ValueError(f"packMatMulNBitsScales failed ({rc})")
+
+
+def quants_from_raw(raw: np.ndarray, N: int, K: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.zeros(N * K // 32 * 4, dtype=np.uint32)
+    _lib.orc_quants_from_raw(_ptr(raw), N, K, _ptr(out))
+    return out
+
+
+def dequantize_q4_k(src: np.ndarray, rows: int, K: int) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    out = np.empty(rows * K, dtype=np.float32)
+    _lib.orc_dequantize_q4_k(_ptr(src), rows, K, _ptr(out))
+    return out.reshape(rows, K)
+
+
+def dequantize_nbits_row(K, quant, scale_bytes, zp, n) -> np.ndarray:
+    quant = np.ascontiguousarray(quant, dtype=np.uint8)
+    scale_bytes = np.ascontiguousarray(scale_bytes).view(np.uint8)
+    zp = None if zp is None else np.ascontiguousarray(zp, dtype=np.uint8)
+    out = np.empty(K, dtype=np.float32)
+    _lib.orc_dequantize_nbits_row(K, _ptr(quant), _ptr(scale_bytes), _ptr(zp), n, _ptr(out))
+    return out
+
+
+def quantize_q4_0(w: np.ndarray) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, K = w.shape
+    out = np.empty(rows * K // 32 * 18, dtype=np.uint8)
+    _lib.orc_quantize_q4_0(_ptr(w), rows, K, _ptr(out))
+    return out
+
+
+def quantize_nbits(w: np.ndarray, zp_blocks: np.ndarray):
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, K = w.shape
+    blocks = K // 32
+    zpb = np.ascontiguousarray(zp_blocks, dtype=np.uint8)
+    quant = np.empty(rows * blocks * 16, dtype=np.uint8)
+    scales = np.empty(rows * blocks, dtype=np.uint16)
+    zp = np.empty(rows * ((blocks + 1) // 2), dtype=np.uint8)
+    _lib.orc_quantize_nbits(_ptr(w), rows, K, _ptr(zpb), _ptr(quant), _ptr(scales), _ptr(zp))
+    return quant, scales, zp
+
+
+def gemv_f64(m: QuantMatrix, x: np.ndarray, threads: int = 0) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, m.K)
+    y = np.empty((x.shape[0], m.N), dtype=np.float64)
+    _lib.orc_gemv_f64(C.byref(m._c()), _ptr(x), x.shape[0], _ptr(y), threads)
+    return y
+
+
+def matmul_split(m: QuantMatrix, x16: np.ndarray, threads: int = 0, split_fragments: int = 4096,
+                 max_split: int = 16) -> np.ndarray:
+    x16 = np.ascontiguousarray(x16, dtype=np.uint16).reshape(-1, m.K)
+    y = np.empty((x16.shape[0], m.N), dtype=np.float32)
+    _lib.orc_matmul_split(C.byref(m._c()), _ptr(x16), x16.shape[0], _ptr(y), threads,
+                          split_fragments, max_split)
+    return y
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    M, D = x.reshape(-1, x.shape[-1]).shape
+    out = np.empty_like(x)
+    _lib.orc_rms_norm(_ptr(x), _ptr(w), M, D, eps, _ptr(out))
+    return out
+
+
+def swiglu(gu: np.ndarray) -> np.ndarray:
+    gu = np.ascontiguousarray(gu, dtype=np.float32)
+    M, F2 = gu.reshape(-1, gu.shape[-1]).shape
+    out = np.empty((M, F2 // 2), dtype=np.float32)
+    _lib.orc_swiglu(_ptr(gu), M, F2 // 2, _ptr(out))
+    return out
+
+
+def rope_table(theta: float, head_dim: int, rotated_dims: int, context: int,
+               freq_dims: int | None = None) -> np.ndarray:
+    rows = _lib.orc_rope_rows(context)
+    t = np.empty((rows, head_dim), dtype=np.float32)
+    _lib.orc_rope_table(theta, head_dim, rotated_dims, freq_dims or head_dim, context, _ptr(t))
+    return t
+
+
+def head_prep(x, norm_w, rope, head_dim, rotated_dims, pos, eps, scale, use_norm) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nw = np.ascontiguousarray(norm_w if norm_w is not None else np.ones(head_dim), dtype=np.float32)
+    rope = np.ascontiguousarray(rope, dtype=np.float32)
+    out = np.empty(head_dim, dtype=np.float32)
+    _lib.orc_head_prep(_ptr(x), _ptr(nw), _ptr(rope), head_dim, rotated_dims, pos, eps, scale,
+                       int(use_norm), _ptr(out))
+    return out
+
+
+def attention_f64(q, kc, vc, heads, kv_heads, head_dim, keys, kv_stride) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    kc = np.ascontiguousarray(kc, dtype=np.uint16)
+    vc = np.ascontiguousarray(vc, dtype=np.uint16)
+    out = np.empty(heads * head_dim, dtype=np.float64)
+    _lib.orc_attention_f64(_ptr(q), _ptr(kc), _ptr(vc), heads, kv_heads, head_dim, keys,
+                           kv_stride, _ptr(out))
+    return out
+
+
+def short_conv(bcx, D, W, taps, state, prefixes=False):
+    bcx = np.ascontiguousarray(bcx, dtype=np.float32).reshape(-1, 3 * D)
+    M = bcx.shape[0]
+    taps = np.ascontiguousarray(taps, dtype=np.float32)
+    state = np.ascontiguousarray(state, dtype=np.float32)
+    out = np.empty((M, D), dtype=np.float32)
+    new_state = np.empty((W - 1, D), dtype=np.float32)
+    pre = np.empty((M, W - 1, D), dtype=np.float32) if prefixes else None
+    _lib.orc_short_conv(_ptr(bcx), M, D, W, _ptr(taps), _ptr(state), _ptr(out), _ptr(new_state),
+                        _ptr(pre))
+    return (out, new_state, pre) if prefixes else (out, new_state)
+
+
+def argmax(logits: np.ndarray):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    top = C.c_float()
+    at = _lib.orc_argmax(_ptr(logits), logits.size, C.byref(top))
+    return at, top.value
+
+
+def now() -> float:
+    return _lib.orc_now()
+
+
+class Mulberry32:
+    """The reference tests' generator (src/q4k-pack.test.ts:6-16)."""
+
+    def __init__(self, seed: int):
+        self.a = seed & 0xFFFFFFFF
+
+    def __call__(self) -> float:
+        self.a = (self.a + 0x6D2B79F5) & 0xFFFFFFFF
+        t = self.a
+        t = _imul(t ^ (t >> 15), t | 1)
+        t ^= (t + _imul(t ^ (t >> 7), t | 61)) & 0xFFFFFFFF
+        return ((t ^ (t >> 14)) & 0xFFFFFFFF) / 4294967296.0
+
+
+def _imul(a: int, b: int) -> int:
+    return (a * b) & 0xFFFFFFFF
+
+
+def q4k_blocks(seed: int, supers: int, zero_scale: bool = False) -> np.ndarray:
+    """Q4_K super-blocks as src/q4k-pack.test.ts:19-36 makes them."""
+    rand = Mulberry32(seed)
+    b = np.zeros(supers * 144, dtype=np.uint8)
+    for s in range(supers):
+        p = s * 144
+        d = to_half(0.001 + 0.004 * rand())
+        dm = to_half(0.002 + 0.006 * rand())
+        b[p], b[p + 1] = d & 255, d >> 8
+        b[p + 2], b[p + 3] = dm & 255, dm >> 8
+        scales = [1 + int(rand() * 63) for _ in range(8)]
+        mins = [int(rand() * 64) for _ in range(8)]
+        if zero_scale:
+            scales[s % 8] = 0
+        for j in range(4):
+            b[p + 4 + j] = (scales[j] & 63) | ((scales[j + 4] >> 4) << 6)
+            b[p + 8 + j] = (mins[j] & 63) | ((mins[j + 4] >> 4) << 6)
+            b[p + 12 + j] = (scales[j + 4] & 15) | ((mins[j + 4] & 15) << 4)
+        for i in range(128):
+            b[p + 16 + i] = int(rand() * 256)
+    return b

@@ -1,0 +1,397 @@
+"""The oracle pinned against the reference's own known-answer tests and
+against closed forms (CPU only). Each test names the reference test or the
+mathematical fact it rests on."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+# --- src/half.test.ts -------------------------------------------------------
+
+def test_half_round_trips_exact_values():
+    # src/half.test.ts:6-10
+    for v in [0, 1, -1, 0.5, 2, 65504, -65504, 6.103515625e-5, 5.960464477539063e-8,
+              0.333251953125]:
+        assert O.from_half(O.to_half(v)) == v
+
+
+def test_half_rounds_to_nearest_even():
+    # src/half.test.ts:12-15
+    assert O.from_half(O.to_half(1 + 2 ** -11)) == 1
+    assert O.from_half(O.to_half(1 + 3 * 2 ** -12)) == 1 + 2 ** -10
+
+
+def test_half_overflow_nan_signed_zero():
+    # src/half.test.ts:17-22
+    assert O.from_half(O.to_half(1e6)) == math.inf
+    assert O.from_half(O.to_half(-1e6)) == -math.inf
+    assert math.isnan(O.from_half(O.to_half(math.nan)))
+    z = O.from_half(O.to_half(-0.0))
+    assert z == 0 and math.copysign(1, z) < 0
+
+
+def test_half_table_values():
+    # src/half.test.ts:24-31
+    want = {0: 0.0, 1: 2 ** -24, 0x3C00: 1.0, 0x7BFF: 65504.0, 0x8001: -(2 ** -24),
+            0xC000: -2.0, 0x7C00: math.inf, 0x0400: 2 ** -14}
+    for h, v in want.items():
+        assert O.from_half(h) == v
+    assert list(O.halves_to_f32(np.array([0x3C00, 0xC000, 0x3800]))) == [1, -2, 0.5]
+
+
+def test_half_matches_numpy_rne_on_float32_grid():
+    # toHalf stores the value as a float32 first, then rounds to nearest
+    # even: for float32 inputs that is IEEE float16 conversion (numpy's).
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(20000).astype(np.float32) * s
+                        for s in (1e-7, 1e-5, 1e-3, 1.0, 1e3, 6e4)])
+    got = np.array([O.to_half(float(v)) for v in x], dtype=np.uint16)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+# --- src/q4k-pack.test.ts ------------------------------------------------------
+
+def _worst(m, want, rows, K, src_rows=None):
+    err = scale = 0.0
+    for r in range(rows):
+        got = m.row(r)
+        frm = (src_rows[r] if src_rows is not None else r)
+        err = max(err, float(np.max(np.abs(got - want[frm]))))
+        scale = max(scale, float(np.max(np.abs(want[frm]))))
+    return err / scale
+
+
+def test_q4k_packed_rows_are_the_files_weights():
+    # src/q4k-pack.test.ts:55-68
+    rows, K = 8, 512
+    b = O.q4k_blocks(1, rows * K // 256)
+    want = O.dequantize_q4_k(b, rows, K)
+    m = O.QuantMatrix(rows, K, "halves")
+    O.pack_q4_k(m, 0, b, rows)
+    assert m.zeros is None and m.zero_halves is not None
+    assert _worst(m, want, rows, K) < 1e-3
+
+
+def test_q4k_rows_land_at_offset_in_order():
+    # src/q4k-pack.test.ts:70-82
+    rows, K = 4, 256
+    b = O.q4k_blocks(2, rows)
+    want = O.dequantize_q4_k(b, rows, K)
+    m = O.QuantMatrix(8, K, "halves")
+    order = [2, 0, 3, 1]
+    O.pack_q4_k(m, 4, b, rows, order)
+    for r in range(4):
+        assert np.all(m.row(r) == 0)
+    err = scale = 0.0
+    for r in range(4):
+        got = m.row(4 + r)
+        err = max(err, float(np.max(np.abs(got - want[order[r]]))))
+        scale = max(scale, float(np.max(np.abs(want[order[r]]))))
+    assert err / scale < 1e-3
+
+
+def test_q4k_zero_scale_subblock_keeps_constant():
+    # src/q4k-pack.test.ts:84-97
+    rows, K = 4, 256
+    b = O.q4k_blocks(3, rows, zero_scale=True)
+    want = O.dequantize_q4_k(b, rows, K)
+    for r in range(rows):
+        at = (r % 8) * 32
+        assert np.all(want[r, at:at + 32] == want[r, at])
+    m = O.QuantMatrix(rows, K, "halves")
+    O.pack_q4_k(m, 0, b, rows)
+    assert _worst(m, want, rows, K) < 1e-3
+    # The constant sub-block is q = 15 with z' = 0 (repack.ts:156-161).
+    for r in range(rows):
+        at = (r % 8) * 32
+        row = m.row(r)
+        assert np.all(row[at:at + 32] == row[at])
+
+
+def test_q4k_needs_fractional_zero_points():
+    # src/q4k-pack.test.ts:99-101
+    with pytest.raises(ValueError, match="fractional zero points"):
+        O.pack_q4_k(O.QuantMatrix(4, 256, True), 0, O.q4k_blocks(4, 4), 4)
+
+
+def test_q4k_scale_chain_by_hand():
+    # repack.ts:149-163 on one hand-built sub-block: d = 1/64, sc = 5,
+    # dmin = 1/128, m = 3 -> d' = 5/64 and z' = half(3/128 / (5/64)) = half(0.3).
+    b = np.zeros(144, dtype=np.uint8)
+    d, dm = O.to_half(1 / 64), O.to_half(1 / 128)
+    b[0], b[1], b[2], b[3] = d & 255, d >> 8, dm & 255, dm >> 8
+    b[4] = 5          # sub-block 0 scale
+    b[8] = 3          # sub-block 0 min
+    b[16:16 + 32] = 0x21  # low nibble 1 (sub-block 0), high nibble 2 (sub-block 1)
+    m = O.QuantMatrix(4, 256, "halves")
+    O.pack_q4_k(m, 0, np.tile(b, 4), 4)
+    assert m.scales[0] == O.to_half(5 / 64)
+    assert m.zero_halves[0] == O.to_half(0.3)
+    assert O.from_half(m.zero_halves[0]) == np.float16(0.3)
+    row = m.row(0)
+    assert row[0] == np.float32(np.float64(5 / 64) * (1 - float(np.float16(0.3))))
+    # sub-block 1 has scale 0 -> q = 15, d' = half(-0/15) = -0, z' = 0.
+    assert m.scales[4] == 0x8000 and m.zero_halves[4] == 0
+    assert np.all(row[32:64] == 0)
+
+
+# --- src/repack-words.test.ts -------------------------------------------------
+
+def test_q4_0_word_copies_offsets_and_permutations():
+    # src/repack-words.test.ts:5-29 (4-bit)
+    nbytes, stride = 16, 18
+    for offset in [0, 1, 2, 3]:
+        raw = np.array([(i * 71 + 19) & 255 for i in range(offset + 4 * 2 * stride)],
+                       dtype=np.uint8)
+        src = raw[offset:]
+        perm = [3, 0, 2, 1]
+        actual = O.QuantMatrix(12, 64, False)
+        want = O.QuantMatrix(12, 64, False)
+        target = want.quants.view(np.uint8)
+        for i in range(4):
+            for b in range(2):
+                at = ((((4 + i) >> 2) * 2 + b) * 4 + ((4 + i) & 3))
+                frm = (perm[i] * 2 + b) * stride
+                want.scales[at] = int(src[frm]) | (int(src[frm + 1]) << 8)
+                target[at * nbytes:(at + 1) * nbytes] = src[frm + 2:frm + stride]
+        O.pack_q4_0(actual, 4, src, 4, perm)
+        assert np.array_equal(actual.quants, want.quants)
+        assert np.array_equal(actual.scales, want.scales)
+
+
+# --- src/q4-repacker.test.ts --------------------------------------------------
+
+@pytest.mark.parametrize("N,K", [(4, 32), (12, 2048), (64, 7680), (8, 64)])
+def test_quants_from_raw_matches_byte_packer(N, K):
+    # src/q4-repacker.test.ts:5-13 pins the word repack to quantsFromRaw; here
+    # quantsFromRaw (words) and packMatMulNBits (bytes) pin each other.
+    i = np.arange(N * K // 2, dtype=np.uint64)
+    raw = (((i + 1) * 2654435761) & 0xFFFFFFFF) >> 24
+    raw = raw.astype(np.uint8)
+    words = O.quants_from_raw(raw, N, K)
+    m = O.QuantMatrix(N, K, True)
+    O.pack_nbits(m, 0, raw, np.zeros(N * K // 32, np.uint16), None, N)
+    assert np.array_equal(words, m.quants)
+
+
+def test_nbits_dequant_paths_agree():
+    # dequantizeNBitsRow (load-onnx.ts:471-501) and matrixRow over packed and
+    # raw rows (repack.ts:865-891) are three statements of one dequant.
+    rng = np.random.default_rng(5)
+    N, K = 8, 96
+    blocks = K // 32
+    quant = rng.integers(0, 256, N * blocks * 16, dtype=np.uint8)
+    scales = np.array([O.to_half(v) for v in rng.uniform(-0.1, 0.1, N * blocks)], np.uint16)
+    zp = rng.integers(0, 256, N * ((blocks + 1) // 2), dtype=np.uint8)
+    packed = O.QuantMatrix(N, K, True)
+    O.pack_nbits(packed, 0, quant, scales, zp, N)
+    raw = O.QuantMatrix(N, K, True)
+    raw.raw = quant
+    O.pack_nbits_scales(raw, 0, scales, zp, N)
+    for n in range(N):
+        want = O.dequantize_nbits_row(K, quant, scales, zp, n)
+        assert np.array_equal(packed.row(n), want)
+        assert np.array_equal(raw.row(n), want)
+    # Closed form: scale * (nibble - zero point), element 2i low nibble of byte i.
+    n, b = 3, 1
+    byte = quant[(n * blocks + b) * 16 + 2]
+    z = (zp[n * ((blocks + 1) // 2) + (b >> 1)] >> ((b & 1) * 4)) & 15
+    s = O.from_half(scales[n * blocks + b])
+    assert packed.row(n)[b * 32 + 4] == np.float32(s * ((byte & 15) - z))
+    assert packed.row(n)[b * 32 + 5] == np.float32(s * ((byte >> 4) - z))
+
+
+def test_gguf_q4_0_zero_block_is_zero():
+    # src/lfm2-gguf.test.ts:17: d = 1.0 (0x3C00), nibbles 0x88 -> weights 0.
+    blk = np.array([0x00, 0x3C] + [0x88] * 16, dtype=np.uint8)
+    m = O.QuantMatrix(4, 64, False)
+    O.pack_q4_0(m, 0, np.tile(blk, 8), 4)
+    assert np.all(m.dense() == 0)
+
+
+def test_q4_0_dequant_closed_form():
+    rng = np.random.default_rng(1)
+    N, K = 4, 64
+    src = rng.integers(0, 256, N * (K // 32) * 18, dtype=np.uint8)
+    for b in range(N * K // 32):
+        h = O.to_half(rng.uniform(-1, 1))
+        src[b * 18], src[b * 18 + 1] = h & 255, h >> 8
+    m = O.QuantMatrix(N, K, False)
+    O.pack_q4_0(m, 0, src, N)
+    for n in range(N):
+        for b in range(K // 32):
+            p = (n * (K // 32) + b) * 18
+            d = O.from_half(int(src[p]) | (int(src[p + 1]) << 8))
+            for j in range(16):
+                byte = int(src[p + 2 + j])
+                assert m.row(n)[b * 32 + j] == np.float32(d * ((byte & 15) - 8))
+                assert m.row(n)[b * 32 + 16 + j] == np.float32(d * ((byte >> 4) - 8))
+
+
+def test_quantize_q4_0_roundtrip_error_bounded():
+    # ggml's Q4_0 maps the largest-magnitude weight m to q = 0 (d = m / -8):
+    # in-range weights round to within |d| / 2, and weights near -m (q = 16)
+    # clamp to 15, so |w - deq(w)| <= |d| = |m| / 8 (plus d's half rounding).
+    rng = np.random.default_rng(2)
+    w = (rng.standard_normal((8, 256)) * 0.02).astype(np.float32)
+    m = O.QuantMatrix(8, 256, False)
+    O.pack_q4_0(m, 0, O.quantize_q4_0(w), 8)
+    deq = m.dense()
+    amax = np.abs(w.reshape(8, -1, 32)).max(-1)
+    err = np.abs(deq - w).reshape(8, -1, 32).max(-1)
+    assert np.all(err <= amax / 8 * 1.001 + 1e-7)
+    assert np.mean(np.abs(deq - w)) < np.mean(amax) / 16
+
+
+# --- matmul -------------------------------------------------------------------
+
+def _random_q4_0(rng, N, K):
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    m = O.QuantMatrix(N, K, False)
+    O.pack_q4_0(m, 0, O.quantize_q4_0(w), N)
+    return m
+
+
+def test_gemv_f64_matches_dense_product():
+    rng = np.random.default_rng(3)
+    m = _random_q4_0(rng, 32, 256)
+    x = rng.standard_normal((3, 256)).astype(np.float32)
+    want = x.astype(np.float64) @ m.dense().astype(np.float64).T
+    assert np.allclose(O.gemv_f64(m, x), want, rtol=1e-12, atol=1e-12)
+
+
+def test_gemv_special_cases():
+    rng = np.random.default_rng(4)
+    m = _random_q4_0(rng, 16, 128)
+    # one-hot x -> a column of W, exactly
+    x = np.zeros((1, 128), np.float32)
+    x[0, 37] = 1
+    assert np.array_equal(O.gemv_f64(m, x)[0], m.dense()[:, 37].astype(np.float64))
+    # all nibbles at the zero point -> 0
+    z = O.QuantMatrix(16, 128, False)
+    z.quants[:] = 0x88888888
+    z.scales[:] = O.to_half(0.5)
+    assert np.all(O.gemv_f64(z, rng.standard_normal((1, 128))) == 0)
+    assert np.all(O.matmul_split(z, O.f32_to_h2(rng.standard_normal((1, 128)))) == 0)
+
+
+@pytest.mark.parametrize("M", [1, 5])
+def test_matmul_split_block_form_matches_f64(M):
+    # sum_b d_b (sum q a - z sum a) = sum w a: the shader's block form equals
+    # the dense product up to float32 rounding.
+    rng = np.random.default_rng(10 + M)
+    m = _random_q4_0(rng, 64, 512)
+    x16 = O.f32_to_h2(rng.standard_normal((M, 512)).astype(np.float32))
+    want = O.gemv_f64(m, O.halves_to_f32(x16))
+    got = O.matmul_split(m, x16)
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel < 1e-5
+    # A planted mistake in the oracle's input (W transposed within a block
+    # row: nibbles read high-first) must fail the bar.
+    bad = O.QuantMatrix(64, 512, False)
+    bad.scales[:] = m.scales
+    qb = m.quants.view(np.uint8)
+    bad.quants.view(np.uint8)[:] = ((qb & 15) << 4) | (qb >> 4)
+    relbad = np.linalg.norm(O.matmul_split(bad, x16) - want) / np.linalg.norm(want)
+    assert relbad > 1e-1
+
+
+# --- attention, RoPE, norms -----------------------------------------------------
+
+def test_attention_closed_forms():
+    rng = np.random.default_rng(6)
+    hd, heads, kvh = 8, 4, 2
+    stride = kvh * hd
+    q = rng.standard_normal(heads * hd).astype(np.float32)
+    kc = O.f32_to_h2(rng.standard_normal((5, stride)).astype(np.float32))
+    vc = O.f32_to_h2(rng.standard_normal((5, stride)).astype(np.float32))
+    # one key -> out = v
+    out = O.attention_f64(q, kc, vc, heads, kvh, hd, 1, stride)
+    for h in range(heads):
+        kh = h // 2
+        assert np.allclose(out[h * hd:(h + 1) * hd], O.halves_to_f32(vc[0, kh * hd:(kh + 1) * hd]))
+    # equal scores (q = 0) -> mean of V
+    out = O.attention_f64(np.zeros_like(q), kc, vc, heads, kvh, hd, 5, stride)
+    vf = O.halves_to_f32(vc).astype(np.float64)
+    assert np.allclose(out[:hd], vf[:, :hd].mean(0))
+    # equal keys: any shift of the scores leaves the output unchanged
+    kc2 = np.tile(kc[:1], (5, 1))
+    a = O.attention_f64(q, kc2, vc, heads, kvh, hd, 5, stride)
+    assert np.allclose(a[:hd], vf[:, :hd].mean(0))
+
+
+def test_rope_and_norm_closed_forms():
+    hd, R = 64, 64
+    rope = O.rope_table(1e6, hd, R, 4096)
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(hd).astype(np.float32)
+    # position 0 is the identity
+    assert np.allclose(O.head_prep(x, None, rope, hd, R, 0, 1e-6, 1.0, False), x, atol=1e-7)
+    # a unit vector with unit weights normalizes to sqrt(hd) * v / |v|
+    v = np.zeros(hd, np.float32)
+    v[3] = 2.0
+    got = O.head_prep(v, np.ones(hd), rope, hd, R, 0, 0.0, 1.0, True)
+    assert np.allclose(got, v / 2 * math.sqrt(hd), atol=1e-5)
+    # rotation keeps each pair's norm; the angle of pair 0 is pos radians
+    for pos in (1, 1023, 1024, 3000):
+        y = O.head_prep(x, None, rope, hd, R, pos, 0.0, 1.0, False)
+        for j in range(R // 2):
+            a = math.hypot(x[j], x[j + R // 2])
+            b = math.hypot(y[j], y[j + R // 2])
+            assert abs(a - b) < 1e-5 * max(1, a)
+        ang = math.atan2(y[R // 2], y[0]) - math.atan2(x[R // 2], x[0])
+        assert abs(math.remainder(ang - pos, 2 * math.pi)) < 1e-4
+
+
+def test_rms_norm_and_swiglu():
+    x = np.array([[3.0, 4.0]], np.float32)
+    out = O.rms_norm(x, np.array([1.0, 2.0]), 0.0)
+    r = math.sqrt((9 + 16) / 2)
+    assert np.allclose(out, [[3 / r, 8 / r]])
+    gu = np.array([[0.0, 2.0, 5.0, 7.0]], np.float32)
+    assert np.allclose(O.swiglu(gu), [[0.0, 2 / (1 + math.exp(-2)) * 7]])
+
+
+# --- short convolution -----------------------------------------------------------
+
+def test_short_conv_closed_forms():
+    rng = np.random.default_rng(8)
+    D, W, M = 16, 3, 5
+    bcx = rng.standard_normal((M, 3 * D)).astype(np.float32)
+    state = rng.standard_normal((W - 1, D)).astype(np.float32)
+    taps = np.zeros((D, W), np.float32)
+    taps[:, W - 1] = 1
+    out, new_state, pre = O.short_conv(bcx, D, W, taps, state, prefixes=True)
+    B, Cm, X = bcx[:, :D], bcx[:, D:2 * D], bcx[:, 2 * D:]
+    assert np.allclose(out, Cm * B * X)
+    assert np.allclose(new_state, (B * X)[-(W - 1):])
+    # prefix p's state equals a fresh run on the first p tokens
+    for p in range(1, M + 1):
+        _, st = O.short_conv(bcx[:p], D, W, taps, state)
+        assert np.array_equal(pre[p - 1], st)
+    # taps on the oldest position read the state for the first token
+    taps2 = np.zeros((D, W), np.float32)
+    taps2[:, 0] = 1
+    out2, _ = O.short_conv(bcx[:1], D, W, taps2, state)
+    assert np.allclose(out2[0], Cm[0] * state[0])
+
+
+# --- greedy pick -------------------------------------------------------------------
+
+def test_argmax_ties_lowest_id_and_nan():
+    v = np.zeros(1000, np.float32)
+    v[300] = 5
+    v[700] = 5
+    assert O.argmax(v) == (300, 5.0)
+    v[10] = np.nan
+    assert O.argmax(v)[0] == 300
+    w = np.full(513, -1.0, np.float32)
+    w[255] = 2.0
+    w[256] = 2.0  # chunk boundary: the earlier chunk wins the tie
+    assert O.argmax(w)[0] == 255
+    assert O.argmax(np.full(10, -np.inf, np.float32))[0] == 0
