@@ -1,0 +1,180 @@
+/*
+ * webgllm_hip: the MI355X (gfx950) backend for webgllm's Q4 decode/prefill
+ * hot path, as a C ABI. Plain pointers and sizes; no torch or HIP types in
+ * the signatures (streams are passed as void*, a hipStream_t or NULL for the
+ * context's own stream).
+ *
+ * Two layers, as the reference's GPU-backend contract has them:
+ *  1. The backend object (reference: class Gpu, src/gpu/gl.ts:47, and the
+ *     PacedGpu contract, src/gpu/paced.ts:11-22): a context per device, device
+ *     buffers standing in for textures, asynchronous readback behind fences.
+ *  2. Typed kernels, one per family of the reference's GLSL generators
+ *     (src/gpu/kernels.ts), the way WebGpu.nativeProgram(spec) adds native
+ *     kernels beside compiled shaders (src/gpu/webgpu.ts:39-46, :413).
+ *
+ * Every call returns WG_OK (0) or a negative status; wg_last_error() gives
+ * the message (thread-local). Statuses map to the reference's GpuError kinds
+ * (src/gpu/gl.ts:110-113, :160-170, :271-275, :502-522).
+ *
+ * Paths cited are relative to packages/webgllm/ of the reference.
+ */
+#ifndef WEBGLLM_HIP_H
+#define WEBGLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------- statuses */
+#define WG_OK 0
+#define WG_ERR_INVALID (-1)     /* bad shape, layout or argument (GpuError "limits") */
+#define WG_ERR_OOM (-2)         /* device allocation failed (Gpu.outOfMemory, gl.ts:440-446) */
+#define WG_ERR_DEVICE (-3)      /* HIP error: the device is unusable (context lost, gl.ts:502) */
+#define WG_ERR_ALIASED (-4)     /* an op reads and writes one buffer (gl.ts:521-522) */
+#define WG_ERR_DISPOSED (-5)    /* use after wg_ctx_destroy / wg_buf_delete */
+#define WG_ERR_UNSUPPORTED (-6) /* no kernel for this variant (a program that won't compile) */
+
+const char *wg_last_error(void);
+const char *wg_version(void);
+
+/* ---------------------------------------------- 1. backend object layer */
+typedef struct wg_ctx wg_ctx;
+typedef struct wg_buf wg_buf;
+typedef struct wg_fence wg_fence;
+
+typedef struct {
+  int32_t device;
+  int32_t compute_units;
+  int64_t global_bytes;
+  int64_t max_alloc_bytes;
+  int32_t lds_bytes_per_block;
+  int32_t wave_size;
+} wg_limits;
+
+/* new Gpu(canvas) / dispose (gl.ts:316-331): a context on `device`, with
+ * its own stream. Destroy frees every buffer it still holds. */
+int wg_ctx_create(int device, wg_ctx **out);
+int wg_ctx_destroy(wg_ctx *ctx);
+/* Gpu.limits (gl.ts:131-140). */
+int wg_ctx_limits(wg_ctx *ctx, wg_limits *out);
+/* The context's stream (a hipStream_t), for callers that launch typed kernels on it. */
+void *wg_ctx_stream(wg_ctx *ctx);
+
+/* Gpu.texture (gl.ts:263-305): a device buffer, optionally initialised. */
+int wg_buf_create(wg_ctx *ctx, size_t bytes, const void *init, wg_buf **out);
+/* Gpu.write (gl.ts:354-374): bytes into [offset, offset + bytes). */
+int wg_buf_write(wg_ctx *ctx, wg_buf *buf, size_t offset, const void *src, size_t bytes);
+/* Gpu.zero (gl.ts:710-726). */
+int wg_buf_zero(wg_ctx *ctx, wg_buf *buf);
+/* Gpu.delete (gl.ts:448-461). */
+int wg_buf_delete(wg_ctx *ctx, wg_buf *buf);
+void *wg_buf_ptr(wg_buf *buf);
+size_t wg_buf_size(wg_buf *buf);
+/* Gpu.bytes: device bytes the context holds. */
+size_t wg_bytes_live(wg_ctx *ctx);
+
+/* Gpu.readStart (gl.ts:740-782): a copy of [offset, offset + bytes) queued
+ * behind the work already issued; wg_fence_ready polls it, wg_read_finish
+ * waits, copies into dst and frees the fence, wg_read_cancel frees it
+ * unread (PendingRead.cancel). */
+int wg_read_start(wg_ctx *ctx, wg_buf *buf, size_t offset, size_t bytes, wg_fence **out);
+int wg_fence_ready(wg_fence *f); /* 1 ready, 0 pending, < 0 error */
+int wg_read_finish(wg_fence *f, void *dst);
+int wg_read_cancel(wg_fence *f);
+/* Gpu.readNow (gl.ts:658-700): the same, blocking. */
+int wg_read_now(wg_ctx *ctx, wg_buf *buf, size_t offset, size_t bytes, void *dst);
+/* Gpu.flush (gl.ts:729-732) and PacedGpu.finish. */
+int wg_flush(wg_ctx *ctx);
+int wg_finish(wg_ctx *ctx);
+
+/* ------------------------------------------------ 2. quantized matrices */
+
+/* Device layouts of a 4-bit matrix.
+ * WG_LAYOUT_ROWGROUP is the reference's QuantMatrix layout (src/weights.ts:1-31,
+ * :153-178): rows in groups of 4, blocks of 32 along K, 16 bytes a block row
+ * in Q4_0 nibble order (byte j: weight j low, weight j + 16 high); word
+ * index ((g * blocks + b) * 4 + r) * 4 + w; scales (half bits) and zero
+ * points at (g * blocks + b) * 4 + r. Weight = scale * (q - zero).
+ * WG_LAYOUT_Q4K is GGUF Q4_K super-blocks (256 weights: fp16 d, fp16 dmin,
+ * 12 bytes of 6-bit scales and mins, 128 nibble bytes) kept at 0.5625
+ * bytes a weight and regrouped by rows of 4: record (g * supers + s) * 4 + r
+ * of 144 bytes; the kernels rebuild packQ4_K's per-32 (d', z')
+ * (src/repack.ts:100-168) in registers. */
+#define WG_LAYOUT_ROWGROUP 0
+#define WG_LAYOUT_Q4K 1
+
+/* Zero points of WG_LAYOUT_ROWGROUP: none (8, Q4_0), one u8 a block
+ * (MatMulNBits), or one half a block (Q4_K repacked: QuantMatrix.zeroHalves). */
+#define WG_ZERO_8 0
+#define WG_ZERO_U8 1
+#define WG_ZERO_F16 2
+
+typedef struct {
+  int32_t N;      /* output rows, a multiple of 4 */
+  int32_t K;      /* inputs per row, a multiple of 32 (256 for WG_LAYOUT_Q4K) */
+  int32_t layout; /* WG_LAYOUT_* */
+  int32_t zero;   /* WG_ZERO_* (WG_LAYOUT_ROWGROUP only) */
+  const void *quants; /* ROWGROUP: N*K/2 bytes; Q4K: N*K/256*144 bytes */
+  const void *scales; /* ROWGROUP: N*K/32 halves; Q4K: unused */
+  const void *zeros;  /* ROWGROUP: N*K/32 u8 or halves, or NULL for WG_ZERO_8 */
+} wg_q4_matrix;
+
+/* Bytes of device memory each array of a matrix needs. */
+int wg_q4_sizes(int32_t N, int32_t K, int32_t layout, int32_t zero, size_t *quant_bytes,
+                size_t *scale_bytes, size_t *zero_bytes);
+
+/* Load-time repacking on the GPU (the reference does these on the CPU while
+ * loading; src/load-gguf.ts, src/load-onnx.ts). Inputs are device copies of
+ * the file's bytes; `rows` rows go to rows row0.. of `dst` (row0 and rows
+ * multiples of 4); src_rows (device int32[rows]) may pick each row's source
+ * row, as the packers' srcRows does, or be NULL. */
+/* packQ4_0 (src/repack.ts:60-88): GGUF Q4_0 blocks (18 bytes) -> ROWGROUP, WG_ZERO_8. */
+int wg_repack_q4_0(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *src,
+                   const int32_t *src_rows, void *stream);
+/* packQ4_K (src/repack.ts:100-168): Q4_K super-blocks -> ROWGROUP, WG_ZERO_F16,
+ * bit-exact to the reference's (d', z') chain. */
+int wg_repack_q4_k(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *src,
+                   const int32_t *src_rows, void *stream);
+/* Q4_K super-blocks -> WG_LAYOUT_Q4K (a regrouping copy). */
+int wg_repack_q4_k_native(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *src,
+                          const int32_t *src_rows, void *stream);
+/* packMatMulNBits (src/repack.ts:342-390; the raw path's quantsFromRaw
+ * :216-245 + packMatMulNBitsScales :312-337): MatMulNBits quant bytes
+ * [rows][K/32][16], fp16 scale bytes [rows][K/32], zero points
+ * [rows][ceil(K/64)] (NULL: 8) -> ROWGROUP with WG_ZERO_U8 (or WG_ZERO_8). */
+int wg_repack_nbits(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *quant,
+                    const void *scales, const void *zp, const int32_t *src_rows, void *stream);
+
+/* matrixRow (src/repack.ts:865-891) on the GPU: rows [row0, row0 + rows)
+ * dequantized to float32, bit-exact: fp32(fp32(q - z) * d). */
+int wg_q4_dequant(const wg_q4_matrix *m, int32_t row0, int32_t rows, float *out, void *stream);
+
+/* ------------------------------------------------------------ matmul */
+
+/* Epilogue of a matmul: y[m][n] = (residual ? residual[m][n] : 0)
+ * + (row_scale ? row_scale[m] : 1) * (A W^T)[m][n]. residual may equal y
+ * (an in-place residual add; Engine.addNormed's add, engine.ts:5695-5803). */
+typedef struct {
+  const float *residual;
+  int32_t ld_residual;
+  const float *row_scale;
+} wg_epilogue;
+
+/* Decode / few-token GEMV (matmulSplitRgba4 and the split matmul,
+ * src/gpu/kernels.ts:744-895, :163-296, dispatched by Engine.splitPartials,
+ * engine.ts:5241-5377): y[m][n] = sum_k W[n][k] x[m][k] for M <= 8 rows of
+ * half activations x ([M][ldx], natural order), fp32 out. No MFMA: 128-bit
+ * loads of nibbles, dequant in registers, wavefront reductions. */
+int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx, float *y,
+               int32_t ldy, const wg_epilogue *ep, void *stream);
+
+/* float32 -> half activations, clamped to +-65504 (packH2, kernels.ts:32-36). */
+int wg_f32_to_f16(const float *x, uint16_t *out, int64_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,84 @@
+"""The C ABI on the CPU: the library loads, exports what the header
+declares, and rejects bad arguments before any device work."""
+import ctypes as C
+
+import pytest
+
+from webgllm_amd import lib as L
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.load()
+    names = L.header_functions()
+    assert len(names) > 20
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_version_and_no_error_initially():
+    lib = L.load()
+    assert b"gfx950" in lib.wg_version()
+
+
+def test_sizes():
+    lib = L.load()
+    q, s, z = C.c_size_t(), C.c_size_t(), C.c_size_t()
+    L.check(lib.wg_q4_sizes(2048, 2048, L.LAYOUT_ROWGROUP, L.ZERO_8, C.byref(q), C.byref(s),
+                            C.byref(z)))
+    # src/weights.ts:153-178: 2048 x 2048 Q4_0 = 524,288 words and 131,072 halves.
+    assert (q.value, s.value, z.value) == (2048 * 2048 // 2, 131072 * 2, 0)
+    L.check(lib.wg_q4_sizes(4096, 4096, L.LAYOUT_ROWGROUP, L.ZERO_U8, C.byref(q), C.byref(s),
+                            C.byref(z)))
+    assert z.value == 4096 * 128
+    L.check(lib.wg_q4_sizes(4096, 4096, L.LAYOUT_Q4K, 0, C.byref(q), C.byref(s), C.byref(z)))
+    assert q.value == 4096 * 16 * 144
+    with pytest.raises(L.WgError, match="multiple of 4"):
+        L.check(lib.wg_q4_sizes(6, 32, 0, 0, None, None, None))
+    with pytest.raises(L.WgError, match="multiple of 256"):
+        L.check(lib.wg_q4_sizes(4, 32, L.LAYOUT_Q4K, 0, None, None, None))
+
+
+def _desc(N=8, K=64, layout=L.LAYOUT_ROWGROUP, zero=L.ZERO_8):
+    # Fake device addresses: these calls must fail validation before any launch.
+    return L.Q4MatrixDesc(N, K, layout, zero, 0x1000, 0x2000, 0x3000 if zero else 0)
+
+
+@pytest.mark.parametrize("desc,M,msg", [
+    (_desc(N=6), 1, "multiple of 4"),
+    (_desc(K=48), 1, "multiple of 32"),
+    (_desc(), 0, "1 to 8"),
+    (_desc(), 9, "1 to 8"),
+    (_desc(zero=7), 1, "zero-point kind"),
+    (_desc(layout=5), 1, "layout"),
+])
+def test_gemv_rejects_bad_shapes(desc, M, msg):
+    lib = L.load()
+    rc = lib.wg_q4_gemv(C.byref(desc), 0x10000, M, 64, 0x20000, 8, None, None)
+    assert rc != 0 and msg in L.last_error()
+
+
+def test_gemv_rejects_overlap_and_alignment():
+    lib = L.load()
+    d = _desc()
+    rc = lib.wg_q4_gemv(C.byref(d), 0x10000, 1, 64, 0x10000 + 8, 8, None, None)
+    assert rc == -1 and "overlap" in L.last_error()
+    rc = lib.wg_q4_gemv(C.byref(d), 0x10002, 1, 64, 0x20000, 8, None, None)
+    assert rc == -1 and "aligned" in L.last_error()
+    ep = L.Epilogue(0x20004, 8, None)
+    rc = lib.wg_q4_gemv(C.byref(d), 0x10000, 1, 64, 0x20000, 8, C.byref(ep), None)
+    assert rc == -1 and "residual overlaps" in L.last_error()
+
+
+def test_repack_rejects_mismatched_layouts():
+    lib = L.load()
+    d = _desc(zero=L.ZERO_U8)
+    assert lib.wg_repack_q4_0(C.byref(d), 0, 8, 0x1000, None, None) == -1
+    assert "without zero points" in L.last_error()
+    d = _desc(zero=L.ZERO_8)
+    assert lib.wg_repack_q4_k(C.byref(d), 0, 8, 0x1000, None, None) == -1
+    assert "fractional zero points" in L.last_error()
+    assert lib.wg_repack_q4_0(C.byref(d), 4, 8, 0x1000, None, None) == -1
+    assert "outside the matrix" in L.last_error()
+    d = _desc(zero=L.ZERO_8)
+    assert lib.wg_repack_nbits(C.byref(d), 0, 8, 0x1, 0x2, 0x3, None, None) == -1
+    assert "without them" in L.last_error()

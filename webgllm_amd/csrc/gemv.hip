@@ -1,0 +1,262 @@
+// Decode / few-token GEMV for 4-bit weights (the reference's
+// matmulSplitRgba4 and split matmul, src/gpu/kernels.ts:744-895, :163-296,
+// dispatched by Engine.splitPartials, src/engine.ts:5241-5377).
+//
+// Bandwidth-bound, no MFMA. Mapping on gfx950 (wave64):
+//  - one wave per row group of 4 rows (the layout keeps a row group's block
+//    rows together: 64 contiguous bytes per block);
+//  - lane l takes blocks l, l + 64, ...: per block it loads the 4 rows'
+//    16-byte nibble rows (4 x 128-bit loads, 64 B contiguous), their 4 half
+//    scales (one 64-bit load) and zero points, and the block's 32 half
+//    activations per token (4 x 128-bit loads, L1/L2 hits: every wave reads
+//    the same x);
+//  - nibbles are unpacked as fp16 subnormals: a byte permute puts two
+//    bytes' nibbles in the two halves of a dword, and masking 0x000f000f
+//    (0x00f000f0) leaves q * 2^-24 (16 q * 2^-24) in each half, exactly. One
+//    v_dot2_f32_f16 then multiplies two weights by two activations with
+//    float32 accumulation, so the block sum b = sum q a costs ~1.25 VALU
+//    ops a weight;
+//  - per block and row, acc += d * (b - z * sa) with sa = sum a (the same
+//    identity the reference's shaders use), kept in units of 2^-24 until the
+//    epilogue;
+//  - a butterfly over the 64 lanes reduces the 4 rows x M tokens.
+#include "common.h"
+
+namespace wg {
+namespace {
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ inline half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+
+__device__ inline float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+}
+
+// Bytes 0 and 1 of w into the low byte of each half; bytes 2 and 3.
+constexpr uint32_t SEL01 = 0x0c010c00u;
+constexpr uint32_t SEL23 = 0x0c030c02u;
+constexpr uint32_t LO4 = 0x000f000fu;
+constexpr uint32_t HI4 = 0x00f000f0u;
+constexpr uint32_t ONES = 0x3c003c00u;  // (1.0h, 1.0h)
+
+// The 16 fp16-subnormal nibble pairs of one 16-byte block row, in the
+// order the activation pairs come: for word w, (q[4w], q[4w+1]) and
+// (q[4w+2], q[4w+3]) (low nibbles, factor 1), then (q[16+4w], q[17+4w]) and
+// (q[18+4w], q[19+4w]) (high nibbles, factor 16).
+struct Nibbles {
+  uint32_t lo[8], hi[8];
+};
+
+__device__ inline void unpack(const uint4 &q, Nibbles &n) {
+  uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    uint32_t p0 = __builtin_amdgcn_perm(0u, w[i], SEL01);
+    uint32_t p1 = __builtin_amdgcn_perm(0u, w[i], SEL23);
+    n.lo[2 * i] = p0 & LO4;
+    n.lo[2 * i + 1] = p1 & LO4;
+    n.hi[2 * i] = p0 & HI4;
+    n.hi[2 * i + 1] = p1 & HI4;
+  }
+}
+
+// sum q a over a block, times 2^-24: a[0..3] are the 32 activations as 16
+// half pairs, a[0], a[1] elements 0..15, a[2], a[3] 16..31.
+__device__ inline float block_dot(const Nibbles &n, const uint4 *a) {
+  const uint32_t lo_a[8] = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w};
+  const uint32_t hi_a[8] = {a[2].x, a[2].y, a[2].z, a[2].w, a[3].x, a[3].y, a[3].z, a[3].w};
+  float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    lo = dot2(n.lo[i], lo_a[i], lo);
+    hi = dot2(n.hi[i], hi_a[i], hi);
+  }
+  return __builtin_fmaf(hi, 0.0625f, lo);
+}
+
+__device__ inline float block_sum(const uint4 *a) {
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    s0 = dot2(a[i].x, ONES, s0);
+    s1 = dot2(a[i].y, ONES, s1);
+    s0 = dot2(a[i].z, ONES, s0);
+    s1 = dot2(a[i].w, ONES, s1);
+  }
+  return s0 + s1;
+}
+
+template <int ZK>
+__device__ inline void load_zeros(const void *zeros, int64_t si, float z[4]) {
+  if constexpr (ZK == WG_ZERO_8) {
+    z[0] = z[1] = z[2] = z[3] = 8.0f;
+  } else if constexpr (ZK == WG_ZERO_U8) {
+    uint32_t v = *reinterpret_cast<const uint32_t *>((const uint8_t *)zeros + si);
+    z[0] = (float)(v & 0xffu);
+    z[1] = (float)((v >> 8) & 0xffu);
+    z[2] = (float)((v >> 16) & 0xffu);
+    z[3] = (float)(v >> 24);
+  } else {
+    uint2 v = *reinterpret_cast<const uint2 *>((const uint16_t *)zeros + si);
+    z[0] = (float)as_h2(v.x).x;
+    z[1] = (float)as_h2(v.x).y;
+    z[2] = (float)as_h2(v.y).x;
+    z[3] = (float)as_h2(v.y).y;
+  }
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int M, int ZK>
+__global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
+    const uint4 *__restrict__ quants, const uint16_t *__restrict__ scales,
+    const void *__restrict__ zeros, const uint16_t *__restrict__ x, int ldx,
+    float *__restrict__ y, int ldy, const float *residual, int ldr,
+    const float *__restrict__ row_scale, int G, int B) {
+  const int lane = threadIdx.x & 63;
+  const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (g >= G) return;  // whole waves leave together
+  float acc[4][M];
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+#pragma unroll
+    for (int m = 0; m < M; m++) acc[r][m] = 0.0f;
+
+  const uint4 *qg = quants + (int64_t)g * B * 4;
+  const uint16_t *sg = scales + (int64_t)g * B * 4;
+  for (int b = lane; b < B; b += 64) {
+    const uint4 *qp = qg + (int64_t)b * 4;
+    uint4 q[4] = {qp[0], qp[1], qp[2], qp[3]};
+    uint2 sc = *reinterpret_cast<const uint2 *>(sg + (int64_t)b * 4);
+    float z[4];
+    load_zeros<ZK>(zeros, ((int64_t)g * B + b) * 4, z);
+    float d[4] = {(float)as_h2(sc.x).x, (float)as_h2(sc.x).y, (float)as_h2(sc.y).x,
+                  (float)as_h2(sc.y).y};
+    uint4 a[M][4];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const uint4 *xp = reinterpret_cast<const uint4 *>(x + (int64_t)m * ldx + b * 32);
+      a[m][0] = xp[0];
+      a[m][1] = xp[1];
+      a[m][2] = xp[2];
+      a[m][3] = xp[3];
+    }
+    float sa[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) sa[m] = block_sum(a[m]) * 0x1p-24f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      Nibbles n;
+      unpack(q[r], n);
+#pragma unroll
+      for (int m = 0; m < M; m++) {
+        float v = block_dot(n, a[m]);
+        v = __builtin_fmaf(-z[r], sa[m], v);
+        acc[r][m] = __builtin_fmaf(d[r], v, acc[r][m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      float v = wave_sum(acc[r][m]) * 0x1p24f;
+      if (lane == r + 4 * m) {
+        int n = 4 * g + r;
+        if (row_scale) v *= row_scale[m];
+        if (residual) v += residual[(int64_t)m * ldr + n];
+        y[(int64_t)m * ldy + n] = v;
+      }
+    }
+}
+
+template <int M>
+int launch_gemv_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
+                  const wg_epilogue *ep, hipStream_t s) {
+  int G = w->N / 4, B = w->K / 32;
+  dim3 grid((G + 3) / 4), block(256);
+  const float *res = ep ? ep->residual : nullptr;
+  int ldr = ep ? ep->ld_residual : 0;
+  const float *rs = ep ? ep->row_scale : nullptr;
+  const uint4 *q = (const uint4 *)w->quants;
+  const uint16_t *sc = (const uint16_t *)w->scales;
+  switch (w->zero) {
+    case WG_ZERO_8:
+      gemv_rowgroup_kernel<M, WG_ZERO_8><<<grid, block, 0, s>>>(q, sc, w->zeros, x, ldx, y, ldy,
+                                                                res, ldr, rs, G, B);
+      break;
+    case WG_ZERO_U8:
+      gemv_rowgroup_kernel<M, WG_ZERO_U8><<<grid, block, 0, s>>>(q, sc, w->zeros, x, ldx, y, ldy,
+                                                                 res, ldr, rs, G, B);
+      break;
+    default:
+      gemv_rowgroup_kernel<M, WG_ZERO_F16><<<grid, block, 0, s>>>(q, sc, w->zeros, x, ldx, y,
+                                                                  ldy, res, ldr, rs, G, B);
+      break;
+  }
+  return launched("wg_q4_gemv");
+}
+
+__global__ void f32_to_f16_kernel(const float *x, uint16_t *out, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float v = fminf(fmaxf(x[i], -65504.0f), 65504.0f);
+  out[i] = __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+}  // namespace
+}  // namespace wg
+
+using namespace wg;
+
+extern "C" {
+
+int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx, float *y,
+               int32_t ldy, const wg_epilogue *ep, void *stream) {
+  int rc = check_matrix(w, "wg_q4_gemv");
+  if (rc) return rc;
+  WG_REQUIRE(M >= 1 && M <= 8, "wg_q4_gemv: %d rows; a few-token matmul takes 1 to 8", M);
+  WG_REQUIRE(x && y, "wg_q4_gemv: null activations or output");
+  WG_REQUIRE(ldx >= w->K && ldx % 8 == 0, "wg_q4_gemv: ldx %d (K %d) must be >= K and a multiple of 8",
+             ldx, w->K);
+  WG_REQUIRE(ldy >= w->N, "wg_q4_gemv: ldy %d < N %d", ldy, w->N);
+  WG_REQUIRE(((uintptr_t)x & 15) == 0, "wg_q4_gemv: activations must be 16-byte aligned");
+  if (ep && ep->residual) {
+    WG_REQUIRE(ep->ld_residual >= w->N, "wg_q4_gemv: residual stride %d < N %d", ep->ld_residual,
+               w->N);
+    // An in-place add reads and writes the same element in one thread:
+    // allowed. Any other overlap would race.
+    WG_REQUIRE(ep->residual == y || !overlaps(ep->residual, (size_t)M * ep->ld_residual * 4, y,
+                                              (size_t)M * ldy * 4),
+               "wg_q4_gemv: residual overlaps the output");
+  }
+  WG_REQUIRE(!overlaps(x, (size_t)M * ldx * 2, y, (size_t)M * ldy * 4),
+             "wg_q4_gemv: activations and output overlap");
+  if (w->layout != WG_LAYOUT_ROWGROUP)
+    return fail(WG_ERR_UNSUPPORTED, "wg_q4_gemv: layout %d not built yet", w->layout);
+  hipStream_t s = as_stream(stream);
+  switch (M) {
+    case 1: return launch_gemv_m<1>(w, x, ldx, y, ldy, ep, s);
+    case 2: return launch_gemv_m<2>(w, x, ldx, y, ldy, ep, s);
+    case 3: return launch_gemv_m<3>(w, x, ldx, y, ldy, ep, s);
+    case 4: return launch_gemv_m<4>(w, x, ldx, y, ldy, ep, s);
+    case 5: return launch_gemv_m<5>(w, x, ldx, y, ldy, ep, s);
+    case 6: return launch_gemv_m<6>(w, x, ldx, y, ldy, ep, s);
+    case 7: return launch_gemv_m<7>(w, x, ldx, y, ldy, ep, s);
+    default: return launch_gemv_m<8>(w, x, ldx, y, ldy, ep, s);
+  }
+}
+
+int wg_f32_to_f16(const float *x, uint16_t *out, int64_t n, void *stream) {
+  WG_REQUIRE(x && out && n >= 0, "wg_f32_to_f16: bad arguments");
+  if (!n) return WG_OK;
+  f32_to_f16_kernel<<<(unsigned)((n + 255) / 256), 256, 0, as_stream(stream)>>>(x, out, n);
+  return launched("wg_f32_to_f16");
+}
+
+}  // extern "C"

@@ -1,0 +1,308 @@
+// Load-time repacking of quantized weights on the GPU, and the bit-exact
+// dequant (the reference's matrixRow). The reference repacks on the CPU
+// while loading (src/repack.ts); here the file's bytes are copied to the
+// device once and rearranged there, one thread per row block.
+#include "common.h"
+
+namespace wg {
+namespace {
+
+__device__ inline uint32_t ld32_unaligned(const uint8_t *p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+__device__ inline uint16_t ld16_unaligned(const uint8_t *p) {
+  return (uint16_t)(p[0] | (p[1] << 8));
+}
+
+// packQ4_0 (src/repack.ts:60-88): thread = (row i, block b).
+__global__ void repack_q4_0_kernel(uint32_t *quants, uint16_t *scales, const uint8_t *src,
+                                   const int32_t *src_rows, int row0, int rows, int blocks) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * blocks) return;
+  int i = (int)(t / blocks), b = (int)(t % blocks);
+  int n = row0 + i;
+  int s = src_rows ? src_rows[i] : i;
+  const uint8_t *p = src + ((int64_t)s * blocks + b) * 18;
+  int64_t si = ((int64_t)(n >> 2) * blocks + b) * 4 + (n & 3);
+  scales[si] = ld16_unaligned(p);
+  uint4 q;
+  q.x = ld32_unaligned(p + 2);
+  q.y = ld32_unaligned(p + 6);
+  q.z = ld32_unaligned(p + 10);
+  q.w = ld32_unaligned(p + 14);
+  reinterpret_cast<uint4 *>(quants)[si] = q;
+}
+
+// packMatMulNBits (src/repack.ts:342-390): output byte j = weight j (low
+// nibble of source byte j/2 ... ) re-interleaved to Q4_0 order; thread =
+// (row i, block b).
+__global__ void repack_nbits_kernel(uint32_t *quants, uint16_t *scales, uint8_t *zeros,
+                                    const uint8_t *quant, const uint8_t *scale_bytes,
+                                    const uint8_t *zp, const int32_t *src_rows, int row0,
+                                    int rows, int blocks) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * blocks) return;
+  int i = (int)(t / blocks), b = (int)(t % blocks);
+  int n = row0 + i;
+  int s = src_rows ? src_rows[i] : i;
+  const uint8_t *p = quant + ((int64_t)s * blocks + b) * 16;
+  int64_t si = ((int64_t)(n >> 2) * blocks + b) * 4 + (n & 3);
+  uint8_t out[16];
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    uint8_t lo = p[k], hi = p[8 + k];
+    out[2 * k] = (uint8_t)((lo & 0x0f) | ((hi & 0x0f) << 4));
+    out[2 * k + 1] = (uint8_t)((lo >> 4) | (hi & 0xf0));
+  }
+  uint4 q;
+  q.x = ld32_unaligned(out);
+  q.y = ld32_unaligned(out + 4);
+  q.z = ld32_unaligned(out + 8);
+  q.w = ld32_unaligned(out + 12);
+  reinterpret_cast<uint4 *>(quants)[si] = q;
+  scales[si] = ld16_unaligned(scale_bytes + ((int64_t)s * blocks + b) * 2);
+  if (zeros) {
+    int zp_stride = (blocks + 1) / 2;
+    zeros[si] = zp ? (zp[(int64_t)s * zp_stride + (b >> 1)] >> ((b & 1) << 2)) & 15 : 8;
+  }
+}
+
+// packQ4_K (src/repack.ts:100-168): thread = (row i, super-block s,
+// sub-block pair is/2). Same (d', z') chain: d' = half(d * sc); z' =
+// half(dmin * m / d') with the quotient in doubles; d' == 0 -> q = 15,
+// d' = half(-dmin * m / 15), z' = 0.
+__global__ void repack_q4_k_kernel(uint32_t *quants, uint16_t *scales, uint16_t *zero_halves,
+                                   const uint8_t *src, const int32_t *src_rows, int row0,
+                                   int rows, int supers) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * supers * 4) return;
+  int pair = (int)(t & 3);
+  int64_t rs = t >> 2;
+  int i = (int)(rs / supers), s = (int)(rs % supers);
+  int n = row0 + i;
+  int sr = src_rows ? src_rows[i] : i;
+  int blocks = supers * 8;
+  const uint8_t *p = src + ((int64_t)sr * supers + s) * 144;
+  double d = half_to_float(ld16_unaligned(p));
+  double dmin = half_to_float(ld16_unaligned(p + 2));
+  int is = 2 * pair;
+  int64_t si = ((int64_t)(n >> 2) * blocks + s * 8 + is) * 4 + (n & 3);
+  const uint8_t *at = p + 16 + is * 16;
+  const uint32_t LOW = 0x0f0f0f0fu;
+  uint4 q0, q1;
+  uint32_t lo[4], hi[4];
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    uint32_t a = ld32_unaligned(at + 4 * w), b = ld32_unaligned(at + 16 + 4 * w);
+    lo[w] = (a & LOW) | ((b & LOW) << 4);
+    hi[w] = ((a >> 4) & LOW) | (b & ~LOW);
+  }
+  q0 = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  q1 = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+  uint4 *qv = reinterpret_cast<uint4 *>(quants);
+  for (int j = 0; j < 2; j++) {
+    int sc, mn;
+    q4k_scale_min(p + 4, is + j, &sc, &mn);
+    double scale = d * sc, mins = dmin * mn;
+    int64_t a2 = si + 4 * j;
+    uint16_t h = double_to_half_ref(scale);
+    float hv = half_to_float(h);
+    if (hv != 0.0f) {
+      scales[a2] = h;
+      zero_halves[a2] = double_to_half_ref(mins / (double)hv);
+      qv[a2] = j ? q1 : q0;
+    } else {
+      scales[a2] = double_to_half_ref(-mins / 15.0);
+      zero_halves[a2] = 0;
+      qv[a2] = make_uint4(0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu);
+    }
+  }
+}
+
+// Q4_K super-blocks regrouped by rows of 4 (record (g * supers + s) * 4 + r):
+// thread = one 16-byte piece of one record.
+__global__ void repack_q4_k_native_kernel(uint8_t *dst, const uint8_t *src,
+                                          const int32_t *src_rows, int row0, int rows,
+                                          int supers) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * supers * 9) return;
+  int piece = (int)(t % 9);
+  int64_t rs = t / 9;
+  int i = (int)(rs / supers), s = (int)(rs % supers);
+  int n = row0 + i;
+  int sr = src_rows ? src_rows[i] : i;
+  const uint8_t *p = src + ((int64_t)sr * supers + s) * 144 + piece * 16;
+  uint8_t *o = dst + (((int64_t)(n >> 2) * supers + s) * 4 + (n & 3)) * 144 + piece * 16;
+#pragma unroll
+  for (int k = 0; k < 16; k++) o[k] = p[k];
+}
+
+// matrixRow (src/repack.ts:865-891), ROWGROUP: thread = (row, block): 32
+// weights fp32(d * (q - z)) with the product and difference in doubles, as
+// the reference computes them.
+__global__ void dequant_rowgroup_kernel(const uint32_t *quants, const uint16_t *scales,
+                                        const void *zeros, int zero_kind, int row0, int rows,
+                                        int blocks, float *out) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * blocks) return;
+  int i = (int)(t / blocks), b = (int)(t % blocks);
+  int n = row0 + i;
+  int64_t si = ((int64_t)(n >> 2) * blocks + b) * 4 + (n & 3);
+  double d = half_to_float(scales[si]);
+  double z = zero_kind == WG_ZERO_U8    ? (double)((const uint8_t *)zeros)[si]
+             : zero_kind == WG_ZERO_F16 ? (double)half_to_float(((const uint16_t *)zeros)[si])
+                                        : 8.0;
+  uint4 q = reinterpret_cast<const uint4 *>(quants)[si];
+  uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  float *o = out + (int64_t)i * blocks * 32 + b * 32;
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    uint32_t byte = (w[j >> 2] >> (8 * (j & 3))) & 0xffu;
+    o[j] = (float)(d * ((double)(byte & 15u) - z));
+    o[j + 16] = (float)(d * ((double)(byte >> 4) - z));
+  }
+}
+
+// The same for WG_LAYOUT_Q4K: thread = (row, super-block, sub-block);
+// (d', z') rebuilt with packQ4_K's chain, weights in the file's order.
+__global__ void dequant_q4k_kernel(const uint8_t *quants, int row0, int rows, int supers,
+                                   float *out) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * supers * 8) return;
+  int j = (int)(t & 7);
+  int64_t rs = t >> 3;
+  int i = (int)(rs / supers), s = (int)(rs % supers);
+  int n = row0 + i;
+  const uint8_t *p = quants + (((int64_t)(n >> 2) * supers + s) * 4 + (n & 3)) * 144;
+  double d = half_to_float(ld16_unaligned(p));
+  double dmin = half_to_float(ld16_unaligned(p + 2));
+  int sc, mn;
+  q4k_scale_min(p + 4, j, &sc, &mn);
+  uint16_t h = double_to_half_ref(d * sc);
+  double mins = dmin * mn;
+  double scale, zero;
+  bool constant = half_to_float(h) == 0.0f;
+  if (!constant) {
+    scale = half_to_float(h);
+    zero = half_to_float(double_to_half_ref(mins / scale));
+  } else {
+    scale = half_to_float(double_to_half_ref(-mins / 15.0));
+    zero = 0.0;
+  }
+  const uint8_t *q = p + 16 + (j >> 1) * 32;
+  float *o = out + (int64_t)i * supers * 256 + s * 256 + j * 32;
+  for (int l = 0; l < 32; l++) {
+    int nib = constant ? 15 : (j & 1) ? q[l] >> 4 : q[l] & 15;
+    o[l] = (float)(scale * ((double)nib - zero));
+  }
+}
+
+inline unsigned grid_for(int64_t threads, int per) { return (unsigned)((threads + per - 1) / per); }
+
+}  // namespace
+}  // namespace wg
+
+using namespace wg;
+
+extern "C" {
+
+static int check_rows(const wg_q4_matrix *m, int row0, int rows, const char *who) {
+  WG_REQUIRE(row0 >= 0 && rows >= 0 && row0 + rows <= m->N,
+             "%s: rows %d..%d are outside the matrix", who, row0, row0 + rows);
+  return WG_OK;
+}
+
+int wg_repack_q4_0(const wg_q4_matrix *m, int32_t row0, int32_t rows, const void *src,
+                   const int32_t *src_rows, void *stream) {
+  int rc = check_matrix(m, "wg_repack_q4_0");
+  if (rc) return rc;
+  if ((rc = check_rows(m, row0, rows, "wg_repack_q4_0"))) return rc;
+  WG_REQUIRE(m->layout == WG_LAYOUT_ROWGROUP && m->zero == WG_ZERO_8,
+             "wg_repack_q4_0: Q4_0 rows go into a row-group matrix without zero points");
+  WG_REQUIRE(src, "wg_repack_q4_0: no source");
+  if (!rows) return WG_OK;
+  int blocks = m->K / 32;
+  int64_t n = (int64_t)rows * blocks;
+  repack_q4_0_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(
+      (uint32_t *)m->quants, (uint16_t *)m->scales, (const uint8_t *)src, src_rows, row0, rows,
+      blocks);
+  return launched("wg_repack_q4_0");
+}
+
+int wg_repack_nbits(const wg_q4_matrix *m, int32_t row0, int32_t rows, const void *quant,
+                    const void *scales, const void *zp, const int32_t *src_rows, void *stream) {
+  int rc = check_matrix(m, "wg_repack_nbits");
+  if (rc) return rc;
+  if ((rc = check_rows(m, row0, rows, "wg_repack_nbits"))) return rc;
+  WG_REQUIRE(m->layout == WG_LAYOUT_ROWGROUP && m->zero != WG_ZERO_F16,
+             "wg_repack_nbits: MatMulNBits rows go into a row-group matrix with u8 or no zeros");
+  WG_REQUIRE(!zp || m->zero == WG_ZERO_U8,
+             "wg_repack_nbits: zero points given for a matrix without them");
+  WG_REQUIRE(quant && scales, "wg_repack_nbits: no source");
+  if (!rows) return WG_OK;
+  int blocks = m->K / 32;
+  int64_t n = (int64_t)rows * blocks;
+  repack_nbits_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(
+      (uint32_t *)m->quants, (uint16_t *)m->scales,
+      m->zero == WG_ZERO_U8 ? (uint8_t *)m->zeros : nullptr, (const uint8_t *)quant,
+      (const uint8_t *)scales, (const uint8_t *)zp, src_rows, row0, rows, blocks);
+  return launched("wg_repack_nbits");
+}
+
+int wg_repack_q4_k(const wg_q4_matrix *m, int32_t row0, int32_t rows, const void *src,
+                   const int32_t *src_rows, void *stream) {
+  int rc = check_matrix(m, "wg_repack_q4_k");
+  if (rc) return rc;
+  if ((rc = check_rows(m, row0, rows, "wg_repack_q4_k"))) return rc;
+  WG_REQUIRE(m->layout == WG_LAYOUT_ROWGROUP && m->zero == WG_ZERO_F16,
+             "wg_repack_q4_k: Q4_K rows go into a matrix with fractional zero points");
+  WG_REQUIRE(m->K % 256 == 0, "wg_repack_q4_k: columns (%d) must be a multiple of 256", m->K);
+  WG_REQUIRE(src, "wg_repack_q4_k: no source");
+  if (!rows) return WG_OK;
+  int supers = m->K / 256;
+  int64_t n = (int64_t)rows * supers * 4;
+  repack_q4_k_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(
+      (uint32_t *)m->quants, (uint16_t *)m->scales, (uint16_t *)m->zeros, (const uint8_t *)src,
+      src_rows, row0, rows, supers);
+  return launched("wg_repack_q4_k");
+}
+
+int wg_repack_q4_k_native(const wg_q4_matrix *m, int32_t row0, int32_t rows, const void *src,
+                          const int32_t *src_rows, void *stream) {
+  int rc = check_matrix(m, "wg_repack_q4_k_native");
+  if (rc) return rc;
+  if ((rc = check_rows(m, row0, rows, "wg_repack_q4_k_native"))) return rc;
+  WG_REQUIRE(m->layout == WG_LAYOUT_Q4K, "wg_repack_q4_k_native: destination is not Q4_K");
+  WG_REQUIRE(row0 % 4 == 0 && rows % 4 == 0,
+             "wg_repack_q4_k_native: rows must start and end on a row group");
+  WG_REQUIRE(src, "wg_repack_q4_k_native: no source");
+  if (!rows) return WG_OK;
+  int supers = m->K / 256;
+  int64_t n = (int64_t)rows * supers * 9;
+  repack_q4_k_native_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(
+      (uint8_t *)m->quants, (const uint8_t *)src, src_rows, row0, rows, supers);
+  return launched("wg_repack_q4_k_native");
+}
+
+int wg_q4_dequant(const wg_q4_matrix *m, int32_t row0, int32_t rows, float *out, void *stream) {
+  int rc = check_matrix(m, "wg_q4_dequant");
+  if (rc) return rc;
+  if ((rc = check_rows(m, row0, rows, "wg_q4_dequant"))) return rc;
+  WG_REQUIRE(out, "wg_q4_dequant: no output");
+  if (!rows) return WG_OK;
+  if (m->layout == WG_LAYOUT_ROWGROUP) {
+    int blocks = m->K / 32;
+    int64_t n = (int64_t)rows * blocks;
+    dequant_rowgroup_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(
+        (const uint32_t *)m->quants, (const uint16_t *)m->scales, m->zeros, m->zero, row0, rows,
+        blocks, out);
+  } else {
+    int supers = m->K / 256;
+    int64_t n = (int64_t)rows * supers * 8;
+    dequant_q4k_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(
+        (const uint8_t *)m->quants, row0, rows, supers, out);
+  }
+  return launched("wg_q4_dequant");
+}
+
+}  // extern "C"

@@ -1,0 +1,116 @@
+"""ctypes binding of libwebgllm_hip.so (the C ABI in include/webgllm_hip.h).
+
+torch supplies device memory and the current stream; every computation runs
+in the HIP library. There is no CPU fallback: if the library is missing the
+import of an op fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libwebgllm_hip.so")
+HEADER = os.path.join(os.path.dirname(_HERE), "include", "webgllm_hip.h")
+
+WG_OK = 0
+STATUS = {-1: "invalid", -2: "out-of-memory", -3: "device", -4: "aliased", -5: "disposed",
+          -6: "unsupported"}
+
+LAYOUT_ROWGROUP, LAYOUT_Q4K = 0, 1
+ZERO_8, ZERO_U8, ZERO_F16 = 0, 1, 2
+
+
+class WgError(RuntimeError):
+    """A failed call; `kind` as the reference's GpuError kinds (src/gpu/gl.ts)."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS.get(status, status)}: {message}")
+        self.status = status
+        self.kind = STATUS.get(status, "unknown")
+
+
+class Q4MatrixDesc(C.Structure):
+    _fields_ = [("N", C.c_int32), ("K", C.c_int32), ("layout", C.c_int32), ("zero", C.c_int32),
+                ("quants", C.c_void_p), ("scales", C.c_void_p), ("zeros", C.c_void_p)]
+
+
+class Epilogue(C.Structure):
+    _fields_ = [("residual", C.c_void_p), ("ld_residual", C.c_int32),
+                ("row_scale", C.c_void_p)]
+
+
+class Limits(C.Structure):
+    _fields_ = [("device", C.c_int32), ("compute_units", C.c_int32),
+                ("global_bytes", C.c_int64), ("max_alloc_bytes", C.c_int64),
+                ("lds_bytes_per_block", C.c_int32), ("wave_size", C.c_int32)]
+
+
+_lib = None
+
+
+def header_functions() -> list[str]:
+    """Every function include/webgllm_hip.h declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wg_[a-z0-9_]+)\s*\(", text)))
+
+
+def load():
+    """The loaded library; raises if it was never built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: build it first (python -c "
+                          "'import __graft_entry__ as g; g.build()')")
+    lib = C.CDLL(LIB_PATH)
+    P, I32, I64, SZ = C.c_void_p, C.c_int32, C.c_int64, C.c_size_t
+    sig = {
+        "wg_last_error": (C.c_char_p, []),
+        "wg_version": (C.c_char_p, []),
+        "wg_ctx_create": (C.c_int, [C.c_int, C.POINTER(P)]),
+        "wg_ctx_destroy": (C.c_int, [P]),
+        "wg_ctx_limits": (C.c_int, [P, C.POINTER(Limits)]),
+        "wg_ctx_stream": (P, [P]),
+        "wg_buf_create": (C.c_int, [P, SZ, P, C.POINTER(P)]),
+        "wg_buf_write": (C.c_int, [P, P, SZ, P, SZ]),
+        "wg_buf_zero": (C.c_int, [P, P]),
+        "wg_buf_delete": (C.c_int, [P, P]),
+        "wg_buf_ptr": (P, [P]),
+        "wg_buf_size": (SZ, [P]),
+        "wg_bytes_live": (SZ, [P]),
+        "wg_read_start": (C.c_int, [P, P, SZ, SZ, C.POINTER(P)]),
+        "wg_fence_ready": (C.c_int, [P]),
+        "wg_read_finish": (C.c_int, [P, P]),
+        "wg_read_cancel": (C.c_int, [P]),
+        "wg_read_now": (C.c_int, [P, P, SZ, SZ, P]),
+        "wg_flush": (C.c_int, [P]),
+        "wg_finish": (C.c_int, [P]),
+        "wg_q4_sizes": (C.c_int, [I32, I32, I32, I32, C.POINTER(SZ), C.POINTER(SZ),
+                                  C.POINTER(SZ)]),
+        "wg_repack_q4_0": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),
+        "wg_repack_q4_k": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),
+        "wg_repack_q4_k_native": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),
+        "wg_repack_nbits": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P, P, P]),
+        "wg_q4_dequant": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P]),
+        "wg_q4_gemv": (C.c_int, [C.POINTER(Q4MatrixDesc), P, I32, I32, P, I32,
+                                 C.POINTER(Epilogue), P]),
+        "wg_f32_to_f16": (C.c_int, [P, P, I64, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != WG_OK:
+        raise WgError(rc, load().wg_last_error().decode())
+
+
+def last_error() -> str:
+    return load().wg_last_error().decode()

@@ -1,0 +1,140 @@
+"""Typed ops over the C ABI, on torch device tensors (memory and streams only).
+
+Each function validates on the host, calls the HIP library on the current
+stream and raises WgError on a failed status. The reference functions each
+one stands in for are cited in include/webgllm_hip.h.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import lib as L
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _dev(t: torch.Tensor, dtype=None) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError("expected a device tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"expected {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError("expected a contiguous tensor")
+    return t
+
+
+def to_device_bytes(b, device="cuda") -> torch.Tensor:
+    """Host bytes (numpy / bytes) as a uint8 device tensor."""
+    arr = np.frombuffer(b, dtype=np.uint8) if isinstance(b, (bytes, bytearray)) else \
+        np.ascontiguousarray(b).view(np.uint8).reshape(-1)
+    return torch.from_numpy(arr.copy()).to(device)
+
+
+class Q4Matrix:
+    """A 4-bit matrix resident on the device (see WG_LAYOUT_* in the header)."""
+
+    def __init__(self, N: int, K: int, layout: int = L.LAYOUT_ROWGROUP, zero: int = L.ZERO_8,
+                 device="cuda"):
+        lib = L.load()
+        qb, sb, zb = C.c_size_t(), C.c_size_t(), C.c_size_t()
+        L.check(lib.wg_q4_sizes(N, K, layout, zero, C.byref(qb), C.byref(sb), C.byref(zb)))
+        self.N, self.K, self.layout, self.zero = N, K, layout, zero
+        self.quants = torch.zeros(qb.value, dtype=torch.uint8, device=device)
+        self.scales = torch.zeros(max(sb.value, 2) // 2, dtype=torch.int16, device=device) \
+            if sb.value else None
+        self.zeros = None
+        if zb.value:
+            self.zeros = torch.full((zb.value,), 8, dtype=torch.uint8, device=device) \
+                if zero == L.ZERO_U8 else torch.zeros(zb.value // 2, dtype=torch.int16,
+                                                      device=device)
+        self.desc = L.Q4MatrixDesc(N, K, layout, zero, _p(self.quants), _p(self.scales),
+                                   _p(self.zeros))
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.quants, self.scales, self.zeros)
+                   if t is not None)
+
+    # --- load-time repacking (the reference's loaders' packers, on the GPU)
+    @classmethod
+    def from_q4_0(cls, src: torch.Tensor, N: int, K: int, src_rows=None) -> "Q4Matrix":
+        m = cls(N, K, L.LAYOUT_ROWGROUP, L.ZERO_8, device=src.device)
+        m.repack_q4_0(0, N, src, src_rows)
+        return m
+
+    @classmethod
+    def from_q4_k(cls, src: torch.Tensor, N: int, K: int, native: bool = True,
+                  src_rows=None) -> "Q4Matrix":
+        if native:
+            m = cls(N, K, L.LAYOUT_Q4K, L.ZERO_8, device=src.device)
+            m.repack_q4_k_native(0, N, src, src_rows)
+        else:
+            m = cls(N, K, L.LAYOUT_ROWGROUP, L.ZERO_F16, device=src.device)
+            m.repack_q4_k(0, N, src, src_rows)
+        return m
+
+    @classmethod
+    def from_nbits(cls, quant: torch.Tensor, scales: torch.Tensor, zp, N: int, K: int,
+                   src_rows=None) -> "Q4Matrix":
+        m = cls(N, K, L.LAYOUT_ROWGROUP, L.ZERO_U8 if zp is not None else L.ZERO_8,
+                device=quant.device)
+        m.repack_nbits(0, N, quant, scales, zp, src_rows)
+        return m
+
+    def repack_q4_0(self, row0, rows, src, src_rows=None):
+        L.check(L.load().wg_repack_q4_0(C.byref(self.desc), row0, rows, _p(_dev(src)),
+                                        _p(src_rows), _stream()))
+
+    def repack_q4_k(self, row0, rows, src, src_rows=None):
+        L.check(L.load().wg_repack_q4_k(C.byref(self.desc), row0, rows, _p(_dev(src)),
+                                        _p(src_rows), _stream()))
+
+    def repack_q4_k_native(self, row0, rows, src, src_rows=None):
+        L.check(L.load().wg_repack_q4_k_native(C.byref(self.desc), row0, rows, _p(_dev(src)),
+                                               _p(src_rows), _stream()))
+
+    def repack_nbits(self, row0, rows, quant, scales, zp=None, src_rows=None):
+        L.check(L.load().wg_repack_nbits(C.byref(self.desc), row0, rows, _p(_dev(quant)),
+                                         _p(_dev(scales)), _p(zp), _p(src_rows), _stream()))
+
+    def dequant(self, row0: int = 0, rows: int | None = None) -> torch.Tensor:
+        rows = self.N - row0 if rows is None else rows
+        out = torch.empty((rows, self.K), dtype=torch.float32, device=self.quants.device)
+        L.check(L.load().wg_q4_dequant(C.byref(self.desc), row0, rows, _p(out), _stream()))
+        return out
+
+
+def gemv(m: Q4Matrix, x16: torch.Tensor, out: torch.Tensor | None = None,
+         residual: torch.Tensor | None = None, row_scale: torch.Tensor | None = None):
+    """y = x W^T for M <= 8 rows of half activations [M, K] (int16/float16 bits)."""
+    if x16.dtype not in (torch.float16, torch.int16):
+        raise ValueError("activations must be halves")
+    x16 = _dev(x16)
+    M = x16.shape[0] if x16.dim() == 2 else 1
+    ldx = x16.shape[-1]
+    if out is None:
+        out = torch.empty((M, m.N), dtype=torch.float32, device=x16.device)
+    _dev(out, torch.float32)
+    ep = None
+    if residual is not None or row_scale is not None:
+        ep = L.Epilogue(_p(residual), residual.shape[-1] if residual is not None else 0,
+                        _p(row_scale))
+    L.check(L.load().wg_q4_gemv(C.byref(m.desc), _p(x16), M, ldx, _p(out), out.shape[-1],
+                                C.byref(ep) if ep is not None else None, _stream()))
+    return out
+
+
+def f32_to_f16(x: torch.Tensor) -> torch.Tensor:
+    x = _dev(x, torch.float32)
+    out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    L.check(L.load().wg_f32_to_f16(_p(x), _p(out), x.numel(), _stream()))
+    return out
