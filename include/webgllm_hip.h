@@ -149,7 +149,8 @@ int wg_repack_nbits(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const v
                     const void *scales, const void *zp, const int32_t *src_rows, void *stream);
 
 /* matrixRow (src/repack.ts:865-891) on the GPU: rows [row0, row0 + rows)
- * dequantized to float32, bit-exact: fp32(fp32(q - z) * d). */
+ * dequantized to float32, bit-exact: fp32(d * (q - z)) with the difference
+ * and product in doubles, as the reference computes them. */
 int wg_q4_dequant(const wg_q4_matrix *m, int32_t row0, int32_t rows, float *out, void *stream);
 
 /* ------------------------------------------------------------ matmul */
@@ -173,6 +174,85 @@ int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx,
 
 /* float32 -> half activations, clamped to +-65504 (packH2, kernels.ts:32-36). */
 int wg_f32_to_f16(const float *x, uint16_t *out, int64_t n, void *stream);
+
+/* ---------------------------------------------- residual-stream glue */
+
+/* RMS norm into half activations (RMS_SCALE + NORM_TO_H2,
+ * src/gpu/kernels.ts:1195-1242): out[m][i] = half(x[m][i] * w[i] / sqrt(mean_i
+ * x[m][i]^2 + eps)), clamped to +-65504; rs_out[m] = the 1 / RMS (or NULL). */
+int wg_rms_norm(const float *x, int32_t M, int32_t D, int32_t ldx, const float *w, float eps,
+                uint16_t *out, int32_t ldo, float *rs_out, void *stream);
+
+/* SwiGLU (REDUCE_SWIGLU / SWIGLU_F16, kernels.ts:1066-1077, :1256-1264):
+ * out[m][i] = half(silu(gu[m][i]) * gu[m][F + i]) (gate rows, then up rows). */
+int wg_swiglu(const float *gu, int32_t M, int32_t F, int32_t ldg, uint16_t *out, int32_t ldo,
+              void *stream);
+
+/* Embedding rows (embed, kernels.ts:1092-1149): h[m] = row ids[m] of the
+ * quantized embedding, dequantized as matrixRow does (src/repack.ts:865-891).
+ * An id outside [0, N) embeds as zeros. */
+int wg_embed(const wg_q4_matrix *emb, const int32_t *ids, int32_t M, float *h, int32_t ldh,
+             void *stream);
+
+/* -------------------------------------------------------- attention */
+
+typedef struct {
+  int32_t heads;        /* query heads */
+  int32_t kv_heads;     /* KV heads (heads % kv_heads == 0: GQA) */
+  int32_t head_dim;
+  int32_t rotated_dims; /* dims RoPE rotates (the loaders put them first) */
+  float eps;            /* QK RMS norm epsilon */
+  int32_t use_norm;     /* 1: RMS-normalise q and k per head (headPrep norm: true) */
+} wg_attn_shape;
+
+/* headPrep + values (kernels.ts:2196-2322, :3030-3045): qkv rows hold heads
+ * * head_dim queries, then kv_heads * head_dim keys, then values. Queries go
+ * to q_out (float32, times 1/sqrt(head_dim)); keys and values to the caches
+ * ([ctx][kv_heads * head_dim] halves) at row *pos0 + m. `rope` is the table
+ * Engine.ropeTable builds (src/engine.ts:1292-1312): rope_rows rows of
+ * head_dim/2 cosines then head_dim/2 sines, rows 0..1023 positions 0..1023,
+ * row 1024 + i position 1024 i. *pos0 is read on the device (a graph
+ * replays at any position); rows outside [0, ctx) store nothing. */
+int wg_head_prep(const float *qkv, int32_t M, int32_t ldq, const wg_attn_shape *shape,
+                 const float *q_norm, const float *k_norm, const float *rope, int32_t rope_rows,
+                 const int32_t *pos0, float *q_out, int32_t ldqo, uint16_t *k_cache,
+                 uint16_t *v_cache, int32_t ctx, void *stream);
+
+/* Decode / verify attention (scores, attend, attendPanel + attendPanelCombine,
+ * kernels.ts:2386-2579, :2803-3027): row m's query at position *pos0 + m
+ * attends keys 0..*pos0 + m (causal) of its KV head; half output. max_keys
+ * is how many rows the caches hold (the position is clamped to it);
+ * scratch holds wg_attn_scratch_bytes(M, heads, head_dim, max_keys) bytes. */
+size_t wg_attn_scratch_bytes(int32_t M, int32_t heads, int32_t head_dim, int32_t max_keys);
+int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *shape,
+                   const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0,
+                   int32_t max_keys, uint16_t *out, int32_t ldo, void *scratch,
+                   size_t scratch_bytes, void *stream);
+
+/* ------------------------------------------------ short convolution */
+
+/* convFused + convPrefixes (kernels.ts:1447-1523; Engine.convolve,
+ * engine.ts:5806-5899): bcx rows B | C | x (3 D floats, src/weights.ts:180-190),
+ * taps [D][W] (tap W-1 is the current token), state [W-1][D] (oldest
+ * first). out[t] = half(C_t * sum_k taps[c][k] * y[t-(W-1)+k]) with y = B * x;
+ * state_out = the last W-1 y rows (may be state itself); prefixes
+ * [M][W-1][D], or NULL, = the state after each prefix of the batch. */
+int wg_short_conv(const float *bcx, int32_t M, int32_t D, int32_t ldb, int32_t W,
+                  const float *taps, const float *state, float *state_out, float *prefixes,
+                  uint16_t *out, int32_t ldo, void *stream);
+/* Engine.accept's rollback (engine.ts:8063-8086, COPY_ROWS kernels.ts:2177-2183):
+ * state <- the state after the first `kept` of `rows` tokens. */
+int wg_conv_accept(const float *prefixes, int32_t kept, int32_t rows, int32_t D, int32_t W,
+                   float *state, void *stream);
+
+/* ------------------------------------------------------ greedy pick */
+
+/* CHUNK_MAX_AT + CHUNK_ARGMAX_ROWS (kernels.ts:3169-3246): ids[m] = the lowest
+ * id holding row m's largest logit (strict > from -3e38 at id 0: NaN never
+ * wins); tops[m] its logit (or NULL). */
+size_t wg_argmax_scratch_bytes(int32_t M, int32_t V);
+int wg_argmax_rows(const float *logits, int32_t M, int32_t V, int32_t ld, int32_t *ids,
+                   float *tops, void *scratch, size_t scratch_bytes, void *stream);
 
 #ifdef __cplusplus
 }

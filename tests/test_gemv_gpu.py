@@ -45,16 +45,17 @@ def _q4_k(rng, N, K, native=False):
     return ops.Q4Matrix.from_q4_k(ops.to_device_bytes(src), N, K, native=native), want
 
 
-MAKERS = {"q4_0": _q4_0, "nbits": _nbits, "q4_k": _q4_k}
+MAKERS = {"q4_0": _q4_0, "nbits": _nbits, "q4_k": _q4_k,
+          "q4_k_native": lambda rng, N, K: _q4_k(rng, N, K, native=True)}
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k"])
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k", "q4_k_native"])
 @pytest.mark.parametrize("N,K", [(2048, 2048), (896, 896), (4864, 896), (896, 4864), (64, 32),
                                  (1024, 4096)])
 @pytest.mark.parametrize("M", [1, 5])
 def test_gemv_matches_oracle(hip, fmt, N, K, M):
     from webgllm_amd import ops
-    if fmt == "q4_k" and K % 256:
+    if fmt.startswith("q4_k") and K % 256:
         pytest.skip("Q4_K rows are super-blocks of 256")
     rng = np.random.default_rng(N * 31 + K + M)
     m, want_m = MAKERS[fmt](rng, N, K)

@@ -1,0 +1,200 @@
+"""Norm, SwiGLU, embedding, headPrep, decode attention, short convolution and
+greedy pick on the GPU against the oracle."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import gguf_q4_0, nbits, random_q4_k_bytes, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def _h(t):
+    return O.halves_to_f32(t.view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+@pytest.mark.parametrize("M,D", [(1, 896), (5, 2048), (1, 4096), (3, 14336)])
+def test_rms_norm(hip, M, D):
+    from webgllm_amd import ops
+    rng = np.random.default_rng(D + M)
+    x = (rng.standard_normal((M, D)) * 3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    rs = torch.empty(M, device="cuda")
+    out = ops.rms_norm(_t(x), _t(w), 1e-5, rs_out=rs)
+    want = O.rms_norm(x, w, 1e-5)
+    got = _h(out)
+    # half outputs: within half rounding of the float64 norm
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -10 + 1e-7)
+    assert np.allclose(rs.cpu().numpy(), 1 / np.sqrt((x.astype(np.float64) ** 2).mean(1) + 1e-5),
+                       rtol=1e-5)
+
+
+def test_swiglu(hip):
+    from webgllm_amd import ops
+    rng = np.random.default_rng(1)
+    gu = (rng.standard_normal((3, 2 * 4864)) * 2).astype(np.float32)
+    got = _h(ops.swiglu(_t(gu)))
+    want = O.swiglu(gu)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -10 + 1e-6)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k", "q4_k_native"])
+def test_embed_bit_exact(hip, fmt):
+    from webgllm_amd import ops
+    rng = np.random.default_rng(11)
+    N, K = 512, 512
+    if fmt == "q4_0":
+        src = gguf_q4_0(rng, N, K)
+        want = O.QuantMatrix(N, K, False)
+        O.pack_q4_0(want, 0, src, N)
+        m = ops.Q4Matrix.from_q4_0(ops.to_device_bytes(src), N, K)
+    elif fmt == "nbits":
+        q, s, z = nbits(rng, N, K)
+        want = O.QuantMatrix(N, K, True)
+        O.pack_nbits(want, 0, q, s, z, N)
+        m = ops.Q4Matrix.from_nbits(ops.to_device_bytes(q), ops.to_device_bytes(s),
+                                    ops.to_device_bytes(z), N, K)
+    else:
+        src = random_q4_k_bytes(rng, N, K, zero_scale_every=3)
+        want = O.QuantMatrix(N, K, "halves")
+        O.pack_q4_k(want, 0, src, N)
+        m = ops.Q4Matrix.from_q4_k(ops.to_device_bytes(src), N, K, native=fmt == "q4_k_native")
+    ids = np.array([0, 5, 511, 300, 7, 1000, -1], np.int32)
+    got = ops.embed(m, _t(ids)).cpu().numpy()
+    for i, n in enumerate(ids):
+        if 0 <= n < N:
+            assert np.array_equal(got[i].view(np.uint32), want.row(int(n)).view(np.uint32))
+        else:
+            assert np.all(got[i] == 0)
+
+
+def _cache_rows(k_cache, rows):
+    return k_cache[:rows].view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("H,KV,hd,R,norm", [(14, 2, 64, 64, False), (32, 8, 128, 128, False),
+                                            (32, 8, 64, 64, True), (8, 2, 128, 64, True)])
+@pytest.mark.parametrize("pos0", [0, 1021, 3000])
+def test_head_prep(hip, H, KV, hd, R, norm, pos0):
+    from webgllm_amd import ops
+    rng = np.random.default_rng(H * hd + pos0)
+    M, ctx = 3, 4096
+    rope = O.rope_table(1e6, hd, R, ctx)
+    qkv = rng.standard_normal((M, (H + 2 * KV) * hd)).astype(np.float32)
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    shape = ops.attn_shape(H, KV, hd, R, 1e-6, norm)
+    kc = torch.zeros((ctx, KV * hd), dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    q = ops.head_prep(_t(qkv), shape, _t(rope), _t(np.array([pos0], np.int32)), kc, vc,
+                      _t(qn) if norm else None, _t(kn) if norm else None).cpu().numpy()
+    kcn = _cache_rows(kc, ctx)
+    vcn = _cache_rows(vc, ctx)
+    for m in range(M):
+        pos = pos0 + m
+        for h in range(H):
+            x = qkv[m, h * hd:(h + 1) * hd]
+            want = O.head_prep(x, qn, rope, hd, R, pos, 1e-6, 1 / math.sqrt(hd), norm)
+            assert np.allclose(q[m, h * hd:(h + 1) * hd], want, rtol=1e-5, atol=1e-6)
+        for h in range(KV):
+            x = qkv[m, (H + h) * hd:(H + h + 1) * hd]
+            want = O.f32_to_h2(O.head_prep(x, kn, rope, hd, R, pos, 1e-6, 1.0, norm))
+            got = kcn[pos, h * hd:(h + 1) * hd]
+            # halves of float32 values that agree to ~1e-6: at most one half ulp apart
+            assert np.max(np.abs(got.astype(np.int32) - want.astype(np.int32))) <= 1
+            v = qkv[m, (H + KV + h) * hd:(H + KV + h + 1) * hd]
+            assert np.array_equal(vcn[pos, h * hd:(h + 1) * hd], O.f32_to_h2(v))
+    # rows outside the written positions stay untouched
+    assert not np.any(kcn[pos0 + M:])
+
+
+@pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (32, 8, 128), (32, 8, 64)])
+@pytest.mark.parametrize("M,pos0", [(1, 0), (1, 63), (1, 64), (1, 4095), (5, 200), (5, 1500)])
+def test_attn_decode(hip, H, KV, hd, M, pos0):
+    from webgllm_amd import ops
+    rng = np.random.default_rng(H + hd + M + pos0)
+    ctx = 4096 + 8
+    shape = ops.attn_shape(H, KV, hd)
+    kd = KV * hd
+    nkeys = pos0 + M
+    k = O.f32_to_h2((rng.standard_normal((nkeys, kd))).astype(np.float32))
+    v = O.f32_to_h2(rng.standard_normal((nkeys, kd)).astype(np.float32))
+    q = (rng.standard_normal((M, H * hd)) / math.sqrt(hd) * 2).astype(np.float32)
+    kc = torch.zeros((ctx, kd), dtype=torch.int16, device="cuda")
+    vc = torch.zeros_like(kc)
+    kc[:nkeys] = _t(k.view(np.int16))
+    vc[:nkeys] = _t(v.view(np.int16))
+    out = ops.attn_decode(_t(q), shape, kc, vc, _t(np.array([pos0], np.int32)))
+    got = _h(out)
+    for m in range(M):
+        want = O.attention_f64(q[m], k, v, H, KV, hd, pos0 + m + 1, kd)
+        err = rel_l2(got[m], want)
+        assert err <= 1e-3, (m, err)
+
+
+def test_attn_decode_single_key_and_uniform(hip):
+    from webgllm_amd import ops
+    H, KV, hd = 4, 2, 64
+    shape = ops.attn_shape(H, KV, hd)
+    rng = np.random.default_rng(2)
+    v = O.f32_to_h2(rng.standard_normal((300, KV * hd)).astype(np.float32))
+    kc = torch.zeros((300, KV * hd), dtype=torch.int16, device="cuda")
+    vc = _t(v.view(np.int16))
+    # one key: out = v[0] exactly (weight 1)
+    q = _t(rng.standard_normal((1, H * hd)).astype(np.float32))
+    got = _h(ops.attn_decode(q, shape, kc, vc, _t(np.array([0], np.int32))))
+    vf = O.halves_to_f32(v)
+    assert np.array_equal(got[0, :hd], vf[0, :hd])
+    # equal scores (zero keys): the mean of the values
+    got = _h(ops.attn_decode(q, shape, kc, vc, _t(np.array([299], np.int32))))
+    assert rel_l2(got[0, :hd], vf[:300, :hd].astype(np.float64).mean(0)) < 1e-3
+
+
+@pytest.mark.parametrize("M,D,W", [(1, 2048, 3), (5, 2048, 3), (8, 1024, 4)])
+def test_short_conv_and_accept(hip, M, D, W):
+    from webgllm_amd import ops
+    rng = np.random.default_rng(M * D + W)
+    bcx = rng.standard_normal((M, 3 * D)).astype(np.float32)
+    taps = rng.standard_normal((D, W)).astype(np.float32)
+    state = rng.standard_normal((W - 1, D)).astype(np.float32)
+    st = _t(state)
+    pre = torch.empty((M, W - 1, D), device="cuda")
+    out = ops.short_conv(_t(bcx), D, W, _t(taps), st, prefixes=pre)
+    want, want_state, want_pre = O.short_conv(bcx, D, W, taps, state, prefixes=True)
+    got = _h(out)
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -10 + 1e-5)
+    assert np.allclose(st.cpu().numpy(), want_state, rtol=1e-6, atol=1e-6)
+    assert np.allclose(pre.cpu().numpy(), want_pre, rtol=1e-6, atol=1e-6)
+    for kept in range(1, M + 1):
+        ops.conv_accept(pre, kept, M, D, W, st)
+        assert np.array_equal(st.cpu().numpy(), want_pre[kept - 1])
+    with pytest.raises(Exception, match="can't keep"):
+        ops.conv_accept(pre, M + 1, M, D, W, st)
+
+
+@pytest.mark.parametrize("V", [1000, 65536, 128256, 151936])
+def test_argmax(hip, V):
+    from webgllm_amd import ops
+    rng = np.random.default_rng(V)
+    x = rng.standard_normal((3, V)).astype(np.float32)
+    x[1, V // 3] = 50
+    x[1, V // 2] = 50          # tie: lower id
+    x[2, :] = -np.inf
+    x[2, 17] = np.nan
+    ids = ops.argmax_rows(_t(x)).cpu().numpy()
+    for m in range(3):
+        assert ids[m] == O.argmax(x[m])[0]
+    assert ids[1] == V // 3 and ids[2] == 0
+    # chunk boundary tie (256-logit chunks in the reference; 4096 here)
+    y = np.full((1, V), -1.0, np.float32)
+    y[0, min(V - 1, 4096)] = 3
+    y[0, min(V - 1, 4095)] = 3
+    assert ops.argmax_rows(_t(y)).cpu().numpy()[0] == O.argmax(y[0])[0]

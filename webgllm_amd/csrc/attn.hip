@@ -1,0 +1,302 @@
+// Attention over the fp16 KV cache for decode and speculative verify.
+//
+// head_prep: the reference's headPrep + values (src/gpu/kernels.ts:2196-2322,
+// :3030-3045): per head, optional RMS norm over head_dim, RoPE on the
+// rotated dims (dim j pairs with j + R/2 at frequency j; the angle of
+// pos = lo + 1024 hi is added from two rows of the table, as
+// Engine.ropeTable builds it, src/engine.ts:1292-1312), times 1/sqrt(hd)
+// for queries; keys and values go into the cache as halves.
+//
+// attn_decode: scores / attend / attendPanel (kernels.ts:2386-2579,
+// :2803-3027) as split-K flash decoding: a workgroup takes one KV head and a
+// chunk of 64 keys for every query row and every query head sharing that KV
+// head (GQA: each key and value is read once for all of them), stages the
+// K and V tiles in LDS, and writes the chunk's (max, sum of weights,
+// weighted sum of values); a combine pass rescales the chunks by their
+// running max (attendPanelCombine's online softmax) into half outputs.
+// The position comes from device memory so a captured graph replays at any
+// position; chunks past the last key leave at once.
+#include "common.h"
+#include "dot.h"
+
+namespace wg {
+namespace {
+
+constexpr int CHUNK = 64;        // keys a workgroup takes
+constexpr int MAX_HD = 256;
+
+__device__ inline uint16_t to_h(float v) {
+  v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+  return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// One wave per (row m, head slot): slots [0, H) queries, [H, H + KV) keys,
+// [H + KV, H + 2 KV) values.
+__global__ __launch_bounds__(64) void head_prep_kernel(
+    const float *qkv, int ldq, int H, int KV, int hd, int R, float eps, int use_norm,
+    const float *q_norm, const float *k_norm, const float *rope, int rope_rows,
+    const int32_t *pos0_dev, float *q_out, int ldqo, uint16_t *k_cache, uint16_t *v_cache,
+    int ctx) {
+  const int slot = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+  const int pos = *pos0_dev + m;
+  const float *x = qkv + (int64_t)m * ldq + (int64_t)slot * hd;
+  const int kvd = KV * hd;
+  if (pos < 0 || pos >= ctx || 1024 + (pos >> 10) >= rope_rows) {
+    // A row past the cache has no position: its query is zero, nothing is stored.
+    if (slot < H)
+      for (int t = lane; t < hd; t += 64) q_out[(int64_t)m * ldqo + (int64_t)slot * hd + t] = 0.0f;
+    return;
+  }
+  if (slot >= H + KV) {  // values: into the cache as they are
+    uint16_t *vo = v_cache + (int64_t)pos * kvd + (int64_t)(slot - H - KV) * hd;
+    for (int t = lane; t < hd; t += 64) vo[t] = to_h(x[t]);
+    return;
+  }
+  const bool is_q = slot < H;
+  const float *nw = is_q ? q_norm : k_norm;
+  float inv = 1.0f;
+  if (use_norm) {
+    float s = 0.0f;
+    for (int t = lane; t < hd; t += 64) s += x[t] * x[t];
+    s = wave_sum(s);
+    inv = 1.0f / sqrtf(s / (float)hd + eps);
+  }
+  const int P = R / 2;
+  const int lo = pos & 1023, hi = 1024 + (pos >> 10);
+  const float *r_lo = rope + (int64_t)lo * hd, *r_hi = rope + (int64_t)hi * hd;
+  const float scale = is_q ? 1.0f / sqrtf((float)hd) : 1.0f;
+  for (int t = lane; t < hd; t += 64) {
+    float v = x[t] * (use_norm ? inv * nw[t] : 1.0f);
+    float r = v;
+    if (t < 2 * P) {
+      bool first = t < P;
+      int tp = first ? t + P : t - P;
+      int f = first ? t : tp;
+      float p = x[tp] * (use_norm ? inv * nw[tp] : 1.0f);
+      float c1 = r_lo[f], s1 = r_lo[hd / 2 + f], c2 = r_hi[f], s2 = r_hi[hd / 2 + f];
+      float cs = c1 * c2 - s1 * s2, sn = s1 * c2 + c1 * s2;
+      r = first ? v * cs - p * sn : v * cs + p * sn;
+    }
+    if (is_q) {
+      q_out[(int64_t)m * ldqo + (int64_t)slot * hd + t] = r * scale;
+    } else {
+      k_cache[(int64_t)pos * kvd + (int64_t)(slot - H) * hd + t] = to_h(r);
+    }
+  }
+}
+
+// Partial results of one (query row, query head, chunk): the chunk's max
+// score, its sum of exp(score - max), and the weighted values.
+struct PartialLayout {
+  int hd, chunks;
+  __device__ int64_t base(int qh_row, int chunk) const {
+    return ((int64_t)qh_row * chunks + chunk) * (hd + 2);
+  }
+};
+
+// Workgroup = (KV head kh, chunk c). Queries: rows m < M of heads
+// kh * G .. kh * G + G - 1, GM = G * M of them.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_chunk_kernel(
+    const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
+    const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int chunks) {
+  constexpr int KSTR = HD + 2;  // LDS row stride in halves (breaks bank conflicts)
+  __shared__ uint16_t ks[CHUNK * KSTR];
+  __shared__ uint16_t vs[CHUNK * KSTR];
+  __shared__ float qs[64 * HD];
+  __shared__ float sc[64 * CHUNK];
+  __shared__ float mx[64], lsum[64];
+  const int kh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+  const int pos0 = *pos0_dev;
+  // The last row sees keys 0 .. pos0 + M - 1; never more than the cache holds.
+  const int n_keys = min(pos0 + M, max_keys);
+  const int j0 = c * CHUNK;
+  if (j0 >= n_keys) return;
+  const int G = H / KV, GM = G * M;
+  const int kvd = KV * HD;
+  const int nk = min(CHUNK, n_keys - j0);
+  // Stage K and V rows j0 .. j0 + nk - 1 of head kh: 16-byte pieces.
+  constexpr int PIECES = HD / 8;
+  for (int i = tid; i < nk * PIECES; i += 256) {
+    int r = i / PIECES, p = i % PIECES;
+    const uint4 *kp = reinterpret_cast<const uint4 *>(k_cache + (int64_t)(j0 + r) * kvd + kh * HD);
+    const uint4 *vp = reinterpret_cast<const uint4 *>(v_cache + (int64_t)(j0 + r) * kvd + kh * HD);
+    uint4 kv = kp[p], vv = vp[p];
+    uint32_t *kd = reinterpret_cast<uint32_t *>(ks + r * KSTR + p * 8);
+    uint32_t *vd = reinterpret_cast<uint32_t *>(vs + r * KSTR + p * 8);
+    kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
+    vd[0] = vv.x; vd[1] = vv.y; vd[2] = vv.z; vd[3] = vv.w;
+  }
+  for (int i = tid; i < GM * HD; i += 256) {
+    int qi = i / HD, d = i % HD;
+    int g = qi % G, m = qi / G;
+    qs[i] = q[(int64_t)m * ldq + (int64_t)(kh * G + g) * HD + d];
+  }
+  __syncthreads();
+  // Scores, causal: row m sees keys j <= pos0 + m.
+  for (int i = tid; i < GM * CHUNK; i += 256) {
+    int qi = i / CHUNK, r = i % CHUNK;
+    int m = qi / G;
+    float s = -INFINITY;
+    if (r < nk && j0 + r <= pos0 + m) {
+      const float *qv = qs + qi * HD;
+      const uint16_t *kr = ks + r * KSTR;
+      float a = 0.0f;
+#pragma unroll 8
+      for (int d = 0; d < HD; d += 2) {
+        uint32_t k2 = *reinterpret_cast<const uint32_t *>(kr + d);
+        half2v kk = as_h2(k2);
+        a = __builtin_fmaf(qv[d], (float)kk.x, a);
+        a = __builtin_fmaf(qv[d + 1], (float)kk.y, a);
+      }
+      s = a;
+    }
+    sc[i] = s;
+  }
+  __syncthreads();
+  // Per query: the chunk's max and sum of weights (one wave per query).
+  const int wave = tid >> 6, lane = tid & 63;
+  for (int qi = wave; qi < GM; qi += 4) {
+    float v = lane < CHUNK ? sc[qi * CHUNK + lane] : -INFINITY;
+    float m_ = v;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m_ = fmaxf(m_, __shfl_xor(m_, off, 64));
+    float e = (m_ == -INFINITY || v == -INFINITY) ? 0.0f : __expf(v - m_);
+    if (lane < CHUNK) sc[qi * CHUNK + lane] = e;
+    float l = wave_sum(e);
+    if (lane == 0) {
+      mx[qi] = m_;
+      lsum[qi] = l;
+    }
+  }
+  __syncthreads();
+  // Weighted values.
+  PartialLayout pl{HD, chunks};
+  for (int i = tid; i < GM * HD; i += 256) {
+    int qi = i / HD, d = i % HD;
+    const float *e = sc + qi * CHUNK;
+    float a = 0.0f;
+    for (int r = 0; r < nk; r++) {
+      half2v vv = as_h2(*reinterpret_cast<const uint32_t *>(vs + r * KSTR + (d & ~1)));
+      a = __builtin_fmaf(e[r], (float)((d & 1) ? vv.y : vv.x), a);
+    }
+    int g = qi % G, m = qi / G;
+    int row = m * H + kh * G + g;
+    float *out = partial + pl.base(row, c);
+    out[2 + d] = a;
+    if (d == 0) {
+      out[0] = mx[qi];
+      out[1] = lsum[qi];
+    }
+  }
+}
+
+// One wave per (row m, query head h): the chunks' online-softmax combine.
+__global__ __launch_bounds__(64) void attn_combine_kernel(const float *partial, int M, int H,
+                                                          int hd, int chunks,
+                                                          const int32_t *pos0_dev,
+                                                          int max_keys, uint16_t *out, int ldo) {
+  const int h = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+  const int n_keys = min(*pos0_dev + m + 1, max_keys);  // keys row m sees
+  if (n_keys <= 0) {
+    for (int d = lane; d < hd; d += 64) out[(int64_t)m * ldo + (int64_t)h * hd + d] = 0;
+    return;
+  }
+  const int used = (n_keys + CHUNK - 1) / CHUNK;
+  const int row = m * H + h;
+  PartialLayout pl{hd, chunks};
+  float gmax = -INFINITY;
+  for (int c = 0; c < used; c++) gmax = fmaxf(gmax, partial[pl.base(row, c)]);
+  float l = 0.0f;
+  float acc[MAX_HD / 64];
+#pragma unroll
+  for (int i = 0; i < MAX_HD / 64; i++) acc[i] = 0.0f;
+  for (int c = 0; c < used; c++) {
+    const float *p = partial + pl.base(row, c);
+    float w = p[0] == -INFINITY ? 0.0f : __expf(p[0] - gmax);
+    l += w * p[1];
+#pragma unroll
+    for (int i = 0; i < MAX_HD / 64; i++) {
+      int d = lane + 64 * i;
+      if (d < hd) acc[i] += w * p[2 + d];
+    }
+  }
+  float inv = 1.0f / l;
+#pragma unroll
+  for (int i = 0; i < MAX_HD / 64; i++) {
+    int d = lane + 64 * i;
+    if (d < hd) out[(int64_t)m * ldo + (int64_t)h * hd + d] = to_h(acc[i] * inv);
+  }
+}
+
+}  // namespace
+}  // namespace wg
+
+using namespace wg;
+
+extern "C" {
+
+int wg_head_prep(const float *qkv, int32_t M, int32_t ldq, const wg_attn_shape *sh,
+                 const float *q_norm, const float *k_norm, const float *rope, int32_t rope_rows,
+                 const int32_t *pos0, float *q_out, int32_t ldqo, uint16_t *k_cache,
+                 uint16_t *v_cache, int32_t ctx, void *stream) {
+  WG_REQUIRE(sh && qkv && rope && pos0 && q_out && k_cache && v_cache,
+             "wg_head_prep: null argument");
+  WG_REQUIRE(M >= 1 && M <= 65535, "wg_head_prep: %d rows", M);
+  WG_REQUIRE(sh->kv_heads > 0 && sh->heads % sh->kv_heads == 0,
+             "wg_head_prep: %d query heads over %d KV heads", sh->heads, sh->kv_heads);
+  WG_REQUIRE(sh->head_dim >= 2 && sh->head_dim <= MAX_HD && sh->head_dim % 2 == 0,
+             "wg_head_prep: head_dim %d", sh->head_dim);
+  WG_REQUIRE(sh->rotated_dims >= 0 && sh->rotated_dims <= sh->head_dim &&
+                 sh->rotated_dims % 2 == 0,
+             "wg_head_prep: rotated dims %d", sh->rotated_dims);
+  WG_REQUIRE(!sh->use_norm || (q_norm && k_norm), "wg_head_prep: norm weights missing");
+  WG_REQUIRE(ctx >= 1 && rope_rows >= 1024 + (ctx + 1023) / 1024,
+             "wg_head_prep: a rope table of %d rows for a %d-position cache (needs %d)",
+             rope_rows, ctx, 1024 + (ctx + 1023) / 1024);
+  int slots = sh->heads + 2 * sh->kv_heads;
+  WG_REQUIRE(ldq >= slots * sh->head_dim && ldqo >= sh->heads * sh->head_dim,
+             "wg_head_prep: strides too small");
+  head_prep_kernel<<<dim3(slots, M), 64, 0, as_stream(stream)>>>(
+      qkv, ldq, sh->heads, sh->kv_heads, sh->head_dim, sh->rotated_dims, sh->eps, sh->use_norm,
+      q_norm, k_norm, rope, rope_rows, pos0, q_out, ldqo, k_cache, v_cache, ctx);
+  return launched("wg_head_prep");
+}
+
+size_t wg_attn_scratch_bytes(int32_t M, int32_t heads, int32_t head_dim, int32_t max_keys) {
+  int64_t chunks = (max_keys + CHUNK - 1) / CHUNK;
+  return (size_t)M * heads * chunks * (head_dim + 2) * sizeof(float);
+}
+
+int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *sh,
+                   const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0,
+                   int32_t max_keys, uint16_t *out, int32_t ldo, void *scratch,
+                   size_t scratch_bytes, void *stream) {
+  WG_REQUIRE(sh && q && k_cache && v_cache && pos0 && out && scratch,
+             "wg_attn_decode: null argument");
+  int H = sh->heads, KV = sh->kv_heads, hd = sh->head_dim;
+  WG_REQUIRE(KV > 0 && H % KV == 0, "wg_attn_decode: %d query heads over %d KV heads", H, KV);
+  WG_REQUIRE(M >= 1 && (H / KV) * M <= 64,
+             "wg_attn_decode: %d rows x %d heads per KV head (at most 64)", M, H / KV);
+  WG_REQUIRE(hd == 64 || hd == 128, "wg_attn_decode: head_dim %d (64 or 128)", hd);
+  WG_REQUIRE(max_keys >= M, "wg_attn_decode: max_keys %d < rows %d", max_keys, M);
+  WG_REQUIRE(ldq >= H * hd && ldo >= H * hd, "wg_attn_decode: strides too small");
+  WG_REQUIRE(scratch_bytes >= wg_attn_scratch_bytes(M, H, hd, max_keys),
+             "wg_attn_decode: scratch of %zu bytes, %zu needed", scratch_bytes,
+             wg_attn_scratch_bytes(M, H, hd, max_keys));
+  int chunks = (max_keys + CHUNK - 1) / CHUNK;
+  hipStream_t s = as_stream(stream);
+  if (hd == 64)
+    attn_chunk_kernel<64><<<dim3(KV, chunks), 256, 0, s>>>(
+        q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, (float *)scratch, chunks);
+  else
+    attn_chunk_kernel<128><<<dim3(KV, chunks), 256, 0, s>>>(
+        q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, (float *)scratch, chunks);
+  int rc = launched("wg_attn_decode");
+  if (rc) return rc;
+  attn_combine_kernel<<<dim3(H, M), 64, 0, s>>>((const float *)scratch, M, H, hd, chunks, pos0,
+                                                max_keys, out, ldo);
+  return launched("wg_attn_decode (combine)");
+}
+
+}  // extern "C"

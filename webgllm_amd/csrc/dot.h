@@ -1,0 +1,56 @@
+// Nibble dot products on gfx950 without MFMA: two 4-bit weights become two
+// fp16 subnormals (q * 2^-24, or 16 q * 2^-24 for a high nibble) in one
+// dword, and v_dot2_f32_f16 multiplies them by two half activations with
+// float32 accumulation. Every product is exact; the 2^-24 (and 1/16) is
+// taken out again once per block.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wg {
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ inline half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+
+__device__ inline float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+}
+
+// v_perm_b32 selectors: bytes 0 and 1 of a dword into the low byte of each
+// half (the other bytes zero); bytes 2 and 3 likewise.
+constexpr uint32_t SEL01 = 0x0c010c00u;
+constexpr uint32_t SEL23 = 0x0c030c02u;
+constexpr uint32_t LO4 = 0x000f000fu;
+constexpr uint32_t HI4 = 0x00f000f0u;
+constexpr uint32_t ONES = 0x3c003c00u;  // (1.0h, 1.0h)
+
+// One dword of nibble bytes (weights k..k+3 low, and their partners high)
+// as 4 subnormal pairs: lo0 = (q_k, q_k+1), lo1 = (q_k+2, q_k+3) and the
+// high nibbles' pairs hi0, hi1 (times 16).
+struct NibblePairs {
+  uint32_t lo0, lo1, hi0, hi1;
+};
+
+__device__ inline NibblePairs split_nibbles(uint32_t w) {
+  uint32_t p0 = __builtin_amdgcn_perm(0u, w, SEL01);
+  uint32_t p1 = __builtin_amdgcn_perm(0u, w, SEL23);
+  return {p0 & LO4, p1 & LO4, p0 & HI4, p1 & HI4};
+}
+
+// Sum of 8 halves held as 4 dwords.
+__device__ inline float sum8(const uint4 &a, float acc) {
+  acc = dot2(a.x, ONES, acc);
+  acc = dot2(a.y, ONES, acc);
+  acc = dot2(a.z, ONES, acc);
+  return dot2(a.w, ONES, acc);
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace wg

@@ -21,24 +21,11 @@
 //    epilogue;
 //  - a butterfly over the 64 lanes reduces the 4 rows x M tokens.
 #include "common.h"
+#include "dot.h"
+#include "kernels.h"
 
 namespace wg {
 namespace {
-
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-
-__device__ inline half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
-
-__device__ inline float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
-}
-
-// Bytes 0 and 1 of w into the low byte of each half; bytes 2 and 3.
-constexpr uint32_t SEL01 = 0x0c010c00u;
-constexpr uint32_t SEL23 = 0x0c030c02u;
-constexpr uint32_t LO4 = 0x000f000fu;
-constexpr uint32_t HI4 = 0x00f000f0u;
-constexpr uint32_t ONES = 0x3c003c00u;  // (1.0h, 1.0h)
 
 // The 16 fp16-subnormal nibble pairs of one 16-byte block row, in the
 // order the activation pairs come: for word w, (q[4w], q[4w+1]) and
@@ -106,11 +93,6 @@ __device__ inline void load_zeros(const void *zeros, int64_t si, float z[4]) {
   }
 }
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
 
 template <int M, int ZK>
 __global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
@@ -237,9 +219,8 @@ int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx,
   }
   WG_REQUIRE(!overlaps(x, (size_t)M * ldx * 2, y, (size_t)M * ldy * 4),
              "wg_q4_gemv: activations and output overlap");
-  if (w->layout != WG_LAYOUT_ROWGROUP)
-    return fail(WG_ERR_UNSUPPORTED, "wg_q4_gemv: layout %d not built yet", w->layout);
   hipStream_t s = as_stream(stream);
+  if (w->layout == WG_LAYOUT_Q4K) return launch_gemv_q4k(w, x, M, ldx, y, ldy, ep, s);
   switch (M) {
     case 1: return launch_gemv_m<1>(w, x, ldx, y, ldy, ep, s);
     case 2: return launch_gemv_m<2>(w, x, ldx, y, ldy, ep, s);

@@ -1,0 +1,174 @@
+// Residual-stream glue between the matmuls: RMS norm into half activations,
+// SwiGLU, and the embedding lookup (the reference's RMS_SCALE / NORM_TO_H2,
+// REDUCE_SWIGLU and embed kernels, src/gpu/kernels.ts:1195-1264,
+// :1066-1077, :1092-1149). Half outputs are clamped to +-65504 as packH2
+// does (kernels.ts:32-36).
+#include "common.h"
+#include "dot.h"
+
+namespace wg {
+namespace {
+
+__device__ inline uint16_t to_h(float v) {
+  v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+  return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// Block-wide sum over 256 threads (4 waves).
+__device__ inline float block_sum256(float v, float *lds) {
+  v = wave_sum(v);
+  int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) lds[w] = v;
+  __syncthreads();
+  float t = lds[0] + lds[1] + lds[2] + lds[3];
+  __syncthreads();
+  return t;
+}
+
+// One workgroup per row: 1 / sqrt(mean x^2 + eps), then half(x * w * r).
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, int D, int ldx,
+                                                       const float *w, float eps, uint16_t *out,
+                                                       int ldo, float *rs_out) {
+  __shared__ float lds[4];
+  const float *xr = x + (int64_t)blockIdx.x * ldx;
+  float s = 0.0f;
+  for (int i = threadIdx.x * 4; i < D; i += 1024) {
+    float4 v = *reinterpret_cast<const float4 *>(xr + i);
+    s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  float r = 1.0f / sqrtf(block_sum256(s, lds) / (float)D + eps);
+  if (rs_out && threadIdx.x == 0) rs_out[blockIdx.x] = r;
+  uint16_t *o = out + (int64_t)blockIdx.x * ldo;
+  for (int i = threadIdx.x * 4; i < D; i += 1024) {
+    float4 v = *reinterpret_cast<const float4 *>(xr + i);
+    float4 g = *reinterpret_cast<const float4 *>(w + i);
+    ushort4 h;
+    h.x = to_h(v.x * r * g.x);
+    h.y = to_h(v.y * r * g.y);
+    h.z = to_h(v.z * r * g.z);
+    h.w = to_h(v.w * r * g.w);
+    *reinterpret_cast<ushort4 *>(o + i) = h;
+  }
+}
+
+// out[m][i] = half(silu(gu[m][i]) * gu[m][F + i]).
+__global__ void swiglu_kernel(const float *gu, int M, int F, int ldg, uint16_t *out, int ldo) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)M * F) return;
+  int m = (int)(t / F), i = (int)(t % F);
+  float g = gu[(int64_t)m * ldg + i], u = gu[(int64_t)m * ldg + F + i];
+  out[(int64_t)m * ldo + i] = to_h(g / (1.0f + __expf(-g)) * u);
+}
+
+// Embedding rows of a ROWGROUP matrix: thread = (token m, block b).
+__global__ void embed_rowgroup_kernel(const uint32_t *quants, const uint16_t *scales,
+                                      const void *zeros, int zero_kind, const int32_t *ids,
+                                      int M, int blocks, int N, float *h, int ldh) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)M * blocks) return;
+  int m = (int)(t / blocks), b = (int)(t % blocks);
+  int n = ids[m];
+  float *o = h + (int64_t)m * ldh + b * 32;
+  if (n < 0 || n >= N) {  // an id outside the vocabulary embeds as zeros
+    for (int j = 0; j < 32; j++) o[j] = 0.0f;
+    return;
+  }
+  int64_t si = ((int64_t)(n >> 2) * blocks + b) * 4 + (n & 3);
+  double d = half_to_float(scales[si]);
+  double z = zero_kind == WG_ZERO_U8    ? (double)((const uint8_t *)zeros)[si]
+             : zero_kind == WG_ZERO_F16 ? (double)half_to_float(((const uint16_t *)zeros)[si])
+                                        : 8.0;
+  uint4 q = reinterpret_cast<const uint4 *>(quants)[si];
+  uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    uint32_t byte = (w[j >> 2] >> (8 * (j & 3))) & 0xffu;
+    o[j] = (float)(d * ((double)(byte & 15u) - z));
+    o[j + 16] = (float)(d * ((double)(byte >> 4) - z));
+  }
+}
+
+// Embedding rows of a Q4_K matrix: thread = (token m, super-block s,
+// sub-block j), with packQ4_K's (d', z') chain (src/repack.ts:100-168).
+__global__ void embed_q4k_kernel(const uint8_t *quants, const int32_t *ids, int M, int supers,
+                                 int N, float *h, int ldh) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)M * supers * 8) return;
+  int j = (int)(t & 7);
+  int64_t ms = t >> 3;
+  int m = (int)(ms / supers), s = (int)(ms % supers);
+  int n = ids[m];
+  float *o = h + (int64_t)m * ldh + s * 256 + j * 32;
+  if (n < 0 || n >= N) {
+    for (int l = 0; l < 32; l++) o[l] = 0.0f;
+    return;
+  }
+  const uint8_t *p = quants + (((int64_t)(n >> 2) * supers + s) * 4 + (n & 3)) * 144;
+  double d = half_to_float((uint16_t)(p[0] | (p[1] << 8)));
+  double dmin = half_to_float((uint16_t)(p[2] | (p[3] << 8)));
+  int sc, mn;
+  q4k_scale_min(p + 4, j, &sc, &mn);
+  uint16_t hq = double_to_half_ref(d * sc);
+  double mins = dmin * mn;
+  bool constant = half_to_float(hq) == 0.0f;
+  double scale = constant ? half_to_float(double_to_half_ref(-mins / 15.0)) : half_to_float(hq);
+  double zero = constant ? 0.0 : half_to_float(double_to_half_ref(mins / scale));
+  const uint8_t *q = p + 16 + (j >> 1) * 32;
+  for (int l = 0; l < 32; l++) {
+    int nib = constant ? 15 : (j & 1) ? q[l] >> 4 : q[l] & 15;
+    o[l] = (float)(scale * ((double)nib - zero));
+  }
+}
+
+}  // namespace
+}  // namespace wg
+
+using namespace wg;
+
+extern "C" {
+
+int wg_rms_norm(const float *x, int32_t M, int32_t D, int32_t ldx, const float *w, float eps,
+                uint16_t *out, int32_t ldo, float *rs_out, void *stream) {
+  WG_REQUIRE(x && w && out, "wg_rms_norm: null argument");
+  WG_REQUIRE(M >= 1 && D >= 4 && D % 4 == 0, "wg_rms_norm: %d rows of %d (a multiple of 4)", M,
+             D);
+  WG_REQUIRE(ldx >= D && ldx % 4 == 0 && ldo >= D && ldo % 4 == 0,
+             "wg_rms_norm: strides %d, %d for rows of %d", ldx, ldo, D);
+  WG_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)out & 7) == 0,
+             "wg_rms_norm: misaligned buffers");
+  rms_norm_kernel<<<M, 256, 0, as_stream(stream)>>>(x, D, ldx, w, eps, out, ldo, rs_out);
+  return launched("wg_rms_norm");
+}
+
+int wg_swiglu(const float *gu, int32_t M, int32_t F, int32_t ldg, uint16_t *out, int32_t ldo,
+              void *stream) {
+  WG_REQUIRE(gu && out, "wg_swiglu: null argument");
+  WG_REQUIRE(M >= 1 && F >= 1 && ldg >= 2 * F && ldo >= F, "wg_swiglu: bad shape");
+  int64_t n = (int64_t)M * F;
+  swiglu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, as_stream(stream)>>>(gu, M, F, ldg, out,
+                                                                            ldo);
+  return launched("wg_swiglu");
+}
+
+int wg_embed(const wg_q4_matrix *emb, const int32_t *ids, int32_t M, float *h, int32_t ldh,
+             void *stream) {
+  int rc = check_matrix(emb, "wg_embed");
+  if (rc) return rc;
+  WG_REQUIRE(ids && h && M >= 1 && ldh >= emb->K, "wg_embed: bad arguments");
+  hipStream_t s = as_stream(stream);
+  if (emb->layout == WG_LAYOUT_ROWGROUP) {
+    int blocks = emb->K / 32;
+    int64_t n = (int64_t)M * blocks;
+    embed_rowgroup_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+        (const uint32_t *)emb->quants, (const uint16_t *)emb->scales, emb->zeros, emb->zero, ids,
+        M, blocks, emb->N, h, ldh);
+  } else {
+    int supers = emb->K / 256;
+    int64_t n = (int64_t)M * supers * 8;
+    embed_q4k_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+        (const uint8_t *)emb->quants, ids, M, supers, emb->N, h, ldh);
+  }
+  return launched("wg_embed");
+}
+
+}  // extern "C"

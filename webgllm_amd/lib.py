@@ -41,6 +41,11 @@ class Epilogue(C.Structure):
                 ("row_scale", C.c_void_p)]
 
 
+class AttnShape(C.Structure):
+    _fields_ = [("heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
+                ("rotated_dims", C.c_int32), ("eps", C.c_float), ("use_norm", C.c_int32)]
+
+
 class Limits(C.Structure):
     _fields_ = [("device", C.c_int32), ("compute_units", C.c_int32),
                 ("global_bytes", C.c_int64), ("max_alloc_bytes", C.c_int64),
@@ -98,6 +103,18 @@ def load():
         "wg_q4_gemv": (C.c_int, [C.POINTER(Q4MatrixDesc), P, I32, I32, P, I32,
                                  C.POINTER(Epilogue), P]),
         "wg_f32_to_f16": (C.c_int, [P, P, I64, P]),
+        "wg_rms_norm": (C.c_int, [P, I32, I32, I32, P, C.c_float, P, I32, P, P]),
+        "wg_swiglu": (C.c_int, [P, I32, I32, I32, P, I32, P]),
+        "wg_embed": (C.c_int, [C.POINTER(Q4MatrixDesc), P, I32, P, I32, P]),
+        "wg_head_prep": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32, P, P, I32,
+                                   P, P, I32, P]),
+        "wg_attn_scratch_bytes": (SZ, [I32, I32, I32, I32]),
+        "wg_attn_decode": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32, P, I32,
+                                     P, SZ, P]),
+        "wg_short_conv": (C.c_int, [P, I32, I32, I32, I32, P, P, P, P, P, I32, P]),
+        "wg_conv_accept": (C.c_int, [P, I32, I32, I32, I32, P, P]),
+        "wg_argmax_scratch_bytes": (SZ, [I32, I32]),
+        "wg_argmax_rows": (C.c_int, [P, I32, I32, I32, P, P, P, SZ, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -138,3 +138,106 @@ def f32_to_f16(x: torch.Tensor) -> torch.Tensor:
     out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
     L.check(L.load().wg_f32_to_f16(_p(x), _p(out), x.numel(), _stream()))
     return out
+
+
+def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | None = None,
+             rs_out: torch.Tensor | None = None) -> torch.Tensor:
+    """half(x * w / rms(x)) per row of x [M, D] (float32)."""
+    x = _dev(x, torch.float32)
+    M, D = (x.shape[0], x.shape[1]) if x.dim() == 2 else (1, x.shape[0])
+    if out is None:
+        out = torch.empty((M, D), dtype=torch.float16, device=x.device)
+    L.check(L.load().wg_rms_norm(_p(x), M, D, x.shape[-1], _p(_dev(w, torch.float32)), eps,
+                                 _p(out), out.shape[-1], _p(rs_out), _stream()))
+    return out
+
+
+def swiglu(gu: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """half(silu(gate) * up) from [M, 2F] (gate columns first)."""
+    gu = _dev(gu, torch.float32)
+    M, F = gu.shape[0], gu.shape[1] // 2
+    if out is None:
+        out = torch.empty((M, F), dtype=torch.float16, device=gu.device)
+    L.check(L.load().wg_swiglu(_p(gu), M, F, gu.shape[1], _p(out), out.shape[-1], _stream()))
+    return out
+
+
+def embed(m: "Q4Matrix", ids: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    ids = _dev(ids, torch.int32)
+    M = ids.numel()
+    if out is None:
+        out = torch.empty((M, m.K), dtype=torch.float32, device=ids.device)
+    L.check(L.load().wg_embed(C.byref(m.desc), _p(ids), M, _p(out), out.shape[-1], _stream()))
+    return out
+
+
+def attn_shape(heads, kv_heads, head_dim, rotated_dims=None, eps=1e-6, use_norm=False):
+    return L.AttnShape(heads, kv_heads, head_dim,
+                       head_dim if rotated_dims is None else rotated_dims, eps, int(use_norm))
+
+
+def head_prep(qkv: torch.Tensor, shape, rope: torch.Tensor, pos0: torch.Tensor,
+              k_cache: torch.Tensor, v_cache: torch.Tensor, q_norm=None, k_norm=None,
+              q_out: torch.Tensor | None = None) -> torch.Tensor:
+    qkv = _dev(qkv, torch.float32)
+    M = qkv.shape[0]
+    qd = shape.heads * shape.head_dim
+    if q_out is None:
+        q_out = torch.empty((M, qd), dtype=torch.float32, device=qkv.device)
+    L.check(L.load().wg_head_prep(_p(qkv), M, qkv.shape[1], C.byref(shape), _p(q_norm),
+                                  _p(k_norm), _p(_dev(rope, torch.float32)), rope.shape[0],
+                                  _p(_dev(pos0, torch.int32)), _p(q_out), q_out.shape[1],
+                                  _p(k_cache), _p(v_cache), k_cache.shape[0], _stream()))
+    return q_out
+
+
+def attn_scratch(M, shape, max_keys, device="cuda") -> torch.Tensor:
+    n = L.load().wg_attn_scratch_bytes(M, shape.heads, shape.head_dim, max_keys)
+    return torch.empty(max(n, 4), dtype=torch.uint8, device=device)
+
+
+def attn_decode(q: torch.Tensor, shape, k_cache, v_cache, pos0: torch.Tensor,
+                scratch: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    q = _dev(q, torch.float32)
+    M = q.shape[0]
+    max_keys = k_cache.shape[0]
+    if scratch is None:
+        scratch = attn_scratch(M, shape, max_keys, q.device)
+    if out is None:
+        out = torch.empty((M, shape.heads * shape.head_dim), dtype=torch.float16,
+                          device=q.device)
+    L.check(L.load().wg_attn_decode(_p(q), M, q.shape[1], C.byref(shape), _p(k_cache),
+                                    _p(v_cache), _p(_dev(pos0, torch.int32)), max_keys, _p(out),
+                                    out.shape[1], _p(scratch), scratch.numel(), _stream()))
+    return out
+
+
+def short_conv(bcx, D, W, taps, state, state_out=None, prefixes=None, out=None):
+    bcx = _dev(bcx, torch.float32)
+    M = bcx.shape[0]
+    if out is None:
+        out = torch.empty((M, D), dtype=torch.float16, device=bcx.device)
+    if state_out is None:
+        state_out = state
+    L.check(L.load().wg_short_conv(_p(bcx), M, D, bcx.shape[1], W, _p(_dev(taps)), _p(state),
+                                   _p(state_out), _p(prefixes), _p(out), out.shape[1],
+                                   _stream()))
+    return out
+
+
+def conv_accept(prefixes, kept, rows, D, W, state):
+    L.check(L.load().wg_conv_accept(_p(prefixes), kept, rows, D, W, _p(state), _stream()))
+
+
+def argmax_rows(logits: torch.Tensor, V: int | None = None, ids=None, tops=None, scratch=None):
+    logits = _dev(logits, torch.float32)
+    M = logits.shape[0]
+    V = logits.shape[1] if V is None else V
+    if ids is None:
+        ids = torch.empty(M, dtype=torch.int32, device=logits.device)
+    if scratch is None:
+        scratch = torch.empty(L.load().wg_argmax_scratch_bytes(M, V), dtype=torch.uint8,
+                              device=logits.device)
+    L.check(L.load().wg_argmax_rows(_p(logits), M, V, logits.shape[1], _p(ids), _p(tops),
+                                    _p(scratch), scratch.numel(), _stream()))
+    return ids
