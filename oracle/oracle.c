@@ -249,6 +249,16 @@ void orc_matrix_row(const orc_qm *m, int n, float *out) {
   }
 }
 
+/* Every row of a matrix as orc_matrix_row gives it (rows in parallel). */
+void orc_matrix_dense(const orc_qm *m, float *out, int threads) {
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+#endif
+  for (int n = 0; n < m->N; n++) orc_matrix_row(m, n, out + (size_t)n * m->K);
+  (void)threads;
+}
+
 /* src/repack.ts:474-511 (ggml's dequantize_row_q4_K as the reference
  * states it): w = d * sc * q - dmin * m, in doubles, stored as float32. */
 void orc_dequantize_q4_k(const uint8_t *src, int rows, int K, float *out) {

@@ -53,6 +53,7 @@ int orc_pack_nbits_scales(orc_qm *m, int row0, const uint8_t *scale_bytes, const
                           int rows);                              /* repack.ts:312-337 */
 void orc_quants_from_raw(const uint8_t *raw, int N, int K, uint32_t *out); /* repack.ts:216-245 */
 void orc_matrix_row(const orc_qm *m, int n, float *out);          /* repack.ts:865-891 */
+void orc_matrix_dense(const orc_qm *m, float *out, int threads);
 void orc_dequantize_q4_k(const uint8_t *src, int rows, int K, float *out); /* repack.ts:474-511 */
 void orc_dequantize_nbits_row(int K, const uint8_t *quant, const uint8_t *scales,
                               const uint8_t *zp, int n, float *out); /* load-onnx.ts:471-501 */

@@ -52,6 +52,7 @@ _lib.orc_pack_nbits.argtypes = [C.POINTER(_QM), _I, _P, _P, _P, _I, _P]
 _lib.orc_pack_nbits_scales.argtypes = [C.POINTER(_QM), _I, _P, _P, _I]
 _lib.orc_quants_from_raw.argtypes = [_P, _I, _I, _P]
 _lib.orc_matrix_row.argtypes = [C.POINTER(_QM), _I, _P]
+_lib.orc_matrix_dense.argtypes = [C.POINTER(_QM), _P, _I]
 _lib.orc_dequantize_q4_k.argtypes = [_P, _I, _I, _P]
 _lib.orc_dequantize_nbits_row.argtypes = [_I, _P, _P, _P, _I, _P]
 _lib.orc_quantize_q4_0.argtypes = [_P, _I, _I, _P]
@@ -119,8 +120,10 @@ class QuantMatrix:
         _lib.orc_matrix_row(C.byref(self._c()), n, _ptr(out))
         return out
 
-    def dense(self) -> np.ndarray:
-        return np.stack([self.row(n) for n in range(self.N)])
+    def dense(self, threads: int = 0) -> np.ndarray:
+        out = np.empty((self.N, self.K), dtype=np.float32)
+        _lib.orc_matrix_dense(C.byref(self._c()), _ptr(out), threads)
+        return out
 
 
 def _rows(src_rows):

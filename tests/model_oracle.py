@@ -1,0 +1,132 @@
+"""A CPU decoder over the oracle's primitives, for end-to-end parity of the
+engine (test infrastructure). It reads the engine's device weights back to
+the host, dequantizes them with the oracle's matrixRow (src/repack.ts:865-891;
+Q4_K through packQ4_K, :100-168) and runs the reference's forward
+(src/engine.ts:8875-9303) in float64 matmuls with the reference's fp16
+rounding points: activations into matmuls (packH2, src/gpu/kernels.ts:32-36),
+keys and values in the cache, attention and SwiGLU outputs."""
+import math
+
+import numpy as np
+
+from oracle import oracle as O
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def dense_of(m, threads=0) -> np.ndarray:
+    """The oracle's float32 weights of an ops.Q4Matrix."""
+    from webgllm_amd import lib as L
+    N, K = m.N, m.K
+    if m.layout == L.LAYOUT_Q4K:
+        G, S = N // 4, K // 256
+        rec = _np(m.quants).reshape(G, S, 4, 144)
+        src = np.ascontiguousarray(rec.transpose(0, 2, 1, 3)).reshape(-1)
+        qm = O.QuantMatrix(N, K, "halves")
+        O.pack_q4_k(qm, 0, src, N)
+        return qm.dense(threads)
+    qm = O.QuantMatrix(N, K, {L.ZERO_8: False, L.ZERO_U8: True, L.ZERO_F16: "halves"}[m.zero])
+    qm.quants[:] = _np(m.quants).view(np.uint32)
+    qm.scales[:] = _np(m.scales).view(np.uint16)
+    if m.zero == L.ZERO_U8:
+        qm.zeros[:] = _np(m.zeros)
+    elif m.zero == L.ZERO_F16:
+        qm.zero_halves[:] = _np(m.zeros).view(np.uint16)
+    return qm.dense(threads)
+
+
+def h16(x):
+    """Through halves and back (clamped to +-65504)."""
+    return O.halves_to_f32(O.f32_to_h2(np.asarray(x, np.float32)))
+
+
+class OracleModel:
+    def __init__(self, weights, ctx):
+        s = self.s = weights.shape
+        self.ctx = ctx
+        # float64 copies of the dequantized weights, made once
+        self.emb = dense_of(weights.embedding).astype(np.float64)
+        self.final = _np(weights.final_norm)
+        self.layers = []
+        for i, lw in enumerate(weights.layers):
+            d = {k: (dense_of(v).astype(np.float64) if hasattr(v, "desc") else _np(v))
+                 for k, v in lw.items()}
+            self.layers.append(d)
+        self.rope = O.rope_table(s.rope_theta, s.head_dim, s.head_dim, ctx)
+        self.reset()
+
+    def reset(self):
+        s = self.s
+        kvd = s.kv_heads * s.head_dim
+        self.k = {i: np.zeros((self.ctx, kvd), np.uint16) for i in range(s.layers)
+                  if s.layer_type(i) == "attn"}
+        self.v = {i: np.zeros((self.ctx, kvd), np.uint16) for i in range(s.layers)
+                  if s.layer_type(i) == "attn"}
+        self.state = {i: np.zeros((s.conv_kernel - 1, s.hidden), np.float32)
+                      for i in range(s.layers) if s.layer_type(i) == "conv"}
+        self.position = 0
+
+    @staticmethod
+    def _mm(x, w):
+        return (x.astype(np.float64) @ w.T).astype(np.float32)
+
+    def forward_rows(self, ids):
+        """One batch; returns (logits [M, V], picks [M])."""
+        s = self.s
+        M = len(ids)
+        pos0 = self.position
+        hd = s.head_dim
+        h = self.emb[np.asarray(ids)].astype(np.float32)
+        for i, lw in enumerate(self.layers):
+            x = h16(O.rms_norm(h, lw["op_norm"], s.eps))
+            if s.layer_type(i) == "conv":
+                bcx = self._mm(x, lw["in_proj"])
+                out, st = O.short_conv(bcx, s.hidden, s.conv_kernel, lw["taps"], self.state[i])
+                self.state[i] = st
+                h = h + self._mm(h16(out), lw["out_proj"])
+            else:
+                qkv = self._mm(x, lw["qkv"])
+                att = np.zeros((M, s.heads * hd), np.float32)
+                qd = s.heads * hd
+                kvd = s.kv_heads * hd
+                for m in range(M):
+                    pos = pos0 + m
+                    q = np.concatenate([
+                        O.head_prep(qkv[m, h_ * hd:(h_ + 1) * hd], lw.get("q_norm"), self.rope, hd,
+                                    hd, pos, s.eps, 1 / math.sqrt(hd), s.qk_norm)
+                        for h_ in range(s.heads)])
+                    for kh in range(s.kv_heads):
+                        kx = qkv[m, qd + kh * hd:qd + (kh + 1) * hd]
+                        self.k[i][pos, kh * hd:(kh + 1) * hd] = O.f32_to_h2(
+                            O.head_prep(kx, lw.get("k_norm"), self.rope, hd, hd, pos, s.eps, 1.0,
+                                        s.qk_norm))
+                        vx = qkv[m, qd + kvd + kh * hd:qd + kvd + (kh + 1) * hd]
+                        self.v[i][pos, kh * hd:(kh + 1) * hd] = O.f32_to_h2(vx)
+                    a = O.attention_f64(q, self.k[i], self.v[i], s.heads, s.kv_heads, hd,
+                                        pos + 1, kvd)
+                    att[m] = h16(a)
+                h = h + self._mm(att, lw["o"])
+            x = h16(O.rms_norm(h, lw["ffn_norm"], s.eps))
+            gu = self._mm(x, lw["gate_up"])
+            h = h + self._mm(h16(O.swiglu(gu)), lw["down"])
+        x = h16(O.rms_norm(h, self.final, s.eps))
+        logits = self._mm(x, self.emb)
+        picks = [O.argmax(logits[m])[0] for m in range(M)]
+        self.position += M
+        return logits, picks
+
+    def forward(self, tokens):
+        logits = picks = None
+        for b0 in range(0, len(tokens), 8):
+            logits, picks = self.forward_rows(tokens[b0:b0 + 8])
+        return logits, picks
+
+    def decode(self, first, steps):
+        out, t = [], first
+        for _ in range(steps):
+            _, p = self.forward_rows([t])
+            t = p[0]
+            out.append(t)
+        return out

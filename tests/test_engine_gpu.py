@@ -1,0 +1,142 @@
+"""End-to-end decode and speculative verify through the HIP kernels against
+the CPU decoder over the oracle: identical greedy tokens, logits within
+rel-L2 1e-3 (the north star's bar)."""
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import rel_l2
+from tests.model_oracle import OracleModel
+
+pytestmark = pytest.mark.gpu
+
+
+def _shape(fmt, conv_layers=(), qk_norm=False, layers=3, hidden=256, heads=4, kv=2, hd=64,
+           inter=512, vocab=1024):
+    from webgllm_amd.engine import ModelShape
+    return ModelShape(f"tiny-{fmt}", hidden, layers, heads, kv, hd, inter, vocab, fmt,
+                      qk_norm=qk_norm, conv_layers=conv_layers)
+
+
+FAMILIES = {
+    "llama-q4_k": dict(fmt="q4_k"),
+    "qwen-nbits": dict(fmt="nbits", heads=7, kv=1),
+    "lfm2-q4_0": dict(fmt="q4_0", conv_layers=(0, 2), qk_norm=True),
+    "q4_k-rowgroup": dict(fmt="q4_k_rowgroup"),
+}
+
+
+def _pair(family, seed=0, ctx=256, **kw):
+    from webgllm_amd.engine import Engine, Weights
+    args = dict(FAMILIES[family])
+    args.update(kw)
+    w = Weights(_shape(**args), seed=seed)
+    return Engine(w, ctx), OracleModel(w, ctx)
+
+
+def _prompt(rng, n, vocab):
+    return [int(t) for t in rng.integers(0, vocab, n)]
+
+
+@pytest.mark.parametrize("family", list(FAMILIES))
+def test_prompt_logits_and_greedy_decode(hip, family):
+    eng, orc = _pair(family)
+    rng = np.random.default_rng(1)
+    prompt = _prompt(rng, 21, eng.shape.vocab)
+    picks = eng.forward(prompt).cpu().numpy()
+    logits_o, picks_o = orc.forward(prompt)
+    got = eng.logits[:len(prompt) % 8 or 8].cpu().numpy()
+    assert rel_l2(got, logits_o) <= 1e-3
+    assert list(picks) == list(picks_o)
+    # greedy decode by graph replay
+    first = int(picks[-1])
+    toks = eng.decode(first, 12)
+    toks_o = orc.decode(first, 12)
+    assert toks == toks_o
+
+
+@pytest.mark.parametrize("family", ["lfm2-q4_0", "llama-q4_k"])
+def test_verify_accept_matches_sequential(hip, family):
+    """A token and 4 drafts in one batch, keeping the agreeing prefix + 1
+    (src/handler.ts:1811-1887, Engine.accept src/engine.ts:8063-8086): the
+    tokens written equal sequential greedy decoding."""
+    eng, orc = _pair(family, seed=3)
+    rng = np.random.default_rng(5)
+    prompt = _prompt(rng, 10, eng.shape.vocab)
+    token = int(eng.forward(prompt).cpu().numpy()[-1])
+    seq = orc.forward(prompt)[1][-1]
+    assert token == seq
+    want = orc.decode(token, 12)
+    written = []
+    while len(written) < 10:
+        # drafts: the true continuation for the first k, then random ids
+        k = len(written) % 3
+        truth = want[len(written):len(written) + 4]
+        drafts = truth[:k] + [int(x) for x in rng.integers(0, eng.shape.vocab, 4 - k)]
+        rows = eng.forward([token] + drafts, draft=True).cpu().numpy()
+        kept = 1
+        for i in range(4):
+            if rows[i] != drafts[i]:
+                break
+            kept += 1
+        eng.accept(kept)
+        new = [int(x) for x in rows[:kept]]
+        written += new
+        token = new[-1]
+    assert written[:10] == want[:10]
+
+
+def test_graph_replay_equals_eager(hip):
+    eng, _ = _pair("lfm2-q4_0", seed=7)
+    rng = np.random.default_rng(9)
+    prompt = _prompt(rng, 9, eng.shape.vocab)
+    first = int(eng.forward(prompt).cpu().numpy()[-1])
+    p = eng.position
+    toks_graph = eng.decode(first, 8)
+    # eager replay of the same steps from the same state
+    eng2, _ = _pair("lfm2-q4_0", seed=7)
+    eng2.forward(prompt)
+    t, eager = first, []
+    for _ in range(8):
+        t = int(eng2.forward([t]).cpu().numpy()[0])
+        eager.append(t)
+    assert eng.position == p + 8
+    assert toks_graph == eager
+
+
+def test_engine_errors(hip):
+    eng, _ = _pair("llama-q4_k", ctx=32)
+    with pytest.raises(ValueError, match="cache holds"):
+        eng.forward(list(range(33)))
+    with pytest.raises(ValueError, match="8 tokens at most"):
+        eng.forward(list(range(9)), draft=True)
+    with pytest.raises(ValueError, match="No draft batch"):
+        eng.accept(1)
+    eng.forward([1, 2, 3], draft=True)
+    with pytest.raises(ValueError, match="keep 4 of a 3"):
+        eng.accept(4)
+
+
+@pytest.mark.parametrize("name,layers", [("qwen2", 2), ("llama3", 2), ("lfm2", 3)])
+def test_full_width_shapes(hip, name, layers):
+    """The workloads' real widths, heads and vocabularies (fewer layers, so
+    the CPU decoder stays quick): identical greedy tokens."""
+    from webgllm_amd import engine as E
+    import dataclasses
+    base = {"qwen2": E.QWEN2_05B, "llama3": E.LLAMA3_8B, "lfm2": E.LFM2_12B}[name]
+    conv = tuple(i for i in base.conv_layers if i < layers)
+    if name == "lfm2":
+        conv = (0, 2)
+    shape = dataclasses.replace(base, layers=layers, conv_layers=conv)
+    w = E.Weights(shape, seed=11)
+    ctx = 128
+    eng, orc = E.Engine(w, ctx), OracleModel(w, ctx)
+    rng = np.random.default_rng(2)
+    prompt = _prompt(rng, 12, shape.vocab)
+    picks = eng.forward(prompt).cpu().numpy()
+    logits_o, picks_o = orc.forward(prompt)
+    got = eng.logits[:4].cpu().numpy()
+    assert rel_l2(got, logits_o) <= 1e-3
+    assert list(picks) == list(picks_o)
+    first = int(picks[-1])
+    assert eng.decode(first, 4) == orc.decode(first, 4)

@@ -1,0 +1,321 @@
+"""The decode/verify hot path driven through the HIP kernels: the host-side
+mirror of the reference's Engine forward, argmax and accept
+(src/engine.ts:7900-8086, forwardBatch :8875-9303, argmax :8271-8336).
+
+One batch of M <= 8 rows (a token, or a token and its drafts) runs as:
+embedding -> per layer [RMS norm -> operator (attention or short conv) ->
+residual add (in the projection's epilogue) -> RMS norm -> gate|up -> SwiGLU
+-> down (+ residual)] -> final norm -> head -> greedy pick. The position
+lives on the device, so a single-token step is captured once as a HIP graph
+and replayed for every token with no host work between kernels.
+
+Weights are random (the reference's speed probe does the same,
+src/speed-probe.ts:258-499) and generated on the device.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from . import lib as L
+from . import ops
+
+MAX_ROWS = 8
+
+
+@dataclass
+class ModelShape:
+    name: str
+    hidden: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    intermediate: int
+    vocab: int
+    fmt: str  # "q4_0" | "nbits" | "q4_k" (native super-blocks) | "q4_k_rowgroup"
+    rope_theta: float = 1e6
+    eps: float = 1e-5
+    qk_norm: bool = False
+    conv_kernel: int = 3
+    # layer i is "conv" when listed here, else attention
+    conv_layers: tuple = ()
+    extra: dict = field(default_factory=dict)
+
+    def layer_type(self, i: int) -> str:
+        return "conv" if i in self.conv_layers else "attn"
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+
+# The workloads' shapes.
+QWEN2_05B = ModelShape("qwen2-0.5b-shape", 896, 24, 14, 2, 64, 4864, 151936, "nbits",
+                       rope_theta=1e6, eps=1e-6)
+LLAMA3_8B = ModelShape("llama3-8b-shape", 4096, 32, 32, 8, 128, 14336, 128256, "q4_k",
+                       rope_theta=5e5, eps=1e-5)
+LFM2_12B = ModelShape("lfm2-1.2b-shape", 2048, 16, 32, 8, 64, 8192, 65536, "q4_0",
+                      rope_theta=1e6, eps=1e-5, qk_norm=True, conv_kernel=3,
+                      conv_layers=(0, 1, 3, 4, 6, 7, 9, 11, 13, 15))
+
+
+class Weights:
+    """Random quantized weights of one model shape, generated on the device."""
+
+    def __init__(self, shape: ModelShape, seed: int = 0, device="cuda"):
+        self.shape = shape
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        self.g = g
+        self.device = device
+        s = shape
+        D = s.hidden
+        self.embedding = self.matrix(s.vocab, D)
+        self.final_norm = self.norm(D)
+        self.layers = []
+        for i in range(s.layers):
+            lw = {"op_norm": self.norm(D), "ffn_norm": self.norm(D),
+                  "gate_up": self.matrix(2 * s.intermediate, D),
+                  "down": self.matrix(D, s.intermediate)}
+            if s.layer_type(i) == "conv":
+                lw["in_proj"] = self.matrix(3 * D, D)
+                lw["out_proj"] = self.matrix(D, D)
+                lw["taps"] = (torch.randn((D, s.conv_kernel), generator=g, device=device)
+                              * 0.5).contiguous()
+            else:
+                lw["qkv"] = self.matrix(s.qkv_rows, D)
+                lw["o"] = self.matrix(D, s.heads * s.head_dim)
+                if s.qk_norm:
+                    lw["q_norm"] = self.norm(s.head_dim)
+                    lw["k_norm"] = self.norm(s.head_dim)
+            self.layers.append(lw)
+
+    def norm(self, n: int) -> torch.Tensor:
+        return (1.0 + 0.1 * torch.randn(n, generator=self.g, device=self.device)).contiguous()
+
+    def matrix(self, N: int, K: int) -> ops.Q4Matrix:
+        fmt = self.shape.fmt
+        g, dev = self.g, self.device
+        if fmt == "q4_k":
+            m = ops.Q4Matrix(N, K, L.LAYOUT_Q4K, device=dev)
+            m.quants.random_(0, 256, generator=g)
+            rec = m.quants.view(-1, 144)
+            # d and dmin small enough that d * sc * q - dmin * m stays ~0.02
+            hdr = torch.empty((rec.shape[0], 2), device=dev)
+            hdr[:, 0].uniform_(1.0e-4, 2.0e-4, generator=g)
+            hdr[:, 1].uniform_(4.0e-4, 8.0e-4, generator=g)
+            rec[:, 0:4] = hdr.half().view(torch.uint8)
+            return m
+        zero = {"q4_0": L.ZERO_8, "nbits": L.ZERO_U8, "q4_k_rowgroup": L.ZERO_F16}[fmt]
+        m = ops.Q4Matrix(N, K, L.LAYOUT_ROWGROUP, zero, device=dev)
+        m.quants.random_(0, 256, generator=g)
+        sc = torch.empty(m.scales.shape, device=dev).uniform_(0.002, 0.006, generator=g)
+        m.scales.copy_(sc.half().view(torch.int16))
+        if zero == L.ZERO_U8:
+            m.zeros.random_(0, 16, generator=g)
+        elif zero == L.ZERO_F16:
+            z = torch.empty(m.zeros.shape, device=dev).uniform_(6.0, 9.0, generator=g)
+            m.zeros.copy_(z.half().view(torch.int16))
+        return m
+
+    @property
+    def nbytes(self) -> int:
+        n = self.embedding.nbytes
+        for lw in self.layers:
+            n += sum(v.nbytes for v in lw.values() if isinstance(v, ops.Q4Matrix))
+        return n
+
+
+class Engine:
+    """Forward, greedy pick and accept over device-resident weights."""
+
+    def __init__(self, weights: Weights, ctx: int):
+        s = self.shape = weights.shape
+        self.w = weights
+        self.ctx = ctx
+        dev = self.device = weights.device
+        D, F = s.hidden, s.intermediate
+        R = MAX_ROWS
+        f32, f16, i32 = torch.float32, torch.float16, torch.int32
+        self.ids = torch.zeros(R, dtype=i32, device=dev)
+        self.pos = torch.zeros(1, dtype=i32, device=dev)
+        self.h = torch.zeros((R, D), dtype=f32, device=dev)
+        self.x16 = torch.zeros((R, D), dtype=f16, device=dev)
+        self.hist = torch.zeros(ctx + 1, dtype=i32, device=dev)
+        self.qkv = torch.zeros((R, s.qkv_rows), dtype=f32, device=dev)
+        self.q = torch.zeros((R, s.heads * s.head_dim), dtype=f32, device=dev)
+        self.att16 = torch.zeros((R, s.heads * s.head_dim), dtype=f16, device=dev)
+        self.gu = torch.zeros((R, 2 * F), dtype=f32, device=dev)
+        self.ff16 = torch.zeros((R, F), dtype=f16, device=dev)
+        self.bcx = torch.zeros((R, 3 * D), dtype=f32, device=dev)
+        self.logits = torch.zeros((R, s.vocab), dtype=f32, device=dev)
+        self.next_ids = torch.zeros(R, dtype=i32, device=dev)
+        self.tops = torch.zeros(R, dtype=f32, device=dev)
+        self.argmax_scratch = torch.empty(L.load().wg_argmax_scratch_bytes(R, s.vocab),
+                                          dtype=torch.uint8, device=dev)
+        self.attn = ops.attn_shape(s.heads, s.kv_heads, s.head_dim, s.head_dim, s.eps, s.qk_norm)
+        self.attn_scratch = ops.attn_scratch(R, self.attn, ctx, dev)
+        self.rope = _rope_table(s.rope_theta, s.head_dim, ctx).to(dev)
+        self.k_cache, self.v_cache, self.state, self.prefixes = {}, {}, {}, {}
+        for i in range(s.layers):
+            if s.layer_type(i) == "conv":
+                self.state[i] = torch.zeros((s.conv_kernel - 1, D), dtype=f32, device=dev)
+                self.prefixes[i] = torch.zeros((R, s.conv_kernel - 1, D), dtype=f32, device=dev)
+            else:
+                kvd = s.kv_heads * s.head_dim
+                self.k_cache[i] = torch.zeros((ctx, kvd), dtype=f16, device=dev)
+                self.v_cache[i] = torch.zeros((ctx, kvd), dtype=f16, device=dev)
+        self.position = 0
+        self.draft = None
+        self.graph = None
+
+    # --- the batch ------------------------------------------------------------
+    def _forward_rows(self, M: int, keep_prefixes: bool) -> None:
+        """Enqueue one batch of M rows (ids[:M] at positions pos..pos+M-1)."""
+        s, w = self.shape, self.w
+        D, F = s.hidden, s.intermediate
+        h = self.h[:M]
+        x16 = self.x16[:M]
+        ops.embed(w.embedding, self.ids[:M], out=h)
+        for i, lw in enumerate(w.layers):
+            ops.rms_norm(h, lw["op_norm"], s.eps, out=x16)
+            if s.layer_type(i) == "conv":
+                bcx = self.bcx[:M]
+                ops.gemv(lw["in_proj"], x16, out=bcx)
+                c16 = x16  # in_proj has read it
+                ops.short_conv(bcx, D, s.conv_kernel, lw["taps"], self.state[i],
+                               prefixes=self.prefixes[i][:M] if keep_prefixes else None,
+                               out=c16)
+                ops.gemv(lw["out_proj"], c16, out=h, residual=h)
+            else:
+                qkv = self.qkv[:M]
+                ops.gemv(lw["qkv"], x16, out=qkv)
+                ops.head_prep(qkv, self.attn, self.rope, self.pos, self.k_cache[i],
+                              self.v_cache[i], lw.get("q_norm"), lw.get("k_norm"),
+                              q_out=self.q[:M])
+                ops.attn_decode(self.q[:M], self.attn, self.k_cache[i], self.v_cache[i],
+                                self.pos, scratch=self.attn_scratch, out=self.att16[:M])
+                ops.gemv(lw["o"], self.att16[:M], out=h, residual=h)
+            ops.rms_norm(h, lw["ffn_norm"], s.eps, out=x16)
+            ops.gemv(lw["gate_up"], x16, out=self.gu[:M])
+            ops.swiglu(self.gu[:M], out=self.ff16[:M])
+            ops.gemv(lw["down"], self.ff16[:M], out=h, residual=h)
+        ops.rms_norm(h, w.final_norm, s.eps, out=x16)
+        ops.gemv(w.embedding, x16, out=self.logits[:M])
+        ops.argmax_rows(self.logits[:M], ids=self.next_ids[:M], tops=self.tops[:M],
+                        scratch=self.argmax_scratch)
+
+    # --- the reference's Engine API -------------------------------------------
+    def reset(self) -> None:
+        self.position = 0
+        self.pos.zero_()
+        for st in self.state.values():
+            st.zero_()
+        self.draft = None
+
+    def forward(self, tokens, draft: bool = False) -> torch.Tensor:
+        """Runs tokens (a prompt in batches of 8, or a token and its drafts)
+        and returns the greedy pick of every row of the last batch."""
+        tokens = list(tokens)
+        if not tokens:
+            raise ValueError("no tokens")
+        if self.position + len(tokens) > self.ctx:
+            raise ValueError(f"The cache holds {self.ctx} tokens; this would need "
+                             f"{self.position + len(tokens)}.")
+        if draft and len(tokens) > MAX_ROWS:
+            raise ValueError(f"A draft batch holds {MAX_ROWS} tokens at most.")
+        out = None
+        for b0 in range(0, len(tokens), MAX_ROWS):
+            batch = tokens[b0:b0 + MAX_ROWS]
+            M = len(batch)
+            self.ids[:M].copy_(torch.tensor(batch, dtype=torch.int32))
+            self.pos.fill_(self.position)
+            self._forward_rows(M, keep_prefixes=draft)
+            self.position += M
+            out = self.next_ids[:M]
+        if draft:
+            self.draft = (self.position - len(tokens), len(tokens))
+        return out.clone()
+
+    def accept(self, count: int) -> None:
+        """Keeps the first `count` tokens of the last draft batch
+        (src/engine.ts:8063-8086): conv states back to that prefix; the
+        cache continues after them."""
+        if self.draft is None:
+            raise ValueError("No draft batch to accept tokens of.")
+        pos0, rows = self.draft
+        self.draft = None
+        if count < 1 or count > rows:
+            raise ValueError(f"Can't keep {count} of a {rows}-token batch.")
+        if count < rows:
+            s = self.shape
+            for i, st in self.state.items():
+                ops.conv_accept(self.prefixes[i], count, rows, s.hidden, s.conv_kernel, st)
+        self.position = pos0 + count
+
+    # --- graph-captured single-token decode -----------------------------------
+    def capture_step(self) -> None:
+        """Captures one decode step: forward of ids[0] at pos, pick into
+        ids[0], pos += 1."""
+        stream = torch.cuda.Stream(device=self.device)
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            # warm-up outside the graph (first-call lazies), state restored after
+            saved = self._save()
+            self._step_body()
+            self._restore(saved)
+            torch.cuda.current_stream().synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                self._step_body()
+        torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        self._restore(saved)
+        self.graph = g
+
+    def _step_body(self) -> None:
+        self._forward_rows(1, keep_prefixes=False)
+        self.ids[0:1].copy_(self.next_ids[0:1])
+        self.pos.add_(1)
+        # hist[pos + 1] = the token picked at pos
+        self.hist.index_copy_(0, self.pos.long(), self.next_ids[0:1])
+
+    def _save(self):
+        return (self.ids.clone(), self.pos.clone(), {i: s.clone() for i, s in self.state.items()})
+
+    def _restore(self, saved) -> None:
+        ids, pos, states = saved
+        self.ids.copy_(ids)
+        self.pos.copy_(pos)
+        for i, s in states.items():
+            self.state[i].copy_(s)
+
+    def decode(self, first_token: int, steps: int) -> list[int]:
+        """Greedy decode `steps` tokens after `first_token` by graph replay."""
+        if self.position + steps > self.ctx:
+            raise ValueError("decode would run past the cache")
+        if self.graph is None:
+            self.capture_step()
+        p0 = self.position
+        self.ids[0] = first_token
+        self.pos.fill_(p0)
+        for _ in range(steps):
+            self.graph.replay()
+        self.position += steps
+        return self.hist[p0 + 1:p0 + steps + 1].tolist()
+
+
+def _rope_table(theta: float, head_dim: int, ctx: int) -> torch.Tensor:
+    """Engine.ropeTable (src/engine.ts:1292-1312): cos and sin in doubles,
+    stored as float32; rows 0..1023 positions, row 1024 + i position 1024 i."""
+    half = head_dim // 2
+    rows = 1024 + (ctx + 1023) // 1024
+    r = torch.arange(rows, dtype=torch.float64)
+    pos = torch.where(r < 1024, r, (r - 1024) * 1024)
+    i = torch.arange(half, dtype=torch.float64)
+    freq = theta ** (-2.0 * i / head_dim)
+    ang = pos[:, None] * freq[None, :]
+    return torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).to(torch.float32).contiguous()
