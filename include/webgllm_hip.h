@@ -40,6 +40,14 @@ extern "C" {
 const char *wg_last_error(void);
 const char *wg_version(void);
 
+/* Launch-shape knobs, as the reference's TUNING table (src/engine.ts:147-625):
+ * "gemv_wg_per_cu", "gemv_wg_per_cu_wide" (matrices of 16384+ row groups),
+ * "q4k_wg_per_cu" (persistent GEMV workgroups per compute unit) and
+ * "gemv_min_waves" (below this many waves a GEMV splits K inside a
+ * workgroup). Process-wide; results never depend on them. */
+int wg_tuning_set(const char *name, int32_t value);
+int wg_tuning_get(const char *name, int32_t *value);
+
 /* ---------------------------------------------- 1. backend object layer */
 typedef struct wg_ctx wg_ctx;
 typedef struct wg_buf wg_buf;
@@ -155,13 +163,56 @@ int wg_q4_dequant(const wg_q4_matrix *m, int32_t row0, int32_t rows, float *out,
 
 /* ------------------------------------------------------------ matmul */
 
-/* Epilogue of a matmul: y[m][n] = (residual ? residual[m][n] : 0)
- * + (row_scale ? row_scale[m] : 1) * (A W^T)[m][n]. residual may equal y
- * (an in-place residual add; Engine.addNormed's add, engine.ts:5695-5803). */
+/* What a GEMV does with its sums (the reference folds the same steps into
+ * its matmul and add passes: the "prescaled" normed matmul, addScaled,
+ * rmsOfAdd and REDUCE_SWIGLU, src/gpu/kernels.ts:744-895, :1169-1361,
+ * :1066-1077; headPrep + values, :2196-2322, :3030-3045).
+ *
+ * Input side: with norm_parts, row m of the result is multiplied by
+ * norm_mult / sqrt(sum of norm_parts[m][0 .. n_parts) / norm_count + eps):
+ * the activations were stored as half(x * w / norm_mult) by the producer,
+ * and the parts are the sums of squares of x it wrote (one a row group).
+ * row_scale[m], if given, multiplies as well.
+ *
+ * Output side, by mode:
+ *  WG_EPI_STORE: y[m][n] = (residual ? residual[m][n] : 0) + s_m * acc; with
+ *    out16, out16[m][n] = half(y[m][n] * out16_w[n] / norm_mult_out) (the
+ *    next norm's input, prescaled); with parts_out, parts_out[m][g] = the sum
+ *    of squares of y[m][4g .. 4g + 3]. residual may equal y (in-place add).
+ *  WG_EPI_SWIGLU: rows come in groups of 4 as (gate 2i, gate 2i + 1, up 2i,
+ *    up 2i + 1); out16[m][2i + j] = half(silu(gate) * up); y is not written.
+ *  WG_EPI_ROPE_KV: the matrix is a q|k|v projection whose q and k rows come
+ *    in groups of 4 as (j, j + hd/2, j + 1, j + 1 + hd/2) of a head (all dims
+ *    rotated); q goes to q_out (rotated, times 1/sqrt(hd)), k (rotated) and
+ *    v to the caches as halves at row *pos0 + m (see wg_head_prep). */
+#define WG_EPI_STORE 0
+#define WG_EPI_SWIGLU 1
+#define WG_EPI_ROPE_KV 2
+
 typedef struct {
+  int32_t mode;
+  /* input normalisation */
+  const float *norm_parts;
+  int32_t n_parts, ld_parts_in;
+  int32_t norm_count;
+  float eps, norm_mult;
+  const float *row_scale;
+  /* WG_EPI_STORE */
   const float *residual;
   int32_t ld_residual;
-  const float *row_scale;
+  uint16_t *out16;
+  int32_t ld_out16;
+  const float *out16_w;
+  float norm_mult_out;
+  float *parts_out;
+  int32_t ld_parts_out;
+  /* WG_EPI_ROPE_KV */
+  int32_t heads, kv_heads, head_dim, ctx, rope_rows;
+  const float *rope;
+  const int32_t *pos0;
+  float *q_out;
+  int32_t ld_q_out;
+  uint16_t *k_cache, *v_cache;
 } wg_epilogue;
 
 /* Decode / few-token GEMV (matmulSplitRgba4 and the split matmul,
@@ -188,11 +239,13 @@ int wg_rms_norm(const float *x, int32_t M, int32_t D, int32_t ldx, const float *
 int wg_swiglu(const float *gu, int32_t M, int32_t F, int32_t ldg, uint16_t *out, int32_t ldo,
               void *stream);
 
-/* Embedding rows (embed, kernels.ts:1092-1149): h[m] = row ids[m] of the
- * quantized embedding, dequantized as matrixRow does (src/repack.ts:865-891).
- * An id outside [0, N) embeds as zeros. */
+/* Embedding rows (embed / embedFold, kernels.ts:1092-1149, :985-1041): h[m] =
+ * row ids[m] of the quantized embedding, dequantized as matrixRow does
+ * (src/repack.ts:865-891); an id outside [0, N) embeds as zeros. With ep
+ * (its STORE outputs out16 and parts_out), also layer 0's prescaled half
+ * input and the sums of squares of each 4 values, as embedFold draws them. */
 int wg_embed(const wg_q4_matrix *emb, const int32_t *ids, int32_t M, float *h, int32_t ldh,
-             void *stream);
+             const wg_epilogue *ep, void *stream);
 
 /* -------------------------------------------------------- attention */
 

@@ -3,8 +3,10 @@ engine (test infrastructure). It reads the engine's device weights back to
 the host, dequantizes them with the oracle's matrixRow (src/repack.ts:865-891;
 Q4_K through packQ4_K, :100-168) and runs the reference's forward
 (src/engine.ts:8875-9303) in float64 matmuls with the reference's fp16
-rounding points: activations into matmuls (packH2, src/gpu/kernels.ts:32-36),
-keys and values in the cache, attention and SwiGLU outputs."""
+rounding points: a normed matmul's input is half(x * w / 32) and its sums
+are scaled by 32 / RMS(x) (addScaled + the prescaled matmul,
+src/gpu/kernels.ts:1313-1331, :744-895); keys and values in the cache,
+attention and SwiGLU outputs are halves (packH2, kernels.ts:32-36)."""
 import math
 
 import numpy as np
@@ -17,7 +19,18 @@ def _np(t):
 
 
 def dense_of(m, threads=0) -> np.ndarray:
-    """The oracle's float32 weights of an ops.Q4Matrix."""
+    """The oracle's float32 weights of an ops.Q4Matrix, rows in logical order
+    (stored row p is logical row m.row_order[p] when the matrix has one)."""
+    d = _dense_stored(m, threads)
+    order = getattr(m, "row_order", None)
+    if order is None:
+        return d
+    out = np.empty_like(d)
+    out[np.asarray(order)] = d
+    return out
+
+
+def _dense_stored(m, threads=0) -> np.ndarray:
     from webgllm_amd import lib as L
     N, K = m.N, m.K
     if m.layout == L.LAYOUT_Q4K:
@@ -72,6 +85,14 @@ class OracleModel:
     def _mm(x, w):
         return (x.astype(np.float64) @ w.T).astype(np.float32)
 
+    def _normed_mm(self, h, norm_w, w):
+        """A matmul over the prescaled norm of h (rows of h), as the reference
+        does it: half(h * w / 32) in, sums times 32 / RMS(h)."""
+        x16 = h16(h.astype(np.float32) * norm_w.astype(np.float32) / np.float32(32.0))
+        ms = (h.astype(np.float64) ** 2).mean(1, keepdims=True)
+        r = 32.0 / np.sqrt(ms + self.s.eps)
+        return ((x16.astype(np.float64) @ w.T) * r).astype(np.float32)
+
     def forward_rows(self, ids):
         """One batch; returns (logits [M, V], picks [M])."""
         s = self.s
@@ -80,14 +101,13 @@ class OracleModel:
         hd = s.head_dim
         h = self.emb[np.asarray(ids)].astype(np.float32)
         for i, lw in enumerate(self.layers):
-            x = h16(O.rms_norm(h, lw["op_norm"], s.eps))
             if s.layer_type(i) == "conv":
-                bcx = self._mm(x, lw["in_proj"])
+                bcx = self._normed_mm(h, lw["op_norm"], lw["in_proj"])
                 out, st = O.short_conv(bcx, s.hidden, s.conv_kernel, lw["taps"], self.state[i])
                 self.state[i] = st
                 h = h + self._mm(h16(out), lw["out_proj"])
             else:
-                qkv = self._mm(x, lw["qkv"])
+                qkv = self._normed_mm(h, lw["op_norm"], lw["qkv"])
                 att = np.zeros((M, s.heads * hd), np.float32)
                 qd = s.heads * hd
                 kvd = s.kv_heads * hd
@@ -108,11 +128,9 @@ class OracleModel:
                                         pos + 1, kvd)
                     att[m] = h16(a)
                 h = h + self._mm(att, lw["o"])
-            x = h16(O.rms_norm(h, lw["ffn_norm"], s.eps))
-            gu = self._mm(x, lw["gate_up"])
+            gu = self._normed_mm(h, lw["ffn_norm"], lw["gate_up"])
             h = h + self._mm(h16(O.swiglu(gu)), lw["down"])
-        x = h16(O.rms_norm(h, self.final, s.eps))
-        logits = self._mm(x, self.emb)
+        logits = self._normed_mm(h, self.final, self.emb)
         picks = [O.argmax(logits[m])[0] for m in range(M)]
         self.position += M
         return logits, picks

@@ -64,9 +64,24 @@ def test_gemv_rejects_overlap_and_alignment():
     assert rc == -1 and "overlap" in L.last_error()
     rc = lib.wg_q4_gemv(C.byref(d), 0x10002, 1, 64, 0x20000, 8, None, None)
     assert rc == -1 and "aligned" in L.last_error()
-    ep = L.Epilogue(0x20004, 8, None)
+    ep = L.Epilogue(mode=L.EPI_STORE, residual=0x20004, ld_residual=8)
     rc = lib.wg_q4_gemv(C.byref(d), 0x10000, 1, 64, 0x20000, 8, C.byref(ep), None)
     assert rc == -1 and "residual overlaps" in L.last_error()
+
+
+@pytest.mark.parametrize("fields,msg", [
+    (dict(mode=7), "epilogue mode"),
+    (dict(mode=L.EPI_STORE, norm_parts=0x5000, n_parts=0), "input norm"),
+    (dict(mode=L.EPI_STORE, out16=0x6000, ld_out16=8), "prescaled half output"),
+    (dict(mode=L.EPI_SWIGLU), "SwiGLU"),
+    (dict(mode=L.EPI_ROPE_KV, heads=1, kv_heads=1, head_dim=4), "RoPE epilogue"),
+])
+def test_gemv_rejects_bad_epilogues(fields, msg):
+    lib = L.load()
+    d = _desc(N=12, K=64)
+    ep = L.Epilogue(**fields)
+    rc = lib.wg_q4_gemv(C.byref(d), 0x10000, 1, 64, 0x20000, 12, C.byref(ep), None)
+    assert rc == -1 and msg in L.last_error(), L.last_error()
 
 
 def test_repack_rejects_mismatched_layouts():
@@ -82,3 +97,15 @@ def test_repack_rejects_mismatched_layouts():
     d = _desc(zero=L.ZERO_8)
     assert lib.wg_repack_nbits(C.byref(d), 0, 8, 0x1, 0x2, 0x3, None, None) == -1
     assert "without them" in L.last_error()
+
+
+def test_tuning_knobs():
+    assert L.tuning_get("gemv_min_waves") >= 0
+    old = L.tuning_get("gemv_wg_per_cu")
+    L.tuning_set("gemv_wg_per_cu", 4)
+    assert L.tuning_get("gemv_wg_per_cu") == 4
+    L.tuning_set("gemv_wg_per_cu", old)
+    with pytest.raises(L.WgError, match="outside"):
+        L.tuning_set("gemv_wg_per_cu", 0)
+    with pytest.raises(L.WgError, match="no knob"):
+        L.tuning_set("nope", 1)

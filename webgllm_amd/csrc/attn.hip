@@ -101,11 +101,16 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
     const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
     const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int chunks) {
   constexpr int KSTR = HD + 2;  // LDS row stride in halves (breaks bank conflicts)
-  __shared__ uint16_t ks[CHUNK * KSTR];
-  __shared__ uint16_t vs[CHUNK * KSTR];
-  __shared__ float qs[64 * HD];
-  __shared__ float sc[64 * CHUNK];
-  __shared__ float mx[64], lsum[64];
+  // LDS, sized by the launch for GM = G * M queries: K and V tiles, the
+  // queries, the chunk's scores, and per query its max and sum of weights.
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int GMq = (H / KV) * M;
+  uint16_t *ks = reinterpret_cast<uint16_t *>(smem);
+  uint16_t *vs = ks + CHUNK * KSTR;
+  float *qs = reinterpret_cast<float *>(vs + CHUNK * KSTR);
+  float *sc = qs + GMq * HD;
+  float *mx = sc + GMq * CHUNK;
+  float *lsum = mx + GMq;
   const int kh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
   const int pos0 = *pos0_dev;
   // The last row sees keys 0 .. pos0 + M - 1; never more than the cache holds.
@@ -191,41 +196,74 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
   }
 }
 
-// One wave per (row m, query head h): the chunks' online-softmax combine.
-__global__ __launch_bounds__(64) void attn_combine_kernel(const float *partial, int M, int H,
-                                                          int hd, int chunks,
-                                                          const int32_t *pos0_dev,
-                                                          int max_keys, uint16_t *out, int ldo) {
-  const int h = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+// One workgroup of 256 per (query head h, row m): the chunks' online-softmax
+// combine. Lanes take chunks for the running max and the weights
+// exp(m_c - max); then each thread sums one dim over the chunks, whose loads
+// are independent (no chain through the chunk loop).
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float *partial, int M, int H,
+                                                           int hd, int chunks,
+                                                           const int32_t *pos0_dev,
+                                                           int max_keys, uint16_t *out, int ldo) {
+  __shared__ float wts[4096 / CHUNK * 16];
+  __shared__ float red[8];
+  const int h = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
   const int n_keys = min(*pos0_dev + m + 1, max_keys);  // keys row m sees
+  uint16_t *o = out + (int64_t)m * ldo + (int64_t)h * hd;
   if (n_keys <= 0) {
-    for (int d = lane; d < hd; d += 64) out[(int64_t)m * ldo + (int64_t)h * hd + d] = 0;
+    for (int d = tid; d < hd; d += 256) o[d] = 0;
     return;
   }
   const int used = (n_keys + CHUNK - 1) / CHUNK;
   const int row = m * H + h;
   PartialLayout pl{hd, chunks};
-  float gmax = -INFINITY;
-  for (int c = 0; c < used; c++) gmax = fmaxf(gmax, partial[pl.base(row, c)]);
-  float l = 0.0f;
-  float acc[MAX_HD / 64];
+  float mx = -INFINITY;
+  for (int c = tid; c < used; c += 256) mx = fmaxf(mx, partial[pl.base(row, c)]);
 #pragma unroll
-  for (int i = 0; i < MAX_HD / 64; i++) acc[i] = 0.0f;
-  for (int c = 0; c < used; c++) {
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  const float gmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float l = 0.0f;
+  for (int c = tid; c < used; c += 256) {
     const float *p = partial + pl.base(row, c);
     float w = p[0] == -INFINITY ? 0.0f : __expf(p[0] - gmax);
+    if (c < (int)(sizeof(wts) / sizeof(float))) wts[c] = w;
     l += w * p[1];
-#pragma unroll
-    for (int i = 0; i < MAX_HD / 64; i++) {
-      int d = lane + 64 * i;
-      if (d < hd) acc[i] += w * p[2 + d];
-    }
   }
-  float inv = 1.0f / l;
-#pragma unroll
-  for (int i = 0; i < MAX_HD / 64; i++) {
-    int d = lane + 64 * i;
-    if (d < hd) out[(int64_t)m * ldo + (int64_t)h * hd + d] = to_h(acc[i] * inv);
+  l = wave_sum(l);
+  __syncthreads();
+  if ((tid & 63) == 0) red[4 + (tid >> 6)] = l;
+  __syncthreads();
+  const float inv = 1.0f / (red[4] + red[5] + red[6] + red[7]);
+  const int cap = (int)(sizeof(wts) / sizeof(float));
+  for (int d = tid; d < hd; d += 256) {
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    int c = 0;
+    for (; c + 4 <= used; c += 4) {
+      float w0, w1, w2, w3;
+      if (c + 3 < cap) {
+        w0 = wts[c]; w1 = wts[c + 1]; w2 = wts[c + 2]; w3 = wts[c + 3];
+      } else {
+        const float *q = partial + pl.base(row, c);
+        w0 = q[0] == -INFINITY ? 0.0f : __expf(q[0] - gmax);
+        q += hd + 2;
+        w1 = q[0] == -INFINITY ? 0.0f : __expf(q[0] - gmax);
+        q += hd + 2;
+        w2 = q[0] == -INFINITY ? 0.0f : __expf(q[0] - gmax);
+        q += hd + 2;
+        w3 = q[0] == -INFINITY ? 0.0f : __expf(q[0] - gmax);
+      }
+      a0 += w0 * partial[pl.base(row, c) + 2 + d];
+      a1 += w1 * partial[pl.base(row, c + 1) + 2 + d];
+      a2 += w2 * partial[pl.base(row, c + 2) + 2 + d];
+      a3 += w3 * partial[pl.base(row, c + 3) + 2 + d];
+    }
+    for (; c < used; c++) {
+      const float *q = partial + pl.base(row, c);
+      float w = c < cap ? wts[c] : (q[0] == -INFINITY ? 0.0f : __expf(q[0] - gmax));
+      a0 += w * q[2 + d];
+    }
+    o[d] = to_h((a0 + a1 + a2 + a3) * inv);
   }
 }
 
@@ -263,6 +301,11 @@ int wg_head_prep(const float *qkv, int32_t M, int32_t ldq, const wg_attn_shape *
   return launched("wg_head_prep");
 }
 
+static size_t attn_lds_bytes(int GM, int hd) {
+  return (size_t)2 * CHUNK * (hd + 2) * 2 + (size_t)GM * hd * 4 + (size_t)GM * CHUNK * 4 +
+         (size_t)GM * 8;
+}
+
 size_t wg_attn_scratch_bytes(int32_t M, int32_t heads, int32_t head_dim, int32_t max_keys) {
   int64_t chunks = (max_keys + CHUNK - 1) / CHUNK;
   return (size_t)M * heads * chunks * (head_dim + 2) * sizeof(float);
@@ -286,16 +329,25 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
              wg_attn_scratch_bytes(M, H, hd, max_keys));
   int chunks = (max_keys + CHUNK - 1) / CHUNK;
   hipStream_t s = as_stream(stream);
+  size_t lds = attn_lds_bytes((H / KV) * M, hd);
+  static bool raised = false;  // allow more than 64 KiB of dynamic LDS, once
+  if (!raised) {
+    WG_HIP(hipFuncSetAttribute((const void *)attn_chunk_kernel<64>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    WG_HIP(hipFuncSetAttribute((const void *)attn_chunk_kernel<128>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    raised = true;
+  }
   if (hd == 64)
-    attn_chunk_kernel<64><<<dim3(KV, chunks), 256, 0, s>>>(
+    attn_chunk_kernel<64><<<dim3(KV, chunks), 256, lds, s>>>(
         q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, (float *)scratch, chunks);
   else
-    attn_chunk_kernel<128><<<dim3(KV, chunks), 256, 0, s>>>(
+    attn_chunk_kernel<128><<<dim3(KV, chunks), 256, lds, s>>>(
         q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, (float *)scratch, chunks);
   int rc = launched("wg_attn_decode");
   if (rc) return rc;
-  attn_combine_kernel<<<dim3(H, M), 64, 0, s>>>((const float *)scratch, M, H, hd, chunks, pos0,
-                                                max_keys, out, ldo);
+  attn_combine_kernel<<<dim3(H, M), 256, 0, s>>>((const float *)scratch, M, H, hd, chunks, pos0,
+                                                 max_keys, out, ldo);
   return launched("wg_attn_decode (combine)");
 }
 

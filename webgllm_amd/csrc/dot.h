@@ -53,4 +53,31 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
+// Reduce-scatter of 4 per-lane values over the 64 lanes in 7 shuffles:
+// afterwards lanes 16 r .. 16 r + 15 all hold the wave's sum of v[r].
+__device__ inline float wave_sum4(float v0, float v1, float v2, float v3) {
+  const int lane = threadIdx.x & 63;
+  const bool hi = lane & 32;
+  float s0 = hi ? v0 : v2, s1 = hi ? v1 : v3;
+  float k0 = hi ? v2 : v0, k1 = hi ? v3 : v1;
+  k0 += __shfl_xor(s0, 32, 64);
+  k1 += __shfl_xor(s1, 32, 64);
+  const bool hi2 = lane & 16;
+  float k = hi2 ? k1 : k0;
+  k += __shfl_xor(hi2 ? k0 : k1, 16, 64);
+  k += __shfl_xor(k, 8, 64);
+  k += __shfl_xor(k, 4, 64);
+  k += __shfl_xor(k, 2, 64);
+  k += __shfl_xor(k, 1, 64);
+  return k;
+}
+
+// The row a lane holds after wave_sum4.
+__device__ inline int wave_sum4_row() { return (threadIdx.x >> 4) & 3; }
+
+// Workgroups a persistent kernel launches per compute unit.
+int persistent_grid(int work_groups, int per_cu);
+// A launch-shape knob's value (see wg_tuning_set).
+int tuning(const char *name);
+
 }  // namespace wg

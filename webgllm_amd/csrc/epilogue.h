@@ -1,0 +1,123 @@
+// The GEMV epilogues (see wg_epilogue in include/webgllm_hip.h). The sums
+// arrive in the wave_sum4 layout: lanes 16 r .. 16 r + 15 hold row 4g + r of
+// every token (tot[m], in units of 2^-24); lane 16 r + m writes token m.
+#pragma once
+
+#include "common.h"
+#include "dot.h"
+
+namespace wg {
+
+__device__ inline uint16_t half_bits(float v) {
+  v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+  return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// The per-token factor: the input's 1 / RMS (times the producer's prescale)
+// and row_scale. Every lane of the wave takes part; all get the result.
+template <int M>
+__device__ inline void input_scales(const wg_epilogue &e, float s[M]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 0; m < M; m++) {
+    float v = 1.0f;
+    if (e.norm_parts) {
+      const float *p = e.norm_parts + (int64_t)m * e.ld_parts_in;
+      float a = 0.0f;
+      // 16-byte loads where the parts are 16-byte aligned (the usual case).
+      if ((((uintptr_t)p) & 15) == 0 && (e.n_parts & 3) == 0) {
+        const float4 *p4 = reinterpret_cast<const float4 *>(p);
+        for (int i = lane; i < (e.n_parts >> 2); i += 64) {
+          float4 t = p4[i];
+          a += (t.x + t.y) + (t.z + t.w);
+        }
+      } else {
+        for (int i = lane; i < e.n_parts; i += 64) a += p[i];
+      }
+      a = wave_sum(a);
+      v = e.norm_mult / sqrtf(a / (float)e.norm_count + e.eps);
+    }
+    if (e.row_scale) v *= e.row_scale[m];
+    s[m] = v;
+  }
+}
+
+// Picks tot[m] for this lane's token without dynamic register indexing.
+template <int M>
+__device__ inline float pick(const float tot[M], int m) {
+  float v = tot[0];
+#pragma unroll
+  for (int i = 1; i < M; i++)
+    if (m == i) v = tot[i];
+  return v;
+}
+
+// Row group g's four rows for tokens 0..M-1. Called by every lane of the
+// wave (the shuffles need all of them), with g >= G for idle waves.
+template <int M>
+__device__ inline void finish(const wg_epilogue &e, int g, int G, const float tot[M],
+                              const float scale[M], float *y, int ldy) {
+  const int lane = threadIdx.x & 63;
+  const int r = (lane >> 4) & 3, m = lane & 15;
+  const bool live = g < G && m < M;
+  const int mm = m < M ? m : 0;
+  float v = pick<M>(tot, mm) * 0x1p24f * scale[mm];
+  const int n = 4 * g + r;
+  if (e.mode == WG_EPI_STORE) {
+    if (live && e.residual) v += e.residual[(int64_t)m * e.ld_residual + n];
+    if (live && y) y[(int64_t)m * ldy + n] = v;
+    if (live && e.out16)
+      e.out16[(int64_t)m * e.ld_out16 + n] = half_bits(v * e.out16_w[n] / e.norm_mult_out);
+    if (e.parts_out) {
+      float sq = live ? v * v : 0.0f;
+      sq += __shfl_xor(sq, 16, 64);
+      sq += __shfl_xor(sq, 32, 64);
+      if (live && r == 0) e.parts_out[(int64_t)m * e.ld_parts_out + g] = sq;
+    }
+  } else if (e.mode == WG_EPI_SWIGLU) {
+    // rows (gate 2i, gate 2i + 1, up 2i, up 2i + 1): row r < 2 meets row r + 2
+    float up = __shfl_xor(v, 32, 64);
+    if (live && r < 2) {
+      float gate = v;
+      float o = gate / (1.0f + __expf(-gate)) * up;
+      e.out16[(int64_t)m * e.ld_out16 + 2 * g + r] = half_bits(o);
+    }
+  } else {  // WG_EPI_ROPE_KV
+    const int hd = e.head_dim, P = hd / 2;
+    const int qd = e.heads * hd, kd = e.kv_heads * hd;
+    float partner = __shfl_xor(v, 16, 64);  // rows 0 <-> 1 and 2 <-> 3
+    const int row = 4 * g;
+    int pos = live ? *e.pos0 + m : -1;
+    bool in_cache = pos >= 0 && pos < e.ctx && 1024 + (pos >> 10) < e.rope_rows;
+    if (row < qd + kd) {
+      const bool is_q = row < qd;
+      const int base = is_q ? 0 : qd;
+      const int head = (row - base) / hd;
+      const int i = ((row - base) % hd) / 4;
+      // dims of rows r = 0..3: 2i, 2i + P, 2i + 1, 2i + 1 + P
+      const int d = 2 * i + (r >> 1) + ((r & 1) ? P : 0);
+      const bool first = (r & 1) == 0;
+      const int f = d % P;
+      float o = 0.0f;
+      if (in_cache) {
+        const int lo = pos & 1023, hi = 1024 + (pos >> 10);
+        const float *r_lo = e.rope + (int64_t)lo * hd, *r_hi = e.rope + (int64_t)hi * hd;
+        float c1 = r_lo[f], s1 = r_lo[P + f], c2 = r_hi[f], s2 = r_hi[P + f];
+        float cs = c1 * c2 - s1 * s2, sn = s1 * c2 + c1 * s2;
+        o = first ? v * cs - partner * sn : v * cs + partner * sn;
+      }
+      if (live) {
+        if (is_q)
+          e.q_out[(int64_t)m * e.ld_q_out + (int64_t)head * hd + d] =
+              in_cache ? o * (1.0f / sqrtf((float)hd)) : 0.0f;
+        else if (in_cache)
+          e.k_cache[(int64_t)pos * kd + (int64_t)head * hd + d] = half_bits(o);
+      }
+    } else if (live && in_cache) {
+      const int dv = row - qd - kd + r;
+      e.v_cache[(int64_t)pos * kd + dv] = half_bits(v);
+    }
+  }
+}
+
+}  // namespace wg

@@ -23,6 +23,7 @@
 #include "common.h"
 #include "dot.h"
 #include "kernels.h"
+#include "epilogue.h"
 
 namespace wg {
 namespace {
@@ -98,8 +99,7 @@ template <int M, int ZK>
 __global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
     const uint4 *__restrict__ quants, const uint16_t *__restrict__ scales,
     const void *__restrict__ zeros, const uint16_t *__restrict__ x, int ldx,
-    float *__restrict__ y, int ldy, const float *residual, int ldr,
-    const float *__restrict__ row_scale, int G, int B) {
+    float *__restrict__ y, int ldy, const wg_epilogue e, int G, int B) {
   const int lane = threadIdx.x & 63;
   const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (g >= G) return;  // whole waves leave together
@@ -143,42 +143,223 @@ __global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
       }
     }
   }
+  float scale[M], tot[M];
+  input_scales<M>(e, scale);
 #pragma unroll
-  for (int r = 0; r < 4; r++)
+  for (int m = 0; m < M; m++) tot[m] = wave_sum4(acc[0][m], acc[1][m], acc[2][m], acc[3][m]);
+  finish<M>(e, g, G, tot, scale, y, ldy);
+}
+
+// ---------------------------------------------------------------------------
+// Streaming variant for 1 or 2 tokens (decode and short verify): persistent
+// workgroups of 4 waves. The K range is split into KS parts (a wave per
+// part, KS waves per row group, reduced through LDS); lane l of a part
+// takes its blocks l and l + 64 (NB of them), whose activations and block
+// sums it loads once into registers: they are the same for every row
+// group. Row groups are streamed: the next row group's nibbles, scales and
+// zero points are loaded before the current one is computed.
+template <int ZK, int NB>
+struct Unit {
+  uint4 q[NB][4];
+  uint2 sc[NB];
+  uint2 zr[NB];  // u8: .x holds 4 zero points; f16: 4 halves
+};
+
+template <int ZK, int NB>
+__device__ inline void load_unit(Unit<ZK, NB> &u, const uint4 *__restrict__ quants,
+                                 const uint16_t *__restrict__ scales,
+                                 const void *__restrict__ zeros, int g, int B, int b0, int b_end,
+                                 bool live) {
 #pragma unroll
-    for (int m = 0; m < M; m++) {
-      float v = wave_sum(acc[r][m]) * 0x1p24f;
-      if (lane == r + 4 * m) {
-        int n = 4 * g + r;
-        if (row_scale) v *= row_scale[m];
-        if (residual) v += residual[(int64_t)m * ldr + n];
-        y[(int64_t)m * ldy + n] = v;
+  for (int j = 0; j < NB; j++) {
+    int b = b0 + 64 * j;
+    if (live && b < b_end) {
+      int64_t si = ((int64_t)g * B + b) * 4;
+      const uint4 *qp = quants + si;
+      u.q[j][0] = qp[0];
+      u.q[j][1] = qp[1];
+      u.q[j][2] = qp[2];
+      u.q[j][3] = qp[3];
+      u.sc[j] = *reinterpret_cast<const uint2 *>(scales + si);
+      if constexpr (ZK == WG_ZERO_U8)
+        u.zr[j].x = *reinterpret_cast<const uint32_t *>((const uint8_t *)zeros + si);
+      if constexpr (ZK == WG_ZERO_F16)
+        u.zr[j] = *reinterpret_cast<const uint2 *>((const uint16_t *)zeros + si);
+    } else {
+      u.sc[j] = make_uint2(0u, 0u);  // scale 0: contributes nothing
+      u.q[j][0] = u.q[j][1] = u.q[j][2] = u.q[j][3] = make_uint4(0u, 0u, 0u, 0u);
+      u.zr[j] = make_uint2(0u, 0u);
+    }
+  }
+}
+
+template <int M, int ZK, int NB, int KS>
+__global__ __launch_bounds__(256) void gemv_stream_kernel(
+    const uint4 *__restrict__ quants, const uint16_t *__restrict__ scales,
+    const void *__restrict__ zeros, const uint16_t *__restrict__ x, int ldx,
+    float *__restrict__ y, int ldy, const wg_epilogue e, int G, int B) {
+  constexpr int RGW = 4 / KS;  // row groups a workgroup takes at a time
+  __shared__ float red[2][4][4 * M];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int part = wave % KS, slot = wave / KS;
+  const int BP = (B + KS - 1) / KS;
+  const int b0 = part * BP + lane;
+  const int b_end = min(B, (part + 1) * BP);
+
+  // The first row group's weights go out first: they need no input, and
+  // everything after them (activations, sums, the norm's parts) overlaps
+  // their flight.
+  const int stride = gridDim.x * RGW;
+  int g = blockIdx.x * RGW + slot;
+  Unit<ZK, NB> next;
+  load_unit<ZK, NB>(next, quants, scales, zeros, g, B, b0, b_end, g < G);
+
+  // This lane's activations and their block sums (times 2^-24), once.
+  uint4 a[M][NB][4];
+  float sa[M][NB];
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      int b = b0 + 64 * j;
+      if (b < b_end) {
+        const uint4 *xp = reinterpret_cast<const uint4 *>(x + (int64_t)m * ldx + b * 32);
+        a[m][j][0] = xp[0];
+        a[m][j][1] = xp[1];
+        a[m][j][2] = xp[2];
+        a[m][j][3] = xp[3];
+      } else {
+        a[m][j][0] = a[m][j][1] = a[m][j][2] = a[m][j][3] = make_uint4(0u, 0u, 0u, 0u);
       }
     }
+  float scale[M];
+  input_scales<M>(e, scale);
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) sa[m][j] = block_sum(a[m][j]) * 0x1p-24f;
+
+  int it = 0;
+  for (int g0 = blockIdx.x * RGW; g0 < G; g0 += stride, g += stride, it ^= 1) {
+    Unit<ZK, NB> u = next;
+    load_unit<ZK, NB>(next, quants, scales, zeros, g + stride, B, b0, b_end, g + stride < G);
+    float acc[4][M];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+      for (int m = 0; m < M; m++) acc[r][m] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      float d[4] = {(float)as_h2(u.sc[j].x).x, (float)as_h2(u.sc[j].x).y,
+                    (float)as_h2(u.sc[j].y).x, (float)as_h2(u.sc[j].y).y};
+      float z[4];
+      if constexpr (ZK == WG_ZERO_8) {
+        z[0] = z[1] = z[2] = z[3] = 8.0f;
+      } else if constexpr (ZK == WG_ZERO_U8) {
+        uint32_t v = u.zr[j].x;
+        z[0] = (float)(v & 0xffu);
+        z[1] = (float)((v >> 8) & 0xffu);
+        z[2] = (float)((v >> 16) & 0xffu);
+        z[3] = (float)(v >> 24);
+      } else {
+        z[0] = (float)as_h2(u.zr[j].x).x;
+        z[1] = (float)as_h2(u.zr[j].x).y;
+        z[2] = (float)as_h2(u.zr[j].y).x;
+        z[3] = (float)as_h2(u.zr[j].y).y;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        Nibbles n;
+        unpack(u.q[j][r], n);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          float v = block_dot(n, a[m][j]);
+          v = __builtin_fmaf(-z[r], sa[m][j], v);
+          acc[r][m] = __builtin_fmaf(d[r], v, acc[r][m]);
+        }
+      }
+    }
+    const int row = wave_sum4_row();
+    float tot[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) tot[m] = wave_sum4(acc[0][m], acc[1][m], acc[2][m], acc[3][m]);
+    if constexpr (KS > 1) {
+      // Parts 1.. hand their sums to part 0 through LDS (double-buffered by
+      // iteration parity, so one barrier a row group suffices).
+      if ((lane & 15) == 0 && part > 0)
+#pragma unroll
+        for (int m = 0; m < M; m++) red[it][wave][row * M + m] = tot[m];
+      __syncthreads();
+      if (part == 0)
+#pragma unroll
+        for (int m = 0; m < M; m++)
+#pragma unroll
+          for (int p = 1; p < KS; p++) tot[m] += red[it][wave + p][row * M + m];
+    }
+    if (part == 0) finish<M>(e, g, G, tot, scale, y, ldy);
+  }
+}
+
+template <int M, int ZK, int NB, int KS>
+int launch_stream(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
+                  const wg_epilogue &e, hipStream_t s) {
+  int G = w->N / 4, B = w->K / 32;
+  constexpr int RGW = 4 / KS;
+  int grid = persistent_grid((G + RGW - 1) / RGW,
+                             tuning(G >= 16384 ? "gemv_wg_per_cu_wide" : "gemv_wg_per_cu"));
+  gemv_stream_kernel<M, ZK, NB, KS><<<grid, 256, 0, s>>>(
+      (const uint4 *)w->quants, (const uint16_t *)w->scales, w->zeros, x, ldx, y, ldy, e, G, B);
+  return launched("wg_q4_gemv");
+}
+
+// K split so a lane holds at most 2 blocks' activations, and further (while
+// every part keeps 64 blocks) when the row groups alone would give fewer
+// than gemv_min_waves waves.
+template <int M, int ZK>
+int launch_stream_k(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
+                    const wg_epilogue &ep, hipStream_t s) {
+  int B = w->K / 32, G = w->N / 4;
+  int ks = B <= 128 ? 1 : B <= 256 ? 2 : B <= 512 ? 4 : 0;
+  if (!ks) return -1;
+  while (ks < 4 && G * ks < tuning("gemv_min_waves") && B / (2 * ks) >= 64) ks *= 2;
+  int nb = (B + ks - 1) / ks > 64 ? 2 : 1;
+  if (ks == 1) return nb == 1 ? launch_stream<M, ZK, 1, 1>(w, x, ldx, y, ldy, ep, s)
+                              : launch_stream<M, ZK, 2, 1>(w, x, ldx, y, ldy, ep, s);
+  if (ks == 2) return nb == 1 ? launch_stream<M, ZK, 1, 2>(w, x, ldx, y, ldy, ep, s)
+                              : launch_stream<M, ZK, 2, 2>(w, x, ldx, y, ldy, ep, s);
+  return nb == 1 ? launch_stream<M, ZK, 1, 4>(w, x, ldx, y, ldy, ep, s)
+                 : launch_stream<M, ZK, 2, 4>(w, x, ldx, y, ldy, ep, s);
+}
+
+template <int M>
+int launch_stream_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
+                    const wg_epilogue &ep, hipStream_t s) {
+  switch (w->zero) {
+    case WG_ZERO_8: return launch_stream_k<M, WG_ZERO_8>(w, x, ldx, y, ldy, ep, s);
+    case WG_ZERO_U8: return launch_stream_k<M, WG_ZERO_U8>(w, x, ldx, y, ldy, ep, s);
+    default: return launch_stream_k<M, WG_ZERO_F16>(w, x, ldx, y, ldy, ep, s);
+  }
 }
 
 template <int M>
 int launch_gemv_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
-                  const wg_epilogue *ep, hipStream_t s) {
+                  const wg_epilogue &e, hipStream_t s) {
   int G = w->N / 4, B = w->K / 32;
   dim3 grid((G + 3) / 4), block(256);
-  const float *res = ep ? ep->residual : nullptr;
-  int ldr = ep ? ep->ld_residual : 0;
-  const float *rs = ep ? ep->row_scale : nullptr;
   const uint4 *q = (const uint4 *)w->quants;
   const uint16_t *sc = (const uint16_t *)w->scales;
   switch (w->zero) {
     case WG_ZERO_8:
       gemv_rowgroup_kernel<M, WG_ZERO_8><<<grid, block, 0, s>>>(q, sc, w->zeros, x, ldx, y, ldy,
-                                                                res, ldr, rs, G, B);
+                                                                e, G, B);
       break;
     case WG_ZERO_U8:
       gemv_rowgroup_kernel<M, WG_ZERO_U8><<<grid, block, 0, s>>>(q, sc, w->zeros, x, ldx, y, ldy,
-                                                                 res, ldr, rs, G, B);
+                                                                 e, G, B);
       break;
     default:
       gemv_rowgroup_kernel<M, WG_ZERO_F16><<<grid, block, 0, s>>>(q, sc, w->zeros, x, ldx, y,
-                                                                  ldy, res, ldr, rs, G, B);
+                                                                  ldy, e, G, B);
       break;
   }
   return launched("wg_q4_gemv");
@@ -198,38 +379,85 @@ using namespace wg;
 
 extern "C" {
 
+// Checks an epilogue against the matrix and the row count.
+static int check_epilogue(const wg_q4_matrix *w, int M, const float *y, int ldy,
+                          const wg_epilogue &e) {
+  const int N = w->N, G = N / 4;
+  WG_REQUIRE(e.mode == WG_EPI_STORE || e.mode == WG_EPI_SWIGLU || e.mode == WG_EPI_ROPE_KV,
+             "wg_q4_gemv: unknown epilogue mode %d", e.mode);
+  if (e.norm_parts) {
+    WG_REQUIRE(e.n_parts >= 1 && e.norm_count >= 1 && e.ld_parts_in >= e.n_parts &&
+                   e.norm_mult != 0.0f,
+               "wg_q4_gemv: input norm needs parts, their count and a prescale");
+  }
+  if (e.mode == WG_EPI_STORE) {
+    WG_REQUIRE(y, "wg_q4_gemv: no output");
+    WG_REQUIRE(ldy >= N, "wg_q4_gemv: ldy %d < N %d", ldy, N);
+    if (e.residual) {
+      WG_REQUIRE(e.ld_residual >= N, "wg_q4_gemv: residual stride %d < N %d", e.ld_residual, N);
+      // An in-place add reads and writes the same element in one thread:
+      // allowed. Any other overlap would race.
+      WG_REQUIRE(e.residual == y || !overlaps(e.residual, (size_t)M * e.ld_residual * 4, y,
+                                              (size_t)M * ldy * 4),
+                 "wg_q4_gemv: residual overlaps the output");
+    }
+    if (e.out16)
+      WG_REQUIRE(e.out16_w && e.ld_out16 >= N && e.norm_mult_out != 0.0f,
+                 "wg_q4_gemv: the prescaled half output needs weights, a stride and a prescale");
+    if (e.parts_out) WG_REQUIRE(e.ld_parts_out >= G, "wg_q4_gemv: parts stride too small");
+  } else if (e.mode == WG_EPI_SWIGLU) {
+    WG_REQUIRE(e.out16 && e.ld_out16 >= N / 2, "wg_q4_gemv: SwiGLU needs a half output of N/2");
+  } else {
+    const int hd = e.head_dim;
+    WG_REQUIRE(e.kv_heads > 0 && e.heads % e.kv_heads == 0 && hd >= 4 && hd % 4 == 0,
+               "wg_q4_gemv: RoPE epilogue: %d heads over %d KV heads of %d", e.heads,
+               e.kv_heads, hd);
+    WG_REQUIRE(N == (e.heads + 2 * e.kv_heads) * hd,
+               "wg_q4_gemv: RoPE epilogue: %d rows for %d q + 2 x %d kv heads of %d", N,
+               e.heads, e.kv_heads, hd);
+    WG_REQUIRE(e.rope && e.pos0 && e.q_out && e.k_cache && e.v_cache,
+               "wg_q4_gemv: RoPE epilogue: null pointer");
+    WG_REQUIRE(e.ld_q_out >= e.heads * hd, "wg_q4_gemv: q stride too small");
+    WG_REQUIRE(e.ctx >= 1 && e.rope_rows >= 1024 + (e.ctx + 1023) / 1024,
+               "wg_q4_gemv: a rope table of %d rows for a %d-position cache", e.rope_rows, e.ctx);
+  }
+  return WG_OK;
+}
+
 int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx, float *y,
                int32_t ldy, const wg_epilogue *ep, void *stream) {
   int rc = check_matrix(w, "wg_q4_gemv");
   if (rc) return rc;
   WG_REQUIRE(M >= 1 && M <= 8, "wg_q4_gemv: %d rows; a few-token matmul takes 1 to 8", M);
-  WG_REQUIRE(x && y, "wg_q4_gemv: null activations or output");
+  WG_REQUIRE(x, "wg_q4_gemv: null activations");
   WG_REQUIRE(ldx >= w->K && ldx % 8 == 0, "wg_q4_gemv: ldx %d (K %d) must be >= K and a multiple of 8",
              ldx, w->K);
-  WG_REQUIRE(ldy >= w->N, "wg_q4_gemv: ldy %d < N %d", ldy, w->N);
   WG_REQUIRE(((uintptr_t)x & 15) == 0, "wg_q4_gemv: activations must be 16-byte aligned");
-  if (ep && ep->residual) {
-    WG_REQUIRE(ep->ld_residual >= w->N, "wg_q4_gemv: residual stride %d < N %d", ep->ld_residual,
-               w->N);
-    // An in-place add reads and writes the same element in one thread:
-    // allowed. Any other overlap would race.
-    WG_REQUIRE(ep->residual == y || !overlaps(ep->residual, (size_t)M * ep->ld_residual * 4, y,
-                                              (size_t)M * ldy * 4),
-               "wg_q4_gemv: residual overlaps the output");
-  }
-  WG_REQUIRE(!overlaps(x, (size_t)M * ldx * 2, y, (size_t)M * ldy * 4),
-             "wg_q4_gemv: activations and output overlap");
+  wg_epilogue e = {};
+  e.mode = WG_EPI_STORE;
+  if (ep) e = *ep;
+  if ((rc = check_epilogue(w, M, y, ldy, e))) return rc;
+  if (y) WG_REQUIRE(!overlaps(x, (size_t)M * ldx * 2, y, (size_t)M * ldy * 4),
+                    "wg_q4_gemv: activations and output overlap");
+  if (e.out16)
+    WG_REQUIRE(!overlaps(x, (size_t)M * ldx * 2, e.out16, (size_t)M * e.ld_out16 * 2),
+               "wg_q4_gemv: activations and half output overlap");
   hipStream_t s = as_stream(stream);
-  if (w->layout == WG_LAYOUT_Q4K) return launch_gemv_q4k(w, x, M, ldx, y, ldy, ep, s);
+  if (w->layout == WG_LAYOUT_Q4K) return launch_gemv_q4k(w, x, M, ldx, y, ldy, e, s);
+  if (M <= 2 && w->K <= 512 * 32) {
+    rc = M == 1 ? launch_stream_m<1>(w, x, ldx, y, ldy, e, s)
+                : launch_stream_m<2>(w, x, ldx, y, ldy, e, s);
+    if (rc != -1) return rc;
+  }
   switch (M) {
-    case 1: return launch_gemv_m<1>(w, x, ldx, y, ldy, ep, s);
-    case 2: return launch_gemv_m<2>(w, x, ldx, y, ldy, ep, s);
-    case 3: return launch_gemv_m<3>(w, x, ldx, y, ldy, ep, s);
-    case 4: return launch_gemv_m<4>(w, x, ldx, y, ldy, ep, s);
-    case 5: return launch_gemv_m<5>(w, x, ldx, y, ldy, ep, s);
-    case 6: return launch_gemv_m<6>(w, x, ldx, y, ldy, ep, s);
-    case 7: return launch_gemv_m<7>(w, x, ldx, y, ldy, ep, s);
-    default: return launch_gemv_m<8>(w, x, ldx, y, ldy, ep, s);
+    case 1: return launch_gemv_m<1>(w, x, ldx, y, ldy, e, s);
+    case 2: return launch_gemv_m<2>(w, x, ldx, y, ldy, e, s);
+    case 3: return launch_gemv_m<3>(w, x, ldx, y, ldy, e, s);
+    case 4: return launch_gemv_m<4>(w, x, ldx, y, ldy, e, s);
+    case 5: return launch_gemv_m<5>(w, x, ldx, y, ldy, e, s);
+    case 6: return launch_gemv_m<6>(w, x, ldx, y, ldy, e, s);
+    case 7: return launch_gemv_m<7>(w, x, ldx, y, ldy, e, s);
+    default: return launch_gemv_m<8>(w, x, ldx, y, ldy, e, s);
   }
 }
 

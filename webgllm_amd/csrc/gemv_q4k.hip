@@ -19,6 +19,7 @@
 #include "common.h"
 #include "dot.h"
 #include "kernels.h"
+#include "epilogue.h"
 
 namespace wg {
 namespace {
@@ -71,9 +72,7 @@ template <int M>
 __global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t *__restrict__ quants,
                                                        const uint16_t *__restrict__ x, int ldx,
                                                        float *__restrict__ y, int ldy,
-                                                       const float *residual, int ldr,
-                                                       const float *__restrict__ row_scale,
-                                                       int G, int S) {
+                                                       const wg_epilogue e, int G, int S) {
   const int lane = threadIdx.x & 63;
   const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (g >= G) return;
@@ -152,41 +151,220 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t *__restrict
       }
     }
   }
-  // Reduce over c (lane bits 0-1) and sb (bits 3-5); rp (bit 2) keeps rows apart.
+  float scale[M], tot[M];
+  input_scales<M>(e, scale);
+  // Rows 2 rp and 2 rp + 1 of each lane; one reduction for every lane (the
+  // shuffles must not run under a lane-dependent branch).
 #pragma unroll
-  for (int r = 0; r < 2; r++)
+  for (int m = 0; m < M; m++) {
+    float a0 = acc[0][m], a1 = acc[1][m];
+    tot[m] = wave_sum4(rp ? 0.0f : a0, rp ? 0.0f : a1, rp ? a0 : 0.0f, rp ? a1 : 0.0f);
+  }
+  finish<M>(e, g, G, tot, scale, y, ldy);
+}
+
+// ---------------------------------------------------------------------------
+// Streaming variant for 1 or 2 tokens: persistent workgroups of 4 waves; K
+// split into KS parts (a wave each, reduced through LDS); a lane keeps the
+// activations (and their sub-block sums) of its NS super-blocks' chunk c
+// in registers for every row group, and streams row groups with the next
+// one's records loaded before the current one is computed.
+template <int NS>
+struct KUnit {
+  uint4 h[NS][2];
+  uint4 q[NS][2][2];
+};
+
+template <int NS>
+__device__ inline void load_kunit(KUnit<NS> &u, const uint8_t *__restrict__ quants, int g, int S,
+                                  int s0, int s_end, int rp, int c, bool live) {
 #pragma unroll
-    for (int m = 0; m < M; m++) {
-      float v = acc[r][m];
-      v += __shfl_xor(v, 1, 64);
-      v += __shfl_xor(v, 2, 64);
-      v += __shfl_xor(v, 8, 64);
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      if ((lane & ~4) == 0) {  // lanes 0 (rows 0, 1) and 4 (rows 2, 3)
-        int n = 4 * g + 2 * rp + r;
-        v *= 0x1p24f;
-        if (row_scale) v *= row_scale[m];
-        if (residual) v += residual[(int64_t)m * ldr + n];
-        y[(int64_t)m * ldy + n] = v;
+  for (int j = 0; j < NS; j++) {
+    int s = s0 + 8 * j;
+    if (live && s < s_end) {
+      const uint8_t *rec = quants + (((int64_t)g * S + s) * 4 + 2 * rp) * 144;
+#pragma unroll
+      for (int r = 0; r < 2; r++) {
+        const uint8_t *p = rec + r * 144;
+        u.h[j][r] = *reinterpret_cast<const uint4 *>(p);
+        u.q[j][r][0] = *reinterpret_cast<const uint4 *>(p + 16 + 32 * c);
+        u.q[j][r][1] = *reinterpret_cast<const uint4 *>(p + 32 + 32 * c);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 2; r++) {
+        u.h[j][r] = make_uint4(0u, 0u, 0u, 0u);  // d = dmin = 0: contributes nothing
+        u.q[j][r][0] = u.q[j][r][1] = make_uint4(0u, 0u, 0u, 0u);
       }
     }
+  }
+}
+
+template <int M, int NS, int KS>
+__global__ __launch_bounds__(256) void gemv_q4k_stream_kernel(
+    const uint8_t *__restrict__ quants, const uint16_t *__restrict__ x, int ldx,
+    float *__restrict__ y, int ldy, const wg_epilogue e, int G, int S) {
+  constexpr int RGW = 4 / KS;
+  __shared__ float red[2][4][4 * M];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int part = wave % KS, slot = wave / KS;
+  const int c = lane & 3, rp = (lane >> 2) & 1, sb = lane >> 3;
+  const int SP = (S + KS - 1) / KS;
+  const int s0 = part * SP + sb;
+  const int s_end = min(S, (part + 1) * SP);
+
+  // The first row group's records go out before the activations (see the
+  // row-group kernel).
+  const int stride = gridDim.x * RGW;
+  int g = blockIdx.x * RGW + slot;
+  KUnit<NS> next;
+  load_kunit<NS>(next, quants, g, S, s0, s_end, rp, c, g < G);
+
+  uint4 a[M][NS][8];
+  float sa0[M][NS], sa1[M][NS];
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+      int s = s0 + 8 * j;
+      if (s < s_end) {
+        const uint4 *xp =
+            reinterpret_cast<const uint4 *>(x + (int64_t)m * ldx + s * 256 + 64 * c);
+#pragma unroll
+        for (int i = 0; i < 8; i++) a[m][j][i] = xp[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) a[m][j][i] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  float scale[M];
+  input_scales<M>(e, scale);
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+      float t0 = sum8(a[m][j][0], 0.0f), t1 = sum8(a[m][j][4], 0.0f);
+      t0 = sum8(a[m][j][1], t0);
+      t1 = sum8(a[m][j][5], t1);
+      t0 = sum8(a[m][j][2], t0);
+      t1 = sum8(a[m][j][6], t1);
+      t0 = sum8(a[m][j][3], t0);
+      t1 = sum8(a[m][j][7], t1);
+      sa0[m][j] = t0 * 0x1p-24f;
+      sa1[m][j] = t1 * 0x1p-24f;
+    }
+
+  int it = 0;
+  for (int g0 = blockIdx.x * RGW; g0 < G; g0 += stride, g += stride, it ^= 1) {
+    KUnit<NS> u = next;
+    load_kunit<NS>(next, quants, g + stride, S, s0, s_end, rp, c, g + stride < G);
+    float acc[2][M];
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+      for (int m = 0; m < M; m++) acc[r][m] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NS; j++)
+#pragma unroll
+      for (int r = 0; r < 2; r++) {
+        SubScales sc = decode(u.h[j][r], c);
+        const uint32_t w[8] = {u.q[j][r][0].x, u.q[j][r][0].y, u.q[j][r][0].z, u.q[j][r][0].w,
+                               u.q[j][r][1].x, u.q[j][r][1].y, u.q[j][r][1].z, u.q[j][r][1].w};
+        NibblePairs np[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) np[i] = split_nibbles(w[i]);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          const uint4 *A0 = a[m][j], *A1 = a[m][j] + 4;
+          float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            const uint4 &p0 = A0[i >> 1], &p1 = A1[i >> 1];
+            uint32_t x0 = (i & 1) ? p0.z : p0.x, x1 = (i & 1) ? p0.w : p0.y;
+            uint32_t y0 = (i & 1) ? p1.z : p1.x, y1 = (i & 1) ? p1.w : p1.y;
+            lo = dot2(np[i].lo0, x0, lo);
+            hi = dot2(np[i].hi0, y0, hi);
+            lo = dot2(np[i].lo1, x1, lo);
+            hi = dot2(np[i].hi1, y1, hi);
+          }
+          float v = acc[r][m];
+          v = __builtin_fmaf(sc.d0, lo, v);
+          v = __builtin_fmaf(-sc.dz0, sa0[m][j], v);
+          v = __builtin_fmaf(sc.d1 * 0.0625f, hi, v);
+          v = __builtin_fmaf(-sc.dz1, sa1[m][j], v);
+          acc[r][m] = v;
+        }
+      }
+    // Rows 2 rp and 2 rp + 1 of each lane, reduced into the wave_sum4 layout.
+    const int row = wave_sum4_row();
+    float tot[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      float a0 = acc[0][m], a1 = acc[1][m];
+      tot[m] = wave_sum4(rp ? 0.0f : a0, rp ? 0.0f : a1, rp ? a0 : 0.0f, rp ? a1 : 0.0f);
+    }
+    if constexpr (KS > 1) {
+      if ((lane & 15) == 0 && part > 0)
+#pragma unroll
+        for (int m = 0; m < M; m++) red[it][wave][row * M + m] = tot[m];
+      __syncthreads();
+      if (part == 0)
+#pragma unroll
+        for (int m = 0; m < M; m++)
+#pragma unroll
+          for (int p = 1; p < KS; p++) tot[m] += red[it][wave + p][row * M + m];
+    }
+    if (part == 0) finish<M>(e, g, G, tot, scale, y, ldy);
+  }
+}
+
+template <int M, int NS, int KS>
+int launch_kstream(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
+                   const wg_epilogue &e, hipStream_t s) {
+  int G = w->N / 4, S = w->K / 256;
+  constexpr int RGW = 4 / KS;
+  int grid = persistent_grid((G + RGW - 1) / RGW, tuning("q4k_wg_per_cu"));
+  gemv_q4k_stream_kernel<M, NS, KS><<<grid, 256, 0, s>>>((const uint8_t *)w->quants, x, ldx, y,
+                                                          ldy, e, G, S);
+  return launched("wg_q4_gemv (Q4_K)");
+}
+
+template <int M>
+int launch_kstream_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
+                     const wg_epilogue &ep, hipStream_t s) {
+  // As the row-group GEMV: at most 2 super-blocks a lane, and a further K
+  // split (while every part keeps 8 super-blocks) for small matrices.
+  int S = w->K / 256, G = w->N / 4;
+  int ks = S <= 16 ? 1 : S <= 32 ? 2 : S <= 64 ? 4 : 0;
+  if (!ks) return -1;
+  while (ks < 4 && G * ks < tuning("gemv_min_waves") && S / (2 * ks) >= 8) ks *= 2;
+  int ns = (S + ks - 1) / ks > 8 ? 2 : 1;
+  if (ks == 1) return ns == 1 ? launch_kstream<M, 1, 1>(w, x, ldx, y, ldy, ep, s)
+                              : launch_kstream<M, 2, 1>(w, x, ldx, y, ldy, ep, s);
+  if (ks == 2) return ns == 1 ? launch_kstream<M, 1, 2>(w, x, ldx, y, ldy, ep, s)
+                              : launch_kstream<M, 2, 2>(w, x, ldx, y, ldy, ep, s);
+  return ns == 1 ? launch_kstream<M, 1, 4>(w, x, ldx, y, ldy, ep, s)
+                 : launch_kstream<M, 2, 4>(w, x, ldx, y, ldy, ep, s);
 }
 
 template <int M>
 int launch_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
-             const wg_epilogue *ep, hipStream_t s) {
+             const wg_epilogue &e, hipStream_t s) {
   int G = w->N / 4, S = w->K / 256;
-  gemv_q4k_kernel<M><<<(G + 3) / 4, 256, 0, s>>>(
-      (const uint8_t *)w->quants, x, ldx, y, ldy, ep ? ep->residual : nullptr,
-      ep ? ep->ld_residual : 0, ep ? ep->row_scale : nullptr, G, S);
+  gemv_q4k_kernel<M><<<(G + 3) / 4, 256, 0, s>>>((const uint8_t *)w->quants, x, ldx, y, ldy, e,
+                                                 G, S);
   return launched("wg_q4_gemv (Q4_K)");
 }
 
 }  // namespace
 
 int launch_gemv_q4k(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y, int ldy,
-                    const wg_epilogue *ep, hipStream_t s) {
+                    const wg_epilogue &ep, hipStream_t s) {
+  if (M <= 2) {
+    int rc = M == 1 ? launch_kstream_m<1>(w, x, ldx, y, ldy, ep, s)
+                    : launch_kstream_m<2>(w, x, ldx, y, ldy, ep, s);
+    if (rc != -1) return rc;
+  }
   switch (M) {
     case 1: return launch_m<1>(w, x, ldx, y, ldy, ep, s);
     case 2: return launch_m<2>(w, x, ldx, y, ldy, ep, s);

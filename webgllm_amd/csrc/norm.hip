@@ -5,6 +5,7 @@
 // does (kernels.ts:32-36).
 #include "common.h"
 #include "dot.h"
+#include "epilogue.h"
 
 namespace wg {
 namespace {
@@ -60,17 +61,35 @@ __global__ void swiglu_kernel(const float *gu, int M, int F, int ldg, uint16_t *
   out[(int64_t)m * ldo + i] = to_h(g / (1.0f + __expf(-g)) * u);
 }
 
+// The embedding's extras (a GEMV epilogue's STORE outputs): the next
+// norm's prescaled half input and the sums of squares of each 4 values.
+__device__ inline void embed_extras(const wg_epilogue &e, int m, int c0, const float *v) {
+  if (e.out16) {
+    uint16_t *o16 = e.out16 + (int64_t)m * e.ld_out16 + c0;
+    for (int j = 0; j < 32; j++) o16[j] = half_bits(v[j] * e.out16_w[c0 + j] / e.norm_mult_out);
+  }
+  if (e.parts_out) {
+    float *pp = e.parts_out + (int64_t)m * e.ld_parts_out + c0 / 4;
+    for (int k = 0; k < 8; k++)
+      pp[k] = v[4 * k] * v[4 * k] + v[4 * k + 1] * v[4 * k + 1] + v[4 * k + 2] * v[4 * k + 2] +
+              v[4 * k + 3] * v[4 * k + 3];
+  }
+}
+
 // Embedding rows of a ROWGROUP matrix: thread = (token m, block b).
 __global__ void embed_rowgroup_kernel(const uint32_t *quants, const uint16_t *scales,
                                       const void *zeros, int zero_kind, const int32_t *ids,
-                                      int M, int blocks, int N, float *h, int ldh) {
+                                      int M, int blocks, int N, float *h, int ldh,
+                                      const wg_epilogue e) {
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (int64_t)M * blocks) return;
   int m = (int)(t / blocks), b = (int)(t % blocks);
   int n = ids[m];
   float *o = h + (int64_t)m * ldh + b * 32;
   if (n < 0 || n >= N) {  // an id outside the vocabulary embeds as zeros
+    float z[32] = {};
     for (int j = 0; j < 32; j++) o[j] = 0.0f;
+    embed_extras(e, m, b * 32, z);
     return;
   }
   int64_t si = ((int64_t)(n >> 2) * blocks + b) * 4 + (n & 3);
@@ -80,18 +99,21 @@ __global__ void embed_rowgroup_kernel(const uint32_t *quants, const uint16_t *sc
                                         : 8.0;
   uint4 q = reinterpret_cast<const uint4 *>(quants)[si];
   uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  float v[32];
 #pragma unroll
   for (int j = 0; j < 16; j++) {
     uint32_t byte = (w[j >> 2] >> (8 * (j & 3))) & 0xffu;
-    o[j] = (float)(d * ((double)(byte & 15u) - z));
-    o[j + 16] = (float)(d * ((double)(byte >> 4) - z));
+    v[j] = (float)(d * ((double)(byte & 15u) - z));
+    v[j + 16] = (float)(d * ((double)(byte >> 4) - z));
   }
+  for (int j = 0; j < 32; j++) o[j] = v[j];
+  embed_extras(e, m, b * 32, v);
 }
 
 // Embedding rows of a Q4_K matrix: thread = (token m, super-block s,
 // sub-block j), with packQ4_K's (d', z') chain (src/repack.ts:100-168).
 __global__ void embed_q4k_kernel(const uint8_t *quants, const int32_t *ids, int M, int supers,
-                                 int N, float *h, int ldh) {
+                                 int N, float *h, int ldh, const wg_epilogue e) {
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (int64_t)M * supers * 8) return;
   int j = (int)(t & 7);
@@ -100,7 +122,9 @@ __global__ void embed_q4k_kernel(const uint8_t *quants, const int32_t *ids, int 
   int n = ids[m];
   float *o = h + (int64_t)m * ldh + s * 256 + j * 32;
   if (n < 0 || n >= N) {
+    float zr[32] = {};
     for (int l = 0; l < 32; l++) o[l] = 0.0f;
+    embed_extras(e, m, s * 256 + j * 32, zr);
     return;
   }
   const uint8_t *p = quants + (((int64_t)(n >> 2) * supers + s) * 4 + (n & 3)) * 144;
@@ -114,10 +138,13 @@ __global__ void embed_q4k_kernel(const uint8_t *quants, const int32_t *ids, int 
   double scale = constant ? half_to_float(double_to_half_ref(-mins / 15.0)) : half_to_float(hq);
   double zero = constant ? 0.0 : half_to_float(double_to_half_ref(mins / scale));
   const uint8_t *q = p + 16 + (j >> 1) * 32;
+  float v[32];
   for (int l = 0; l < 32; l++) {
     int nib = constant ? 15 : (j & 1) ? q[l] >> 4 : q[l] & 15;
-    o[l] = (float)(scale * ((double)nib - zero));
+    v[l] = (float)(scale * ((double)nib - zero));
+    o[l] = v[l];
   }
+  embed_extras(e, m, s * 256 + j * 32, v);
 }
 
 }  // namespace
@@ -151,22 +178,29 @@ int wg_swiglu(const float *gu, int32_t M, int32_t F, int32_t ldg, uint16_t *out,
 }
 
 int wg_embed(const wg_q4_matrix *emb, const int32_t *ids, int32_t M, float *h, int32_t ldh,
-             void *stream) {
+             const wg_epilogue *ep, void *stream) {
   int rc = check_matrix(emb, "wg_embed");
   if (rc) return rc;
   WG_REQUIRE(ids && h && M >= 1 && ldh >= emb->K, "wg_embed: bad arguments");
+  wg_epilogue e = {};
+  if (ep) e = *ep;
+  if (e.out16)
+    WG_REQUIRE(e.out16_w && e.ld_out16 >= emb->K && e.norm_mult_out != 0.0f,
+               "wg_embed: the prescaled half output needs weights, a stride and a prescale");
+  if (e.parts_out)
+    WG_REQUIRE(e.ld_parts_out >= emb->K / 4, "wg_embed: parts stride too small");
   hipStream_t s = as_stream(stream);
   if (emb->layout == WG_LAYOUT_ROWGROUP) {
     int blocks = emb->K / 32;
     int64_t n = (int64_t)M * blocks;
     embed_rowgroup_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
         (const uint32_t *)emb->quants, (const uint16_t *)emb->scales, emb->zeros, emb->zero, ids,
-        M, blocks, emb->N, h, ldh);
+        M, blocks, emb->N, h, ldh, e);
   } else {
     int supers = emb->K / 256;
     int64_t n = (int64_t)M * supers * 8;
     embed_q4k_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
-        (const uint8_t *)emb->quants, ids, M, supers, emb->N, h, ldh);
+        (const uint8_t *)emb->quants, ids, M, supers, emb->N, h, ldh, e);
   }
   return launched("wg_embed");
 }

@@ -10,6 +10,7 @@
 #include <unordered_set>
 
 #include "common.h"
+#include "dot.h"
 
 namespace wg {
 
@@ -50,6 +51,39 @@ int check_matrix(const wg_q4_matrix *m, const char *who) {
   return WG_OK;
 }
 
+// Launch-shape knobs (the reference keeps its own in a TUNING table,
+// src/engine.ts:147-625): read by the launchers, set through wg_tuning_set.
+struct Knob {
+  const char *name;
+  int value, lo, hi;
+};
+static Knob g_knobs[] = {
+    {"gemv_wg_per_cu", 2, 1, 16},        // persistent row-group GEMV workgroups per CU
+    {"gemv_wg_per_cu_wide", 8, 1, 16},   // the same for matrices of 16384+ row groups
+    {"q4k_wg_per_cu", 2, 1, 16},         // persistent Q4_K GEMV workgroups per CU
+    {"gemv_min_waves", 8192, 0, 1 << 20},  // split K within a workgroup below this
+};
+
+int tuning(const char *name) {
+  for (auto &k : g_knobs)
+    if (!strcmp(k.name, name)) return k.value;
+  return 0;
+}
+
+int persistent_grid(int work_groups, int per_cu) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  int cap = cus[dev] * per_cu;
+  return work_groups < cap ? work_groups : cap;
+}
+
 }  // namespace wg
 
 using namespace wg;
@@ -76,6 +110,28 @@ struct wg_fence {
 };
 
 extern "C" {
+
+int wg_tuning_set(const char *name, int32_t value) {
+  WG_REQUIRE(name, "wg_tuning_set: no name");
+  for (auto &k : g_knobs)
+    if (!strcmp(k.name, name)) {
+      WG_REQUIRE(value >= k.lo && value <= k.hi, "wg_tuning_set: %s = %d is outside [%d, %d]",
+                 name, value, k.lo, k.hi);
+      k.value = value;
+      return WG_OK;
+    }
+  return fail(WG_ERR_INVALID, "wg_tuning_set: no knob named %s", name);
+}
+
+int wg_tuning_get(const char *name, int32_t *value) {
+  WG_REQUIRE(name && value, "wg_tuning_get: null argument");
+  for (auto &k : g_knobs)
+    if (!strcmp(k.name, name)) {
+      *value = k.value;
+      return WG_OK;
+    }
+  return fail(WG_ERR_INVALID, "wg_tuning_get: no knob named %s", name);
+}
 
 const char *wg_last_error(void) { return g_error; }
 const char *wg_version(void) { return "webgllm_hip 0.1 gfx950"; }

@@ -3,11 +3,16 @@ mirror of the reference's Engine forward, argmax and accept
 (src/engine.ts:7900-8086, forwardBatch :8875-9303, argmax :8271-8336).
 
 One batch of M <= 8 rows (a token, or a token and its drafts) runs as:
-embedding -> per layer [RMS norm -> operator (attention or short conv) ->
-residual add (in the projection's epilogue) -> RMS norm -> gate|up -> SwiGLU
--> down (+ residual)] -> final norm -> head -> greedy pick. The position
-lives on the device, so a single-token step is captured once as a HIP graph
-and replayed for every token with no host work between kernels.
+embedding -> per layer [operator (attention or short conv) -> gate|up ->
+down] -> head -> greedy pick, where every norm, residual add, SwiGLU and
+RoPE + cache write happens in a GEMV's epilogue, as the reference folds
+them into its passes: a projection that adds into the residual also writes
+the next norm's input as half(x * w / 32) and the sums of squares of x
+(addScaled + rmsOfAdd, src/gpu/kernels.ts:1290-1361), and the matmul that
+reads it applies 32 / RMS to its sums ("prescaled", kernels.ts:744-895).
+The position lives on the device, so a single-token step is captured once
+as a HIP graph and replayed for every token with no host work between
+kernels.
 
 Weights are random (the reference's speed probe does the same,
 src/speed-probe.ts:258-499) and generated on the device.
@@ -23,6 +28,32 @@ from . import lib as L
 from . import ops
 
 MAX_ROWS = 8
+PRESCALE = 32.0  # the reference's PRESCALE (src/gpu/kernels.ts:89)
+
+
+def qkv_row_order(shape) -> list:
+    """Logical row of each stored row of a q|k|v matrix whose epilogue does
+    RoPE: each head's rows in groups (j, j + hd/2, j + 1, j + 1 + hd/2), so a
+    rotation pair meets in one row group; v rows as they are."""
+    hd, P = shape.head_dim, shape.head_dim // 2
+    order = []
+    for head in range(shape.heads + shape.kv_heads):
+        base = head * hd
+        for i in range(hd // 4):
+            j = 2 * i
+            order += [base + j, base + j + P, base + j + 1, base + j + 1 + P]
+    v0 = (shape.heads + shape.kv_heads) * hd
+    order += list(range(v0, v0 + shape.kv_heads * hd))
+    return order
+
+
+def gate_up_row_order(F: int) -> list:
+    """Logical row of each stored row of a gate|up matrix whose epilogue does
+    SwiGLU: groups (gate 2i, gate 2i + 1, up 2i, up 2i + 1)."""
+    order = []
+    for i in range(F // 2):
+        order += [2 * i, 2 * i + 1, F + 2 * i, F + 2 * i + 1]
+    return order
 
 
 @dataclass
@@ -51,12 +82,22 @@ class ModelShape:
     def qkv_rows(self) -> int:
         return (self.heads + 2 * self.kv_heads) * self.head_dim
 
+    @property
+    def rope_in_epilogue(self) -> bool:
+        """RoPE and the cache writes fold into the q|k|v GEMV unless q and k
+        are RMS-normalised per head first (headPrep's norm)."""
+        return not self.qk_norm
+
 
 # The workloads' shapes.
 QWEN2_05B = ModelShape("qwen2-0.5b-shape", 896, 24, 14, 2, 64, 4864, 151936, "nbits",
                        rope_theta=1e6, eps=1e-6)
-LLAMA3_8B = ModelShape("llama3-8b-shape", 4096, 32, 32, 8, 128, 14336, 128256, "q4_k",
-                       rope_theta=5e5, eps=1e-5)
+# GGUF Q4_K weights, repacked at load into the reference's 32-blocks with half
+# scale and zero point (packQ4_K, src/repack.ts:100-168): measured faster than
+# streaming the super-blocks as they are, whose per-sub-block (d', z')
+# rebuild makes that GEMV VALU-bound.
+LLAMA3_8B = ModelShape("llama3-8b-shape", 4096, 32, 32, 8, 128, 14336, 128256,
+                       "q4_k_rowgroup", rope_theta=5e5, eps=1e-5)
 LFM2_12B = ModelShape("lfm2-1.2b-shape", 2048, 16, 32, 8, 64, 8192, 65536, "q4_0",
                       rope_theta=1e6, eps=1e-5, qk_norm=True, conv_kernel=3,
                       conv_layers=(0, 1, 3, 4, 6, 7, 9, 11, 13, 15))
@@ -78,7 +119,8 @@ class Weights:
         self.layers = []
         for i in range(s.layers):
             lw = {"op_norm": self.norm(D), "ffn_norm": self.norm(D),
-                  "gate_up": self.matrix(2 * s.intermediate, D),
+                  "gate_up": self.matrix(2 * s.intermediate, D,
+                                         gate_up_row_order(s.intermediate)),
                   "down": self.matrix(D, s.intermediate)}
             if s.layer_type(i) == "conv":
                 lw["in_proj"] = self.matrix(3 * D, D)
@@ -86,7 +128,8 @@ class Weights:
                 lw["taps"] = (torch.randn((D, s.conv_kernel), generator=g, device=device)
                               * 0.5).contiguous()
             else:
-                lw["qkv"] = self.matrix(s.qkv_rows, D)
+                lw["qkv"] = self.matrix(s.qkv_rows, D,
+                                        qkv_row_order(s) if s.rope_in_epilogue else None)
                 lw["o"] = self.matrix(D, s.heads * s.head_dim)
                 if s.qk_norm:
                     lw["q_norm"] = self.norm(s.head_dim)
@@ -96,29 +139,42 @@ class Weights:
     def norm(self, n: int) -> torch.Tensor:
         return (1.0 + 0.1 * torch.randn(n, generator=self.g, device=self.device)).contiguous()
 
-    def matrix(self, N: int, K: int) -> ops.Q4Matrix:
+    def matrix(self, N: int, K: int, row_order=None) -> ops.Q4Matrix:
+        """Random weights as a file holds them (GGUF Q4_0 or Q4_K blocks,
+        MatMulNBits rows), uploaded through the GPU repackers with `row_order`
+        as the loaders' srcRows (the logical row of each stored row)."""
         fmt = self.shape.fmt
         g, dev = self.g, self.device
-        if fmt == "q4_k":
-            m = ops.Q4Matrix(N, K, L.LAYOUT_Q4K, device=dev)
-            m.quants.random_(0, 256, generator=g)
-            rec = m.quants.view(-1, 144)
-            # d and dmin small enough that d * sc * q - dmin * m stays ~0.02
+        src_rows = None if row_order is None else \
+            torch.tensor(row_order, dtype=torch.int32, device=dev)
+        if fmt in ("q4_k", "q4_k_rowgroup"):
+            src = torch.empty(N * (K // 256) * 144, dtype=torch.uint8, device=dev)
+            src.random_(0, 256, generator=g)
+            rec = src.view(-1, 144)
+            # d and dmin keep d * sc * q - dmin * m near the 0.02 scale of a layer
             hdr = torch.empty((rec.shape[0], 2), device=dev)
             hdr[:, 0].uniform_(1.0e-4, 2.0e-4, generator=g)
             hdr[:, 1].uniform_(4.0e-4, 8.0e-4, generator=g)
             rec[:, 0:4] = hdr.half().view(torch.uint8)
-            return m
-        zero = {"q4_0": L.ZERO_8, "nbits": L.ZERO_U8, "q4_k_rowgroup": L.ZERO_F16}[fmt]
-        m = ops.Q4Matrix(N, K, L.LAYOUT_ROWGROUP, zero, device=dev)
-        m.quants.random_(0, 256, generator=g)
-        sc = torch.empty(m.scales.shape, device=dev).uniform_(0.002, 0.006, generator=g)
-        m.scales.copy_(sc.half().view(torch.int16))
-        if zero == L.ZERO_U8:
-            m.zeros.random_(0, 16, generator=g)
-        elif zero == L.ZERO_F16:
-            z = torch.empty(m.zeros.shape, device=dev).uniform_(6.0, 9.0, generator=g)
-            m.zeros.copy_(z.half().view(torch.int16))
+            m = ops.Q4Matrix.from_q4_k(src, N, K, native=fmt == "q4_k", src_rows=src_rows)
+        elif fmt == "q4_0":
+            src = torch.empty(N * (K // 32) * 18, dtype=torch.uint8, device=dev)
+            src.random_(0, 256, generator=g)
+            blk = src.view(-1, 18)
+            d = torch.empty(blk.shape[0], device=dev).uniform_(0.002, 0.006, generator=g)
+            blk[:, 0:2] = d.half().view(torch.uint8).view(-1, 2)
+            m = ops.Q4Matrix.from_q4_0(src, N, K, src_rows=src_rows)
+        elif fmt == "nbits":
+            quant = torch.empty(N * (K // 32) * 16, dtype=torch.uint8, device=dev)
+            quant.random_(0, 256, generator=g)
+            sc = torch.empty(N * (K // 32), device=dev).uniform_(0.002, 0.006, generator=g)
+            zp = torch.empty(N * ((K // 32 + 1) // 2), dtype=torch.uint8, device=dev)
+            zp.random_(0, 256, generator=g)
+            m = ops.Q4Matrix.from_nbits(quant, sc.half().view(torch.uint8), zp, N, K,
+                                        src_rows=src_rows)
+        else:
+            raise ValueError(f"unknown weight format {fmt}")
+        m.row_order = row_order
         return m
 
     @property
@@ -144,6 +200,8 @@ class Engine:
         self.pos = torch.zeros(1, dtype=i32, device=dev)
         self.h = torch.zeros((R, D), dtype=f32, device=dev)
         self.x16 = torch.zeros((R, D), dtype=f16, device=dev)
+        self.c16 = torch.zeros((R, D), dtype=f16, device=dev)
+        self.parts = torch.zeros((R, D // 4), dtype=f32, device=dev)
         self.hist = torch.zeros(ctx + 1, dtype=i32, device=dev)
         self.qkv = torch.zeros((R, s.qkv_rows), dtype=f32, device=dev)
         self.q = torch.zeros((R, s.heads * s.head_dim), dtype=f32, device=dev)
@@ -173,38 +231,74 @@ class Engine:
         self.graph = None
 
     # --- the batch ------------------------------------------------------------
+    def _norm_in(self, ep: "L.Epilogue") -> "L.Epilogue":
+        """The input side of a GEMV that reads the prescaled residual."""
+        D = self.shape.hidden
+        ep.norm_parts = self.parts.data_ptr()
+        ep.n_parts = D // 4
+        ep.ld_parts_in = D // 4
+        ep.norm_count = D
+        ep.eps = self.shape.eps
+        ep.norm_mult = PRESCALE
+        return ep
+
+    def _residual_out(self, M: int, next_norm: torch.Tensor) -> "L.Epilogue":
+        """h += result; the next norm's prescaled input and the parts."""
+        D = self.shape.hidden
+        return L.Epilogue(mode=L.EPI_STORE, residual=self.h.data_ptr(), ld_residual=D,
+                          out16=self.x16.data_ptr(), ld_out16=D, out16_w=next_norm.data_ptr(),
+                          norm_mult_out=PRESCALE, parts_out=self.parts.data_ptr(),
+                          ld_parts_out=D // 4)
+
     def _forward_rows(self, M: int, keep_prefixes: bool) -> None:
         """Enqueue one batch of M rows (ids[:M] at positions pos..pos+M-1)."""
         s, w = self.shape, self.w
         D, F = s.hidden, s.intermediate
         h = self.h[:M]
         x16 = self.x16[:M]
-        ops.embed(w.embedding, self.ids[:M], out=h)
+        first_norm = w.layers[0]["op_norm"] if w.layers else w.final_norm
+        ops.embed(w.embedding, self.ids[:M], out=h,
+                  epilogue=L.Epilogue(mode=L.EPI_STORE, out16=self.x16.data_ptr(), ld_out16=D,
+                                      out16_w=first_norm.data_ptr(), norm_mult_out=PRESCALE,
+                                      parts_out=self.parts.data_ptr(), ld_parts_out=D // 4))
         for i, lw in enumerate(w.layers):
-            ops.rms_norm(h, lw["op_norm"], s.eps, out=x16)
             if s.layer_type(i) == "conv":
                 bcx = self.bcx[:M]
-                ops.gemv(lw["in_proj"], x16, out=bcx)
-                c16 = x16  # in_proj has read it
+                ops.gemv(lw["in_proj"], x16, out=bcx,
+                         epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
+                c16 = self.c16[:M]
                 ops.short_conv(bcx, D, s.conv_kernel, lw["taps"], self.state[i],
                                prefixes=self.prefixes[i][:M] if keep_prefixes else None,
                                out=c16)
-                ops.gemv(lw["out_proj"], c16, out=h, residual=h)
+                ops.gemv(lw["out_proj"], c16, out=h,
+                         epilogue=self._residual_out(M, lw["ffn_norm"]))
             else:
-                qkv = self.qkv[:M]
-                ops.gemv(lw["qkv"], x16, out=qkv)
-                ops.head_prep(qkv, self.attn, self.rope, self.pos, self.k_cache[i],
-                              self.v_cache[i], lw.get("q_norm"), lw.get("k_norm"),
-                              q_out=self.q[:M])
+                if s.rope_in_epilogue:
+                    ep = self._norm_in(L.Epilogue(
+                        mode=L.EPI_ROPE_KV, heads=s.heads, kv_heads=s.kv_heads,
+                        head_dim=s.head_dim, ctx=self.ctx, rope_rows=self.rope.shape[0],
+                        rope=self.rope.data_ptr(), pos0=self.pos.data_ptr(),
+                        q_out=self.q.data_ptr(), ld_q_out=s.heads * s.head_dim,
+                        k_cache=self.k_cache[i].data_ptr(), v_cache=self.v_cache[i].data_ptr()))
+                    ops.gemv(lw["qkv"], x16, epilogue=ep)
+                else:
+                    qkv = self.qkv[:M]
+                    ops.gemv(lw["qkv"], x16, out=qkv,
+                             epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
+                    ops.head_prep(qkv, self.attn, self.rope, self.pos, self.k_cache[i],
+                                  self.v_cache[i], lw.get("q_norm"), lw.get("k_norm"),
+                                  q_out=self.q[:M])
                 ops.attn_decode(self.q[:M], self.attn, self.k_cache[i], self.v_cache[i],
                                 self.pos, scratch=self.attn_scratch, out=self.att16[:M])
-                ops.gemv(lw["o"], self.att16[:M], out=h, residual=h)
-            ops.rms_norm(h, lw["ffn_norm"], s.eps, out=x16)
-            ops.gemv(lw["gate_up"], x16, out=self.gu[:M])
-            ops.swiglu(self.gu[:M], out=self.ff16[:M])
-            ops.gemv(lw["down"], self.ff16[:M], out=h, residual=h)
-        ops.rms_norm(h, w.final_norm, s.eps, out=x16)
-        ops.gemv(w.embedding, x16, out=self.logits[:M])
+                ops.gemv(lw["o"], self.att16[:M], out=h,
+                         epilogue=self._residual_out(M, lw["ffn_norm"]))
+            ops.gemv(lw["gate_up"], x16,
+                     epilogue=self._norm_in(L.Epilogue(mode=L.EPI_SWIGLU,
+                                                       out16=self.ff16.data_ptr(), ld_out16=F)))
+            nxt = w.layers[i + 1]["op_norm"] if i + 1 < len(w.layers) else w.final_norm
+            ops.gemv(lw["down"], self.ff16[:M], out=h, epilogue=self._residual_out(M, nxt))
+        ops.gemv(w.embedding, x16, out=self.logits[:M],
+                 epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
         ops.argmax_rows(self.logits[:M], ids=self.next_ids[:M], tops=self.tops[:M],
                         scratch=self.argmax_scratch)
 

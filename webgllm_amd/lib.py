@@ -36,9 +36,24 @@ class Q4MatrixDesc(C.Structure):
                 ("quants", C.c_void_p), ("scales", C.c_void_p), ("zeros", C.c_void_p)]
 
 
+EPI_STORE, EPI_SWIGLU, EPI_ROPE_KV = 0, 1, 2
+
+
 class Epilogue(C.Structure):
-    _fields_ = [("residual", C.c_void_p), ("ld_residual", C.c_int32),
-                ("row_scale", C.c_void_p)]
+    """wg_epilogue (include/webgllm_hip.h)."""
+    _fields_ = [("mode", C.c_int32),
+                ("norm_parts", C.c_void_p), ("n_parts", C.c_int32), ("ld_parts_in", C.c_int32),
+                ("norm_count", C.c_int32), ("eps", C.c_float), ("norm_mult", C.c_float),
+                ("row_scale", C.c_void_p),
+                ("residual", C.c_void_p), ("ld_residual", C.c_int32),
+                ("out16", C.c_void_p), ("ld_out16", C.c_int32), ("out16_w", C.c_void_p),
+                ("norm_mult_out", C.c_float),
+                ("parts_out", C.c_void_p), ("ld_parts_out", C.c_int32),
+                ("heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
+                ("ctx", C.c_int32), ("rope_rows", C.c_int32),
+                ("rope", C.c_void_p), ("pos0", C.c_void_p),
+                ("q_out", C.c_void_p), ("ld_q_out", C.c_int32),
+                ("k_cache", C.c_void_p), ("v_cache", C.c_void_p)]
 
 
 class AttnShape(C.Structure):
@@ -74,6 +89,8 @@ def load():
     P, I32, I64, SZ = C.c_void_p, C.c_int32, C.c_int64, C.c_size_t
     sig = {
         "wg_last_error": (C.c_char_p, []),
+        "wg_tuning_set": (C.c_int, [C.c_char_p, I32]),
+        "wg_tuning_get": (C.c_int, [C.c_char_p, C.POINTER(I32)]),
         "wg_version": (C.c_char_p, []),
         "wg_ctx_create": (C.c_int, [C.c_int, C.POINTER(P)]),
         "wg_ctx_destroy": (C.c_int, [P]),
@@ -105,7 +122,8 @@ def load():
         "wg_f32_to_f16": (C.c_int, [P, P, I64, P]),
         "wg_rms_norm": (C.c_int, [P, I32, I32, I32, P, C.c_float, P, I32, P, P]),
         "wg_swiglu": (C.c_int, [P, I32, I32, I32, P, I32, P]),
-        "wg_embed": (C.c_int, [C.POINTER(Q4MatrixDesc), P, I32, P, I32, P]),
+        "wg_embed": (C.c_int, [C.POINTER(Q4MatrixDesc), P, I32, P, I32, C.POINTER(Epilogue),
+                               P]),
         "wg_head_prep": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32, P, P, I32,
                                    P, P, I32, P]),
         "wg_attn_scratch_bytes": (SZ, [I32, I32, I32, I32]),
@@ -131,3 +149,13 @@ def check(rc: int) -> None:
 
 def last_error() -> str:
     return load().wg_last_error().decode()
+
+
+def tuning_set(name: str, value: int) -> None:
+    check(load().wg_tuning_set(name.encode(), int(value)))
+
+
+def tuning_get(name: str) -> int:
+    v = C.c_int32()
+    check(load().wg_tuning_get(name.encode(), C.byref(v)))
+    return v.value

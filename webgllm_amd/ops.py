@@ -114,21 +114,27 @@ class Q4Matrix:
 
 
 def gemv(m: Q4Matrix, x16: torch.Tensor, out: torch.Tensor | None = None,
-         residual: torch.Tensor | None = None, row_scale: torch.Tensor | None = None):
-    """y = x W^T for M <= 8 rows of half activations [M, K] (int16/float16 bits)."""
+         residual: torch.Tensor | None = None, row_scale: torch.Tensor | None = None,
+         epilogue: "L.Epilogue | None" = None):
+    """y = x W^T for M <= 8 rows of half activations [M, K] (int16/float16 bits).
+    `epilogue` (an L.Epilogue) overrides residual/row_scale when given."""
     if x16.dtype not in (torch.float16, torch.int16):
         raise ValueError("activations must be halves")
     x16 = _dev(x16)
     M = x16.shape[0] if x16.dim() == 2 else 1
     ldx = x16.shape[-1]
-    if out is None:
-        out = torch.empty((M, m.N), dtype=torch.float32, device=x16.device)
-    _dev(out, torch.float32)
-    ep = None
-    if residual is not None or row_scale is not None:
-        ep = L.Epilogue(_p(residual), residual.shape[-1] if residual is not None else 0,
-                        _p(row_scale))
-    L.check(L.load().wg_q4_gemv(C.byref(m.desc), _p(x16), M, ldx, _p(out), out.shape[-1],
+    ep = epilogue
+    if ep is None:
+        if out is None:
+            out = torch.empty((M, m.N), dtype=torch.float32, device=x16.device)
+        if residual is not None or row_scale is not None:
+            ep = L.Epilogue(mode=L.EPI_STORE, residual=_p(residual),
+                            ld_residual=residual.shape[-1] if residual is not None else 0,
+                            row_scale=_p(row_scale))
+    if out is not None:
+        _dev(out, torch.float32)
+    L.check(L.load().wg_q4_gemv(C.byref(m.desc), _p(x16), M, ldx, _p(out),
+                                out.shape[-1] if out is not None else 0,
                                 C.byref(ep) if ep is not None else None, _stream()))
     return out
 
@@ -162,12 +168,14 @@ def swiglu(gu: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     return out
 
 
-def embed(m: "Q4Matrix", ids: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+def embed(m: "Q4Matrix", ids: torch.Tensor, out: torch.Tensor | None = None,
+          epilogue: "L.Epilogue | None" = None) -> torch.Tensor:
     ids = _dev(ids, torch.int32)
     M = ids.numel()
     if out is None:
         out = torch.empty((M, m.K), dtype=torch.float32, device=ids.device)
-    L.check(L.load().wg_embed(C.byref(m.desc), _p(ids), M, _p(out), out.shape[-1], _stream()))
+    L.check(L.load().wg_embed(C.byref(m.desc), _p(ids), M, _p(out), out.shape[-1],
+                              C.byref(epilogue) if epilogue is not None else None, _stream()))
     return out
 
 
