@@ -223,6 +223,17 @@ typedef struct {
 int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx, float *y,
                int32_t ldy, const wg_epilogue *ep, void *stream);
 
+/* Prefill GEMM (Engine.matmul -> matmulQuad, or dequant + matmulF16,
+ * kernels.ts:370-429, :436-735; Engine.f16Plan, engine.ts:980-995):
+ * C[m][n] = (residual ? residual[m][n] : 0) + sum_k A[m][k] W[n][k] for M
+ * tokens of half activations A ([M][lda], 16-byte aligned) and a row-group
+ * matrix (N and K multiples of 64); float32 C [M][ldc]. Weights are
+ * dequantized in registers to halves, d (q - z) rounded once as dequantOut
+ * does (kernels.ts:436-597), and multiplied on MFMA (v_mfma_f32_32x32x16_f16)
+ * with float32 accumulation. residual may equal C. */
+int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda, float *C,
+               int32_t ldc, const float *residual, int32_t ldr, void *stream);
+
 /* float32 -> half activations, clamped to +-65504 (packH2, kernels.ts:32-36). */
 int wg_f32_to_f16(const float *x, uint16_t *out, int64_t n, void *stream);
 

@@ -1,0 +1,87 @@
+"""Prefill GEMM on MFMA against the oracle. Two references: the exact
+dequantized weights in float64 (the north star's rel-L2 <= 1e-3 bar), and
+the weights rounded to halves the way the reference's dequantOut stores them
+(src/gpu/kernels.ts:436-597), which the GEMM must match to float32
+accumulation error."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import nbits, rel_l2
+from tests.model_oracle import dense_of
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _matrix(fmt, N, K, seed):
+    from webgllm_amd import engine as E
+    shape = E.ModelShape("t", K, 1, 1, 1, 4, 4, 4, fmt)
+    w = E.Weights.__new__(E.Weights)
+    w.shape, w.device = shape, "cuda"
+    w.g = torch.Generator(device="cuda")
+    w.g.manual_seed(seed)
+    return w.matrix(N, K)
+
+
+def _check(m, M, seed, residual=False):
+    from webgllm_amd import ops
+    rng = np.random.default_rng(seed)
+    K = m.K
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    a16 = O.f32_to_h2(a)
+    af = O.halves_to_f32(a16).astype(np.float64)
+    W = dense_of(m)
+    res = rng.standard_normal((M, m.N)).astype(np.float32) if residual else None
+    out = _t(res.copy()) if residual else None
+    got = ops.gemm(m, _t(a16.view(np.int16)), out=out,
+                   residual=out if residual else None).cpu().numpy()
+    base = res.astype(np.float64) if residual else 0.0
+    want = base + af @ W.astype(np.float64).T
+    # dequantOut's halves: (q - z) d rounded once to half
+    W16 = O.halves_to_f32(O.f32_to_h2(W)).astype(np.float64)
+    want16 = base + af @ W16.T
+    return rel_l2(got, want), rel_l2(got, want16)
+
+
+@pytest.mark.parametrize("N", [4096, 14336])
+def test_c2_matmulnbits_prefill(hip, N):
+    # 512 tokens x 4096 -> N, MatMulNBits with u8 zero points (the prefill workload)
+    m = _matrix("nbits", N, 4096, seed=N)
+    e, e16 = _check(m, 512, seed=1)
+    print(f"N={N} rel-L2 vs exact {e:.2e}, vs half-rounded weights {e16:.2e}")
+    assert e <= 1e-3
+    assert e16 <= 1e-5
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup"])
+@pytest.mark.parametrize("M,N,K", [(1, 64, 64), (37, 192, 128), (200, 512, 1024),
+                                   (128, 1024, 2048)])
+def test_gemm_shapes_and_formats(hip, fmt, M, N, K):
+    if fmt.startswith("q4_k") and K % 256:
+        pytest.skip("Q4_K rows are super-blocks of 256")
+    m = _matrix(fmt, N, K, seed=M + N)
+    e, e16 = _check(m, M, seed=M)
+    assert e <= 1e-3
+    # fractional zero points dequantize through float32 like the reference
+    assert e16 <= 1e-5
+
+
+def test_gemm_residual_in_place(hip):
+    m = _matrix("q4_0", 256, 512, seed=3)
+    e, e16 = _check(m, 64, seed=4, residual=True)
+    assert e16 <= 1e-5
+
+
+def test_gemm_rejects(hip):
+    from webgllm_amd import ops, lib as L
+    m = _matrix("q4_0", 96, 64, seed=1)   # N not a multiple of 64
+    with pytest.raises(L.WgError, match="multiple of 64"):
+        ops.gemm(m, torch.zeros((4, 64), dtype=torch.float16, device="cuda"))
+    m2 = _matrix("q4_k", 64, 256, seed=1)
+    with pytest.raises(L.WgError, match="row-group"):
+        ops.gemm(m2, torch.zeros((4, 256), dtype=torch.float16, device="cuda"))

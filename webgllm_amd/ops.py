@@ -139,6 +139,22 @@ def gemv(m: Q4Matrix, x16: torch.Tensor, out: torch.Tensor | None = None,
     return out
 
 
+def gemm(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
+         residual: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A W^T on MFMA for M tokens of half activations A [M, K]."""
+    if a16.dtype not in (torch.float16, torch.int16):
+        raise ValueError("activations must be halves")
+    a16 = _dev(a16)
+    M = a16.shape[0]
+    if out is None:
+        out = torch.empty((M, m.N), dtype=torch.float32, device=a16.device)
+    _dev(out, torch.float32)
+    L.check(L.load().wg_q4_gemm(C.byref(m.desc), _p(a16), M, a16.shape[1], _p(out), out.shape[1],
+                                _p(residual), residual.shape[1] if residual is not None else 0,
+                                _stream()))
+    return out
+
+
 def f32_to_f16(x: torch.Tensor) -> torch.Tensor:
     x = _dev(x, torch.float32)
     out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
