@@ -54,7 +54,7 @@ __device__ inline float pick(const float tot[M], int m) {
 
 // Row group g's four rows for tokens 0..M-1. Called by every lane of the
 // wave (the shuffles need all of them), with g >= G for idle waves.
-template <int M>
+template <int M, int MODE>
 __device__ inline void finish(const wg_epilogue &e, int g, int G, const float tot[M],
                               const float scale[M], float *y, int ldy) {
   const int lane = threadIdx.x & 63;
@@ -63,7 +63,7 @@ __device__ inline void finish(const wg_epilogue &e, int g, int G, const float to
   const int mm = m < M ? m : 0;
   float v = pick<M>(tot, mm) * 0x1p24f * scale[mm];
   const int n = 4 * g + r;
-  if (e.mode == WG_EPI_STORE) {
+  if constexpr (MODE == WG_EPI_STORE) {
     if (live && e.residual) v += e.residual[(int64_t)m * e.ld_residual + n];
     if (live && y) y[(int64_t)m * ldy + n] = v;
     if (live && e.out16)
@@ -74,7 +74,7 @@ __device__ inline void finish(const wg_epilogue &e, int g, int G, const float to
       sq += __shfl_xor(sq, 32, 64);
       if (live && r == 0) e.parts_out[(int64_t)m * e.ld_parts_out + g] = sq;
     }
-  } else if (e.mode == WG_EPI_SWIGLU) {
+  } else if constexpr (MODE == WG_EPI_SWIGLU) {
     // rows (gate 2i, gate 2i + 1, up 2i, up 2i + 1): row r < 2 meets row r + 2
     float up = __shfl_xor(v, 32, 64);
     if (live && r < 2) {

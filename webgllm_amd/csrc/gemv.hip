@@ -95,7 +95,7 @@ __device__ inline void load_zeros(const void *zeros, int64_t si, float z[4]) {
 }
 
 
-template <int M, int ZK>
+template <int M, int ZK, int MODE>
 __global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
     const uint4 *__restrict__ quants, const uint16_t *__restrict__ scales,
     const void *__restrict__ zeros, const uint16_t *__restrict__ x, int ldx,
@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
   input_scales<M>(e, scale);
 #pragma unroll
   for (int m = 0; m < M; m++) tot[m] = wave_sum4(acc[0][m], acc[1][m], acc[2][m], acc[3][m]);
-  finish<M>(e, g, G, tot, scale, y, ldy);
+  finish<M, MODE>(e, g, G, tot, scale, y, ldy);
 }
 
 // ---------------------------------------------------------------------------
@@ -193,7 +193,7 @@ __device__ inline void load_unit(Unit<ZK, NB> &u, const uint4 *__restrict__ quan
   }
 }
 
-template <int M, int ZK, int NB, int KS>
+template <int M, int ZK, int NB, int KS, int MODE>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(
     const uint4 *__restrict__ quants, const uint16_t *__restrict__ scales,
     const void *__restrict__ zeros, const uint16_t *__restrict__ x, int ldx,
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
 #pragma unroll
           for (int p = 1; p < KS; p++) tot[m] += red[it][wave + p][row * M + m];
     }
-    if (part == 0) finish<M>(e, g, G, tot, scale, y, ldy);
+    if (part == 0) finish<M, MODE>(e, g, G, tot, scale, y, ldy);
   }
 }
 
@@ -307,8 +307,17 @@ int launch_stream(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, i
   constexpr int RGW = 4 / KS;
   int grid = persistent_grid((G + RGW - 1) / RGW,
                              tuning(G >= 16384 ? "gemv_wg_per_cu_wide" : "gemv_wg_per_cu"));
-  gemv_stream_kernel<M, ZK, NB, KS><<<grid, 256, 0, s>>>(
-      (const uint4 *)w->quants, (const uint16_t *)w->scales, w->zeros, x, ldx, y, ldy, e, G, B);
+  auto q = (const uint4 *)w->quants;
+  auto sc = (const uint16_t *)w->scales;
+  if (e.mode == WG_EPI_SWIGLU)
+    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_SWIGLU><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, ldx,
+                                                                         y, ldy, e, G, B);
+  else if (e.mode == WG_EPI_ROPE_KV)
+    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_ROPE_KV><<<grid, 256, 0, s>>>(q, sc, w->zeros, x,
+                                                                          ldx, y, ldy, e, G, B);
+  else
+    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_STORE><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, ldx,
+                                                                        y, ldy, e, G, B);
   return launched("wg_q4_gemv");
 }
 
@@ -341,26 +350,29 @@ int launch_stream_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y,
   }
 }
 
+template <int M, int ZK, int MODE>
+void launch_rowgroup(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
+                     const wg_epilogue &e, hipStream_t s) {
+  int G = w->N / 4, B = w->K / 32;
+  gemv_rowgroup_kernel<M, ZK, MODE><<<(G + 3) / 4, 256, 0, s>>>(
+      (const uint4 *)w->quants, (const uint16_t *)w->scales, w->zeros, x, ldx, y, ldy, e, G, B);
+}
+
+template <int M, int ZK>
+void launch_rowgroup_mode(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
+                          const wg_epilogue &e, hipStream_t s) {
+  if (e.mode == WG_EPI_SWIGLU) launch_rowgroup<M, ZK, WG_EPI_SWIGLU>(w, x, ldx, y, ldy, e, s);
+  else if (e.mode == WG_EPI_ROPE_KV) launch_rowgroup<M, ZK, WG_EPI_ROPE_KV>(w, x, ldx, y, ldy, e, s);
+  else launch_rowgroup<M, ZK, WG_EPI_STORE>(w, x, ldx, y, ldy, e, s);
+}
+
 template <int M>
 int launch_gemv_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
                   const wg_epilogue &e, hipStream_t s) {
-  int G = w->N / 4, B = w->K / 32;
-  dim3 grid((G + 3) / 4), block(256);
-  const uint4 *q = (const uint4 *)w->quants;
-  const uint16_t *sc = (const uint16_t *)w->scales;
   switch (w->zero) {
-    case WG_ZERO_8:
-      gemv_rowgroup_kernel<M, WG_ZERO_8><<<grid, block, 0, s>>>(q, sc, w->zeros, x, ldx, y, ldy,
-                                                                e, G, B);
-      break;
-    case WG_ZERO_U8:
-      gemv_rowgroup_kernel<M, WG_ZERO_U8><<<grid, block, 0, s>>>(q, sc, w->zeros, x, ldx, y, ldy,
-                                                                 e, G, B);
-      break;
-    default:
-      gemv_rowgroup_kernel<M, WG_ZERO_F16><<<grid, block, 0, s>>>(q, sc, w->zeros, x, ldx, y,
-                                                                  ldy, e, G, B);
-      break;
+    case WG_ZERO_8: launch_rowgroup_mode<M, WG_ZERO_8>(w, x, ldx, y, ldy, e, s); break;
+    case WG_ZERO_U8: launch_rowgroup_mode<M, WG_ZERO_U8>(w, x, ldx, y, ldy, e, s); break;
+    default: launch_rowgroup_mode<M, WG_ZERO_F16>(w, x, ldx, y, ldy, e, s); break;
   }
   return launched("wg_q4_gemv");
 }

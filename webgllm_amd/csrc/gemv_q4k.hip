@@ -68,7 +68,7 @@ __device__ inline SubScales decode(const uint4 &h, int c) {
   return s;
 }
 
-template <int M>
+template <int M, int MODE>
 __global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t *__restrict__ quants,
                                                        const uint16_t *__restrict__ x, int ldx,
                                                        float *__restrict__ y, int ldy,
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t *__restrict
     float a0 = acc[0][m], a1 = acc[1][m];
     tot[m] = wave_sum4(rp ? 0.0f : a0, rp ? 0.0f : a1, rp ? a0 : 0.0f, rp ? a1 : 0.0f);
   }
-  finish<M>(e, g, G, tot, scale, y, ldy);
+  finish<M, MODE>(e, g, G, tot, scale, y, ldy);
 }
 
 // ---------------------------------------------------------------------------
@@ -200,7 +200,7 @@ __device__ inline void load_kunit(KUnit<NS> &u, const uint8_t *__restrict__ quan
   }
 }
 
-template <int M, int NS, int KS>
+template <int M, int NS, int KS, int MODE>
 __global__ __launch_bounds__(256) void gemv_q4k_stream_kernel(
     const uint8_t *__restrict__ quants, const uint16_t *__restrict__ x, int ldx,
     float *__restrict__ y, int ldy, const wg_epilogue e, int G, int S) {
@@ -314,7 +314,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_stream_kernel(
 #pragma unroll
           for (int p = 1; p < KS; p++) tot[m] += red[it][wave + p][row * M + m];
     }
-    if (part == 0) finish<M>(e, g, G, tot, scale, y, ldy);
+    if (part == 0) finish<M, MODE>(e, g, G, tot, scale, y, ldy);
   }
 }
 
@@ -324,8 +324,16 @@ int launch_kstream(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, 
   int G = w->N / 4, S = w->K / 256;
   constexpr int RGW = 4 / KS;
   int grid = persistent_grid((G + RGW - 1) / RGW, tuning("q4k_wg_per_cu"));
-  gemv_q4k_stream_kernel<M, NS, KS><<<grid, 256, 0, s>>>((const uint8_t *)w->quants, x, ldx, y,
-                                                          ldy, e, G, S);
+  auto q = (const uint8_t *)w->quants;
+  if (e.mode == WG_EPI_SWIGLU)
+    gemv_q4k_stream_kernel<M, NS, KS, WG_EPI_SWIGLU><<<grid, 256, 0, s>>>(q, x, ldx, y, ldy, e,
+                                                                         G, S);
+  else if (e.mode == WG_EPI_ROPE_KV)
+    gemv_q4k_stream_kernel<M, NS, KS, WG_EPI_ROPE_KV><<<grid, 256, 0, s>>>(q, x, ldx, y, ldy, e,
+                                                                          G, S);
+  else
+    gemv_q4k_stream_kernel<M, NS, KS, WG_EPI_STORE><<<grid, 256, 0, s>>>(q, x, ldx, y, ldy, e,
+                                                                        G, S);
   return launched("wg_q4_gemv (Q4_K)");
 }
 
@@ -351,8 +359,13 @@ template <int M>
 int launch_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
              const wg_epilogue &e, hipStream_t s) {
   int G = w->N / 4, S = w->K / 256;
-  gemv_q4k_kernel<M><<<(G + 3) / 4, 256, 0, s>>>((const uint8_t *)w->quants, x, ldx, y, ldy, e,
-                                                 G, S);
+  auto q = (const uint8_t *)w->quants;
+  if (e.mode == WG_EPI_SWIGLU)
+    gemv_q4k_kernel<M, WG_EPI_SWIGLU><<<(G + 3) / 4, 256, 0, s>>>(q, x, ldx, y, ldy, e, G, S);
+  else if (e.mode == WG_EPI_ROPE_KV)
+    gemv_q4k_kernel<M, WG_EPI_ROPE_KV><<<(G + 3) / 4, 256, 0, s>>>(q, x, ldx, y, ldy, e, G, S);
+  else
+    gemv_q4k_kernel<M, WG_EPI_STORE><<<(G + 3) / 4, 256, 0, s>>>(q, x, ldx, y, ldy, e, G, S);
   return launched("wg_q4_gemv (Q4_K)");
 }
 
