@@ -89,8 +89,9 @@ def oracle_matrix(m):
     return qm
 
 
-def cpu_baseline(engine, threads):
-    """Oracle split matmul (float32, shader order) on one layer + the head."""
+def cpu_baseline(engine, threads, seconds=12.0):
+    """Oracle split matmul (float32, shader order) on one layer + the head,
+    repeated for about `seconds` of CPU time."""
     import numpy as np
     from oracle import oracle as O
     s = engine.shape
@@ -101,20 +102,26 @@ def cpu_baseline(engine, threads):
     xs = {m.K: O.f32_to_h2(rng.standard_normal((1, m.K)).astype(np.float32))
           for m in layer + [head]}
     O.matmul_split(layer[0], xs[layer[0].K], threads)  # warm the threads
-    t0 = O.now()
-    for m in layer:
-        O.matmul_split(m, xs[m.K], threads)
-    t_layer = O.now() - t0
-    t0 = O.now()
-    O.matmul_split(head, xs[head.K], threads)
-    t_head = O.now() - t0
-    per_token = s.layers * t_layer + t_head
+    # repeat the layer + head sample until about `seconds` of CPU work is done
+    t_layer = t_head = 0.0
+    reps = 0
+    while reps < 400 and (t_layer + t_head < seconds or reps < 2):
+        t0 = O.now()
+        for m in layer:
+            O.matmul_split(m, xs[m.K], threads)
+        t1 = O.now()
+        O.matmul_split(head, xs[head.K], threads)
+        t_layer += t1 - t0
+        t_head += O.now() - t1
+        reps += 1
+    per_token = (s.layers * t_layer + t_head) / reps
     return {"value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": threads,
             "kind": "port",
             "sample": f"oracle shader-order fp32 split matmul (OpenMP, {threads} threads) on "
-                      f"layer 0's qkv/o/gate|up/down ({t_layer:.3f} s) and the 128256x4096 head "
-                      f"({t_head:.3f} s) at batch 1, extrapolated to 32 layers; attention "
-                      f"and norms not included"}
+                      f"layer 0's qkv/o/gate|up/down and the 128256x4096 head at batch 1, "
+                      f"{reps} repetitions ({t_layer + t_head:.1f} s: {t_layer / reps * 1e3:.1f} ms "
+                      f"a layer, {t_head / reps * 1e3:.1f} ms the head), extrapolated to 32 "
+                      f"layers; attention and norms not included"}
 
 
 def main():

@@ -323,6 +323,29 @@ def test_attention_closed_forms():
     kc2 = np.tile(kc[:1], (5, 1))
     a = O.attention_f64(q, kc2, vc, heads, kvh, hd, 5, stride)
     assert np.allclose(a[:hd], vf[:, :hd].mean(0))
+    # shift invariance: adding one vector c to every key adds q.c to every
+    # score of a head. Keys on a 1/8 grid stay exact halves after the shift.
+    kg = (rng.integers(-16, 16, (5, stride)) / 8).astype(np.float32)
+    c = (rng.integers(-8, 8, stride) / 8).astype(np.float32)
+    base = O.attention_f64(q, O.f32_to_h2(kg), vc, heads, kvh, hd, 5, stride)
+    shifted = O.attention_f64(q, O.f32_to_h2(kg + c), vc, heads, kvh, hd, 5, stride)
+    assert np.allclose(base, shifted, rtol=1e-9, atol=1e-12)
+    # the softmax weights really depend on the scores (a wrong sign fails)
+    assert not np.allclose(base, O.attention_f64(-q, O.f32_to_h2(kg), vc, heads, kvh, hd, 5,
+                                                 stride))
+    # causal: keys past the count are never read
+    kc3, vc3 = kc.copy(), vc.copy()
+    kc3[3:] = O.f32_to_h2(np.full((2, stride), 50.0, np.float32))
+    vc3[3:] = O.f32_to_h2(np.full((2, stride), -7.0, np.float32))
+    assert np.array_equal(O.attention_f64(q, kc, vc, heads, kvh, hd, 3, stride),
+                          O.attention_f64(q, kc3, vc3, heads, kvh, hd, 3, stride))
+    # a brute-force softmax for one head on the CPU
+    kf = O.halves_to_f32(kc).astype(np.float64)
+    s_ = kf[:, :hd] @ q[:hd].astype(np.float64)
+    wts = np.exp(s_ - s_.max())
+    wts /= wts.sum()
+    full = O.attention_f64(q, kc, vc, heads, kvh, hd, 5, stride)
+    assert np.allclose(full[:hd], wts @ vf[:, :hd], rtol=1e-12, atol=1e-12)
 
 
 def test_rope_and_norm_closed_forms():
@@ -344,8 +367,11 @@ def test_rope_and_norm_closed_forms():
             a = math.hypot(x[j], x[j + R // 2])
             b = math.hypot(y[j], y[j + R // 2])
             assert abs(a - b) < 1e-5 * max(1, a)
-        ang = math.atan2(y[R // 2], y[0]) - math.atan2(x[R // 2], x[0])
-        assert abs(math.remainder(ang - pos, 2 * math.pi)) < 1e-4
+        # pair j turns by pos * theta^(-2j/hd)
+        for j in (0, 1, 7, R // 2 - 1):
+            ang = math.atan2(y[j + R // 2], y[j]) - math.atan2(x[j + R // 2], x[j])
+            want = pos * 1e6 ** (-2 * j / hd)
+            assert abs(math.remainder(ang - want, 2 * math.pi)) < 1e-4
 
 
 def test_rms_norm_and_swiglu():
@@ -355,6 +381,9 @@ def test_rms_norm_and_swiglu():
     assert np.allclose(out, [[3 / r, 8 / r]])
     gu = np.array([[0.0, 2.0, 5.0, 7.0]], np.float32)
     assert np.allclose(O.swiglu(gu), [[0.0, 2 / (1 + math.exp(-2)) * 7]])
+    # silu(g) -> g for large g and -> 0 for very negative g
+    big = O.swiglu(np.array([[40.0, -40.0, 3.0, 3.0]], np.float32))
+    assert big[0, 0] == np.float32(120.0) and abs(big[0, 1]) < 1e-15
 
 
 # --- short convolution -----------------------------------------------------------
