@@ -30,40 +30,78 @@ METRIC = "Q4 GEMV HBM GB/s (% of peak); decode tok/s, 8B-shape Q4 batch 1"
 HBM_PEAK_GBPS = 8000.0
 
 
-def gemv_roofline(engine, reps=6):
+def gemv_roofline(mats, x, parts, out16, eps, reps=6):
     """Average duration of the gate|up GEMV, launched as the decode launches
-    it (prescaled norm in, SwiGLU out), over the layers' own matrices."""
+    it (prescaled norm in, SwiGLU out), over distinct matrices."""
     import torch
     from webgllm_amd import lib as L, ops
-    s = engine.shape
-    F, D = s.intermediate, s.hidden
-    mats = [lw["gate_up"] for lw in engine.w.layers]
-    x = engine.x16[:1]
-    ep = engine._norm_in(L.Epilogue(mode=L.EPI_SWIGLU, out16=engine.ff16.data_ptr(),
-                                    ld_out16=F))
+    m = mats[0]
+    F, D = m.N // 2, m.K
+    ep = L.Epilogue(mode=L.EPI_SWIGLU, out16=out16.data_ptr(), ld_out16=F,
+                    norm_parts=parts.data_ptr(), n_parts=D // 4, ld_parts_in=D // 4,
+                    norm_count=D, eps=eps, norm_mult=32.0)
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
-        for m in mats[:4]:
-            ops.gemv(m, x, epilogue=ep)
+        for mm in mats[:4]:
+            ops.gemv(mm, x, epilogue=ep)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(reps):
-            for m in mats:
-                ops.gemv(m, x, epilogue=ep)
+            for mm in mats:
+                ops.gemv(mm, x, epilogue=ep)
         e1.record(stream)
     stream.synchronize()
     launches = reps * len(mats)
     us = e0.elapsed_time(e1) * 1e3 / launches
-    m = mats[0]
     # weights (nibbles, half scales, half zero points) + x (halves) + the
     # norm's parts + the half SwiGLU output
     algo = m.nbytes + D * 2 + (D // 4) * 4 + F * 2
     achieved = algo / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": measured_traffic(),
             "kernel": f"gemv_stream_kernel gate|up {m.N}x{m.K} (Q4_K repacked: 4-bit + "
                       f"half scale + half zero per 32), SwiGLU epilogue",
             "bytes_per_launch": algo, "avg_launch_us": round(us, 3), "launches": launches}
+
+
+def measured_traffic():
+    """HBM bytes per launch of the gate|up GEMV from the FETCH_SIZE and
+    WRITE_SIZE counter runs of `bench.py --roofline-only`, each scaled by
+    what the counter reads for a copy of known size; the figure is kept in
+    the traffic summary beside the kernel's rocprof summary."""
+    path = os.path.join(ROOT, "profiles", "gemv_gate_up_llama8b_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1].replace(",", "").strip())
+    except OSError:
+        pass
+    return None
+
+
+def roofline_only(args):
+    """The gate|up GEMV alone over 32 distinct 28672 x 4096 Q4_K matrices,
+    then a 256 MiB device copy: a short program for counter runs."""
+    import torch
+    from webgllm_amd import engine as E
+    shape = E.LLAMA3_8B
+    F, D = shape.intermediate, shape.hidden
+    w = E.Weights.blank(shape, seed=0)
+    mats = [w.matrix(2 * F, D, E.gate_up_row_order(F)) for _ in range(shape.layers)]
+    x = (torch.randn((1, D), device="cuda") * 0.1).half()
+    parts = torch.ones((1, D // 4), device="cuda")
+    out16 = torch.zeros((1, F), dtype=torch.float16, device="cuda")
+    torch.cuda.synchronize()
+    roof = gemv_roofline(mats, x, parts, out16, shape.eps, reps=args.reps)
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)  # reads and writes 256 MiB: the counters' scale
+    torch.cuda.synchronize()
+    print(json.dumps({"roofline": roof, "copy_bytes_each_way": n, "copies": 3}), flush=True)
 
 
 def oracle_matrix(m):
@@ -132,11 +170,17 @@ def main():
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--layers", type=int, default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the gate|up GEMV launches and a copy (for counter runs)")
+    ap.add_argument("--reps", type=int, default=6, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(--gpus {args.gpus} asked)", file=sys.stderr)
         sys.exit(2)
+    if args.roofline_only:
+        roofline_only(args)
+        return
 
     import dataclasses
 
@@ -177,7 +221,8 @@ def main():
     ms = e0.elapsed_time(e1) / args.steps
     tok_s = 1000.0 / ms
 
-    roof = gemv_roofline(eng)
+    roof = gemv_roofline([lw["gate_up"] for lw in w.layers], eng.x16[:1], eng.parts[:1],
+                         eng.ff16[:1], shape.eps)
     kv_bytes = shape.layers * 2 * shape.kv_heads * shape.head_dim * 2 * (p0 + args.steps // 2)
     token_bytes = w.nbytes + kv_bytes
     cpu = None

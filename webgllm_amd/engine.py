@@ -136,6 +136,17 @@ class Weights:
                     lw["k_norm"] = self.norm(s.head_dim)
             self.layers.append(lw)
 
+    @classmethod
+    def blank(cls, shape: ModelShape, seed: int = 0, device="cuda") -> "Weights":
+        """The generator alone, with no matrices: matrix() then makes single
+        weight matrices of this shape's format."""
+        w = cls.__new__(cls)
+        w.shape, w.device = shape, device
+        w.g = torch.Generator(device=device)
+        w.g.manual_seed(seed)
+        w.embedding, w.final_norm, w.layers = None, None, []
+        return w
+
     def norm(self, n: int) -> torch.Tensor:
         return (1.0 + 0.1 * torch.randn(n, generator=self.g, device=self.device)).contiguous()
 
