@@ -173,6 +173,8 @@ def main():
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the gate|up GEMV launches and a copy (for counter runs)")
     ap.add_argument("--reps", type=int, default=6, help=argparse.SUPPRESS)
+    ap.add_argument("--persistent", action="store_true",
+                    help="decode every layer in one persistent launch (wg_decode_run)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -193,7 +195,7 @@ def main():
         shape = dataclasses.replace(shape, layers=args.layers)
     t0 = time.time()
     w = E.Weights(shape, seed=0)
-    eng = E.Engine(w, args.ctx)
+    eng = E.Engine(w, args.ctx, persistent=args.persistent)
     prompt_len = args.ctx - args.warmup - args.steps - 1
     rng = torch.Generator().manual_seed(1)
     prompt = torch.randint(0, shape.vocab, (prompt_len,), generator=rng).tolist()
@@ -251,6 +253,7 @@ def main():
                        "reference's 32-blocks (packQ4_K)",
             "activations": "f16", "accumulate": "f32",
             "global_batch": 1, "seq_len": args.ctx, "parallelism": "none",
+            "decode_path": "persistent" if eng.plan is not None else "per-op kernels",
         },
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -237,6 +237,53 @@ int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda,
 /* float32 -> half activations, clamped to +-65504 (packH2, kernels.ts:32-36). */
 int wg_f32_to_f16(const float *x, uint16_t *out, int64_t n, void *stream);
 
+/* ---------------------------------------------- persistent batch-1 decode
+ * The attention layers of one token's forward (Engine.forwardBatch at one
+ * row, src/engine.ts:8875-9303: per layer the qkv matmul with RoPE and the
+ * KV write, attention over the cache, o + residual + norm, gate|up +
+ * SwiGLU, down + residual + the next norm) in ONE launch: a persistent
+ * workgroup per compute-unit slot runs the phases in order, with a grid
+ * barrier between them, and loads its first weights of the next phase
+ * before it waits at a barrier, so weight streaming continues across phase
+ * boundaries. Each layer is given as the four wg_q4_gemv calls (M = 1) the
+ * per-op path makes:
+ *  - qkv: WG_EPI_ROPE_KV (q_out, the caches, pos0 and ctx define the
+ *    attention too);
+ *  - o: WG_EPI_STORE, x = the attention output (heads * head_dim halves);
+ *  - gate_up: WG_EPI_SWIGLU, its out16 = down's x;
+ *  - down: WG_EPI_STORE.
+ * All matrices ROWGROUP with one zero kind; head_dim 64 or 128; at most 8
+ * query heads per KV head and 64 KV heads; ctx <= 16384. Unsupported
+ * shapes return WG_ERR_UNSUPPORTED at plan creation. The plan copies the
+ * calls to device memory and owns its attention partials and barrier
+ * state; wg_decode_run launches one kernel (capturable in a graph: it
+ * allocates nothing and sets no memory). Runs of one plan must not
+ * overlap. A barrier wait that runs past its poll limit ends the kernel
+ * early with its results undefined and is reported by wg_decode_status. */
+typedef struct {
+  wg_q4_matrix w;
+  const uint16_t *x;
+  int32_t ldx;
+  float *y;
+  int32_t ldy;
+  wg_epilogue ep;
+} wg_gemv_call;
+
+typedef struct {
+  wg_gemv_call qkv, o, gate_up, down;
+} wg_decode_layer;
+
+typedef struct wg_decode_plan wg_decode_plan;
+
+int wg_decode_plan_create(const wg_decode_layer *layers, int32_t n_layers, wg_decode_plan **out);
+int wg_decode_run(wg_decode_plan *plan, void *stream);
+/* After the stream has finished: WG_OK, or WG_ERR_DEVICE if a barrier wait
+ * ran past its limit (the plan's barrier state is then reset). */
+int wg_decode_status(wg_decode_plan *plan);
+/* The polls a barrier wait makes before it gives up (default 1 << 20). */
+int wg_decode_set_spin_limit(wg_decode_plan *plan, int32_t polls);
+int wg_decode_plan_destroy(wg_decode_plan *plan);
+
 /* ---------------------------------------------- residual-stream glue */
 
 /* RMS norm into half activations (RMS_SCALE + NORM_TO_H2,

@@ -16,13 +16,13 @@
 // running max (attendPanelCombine's online softmax) into half outputs.
 // The position comes from device memory so a captured graph replays at any
 // position; chunks past the last key leave at once.
+#include "attn_core.h"
 #include "common.h"
 #include "dot.h"
 
 namespace wg {
 namespace {
 
-constexpr int CHUNK = 64;        // keys a workgroup takes
 constexpr int MAX_HD = 256;
 
 __device__ inline uint16_t to_h(float v) {
@@ -85,115 +85,18 @@ __global__ __launch_bounds__(64) void head_prep_kernel(
   }
 }
 
-// Partial results of one (query row, query head, chunk): the chunk's max
-// score, its sum of exp(score - max), and the weighted values.
-struct PartialLayout {
-  int hd, chunks;
-  __device__ int64_t base(int qh_row, int chunk) const {
-    return ((int64_t)qh_row * chunks + chunk) * (hd + 2);
-  }
-};
-
-// Workgroup = (KV head kh, chunk c). Queries: rows m < M of heads
-// kh * G .. kh * G + G - 1, GM = G * M of them.
+// Workgroup = (KV head kh, chunk c); chunks past the last key leave at once.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_chunk_kernel(
     const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
     const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int chunks) {
-  constexpr int KSTR = HD + 2;  // LDS row stride in halves (breaks bank conflicts)
-  // LDS, sized by the launch for GM = G * M queries: K and V tiles, the
-  // queries, the chunk's scores, and per query its max and sum of weights.
   extern __shared__ __align__(16) unsigned char smem[];
-  const int GMq = (H / KV) * M;
-  uint16_t *ks = reinterpret_cast<uint16_t *>(smem);
-  uint16_t *vs = ks + CHUNK * KSTR;
-  float *qs = reinterpret_cast<float *>(vs + CHUNK * KSTR);
-  float *sc = qs + GMq * HD;
-  float *mx = sc + GMq * CHUNK;
-  float *lsum = mx + GMq;
-  const int kh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
   const int pos0 = *pos0_dev;
   // The last row sees keys 0 .. pos0 + M - 1; never more than the cache holds.
   const int n_keys = min(pos0 + M, max_keys);
-  const int j0 = c * CHUNK;
-  if (j0 >= n_keys) return;
-  const int G = H / KV, GM = G * M;
-  const int kvd = KV * HD;
-  const int nk = min(CHUNK, n_keys - j0);
-  // Stage K and V rows j0 .. j0 + nk - 1 of head kh: 16-byte pieces.
-  constexpr int PIECES = HD / 8;
-  for (int i = tid; i < nk * PIECES; i += 256) {
-    int r = i / PIECES, p = i % PIECES;
-    const uint4 *kp = reinterpret_cast<const uint4 *>(k_cache + (int64_t)(j0 + r) * kvd + kh * HD);
-    const uint4 *vp = reinterpret_cast<const uint4 *>(v_cache + (int64_t)(j0 + r) * kvd + kh * HD);
-    uint4 kv = kp[p], vv = vp[p];
-    uint32_t *kd = reinterpret_cast<uint32_t *>(ks + r * KSTR + p * 8);
-    uint32_t *vd = reinterpret_cast<uint32_t *>(vs + r * KSTR + p * 8);
-    kd[0] = kv.x; kd[1] = kv.y; kd[2] = kv.z; kd[3] = kv.w;
-    vd[0] = vv.x; vd[1] = vv.y; vd[2] = vv.z; vd[3] = vv.w;
-  }
-  for (int i = tid; i < GM * HD; i += 256) {
-    int qi = i / HD, d = i % HD;
-    int g = qi % G, m = qi / G;
-    qs[i] = q[(int64_t)m * ldq + (int64_t)(kh * G + g) * HD + d];
-  }
-  __syncthreads();
-  // Scores, causal: row m sees keys j <= pos0 + m.
-  for (int i = tid; i < GM * CHUNK; i += 256) {
-    int qi = i / CHUNK, r = i % CHUNK;
-    int m = qi / G;
-    float s = -INFINITY;
-    if (r < nk && j0 + r <= pos0 + m) {
-      const float *qv = qs + qi * HD;
-      const uint16_t *kr = ks + r * KSTR;
-      float a = 0.0f;
-#pragma unroll 8
-      for (int d = 0; d < HD; d += 2) {
-        uint32_t k2 = *reinterpret_cast<const uint32_t *>(kr + d);
-        half2v kk = as_h2(k2);
-        a = __builtin_fmaf(qv[d], (float)kk.x, a);
-        a = __builtin_fmaf(qv[d + 1], (float)kk.y, a);
-      }
-      s = a;
-    }
-    sc[i] = s;
-  }
-  __syncthreads();
-  // Per query: the chunk's max and sum of weights (one wave per query).
-  const int wave = tid >> 6, lane = tid & 63;
-  for (int qi = wave; qi < GM; qi += 4) {
-    float v = lane < CHUNK ? sc[qi * CHUNK + lane] : -INFINITY;
-    float m_ = v;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m_ = fmaxf(m_, __shfl_xor(m_, off, 64));
-    float e = (m_ == -INFINITY || v == -INFINITY) ? 0.0f : __expf(v - m_);
-    if (lane < CHUNK) sc[qi * CHUNK + lane] = e;
-    float l = wave_sum(e);
-    if (lane == 0) {
-      mx[qi] = m_;
-      lsum[qi] = l;
-    }
-  }
-  __syncthreads();
-  // Weighted values.
-  PartialLayout pl{HD, chunks};
-  for (int i = tid; i < GM * HD; i += 256) {
-    int qi = i / HD, d = i % HD;
-    const float *e = sc + qi * CHUNK;
-    float a = 0.0f;
-    for (int r = 0; r < nk; r++) {
-      half2v vv = as_h2(*reinterpret_cast<const uint32_t *>(vs + r * KSTR + (d & ~1)));
-      a = __builtin_fmaf(e[r], (float)((d & 1) ? vv.y : vv.x), a);
-    }
-    int g = qi % G, m = qi / G;
-    int row = m * H + kh * G + g;
-    float *out = partial + pl.base(row, c);
-    out[2 + d] = a;
-    if (d == 0) {
-      out[0] = mx[qi];
-      out[1] = lsum[qi];
-    }
-  }
+  if ((int)blockIdx.y * CHUNK >= n_keys) return;
+  attn_chunk_item<HD>(q, ldq, M, H, KV, k_cache, v_cache, pos0, n_keys, blockIdx.x, blockIdx.y,
+                      partial, chunks, smem);
 }
 
 // One workgroup of 256 per (query head h, row m): the chunks' online-softmax
@@ -299,11 +202,6 @@ int wg_head_prep(const float *qkv, int32_t M, int32_t ldq, const wg_attn_shape *
       qkv, ldq, sh->heads, sh->kv_heads, sh->head_dim, sh->rotated_dims, sh->eps, sh->use_norm,
       q_norm, k_norm, rope, rope_rows, pos0, q_out, ldqo, k_cache, v_cache, ctx);
   return launched("wg_head_prep");
-}
-
-static size_t attn_lds_bytes(int GM, int hd) {
-  return (size_t)2 * CHUNK * (hd + 2) * 2 + (size_t)GM * hd * 4 + (size_t)GM * CHUNK * 4 +
-         (size_t)GM * 8;
 }
 
 size_t wg_attn_scratch_bytes(int32_t M, int32_t heads, int32_t head_dim, int32_t max_keys) {

@@ -24,76 +24,10 @@
 #include "dot.h"
 #include "kernels.h"
 #include "epilogue.h"
+#include "gemv_core.h"
 
 namespace wg {
 namespace {
-
-// The 16 fp16-subnormal nibble pairs of one 16-byte block row, in the
-// order the activation pairs come: for word w, (q[4w], q[4w+1]) and
-// (q[4w+2], q[4w+3]) (low nibbles, factor 1), then (q[16+4w], q[17+4w]) and
-// (q[18+4w], q[19+4w]) (high nibbles, factor 16).
-struct Nibbles {
-  uint32_t lo[8], hi[8];
-};
-
-__device__ inline void unpack(const uint4 &q, Nibbles &n) {
-  uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    uint32_t p0 = __builtin_amdgcn_perm(0u, w[i], SEL01);
-    uint32_t p1 = __builtin_amdgcn_perm(0u, w[i], SEL23);
-    n.lo[2 * i] = p0 & LO4;
-    n.lo[2 * i + 1] = p1 & LO4;
-    n.hi[2 * i] = p0 & HI4;
-    n.hi[2 * i + 1] = p1 & HI4;
-  }
-}
-
-// sum q a over a block, times 2^-24: a[0..3] are the 32 activations as 16
-// half pairs, a[0], a[1] elements 0..15, a[2], a[3] 16..31.
-__device__ inline float block_dot(const Nibbles &n, const uint4 *a) {
-  const uint32_t lo_a[8] = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w};
-  const uint32_t hi_a[8] = {a[2].x, a[2].y, a[2].z, a[2].w, a[3].x, a[3].y, a[3].z, a[3].w};
-  float lo = 0.0f, hi = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    lo = dot2(n.lo[i], lo_a[i], lo);
-    hi = dot2(n.hi[i], hi_a[i], hi);
-  }
-  return __builtin_fmaf(hi, 0.0625f, lo);
-}
-
-__device__ inline float block_sum(const uint4 *a) {
-  float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    s0 = dot2(a[i].x, ONES, s0);
-    s1 = dot2(a[i].y, ONES, s1);
-    s0 = dot2(a[i].z, ONES, s0);
-    s1 = dot2(a[i].w, ONES, s1);
-  }
-  return s0 + s1;
-}
-
-template <int ZK>
-__device__ inline void load_zeros(const void *zeros, int64_t si, float z[4]) {
-  if constexpr (ZK == WG_ZERO_8) {
-    z[0] = z[1] = z[2] = z[3] = 8.0f;
-  } else if constexpr (ZK == WG_ZERO_U8) {
-    uint32_t v = *reinterpret_cast<const uint32_t *>((const uint8_t *)zeros + si);
-    z[0] = (float)(v & 0xffu);
-    z[1] = (float)((v >> 8) & 0xffu);
-    z[2] = (float)((v >> 16) & 0xffu);
-    z[3] = (float)(v >> 24);
-  } else {
-    uint2 v = *reinterpret_cast<const uint2 *>((const uint16_t *)zeros + si);
-    z[0] = (float)as_h2(v.x).x;
-    z[1] = (float)as_h2(v.x).y;
-    z[2] = (float)as_h2(v.y).x;
-    z[3] = (float)as_h2(v.y).y;
-  }
-}
-
 
 template <int M, int ZK, int MODE>
 __global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
@@ -158,41 +92,6 @@ __global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
 // sums it loads once into registers: they are the same for every row
 // group. Row groups are streamed: the next row group's nibbles, scales and
 // zero points are loaded before the current one is computed.
-template <int ZK, int NB>
-struct Unit {
-  uint4 q[NB][4];
-  uint2 sc[NB];
-  uint2 zr[NB];  // u8: .x holds 4 zero points; f16: 4 halves
-};
-
-template <int ZK, int NB>
-__device__ inline void load_unit(Unit<ZK, NB> &u, const uint4 *__restrict__ quants,
-                                 const uint16_t *__restrict__ scales,
-                                 const void *__restrict__ zeros, int g, int B, int b0, int b_end,
-                                 bool live) {
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    int b = b0 + 64 * j;
-    if (live && b < b_end) {
-      int64_t si = ((int64_t)g * B + b) * 4;
-      const uint4 *qp = quants + si;
-      u.q[j][0] = qp[0];
-      u.q[j][1] = qp[1];
-      u.q[j][2] = qp[2];
-      u.q[j][3] = qp[3];
-      u.sc[j] = *reinterpret_cast<const uint2 *>(scales + si);
-      if constexpr (ZK == WG_ZERO_U8)
-        u.zr[j].x = *reinterpret_cast<const uint32_t *>((const uint8_t *)zeros + si);
-      if constexpr (ZK == WG_ZERO_F16)
-        u.zr[j] = *reinterpret_cast<const uint2 *>((const uint16_t *)zeros + si);
-    } else {
-      u.sc[j] = make_uint2(0u, 0u);  // scale 0: contributes nothing
-      u.q[j][0] = u.q[j][1] = u.q[j][2] = u.q[j][3] = make_uint4(0u, 0u, 0u, 0u);
-      u.zr[j] = make_uint2(0u, 0u);
-    }
-  }
-}
-
 template <int M, int ZK, int NB, int KS, int MODE>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(
     const uint4 *__restrict__ quants, const uint16_t *__restrict__ scales,
@@ -248,37 +147,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
     for (int r = 0; r < 4; r++)
 #pragma unroll
       for (int m = 0; m < M; m++) acc[r][m] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-      float d[4] = {(float)as_h2(u.sc[j].x).x, (float)as_h2(u.sc[j].x).y,
-                    (float)as_h2(u.sc[j].y).x, (float)as_h2(u.sc[j].y).y};
-      float z[4];
-      if constexpr (ZK == WG_ZERO_8) {
-        z[0] = z[1] = z[2] = z[3] = 8.0f;
-      } else if constexpr (ZK == WG_ZERO_U8) {
-        uint32_t v = u.zr[j].x;
-        z[0] = (float)(v & 0xffu);
-        z[1] = (float)((v >> 8) & 0xffu);
-        z[2] = (float)((v >> 16) & 0xffu);
-        z[3] = (float)(v >> 24);
-      } else {
-        z[0] = (float)as_h2(u.zr[j].x).x;
-        z[1] = (float)as_h2(u.zr[j].x).y;
-        z[2] = (float)as_h2(u.zr[j].y).x;
-        z[3] = (float)as_h2(u.zr[j].y).y;
-      }
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        Nibbles n;
-        unpack(u.q[j][r], n);
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-          float v = block_dot(n, a[m][j]);
-          v = __builtin_fmaf(-z[r], sa[m][j], v);
-          acc[r][m] = __builtin_fmaf(d[r], v, acc[r][m]);
-        }
-      }
-    }
+    accumulate_unit<M, ZK, NB>(u, a, sa, acc);
     const int row = wave_sum4_row();
     float tot[M];
 #pragma unroll
@@ -385,14 +254,9 @@ __global__ void f32_to_f16_kernel(const float *x, uint16_t *out, int64_t n) {
 }
 
 }  // namespace
-}  // namespace wg
-
-using namespace wg;
-
-extern "C" {
 
 // Checks an epilogue against the matrix and the row count.
-static int check_epilogue(const wg_q4_matrix *w, int M, const float *y, int ldy,
+int check_epilogue(const wg_q4_matrix *w, int M, const float *y, int ldy,
                           const wg_epilogue &e) {
   const int N = w->N, G = N / 4;
   WG_REQUIRE(e.mode == WG_EPI_STORE || e.mode == WG_EPI_SWIGLU || e.mode == WG_EPI_ROPE_KV,
@@ -435,6 +299,11 @@ static int check_epilogue(const wg_q4_matrix *w, int M, const float *y, int ldy,
   }
   return WG_OK;
 }
+}  // namespace wg
+
+using namespace wg;
+
+extern "C" {
 
 int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx, float *y,
                int32_t ldy, const wg_epilogue *ep, void *stream) {

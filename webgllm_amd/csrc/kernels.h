@@ -5,6 +5,10 @@
 
 namespace wg {
 
+// The epilogue checks of wg_q4_gemv for M rows (0, or a status with the
+// error message set).
+int check_epilogue(const wg_q4_matrix *w, int M, const float *y, int ldy, const wg_epilogue &e);
+
 int launch_gemv_q4k(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y, int ldy,
                     const wg_epilogue &e, hipStream_t s);
 

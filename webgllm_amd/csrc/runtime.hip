@@ -62,6 +62,7 @@ static Knob g_knobs[] = {
     {"gemv_wg_per_cu_wide", 8, 1, 16},   // the same for matrices of 16384+ row groups
     {"q4k_wg_per_cu", 2, 1, 16},         // persistent Q4_K GEMV workgroups per CU
     {"gemv_min_waves", 8192, 0, 1 << 20},  // split K within a workgroup below this
+    {"decode_wg_per_cu", 1, 1, 4},       // persistent decode workgroups (8 waves) per CU
 };
 
 int tuning(const char *name) {

@@ -199,7 +199,7 @@ class Weights:
 class Engine:
     """Forward, greedy pick and accept over device-resident weights."""
 
-    def __init__(self, weights: Weights, ctx: int):
+    def __init__(self, weights: Weights, ctx: int, persistent: bool = False):
         s = self.shape = weights.shape
         self.w = weights
         self.ctx = ctx
@@ -240,6 +240,12 @@ class Engine:
         self.position = 0
         self.draft = None
         self.graph = None
+        # persistent=True: single-row forwards of attention-only models run as
+        # one persistent launch (wg_decode_run); other shapes, and the
+        # default, take the per-op path. On MI355X a grid barrier costs about
+        # as much as a kernel boundary (~4 us), so the per-op path is the
+        # faster one at the Llama-3-8B shape.
+        self.plan = self._build_plan() if persistent else None
 
     # --- the batch ------------------------------------------------------------
     def _norm_in(self, ep: "L.Epilogue") -> "L.Epilogue":
@@ -261,6 +267,54 @@ class Engine:
                           norm_mult_out=PRESCALE, parts_out=self.parts.data_ptr(),
                           ld_parts_out=D // 4)
 
+    def _qkv_epilogue(self, i: int) -> "L.Epilogue":
+        """qkv's epilogue when RoPE and the KV write are fused into it."""
+        s = self.shape
+        return self._norm_in(L.Epilogue(
+            mode=L.EPI_ROPE_KV, heads=s.heads, kv_heads=s.kv_heads,
+            head_dim=s.head_dim, ctx=self.ctx, rope_rows=self.rope.shape[0],
+            rope=self.rope.data_ptr(), pos0=self.pos.data_ptr(),
+            q_out=self.q.data_ptr(), ld_q_out=s.heads * s.head_dim,
+            k_cache=self.k_cache[i].data_ptr(), v_cache=self.v_cache[i].data_ptr()))
+
+    def _next_norm(self, i: int) -> torch.Tensor:
+        w = self.w
+        return w.layers[i + 1]["op_norm"] if i + 1 < len(w.layers) else w.final_norm
+
+    def _build_plan(self):
+        """The persistent decode plan of every layer at one row, or None when
+        a layer is not attention with RoPE in the qkv epilogue, or the
+        library does not support the shape (e.g. native Q4_K matrices)."""
+        s, w = self.shape, self.w
+        if not s.rope_in_epilogue or not w.layers or \
+                any(s.layer_type(i) == "conv" for i in range(s.layers)):
+            return None
+        F = s.intermediate
+        x16, h = self.x16[:1], self.h[:1]
+        layers = []
+        for i, lw in enumerate(w.layers):
+            layers.append(L.DecodeLayer(
+                qkv=ops.gemv_call(lw["qkv"], x16, epilogue=self._qkv_epilogue(i)),
+                o=ops.gemv_call(lw["o"], self.att16[:1], out=h,
+                                epilogue=self._residual_out(1, lw["ffn_norm"])),
+                gate_up=ops.gemv_call(lw["gate_up"], x16, epilogue=self._norm_in(
+                    L.Epilogue(mode=L.EPI_SWIGLU, out16=self.ff16.data_ptr(), ld_out16=F))),
+                down=ops.gemv_call(lw["down"], self.ff16[:1], out=h,
+                                   epilogue=self._residual_out(1, self._next_norm(i)))))
+        try:
+            return ops.DecodePlan(layers)
+        except L.WgError as e:
+            if e.kind == "unsupported":
+                return None
+            raise
+
+    def check_plan(self) -> None:
+        """Raises if a persistent launch's barrier wait gave up (waits for
+        the current stream first)."""
+        if self.plan is not None:
+            torch.cuda.current_stream().synchronize()
+            self.plan.status()
+
     def _forward_rows(self, M: int, keep_prefixes: bool) -> None:
         """Enqueue one batch of M rows (ids[:M] at positions pos..pos+M-1)."""
         s, w = self.shape, self.w
@@ -272,7 +326,10 @@ class Engine:
                   epilogue=L.Epilogue(mode=L.EPI_STORE, out16=self.x16.data_ptr(), ld_out16=D,
                                       out16_w=first_norm.data_ptr(), norm_mult_out=PRESCALE,
                                       parts_out=self.parts.data_ptr(), ld_parts_out=D // 4))
-        for i, lw in enumerate(w.layers):
+        persistent = M == 1 and self.plan is not None
+        if persistent:
+            self.plan.run()
+        for i, lw in enumerate(() if persistent else w.layers):
             if s.layer_type(i) == "conv":
                 bcx = self.bcx[:M]
                 ops.gemv(lw["in_proj"], x16, out=bcx,
@@ -285,13 +342,7 @@ class Engine:
                          epilogue=self._residual_out(M, lw["ffn_norm"]))
             else:
                 if s.rope_in_epilogue:
-                    ep = self._norm_in(L.Epilogue(
-                        mode=L.EPI_ROPE_KV, heads=s.heads, kv_heads=s.kv_heads,
-                        head_dim=s.head_dim, ctx=self.ctx, rope_rows=self.rope.shape[0],
-                        rope=self.rope.data_ptr(), pos0=self.pos.data_ptr(),
-                        q_out=self.q.data_ptr(), ld_q_out=s.heads * s.head_dim,
-                        k_cache=self.k_cache[i].data_ptr(), v_cache=self.v_cache[i].data_ptr()))
-                    ops.gemv(lw["qkv"], x16, epilogue=ep)
+                    ops.gemv(lw["qkv"], x16, epilogue=self._qkv_epilogue(i))
                 else:
                     qkv = self.qkv[:M]
                     ops.gemv(lw["qkv"], x16, out=qkv,
@@ -306,8 +357,8 @@ class Engine:
             ops.gemv(lw["gate_up"], x16,
                      epilogue=self._norm_in(L.Epilogue(mode=L.EPI_SWIGLU,
                                                        out16=self.ff16.data_ptr(), ld_out16=F)))
-            nxt = w.layers[i + 1]["op_norm"] if i + 1 < len(w.layers) else w.final_norm
-            ops.gemv(lw["down"], self.ff16[:M], out=h, epilogue=self._residual_out(M, nxt))
+            ops.gemv(lw["down"], self.ff16[:M], out=h,
+                     epilogue=self._residual_out(M, self._next_norm(i)))
         ops.gemv(w.embedding, x16, out=self.logits[:M],
                  epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
         ops.argmax_rows(self.logits[:M], ids=self.next_ids[:M], tops=self.tops[:M],
@@ -343,7 +394,10 @@ class Engine:
             out = self.next_ids[:M]
         if draft:
             self.draft = (self.position - len(tokens), len(tokens))
-        return out.clone()
+        out = out.clone()
+        if len(tokens) % MAX_ROWS == 1:
+            self.check_plan()
+        return out
 
     def accept(self, count: int) -> None:
         """Keeps the first `count` tokens of the last draft batch
@@ -410,7 +464,9 @@ class Engine:
         for _ in range(steps):
             self.graph.replay()
         self.position += steps
-        return self.hist[p0 + 1:p0 + steps + 1].tolist()
+        toks = self.hist[p0 + 1:p0 + steps + 1].tolist()
+        self.check_plan()
+        return toks
 
 
 def _rope_table(theta: float, head_dim: int, ctx: int) -> torch.Tensor:
