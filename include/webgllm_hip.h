@@ -44,7 +44,9 @@ const char *wg_version(void);
  * "gemv_wg_per_cu", "gemv_wg_per_cu_wide" (matrices of 16384+ row groups),
  * "q4k_wg_per_cu" (persistent GEMV workgroups per compute unit) and
  * "gemv_min_waves" (below this many waves a GEMV splits K inside a
- * workgroup). Process-wide; results never depend on them. */
+ * workgroup) and "decode_wg_per_cu" (persistent decode workgroups per
+ * compute unit, read at plan creation). Process-wide; results never depend
+ * on them. */
 int wg_tuning_set(const char *name, int32_t value);
 int wg_tuning_get(const char *name, int32_t *value);
 
@@ -333,7 +335,11 @@ int wg_head_prep(const float *qkv, int32_t M, int32_t ldq, const wg_attn_shape *
  * kernels.ts:2386-2579, :2803-3027): row m's query at position *pos0 + m
  * attends keys 0..*pos0 + m (causal) of its KV head; half output. max_keys
  * is how many rows the caches hold (the position is clamped to it);
- * scratch holds wg_attn_scratch_bytes(M, heads, head_dim, max_keys) bytes. */
+ * (at most 16384); scratch holds wg_attn_scratch_bytes(M, heads, head_dim,
+ * max_keys) bytes of per-chunk partial results; calls that share a scratch
+ * must not overlap. Two launches: the chunks of 64 keys (a wave per query
+ * when heads / kv_heads * M <= 8, else an LDS-staged workgroup per chunk),
+ * then the online-softmax combine. */
 size_t wg_attn_scratch_bytes(int32_t M, int32_t heads, int32_t head_dim, int32_t max_keys);
 int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *shape,
                    const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0,

