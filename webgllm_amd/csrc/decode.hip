@@ -184,6 +184,9 @@ __device__ void gemv_phase(const Phase &P, const Unit<ZK, NB> &first, float (*re
   const int stride = gridDim.x * o.rgw;
   int g = blockIdx.x * o.rgw + o.slot;
   Unit<ZK, NB> next = first;
+  const int pos0 = epi_pos0<MODE>(e);
+  EpiPre pnext = {};
+  if (o.part == 0) epi_prefetch<1, MODE>(e, g, o.G, pos0, pnext);
 
   uint4 a[1][NB][4];
   float sa[1][NB];
@@ -210,6 +213,8 @@ __device__ void gemv_phase(const Phase &P, const Unit<ZK, NB> &first, float (*re
     Unit<ZK, NB> u = next;
     load_unit<ZK, NB>(next, quants, scales, zeros, g + stride, o.B, o.b0, o.b_end,
                       g + stride < o.G);
+    const EpiPre pe = pnext;
+    if (o.part == 0) epi_prefetch<1, MODE>(e, g + stride, o.G, pos0, pnext);
     float acc[4][1] = {{0.0f}, {0.0f}, {0.0f}, {0.0f}};
     accumulate_unit<1, ZK, NB>(u, a, sa, acc);
     const int row = wave_sum4_row();
@@ -220,7 +225,7 @@ __device__ void gemv_phase(const Phase &P, const Unit<ZK, NB> &first, float (*re
       if (o.part == 0)
         for (int p = 1; p < KS; p++) tot[0] += red[it][wave + p][row];
     }
-    if (o.part == 0) finish<1, MODE>(e, g, o.G, tot, scale, P.c.y, P.c.ldy);
+    if (o.part == 0) finish<1, MODE>(e, g, o.G, tot, scale, P.c.y, P.c.ldy, pe, pos0);
   }
 }
 

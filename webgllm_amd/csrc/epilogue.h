@@ -42,6 +42,54 @@ __device__ inline void input_scales(const wg_epilogue &e, float s[M]) {
   }
 }
 
+// The epilogue's operands of one row group that do not depend on its sums,
+// loaded ahead (with the row group's weights) so the epilogue does not wait
+// for memory: the residual and the next norm's weight (STORE), the rope
+// table entries of the lane's dim at its position (ROPE_KV).
+struct EpiPre {
+  float res, w16;
+  float c1, s1, c2, s2;
+};
+
+// The position the epilogue uses (ROPE_KV), read once per kernel.
+template <int MODE>
+__device__ inline int epi_pos0(const wg_epilogue &e) {
+  if constexpr (MODE == WG_EPI_ROPE_KV) return *e.pos0;
+  return 0;
+}
+
+// Row (4 g + r, r = lane / 16 % 4) for token m = lane % 16 (m < M): the
+// operands finish<M, MODE> needs. g >= G loads nothing.
+template <int M, int MODE>
+__device__ inline void epi_prefetch(const wg_epilogue &e, int g, int G, int pos0, EpiPre &p) {
+  const int lane = threadIdx.x & 63;
+  const int r = (lane >> 4) & 3, m = lane & 15;
+  const bool live = g < G && m < M;
+  const int n = 4 * g + r;
+  p.res = p.w16 = p.c1 = p.s1 = p.c2 = p.s2 = 0.0f;
+  if constexpr (MODE == WG_EPI_STORE) {
+    if (live && e.residual) p.res = e.residual[(int64_t)m * e.ld_residual + n];
+    if (live && e.out16) p.w16 = e.out16_w[n];
+  } else if constexpr (MODE == WG_EPI_ROPE_KV) {
+    const int hd = e.head_dim, P = hd / 2;
+    const int qd = e.heads * hd, kd = e.kv_heads * hd;
+    const int row = 4 * g;
+    const int pos = live ? pos0 + m : -1;
+    const bool in_cache = pos >= 0 && pos < e.ctx && 1024 + (pos >> 10) < e.rope_rows;
+    if (in_cache && row < qd + kd) {
+      const int base = row < qd ? 0 : qd;
+      const int i = ((row - base) % hd) / 4;
+      const int f = (2 * i + (r >> 1) + ((r & 1) ? P : 0)) % P;
+      const float *r_lo = e.rope + (int64_t)(pos & 1023) * hd;
+      const float *r_hi = e.rope + (int64_t)(1024 + (pos >> 10)) * hd;
+      p.c1 = r_lo[f];
+      p.s1 = r_lo[P + f];
+      p.c2 = r_hi[f];
+      p.s2 = r_hi[P + f];
+    }
+  }
+}
+
 // Picks tot[m] for this lane's token without dynamic register indexing.
 template <int M>
 __device__ inline float pick(const float tot[M], int m) {
@@ -52,11 +100,13 @@ __device__ inline float pick(const float tot[M], int m) {
   return v;
 }
 
-// Row group g's four rows for tokens 0..M-1. Called by every lane of the
-// wave (the shuffles need all of them), with g >= G for idle waves.
+// Row group g's four rows for tokens 0..M-1, with the operands
+// epi_prefetch<M, MODE> loaded for g. Called by every lane of the wave (the
+// shuffles need all of them), with g >= G for idle waves.
 template <int M, int MODE>
 __device__ inline void finish(const wg_epilogue &e, int g, int G, const float tot[M],
-                              const float scale[M], float *y, int ldy) {
+                              const float scale[M], float *y, int ldy, const EpiPre &pre,
+                              int pos0) {
   const int lane = threadIdx.x & 63;
   const int r = (lane >> 4) & 3, m = lane & 15;
   const bool live = g < G && m < M;
@@ -64,10 +114,10 @@ __device__ inline void finish(const wg_epilogue &e, int g, int G, const float to
   float v = pick<M>(tot, mm) * 0x1p24f * scale[mm];
   const int n = 4 * g + r;
   if constexpr (MODE == WG_EPI_STORE) {
-    if (live && e.residual) v += e.residual[(int64_t)m * e.ld_residual + n];
+    if (live && e.residual) v += pre.res;
     if (live && y) y[(int64_t)m * ldy + n] = v;
     if (live && e.out16)
-      e.out16[(int64_t)m * e.ld_out16 + n] = half_bits(v * e.out16_w[n] / e.norm_mult_out);
+      e.out16[(int64_t)m * e.ld_out16 + n] = half_bits(v * pre.w16 / e.norm_mult_out);
     if (e.parts_out) {
       float sq = live ? v * v : 0.0f;
       sq += __shfl_xor(sq, 16, 64);
@@ -87,7 +137,7 @@ __device__ inline void finish(const wg_epilogue &e, int g, int G, const float to
     const int qd = e.heads * hd, kd = e.kv_heads * hd;
     float partner = __shfl_xor(v, 16, 64);  // rows 0 <-> 1 and 2 <-> 3
     const int row = 4 * g;
-    int pos = live ? *e.pos0 + m : -1;
+    int pos = live ? pos0 + m : -1;
     bool in_cache = pos >= 0 && pos < e.ctx && 1024 + (pos >> 10) < e.rope_rows;
     if (row < qd + kd) {
       const bool is_q = row < qd;
@@ -97,13 +147,9 @@ __device__ inline void finish(const wg_epilogue &e, int g, int G, const float to
       // dims of rows r = 0..3: 2i, 2i + P, 2i + 1, 2i + 1 + P
       const int d = 2 * i + (r >> 1) + ((r & 1) ? P : 0);
       const bool first = (r & 1) == 0;
-      const int f = d % P;
       float o = 0.0f;
       if (in_cache) {
-        const int lo = pos & 1023, hi = 1024 + (pos >> 10);
-        const float *r_lo = e.rope + (int64_t)lo * hd, *r_hi = e.rope + (int64_t)hi * hd;
-        float c1 = r_lo[f], s1 = r_lo[P + f], c2 = r_hi[f], s2 = r_hi[P + f];
-        float cs = c1 * c2 - s1 * s2, sn = s1 * c2 + c1 * s2;
+        float cs = pre.c1 * pre.c2 - pre.s1 * pre.s2, sn = pre.s1 * pre.c2 + pre.c1 * pre.s2;
         o = first ? v * cs - partner * sn : v * cs + partner * sn;
       }
       if (live) {

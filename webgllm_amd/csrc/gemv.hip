@@ -37,6 +37,9 @@ __global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
   const int lane = threadIdx.x & 63;
   const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (g >= G) return;  // whole waves leave together
+  const int pos0 = epi_pos0<MODE>(e);
+  EpiPre pre;
+  epi_prefetch<M, MODE>(e, g, G, pos0, pre);
   float acc[4][M];
 #pragma unroll
   for (int r = 0; r < 4; r++)
@@ -81,7 +84,7 @@ __global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
   input_scales<M>(e, scale);
 #pragma unroll
   for (int m = 0; m < M; m++) tot[m] = wave_sum4(acc[0][m], acc[1][m], acc[2][m], acc[3][m]);
-  finish<M, MODE>(e, g, G, tot, scale, y, ldy);
+  finish<M, MODE>(e, g, G, tot, scale, y, ldy, pre, pos0);
 }
 
 // ---------------------------------------------------------------------------
@@ -112,6 +115,10 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
   int g = blockIdx.x * RGW + slot;
   Unit<ZK, NB> next;
   load_unit<ZK, NB>(next, quants, scales, zeros, g, B, b0, b_end, g < G);
+  // and the first row group's epilogue operands (the waves that finish)
+  const int pos0 = epi_pos0<MODE>(e);
+  EpiPre pnext = {};
+  if (part == 0) epi_prefetch<M, MODE>(e, g, G, pos0, pnext);
 
   // This lane's activations and their block sums (times 2^-24), once.
   uint4 a[M][NB][4];
@@ -142,6 +149,8 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
   for (int g0 = blockIdx.x * RGW; g0 < G; g0 += stride, g += stride, it ^= 1) {
     Unit<ZK, NB> u = next;
     load_unit<ZK, NB>(next, quants, scales, zeros, g + stride, B, b0, b_end, g + stride < G);
+    const EpiPre pe = pnext;
+    if (part == 0) epi_prefetch<M, MODE>(e, g + stride, G, pos0, pnext);
     float acc[4][M];
 #pragma unroll
     for (int r = 0; r < 4; r++)
@@ -165,7 +174,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
 #pragma unroll
           for (int p = 1; p < KS; p++) tot[m] += red[it][wave + p][row * M + m];
     }
-    if (part == 0) finish<M, MODE>(e, g, G, tot, scale, y, ldy);
+    if (part == 0) finish<M, MODE>(e, g, G, tot, scale, y, ldy, pe, pos0);
   }
 }
 

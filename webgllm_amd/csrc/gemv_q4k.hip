@@ -76,6 +76,9 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t *__restrict
   const int lane = threadIdx.x & 63;
   const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (g >= G) return;
+  const int pos0 = epi_pos0<MODE>(e);
+  EpiPre pre;
+  epi_prefetch<M, MODE>(e, g, G, pos0, pre);
   const int c = lane & 3, rp = (lane >> 2) & 1, sb = lane >> 3;
   float acc[2][M];
 #pragma unroll
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t *__restrict
     float a0 = acc[0][m], a1 = acc[1][m];
     tot[m] = wave_sum4(rp ? 0.0f : a0, rp ? 0.0f : a1, rp ? a0 : 0.0f, rp ? a1 : 0.0f);
   }
-  finish<M, MODE>(e, g, G, tot, scale, y, ldy);
+  finish<M, MODE>(e, g, G, tot, scale, y, ldy, pre, pos0);
 }
 
 // ---------------------------------------------------------------------------
@@ -219,6 +222,9 @@ __global__ __launch_bounds__(256) void gemv_q4k_stream_kernel(
   int g = blockIdx.x * RGW + slot;
   KUnit<NS> next;
   load_kunit<NS>(next, quants, g, S, s0, s_end, rp, c, g < G);
+  const int pos0 = epi_pos0<MODE>(e);
+  EpiPre pnext = {};
+  if (part == 0) epi_prefetch<M, MODE>(e, g, G, pos0, pnext);
 
   uint4 a[M][NS][8];
   float sa0[M][NS], sa1[M][NS];
@@ -258,6 +264,8 @@ __global__ __launch_bounds__(256) void gemv_q4k_stream_kernel(
   for (int g0 = blockIdx.x * RGW; g0 < G; g0 += stride, g += stride, it ^= 1) {
     KUnit<NS> u = next;
     load_kunit<NS>(next, quants, g + stride, S, s0, s_end, rp, c, g + stride < G);
+    const EpiPre pe = pnext;
+    if (part == 0) epi_prefetch<M, MODE>(e, g + stride, G, pos0, pnext);
     float acc[2][M];
 #pragma unroll
     for (int r = 0; r < 2; r++)
@@ -314,7 +322,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_stream_kernel(
 #pragma unroll
           for (int p = 1; p < KS; p++) tot[m] += red[it][wave + p][row * M + m];
     }
-    if (part == 0) finish<M, MODE>(e, g, G, tot, scale, y, ldy);
+    if (part == 0) finish<M, MODE>(e, g, G, tot, scale, y, ldy, pe, pos0);
   }
 }
 
