@@ -127,39 +127,288 @@ def oracle_matrix(m):
     return qm
 
 
-def cpu_baseline(engine, threads, seconds=12.0):
-    """Oracle split matmul (float32, shader order) on one layer + the head,
-    repeated for about `seconds` of CPU time."""
+def cpu_step_time(groups, M, threads, seconds=12.0):
+    """The oracle's shader-order float32 split matmul (OpenMP) over one matrix
+    of each group, M rows of half activations, repeated for about `seconds`.
+    groups: (label, device matrix, times a step uses it). Returns (seconds
+    per step, a description of the sample)."""
     import numpy as np
     from oracle import oracle as O
+    qms = [(label, oracle_matrix(m), k) for label, m, k in groups]
+    rng = np.random.default_rng(0)
+    xs = {qm.K: O.f32_to_h2(rng.standard_normal((M, qm.K)).astype(np.float32))
+          for _, qm, _ in qms}
+    O.matmul_split(qms[0][1], xs[qms[0][1].K], threads)  # warm the threads
+    spent = {label: 0.0 for label, _, _ in qms}
+    reps = 0
+    while reps < 100000 and (sum(spent.values()) < seconds or reps < 2):
+        for label, qm, _ in qms:
+            t0 = O.now()
+            O.matmul_split(qm, xs[qm.K], threads)
+            spent[label] += O.now() - t0
+        reps += 1
+    per_step = sum(spent[label] / reps * k for label, _, k in qms)
+    parts = ", ".join(f"{label} {spent[label] / reps * 1e3:.1f} ms x{k}" for label, _, k in qms)
+    desc = (f"oracle shader-order fp32 split matmul (OpenMP, {threads} threads), {M} row(s): "
+            f"{parts}; {reps} repetitions ({sum(spent.values()):.1f} s), extrapolated to the "
+            f"step; attention and norms not included")
+    return per_step, desc
+
+
+def cpu_baseline(engine, threads, seconds=12.0):
+    """Oracle split matmul (float32, shader order) on one layer + the head,
+    repeated for about `seconds` of CPU time, extrapolated to a token."""
     s = engine.shape
     lw = engine.w.layers[0]
-    layer = [oracle_matrix(lw[k]) for k in ("qkv", "o", "gate_up", "down")]
-    head = oracle_matrix(engine.w.embedding)
-    rng = np.random.default_rng(0)
-    xs = {m.K: O.f32_to_h2(rng.standard_normal((1, m.K)).astype(np.float32))
-          for m in layer + [head]}
-    O.matmul_split(layer[0], xs[layer[0].K], threads)  # warm the threads
-    # repeat the layer + head sample until about `seconds` of CPU work is done
-    t_layer = t_head = 0.0
-    reps = 0
-    while reps < 400 and (t_layer + t_head < seconds or reps < 2):
-        t0 = O.now()
-        for m in layer:
-            O.matmul_split(m, xs[m.K], threads)
-        t1 = O.now()
-        O.matmul_split(head, xs[head.K], threads)
-        t_layer += t1 - t0
-        t_head += O.now() - t1
-        reps += 1
-    per_token = (s.layers * t_layer + t_head) / reps
+    groups = [(k, lw[k], s.layers) for k in ("qkv", "o", "gate_up", "down")]
+    groups.append(("head", engine.w.embedding, 1))
+    per_token, desc = cpu_step_time(groups, 1, threads, seconds)
     return {"value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": threads,
-            "kind": "port",
-            "sample": f"oracle shader-order fp32 split matmul (OpenMP, {threads} threads) on "
-                      f"layer 0's qkv/o/gate|up/down and the 128256x4096 head at batch 1, "
-                      f"{reps} repetitions ({t_layer + t_head:.1f} s: {t_layer / reps * 1e3:.1f} ms "
-                      f"a layer, {t_head / reps * 1e3:.1f} ms the head), extrapolated to 32 "
-                      f"layers; attention and norms not included"}
+            "kind": "port", "sample": desc}
+
+
+def line(metric, value, unit, steps, warmup, ms, config, roofline, cpu, dtype="f32", **extra):
+    out = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps,
+           "warmup": warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic",
+           "config": config, "roofline": roofline, "cpu_baseline": cpu}
+    out.update(extra)
+    return out
+
+
+def timed(fn, reps):
+    """Average milliseconds of fn() over reps runs, between HIP events on the
+    current stream."""
+    import torch
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def workload_q4_0_gemv(args):
+    """Q4_0 GEMV 2048 x 2048, batch 1 (a decode step's matmul): graph-captured
+    launches over 256 distinct weight copies (604 MB, more than the 256 MB
+    infinity cache), each moving 2,359,296 weight bytes + the half input + the
+    float32 output."""
+    import torch
+    from webgllm_amd import engine as E, ops
+    N = K = 2048
+    copies = 256
+    shape = E.ModelShape("q4_0-gemv", K, 1, 1, 1, 4, 4, 4, "q4_0")
+    w = E.Weights.blank(shape, seed=0)
+    mats = [w.matrix(N, K) for _ in range(copies)]
+    x = (torch.randn((1, K), device="cuda", generator=torch.Generator(device="cuda")
+                     .manual_seed(1))).half()
+    y = torch.empty((1, N), device="cuda")
+    algo = mats[0].nbytes + K * 2 + N * 4
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for m in mats[:4]:
+            ops.gemv(m, x, out=y)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for m in mats:
+                ops.gemv(m, x, out=y)
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // 16)
+    for _ in range(args.warmup // 8 + 1):
+        g.replay()
+    ms_graph = timed(g.replay, reps)
+    us = ms_graph * 1e3 / copies
+    gbps = algo / (us * 1e-6) / 1e9
+    # the same matrix over and over (held in the caches)
+    with torch.cuda.stream(s):
+        gh = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gh, stream=s):
+            for _ in range(copies):
+                ops.gemv(mats[0], x, out=y)
+    torch.cuda.synchronize()
+    gh.replay()
+    hot = timed(gh.replay, reps) * 1e3 / copies
+    cpu = None
+    if not args.no_cpu:
+        threads = min(os.cpu_count() or 1, 16)
+        t, desc = cpu_step_time([("2048x2048", mats[0], 1)], 1, threads, 10.0)
+        cpu = {"value": round(algo / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+               "kind": "port", "sample": desc}
+    roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+            "kernel": "gemv_stream_kernel 2048x2048 Q4_0 (cold: 256 distinct copies)",
+            "bytes_per_launch": algo, "avg_launch_us": round(us, 3),
+            "launches": reps * copies}
+    cfg = {"workload": "Q4_0 GEMV 2048x2048 batch 1, half input, float32 output, 256 "
+                       "distinct weight copies in one captured graph",
+           "weights": "random GGUF Q4_0 blocks (18 bytes / 32 weights) repacked on the GPU "
+                      "(packQ4_0)", "global_batch": 1, "parallelism": "none"}
+    return line("Q4_0 GEMV HBM GB/s", round(gbps, 1), "GB/s", reps * copies, args.warmup,
+                ms_graph / copies, cfg, roof, cpu, hot_launch_us=round(hot, 3),
+                hot_GBps=round(algo / (hot * 1e-6) / 1e9, 1))
+
+
+def workload_nbits_gemm(args):
+    """Prefill GEMM on MFMA: A half [512 x 4096] times MatMulNBits weights
+    (4-bit, half scales, u8 zero points, block 32) at N = 4096 and 14336,
+    float32 output."""
+    import torch
+    from webgllm_amd import engine as E, ops
+    M, K = 512, 4096
+    shape = E.ModelShape("nbits-gemm", K, 1, 1, 1, 4, 4, 4, "nbits")
+    w = E.Weights.blank(shape, seed=0)
+    a = torch.randn((M, K), device="cuda", generator=torch.Generator(device="cuda")
+                    .manual_seed(2)).half()
+    res = {}
+    for N in (4096, 14336):
+        mats = [w.matrix(N, K) for _ in range(4)]
+        c = torch.empty((M, N), device="cuda")
+        for m in mats:
+            ops.gemm(m, a, out=c)
+        it = iter(range(1 << 30))
+        ms = timed(lambda: ops.gemm(mats[next(it) % 4], a, out=c), max(8, args.steps // 2))
+        res[N] = (ms, 2.0 * M * N * K / (ms * 1e-3) / 1e12, mats[0])
+    tot_flop = sum(2.0 * M * N * K for N in res)
+    tot_ms = sum(r[0] for r in res.values())
+    tflops = tot_flop / (tot_ms * 1e-3) / 1e12
+    cpu = None
+    if not args.no_cpu:
+        threads = min(os.cpu_count() or 1, 16)
+        t, desc = cpu_step_time([("4096x4096", res[4096][2], 1),
+                                 ("14336x4096", res[14336][2], 1)], 8, threads, 10.0)
+        cpu = {"value": round(tot_flop / 64 / t / 1e12, 5), "unit": "TFLOP/s",
+               "cores": threads, "kind": "port",
+               "sample": desc + " (8 of the 512 rows; the rate scales with rows)"}
+    roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
+            "frac": round(tflops / 2500.0, 4), "traffic": None,
+            "kernel": "gemm_q4_kernel (v_mfma_f32_32x32x16_f16, dequant in registers)",
+            "flops_per_launch": {str(N): 2 * M * N * K for N in res},
+            "avg_launch_us": {str(N): round(r[0] * 1e3, 2) for N, r in res.items()}}
+    cfg = {"workload": "MatMulNBits prefill GEMM, M=512, K=4096, N in {4096, 14336}",
+           "weights": "random MatMulNBits q4 rows (u8 zero points) repacked on the GPU",
+           "global_batch": M, "parallelism": "none"}
+    return line("prefill GEMM TFLOP/s (MatMulNBits q4, M=512)", round(tflops, 1), "TFLOP/s",
+                args.steps, 4, tot_ms, cfg, roof, cpu, dtype="f16 x f16 -> f32",
+                per_shape_tflops={str(N): round(r[1], 1) for N, r in res.items()})
+
+
+def decode_engine_run(shape, ctx, prompt_len, steps, warmup):
+    """Prefill random ids, capture the token step, warm up, then time
+    `steps` graph replays. Returns (engine, weights, ms a token, first
+    timed position)."""
+    import torch
+    from webgllm_amd import engine as E
+    w = E.Weights(shape, seed=0)
+    eng = E.Engine(w, ctx)
+    prompt = torch.randint(0, shape.vocab, (prompt_len,),
+                           generator=torch.Generator().manual_seed(1)).tolist()
+    first = int(eng.forward(prompt)[-1])
+    eng.capture_step()
+    eng.decode(first, warmup)
+    p0 = eng.position
+    eng.ids[0] = int(eng.hist[p0].item())
+    eng.pos.fill_(p0)
+    ms = timed(eng.graph.replay, steps)
+    eng.position += steps
+    eng.check_plan()
+    return eng, w, ms, p0
+
+
+def workload_qwen2_decode(args):
+    """Qwen2-0.5B-shape greedy decode (MatMulNBits q4, fp16 KV cache of 1024):
+    a 512-id random prompt, then decode to position 1024."""
+    from webgllm_amd import engine as E
+    shape = E.QWEN2_05B
+    steps = 1024 - 512 - args.warmup - 1
+    eng, w, ms, p0 = decode_engine_run(shape, 1024, 512, steps, args.warmup)
+    kv = shape.layers * 2 * shape.kv_heads * shape.head_dim * 2 * (p0 + steps // 2)
+    token_bytes = w.nbytes + kv
+    cpu = cpu_baseline(eng, min(os.cpu_count() or 1, 16), 10.0) if not args.no_cpu else None
+    gbps = token_bytes / (ms * 1e-3) / 1e9
+    roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+            "kernel": "whole token (weights ~286 MB, about the infinity cache's size: "
+                      "'effective' GB/s)", "bytes_per_launch": token_bytes,
+            "avg_launch_us": round(ms * 1e3, 2), "launches": steps}
+    cfg = {"workload": f"Qwen2-0.5B-shape greedy decode, positions {p0}..{p0 + steps - 1}",
+           "model": shape.name, "layers": shape.layers, "hidden": shape.hidden,
+           "vocab": shape.vocab, "weights": "random MatMulNBits q4 (u8 zero points)",
+           "global_batch": 1, "seq_len": 1024, "parallelism": "none"}
+    return line("decode tok/s, Qwen2-0.5B-shape MatMulNBits batch 1", round(1000.0 / ms, 2),
+                "tok/s", steps, args.warmup, ms, cfg, roof, cpu)
+
+
+def workload_lfm2_verify(args):
+    """LFM2-1.2B-shape hybrid (10 short-conv + 6 attention layers, Q4_0):
+    speculative verify of a token and 4 random draft ids (M = 5), keeping
+    the agreeing prefix + 1 and rolling the conv states back (the
+    reference's handler loop, src/handler.ts:1811-1887)."""
+    import torch
+    from webgllm_amd import engine as E
+    shape = E.LFM2_12B
+    w = E.Weights(shape, seed=0)
+    ctx = 2048
+    eng = E.Engine(w, ctx)
+    g = torch.Generator().manual_seed(3)
+    prompt = torch.randint(0, shape.vocab, (256,), generator=g).tolist()
+    token = int(eng.forward(prompt)[-1])
+    steps = min(args.steps, (ctx - 300) // 5)
+
+    def verify(n):
+        nonlocal token
+        written = 0
+        for _ in range(n):
+            drafts = torch.randint(0, shape.vocab, (4,), generator=g).tolist()
+            rows = eng.forward([token] + drafts, draft=True).tolist()
+            kept = 1
+            for i in range(4):
+                if rows[i] != drafts[i]:
+                    break
+                kept += 1
+            eng.accept(kept)
+            token = rows[kept - 1]
+            written += kept
+        return written
+
+    verify(args.warmup)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    written = verify(steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms = dt * 1e3 / steps
+    cpu = None
+    if not args.no_cpu:
+        threads = min(os.cpu_count() or 1, 16)
+        conv = next(i for i in range(shape.layers) if shape.layer_type(i) == "conv")
+        att = next(i for i in range(shape.layers) if shape.layer_type(i) == "attn")
+        n_conv = len(shape.conv_layers)
+        n_att = shape.layers - n_conv
+        lc, la = w.layers[conv], w.layers[att]
+        groups = [("in_proj", lc["in_proj"], n_conv), ("out_proj", lc["out_proj"], n_conv),
+                  ("qkv", la["qkv"], n_att), ("o", la["o"], n_att),
+                  ("gate_up", lc["gate_up"], shape.layers), ("down", lc["down"], shape.layers),
+                  ("head", w.embedding, 1)]
+        t, desc = cpu_step_time(groups, 5, threads, 10.0)
+        cpu = {"value": round(1.0 / t, 4), "unit": "verify steps/s", "cores": threads,
+               "kind": "port", "sample": desc}
+    cfg = {"workload": "LFM2-1.2B-shape speculative verify, token + 4 random draft ids a "
+                       "step (M = 5), accept + conv-state rollback, host loop with readback",
+           "model": shape.name, "layers": shape.layers, "hidden": shape.hidden,
+           "vocab": shape.vocab, "weights": "random GGUF Q4_0", "global_batch": 5,
+           "seq_len": ctx, "parallelism": "none"}
+    return line("verify steps/s, LFM2-1.2B-shape Q4_0, 4 drafts", round(steps / dt, 2),
+                "verify steps/s", steps, args.warmup, ms, cfg, None, cpu,
+                tokens_per_s=round(written / dt, 2), tokens_per_step=round(written / steps, 3),
+                weight_bytes=w.nbytes)
+
+
+WORKLOADS = {"q4_0-gemv": workload_q4_0_gemv, "nbits-gemm": workload_nbits_gemm,
+             "qwen2-decode": workload_qwen2_decode, "lfm2-verify": workload_lfm2_verify}
 
 
 def main():
@@ -175,6 +424,10 @@ def main():
     ap.add_argument("--reps", type=int, default=6, help=argparse.SUPPRESS)
     ap.add_argument("--persistent", action="store_true",
                     help="decode every layer in one persistent launch (wg_decode_run)")
+    ap.add_argument("--workload", default="llama8b-decode",
+                    choices=["llama8b-decode"] + sorted(WORKLOADS),
+                    help="the headline Llama-3-8B-shape decode (default) or another "
+                         "configuration's measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -182,6 +435,9 @@ def main():
         sys.exit(2)
     if args.roofline_only:
         roofline_only(args)
+        return
+    if args.workload != "llama8b-decode":
+        print(json.dumps(WORKLOADS[args.workload](args)), flush=True)
         return
 
     import dataclasses
