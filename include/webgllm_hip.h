@@ -44,9 +44,10 @@ const char *wg_version(void);
  * "gemv_wg_per_cu", "gemv_wg_per_cu_wide" (matrices of 16384+ row groups),
  * "q4k_wg_per_cu" (persistent GEMV workgroups per compute unit) and
  * "gemv_min_waves" (below this many waves a GEMV splits K inside a
- * workgroup) and "decode_wg_per_cu" (persistent decode workgroups per
- * compute unit, read at plan creation). Process-wide; results never depend
- * on them. */
+ * workgroup), "decode_wg_per_cu" (persistent decode workgroups per
+ * compute unit, read at plan creation) and "gemm_tile_m" (prefill GEMM
+ * tile rows: 64, 128, or 0 to choose by shape). Process-wide; results never
+ * depend on them. */
 int wg_tuning_set(const char *name, int32_t value);
 int wg_tuning_get(const char *name, int32_t *value);
 

@@ -5,21 +5,33 @@
 // 4-bit matrix, C float32.
 //
 // gfx950 mapping:
-//  - a workgroup (4 waves) owns a BM x BN tile of C (BM = 128 tokens; BN =
-//    128 features, or 64 for narrow matrices so the grid still covers the
-//    256 compute units); each wave owns WM x 32 of it (WM = 128 or 64);
-//  - A goes through LDS, BK = 64 at a time, double-buffered; each wave
-//    loads its 32 weight rows straight into registers (8 nibble bytes a
-//    lane a block) and dequantizes there to halves, d (q - z) rounded once
-//    to half as the reference's dequantOut does (packed f16 math: q - z is
-//    exact, the product is rounded once);
-//  - v_mfma_f32_32x32x16_f16 with float32 accumulation. A 32-weight block
-//    is two K = 16 steps: lane half h holds bytes 8h..8h+7, whose low
-//    nibbles are weights 8h..8h+7 (the first step) and high nibbles
-//    weights 16+8h.. (the second) - natural K order on both operands;
-//  - workgroups on one XCD (dispatch order mod 8) take the M tiles of one
-//    weight tile one after another, so it is read from HBM once into that
-//    XCD's L2.
+//  - a workgroup (4 waves, 2 x 2) owns a BM x BN tile of C; a wave owns
+//    (BM / 2) x (BN / 2) as MT x NT MFMA tiles of 32 x 32
+//    (v_mfma_f32_32x32x16_f16, float32 accumulation);
+//  - K goes in steps of 64 (two 32-weight blocks) through an S-stage ring
+//    in LDS: each stage holds the A tile (16-byte chunk c of row r at
+//    position c ^ (r / 2 % 8), so the 16 rows an operand read takes at once
+//    fill all 64 banks), the
+//    weight tile's raw nibbles (a row group's two blocks are 128 contiguous
+//    bytes), its half scales and its zero points;
+//  - stages are filled by direct global-to-LDS loads
+//    (global_load_lds_dwordx4), issued S - 1 steps ahead of their use, so
+//    every step computes while the next ones stream in. Every wave issues
+//    the same number of loads a stage, so "this wave's loads of stage kt
+//    have landed" is one vmcnt wait; a workgroup barrier then covers the
+//    other waves'. The loads are issued from inline assembly: the compiler
+//    cannot tell which in-flight stage a later LDS read depends on and would
+//    otherwise wait for all of them;
+//  - weights are dequantized from LDS to halves in registers, d (q - z)
+//    rounded once as the reference's dequantOut does: 1024 + q as a half
+//    minus 1024 + z is exact in packed f16, then one multiply by d. A
+//    32-weight block is two K = 16 MFMA steps: lane half h takes bytes
+//    8h..8h+7 of the block's row, whose low nibbles are weights 8h.. (the
+//    first step) and high nibbles 16 + 8h.. (the second) - natural K order
+//    on both operands;
+//  - workgroups on one XCD (ids equal mod 8, as the dispatcher deals them
+//    round-robin) take the M tiles of one weight tile one after another, so
+//    it is read from HBM once into that XCD's L2.
 #include "common.h"
 #include "dot.h"
 
@@ -28,9 +40,6 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
-
-constexpr int BM = 128, BK = 64;
-constexpr int ASTR = BK + 8;  // LDS row stride of the A tile, in halves
 
 // 8 nibble bytes of one weight row and block -> the two K = 16 operands
 // (low nibbles, high nibbles) as d (q - z), one rounding to half.
@@ -76,15 +85,40 @@ __device__ inline void dequant8(uint2 bytes, uint16_t scale_bits, float zero, ha
   }
 }
 
-template <int ZK>
-__device__ inline float zero_of(const void *zeros, int64_t si) {
-  if constexpr (ZK == WG_ZERO_8) return 8.0f;
-  else if constexpr (ZK == WG_ZERO_U8) return (float)((const uint8_t *)zeros)[si];
-  else return (float)__builtin_bit_cast(_Float16, ((const uint16_t *)zeros)[si]);
+// 16 bytes a lane from `src` into LDS at byte address lds + 16 * lane
+// (lds uniform across the wave); `lanes` of the wave take part.
+__device__ inline void dma16(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
+               : "memory");
+}
+// 4 bytes a lane into LDS at lds + 4 * lane.
+__device__ inline void dma4(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(src)
+               : "memory");
 }
 
-// WAVES_N waves across N (32 columns each), 4 / WAVES_N across M (WM rows).
-template <int ZK, int WAVES_N>
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14).
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+__device__ inline void barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int ZK, int BN>
+struct Stage {
+  static constexpr int WQ = BN * 32;  // raw nibbles: BN / 4 row groups x 128 bytes
+  static constexpr int WS = BN * 4;   // scales: BN / 4 row groups x 8 halves
+  static constexpr int WZ = ZK == WG_ZERO_F16 ? BN * 4 : ZK == WG_ZERO_U8 ? BN * 2 : 0;
+};
+
+// BM x BN tiles, S stages of BK = 64.
+template <int ZK, int BM, int BN, int S>
 __global__ __launch_bounds__(256) void gemm_q4_kernel(const uint8_t *__restrict__ quants,
                                                       const uint16_t *__restrict__ scales,
                                                       const void *__restrict__ zeros,
@@ -92,15 +126,17 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(const uint8_t *__restrict_
                                                       float *__restrict__ C, int ldc,
                                                       const float *residual, int ldr, int M,
                                                       int N, int K) {
-  constexpr int BN = 32 * WAVES_N;
-  constexpr int WAVES_M = 4 / WAVES_N;
-  constexpr int WM = BM / WAVES_M;
-  constexpr int MT = WM / 32;  // 32-row MFMA tiles a wave owns
-  __shared__ __align__(16) uint16_t As[2][BM * ASTR];
+  constexpr int WM = BM / 2, WN = BN / 2, MT = WM / 32, NT = WN / 32;
+  constexpr int A_BYTES = BM * 128;
+  constexpr int WQ = Stage<ZK, BN>::WQ, WS = Stage<ZK, BN>::WS, WZ = Stage<ZK, BN>::WZ;
+  constexpr int STAGE = A_BYTES + WQ + WS + WZ;
+  constexpr int IA = BM / 32;  // A loads a wave issues a stage
+  constexpr int NW = IA + 2 + (ZK == WG_ZERO_U8 ? 1 : 0);  // loads a wave issues a stage
+  extern __shared__ __align__(16) unsigned char smem[];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wn = wave % WAVES_N, wm = wave / WAVES_N;
-  // Tile order: XCD x = id % 8 runs the M tiles of weight tile 8 q + x in turn.
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+  // Tile order: ids equal mod 8 (one XCD) run the M tiles of one weight tile in turn.
   const int tiles_m = (M + BM - 1) / BM, tiles_n = N / BN;
   int id = blockIdx.x, tm, tn;
   if (tiles_n % 8 == 0) {
@@ -111,127 +147,168 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(const uint8_t *__restrict_
     tm = id % tiles_m;
     tn = id / tiles_m;
   }
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int B = K / 32;
+  const int m0 = tm * BM, n0 = tn * BN, g0 = n0 / 4;
+  const int B = K / 32, KT = K / 64;
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
 
-  // This lane's weight row and 8-byte half of each block.
-  const int n = n0 + wn * 32 + (lane & 31), h = lane >> 5;
-  const int64_t row_base = (int64_t)(n >> 2) * B * 4 + (n & 3);  // scale index at block 0
-  auto wq = [&](int b) -> uint2 {
-    return *reinterpret_cast<const uint2 *>(quants + (row_base + 4 * (int64_t)b) * 16 + 8 * h);
-  };
-
-  // A tile loader: 128 rows x 64 halves = 1024 pieces of 16 bytes, 4 a thread.
-  uint4 stage[4];
-  auto load_a = [&](int kt) {
+  // Issue this wave's loads of step kt into stage st.
+  auto issue = [&](int kt, int st) {
+    const uint32_t base = sbase + st * STAGE;
+    const int b0 = 2 * kt;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      int piece = tid + 256 * i;
-      int r = piece >> 3, c = piece & 7;
-      int m = m0 + r;
-      stage[i] = m < M ? *reinterpret_cast<const uint4 *>(A + (int64_t)m * lda + kt * BK + 8 * c)
-                       : make_uint4(0u, 0u, 0u, 0u);
+    for (int i = 0; i < IA; i++) {
+      const int p = (i * 4 + wave) * 64 + lane;  // 16-byte piece of the A tile
+      const int row = p >> 3, c = (p & 7) ^ ((row >> 1) & 7);
+      const int m = min(m0 + row, M - 1);
+      dma16(A + (int64_t)m * lda + kt * 64 + c * 8,
+            __builtin_amdgcn_readfirstlane(base + (i * 4 + wave) * 1024));
+    }
+    {  // raw nibbles: BN / 2 pieces a wave
+      constexpr int PW = BN / 2;
+      const int q = wave * PW + lane;
+      if (lane < PW)
+        dma16(quants + ((int64_t)(g0 + (q >> 3)) * B + b0) * 64 + (q & 7) * 16,
+              __builtin_amdgcn_readfirstlane(base + A_BYTES + wave * PW * 16));
+    }
+    {  // scales (and half zero points) of the BN / 4 row groups
+      constexpr int NS = BN / 4, PIECES = ZK == WG_ZERO_F16 ? 2 * NS : NS, PW = PIECES / 4;
+      const int q = wave * PW + lane;
+      if (lane < PW) {
+        const void *src = q < NS ? (const void *)(scales + ((int64_t)(g0 + q) * B + b0) * 4)
+                                 : (const void *)((const uint16_t *)zeros +
+                                                  ((int64_t)(g0 + q - NS) * B + b0) * 4);
+        dma16(src, __builtin_amdgcn_readfirstlane(base + A_BYTES + WQ + wave * PW * 16));
+      }
+    }
+    if constexpr (ZK == WG_ZERO_U8) {  // 8 zero-point bytes a row group, 4 at a time
+      constexpr int PW = BN / 8;
+      const int q = wave * PW + lane;
+      if (lane < PW)
+        dma4((const uint8_t *)zeros + ((int64_t)(g0 + (q >> 1)) * B + b0) * 4 + (q & 1) * 4,
+             __builtin_amdgcn_readfirstlane(base + A_BYTES + WQ + WS + wave * PW * 4));
     }
   };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      int piece = tid + 256 * i;
-      int r = piece >> 3, c = piece & 7;
-      *reinterpret_cast<uint4 *>(&As[buf][r * ASTR + 8 * c]) = stage[i];
-    }
-  };
 
-  float16v acc[MT];
+  float16v acc[MT][NT];
 #pragma unroll
   for (int t = 0; t < MT; t++)
 #pragma unroll
-    for (int j = 0; j < 16; j++) acc[t][j] = 0.0f;
-
-  const int KT = K / BK;
-  uint2 wcur[2], wnext[2];
-  uint16_t scur[2], snext[2];
-  float zcur[2], znext[2];
-  auto load_w = [&](int kt, uint2 *wv, uint16_t *sv, float *zv) {
+    for (int u = 0; u < NT; u++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      int b = kt * 2 + j;
-      wv[j] = wq(b);
-      int64_t si = row_base + 4 * (int64_t)b;
-      sv[j] = scales[si];
-      zv[j] = zero_of<ZK>(zeros, si);
-    }
-  };
+      for (int j = 0; j < 16; j++) acc[t][u][j] = 0.0f;
 
-  load_a(0);
-  load_w(0, wcur, scur, zcur);
-  store_a(0);
+  for (int s = 0; s < S - 1; s++)
+    if (s < KT) issue(s, s);
   for (int kt = 0; kt < KT; kt++) {
-    __syncthreads();  // tile kt is in LDS; tile kt - 1's buffer is free
-    const bool more = kt + 1 < KT;
-    if (more) {
-      load_a(kt + 1);
-      load_w(kt + 1, wnext, snext, znext);
-    }
-    const uint16_t *Ab = As[kt & 1];
+    // this wave's loads of step kt have landed (younger stages may fly on)
+    if (kt + S - 2 < KT) wait_vm<NW * (S - 2)>();
+    else wait_vm<0>();
+    barrier();  // every wave's have, and every wave is done with step kt - 1
+    if (kt + S - 1 < KT) issue(kt + S - 1, (kt + S - 1) % S);
+    const unsigned char *st = smem + (kt % S) * STAGE;
+    const uint16_t *As = reinterpret_cast<const uint16_t *>(st);
+    const unsigned char *Wq = st + A_BYTES;
+    const uint16_t *Ws = reinterpret_cast<const uint16_t *>(st + A_BYTES + WQ);
+    // Every LDS read of the step first (weights, scales, zeros, A chunks),
+    // so their latencies overlap; then the dequant and the MFMAs.
+    uint2 wbytes[2][NT];
+    uint16_t wsc[2][NT];
+    float wz[2][NT];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {  // the two blocks of this BK
-      half8 blo, bhi;
-      dequant8<ZK>(wcur[j], scur[j], zcur[j], blo, bhi);
+    for (int j = 0; j < 2; j++)
 #pragma unroll
-      for (int step = 0; step < 2; step++) {  // low nibbles: K 0..15, high: 16..31
-        const int k = j * 32 + step * 16 + 8 * h;
+      for (int u = 0; u < NT; u++) {
+        const int nl = wn * WN + u * 32 + (lane & 31);  // tile-local weight row
+        const int rg = nl >> 2, r = nl & 3;
+        wbytes[j][u] =
+            *reinterpret_cast<const uint2 *>(Wq + rg * 128 + j * 64 + r * 16 + 8 * h);
+        wsc[j][u] = Ws[rg * 8 + j * 4 + r];
+        if constexpr (ZK == WG_ZERO_8) wz[j][u] = 8.0f;
+        else if constexpr (ZK == WG_ZERO_U8)
+          wz[j][u] = (float)(st + A_BYTES + WQ + WS)[rg * 8 + j * 4 + r];
+        else
+          wz[j][u] = (float)__builtin_bit_cast(
+              _Float16, reinterpret_cast<const uint16_t *>(st + A_BYTES + WQ + WS)[rg * 8 + j * 4 + r]);
+      }
+    half8 av[2][2][MT];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int step = 0; step < 2; step++) {
+        const int c = 4 * j + 2 * step + h;  // 16-byte chunk of the A rows
 #pragma unroll
         for (int t = 0; t < MT; t++) {
-          const int r = wm * WM + t * 32 + (lane & 31);
-          half8 a = *reinterpret_cast<const half8 *>(&Ab[r * ASTR + k]);
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, step ? bhi : blo, acc[t], 0, 0, 0);
+          const int row = wm * WM + t * 32 + (lane & 31);
+          av[j][step][t] =
+              *reinterpret_cast<const half8 *>(As + row * 64 + (c ^ ((row >> 1) & 7)) * 8);
         }
       }
-    }
-    if (more) {
-      store_a((kt + 1) & 1);
-      wcur[0] = wnext[0];
-      wcur[1] = wnext[1];
-      scur[0] = snext[0];
-      scur[1] = snext[1];
-      zcur[0] = znext[0];
-      zcur[1] = znext[1];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {  // the two blocks of the step
+      half8 blo[NT], bhi[NT];
+#pragma unroll
+      for (int u = 0; u < NT; u++) dequant8<ZK>(wbytes[j][u], wsc[j][u], wz[j][u], blo[u], bhi[u]);
+#pragma unroll
+      for (int step = 0; step < 2; step++)  // low nibbles: K 0..15, high: 16..31
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+          for (int u = 0; u < NT; u++)
+            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[j][step][t],
+                                                              step ? bhi[u] : blo[u], acc[t][u],
+                                                              0, 0, 0);
     }
   }
 
   // D[j] of lane i: row 8 (j / 4) + 4 (i / 32) + j % 4, column i % 32.
-  const int col = n0 + wn * 32 + (lane & 31);
 #pragma unroll
-  for (int t = 0; t < MT; t++)
+  for (int u = 0; u < NT; u++) {
+    const int col = n0 + wn * WN + u * 32 + (lane & 31);
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-      int m = m0 + wm * WM + t * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
-      if (m < M) {
-        float v = acc[t][j];
-        if (residual) v += residual[(int64_t)m * ldr + col];
-        C[(int64_t)m * ldc + col] = v;
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const int m = m0 + wm * WM + t * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
+        if (m < M) {
+          float v = acc[t][u][j];
+          if (residual) v += residual[(int64_t)m * ldr + col];
+          C[(int64_t)m * ldc + col] = v;
+        }
       }
-    }
+  }
+}
+
+template <int ZK, int BM, int BN, int S>
+int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
+                 const float *residual, int ldr, hipStream_t s) {
+  constexpr int STAGE = BM * 128 + Stage<ZK, BN>::WQ + Stage<ZK, BN>::WS + Stage<ZK, BN>::WZ;
+  constexpr size_t LDS = (size_t)S * STAGE;
+  static bool raised = false;  // allow more than 64 KiB of dynamic LDS, once
+  if (!raised && LDS > 64 * 1024) {
+    WG_HIP(hipFuncSetAttribute((const void *)gemm_q4_kernel<ZK, BM, BN, S>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS));
+    raised = true;
+  }
+  const int grid = ((M + BM - 1) / BM) * (w->N / BN);
+  gemm_q4_kernel<ZK, BM, BN, S><<<grid, 256, LDS, s>>>(
+      (const uint8_t *)w->quants, (const uint16_t *)w->scales, w->zeros, A, lda, C, ldc,
+      residual, ldr, M, w->N, w->K);
+  return launched("wg_q4_gemm");
 }
 
 template <int ZK>
 int launch(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
            const float *residual, int ldr, hipStream_t s) {
-  const int tiles_m = (M + BM - 1) / BM;
-  // 128-wide tiles when they alone cover the compute units, else 64.
-  if ((int64_t)tiles_m * (w->N / 128) >= 256 && w->N % 128 == 0) {
-    int grid = tiles_m * (w->N / 128);
-    gemm_q4_kernel<ZK, 4><<<grid, 256, 0, s>>>((const uint8_t *)w->quants,
-                                                (const uint16_t *)w->scales, w->zeros, A, lda,
-                                                C, ldc, residual, ldr, M, w->N, w->K);
-  } else {
-    int grid = tiles_m * (w->N / 64);
-    gemm_q4_kernel<ZK, 2><<<grid, 256, 0, s>>>((const uint8_t *)w->quants,
-                                                (const uint16_t *)w->scales, w->zeros, A, lda,
-                                                C, ldc, residual, ldr, M, w->N, w->K);
+  // 128 x 128 tiles when they alone cover the compute units, else 64-row
+  // tiles (more workgroups, a deeper ring); 64-wide tiles for N not a
+  // multiple of 128.
+  if (w->N % 128 == 0) {
+    const int tm = tuning("gemm_tile_m");
+    if (tm == 128 || (tm != 64 && (int64_t)((M + 127) / 128) * (w->N / 128) >= 256))
+      return launch_tiles<ZK, 128, 128, 3>(w, A, M, lda, C, ldc, residual, ldr, s);
+    return launch_tiles<ZK, 64, 128, 5>(w, A, M, lda, C, ldc, residual, ldr, s);
   }
-  return launched("wg_q4_gemm");
+  return launch_tiles<ZK, 64, 64, 5>(w, A, M, lda, C, ldc, residual, ldr, s);
 }
 
 }  // namespace
