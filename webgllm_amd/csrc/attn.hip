@@ -19,6 +19,7 @@
 #include "attn_core.h"
 #include "common.h"
 #include "dot.h"
+#include "lds_load.h"
 
 namespace wg {
 namespace {
@@ -100,86 +101,96 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
 }
 
 // Decode attention for GM = G * M <= 8 queries per KV head. Workgroup =
-// (KV head kh, chunk c of 64 keys), one wave per query (GM waves), lane =
-// key. Every load of the chunk is issued at the start: the lane's K row,
-// and V in 16-byte pieces (LPR lanes per row). The query is the same for
-// the whole wave and comes in through scalar loads, so the scores need
-// neither LDS nor shuffles; the chunk's softmax is a wave reduction; each V
-// row's weight comes from its lane by a shuffle; waves never wait for each
-// other. The chunk's (max, sum of weights, weighted values) go to the
-// scratch for attn_combine_kernel. (Combining in the last workgroup to
-// finish a KV head costs more here than a second launch: its agent-scope
-// release writes an XCD's L2 back once per workgroup.)
+// (KV head kh, chunk c of 64 keys), one wave per query (GM waves). Every
+// load is issued at the start, straight into LDS: each wave's query (HD
+// floats), then the chunk's K and V tiles, 1 KB an instruction, the waves
+// taking the instructions in turn, so each key and value crosses the memory
+// system once for all GM queries. K row r keeps its 16-byte piece t at slot
+// t ^ swz(r): the score loop (lane = key, reading its row piece by piece)
+// then touches 16 distinct 16-byte bank groups in any 16 consecutive lanes
+// (with 128-byte rows, rows r and r + 8 flip the slot's low bit); V rows are read whole, 16 lanes a
+// row, and keep their order. The position is read while the loads fly, and
+// the kernel waits for memory once. The chunk's softmax is a wave
+// reduction; each V row's weight comes from its lane by a shuffle. The
+// chunk's (max, sum of weights, weighted values) go to the scratch for
+// attn_combine_kernel. (Combining in the last workgroup to finish a KV
+// head costs more here than a second launch: its agent-scope release
+// writes an XCD's L2 back once per workgroup.)
 constexpr int WK = 64;   // keys a workgroup takes (the partials' chunk)
 constexpr int FGM = 8;   // queries per KV head (waves per workgroup) at most
 
 template <int HD>
-__global__ __launch_bounds__(FGM * 64) void attn_wave_kernel(
+__global__ __launch_bounds__(FGM * 64) void attn_tile_kernel(
     const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
     const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int chunks,
     uint16_t *out, int ldo) {
-  constexpr int KP = HD / 8;       // 16-byte pieces of a K row
-  constexpr int LPR = HD / 8;      // lanes per V row
-  constexpr int RPI = 64 / LPR;    // V rows per load instruction
-  constexpr int NV = WK / RPI;     // V load instructions
+  constexpr int KP = HD / 8;       // 16-byte pieces of a row
+  constexpr int ROWB = HD * 2;     // bytes of a row
+  constexpr int TILE = WK * ROWB;  // bytes of the K (or V) tile
+  constexpr int RPI = 64 / KP;     // rows one 1 KB load instruction covers
+  constexpr int NI = WK / RPI;     // load instructions a tile
+  constexpr int QOFF = 2 * TILE;   // the queries, HD floats each
+  static_assert(HD * 4 <= 1024, "a query fits one load instruction");
+  auto swz = [](int r) { return KP == 16 ? (r & 15) : ((r ^ (r >> 3)) & (KP - 1)); };
+  __shared__ __align__(16) unsigned char smem[2 * TILE + FGM * HD * 4];
   const int kh = blockIdx.x % KV, c = blockIdx.x / KV;
   const int lane = threadIdx.x & 63;
-  const int qi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int G = H / KV, g = qi % G, m = qi / G;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;  // = G * M
+  const int G = H / KV, g = wave % G, m = wave / G;
   const int j0 = c * WK;
   const int kvd = KV * HD;
-  // All loads first, before the position is known (the chunk's rows exist:
-  // j0 < max_keys), so the kernel waits for memory once: this lane's K row,
-  // then the V pieces. Keys past the position are masked below.
+  // rows at or past max_keys do not exist: their lanes load row j0 again
+  // (j0 < max_keys), and the rows are masked below like rows past the position
   const int nk_max = min(WK, max_keys - j0);
-  uint4 kr[KP];
-  {
-    const bool ok = lane < nk_max;
-    const uint4 *kp = reinterpret_cast<const uint4 *>(k_cache + (int64_t)(j0 + lane) * kvd +
-                                                      kh * HD);
-#pragma unroll
-    for (int i = 0; i < KP; i++) kr[i] = ok ? kp[i] : make_uint4(0u, 0u, 0u, 0u);
-  }
-  uint4 vr[NV];
-  const int d0 = (lane % LPR) * 8;
-#pragma unroll
-  for (int i = 0; i < NV; i++) {
-    const int r = lane / LPR + RPI * i;
-    vr[i] = r < nk_max ? *reinterpret_cast<const uint4 *>(v_cache + (int64_t)(j0 + r) * kvd +
-                                                          kh * HD + d0)
-                       : make_uint4(0u, 0u, 0u, 0u);
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  if (lane < HD / 4)
+    dma16(q + (int64_t)m * ldq + (int64_t)(kh * G + g) * HD + lane * 4,
+          __builtin_amdgcn_readfirstlane(sbase + QOFF + wave * HD * 4));
+  for (int i = wave; i < 2 * NI; i += nw) {
+    const bool is_v = i >= NI;
+    const int ii = is_v ? i - NI : i;
+    const int r = ii * RPI + lane / KP;
+    const int slot = lane % KP;
+    const int piece = is_v ? slot : (slot ^ swz(r));
+    const int rr = r < nk_max ? r : 0;
+    dma16((is_v ? v_cache : k_cache) + (int64_t)(j0 + rr) * kvd + kh * HD + piece * 8,
+          __builtin_amdgcn_readfirstlane(sbase + (is_v ? TILE : 0) + ii * 1024));
   }
   const int pos0 = *pos0_dev;
   const int n_keys = min(pos0 + M, max_keys);
-  uint16_t *o = out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD;
+  // every load has landed before any wave leaves: LDS still being written
+  // must not pass to the next workgroup
+  wait_vm<0>();
   if (n_keys <= 0) {  // no position in the cache: the output is zero
-    if (c == 0)
+    if (c == 0) {
+      uint16_t *o = out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD;
       for (int d = lane; d < HD; d += 64) o[d] = 0;
+    }
     return;
   }
   if (j0 >= n_keys) return;
+  barrier();
   const int nk = min(WK, n_keys - j0);
-  // rows past the position may hold any bits (a zero weight times a NaN is
-  // NaN): clear them
-#pragma unroll
-  for (int i = 0; i < NV; i++)
-    if (lane / LPR + RPI * i >= nk) vr[i] = make_uint4(0u, 0u, 0u, 0u);
 
-  // score of key lane: q (uniform, scalar loads) . k
-  const float *qv = q + (int64_t)m * ldq + (int64_t)(kh * G + g) * HD;
+  // score of key lane: q . k, the query read from LDS (every lane the same
+  // address: a broadcast)
+  const float4 *ql = reinterpret_cast<const float4 *>(smem + QOFF + wave * HD * 4);
+  const unsigned char *krow = smem + lane * ROWB;
   float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
 #pragma unroll
   for (int i = 0; i < KP; i++) {
-    const half2v a = as_h2(kr[i].x), b = as_h2(kr[i].y), cc = as_h2(kr[i].z),
-                 dd = as_h2(kr[i].w);
-    s0 = __builtin_fmaf(qv[8 * i + 0], (float)a.x, s0);
-    s1 = __builtin_fmaf(qv[8 * i + 1], (float)a.y, s1);
-    s2 = __builtin_fmaf(qv[8 * i + 2], (float)b.x, s2);
-    s3 = __builtin_fmaf(qv[8 * i + 3], (float)b.y, s3);
-    s0 = __builtin_fmaf(qv[8 * i + 4], (float)cc.x, s0);
-    s1 = __builtin_fmaf(qv[8 * i + 5], (float)cc.y, s1);
-    s2 = __builtin_fmaf(qv[8 * i + 6], (float)dd.x, s2);
-    s3 = __builtin_fmaf(qv[8 * i + 7], (float)dd.y, s3);
+    const uint4 kr = *reinterpret_cast<const uint4 *>(krow + ((i ^ swz(lane)) * 16));
+    const half2v a = as_h2(kr.x), b = as_h2(kr.y), cc = as_h2(kr.z), dd = as_h2(kr.w);
+    const float4 qa = ql[2 * i], qb = ql[2 * i + 1];
+    s0 = __builtin_fmaf(qa.x, (float)a.x, s0);
+    s1 = __builtin_fmaf(qa.y, (float)a.y, s1);
+    s2 = __builtin_fmaf(qa.z, (float)b.x, s2);
+    s3 = __builtin_fmaf(qa.w, (float)b.y, s3);
+    s0 = __builtin_fmaf(qb.x, (float)cc.x, s0);
+    s1 = __builtin_fmaf(qb.y, (float)cc.y, s1);
+    s2 = __builtin_fmaf(qb.z, (float)dd.x, s2);
+    s3 = __builtin_fmaf(qb.w, (float)dd.y, s3);
   }
   const bool vis = lane < nk && j0 + lane <= pos0 + m;  // causal
   const float sc = vis ? (s0 + s1) + (s2 + s3) : -INFINITY;
@@ -189,12 +200,18 @@ __global__ __launch_bounds__(FGM * 64) void attn_wave_kernel(
   const float e = (mx == -INFINITY || !vis) ? 0.0f : __expf(sc - mx);
   const float lsum = wave_sum(e);
 
-  // weighted values: lane holds dims d0..d0+7 of rows lane / LPR + RPI i
+  // weighted values: lane holds dims d0..d0+7 of rows lane / KP + RPI i;
+  // rows past the position may hold any bits (a zero weight times a NaN is
+  // NaN): they are read as zero
+  const int d0 = (lane % KP) * 8;
   float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int i = 0; i < NV; i++) {
-    const float w = __shfl(e, lane / LPR + RPI * i, 64);
-    const uint32_t w4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+  for (int i = 0; i < NI; i++) {
+    const int r = lane / KP + RPI * i;
+    uint4 vr = *reinterpret_cast<const uint4 *>(smem + TILE + r * ROWB + (lane % KP) * 16);
+    if (r >= nk) vr = make_uint4(0u, 0u, 0u, 0u);
+    const float w = __shfl(e, r, 64);
+    const uint32_t w4[4] = {vr.x, vr.y, vr.z, vr.w};
 #pragma unroll
     for (int t = 0; t < 4; t++) {
       const half2v hv = as_h2(w4[t]);
@@ -203,19 +220,18 @@ __global__ __launch_bounds__(FGM * 64) void attn_wave_kernel(
     }
   }
 #pragma unroll
-  for (int off = LPR; off < 64; off <<= 1)
+  for (int off = KP; off < 64; off <<= 1)
 #pragma unroll
     for (int t = 0; t < 8; t++) acc[t] += __shfl_xor(acc[t], off, 64);
   PartialLayout pl{HD, chunks};
   float *po = partial + pl.base(m * H + kh * G + g, c);
-  if (lane < LPR)
+  if (lane < KP)
 #pragma unroll
     for (int t = 0; t < 8; t++) po[2 + d0 + t] = acc[t];
   if (lane == 0) {
     po[0] = mx;
     po[1] = lsum;
   }
-
 }
 
 // The chunks' online-softmax combine (attendPanelCombine): one wave per
@@ -367,10 +383,10 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
   if ((H / KV) * M <= FGM) {
     dim3 grid((unsigned)(KV * chunks));
     if (hd == 64)
-      attn_wave_kernel<64><<<grid, 64 * (H / KV) * M, 0, s>>>(
+      attn_tile_kernel<64><<<grid, 64 * (H / KV) * M, 0, s>>>(
           q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, partial, chunks, out, ldo);
     else
-      attn_wave_kernel<128><<<grid, 64 * (H / KV) * M, 0, s>>>(
+      attn_tile_kernel<128><<<grid, 64 * (H / KV) * M, 0, s>>>(
           q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, partial, chunks, out, ldo);
   } else {
     size_t lds = attn_lds_bytes((H / KV) * M, hd);

@@ -34,6 +34,7 @@
 //    it is read from HBM once into that XCD's L2.
 #include "common.h"
 #include "dot.h"
+#include "lds_load.h"
 
 namespace wg {
 namespace {
@@ -83,31 +84,6 @@ __device__ inline void dequant8(uint2 bytes, uint16_t scale_bits, float zero, ha
       hi[t] = (_Float16)(((float)(byte >> 4) - zero) * df);
     }
   }
-}
-
-// 16 bytes a lane from `src` into LDS at byte address lds + 16 * lane
-// (lds uniform across the wave); `lanes` of the wave take part.
-__device__ inline void dma16(const void *src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
-               : "memory");
-}
-// 4 bytes a lane into LDS at lds + 4 * lane.
-__device__ inline void dma4(const void *src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(src)
-               : "memory");
-}
-
-// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14).
-template <int N>
-__device__ inline void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-
-__device__ inline void barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 template <int ZK, int BN>
