@@ -371,6 +371,17 @@ int wg_conv_accept(const float *prefixes, int32_t kept, int32_t rows, int32_t D,
 size_t wg_argmax_scratch_bytes(int32_t M, int32_t V);
 int wg_argmax_rows(const float *logits, int32_t M, int32_t V, int32_t ld, int32_t *ids,
                    float *tops, void *scratch, size_t scratch_bytes, void *stream);
+/* One greedy decode step's pick and advance, on the device: the pick of one
+ * row of V logits (as wg_argmax_rows, same scratch size for M = 1), then
+ * ids[0] = the pick, hist[*pos + 1] = the pick when 0 <= *pos + 1 < hist_len
+ * (hist may be NULL with hist_len 0), *pos += 1. A captured decode step
+ * thereby replays at successive positions, its input the previous pick, as
+ * the reference's guessed forward reads CHUNK_ARGMAX's pick from the ids
+ * texture without the host (Engine.forwardGuess, engine.ts:8095-8110,
+ * Engine.argmax guess, :8318-8336). */
+int wg_argmax_advance(const float *logits, int32_t V, int32_t *ids, int32_t *pos, int32_t *hist,
+                      int32_t hist_len, float *tops, void *scratch, size_t scratch_bytes,
+                      void *stream);
 
 #ifdef __cplusplus
 }

@@ -134,3 +134,16 @@ def test_decode_plan_rejects_before_any_device_work():
     assert lib.wg_decode_plan_create(arr, 1, C.byref(h)) == -6  # unsupported
     assert "row-group" in L.last_error()
     assert not h.value
+
+
+def test_argmax_advance_rejects_before_any_device_work():
+    lib = L.load()
+    f = 0x1000  # fake device addresses: validation fails before a launch
+    with pytest.raises(L.WgError, match="null argument"):
+        L.check(lib.wg_argmax_advance(f, 100, f, None, None, 0, None, f, 4096, None))
+    with pytest.raises(L.WgError, match="history of 4 entries"):
+        L.check(lib.wg_argmax_advance(f, 100, f, f, None, 4, None, f, 4096, None))
+    need = lib.wg_argmax_scratch_bytes(1, 128256)
+    assert need == 2 * 4 * ((128256 + 1023) // 1024)
+    with pytest.raises(L.WgError, match="scratch of"):
+        L.check(lib.wg_argmax_advance(f, 128256, f, f, None, 0, None, f, need - 1, None))

@@ -240,8 +240,42 @@ def test_argmax(hip, V):
     for m in range(3):
         assert ids[m] == O.argmax(x[m])[0]
     assert ids[1] == V // 3 and ids[2] == 0
-    # chunk boundary tie (256-logit chunks in the reference; 4096 here)
-    y = np.full((1, V), -1.0, np.float32)
-    y[0, min(V - 1, 4096)] = 3
-    y[0, min(V - 1, 4095)] = 3
-    assert ops.argmax_rows(_t(y)).cpu().numpy()[0] == O.argmax(y[0])[0]
+    # chunk boundary ties (256-logit chunks in the reference; 1024-logit
+    # workgroups and 256-logit thread strides here)
+    for b in (256, 1024, 4096):
+        y = np.full((1, V), -1.0, np.float32)
+        y[0, min(V - 1, b)] = 3
+        y[0, min(V - 1, b - 1)] = 3
+        assert ops.argmax_rows(_t(y)).cpu().numpy()[0] == O.argmax(y[0])[0]
+
+
+@pytest.mark.parametrize("V", [1000, 128256])
+def test_argmax_advance(hip, V):
+    """The decode step's pick and advance: ids[0] = the pick, hist[pos + 1]
+    = the pick, pos + 1; at the history's end the pick is not stored."""
+    import torch
+    from webgllm_amd import ops
+    rng = np.random.default_rng(V + 1)
+    x = rng.standard_normal(V).astype(np.float32)
+    x[V // 5] = 9.0
+    x[V // 2] = 9.0  # tie: lower id
+    ids = torch.full((8,), -1, dtype=torch.int32, device="cuda")
+    pos = torch.tensor([5], dtype=torch.int32, device="cuda")
+    hist = torch.full((8,), -1, dtype=torch.int32, device="cuda")
+    tops = torch.zeros(1, device="cuda")
+    ops.argmax_advance(_t(x), ids, pos, hist=hist, tops=tops)
+    want = O.argmax(x)[0]
+    assert want == V // 5
+    assert ids.cpu().tolist() == [want] + [-1] * 7
+    assert pos.item() == 6
+    assert hist.cpu().tolist() == [-1] * 6 + [want, -1]
+    assert tops.item() == 9.0
+    # twice more: pos 6 -> hist[7], then pos 7 -> hist[8] is past the end
+    x[3] = 20.0
+    ops.argmax_advance(_t(x), ids, pos, hist=hist)
+    ops.argmax_advance(_t(x), ids, pos, hist=hist)
+    assert pos.item() == 8 and ids[0].item() == 3
+    assert hist.cpu().tolist() == [-1] * 6 + [want, 3]
+    # no history
+    ops.argmax_advance(_t(x), ids, pos)
+    assert pos.item() == 9

@@ -42,6 +42,48 @@ __device__ inline void input_scales(const wg_epilogue &e, float s[M]) {
   }
 }
 
+// input_scales computed by a workgroup of NW waves together: wave w sums
+// the 16-byte pieces w, w + NW, ... of the parts, and the waves' sums meet
+// in LDS (`lds`: NW * M floats), so a workgroup reads the parts once rather
+// than once a wave (every wave of every workgroup reads the same lines at
+// the kernel's start). Every thread of the workgroup calls it: it holds a
+// barrier.
+template <int M, int NW>
+__device__ inline void input_scales_wg(const wg_epilogue &e, float s[M], float *lds) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (e.norm_parts) {
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const float *p = e.norm_parts + (int64_t)m * e.ld_parts_in;
+      float a = 0.0f;
+      if ((((uintptr_t)p) & 15) == 0 && (e.n_parts & 3) == 0) {
+        const float4 *p4 = reinterpret_cast<const float4 *>(p);
+        for (int i = wave * 64 + lane; i < (e.n_parts >> 2); i += NW * 64) {
+          float4 t = p4[i];
+          a += (t.x + t.y) + (t.z + t.w);
+        }
+      } else {
+        for (int i = wave * 64 + lane; i < e.n_parts; i += NW * 64) a += p[i];
+      }
+      a = wave_sum(a);
+      if (lane == 0) lds[wave * M + m] = a;
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int m = 0; m < M; m++) {
+    float v = 1.0f;
+    if (e.norm_parts) {
+      float a = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; w++) a += lds[w * M + m];
+      v = e.norm_mult / sqrtf(a / (float)e.norm_count + e.eps);
+    }
+    if (e.row_scale) v *= e.row_scale[m];
+    s[m] = v;
+  }
+}
+
 // The epilogue's operands of one row group that do not depend on its sums,
 // loaded ahead (with the row group's weights) so the epilogue does not wait
 // for memory: the residual and the next norm's weight (STORE), the rope

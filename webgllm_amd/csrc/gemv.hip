@@ -102,6 +102,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
     float *__restrict__ y, int ldy, const wg_epilogue e, int G, int B) {
   constexpr int RGW = 4 / KS;  // row groups a workgroup takes at a time
   __shared__ float red[2][4][4 * M];
+  __shared__ float nred[4 * M];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int part = wave % KS, slot = wave / KS;
   const int BP = (B + KS - 1) / KS;
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
       }
     }
   float scale[M];
-  input_scales<M>(e, scale);
+  input_scales_wg<M, 4>(e, scale, nred);
 #pragma unroll
   for (int m = 0; m < M; m++)
 #pragma unroll

@@ -315,8 +315,10 @@ class Engine:
             torch.cuda.current_stream().synchronize()
             self.plan.status()
 
-    def _forward_rows(self, M: int, keep_prefixes: bool) -> None:
-        """Enqueue one batch of M rows (ids[:M] at positions pos..pos+M-1)."""
+    def _forward_rows(self, M: int, keep_prefixes: bool, pick: bool = True) -> None:
+        """Enqueue one batch of M rows (ids[:M] at positions pos..pos+M-1);
+        the greedy picks into next_ids unless `pick` is False (the caller
+        picks)."""
         s, w = self.shape, self.w
         D, F = s.hidden, s.intermediate
         h = self.h[:M]
@@ -361,8 +363,9 @@ class Engine:
                      epilogue=self._residual_out(M, self._next_norm(i)))
         ops.gemv(w.embedding, x16, out=self.logits[:M],
                  epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
-        ops.argmax_rows(self.logits[:M], ids=self.next_ids[:M], tops=self.tops[:M],
-                        scratch=self.argmax_scratch)
+        if pick:
+            ops.argmax_rows(self.logits[:M], ids=self.next_ids[:M], tops=self.tops[:M],
+                            scratch=self.argmax_scratch)
 
     # --- the reference's Engine API -------------------------------------------
     def reset(self) -> None:
@@ -436,11 +439,11 @@ class Engine:
         self.graph = g
 
     def _step_body(self) -> None:
-        self._forward_rows(1, keep_prefixes=False)
-        self.ids[0:1].copy_(self.next_ids[0:1])
-        self.pos.add_(1)
-        # hist[pos + 1] = the token picked at pos
-        self.hist.index_copy_(0, self.pos.long(), self.next_ids[0:1])
+        # the pick goes to ids[0] and hist[pos + 1], then pos += 1: the next
+        # replay runs the picked token at the next position
+        self._forward_rows(1, keep_prefixes=False, pick=False)
+        ops.argmax_advance(self.logits[0], self.ids, self.pos, hist=self.hist,
+                           tops=self.tops[:1], scratch=self.argmax_scratch)
 
     def _save(self):
         return (self.ids.clone(), self.pos.clone(), {i: s.clone() for i, s in self.state.items()})

@@ -144,6 +144,7 @@ def load():
         "wg_conv_accept": (C.c_int, [P, I32, I32, I32, I32, P, P]),
         "wg_argmax_scratch_bytes": (SZ, [I32, I32]),
         "wg_argmax_rows": (C.c_int, [P, I32, I32, I32, P, P, P, SZ, P]),
+        "wg_argmax_advance": (C.c_int, [P, I32, P, P, P, I32, P, P, SZ, P]),
         "wg_decode_plan_create": (C.c_int, [C.POINTER(DecodeLayer), I32, C.POINTER(P)]),
         "wg_decode_run": (C.c_int, [P, P]),
         "wg_decode_status": (C.c_int, [P]),

@@ -315,3 +315,20 @@ def argmax_rows(logits: torch.Tensor, V: int | None = None, ids=None, tops=None,
     L.check(L.load().wg_argmax_rows(_p(logits), M, V, logits.shape[1], _p(ids), _p(tops),
                                     _p(scratch), scratch.numel(), _stream()))
     return ids
+
+
+def argmax_advance(logits: torch.Tensor, ids: torch.Tensor, pos: torch.Tensor,
+                   hist: torch.Tensor | None = None, tops=None, scratch=None) -> None:
+    """A decode step's greedy pick and advance on the device: ids[0] = the
+    pick of logits' one row, hist[pos + 1] = the pick, pos += 1."""
+    logits = _dev(logits, torch.float32).reshape(-1)
+    V = logits.numel()
+    for t, name in ((ids, "ids"), (pos, "pos"), (hist, "hist")):
+        if t is not None and (t.dtype != torch.int32 or not t.is_cuda):
+            raise ValueError(f"{name} must be an int32 device tensor")
+    if scratch is None:
+        scratch = torch.empty(L.load().wg_argmax_scratch_bytes(1, V), dtype=torch.uint8,
+                              device=logits.device)
+    L.check(L.load().wg_argmax_advance(_p(logits), V, _p(ids), _p(pos), _p(hist),
+                                       0 if hist is None else hist.numel(), _p(tops),
+                                       _p(scratch), scratch.numel(), _stream()))
