@@ -45,9 +45,9 @@ const char *wg_version(void);
  * "q4k_wg_per_cu" (persistent GEMV workgroups per compute unit) and
  * "gemv_min_waves" (below this many waves a GEMV splits K inside a
  * workgroup), "decode_wg_per_cu" (persistent decode workgroups per
- * compute unit, read at plan creation) and "gemm_tile_m" (prefill GEMM
- * tile rows: 64, 128, or 0 to choose by shape). Process-wide; results never
- * depend on them. */
+ * compute unit, read at plan creation) and "gemm_tile" (prefill GEMM tile:
+ * 1 64 x 128, 2 128 x 128, 3 128 x 256, or 0 to choose by shape).
+ * Process-wide; results never depend on them. */
 int wg_tuning_set(const char *name, int32_t value);
 int wg_tuning_get(const char *name, int32_t *value);
 

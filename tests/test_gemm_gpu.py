@@ -85,3 +85,19 @@ def test_gemm_rejects(hip):
     m2 = _matrix("q4_k", 64, 256, seed=1)
     with pytest.raises(L.WgError, match="row-group"):
         ops.gemm(m2, torch.zeros((4, 256), dtype=torch.float16, device="cuda"))
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3])
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup"])
+def test_gemm_every_tile(hip, fmt, tile):
+    """Each tile shape (64 x 128, 128 x 128, 128 x 256), forced through the
+    gemm_tile knob, on ragged rows (M = 200 leaves a partial 128-row tile)."""
+    from webgllm_amd import lib as L
+    m = _matrix(fmt, 512, 1024, seed=tile)
+    L.tuning_set("gemm_tile", tile)
+    try:
+        e, e16 = _check(m, 200, seed=tile + 7)
+    finally:
+        L.tuning_set("gemm_tile", 0)
+    assert e <= 1e-3
+    assert e16 <= 1e-5

@@ -5,9 +5,12 @@
 // 4-bit matrix, C float32.
 //
 // gfx950 mapping:
-//  - a workgroup (4 waves, 2 x 2) owns a BM x BN tile of C; a wave owns
-//    (BM / 2) x (BN / 2) as MT x NT MFMA tiles of 32 x 32
-//    (v_mfma_f32_32x32x16_f16, float32 accumulation);
+//  - a workgroup owns a BM x BN tile of C (128 x 256, 128 x 128 or 64 x 128
+//    by shape); its waves split the tile's columns, 32 each, so a wave owns
+//    BM x 32 as BM / 32 MFMA tiles of 32 x 32 (v_mfma_f32_32x32x16_f16,
+//    float32 accumulation) and every weight is dequantized once per
+//    workgroup, feeding BM / 32 MFMAs (the vector work per MFMA, not HBM or
+//    LDS, is what bounds this kernel at M = 512);
 //  - K goes in steps of 64 (two 32-weight blocks) through an S-stage ring
 //    in LDS: each stage holds the A tile (16-byte chunk c of row r at
 //    position c ^ (r / 2 % 8), so the 16 rows an operand read takes at once
@@ -15,15 +18,20 @@
 //    weight tile's raw nibbles (a row group's two blocks are 128 contiguous
 //    bytes), its half scales and its zero points;
 //  - stages are filled by direct global-to-LDS loads
-//    (global_load_lds_dwordx4), issued S - 1 steps ahead of their use, so
+//    (global_load_lds_dwordx4, per-lane offsets fixed for the whole K loop
+//    from scalar bases that step by a constant), issued S - 1 steps ahead
+//    of their use, so
 //    every step computes while the next ones stream in. Every wave issues
 //    the same number of loads a stage, so "this wave's loads of stage kt
 //    have landed" is one vmcnt wait; a workgroup barrier then covers the
 //    other waves'. The loads are issued from inline assembly: the compiler
 //    cannot tell which in-flight stage a later LDS read depends on and would
 //    otherwise wait for all of them;
+//  - the K loop is unrolled by S, so every LDS address is an immediate
+//    offset;
 //  - weights are dequantized from LDS to halves in registers, d (q - z)
 //    rounded once as the reference's dequantOut does: 1024 + q as a half
+//    (a nibble byte under a 0x64 exponent byte, one byte permute a pair)
 //    minus 1024 + z is exact in packed f16, then one multiply by d. A
 //    32-weight block is two K = 16 MFMA steps: lane half h takes bytes
 //    8h..8h+7 of the block's row, whose low nibbles are weights 8h.. (the
@@ -53,14 +61,17 @@ __device__ inline void dequant8(uint2 bytes, uint16_t scale_bits, float zero, ha
     // 1024 + q as a half (q in the low mantissa bits), minus 1024 + z: exact.
     const _Float16 off = (_Float16)(1024.0f + zero);
     half2v off2 = {off, off}, d2 = {d, d};
+    // The nibbles of a word masked once, low and high; then each half pair
+    // is one byte permute that takes two nibble bytes and puts the 0x64
+    // exponent byte (from k64) above each.
+    const uint32_t k64 = 0x64646464u;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-      uint32_t p0 = __builtin_amdgcn_perm(0u, w[i], SEL01);
-      uint32_t p1 = __builtin_amdgcn_perm(0u, w[i], SEL23);
-      half2v l0 = as_h2((p0 & LO4) | 0x64006400u) - off2;
-      half2v l1 = as_h2((p1 & LO4) | 0x64006400u) - off2;
-      half2v h0 = as_h2(((p0 >> 4) & LO4) | 0x64006400u) - off2;
-      half2v h1 = as_h2(((p1 >> 4) & LO4) | 0x64006400u) - off2;
+      const uint32_t lo4 = w[i] & 0x0f0f0f0fu, hi4 = (w[i] >> 4) & 0x0f0f0f0fu;
+      half2v l0 = as_h2(__builtin_amdgcn_perm(k64, lo4, 0x04010400u)) - off2;
+      half2v l1 = as_h2(__builtin_amdgcn_perm(k64, lo4, 0x04030402u)) - off2;
+      half2v h0 = as_h2(__builtin_amdgcn_perm(k64, hi4, 0x04010400u)) - off2;
+      half2v h1 = as_h2(__builtin_amdgcn_perm(k64, hi4, 0x04030402u)) - off2;
       l0 = l0 * d2;
       l1 = l1 * d2;
       h0 = h0 * d2;
@@ -93,26 +104,31 @@ struct Stage {
   static constexpr int WZ = ZK == WG_ZERO_F16 ? BN * 4 : ZK == WG_ZERO_U8 ? BN * 2 : 0;
 };
 
-// BM x BN tiles, S stages of BK = 64.
-template <int ZK, int BM, int BN, int S>
-__global__ __launch_bounds__(256) void gemm_q4_kernel(const uint8_t *__restrict__ quants,
+// BM x BN tiles, S stages of BK = 64, a WGM x WGN grid of waves.
+template <int ZK, int BM, int BN, int S, int WGM, int WGN>
+__global__ __launch_bounds__(WGM * WGN * 64) void gemm_q4_kernel(const uint8_t *__restrict__ quants,
                                                       const uint16_t *__restrict__ scales,
                                                       const void *__restrict__ zeros,
                                                       const uint16_t *__restrict__ A, int lda,
                                                       float *__restrict__ C, int ldc,
                                                       const float *residual, int ldr, int M,
                                                       int N, int K) {
-  constexpr int WM = BM / 2, WN = BN / 2, MT = WM / 32, NT = WN / 32;
+  constexpr int NWV = WGM * WGN;  // waves
+  constexpr int WM = BM / WGM, WN = BN / WGN, MT = WM / 32, NT = WN / 32;
+  static_assert(MT >= 1 && NT >= 1 && WM % 32 == 0 && WN % 32 == 0, "32 x 32 MFMA tiles");
   constexpr int A_BYTES = BM * 128;
   constexpr int WQ = Stage<ZK, BN>::WQ, WS = Stage<ZK, BN>::WS, WZ = Stage<ZK, BN>::WZ;
   constexpr int STAGE = A_BYTES + WQ + WS + WZ;
-  constexpr int IA = BM / 32;  // A loads a wave issues a stage
+  constexpr int IA = BM * 128 / 1024 / NWV;  // A loads (1 KB each) a wave issues a stage
+  static_assert(IA >= 1 && IA * NWV * 1024 == A_BYTES, "A tile splits evenly over the waves");
   constexpr int NW = IA + 2 + (ZK == WG_ZERO_U8 ? 1 : 0);  // loads a wave issues a stage
   extern __shared__ __align__(16) unsigned char smem[];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
-  // Tile order: ids equal mod 8 (one XCD) run the M tiles of one weight tile in turn.
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN, h = lane >> 5;
+  // Tile order: ids equal mod 8 (one XCD) run the M tiles of one weight
+  // tile in turn, so it is read from HBM once into that XCD's L2.
   const int tiles_m = (M + BM - 1) / BM, tiles_n = N / BN;
   int id = blockIdx.x, tm, tn;
   if (tiles_n % 8 == 0) {
@@ -127,41 +143,49 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(const uint8_t *__restrict_
   const int B = K / 32, KT = K / 64;
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
 
-  // Issue this wave's loads of step kt into stage st.
+  // This wave's loads of a step: per-lane byte offsets fixed for the whole
+  // K loop, from wave-uniform bases that step kt moves by a fixed stride
+  // (A: 64 halves; nibbles: two blocks of 64 bytes a row group; scales and
+  // half zero points: 8 halves; u8 zero points: 8 bytes).
+  constexpr int PWQ = 2 * BN / NWV;  // nibble pieces (16 bytes) a wave
+  static_assert(PWQ >= 1 && PWQ <= 64 && PWQ * NWV == 2 * BN, "nibble pieces");
+  constexpr int NSC = BN / 4, PIECES = ZK == WG_ZERO_F16 ? 2 * NSC : NSC, PWS = PIECES / NWV;
+  static_assert(PWS >= 1 && PWS * NWV == PIECES && NSC % PWS == 0, "scale pieces");
+  constexpr int PWZ = ZK == WG_ZERO_U8 ? 2 * BN / 4 / NWV : 1;
+  static_assert(ZK != WG_ZERO_U8 || (PWZ >= 1 && PWZ * NWV * 4 == 2 * BN), "zero-point pieces");
+  uint32_t off_a[IA];
+#pragma unroll
+  for (int i = 0; i < IA; i++) {
+    const int p = (i * NWV + wave) * 64 + lane;  // 16-byte piece of the A tile
+    const int row = p >> 3, c = (p & 7) ^ ((row >> 1) & 7);
+    const int m = min(m0 + row, M - 1);
+    off_a[i] = (uint32_t)(((int64_t)m * lda + c * 8) * 2);
+  }
+  const int qq = wave * PWQ + lane;
+  const uint32_t off_q = (uint32_t)(((int64_t)(g0 + (qq >> 3)) * B) * 64 + (qq & 7) * 16);
+  const int qs = wave * PWS + lane;
+  const bool s_is_zero = wave * PWS >= NSC;  // wave-uniform
+  const uint32_t off_s = (uint32_t)((int64_t)(g0 + (s_is_zero ? qs - NSC : qs)) * B * 8);
+  const int qz = wave * PWZ + lane;
+  const uint32_t off_z = (uint32_t)(((int64_t)(g0 + (qz >> 1)) * B) * 4 + (qz & 1) * 4);
+  const unsigned char *s_base =
+      s_is_zero ? (const unsigned char *)zeros : (const unsigned char *)scales;
   auto issue = [&](int kt, int st) {
     const uint32_t base = sbase + st * STAGE;
-    const int b0 = 2 * kt;
 #pragma unroll
-    for (int i = 0; i < IA; i++) {
-      const int p = (i * 4 + wave) * 64 + lane;  // 16-byte piece of the A tile
-      const int row = p >> 3, c = (p & 7) ^ ((row >> 1) & 7);
-      const int m = min(m0 + row, M - 1);
-      dma16(A + (int64_t)m * lda + kt * 64 + c * 8,
-            __builtin_amdgcn_readfirstlane(base + (i * 4 + wave) * 1024));
-    }
-    {  // raw nibbles: BN / 2 pieces a wave
-      constexpr int PW = BN / 2;
-      const int q = wave * PW + lane;
-      if (lane < PW)
-        dma16(quants + ((int64_t)(g0 + (q >> 3)) * B + b0) * 64 + (q & 7) * 16,
-              __builtin_amdgcn_readfirstlane(base + A_BYTES + wave * PW * 16));
-    }
-    {  // scales (and half zero points) of the BN / 4 row groups
-      constexpr int NS = BN / 4, PIECES = ZK == WG_ZERO_F16 ? 2 * NS : NS, PW = PIECES / 4;
-      const int q = wave * PW + lane;
-      if (lane < PW) {
-        const void *src = q < NS ? (const void *)(scales + ((int64_t)(g0 + q) * B + b0) * 4)
-                                 : (const void *)((const uint16_t *)zeros +
-                                                  ((int64_t)(g0 + q - NS) * B + b0) * 4);
-        dma16(src, __builtin_amdgcn_readfirstlane(base + A_BYTES + WQ + wave * PW * 16));
-      }
-    }
+    for (int i = 0; i < IA; i++)
+      dma16((const unsigned char *)A + kt * 128, off_a[i],
+            __builtin_amdgcn_readfirstlane(base + (i * NWV + wave) * 1024));
+    if (lane < PWQ)
+      dma16(quants + kt * 128, off_q,
+            __builtin_amdgcn_readfirstlane(base + A_BYTES + wave * PWQ * 16));
+    if (lane < PWS)
+      dma16(s_base + kt * 16, off_s,
+            __builtin_amdgcn_readfirstlane(base + A_BYTES + WQ + wave * PWS * 16));
     if constexpr (ZK == WG_ZERO_U8) {  // 8 zero-point bytes a row group, 4 at a time
-      constexpr int PW = BN / 8;
-      const int q = wave * PW + lane;
-      if (lane < PW)
-        dma4((const uint8_t *)zeros + ((int64_t)(g0 + (q >> 1)) * B + b0) * 4 + (q & 1) * 4,
-             __builtin_amdgcn_readfirstlane(base + A_BYTES + WQ + WS + wave * PW * 4));
+      if (lane < PWZ)
+        dma4((const uint8_t *)zeros + kt * 8, off_z,
+             __builtin_amdgcn_readfirstlane(base + A_BYTES + WQ + WS + wave * PWZ * 4));
     }
   };
 
@@ -175,13 +199,19 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(const uint8_t *__restrict_
 
   for (int s = 0; s < S - 1; s++)
     if (s < KT) issue(s, s);
-  for (int kt = 0; kt < KT; kt++) {
+  // Unrolled by S: a step's stage is a constant, so its LDS addresses are
+  // immediate offsets.
+  for (int k0 = 0; k0 < KT; k0 += S) {
+#pragma unroll
+  for (int ss = 0; ss < S; ss++) {
+    const int kt = k0 + ss;
+    if (kt >= KT) break;
     // this wave's loads of step kt have landed (younger stages may fly on)
     if (kt + S - 2 < KT) wait_vm<NW * (S - 2)>();
     else wait_vm<0>();
     barrier();  // every wave's have, and every wave is done with step kt - 1
-    if (kt + S - 1 < KT) issue(kt + S - 1, (kt + S - 1) % S);
-    const unsigned char *st = smem + (kt % S) * STAGE;
+    if (kt + S - 1 < KT) issue(kt + S - 1, (ss + S - 1) % S);
+    const unsigned char *st = smem + ss * STAGE;
     const uint16_t *As = reinterpret_cast<const uint16_t *>(st);
     const unsigned char *Wq = st + A_BYTES;
     const uint16_t *Ws = reinterpret_cast<const uint16_t *>(st + A_BYTES + WQ);
@@ -235,6 +265,7 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(const uint8_t *__restrict_
                                                               0, 0, 0);
     }
   }
+  }
 
   // D[j] of lane i: row 8 (j / 4) + 4 (i / 32) + j % 4, column i % 32.
 #pragma unroll
@@ -254,19 +285,19 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(const uint8_t *__restrict_
   }
 }
 
-template <int ZK, int BM, int BN, int S>
+template <int ZK, int BM, int BN, int S, int WGM = 2, int WGN = 2>
 int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
                  const float *residual, int ldr, hipStream_t s) {
   constexpr int STAGE = BM * 128 + Stage<ZK, BN>::WQ + Stage<ZK, BN>::WS + Stage<ZK, BN>::WZ;
   constexpr size_t LDS = (size_t)S * STAGE;
   static bool raised = false;  // allow more than 64 KiB of dynamic LDS, once
   if (!raised && LDS > 64 * 1024) {
-    WG_HIP(hipFuncSetAttribute((const void *)gemm_q4_kernel<ZK, BM, BN, S>,
+    WG_HIP(hipFuncSetAttribute((const void *)gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS));
     raised = true;
   }
   const int grid = ((M + BM - 1) / BM) * (w->N / BN);
-  gemm_q4_kernel<ZK, BM, BN, S><<<grid, 256, LDS, s>>>(
+  gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN><<<grid, WGM * WGN * 64, LDS, s>>>(
       (const uint8_t *)w->quants, (const uint16_t *)w->scales, w->zeros, A, lda, C, ldc,
       residual, ldr, M, w->N, w->K);
   return launched("wg_q4_gemm");
@@ -275,16 +306,25 @@ int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float
 template <int ZK>
 int launch(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
            const float *residual, int ldr, hipStream_t s) {
-  // 128 x 128 tiles when they alone cover the compute units, else 64-row
-  // tiles (more workgroups, a deeper ring); 64-wide tiles for N not a
-  // multiple of 128.
-  if (w->N % 128 == 0) {
-    const int tm = tuning("gemm_tile_m");
-    if (tm == 128 || (tm != 64 && (int64_t)((M + 127) / 128) * (w->N / 128) >= 256))
-      return launch_tiles<ZK, 128, 128, 3>(w, A, M, lda, C, ldc, residual, ldr, s);
-    return launch_tiles<ZK, 64, 128, 5>(w, A, M, lda, C, ldc, residual, ldr, s);
+  // The largest tile whose count still covers most compute units: each
+  // weight is dequantized once per tile, so taller tiles (more rows a
+  // wave) spend fewer vector instructions per MFMA. The knob gemm_tile
+  // forces one (1: 64 x 128, 2: 128 x 128, 3: 128 x 256).
+  const int cus = persistent_grid(1 << 30, 1);
+  const int64_t tm128 = (M + 127) / 128;
+  int t = tuning("gemm_tile");
+  if (t == 0) {
+    if (w->N % 256 == 0 && tm128 * (w->N / 256) * 4 >= (int64_t)cus * 3) t = 3;
+    else if (w->N % 128 == 0 && tm128 * (w->N / 128) * 4 >= (int64_t)cus * 3) t = 2;
+    else if (w->N % 128 == 0) t = 1;
   }
-  return launch_tiles<ZK, 64, 64, 5>(w, A, M, lda, C, ldc, residual, ldr, s);
+  if (t == 3 && w->N % 256 == 0)
+    return launch_tiles<ZK, 128, 256, 3, 1, 8>(w, A, M, lda, C, ldc, residual, ldr, s);
+  if (t == 2 && w->N % 128 == 0)
+    return launch_tiles<ZK, 128, 128, 3, 1, 4>(w, A, M, lda, C, ldc, residual, ldr, s);
+  if (w->N % 128 == 0)
+    return launch_tiles<ZK, 64, 128, 4, 1, 4>(w, A, M, lda, C, ldc, residual, ldr, s);
+  return launch_tiles<ZK, 64, 64, 5, 1, 2>(w, A, M, lda, C, ldc, residual, ldr, s);
 }
 
 }  // namespace
@@ -306,6 +346,9 @@ int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda,
   WG_REQUIRE(lda >= w->K && lda % 8 == 0 && ((uintptr_t)A & 15) == 0,
              "wg_q4_gemm: activations need a 16-byte aligned stride >= K");
   WG_REQUIRE(ldc >= w->N, "wg_q4_gemm: ldc %d < N %d", ldc, w->N);
+  WG_REQUIRE((int64_t)M * lda * 2 < ((int64_t)1 << 31) && (int64_t)w->N * w->K < ((int64_t)1 << 32),
+             "wg_q4_gemm: %d x %d activations or a %d x %d matrix past 2 GiB", M, lda, w->N,
+             w->K);
   WG_REQUIRE(!overlaps(A, (size_t)M * lda * 2, C, (size_t)M * ldc * 4),
              "wg_q4_gemm: activations and output overlap");
   if (residual) {

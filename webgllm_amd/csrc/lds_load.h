@@ -16,6 +16,19 @@ __device__ inline void dma16(const void *src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
                : "memory");
 }
+// The same from base + off: a wave-uniform 64-bit base in SGPRs (stepped by
+// scalar adds) and a 32-bit per-lane byte offset, so a stream that advances
+// by a fixed stride costs no vector instructions a step.
+__device__ inline void dma16(const void *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off),
+               "s"(base)
+               : "memory");
+}
+__device__ inline void dma4(const void *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(off),
+               "s"(base)
+               : "memory");
+}
 // 4 bytes a lane into LDS at lds + 4 * lane.
 __device__ inline void dma4(const void *src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(src)
