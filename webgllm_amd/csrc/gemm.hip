@@ -104,9 +104,20 @@ struct Stage {
   static constexpr int WZ = ZK == WG_ZERO_F16 ? BN * 4 : ZK == WG_ZERO_U8 ? BN * 2 : 0;
 };
 
+// Waves a SIMD holds at once, as the LDS ring allows (160 KB a compute
+// unit, 4 SIMDs): the register budget the compiler may spend.
+template <int ZK, int BM, int BN, int S, int NWV>
+constexpr int gemm_waves_per_simd() {
+  constexpr int stage = BM * 128 + Stage<ZK, BN>::WQ + Stage<ZK, BN>::WS + Stage<ZK, BN>::WZ;
+  constexpr int wgs = (160 * 1024) / (S * stage);
+  constexpr int w = (wgs * NWV + 3) / 4;
+  return w < 1 ? 1 : w > 8 ? 8 : w;
+}
+
 // BM x BN tiles, S stages of BK = 64, a WGM x WGN grid of waves.
 template <int ZK, int BM, int BN, int S, int WGM, int WGN>
-__global__ __launch_bounds__(WGM * WGN * 64) void gemm_q4_kernel(const uint8_t *__restrict__ quants,
+__global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
+    1, gemm_waves_per_simd<ZK, BM, BN, S, WGM * WGN>()))) void gemm_q4_kernel(const uint8_t *__restrict__ quants,
                                                       const uint16_t *__restrict__ scales,
                                                       const void *__restrict__ zeros,
                                                       const uint16_t *__restrict__ A, int lda,
