@@ -233,9 +233,14 @@ int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx,
  * matrix (N and K multiples of 64); float32 C [M][ldc]. Weights are
  * dequantized in registers to halves, d (q - z) rounded once as dequantOut
  * does (kernels.ts:436-597), and multiplied on MFMA (v_mfma_f32_32x32x16_f16)
- * with float32 accumulation. residual may equal C. */
+ * with float32 accumulation. residual may equal C. col_of (or NULL for
+ * n -> n) maps the matrix's stored row n to its output column: a matrix
+ * uploaded with a row order (the loaders' srcRows, stored row n = logical
+ * row col_of[n]) then comes out in logical order; entries outside 0..N-1
+ * are not written. */
 int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda, float *C,
-               int32_t ldc, const float *residual, int32_t ldr, void *stream);
+               int32_t ldc, const float *residual, int32_t ldr, const int32_t *col_of,
+               void *stream);
 
 /* float32 -> half activations, clamped to +-65504 (packH2, kernels.ts:32-36). */
 int wg_f32_to_f16(const float *x, uint16_t *out, int64_t n, void *stream);
@@ -332,6 +337,16 @@ int wg_head_prep(const float *qkv, int32_t M, int32_t ldq, const wg_attn_shape *
                  const int32_t *pos0, float *q_out, int32_t ldqo, uint16_t *k_cache,
                  uint16_t *v_cache, int32_t ctx, void *stream);
 
+/* Prefill attention for a prompt batch: the reference's chunked scores /
+ * attend plan for many query rows (Engine.attention, engine.ts:6359-6630).
+ * q [M][ldq] f32 (as wg_head_prep writes it), rows at positions *pos0 + m,
+ * each row m seeing keys 0 .. *pos0 + m of the caches (rows < max_keys);
+ * out [M][ldo] halves. Scores and softmax in f32 with an online softmax
+ * over 64-key chunks; no scratch. head_dim 64 or 128, at most 32 query
+ * heads per KV head, q 16-byte aligned with ldq % 4 == 0. */
+int wg_attn_prefill(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *shape,
+                    const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0,
+                    int32_t max_keys, uint16_t *out, int32_t ldo, void *stream);
 /* Decode / verify attention (scores, attend, attendPanel + attendPanelCombine,
  * kernels.ts:2386-2579, :2803-3027): row m's query at position *pos0 + m
  * attends keys 0..*pos0 + m (causal) of its KV head; half output. max_keys

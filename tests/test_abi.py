@@ -147,3 +147,16 @@ def test_argmax_advance_rejects_before_any_device_work():
     assert need == 2 * 4 * ((128256 + 1023) // 1024)
     with pytest.raises(L.WgError, match="scratch of"):
         L.check(lib.wg_argmax_advance(f, 128256, f, f, None, 0, None, f, need - 1, None))
+
+
+def test_attn_prefill_rejects_before_any_device_work():
+    lib = L.load()
+    f = 0x1000
+    sh = L.AttnShape(32, 8, 96, 96, 1e-6, 0)
+    with pytest.raises(L.WgError, match="head_dim 96"):
+        L.check(lib.wg_attn_prefill(f, 4, 4096, C.byref(sh), f, f, f, 64, f, 4096, None))
+    sh = L.AttnShape(32, 8, 128, 128, 1e-6, 0)
+    with pytest.raises(L.WgError, match="null argument"):
+        L.check(lib.wg_attn_prefill(None, 4, 4096, C.byref(sh), f, f, f, 64, f, 4096, None))
+    with pytest.raises(L.WgError, match="16-byte aligned"):
+        L.check(lib.wg_attn_prefill(f + 4, 4, 4096, C.byref(sh), f, f, f, 64, f, 4096, None))

@@ -213,3 +213,23 @@ def test_persistent_decode_reports_a_barrier_timeout(hip):
     eng.position = saved_pos
     orc.forward(prompt)
     assert eng.decode(first, 6) == orc.decode(first, 6)
+
+
+@pytest.mark.parametrize("family", ["q4_k-rowgroup", "lfm2-q4_0", "qwen-nbits"])
+def test_long_prompt_through_gemm_batches(hip, family):
+    """A 600-token prompt: rows 0..591 in GEMM batches of 512 and 80 (MFMA
+    GEMMs, flash prefill attention, batched short conv), the last 8 through
+    the few-token path. Logits of the last batch and the greedy tokens after
+    it match the CPU decoder."""
+    from webgllm_amd import engine as E
+    eng, orc = _pair(family, seed=23, ctx=640)
+    assert eng._prefill_ok()
+    rng = np.random.default_rng(17)
+    prompt = _prompt(rng, 600, eng.shape.vocab)
+    assert E.PREFILL_ROWS < 592
+    picks = eng.forward(prompt).cpu().numpy()
+    logits_o, picks_o = orc.forward(prompt)
+    assert rel_l2(eng.logits[:8].cpu().numpy(), logits_o) <= 1e-3
+    assert list(picks) == list(picks_o)
+    first = int(picks[-1])
+    assert eng.decode(first, 6) == orc.decode(first, 6)

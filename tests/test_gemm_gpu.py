@@ -101,3 +101,27 @@ def test_gemm_every_tile(hip, fmt, tile):
         L.tuning_set("gemm_tile", 0)
     assert e <= 1e-3
     assert e16 <= 1e-5
+
+
+def test_gemm_column_map(hip):
+    """col_of sends stored row n to output column col_of[n]: the mapped
+    product equals the plain one with its columns permuted (bit for bit);
+    an entry outside 0..N-1 leaves nothing written."""
+    from webgllm_amd import ops
+    N, K, M = 256, 512, 40
+    m = _matrix("nbits", N, K, seed=4)
+    rng = np.random.default_rng(3)
+    a = _t(O.f32_to_h2(rng.standard_normal((M, K)).astype(np.float32)).view(np.int16))
+    plain = ops.gemm(m, a).cpu().numpy()
+    perm = rng.permutation(N).astype(np.int32)
+    mapped = ops.gemm(m, a, col_of=_t(perm)).cpu().numpy()
+    assert np.array_equal(mapped[:, perm], plain)
+    perm[7] = N + 5  # out of range: column perm-less, stays as it was
+    out = torch.full((M, N), 123.0, device="cuda")
+    ops.gemm(m, a, out=out, col_of=_t(perm))
+    got = out.cpu().numpy()
+    ok = np.ones(N, bool)
+    ok[7] = False
+    assert np.array_equal(got[:, perm[ok]], plain[:, ok])
+    missing = np.setdiff1d(np.arange(N), perm[ok])
+    assert (got[:, missing] == 123.0).all()

@@ -205,7 +205,66 @@ def test_attn_decode_single_key_and_uniform(hip):
     assert rel_l2(got[0, :hd], vf[:300, :hd].astype(np.float64).mean(0)) < 1e-3
 
 
-@pytest.mark.parametrize("M,D,W", [(1, 2048, 3), (5, 2048, 3), (8, 1024, 4)])
+def _prefill_case(H, KV, hd, M, pos0, seed, ctx=None, nan_past=False):
+    from webgllm_amd import ops
+    rng = np.random.default_rng(seed)
+    kd = KV * hd
+    nkeys = pos0 + M
+    ctx = ctx or nkeys + 8
+    k = O.f32_to_h2(rng.standard_normal((ctx, kd)).astype(np.float32))
+    v = O.f32_to_h2(rng.standard_normal((ctx, kd)).astype(np.float32))
+    if nan_past:
+        k[nkeys:] = 0x7e00
+        v[nkeys:] = 0x7e00
+    q = (rng.standard_normal((M, H * hd)) / math.sqrt(hd) * 2).astype(np.float32)
+    out = ops.attn_prefill(_t(q), ops.attn_shape(H, KV, hd), _t(k.view(np.int16)),
+                           _t(v.view(np.int16)), _t(np.array([pos0], np.int32)))
+    return q, k, v, _h(out)
+
+
+@pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (32, 8, 128), (32, 8, 64), (4, 2, 64)])
+@pytest.mark.parametrize("M,pos0", [(1, 0), (37, 0), (64, 1000), (200, 63), (130, 3000)])
+def test_attn_prefill(hip, H, KV, hd, M, pos0):
+    """Prompt-batch attention (row m at position pos0 + m sees keys up to
+    it) against the float64 oracle, on the first and last rows, the rows at
+    block and chunk edges and a few random ones."""
+    q, k, v, got = _prefill_case(H, KV, hd, M, pos0, seed=H + hd + M + pos0)
+    kd = KV * hd
+    rng = np.random.default_rng(M)
+    rows = sorted({0, M - 1, min(M - 1, 7), min(M - 1, 8), min(M - 1, 63 - pos0 % 64)} |
+                  set(rng.integers(0, M, 4).tolist()))
+    assert np.isfinite(got).all()
+    for m in rows:
+        want = O.attention_f64(q[m], k, v, H, KV, hd, pos0 + m + 1, kd)
+        assert rel_l2(got[m], want) <= 1e-3, (m, rel_l2(got[m], want))
+
+
+def test_attn_prefill_ignores_rows_past_the_position(hip):
+    """Cache rows past the batch's last position hold NaN bits: they never
+    reach the output (masked scores, zero-read values)."""
+    H, KV, hd, M, pos0 = 32, 8, 128, 45, 100
+    q, k, v, got = _prefill_case(H, KV, hd, M, pos0, seed=5, ctx=1024, nan_past=True)
+    assert np.isfinite(got).all()
+    for m in (0, 20, M - 1):
+        want = O.attention_f64(q[m], k, v, H, KV, hd, pos0 + m + 1, KV * hd)
+        assert rel_l2(got[m], want) <= 1e-3
+
+
+def test_attn_prefill_matches_decode_rows(hip):
+    """A batch's row m equals the decode kernel's answer for that row alone
+    at position pos0 + m (both against the same cache), to f32 rounding."""
+    from webgllm_amd import ops
+    H, KV, hd, M, pos0 = 32, 8, 128, 24, 777
+    q, k, v, got = _prefill_case(H, KV, hd, M, pos0, seed=9)
+    shape = ops.attn_shape(H, KV, hd)
+    kc, vc = _t(k.view(np.int16)), _t(v.view(np.int16))
+    for m in (0, 11, 23):
+        one = _h(ops.attn_decode(_t(q[m:m + 1]), shape, kc, vc,
+                                 _t(np.array([pos0 + m], np.int32))))
+        assert rel_l2(got[m], one[0]) <= 1e-4
+
+
+@pytest.mark.parametrize("M,D,W", [(1, 2048, 3), (5, 2048, 3), (8, 1024, 4), (40, 512, 3)])
 def test_short_conv_and_accept(hip, M, D, W):
     from webgllm_amd import ops
     rng = np.random.default_rng(M * D + W)

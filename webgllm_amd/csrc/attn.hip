@@ -319,6 +319,174 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *partial,
   }
 }
 
+
+// Prefill attention (the reference's chunked scores / attend for a prompt
+// batch, Engine.attention src/engine.ts:6359-6630) as flash attention: a
+// workgroup per (KV head kh, block of BR query rows) holds the block's
+// GM = G * BR <= 32 queries (the KV head's G query heads for each row) and
+// walks the keys in chunks of 64 up to the block's last visible key, with an
+// online softmax, so it needs no partials and no combine pass. Four waves;
+// wave w owns query slots w, w + 4, ..., 8 of them.
+//  - each chunk's K and V tiles go to LDS by direct loads, K rows swizzled
+//    as in attn_tile_kernel;
+//  - scores: lane = key, its K row in registers, each query read from LDS
+//    as a broadcast;
+//  - per query the chunk's max and sum are DPP wave reductions; the
+//    running max, sum and output are rescaled as the max grows;
+//  - weighted values: lane = dim (HD / 64 of them), the weights of four
+//    keys read from LDS at once as a broadcast.
+// Keys past a row's position are masked; value rows past the block's last
+// visible key are read as zero (stale bits times a zero weight could be NaN).
+constexpr int PF_Q = 32;    // query slots a workgroup
+constexpr int PF_QPW = 8;   // query slots a wave
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(
+    const float *q, int ldq, int M, int H, int KV, int BR, const uint16_t *k_cache,
+    const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, uint16_t *out, int ldo) {
+  constexpr int KP = HD / 8, ROWB = HD * 2, TILE = WK * ROWB, RPI = 64 / KP, NI = WK / RPI;
+  constexpr int DPL = HD / 64;  // value dims a lane
+  static_assert(DPL == 1 || DPL == 2, "head_dim 64 or 128");
+  constexpr int QOFF = 2 * TILE, POFF = QOFF + PF_Q * HD * 4;
+  __shared__ __align__(16) unsigned char smem[POFF + 4 * PF_QPW * WK * 4];
+  auto swz = [](int r) { return KP == 16 ? (r & 15) : ((r ^ (r >> 3)) & (KP - 1)); };
+  const int kh = blockIdx.x % KV, blk = blockIdx.x / KV;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int G = H / KV, GM = G * BR;
+  const int m0 = blk * BR;
+  const int m_last = min(M, m0 + BR) - 1;
+  const int kvd = KV * HD;
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  const int pos0 = *pos0_dev;
+  // the block's queries: slot qi = (row m0 + qi / G, head kh G + qi % G)
+  for (int k = 0; k < PF_QPW; k++) {
+    const int qi = wave + 4 * k;
+    const int m = m0 + qi / G;
+    if (qi < GM && m < M) {
+      constexpr int LPQ = HD / 4;  // lanes a query (16 bytes each)
+      if (lane < LPQ)
+        dma16(q + (int64_t)m * ldq + (int64_t)(kh * G + qi % G) * HD + lane * 4,
+              __builtin_amdgcn_readfirstlane(sbase + QOFF + qi * HD * 4));
+    }
+  }
+  const int last_key = min(pos0 + m_last, max_keys - 1);  // the block's last visible key
+  const int nchunks = last_key < 0 ? 0 : last_key / WK + 1;
+  float m_run[PF_QPW], l_run[PF_QPW], acc[PF_QPW][DPL];
+#pragma unroll
+  for (int k = 0; k < PF_QPW; k++) {
+    m_run[k] = -INFINITY;
+    l_run[k] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < DPL; t++) acc[k][t] = 0.0f;
+  }
+  float *pw = reinterpret_cast<float *>(smem + POFF) + wave * PF_QPW * WK;
+  for (int c = 0; c < nchunks; c++) {
+    const int j0 = c * WK;
+    const int nk_max = min(WK, max_keys - j0);
+    for (int i = wave; i < 2 * NI; i += 4) {
+      const bool is_v = i >= NI;
+      const int ii = is_v ? i - NI : i;
+      const int r = ii * RPI + lane / KP;
+      const int slot = lane % KP;
+      const int piece = is_v ? slot : (slot ^ swz(r));
+      const int rr = r < nk_max ? r : 0;
+      dma16((is_v ? v_cache : k_cache) + (int64_t)(j0 + rr) * kvd + kh * HD + piece * 8,
+            __builtin_amdgcn_readfirstlane(sbase + (is_v ? TILE : 0) + ii * 1024));
+    }
+    wait_vm<0>();
+    barrier();
+    // this lane's key row
+    uint4 kr[KP];
+    const unsigned char *krow = smem + lane * ROWB;
+#pragma unroll
+    for (int i = 0; i < KP; i++)
+      kr[i] = *reinterpret_cast<const uint4 *>(krow + ((i ^ swz(lane)) * 16));
+    const int jg = j0 + lane;
+    float corr[PF_QPW];
+#pragma unroll
+    for (int k = 0; k < PF_QPW; k++) {
+      const int qi = wave + 4 * k;
+      const int m = m0 + qi / G;
+      corr[k] = 1.0f;
+      if (qi >= GM || m >= M) continue;  // wave-uniform
+      const float4 *ql = reinterpret_cast<const float4 *>(smem + QOFF + qi * HD * 4);
+      float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+      for (int i = 0; i < KP; i++) {
+        const half2v a = as_h2(kr[i].x), b = as_h2(kr[i].y), cc = as_h2(kr[i].z),
+                     dd = as_h2(kr[i].w);
+        const float4 qa = ql[2 * i], qb = ql[2 * i + 1];
+        s0 = __builtin_fmaf(qa.x, (float)a.x, s0);
+        s1 = __builtin_fmaf(qa.y, (float)a.y, s1);
+        s2 = __builtin_fmaf(qa.z, (float)b.x, s2);
+        s3 = __builtin_fmaf(qa.w, (float)b.y, s3);
+        s0 = __builtin_fmaf(qb.x, (float)cc.x, s0);
+        s1 = __builtin_fmaf(qb.y, (float)cc.y, s1);
+        s2 = __builtin_fmaf(qb.z, (float)dd.x, s2);
+        s3 = __builtin_fmaf(qb.w, (float)dd.y, s3);
+      }
+      const bool vis = lane < nk_max && jg <= pos0 + m;
+      const float sc = vis ? (s0 + s1) + (s2 + s3) : -INFINITY;
+      const float m_new = fmaxf(m_run[k], wave_max_u(sc));
+      const float p = (!vis || m_new == -INFINITY) ? 0.0f : __expf(sc - m_new);
+      corr[k] = m_run[k] == -INFINITY ? 0.0f : __expf(m_run[k] - m_new);
+      l_run[k] = l_run[k] * corr[k] + wave_sum_u(p);
+      m_run[k] = m_new;
+      pw[k * WK + lane] = p;
+    }
+    // weighted values: lane = dim(s); rows at or past nkv read as zero
+    const int nkv = min(WK, last_key - j0 + 1);
+#pragma unroll
+    for (int k = 0; k < PF_QPW; k++)
+#pragma unroll
+      for (int t = 0; t < DPL; t++) acc[k][t] *= corr[k];
+    const unsigned char *vrow = smem + TILE + lane * DPL * 2;
+    for (int jb = 0; jb < (nkv + 3) / 4; jb++) {
+      float v[4][DPL];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int j = 4 * jb + u;
+        if constexpr (DPL == 2) {
+          const half2v hv = as_h2(*reinterpret_cast<const uint32_t *>(vrow + j * ROWB));
+          v[u][0] = j < nkv ? (float)hv.x : 0.0f;
+          v[u][1] = j < nkv ? (float)hv.y : 0.0f;
+        } else {
+          const _Float16 hv = *reinterpret_cast<const _Float16 *>(vrow + j * ROWB);
+          v[u][0] = j < nkv ? (float)hv : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < PF_QPW; k++) {
+        const int qi = wave + 4 * k;
+        if (qi >= GM || m0 + qi / G >= M) continue;  // wave-uniform
+        const float4 p4 = reinterpret_cast<const float4 *>(pw + k * WK)[jb];
+#pragma unroll
+        for (int t = 0; t < DPL; t++) {
+          float a = acc[k][t];
+          a = __builtin_fmaf(p4.x, v[0][t], a);
+          a = __builtin_fmaf(p4.y, v[1][t], a);
+          a = __builtin_fmaf(p4.z, v[2][t], a);
+          a = __builtin_fmaf(p4.w, v[3][t], a);
+          acc[k][t] = a;
+        }
+      }
+    }
+    barrier();  // every wave is done with this chunk's tiles
+  }
+  wait_vm<0>();  // (no chunk: the query loads must still land before the workgroup ends)
+#pragma unroll
+  for (int k = 0; k < PF_QPW; k++) {
+    const int qi = wave + 4 * k;
+    const int m = m0 + qi / G;
+    if (qi >= GM || m >= M) continue;
+    const float inv = l_run[k] > 0.0f ? 1.0f / l_run[k] : 0.0f;
+    uint16_t *o = out + (int64_t)m * ldo + (int64_t)(kh * G + qi % G) * HD + lane * DPL;
+#pragma unroll
+    for (int t = 0; t < DPL; t++) o[t] = to_h(acc[k][t] * inv);
+  }
+}
+
 }  // namespace
 }  // namespace wg
 
@@ -356,6 +524,31 @@ int wg_head_prep(const float *qkv, int32_t M, int32_t ldq, const wg_attn_shape *
 size_t wg_attn_scratch_bytes(int32_t M, int32_t heads, int32_t head_dim, int32_t max_keys) {
   int64_t chunks = (max_keys + CHUNK - 1) / CHUNK;
   return (size_t)M * heads * chunks * (head_dim + 2) * sizeof(float);
+}
+
+int wg_attn_prefill(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *sh,
+                    const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0,
+                    int32_t max_keys, uint16_t *out, int32_t ldo, void *stream) {
+  WG_REQUIRE(sh && q && k_cache && v_cache && pos0 && out, "wg_attn_prefill: null argument");
+  int H = sh->heads, KV = sh->kv_heads, hd = sh->head_dim;
+  WG_REQUIRE(KV > 0 && H % KV == 0 && H / KV <= PF_Q,
+             "wg_attn_prefill: %d query heads over %d KV heads", H, KV);
+  WG_REQUIRE(hd == 64 || hd == 128, "wg_attn_prefill: head_dim %d (64 or 128)", hd);
+  WG_REQUIRE(M >= 1 && max_keys >= 1, "wg_attn_prefill: %d rows, %d keys", M, max_keys);
+  WG_REQUIRE(ldq >= H * hd && ldo >= H * hd, "wg_attn_prefill: strides too small");
+  WG_REQUIRE(((uintptr_t)q & 15) == 0 && ldq % 4 == 0,
+             "wg_attn_prefill: queries must be 16-byte aligned with a stride of 4k floats");
+  const int BR = PF_Q / (H / KV);
+  const int64_t blocks = (int64_t)KV * ((M + BR - 1) / BR);
+  WG_REQUIRE(blocks <= 0x7fffffff, "wg_attn_prefill: %d rows", M);
+  hipStream_t s = as_stream(stream);
+  if (hd == 64)
+    attn_prefill_kernel<64><<<(unsigned)blocks, 256, 0, s>>>(q, ldq, M, H, KV, BR, k_cache,
+                                                            v_cache, pos0, max_keys, out, ldo);
+  else
+    attn_prefill_kernel<128><<<(unsigned)blocks, 256, 0, s>>>(q, ldq, M, H, KV, BR, k_cache,
+                                                             v_cache, pos0, max_keys, out, ldo);
+  return launched("wg_attn_prefill");
 }
 
 int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *sh,

@@ -53,6 +53,33 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
+// Wave64 reductions through DPP (no LDS round trip): within quads, half
+// rows and rows, then rows into lane 63 by the row broadcasts; the result is
+// read back from lane 63, so it is wave-uniform. `id` is the operation's
+// identity, taken by lanes a step does not write.
+template <int CTRL, int ROW_MASK>
+__device__ inline float dpp_f(float x, float id) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, id),
+                                                               __builtin_bit_cast(int, x), CTRL,
+                                                               ROW_MASK, 0xf, false));
+}
+template <typename Op>
+__device__ inline float wave_reduce_dpp(float v, float id, Op op) {
+  v = op(v, dpp_f<0xb1, 0xf>(v, id));   // quad_perm [1, 0, 3, 2]
+  v = op(v, dpp_f<0x4e, 0xf>(v, id));   // quad_perm [2, 3, 0, 1]
+  v = op(v, dpp_f<0x141, 0xf>(v, id));  // row_half_mirror
+  v = op(v, dpp_f<0x140, 0xf>(v, id));  // row_mirror: every lane holds its row's result
+  v = op(v, dpp_f<0x142, 0xa>(v, id));  // row_bcast:15 into rows 1 and 3
+  v = op(v, dpp_f<0x143, 0xc>(v, id));  // row_bcast:31 into rows 2 and 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ inline float wave_max_u(float v) {
+  return wave_reduce_dpp(v, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
+}
+__device__ inline float wave_sum_u(float v) {
+  return wave_reduce_dpp(v, 0.0f, [](float a, float b) { return a + b; });
+}
+
 // Reduce-scatter of 4 per-lane values over the 64 lanes in 7 shuffles:
 // afterwards lanes 16 r .. 16 r + 15 all hold the wave's sum of v[r].
 __device__ inline float wave_sum4(float v0, float v1, float v2, float v3) {

@@ -28,6 +28,7 @@ from . import lib as L
 from . import ops
 
 MAX_ROWS = 8
+PREFILL_ROWS = 512  # prompt rows a GEMM batch takes
 PRESCALE = 32.0  # the reference's PRESCALE (src/gpu/kernels.ts:89)
 
 
@@ -240,6 +241,8 @@ class Engine:
         self.position = 0
         self.draft = None
         self.graph = None
+        self._pre = None  # prefill buffers, made on the first prompt batch
+        self._cols = {}   # device row orders of the matrices (GEMM column maps)
         # persistent=True: single-row forwards of attention-only models run as
         # one persistent launch (wg_decode_run); other shapes, and the
         # default, take the per-op path. On MI355X a grid barrier costs about
@@ -367,6 +370,79 @@ class Engine:
             ops.argmax_rows(self.logits[:M], ids=self.next_ids[:M], tops=self.tops[:M],
                             scratch=self.argmax_scratch)
 
+    # --- prompt batches on MFMA ----------------------------------------------
+    def _prefill_ok(self) -> bool:
+        """Whether prompt batches can run as GEMMs: every matrix of a layer in
+        the row-group layout with N and K multiples of 64."""
+        for lw in self.w.layers:
+            for m in lw.values():
+                if isinstance(m, ops.Q4Matrix) and (m.layout != L.LAYOUT_ROWGROUP or
+                                                    m.N % 64 or m.K % 64):
+                    return False
+        s = self.shape
+        return s.head_dim in (64, 128)
+
+    def _pre_buffers(self) -> dict:
+        if self._pre is None:
+            s, R, dev = self.shape, PREFILL_ROWS, self.device
+            D, F, A = s.hidden, s.intermediate, s.heads * s.head_dim
+            f32, f16 = torch.float32, torch.float16
+            self._pre = {
+                "ids": torch.zeros(R, dtype=torch.int32, device=dev),
+                "h": torch.zeros((R, D), dtype=f32, device=dev),
+                "x16": torch.zeros((R, D), dtype=f16, device=dev),
+                "c16": torch.zeros((R, D), dtype=f16, device=dev),
+                "bcx": torch.zeros((R, 3 * D), dtype=f32, device=dev),
+                "qkv": torch.zeros((R, s.qkv_rows), dtype=f32, device=dev),
+                "q": torch.zeros((R, A), dtype=f32, device=dev),
+                "att16": torch.zeros((R, A), dtype=f16, device=dev),
+                "gu": torch.zeros((R, 2 * F), dtype=f32, device=dev),
+                "ff16": torch.zeros((R, F), dtype=f16, device=dev),
+            }
+        return self._pre
+
+    def _col_of(self, m: "ops.Q4Matrix"):
+        """The GEMM column map of a matrix uploaded in a row order (stored row
+        n holds logical row row_order[n]), or None."""
+        order = getattr(m, "row_order", None)
+        if order is None:
+            return None
+        key = id(m)
+        if key not in self._cols:
+            self._cols[key] = torch.tensor(order, dtype=torch.int32, device=self.device)
+        return self._cols[key]
+
+    def _prefill_rows(self, M: int) -> None:
+        """A prompt batch of M rows (pre ids[:M] at positions pos ..) through
+        the GEMMs on MFMA, as the reference's forwardBatch takes batches larger
+        than the split path's (Engine.matmul, src/engine.ts:4969-5234, and its
+        attention plan for a prompt, :6359-6630). Inputs are normalized to
+        halves by a norm kernel; the caches and conv states advance; no head,
+        no picks (the prompt's last rows go through _forward_rows)."""
+        s, w, b = self.shape, self.w, self._pre_buffers()
+        D = s.hidden
+        h, x16 = b["h"][:M], b["x16"][:M]
+        ops.embed(w.embedding, b["ids"][:M], out=h)
+        for i, lw in enumerate(w.layers):
+            ops.rms_norm(h, lw["op_norm"], s.eps, out=x16)
+            if s.layer_type(i) == "conv":
+                bcx = ops.gemm(lw["in_proj"], x16, out=b["bcx"][:M])
+                ops.short_conv(bcx, D, s.conv_kernel, lw["taps"], self.state[i], out=b["c16"][:M])
+                ops.gemm(lw["out_proj"], b["c16"][:M], out=h, residual=h)
+            else:
+                qkv = ops.gemm(lw["qkv"], x16, out=b["qkv"][:M], col_of=self._col_of(lw["qkv"]))
+                ops.head_prep(qkv, self.attn, self.rope, self.pos, self.k_cache[i],
+                              self.v_cache[i], lw.get("q_norm"), lw.get("k_norm"),
+                              q_out=b["q"][:M])
+                ops.attn_prefill(b["q"][:M], self.attn, self.k_cache[i], self.v_cache[i],
+                                 self.pos, out=b["att16"][:M])
+                ops.gemm(lw["o"], b["att16"][:M], out=h, residual=h)
+            ops.rms_norm(h, lw["ffn_norm"], s.eps, out=x16)
+            gu = ops.gemm(lw["gate_up"], x16, out=b["gu"][:M],
+                          col_of=self._col_of(lw["gate_up"]))
+            ops.swiglu(gu, out=b["ff16"][:M])
+            ops.gemm(lw["down"], b["ff16"][:M], out=h, residual=h)
+
     # --- the reference's Engine API -------------------------------------------
     def reset(self) -> None:
         self.position = 0
@@ -387,7 +463,19 @@ class Engine:
         if draft and len(tokens) > MAX_ROWS:
             raise ValueError(f"A draft batch holds {MAX_ROWS} tokens at most.")
         out = None
-        for b0 in range(0, len(tokens), MAX_ROWS):
+        # a prompt's leading rows in GEMM batches; its last (up to 8) rows, whose
+        # picks are returned, through the few-token path
+        big = 0
+        if not draft and len(tokens) > MAX_ROWS and self._prefill_ok():
+            big = len(tokens) - (len(tokens) % MAX_ROWS or MAX_ROWS)
+        for b0 in range(0, big, PREFILL_ROWS):
+            batch = tokens[b0:min(big, b0 + PREFILL_ROWS)]
+            M = len(batch)
+            self._pre_buffers()["ids"][:M].copy_(torch.tensor(batch, dtype=torch.int32))
+            self.pos.fill_(self.position)
+            self._prefill_rows(M)
+            self.position += M
+        for b0 in range(big, len(tokens), MAX_ROWS):
             batch = tokens[b0:b0 + MAX_ROWS]
             M = len(batch)
             self.ids[:M].copy_(torch.tensor(batch, dtype=torch.int32))

@@ -189,8 +189,9 @@ class DecodePlan:
 
 
 def gemm(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
-         residual: torch.Tensor | None = None) -> torch.Tensor:
-    """C = A W^T on MFMA for M tokens of half activations A [M, K]."""
+         residual: torch.Tensor | None = None, col_of: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A W^T on MFMA for M tokens of half activations A [M, K]; col_of
+    (int32 [N], optional) sends stored row n to output column col_of[n]."""
     if a16.dtype not in (torch.float16, torch.int16):
         raise ValueError("activations must be halves")
     a16 = _dev(a16)
@@ -200,6 +201,7 @@ def gemm(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
     _dev(out, torch.float32)
     L.check(L.load().wg_q4_gemm(C.byref(m.desc), _p(a16), M, a16.shape[1], _p(out), out.shape[1],
                                 _p(residual), residual.shape[1] if residual is not None else 0,
+                                _p(None if col_of is None else _dev(col_of, torch.int32)),
                                 _stream()))
     return out
 
@@ -283,6 +285,21 @@ def attn_decode(q: torch.Tensor, shape, k_cache, v_cache, pos0: torch.Tensor,
     L.check(L.load().wg_attn_decode(_p(q), M, q.shape[1], C.byref(shape), _p(k_cache),
                                     _p(v_cache), _p(_dev(pos0, torch.int32)), max_keys, _p(out),
                                     out.shape[1], _p(scratch), scratch.numel(), _stream()))
+    return out
+
+
+def attn_prefill(q: torch.Tensor, shape, k_cache, v_cache, pos0: torch.Tensor,
+                 out: torch.Tensor | None = None):
+    """Causal attention of a prompt batch (rows at pos0, pos0 + 1, ...)
+    over the caches, flash style (no scratch)."""
+    q = _dev(q, torch.float32)
+    M = q.shape[0]
+    if out is None:
+        out = torch.empty((M, shape.heads * shape.head_dim), dtype=torch.float16,
+                          device=q.device)
+    L.check(L.load().wg_attn_prefill(_p(q), M, q.shape[1], C.byref(shape), _p(k_cache),
+                                     _p(v_cache), _p(_dev(pos0, torch.int32)), k_cache.shape[0],
+                                     _p(out), out.shape[1], _stream()))
     return out
 
 
