@@ -409,8 +409,65 @@ def workload_lfm2_verify(args):
                 weight_bytes=w.nbytes)
 
 
+def workload_llama8b_prefill(args):
+    """Llama-3-8B-shape prompt processing: a 2048-token random prompt from
+    position 0, its first 2040 rows in GEMM batches of 512 (MFMA GEMMs, flash
+    prefill attention), the last 8 through the few-token path with the head
+    and the picks; tokens/s of the whole prompt, repeated from a reset
+    cache."""
+    import torch
+    from webgllm_amd import engine as E, ops
+    shape = E.LLAMA3_8B
+    w = E.Weights(shape, seed=0)
+    n = 2048
+    eng = E.Engine(w, n + 8)
+    assert eng._prefill_ok()
+    prompt = torch.randint(0, shape.vocab, (n,),
+                           generator=torch.Generator().manual_seed(4)).tolist()
+
+    def run():
+        eng.reset()
+        eng.forward(prompt)
+    for _ in range(2):
+        run()
+    reps = max(3, args.steps // 16)
+    ms = timed(run, reps)
+    tok_s = n / (ms * 1e-3)
+    # the dominant kernel: layer 0's gate|up GEMM at 512 rows, as the batches launch it
+    lw = w.layers[0]
+    F, D = shape.intermediate, shape.hidden
+    a = torch.randn((512, D), device="cuda").half()
+    gu = torch.empty((512, 2 * F), device="cuda")
+    col = eng._col_of(lw["gate_up"])
+    for _ in range(20):
+        ops.gemm(lw["gate_up"], a, out=gu, col_of=col)
+    gms = timed(lambda: ops.gemm(lw["gate_up"], a, out=gu, col_of=col), 60)
+    flop = 2.0 * 512 * 2 * F * D
+    tf = flop / (gms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
+            "frac": round(tf / 2500.0, 4), "traffic": None,
+            "kernel": f"gemm_q4_kernel gate|up 512 x {2 * F} x {D} (Q4_K repacked, f16 zero "
+                      f"points), column map to gate | up", "flops_per_launch": flop,
+            "avg_launch_us": round(gms * 1e3, 2), "launches": 60}
+    cpu = None
+    if not args.no_cpu:
+        threads = min(os.cpu_count() or 1, 16)
+        t, desc = cpu_step_time([("qkv", lw["qkv"], shape.layers), ("o", lw["o"], shape.layers),
+                                 ("gate_up", lw["gate_up"], shape.layers),
+                                 ("down", lw["down"], shape.layers)], 8, threads, 10.0)
+        cpu = {"value": round(8 / t, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": desc + " (8 prompt rows a step; the head is left out)"}
+    cfg = {"workload": f"Llama-3-8B-shape Q4_K prompt of {n} random ids from position 0",
+           "model": shape.name, "layers": shape.layers, "hidden": shape.hidden,
+           "weights": "random GGUF Q4_K super-blocks, repacked on the GPU (packQ4_K)",
+           "global_batch": n, "seq_len": n, "parallelism": "none"}
+    return line("prefill tok/s, Llama-3-8B-shape Q4_K", round(tok_s, 1), "tok/s", reps, 2, ms,
+                cfg, roof, cpu, dtype="f16 x f16 -> f32")
+
+
 WORKLOADS = {"q4_0-gemv": workload_q4_0_gemv, "nbits-gemm": workload_nbits_gemm,
-             "qwen2-decode": workload_qwen2_decode, "lfm2-verify": workload_lfm2_verify}
+             "qwen2-decode": workload_qwen2_decode, "lfm2-verify": workload_lfm2_verify,
+             "llama8b-prefill": workload_llama8b_prefill}
 
 
 def main():
