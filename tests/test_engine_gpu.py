@@ -216,12 +216,13 @@ def test_persistent_decode_reports_a_barrier_timeout(hip):
 
 
 @pytest.mark.parametrize("family", ["q4_k-rowgroup", "lfm2-q4_0", "qwen-nbits"])
-def test_long_prompt_through_gemm_batches(hip, family):
+def test_long_prompt_through_gemm_batches(hip, family, monkeypatch):
     """A 600-token prompt: rows 0..591 in GEMM batches of 512 and 80 (MFMA
     GEMMs, flash prefill attention, batched short conv), the last 8 through
     the few-token path. Logits of the last batch and the greedy tokens after
     it match the CPU decoder."""
     from webgllm_amd import engine as E
+    monkeypatch.setattr(E, "PREFILL_ROWS", 512)
     eng, orc = _pair(family, seed=23, ctx=640)
     assert eng._prefill_ok()
     rng = np.random.default_rng(17)

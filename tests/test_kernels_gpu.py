@@ -222,9 +222,19 @@ def _prefill_case(H, KV, hd, M, pos0, seed, ctx=None, nan_past=False):
     return q, k, v, _h(out)
 
 
+@pytest.fixture(params=[4, 1, 0], ids=["mfma4", "mfma1", "valu"])
+def prefill_kernel(request):
+    """wg_attn_prefill's kernel: MFMA with 4 or 1 waves a workgroup, or VALU."""
+    from webgllm_amd import lib as L
+    old = L.tuning_get("attn_prefill_mfma")
+    L.tuning_set("attn_prefill_mfma", request.param)
+    yield request.param
+    L.tuning_set("attn_prefill_mfma", old)
+
+
 @pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (32, 8, 128), (32, 8, 64), (4, 2, 64)])
 @pytest.mark.parametrize("M,pos0", [(1, 0), (37, 0), (64, 1000), (200, 63), (130, 3000)])
-def test_attn_prefill(hip, H, KV, hd, M, pos0):
+def test_attn_prefill(hip, prefill_kernel, H, KV, hd, M, pos0):
     """Prompt-batch attention (row m at position pos0 + m sees keys up to
     it) against the float64 oracle, on the first and last rows, the rows at
     block and chunk edges and a few random ones."""
@@ -239,7 +249,7 @@ def test_attn_prefill(hip, H, KV, hd, M, pos0):
         assert rel_l2(got[m], want) <= 1e-3, (m, rel_l2(got[m], want))
 
 
-def test_attn_prefill_ignores_rows_past_the_position(hip):
+def test_attn_prefill_ignores_rows_past_the_position(hip, prefill_kernel):
     """Cache rows past the batch's last position hold NaN bits: they never
     reach the output (masked scores, zero-read values)."""
     H, KV, hd, M, pos0 = 32, 8, 128, 45, 100
@@ -250,7 +260,7 @@ def test_attn_prefill_ignores_rows_past_the_position(hip):
         assert rel_l2(got[m], want) <= 1e-3
 
 
-def test_attn_prefill_matches_decode_rows(hip):
+def test_attn_prefill_matches_decode_rows(hip, prefill_kernel):
     """A batch's row m equals the decode kernel's answer for that row alone
     at position pos0 + m (both against the same cache), to f32 rounding."""
     from webgllm_amd import ops

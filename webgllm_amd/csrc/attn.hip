@@ -487,6 +487,171 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
   }
 }
 
+// The same prompt attention on MFMA (v_mfma_f32_32x32x16_f16, f32
+// accumulation). A wave owns 32 queries (slots of the workgroup's rows x the
+// KV head's G query heads) and walks the keys 32 at a time:
+//  - scores as S^T = K Q^T: A = 32 key rows of the K tile (16-byte pieces,
+//    swizzled as in attn_tile_kernel), B = the wave's queries. The queries
+//    are f32; each is split into hi = half(q) and lo = half(q - hi), two
+//    MFMAs, so the scores keep ~22 bits (the keys are halves already);
+//  - in that orientation lane i holds 16 keys of query i % 32 (keys
+//    8 (j / 4) + 4 (i / 32) + j % 4 of the tile), so the softmax max and sum
+//    are in-lane plus one exchange between the half-waves;
+//  - weighted values as O^T = V^T P^T: B = the lane's own weights (slice s
+//    of 16 keys = registers 8 s .. 8 s + 7, split hi / lo like the queries),
+//    A = the values of those keys (k-index 8 h + t = key 16 s + 8 (t / 4) +
+//    4 h + t % 4) read from LDS; O^T keeps every output of a lane in its
+//    query, so the online-softmax rescale is per lane.
+// K and V rows past the block's last visible key (or the cache) are loaded
+// from the chunk's first row instead: stale bits never reach an MFMA.
+template <int HD, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_prefill_mfma_kernel(
+    const float *q, int ldq, int M, int H, int KV, int R, const uint16_t *k_cache,
+    const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, uint16_t *out, int ldo) {
+  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+  typedef float float16v __attribute__((ext_vector_type(16)));
+  constexpr int KP = HD / 8, ROWB = HD * 2, TILE = WK * ROWB, RPI = 64 / KP, NI = WK / RPI;
+  constexpr int KS = HD / 16, DT = HD / 32;
+  __shared__ __align__(16) unsigned char smem[2 * TILE];
+  auto swz = [](int r) { return KP == 16 ? (r & 15) : ((r ^ (r >> 3)) & (KP - 1)); };
+  const int kh = blockIdx.x % KV, blk = blockIdx.x / KV;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hh = lane >> 5, c32 = lane & 31;
+  const int G = H / KV, GM = G * R;
+  const int m0 = blk * R;
+  const int m_last = min(M, m0 + R) - 1;
+  const int kvd = KV * HD;
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  const int pos0 = *pos0_dev;
+  // this lane's query (slot qs) and the wave's last visible key
+  const int qs = wave * 32 + c32;
+  const int qm = m0 + qs / G;
+  const bool qvalid = qs < GM && qm < M;
+  const int q_last = pos0 + qm;  // the last key this query sees
+  const int wlast_slot = min(wave * 32 + 31, GM - 1);
+  const int w_row = min(m0 + wlast_slot / G, m_last);
+  const bool w_any = wave * 32 < GM && m0 + (wave * 32) / G <= m_last;
+  const int w_last_key = min(pos0 + w_row, max_keys - 1);
+  const int last_key = min(pos0 + m_last, max_keys - 1);
+  const int nchunks = last_key < 0 ? 0 : last_key / WK + 1;
+  half8 qb_hi[KS], qb_lo[KS];
+  {
+    const float *qp = q + (int64_t)(qvalid ? qm : 0) * ldq + (int64_t)(kh * G + qs % G) * HD + 8 * hh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+      if (qvalid) {
+        a = *reinterpret_cast<const float4 *>(qp + 16 * ks);
+        b = *reinterpret_cast<const float4 *>(qp + 16 * ks + 4);
+      }
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const _Float16 hi = (_Float16)v[t];
+        qb_hi[ks][t] = hi;
+        qb_lo[ks][t] = (_Float16)(v[t] - (float)hi);
+      }
+    }
+  }
+  float m_run = -INFINITY, l_run = 0.0f;
+  float16v o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+    for (int j = 0; j < 16; j++) o[dt][j] = 0.0f;
+  for (int c = 0; c < nchunks; c++) {
+    const int j0 = c * WK;
+    const int nk_load = min(WK, last_key - j0 + 1);  // rows worth loading (>= 1)
+    for (int i = wave; i < 2 * NI; i += NW) {
+      const bool is_v = i >= NI;
+      const int ii = is_v ? i - NI : i;
+      const int r = ii * RPI + lane / KP;
+      const int slot = lane % KP;
+      const int piece = is_v ? slot : (slot ^ swz(r));
+      const int rr = r < nk_load ? r : 0;
+      dma16((is_v ? v_cache : k_cache) + (int64_t)(j0 + rr) * kvd + kh * HD + piece * 8,
+            __builtin_amdgcn_readfirstlane(sbase + (is_v ? TILE : 0) + ii * 1024));
+    }
+    wait_vm<0>();
+    barrier();
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) {
+      const int kb = j0 + 32 * kt;
+      if (!w_any || kb > w_last_key) continue;  // wave-uniform
+      float16v st;
+#pragma unroll
+      for (int j = 0; j < 16; j++) st[j] = 0.0f;
+      const int r = 32 * kt + c32;
+#pragma unroll
+      for (int ks = 0; ks < KS; ks++) {
+        const half8 ka = *reinterpret_cast<const half8 *>(smem + r * ROWB +
+                                                         (((2 * ks + hh) ^ swz(r)) * 16));
+        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qb_hi[ks], st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qb_lo[ks], st, 0, 0, 0);
+      }
+      float p[16];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const int key = kb + 8 * (j >> 2) + 4 * hh + (j & 3);
+        const bool vis = qvalid && key <= q_last && key < max_keys;
+        p[j] = vis ? st[j] : -INFINITY;
+        tmax = fmaxf(tmax, p[j]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m_run, tmax);
+      const float corr = m_new == -INFINITY ? 1.0f : __expf(m_run - m_new);
+      float psum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        p[j] = p[j] == -INFINITY ? 0.0f : __expf(p[j] - m_new);
+        psum += p[j];
+      }
+      psum += __shfl_xor(psum, 32, 64);
+      l_run = l_run * corr + psum;
+      m_run = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) o[dt][j] *= corr;
+#pragma unroll
+      for (int sl = 0; sl < 2; sl++) {
+        half8 pb_hi, pb_lo;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          const _Float16 hi = (_Float16)p[8 * sl + t];
+          pb_hi[t] = hi;
+          pb_lo[t] = (_Float16)(p[8 * sl + t] - (float)hi);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+          half8 va;
+#pragma unroll
+          for (int t = 0; t < 8; t++) {
+            const int vr = 32 * kt + 16 * sl + 8 * (t >> 2) + 4 * hh + (t & 3);
+            va[t] = *reinterpret_cast<const _Float16 *>(smem + TILE + vr * ROWB +
+                                                        (32 * dt + c32) * 2);
+          }
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb_hi, o[dt], 0, 0, 0);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb_lo, o[dt], 0, 0, 0);
+        }
+      }
+    }
+    barrier();  // every wave is done with this chunk's tiles
+  }
+  wait_vm<0>();
+  if (qvalid) {
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    uint16_t *op = out + (int64_t)qm * ldo + (int64_t)(kh * G + qs % G) * HD;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+      for (int j = 0; j < 16; j++)
+        op[32 * dt + 8 * (j >> 2) + 4 * hh + (j & 3)] = to_h(o[dt][j] * inv);
+  }
+}
+
 }  // namespace
 }  // namespace wg
 
@@ -538,10 +703,30 @@ int wg_attn_prefill(const float *q, int32_t M, int32_t ldq, const wg_attn_shape 
   WG_REQUIRE(ldq >= H * hd && ldo >= H * hd, "wg_attn_prefill: strides too small");
   WG_REQUIRE(((uintptr_t)q & 15) == 0 && ldq % 4 == 0,
              "wg_attn_prefill: queries must be 16-byte aligned with a stride of 4k floats");
+  hipStream_t s = as_stream(stream);
+  if (const int nw = tuning("attn_prefill_mfma")) {  // waves (32 queries each) a workgroup
+    const int R = nw * 32 / (H / KV);
+    WG_REQUIRE(R >= 1, "wg_attn_prefill: %d query heads a KV head", H / KV);
+    const int64_t blocks = (int64_t)KV * ((M + R - 1) / R);
+    WG_REQUIRE(blocks <= 0x7fffffff, "wg_attn_prefill: %d rows", M);
+#define WG_PF_LAUNCH(NWP)                                                                      \
+  do {                                                                                         \
+    if (hd == 64)                                                                              \
+      attn_prefill_mfma_kernel<64, NWP><<<(unsigned)blocks, NWP * 64, 0, s>>>(                 \
+          q, ldq, M, H, KV, R, k_cache, v_cache, pos0, max_keys, out, ldo);                    \
+    else                                                                                       \
+      attn_prefill_mfma_kernel<128, NWP><<<(unsigned)blocks, NWP * 64, 0, s>>>(                \
+          q, ldq, M, H, KV, R, k_cache, v_cache, pos0, max_keys, out, ldo);                    \
+  } while (0)
+    if (nw == 1) WG_PF_LAUNCH(1);
+    else if (nw == 4) WG_PF_LAUNCH(4);
+    else WG_PF_LAUNCH(2);
+#undef WG_PF_LAUNCH
+    return launched("wg_attn_prefill");
+  }
   const int BR = PF_Q / (H / KV);
   const int64_t blocks = (int64_t)KV * ((M + BR - 1) / BR);
   WG_REQUIRE(blocks <= 0x7fffffff, "wg_attn_prefill: %d rows", M);
-  hipStream_t s = as_stream(stream);
   if (hd == 64)
     attn_prefill_kernel<64><<<(unsigned)blocks, 256, 0, s>>>(q, ldq, M, H, KV, BR, k_cache,
                                                             v_cache, pos0, max_keys, out, ldo);

@@ -28,7 +28,7 @@ from . import lib as L
 from . import ops
 
 MAX_ROWS = 8
-PREFILL_ROWS = 512  # prompt rows a GEMM batch takes
+PREFILL_ROWS = 2048  # prompt rows a GEMM batch takes
 PRESCALE = 32.0  # the reference's PRESCALE (src/gpu/kernels.ts:89)
 
 
