@@ -309,7 +309,7 @@ def decode_engine_run(shape, ctx, prompt_len, steps, warmup):
     prompt = torch.randint(0, shape.vocab, (prompt_len,),
                            generator=torch.Generator().manual_seed(1)).tolist()
     first = int(eng.forward(prompt)[-1])
-    eng.capture_step()
+    eng.capture_step(first)
     eng.decode(first, warmup)
     p0 = eng.position
     eng.ids[0] = int(eng.hist[p0].item())
@@ -518,7 +518,7 @@ def main():
     torch.cuda.synchronize()
     t_prefill = time.time() - t0
     first = int(picks[-1])
-    eng.capture_step()
+    eng.capture_step(first)
     # warmup, then exactly `steps` timed tokens
     eng.decode(first, args.warmup)
     last = int(eng.hist[eng.position].item())

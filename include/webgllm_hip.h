@@ -233,14 +233,15 @@ int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx,
  * matrix (N and K multiples of 64); float32 C [M][ldc]. Weights are
  * dequantized in registers to halves, d (q - z) rounded once as dequantOut
  * does (kernels.ts:436-597), and multiplied on MFMA (v_mfma_f32_32x32x16_f16)
- * with float32 accumulation. residual may equal C. col_of (or NULL for
- * n -> n) maps the matrix's stored row n to its output column: a matrix
- * uploaded with a row order (the loaders' srcRows, stored row n = logical
- * row col_of[n]) then comes out in logical order; entries outside 0..N-1
- * are not written. */
+ * with float32 accumulation. residual may equal C. row_scale (or NULL)
+ * multiplies row m's sums before the residual is added (a prescaled norm's
+ * 32 / RMS, see wg_norm_to_h2). col_of (or NULL for n -> n) maps the
+ * matrix's stored row n to its output column: a matrix uploaded with a row
+ * order (the loaders' srcRows, stored row n = logical row col_of[n]) then
+ * comes out in logical order; entries outside 0..N-1 are not written. */
 int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda, float *C,
-               int32_t ldc, const float *residual, int32_t ldr, const int32_t *col_of,
-               void *stream);
+               int32_t ldc, const float *residual, int32_t ldr, const float *row_scale,
+               const int32_t *col_of, void *stream);
 
 /* float32 -> half activations, clamped to +-65504 (packH2, kernels.ts:32-36). */
 int wg_f32_to_f16(const float *x, uint16_t *out, int64_t n, void *stream);
@@ -299,6 +300,13 @@ int wg_decode_plan_destroy(wg_decode_plan *plan);
  * x[m][i]^2 + eps)), clamped to +-65504; rs_out[m] = the 1 / RMS (or NULL). */
 int wg_rms_norm(const float *x, int32_t M, int32_t D, int32_t ldx, const float *w, float eps,
                 uint16_t *out, int32_t ldo, float *rs_out, void *stream);
+/* The prescaled form the reference's matmuls read (NORM_TO_H2 with PRESCALE
+ * 32, src/gpu/kernels.ts:89, :1195-1242): out[m][i] = half(x[m][i] * w[i] /
+ * 32), clamped to +-65504, and row_scale[m] = 32 / sqrt(mean_i x[m][i]^2 +
+ * eps), the factor a product over out takes afterwards (the GEMV's and
+ * GEMM's row scale). */
+int wg_norm_to_h2(const float *x, int32_t M, int32_t D, int32_t ldx, const float *w, float eps,
+                  uint16_t *out, int32_t ldo, float *row_scale, void *stream);
 
 /* SwiGLU (REDUCE_SWIGLU / SWIGLU_F16, kernels.ts:1066-1077, :1256-1264):
  * out[m][i] = half(silu(gu[m][i]) * gu[m][F + i]) (gate rows, then up rows). */

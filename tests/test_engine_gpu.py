@@ -234,3 +234,20 @@ def test_long_prompt_through_gemm_batches(hip, family, monkeypatch):
     assert list(picks) == list(picks_o)
     first = int(picks[-1])
     assert eng.decode(first, 6) == orc.decode(first, 6)
+
+
+def test_capture_leaves_the_cache_alone(hip):
+    """Capturing the decode step after a prompt runs it once eagerly: every
+    cache row before the current position stays as the prompt wrote it, and
+    graph replay then decodes as the CPU decoder does."""
+    eng, orc = _pair("qwen-nbits", seed=0)
+    rng = np.random.default_rng(1)
+    prompt = _prompt(rng, 21, eng.shape.vocab)
+    first = int(eng.forward(prompt).cpu()[-1])
+    orc.forward(prompt)
+    before = {i: (k[:21].clone(), v[:21].clone()) for i, (k, v) in
+              enumerate(zip(eng.k_cache.values(), eng.v_cache.values()))}
+    eng.capture_step(first)
+    for i, (k, v) in enumerate(zip(eng.k_cache.values(), eng.v_cache.values())):
+        assert torch.equal(k[:21], before[i][0]) and torch.equal(v[:21], before[i][1])
+    assert eng.decode(first, 12) == orc.decode(first, 12)

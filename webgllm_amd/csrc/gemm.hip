@@ -123,6 +123,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
                                                       const uint16_t *__restrict__ A, int lda,
                                                       float *__restrict__ C, int ldc,
                                                       const float *residual, int ldr,
+                                                      const float *row_scale,
                                                       const int32_t *col_of, int M, int N,
                                                       int K) {
   constexpr int NWV = WGM * WGN;  // waves
@@ -292,6 +293,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
         const int m = m0 + wm * WM + t * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
         if (m < M) {
           float v = acc[t][u][j];
+          if (row_scale) v *= row_scale[m];
           if (residual) v += residual[(int64_t)m * ldr + col];
           C[(int64_t)m * ldc + col] = v;
         }
@@ -301,7 +303,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
 
 template <int ZK, int BM, int BN, int S, int WGM = 2, int WGN = 2>
 int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
-                 const float *residual, int ldr, const int32_t *col_of, hipStream_t s) {
+                 const float *residual, int ldr, const float *row_scale, const int32_t *col_of,
+                 hipStream_t s) {
   constexpr int STAGE = BM * 128 + Stage<ZK, BN>::WQ + Stage<ZK, BN>::WS + Stage<ZK, BN>::WZ;
   constexpr size_t LDS = (size_t)S * STAGE;
   static bool raised = false;  // allow more than 64 KiB of dynamic LDS, once
@@ -313,13 +316,14 @@ int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float
   const int grid = ((M + BM - 1) / BM) * (w->N / BN);
   gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN><<<grid, WGM * WGN * 64, LDS, s>>>(
       (const uint8_t *)w->quants, (const uint16_t *)w->scales, w->zeros, A, lda, C, ldc,
-      residual, ldr, col_of, M, w->N, w->K);
+      residual, ldr, row_scale, col_of, M, w->N, w->K);
   return launched("wg_q4_gemm");
 }
 
 template <int ZK>
 int launch(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
-           const float *residual, int ldr, const int32_t *col_of, hipStream_t s) {
+           const float *residual, int ldr, const float *row_scale, const int32_t *col_of,
+           hipStream_t s) {
   // The largest tile whose count still covers most compute units: each
   // weight is dequantized once per tile, so taller tiles (more rows a
   // wave) spend fewer vector instructions per MFMA. The knob gemm_tile
@@ -333,12 +337,12 @@ int launch(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, i
     else if (w->N % 128 == 0) t = 1;
   }
   if (t == 3 && w->N % 256 == 0)
-    return launch_tiles<ZK, 128, 256, 3, 1, 8>(w, A, M, lda, C, ldc, residual, ldr, col_of, s);
+    return launch_tiles<ZK, 128, 256, 3, 1, 8>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
   if (t == 2 && w->N % 128 == 0)
-    return launch_tiles<ZK, 128, 128, 3, 1, 4>(w, A, M, lda, C, ldc, residual, ldr, col_of, s);
+    return launch_tiles<ZK, 128, 128, 3, 1, 4>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
   if (w->N % 128 == 0)
-    return launch_tiles<ZK, 64, 128, 4, 1, 4>(w, A, M, lda, C, ldc, residual, ldr, col_of, s);
-  return launch_tiles<ZK, 64, 64, 5, 1, 2>(w, A, M, lda, C, ldc, residual, ldr, col_of, s);
+    return launch_tiles<ZK, 64, 128, 4, 1, 4>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+  return launch_tiles<ZK, 64, 64, 5, 1, 2>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
 }
 
 }  // namespace
@@ -349,8 +353,8 @@ using namespace wg;
 extern "C" {
 
 int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda, float *C,
-               int32_t ldc, const float *residual, int32_t ldr, const int32_t *col_of,
-               void *stream) {
+               int32_t ldc, const float *residual, int32_t ldr, const float *row_scale,
+               const int32_t *col_of, void *stream) {
   int rc = check_matrix(w, "wg_q4_gemm");
   if (rc) return rc;
   WG_REQUIRE(w->layout == WG_LAYOUT_ROWGROUP,
@@ -373,9 +377,9 @@ int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda,
   }
   hipStream_t s = as_stream(stream);
   switch (w->zero) {
-    case WG_ZERO_8: return launch<WG_ZERO_8>(w, A, M, lda, C, ldc, residual, ldr, col_of, s);
-    case WG_ZERO_U8: return launch<WG_ZERO_U8>(w, A, M, lda, C, ldc, residual, ldr, col_of, s);
-    default: return launch<WG_ZERO_F16>(w, A, M, lda, C, ldc, residual, ldr, col_of, s);
+    case WG_ZERO_8: return launch<WG_ZERO_8>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+    case WG_ZERO_U8: return launch<WG_ZERO_U8>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+    default: return launch<WG_ZERO_F16>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
   }
 }
 

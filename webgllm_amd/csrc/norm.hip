@@ -52,6 +52,34 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, int D, in
   }
 }
 
+// The reference's prescaled form (NORM_TO_H2 with PRESCALE): out =
+// half(x * w / mult), rs_out[m] = mult / sqrt(mean x^2 + eps), the factor a
+// product over out takes afterwards.
+__global__ __launch_bounds__(256) void norm_to_h2_kernel(const float *x, int D, int ldx,
+                                                         const float *w, float eps, float mult,
+                                                         uint16_t *out, int ldo, float *rs_out) {
+  __shared__ float lds[4];
+  const float *xr = x + (int64_t)blockIdx.x * ldx;
+  float s = 0.0f;
+  for (int i = threadIdx.x * 4; i < D; i += 1024) {
+    float4 v = *reinterpret_cast<const float4 *>(xr + i);
+    s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  const float ms = block_sum256(s, lds) / (float)D;
+  if (threadIdx.x == 0) rs_out[blockIdx.x] = mult / sqrtf(ms + eps);
+  uint16_t *o = out + (int64_t)blockIdx.x * ldo;
+  for (int i = threadIdx.x * 4; i < D; i += 1024) {
+    float4 v = *reinterpret_cast<const float4 *>(xr + i);
+    float4 g = *reinterpret_cast<const float4 *>(w + i);
+    ushort4 h;
+    h.x = to_h(v.x * g.x / mult);
+    h.y = to_h(v.y * g.y / mult);
+    h.z = to_h(v.z * g.z / mult);
+    h.w = to_h(v.w * g.w / mult);
+    *reinterpret_cast<ushort4 *>(o + i) = h;
+  }
+}
+
 // out[m][i] = half(silu(gu[m][i]) * gu[m][F + i]).
 __global__ void swiglu_kernel(const float *gu, int M, int F, int ldg, uint16_t *out, int ldo) {
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -165,6 +193,19 @@ int wg_rms_norm(const float *x, int32_t M, int32_t D, int32_t ldx, const float *
              "wg_rms_norm: misaligned buffers");
   rms_norm_kernel<<<M, 256, 0, as_stream(stream)>>>(x, D, ldx, w, eps, out, ldo, rs_out);
   return launched("wg_rms_norm");
+}
+
+int wg_norm_to_h2(const float *x, int32_t M, int32_t D, int32_t ldx, const float *w, float eps,
+                  uint16_t *out, int32_t ldo, float *row_scale, void *stream) {
+  WG_REQUIRE(x && w && out && row_scale, "wg_norm_to_h2: null argument");
+  WG_REQUIRE(M >= 1 && D >= 4 && D % 4 == 0 && ldx >= D && ldo >= D && ldx % 4 == 0 &&
+                 ldo % 4 == 0,
+             "wg_norm_to_h2: strides %d, %d for rows of %d", ldx, ldo, D);
+  WG_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)out & 7) == 0,
+             "wg_norm_to_h2: misaligned buffers");
+  norm_to_h2_kernel<<<M, 256, 0, as_stream(stream)>>>(x, D, ldx, w, eps, 32.0f, out, ldo,
+                                                      row_scale);
+  return launched("wg_norm_to_h2");
 }
 
 int wg_swiglu(const float *gu, int32_t M, int32_t F, int32_t ldg, uint16_t *out, int32_t ldo,

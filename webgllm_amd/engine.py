@@ -390,6 +390,7 @@ class Engine:
             self._pre = {
                 "ids": torch.zeros(R, dtype=torch.int32, device=dev),
                 "h": torch.zeros((R, D), dtype=f32, device=dev),
+                "rs": torch.zeros(R, dtype=f32, device=dev),
                 "x16": torch.zeros((R, D), dtype=f16, device=dev),
                 "c16": torch.zeros((R, D), dtype=f16, device=dev),
                 "bcx": torch.zeros((R, 3 * D), dtype=f32, device=dev),
@@ -416,32 +417,44 @@ class Engine:
         """A prompt batch of M rows (pre ids[:M] at positions pos ..) through
         the GEMMs on MFMA, as the reference's forwardBatch takes batches larger
         than the split path's (Engine.matmul, src/engine.ts:4969-5234, and its
-        attention plan for a prompt, :6359-6630). Inputs are normalized to
-        halves by a norm kernel; the caches and conv states advance; no head,
-        no picks (the prompt's last rows go through _forward_rows)."""
+        attention plan for a prompt, :6359-6630). A norm's output is the
+        reference's prescaled half(h w / 32), its 32 / RMS the GEMM's row
+        scale, as in the few-token path; the caches and conv states advance;
+        no head here (_prefill_head)."""
         s, w, b = self.shape, self.w, self._pre_buffers()
         D = s.hidden
-        h, x16 = b["h"][:M], b["x16"][:M]
+        h, x16, rs = b["h"][:M], b["x16"][:M], b["rs"][:M]
         ops.embed(w.embedding, b["ids"][:M], out=h)
         for i, lw in enumerate(w.layers):
-            ops.rms_norm(h, lw["op_norm"], s.eps, out=x16)
+            ops.norm_to_h2(h, lw["op_norm"], s.eps, x16, rs)
             if s.layer_type(i) == "conv":
-                bcx = ops.gemm(lw["in_proj"], x16, out=b["bcx"][:M])
+                bcx = ops.gemm(lw["in_proj"], x16, out=b["bcx"][:M], row_scale=rs)
                 ops.short_conv(bcx, D, s.conv_kernel, lw["taps"], self.state[i], out=b["c16"][:M])
                 ops.gemm(lw["out_proj"], b["c16"][:M], out=h, residual=h)
             else:
-                qkv = ops.gemm(lw["qkv"], x16, out=b["qkv"][:M], col_of=self._col_of(lw["qkv"]))
+                qkv = ops.gemm(lw["qkv"], x16, out=b["qkv"][:M], col_of=self._col_of(lw["qkv"]),
+                               row_scale=rs)
                 ops.head_prep(qkv, self.attn, self.rope, self.pos, self.k_cache[i],
                               self.v_cache[i], lw.get("q_norm"), lw.get("k_norm"),
                               q_out=b["q"][:M])
                 ops.attn_prefill(b["q"][:M], self.attn, self.k_cache[i], self.v_cache[i],
                                  self.pos, out=b["att16"][:M])
                 ops.gemm(lw["o"], b["att16"][:M], out=h, residual=h)
-            ops.rms_norm(h, lw["ffn_norm"], s.eps, out=x16)
+            ops.norm_to_h2(h, lw["ffn_norm"], s.eps, x16, rs)
             gu = ops.gemm(lw["gate_up"], x16, out=b["gu"][:M],
-                          col_of=self._col_of(lw["gate_up"]))
+                          col_of=self._col_of(lw["gate_up"]), row_scale=rs)
             ops.swiglu(gu, out=b["ff16"][:M])
             ops.gemm(lw["down"], b["ff16"][:M], out=h, residual=h)
+
+    def _prefill_head(self, r0: int, T: int) -> None:
+        """Logits and picks of rows r0 .. r0 + T - 1 (T <= 8) of the last
+        prompt batch: the final norm to halves, the head GEMV, the picks."""
+        s, w, b = self.shape, self.w, self._pre_buffers()
+        x16, rs = b["x16"][r0:r0 + T], b["rs"][r0:r0 + T]
+        ops.norm_to_h2(b["h"][r0:r0 + T], w.final_norm, s.eps, x16, rs)
+        ops.gemv(w.embedding, x16, out=self.logits[:T], row_scale=rs)
+        ops.argmax_rows(self.logits[:T], ids=self.next_ids[:T], tops=self.tops[:T],
+                        scratch=self.argmax_scratch)
 
     # --- the reference's Engine API -------------------------------------------
     def reset(self) -> None:
@@ -467,7 +480,7 @@ class Engine:
         # picks are returned, through the few-token path
         big = 0
         if not draft and len(tokens) > MAX_ROWS and self._prefill_ok():
-            big = len(tokens) - (len(tokens) % MAX_ROWS or MAX_ROWS)
+            big = len(tokens)
         for b0 in range(0, big, PREFILL_ROWS):
             batch = tokens[b0:min(big, b0 + PREFILL_ROWS)]
             M = len(batch)
@@ -475,7 +488,14 @@ class Engine:
             self.pos.fill_(self.position)
             self._prefill_rows(M)
             self.position += M
-        for b0 in range(big, len(tokens), MAX_ROWS):
+        if big:
+            # the picks of the last batch of 8 (len mod 8 rows, or 8): the head
+            # over the last rows of the final GEMM batch only
+            T = len(tokens) % MAX_ROWS or MAX_ROWS
+            M = len(tokens) - (len(tokens) - 1) // PREFILL_ROWS * PREFILL_ROWS
+            self._prefill_head(M - T, T)
+            out = self.next_ids[:T]
+        for b0 in range(big if big else 0, len(tokens), MAX_ROWS):
             batch = tokens[b0:b0 + MAX_ROWS]
             M = len(batch)
             self.ids[:M].copy_(torch.tensor(batch, dtype=torch.int32))
@@ -507,9 +527,14 @@ class Engine:
         self.position = pos0 + count
 
     # --- graph-captured single-token decode -----------------------------------
-    def capture_step(self) -> None:
+    def capture_step(self, token: int) -> None:
         """Captures one decode step: forward of ids[0] at pos, pick into
-        ids[0], pos += 1."""
+        ids[0], pos += 1. The capture first runs the step once eagerly with
+        ids[0] = token at pos = position (the token the first replay will
+        run): that run writes this position's K and V, which the first replay
+        writes again, and everything else it changes is put back."""
+        self.ids[0] = token
+        self.pos.fill_(self.position)
         stream = torch.cuda.Stream(device=self.device)
         stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(stream):
@@ -548,7 +573,7 @@ class Engine:
         if self.position + steps > self.ctx:
             raise ValueError("decode would run past the cache")
         if self.graph is None:
-            self.capture_step()
+            self.capture_step(first_token)
         p0 = self.position
         self.ids[0] = first_token
         self.pos.fill_(p0)

@@ -189,9 +189,11 @@ class DecodePlan:
 
 
 def gemm(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
-         residual: torch.Tensor | None = None, col_of: torch.Tensor | None = None) -> torch.Tensor:
+         residual: torch.Tensor | None = None, col_of: torch.Tensor | None = None,
+         row_scale: torch.Tensor | None = None) -> torch.Tensor:
     """C = A W^T on MFMA for M tokens of half activations A [M, K]; col_of
-    (int32 [N], optional) sends stored row n to output column col_of[n]."""
+    (int32 [N], optional) sends stored row n to output column col_of[n];
+    row_scale (float32 [M], optional) multiplies row m's sums."""
     if a16.dtype not in (torch.float16, torch.int16):
         raise ValueError("activations must be halves")
     a16 = _dev(a16)
@@ -201,6 +203,7 @@ def gemm(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
     _dev(out, torch.float32)
     L.check(L.load().wg_q4_gemm(C.byref(m.desc), _p(a16), M, a16.shape[1], _p(out), out.shape[1],
                                 _p(residual), residual.shape[1] if residual is not None else 0,
+                                _p(None if row_scale is None else _dev(row_scale, torch.float32)),
                                 _p(None if col_of is None else _dev(col_of, torch.int32)),
                                 _stream()))
     return out
@@ -222,6 +225,18 @@ def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | N
         out = torch.empty((M, D), dtype=torch.float16, device=x.device)
     L.check(L.load().wg_rms_norm(_p(x), M, D, x.shape[-1], _p(_dev(w, torch.float32)), eps,
                                  _p(out), out.shape[-1], _p(rs_out), _stream()))
+    return out
+
+
+def norm_to_h2(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor,
+               row_scale: torch.Tensor) -> torch.Tensor:
+    """The reference's prescaled norm: out = half(x * w / 32) per row of x
+    [M, D] (float32), row_scale[m] = 32 / RMS(x[m])."""
+    x = _dev(x, torch.float32)
+    M, D = x.shape
+    L.check(L.load().wg_norm_to_h2(_p(x), M, D, x.shape[-1], _p(_dev(w, torch.float32)), eps,
+                                   _p(out), out.shape[-1], _p(_dev(row_scale, torch.float32)),
+                                   _stream()))
     return out
 
 
