@@ -134,7 +134,9 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
   constexpr int STAGE = A_BYTES + WQ + WS + WZ;
   constexpr int IA = BM * 128 / 1024 / NWV;  // A loads (1 KB each) a wave issues a stage
   static_assert(IA >= 1 && IA * NWV * 1024 == A_BYTES, "A tile splits evenly over the waves");
-  constexpr int NW = IA + 2 + (ZK == WG_ZERO_U8 ? 1 : 0);  // loads a wave issues a stage
+  constexpr int QP = 2 * BN;  // nibble pieces (16 bytes) a stage
+  constexpr int IQ = QP > 64 * NWV ? QP / (64 * NWV) : 1;  // nibble loads a wave issues
+  constexpr int NW = IA + IQ + 1 + (ZK == WG_ZERO_U8 ? 1 : 0);  // loads a wave issues a stage
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -160,8 +162,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
   // K loop, from wave-uniform bases that step kt moves by a fixed stride
   // (A: 64 halves; nibbles: two blocks of 64 bytes a row group; scales and
   // half zero points: 8 halves; u8 zero points: 8 bytes).
-  constexpr int PWQ = 2 * BN / NWV;  // nibble pieces (16 bytes) a wave
-  static_assert(PWQ >= 1 && PWQ <= 64 && PWQ * NWV == 2 * BN, "nibble pieces");
+  constexpr int PWQ = QP > 64 * NWV ? 64 : QP / NWV;  // lanes a nibble load
+  static_assert(PWQ >= 1 && IQ * NWV * PWQ == QP, "nibble pieces");
   constexpr int NSC = BN / 4, PIECES = ZK == WG_ZERO_F16 ? 2 * NSC : NSC, PWS = PIECES / NWV;
   static_assert(PWS >= 1 && PWS * NWV == PIECES && NSC % PWS == 0, "scale pieces");
   constexpr int PWZ = ZK == WG_ZERO_U8 ? 2 * BN / 4 / NWV : 1;
@@ -174,8 +176,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
     const int m = min(m0 + row, M - 1);
     off_a[i] = (uint32_t)(((int64_t)m * lda + c * 8) * 2);
   }
-  const int qq = wave * PWQ + lane;
-  const uint32_t off_q = (uint32_t)(((int64_t)(g0 + (qq >> 3)) * B) * 64 + (qq & 7) * 16);
+  uint32_t off_q[IQ];
+#pragma unroll
+  for (int i = 0; i < IQ; i++) {
+    const int qq = (i * NWV + wave) * PWQ + lane;
+    off_q[i] = (uint32_t)(((int64_t)(g0 + (qq >> 3)) * B) * 64 + (qq & 7) * 16);
+  }
   const int qs = wave * PWS + lane;
   const bool s_is_zero = wave * PWS >= NSC;  // wave-uniform
   const uint32_t off_s = (uint32_t)((int64_t)(g0 + (s_is_zero ? qs - NSC : qs)) * B * 8);
@@ -189,9 +195,11 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
     for (int i = 0; i < IA; i++)
       dma16((const unsigned char *)A + kt * 128, off_a[i],
             __builtin_amdgcn_readfirstlane(base + (i * NWV + wave) * 1024));
-    if (lane < PWQ)
-      dma16(quants + kt * 128, off_q,
-            __builtin_amdgcn_readfirstlane(base + A_BYTES + wave * PWQ * 16));
+#pragma unroll
+    for (int i = 0; i < IQ; i++)
+      if (lane < PWQ)
+        dma16(quants + kt * 128, off_q[i],
+              __builtin_amdgcn_readfirstlane(base + A_BYTES + (i * NWV + wave) * PWQ * 16));
     if (lane < PWS)
       dma16(s_base + kt * 16, off_s,
             __builtin_amdgcn_readfirstlane(base + A_BYTES + WQ + wave * PWS * 16));
