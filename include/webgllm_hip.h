@@ -103,7 +103,7 @@ int wg_finish(wg_ctx *ctx);
 
 /* ------------------------------------------------ 2. quantized matrices */
 
-/* Device layouts of a 4-bit matrix.
+/* Device layouts of a quantized matrix.
  * WG_LAYOUT_ROWGROUP is the reference's QuantMatrix layout (src/weights.ts:1-31,
  * :153-178): rows in groups of 4, blocks of 32 along K, 16 bytes a block row
  * in Q4_0 nibble order (byte j: weight j low, weight j + 16 high); word
@@ -113,9 +113,21 @@ int wg_finish(wg_ctx *ctx);
  * 12 bytes of 6-bit scales and mins, 128 nibble bytes) kept at 0.5625
  * bytes a weight and regrouped by rows of 4: record (g * supers + s) * 4 + r
  * of 144 bytes; the kernels rebuild packQ4_K's per-32 (d', z')
- * (src/repack.ts:100-168) in registers. */
+ * (src/repack.ts:100-168) in registers.
+ * WG_LAYOUT_Q8 is the reference's 8-bit QuantMatrix (src/weights.ts:9-11,
+ * :24-25): the same row groups and blocks of 32, a block row 32 signed
+ * bytes (weight j in byte j), byte index ((g * blocks + b) * 4 + r) * 32 +
+ * j, half scales at (g * blocks + b) * 4 + r; weight = scale * q.
+ * WG_LAYOUT_Q6K is the reference's 6-bit QuantMatrix (src/weights.ts:23-30):
+ * GGUF Q6_K super-blocks of 256 weights kept as they are, a row's
+ * super-block 208 bytes (ql[128], qh[64], int8 scales[16]) at byte
+ * ((g * supers + s) * 4 + r) * 208, its half d in `scales` at (g * supers
+ * + s) * 4 + r; weight = d * scales[sub-block of 16] * (q - 32) as
+ * dequantize_row_q6_K. `zero` is WG_ZERO_8 (unused) for both. */
 #define WG_LAYOUT_ROWGROUP 0
 #define WG_LAYOUT_Q4K 1
+#define WG_LAYOUT_Q8 2
+#define WG_LAYOUT_Q6K 3
 
 /* Zero points of WG_LAYOUT_ROWGROUP: none (8, Q4_0), one u8 a block
  * (MatMulNBits), or one half a block (Q4_K repacked: QuantMatrix.zeroHalves). */
@@ -123,13 +135,15 @@ int wg_finish(wg_ctx *ctx);
 #define WG_ZERO_U8 1
 #define WG_ZERO_F16 2
 
+/* A quantized matrix of any layout above (the name is historical: 8- and
+ * 6-bit layouts use the same descriptor). */
 typedef struct {
   int32_t N;      /* output rows, a multiple of 4 */
-  int32_t K;      /* inputs per row, a multiple of 32 (256 for WG_LAYOUT_Q4K) */
+  int32_t K;      /* inputs per row, a multiple of 32 (256 for WG_LAYOUT_Q4K, Q6K) */
   int32_t layout; /* WG_LAYOUT_* */
   int32_t zero;   /* WG_ZERO_* (WG_LAYOUT_ROWGROUP only) */
-  const void *quants; /* ROWGROUP: N*K/2 bytes; Q4K: N*K/256*144 bytes */
-  const void *scales; /* ROWGROUP: N*K/32 halves; Q4K: unused */
+  const void *quants; /* ROWGROUP: N*K/2 bytes; Q4K: N*K/256*144; Q8: N*K; Q6K: N*K/256*208 */
+  const void *scales; /* ROWGROUP, Q8: N*K/32 halves; Q6K: N*K/256 halves; Q4K: unused */
   const void *zeros;  /* ROWGROUP: N*K/32 u8 or halves, or NULL for WG_ZERO_8 */
 } wg_q4_matrix;
 
@@ -158,10 +172,29 @@ int wg_repack_q4_k_native(const wg_q4_matrix *dst, int32_t row0, int32_t rows, c
  * [rows][ceil(K/64)] (NULL: 8) -> ROWGROUP with WG_ZERO_U8 (or WG_ZERO_8). */
 int wg_repack_nbits(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *quant,
                     const void *scales, const void *zp, const int32_t *src_rows, void *stream);
+/* packQ8_0 (src/repack.ts:171-200): GGUF Q8_0 blocks (34 bytes: half scale,
+ * 32 int8) -> WG_LAYOUT_Q8, bytes as they are. */
+int wg_repack_q8_0(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *src,
+                   const int32_t *src_rows, void *stream);
+/* quantizeQ8 (src/repack.ts:634-704): float32 rows [rows][K] (device) ->
+ * WG_LAYOUT_Q8, bit-exact: per block of 32, scale = toHalf(max |v| / 127)
+ * and q = clamp(floor(v / scale + 0.5), -127, 127) with the quotient in
+ * doubles (q = 0 where the scale is 0); the path the reference's GGUF
+ * loader takes for every tensor it does not keep in its own format
+ * (packRows, src/load-gguf.ts:509-555). */
+int wg_quantize_q8(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const float *src,
+                   void *stream);
+/* packQ6_K (src/repack.ts:706-728): GGUF Q6_K super-blocks (210 bytes)
+ * -> WG_LAYOUT_Q6K, the first 208 bytes of each as they are and its half d
+ * into the scales. */
+int wg_repack_q6_k(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *src,
+                   const int32_t *src_rows, void *stream);
 
 /* matrixRow (src/repack.ts:865-891) on the GPU: rows [row0, row0 + rows)
  * dequantized to float32, bit-exact: fp32(d * (q - z)) with the difference
- * and product in doubles, as the reference computes them. */
+ * and product in doubles, as the reference computes them; 8-bit: fp32(d *
+ * q); 6-bit: fp32(d * sc * (q - 32)) as dequantizeQ6_K (src/repack.ts:405-440)
+ * on the same bytes. */
 int wg_q4_dequant(const wg_q4_matrix *m, int32_t row0, int32_t rows, float *out, void *stream);
 
 /* ------------------------------------------------------------ matmul */
@@ -222,7 +255,11 @@ typedef struct {
  * src/gpu/kernels.ts:744-895, :163-296, dispatched by Engine.splitPartials,
  * engine.ts:5241-5377): y[m][n] = sum_k W[n][k] x[m][k] for M <= 8 rows of
  * half activations x ([M][ldx], natural order), fp32 out. No MFMA: 128-bit
- * loads of nibbles, dequant in registers, wavefront reductions. */
+ * loads of nibbles, dequant in registers, wavefront reductions. Every
+ * layout: 8-bit matrices as the 8-bit split matmul sums them (per block
+ * acc += d * sum q a, kernels.ts:219-246), Q6_K as the Q6_K head does (per
+ * super-block acc += d * sum_sub sc * sum (q - 32) a, kernels.ts:3593-3686),
+ * with every epilogue. */
 int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx, float *y,
                int32_t ldy, const wg_epilogue *ep, void *stream);
 
@@ -315,7 +352,8 @@ int wg_swiglu(const float *gu, int32_t M, int32_t F, int32_t ldg, uint16_t *out,
 
 /* Embedding rows (embed / embedFold, kernels.ts:1092-1149, :985-1041): h[m] =
  * row ids[m] of the quantized embedding, dequantized as matrixRow does
- * (src/repack.ts:865-891); an id outside [0, N) embeds as zeros. With ep
+ * (src/repack.ts:865-891; a Q6_K embedding as dequantizeQ6_K, src/repack.ts:405-440);
+ * an id outside [0, N) embeds as zeros. With ep
  * (its STORE outputs out16 and parts_out), also layer 0's prescaled half
  * input and the sums of squares of each 4 values, as embedFold draws them. */
 int wg_embed(const wg_q4_matrix *emb, const int32_t *ids, int32_t M, float *h, int32_t ldh,

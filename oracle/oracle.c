@@ -472,6 +472,241 @@ void orc_matmul_split(const orc_qm *m, const uint16_t *x16, int M, float *y, int
   (void)threads;
 }
 
+/* -------------------------------------------- 8-bit and Q6_K matrices */
+
+/* src/repack.ts:174-200: GGUF Q8_0 blocks (fp16 d, 32 int8) into an 8-bit
+ * matrix: scale index si = (n >> 2) * blocks * 4 + (n & 3) + 4 b, the 32
+ * codes at bytes 32 si.. as they are. */
+int orc_pack_q8_0(uint8_t *quants, uint16_t *scales, int N, int K, int row0, const uint8_t *src,
+                  size_t src_len, int rows, const int32_t *src_rows) {
+  int blocks = K / 32;
+  if (row0 < 0 || row0 + rows > N) return -1;
+  for (int i = 0; i < rows; i++) {
+    int n = row0 + i;
+    int from = src_rows ? src_rows[i] : i;
+    if ((size_t)(from + 1) * blocks * 34 > src_len) return -1;
+    const uint8_t *p = src + (size_t)from * blocks * 34;
+    size_t si = (size_t)(n >> 2) * blocks * 4 + (n & 3);
+    for (int b = 0; b < blocks; b++, p += 34, si += 4) {
+      scales[si] = rd16(p);
+      memcpy(quants + si * 32, p + 2, 32);
+    }
+  }
+  return 0;
+}
+
+/* src/repack.ts:634-704 (quantizeQ8): per block of 32, max = the largest
+ * |v| (NaN if any is: Math.max), h = toHalf(max / 127); a scale that is not
+ * > 0 gives q = 0; otherwise q = ((v / scale + 128.5) | 0) - 128 clamped to
+ * +-127, the quotient and sum in doubles and `| 0` JavaScript's ToInt32
+ * (truncation toward zero; NaN and infinities give 0). */
+static int32_t to_int32(double x) {
+  if (!(x == x) || isinf(x)) return 0;
+  double t = trunc(x);
+  double m = fmod(t, 4294967296.0);
+  if (m < 0) m += 4294967296.0;
+  return (int32_t)(uint32_t)m;
+}
+
+int orc_quantize_q8(uint8_t *quants, uint16_t *scales, int N, int K, int row0,
+                    const float *values, int rows) {
+  const float *half = htab();
+  int blocks = K / 32;
+  if (row0 < 0 || row0 + rows > N) return -1;
+  for (int i = 0; i < rows; i++) {
+    int n = row0 + i;
+    const float *v = values + (size_t)i * K;
+    size_t si = (size_t)(n >> 2) * blocks * 4 + (n & 3);
+    for (int b = 0; b < blocks; b++, v += 32, si += 4) {
+      double max = 0;
+      for (int j = 0; j < 32; j++) {
+        double a = fabs((double)v[j]);
+        max = (a != a || max != max) ? NAN : (a > max ? a : max);
+      }
+      uint16_t h = orc_to_half(max / 127);
+      double scale = half[h];
+      scales[si] = h;
+      int8_t *q = (int8_t *)(quants + si * 32);
+      if (!(scale > 0)) {
+        memset(q, 0, 32);
+        continue;
+      }
+      for (int j = 0; j < 32; j++) {
+        int32_t x = to_int32((double)v[j] / scale + 128.5) - 128;
+        q[j] = (int8_t)(x > 127 ? 127 : x < -127 ? -127 : x);
+      }
+    }
+  }
+  return 0;
+}
+
+/* src/repack.ts:706-728 (packQ6_K): a row's super-block (210 bytes: ql[128],
+ * qh[64], int8 scales[16], fp16 d) kept as its first 208 bytes at record
+ * (g * supers + s) * 4 + r, its d in the scales there. (src_rows, which the
+ * reference's packer does not take, picks each row's source row.) */
+int orc_pack_q6_k(uint8_t *quants, uint16_t *scales, int N, int K, int row0, const uint8_t *src,
+                  size_t src_len, int rows, const int32_t *src_rows) {
+  int supers = K / 256;
+  if (row0 < 0 || row0 + rows > N) return -1;
+  for (int i = 0; i < rows; i++) {
+    int n = row0 + i, g = n >> 2, r = n & 3;
+    int from = src_rows ? src_rows[i] : i;
+    if ((size_t)(from + 1) * supers * 210 > src_len) return -1;
+    for (int s = 0; s < supers; s++) {
+      const uint8_t *p = src + ((size_t)from * supers + s) * 210;
+      size_t at = ((size_t)g * supers + s) * 4 + r;
+      memcpy(quants + at * 208, p, 208);
+      scales[at] = rd16(p + 208);
+    }
+  }
+  return 0;
+}
+
+/* src/repack.ts:514-528: out = d * int8, per 34-byte block. */
+void orc_dequantize_q8_0(const uint8_t *src, int rows, int K, float *out) {
+  const float *half = htab();
+  size_t blocks = (size_t)rows * K / 32;
+  for (size_t b = 0; b < blocks; b++) {
+    const uint8_t *p = src + b * 34;
+    double d = half[rd16(p)];
+    for (int j = 0; j < 32; j++) out[b * 32 + j] = (float)(d * (int8_t)p[2 + j]);
+  }
+}
+
+/* src/repack.ts:405-440 (ggml's dequantize_row_q6_K as the reference states
+ * it): in half n of a super-block, for l = 0..31 and is = l / 16,
+ *   y[128n + l]      = d sc[8n + is]     (ql[64n + l] & 15       | (qh[32n + l] & 3) << 4      - 32)
+ *   y[128n + l + 32] = d sc[8n + is + 2] (ql[64n + l + 32] & 15  | (qh[32n + l] >> 2 & 3) << 4 - 32)
+ *   y[128n + l + 64] = d sc[8n + is + 4] (ql[64n + l] >> 4       | (qh[32n + l] >> 4 & 3) << 4 - 32)
+ *   y[128n + l + 96] = d sc[8n + is + 6] (ql[64n + l + 32] >> 4  | (qh[32n + l] >> 6) << 4     - 32)
+ * d sc exact in doubles, each product rounded once to float32. */
+static void q6k_super(const uint8_t *p, double d, float *y) {
+  for (int n = 0; n < 2; n++, y += 128) {
+    const uint8_t *ql = p + n * 64, *qh = p + 128 + n * 32;
+    const int8_t *sc = (const int8_t *)(p + 192 + n * 8);
+    for (int l = 0; l < 32; l++) {
+      int is = l / 16;
+      int h = qh[l];
+      y[l] = (float)(d * sc[is] * (((ql[l] & 15) | ((h & 3) << 4)) - 32));
+      y[l + 32] = (float)(d * sc[is + 2] * (((ql[l + 32] & 15) | (((h >> 2) & 3) << 4)) - 32));
+      y[l + 64] = (float)(d * sc[is + 4] * (((ql[l] >> 4) | (((h >> 4) & 3) << 4)) - 32));
+      y[l + 96] = (float)(d * sc[is + 6] * (((ql[l + 32] >> 4) | (((h >> 6) & 3) << 4)) - 32));
+    }
+  }
+}
+
+void orc_dequantize_q6_k(const uint8_t *src, int rows, int K, float *out) {
+  const float *half = htab();
+  size_t supers = (size_t)rows * K / 256;
+  for (size_t s = 0; s < supers; s++) {
+    const uint8_t *p = src + s * 210;
+    q6k_super(p, half[rd16(p + 208)], out + s * 256);
+  }
+}
+
+/* matrixRow of an 8-bit matrix (src/repack.ts:873-876): scale * signed byte. */
+void orc_q8_row(const uint8_t *quants, const uint16_t *scales, int K, int n, float *out) {
+  const float *half = htab();
+  int blocks = K / 32;
+  for (int b = 0; b < blocks; b++) {
+    size_t si = (size_t)(n >> 2) * blocks * 4 + (n & 3) + 4 * (size_t)b;
+    double d = half[scales[si]];
+    for (int j = 0; j < 32; j++) out[b * 32 + j] = (float)(d * (int8_t)quants[si * 32 + j]);
+  }
+}
+
+/* Row n of a 6-bit matrix: each record's bytes as dequantize_row_q6_K reads
+ * them (src/weights.ts:23-30; the Q6_K head's formula, src/gpu/kernels.ts:
+ * 3376-3390). */
+void orc_q6k_row(const uint8_t *quants, const uint16_t *scales, int K, int n, float *out) {
+  const float *half = htab();
+  int supers = K / 256;
+  for (int s = 0; s < supers; s++) {
+    size_t at = ((size_t)(n >> 2) * supers + s) * 4 + (n & 3);
+    q6k_super(quants + at * 208, half[scales[at]], out + s * 256);
+  }
+}
+
+/* The 8-bit matmul (src/gpu/kernels.ts:219-246; split as orc_matmul_split):
+ * per block and row, b = sum over the 8 words of dot(q, A_w) with q the
+ * signed bytes as floats, then acc += d * b, float32; slices summed in
+ * order. */
+void orc_matmul_q8(const uint8_t *quants, const uint16_t *scales, int N, int K,
+                   const uint16_t *x16, int M, float *y, int threads, int split_fragments,
+                   int max_split) {
+  const float *half = htab();
+  int blocks = K / 32, groups = N / 4;
+  int kb_slice, slices;
+  split_rule(groups, blocks, split_fragments, max_split, &kb_slice, &slices);
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static) collapse(2)
+#endif
+  for (int g = 0; g < groups; g++)
+    for (int t = 0; t < M; t++) {
+      float total[4] = {0, 0, 0, 0};
+      const uint16_t *xa = x16 + (size_t)t * K;
+      for (int s = 0; s < slices; s++) {
+        int kb0 = s * kb_slice, kb1 = kb0 + kb_slice < blocks ? kb0 + kb_slice : blocks;
+        float acc[4] = {0, 0, 0, 0};
+        for (int kb = kb0; kb < kb1; kb++)
+          for (int r = 0; r < 4; r++) {
+            size_t si = ((size_t)g * blocks + kb) * 4 + r;
+            const int8_t *q = (const int8_t *)(quants + si * 32);
+            float b = 0.0f;
+            for (int w = 0; w < 8; w++) {
+              float dw = 0.0f;
+              for (int c = 0; c < 4; c++)
+                dw += (float)q[4 * w + c] * half[xa[kb * 32 + 4 * w + c]];
+              b += dw;
+            }
+            acc[r] += half[scales[si]] * b;
+          }
+        for (int r = 0; r < 4; r++) total[r] += acc[r];
+      }
+      for (int r = 0; r < 4; r++) y[(size_t)t * N + 4 * g + r] = total[r];
+    }
+  (void)threads;
+}
+
+/* The Q6_K head (src/gpu/kernels.ts:3593-3686): per row and super-block, P
+ * = sum over the 16 sub-blocks of sc * sum (q - 32) a (float32), then acc
+ * += d * P. */
+void orc_matmul_q6k(const uint8_t *quants, const uint16_t *scales, int N, int K,
+                    const uint16_t *x16, int M, float *y, int threads) {
+  const float *half = htab();
+  int supers = K / 256;
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static) collapse(2)
+#endif
+  for (int n = 0; n < N; n++)
+    for (int t = 0; t < M; t++) {
+      const uint16_t *xa = x16 + (size_t)t * K;
+      float acc = 0.0f;
+      for (int s = 0; s < supers; s++) {
+        size_t at = ((size_t)(n >> 2) * supers + s) * 4 + (n & 3);
+        const uint8_t *p = quants + at * 208;
+        float P = 0.0f;
+        for (int sub = 0; sub < 16; sub++) {
+          /* sub-block sub covers weights 16 sub .. 16 sub + 15: half n = sub / 8,
+           * group i = sub % 8 / 2, l = 16 (sub % 2) + 0..15 */
+          int hn = sub / 8, i = (sub % 8) / 2, l0 = 16 * (sub % 2);
+          const uint8_t *ql = p + 64 * hn + 32 * (i & 1), *qh = p + 128 + 32 * hn;
+          float dot = 0.0f;
+          for (int l = l0; l < l0 + 16; l++) {
+            int q = ((ql[l] >> (4 * (i >> 1))) & 15) | (((qh[l] >> (2 * i)) & 3) << 4);
+            dot += (float)(q - 32) * half[xa[256 * s + 128 * hn + 32 * i + l]];
+          }
+          P += (float)((const int8_t *)(p + 192))[8 * hn + 2 * i + l0 / 16] * dot;
+        }
+        acc += half[scales[at]] * P;
+      }
+      y[(size_t)t * N + n] = acc;
+    }
+  (void)threads;
+}
+
 /* ------------------------------------------------------------ elementwise */
 
 /* packH2 (src/gpu/kernels.ts:32-36): clamped to +-65504, then to halves. */

@@ -64,6 +64,27 @@ void orc_quantize_q4_0(const float *w, int rows, int K, uint8_t *out);  /* ggml 
 void orc_quantize_nbits(const float *w, int rows, int K, const uint8_t *zp_per_block,
                         uint8_t *quant, uint16_t *scales, uint8_t *zp_packed);
 
+/* ---- 8-bit and Q6_K matrices (src/weights.ts:9-11, :23-30) ----
+ * 8-bit: codes at bytes 32 si .. 32 si + 31, half scales at si =
+ * (g*blocks+b)*4+r. Q6_K: 208-byte records and half d at (g*supers+s)*4+r. */
+int orc_pack_q8_0(uint8_t *quants, uint16_t *scales, int N, int K, int row0, const uint8_t *src,
+                  size_t src_len, int rows, const int32_t *src_rows);  /* repack.ts:174-200 */
+int orc_quantize_q8(uint8_t *quants, uint16_t *scales, int N, int K, int row0,
+                    const float *values, int rows);                   /* repack.ts:634-704 */
+int orc_pack_q6_k(uint8_t *quants, uint16_t *scales, int N, int K, int row0, const uint8_t *src,
+                  size_t src_len, int rows, const int32_t *src_rows);  /* repack.ts:706-728 */
+void orc_dequantize_q8_0(const uint8_t *src, int rows, int K, float *out); /* repack.ts:514-528 */
+void orc_dequantize_q6_k(const uint8_t *src, int rows, int K, float *out); /* repack.ts:405-440 */
+void orc_q8_row(const uint8_t *quants, const uint16_t *scales, int K, int n, float *out);
+                                                                   /* repack.ts:873-876 */
+void orc_q6k_row(const uint8_t *quants, const uint16_t *scales, int K, int n, float *out);
+                                                                   /* kernels.ts:3376-3390 */
+void orc_matmul_q8(const uint8_t *quants, const uint16_t *scales, int N, int K,
+                   const uint16_t *x16, int M, float *y, int threads, int split_fragments,
+                   int max_split);                                 /* kernels.ts:219-246 */
+void orc_matmul_q6k(const uint8_t *quants, const uint16_t *scales, int N, int K,
+                    const uint16_t *x16, int M, float *y, int threads); /* kernels.ts:3593-3686 */
+
 /* ---- matmul ---- */
 /* y[m][n] = sum_k W[n][k] * x[m][k], W as orc_matrix_row dequantizes it, in fp64. */
 void orc_gemv_f64(const orc_qm *m, const float *x, int M, double *y, int threads);

@@ -57,6 +57,15 @@ _lib.orc_dequantize_q4_k.argtypes = [_P, _I, _I, _P]
 _lib.orc_dequantize_nbits_row.argtypes = [_I, _P, _P, _P, _I, _P]
 _lib.orc_quantize_q4_0.argtypes = [_P, _I, _I, _P]
 _lib.orc_quantize_nbits.argtypes = [_P, _I, _I, _P, _P, _P, _P]
+_lib.orc_pack_q8_0.argtypes = [_P, _P, _I, _I, _I, _P, C.c_size_t, _I, _P]
+_lib.orc_quantize_q8.argtypes = [_P, _P, _I, _I, _I, _P, _I]
+_lib.orc_pack_q6_k.argtypes = [_P, _P, _I, _I, _I, _P, C.c_size_t, _I, _P]
+_lib.orc_dequantize_q8_0.argtypes = [_P, _I, _I, _P]
+_lib.orc_dequantize_q6_k.argtypes = [_P, _I, _I, _P]
+_lib.orc_q8_row.argtypes = [_P, _P, _I, _I, _P]
+_lib.orc_q6k_row.argtypes = [_P, _P, _I, _I, _P]
+_lib.orc_matmul_q8.argtypes = [_P, _P, _I, _I, _P, _I, _P, _I, _I, _I]
+_lib.orc_matmul_q6k.argtypes = [_P, _P, _I, _I, _P, _I, _P, _I]
 _lib.orc_gemv_f64.argtypes = [C.POINTER(_QM), _P, _I, _P, _I]
 _lib.orc_matmul_split.argtypes = [C.POINTER(_QM), _P, _I, _P, _I, _I, _I]
 _lib.orc_f32_to_h2.argtypes = [_P, C.c_size_t, _P]
@@ -124,6 +133,81 @@ class QuantMatrix:
         out = np.empty((self.N, self.K), dtype=np.float32)
         _lib.orc_matrix_dense(C.byref(self._c()), _ptr(out), threads)
         return out
+
+
+class WideMatrix:
+    """An 8-bit or 6-bit QuantMatrix (src/weights.ts:9-11, :23-30) as numpy
+    arrays: `quants` bytes and half `scales` in the reference's order."""
+
+    def __init__(self, N: int, K: int, bits: int):
+        unit = 256 if bits == 6 else 32
+        if N % 4:
+            raise ValueError(f"matrix rows ({N}) must be a multiple of 4")
+        if K % unit:
+            raise ValueError(f"matrix columns ({K}) must be a multiple of {unit}")
+        self.N, self.K, self.bits = N, K, bits
+        self.quants = np.zeros(N * K if bits == 8 else N * (K // 256) * 208, dtype=np.uint8)
+        self.scales = np.zeros(N * (K // unit), dtype=np.uint16)
+
+    def row(self, n: int) -> np.ndarray:
+        out = np.empty(self.K, dtype=np.float32)
+        fn = _lib.orc_q8_row if self.bits == 8 else _lib.orc_q6k_row
+        fn(_ptr(self.quants), _ptr(self.scales), self.K, n, _ptr(out))
+        return out
+
+    def dense(self) -> np.ndarray:
+        return np.stack([self.row(n) for n in range(self.N)])
+
+    def matmul(self, x16: np.ndarray, threads: int = 0, split_fragments: int = 4096,
+               max_split: int = 16) -> np.ndarray:
+        """The reference's float32 block form (8-bit: the split matmul; 6-bit:
+        the Q6_K head) of y = x W^T for half activations x16 [M, K]."""
+        x16 = np.ascontiguousarray(x16, dtype=np.uint16).reshape(-1, self.K)
+        y = np.empty((x16.shape[0], self.N), dtype=np.float32)
+        if self.bits == 8:
+            _lib.orc_matmul_q8(_ptr(self.quants), _ptr(self.scales), self.N, self.K, _ptr(x16),
+                               x16.shape[0], _ptr(y), threads, split_fragments, max_split)
+        else:
+            _lib.orc_matmul_q6k(_ptr(self.quants), _ptr(self.scales), self.N, self.K, _ptr(x16),
+                                x16.shape[0], _ptr(y), threads)
+        return y
+
+
+def pack_q8_0(m: WideMatrix, row0: int, src: np.ndarray, rows: int, src_rows=None) -> None:
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    sr = _rows(src_rows)
+    if _lib.orc_pack_q8_0(_ptr(m.quants), _ptr(m.scales), m.N, m.K, row0, _ptr(src), src.size,
+                          rows, _ptr(sr)):
+        raise ValueError("packQ8_0 failed")
+
+
+def quantize_q8(m: WideMatrix, row0: int, values: np.ndarray) -> None:
+    values = np.ascontiguousarray(values, dtype=np.float32).reshape(-1, m.K)
+    if _lib.orc_quantize_q8(_ptr(m.quants), _ptr(m.scales), m.N, m.K, row0, _ptr(values),
+                            values.shape[0]):
+        raise ValueError("quantizeQ8 failed")
+
+
+def pack_q6_k(m: WideMatrix, row0: int, src: np.ndarray, rows: int, src_rows=None) -> None:
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    sr = _rows(src_rows)
+    if _lib.orc_pack_q6_k(_ptr(m.quants), _ptr(m.scales), m.N, m.K, row0, _ptr(src), src.size,
+                          rows, _ptr(sr)):
+        raise ValueError("packQ6_K failed")
+
+
+def dequantize_q8_0(src: np.ndarray, rows: int, K: int) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    out = np.empty(rows * K, dtype=np.float32)
+    _lib.orc_dequantize_q8_0(_ptr(src), rows, K, _ptr(out))
+    return out.reshape(rows, K)
+
+
+def dequantize_q6_k(src: np.ndarray, rows: int, K: int) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    out = np.empty(rows * K, dtype=np.float32)
+    _lib.orc_dequantize_q6_k(_ptr(src), rows, K, _ptr(out))
+    return out.reshape(rows, K)
 
 
 def _rows(src_rows):

@@ -63,3 +63,49 @@ def rel_l2(got, want):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-300))
+
+
+def lcg_bytes(n, seed):
+    """src/q6-expanded.test.ts:11-16: seed = seed * 1664525 + 1013904223
+    (mod 2^32), byte = seed >> 24."""
+    out = np.empty(n, dtype=np.uint8)
+    for i in range(n):
+        seed = (seed * 1664525 + 1013904223) & 0xFFFFFFFF
+        out[i] = seed >> 24
+    return out
+
+
+def imul_bytes(n, offset):
+    """src/q6-split.test.ts:7 and q8-converter.test.ts:5: Math.imul(i +
+    offset, 2654435761) >>> 24."""
+    i = np.arange(n, dtype=np.uint64) + np.uint64(offset)
+    return ((i * np.uint64(2654435761)) & np.uint64(0xFFFFFFFF)) >> np.uint64(24)
+
+
+def encode_q6_k(q, sc, d_bits):
+    """GGUF Q6_K super-blocks from 6-bit codes q [supers, 256] (0..63), int8
+    sub-block scales sc [supers, 16] and half d bits [supers]: the packing
+    loop of ggml's quantize_row_q6_K (per 128 weights j, l = 0..31: ql[l] =
+    q[j+l] & 15 | (q[j+l+64] & 15) << 4, ql[l+32] = q[j+l+32] & 15 |
+    (q[j+l+96] & 15) << 4, qh[l] = q[j+l] >> 4 | q[j+l+32] >> 4 << 2 |
+    q[j+l+64] >> 4 << 4 | q[j+l+96] >> 4 << 6), ql then qh then scales then
+    d, 210 bytes each."""
+    q = np.asarray(q, dtype=np.int64)
+    supers = q.shape[0]
+    out = np.zeros((supers, 210), dtype=np.uint8)
+    for s in range(supers):
+        ql = np.zeros(128, np.int64)
+        qh = np.zeros(64, np.int64)
+        for half in range(2):
+            L = q[s, 128 * half:128 * half + 128]
+            for l in range(32):
+                ql[64 * half + l] = (L[l] & 15) | ((L[l + 64] & 15) << 4)
+                ql[64 * half + l + 32] = (L[l + 32] & 15) | ((L[l + 96] & 15) << 4)
+                qh[32 * half + l] = ((L[l] >> 4) | ((L[l + 32] >> 4) << 2) |
+                                     ((L[l + 64] >> 4) << 4) | ((L[l + 96] >> 4) << 6))
+        out[s, :128] = ql
+        out[s, 128:192] = qh
+        out[s, 192:208] = np.asarray(sc[s], dtype=np.int8).view(np.uint8)
+        out[s, 208] = int(d_bits[s]) & 255
+        out[s, 209] = int(d_bits[s]) >> 8
+    return out.reshape(-1)

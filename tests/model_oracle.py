@@ -33,6 +33,11 @@ def dense_of(m, threads=0) -> np.ndarray:
 def _dense_stored(m, threads=0) -> np.ndarray:
     from webgllm_amd import lib as L
     N, K = m.N, m.K
+    if m.layout in (L.LAYOUT_Q8, L.LAYOUT_Q6K):
+        wm = O.WideMatrix(N, K, 8 if m.layout == L.LAYOUT_Q8 else 6)
+        wm.quants[:] = _np(m.quants)
+        wm.scales[:] = _np(m.scales).view(np.uint16)
+        return wm.dense()
     if m.layout == L.LAYOUT_Q4K:
         G, S = N // 4, K // 256
         rec = _np(m.quants).reshape(G, S, 4, 144)

@@ -160,3 +160,30 @@ def test_attn_prefill_rejects_before_any_device_work():
         L.check(lib.wg_attn_prefill(None, 4, 4096, C.byref(sh), f, f, f, 64, f, 4096, None))
     with pytest.raises(L.WgError, match="16-byte aligned"):
         L.check(lib.wg_attn_prefill(f + 4, 4, 4096, C.byref(sh), f, f, f, 64, f, 4096, None))
+
+
+def test_wide_sizes_and_rejections():
+    """8-bit and Q6_K matrices: sizes as newQuantMatrix (src/repack.ts:14-35)
+    makes them; packers refuse the wrong destination; the GEMM takes 4-bit
+    row groups only."""
+    lib = L.load()
+    q, s, z = C.c_size_t(), C.c_size_t(), C.c_size_t()
+    L.check(lib.wg_q4_sizes(128, 4096, L.LAYOUT_Q8, 0, C.byref(q), C.byref(s), C.byref(z)))
+    assert (q.value, s.value, z.value) == (128 * 4096, 128 * 128 * 2, 0)
+    L.check(lib.wg_q4_sizes(128, 4096, L.LAYOUT_Q6K, 0, C.byref(q), C.byref(s), C.byref(z)))
+    assert (q.value, s.value, z.value) == (128 * 16 * 208, 128 * 16 * 2, 0)
+    with pytest.raises(L.WgError, match="multiple of 256"):
+        L.check(lib.wg_q4_sizes(4, 512 + 32, L.LAYOUT_Q6K, 0, None, None, None))
+    q4 = _desc()
+    q8 = _desc(layout=L.LAYOUT_Q8)
+    q6 = _desc(K=256, layout=L.LAYOUT_Q6K)
+    for fn, d, msg in ((lib.wg_repack_q8_0, q4, "8-bit"), (lib.wg_repack_q6_k, q8, "Q6_K"),
+                       (lib.wg_repack_q4_0, q8, "row-group")):
+        rc = fn(C.byref(d), 0, 4, 0x5000, None, None)
+        assert rc == -1 and msg in L.last_error()
+    rc = lib.wg_quantize_q8(C.byref(q6), 0, 4, 0x5000, None)
+    assert rc == -1 and "8-bit" in L.last_error()
+    rc = lib.wg_repack_q8_0(C.byref(q8), 4, 8, 0x5000, None, None)
+    assert rc == -1 and "outside" in L.last_error()
+    rc = lib.wg_q4_gemm(C.byref(q8), 0x10000, 64, 64, 0x20000, 8, None, 0, None, None, None)
+    assert rc != 0

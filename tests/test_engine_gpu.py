@@ -12,10 +12,10 @@ pytestmark = pytest.mark.gpu
 
 
 def _shape(fmt, conv_layers=(), qk_norm=False, layers=3, hidden=256, heads=4, kv=2, hd=64,
-           inter=512, vocab=1024):
+           inter=512, vocab=1024, embed_fmt=None):
     from webgllm_amd.engine import ModelShape
     return ModelShape(f"tiny-{fmt}", hidden, layers, heads, kv, hd, inter, vocab, fmt,
-                      qk_norm=qk_norm, conv_layers=conv_layers)
+                      qk_norm=qk_norm, conv_layers=conv_layers, embed_fmt=embed_fmt)
 
 
 FAMILIES = {
@@ -23,6 +23,11 @@ FAMILIES = {
     "qwen-nbits": dict(fmt="nbits", heads=7, kv=1),
     "lfm2-q4_0": dict(fmt="q4_0", conv_layers=(0, 2), qk_norm=True),
     "q4_k-rowgroup": dict(fmt="q4_k_rowgroup"),
+    # as real GGUF files: a Q6_K embedding and output head; Q8_0 tensors; and
+    # tensors the loader requantizes to 8 bits (Q4_K_M's Q6_K/Q5_K ones)
+    "gguf-q4_k-q6_k-head": dict(fmt="q4_k_rowgroup", embed_fmt="q6_k"),
+    "gguf-q8_0": dict(fmt="q8_0", conv_layers=(1,), qk_norm=True),
+    "gguf-requant-q8": dict(fmt="q8", embed_fmt="q6_k", heads=7, kv=1),
 }
 
 

@@ -33,7 +33,7 @@ def _matrix(fmt, N, K, seed, row_order=None):
     return w.matrix(N, K, row_order)
 
 
-FMTS = ["q4_0", "nbits", "q4_k", "q4_k_rowgroup"]
+FMTS = ["q4_0", "nbits", "q4_k", "q4_k_rowgroup", "q8_0", "q6_k"]
 
 
 @pytest.mark.parametrize("fmt", FMTS)
@@ -90,7 +90,7 @@ def test_swiglu_epilogue(hip, fmt, M):
     assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -9 + 1e-3 * np.abs(want).max())
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q4_k"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "q8"])
 @pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (32, 8, 128)])
 @pytest.mark.parametrize("M,pos0", [(1, 0), (1, 1500), (4, 1022)])
 def test_rope_kv_epilogue(hip, fmt, H, KV, hd, M, pos0):

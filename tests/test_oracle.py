@@ -424,3 +424,178 @@ def test_argmax_ties_lowest_id_and_nan():
     w[256] = 2.0  # chunk boundary: the earlier chunk wins the tie
     assert O.argmax(w)[0] == 255
     assert O.argmax(np.full(10, -np.inf, np.float32))[0] == 0
+
+
+# ------------------------------------------------- 8-bit and Q6_K matrices
+
+def test_q8_0_dequant_known_answer():
+    """src/q4k-pack.test.ts:103-118: d = 0.5 with codes j - 16, d = 0.25 with
+    codes 4 j - 64."""
+    b = np.zeros(68, np.uint8)
+    for p, d in ((0, 0.5), (34, 0.25)):
+        h = O.to_half(d)
+        b[p], b[p + 1] = h & 255, h >> 8
+    for j in range(32):
+        b[2 + j] = (j - 16) & 255
+        b[36 + j] = (4 * j - 64) & 255
+    out = O.dequantize_q8_0(b, 2, 32)
+    assert np.array_equal(out[0], 0.5 * (np.arange(32) - 16))
+    assert np.array_equal(out[1], 0.25 * (4 * np.arange(32) - 64))
+
+
+def test_pack_q8_0_rows_are_the_files_weights():
+    """An 8-bit matrix's rows (matrixRow) equal dequantizeQ8_0 of the rows
+    the packer took, at an offset and through a row permutation."""
+    from tests.helpers import imul_bytes
+    N, K = 12, 96
+    src = imul_bytes(16 * (K // 32) * 34, 5).astype(np.uint8)
+    for b in range(16 * K // 32):  # sane halves for d
+        src[b * 34], src[b * 34 + 1] = 0x66, 0x1e
+    want = O.dequantize_q8_0(src, 16, K)
+    m = O.WideMatrix(N, K, 8)
+    perm = [7, 0, 15, 3]
+    O.pack_q8_0(m, 4, src, 4, src_rows=perm)
+    O.pack_q8_0(m, 0, src, 4)
+    for i, r in enumerate(perm):
+        assert np.array_equal(m.row(4 + i), want[r])
+    for n in range(4):
+        assert np.array_equal(m.row(n), want[n])
+    assert not m.quants[8 * K:].any()  # rows 8..11 untouched
+
+
+def _q6k_reference_matrix(kind):
+    from tests.helpers import imul_bytes, lcg_bytes
+    if kind == "expanded":  # src/q6-expanded.test.ts:8-20
+        rows, K = 12, 512
+        raw = lcg_bytes(rows * (K // 256) * 210, 7)
+        raw.reshape(-1, 210)[:, 208] = 0x00
+        raw.reshape(-1, 210)[:, 209] = 0x24
+    else:  # src/q6-split.test.ts:6-8
+        rows, K = 8, 512
+        raw = imul_bytes(rows * K // 256 * 210, 11).astype(np.uint8)
+        raw.reshape(-1, 210)[:, 208] = 0x66
+        raw.reshape(-1, 210)[:, 209] = 0x1e
+    return rows, K, raw
+
+
+@pytest.mark.parametrize("kind", ["expanded", "split"])
+def test_q6_k_packed_rows_equal_dequantize_q6_k(kind):
+    """The reference's Q6_K layout tests: a packQ6_K matrix read as its
+    shaders index it gives dequantizeQ6_K's weights exactly
+    (src/q6-expanded.test.ts:7-46, src/q6-split.test.ts:6-28)."""
+    rows, K, raw = _q6k_reference_matrix(kind)
+    want = O.dequantize_q6_k(raw, rows, K)
+    m = O.WideMatrix(rows, K, 6)
+    O.pack_q6_k(m, 0, raw, rows)
+    got = m.dense()
+    assert np.array_equal(got, want)
+    # and the scales texture holds each super-block's d
+    d = raw.reshape(rows, K // 256, 210)[:, :, 208:210].copy().view(np.uint16)[..., 0]
+    g = np.arange(rows) // 4
+    r = np.arange(rows) % 4
+    for s in range(K // 256):
+        at = (g * (K // 256) + s) * 4 + r
+        assert np.array_equal(m.scales[at], d[:, s])
+
+
+def test_q6_k_decode_inverts_ggml_packing():
+    """Codes, scales and d packed by ggml's Q6_K packing loop (an encoder
+    independent of the decoder) come back as d * sc[k / 16] * (q - 32), at
+    every position."""
+    from tests.helpers import encode_q6_k
+    rng = np.random.default_rng(9)
+    supers = 6
+    q = rng.integers(0, 64, (supers, 256))
+    q[0, :] = np.arange(256) % 64  # every code at every position class
+    sc = rng.integers(-128, 128, (supers, 16))
+    sc[1, :] = [-128, 127, 0, 1, -1, 64, -64, 2, 3, 5, 7, 11, 13, 17, 19, 23]
+    d_bits = np.array([O.to_half(v) for v in (0.001, 0.5, 2.0 ** -20, 3.0, 1e-3, 65504.0)])
+    raw = encode_q6_k(q, sc, d_bits)
+    got = O.dequantize_q6_k(raw, 1, supers * 256).reshape(supers, 256)
+    d = np.array([O.from_half(int(h)) for h in d_bits], np.float64)
+    want = (d[:, None] * np.repeat(sc, 16, axis=1) * (q - 32)).astype(np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_quantize_q8_hand_cases():
+    """quantizeQ8 (src/repack.ts:634-704) on blocks worked out by hand:
+    ties round up (floor(x + 0.5)), the clamp is +-127, a zero or NaN scale
+    gives zeros, an infinite scale maps an infinity to -127 (NaN quotient ->
+    ToInt32 0) and finite values to 0, a subnormal scale clamps."""
+    K = 32 * 6
+    v = np.zeros((4, K), np.float32)
+    # block 0: max 127 -> scale exactly 1
+    v[0, :8] = [127, 2.5, -2.5, 0.49, -0.5, 126.6, -127, 3.0]
+    # block 1: all zero; block 2: a NaN; block 3: +inf; block 4: subnormal scale
+    v[0, 64] = np.nan
+    v[0, 65] = 1.0
+    v[0, 96] = np.inf
+    v[0, 97] = 5.0
+    tiny = np.float32(127 * 1.25 * 2.0 ** -24)
+    v[0, 128:131] = [tiny, -tiny, tiny / 2]
+    # block 5: max 63.5 -> scale half(0.5) = 0.5
+    v[0, 160:164] = [63.5, 0.25, -0.25, 0.75]
+    v[1:] = np.random.default_rng(1).standard_normal((3, K)).astype(np.float32)
+    m = O.WideMatrix(4, K, 8)
+    O.quantize_q8(m, 0, v)
+    q = m.quants.view(np.int8)
+
+    def block(b):  # row 0's block b: si = b * 4
+        return q[b * 4 * 32:(b * 4 + 1) * 32], int(m.scales[b * 4])
+
+    c, s = block(0)
+    assert s == O.to_half(1.0)
+    assert list(c[:8]) == [127, 3, -2, 0, 0, 127, -127, 3] and not c[8:].any()
+    c, s = block(1)
+    assert s == 0 and not c.any()
+    c, s = block(2)
+    assert (s & 0x7C00) == 0x7C00 and (s & 0x3FF) and not c.any()
+    c, s = block(3)
+    assert s == 0x7C00 and c[0] == -127 and not c[1:].any()
+    c, s = block(4)
+    assert s == 1  # 2^-24
+    assert list(c[:3]) == [127, -127, 79]  # 158.75 -> clamp; 79.375 -> 79
+    c, s = block(5)
+    assert s == O.to_half(0.5)
+    assert list(c[:4]) == [127, 1, 0, 2]  # 0.5 + 0.5 -> 1; -0.5 + 0.5 -> 0; 1.5 + .5 -> 2
+
+
+def test_quantize_q8_error_bound_and_layout():
+    """Every code is the nearest to v / scale (within half a step, ties up)
+    and sits at the layout's index; the max maps to +-127."""
+    rng = np.random.default_rng(3)
+    N, K = 8, 256
+    v = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    m = O.WideMatrix(N, K, 8)
+    O.quantize_q8(m, 0, v)
+    dense = m.dense()
+    for n in range(N):
+        for b in range(K // 32):
+            blk = v[n, 32 * b:32 * b + 32].astype(np.float64)
+            s = O.from_half(int(m.scales[(n // 4 * (K // 32) + b) * 4 + n % 4]))
+            assert s > 0
+            err = np.abs(dense[n, 32 * b:32 * b + 32] - blk)
+            assert np.all(err <= s / 2 * (1 + 1e-6))
+            assert np.abs(np.round(np.abs(blk).max() / s)) >= 126
+
+
+@pytest.mark.parametrize("bits", [8, 6])
+def test_wide_matmul_block_form_matches_f64(bits):
+    """The reference's float32 block forms (the 8-bit split matmul, the Q6_K
+    head) against a float64 product of the pinned dequant."""
+    from tests.helpers import encode_q6_k
+    rng = np.random.default_rng(bits)
+    N, K, M = 16, 512, 3
+    m = O.WideMatrix(N, K, bits)
+    if bits == 8:
+        O.quantize_q8(m, 0, rng.standard_normal((N, K)).astype(np.float32) * 0.1)
+    else:
+        supers = N * K // 256
+        raw = encode_q6_k(rng.integers(0, 64, (supers, 256)),
+                          rng.integers(-128, 128, (supers, 16)),
+                          [O.to_half(v) for v in rng.uniform(1e-4, 1e-3, supers)])
+        O.pack_q6_k(m, 0, raw, N)
+    x16 = O.f32_to_h2(rng.standard_normal((M, K)).astype(np.float32))
+    got = m.matmul(x16)
+    want = O.halves_to_f32(x16).astype(np.float64) @ m.dense().astype(np.float64).T
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.abs(want).max()

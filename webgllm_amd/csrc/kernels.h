@@ -11,5 +11,8 @@ int check_epilogue(const wg_q4_matrix *w, int M, const float *y, int ldy, const 
 
 int launch_gemv_q4k(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y, int ldy,
                     const wg_epilogue &e, hipStream_t s);
+// WG_LAYOUT_Q8 and WG_LAYOUT_Q6K matrices.
+int launch_gemv_wide(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y, int ldy,
+                     const wg_epilogue &e, hipStream_t s);
 
 }  // namespace wg

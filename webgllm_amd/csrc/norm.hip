@@ -6,6 +6,7 @@
 #include "common.h"
 #include "dot.h"
 #include "epilogue.h"
+#include "wide.h"
 
 namespace wg {
 namespace {
@@ -175,6 +176,32 @@ __global__ void embed_q4k_kernel(const uint8_t *quants, const int32_t *ids, int 
   embed_extras(e, m, s * 256 + j * 32, v);
 }
 
+// Embedding rows of an 8-bit or Q6_K matrix: thread = (token m, 32-weight
+// piece c), each piece dequantized as wg_q4_dequant does.
+template <int LAYOUT>
+__global__ void embed_wide_kernel(const uint8_t *quants, const uint16_t *scales,
+                                  const int32_t *ids, int M, int K, int N, float *h, int ldh,
+                                  const wg_epilogue e) {
+  const int pieces = K / 32;
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)M * pieces) return;
+  int m = (int)(t / pieces), c = (int)(t % pieces);
+  int n = ids[m];
+  float v[32];
+  if (n < 0 || n >= N) {
+    for (int j = 0; j < 32; j++) v[j] = 0.0f;
+  } else if constexpr (LAYOUT == WG_LAYOUT_Q8) {
+    dequant32_q8(reinterpret_cast<const int8_t *>(quants), scales, n, c, pieces, v);
+  } else {
+    const int supers = K / 256;
+    const int64_t at = q6k_index(n, c >> 3, supers);
+    dequant32_q6k(quants + at * 208, half_to_float(scales[at]), c & 7, v);
+  }
+  float *o = h + (int64_t)m * ldh + c * 32;
+  for (int j = 0; j < 32; j++) o[j] = v[j];
+  embed_extras(e, m, c * 32, v);
+}
+
 }  // namespace
 }  // namespace wg
 
@@ -237,6 +264,13 @@ int wg_embed(const wg_q4_matrix *emb, const int32_t *ids, int32_t M, float *h, i
     embed_rowgroup_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
         (const uint32_t *)emb->quants, (const uint16_t *)emb->scales, emb->zeros, emb->zero, ids,
         M, blocks, emb->N, h, ldh, e);
+  } else if (emb->layout == WG_LAYOUT_Q8 || emb->layout == WG_LAYOUT_Q6K) {
+    int64_t n = (int64_t)M * (emb->K / 32);
+    auto kernel = emb->layout == WG_LAYOUT_Q8 ? embed_wide_kernel<WG_LAYOUT_Q8>
+                                              : embed_wide_kernel<WG_LAYOUT_Q6K>;
+    kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>((const uint8_t *)emb->quants,
+                                                       (const uint16_t *)emb->scales, ids, M,
+                                                       emb->K, emb->N, h, ldh, e);
   } else {
     int supers = emb->K / 256;
     int64_t n = (int64_t)M * supers * 8;

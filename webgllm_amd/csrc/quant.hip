@@ -3,6 +3,7 @@
 // while loading (src/repack.ts); here the file's bytes are copied to the
 // device once and rearranged there, one thread per row block.
 #include "common.h"
+#include "wide.h"
 
 namespace wg {
 namespace {
@@ -197,6 +198,103 @@ __global__ void dequant_q4k_kernel(const uint8_t *quants, int row0, int rows, in
   }
 }
 
+// packQ8_0 (src/repack.ts:174-200): thread = (row i, block b); the 34-byte
+// block's half scale and 32 codes as they are.
+__global__ void repack_q8_0_kernel(uint8_t *quants, uint16_t *scales, const uint8_t *src,
+                                   const int32_t *src_rows, int row0, int rows, int blocks) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * blocks) return;
+  int i = (int)(t / blocks), b = (int)(t % blocks);
+  int n = row0 + i;
+  int s = src_rows ? src_rows[i] : i;
+  const uint8_t *p = src + ((int64_t)s * blocks + b) * 34;
+  int64_t si = q8_index(n, b, blocks);
+  scales[si] = ld16_unaligned(p);
+  uint4 *q = reinterpret_cast<uint4 *>(quants + si * 32);
+  q[0] = make_uint4(ld32_unaligned(p + 2), ld32_unaligned(p + 6), ld32_unaligned(p + 10),
+                    ld32_unaligned(p + 14));
+  q[1] = make_uint4(ld32_unaligned(p + 18), ld32_unaligned(p + 22), ld32_unaligned(p + 26),
+                    ld32_unaligned(p + 30));
+}
+
+// quantizeQ8 (src/repack.ts:634-704): thread = (row i, block b). max is
+// the largest |v| (NaN if any v is, as Math.max); scale = toHalf(max / 127);
+// a block whose scale is not > 0 (zero or NaN) gets q = 0; otherwise q =
+// ToInt32(v / scale + 128.5) - 128 clamped to +-127, the quotient and sum
+// in doubles (ToInt32 truncates toward zero and maps NaN and infinities to
+// 0; |v / scale| stays below 2^9, so it never wraps).
+__global__ void quantize_q8_kernel(uint8_t *quants, uint16_t *scales, const float *src, int K,
+                                   int row0, int rows, int blocks) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * blocks) return;
+  int i = (int)(t / blocks), b = (int)(t % blocks);
+  int n = row0 + i;
+  const float *v = src + (int64_t)i * K + b * 32;
+  float mx = 0.0f;
+  for (int j = 0; j < 32; j++) {
+    float a = fabsf(v[j]);
+    if (a > mx || a != a) mx = a;
+    if (mx != mx) break;
+  }
+  int64_t si = q8_index(n, b, blocks);
+  uint16_t h = double_to_half_ref((double)mx / 127.0);
+  double scale = half_to_float(h);
+  scales[si] = h;
+  int8_t *q = reinterpret_cast<int8_t *>(quants + si * 32);
+  if (!(scale > 0.0)) {
+    for (int j = 0; j < 32; j++) q[j] = 0;
+    return;
+  }
+  for (int j = 0; j < 32; j++) {
+    double x = (double)v[j] / scale + 128.5;
+    int iv = (x == x && x > -2147483648.0 && x < 2147483648.0) ? (int)x : 0;  // trunc
+    iv -= 128;
+    q[j] = (int8_t)(iv > 127 ? 127 : iv < -127 ? -127 : iv);
+  }
+}
+
+// packQ6_K (src/repack.ts:706-728): thread = (row i, super-block s, 16-byte
+// piece p of the 208 kept bytes); piece 0 also moves the half d.
+__global__ void repack_q6_k_kernel(uint8_t *quants, uint16_t *scales, const uint8_t *src,
+                                   const int32_t *src_rows, int row0, int rows, int supers) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * supers * 13) return;
+  int piece = (int)(t % 13);
+  int64_t rs = t / 13;
+  int i = (int)(rs / supers), s = (int)(rs % supers);
+  int n = row0 + i;
+  int sr = src_rows ? src_rows[i] : i;
+  const uint8_t *p = src + ((int64_t)sr * supers + s) * 210;
+  int64_t at = q6k_index(n, s, supers);
+  const uint8_t *from = p + piece * 16;
+  reinterpret_cast<uint4 *>(quants + at * 208)[piece] =
+      make_uint4(ld32_unaligned(from), ld32_unaligned(from + 4), ld32_unaligned(from + 8),
+                 ld32_unaligned(from + 12));
+  if (piece == 0) scales[at] = ld16_unaligned(p + 208);
+}
+
+// matrixRow of an 8-bit matrix: thread = (row, block).
+__global__ void dequant_q8_kernel(const int8_t *quants, const uint16_t *scales, int row0, int rows,
+                                  int blocks, float *out) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * blocks) return;
+  int i = (int)(t / blocks), b = (int)(t % blocks);
+  dequant32_q8(quants, scales, row0 + i, b, blocks, out + (int64_t)i * blocks * 32 + b * 32);
+}
+
+// A Q6_K matrix's rows as dequantizeQ6_K: thread = (row, super-block, 32-piece).
+__global__ void dequant_q6k_kernel(const uint8_t *quants, const uint16_t *scales, int row0,
+                                   int rows, int supers, float *out) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)rows * supers * 8) return;
+  int j = (int)(t & 7);
+  int64_t rs = t >> 3;
+  int i = (int)(rs / supers), s = (int)(rs % supers);
+  int64_t at = q6k_index(row0 + i, s, supers);
+  dequant32_q6k(quants + at * 208, half_to_float(scales[at]), j,
+                out + (int64_t)i * supers * 256 + s * 256 + j * 32);
+}
+
 inline unsigned grid_for(int64_t threads, int per) { return (unsigned)((threads + per - 1) / per); }
 
 }  // namespace
@@ -284,6 +382,50 @@ int wg_repack_q4_k_native(const wg_q4_matrix *m, int32_t row0, int32_t rows, con
   return launched("wg_repack_q4_k_native");
 }
 
+int wg_repack_q8_0(const wg_q4_matrix *m, int32_t row0, int32_t rows, const void *src,
+                   const int32_t *src_rows, void *stream) {
+  int rc = check_matrix(m, "wg_repack_q8_0");
+  if (rc) return rc;
+  if ((rc = check_rows(m, row0, rows, "wg_repack_q8_0"))) return rc;
+  WG_REQUIRE(m->layout == WG_LAYOUT_Q8, "wg_repack_q8_0: Q8_0 rows go into an 8-bit matrix");
+  WG_REQUIRE(src, "wg_repack_q8_0: no source");
+  if (!rows) return WG_OK;
+  int blocks = m->K / 32;
+  repack_q8_0_kernel<<<grid_for((int64_t)rows * blocks, 256), 256, 0, as_stream(stream)>>>(
+      (uint8_t *)m->quants, (uint16_t *)m->scales, (const uint8_t *)src, src_rows, row0, rows,
+      blocks);
+  return launched("wg_repack_q8_0");
+}
+
+int wg_quantize_q8(const wg_q4_matrix *m, int32_t row0, int32_t rows, const float *src,
+                   void *stream) {
+  int rc = check_matrix(m, "wg_quantize_q8");
+  if (rc) return rc;
+  if ((rc = check_rows(m, row0, rows, "wg_quantize_q8"))) return rc;
+  WG_REQUIRE(m->layout == WG_LAYOUT_Q8, "wg_quantize_q8: the destination is not an 8-bit matrix");
+  WG_REQUIRE(src, "wg_quantize_q8: no source");
+  if (!rows) return WG_OK;
+  int blocks = m->K / 32;
+  quantize_q8_kernel<<<grid_for((int64_t)rows * blocks, 256), 256, 0, as_stream(stream)>>>(
+      (uint8_t *)m->quants, (uint16_t *)m->scales, src, m->K, row0, rows, blocks);
+  return launched("wg_quantize_q8");
+}
+
+int wg_repack_q6_k(const wg_q4_matrix *m, int32_t row0, int32_t rows, const void *src,
+                   const int32_t *src_rows, void *stream) {
+  int rc = check_matrix(m, "wg_repack_q6_k");
+  if (rc) return rc;
+  if ((rc = check_rows(m, row0, rows, "wg_repack_q6_k"))) return rc;
+  WG_REQUIRE(m->layout == WG_LAYOUT_Q6K, "wg_repack_q6_k: Q6_K rows go into a Q6_K matrix");
+  WG_REQUIRE(src, "wg_repack_q6_k: no source");
+  if (!rows) return WG_OK;
+  int supers = m->K / 256;
+  repack_q6_k_kernel<<<grid_for((int64_t)rows * supers * 13, 256), 256, 0, as_stream(stream)>>>(
+      (uint8_t *)m->quants, (uint16_t *)m->scales, (const uint8_t *)src, src_rows, row0, rows,
+      supers);
+  return launched("wg_repack_q6_k");
+}
+
 int wg_q4_dequant(const wg_q4_matrix *m, int32_t row0, int32_t rows, float *out, void *stream) {
   int rc = check_matrix(m, "wg_q4_dequant");
   if (rc) return rc;
@@ -296,6 +438,14 @@ int wg_q4_dequant(const wg_q4_matrix *m, int32_t row0, int32_t rows, float *out,
     dequant_rowgroup_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(
         (const uint32_t *)m->quants, (const uint16_t *)m->scales, m->zeros, m->zero, row0, rows,
         blocks, out);
+  } else if (m->layout == WG_LAYOUT_Q8) {
+    int blocks = m->K / 32;
+    dequant_q8_kernel<<<grid_for((int64_t)rows * blocks, 256), 256, 0, as_stream(stream)>>>(
+        (const int8_t *)m->quants, (const uint16_t *)m->scales, row0, rows, blocks, out);
+  } else if (m->layout == WG_LAYOUT_Q6K) {
+    int supers = m->K / 256;
+    dequant_q6k_kernel<<<grid_for((int64_t)rows * supers * 8, 256), 256, 0, as_stream(stream)>>>(
+        (const uint8_t *)m->quants, (const uint16_t *)m->scales, row0, rows, supers, out);
   } else {
     int supers = m->K / 256;
     int64_t n = (int64_t)rows * supers * 8;

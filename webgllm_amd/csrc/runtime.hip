@@ -45,6 +45,12 @@ int check_matrix(const wg_q4_matrix *m, const char *who) {
   } else if (m->layout == WG_LAYOUT_Q4K) {
     WG_REQUIRE(m->K > 0 && m->K % 256 == 0,
                "%s: Q4_K matrix columns (%d) must be a positive multiple of 256", who, m->K);
+  } else if (m->layout == WG_LAYOUT_Q8 || m->layout == WG_LAYOUT_Q6K) {
+    const int unit = m->layout == WG_LAYOUT_Q8 ? 32 : 256;
+    WG_REQUIRE(m->K > 0 && m->K % unit == 0,
+               "%s: %d-bit matrix columns (%d) must be a positive multiple of %d", who,
+               m->layout == WG_LAYOUT_Q8 ? 8 : 6, m->K, unit);
+    WG_REQUIRE(m->scales, "%s: matrix has no scales", who);
   } else {
     return fail(WG_ERR_UNSUPPORTED, "%s: unknown matrix layout %d", who, m->layout);
   }
@@ -346,6 +352,15 @@ int wg_q4_sizes(int32_t N, int32_t K, int32_t layout, int32_t zero, size_t *qb, 
     WG_REQUIRE(K > 0 && K % 256 == 0, "wg_q4_sizes: Q4_K columns (%d) must be a multiple of 256",
                K);
     q = (size_t)N * (K / 256) * 144;
+  } else if (layout == WG_LAYOUT_Q8) {
+    WG_REQUIRE(K > 0 && K % 32 == 0, "wg_q4_sizes: 8-bit columns (%d) must be a multiple of 32", K);
+    q = (size_t)N * K;
+    s = (size_t)N * (K / 32) * 2;
+  } else if (layout == WG_LAYOUT_Q6K) {
+    WG_REQUIRE(K > 0 && K % 256 == 0, "wg_q4_sizes: Q6_K columns (%d) must be a multiple of 256",
+               K);
+    q = (size_t)N * (K / 256) * 208;
+    s = (size_t)N * (K / 256) * 2;
   } else {
     return fail(WG_ERR_UNSUPPORTED, "wg_q4_sizes: unknown layout %d", layout);
   }

@@ -67,13 +67,18 @@ class ModelShape:
     head_dim: int
     intermediate: int
     vocab: int
-    fmt: str  # "q4_0" | "nbits" | "q4_k" (native super-blocks) | "q4_k_rowgroup"
+    # "q4_0" | "nbits" | "q4_k" (native super-blocks) | "q4_k_rowgroup" |
+    # "q8_0" (GGUF Q8_0) | "q8" (floats requantized to 8 bits) | "q6_k"
+    fmt: str
     rope_theta: float = 1e6
     eps: float = 1e-5
     qk_norm: bool = False
     conv_kernel: int = 3
     # layer i is "conv" when listed here, else attention
     conv_layers: tuple = ()
+    # the embedding's (and tied output head's) format when not `fmt`: real
+    # Q4 GGUF files store it as Q6_K (src/load-gguf.ts:428-442)
+    embed_fmt: str | None = None
     extra: dict = field(default_factory=dict)
 
     def layer_type(self, i: int) -> str:
@@ -115,7 +120,7 @@ class Weights:
         self.device = device
         s = shape
         D = s.hidden
-        self.embedding = self.matrix(s.vocab, D)
+        self.embedding = self.matrix(s.vocab, D, fmt=s.embed_fmt)
         self.final_norm = self.norm(D)
         self.layers = []
         for i in range(s.layers):
@@ -151,11 +156,12 @@ class Weights:
     def norm(self, n: int) -> torch.Tensor:
         return (1.0 + 0.1 * torch.randn(n, generator=self.g, device=self.device)).contiguous()
 
-    def matrix(self, N: int, K: int, row_order=None) -> ops.Q4Matrix:
-        """Random weights as a file holds them (GGUF Q4_0 or Q4_K blocks,
-        MatMulNBits rows), uploaded through the GPU repackers with `row_order`
-        as the loaders' srcRows (the logical row of each stored row)."""
-        fmt = self.shape.fmt
+    def matrix(self, N: int, K: int, row_order=None, fmt: str | None = None) -> ops.Q4Matrix:
+        """Random weights as a file holds them (GGUF Q4_0, Q4_K, Q8_0 or Q6_K
+        blocks, MatMulNBits rows, or floats the loader requantizes to 8 bits),
+        uploaded through the GPU repackers with `row_order` as the loaders'
+        srcRows (the logical row of each stored row)."""
+        fmt = fmt or self.shape.fmt
         g, dev = self.g, self.device
         src_rows = None if row_order is None else \
             torch.tensor(row_order, dtype=torch.int32, device=dev)
@@ -184,6 +190,25 @@ class Weights:
             zp.random_(0, 256, generator=g)
             m = ops.Q4Matrix.from_nbits(quant, sc.half().view(torch.uint8), zp, N, K,
                                         src_rows=src_rows)
+        elif fmt == "q8_0":
+            src = torch.empty(N * (K // 32) * 34, dtype=torch.uint8, device=dev)
+            src.random_(0, 256, generator=g)
+            blk = src.view(-1, 34)
+            d = torch.empty(blk.shape[0], device=dev).uniform_(1.0e-4, 3.0e-4, generator=g)
+            blk[:, 0:2] = d.half().view(torch.uint8).view(-1, 2)
+            m = ops.Q4Matrix.from_q8_0(src, N, K, src_rows=src_rows)
+        elif fmt == "q8":
+            vals = torch.randn((N, K), generator=g, device=dev) * 0.02
+            if row_order is not None:
+                vals = vals[src_rows.long()].contiguous()
+            m = ops.Q4Matrix.from_floats_q8(vals)
+        elif fmt == "q6_k":
+            src = torch.empty(N * (K // 256) * 210, dtype=torch.uint8, device=dev)
+            src.random_(0, 256, generator=g)
+            rec = src.view(-1, 210)
+            d = torch.empty(rec.shape[0], device=dev).uniform_(2.0e-5, 5.0e-5, generator=g)
+            rec[:, 208:210] = d.half().view(torch.uint8).view(-1, 2)
+            m = ops.Q4Matrix.from_q6_k(src, N, K, src_rows=src_rows)
         else:
             raise ValueError(f"unknown weight format {fmt}")
         m.row_order = row_order

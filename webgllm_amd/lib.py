@@ -18,7 +18,7 @@ WG_OK = 0
 STATUS = {-1: "invalid", -2: "out-of-memory", -3: "device", -4: "aliased", -5: "disposed",
           -6: "unsupported"}
 
-LAYOUT_ROWGROUP, LAYOUT_Q4K = 0, 1
+LAYOUT_ROWGROUP, LAYOUT_Q4K, LAYOUT_Q8, LAYOUT_Q6K = 0, 1, 2, 3
 ZERO_8, ZERO_U8, ZERO_F16 = 0, 1, 2
 
 
@@ -126,6 +126,9 @@ def load():
         "wg_repack_q4_k": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),
         "wg_repack_q4_k_native": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),
         "wg_repack_nbits": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P, P, P]),
+        "wg_repack_q8_0": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),
+        "wg_quantize_q8": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P]),
+        "wg_repack_q6_k": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),
         "wg_q4_dequant": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P]),
         "wg_q4_gemv": (C.c_int, [C.POINTER(Q4MatrixDesc), P, I32, I32, P, I32,
                                  C.POINTER(Epilogue), P]),

@@ -40,7 +40,8 @@ def to_device_bytes(b, device="cuda") -> torch.Tensor:
 
 
 class Q4Matrix:
-    """A 4-bit matrix resident on the device (see WG_LAYOUT_* in the header)."""
+    """A quantized matrix (4-, 8- or 6-bit) resident on the device (see WG_LAYOUT_* in the
+    header)."""
 
     def __init__(self, N: int, K: int, layout: int = L.LAYOUT_ROWGROUP, zero: int = L.ZERO_8,
                  device="cuda"):
@@ -83,6 +84,28 @@ class Q4Matrix:
         return m
 
     @classmethod
+    def from_q8_0(cls, src: torch.Tensor, N: int, K: int, src_rows=None) -> "Q4Matrix":
+        """An 8-bit matrix from GGUF Q8_0 rows (packQ8_0)."""
+        m = cls(N, K, L.LAYOUT_Q8, L.ZERO_8, device=src.device)
+        m.repack_q8_0(0, N, src, src_rows)
+        return m
+
+    @classmethod
+    def from_floats_q8(cls, values: torch.Tensor) -> "Q4Matrix":
+        """An 8-bit matrix quantized from float32 rows [N, K] (quantizeQ8)."""
+        N, K = values.shape
+        m = cls(N, K, L.LAYOUT_Q8, L.ZERO_8, device=values.device)
+        m.quantize_q8(0, N, values)
+        return m
+
+    @classmethod
+    def from_q6_k(cls, src: torch.Tensor, N: int, K: int, src_rows=None) -> "Q4Matrix":
+        """A 6-bit matrix from GGUF Q6_K rows (packQ6_K)."""
+        m = cls(N, K, L.LAYOUT_Q6K, L.ZERO_8, device=src.device)
+        m.repack_q6_k(0, N, src, src_rows)
+        return m
+
+    @classmethod
     def from_nbits(cls, quant: torch.Tensor, scales: torch.Tensor, zp, N: int, K: int,
                    src_rows=None) -> "Q4Matrix":
         m = cls(N, K, L.LAYOUT_ROWGROUP, L.ZERO_U8 if zp is not None else L.ZERO_8,
@@ -105,6 +128,18 @@ class Q4Matrix:
     def repack_nbits(self, row0, rows, quant, scales, zp=None, src_rows=None):
         L.check(L.load().wg_repack_nbits(C.byref(self.desc), row0, rows, _p(_dev(quant)),
                                          _p(_dev(scales)), _p(zp), _p(src_rows), _stream()))
+
+    def repack_q8_0(self, row0, rows, src, src_rows=None):
+        L.check(L.load().wg_repack_q8_0(C.byref(self.desc), row0, rows, _p(_dev(src)),
+                                        _p(src_rows), _stream()))
+
+    def quantize_q8(self, row0, rows, values):
+        L.check(L.load().wg_quantize_q8(C.byref(self.desc), row0, rows,
+                                        _p(_dev(values, torch.float32)), _stream()))
+
+    def repack_q6_k(self, row0, rows, src, src_rows=None):
+        L.check(L.load().wg_repack_q6_k(C.byref(self.desc), row0, rows, _p(_dev(src)),
+                                        _p(src_rows), _stream()))
 
     def dequant(self, row0: int = 0, rows: int | None = None) -> torch.Tensor:
         rows = self.N - row0 if rows is None else rows
