@@ -465,7 +465,91 @@ def workload_llama8b_prefill(args):
                 cfg, roof, cpu, dtype="f16 x f16 -> f32")
 
 
+def workload_wide_gemv(args, fmt, N, K, copies, what):
+    """A batch-1 GEMV over an 8-bit or Q6_K matrix as the decode launches the
+    head (prescaled-norm input from the sums of squares, float32 out),
+    graph-captured over `copies` distinct matrices."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    from webgllm_amd import engine as E, lib as L, ops
+    shape = E.ModelShape(f"{fmt}-gemv", K, 1, 1, 1, 4, 4, 4, fmt)
+    w = E.Weights.blank(shape, seed=0)
+    mats = [w.matrix(N, K) for _ in range(copies)]
+    x = (torch.randn((1, K), device="cuda", generator=torch.Generator(device="cuda")
+                     .manual_seed(1)) * 0.1).half()
+    parts = torch.ones((1, K // 4), device="cuda")
+    y = torch.empty((1, N), device="cuda")
+    ep = L.Epilogue(mode=L.EPI_STORE, norm_parts=parts.data_ptr(), n_parts=K // 4,
+                    ld_parts_in=K // 4, norm_count=K, eps=1e-5, norm_mult=32.0)
+    algo = mats[0].nbytes + K * 2 + (K // 4) * 4 + N * 4
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for m in mats:
+            ops.gemv(m, x, out=y, epilogue=ep)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for m in mats:
+                ops.gemv(m, x, out=y, epilogue=ep)
+    torch.cuda.synchronize()
+    # warm up for a third of a second: the first launches after the
+    # matrices are made run slower
+    t_end = time.time() + 0.33
+    n_warm = 0
+    while n_warm < max(3, args.warmup) or time.time() < t_end:
+        g.replay()
+        torch.cuda.synchronize()
+        n_warm += 1
+    reps = max(10, args.steps // 2)
+    ms_graph = timed(g.replay, reps)
+    us = ms_graph * 1e3 / copies
+    gbps = algo / (us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        threads = min(os.cpu_count() or 1, 16)
+        m = mats[0]
+        wm = O.WideMatrix(m.N, m.K, 8 if m.layout == L.LAYOUT_Q8 else 6)
+        wm.quants[:] = m.quants.cpu().numpy()
+        wm.scales[:] = m.scales.cpu().numpy().view(np.uint16)
+        x16 = x.cpu().numpy().view(np.uint16)
+        wm.matmul(x16, threads)
+        spent, n = 0.0, 0
+        while spent < 10.0 or n < 2:
+            t0 = O.now()
+            wm.matmul(x16, threads)
+            spent += O.now() - t0
+            n += 1
+        cpu = {"value": round(algo / (spent / n) / 1e9, 3), "unit": "GB/s", "cores": threads,
+               "kind": "port",
+               "sample": f"oracle float32 block form of the reference's shader (OpenMP, "
+                         f"{threads} threads) on one {N}x{K} matrix, 1 row, {n} repetitions "
+                         f"({spent:.1f} s)"}
+    kname = "gemv_wide_stream_kernel<Q6K>" if fmt == "q6_k" else "gemv_wide_stream_kernel<Q8>"
+    roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+            "kernel": f"{kname} {N}x{K} ({what}), prescaled-norm input",
+            "bytes_per_launch": algo, "avg_launch_us": round(us, 3), "launches": reps * copies}
+    cfg = {"workload": f"{what}: {fmt} GEMV {N}x{K} batch 1, {copies} distinct matrices in "
+                       f"one captured graph", "global_batch": 1, "parallelism": "none"}
+    return line(f"{fmt} GEMV HBM GB/s", round(gbps, 1), "GB/s", reps * copies, args.warmup,
+                ms_graph / copies, cfg, roof, cpu)
+
+
+def workload_q6_k_head(args):
+    """The Llama-3-8B output head as a Q4_K_M GGUF stores it (Q6_K,
+    128256 x 4096, 431 MB a copy)."""
+    return workload_wide_gemv(args, "q6_k", 128256, 4096, 2, "Llama-3-8B Q6_K output head")
+
+
+def workload_q8_gemv(args):
+    """The 8B gate|up matrix (28672 x 4096) requantized to 8 bits, as the
+    reference's GGUF loader stores tensors it does not keep in 4 bits."""
+    return workload_wide_gemv(args, "q8", 28672, 4096, 8, "Llama-3-8B gate|up, 8-bit")
+
+
 WORKLOADS = {"q4_0-gemv": workload_q4_0_gemv, "nbits-gemm": workload_nbits_gemm,
+             "q6_k-head": workload_q6_k_head, "q8-gemv": workload_q8_gemv,
              "qwen2-decode": workload_qwen2_decode, "lfm2-verify": workload_lfm2_verify,
              "llama8b-prefill": workload_llama8b_prefill}
 

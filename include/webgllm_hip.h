@@ -42,7 +42,8 @@ const char *wg_version(void);
 
 /* Launch-shape knobs, as the reference's TUNING table (src/engine.ts:147-625):
  * "gemv_wg_per_cu", "gemv_wg_per_cu_wide" (matrices of 16384+ row groups),
- * "q4k_wg_per_cu" (persistent GEMV workgroups per compute unit) and
+ * "q4k_wg_per_cu", "wide_wg_per_cu" (8-bit and Q6_K matrices: persistent
+ * GEMV workgroups per compute unit) and
  * "gemv_min_waves" (below this many waves a GEMV splits K inside a
  * workgroup), "decode_wg_per_cu" (persistent decode workgroups per
  * compute unit, read at plan creation) and "gemm_tile" (prefill GEMM tile:

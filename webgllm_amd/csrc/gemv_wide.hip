@@ -363,8 +363,7 @@ template <class F, int M, int NB, int KS>
 int launch_stream(const Mat &mat, int G, const uint16_t *x, int ldx, float *y, int ldy,
                   const wg_epilogue &e, hipStream_t s) {
   constexpr int RGW = 4 / KS;
-  int grid = persistent_grid((G + RGW - 1) / RGW,
-                             tuning(G >= 16384 ? "gemv_wg_per_cu_wide" : "gemv_wg_per_cu"));
+  int grid = persistent_grid((G + RGW - 1) / RGW, tuning("wide_wg_per_cu"));
   if (e.mode == WG_EPI_SWIGLU)
     gemv_wide_stream_kernel<F, M, NB, KS, WG_EPI_SWIGLU><<<grid, 256, 0, s>>>(mat, x, ldx, y, ldy,
                                                                              e, G);

@@ -67,6 +67,7 @@ static Knob g_knobs[] = {
     {"gemv_wg_per_cu", 2, 1, 16},        // persistent row-group GEMV workgroups per CU
     {"gemv_wg_per_cu_wide", 8, 1, 16},   // the same for matrices of 16384+ row groups
     {"q4k_wg_per_cu", 2, 1, 16},         // persistent Q4_K GEMV workgroups per CU
+    {"wide_wg_per_cu", 2, 1, 16},        // the same for 8-bit and Q6_K GEMVs
     {"gemv_min_waves", 8192, 0, 1 << 20},  // split K within a workgroup below this
     {"decode_wg_per_cu", 1, 1, 4},       // persistent decode workgroups (8 waves) per CU
     {"attn_prefill_mfma", 4, 0, 4},      // prompt attention: MFMA waves a workgroup (1, 2, 4), 0 VALU

@@ -95,6 +95,9 @@ def load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"{LIB_PATH} is missing: build it first (python -c "
                           "'import __graft_entry__ as g; g.build()')")
+    # torch brings its own HIP runtime; loaded first, it is the one the
+    # library binds to (two runtimes in one process do not share devices).
+    import torch  # noqa: F401
     lib = C.CDLL(LIB_PATH)
     P, I32, I64, SZ = C.c_void_p, C.c_int32, C.c_int64, C.c_size_t
     sig = {
