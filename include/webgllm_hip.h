@@ -191,6 +191,57 @@ int wg_quantize_q8(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const fl
 int wg_repack_q6_k(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *src,
                    const int32_t *src_rows, void *stream);
 
+/* ---------------------------------------------------- GGUF files
+ * readGgufHeader (src/gguf.ts:276-328) over a read-only memory map of the
+ * file: metadata and tensor infos; the tensor bytes stay in the map (copy
+ * them to the device and repack them there). Values and names point into
+ * the reader and live until wg_gguf_close. */
+typedef struct wg_gguf wg_gguf;
+
+typedef struct {
+  const char *name;    /* NUL-terminated */
+  int32_t n_dims;
+  int64_t dims[4];     /* ggml order: dims[0] is the contiguous one */
+  int32_t type;        /* a ggml type (src/gguf.ts:27-48) */
+  uint64_t offset;     /* absolute file offset of the data */
+  uint64_t bytes;      /* data bytes; 0 for a type the reader does not know */
+  const void *data;    /* the mapped bytes, or NULL with bytes == 0 */
+} wg_gguf_tensor_info;
+
+typedef struct {
+  const char *key;     /* NUL-terminated */
+  int32_t type;        /* a GGUF value type (src/gguf.ts:9-23): 8 string, 9 array */
+  int32_t elem_type;   /* arrays: the elements' type */
+  uint64_t length;     /* arrays: elements; strings: bytes of s */
+  int64_t i;           /* integers and booleans (floats truncated) */
+  double f;            /* floats (integers converted) */
+  const char *s;       /* strings: `length` bytes, not NUL-terminated */
+  uint64_t offset;     /* file offset of the value (arrays: first element) */
+} wg_gguf_value;
+
+int wg_gguf_open(const char *path, wg_gguf **out);
+int wg_gguf_close(wg_gguf *g);
+int32_t wg_gguf_version(const wg_gguf *g);
+int64_t wg_gguf_data_offset(const wg_gguf *g);
+int64_t wg_gguf_tensor_count(const wg_gguf *g);
+int64_t wg_gguf_meta_count(const wg_gguf *g);
+/* Index of a tensor or key, or -1. */
+int64_t wg_gguf_find_tensor(const wg_gguf *g, const char *name);
+int64_t wg_gguf_find_meta(const wg_gguf *g, const char *key);
+int wg_gguf_tensor(const wg_gguf *g, int64_t i, wg_gguf_tensor_info *out);
+int wg_gguf_meta(const wg_gguf *g, int64_t i, wg_gguf_value *out);
+/* Element j of array key i (readGgufArray, src/gguf.ts:346-360). */
+int wg_gguf_meta_element(const wg_gguf *g, int64_t i, uint64_t j, wg_gguf_value *out);
+
+/* rowsToFloats (src/load-gguf.ts:557-580) on the GPU: `rows` rows of K
+ * weights of ggml type `type` (device bytes as the file has them) to
+ * float32, bit-exact to the reference's dequantizers: F32, F16, Q8_0
+ * (repack.ts:514-528), Q4_1 (:447-466), Q4_K (:474-511), Q5_K (:535-572)
+ * and Q6_K (:405-440); other types return WG_ERR_UNSUPPORTED. The loader
+ * feeds them to wg_quantize_q8 for tensors it keeps in 8 bits. */
+int wg_rows_to_floats(int32_t type, const void *src, int32_t rows, int32_t K, float *out,
+                      void *stream);
+
 /* matrixRow (src/repack.ts:865-891) on the GPU: rows [row0, row0 + rows)
  * dequantized to float32, bit-exact: fp32(d * (q - z)) with the difference
  * and product in doubles, as the reference computes them; 8-bit: fp32(d *

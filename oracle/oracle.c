@@ -562,6 +562,46 @@ int orc_pack_q6_k(uint8_t *quants, uint16_t *scales, int N, int K, int row0, con
   return 0;
 }
 
+/* src/repack.ts:447-466 (dequantize_row_q4_1 as the reference states it):
+ * blocks of 32 (fp16 d, fp16 m, 16 nibble bytes: weight j low, j + 16
+ * high), w = q d + m in doubles, stored as float32. */
+void orc_dequantize_q4_1(const uint8_t *src, int rows, int K, float *out) {
+  const float *half = htab();
+  size_t blocks = (size_t)rows * K / 32;
+  for (size_t b = 0; b < blocks; b++) {
+    const uint8_t *p = src + b * 20;
+    double d = half[rd16(p)], m = half[rd16(p + 2)];
+    for (int j = 0; j < 16; j++) {
+      out[b * 32 + j] = (float)((p[4 + j] & 15) * d + m);
+      out[b * 32 + j + 16] = (float)((p[4 + j] >> 4) * d + m);
+    }
+  }
+}
+
+/* src/repack.ts:535-572 (dequantize_row_q5_K as the reference states it):
+ * super-blocks of 256 (fp16 d, fp16 dmin, 12 scale/min bytes, qh[32],
+ * qs[128]); sub-block j: w = d sc (q + 16 (qh bit j)) - dmin m. */
+void orc_dequantize_q5_k(const uint8_t *src, int rows, int K, float *out) {
+  const float *half = htab();
+  size_t supers = (size_t)rows * K / 256;
+  for (size_t s = 0; s < supers; s++) {
+    const uint8_t *p = src + s * 176;
+    double d = half[rd16(p)], dmin = half[rd16(p + 2)];
+    const uint8_t *qh = p + 16;
+    float *y = out + s * 256;
+    for (int is = 0; is < 8; is += 2) {
+      const uint8_t *ql = p + 48 + is * 16;
+      int s1, m1, s2, m2;
+      scale_min_pair(p + 4, is, &s1, &m1, &s2, &m2);
+      double d1 = d * s1, min1 = dmin * m1, d2 = d * s2, min2 = dmin * m2;
+      for (int l = 0; l < 32; l++)
+        *y++ = (float)(d1 * ((ql[l] & 15) + ((qh[l] >> is) & 1 ? 16 : 0)) - min1);
+      for (int l = 0; l < 32; l++)
+        *y++ = (float)(d2 * ((ql[l] >> 4) + ((qh[l] >> (is + 1)) & 1 ? 16 : 0)) - min2);
+    }
+  }
+}
+
 /* src/repack.ts:514-528: out = d * int8, per 34-byte block. */
 void orc_dequantize_q8_0(const uint8_t *src, int rows, int K, float *out) {
   const float *half = htab();

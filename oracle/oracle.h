@@ -74,6 +74,8 @@ int orc_quantize_q8(uint8_t *quants, uint16_t *scales, int N, int K, int row0,
 int orc_pack_q6_k(uint8_t *quants, uint16_t *scales, int N, int K, int row0, const uint8_t *src,
                   size_t src_len, int rows, const int32_t *src_rows);  /* repack.ts:706-728 */
 void orc_dequantize_q8_0(const uint8_t *src, int rows, int K, float *out); /* repack.ts:514-528 */
+void orc_dequantize_q4_1(const uint8_t *src, int rows, int K, float *out); /* repack.ts:447-466 */
+void orc_dequantize_q5_k(const uint8_t *src, int rows, int K, float *out); /* repack.ts:535-572 */
 void orc_dequantize_q6_k(const uint8_t *src, int rows, int K, float *out); /* repack.ts:405-440 */
 void orc_q8_row(const uint8_t *quants, const uint16_t *scales, int K, int n, float *out);
                                                                    /* repack.ts:873-876 */

@@ -62,6 +62,8 @@ _lib.orc_quantize_q8.argtypes = [_P, _P, _I, _I, _I, _P, _I]
 _lib.orc_pack_q6_k.argtypes = [_P, _P, _I, _I, _I, _P, C.c_size_t, _I, _P]
 _lib.orc_dequantize_q8_0.argtypes = [_P, _I, _I, _P]
 _lib.orc_dequantize_q6_k.argtypes = [_P, _I, _I, _P]
+_lib.orc_dequantize_q4_1.argtypes = [_P, _I, _I, _P]
+_lib.orc_dequantize_q5_k.argtypes = [_P, _I, _I, _P]
 _lib.orc_q8_row.argtypes = [_P, _P, _I, _I, _P]
 _lib.orc_q6k_row.argtypes = [_P, _P, _I, _I, _P]
 _lib.orc_matmul_q8.argtypes = [_P, _P, _I, _I, _P, _I, _P, _I, _I, _I]
@@ -207,6 +209,20 @@ def dequantize_q6_k(src: np.ndarray, rows: int, K: int) -> np.ndarray:
     src = np.ascontiguousarray(src, dtype=np.uint8)
     out = np.empty(rows * K, dtype=np.float32)
     _lib.orc_dequantize_q6_k(_ptr(src), rows, K, _ptr(out))
+    return out.reshape(rows, K)
+
+
+def dequantize_q4_1(src: np.ndarray, rows: int, K: int) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    out = np.empty(rows * K, dtype=np.float32)
+    _lib.orc_dequantize_q4_1(_ptr(src), rows, K, _ptr(out))
+    return out.reshape(rows, K)
+
+
+def dequantize_q5_k(src: np.ndarray, rows: int, K: int) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    out = np.empty(rows * K, dtype=np.float32)
+    _lib.orc_dequantize_q5_k(_ptr(src), rows, K, _ptr(out))
     return out.reshape(rows, K)
 
 

@@ -109,3 +109,34 @@ def encode_q6_k(q, sc, d_bits):
         out[s, 208] = int(d_bits[s]) & 255
         out[s, 209] = int(d_bits[s]) >> 8
     return out.reshape(-1)
+
+
+def encode_q5_k(q, sc, mn, d_bits, dmin_bits):
+    """GGUF Q5_K super-blocks from 5-bit codes q [supers, 256] (0..31), 6-bit
+    sub-block scales sc and mins mn [supers, 8] and half d, dmin bits: the
+    packing of ggml's quantize_row_q5_K (the scales and mins as Q4_K packs
+    them: sub-blocks 0..3 in the low 6 bits of bytes j and j + 4, 4..7 split
+    over the nibbles of bytes j + 8 and the top 2 bits of bytes j - 4 and j;
+    per 64 weights, ql[l] = q[l] & 15 | (q[l + 32] & 15) << 4 and bits 2j,
+    2j + 1 of qh[l] their fifth bits), 176 bytes each."""
+    q = np.asarray(q, dtype=np.int64)
+    supers = q.shape[0]
+    out = np.zeros((supers, 176), dtype=np.uint8)
+    for s in range(supers):
+        out[s, 0], out[s, 1] = int(d_bits[s]) & 255, int(d_bits[s]) >> 8
+        out[s, 2], out[s, 3] = int(dmin_bits[s]) & 255, int(dmin_bits[s]) >> 8
+        scales = out[s, 4:16]
+        for j in range(4):
+            scales[j] = (sc[s][j] & 63) | ((sc[s][j + 4] >> 4) << 6)
+            scales[j + 4] = (mn[s][j] & 63) | ((mn[s][j + 4] >> 4) << 6)
+            scales[j + 8] = (sc[s][j + 4] & 15) | ((mn[s][j + 4] & 15) << 4)
+        qh = np.zeros(32, np.int64)
+        ql = np.zeros(128, np.int64)
+        for pair in range(4):
+            lo, hi = q[s, 64 * pair:64 * pair + 32], q[s, 64 * pair + 32:64 * pair + 64]
+            ql[32 * pair:32 * pair + 32] = (lo & 15) | ((hi & 15) << 4)
+            qh |= ((lo >> 4) & 1) << (2 * pair)
+            qh |= ((hi >> 4) & 1) << (2 * pair + 1)
+        out[s, 16:48] = qh
+        out[s, 48:176] = ql
+    return out.reshape(-1)

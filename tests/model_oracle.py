@@ -140,10 +140,27 @@ class OracleModel:
         self.position += M
         return logits, picks
 
-    def forward(self, tokens):
-        logits = picks = None
-        for b0 in range(0, len(tokens), 8):
-            logits, picks = self.forward_rows(tokens[b0:b0 + 8])
+    # the quantized matrices of a layer (the rest are vectors and conv taps)
+    MATRICES = ("qkv", "o", "gate_up", "down", "in_proj", "out_proj")
+
+    def forward(self, tokens, f16_weights=False):
+        """A prompt, 8 rows a batch; returns the last batch's (logits, picks).
+        With f16_weights the layers' matmuls use the dequantized weights
+        rounded to halves, as the reference's prompt plan computes them
+        (dequant to an f16 texture, then matmulF16: src/gpu/kernels.ts:
+        436-735, Engine.f16Plan, src/engine.ts:980-995); the head keeps
+        exact weights. The engine takes that path for prompts longer than a
+        verify batch when every layer matrix is a 4-bit row-group one."""
+        layers = self.layers
+        if f16_weights:
+            self.layers = [{k: (h16(v).astype(np.float64) if k in self.MATRICES else v)
+                            for k, v in lw.items()} for lw in layers]
+        try:
+            logits = picks = None
+            for b0 in range(0, len(tokens), 8):
+                logits, picks = self.forward_rows(tokens[b0:b0 + 8])
+        finally:
+            self.layers = layers
         return logits, picks
 
     def decode(self, first, steps):

@@ -49,7 +49,7 @@ def test_prompt_logits_and_greedy_decode(hip, family):
     rng = np.random.default_rng(1)
     prompt = _prompt(rng, 21, eng.shape.vocab)
     picks = eng.forward(prompt).cpu().numpy()
-    logits_o, picks_o = orc.forward(prompt)
+    logits_o, picks_o = orc.forward(prompt, f16_weights=eng._prefill_ok())
     got = eng.logits[:len(prompt) % 8 or 8].cpu().numpy()
     assert rel_l2(got, logits_o) <= 1e-3
     assert list(picks) == list(picks_o)
@@ -139,7 +139,7 @@ def test_full_width_shapes(hip, name, layers):
     rng = np.random.default_rng(2)
     prompt = _prompt(rng, 12, shape.vocab)
     picks = eng.forward(prompt).cpu().numpy()
-    logits_o, picks_o = orc.forward(prompt)
+    logits_o, picks_o = orc.forward(prompt, f16_weights=eng._prefill_ok())
     got = eng.logits[:4].cpu().numpy()
     assert rel_l2(got, logits_o) <= 1e-3
     assert list(picks) == list(picks_o)
@@ -234,7 +234,7 @@ def test_long_prompt_through_gemm_batches(hip, family, monkeypatch):
     prompt = _prompt(rng, 600, eng.shape.vocab)
     assert E.PREFILL_ROWS < 592
     picks = eng.forward(prompt).cpu().numpy()
-    logits_o, picks_o = orc.forward(prompt)
+    logits_o, picks_o = orc.forward(prompt, f16_weights=eng._prefill_ok())
     assert rel_l2(eng.logits[:8].cpu().numpy(), logits_o) <= 1e-3
     assert list(picks) == list(picks_o)
     first = int(picks[-1])

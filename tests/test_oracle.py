@@ -599,3 +599,40 @@ def test_wide_matmul_block_form_matches_f64(bits):
     got = m.matmul(x16)
     want = O.halves_to_f32(x16).astype(np.float64) @ m.dense().astype(np.float64).T
     assert np.max(np.abs(got - want)) <= 1e-5 * np.abs(want).max()
+
+
+def test_q4_1_dequant_closed_form():
+    """dequantizeQ4_1 (src/repack.ts:447-466): w = q d + m, weight j in byte
+    j's low nibble and j + 16 in its high one."""
+    b = np.zeros(40, np.uint8)
+    for p, d, m in ((0, 0.5, -2.0), (20, 0.25, 1.5)):
+        hd, hm = O.to_half(d), O.to_half(m)
+        b[p:p + 4] = [hd & 255, hd >> 8, hm & 255, hm >> 8]
+        b[p + 4:p + 20] = [(j & 15) | ((15 - j) << 4) for j in range(16)]
+    out = O.dequantize_q4_1(b, 1, 64)[0]
+    j = np.arange(16)
+    assert np.array_equal(out[:16], j * 0.5 - 2.0)
+    assert np.array_equal(out[16:32], (15 - j) * 0.5 - 2.0)
+    assert np.array_equal(out[32:48], j * 0.25 + 1.5)
+    assert np.array_equal(out[48:64], (15 - j) * 0.25 + 1.5)
+
+
+def test_q5_k_decode_inverts_ggml_packing():
+    """Codes, 6-bit scales and mins packed by ggml's Q5_K packing (an
+    encoder independent of the decoder) come back as d sc q - dmin m at
+    every position; the Q4_K decode of the same scale bytes agrees."""
+    from tests.helpers import encode_q5_k
+    rng = np.random.default_rng(11)
+    supers = 5
+    q = rng.integers(0, 32, (supers, 256))
+    q[0] = np.arange(256) % 32
+    sc = rng.integers(0, 64, (supers, 8))
+    mn = rng.integers(0, 64, (supers, 8))
+    sc[1] = [63, 0, 1, 62, 32, 31, 17, 48]
+    d = [O.to_half(v) for v in rng.uniform(1e-3, 1e-2, supers)]
+    dm = [O.to_half(v) for v in rng.uniform(1e-3, 1e-2, supers)]
+    got = O.dequantize_q5_k(encode_q5_k(q, sc, mn, d, dm), 1, supers * 256).reshape(supers, 256)
+    dd = np.array([O.from_half(h) for h in d], np.float64)[:, None]
+    dmm = np.array([O.from_half(h) for h in dm], np.float64)[:, None]
+    want = (dd * np.repeat(sc, 32, axis=1) * q - dmm * np.repeat(mn, 32, axis=1))
+    assert np.array_equal(got, want.astype(np.float32))

@@ -5,12 +5,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/webgllm_hip.h"
+#include "status.h"
 
 namespace wg {
 
-// Records the message for wg_last_error() and returns `code`.
-int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 // After a launch: WG_OK, or WG_ERR_DEVICE with HIP's message.
 int launched(const char *what);
 
@@ -21,10 +19,6 @@ int launched(const char *what);
       return ::wg::fail(WG_ERR_DEVICE, "%s: %s", #expr, hipGetErrorString(e_));        \
   } while (0)
 
-#define WG_REQUIRE(cond, ...)                                                          \
-  do {                                                                                 \
-    if (!(cond)) return ::wg::fail(WG_ERR_INVALID, __VA_ARGS__);                       \
-  } while (0)
 
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -295,6 +295,57 @@ __global__ void dequant_q6k_kernel(const uint8_t *quants, const uint16_t *scales
                 out + (int64_t)i * supers * 256 + s * 256 + j * 32);
 }
 
+// rowsToFloats (src/load-gguf.ts:557-580): thread = one 32-weight piece of
+// one row (`pieces` a row). Each format as the reference's dequantizer
+// computes it: the arithmetic in doubles, each weight rounded once to float.
+constexpr int GGML_F32 = 0, GGML_F16 = 1, GGML_Q4_1 = 3, GGML_Q8_0 = 8, GGML_Q4_K = 12,
+              GGML_Q5_K = 13, GGML_Q6_K = 14;
+
+__global__ void rows_to_floats_kernel(int type, const uint8_t *src, int64_t pieces_total,
+                                      float *out) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= pieces_total) return;
+  float *o = out + t * 32;
+  if (type == GGML_F32) {  // thread = one value
+    out[t] = __builtin_bit_cast(float, ld32_unaligned(src + t * 4));
+  } else if (type == GGML_F16) {
+    out[t] = half_to_float(ld16_unaligned(src + t * 2));
+  } else if (type == GGML_Q8_0) {  // dequantizeQ8_0 (src/repack.ts:514-528)
+    const uint8_t *p = src + t * 34;
+    double d = half_to_float(ld16_unaligned(p));
+    for (int j = 0; j < 32; j++) o[j] = (float)(d * (int8_t)p[2 + j]);
+  } else if (type == GGML_Q4_1) {  // dequantizeQ4_1 (src/repack.ts:447-466)
+    const uint8_t *p = src + t * 20;
+    double d = half_to_float(ld16_unaligned(p)), m = half_to_float(ld16_unaligned(p + 2));
+    for (int j = 0; j < 16; j++) {
+      o[j] = (float)((p[4 + j] & 15) * d + m);
+      o[j + 16] = (float)((p[4 + j] >> 4) * d + m);
+    }
+  } else if (type == GGML_Q4_K || type == GGML_Q5_K) {
+    // dequantizeQ4_K / dequantizeQ5_K (src/repack.ts:474-511, :535-572):
+    // sub-block j = 2 is + hi of a super-block, d * sc * q - dmin * m.
+    const int64_t s = t >> 3;
+    const int j = (int)(t & 7);
+    const bool five = type == GGML_Q5_K;
+    const uint8_t *p = src + s * (five ? 176 : 144);
+    double d = half_to_float(ld16_unaligned(p)), dmin = half_to_float(ld16_unaligned(p + 2));
+    int sc, mn;
+    q4k_scale_min(p + 4, j, &sc, &mn);
+    const double d1 = d * sc, min1 = dmin * mn;
+    const uint8_t *q = p + (five ? 48 : 16) + (j >> 1) * 32;
+    const int shift = (j & 1) * 4;
+    for (int l = 0; l < 32; l++) {
+      int v = (q[l] >> shift) & 15;
+      if (five && (p[16 + l] & (1 << j))) v += 16;
+      o[l] = (float)(d1 * v - min1);
+    }
+  } else {  // GGML_Q6_K (src/repack.ts:405-440)
+    const int64_t s = t >> 3;
+    const uint8_t *p = src + s * 210;
+    dequant32_q6k(p, half_to_float(ld16_unaligned(p + 208)), (int)(t & 7), o);
+  }
+}
+
 inline unsigned grid_for(int64_t threads, int per) { return (unsigned)((threads + per - 1) / per); }
 
 }  // namespace
@@ -424,6 +475,29 @@ int wg_repack_q6_k(const wg_q4_matrix *m, int32_t row0, int32_t rows, const void
       (uint8_t *)m->quants, (uint16_t *)m->scales, (const uint8_t *)src, src_rows, row0, rows,
       supers);
   return launched("wg_repack_q6_k");
+}
+
+int wg_rows_to_floats(int32_t type, const void *src, int32_t rows, int32_t K, float *out,
+                      void *stream) {
+  WG_REQUIRE(src && out && rows >= 0 && K > 0, "wg_rows_to_floats: bad arguments");
+  int unit;
+  switch (type) {
+    case GGML_F32: case GGML_F16: unit = 1; break;
+    case GGML_Q4_1: case GGML_Q8_0: unit = 32; break;
+    case GGML_Q4_K: case GGML_Q5_K: case GGML_Q6_K: unit = 256; break;
+    default:
+      return fail(WG_ERR_UNSUPPORTED,
+                  "wg_rows_to_floats: ggml type %d (F32, F16, Q4_1, Q4_K, Q5_K, Q6_K and Q8_0 "
+                  "convert)", type);
+  }
+  WG_REQUIRE(K % unit == 0, "wg_rows_to_floats: a row of %d weights is not whole blocks of %d",
+             K, unit);
+  if (!rows) return WG_OK;
+  // a thread per value (F32, F16) or per 32-weight piece
+  const int64_t total = (int64_t)rows * (unit == 1 ? K : K / 32);
+  rows_to_floats_kernel<<<grid_for(total, 256), 256, 0, as_stream(stream)>>>(
+      type, (const uint8_t *)src, total, out);
+  return launched("wg_rows_to_floats");
 }
 
 int wg_q4_dequant(const wg_q4_matrix *m, int32_t row0, int32_t rows, float *out, void *stream) {

@@ -71,6 +71,20 @@ class AttnShape(C.Structure):
                 ("rotated_dims", C.c_int32), ("eps", C.c_float), ("use_norm", C.c_int32)]
 
 
+class GgufTensorInfo(C.Structure):
+    """wg_gguf_tensor_info."""
+    _fields_ = [("name", C.c_char_p), ("n_dims", C.c_int32), ("dims", C.c_int64 * 4),
+                ("type", C.c_int32), ("offset", C.c_uint64), ("bytes", C.c_uint64),
+                ("data", C.c_void_p)]
+
+
+class GgufValue(C.Structure):
+    """wg_gguf_value."""
+    _fields_ = [("key", C.c_char_p), ("type", C.c_int32), ("elem_type", C.c_int32),
+                ("length", C.c_uint64), ("i", C.c_int64), ("f", C.c_double),
+                ("s", C.c_void_p), ("offset", C.c_uint64)]
+
+
 class Limits(C.Structure):
     _fields_ = [("device", C.c_int32), ("compute_units", C.c_int32),
                 ("global_bytes", C.c_int64), ("max_alloc_bytes", C.c_int64),
@@ -153,6 +167,18 @@ def load():
         "wg_argmax_scratch_bytes": (SZ, [I32, I32]),
         "wg_argmax_rows": (C.c_int, [P, I32, I32, I32, P, P, P, SZ, P]),
         "wg_argmax_advance": (C.c_int, [P, I32, P, P, P, I32, P, P, SZ, P]),
+        "wg_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+        "wg_gguf_close": (C.c_int, [P]),
+        "wg_gguf_version": (I32, [P]),
+        "wg_gguf_data_offset": (I64, [P]),
+        "wg_gguf_tensor_count": (I64, [P]),
+        "wg_gguf_meta_count": (I64, [P]),
+        "wg_gguf_find_tensor": (I64, [P, C.c_char_p]),
+        "wg_gguf_find_meta": (I64, [P, C.c_char_p]),
+        "wg_gguf_tensor": (C.c_int, [P, I64, C.POINTER(GgufTensorInfo)]),
+        "wg_gguf_meta": (C.c_int, [P, I64, C.POINTER(GgufValue)]),
+        "wg_gguf_meta_element": (C.c_int, [P, I64, C.c_uint64, C.POINTER(GgufValue)]),
+        "wg_rows_to_floats": (C.c_int, [I32, P, I32, I32, P, P]),
         "wg_decode_plan_create": (C.c_int, [C.POINTER(DecodeLayer), I32, C.POINTER(P)]),
         "wg_decode_run": (C.c_int, [P, P]),
         "wg_decode_status": (C.c_int, [P]),
