@@ -548,7 +548,108 @@ def workload_q8_gemv(args):
     return workload_wide_gemv(args, "q8", 28672, 4096, 8, "Llama-3-8B gate|up, 8-bit")
 
 
+def workload_gguf_load(args):
+    """Loading an LFM2-1.2B-shape GGUF (16 layers, 10 of them short conv;
+    Q4_0 layer matrices and a Q6_K embedding as Liquid AI's files have them)
+    from a file into the engine's device layout: read through the library's
+    memory-mapped reader, copied over, repacked on the GPU. GB/s of file
+    bytes, best of a few loads of the page-cached file."""
+    import tempfile
+    import numpy as np
+    import torch
+    from tests import gguf_writer as W
+    from webgllm_amd import load_gguf as LG, ops
+    D, layers, heads, kv, hd, F, V = 2048, 16, 32, 8, 64, 8192, 65536
+    conv = (0, 1, 3, 4, 6, 7, 9, 11, 13, 15)
+    rng = np.random.default_rng(0)
+
+    def q4_0(rows, K):
+        b = rng.integers(0, 256, (rows * K // 32, 18), dtype=np.uint8)
+        h = rng.uniform(0.002, 0.006, b.shape[0]).astype(np.float16).view(np.uint16)
+        b[:, 0], b[:, 1] = h & 255, h >> 8
+        return b
+
+    tensors = []
+    for i in range(layers):
+        p = f"blk.{i}."
+        for n in ("attn_norm", "ffn_norm"):
+            tensors.append((p + n + ".weight", (D,), 0, np.ones(D, np.float32)))
+        if i in conv:
+            tensors += [(p + "shortconv.in_proj.weight", (D, 3 * D), 2, q4_0(3 * D, D)),
+                        (p + "shortconv.out_proj.weight", (D, D), 2, q4_0(D, D)),
+                        (p + "shortconv.conv.weight", (3, D), 0,
+                         rng.standard_normal(3 * D).astype(np.float32))]
+        else:
+            tensors += [(p + "attn_q.weight", (D, heads * hd), 2, q4_0(heads * hd, D)),
+                        (p + "attn_k.weight", (D, kv * hd), 2, q4_0(kv * hd, D)),
+                        (p + "attn_v.weight", (D, kv * hd), 2, q4_0(kv * hd, D)),
+                        (p + "attn_output.weight", (heads * hd, D), 2, q4_0(D, heads * hd)),
+                        (p + "attn_q_norm.weight", (hd,), 0, np.ones(hd, np.float32)),
+                        (p + "attn_k_norm.weight", (hd,), 0, np.ones(hd, np.float32))]
+        tensors += [(p + "ffn_gate.weight", (D, F), 2, q4_0(F, D)),
+                    (p + "ffn_up.weight", (D, F), 2, q4_0(F, D)),
+                    (p + "ffn_down.weight", (F, D), 2, q4_0(D, F))]
+    tensors.append(("token_embd_norm.weight", (D,), 0, np.ones(D, np.float32)))
+    emb = rng.integers(0, 256, (V * D // 256, 210), dtype=np.uint8)
+    h = rng.uniform(1e-5, 2e-5, emb.shape[0]).astype(np.float16).view(np.uint16)
+    emb[:, 208], emb[:, 209] = h & 255, h >> 8
+    tensors.append(("token_embd.weight", (D, V), 14, emb))
+    kvs = [0 if i in conv else kv for i in range(layers)]
+    meta = [("general.architecture", W.STRING, "lfm2"), ("lfm2.block_count", W.U32, layers),
+            ("lfm2.embedding_length", W.U32, D), ("lfm2.attention.head_count", W.U32, heads),
+            ("lfm2.attention.head_count_kv", W.ARRAY, (W.I32, kvs)),
+            ("lfm2.feed_forward_length", W.U32, F), ("lfm2.rope.freq_base", W.F32, 1e6),
+            ("lfm2.attention.layer_norm_rms_epsilon", W.F32, 1e-5),
+            ("lfm2.shortconv.l_cache", W.U32, 3)]
+    path = os.path.join(tempfile.mkdtemp(), "lfm2-1.2b-shape-q4_0.gguf")
+    W.write_gguf(path, meta, tensors)
+    size = os.path.getsize(path)
+    del tensors
+    times = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.time()
+        w = LG.load_gguf(path)
+        torch.cuda.synchronize()
+        times.append(time.time() - t0)
+        del w
+    best = min(times)
+    gbps = size / best / 1e9
+    # the dominant kernel: packQ4_0 of one gate|up-sized matrix, HIP events
+    src = torch.from_numpy(q4_0(2 * F, D).reshape(-1)).cuda()
+    m = ops.Q4Matrix(2 * F, D)
+    m.repack_q4_0(0, 2 * F, src)
+    ms = timed(lambda: m.repack_q4_0(0, 2 * F, src), 20)
+    kbytes = 2 * src.numel()  # block bytes read, the same written
+    kgbps = kbytes / (ms * 1e-3) / 1e9
+    roof = {"bound": "hbm", "achieved": round(kgbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(kgbps / HBM_PEAK_GBPS, 4), "traffic": None,
+            "kernel": f"repack_q4_0_kernel {2 * F}x{D} (packQ4_0: 18-byte blocks read, "
+                      f"written as 16-byte rows + half scales)",
+            "bytes_per_launch": kbytes, "avg_launch_us": round(ms * 1e3, 2), "launches": 20}
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        blocks = q4_0(2 * F, D).reshape(-1)
+        qm = O.QuantMatrix(2 * F, D)
+        spent, n = 0.0, 0
+        while spent < 5.0 or n < 2:
+            t0 = O.now()
+            O.pack_q4_0(qm, 0, blocks, 2 * F)
+            spent += O.now() - t0
+            n += 1
+        cpu = {"value": round(blocks.size / (spent / n) / 1e9, 3), "unit": "GB/s", "cores": 1,
+               "kind": "port", "sample": f"oracle packQ4_0 (one thread) of one {2 * F}x{D} "
+                                         f"matrix, {n} repetitions ({spent:.1f} s)"}
+    cfg = {"workload": f"LFM2-1.2B-shape GGUF ({size / 1e9:.2f} GB: Q4_0 layer matrices, "
+                       f"Q6_K embedding) loaded into the device layout, page-cached file",
+           "loads_s": [round(t, 3) for t in times], "parallelism": "none"}
+    return line("GGUF load GB/s (file bytes into the device layout)", round(gbps, 2), "GB/s",
+                3, 0, best * 1e3, cfg, roof, cpu, dtype="u8")
+
+
 WORKLOADS = {"q4_0-gemv": workload_q4_0_gemv, "nbits-gemm": workload_nbits_gemm,
+             "gguf-load": workload_gguf_load,
              "q6_k-head": workload_q6_k_head, "q8-gemv": workload_q8_gemv,
              "qwen2-decode": workload_qwen2_decode, "lfm2-verify": workload_lfm2_verify,
              "llama8b-prefill": workload_llama8b_prefill}
