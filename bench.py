@@ -252,14 +252,15 @@ def workload_q4_0_gemv(args):
                 hot_GBps=round(algo / (hot * 1e-6) / 1e9, 1))
 
 
-def workload_nbits_gemm(args):
+def workload_nbits_gemm(args, fmt="nbits"):
     """Prefill GEMM on MFMA: A half [512 x 4096] times MatMulNBits weights
     (4-bit, half scales, u8 zero points, block 32) at N = 4096 and 14336,
-    float32 output."""
+    float32 output. With fmt "q8": 8-bit matrices (floats requantized as
+    the GGUF loader does) on the same kernel."""
     import torch
     from webgllm_amd import engine as E, ops
     M, K = 512, 4096
-    shape = E.ModelShape("nbits-gemm", K, 1, 1, 1, 4, 4, 4, "nbits")
+    shape = E.ModelShape(f"{fmt}-gemm", K, 1, 1, 1, 4, 4, 4, fmt)
     w = E.Weights.blank(shape, seed=0)
     a = torch.randn((M, K), device="cuda", generator=torch.Generator(device="cuda")
                     .manual_seed(2)).half()
@@ -278,22 +279,45 @@ def workload_nbits_gemm(args):
     tot_ms = sum(r[0] for r in res.values())
     tflops = tot_flop / (tot_ms * 1e-3) / 1e12
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and fmt == "nbits":
         threads = min(os.cpu_count() or 1, 16)
         t, desc = cpu_step_time([("4096x4096", res[4096][2], 1),
                                  ("14336x4096", res[14336][2], 1)], 8, threads, 10.0)
         cpu = {"value": round(tot_flop / 64 / t / 1e12, 5), "unit": "TFLOP/s",
                "cores": threads, "kind": "port",
                "sample": desc + " (8 of the 512 rows; the rate scales with rows)"}
+    elif not args.no_cpu:
+        import numpy as np
+        from oracle import oracle as O
+        from webgllm_amd import lib as L
+        threads = min(os.cpu_count() or 1, 16)
+        m = res[14336][2]
+        wm = O.WideMatrix(m.N, m.K, 8)
+        wm.quants[:] = m.quants.cpu().numpy()
+        wm.scales[:] = m.scales.cpu().numpy().view(np.uint16)
+        x16 = O.f32_to_h2(np.random.default_rng(0).standard_normal((8, K)).astype(np.float32))
+        spent, n = 0.0, 0
+        while spent < 10.0 or n < 2:
+            t0 = O.now()
+            wm.matmul(x16, threads)
+            spent += O.now() - t0
+            n += 1
+        cpu = {"value": round(2.0 * 8 * m.N * K / (spent / n) / 1e12, 5), "unit": "TFLOP/s",
+               "cores": threads, "kind": "port",
+               "sample": f"oracle float32 8-bit block form (OpenMP, {threads} threads), 8 rows x "
+                         f"the 14336x4096 matrix, {n} repetitions ({spent:.1f} s)"}
     roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
             "frac": round(tflops / 2500.0, 4), "traffic": None,
             "kernel": "gemm_q4_kernel (v_mfma_f32_32x32x16_f16, dequant in registers)",
             "flops_per_launch": {str(N): 2 * M * N * K for N in res},
             "avg_launch_us": {str(N): round(r[0] * 1e3, 2) for N, r in res.items()}}
-    cfg = {"workload": "MatMulNBits prefill GEMM, M=512, K=4096, N in {4096, 14336}",
-           "weights": "random MatMulNBits q4 rows (u8 zero points) repacked on the GPU",
+    what = "MatMulNBits q4" if fmt == "nbits" else "8-bit"
+    cfg = {"workload": f"{what} prefill GEMM, M=512, K=4096, N in {{4096, 14336}}",
+           "weights": "random MatMulNBits q4 rows (u8 zero points) repacked on the GPU"
+                      if fmt == "nbits" else "random floats requantized to 8 bits on the GPU "
+                                             "(quantizeQ8)",
            "global_batch": M, "parallelism": "none"}
-    return line("prefill GEMM TFLOP/s (MatMulNBits q4, M=512)", round(tflops, 1), "TFLOP/s",
+    return line(f"prefill GEMM TFLOP/s ({what}, M=512)", round(tflops, 1), "TFLOP/s",
                 args.steps, 4, tot_ms, cfg, roof, cpu, dtype="f16 x f16 -> f32",
                 per_shape_tflops={str(N): round(r[1], 1) for N, r in res.items()})
 
@@ -650,6 +674,7 @@ def workload_gguf_load(args):
 
 WORKLOADS = {"q4_0-gemv": workload_q4_0_gemv, "nbits-gemm": workload_nbits_gemm,
              "gguf-load": workload_gguf_load,
+             "q8-gemm": lambda args: workload_nbits_gemm(args, "q8"),
              "q6_k-head": workload_q6_k_head, "q8-gemv": workload_q8_gemv,
              "qwen2-decode": workload_qwen2_decode, "lfm2-verify": workload_lfm2_verify,
              "llama8b-prefill": workload_llama8b_prefill}

@@ -318,10 +318,11 @@ int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx,
 /* Prefill GEMM (Engine.matmul -> matmulQuad, or dequant + matmulF16,
  * kernels.ts:370-429, :436-735; Engine.f16Plan, engine.ts:980-995):
  * C[m][n] = (residual ? residual[m][n] : 0) + sum_k A[m][k] W[n][k] for M
- * tokens of half activations A ([M][lda], 16-byte aligned) and a row-group
- * matrix (N and K multiples of 64); float32 C [M][ldc]. Weights are
- * dequantized in registers to halves, d (q - z) rounded once as dequantOut
- * does (kernels.ts:436-597), and multiplied on MFMA (v_mfma_f32_32x32x16_f16)
+ * tokens of half activations A ([M][lda], 16-byte aligned) and a 4-bit
+ * row-group or an 8-bit matrix (N and K multiples of 64); float32 C
+ * [M][ldc]. Weights are dequantized in registers to halves, d (q - z) (or d
+ * q) rounded once as dequantOut does (kernels.ts:436-597), and multiplied
+ * on MFMA (v_mfma_f32_32x32x16_f16)
  * with float32 accumulation. residual may equal C. row_scale (or NULL)
  * multiplies row m's sums before the residual is added (a prescaled norm's
  * 32 / RMS, see wg_norm_to_h2). col_of (or NULL for n -> n) maps the

@@ -150,7 +150,7 @@ class OracleModel:
         (dequant to an f16 texture, then matmulF16: src/gpu/kernels.ts:
         436-735, Engine.f16Plan, src/engine.ts:980-995); the head keeps
         exact weights. The engine takes that path for prompts longer than a
-        verify batch when every layer matrix is a 4-bit row-group one."""
+        verify batch when every layer matrix is a 4- or 8-bit row-group one."""
         layers = self.layers
         if f16_weights:
             self.layers = [{k: (h16(v).astype(np.float64) if k in self.MATRICES else v)

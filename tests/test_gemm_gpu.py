@@ -58,7 +58,7 @@ def test_c2_matmulnbits_prefill(hip, N):
     assert e16 <= 1e-5
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup"])
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup", "q8_0", "q8"])
 @pytest.mark.parametrize("M,N,K", [(1, 64, 64), (37, 192, 128), (200, 512, 1024),
                                    (128, 1024, 2048)])
 def test_gemm_shapes_and_formats(hip, fmt, M, N, K):
@@ -82,13 +82,24 @@ def test_gemm_rejects(hip):
     m = _matrix("q4_0", 96, 64, seed=1)   # N not a multiple of 64
     with pytest.raises(L.WgError, match="multiple of 64"):
         ops.gemm(m, torch.zeros((4, 64), dtype=torch.float16, device="cuda"))
-    m2 = _matrix("q4_k", 64, 256, seed=1)
-    with pytest.raises(L.WgError, match="row-group"):
-        ops.gemm(m2, torch.zeros((4, 256), dtype=torch.float16, device="cuda"))
+    for fmt in ("q4_k", "q6_k"):
+        m2 = _matrix(fmt, 64, 256, seed=1)
+        with pytest.raises(L.WgError, match="row-group"):
+            ops.gemm(m2, torch.zeros((4, 256), dtype=torch.float16, device="cuda"))
+
+
+def test_gemm_8bit_c2_shape(hip):
+    """An 8-bit gate|up-sized matrix at 512 rows (the prompt batches of a
+    Q8_0 or requantized GGUF model): within float32 summation of the
+    half-rounded weights."""
+    m = _matrix("q8", 14336, 4096, seed=9)
+    e, e16 = _check(m, 512, seed=2)
+    assert e <= 1e-3
+    assert e16 <= 1e-5
 
 
 @pytest.mark.parametrize("tile", [1, 2, 3])
-@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup"])
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup", "q8_0"])
 def test_gemm_every_tile(hip, fmt, tile):
     """Each tile shape (64 x 128, 128 x 128, 128 x 256), forced through the
     gemm_tile knob, on ragged rows (M = 200 leaves a partial 128-row tile)."""

@@ -97,9 +97,38 @@ __device__ inline void dequant8(uint2 bytes, uint16_t scale_bits, float zero, ha
   }
 }
 
+// The weight form of a launch: the three zero-point kinds of 4-bit row
+// groups, or Q8 for WG_LAYOUT_Q8 (signed bytes, no zero point).
+constexpr int Q8 = 3;
+
+// 8 code bytes of one weight row for each K = 16 step of a block (weights
+// 8h.. and 16 + 8h..) -> the two operands as half(d q), rounded once:
+// q + 128 (one xor a dword) under a 0x64 exponent byte is the half 1024 +
+// q + 128, minus 1152 exact, then one multiply by d.
+__device__ inline void dequant8_q8(uint2 b0, uint2 b1, uint16_t scale_bits, half8 &lo,
+                                   half8 &hi) {
+  const _Float16 d = __builtin_bit_cast(_Float16, scale_bits);
+  const half2v off2 = {(_Float16)1152.0f, (_Float16)1152.0f}, d2 = {d, d};
+  const uint32_t k64 = 0x64646464u;
+  const uint32_t w[4] = {b0.x ^ 0x80808080u, b0.y ^ 0x80808080u, b1.x ^ 0x80808080u,
+                         b1.y ^ 0x80808080u};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    half2v p0 = (as_h2(__builtin_amdgcn_perm(k64, w[i], 0x04010400u)) - off2) * d2;
+    half2v p1 = (as_h2(__builtin_amdgcn_perm(k64, w[i], 0x04030402u)) - off2) * d2;
+    half8 &o = i < 2 ? lo : hi;
+    const int t = (i & 1) * 4;
+    o[t + 0] = p0.x;
+    o[t + 1] = p0.y;
+    o[t + 2] = p1.x;
+    o[t + 3] = p1.y;
+  }
+}
+
 template <int ZK, int BN>
 struct Stage {
-  static constexpr int WQ = BN * 32;  // raw nibbles: BN / 4 row groups x 128 bytes
+  // weights: BN / 4 row groups x 128 nibble bytes, or x 256 code bytes
+  static constexpr int WQ = ZK == Q8 ? BN * 64 : BN * 32;
   static constexpr int WS = BN * 4;   // scales: BN / 4 row groups x 8 halves
   static constexpr int WZ = ZK == WG_ZERO_F16 ? BN * 4 : ZK == WG_ZERO_U8 ? BN * 2 : 0;
 };
@@ -134,7 +163,9 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
   constexpr int STAGE = A_BYTES + WQ + WS + WZ;
   constexpr int IA = BM * 128 / 1024 / NWV;  // A loads (1 KB each) a wave issues a stage
   static_assert(IA >= 1 && IA * NWV * 1024 == A_BYTES, "A tile splits evenly over the waves");
-  constexpr int QP = 2 * BN;  // nibble pieces (16 bytes) a stage
+  // weight pieces (16 bytes) a stage; RGP of them a row group
+  constexpr int RGP = ZK == Q8 ? 16 : 8, QP = BN / 4 * RGP;
+  constexpr int QSTEP = RGP * 16;  // weight bytes a row group moves a step
   constexpr int IQ = QP > 64 * NWV ? QP / (64 * NWV) : 1;  // nibble loads a wave issues
   constexpr int NW = IA + IQ + 1 + (ZK == WG_ZERO_U8 ? 1 : 0);  // loads a wave issues a stage
   extern __shared__ __align__(16) unsigned char smem[];
@@ -180,7 +211,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
   for (int i = 0; i < IQ; i++) {
     const int qq = (i * NWV + wave) * PWQ + lane;
-    off_q[i] = (uint32_t)(((int64_t)(g0 + (qq >> 3)) * B) * 64 + (qq & 7) * 16);
+    off_q[i] = (uint32_t)(((int64_t)(g0 + qq / RGP) * B) * (QSTEP / 2) + (qq % RGP) * 16);
   }
   const int qs = wave * PWS + lane;
   const bool s_is_zero = wave * PWS >= NSC;  // wave-uniform
@@ -198,7 +229,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int i = 0; i < IQ; i++)
       if (lane < PWQ)
-        dma16(quants + kt * 128, off_q[i],
+        dma16(quants + kt * QSTEP, off_q[i],
               __builtin_amdgcn_readfirstlane(base + A_BYTES + (i * NWV + wave) * PWQ * 16));
     if (lane < PWS)
       dma16(s_base + kt * 16, off_s,
@@ -238,7 +269,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
     const uint16_t *Ws = reinterpret_cast<const uint16_t *>(st + A_BYTES + WQ);
     // Every LDS read of the step first (weights, scales, zeros, A chunks),
     // so their latencies overlap; then the dequant and the MFMAs.
-    uint2 wbytes[2][NT];
+    uint2 wbytes[2][NT], wbytes2[2][NT];
     uint16_t wsc[2][NT];
     float wz[2][NT];
 #pragma unroll
@@ -247,10 +278,16 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
       for (int u = 0; u < NT; u++) {
         const int nl = wn * WN + u * 32 + (lane & 31);  // tile-local weight row
         const int rg = nl >> 2, r = nl & 3;
-        wbytes[j][u] =
-            *reinterpret_cast<const uint2 *>(Wq + rg * 128 + j * 64 + r * 16 + 8 * h);
+        if constexpr (ZK == Q8) {  // a block row is 32 code bytes, weight j in byte j
+          const unsigned char *row = Wq + rg * 256 + j * 128 + r * 32 + 8 * h;
+          wbytes[j][u] = *reinterpret_cast<const uint2 *>(row);
+          wbytes2[j][u] = *reinterpret_cast<const uint2 *>(row + 16);
+        } else {
+          wbytes[j][u] =
+              *reinterpret_cast<const uint2 *>(Wq + rg * 128 + j * 64 + r * 16 + 8 * h);
+        }
         wsc[j][u] = Ws[rg * 8 + j * 4 + r];
-        if constexpr (ZK == WG_ZERO_8) wz[j][u] = 8.0f;
+        if constexpr (ZK == WG_ZERO_8 || ZK == Q8) wz[j][u] = 8.0f;
         else if constexpr (ZK == WG_ZERO_U8)
           wz[j][u] = (float)(st + A_BYTES + WQ + WS)[rg * 8 + j * 4 + r];
         else
@@ -274,7 +311,10 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
     for (int j = 0; j < 2; j++) {  // the two blocks of the step
       half8 blo[NT], bhi[NT];
 #pragma unroll
-      for (int u = 0; u < NT; u++) dequant8<ZK>(wbytes[j][u], wsc[j][u], wz[j][u], blo[u], bhi[u]);
+      for (int u = 0; u < NT; u++) {
+        if constexpr (ZK == Q8) dequant8_q8(wbytes[j][u], wbytes2[j][u], wsc[j][u], blo[u], bhi[u]);
+        else dequant8<ZK>(wbytes[j][u], wsc[j][u], wz[j][u], blo[u], bhi[u]);
+      }
 #pragma unroll
       for (int step = 0; step < 2; step++)  // low nibbles: K 0..15, high: 16..31
 #pragma unroll
@@ -365,8 +405,8 @@ int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda,
                const int32_t *col_of, void *stream) {
   int rc = check_matrix(w, "wg_q4_gemm");
   if (rc) return rc;
-  WG_REQUIRE(w->layout == WG_LAYOUT_ROWGROUP,
-             "wg_q4_gemm: the prefill GEMM reads row-group matrices");
+  WG_REQUIRE(w->layout == WG_LAYOUT_ROWGROUP || w->layout == WG_LAYOUT_Q8,
+             "wg_q4_gemm: the prefill GEMM reads 4-bit and 8-bit row-group matrices");
   WG_REQUIRE(w->K % 64 == 0, "wg_q4_gemm: columns (%d) must be a multiple of 64", w->K);
   WG_REQUIRE(w->N % 64 == 0, "wg_q4_gemm: rows (%d) must be a multiple of 64", w->N);
   WG_REQUIRE(A && C && M >= 1, "wg_q4_gemm: bad arguments");
@@ -384,6 +424,8 @@ int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda,
                "wg_q4_gemm: residual overlaps the output");
   }
   hipStream_t s = as_stream(stream);
+  if (w->layout == WG_LAYOUT_Q8)
+    return launch<Q8>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
   switch (w->zero) {
     case WG_ZERO_8: return launch<WG_ZERO_8>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
     case WG_ZERO_U8: return launch<WG_ZERO_U8>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);

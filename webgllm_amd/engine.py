@@ -398,11 +398,12 @@ class Engine:
     # --- prompt batches on MFMA ----------------------------------------------
     def _prefill_ok(self) -> bool:
         """Whether prompt batches can run as GEMMs: every matrix of a layer in
-        the row-group layout with N and K multiples of 64."""
+        a row-group layout (4- or 8-bit) with N and K multiples of 64."""
         for lw in self.w.layers:
             for m in lw.values():
-                if isinstance(m, ops.Q4Matrix) and (m.layout != L.LAYOUT_ROWGROUP or
-                                                    m.N % 64 or m.K % 64):
+                if isinstance(m, ops.Q4Matrix) and (
+                        m.layout not in (L.LAYOUT_ROWGROUP, L.LAYOUT_Q8) or m.N % 64 or
+                        m.K % 64):
                     return False
         s = self.shape
         return s.head_dim in (64, 128)
