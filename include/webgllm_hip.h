@@ -333,6 +333,17 @@ int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda,
                int32_t ldc, const float *residual, int32_t ldr, const float *row_scale,
                const int32_t *col_of, void *stream);
 
+/* The gate|up GEMM with the SwiGLU folded into it, for prompt batches (the
+ * fused FFN passes of the reference's WebGPU kernels, src/gpu/native.ts:33,
+ * and REDUCE_SWIGLU, kernels.ts:1066-1077): the matrix's rows come in
+ * groups of 4 as (gate 2i, gate 2i + 1, up 2i, up 2i + 1), as for
+ * WG_EPI_SWIGLU; out16[m][i] = half(silu(g) * u) of the float32 sums
+ * (times row_scale[m] when given), N / 2 columns, no float32 product
+ * written. Equals wg_q4_gemm (with the matrix's column map) followed by
+ * wg_swiglu, bit for bit. */
+int wg_q4_gemm_swiglu(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda,
+                      uint16_t *out16, int32_t ldo, const float *row_scale, void *stream);
+
 /* float32 -> half activations, clamped to +-65504 (packH2, kernels.ts:32-36). */
 int wg_f32_to_f16(const float *x, uint16_t *out, int64_t n, void *stream);
 

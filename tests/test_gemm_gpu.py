@@ -3,6 +3,8 @@ dequantized weights in float64 (the north star's rel-L2 <= 1e-3 bar), and
 the weights rounded to halves the way the reference's dequantOut stores them
 (src/gpu/kernels.ts:436-597), which the GEMM must match to float32
 accumulation error."""
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -136,3 +138,37 @@ def test_gemm_column_map(hip):
     assert np.array_equal(got[:, perm[ok]], plain[:, ok])
     missing = np.setdiff1d(np.arange(N), perm[ok])
     assert (got[:, missing] == 123.0).all()
+
+
+@pytest.mark.parametrize("fmt,tile", [("q4_k_rowgroup", 0), ("q4_0", 1), ("nbits", 2),
+                                      ("q8_0", 3), ("q8", 0)])
+@pytest.mark.parametrize("M", [1, 77, 300])
+def test_gemm_swiglu_equals_gemm_then_swiglu(hip, fmt, tile, M):
+    """The fused gate|up GEMM + SwiGLU writes, bit for bit, what the GEMM
+    (through the matrix's column map) then wg_swiglu write, with a row
+    scale, on every tile shape and ragged row counts."""
+    from webgllm_amd import engine as E, lib as L, ops
+    F, K = 768, 1024
+    shape = E.ModelShape("t", K, 1, 1, 1, 4, 4, 4, fmt)
+    w = E.Weights.blank(shape, seed=M)
+    m = w.matrix(2 * F, K, E.gate_up_row_order(F))
+    rng = np.random.default_rng(M)
+    a = _t(O.f32_to_h2(rng.standard_normal((M, K)).astype(np.float32)).view(np.int16))
+    rs = _t(rng.uniform(0.5, 2.0, M).astype(np.float32))
+    col = _t(np.asarray(m.row_order, np.int32))
+    L.tuning_set("gemm_tile", tile)
+    try:
+        gu = ops.gemm(m, a, col_of=col, row_scale=rs)
+        want = ops.swiglu(gu).cpu().numpy().view(np.uint16)
+        got = ops.gemm_swiglu(m, a, row_scale=rs).cpu().numpy().view(np.uint16)
+    finally:
+        L.tuning_set("gemm_tile", 0)
+    assert np.array_equal(got, want)
+
+
+def test_gemm_swiglu_rejects(hip):
+    from webgllm_amd import lib as L
+    m = _matrix("q4_0", 128, 64, seed=1)
+    lib = L.load()
+    rc = lib.wg_q4_gemm_swiglu(C.byref(m.desc), 0x10000, 4, 64, 0x20000, 32, None, None)
+    assert rc == -1 and "N / 2" in L.last_error()

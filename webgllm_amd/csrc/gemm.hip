@@ -143,8 +143,17 @@ constexpr int gemm_waves_per_simd() {
   return w < 1 ? 1 : w > 8 ? 8 : w;
 }
 
-// BM x BN tiles, S stages of BK = 64, a WGM x WGN grid of waves.
-template <int ZK, int BM, int BN, int S, int WGM, int WGN>
+__device__ inline uint16_t half_clamped(float v) {
+  v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+  return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// BM x BN tiles, S stages of BK = 64, a WGM x WGN grid of waves. With SW the
+// matrix's rows come in groups of 4 as (gate 2i, gate 2i + 1, up 2i, up 2i
+// + 1) and C is a half output [M][ldc] of N / 2 columns: half(silu(gate) *
+// up), as REDUCE_SWIGLU (src/gpu/kernels.ts:1066-1077) computes it from
+// the float32 sums.
+template <int ZK, int BM, int BN, int S, int WGM, int WGN, bool SW = false>
 __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
     1, gemm_waves_per_simd<ZK, BM, BN, S, WGM * WGN>()))) void gemm_q4_kernel(const uint8_t *__restrict__ quants,
                                                       const uint16_t *__restrict__ scales,
@@ -329,6 +338,30 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
   }
 
   // D[j] of lane i: row 8 (j / 4) + 4 (i / 32) + j % 4, column i % 32.
+  if constexpr (SW) {
+    // Column i % 32's row in its group is i % 4: the gate rows' lanes (0, 1)
+    // meet their up rows (2, 3) by a swap within each quad (DPP [2,3,0,1]),
+    // which every lane takes part in.
+    uint16_t *out16 = reinterpret_cast<uint16_t *>(C);
+    const int r = lane & 3;
+#pragma unroll
+    for (int u = 0; u < NT; u++) {
+      const int n = n0 + wn * WN + u * 32 + (lane & 31);
+#pragma unroll
+      for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          const int m = m0 + wm * WM + t * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
+          float v = acc[t][u][j];
+          if (row_scale) v *= row_scale[m < M ? m : M - 1];
+          const float up = dpp_f<0x4e, 0xf>(v, 0.0f);
+          if (m < M && r < 2)
+            out16[(int64_t)m * ldc + 2 * (n >> 2) + r] =
+                half_clamped(v / (1.0f + __expf(-v)) * up);
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < NT; u++) {
     const int n = n0 + wn * WN + u * 32 + (lane & 31);
@@ -349,7 +382,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
   }
 }
 
-template <int ZK, int BM, int BN, int S, int WGM = 2, int WGN = 2>
+template <int ZK, int BM, int BN, int S, int WGM = 2, int WGN = 2, bool SW = false>
 int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
                  const float *residual, int ldr, const float *row_scale, const int32_t *col_of,
                  hipStream_t s) {
@@ -357,18 +390,18 @@ int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float
   constexpr size_t LDS = (size_t)S * STAGE;
   static bool raised = false;  // allow more than 64 KiB of dynamic LDS, once
   if (!raised && LDS > 64 * 1024) {
-    WG_HIP(hipFuncSetAttribute((const void *)gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN>,
+    WG_HIP(hipFuncSetAttribute((const void *)gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS));
     raised = true;
   }
   const int grid = ((M + BM - 1) / BM) * (w->N / BN);
-  gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN><<<grid, WGM * WGN * 64, LDS, s>>>(
+  gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW><<<grid, WGM * WGN * 64, LDS, s>>>(
       (const uint8_t *)w->quants, (const uint16_t *)w->scales, w->zeros, A, lda, C, ldc,
       residual, ldr, row_scale, col_of, M, w->N, w->K);
-  return launched("wg_q4_gemm");
+  return launched(SW ? "wg_q4_gemm_swiglu" : "wg_q4_gemm");
 }
 
-template <int ZK>
+template <int ZK, bool SW = false>
 int launch(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
            const float *residual, int ldr, const float *row_scale, const int32_t *col_of,
            hipStream_t s) {
@@ -385,12 +418,12 @@ int launch(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, i
     else if (w->N % 128 == 0) t = 1;
   }
   if (t == 3 && w->N % 256 == 0)
-    return launch_tiles<ZK, 128, 256, 3, 1, 8>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+    return launch_tiles<ZK, 128, 256, 3, 1, 8, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
   if (t == 2 && w->N % 128 == 0)
-    return launch_tiles<ZK, 128, 128, 3, 1, 4>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+    return launch_tiles<ZK, 128, 128, 3, 1, 4, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
   if (w->N % 128 == 0)
-    return launch_tiles<ZK, 64, 128, 4, 1, 4>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
-  return launch_tiles<ZK, 64, 64, 5, 1, 2>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+    return launch_tiles<ZK, 64, 128, 4, 1, 4, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+  return launch_tiles<ZK, 64, 64, 5, 1, 2, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
 }
 
 }  // namespace
@@ -398,7 +431,47 @@ int launch(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, i
 
 using namespace wg;
 
+static int check_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda,
+                      const void *C, const char *who) {
+  int rc = check_matrix(w, who);
+  if (rc) return rc;
+  WG_REQUIRE(w->layout == WG_LAYOUT_ROWGROUP || w->layout == WG_LAYOUT_Q8,
+             "%s: the prefill GEMM reads 4-bit and 8-bit row-group matrices", who);
+  WG_REQUIRE(w->K % 64 == 0, "%s: columns (%d) must be a multiple of 64", who, w->K);
+  WG_REQUIRE(w->N % 64 == 0, "%s: rows (%d) must be a multiple of 64", who, w->N);
+  WG_REQUIRE(A && C && M >= 1, "%s: bad arguments", who);
+  WG_REQUIRE(lda >= w->K && lda % 8 == 0 && ((uintptr_t)A & 15) == 0,
+             "%s: activations need a 16-byte aligned stride >= K", who);
+  WG_REQUIRE((int64_t)M * lda * 2 < ((int64_t)1 << 31) && (int64_t)w->N * w->K < ((int64_t)1 << 32),
+             "%s: %d x %d activations or a %d x %d matrix past 2 GiB", who, M, lda, w->N, w->K);
+  return WG_OK;
+}
+
+template <bool SW>
+static int dispatch(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
+                    const float *residual, int ldr, const float *row_scale,
+                    const int32_t *col_of, hipStream_t s) {
+  if (w->layout == WG_LAYOUT_Q8)
+    return launch<Q8, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+  switch (w->zero) {
+    case WG_ZERO_8: return launch<WG_ZERO_8, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+    case WG_ZERO_U8: return launch<WG_ZERO_U8, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+    default: return launch<WG_ZERO_F16, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+  }
+}
+
 extern "C" {
+
+int wg_q4_gemm_swiglu(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda,
+                      uint16_t *out16, int32_t ldo, const float *row_scale, void *stream) {
+  int rc = check_gemm(w, A, M, lda, out16, "wg_q4_gemm_swiglu");
+  if (rc) return rc;
+  WG_REQUIRE(ldo >= w->N / 2, "wg_q4_gemm_swiglu: ldo %d < N / 2 = %d", ldo, w->N / 2);
+  WG_REQUIRE(!overlaps(A, (size_t)M * lda * 2, out16, (size_t)M * ldo * 2),
+             "wg_q4_gemm_swiglu: activations and output overlap");
+  return dispatch<true>(w, A, M, lda, reinterpret_cast<float *>(out16), ldo, nullptr, 0,
+                        row_scale, nullptr, as_stream(stream));
+}
 
 int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda, float *C,
                int32_t ldc, const float *residual, int32_t ldr, const float *row_scale,

@@ -423,7 +423,6 @@ class Engine:
                 "qkv": torch.zeros((R, s.qkv_rows), dtype=f32, device=dev),
                 "q": torch.zeros((R, A), dtype=f32, device=dev),
                 "att16": torch.zeros((R, A), dtype=f16, device=dev),
-                "gu": torch.zeros((R, 2 * F), dtype=f32, device=dev),
                 "ff16": torch.zeros((R, F), dtype=f16, device=dev),
             }
         return self._pre
@@ -467,9 +466,7 @@ class Engine:
                                  self.pos, out=b["att16"][:M])
                 ops.gemm(lw["o"], b["att16"][:M], out=h, residual=h)
             ops.norm_to_h2(h, lw["ffn_norm"], s.eps, x16, rs)
-            gu = ops.gemm(lw["gate_up"], x16, out=b["gu"][:M],
-                          col_of=self._col_of(lw["gate_up"]), row_scale=rs)
-            ops.swiglu(gu, out=b["ff16"][:M])
+            ops.gemm_swiglu(lw["gate_up"], x16, out=b["ff16"][:M], row_scale=rs)
             ops.gemm(lw["down"], b["ff16"][:M], out=h, residual=h)
 
     def _prefill_head(self, r0: int, T: int) -> None:

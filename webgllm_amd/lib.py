@@ -151,6 +151,7 @@ def load():
                                  C.POINTER(Epilogue), P]),
         "wg_f32_to_f16": (C.c_int, [P, P, I64, P]),
         "wg_q4_gemm": (C.c_int, [C.POINTER(Q4MatrixDesc), P, I32, I32, P, I32, P, I32, P, P, P]),
+        "wg_q4_gemm_swiglu": (C.c_int, [C.POINTER(Q4MatrixDesc), P, I32, I32, P, I32, P, P]),
         "wg_rms_norm": (C.c_int, [P, I32, I32, I32, P, C.c_float, P, I32, P, P]),
         "wg_norm_to_h2": (C.c_int, [P, I32, I32, I32, P, C.c_float, P, I32, P, P]),
         "wg_swiglu": (C.c_int, [P, I32, I32, I32, P, I32, P]),

@@ -244,6 +244,25 @@ def gemm(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
     return out
 
 
+def gemm_swiglu(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
+                row_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """half(silu(gate) * up) [M, N / 2] of A W^T on MFMA, for a gate|up
+    matrix stored in the SwiGLU row order (gate 2i, gate 2i + 1, up 2i,
+    up 2i + 1 per row group)."""
+    if a16.dtype not in (torch.float16, torch.int16):
+        raise ValueError("activations must be halves")
+    a16 = _dev(a16)
+    M = a16.shape[0]
+    if out is None:
+        out = torch.empty((M, m.N // 2), dtype=torch.float16, device=a16.device)
+    _dev(out)
+    L.check(L.load().wg_q4_gemm_swiglu(C.byref(m.desc), _p(a16), M, a16.shape[1], _p(out),
+                                       out.shape[1],
+                                       _p(None if row_scale is None else
+                                          _dev(row_scale, torch.float32)), _stream()))
+    return out
+
+
 def f32_to_f16(x: torch.Tensor) -> torch.Tensor:
     x = _dev(x, torch.float32)
     out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
