@@ -672,7 +672,78 @@ def workload_gguf_load(args):
                 3, 0, best * 1e3, cfg, roof, cpu, dtype="u8")
 
 
+def workload_sample_pick(args):
+    """The sampling pick of one Llama-3-8B-vocabulary row (128256 logits):
+    wg_pick_candidates with a repetition and presence penalty and a window
+    of 64 seen tokens, the best 64 chunks (16384 candidates) gathered; then
+    their read-back and the host sampler (top-k 40, top-p 0.95, temperature
+    0.8). Microseconds a pick."""
+    import numpy as np
+    import torch
+    from webgllm_amd import lib as L, ops
+    from webgllm_amd.sampler import Sampler, draw
+    V, count = 128256, 64
+    g = torch.Generator(device="cuda").manual_seed(3)
+    logits = torch.randn((1, V), device="cuda", generator=g) * 3
+    mask = torch.zeros(V, dtype=torch.uint8, device="cuda")
+    mask[torch.randint(0, V, (64,), device="cuda", generator=g)] = 1
+    scratch = torch.empty(int(L.load().wg_pick_scratch_bytes(1, V)), dtype=torch.uint8,
+                          device="cuda")
+
+    def pick():
+        return ops.pick_candidates(logits, count, mask=mask, penalty=1.1,
+                                   presence_penalty=0.2, scratch=scratch)
+    chunks_out = torch.empty((1, count), dtype=torch.int32, device="cuda")
+    cand_out = torch.empty((1, count, 256), device="cuda")
+    lib = L.load()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch():  # the C call alone, outputs preallocated
+        L.check(lib.wg_pick_candidates(logits.data_ptr(), 1, V, V, mask.data_ptr(), None, 0, 0,
+                                       1.1, 0.2, None, 0, 0, count, chunks_out.data_ptr(),
+                                       cand_out.data_ptr(), scratch.data_ptr(), scratch.numel(),
+                                       stream))
+    for _ in range(20):
+        launch()
+    reps = max(100, 4 * args.steps)
+    ms = timed(launch, reps)
+    algo = V * 4 + V + 2 * count * 256 * 4 + count * 4  # logits, mask, gather reread + out
+    gbps = algo / (ms * 1e-3) / 1e9
+    s = Sampler(0.8, 40, top_p=0.95, repetition_penalty=1.1, presence_penalty=0.2)
+    r = np.random.default_rng(0)
+    t0 = time.time()
+    n = 200
+    for _ in range(n):
+        chunks, cand = pick()
+        d = s.candidates(chunks.cpu().numpy()[0], cand.cpu().numpy()[0])
+        draw(d, r.random)
+    host_ms = (time.time() - t0) * 1e3 / n
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        lg, mk = logits.cpu().numpy(), mask.cpu().numpy()
+        spent, k = 0.0, 0
+        while spent < 5.0 or k < 2:
+            t1 = O.now()
+            O.pick_candidates(lg, count, mask=mk, penalty=1.1, presence=0.2)
+            spent += O.now() - t1
+            k += 1
+        cpu = {"value": round(spent / k * 1e6, 1), "unit": "us", "cores": 1, "kind": "port",
+               "sample": f"oracle restatement of the pick (one thread), the same row, {k} "
+                         f"repetitions ({spent:.1f} s)"}
+    roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 5), "traffic": None,
+            "kernel": "chunk_max_kernel + chunk_gather_kernel (one row, 128256 logits, 64 chunks)",
+            "bytes_per_launch": algo, "avg_launch_us": round(ms * 1e3, 2), "launches": reps}
+    cfg = {"workload": "sampling pick of one 128256-logit row: penalties, best 64 chunks, "
+                       "then the host sampler", "pick_and_sample_ms": round(host_ms, 3),
+           "parallelism": "none"}
+    return line("sampling pick us (128256-logit row, 64 chunks)", round(ms * 1e3, 2), "us",
+                reps, 20, ms, cfg, roof, cpu, higher_is_better=False)
+
+
 WORKLOADS = {"q4_0-gemv": workload_q4_0_gemv, "nbits-gemm": workload_nbits_gemm,
+             "sample-pick": workload_sample_pick,
              "gguf-load": workload_gguf_load,
              "q8-gemm": lambda args: workload_nbits_gemm(args, "q8"),
              "q6_k-head": workload_q6_k_head, "q8-gemv": workload_q8_gemv,

@@ -508,6 +508,61 @@ int wg_argmax_advance(const float *logits, int32_t V, int32_t *ids, int32_t *pos
                       int32_t hist_len, float *tops, void *scratch, size_t scratch_bytes,
                       void *stream);
 
+/* -------------------------------------------------- sampling candidates */
+
+/* Engine.pick (src/engine.ts:8352-8473; PENALIZED, CHUNK_MAX, CHUNK_RANK,
+ * CHUNK_BY_RANK, CHUNK_GATHER, src/gpu/kernels.ts:3085-3163, :3265-3323):
+ * for each of M rows of V logits, the `count` (1..64) 256-token chunks with
+ * the largest penalized logit, in rank order (ties to the lower chunk), and
+ * their penalized logits: chunks_out [M][count] chunk indices, candidates
+ * [M][count][256] (token chunk * 256 + t; past V, -1e30). Penalized as the
+ * reference does for batch row r = row0 + m:
+ *  - -1e30 where the allowed bitmap (allowed [allowed_rows][ld_allowed]
+ *    words, bit id % 32 of word id / 32 of row r, or row 0 when
+ *    allowed_rows is 1; rows past allowed_rows allow nothing), if given,
+ *    has the bit clear, or where mask[id] is 2 (never draw);
+ *  - the token's state, mask[id] (0 unseen, 1 in the window from the
+ *    prompt, 3 written; mask may be NULL for all 0), replaced by the last
+ *    of seen_rows [n_seen][4] (token, state, first row, end row: at most 16)
+ *    that covers row r;
+ *  - a seen token (state 1 or 3): v < 0 ? v * penalty : v / penalty, then
+ *    minus presence_penalty.
+ * scratch: wg_pick_scratch_bytes(M, V) bytes (calls sharing it must not
+ * overlap). The host samples from the candidates (see webgllm_amd/sampler.py,
+ * the reference's createSampler with penalize = false); for top-k with k <=
+ * count they hold the k largest penalized logits. */
+size_t wg_pick_scratch_bytes(int32_t M, int32_t V);
+int wg_pick_candidates(const float *logits, int32_t M, int32_t V, int32_t ld,
+                       const uint8_t *mask, const int32_t *seen_rows, int32_t n_seen,
+                       int32_t row0, float penalty, float presence_penalty,
+                       const uint32_t *allowed, int32_t allowed_rows, int32_t ld_allowed,
+                       int32_t count, int32_t *chunks_out, float *candidates, void *scratch,
+                       size_t scratch_bytes, void *stream);
+
+/* The host sampler (createSampler's distribution, draw, drawAt:
+ * src/sampler.ts:27-242), over candidates the pick read back: settings as
+ * the reference's Sampling (doubles, as JavaScript numbers). */
+typedef struct {
+  double temperature; /* <= 0: greedy */
+  double top_p;       /* 1: off */
+  double min_p;       /* 0: off */
+  int32_t top_k;      /* <= 0: every candidate */
+} wg_sampling;
+
+/* distribution(logits, penalize = false): the kept candidates (ids_out,
+ * from ids_in[i], or i when ids_in is NULL) and their probabilities, after
+ * top-k (a min-heap of slots: the reference's order), top-p, min-p and the
+ * temperature, with its float32 stores; *n_out of them (1 when greedy).
+ * ids_out and p_out hold n entries. Host code; no device work. */
+int wg_sample_distribution(const wg_sampling *s, const float *logits, const int32_t *ids_in,
+                           int32_t n, int32_t *ids_out, float *p_out, int32_t *n_out);
+/* draw (src/sampler.ts:188-200): the token a uniform u in [0, 1) picks,
+ * candidates in their slot order. */
+int32_t wg_sample_draw(const int32_t *ids, const float *p, int32_t n, double u);
+/* drawAt (src/sampler.ts:227-242): the same, candidates in ascending id
+ * order (seeded sampling). */
+int32_t wg_sample_draw_at(const int32_t *ids, const float *p, int32_t n, double u);
+
 #ifdef __cplusplus
 }
 #endif

@@ -747,6 +747,75 @@ void orc_matmul_q6k(const uint8_t *quants, const uint16_t *scales, int N, int K,
   (void)threads;
 }
 
+/* ---------------------------------------------------- sampling candidates */
+
+/* PENALIZED (src/gpu/kernels.ts:3102-3122) for token id of batch row r:
+ * -1e30 where it may not be drawn (allowed bit clear, mask 2, past V),
+ * else a seen token's logit divided (positive) or multiplied (negative) by
+ * the penalty and less the presence penalty. */
+static float orc_penalized(float v, int id, int r, int V, const uint8_t *mask,
+                           const int32_t *seen, int n_seen, float penalty, float presence,
+                           const uint32_t *allowed, int allowed_rows, int ld_allowed) {
+  if (id >= V) return -1e30f;
+  if (allowed) {
+    int row = allowed_rows == 1 ? 0 : r;
+    if (row >= allowed_rows) return -1e30f;
+    if (!((allowed[(size_t)row * ld_allowed + (id >> 5)] >> (id & 31)) & 1u)) return -1e30f;
+  }
+  int m = mask ? mask[id] : 0;
+  if (m == 2) return -1e30f;
+  int state = m;
+  for (int k = 0; k < n_seen; k++)
+    if (seen[4 * k] == id && r >= seen[4 * k + 2] && r < seen[4 * k + 3]) state = seen[4 * k + 1];
+  if (state == 1 || state == 3) {
+    v = v < 0.0f ? v * penalty : v / penalty;
+    v -= presence;
+  }
+  return v;
+}
+
+/* CHUNK_MAX + CHUNK_RANK + CHUNK_BY_RANK + CHUNK_GATHER (src/gpu/kernels.ts:
+ * 3147-3163, :3265-3323; Engine.pick, src/engine.ts:8352-8473): per row,
+ * each 256-token chunk's largest penalized logit, the chunks ranked (larger
+ * first, ties to the lower index), the first `count` chunks' indices and
+ * penalized logits. */
+void orc_pick_candidates(const float *logits, int M, int V, const uint8_t *mask,
+                         const int32_t *seen, int n_seen, int row0, float penalty,
+                         float presence, const uint32_t *allowed, int allowed_rows,
+                         int ld_allowed, int count, int32_t *chunks_out, float *cand_out) {
+  int total = (V + 255) / 256;
+  float *mx = malloc(sizeof(float) * total);
+  for (int m = 0; m < M; m++) {
+    const float *row = logits + (size_t)m * V;
+    int r = row0 + m;
+    for (int c = 0; c < total; c++) {
+      float best = -1e30f;
+      for (int t = 0; t < 256; t++) {
+        int id = c * 256 + t;
+        float v = orc_penalized(id < V ? row[id] : 0.0f, id, r, V, mask, seen, n_seen, penalty,
+                                presence, allowed, allowed_rows, ld_allowed);
+        if (v > best) best = v;
+      }
+      mx[c] = best;
+    }
+    for (int c = 0; c < total; c++) {
+      int rank = 0;
+      for (int i = 0; i < total; i++) rank += mx[i] > mx[c] || (mx[i] == mx[c] && i < c);
+      if (rank < count) chunks_out[(size_t)m * count + rank] = c;
+    }
+    for (int k = 0; k < count; k++) {
+      int c = chunks_out[(size_t)m * count + k];
+      for (int t = 0; t < 256; t++) {
+        int id = c * 256 + t;
+        cand_out[((size_t)m * count + k) * 256 + t] =
+            orc_penalized(id < V ? row[id] : 0.0f, id, r, V, mask, seen, n_seen, penalty,
+                          presence, allowed, allowed_rows, ld_allowed);
+      }
+    }
+  }
+  free(mx);
+}
+
 /* ------------------------------------------------------------ elementwise */
 
 /* packH2 (src/gpu/kernels.ts:32-36): clamped to +-65504, then to halves. */

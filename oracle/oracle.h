@@ -117,6 +117,12 @@ void orc_attention_f64(const float *q, const uint16_t *kc, const uint16_t *vc, i
 void orc_short_conv(const float *bcx, int M, int D, int W, const float *taps, const float *state,
                     float *out, float *new_state, float *prefixes);
 
+/* ---- sampling candidates (kernels.ts:3085-3163, :3265-3323) ---- */
+void orc_pick_candidates(const float *logits, int M, int V, const uint8_t *mask,
+                         const int32_t *seen, int n_seen, int row0, float penalty,
+                         float presence, const uint32_t *allowed, int allowed_rows,
+                         int ld_allowed, int count, int32_t *chunks_out, float *cand_out);
+
 /* ---- greedy pick (kernels.ts:3169-3246) ---- */
 int orc_argmax(const float *logits, int V, float *top);
 

@@ -78,6 +78,8 @@ _lib.orc_rope_rows.argtypes = [_I]
 _lib.orc_head_prep.argtypes = [_P, _P, _P, _I, _I, _I, C.c_float, C.c_float, _I, _P]
 _lib.orc_attention_f64.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _P]
 _lib.orc_short_conv.argtypes = [_P, _I, _I, _I, _P, _P, _P, _P, _P]
+_lib.orc_pick_candidates.argtypes = [_P, _I, _I, _P, _P, _I, _I, C.c_float, C.c_float, _P, _I,
+                                     _I, _I, _P, _P]
 _lib.orc_argmax.restype = _I
 _lib.orc_argmax.argtypes = [_P, _I, C.POINTER(C.c_float)]
 _lib.orc_now.restype = C.c_double
@@ -382,6 +384,25 @@ def short_conv(bcx, D, W, taps, state, prefixes=False):
     _lib.orc_short_conv(_ptr(bcx), M, D, W, _ptr(taps), _ptr(state), _ptr(out), _ptr(new_state),
                         _ptr(pre))
     return (out, new_state, pre) if prefixes else (out, new_state)
+
+
+def pick_candidates(logits, count, mask=None, seen_rows=None, row0=0, penalty=1.0,
+                    presence=0.0, allowed=None):
+    """(chunks [M, count], candidates [M, count, 256]) as wg_pick_candidates."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    logits2 = logits.reshape(-1, logits.shape[-1])
+    M, V = logits2.shape
+    mask = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
+    seen = None if not seen_rows else np.ascontiguousarray(seen_rows, dtype=np.int32).reshape(-1, 4)
+    allowed = None if allowed is None else np.ascontiguousarray(allowed, dtype=np.uint32)
+    chunks = np.empty((M, count), np.int32)
+    cand = np.empty((M, count, 256), np.float32)
+    _lib.orc_pick_candidates(_ptr(logits2), M, V, _ptr(mask), _ptr(seen),
+                             0 if seen is None else seen.shape[0], row0, penalty, presence,
+                             _ptr(allowed), 0 if allowed is None else allowed.shape[0],
+                             0 if allowed is None else allowed.shape[1], count, _ptr(chunks),
+                             _ptr(cand))
+    return chunks, cand
 
 
 def argmax(logits: np.ndarray):

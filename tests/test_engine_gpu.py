@@ -256,3 +256,36 @@ def test_capture_leaves_the_cache_alone(hip):
     for i, (k, v) in enumerate(zip(eng.k_cache.values(), eng.v_cache.values())):
         assert torch.equal(k[:21], before[i][0]) and torch.equal(v[:21], before[i][1])
     assert eng.decode(first, 12) == orc.decode(first, 12)
+
+
+@pytest.mark.parametrize("family", ["llama-q4_k", "lfm2-q4_0", "gguf-q4_k-q6_k-head"])
+def test_sampled_generate_with_penalties(hip, family):
+    """Sampled decoding through the GPU's candidate pick and the host
+    sampler: at temperature 0 with repetition and presence penalties it
+    writes the oracle decoder's penalized greedy tokens (the host sampler
+    over the oracle's full logits); at temperature 0.8 two seeded runs
+    write the same tokens."""
+    import random as pyrandom
+    from webgllm_amd.sampler import Sampler
+    eng, orc = _pair(family, seed=2)
+    rng = np.random.default_rng(11)
+    prompt = _prompt(rng, 13, eng.shape.vocab)
+    got = eng.generate(prompt, 12, Sampler(0, 40, repetition_penalty=1.3,
+                                           presence_penalty=0.2))
+    s = Sampler(0, 40, repetition_penalty=1.3, presence_penalty=0.2)
+    s.see(prompt)
+    want, tokens = [], prompt
+    for _ in range(12):
+        logits, _ = orc.forward(tokens)
+        t = s.sample(np.ascontiguousarray(logits[-1], np.float32))
+        want.append(t)
+        s.see([t], True)
+        tokens = [t]
+    assert got == want
+    runs = []
+    for _ in range(2):
+        e2, _ = _pair(family, seed=2)
+        r = pyrandom.Random(5)
+        runs.append(e2.generate(prompt, 10, Sampler(0.8, 50, top_p=0.95,
+                                                    repetition_penalty=1.1), r.random))
+    assert runs[0] == runs[1] and all(0 <= t < eng.shape.vocab for t in runs[0])

@@ -607,6 +607,40 @@ class Engine:
         self.check_plan()
         return toks
 
+    # --- sampled decoding -------------------------------------------------
+    def generate(self, prompt: list[int], steps: int, sampler, random=None,
+                 count: int = 64) -> list[int]:
+        """Sampled decoding (Engine.pick + the host sampler, src/engine.ts:
+        8352-8473, src/sampler.ts): each step's last logits row goes through
+        wg_pick_candidates (the penalties of the sampler's window on the
+        device, the best `count` chunks read back) and the sampler draws
+        the token from them. The window sees the prompt, then each token
+        written. Returns the `steps` tokens drawn."""
+        from . import sampler as S
+        s = self.shape
+        V = s.vocab
+        mask = torch.zeros(V, dtype=torch.uint8, device=self.device)
+        scratch = torch.empty(int(L.load().wg_pick_scratch_bytes(1, V)), dtype=torch.uint8,
+                              device=self.device)
+        changes = sampler.see(prompt)
+        out = []
+        tokens = list(prompt)
+        for _ in range(steps):
+            self.forward(tokens)
+            for t, st in changes:
+                mask[t] = st
+            row = (len(tokens) - 1) % 8
+            chunks, cand = ops.pick_candidates(
+                self.logits[row:row + 1], min(count, (V + 255) // 256), mask=mask,
+                penalty=sampler.repetition_penalty, presence_penalty=sampler.presence_penalty,
+                scratch=scratch)
+            d = sampler.candidates(chunks.cpu().numpy()[0], cand.cpu().numpy()[0])
+            t = S.draw(d, random)
+            out.append(t)
+            changes = sampler.see([t], True)
+            tokens = [t]
+        return out
+
 
 def _rope_table(theta: float, head_dim: int, ctx: int) -> torch.Tensor:
     """Engine.ropeTable (src/engine.ts:1292-1312): cos and sin in doubles,

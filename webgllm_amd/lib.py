@@ -180,6 +180,9 @@ def load():
         "wg_gguf_meta": (C.c_int, [P, I64, C.POINTER(GgufValue)]),
         "wg_gguf_meta_element": (C.c_int, [P, I64, C.c_uint64, C.POINTER(GgufValue)]),
         "wg_rows_to_floats": (C.c_int, [I32, P, I32, I32, P, P]),
+        "wg_pick_scratch_bytes": (SZ, [I32, I32]),
+        "wg_pick_candidates": (C.c_int, [P, I32, I32, I32, P, P, I32, I32, C.c_float,
+                                         C.c_float, P, I32, I32, I32, P, P, P, SZ, P]),
         "wg_decode_plan_create": (C.c_int, [C.POINTER(DecodeLayer), I32, C.POINTER(P)]),
         "wg_decode_run": (C.c_int, [P, P]),
         "wg_decode_status": (C.c_int, [P]),

@@ -418,3 +418,36 @@ def argmax_advance(logits: torch.Tensor, ids: torch.Tensor, pos: torch.Tensor,
     L.check(L.load().wg_argmax_advance(_p(logits), V, _p(ids), _p(pos), _p(hist),
                                        0 if hist is None else hist.numel(), _p(tops),
                                        _p(scratch), scratch.numel(), _stream()))
+
+
+def pick_candidates(logits: torch.Tensor, count: int, mask: torch.Tensor | None = None,
+                    seen_rows=None, row0: int = 0, penalty: float = 1.0,
+                    presence_penalty: float = 0.0, allowed: torch.Tensor | None = None,
+                    scratch: torch.Tensor | None = None):
+    """The `count` best 256-token chunks of each row of logits [M, V] by
+    penalized maximum, and their penalized logits (wg_pick_candidates):
+    (chunks int32 [M, count], candidates float32 [M, count, 256]).
+    seen_rows: [(token, state, first row, end row)], at most 16; allowed:
+    uint32 bitmap [rows, words] or None."""
+    logits = _dev(logits, torch.float32)
+    M, V = (logits.shape[0], logits.shape[1]) if logits.dim() == 2 else (1, logits.shape[0])
+    dev = logits.device
+    chunks = torch.empty((M, count), dtype=torch.int32, device=dev)
+    cand = torch.empty((M, count, 256), dtype=torch.float32, device=dev)
+    need = int(L.load().wg_pick_scratch_bytes(M, V))
+    if scratch is None or scratch.numel() < need:
+        scratch = torch.empty(need, dtype=torch.uint8, device=dev)
+    seen = None
+    if seen_rows:
+        seen = torch.tensor(list(seen_rows), dtype=torch.int32, device=dev).reshape(-1, 4)
+    if mask is not None:
+        _dev(mask, torch.uint8)
+    if allowed is not None:
+        _dev(allowed, torch.int32)
+    L.check(L.load().wg_pick_candidates(
+        _p(logits), M, V, V if logits.dim() == 1 else logits.stride(0), _p(mask), _p(seen),
+        0 if seen is None else seen.shape[0], row0, penalty, presence_penalty, _p(allowed),
+        0 if allowed is None else allowed.shape[0],
+        0 if allowed is None else allowed.shape[1], count, _p(chunks), _p(cand), _p(scratch),
+        scratch.numel(), _stream()))
+    return chunks, cand
