@@ -636,3 +636,62 @@ def test_q5_k_decode_inverts_ggml_packing():
     dmm = np.array([O.from_half(h) for h in dm], np.float64)[:, None]
     want = (dd * np.repeat(sc, 32, axis=1) * q - dmm * np.repeat(mn, 32, axis=1))
     assert np.array_equal(got, want.astype(np.float32))
+
+
+# --- sampling candidates (src/gpu/kernels.ts:3085-3163, :3265-3323) ---------
+
+def test_pick_candidates_hand_cases():
+    """Hand-worked penalties: a logit 2.0 under penalty 2 and presence 0.5
+    becomes 2/2 - 0.5 = 0.5, a logit -1.0 becomes -1*2 - 0.5 = -2.5; mask
+    byte 2, a cleared allowed bit and ids past the vocabulary become -1e30;
+    a seen row's state replaces the mask's only on its rows (state 0 lifts
+    the penalty; only the mask byte forbids); chunks rank by maximum, ties
+    to the lower chunk."""
+    V = 600  # three chunks, the last one 88 ids long
+    logits = np.zeros((3, V), np.float32)
+    logits[:, 5] = 2.0     # chunk 0
+    logits[:, 6] = -1.0
+    logits[:, 300] = 2.0   # chunk 1
+    logits[:, 520] = 1.0   # chunk 2
+    logits[:, 530] = 5.0   # chunk 2, never drawn
+    mask = np.zeros(V, np.uint8)
+    mask[5], mask[6], mask[530] = 3, 1, 2
+    # rows 1-2 see token 300 as written; row 2 no longer sees token 5
+    seen = [[300, 3, 1, 3], [5, 0, 2, 3]]
+    chunks, cand = O.pick_candidates(logits, 3, mask=mask, seen_rows=seen, row0=0,
+                                     penalty=2.0, presence=0.5)
+    # row 0: chunk 1 keeps 2.0, chunk 2 has 1.0, chunk 0 has 0.5
+    assert list(chunks[0]) == [1, 2, 0]
+    assert cand[0, 2, 5] == np.float32(0.5) and cand[0, 2, 6] == np.float32(-2.5)
+    assert cand[0, 1, 530 - 512] == np.float32(-1e30)
+    assert np.all(cand[0, 1, V - 512:] == np.float32(-1e30))
+    # row 1: token 300 falls to 0.5 and ties chunk 0: chunk 2 first, then 0, then 1
+    assert list(chunks[1]) == [2, 0, 1] and cand[1, 2, 300 - 256] == np.float32(0.5)
+    # row 2: token 5 is unpenalized again (2.0); token 6 keeps its penalty
+    assert list(chunks[2]) == [0, 2, 1]
+    assert cand[2, 0, 5] == np.float32(2.0) and cand[2, 0, 6] == np.float32(-2.5)
+    # the same rows picked one at a time (row0 names the batch row)
+    c1, v1 = O.pick_candidates(logits[1:2], 3, mask=mask, seen_rows=seen, row0=1,
+                               penalty=2.0, presence=0.5)
+    assert np.array_equal(c1[0], chunks[1]) and np.array_equal(v1[0], cand[1])
+    # an allowed bitmap with token 300's bit cleared
+    allowed = np.full((1, (V + 31) // 32), 0xFFFFFFFF, np.uint32)
+    allowed[0, 300 // 32] &= ~np.uint32(1 << (300 % 32))
+    chunks, cand = O.pick_candidates(logits[:1], 3, allowed=allowed)
+    assert list(chunks[0]) == [2, 0, 1] and cand[0, 2, 300 - 256] == np.float32(-1e30)
+
+
+def test_pick_candidates_hold_the_top_k():
+    """For k <= count, the k largest penalized logits all lie in the kept
+    chunks (each lies in a chunk whose maximum is among the k largest):
+    checked against a sort of the whole penalized row."""
+    rng = np.random.default_rng(3)
+    V, count = 5000, 6
+    logits = rng.standard_normal((2, V)).astype(np.float32)
+    chunks, cand = O.pick_candidates(logits, count)
+    for m in range(2):
+        top = np.argsort(-logits[m], kind="stable")[:count]
+        kept = set(int(c) for c in chunks[m])
+        assert all(int(t) // 256 in kept for t in top)
+        got = np.sort(cand[m].reshape(-1))[::-1][:count]
+        assert np.array_equal(got, np.sort(logits[m])[::-1][:count])
