@@ -488,6 +488,45 @@ int wg_short_conv(const float *bcx, int32_t M, int32_t D, int32_t ldb, int32_t W
 int wg_conv_accept(const float *prefixes, int32_t kept, int32_t rows, int32_t D, int32_t W,
                    float *state, void *stream);
 
+/* ------------------------------------------------- Gated DeltaNet */
+
+/* A Gated DeltaNet layer's shape (Qwen3.5's linear attention,
+ * src/load-gguf.ts:715-726): as many key as value heads (the reference
+ * refuses others), key_dim at most 256. */
+typedef struct {
+  int32_t heads, key_dim, value_dim;
+} wg_delta_shape;
+
+/* Engine.linearAttend's recurrence for M rows (engine.ts:6697-6815): per row
+ * LIN_GATES, LIN_PREP, LIN_DELTA, LIN_STATE (kernels.ts:1544-1862; one row:
+ * LIN_DELTA_FUSED), in one launch. qkv rows: the convolution's output q
+ * (heads * key_dim) | k | v (heads * value_dim); ba rows: b (heads) | a
+ * (heads); A = -exp(A_log) and dt_bias per head. Per head, beta =
+ * sigmoid(b), decay = exp(A softplus(a + dt_bias)), q^ = q / sqrt(|q|^2 +
+ * 1e-6) / sqrt(key_dim), k^ = k / sqrt(|k|^2 + 1e-6); d = beta (v - decay
+ * S^T k^), S <- decay S + k^ d^T, out = S^T q^. state [heads][key_dim]
+ * [value_dim] float32, updated in place; with save_at in 1..M, snapshot (its
+ * size, not overlapping) receives the state after row save_at (the
+ * reference's saveAt). */
+int wg_delta_rule(const float *qkv, int32_t M, int32_t ldq, const float *ba, int32_t ldba,
+                  const float *A, const float *dt_bias, const wg_delta_shape *shape,
+                  float *state, float *snapshot, int32_t save_at, float *out, int32_t ldo,
+                  void *stream);
+/* LIN_CONV + LIN_CONV_STATE (kernels.ts:1564-1641): out[m][c] = silu(sum_k
+ * taps[c][k] * x[m - (W-1) + k][c]) over the first C channels of each in
+ * row (W at most 16; tap W-1 the current row), earlier rows from state
+ * [W-1][C] (oldest first); state_out (apart from state) = the last W-1 raw
+ * rows. */
+int wg_delta_conv(const float *in, int32_t M, int32_t ldi, int32_t C, int32_t W,
+                  const float *taps, const float *state, float *state_out, float *out,
+                  int32_t ldo, void *stream);
+/* LIN_NORM (kernels.ts:1836-1860): out16[m][h dv + i] = half(o * w[i] *
+ * silu(z) / sqrt(mean of the head's o^2 + eps)), out_proj's input (value_dim
+ * at most 256). */
+int wg_delta_norm(const float *o, int32_t M, int32_t ldo, const wg_delta_shape *shape,
+                  const float *z, int32_t ldz, const float *weight, float eps, uint16_t *out16,
+                  int32_t ldh, void *stream);
+
 /* ------------------------------------------------------ greedy pick */
 
 /* CHUNK_MAX_AT + CHUNK_ARGMAX_ROWS (kernels.ts:3169-3246): ids[m] = the lowest

@@ -989,6 +989,215 @@ int orc_argmax(const float *logits, int V, float *top) {
   return at;
 }
 
+/* ------------------------------------------------------ Gated DeltaNet */
+
+/* deltaSequential (src/delta-rule.ts:38-62): one head, token by token, in
+ * doubles. q, k [T][dk] (q already over sqrt(dk)), v [T][dv], beta and g
+ * (the log-decay) [T]; S [dk][dv] in and out; o [T][dv]. Per token, with
+ * a = exp(g): d = beta (v - a S^T k), S <- a S + k d^T, o = S^T q, the last
+ * taken as a S^T q + (q.k) d. */
+void orc_delta_sequential(int dk, int dv, int T, const double *q, const double *k,
+                          const double *v, const double *beta, const double *g, double *S,
+                          double *o) {
+  double *d = malloc(sizeof(double) * dv);
+  for (int t = 0; t < T; t++) {
+    const double *qt = q + (size_t)t * dk, *kt = k + (size_t)t * dk;
+    double a = exp(g[t]), qk = 0.0;
+    for (int i = 0; i < dk; i++) qk += qt[i] * kt[i];
+    for (int j = 0; j < dv; j++) {
+      double kv = 0.0, qs = 0.0;
+      for (int i = 0; i < dk; i++) {
+        kv += S[(size_t)i * dv + j] * kt[i];
+        qs += S[(size_t)i * dv + j] * qt[i];
+      }
+      d[j] = beta[t] * (v[(size_t)t * dv + j] - a * kv);
+      o[(size_t)t * dv + j] = a * qs + qk * d[j];
+    }
+    for (int i = 0; i < dk; i++)
+      for (int j = 0; j < dv; j++) S[(size_t)i * dv + j] = a * S[(size_t)i * dv + j] + kt[i] * d[j];
+  }
+  free(d);
+}
+
+/* deltaChunked (src/delta-rule.ts:73-166): the same recurrence in chunks of
+ * `chunk` tokens after a first chunk of `first` (0: chunk). Within a chunk
+ * of n tokens, G the running sum of g from its start:
+ *   A[r][s] = beta_r e^{G_r - G_s} k_r.k_s (s < r), T = (I + A)^-1,
+ *   U = T diag(beta) V, W = T diag(beta e^G) K, P[r][s] = e^{G_r - G_s} q_r.k_s
+ *   (s <= r), Oi = P U, Q' = e^G Q - P W;
+ * then from the chunk's starting state S0: D = U - W S0, O = Oi + Q' S0,
+ * S = e^{G_last} S0 + sum_s e^{G_last - G_s} k_s d_s^T. With save_at > 0 the
+ * state after token save_at (a chunk end) is copied to snap. This code is
+ * arranged chunk by chunk; the reference computes the state-free tensors
+ * for all chunks first, which changes no value. */
+void orc_delta_chunked(int dk, int dv, int T, const double *q, const double *k,
+                       const double *v, const double *beta, const double *g, double *S,
+                       double *o, int chunk, int first, int save_at, double *snap) {
+  if (first <= 0 || first > chunk) first = chunk;
+  const int C = chunk;
+  double *G = malloc(sizeof(double) * C), *A = calloc((size_t)C * C, sizeof(double));
+  double *Ti = calloc((size_t)C * C, sizeof(double)), *P = calloc((size_t)C * C, sizeof(double));
+  double *U = malloc(sizeof(double) * C * dv), *W = malloc(sizeof(double) * C * dk);
+  double *Oi = malloc(sizeof(double) * C * dv), *Qp = malloc(sizeof(double) * C * dk);
+  double *D = malloc(sizeof(double) * C * dv), *next = malloc(sizeof(double) * dk * dv);
+  for (int c0 = 0; c0 < T;) {
+    const int n = (c0 == 0 ? first : C) < T - c0 ? (c0 == 0 ? first : C) : T - c0;
+    const double *qc = q + (size_t)c0 * dk, *kc = k + (size_t)c0 * dk, *vc = v + (size_t)c0 * dv;
+    for (int r = 0; r < n; r++) G[r] = (r ? G[r - 1] : 0.0) + g[c0 + r];
+    for (int r = 0; r < n; r++)
+      for (int s = 0; s <= r; s++) {
+        double kk = 0.0, qk = 0.0;
+        for (int i = 0; i < dk; i++) {
+          kk += kc[(size_t)r * dk + i] * kc[(size_t)s * dk + i];
+          qk += qc[(size_t)r * dk + i] * kc[(size_t)s * dk + i];
+        }
+        const double e = exp(G[r] - G[s]);
+        A[r * C + s] = s < r ? beta[c0 + r] * e * kk : 0.0;
+        P[r * C + s] = e * qk;
+      }
+    /* forward substitution: row r of (I + A)^-1 from the rows above it */
+    for (int r = 0; r < n; r++)
+      for (int j = 0; j <= r; j++) {
+        double acc = j == r ? 1.0 : 0.0;
+        for (int s = j; s < r; s++) acc -= A[r * C + s] * Ti[s * C + j];
+        Ti[r * C + j] = acc;
+      }
+    for (int r = 0; r < n; r++) {
+      for (int j = 0; j < dv; j++) U[(size_t)r * dv + j] = 0.0;
+      for (int i = 0; i < dk; i++) W[(size_t)r * dk + i] = 0.0;
+      for (int s = 0; s <= r; s++) {
+        const double tb = Ti[r * C + s] * beta[c0 + s], eg = exp(G[s]);
+        for (int j = 0; j < dv; j++) U[(size_t)r * dv + j] += tb * vc[(size_t)s * dv + j];
+        for (int i = 0; i < dk; i++) W[(size_t)r * dk + i] += tb * eg * kc[(size_t)s * dk + i];
+      }
+    }
+    for (int r = 0; r < n; r++) {
+      const double eg = exp(G[r]);
+      for (int j = 0; j < dv; j++) Oi[(size_t)r * dv + j] = 0.0;
+      for (int i = 0; i < dk; i++) Qp[(size_t)r * dk + i] = eg * qc[(size_t)r * dk + i];
+      for (int s = 0; s <= r; s++) {
+        const double p = P[r * C + s];
+        for (int j = 0; j < dv; j++) Oi[(size_t)r * dv + j] += p * U[(size_t)s * dv + j];
+        for (int i = 0; i < dk; i++) Qp[(size_t)r * dk + i] -= p * W[(size_t)s * dk + i];
+      }
+    }
+    for (int r = 0; r < n; r++)
+      for (int j = 0; j < dv; j++) {
+        double ws = 0.0, qs = 0.0;
+        for (int i = 0; i < dk; i++) {
+          ws += W[(size_t)r * dk + i] * S[(size_t)i * dv + j];
+          qs += Qp[(size_t)r * dk + i] * S[(size_t)i * dv + j];
+        }
+        D[(size_t)r * dv + j] = U[(size_t)r * dv + j] - ws;
+        o[(size_t)(c0 + r) * dv + j] = Oi[(size_t)r * dv + j] + qs;
+      }
+    const double last = G[n - 1];
+    for (int i = 0; i < dk; i++)
+      for (int j = 0; j < dv; j++) {
+        double acc = exp(last) * S[(size_t)i * dv + j];
+        for (int s = 0; s < n; s++)
+          acc += exp(last - G[s]) * kc[(size_t)s * dk + i] * D[(size_t)s * dv + j];
+        next[(size_t)i * dv + j] = acc;
+      }
+    memcpy(S, next, sizeof(double) * dk * dv);
+    c0 += n;
+    if (snap && c0 == save_at) memcpy(snap, S, sizeof(double) * dk * dv);
+  }
+  free(G); free(A); free(Ti); free(P); free(U); free(W); free(Oi); free(Qp); free(D); free(next);
+}
+
+/* LIN_GATES (src/gpu/kernels.ts:1544-1562): from one row of the b|a
+ * projection (b of the H heads, then a), beta = sigmoid(b) and the
+ * log-decay A * softplus(a + dt_bias) (A = -exp(A_log), negative). */
+void orc_delta_gates(const float *ba, int ldba, int H, const float *A, const float *dt,
+                     double *beta, double *log_decay) {
+  (void)ldba;
+  for (int h = 0; h < H; h++) {
+    beta[h] = 1.0 / (1.0 + exp(-(double)ba[h]));
+    const double t = (double)ba[H + h] + dt[h];
+    const double softplus = (t > 0.0 ? t : 0.0) + log1p(exp(-fabs(t)));
+    log_decay[h] = (double)A[h] * softplus;
+  }
+}
+
+/* LIN_PREP (src/gpu/kernels.ts:1646-1665): one head's q or k over
+ * sqrt(sum of squares + 1e-6), q also over sqrt(dk). */
+void orc_delta_prep(const float *x, int dk, int is_q, double *out) {
+  double ss = 0.0;
+  for (int i = 0; i < dk; i++) ss += (double)x[i] * x[i];
+  const double inv = 1.0 / sqrt(ss + 1e-6) * (is_q ? 1.0 / sqrt((double)dk) : 1.0);
+  for (int i = 0; i < dk; i++) out[i] = x[i] * inv;
+}
+
+/* linearAttend's recurrence for M rows (src/engine.ts:6697-6815): each
+ * row's gates and q/k prep, then the delta rule per head, in doubles.
+ * qkv rows hold q (H dk) | k (H dk) | v (H dv), ba rows b (H) | a (H);
+ * state [H][dk][dv] in and out; snap (if save_at in 1..M) the state after
+ * row save_at; out [M][H dv]. */
+void orc_delta_rule(const float *qkv, int ldq, const float *ba, int ldba, const float *A,
+                    const float *dt, int H, int dk, int dv, int M, double *state, int save_at,
+                    double *snap, double *out) {
+  const int K = H * dk;
+  double *q = malloc(sizeof(double) * dk), *k = malloc(sizeof(double) * dk);
+  double *v = malloc(sizeof(double) * dv), *o = malloc(sizeof(double) * dv);
+  double *beta = malloc(sizeof(double) * H), *lg = malloc(sizeof(double) * H);
+  for (int m = 0; m < M; m++) {
+    const float *row = qkv + (size_t)m * ldq;
+    orc_delta_gates(ba + (size_t)m * ldba, ldba, H, A, dt, beta, lg);
+    for (int h = 0; h < H; h++) {
+      orc_delta_prep(row + (size_t)h * dk, dk, 1, q);
+      orc_delta_prep(row + K + (size_t)h * dk, dk, 0, k);
+      for (int j = 0; j < dv; j++) v[j] = row[2 * K + (size_t)h * dv + j];
+      orc_delta_sequential(dk, dv, 1, q, k, v, beta + h, lg + h,
+                           state + (size_t)h * dk * dv, o);
+      for (int j = 0; j < dv; j++) out[(size_t)m * H * dv + (size_t)h * dv + j] = o[j];
+    }
+    if (snap && m + 1 == save_at) memcpy(snap, state, sizeof(double) * H * dk * dv);
+  }
+  free(q); free(k); free(v); free(o); free(beta); free(lg);
+}
+
+/* LIN_CONV + LIN_CONV_STATE (src/gpu/kernels.ts:1564-1641): silu of the
+ * depthwise causal convolution over the first C channels of each input
+ * row (w [C][W], tap W-1 the current token), earlier tokens from state
+ * [W-1][C] (oldest first); state_out = the last W-1 raw input rows. */
+void orc_delta_conv(const float *in, int ldi, int M, int C, int W, const float *w,
+                    const float *state, double *out, float *state_out) {
+  for (int m = 0; m < M; m++)
+    for (int c = 0; c < C; c++) {
+      double acc = 0.0;
+      for (int k = 0; k < W; k++) {
+        const int t = m - (W - 1) + k;
+        const double x = t >= 0 ? in[(size_t)t * ldi + c] : state[(size_t)(W - 1 + t) * C + c];
+        acc += (double)w[(size_t)c * W + k] * x;
+      }
+      out[(size_t)m * C + c] = acc / (1.0 + exp(-acc));
+    }
+  for (int i = 0; i < W - 1; i++)
+    for (int c = 0; c < C; c++) {
+      const int t = M - (W - 1) + i;
+      state_out[(size_t)i * C + c] =
+          t >= 0 ? in[(size_t)t * ldi + c] : state[(size_t)(M + i) * C + c];
+    }
+}
+
+/* LIN_NORM (src/gpu/kernels.ts:1836-1860): each head's output over its
+ * RMS (eps inside), times the shared weights w [dv] and silu(z). */
+void orc_delta_norm(const float *o, int ldo, int M, int H, int dv, const float *z, int ldz,
+                    const float *w, float eps, double *out) {
+  for (int m = 0; m < M; m++)
+    for (int h = 0; h < H; h++) {
+      const float *oh = o + (size_t)m * ldo + (size_t)h * dv;
+      const float *zh = z + (size_t)m * ldz + (size_t)h * dv;
+      double ss = 0.0;
+      for (int j = 0; j < dv; j++) ss += (double)oh[j] * oh[j];
+      const double inv = 1.0 / sqrt(ss / dv + (double)eps);
+      for (int j = 0; j < dv; j++)
+        out[(size_t)m * H * dv + (size_t)h * dv + j] =
+            oh[j] * inv * w[j] * (zh[j] / (1.0 + exp(-(double)zh[j])));
+    }
+}
+
 double orc_now(void) {
   struct timespec ts;
   clock_gettime(CLOCK_MONOTONIC, &ts);

@@ -123,6 +123,26 @@ void orc_pick_candidates(const float *logits, int M, int V, const uint8_t *mask,
                          float presence, const uint32_t *allowed, int allowed_rows,
                          int ld_allowed, int count, int32_t *chunks_out, float *cand_out);
 
+/* ---- Gated DeltaNet (delta-rule.ts:38-166; kernels.ts:1544-1862) ---- */
+void orc_delta_sequential(int dk, int dv, int T, const double *q, const double *k,
+                          const double *v, const double *beta, const double *g, double *S,
+                          double *o);                               /* delta-rule.ts:38-62 */
+void orc_delta_chunked(int dk, int dv, int T, const double *q, const double *k,
+                       const double *v, const double *beta, const double *g, double *S,
+                       double *o, int chunk, int first, int save_at, double *snap);
+                                                                   /* delta-rule.ts:73-166 */
+void orc_delta_gates(const float *ba, int ldba, int H, const float *A, const float *dt,
+                     double *beta, double *log_decay);            /* kernels.ts:1544-1562 */
+void orc_delta_prep(const float *x, int dk, int is_q, double *out); /* kernels.ts:1646-1665 */
+void orc_delta_rule(const float *qkv, int ldq, const float *ba, int ldba, const float *A,
+                    const float *dt, int H, int dk, int dv, int M, double *state, int save_at,
+                    double *snap, double *out);
+void orc_delta_conv(const float *in, int ldi, int M, int C, int W, const float *w,
+                    const float *state, double *out, float *state_out);
+                                                                   /* kernels.ts:1564-1641 */
+void orc_delta_norm(const float *o, int ldo, int M, int H, int dv, const float *z, int ldz,
+                    const float *w, float eps, double *out);     /* kernels.ts:1836-1860 */
+
 /* ---- greedy pick (kernels.ts:3169-3246) ---- */
 int orc_argmax(const float *logits, int V, float *top);
 

@@ -455,3 +455,82 @@ def q4k_blocks(seed: int, supers: int, zero_scale: bool = False) -> np.ndarray:
         for i in range(128):
             b[p + 16 + i] = int(rand() * 256)
     return b
+
+
+# --- Gated DeltaNet (src/delta-rule.ts:38-166, src/gpu/kernels.ts:1544-1862) ---
+
+_lib.orc_delta_sequential.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P]
+_lib.orc_delta_chunked.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P]
+_lib.orc_delta_rule.argtypes = [_P, _I, _P, _I, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P]
+_lib.orc_delta_conv.argtypes = [_P, _I, _I, _I, _I, _P, _P, _P, _P]
+_lib.orc_delta_norm.argtypes = [_P, _I, _I, _I, _I, _P, _I, _P, C.c_float, _P]
+
+
+def _f64(a):
+    return np.ascontiguousarray(a, dtype=np.float64)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def delta_sequential(q, k, v, beta, g, state):
+    """deltaSequential: one head's (outputs [T][dv], new state [dk][dv])."""
+    q, k, v, beta, g = map(_f64, (q, k, v, beta, g))
+    T, dk = q.shape
+    dv = v.shape[1]
+    S = _f64(state).copy()
+    o = np.empty((T, dv))
+    _lib.orc_delta_sequential(dk, dv, T, _ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(g),
+                              _ptr(S), _ptr(o))
+    return o, S
+
+
+def delta_chunked(q, k, v, beta, g, state, chunk, first=0, save_at=0):
+    """deltaChunked: (outputs, new state, the state after token save_at or None)."""
+    q, k, v, beta, g = map(_f64, (q, k, v, beta, g))
+    T, dk = q.shape
+    dv = v.shape[1]
+    S = _f64(state).copy()
+    o = np.empty((T, dv))
+    snap = np.full((dk, dv), np.nan) if save_at else None
+    _lib.orc_delta_chunked(dk, dv, T, _ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(g), _ptr(S),
+                           _ptr(o), chunk, first, save_at, _ptr(snap))
+    return o, S, snap
+
+
+def delta_rule(qkv, ba, A, dt, heads, key_dim, value_dim, state, save_at=0):
+    """The recurrence of a Gated DeltaNet layer over M rows (gates, q/k prep,
+    the delta rule per head), as wg_delta_rule: (out [M][H dv] float64,
+    state [H][dk][dv] float64, the state after row save_at or None)."""
+    qkv, ba, A, dt = map(_f32, (qkv, ba, A, dt))
+    M = qkv.shape[0]
+    S = _f64(state).copy()
+    out = np.empty((M, heads * value_dim))
+    snap = np.full(S.shape, np.nan) if save_at else None
+    _lib.orc_delta_rule(_ptr(qkv), qkv.shape[1], _ptr(ba), ba.shape[1], _ptr(A), _ptr(dt),
+                        heads, key_dim, value_dim, M, _ptr(S), save_at, _ptr(snap), _ptr(out))
+    return out, S, snap
+
+
+def delta_conv(inp, channels, weights, state):
+    """silu(causal depthwise conv) of the first `channels` of each row:
+    (out [M][C] float64, the new state [W-1][C] float32)."""
+    inp, weights, state = map(_f32, (inp, weights, state))
+    M = inp.shape[0]
+    W = weights.shape[1]
+    out = np.empty((M, channels))
+    new_state = np.empty((W - 1, channels), np.float32)
+    _lib.orc_delta_conv(_ptr(inp), inp.shape[1], M, channels, W, _ptr(weights), _ptr(state),
+                        _ptr(out), _ptr(new_state))
+    return out, new_state
+
+
+def delta_norm(o, heads, value_dim, z, weights, eps):
+    """The gated RMSNorm of each head's output (float64 [M][H dv])."""
+    o, z, weights = map(_f32, (o, z, weights))
+    M = o.shape[0]
+    out = np.empty((M, heads * value_dim))
+    _lib.orc_delta_norm(_ptr(o), o.shape[1], M, heads, value_dim, _ptr(z), z.shape[1],
+                        _ptr(weights), eps, _ptr(out))
+    return out

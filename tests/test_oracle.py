@@ -695,3 +695,160 @@ def test_pick_candidates_hold_the_top_k():
         assert all(int(t) // 256 in kept for t in top)
         got = np.sort(cand[m].reshape(-1))[::-1][:count]
         assert np.array_equal(got, np.sort(logits[m])[::-1][:count])
+
+
+# --- Gated DeltaNet (src/delta-rule.test.ts) ----------------------------------
+
+def _delta_inputs(seed, dk, dv, tokens, similar=0.0, decay=0.2):
+    """src/delta-rule.test.ts:23-53: unit q (over sqrt(dk)) and k, beta in
+    (0, 1), log-decays -decay * softplus(normal), from mulberry32."""
+    rand = O.Mulberry32(seed)
+
+    def normal():
+        u = max(rand(), 1e-12)
+        return math.sqrt(-2 * math.log(u)) * math.cos(2 * math.pi * rand())
+    shared = [normal() for _ in range(dk)]
+
+    def unit(scale):
+        x = np.array([similar * shared[i] + normal() for i in range(dk)])
+        return x / math.hypot(*x) * scale
+    q = np.zeros((tokens, dk))
+    k = np.zeros((tokens, dk))
+    v = np.zeros((tokens, dv))
+    beta = np.zeros(tokens)
+    g = np.zeros(tokens)
+    for t in range(tokens):
+        q[t] = unit(1 / math.sqrt(dk))
+        k[t] = unit(1)
+        v[t] = [normal() for _ in range(dv)]
+        beta[t] = 1 / (1 + math.exp(-2 * normal()))
+        g[t] = -decay * math.log(1 + math.exp(normal()))
+    return q, k, v, beta, g
+
+
+def _random_state(seed, dk, dv):
+    rand = O.Mulberry32(seed)
+    return np.array([rand() - 0.5 for _ in range(dk * dv)]).reshape(dk, dv)
+
+
+def _rel(a, b):
+    return np.max(np.abs(a - b)) / np.max(np.abs(b))
+
+
+@pytest.mark.parametrize("tokens,chunk", [(64, 16), (64, 32), (50, 16), (37, 32), (5, 16),
+                                          (1, 16), (96, 64)])
+def test_delta_chunked_matches_sequential(tokens, chunk):
+    # src/delta-rule.test.ts:70-92
+    x = _delta_inputs(tokens * 31 + chunk, 16, 12, tokens)
+    s0 = _random_state(tokens + chunk, 16, 12)
+    o1, s1 = O.delta_sequential(*x, s0)
+    o2, s2, _ = O.delta_chunked(*x, s0, chunk)
+    assert _rel(o2, o1) < 1e-10 and _rel(s2, s1) < 1e-10
+
+
+def test_delta_collinear_keys_and_fast_decay():
+    # src/delta-rule.test.ts:94-113
+    x = _delta_inputs(7, 32, 8, 64, similar=6, decay=0.01)
+    s0 = _random_state(8, 32, 8)
+    o1, s1 = O.delta_sequential(*x, s0)
+    o2, s2, _ = O.delta_chunked(*x, s0, 32)
+    assert _rel(o2, o1) < 1e-8 and _rel(s2, s1) < 1e-8
+    x = _delta_inputs(9, 16, 8, 48, decay=20)
+    s0 = _random_state(10, 16, 8)
+    o1, s1 = O.delta_sequential(*x, s0)
+    o2, s2, _ = O.delta_chunked(*x, s0, 16)
+    assert np.all(np.isfinite(o2)) and _rel(o2, o1) < 1e-10 and _rel(s2, s1) < 1e-10
+
+
+@pytest.mark.parametrize("tokens,save_at", [(50, 7), (50, 39), (64, 1), (37, 31), (5, 3)])
+def test_delta_chunk_ends_at_the_snapshot(tokens, save_at):
+    # src/delta-rule.test.ts:115-141: a shorter first chunk so that one ends at save_at
+    first = save_at % 16 or 16
+    x = _delta_inputs(tokens * 7 + save_at, 16, 12, tokens)
+    s0 = _random_state(tokens + save_at, 16, 12)
+    o1, s1 = O.delta_sequential(*x, s0)
+    o2, s2, snap = O.delta_chunked(*x, s0, 16, first=first, save_at=save_at)
+    assert _rel(o2, o1) < 1e-10 and _rel(s2, s1) < 1e-10
+    _, prefix = O.delta_sequential(*(a[:save_at] for a in x), s0)
+    assert _rel(snap, prefix) < 1e-10
+
+
+def test_delta_chunked_then_token_steps():
+    # src/delta-rule.test.ts:143-165
+    x = _delta_inputs(11, 16, 16, 40)
+    s0 = _random_state(12, 16, 16)
+    _, after, _ = O.delta_chunked(*(a[:33] for a in x), s0, 16)
+    o_rest, s_rest = O.delta_sequential(*(a[33:] for a in x), after)
+    o_all, s_all = O.delta_sequential(*x, s0)
+    assert _rel(o_rest, o_all[33:]) < 1e-10 and _rel(s_rest, s_all) < 1e-10
+
+
+def test_delta_rule_closed_forms():
+    """The delta rule's defining facts: with a = 1, beta = 1 and a unit key,
+    the new state reads v back (S'^T k = v); the output is the new state
+    read by q (o = S'^T q); with beta = 0 the state only decays."""
+    rng = np.random.default_rng(0)
+    dk, dv = 8, 5
+    S = rng.standard_normal((dk, dv))
+    k = rng.standard_normal(dk)
+    k /= np.linalg.norm(k)
+    q = rng.standard_normal(dk)
+    v = rng.standard_normal(dv)
+    o, S1 = O.delta_sequential(q[None], k[None], v[None], [1.0], [0.0], S)
+    assert np.allclose(S1.T @ k, v, atol=1e-12)
+    assert np.allclose(o[0], S1.T @ q, atol=1e-12)
+    o, S2 = O.delta_sequential(q[None], k[None], v[None], [0.0], [math.log(0.25)], S)
+    assert np.allclose(S2, 0.25 * S, atol=1e-15) and np.allclose(o[0], 0.25 * S.T @ q)
+
+
+def test_delta_layer_gates_prep_conv_norm():
+    """LIN_GATES: sigmoid(0) = 1/2, softplus(0) = ln 2, softplus(t) -> t for
+    large t, the log-decay A * softplus. LIN_PREP: unit k, q of norm
+    1/sqrt(dk) (up to the 1e-6 inside the root). orc_delta_rule composes
+    these with the sequential rule head by head. LIN_CONV: taps
+    (0, ..., 0, 1) give silu(x); a batch split in two through the carried
+    state equals the whole batch. LIN_NORM: a constant head output c gives
+    c / sqrt(c^2 + eps) * w * silu(z)."""
+    H, dk, dv = 2, 4, 3
+    ba = np.array([[0.0, 3.0, 0.0, 40.0]], np.float32)
+    A = np.array([-0.5, -2.0], np.float32)
+    dt = np.zeros(2, np.float32)
+    rng = np.random.default_rng(1)
+    qkv = rng.standard_normal((1, 2 * H * dk + H * dv)).astype(np.float32)
+    S0 = rng.standard_normal((H, dk, dv))
+    out, S1, _ = O.delta_rule(qkv, ba, A, dt, H, dk, dv, S0)
+    betas = [0.5, 1 / (1 + math.exp(-3.0))]
+    logs = [-0.5 * math.log(2.0), -2.0 * 40.0]
+    for h in range(H):
+        q = qkv[0, h * dk:(h + 1) * dk].astype(np.float64)
+        k = qkv[0, H * dk + h * dk:H * dk + (h + 1) * dk].astype(np.float64)
+        v = qkv[0, 2 * H * dk + h * dv:2 * H * dk + (h + 1) * dv]
+        qh = q / math.sqrt(q @ q + 1e-6) / math.sqrt(dk)
+        kh = k / math.sqrt(k @ k + 1e-6)
+        assert abs(np.linalg.norm(kh) - 1) < 1e-5
+        o, S = O.delta_sequential(qh[None], kh[None], v[None], [betas[h]], [logs[h]], S0[h])
+        assert np.allclose(out[0, h * dv:(h + 1) * dv], o[0], rtol=1e-12, atol=1e-12)
+        assert np.allclose(S1[h], S, rtol=1e-12, atol=1e-12)
+    # the convolution
+    M, C, W = 6, 5, 4
+    x = rng.standard_normal((M, C + 3)).astype(np.float32)
+    st = rng.standard_normal((W - 1, C)).astype(np.float32)
+    taps = np.zeros((C, W), np.float32)
+    taps[:, -1] = 1
+    y, _ = O.delta_conv(x, C, taps, st)
+    xs = x[:, :C].astype(np.float64)
+    assert np.allclose(y, xs / (1 + np.exp(-xs)), rtol=1e-14)
+    taps = rng.standard_normal((C, W)).astype(np.float32)
+    y, s_all = O.delta_conv(x, C, taps, st)
+    y1, s1 = O.delta_conv(x[:2], C, taps, st)
+    y2, s2 = O.delta_conv(x[2:], C, taps, s1)
+    assert np.array_equal(np.vstack([y1, y2]), y) and np.array_equal(s2, s_all)
+    assert np.array_equal(s_all, x[M - 3:, :C])
+    # the gated norm
+    o = np.full((1, H * dv), 0.75, np.float32)
+    z = rng.standard_normal((1, H * dv)).astype(np.float32)
+    w = rng.standard_normal(dv).astype(np.float32)
+    got = O.delta_norm(o, H, dv, z, w, 1e-6)
+    zz = z[0].astype(np.float64)
+    want = 0.75 / math.sqrt(0.75 ** 2 + float(np.float32(1e-6))) * np.tile(w, H) * zz / (1 + np.exp(-zz))
+    assert np.allclose(got[0], want, rtol=1e-12)

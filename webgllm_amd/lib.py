@@ -71,6 +71,11 @@ class AttnShape(C.Structure):
                 ("rotated_dims", C.c_int32), ("eps", C.c_float), ("use_norm", C.c_int32)]
 
 
+class DeltaShape(C.Structure):
+    """wg_delta_shape."""
+    _fields_ = [("heads", C.c_int32), ("key_dim", C.c_int32), ("value_dim", C.c_int32)]
+
+
 class GgufTensorInfo(C.Structure):
     """wg_gguf_tensor_info."""
     _fields_ = [("name", C.c_char_p), ("n_dims", C.c_int32), ("dims", C.c_int64 * 4),
@@ -183,6 +188,11 @@ def load():
         "wg_pick_scratch_bytes": (SZ, [I32, I32]),
         "wg_pick_candidates": (C.c_int, [P, I32, I32, I32, P, P, I32, I32, C.c_float,
                                          C.c_float, P, I32, I32, I32, P, P, P, SZ, P]),
+        "wg_delta_rule": (C.c_int, [P, I32, I32, P, I32, P, P, C.POINTER(DeltaShape), P, P, I32,
+                                    P, I32, P]),
+        "wg_delta_conv": (C.c_int, [P, I32, I32, I32, I32, P, P, P, P, I32, P]),
+        "wg_delta_norm": (C.c_int, [P, I32, I32, C.POINTER(DeltaShape), P, I32, P, C.c_float, P,
+                                    I32, P]),
         "wg_decode_plan_create": (C.c_int, [C.POINTER(DecodeLayer), I32, C.POINTER(P)]),
         "wg_decode_run": (C.c_int, [P, P]),
         "wg_decode_status": (C.c_int, [P]),

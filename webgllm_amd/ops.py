@@ -32,6 +32,17 @@ def _dev(t: torch.Tensor, dtype=None) -> torch.Tensor:
     return t
 
 
+def _rows(t: torch.Tensor, dtype=torch.float32) -> torch.Tensor:
+    """A device matrix whose rows may be strided (a view of wider rows)."""
+    if not t.is_cuda:
+        raise ValueError("expected a device tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"expected {dtype}, got {t.dtype}")
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError("expected a matrix with unit column stride")
+    return t
+
+
 def to_device_bytes(b, device="cuda") -> torch.Tensor:
     """Host bytes (numpy / bytes) as a uint8 device tensor."""
     arr = np.frombuffer(b, dtype=np.uint8) if isinstance(b, (bytes, bytearray)) else \
@@ -451,3 +462,58 @@ def pick_candidates(logits: torch.Tensor, count: int, mask: torch.Tensor | None 
         0 if allowed is None else allowed.shape[1], count, _p(chunks), _p(cand), _p(scratch),
         scratch.numel(), _stream()))
     return chunks, cand
+
+
+# ------------------------------------------------------------- Gated DeltaNet
+
+def delta_rule(qkv: torch.Tensor, ba: torch.Tensor, A: torch.Tensor, dt_bias: torch.Tensor,
+               heads: int, key_dim: int, value_dim: int, state: torch.Tensor,
+               save_at: int = 0, snapshot: torch.Tensor | None = None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """A Gated DeltaNet layer's recurrence over the rows of qkv [M, >= 2 H dk
+    + H dv] (q | k | v after the convolution) and ba [M, >= 2 H] (b | a):
+    out [M, H dv] float32; state [H, dk, dv] float32 is updated in place, and
+    with save_at in 1..M the state after that row goes to snapshot
+    (wg_delta_rule)."""
+    qkv, ba = _rows(qkv), _rows(ba)
+    _dev(A, torch.float32), _dev(dt_bias, torch.float32), _dev(state, torch.float32)
+    M = qkv.shape[0]
+    if out is None:
+        out = torch.empty((M, heads * value_dim), dtype=torch.float32, device=qkv.device)
+    if save_at and snapshot is None:
+        snapshot = torch.empty_like(state)
+    shape = L.DeltaShape(heads, key_dim, value_dim)
+    L.check(L.load().wg_delta_rule(_p(qkv), M, qkv.stride(0), _p(ba), ba.stride(0), _p(A),
+                                   _p(dt_bias), C.byref(shape), _p(state), _p(snapshot),
+                                   save_at, _p(out), out.stride(0), _stream()))
+    return (out, snapshot) if save_at else out
+
+
+def delta_conv(inp: torch.Tensor, channels: int, taps: torch.Tensor, state: torch.Tensor,
+               state_out: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu of the causal depthwise convolution over the first `channels`
+    of each row of inp (taps [C, W], state [W-1, C] -> state_out): out
+    [M, C] float32 (wg_delta_conv)."""
+    inp = _rows(inp)
+    M, W = inp.shape[0], taps.shape[1]
+    if out is None:
+        out = torch.empty((M, channels), dtype=torch.float32, device=inp.device)
+    L.check(L.load().wg_delta_conv(_p(inp), M, inp.stride(0), channels, W,
+                                   _p(_dev(taps, torch.float32)), _p(state), _p(state_out),
+                                   _p(out), out.stride(0), _stream()))
+    return out
+
+
+def delta_norm(o: torch.Tensor, heads: int, value_dim: int, z: torch.Tensor,
+               weight: torch.Tensor, eps: float, out16: torch.Tensor | None = None):
+    """The gated RMSNorm of each head's output, as halves for out_proj
+    (wg_delta_norm): float16 [M, H dv]."""
+    o, z = _rows(o), _rows(z)
+    M = o.shape[0]
+    if out16 is None:
+        out16 = torch.empty((M, heads * value_dim), dtype=torch.float16, device=o.device)
+    shape = L.DeltaShape(heads, 0, value_dim)
+    L.check(L.load().wg_delta_norm(_p(o), M, o.stride(0), C.byref(shape), _p(z), z.stride(0),
+                                   _p(_dev(weight, torch.float32)), eps, _p(out16),
+                                   out16.stride(0), _stream()))
+    return out16
