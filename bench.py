@@ -742,8 +742,89 @@ def workload_sample_pick(args):
                 reps, 20, ms, cfg, roof, cpu, higher_is_better=False)
 
 
+def workload_delta_rule(args):
+    """A Qwen3.5-shaped Gated DeltaNet layer's recurrence (16 heads, key and
+    value dims 128): wg_delta_rule for one decode row, cycling over 320
+    layers' states (320 MB, past the 256 MB MALL, so every launch reads its
+    state from HBM); also a 2048-row prompt batch in one launch.
+    Microseconds a decode row."""
+    import ctypes as C
+    import torch
+    from webgllm_amd import lib as L
+    H, dk, dv = 16, 128, 128
+    K, V = H * dk, H * dv
+    layers = 320
+    g = torch.Generator(device="cuda").manual_seed(5)
+    states = torch.randn((layers, H, dk, dv), device="cuda", generator=g) * 0.1
+    qkv = torch.randn((2048, 2 * K + V), device="cuda", generator=g)
+    ba = torch.randn((2048, 2 * H), device="cuda", generator=g)
+    A = -torch.rand(H, device="cuda", generator=g) - 0.5
+    dt = torch.randn(H, device="cuda", generator=g) * 0.5
+    out = torch.empty((2048, V), device="cuda")
+    lib = L.load()
+    shape = L.DeltaShape(H, dk, dv)
+
+    def launch(st, M, stream):
+        L.check(lib.wg_delta_rule(qkv.data_ptr(), M, qkv.stride(0), ba.data_ptr(), ba.stride(0),
+                                  A.data_ptr(), dt.data_ptr(), C.byref(shape), st.data_ptr(),
+                                  None, 0, out.data_ptr(), out.stride(0), stream))
+    # One decode row for each of the 320 layers' states, captured in a graph
+    # so that the host's call overhead is not what gets timed.
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch(states[0], 1, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        cur = torch.cuda.current_stream().cuda_stream
+        for layer in range(layers):
+            launch(states[layer], 1, cur)
+    for _ in range(2):
+        graph.replay()
+    reps = max(4, args.steps // 8)
+    ms = timed(graph.replay, reps) / layers
+    state_bytes = H * dk * dv * 4
+    algo = 2 * state_bytes + (2 * K + V) * 4 + 2 * H * 4 + V * 4  # state in and out, row, out
+    gbps = algo / (ms * 1e-3) / 1e9
+    cur = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        launch(states[0], 2048, cur)
+    pf_ms = timed(lambda: launch(states[0], 2048, cur), 10)
+    L.check(lib.wg_tuning_set(b"delta_narrow_rows", 4096))  # 16-column workgroups at 2048
+    pf_narrow_ms = timed(lambda: launch(states[0], 2048, cur), 10)
+    L.check(lib.wg_tuning_set(b"delta_narrow_rows", 16))
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        q1, b1 = qkv[:1].cpu().numpy(), ba[:1].cpu().numpy()
+        a1, d1, s1 = A.cpu().numpy(), dt.cpu().numpy(), states[0].cpu().numpy()
+        spent, k = 0.0, 0
+        while spent < 5.0 or k < 2:
+            t1 = O.now()
+            O.delta_rule(q1, b1, a1, d1, H, dk, dv, s1)
+            spent += O.now() - t1
+            k += 1
+        cpu = {"value": round(spent / k * 1e6, 1), "unit": "us", "cores": 1, "kind": "port",
+               "sample": f"oracle restatement of the recurrence for one row (float64, one "
+                         f"thread), {k} repetitions ({spent:.1f} s)"}
+    roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+            "kernel": "delta_rule_kernel<16> (one row, 16 heads of 128, state from HBM)",
+            "bytes_per_launch": algo, "avg_launch_us": round(ms * 1e3, 2),
+            "launches": reps * layers}
+    cfg = {"workload": "Gated DeltaNet recurrence of one Qwen3.5-shaped layer (16 heads, "
+                       "key/value dims 128), one decode row", "heads": H, "key_dim": dk,
+           "value_dim": dv, "prompt_rows": 2048, "prompt_ms": round(pf_ms, 3),
+           "prompt_rows_per_s": round(2048 / (pf_ms * 1e-3)),
+           "prompt_ms_16_column_workgroups": round(pf_narrow_ms, 3), "parallelism": "none"}
+    return line("Gated DeltaNet recurrence us a decode row (16 heads of 128)",
+                round(ms * 1e3, 2), "us", reps * layers, 3 * layers, ms, cfg, roof, cpu,
+                higher_is_better=False)
+
+
 WORKLOADS = {"q4_0-gemv": workload_q4_0_gemv, "nbits-gemm": workload_nbits_gemm,
-             "sample-pick": workload_sample_pick,
+             "sample-pick": workload_sample_pick, "delta-rule": workload_delta_rule,
              "gguf-load": workload_gguf_load,
              "q8-gemm": lambda args: workload_nbits_gemm(args, "q8"),
              "q6_k-head": workload_q6_k_head, "q8-gemv": workload_q8_gemv,

@@ -10,11 +10,12 @@
 // batch of rows in one launch (LIN_GATES + LIN_PREP + LIN_DELTA + LIN_STATE
 // per token, or LIN_DELTA_FUSED at one). The columns of a head's state are
 // independent given q^, k^ and the gates, so a workgroup takes one head and
-// 64 state columns (one a lane) and its 8 waves split the dk rows: each
-// lane keeps its dk / 8 state values in registers for the whole batch, so
-// the state is read and written once a launch, whatever the row count.
-// Per token, two barriers: one after q, k and the gates are in LDS, one
-// after each wave's partial S^T k^ and S^T q^ are.
+// CB state columns (16 for short batches, 64 for long ones), and the 512 / CB
+// threads of a column split its dk rows: each thread keeps its rows' state
+// values in registers for the whole batch, so the state is read and written
+// once a launch, whatever the row count. Per row, two barriers that wait on
+// LDS only: one after q, k and the gates are in LDS, one after the partial
+// S^T k^ and S^T q^ are; the next row's inputs load across them.
 #include "common.h"
 #include "epilogue.h"
 
@@ -45,49 +46,77 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
-template <int ROWS>
+// A workgroup barrier that waits for this wave's LDS operations only: the
+// next row's global loads, issued before it, stay in flight across it.
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One row's inputs for this thread: q[t], k[t] (threads t < MAX_DK), v at
+// this thread's column, b and a of the head (thread MAX_DK).
+struct RowIn {
+  float q, k, v, b, a;
+};
+
+__device__ inline RowIn load_row(const DeltaArgs &a, int m, int h, int j, bool col) {
+  const float *row = a.qkv + (int64_t)m * a.ldq;
+  const int t = threadIdx.x, K = a.H * a.dk;
+  RowIn r{0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  if (t < a.dk) {
+    r.q = row[h * a.dk + t];
+    r.k = row[K + h * a.dk + t];
+  } else if (t == MAX_DK) {
+    const float *g = a.ba + (int64_t)m * a.ldba;
+    r.b = g[h];
+    r.a = g[a.H + h];
+  }
+  if (col) r.v = row[2 * K + h * a.dv + j];
+  return r;
+}
+
+// CB state columns a workgroup, one a thread; the 512 / CB threads of a
+// column split its dk rows, ROWS each.
+template <int ROWS, int CB>
 __global__ __launch_bounds__(64 * DW) void delta_rule_kernel(DeltaArgs a) {
-  static_assert(ROWS * DW <= MAX_DK, "rows a lane");
-  // By token parity, so a token's writes never meet the previous token's reads.
+  constexpr int RG = 64 * DW / CB;  // row groups
+  static_assert(ROWS * RG <= MAX_DK, "rows a thread");
+  // By row parity, so a row's writes never meet the previous row's reads.
   __shared__ float qn[2][MAX_DK], kn[2][MAX_DK];  // raw q, k (0 past dk)
   __shared__ float part[2][3][4];                 // sums of q^2, k^2, q k per wave
   __shared__ float gate[2][2];                    // beta, decay
-  __shared__ float redk[2][DW][64], redq[2][DW][64];
+  __shared__ float redk[2][DW][CB], redq[2][DW][CB];
   const int h = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int j = blockIdx.x * 64 + lane;
+  const int c = threadIdx.x % CB, rg = threadIdx.x / CB;
+  const int j = blockIdx.x * CB + c;
   const bool col = j < a.dv;
-  const int i0 = w * ROWS;
-  const int K = a.H * a.dk;
+  const int i0 = rg * ROWS;
   const float scale = 1.0f / sqrtf((float)a.dk);
   float *Sh = a.state + (int64_t)h * a.dk * a.dv;
   float s[ROWS];
 #pragma unroll
   for (int r = 0; r < ROWS; r++)
     s[r] = col && i0 + r < a.dk ? Sh[(int64_t)(i0 + r) * a.dv + j] : 0.0f;
+  RowIn in = load_row(a, 0, h, j, col);
   for (int m = 0; m < a.M; m++) {
     const int p = m & 1;
-    const float *row = a.qkv + (int64_t)m * a.ldq;
     const int t = threadIdx.x;
     if (t < MAX_DK) {  // waves 0-3: the head's q and k, their squares and products
-      const float qv = t < a.dk ? row[h * a.dk + t] : 0.0f;
-      const float kv = t < a.dk ? row[K + h * a.dk + t] : 0.0f;
-      qn[p][t] = qv;
-      kn[p][t] = kv;
-      const float x0 = wave_sum(qv * qv), x1 = wave_sum(kv * kv), x2 = wave_sum(qv * kv);
+      qn[p][t] = in.q;
+      kn[p][t] = in.k;
+      const float x0 = wave_sum(in.q * in.q), x1 = wave_sum(in.k * in.k);
+      const float x2 = wave_sum(in.q * in.k);
       if (lane == 0) {
         part[p][0][w] = x0;
         part[p][1][w] = x1;
         part[p][2][w] = x2;
       }
     } else if (t == MAX_DK) {  // LIN_GATES for this head
-      const float *g = a.ba + (int64_t)m * a.ldba;
-      const float x = g[a.H + h] + a.dt[h];
+      const float x = in.a + a.dt[h];
       const float softplus = fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
-      gate[p][0] = 1.0f / (1.0f + expf(-g[h]));
+      gate[p][0] = 1.0f / (1.0f + expf(-in.b));
       gate[p][1] = expf(a.A[h] * softplus);
     }
-    const float vj = col ? row[2 * K + h * a.dv + j] : 0.0f;
-    __syncthreads();
+    const float vj = in.v;
+    if (m + 1 < a.M) in = load_row(a, m + 1, h, j, col);
+    lds_barrier();
     const float sq = part[p][0][0] + part[p][0][1] + part[p][0][2] + part[p][0][3];
     const float sk = part[p][1][0] + part[p][1][1] + part[p][1][2] + part[p][1][3];
     const float sqk = part[p][2][0] + part[p][2][1] + part[p][2][2] + part[p][2][3];
@@ -98,18 +127,25 @@ __global__ __launch_bounds__(64 * DW) void delta_rule_kernel(DeltaArgs a) {
       pk = fmaf(s[r], kn[p][i0 + r], pk);
       pq = fmaf(s[r], qn[p][i0 + r], pq);
     }
-    redk[p][w][lane] = pk * invk;
-    redq[p][w][lane] = pq * invq;
-    __syncthreads();
+#pragma unroll
+    for (int off = CB; off < 64; off <<= 1) {  // the wave's row groups of this column
+      pk += __shfl_xor(pk, off, 64);
+      pq += __shfl_xor(pq, off, 64);
+    }
+    if (lane < CB) {
+      redk[p][w][c] = pk * invk;
+      redq[p][w][c] = pq * invq;
+    }
+    lds_barrier();
     float kvs = 0.0f, qss = 0.0f;
 #pragma unroll
     for (int u = 0; u < DW; u++) {
-      kvs += redk[p][u][lane];
-      qss += redq[p][u][lane];
+      kvs += redk[p][u][c];
+      qss += redq[p][u][c];
     }
     const float beta = gate[p][0], decay = gate[p][1];
     const float d = beta * (vj - decay * kvs);
-    if (w == 0 && col)
+    if (rg == 0 && col)
       a.out[(int64_t)m * a.ldo + h * a.dv + j] = decay * qss + sqk * invq * invk * d;
 #pragma unroll
     for (int r = 0; r < ROWS; r++) s[r] = fmaf(decay, s[r], kn[p][i0 + r] * invk * d);
@@ -125,6 +161,25 @@ __global__ __launch_bounds__(64 * DW) void delta_rule_kernel(DeltaArgs a) {
     for (int r = 0; r < ROWS; r++)
       if (i0 + r < a.dk) Sh[(int64_t)(i0 + r) * a.dv + j] = s[r];
   }
+}
+
+template <int CB>
+void launch_delta_rule(const DeltaArgs &a, hipStream_t s) {
+  constexpr int RG = 64 * DW / CB;
+  const dim3 grid((a.dv + CB - 1) / CB, a.H);
+  const int rows = (a.dk + RG - 1) / RG;
+  if (rows <= 1 && RG <= MAX_DK)
+    delta_rule_kernel<1, CB><<<grid, 64 * DW, 0, s>>>(a);
+  else if (rows <= 2 && 2 * RG <= MAX_DK)
+    delta_rule_kernel<(2 * RG <= MAX_DK ? 2 : 1), CB><<<grid, 64 * DW, 0, s>>>(a);
+  else if (rows <= 4 && 4 * RG <= MAX_DK)
+    delta_rule_kernel<(4 * RG <= MAX_DK ? 4 : 1), CB><<<grid, 64 * DW, 0, s>>>(a);
+  else if (rows <= 8 && 8 * RG <= MAX_DK)
+    delta_rule_kernel<(8 * RG <= MAX_DK ? 8 : 1), CB><<<grid, 64 * DW, 0, s>>>(a);
+  else if (rows <= 16 && 16 * RG <= MAX_DK)
+    delta_rule_kernel<(16 * RG <= MAX_DK ? 16 : 1), CB><<<grid, 64 * DW, 0, s>>>(a);
+  else
+    delta_rule_kernel<(32 * RG <= MAX_DK ? 32 : 1), CB><<<grid, 64 * DW, 0, s>>>(a);
 }
 
 // LIN_CONV + LIN_CONV_STATE: a thread per output (row, channel), then per
@@ -208,18 +263,12 @@ int wg_delta_rule(const float *qkv, int32_t M, int32_t ldq, const float *ba, int
   WG_REQUIRE(!snapshot || !overlaps(snapshot, state_bytes, state, state_bytes),
              "wg_delta_rule: the snapshot overlaps the state");
   DeltaArgs a{qkv, ldq, ba, ldba, A, dt_bias, H, dk, dv, M, state, snapshot, save_at, out, ldo};
-  const dim3 grid((dv + 63) / 64, H);
-  hipStream_t s = as_stream(stream);
-  if (dk <= DW * 2)
-    delta_rule_kernel<2><<<grid, 64 * DW, 0, s>>>(a);
-  else if (dk <= DW * 4)
-    delta_rule_kernel<4><<<grid, 64 * DW, 0, s>>>(a);
-  else if (dk <= DW * 8)
-    delta_rule_kernel<8><<<grid, 64 * DW, 0, s>>>(a);
-  else if (dk <= DW * 16)
-    delta_rule_kernel<16><<<grid, 64 * DW, 0, s>>>(a);
+  // Short batches: 16 columns a workgroup (128 workgroups at 16 heads of
+  // 128), so more CUs read the state; long ones: 64 (fewer shuffles a row).
+  if (M <= tuning("delta_narrow_rows"))
+    launch_delta_rule<16>(a, as_stream(stream));
   else
-    delta_rule_kernel<32><<<grid, 64 * DW, 0, s>>>(a);
+    launch_delta_rule<64>(a, as_stream(stream));
   return launched("wg_delta_rule");
 }
 
