@@ -823,9 +823,67 @@ def workload_delta_rule(args):
                 higher_is_better=False)
 
 
+def workload_onnx_load(args):
+    """Loading the MatMulNBits weights of an LFM2-350M q4f16 ONNX export
+    (the onnxruntime-genai graph, with zero points) into the device layout:
+    the graph read by the library's reader, each weight's quants, scales and
+    zero points read from the external data file and repacked on the GPU
+    (wg_repack_nbits). The data file holds random weights at the graph's
+    offsets. GB/s of weight bytes, best of a few loads of the page-cached
+    file."""
+    import shutil
+    import tempfile
+    import numpy as np
+    import torch
+    from webgllm_amd.onnx import OnnxFile, OnnxModel, upload_nbits
+    src = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden", "onnx",
+                       "lfm2-350m", "model_q4f16.onnx")
+    d = tempfile.mkdtemp()
+    graph = os.path.join(d, "model_q4f16.onnx")
+    shutil.copy(src, graph)
+    f = OnnxFile(graph)
+    m = OnnxModel(f)
+    paths = sorted({n.name.rsplit("/", 1)[0] + "/" for n in f.nodes
+                    if n.op_type == "MatMulNBits"})
+    weights = [m.nbits(p) for p in paths]
+    rng = np.random.default_rng(0)
+    total = 0
+    with open(os.path.join(d, "model_q4f16.onnx_data"), "wb") as out:
+        for w in weights:
+            for t in (w.quant, w.scales, w.zp):
+                if t is None:
+                    continue
+                n = t.external[2]
+                if t is w.scales:
+                    data = rng.uniform(0.002, 0.02, n // 2).astype(np.float16).view(np.uint8)
+                else:
+                    data = rng.integers(0, 256, n, dtype=np.uint8)
+                out.seek(t.external[1])
+                out.write(data.tobytes())
+                total += n
+    times = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.time()
+        mats = [upload_nbits(f, w) for w in weights]
+        torch.cuda.synchronize()
+        times.append(time.time() - t0)
+        del mats
+    best = min(times)
+    gbps = total / best / 1e9
+    f.close()
+    shutil.rmtree(d, ignore_errors=True)
+    cfg = {"workload": "LFM2-350M q4f16 ONNX export's MatMulNBits weights (random values at "
+                       "the graph's offsets) into the device layout",
+           "matrices": len(weights), "weight_bytes": total,
+           "load_s": [round(t, 3) for t in times], "parallelism": "none"}
+    return line("ONNX MatMulNBits load GB/s (LFM2-350M export)", round(gbps, 2), "GB/s", 3, 0,
+                best * 1e3, cfg, None, None)
+
+
 WORKLOADS = {"q4_0-gemv": workload_q4_0_gemv, "nbits-gemm": workload_nbits_gemm,
              "sample-pick": workload_sample_pick, "delta-rule": workload_delta_rule,
-             "gguf-load": workload_gguf_load,
+             "gguf-load": workload_gguf_load, "onnx-load": workload_onnx_load,
              "q8-gemm": lambda args: workload_nbits_gemm(args, "q8"),
              "q6_k-head": workload_q6_k_head, "q8-gemv": workload_q8_gemv,
              "qwen2-decode": workload_qwen2_decode, "lfm2-verify": workload_lfm2_verify,

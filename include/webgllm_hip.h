@@ -233,6 +233,66 @@ int wg_gguf_meta(const wg_gguf *g, int64_t i, wg_gguf_value *out);
 /* Element j of array key i (readGgufArray, src/gguf.ts:346-360). */
 int wg_gguf_meta_element(const wg_gguf *g, int64_t i, uint64_t j, wg_gguf_value *out);
 
+/* ---------------------------------------------------- ONNX files
+ * parseOnnxModel (src/onnx.ts:71-282) over a read-only memory map of a
+ * ModelProto: the graph's nodes and initializers. Inline tensor bytes
+ * stay in the map; external ones are named by location, offset and
+ * length (the loader reads them from that file). Names and arrays point
+ * into the reader and live until wg_onnx_close. */
+typedef struct wg_onnx wg_onnx;
+
+typedef struct {
+  const char *name;
+  int32_t n_dims;
+  int64_t dims[8];
+  int32_t data_type;         /* TensorProto.DataType (src/onnx.ts:8-25) */
+  const uint8_t *raw;        /* raw_data in the map, or NULL */
+  uint64_t raw_bytes;
+  const char *location;      /* external data file, or NULL when inline */
+  int64_t offset, length;    /* in that file (length -1 when absent) */
+  const int64_t *int64_data; /* the typed fields small constants use */
+  int64_t n_int64;
+  const float *float_data;
+  int64_t n_float;
+} wg_onnx_tensor_info;
+
+typedef struct {
+  const char *name, *op_type, *domain;
+  int32_t n_inputs, n_outputs, n_attrs;
+} wg_onnx_node_info;
+
+typedef struct {
+  const char *name;
+  int32_t type;              /* AttributeProto.AttributeType: 1 float, 2 int, 3 string, 4 tensor, 6 floats, 7 ints, 8 strings */
+  float f;
+  int64_t i;
+  const char *s;             /* `s_len` bytes, not NUL-terminated */
+  uint64_t s_len;
+  const int64_t *ints;
+  int64_t n_ints;
+  const float *floats;
+  int64_t n_floats;
+  int64_t n_strings;
+  int64_t tensor;            /* its tensor's index (wg_onnx_tensor), or -1 */
+} wg_onnx_attr;
+
+int wg_onnx_open(const char *path, wg_onnx **out);
+int wg_onnx_close(wg_onnx *f);
+const char *wg_onnx_graph_name(const wg_onnx *f);
+int64_t wg_onnx_node_count(const wg_onnx *f);
+/* Tensors: the initializers (0 .. wg_onnx_init_count - 1), then the
+ * attributes' tensors (a Constant node's value). */
+int64_t wg_onnx_tensor_count(const wg_onnx *f);
+int64_t wg_onnx_init_count(const wg_onnx *f);
+/* Index of an initializer, or -1. */
+int64_t wg_onnx_find_init(const wg_onnx *f, const char *name);
+int wg_onnx_tensor(const wg_onnx *f, int64_t i, wg_onnx_tensor_info *out);
+int wg_onnx_node(const wg_onnx *f, int64_t i, wg_onnx_node_info *out);
+/* Input or output j of node i, or NULL. */
+const char *wg_onnx_node_input(const wg_onnx *f, int64_t i, int32_t j);
+const char *wg_onnx_node_output(const wg_onnx *f, int64_t i, int32_t j);
+int wg_onnx_node_attr(const wg_onnx *f, int64_t i, int32_t j, wg_onnx_attr *out);
+
 /* rowsToFloats (src/load-gguf.ts:557-580) on the GPU: `rows` rows of K
  * weights of ggml type `type` (device bytes as the file has them) to
  * float32, bit-exact to the reference's dequantizers: F32, F16, Q8_0

@@ -76,6 +76,29 @@ class DeltaShape(C.Structure):
     _fields_ = [("heads", C.c_int32), ("key_dim", C.c_int32), ("value_dim", C.c_int32)]
 
 
+class OnnxTensorInfo(C.Structure):
+    """wg_onnx_tensor_info."""
+    _fields_ = [("name", C.c_char_p), ("n_dims", C.c_int32), ("dims", C.c_int64 * 8),
+                ("data_type", C.c_int32), ("raw", C.c_void_p), ("raw_bytes", C.c_uint64),
+                ("location", C.c_char_p), ("offset", C.c_int64), ("length", C.c_int64),
+                ("int64_data", C.POINTER(C.c_int64)), ("n_int64", C.c_int64),
+                ("float_data", C.POINTER(C.c_float)), ("n_float", C.c_int64)]
+
+
+class OnnxNodeInfo(C.Structure):
+    """wg_onnx_node_info."""
+    _fields_ = [("name", C.c_char_p), ("op_type", C.c_char_p), ("domain", C.c_char_p),
+                ("n_inputs", C.c_int32), ("n_outputs", C.c_int32), ("n_attrs", C.c_int32)]
+
+
+class OnnxAttr(C.Structure):
+    """wg_onnx_attr."""
+    _fields_ = [("name", C.c_char_p), ("type", C.c_int32), ("f", C.c_float), ("i", C.c_int64),
+                ("s", C.c_void_p), ("s_len", C.c_uint64), ("ints", C.POINTER(C.c_int64)),
+                ("n_ints", C.c_int64), ("floats", C.POINTER(C.c_float)), ("n_floats", C.c_int64),
+                ("n_strings", C.c_int64), ("tensor", C.c_int64)]
+
+
 class GgufTensorInfo(C.Structure):
     """wg_gguf_tensor_info."""
     _fields_ = [("name", C.c_char_p), ("n_dims", C.c_int32), ("dims", C.c_int64 * 4),
@@ -184,6 +207,18 @@ def load():
         "wg_gguf_tensor": (C.c_int, [P, I64, C.POINTER(GgufTensorInfo)]),
         "wg_gguf_meta": (C.c_int, [P, I64, C.POINTER(GgufValue)]),
         "wg_gguf_meta_element": (C.c_int, [P, I64, C.c_uint64, C.POINTER(GgufValue)]),
+        "wg_onnx_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+        "wg_onnx_close": (C.c_int, [P]),
+        "wg_onnx_graph_name": (C.c_char_p, [P]),
+        "wg_onnx_node_count": (I64, [P]),
+        "wg_onnx_tensor_count": (I64, [P]),
+        "wg_onnx_init_count": (I64, [P]),
+        "wg_onnx_find_init": (I64, [P, C.c_char_p]),
+        "wg_onnx_tensor": (C.c_int, [P, I64, C.POINTER(OnnxTensorInfo)]),
+        "wg_onnx_node": (C.c_int, [P, I64, C.POINTER(OnnxNodeInfo)]),
+        "wg_onnx_node_input": (C.c_char_p, [P, I64, I32]),
+        "wg_onnx_node_output": (C.c_char_p, [P, I64, I32]),
+        "wg_onnx_node_attr": (C.c_int, [P, I64, I32, C.POINTER(OnnxAttr)]),
         "wg_rows_to_floats": (C.c_int, [I32, P, I32, I32, P, P]),
         "wg_pick_scratch_bytes": (SZ, [I32, I32]),
         "wg_pick_candidates": (C.c_int, [P, I32, I32, I32, P, P, I32, I32, C.c_float,
