@@ -791,9 +791,17 @@ def workload_delta_rule(args):
     for _ in range(3):
         launch(states[0], 2048, cur)
     pf_ms = timed(lambda: launch(states[0], 2048, cur), 10)
-    L.check(lib.wg_tuning_set(b"delta_narrow_rows", 4096))  # 16-column workgroups at 2048
-    pf_narrow_ms = timed(lambda: launch(states[0], 2048, cur), 10)
-    L.check(lib.wg_tuning_set(b"delta_narrow_rows", 16))
+    need = int(lib.wg_delta_chunk_scratch_bytes(2048, C.byref(shape), 0))
+    scratch = torch.empty(need // 4 + 4, device="cuda")
+
+    def chunked():
+        L.check(lib.wg_delta_rule_chunked(
+            qkv.data_ptr(), 2048, qkv.stride(0), ba.data_ptr(), ba.stride(0), A.data_ptr(),
+            dt.data_ptr(), C.byref(shape), states[0].data_ptr(), None, 0, out.data_ptr(),
+            out.stride(0), scratch.data_ptr(), need, cur))
+    for _ in range(3):
+        chunked()
+    pf_chunked_ms = timed(chunked, 10)
     cpu = None
     if not args.no_cpu:
         from oracle import oracle as O
@@ -817,7 +825,9 @@ def workload_delta_rule(args):
                        "key/value dims 128), one decode row", "heads": H, "key_dim": dk,
            "value_dim": dv, "prompt_rows": 2048, "prompt_ms": round(pf_ms, 3),
            "prompt_rows_per_s": round(2048 / (pf_ms * 1e-3)),
-           "prompt_ms_16_column_workgroups": round(pf_narrow_ms, 3), "parallelism": "none"}
+           "prompt_chunked_ms": round(pf_chunked_ms, 3),
+           "prompt_chunked_rows_per_s": round(2048 / (pf_chunked_ms * 1e-3)),
+           "parallelism": "none"}
     return line("Gated DeltaNet recurrence us a decode row (16 heads of 128)",
                 round(ms * 1e3, 2), "us", reps * layers, 3 * layers, ms, cfg, roof, cpu,
                 higher_is_better=False)

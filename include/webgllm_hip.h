@@ -572,6 +572,21 @@ int wg_delta_rule(const float *qkv, int32_t M, int32_t ldq, const float *ba, int
                   const float *A, const float *dt_bias, const wg_delta_shape *shape,
                   float *state, float *snapshot, int32_t save_at, float *out, int32_t ldo,
                   void *stream);
+/* The same recurrence in chunks of 64 rows, as Engine.recurrenceChunks
+ * runs prompt batches (engine.ts:6950-7050; delta-rule.ts:73-166): per
+ * chunk the gates, q/k prep, A = beta e^(G_r - G_s) k.k, T = (I + A)^-1,
+ * U, W, P, Oi, Q' for all chunks at once, then the state chain, two steps
+ * a chunk. The first chunk is shorter when save_at is not a multiple of
+ * 64, so that a chunk ends there. key_dim a multiple of 4, key_dim and
+ * value_dim at most 128; scratch (16-byte aligned) of
+ * wg_delta_chunk_scratch_bytes(M, shape, save_at) bytes. Otherwise as
+ * wg_delta_rule. */
+size_t wg_delta_chunk_scratch_bytes(int32_t M, const wg_delta_shape *shape, int32_t save_at);
+int wg_delta_rule_chunked(const float *qkv, int32_t M, int32_t ldq, const float *ba,
+                          int32_t ldba, const float *A, const float *dt_bias,
+                          const wg_delta_shape *shape, float *state, float *snapshot,
+                          int32_t save_at, float *out, int32_t ldo, void *scratch,
+                          size_t scratch_bytes, void *stream);
 /* LIN_CONV + LIN_CONV_STATE (kernels.ts:1564-1641): out[m][c] = silu(sum_k
  * taps[c][k] * x[m - (W-1) + k][c]) over the first C channels of each in
  * row (W at most 16; tap W-1 the current row), earlier rows from state

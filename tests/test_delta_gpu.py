@@ -87,6 +87,51 @@ def test_delta_rule_long_batch_stays_on_the_oracle(hip):
     assert _rel(out.cpu().numpy(), want_o) < TOL and _rel(s.cpu().numpy(), want_s) < TOL
 
 
+@pytest.mark.parametrize("H,dk,dv,M,save_at", [(16, 128, 128, 1, 0), (16, 128, 128, 64, 0),
+                                               (16, 128, 128, 65, 0), (4, 128, 128, 300, 0),
+                                               (3, 64, 80, 100, 37), (2, 16, 12, 37, 0),
+                                               (2, 128, 100, 130, 64), (1, 4, 1, 5, 3),
+                                               (2, 32, 128, 129, 128)])
+def test_delta_chunked_matches_oracle(hip, H, dk, dv, M, save_at):
+    """The chunked form (deltaChunked) against the float64 sequential rule:
+    outputs, state, and the snapshot at a chunk end (the first chunk made
+    shorter to end at save_at)."""
+    from webgllm_amd import ops
+    rng = np.random.default_rng(H * 100 + dk + M + save_at)
+    qkv, ba, A, dt, state = _layer(rng, H, dk, dv, M, pad=2)
+    want_o, want_s, want_snap = O.delta_rule(qkv, ba, A, dt, H, dk, dv, state, save_at=save_at)
+    s = _t(state)
+    got = ops.delta_rule_chunked(_t(qkv), _t(ba), _t(A), _t(dt), H, dk, dv, s, save_at=save_at)
+    out, snap = got if save_at else (got, None)
+    torch.cuda.synchronize()
+    assert _rel(out.cpu().numpy(), want_o) < TOL
+    assert _rel(s.cpu().numpy(), want_s) < TOL
+    if save_at:
+        assert _rel(snap.cpu().numpy(), want_snap) < TOL
+
+
+def test_delta_chunked_equals_token_steps_at_prompt_size(hip):
+    """A 2048-row batch at the layer shape: the chunked form and the
+    row-at-a-time kernel agree (two float32 orders of the same sums), and a
+    chunked batch continued by token steps equals the whole batch in chunks."""
+    from webgllm_amd import ops
+    rng = np.random.default_rng(21)
+    H, dk, dv, M = 16, 128, 128, 2048
+    qkv, ba, A, dt, state = _layer(rng, H, dk, dv, M)
+    q, b, a, d = _t(qkv), _t(ba), _t(A), _t(dt)
+    s1, s2, s3 = _t(state), _t(state), _t(state)
+    o1 = ops.delta_rule_chunked(q, b, a, d, H, dk, dv, s1)
+    o2 = ops.delta_rule(q, b, a, d, H, dk, dv, s2)
+    o3 = ops.delta_rule_chunked(q[:2000], b[:2000], a, d, H, dk, dv, s3)
+    o3b = ops.delta_rule(q[2000:], b[2000:], a, d, H, dk, dv, s3)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o1).all()
+    assert _rel(o1.cpu().numpy(), o2.cpu().numpy()) < TOL
+    assert _rel(s1.cpu().numpy(), s2.cpu().numpy()) < TOL
+    assert _rel(torch.cat([o3, o3b]).cpu().numpy(), o1.cpu().numpy()) < TOL
+    assert _rel(s3.cpu().numpy(), s1.cpu().numpy()) < TOL
+
+
 @pytest.mark.parametrize("M,C,W", [(1, 6144, 4), (7, 100, 4), (2, 33, 4), (5, 64, 1),
                                    (300, 6144, 4), (3, 10, 16)])
 def test_delta_conv_matches_oracle(hip, M, C, W):
@@ -144,6 +189,14 @@ def test_delta_rejections(hip):
     with pytest.raises(L.WgError, match="1 to 16"):
         ops.delta_conv(torch.zeros((2, 8), device=dev), 8, torch.zeros((8, 17), device=dev),
                        torch.zeros((16, 8), device=dev), torch.zeros((16, 8), device=dev))
+    with pytest.raises(L.WgError, match="a multiple of 4"):
+        ops.delta_rule_chunked(torch.zeros((2, 2 * H * 6 + H * dv), device=dev), ba, A, A, H, 6,
+                               dv, torch.zeros((H, 6, dv), device=dev))
+    with pytest.raises(L.WgError, match="at most 128"):
+        ops.delta_rule_chunked(torch.zeros((2, 2 * H * 256 + H * dv), device=dev), ba, A, A, H,
+                               256, dv, torch.zeros((H, 256, dv), device=dev))
+    with pytest.raises(L.WgError, match="needed"):
+        ops.delta_rule_chunked(qkv, ba, A, A, H, dk, dv, s, scratch=torch.zeros(4, device=dev))
     with pytest.raises(L.WgError, match="1 to 256"):
         ops.delta_norm(torch.zeros((1, 300), device=dev), 1, 300, torch.zeros((1, 300), device=dev),
                        torch.zeros(300, device=dev), 1e-6)

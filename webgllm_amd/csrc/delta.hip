@@ -238,6 +238,299 @@ __global__ __launch_bounds__(256) void delta_norm_kernel(const float *o, int ldo
   }
 }
 
+// ---------------------------------------------------- the chunked form
+//
+// deltaChunked (src/delta-rule.ts:73-166; the reference's linCum, linGram,
+// linSolve, linUW, linQO, linChunkOut and linChunkState passes): rows in
+// chunks of CH (a first chunk of `first` rows, so that one ends at a
+// snapshot), G the running sum of the log-decays within a chunk:
+//   A[r][s] = beta_r e^{G_r - G_s} k^_r.k^_s (s < r), T = (I + A)^-1,
+//   U = T diag(beta) V, W = T diag(beta e^G) K^, P[r][s] = e^{G_r - G_s} q^_r.k^_s,
+//   Oi = P U, Q' = e^G Q^ - P W, K~_s = e^{G_last - G_s} k^_s;
+// then from each chunk's starting state S: D = U - W S, O = Oi + Q' S,
+// S <- e^{G_last} S + K~^T D. `delta_chunk_prep_kernel` does the first
+// part for every (head, chunk) at once; `delta_chunk_chain_kernel` the
+// state chain, a workgroup per (head, 16 state columns).
+
+constexpr int CH = 64;        // rows a chunk
+constexpr int CMAX = 128;     // key and value dims the chunked form takes
+constexpr int RS = CMAX + 4;  // LDS row stride (floats) of the row tiles
+constexpr int AS = CH + 4;    // LDS row stride of A (then T) and P
+constexpr int CBW = 16;       // state columns a chain workgroup
+constexpr size_t PREP_LDS = (3 * CH * RS + 2 * CH * AS + 3 * CH) * sizeof(float);
+constexpr size_t CHAIN_LDS = (CMAX * CBW + 3 * CH * RS + CH * CBW) * sizeof(float);
+
+struct ChunkArgs {
+  const float *qkv;
+  int ldq;
+  const float *ba;
+  int ldba;
+  const float *A, *dt;
+  int H, dk, dv, M, first, nch;
+  float *U, *W, *Oi, *Qp, *Kt, *eg;  // [H][nch][CH][dv or dk]; eg [H][nch]
+  float *state, *snap;
+  int save_at;
+  float *out;
+  int ldo;
+};
+
+__device__ inline void chunk_rows(const ChunkArgs &a, int c, int &c0, int &n) {
+  c0 = c == 0 ? 0 : a.first + (c - 1) * CH;
+  n = min(c == 0 ? a.first : CH, a.M - c0);
+}
+
+__device__ inline float dot4(float4 x, float4 y) {
+  return fmaf(x.x, y.x, fmaf(x.y, y.y, fmaf(x.z, y.z, x.w * y.w)));
+}
+
+__global__ __launch_bounds__(256) void delta_chunk_prep_kernel(ChunkArgs a) {
+  extern __shared__ __align__(16) float sm[];
+  float *sq = sm, *sk = sq + CH * RS, *sv = sk + CH * RS;  // q^, k^, v rows (0 past n, dims)
+  float *sA = sv + CH * RS, *sP = sA + CH * AS;             // A (then T) and P
+  float *sG = sP + CH * AS, *sB = sG + CH, *sE = sB + CH;  // G, beta, e^G
+  const int c = blockIdx.x, h = blockIdx.y, t = threadIdx.x, lane = t & 63;
+  int c0, n;
+  chunk_rows(a, c, c0, n);
+  const int K = a.H * a.dk, dk = a.dk, dv = a.dv;
+  for (int idx = t; idx < CH * CMAX; idx += 256) {
+    const int r = idx / CMAX, i = idx % CMAX;
+    const float *row = a.qkv + (int64_t)(c0 + r) * a.ldq;
+    const bool in = r < n;
+    sq[r * RS + i] = in && i < dk ? row[h * dk + i] : 0.0f;
+    sk[r * RS + i] = in && i < dk ? row[K + h * dk + i] : 0.0f;
+    sv[r * RS + i] = in && i < dv ? row[2 * K + h * dv + i] : 0.0f;
+  }
+  if (t < CH) {  // wave 0: the gates (LIN_GATES) and G by a shuffle scan (linCum)
+    float beta = 0.0f, g = 0.0f;
+    if (t < n) {
+      const float *gb = a.ba + (int64_t)(c0 + t) * a.ldba;
+      const float x = gb[a.H + h] + a.dt[h];
+      beta = 1.0f / (1.0f + expf(-gb[h]));
+      g = a.A[h] * (fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x))));
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(g, off, 64);
+      if (lane >= off) g += y;
+    }
+    sB[t] = beta;
+    sG[t] = g;
+    sE[t] = expf(g);
+  }
+  __syncthreads();
+  {  // LIN_PREP: four threads a row
+    const int r = t >> 2, part = t & 3;
+    float ssq = 0.0f, ssk = 0.0f;
+    for (int i = part; i < dk; i += 4) {
+      ssq = fmaf(sq[r * RS + i], sq[r * RS + i], ssq);
+      ssk = fmaf(sk[r * RS + i], sk[r * RS + i], ssk);
+    }
+    ssq += __shfl_xor(ssq, 1, 64);
+    ssq += __shfl_xor(ssq, 2, 64);
+    ssk += __shfl_xor(ssk, 1, 64);
+    ssk += __shfl_xor(ssk, 2, 64);
+    const float invq = 1.0f / sqrtf((float)dk) / sqrtf(ssq + 1e-6f);
+    const float invk = 1.0f / sqrtf(ssk + 1e-6f);
+    for (int i = part; i < dk; i += 4) {
+      sq[r * RS + i] *= invq;
+      sk[r * RS + i] *= invk;
+    }
+  }
+  __syncthreads();
+  {  // linGram: a 4 x 4 block of (row, key) pairs a thread, lower triangle only
+    const int rb = t >> 4, sb = t & 15;
+    float kk[4][4] = {}, qk[4][4] = {};
+    if (sb <= rb) {
+      for (int i = 0; i < dk; i += 4) {
+        float4 kr[4], qr[4], ks[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          kr[u] = *reinterpret_cast<const float4 *>(&sk[(4 * rb + u) * RS + i]);
+          qr[u] = *reinterpret_cast<const float4 *>(&sq[(4 * rb + u) * RS + i]);
+          ks[u] = *reinterpret_cast<const float4 *>(&sk[(4 * sb + u) * RS + i]);
+        }
+#pragma unroll
+        for (int x = 0; x < 4; x++)
+#pragma unroll
+          for (int y = 0; y < 4; y++) {
+            kk[x][y] += dot4(kr[x], ks[y]);
+            qk[x][y] += dot4(qr[x], ks[y]);
+          }
+      }
+    }
+#pragma unroll
+    for (int x = 0; x < 4; x++)
+#pragma unroll
+      for (int y = 0; y < 4; y++) {
+        const int r = 4 * rb + x, s = 4 * sb + y;
+        const bool ok = r < n && s <= r;
+        const float e = ok ? expf(sG[r] - sG[s]) : 0.0f;
+        sA[r * AS + s] = ok && s < r ? sB[r] * e * kk[x][y] : 0.0f;
+        sP[r * AS + s] = ok ? e * qk[x][y] : 0.0f;
+      }
+  }
+  const float gl = sG[n - 1];
+  const int64_t base = (int64_t)(h * a.nch + c) * CH;
+  for (int idx = t; idx < n * dk; idx += 256) {
+    const int r = idx / dk, i = idx % dk;
+    a.Kt[(base + r) * dk + i] = expf(gl - sG[r]) * sk[r * RS + i];
+  }
+  if (t == 0) a.eg[h * a.nch + c] = expf(gl);
+  __syncthreads();
+  if (t < 64) {  // linSolve: T = (I + A)^-1 by forward substitution, lane = column
+    float Tc[CH];
+#pragma unroll
+    for (int r = 0; r < CH; r++) {
+      float acc = lane == r ? 1.0f : 0.0f;
+#pragma unroll
+      for (int s = 0; s < r; s++) acc = fmaf(-sA[r * AS + s], Tc[s], acc);
+      Tc[r] = acc;
+    }
+#pragma unroll
+    for (int r = 0; r < CH; r++) sA[r * AS + lane] = Tc[r];
+  }
+  __syncthreads();
+  // linUW, then linQO: 4 rows x 8 columns (16 apart) a thread
+  const int rb = t >> 4, jb = t & 15;
+  const int smax = min(4 * rb + 3, n - 1);
+  float u[4][8] = {}, w[4][8] = {};
+  for (int s = 0; s <= smax; s++) {
+    const float bs = sB[s], be = bs * sE[s];
+    float tr[4];
+#pragma unroll
+    for (int x = 0; x < 4; x++) tr[x] = sA[(4 * rb + x) * AS + s];
+#pragma unroll
+    for (int y = 0; y < 8; y++) {
+      const float vv = sv[s * RS + jb + 16 * y] * bs, kv = sk[s * RS + jb + 16 * y] * be;
+#pragma unroll
+      for (int x = 0; x < 4; x++) {
+        u[x][y] = fmaf(tr[x], vv, u[x][y]);
+        w[x][y] = fmaf(tr[x], kv, w[x][y]);
+      }
+    }
+  }
+  __syncthreads();  // every read of v and k^ is done: U and W take their places
+#pragma unroll
+  for (int x = 0; x < 4; x++) {
+    const int r = 4 * rb + x;
+#pragma unroll
+    for (int y = 0; y < 8; y++) {
+      const int j = jb + 16 * y;
+      sv[r * RS + j] = u[x][y];
+      sk[r * RS + j] = w[x][y];
+      if (r < n && j < dv) a.U[(base + r) * dv + j] = u[x][y];
+      if (r < n && j < dk) a.W[(base + r) * dk + j] = w[x][y];
+    }
+  }
+  __syncthreads();
+  float o[4][8] = {}, qp[4][8];
+#pragma unroll
+  for (int x = 0; x < 4; x++)
+#pragma unroll
+    for (int y = 0; y < 8; y++) qp[x][y] = sE[4 * rb + x] * sq[(4 * rb + x) * RS + jb + 16 * y];
+  for (int s = 0; s <= smax; s++) {
+    float pr[4];
+#pragma unroll
+    for (int x = 0; x < 4; x++) pr[x] = sP[(4 * rb + x) * AS + s];
+#pragma unroll
+    for (int y = 0; y < 8; y++) {
+      const float us = sv[s * RS + jb + 16 * y], ws = sk[s * RS + jb + 16 * y];
+#pragma unroll
+      for (int x = 0; x < 4; x++) {
+        o[x][y] = fmaf(pr[x], us, o[x][y]);
+        qp[x][y] = fmaf(-pr[x], ws, qp[x][y]);
+      }
+    }
+  }
+#pragma unroll
+  for (int x = 0; x < 4; x++) {
+    const int r = 4 * rb + x;
+    if (r >= n) continue;
+#pragma unroll
+    for (int y = 0; y < 8; y++) {
+      const int j = jb + 16 * y;
+      if (j < dv) a.Oi[(base + r) * dv + j] = o[x][y];
+      if (j < dk) a.Qp[(base + r) * dk + j] = qp[x][y];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void delta_chunk_chain_kernel(ChunkArgs a) {
+  extern __shared__ __align__(16) float sm[];
+  float *sS = sm;                                           // [CMAX][CBW] state block
+  float *sW = sS + CMAX * CBW, *sQ = sW + CH * RS, *sK = sQ + CH * RS;  // [CH][RS]
+  float *sD = sK + CH * RS;                                 // [CH][CBW]
+  const int h = blockIdx.y, t = threadIdx.x, j = t & (CBW - 1), g = t / CBW;
+  const int jj = blockIdx.x * CBW + j;
+  const bool col = jj < a.dv;
+  const int dk = a.dk, dv = a.dv;
+  float *Sh = a.state + (int64_t)h * dk * dv;
+  for (int i = g; i < CMAX; i += 256 / CBW)
+    sS[i * CBW + j] = col && i < dk ? Sh[(int64_t)i * dv + jj] : 0.0f;
+  for (int c = 0; c < a.nch; c++) {
+    int c0, n;
+    chunk_rows(a, c, c0, n);
+    const int64_t base = (int64_t)(h * a.nch + c) * CH;
+    for (int idx = t; idx < CH * CMAX / 4; idx += 256) {
+      const int r = idx / (CMAX / 4), i = (idx % (CMAX / 4)) * 4;
+      float4 w4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), q4 = w4, k4 = w4;
+      if (r < n && i < dk) {
+        w4 = *reinterpret_cast<const float4 *>(&a.W[(base + r) * dk + i]);
+        q4 = *reinterpret_cast<const float4 *>(&a.Qp[(base + r) * dk + i]);
+        k4 = *reinterpret_cast<const float4 *>(&a.Kt[(base + r) * dk + i]);
+      }
+      *reinterpret_cast<float4 *>(&sW[r * RS + i]) = w4;
+      *reinterpret_cast<float4 *>(&sQ[r * RS + i]) = q4;
+      *reinterpret_cast<float4 *>(&sK[r * RS + i]) = k4;
+    }
+    float d[4], o[4];
+#pragma unroll
+    for (int x = 0; x < 4; x++) {
+      const int r = 4 * g + x;
+      const bool in = r < n && col;
+      d[x] = in ? a.U[(base + r) * dv + jj] : 0.0f;
+      o[x] = in ? a.Oi[(base + r) * dv + jj] : 0.0f;
+    }
+    __syncthreads();
+    // linChunkOut: D = U - W S, O = Oi + Q' S, rows 4g .. 4g + 3
+    for (int i = 0; i < dk; i += 4) {
+      const float4 s4 = make_float4(sS[i * CBW + j], sS[(i + 1) * CBW + j],
+                                    sS[(i + 2) * CBW + j], sS[(i + 3) * CBW + j]);
+#pragma unroll
+      for (int x = 0; x < 4; x++) {
+        d[x] -= dot4(*reinterpret_cast<const float4 *>(&sW[(4 * g + x) * RS + i]), s4);
+        o[x] += dot4(*reinterpret_cast<const float4 *>(&sQ[(4 * g + x) * RS + i]), s4);
+      }
+    }
+#pragma unroll
+    for (int x = 0; x < 4; x++) {
+      const int r = 4 * g + x;
+      sD[r * CBW + j] = r < n ? d[x] : 0.0f;
+      if (r < n && col) a.out[(int64_t)(c0 + r) * a.ldo + h * dv + jj] = o[x];
+    }
+    __syncthreads();
+    // linChunkState: S <- e^{G_last} S + K~^T D
+    const float e = a.eg[h * a.nch + c];
+    for (int i = g; i < dk; i += 256 / CBW) {
+      float acc = e * sS[i * CBW + j];
+      for (int r = 0; r < n; r++) acc = fmaf(sK[r * RS + i], sD[r * CBW + j], acc);
+      sS[i * CBW + j] = acc;
+      if (a.snap && c0 + n == a.save_at && col)
+        a.snap[(int64_t)h * dk * dv + (int64_t)i * dv + jj] = acc;
+    }
+    __syncthreads();
+  }
+  if (col)
+    for (int i = g; i < dk; i += 256 / CBW) Sh[(int64_t)i * dv + jj] = sS[i * CBW + j];
+}
+
+// Chunks of a batch of M rows whose first chunk has `first` rows.
+inline int chunk_count(int M, int first) { return M <= first ? 1 : 1 + (M - first + CH - 1) / CH; }
+
+// The first chunk's rows: shorter, so that a chunk ends at save_at
+// (Engine.recurrenceChunks' rule), else CH.
+inline int first_rows(int save_at) { return save_at > 0 && save_at % CH ? save_at % CH : CH; }
+
 }  // namespace
 }  // namespace wg
 
@@ -270,6 +563,59 @@ int wg_delta_rule(const float *qkv, int32_t M, int32_t ldq, const float *ba, int
   else
     launch_delta_rule<64>(a, as_stream(stream));
   return launched("wg_delta_rule");
+}
+
+size_t wg_delta_chunk_scratch_bytes(int32_t M, const wg_delta_shape *shape, int32_t save_at) {
+  if (!shape || M < 1) return 0;
+  const size_t nch = (size_t)chunk_count(M, first_rows(save_at));
+  return sizeof(float) * ((size_t)shape->heads * nch * CH *
+                              (2 * (size_t)shape->value_dim + 3 * (size_t)shape->key_dim) +
+                          (size_t)shape->heads * nch);
+}
+
+int wg_delta_rule_chunked(const float *qkv, int32_t M, int32_t ldq, const float *ba,
+                          int32_t ldba, const float *A, const float *dt_bias,
+                          const wg_delta_shape *shape, float *state, float *snapshot,
+                          int32_t save_at, float *out, int32_t ldo, void *scratch,
+                          size_t scratch_bytes, void *stream) {
+  WG_REQUIRE(qkv && ba && A && dt_bias && shape && state && out && scratch && M >= 1,
+             "wg_delta_rule_chunked: bad arguments");
+  const int H = shape->heads, dk = shape->key_dim, dv = shape->value_dim;
+  WG_REQUIRE(H >= 1 && dk >= 4 && dk <= CMAX && dk % 4 == 0 && dv >= 1 && dv <= CMAX,
+             "wg_delta_rule_chunked: %d key and %d value dims (key dims a multiple of 4, "
+             "both at most %d)", dk, dv, CMAX);
+  WG_REQUIRE(ldq >= 2 * H * dk + H * dv && ldba >= 2 * H && ldo >= H * dv,
+             "wg_delta_rule_chunked: row strides too short for the heads");
+  WG_REQUIRE(save_at >= 0 && save_at <= M && (save_at == 0 || snapshot),
+             "wg_delta_rule_chunked: save_at %d of %d rows needs a snapshot buffer", save_at, M);
+  const size_t state_bytes = (size_t)H * dk * dv * sizeof(float);
+  WG_REQUIRE(!snapshot || !overlaps(snapshot, state_bytes, state, state_bytes),
+             "wg_delta_rule_chunked: the snapshot overlaps the state");
+  const size_t need = wg_delta_chunk_scratch_bytes(M, shape, save_at);
+  WG_REQUIRE(scratch_bytes >= need, "wg_delta_rule_chunked: scratch of %zu bytes, %zu needed",
+             scratch_bytes, need);
+  WG_REQUIRE(((uintptr_t)scratch & 15) == 0, "wg_delta_rule_chunked: scratch not 16-byte aligned");
+  static bool lds_set = false;
+  if (!lds_set) {
+    WG_HIP(hipFuncSetAttribute((const void *)delta_chunk_prep_kernel,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)PREP_LDS));
+    WG_HIP(hipFuncSetAttribute((const void *)delta_chunk_chain_kernel,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)CHAIN_LDS));
+    lds_set = true;
+  }
+  const int first = first_rows(save_at), nch = chunk_count(M, first);
+  const size_t rows = (size_t)H * nch * CH;
+  float *f = static_cast<float *>(scratch);
+  ChunkArgs a{qkv, ldq, ba, ldba, A, dt_bias, H, dk, dv, M, first, nch,
+              f, f + rows * dv, f + rows * (dv + dk), f + rows * (2 * dv + dk),
+              f + rows * (2 * dv + 2 * dk), f + rows * (2 * dv + 3 * dk),
+              state, snapshot, save_at, out, ldo};
+  hipStream_t s = as_stream(stream);
+  delta_chunk_prep_kernel<<<dim3(nch, H), 256, PREP_LDS, s>>>(a);
+  int rc = launched("wg_delta_rule_chunked");
+  if (rc) return rc;
+  delta_chunk_chain_kernel<<<dim3((dv + CBW - 1) / CBW, H), 256, CHAIN_LDS, s>>>(a);
+  return launched("wg_delta_rule_chunked");
 }
 
 int wg_delta_conv(const float *in, int32_t M, int32_t ldi, int32_t C, int32_t W,

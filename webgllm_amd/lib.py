@@ -225,6 +225,9 @@ def load():
                                          C.c_float, P, I32, I32, I32, P, P, P, SZ, P]),
         "wg_delta_rule": (C.c_int, [P, I32, I32, P, I32, P, P, C.POINTER(DeltaShape), P, P, I32,
                                     P, I32, P]),
+        "wg_delta_chunk_scratch_bytes": (SZ, [I32, C.POINTER(DeltaShape), I32]),
+        "wg_delta_rule_chunked": (C.c_int, [P, I32, I32, P, I32, P, P, C.POINTER(DeltaShape),
+                                            P, P, I32, P, I32, P, SZ, P]),
         "wg_delta_conv": (C.c_int, [P, I32, I32, I32, I32, P, P, P, P, I32, P]),
         "wg_delta_norm": (C.c_int, [P, I32, I32, C.POINTER(DeltaShape), P, I32, P, C.c_float, P,
                                     I32, P]),

@@ -489,6 +489,32 @@ def delta_rule(qkv: torch.Tensor, ba: torch.Tensor, A: torch.Tensor, dt_bias: to
     return (out, snapshot) if save_at else out
 
 
+def delta_rule_chunked(qkv: torch.Tensor, ba: torch.Tensor, A: torch.Tensor,
+                       dt_bias: torch.Tensor, heads: int, key_dim: int, value_dim: int,
+                       state: torch.Tensor, save_at: int = 0,
+                       snapshot: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                       scratch: torch.Tensor | None = None):
+    """delta_rule in chunks of 64 rows (wg_delta_rule_chunked): the same
+    results, for prompt batches."""
+    qkv, ba = _rows(qkv), _rows(ba)
+    _dev(A, torch.float32), _dev(dt_bias, torch.float32), _dev(state, torch.float32)
+    M = qkv.shape[0]
+    if out is None:
+        out = torch.empty((M, heads * value_dim), dtype=torch.float32, device=qkv.device)
+    if save_at and snapshot is None:
+        snapshot = torch.empty_like(state)
+    shape = L.DeltaShape(heads, key_dim, value_dim)
+    lib = L.load()
+    if scratch is None:
+        need = int(lib.wg_delta_chunk_scratch_bytes(M, C.byref(shape), save_at))
+        scratch = torch.empty((need + 3) // 4, dtype=torch.float32, device=qkv.device)
+    L.check(lib.wg_delta_rule_chunked(_p(qkv), M, qkv.stride(0), _p(ba), ba.stride(0), _p(A),
+                                      _p(dt_bias), C.byref(shape), _p(state), _p(snapshot),
+                                      save_at, _p(out), out.stride(0), _p(scratch),
+                                      scratch.numel() * scratch.element_size(), _stream()))
+    return (out, snapshot) if save_at else out
+
+
 def delta_conv(inp: torch.Tensor, channels: int, taps: torch.Tensor, state: torch.Tensor,
                state_out: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """silu of the causal depthwise convolution over the first `channels`
