@@ -292,13 +292,25 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(ChunkArgs a) {
   int c0, n;
   chunk_rows(a, c, c0, n);
   const int K = a.H * a.dk, dk = a.dk, dv = a.dv;
-  for (int idx = t; idx < CH * CMAX; idx += 256) {
-    const int r = idx / CMAX, i = idx % CMAX;
-    const float *row = a.qkv + (int64_t)(c0 + r) * a.ldq;
-    const bool in = r < n;
-    sq[r * RS + i] = in && i < dk ? row[h * dk + i] : 0.0f;
-    sk[r * RS + i] = in && i < dk ? row[K + h * dk + i] : 0.0f;
-    sv[r * RS + i] = in && i < dv ? row[2 * K + h * dv + i] : 0.0f;
+  {  // every load issued before the first store: thread t takes column t % 128 of rows 2u + t / 128
+    const int i = t & (CMAX - 1), r0 = t >> 7;
+    float rq[CH / 2], rk[CH / 2], rv[CH / 2];
+#pragma unroll
+    for (int u = 0; u < CH / 2; u++) {
+      const int r = 2 * u + r0;
+      const float *row = a.qkv + (int64_t)(c0 + r) * a.ldq;
+      const bool in = r < n;
+      rq[u] = in && i < dk ? row[h * dk + i] : 0.0f;
+      rk[u] = in && i < dk ? row[K + h * dk + i] : 0.0f;
+      rv[u] = in && i < dv ? row[2 * K + h * dv + i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < CH / 2; u++) {
+      const int r = 2 * u + r0;
+      sq[r * RS + i] = rq[u];
+      sk[r * RS + i] = rk[u];
+      sv[r * RS + i] = rv[u];
+    }
   }
   if (t < CH) {  // wave 0: the gates (LIN_GATES) and G by a shuffle scan (linCum)
     float beta = 0.0f, g = 0.0f;
@@ -317,7 +329,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(ChunkArgs a) {
     sG[t] = g;
     sE[t] = expf(g);
   }
-  __syncthreads();
+  lds_barrier();
   {  // LIN_PREP: four threads a row
     const int r = t >> 2, part = t & 3;
     float ssq = 0.0f, ssk = 0.0f;
@@ -336,7 +348,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(ChunkArgs a) {
       sk[r * RS + i] *= invk;
     }
   }
-  __syncthreads();
+  lds_barrier();
   {  // linGram: a 4 x 4 block of (row, key) pairs a thread, lower triangle only
     const int rb = t >> 4, sb = t & 15;
     float kk[4][4] = {}, qk[4][4] = {};
@@ -376,24 +388,25 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(ChunkArgs a) {
     a.Kt[(base + r) * dk + i] = expf(gl - sG[r]) * sk[r * RS + i];
   }
   if (t == 0) a.eg[h * a.nch + c] = expf(gl);
-  __syncthreads();
+  lds_barrier();
   if (t < 64) {  // linSolve: T = (I + A)^-1 by forward substitution, lane = column
     float Tc[CH];
 #pragma unroll
     for (int r = 0; r < CH; r++) {
-      float acc = lane == r ? 1.0f : 0.0f;
+      float acc[4] = {lane == r ? 1.0f : 0.0f, 0.0f, 0.0f, 0.0f};  // 4 chains, not one
 #pragma unroll
-      for (int s = 0; s < r; s++) acc = fmaf(-sA[r * AS + s], Tc[s], acc);
-      Tc[r] = acc;
+      for (int s = 0; s < r; s++) acc[s & 3] = fmaf(-sA[r * AS + s], Tc[s], acc[s & 3]);
+      Tc[r] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     }
 #pragma unroll
     for (int r = 0; r < CH; r++) sA[r * AS + lane] = Tc[r];
   }
-  __syncthreads();
+  lds_barrier();
   // linUW, then linQO: 4 rows x 8 columns (16 apart) a thread
   const int rb = t >> 4, jb = t & 15;
   const int smax = min(4 * rb + 3, n - 1);
   float u[4][8] = {}, w[4][8] = {};
+#pragma unroll 2
   for (int s = 0; s <= smax; s++) {
     const float bs = sB[s], be = bs * sE[s];
     float tr[4];
@@ -409,7 +422,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(ChunkArgs a) {
       }
     }
   }
-  __syncthreads();  // every read of v and k^ is done: U and W take their places
+  lds_barrier();  // every read of v and k^ is done: U and W take their places
 #pragma unroll
   for (int x = 0; x < 4; x++) {
     const int r = 4 * rb + x;
@@ -422,12 +435,13 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(ChunkArgs a) {
       if (r < n && j < dk) a.W[(base + r) * dk + j] = w[x][y];
     }
   }
-  __syncthreads();
+  lds_barrier();
   float o[4][8] = {}, qp[4][8];
 #pragma unroll
   for (int x = 0; x < 4; x++)
 #pragma unroll
     for (int y = 0; y < 8; y++) qp[x][y] = sE[4 * rb + x] * sq[(4 * rb + x) * RS + jb + 16 * y];
+#pragma unroll 2
   for (int s = 0; s <= smax; s++) {
     float pr[4];
 #pragma unroll
@@ -455,7 +469,42 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(ChunkArgs a) {
   }
 }
 
-__global__ __launch_bounds__(256) void delta_chunk_chain_kernel(ChunkArgs a) {
+constexpr int CT = 512;                   // chain threads
+constexpr int CG = CT / CBW;              // their groups (32)
+constexpr int DROWS = CH / CG;            // D and O rows a thread
+constexpr int SROWS = CMAX / CG;          // state rows a thread
+constexpr int SPT = CH * CMAX / 4 / CT;   // float4 of each staged tile a thread
+
+__device__ __forceinline__ void chain_fetch(const ChunkArgs &a, int c, int h, int t, int g,
+                                            int jj, bool col, float4 (&pw)[SPT],
+                                            float4 (&pq)[SPT], float4 (&pk)[SPT],
+                                            float (&pu)[DROWS], float (&po)[DROWS],
+                                            float &pe) {
+  int c0, n;
+  chunk_rows(a, c, c0, n);
+  const int64_t base = (int64_t)(h * a.nch + c) * CH;
+  const int dk = a.dk, dv = a.dv;
+#pragma unroll
+  for (int u = 0; u < SPT; u++) {
+    const int idx = t + CT * u, r = idx / (CMAX / 4), i = (idx % (CMAX / 4)) * 4;
+    pw[u] = pq[u] = pk[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (r < n && i < dk) {  // (a select of the two would put the zero in memory)
+      pw[u] = *reinterpret_cast<const float4 *>(&a.W[(base + r) * dk + i]);
+      pq[u] = *reinterpret_cast<const float4 *>(&a.Qp[(base + r) * dk + i]);
+      pk[u] = *reinterpret_cast<const float4 *>(&a.Kt[(base + r) * dk + i]);
+    }
+  }
+#pragma unroll
+  for (int x = 0; x < DROWS; x++) {
+    const int r = DROWS * g + x;
+    const bool in = r < n && col;
+    pu[x] = in ? a.U[(base + r) * dv + jj] : 0.0f;
+    po[x] = in ? a.Oi[(base + r) * dv + jj] : 0.0f;
+  }
+  pe = a.eg[h * a.nch + c];
+}
+
+__global__ __launch_bounds__(CT) void delta_chunk_chain_kernel(ChunkArgs a) {
   extern __shared__ __align__(16) float sm[];
   float *sS = sm;                                           // [CMAX][CBW] state block
   float *sW = sS + CMAX * CBW, *sQ = sW + CH * RS, *sK = sQ + CH * RS;  // [CH][RS]
@@ -465,63 +514,90 @@ __global__ __launch_bounds__(256) void delta_chunk_chain_kernel(ChunkArgs a) {
   const bool col = jj < a.dv;
   const int dk = a.dk, dv = a.dv;
   float *Sh = a.state + (int64_t)h * dk * dv;
-  for (int i = g; i < CMAX; i += 256 / CBW)
-    sS[i * CBW + j] = col && i < dk ? Sh[(int64_t)i * dv + jj] : 0.0f;
+  for (int i = g; i < CMAX; i += CG) sS[i * CBW + j] = col && i < dk ? Sh[(int64_t)i * dv + jj] : 0.0f;
+  // A chunk's W, Q', K~ tiles and this thread's U and Oi, fetched into
+  // registers one chunk ahead.
+  float4 pw[SPT], pq[SPT], pk[SPT];
+  float pu[DROWS], po[DROWS], pe;
+  chain_fetch(a, 0, h, t, g, jj, col, pw, pq, pk, pu, po, pe);
   for (int c = 0; c < a.nch; c++) {
     int c0, n;
     chunk_rows(a, c, c0, n);
-    const int64_t base = (int64_t)(h * a.nch + c) * CH;
-    for (int idx = t; idx < CH * CMAX / 4; idx += 256) {
-      const int r = idx / (CMAX / 4), i = (idx % (CMAX / 4)) * 4;
-      float4 w4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), q4 = w4, k4 = w4;
-      if (r < n && i < dk) {
-        w4 = *reinterpret_cast<const float4 *>(&a.W[(base + r) * dk + i]);
-        q4 = *reinterpret_cast<const float4 *>(&a.Qp[(base + r) * dk + i]);
-        k4 = *reinterpret_cast<const float4 *>(&a.Kt[(base + r) * dk + i]);
+#pragma unroll
+    for (int u = 0; u < SPT; u++) {
+      const int idx = t + CT * u, r = idx / (CMAX / 4), i = (idx % (CMAX / 4)) * 4;
+      *reinterpret_cast<float4 *>(&sW[r * RS + i]) = pw[u];
+      *reinterpret_cast<float4 *>(&sQ[r * RS + i]) = pq[u];
+      *reinterpret_cast<float4 *>(&sK[r * RS + i]) = pk[u];
+    }
+    float d[DROWS], o[DROWS];
+#pragma unroll
+    for (int x = 0; x < DROWS; x++) {
+      d[x] = pu[x];
+      o[x] = po[x];
+    }
+    const float e = pe;
+    lds_barrier();
+    if (c + 1 < a.nch)  // in flight while this chunk computes
+      chain_fetch(a, c + 1, h, t, g, jj, col, pw, pq, pk, pu, po, pe);
+    // linChunkOut: D = U - W S, O = Oi + Q' S, rows DROWS g ..
+    for (int i = 0; i < dk; i += 8) {  // dk is a multiple of 4: the operands of two steps first
+      float sv[8];
+      float4 wv[2][DROWS], qv[2][DROWS];
+#pragma unroll
+      for (int q = 0; q < 8; q++) sv[q] = sS[(i + q) * CBW + j];  // rows dk.. (< 128) are 0
+#pragma unroll
+      for (int q = 0; q < 2; q++)
+#pragma unroll
+        for (int x = 0; x < DROWS; x++) {
+          wv[q][x] = *reinterpret_cast<const float4 *>(&sW[(DROWS * g + x) * RS + i + 4 * q]);
+          qv[q][x] = *reinterpret_cast<const float4 *>(&sQ[(DROWS * g + x) * RS + i + 4 * q]);
+        }
+#pragma unroll
+      for (int q = 0; q < 2; q++) {
+        const float4 s4 = make_float4(sv[4 * q], sv[4 * q + 1], sv[4 * q + 2], sv[4 * q + 3]);
+#pragma unroll
+        for (int x = 0; x < DROWS; x++) {
+          d[x] -= dot4(wv[q][x], s4);
+          o[x] += dot4(qv[q][x], s4);
+        }
       }
-      *reinterpret_cast<float4 *>(&sW[r * RS + i]) = w4;
-      *reinterpret_cast<float4 *>(&sQ[r * RS + i]) = q4;
-      *reinterpret_cast<float4 *>(&sK[r * RS + i]) = k4;
-    }
-    float d[4], o[4];
-#pragma unroll
-    for (int x = 0; x < 4; x++) {
-      const int r = 4 * g + x;
-      const bool in = r < n && col;
-      d[x] = in ? a.U[(base + r) * dv + jj] : 0.0f;
-      o[x] = in ? a.Oi[(base + r) * dv + jj] : 0.0f;
-    }
-    __syncthreads();
-    // linChunkOut: D = U - W S, O = Oi + Q' S, rows 4g .. 4g + 3
-    for (int i = 0; i < dk; i += 4) {
-      const float4 s4 = make_float4(sS[i * CBW + j], sS[(i + 1) * CBW + j],
-                                    sS[(i + 2) * CBW + j], sS[(i + 3) * CBW + j]);
-#pragma unroll
-      for (int x = 0; x < 4; x++) {
-        d[x] -= dot4(*reinterpret_cast<const float4 *>(&sW[(4 * g + x) * RS + i]), s4);
-        o[x] += dot4(*reinterpret_cast<const float4 *>(&sQ[(4 * g + x) * RS + i]), s4);
-      }
     }
 #pragma unroll
-    for (int x = 0; x < 4; x++) {
-      const int r = 4 * g + x;
+    for (int x = 0; x < DROWS; x++) {
+      const int r = DROWS * g + x;
       sD[r * CBW + j] = r < n ? d[x] : 0.0f;
       if (r < n && col) a.out[(int64_t)(c0 + r) * a.ldo + h * dv + jj] = o[x];
     }
-    __syncthreads();
-    // linChunkState: S <- e^{G_last} S + K~^T D
-    const float e = a.eg[h * a.nch + c];
-    for (int i = g; i < dk; i += 256 / CBW) {
-      float acc = e * sS[i * CBW + j];
-      for (int r = 0; r < n; r++) acc = fmaf(sK[r * RS + i], sD[r * CBW + j], acc);
-      sS[i * CBW + j] = acc;
-      if (a.snap && c0 + n == a.save_at && col)
-        a.snap[(int64_t)h * dk * dv + (int64_t)i * dv + jj] = acc;
+    lds_barrier();
+    // linChunkState: S <- e^{G_last} S + K~^T D, state rows g + CG u
+    float acc[SROWS];
+#pragma unroll
+    for (int u = 0; u < SROWS; u++) acc[u] = e * sS[(g + CG * u) * CBW + j];
+    for (int r = 0; r < n; r += 4) {  // rows past n hold D = 0 and K~ = 0
+      float dr[4], kv[4][SROWS];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        dr[q] = sD[(r + q) * CBW + j];
+#pragma unroll
+        for (int u = 0; u < SROWS; u++) kv[q][u] = sK[(r + q) * RS + g + CG * u];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int u = 0; u < SROWS; u++) acc[u] = fmaf(kv[q][u], dr[q], acc[u]);
     }
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < SROWS; u++) {
+      const int i = g + CG * u;
+      sS[i * CBW + j] = acc[u];
+      if (a.snap && c0 + n == a.save_at && col && i < dk)
+        a.snap[(int64_t)h * dk * dv + (int64_t)i * dv + jj] = acc[u];
+    }
+    lds_barrier();
   }
   if (col)
-    for (int i = g; i < dk; i += 256 / CBW) Sh[(int64_t)i * dv + jj] = sS[i * CBW + j];
+    for (int i = g; i < dk; i += CG) Sh[(int64_t)i * dv + jj] = sS[i * CBW + j];
 }
 
 // Chunks of a batch of M rows whose first chunk has `first` rows.
@@ -614,7 +690,7 @@ int wg_delta_rule_chunked(const float *qkv, int32_t M, int32_t ldq, const float 
   delta_chunk_prep_kernel<<<dim3(nch, H), 256, PREP_LDS, s>>>(a);
   int rc = launched("wg_delta_rule_chunked");
   if (rc) return rc;
-  delta_chunk_chain_kernel<<<dim3((dv + CBW - 1) / CBW, H), 256, CHAIN_LDS, s>>>(a);
+  delta_chunk_chain_kernel<<<dim3((dv + CBW - 1) / CBW, H), CT, CHAIN_LDS, s>>>(a);
   return launched("wg_delta_rule_chunked");
 }
 
