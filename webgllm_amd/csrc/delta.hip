@@ -509,8 +509,11 @@ __global__ __launch_bounds__(CT) void delta_chunk_chain_kernel(ChunkArgs a) {
   float *sS = sm;                                           // [CMAX][CBW] state block
   float *sW = sS + CMAX * CBW, *sQ = sW + CH * RS, *sK = sQ + CH * RS;  // [CH][RS]
   float *sD = sK + CH * RS;                                 // [CH][CBW]
-  const int h = blockIdx.y, t = threadIdx.x, j = t & (CBW - 1), g = t / CBW;
-  const int jj = blockIdx.x * CBW + j;
+  // blockIdx.x is the head: the workgroups of one head (consecutive in
+  // blockIdx.y, H apart in launch order) land on one XCD, whose L2 then
+  // serves the head's tiles to all of them.
+  const int h = blockIdx.x, t = threadIdx.x, j = t & (CBW - 1), g = t / CBW;
+  const int jj = blockIdx.y * CBW + j;
   const bool col = jj < a.dv;
   const int dk = a.dk, dv = a.dv;
   float *Sh = a.state + (int64_t)h * dk * dv;
@@ -690,7 +693,7 @@ int wg_delta_rule_chunked(const float *qkv, int32_t M, int32_t ldq, const float 
   delta_chunk_prep_kernel<<<dim3(nch, H), 256, PREP_LDS, s>>>(a);
   int rc = launched("wg_delta_rule_chunked");
   if (rc) return rc;
-  delta_chunk_chain_kernel<<<dim3((dv + CBW - 1) / CBW, H), CT, CHAIN_LDS, s>>>(a);
+  delta_chunk_chain_kernel<<<dim3(H, (dv + CBW - 1) / CBW), CT, CHAIN_LDS, s>>>(a);
   return launched("wg_delta_rule_chunked");
 }
 
