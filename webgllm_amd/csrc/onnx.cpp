@@ -290,6 +290,8 @@ int wg_onnx_open(const char *path, wg_onnx **out) {
     rc = wg::fail(WG_ERR_INVALID, "ONNX: truncated message");
   } catch (int wire) {
     rc = wg::fail(WG_ERR_INVALID, "ONNX: unsupported wire type %d", wire);
+  } catch (...) {  // no exception leaves the C ABI (a huge count: bad_alloc)
+    rc = wg::fail(WG_ERR_OOM, "ONNX: %s: out of host memory while parsing", path);
   }
   if (rc != WG_OK) {
     if (f->map) munmap((void *)f->map, f->size);
