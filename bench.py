@@ -681,7 +681,7 @@ def workload_sample_pick(args):
     import numpy as np
     import torch
     from webgllm_amd import lib as L, ops
-    from webgllm_amd.sampler import Sampler, draw
+    from webgllm_amd.sampler import GpuPick, Sampler, draw
     V, count = 128256, 64
     g = torch.Generator(device="cuda").manual_seed(3)
     logits = torch.randn((1, V), device="cuda", generator=g) * 3
@@ -690,9 +690,6 @@ def workload_sample_pick(args):
     scratch = torch.empty(int(L.load().wg_pick_scratch_bytes(1, V)), dtype=torch.uint8,
                           device="cuda")
 
-    def pick():
-        return ops.pick_candidates(logits, count, mask=mask, penalty=1.1,
-                                   presence_penalty=0.2, scratch=scratch)
     chunks_out = torch.empty((1, count), dtype=torch.int32, device="cuda")
     cand_out = torch.empty((1, count, 256), device="cuda")
     lib = L.load()
@@ -710,13 +707,15 @@ def workload_sample_pick(args):
     algo = V * 4 + V + 2 * count * 256 * 4 + count * 4  # logits, mask, gather reread + out
     gbps = algo / (ms * 1e-3) / 1e9
     s = Sampler(0.8, 40, top_p=0.95, repetition_penalty=1.1, presence_penalty=0.2)
+    gp = GpuPick(V, count)
+    gp.mask.copy_(mask)
     r = np.random.default_rng(0)
+    for _ in range(20):
+        draw(gp(logits[0], s), r.random)
     t0 = time.time()
     n = 200
     for _ in range(n):
-        chunks, cand = pick()
-        d = s.candidates(chunks.cpu().numpy()[0], cand.cpu().numpy()[0])
-        draw(d, r.random)
+        draw(gp(logits[0], s), r.random)
     host_ms = (time.time() - t0) * 1e3 / n
     cpu = None
     if not args.no_cpu:

@@ -617,27 +617,16 @@ class Engine:
         the token from them. The window sees the prompt, then each token
         written. Returns the `steps` tokens drawn."""
         from . import sampler as S
-        s = self.shape
-        V = s.vocab
-        mask = torch.zeros(V, dtype=torch.uint8, device=self.device)
-        scratch = torch.empty(int(L.load().wg_pick_scratch_bytes(1, V)), dtype=torch.uint8,
-                              device=self.device)
-        changes = sampler.see(prompt)
+        pick = S.GpuPick(self.shape.vocab, count, device=self.device)
+        pick.see(sampler.see(prompt))
         out = []
         tokens = list(prompt)
         for _ in range(steps):
             self.forward(tokens)
-            for t, st in changes:
-                mask[t] = st
             row = (len(tokens) - 1) % 8
-            chunks, cand = ops.pick_candidates(
-                self.logits[row:row + 1], min(count, (V + 255) // 256), mask=mask,
-                penalty=sampler.repetition_penalty, presence_penalty=sampler.presence_penalty,
-                scratch=scratch)
-            d = sampler.candidates(chunks.cpu().numpy()[0], cand.cpu().numpy()[0])
-            t = S.draw(d, random)
+            t = S.draw(pick(self.logits[row], sampler), random)
             out.append(t)
-            changes = sampler.see([t], True)
+            pick.see(sampler.see([t], True))
             tokens = [t]
         return out
 

@@ -211,6 +211,52 @@ class Sampler:
                                  penalize=False, ids=ids)
 
 
+class GpuPick:
+    """Engine.pick's device half for one vocabulary (src/engine.ts:8352-8473)
+    with its buffers kept: the penalty mask on the device (updated from the
+    window's changes in one write), wg_pick_candidates into preallocated
+    outputs, and one read-back into pinned host memory."""
+
+    def __init__(self, vocab: int, count: int = 64, device="cuda"):
+        import torch
+        from . import ops
+        self.V = vocab
+        self.count = min(count, (vocab + 255) // 256)
+        self.mask = torch.zeros(vocab, dtype=torch.uint8, device=device)
+        self.scratch = torch.empty(int(_bind().wg_pick_scratch_bytes(1, vocab)),
+                                   dtype=torch.uint8, device=device)
+        n = self.count * 256
+        # chunk ids then candidates, one buffer so that one copy reads both back
+        self.dev = torch.empty(self.count + n, dtype=torch.float32, device=device)
+        self.host = torch.empty(self.count + n, dtype=torch.float32, pin_memory=True)
+        self.offsets = np.arange(256, dtype=np.int64)
+        self._ops = ops
+
+    def see(self, changes) -> None:
+        """The window's state changes [(token, state)] into the device mask."""
+        import torch
+        if changes:
+            t = torch.tensor([c[0] for c in changes], dtype=torch.int64)
+            v = torch.tensor([c[1] for c in changes], dtype=torch.uint8)
+            self.mask[t.to(self.mask.device)] = v.to(self.mask.device)
+
+    def __call__(self, logits_row, sampler: "Sampler") -> Distribution:
+        import torch
+        lib = L.load()
+        chunks = self.dev[:self.count].view(torch.int32)
+        L.check(lib.wg_pick_candidates(
+            logits_row.data_ptr(), 1, self.V, self.V, self.mask.data_ptr(), None, 0, 0,
+            float(sampler.repetition_penalty), float(sampler.presence_penalty), None, 0, 0,
+            self.count, chunks.data_ptr(), self.dev[self.count:].data_ptr(),
+            self.scratch.data_ptr(), self.scratch.numel(), self._ops._stream()))
+        self.host.copy_(self.dev, non_blocking=True)
+        torch.cuda.current_stream().synchronize()
+        h = self.host.numpy()
+        ch = h[:self.count].view(np.int32).astype(np.int64)
+        ids = (ch[:, None] * 256 + self.offsets[None, :]).astype(np.int32).reshape(-1)
+        return sampler.distribution(h[self.count:].copy(), penalize=False, ids=ids)
+
+
 def _random(random):
     import random as _r
     return random if random is not None else _r.random
