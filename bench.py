@@ -916,7 +916,13 @@ def main():
                     choices=["llama8b-decode"] + sorted(WORKLOADS),
                     help="the headline Llama-3-8B-shape decode (default) or another "
                          "configuration's measurement")
+    ap.add_argument("--tuning", action="append", default=[], metavar="NAME=VALUE",
+                    help="set a launch-shape knob of the library (wg_tuning_set) first")
     args = ap.parse_args()
+    for kv in args.tuning:
+        from webgllm_amd import lib as _L
+        name, value = kv.split("=")
+        _L.check(_L.load().wg_tuning_set(name.encode(), int(value)))
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(--gpus {args.gpus} asked)", file=sys.stderr)

@@ -132,28 +132,31 @@ __device__ inline void epi_prefetch(const wg_epilogue &e, int g, int G, int pos0
   }
 }
 
-// Picks tot[m] for this lane's token without dynamic register indexing.
-template <int M>
-__device__ inline float pick(const float tot[M], int m) {
-  float v = tot[0];
-#pragma unroll
-  for (int i = 1; i < M; i++)
-    if (m == i) v = tot[i];
-  return v;
+// Picks tot[m] for this lane's token without dynamic register indexing:
+// a chain of selects on constant indices, written as a compile-time
+// recursion (a loop over i, not yet unrolled when the compiler looks for
+// dynamically indexed arrays, moved the M floats into LDS from M = 3 on).
+template <int M, int I = 0>
+__device__ inline float pick(const float (&tot)[M], int m) {
+  if constexpr (I + 1 >= M) {
+    return tot[I];
+  } else {
+    return m == I ? tot[I] : pick<M, I + 1>(tot, m);
+  }
 }
 
 // Row group g's four rows for tokens 0..M-1, with the operands
 // epi_prefetch<M, MODE> loaded for g. Called by every lane of the wave (the
 // shuffles need all of them), with g >= G for idle waves.
 template <int M, int MODE>
-__device__ inline void finish(const wg_epilogue &e, int g, int G, const float tot[M],
-                              const float scale[M], float *y, int ldy, const EpiPre &pre,
+__device__ inline void finish(const wg_epilogue &e, int g, int G, const float (&tot)[M],
+                              const float (&scale)[M], float *y, int ldy, const EpiPre &pre,
                               int pos0) {
   const int lane = threadIdx.x & 63;
   const int r = (lane >> 4) & 3, m = lane & 15;
   const bool live = g < G && m < M;
   const int mm = m < M ? m : 0;
-  float v = pick<M>(tot, mm) * 0x1p24f * scale[mm];
+  float v = pick<M>(tot, mm) * 0x1p24f * pick<M>(scale, mm);  // (an index would put scale in LDS)
   const int n = 4 * g + r;
   if constexpr (MODE == WG_EPI_STORE) {
     if (live && e.residual) v += pre.res;

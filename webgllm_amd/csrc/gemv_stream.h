@@ -1,0 +1,128 @@
+// The streaming GEMV kernel for 4-bit row-group matrices, shared by the
+// decode launcher (1 or 2 tokens, gemv.hip) and the few-token one (3 to 8
+// tokens, gemv_few.hip), each translation unit instantiating its own forms.
+#pragma once
+
+#include "common.h"
+#include "dot.h"
+#include "epilogue.h"
+#include "gemv_core.h"
+
+namespace wg {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Streaming variant (decode, and verify batches of up to 8 tokens): persistent
+// workgroups of 4 waves. The K range is split into KS parts (a wave per
+// part, KS waves per row group, reduced through LDS); lane l of a part
+// takes its blocks l and l + 64 (NB of them), whose activations and block
+// sums it loads once into registers: they are the same for every row
+// group. Row groups are streamed: the next row group's nibbles, scales and
+// zero points are loaded before the current one is computed.
+template <int M, int ZK, int NB, int KS, int MODE>
+__global__ __launch_bounds__(256) void gemv_stream_kernel(
+    const uint4 *__restrict__ quants, const uint16_t *__restrict__ scales,
+    const void *__restrict__ zeros, const uint16_t *__restrict__ x, int ldx,
+    float *__restrict__ y, int ldy, const wg_epilogue e, int G, int B) {
+  constexpr int RGW = 4 / KS;  // row groups a workgroup takes at a time
+  __shared__ float red[2][4][4 * M];
+  __shared__ float nred[4 * M];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int part = wave % KS, slot = wave / KS;
+  const int BP = (B + KS - 1) / KS;
+  const int b0 = part * BP + lane;
+  const int b_end = min(B, (part + 1) * BP);
+
+  // The first row group's weights go out first: they need no input, and
+  // everything after them (activations, sums, the norm's parts) overlaps
+  // their flight.
+  const int stride = gridDim.x * RGW;
+  int g = blockIdx.x * RGW + slot;
+  Unit<ZK, NB> next;
+  load_unit<ZK, NB>(next, quants, scales, zeros, g, B, b0, b_end, g < G);
+  // and the first row group's epilogue operands (the waves that finish)
+  const int pos0 = epi_pos0<MODE>(e);
+  EpiPre pnext = {};
+  if (part == 0) epi_prefetch<M, MODE>(e, g, G, pos0, pnext);
+
+  // This lane's activations and their block sums (times 2^-24), once.
+  uint4 a[M][NB][4];
+  float sa[M][NB];
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      int b = b0 + 64 * j;
+      if (b < b_end) {
+        const uint4 *xp = reinterpret_cast<const uint4 *>(x + (int64_t)m * ldx + b * 32);
+        a[m][j][0] = xp[0];
+        a[m][j][1] = xp[1];
+        a[m][j][2] = xp[2];
+        a[m][j][3] = xp[3];
+      } else {
+        a[m][j][0] = a[m][j][1] = a[m][j][2] = a[m][j][3] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  float scale[M];
+  input_scales_wg<M, 4>(e, scale, nred);
+#pragma unroll
+  for (int m = 0; m < M; m++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) sa[m][j] = block_sum(a[m][j]) * 0x1p-24f;
+
+  int it = 0;
+  for (int g0 = blockIdx.x * RGW; g0 < G; g0 += stride, g += stride, it ^= 1) {
+    Unit<ZK, NB> u = next;
+    load_unit<ZK, NB>(next, quants, scales, zeros, g + stride, B, b0, b_end, g + stride < G);
+    const EpiPre pe = pnext;
+    if (part == 0) epi_prefetch<M, MODE>(e, g + stride, G, pos0, pnext);
+    float acc[4][M];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+      for (int m = 0; m < M; m++) acc[r][m] = 0.0f;
+    accumulate_unit<M, ZK, NB>(u, a, sa, acc);
+    const int row = wave_sum4_row();
+    float tot[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) tot[m] = wave_sum4(acc[0][m], acc[1][m], acc[2][m], acc[3][m]);
+    if constexpr (KS > 1) {
+      // Parts 1.. hand their sums to part 0 through LDS (double-buffered by
+      // iteration parity, so one barrier a row group suffices).
+      if ((lane & 15) == 0 && part > 0)
+#pragma unroll
+        for (int m = 0; m < M; m++) red[it][wave][row * M + m] = tot[m];
+      __syncthreads();
+      if (part == 0)
+#pragma unroll
+        for (int m = 0; m < M; m++)
+#pragma unroll
+          for (int p = 1; p < KS; p++) tot[m] += red[it][wave + p][row * M + m];
+    }
+    if (part == 0) finish<M, MODE>(e, g, G, tot, scale, y, ldy, pe, pos0);
+  }
+}
+
+template <int M, int ZK, int NB, int KS>
+int launch_stream(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
+                  const wg_epilogue &e, hipStream_t s) {
+  int G = w->N / 4, B = w->K / 32;
+  constexpr int RGW = 4 / KS;
+  int grid = persistent_grid((G + RGW - 1) / RGW,
+                             tuning(G >= 16384 ? "gemv_wg_per_cu_wide" : "gemv_wg_per_cu"));
+  auto q = (const uint4 *)w->quants;
+  auto sc = (const uint16_t *)w->scales;
+  if (e.mode == WG_EPI_SWIGLU)
+    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_SWIGLU><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, ldx,
+                                                                         y, ldy, e, G, B);
+  else if (e.mode == WG_EPI_ROPE_KV)
+    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_ROPE_KV><<<grid, 256, 0, s>>>(q, sc, w->zeros, x,
+                                                                          ldx, y, ldy, e, G, B);
+  else
+    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_STORE><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, ldx,
+                                                                        y, ldy, e, G, B);
+  return launched("wg_q4_gemv");
+}
+
+}  // namespace
+}  // namespace wg

@@ -12,6 +12,11 @@ int check_epilogue(const wg_q4_matrix *w, int M, const float *y, int ldy, const 
 int launch_gemv_q4k(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y, int ldy,
                     const wg_epilogue &e, hipStream_t s);
 // WG_LAYOUT_Q8 and WG_LAYOUT_Q6K matrices.
+// 4-bit row-group GEMV of 3 to 8 tokens on the streaming kernel, or -1
+// when the shape (more than 256 blocks a row) or the knob leaves it to the
+// row-group kernel.
+int launch_gemv_few(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y,
+                    int ldy, const wg_epilogue &e, hipStream_t s);
 int launch_gemv_wide(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y, int ldy,
                      const wg_epilogue &e, hipStream_t s);
 
