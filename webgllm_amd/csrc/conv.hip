@@ -20,30 +20,62 @@ __device__ inline uint16_t to_h(float v) {
 
 // Thread = channel c: it reads its channel's old state before writing, so
 // state_out may be the state itself.
-__global__ void short_conv_kernel(const float *bcx, int M, int D, int ldb, int W,
-                                  const float *taps, const float *state, float *state_out,
-                                  float *prefixes, uint16_t *out, int ldo) {
-  int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= D) return;
-  const int w1 = W - 1;
-  // win: the last W - 1 values of y (oldest first), slid along the tokens
-  float win[MAX_W - 1];
-  for (int i = 0; i < w1; i++) win[i] = state[(int64_t)i * D + c];
-  float tp[MAX_W];
-  for (int k = 0; k < W; k++) tp[k] = taps[(int64_t)c * W + k];
-  for (int t = 0; t < M; t++) {
-    const float *row = bcx + (int64_t)t * ldb;
-    const float y = row[c] * row[2 * D + c];
-    float a = 0.0f;
-    for (int k = 0; k < w1; k++) a += tp[k] * win[k];
-    a += tp[w1] * y;
-    out[(int64_t)t * ldo + c] = to_h(row[D + c] * a);
-    for (int k = 0; k + 1 < w1; k++) win[k] = win[k + 1];
-    win[w1 - 1] = y;
-    if (prefixes)  // the state after the first t + 1 tokens
-      for (int i = 0; i < w1; i++) prefixes[((int64_t)t * w1 + i) * D + c] = win[i];
+// A workgroup takes CONV_CH channels and all the batch's tokens, CONV_TOK
+// at a time: each thread computes one token's output from the W values of
+// y = B x it needs (from the batch, or the state for the first W - 1), so
+// the tokens of a channel do not wait on each other. The new state is
+// written after a barrier, when every read of the old one (which it may
+// replace in place) is done.
+constexpr int CONV_CH = 32, CONV_TOK = 8;
+
+template <int W>
+__global__ __launch_bounds__(CONV_CH * CONV_TOK) void short_conv_kernel(
+    const float *bcx, int M, int D, int ldb, const float *taps, const float *state,
+    float *state_out, float *prefixes, uint16_t *out, int ldo) {
+  const int tl = threadIdx.x / CONV_CH, c = blockIdx.x * CONV_CH + threadIdx.x % CONV_CH;
+  const bool live = c < D;
+  // y of token s (s < 0: row W - 1 + s of the state, oldest first)
+  auto yval = [&](int s) -> float {
+    if (s >= 0) {
+      const float *row = bcx + (int64_t)s * ldb;
+      return row[c] * row[2 * D + c];
+    }
+    return state[(int64_t)(W - 1 + s) * D + c];
+  };
+  if (live) {
+    float tp[W];
+#pragma unroll
+    for (int k = 0; k < W; k++) tp[k] = taps[(int64_t)c * W + k];
+    for (int t = tl; t < M; t += CONV_TOK) {
+      float y[W];
+#pragma unroll
+      for (int k = 0; k < W; k++) y[k] = yval(t - (W - 1) + k);
+      const float gate = bcx[(int64_t)t * ldb + D + c];
+      float a = 0.0f;
+#pragma unroll
+      for (int k = 0; k < W; k++) a += tp[k] * y[k];
+      out[(int64_t)t * ldo + c] = to_h(gate * a);
+      if (prefixes)  // the state after the first t + 1 tokens
+#pragma unroll
+        for (int i = 0; i < W - 1; i++) prefixes[((int64_t)t * (W - 1) + i) * D + c] = y[i + 1];
+    }
   }
-  for (int i = 0; i < w1; i++) state_out[(int64_t)i * D + c] = win[i];
+  float ns[W - 1];
+  if (tl == 0 && live)
+#pragma unroll
+    for (int i = 0; i < W - 1; i++) ns[i] = yval(M - (W - 1) + i);
+  __syncthreads();
+  if (tl == 0 && live)
+#pragma unroll
+    for (int i = 0; i < W - 1; i++) state_out[(int64_t)i * D + c] = ns[i];
+}
+
+template <int W>
+void launch_short_conv(const float *bcx, int M, int D, int ldb, const float *taps,
+                       const float *state, float *state_out, float *prefixes, uint16_t *out,
+                       int ldo, hipStream_t s) {
+  short_conv_kernel<W><<<(D + CONV_CH - 1) / CONV_CH, CONV_CH * CONV_TOK, 0, s>>>(
+      bcx, M, D, ldb, taps, state, state_out, prefixes, out, ldo);
 }
 
 __global__ void copy_rows_kernel(const float *src, float *dst, int64_t n) {
@@ -68,8 +100,14 @@ int wg_short_conv(const float *bcx, int32_t M, int32_t D, int32_t ldb, int32_t W
   WG_REQUIRE(state == state_out || !overlaps(state, (size_t)(W - 1) * D * 4, state_out,
                                              (size_t)(W - 1) * D * 4),
              "wg_short_conv: state and new state partly overlap");
-  short_conv_kernel<<<(D + 255) / 256, 256, 0, as_stream(stream)>>>(
-      bcx, M, D, ldb, W, taps, state, state_out, prefixes, out, ldo);
+  hipStream_t s = as_stream(stream);
+  switch (W) {
+#define WG_CONV_W(n) \
+  case n: launch_short_conv<n>(bcx, M, D, ldb, taps, state, state_out, prefixes, out, ldo, s); break;
+    WG_CONV_W(2) WG_CONV_W(3) WG_CONV_W(4) WG_CONV_W(5) WG_CONV_W(6) WG_CONV_W(7) WG_CONV_W(8)
+#undef WG_CONV_W
+    default: return wg::fail(WG_ERR_INVALID, "wg_short_conv: width %d", W);
+  }
   return launched("wg_short_conv");
 }
 
