@@ -322,14 +322,14 @@ def workload_nbits_gemm(args, fmt="nbits"):
                 per_shape_tflops={str(N): round(r[1], 1) for N, r in res.items()})
 
 
-def decode_engine_run(shape, ctx, prompt_len, steps, warmup):
+def decode_engine_run(shape, ctx, prompt_len, steps, warmup, persistent=False):
     """Prefill random ids, capture the token step, warm up, then time
     `steps` graph replays. Returns (engine, weights, ms a token, first
     timed position)."""
     import torch
     from webgllm_amd import engine as E
     w = E.Weights(shape, seed=0)
-    eng = E.Engine(w, ctx)
+    eng = E.Engine(w, ctx, persistent=persistent)
     prompt = torch.randint(0, shape.vocab, (prompt_len,),
                            generator=torch.Generator().manual_seed(1)).tolist()
     first = int(eng.forward(prompt)[-1])
@@ -350,7 +350,7 @@ def workload_qwen2_decode(args):
     from webgllm_amd import engine as E
     shape = E.QWEN2_05B
     steps = 1024 - 512 - args.warmup - 1
-    eng, w, ms, p0 = decode_engine_run(shape, 1024, 512, steps, args.warmup)
+    eng, w, ms, p0 = decode_engine_run(shape, 1024, 512, steps, args.warmup, args.persistent)
     kv = shape.layers * 2 * shape.kv_heads * shape.head_dim * 2 * (p0 + steps // 2)
     token_bytes = w.nbytes + kv
     cpu = cpu_baseline(eng, min(os.cpu_count() or 1, 16), 10.0) if not args.no_cpu else None
@@ -363,7 +363,8 @@ def workload_qwen2_decode(args):
     cfg = {"workload": f"Qwen2-0.5B-shape greedy decode, positions {p0}..{p0 + steps - 1}",
            "model": shape.name, "layers": shape.layers, "hidden": shape.hidden,
            "vocab": shape.vocab, "weights": "random MatMulNBits q4 (u8 zero points)",
-           "global_batch": 1, "seq_len": 1024, "parallelism": "none"}
+           "global_batch": 1, "seq_len": 1024, "parallelism": "none",
+           "decode_path": "persistent" if eng.plan is not None else "per-op kernels"}
     return line("decode tok/s, Qwen2-0.5B-shape MatMulNBits batch 1", round(1000.0 / ms, 2),
                 "tok/s", steps, args.warmup, ms, cfg, roof, cpu)
 

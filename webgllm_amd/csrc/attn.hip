@@ -768,14 +768,9 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
           q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, partial, chunks, out, ldo);
   } else {
     size_t lds = attn_lds_bytes((H / KV) * M, hd);
-    static bool raised = false;  // allow more than 64 KiB of dynamic LDS, once
-    if (!raised) {
-      WG_HIP(hipFuncSetAttribute((const void *)attn_chunk_kernel<64>,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-      WG_HIP(hipFuncSetAttribute((const void *)attn_chunk_kernel<128>,
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-      raised = true;
-    }
+    int rc = raise_lds((const void *)attn_chunk_kernel<64>, 160 * 1024);  // past 64 KiB
+    if (!rc) rc = raise_lds((const void *)attn_chunk_kernel<128>, 160 * 1024);
+    if (rc) return rc;
     if (hd == 64)
       attn_chunk_kernel<64><<<dim3(KV, chunks), 256, lds, s>>>(
           q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, partial, chunks);

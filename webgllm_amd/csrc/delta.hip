@@ -674,14 +674,9 @@ int wg_delta_rule_chunked(const float *qkv, int32_t M, int32_t ldq, const float 
   WG_REQUIRE(scratch_bytes >= need, "wg_delta_rule_chunked: scratch of %zu bytes, %zu needed",
              scratch_bytes, need);
   WG_REQUIRE(((uintptr_t)scratch & 15) == 0, "wg_delta_rule_chunked: scratch not 16-byte aligned");
-  static bool lds_set = false;
-  if (!lds_set) {
-    WG_HIP(hipFuncSetAttribute((const void *)delta_chunk_prep_kernel,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)PREP_LDS));
-    WG_HIP(hipFuncSetAttribute((const void *)delta_chunk_chain_kernel,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)CHAIN_LDS));
-    lds_set = true;
-  }
+  int rc = raise_lds((const void *)delta_chunk_prep_kernel, (int)PREP_LDS);
+  if (!rc) rc = raise_lds((const void *)delta_chunk_chain_kernel, (int)CHAIN_LDS);
+  if (rc) return rc;
   const int first = first_rows(save_at), nch = chunk_count(M, first);
   const size_t rows = (size_t)H * nch * CH;
   float *f = static_cast<float *>(scratch);
@@ -691,7 +686,7 @@ int wg_delta_rule_chunked(const float *qkv, int32_t M, int32_t ldq, const float 
               state, snapshot, save_at, out, ldo};
   hipStream_t s = as_stream(stream);
   delta_chunk_prep_kernel<<<dim3(nch, H), 256, PREP_LDS, s>>>(a);
-  int rc = launched("wg_delta_rule_chunked");
+  rc = launched("wg_delta_rule_chunked");
   if (rc) return rc;
   delta_chunk_chain_kernel<<<dim3(H, (dv + CBW - 1) / CBW), CT, CHAIN_LDS, s>>>(a);
   return launched("wg_delta_rule_chunked");

@@ -104,6 +104,8 @@ __device__ inline int wave_sum4_row() { return (threadIdx.x >> 4) & 3; }
 
 // Workgroups a persistent kernel launches per compute unit.
 int persistent_grid(int work_groups, int per_cu);
+// Allows `kernel` `bytes` of dynamic LDS on the current device (once a device).
+int raise_lds(const void *kernel, int bytes);
 // A launch-shape knob's value (see wg_tuning_set).
 int tuning(const char *name);
 

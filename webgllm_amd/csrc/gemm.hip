@@ -388,11 +388,9 @@ int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float
                  hipStream_t s) {
   constexpr int STAGE = BM * 128 + Stage<ZK, BN>::WQ + Stage<ZK, BN>::WS + Stage<ZK, BN>::WZ;
   constexpr size_t LDS = (size_t)S * STAGE;
-  static bool raised = false;  // allow more than 64 KiB of dynamic LDS, once
-  if (!raised && LDS > 64 * 1024) {
-    WG_HIP(hipFuncSetAttribute((const void *)gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS));
-    raised = true;
+  if (LDS > 64 * 1024) {  // more than 64 KiB of dynamic LDS
+    const int rc = raise_lds((const void *)gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW>, (int)LDS);
+    if (rc) return rc;
   }
   const int grid = ((M + BM - 1) / BM) * (w->N / BN);
   gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW><<<grid, WGM * WGN * 64, LDS, s>>>(

@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <string>
 #include <unordered_set>
 
 #include "common.h"
@@ -80,6 +81,22 @@ int tuning(const char *name) {
   for (auto &k : g_knobs)
     if (!strcmp(k.name, name)) return k.value;
   return 0;
+}
+
+// Kernels whose dynamic LDS limit was raised, per device (the attribute
+// is a property of the kernel on the current device).
+int raise_lds(const void *kernel, int bytes) {
+  static std::mutex mu;
+  static std::unordered_set<std::string> done;
+  int dev = 0;
+  WG_HIP(hipGetDevice(&dev));
+  char key[64];
+  snprintf(key, sizeof key, "%p/%d/%d", kernel, dev, bytes);
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count(key)) return WG_OK;
+  WG_HIP(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+  done.insert(key);
+  return WG_OK;
 }
 
 int persistent_grid(int work_groups, int per_cu) {
