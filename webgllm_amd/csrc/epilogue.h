@@ -18,24 +18,37 @@ __device__ inline uint16_t half_bits(float v) {
 template <int M>
 __device__ inline void input_scales(const wg_epilogue &e, float s[M]) {
   const int lane = threadIdx.x & 63;
+  float a[M];
+#pragma unroll
+  for (int m = 0; m < M; m++) a[m] = 0.0f;
+  if (e.norm_parts) {  // the M tokens' loads together, each token's sums in order
+    const float *p = e.norm_parts;
+    // 16-byte loads where the parts are 16-byte aligned (the usual case).
+    if ((((uintptr_t)p) & 15) == 0 && (e.n_parts & 3) == 0 && (e.ld_parts_in & 3) == 0) {
+      for (int i = lane; i < (e.n_parts >> 2); i += 64) {
+        float4 t[M];
+#pragma unroll
+        for (int m = 0; m < M; m++)
+          t[m] = reinterpret_cast<const float4 *>(p + (int64_t)m * e.ld_parts_in)[i];
+#pragma unroll
+        for (int m = 0; m < M; m++) a[m] += (t[m].x + t[m].y) + (t[m].z + t[m].w);
+      }
+    } else {
+      for (int i = lane; i < e.n_parts; i += 64) {
+        float t[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) t[m] = p[(int64_t)m * e.ld_parts_in + i];
+#pragma unroll
+        for (int m = 0; m < M; m++) a[m] += t[m];
+      }
+    }
+  }
 #pragma unroll
   for (int m = 0; m < M; m++) {
     float v = 1.0f;
     if (e.norm_parts) {
-      const float *p = e.norm_parts + (int64_t)m * e.ld_parts_in;
-      float a = 0.0f;
-      // 16-byte loads where the parts are 16-byte aligned (the usual case).
-      if ((((uintptr_t)p) & 15) == 0 && (e.n_parts & 3) == 0) {
-        const float4 *p4 = reinterpret_cast<const float4 *>(p);
-        for (int i = lane; i < (e.n_parts >> 2); i += 64) {
-          float4 t = p4[i];
-          a += (t.x + t.y) + (t.z + t.w);
-        }
-      } else {
-        for (int i = lane; i < e.n_parts; i += 64) a += p[i];
-      }
-      a = wave_sum(a);
-      v = e.norm_mult / sqrtf(a / (float)e.norm_count + e.eps);
+      const float sum = wave_sum(a[m]);
+      v = e.norm_mult / sqrtf(sum / (float)e.norm_count + e.eps);
     }
     if (e.row_scale) v *= e.row_scale[m];
     s[m] = v;
@@ -52,21 +65,35 @@ template <int M, int NW>
 __device__ inline void input_scales_wg(const wg_epilogue &e, float s[M], float *lds) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (e.norm_parts) {
+    // The M tokens' loads go out together (a token at a time, each waited
+    // for its loads and wave sum before the next began); each token's sums
+    // keep their order, so the results are unchanged.
+    float a[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) a[m] = 0.0f;
+    const float *p = e.norm_parts;
+    if ((((uintptr_t)p) & 15) == 0 && (e.n_parts & 3) == 0 && (e.ld_parts_in & 3) == 0) {
+      for (int i = wave * 64 + lane; i < (e.n_parts >> 2); i += NW * 64) {
+        float4 t[M];
+#pragma unroll
+        for (int m = 0; m < M; m++)
+          t[m] = reinterpret_cast<const float4 *>(p + (int64_t)m * e.ld_parts_in)[i];
+#pragma unroll
+        for (int m = 0; m < M; m++) a[m] += (t[m].x + t[m].y) + (t[m].z + t[m].w);
+      }
+    } else {
+      for (int i = wave * 64 + lane; i < e.n_parts; i += NW * 64) {
+        float t[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) t[m] = p[(int64_t)m * e.ld_parts_in + i];
+#pragma unroll
+        for (int m = 0; m < M; m++) a[m] += t[m];
+      }
+    }
 #pragma unroll
     for (int m = 0; m < M; m++) {
-      const float *p = e.norm_parts + (int64_t)m * e.ld_parts_in;
-      float a = 0.0f;
-      if ((((uintptr_t)p) & 15) == 0 && (e.n_parts & 3) == 0) {
-        const float4 *p4 = reinterpret_cast<const float4 *>(p);
-        for (int i = wave * 64 + lane; i < (e.n_parts >> 2); i += NW * 64) {
-          float4 t = p4[i];
-          a += (t.x + t.y) + (t.z + t.w);
-        }
-      } else {
-        for (int i = wave * 64 + lane; i < e.n_parts; i += NW * 64) a += p[i];
-      }
-      a = wave_sum(a);
-      if (lane == 0) lds[wave * M + m] = a;
+      const float sum = wave_sum(a[m]);
+      if (lane == 0) lds[wave * M + m] = sum;
     }
     __syncthreads();
   }
