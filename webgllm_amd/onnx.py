@@ -121,8 +121,8 @@ class OnnxFile:
             [t.float_data[k] for k in range(t.n_float)] if t.n_float else None)
 
     def data(self, t: OnnxTensor) -> np.ndarray:
-        """The tensor's bytes: the inline view, or read from its external data
-        file (beside the model file)."""
+        """The tensor's bytes: the inline view, or a read-only view of its
+        external data file (beside the model file, memory-mapped once)."""
         if t.external is None:
             if t.raw is None:
                 raise ValueError(f"ONNX: {t.name} has no raw bytes")
@@ -130,14 +130,17 @@ class OnnxFile:
         location, offset, length = t.external
         if length < 0:
             length = tensor_bytes(t)
-        with open(os.path.join(os.path.dirname(self.path), location), "rb") as f:
-            f.seek(offset)
-            data = np.fromfile(f, np.uint8, length)
-        if data.size != length:
+        maps = self.__dict__.setdefault("_maps", {})
+        if location not in maps:  # each data file mapped once, read-only
+            maps[location] = np.memmap(os.path.join(os.path.dirname(self.path), location),
+                                       dtype=np.uint8, mode="r")
+        m = maps[location]
+        if offset < 0 or offset + length > m.size:
             raise ValueError(f"ONNX: {t.name}: {location} ends before byte {offset + length}")
-        return data
+        return m[offset:offset + length]
 
     def close(self):
+        self.__dict__.pop("_maps", None)
         if self._h:
             self._lib.wg_onnx_close(self._h)
             self._h = None
