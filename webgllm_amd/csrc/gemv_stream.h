@@ -108,8 +108,11 @@ int launch_stream(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, i
                   const wg_epilogue &e, hipStream_t s) {
   int G = w->N / 4, B = w->K / 32;
   constexpr int RGW = 4 / KS;
-  int grid = persistent_grid((G + RGW - 1) / RGW,
-                             tuning(G >= 16384 ? "gemv_wg_per_cu_wide" : "gemv_wg_per_cu"));
+  // 3 tokens and more: one workgroup a CU (each wave then takes more row
+  // groups for the activations it holds)
+  const char *knob = M >= 3 ? "gemv_few_wg_per_cu"
+                            : G >= 16384 ? "gemv_wg_per_cu_wide" : "gemv_wg_per_cu";
+  int grid = persistent_grid((G + RGW - 1) / RGW, tuning(knob));
   auto q = (const uint4 *)w->quants;
   auto sc = (const uint16_t *)w->scales;
   if (e.mode == WG_EPI_SWIGLU)

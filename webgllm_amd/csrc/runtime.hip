@@ -71,6 +71,7 @@ static Knob g_knobs[] = {
     {"wide_wg_per_cu", 2, 1, 16},        // the same for 8-bit and Q6_K GEMVs
     {"gemv_min_waves", 8192, 0, 1 << 20},  // split K within a workgroup below this
     {"gemv_few_stream", 1, 0, 1},        // 3 to 8 tokens on the streaming kernel (0: row groups)
+    {"gemv_few_wg_per_cu", 1, 1, 16},    // its persistent workgroups per CU
     {"decode_wg_per_cu", 1, 1, 4},       // persistent decode workgroups (8 waves) per CU
     {"attn_prefill_mfma", 4, 0, 4},      // prompt attention: MFMA waves a workgroup (1, 2, 4), 0 VALU
     {"gemm_tile", 0, 0, 3},              // prefill GEMM tile: 0 chooses; 1 64x128, 2 128x128, 3 128x256
