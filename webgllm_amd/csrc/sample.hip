@@ -8,10 +8,11 @@
 //
 // Stage 1 (`chunk_max_kernel`): a wave per (row, chunk) reads the chunk's
 // 256 logits and mask bytes (4 a lane), penalizes each and
-// reduces the maximum. Stage 2 (`chunk_gather_kernel`): a workgroup of
-// 1024 threads per row sorts the chunks by maximum (larger first, ties to
-// the lower index: the order the reference's ranks give), keeps the first
-// `count`, and writes their penalized logits.
+// reduces the maximum. Stage 2 (`chunk_rank_kernel`): a workgroup of 256
+// threads per row sorts the chunks by maximum (larger first, ties to the
+// lower index: the order the reference's ranks give) and keeps the first
+// `count`. Stage 3 (`chunk_gather_kernel`): a workgroup per kept chunk
+// writes its penalized logits.
 #include "common.h"
 
 namespace wg {
@@ -78,30 +79,27 @@ __global__ __launch_bounds__(256) void chunk_max_kernel(const float *logits, int
   if (lane == 0) maxima[w] = mx;
 }
 
-__global__ __launch_bounds__(1024) void chunk_gather_kernel(const float *logits, int V, int ld,
-                                                           Penalty p, int total,
-                                                           const float *maxima, int count,
-                                                           int32_t *chunks_out,
-                                                           float *cand_out) {
+constexpr int RANK_THREADS = 256;  // one compare-exchange a thread a pass up to 512 chunks
+
+__global__ __launch_bounds__(RANK_THREADS) void chunk_rank_kernel(int total, const float *maxima,
+                                                                 int count, int32_t *chunks_out) {
   __shared__ float sv[MAX_TOTAL];
   __shared__ int si[MAX_TOTAL];
-  __shared__ int by_rank[64];
   const int r = blockIdx.x;
-  const float *row = logits + (int64_t)r * ld;
   // CHUNK_RANK + CHUNK_BY_RANK: the chunks sorted by maximum, larger first,
   // ties to the lower index (the reference's order), by a bitonic sort in
   // LDS over the next power of two, padded with -inf (every maximum is at
   // least -1e30, so the padding sorts last).
   int n2 = 1;
   while (n2 < total) n2 <<= 1;
-  for (int c = threadIdx.x; c < n2; c += 1024) {
+  for (int c = threadIdx.x; c < n2; c += RANK_THREADS) {
     sv[c] = c < total ? maxima[(int64_t)r * total + c] : -INFINITY;
     si[c] = c;
   }
   __syncthreads();
   for (int k = 2; k <= n2; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int t = threadIdx.x; t < n2 / 2; t += 1024) {
+      for (int t = threadIdx.x; t < n2 / 2; t += RANK_THREADS) {
         const int a = 2 * t - (t & (j - 1)), b = a + j;  // pair (a, b), a's bit j clear
         const bool desc = (a & k) == 0;                   // this run sorts best first
         const float va = sv[a], vb = sv[b];
@@ -117,30 +115,21 @@ __global__ __launch_bounds__(1024) void chunk_gather_kernel(const float *logits,
       __syncthreads();
     }
   }
-  if (threadIdx.x < count) by_rank[threadIdx.x] = si[threadIdx.x];
-  __syncthreads();
-  // CHUNK_GATHER: the ranked chunks' penalized logits (at most 16 a thread:
-  // every logit and mask byte is loaded before the first is used, so the
-  // loads overlap instead of each waiting in turn).
-  constexpr int PER_T = 64 * CHUNK / 1024;
-  float v[PER_T];
-  int m[PER_T];
-#pragma unroll
-  for (int j = 0; j < PER_T; j++) {
-    const int i = threadIdx.x + j * 1024;
-    const int id = i < count * CHUNK ? by_rank[i / CHUNK] * CHUNK + i % CHUNK : V;
-    v[j] = id < V ? row[id] : 0.0f;
-    m[j] = id < V && p.mask ? p.mask[id] : 0;
-  }
-#pragma unroll
-  for (int j = 0; j < PER_T; j++) {
-    const int i = threadIdx.x + j * 1024;
-    if (i < count * CHUNK) {
-      const int id = by_rank[i / CHUNK] * CHUNK + i % CHUNK;
-      cand_out[(int64_t)r * count * CHUNK + i] = penalized(v[j], id, r + p.row0, p, V, m[j]);
-    }
-  }
-  if (threadIdx.x < count) chunks_out[(int64_t)r * count + threadIdx.x] = by_rank[threadIdx.x];
+  for (int k = threadIdx.x; k < count; k += RANK_THREADS)
+    chunks_out[(int64_t)r * count + k] = si[k];
+}
+
+// CHUNK_GATHER: a workgroup per (ranked chunk, row) writes that chunk's
+// penalized logits.
+__global__ __launch_bounds__(CHUNK) void chunk_gather_kernel(const float *logits, int V, int ld,
+                                                            Penalty p, int count,
+                                                            const int32_t *chunks,
+                                                            float *cand_out) {
+  const int k = blockIdx.x, r = blockIdx.y;
+  const int id = chunks[(int64_t)r * count + k] * CHUNK + threadIdx.x;
+  const float v = id < V ? logits[(int64_t)r * ld + id] : 0.0f;
+  const int m = id < V && p.mask ? p.mask[id] : 0;
+  cand_out[((int64_t)r * count + k) * CHUNK + threadIdx.x] = penalized(v, id, r + p.row0, p, V, m);
 }
 
 }  // namespace
@@ -185,8 +174,11 @@ int wg_pick_candidates(const float *logits, int32_t M, int32_t V, int32_t ld,
                                                                maxima);
   int rc = launched("wg_pick_candidates");
   if (rc) return rc;
-  chunk_gather_kernel<<<M, 1024, 0, s>>>(logits, V, ld, p, total, maxima, count, chunks_out,
-                                        candidates);
+  chunk_rank_kernel<<<M, RANK_THREADS, 0, s>>>(total, maxima, count, chunks_out);
+  rc = launched("wg_pick_candidates");
+  if (rc) return rc;
+  chunk_gather_kernel<<<dim3(count, M), CHUNK, 0, s>>>(logits, V, ld, p, count, chunks_out,
+                                                     candidates);
   return launched("wg_pick_candidates");
 }
 
