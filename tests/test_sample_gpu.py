@@ -26,7 +26,7 @@ def _case(rng, M, V):
 
 
 @pytest.mark.parametrize("M,V,count", [(1, 128256, 64), (5, 1000, 3), (3, 65536, 8),
-                                       (2, 513, 3)])
+                                       (2, 513, 3), (1, 131072, 64), (2, 262144, 64)])
 @pytest.mark.parametrize("allow", [False, True])
 def test_candidates_match_oracle(hip, M, V, count, allow):
     from webgllm_amd import ops
