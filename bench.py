@@ -29,10 +29,59 @@ sys.path.insert(0, ROOT)
 METRIC = "Q4 GEMV HBM GB/s (% of peak); decode tok/s, 8B-shape Q4 batch 1"
 HBM_PEAK_GBPS = 8000.0
 
+# Algorithmic bytes a weight of each weight file format: what a GEMV must
+# read at least, whatever layout the device keeps (GGUF Q4_0 18 B / 32,
+# Q4_K 144 B / 256, MatMulNBits q4 16 B of nibbles + a half scale + half a
+# byte of zero point / 32, Q8_0 34 B / 32, Q6_K 210 B / 256).
+BPW = {"q4_0": 18 / 32, "q4_k": 144 / 256, "q4_k_rowgroup": 144 / 256, "nbits": 18.5 / 32,
+       "q8_0": 34 / 32, "q8": 34 / 32, "q6_k": 210 / 256}
 
-def gemv_roofline(mats, x, parts, out16, eps, reps=6):
+
+def gemv_bytes(N, K, M, fmt):
+    """Algorithmic bytes of an N x K GEMV over M rows: the weights at their
+    file format's bytes a weight, the half inputs and float32 outputs."""
+    return int(round(N * K * BPW[fmt])) + M * K * 2 + M * N * 4
+
+
+def token_bytes(shape, keys, M=1):
+    """Algorithmic bytes of one forward of M rows of a model shape: every
+    layer's GEMVs, the head, the keys and values of `keys` cache positions in
+    every attention layer (read once for all M rows), and the conv states."""
+    s, D, F = shape, shape.hidden, shape.intermediate
+    total = 0
+    for i in range(s.layers):
+        if s.layer_type(i) == "conv":
+            total += gemv_bytes(3 * D, D, M, s.fmt) + gemv_bytes(D, D, M, s.fmt)
+            total += (s.conv_kernel - 1) * D * 4 * 2  # state read and written
+        else:
+            total += gemv_bytes(s.qkv_rows, D, M, s.fmt)
+            total += gemv_bytes(D, s.heads * s.head_dim, M, s.fmt)
+            total += 2 * s.kv_heads * s.head_dim * 2 * keys
+        total += gemv_bytes(2 * F, D, M, s.fmt) + gemv_bytes(D, F, M, s.fmt)
+    return total + gemv_bytes(s.vocab, D, M, s.embed_fmt or s.fmt)
+
+
+def host_threads():
+    """Threads for a CPU baseline: every CPU in the process's affinity mask,
+    capped by OMP_NUM_THREADS where the host sets it (a shared machine's CPU
+    share for one GPU job). Returns (threads, a note saying so)."""
+    allowed = len(os.sched_getaffinity(0))
+    host = os.cpu_count() or allowed
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    threads = allowed
+    note = f"{allowed} CPUs in the affinity mask, {host} on the host"
+    if env.isdigit() and 0 < int(env) < allowed:
+        threads = int(env)
+        note += f"; OMP_NUM_THREADS={env}, the host's CPU share for one GPU job"
+    return threads, note
+
+
+def gemv_roofline(mats, x, parts, out16, eps, reps=6, fmt="q4_k"):
     """Average duration of the gate|up GEMV, launched as the decode launches
-    it (prescaled norm in, SwiGLU out), over distinct matrices."""
+    it (prescaled norm in, SwiGLU out), over distinct matrices. `achieved`
+    counts the GEMV's algorithmic bytes at the weight file format's bytes a
+    weight (gemv_bytes); the bytes of the layout the device keeps are
+    reported beside them."""
     import torch
     from webgllm_amd import lib as L, ops
     m = mats[0]
@@ -53,16 +102,24 @@ def gemv_roofline(mats, x, parts, out16, eps, reps=6):
     stream.synchronize()
     launches = reps * len(mats)
     us = e0.elapsed_time(e1) * 1e3 / launches
-    # weights (nibbles, half scales, half zero points) + x (halves) + the
-    # norm's parts + the half SwiGLU output
-    algo = m.nbytes + D * 2 + (D // 4) * 4 + F * 2
+    algo = gemv_bytes(m.N, m.K, 1, fmt)
     achieved = algo / (us * 1e-6) / 1e9
+    # the device layout's bytes: nibbles, half scales, half zero points, x
+    # (halves), the norm's parts and the half SwiGLU output
+    stored = m.nbytes + D * 2 + (D // 4) * 4 + F * 2
+    stored_gbps = stored / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": measured_traffic(),
-            "kernel": f"gemv_stream_kernel gate|up {m.N}x{m.K} (Q4_K repacked: 4-bit + "
-                      f"half scale + half zero per 32), SwiGLU epilogue",
-            "bytes_per_launch": algo, "avg_launch_us": round(us, 3), "launches": launches}
+            "kernel": f"gemv_stream_kernel gate|up {m.N}x{m.K}, SwiGLU epilogue",
+            "bytes_per_launch": algo,
+            "bytes_rule": f"N*K*{BPW[fmt]:.4f} ({fmt} file bytes a weight) + K*2 (half x) "
+                          f"+ N*4 (float32 y)",
+            "avg_launch_us": round(us, 3), "launches": launches,
+            "stored_layout": {"bytes_per_launch": stored, "achieved": round(stored_gbps, 1),
+                              "frac": round(stored_gbps / HBM_PEAK_GBPS, 4),
+                              "what": "the device's layout: 4-bit + half scale + half zero "
+                                      "per 32 weights, x, norm parts, half SwiGLU out"}}
 
 
 def measured_traffic():
@@ -149,20 +206,48 @@ def cpu_step_time(groups, M, threads, seconds=12.0):
         reps += 1
     per_step = sum(spent[label] / reps * k for label, _, k in qms)
     parts = ", ".join(f"{label} {spent[label] / reps * 1e3:.1f} ms x{k}" for label, _, k in qms)
-    desc = (f"oracle shader-order fp32 split matmul (OpenMP, {threads} threads), {M} row(s): "
-            f"{parts}; {reps} repetitions ({sum(spent.values()):.1f} s), extrapolated to the "
-            f"step; attention and norms not included")
+    desc = (f"oracle shader-order fp32 split matmul (OpenMP, {threads} threads: "
+            f"{host_threads()[1]}), {M} row(s): {parts}; {reps} repetitions "
+            f"({sum(spent.values()):.1f} s), extrapolated to the step")
     return per_step, desc
 
 
-def cpu_baseline(engine, threads, seconds=12.0):
+def cpu_attention_time(engine, layer, keys, threads, seconds=2.0):
+    """The oracle's float32 attention (the shaders' scores and attend, heads
+    in parallel) of one query row over `keys` rows of a layer's cache."""
+    import numpy as np
+    from oracle import oracle as O
+    s = engine.shape
+    kc = engine.k_cache[layer][:keys].cpu().numpy().view(np.uint16)
+    vc = engine.v_cache[layer][:keys].cpu().numpy().view(np.uint16)
+    q = (np.random.default_rng(0).standard_normal(s.heads * s.head_dim) /
+         np.sqrt(s.head_dim)).astype(np.float32)
+    kvd = s.kv_heads * s.head_dim
+    O.attention_f32(q, kc, vc, s.heads, s.kv_heads, s.head_dim, keys, kvd, threads)
+    spent, n = 0.0, 0
+    while spent < seconds or n < 2:
+        t0 = O.now()
+        O.attention_f32(q, kc, vc, s.heads, s.kv_heads, s.head_dim, keys, kvd, threads)
+        spent += O.now() - t0
+        n += 1
+    return spent / n
+
+
+def cpu_baseline(engine, threads, seconds=12.0, keys=None):
     """Oracle split matmul (float32, shader order) on one layer + the head,
-    repeated for about `seconds` of CPU time, extrapolated to a token."""
+    repeated for about `seconds` of CPU time, plus the float32 attention of
+    one layer over `keys` cache rows, extrapolated to a token (norms, the
+    embedding row and the pick are left out: under 0.1% of the bytes)."""
     s = engine.shape
     lw = engine.w.layers[0]
     groups = [(k, lw[k], s.layers) for k in ("qkv", "o", "gate_up", "down")]
     groups.append(("head", engine.w.embedding, 1))
     per_token, desc = cpu_step_time(groups, 1, threads, seconds)
+    if keys:
+        att = cpu_attention_time(engine, 0, keys, threads)
+        per_token += att * s.layers
+        desc += (f"; attention: the oracle's float32 scores/attend over {keys} keys, "
+                 f"{att * 1e3:.2f} ms x{s.layers}")
     return {"value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": threads,
             "kind": "port", "sample": desc}
 
@@ -234,7 +319,7 @@ def workload_q4_0_gemv(args):
     hot = timed(gh.replay, reps) * 1e3 / copies
     cpu = None
     if not args.no_cpu:
-        threads = min(os.cpu_count() or 1, 16)
+        threads = host_threads()[0]
         t, desc = cpu_step_time([("2048x2048", mats[0], 1)], 1, threads, 10.0)
         cpu = {"value": round(algo / t / 1e9, 3), "unit": "GB/s", "cores": threads,
                "kind": "port", "sample": desc}
@@ -280,7 +365,7 @@ def workload_nbits_gemm(args, fmt="nbits"):
     tflops = tot_flop / (tot_ms * 1e-3) / 1e12
     cpu = None
     if not args.no_cpu and fmt == "nbits":
-        threads = min(os.cpu_count() or 1, 16)
+        threads = host_threads()[0]
         t, desc = cpu_step_time([("4096x4096", res[4096][2], 1),
                                  ("14336x4096", res[14336][2], 1)], 8, threads, 10.0)
         cpu = {"value": round(tot_flop / 64 / t / 1e12, 5), "unit": "TFLOP/s",
@@ -290,7 +375,7 @@ def workload_nbits_gemm(args, fmt="nbits"):
         import numpy as np
         from oracle import oracle as O
         from webgllm_amd import lib as L
-        threads = min(os.cpu_count() or 1, 16)
+        threads = host_threads()[0]
         m = res[14336][2]
         wm = O.WideMatrix(m.N, m.K, 8)
         wm.quants[:] = m.quants.cpu().numpy()
@@ -351,14 +436,14 @@ def workload_qwen2_decode(args):
     shape = E.QWEN2_05B
     steps = 1024 - 512 - args.warmup - 1
     eng, w, ms, p0 = decode_engine_run(shape, 1024, 512, steps, args.warmup, args.persistent)
-    kv = shape.layers * 2 * shape.kv_heads * shape.head_dim * 2 * (p0 + steps // 2)
-    token_bytes = w.nbytes + kv
-    cpu = cpu_baseline(eng, min(os.cpu_count() or 1, 16), 10.0) if not args.no_cpu else None
-    gbps = token_bytes / (ms * 1e-3) / 1e9
+    keys = p0 + (steps + 1) // 2
+    tok_bytes = token_bytes(shape, keys)
+    cpu = cpu_baseline(eng, host_threads()[0], 10.0, keys=keys) if not args.no_cpu else None
+    gbps = tok_bytes / (ms * 1e-3) / 1e9
     roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-            "kernel": "whole token (weights ~286 MB, about the infinity cache's size: "
-                      "'effective' GB/s)", "bytes_per_launch": token_bytes,
+            "kernel": "whole token (MatMulNBits weights at 18.5 B / 32, ~286 MB, about the "
+                      "infinity cache's size: 'effective' GB/s)", "bytes_per_launch": tok_bytes,
             "avg_launch_us": round(ms * 1e3, 2), "launches": steps}
     cfg = {"workload": f"Qwen2-0.5B-shape greedy decode, positions {p0}..{p0 + steps - 1}",
            "model": shape.name, "layers": shape.layers, "hidden": shape.hidden,
@@ -403,14 +488,26 @@ def workload_lfm2_verify(args):
 
     verify(args.warmup)
     torch.cuda.synchronize()
+    pos_start = eng.position
     t0 = time.perf_counter()
     written = verify(steps)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms = dt * 1e3 / steps
+    # a step's algorithmic bytes: the Q4_0 weights once for the 5 rows, the
+    # cache rows the batch reads (keys at the steps' mean position + 5)
+    keys = (pos_start + eng.position) // 2 + 5
+    step_bytes = token_bytes(shape, keys, M=5)
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+    roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+            "kernel": "whole verify step (5 rows: Q4_0 weights at 18 B / 32 read once, the "
+                      "cache, the picks' readback and the host's accept)",
+            "bytes_per_launch": step_bytes, "avg_launch_us": round(ms * 1e3, 2),
+            "launches": steps}
     cpu = None
     if not args.no_cpu:
-        threads = min(os.cpu_count() or 1, 16)
+        threads = host_threads()[0]
         conv = next(i for i in range(shape.layers) if shape.layer_type(i) == "conv")
         att = next(i for i in range(shape.layers) if shape.layer_type(i) == "attn")
         n_conv = len(shape.conv_layers)
@@ -429,7 +526,7 @@ def workload_lfm2_verify(args):
            "vocab": shape.vocab, "weights": "random GGUF Q4_0", "global_batch": 5,
            "seq_len": ctx, "parallelism": "none"}
     return line("verify steps/s, LFM2-1.2B-shape Q4_0, 4 drafts", round(steps / dt, 2),
-                "verify steps/s", steps, args.warmup, ms, cfg, None, cpu,
+                "verify steps/s", steps, args.warmup, ms, cfg, roof, cpu,
                 tokens_per_s=round(written / dt, 2), tokens_per_step=round(written / steps, 3),
                 weight_bytes=w.nbytes)
 
@@ -476,7 +573,7 @@ def workload_llama8b_prefill(args):
             "avg_launch_us": round(gms * 1e3, 2), "launches": 60}
     cpu = None
     if not args.no_cpu:
-        threads = min(os.cpu_count() or 1, 16)
+        threads = host_threads()[0]
         t, desc = cpu_step_time([("qkv", lw["qkv"], shape.layers), ("o", lw["o"], shape.layers),
                                  ("gate_up", lw["gate_up"], shape.layers),
                                  ("down", lw["down"], shape.layers)], 8, threads, 10.0)
@@ -532,7 +629,7 @@ def workload_wide_gemv(args, fmt, N, K, copies, what):
     gbps = algo / (us * 1e-6) / 1e9
     cpu = None
     if not args.no_cpu:
-        threads = min(os.cpu_count() or 1, 16)
+        threads = host_threads()[0]
         m = mats[0]
         wm = O.WideMatrix(m.N, m.K, 8 if m.layout == L.LAYOUT_Q8 else 6)
         wm.quants[:] = m.quants.cpu().numpy()
@@ -976,12 +1073,15 @@ def main():
 
     roof = gemv_roofline([lw["gate_up"] for lw in w.layers], eng.x16[:1], eng.parts[:1],
                          eng.ff16[:1], shape.eps)
-    kv_bytes = shape.layers * 2 * shape.kv_heads * shape.head_dim * 2 * (p0 + args.steps // 2)
-    token_bytes = w.nbytes + kv_bytes
+    # keys a timed token attends over, on average (positions p0 .. p0 + steps - 1)
+    keys = p0 + (args.steps + 1) // 2
+    tok_bytes = token_bytes(shape, keys)
+    kv_bytes = shape.layers * 2 * shape.kv_heads * shape.head_dim * 2 * keys
+    stored_bytes = w.nbytes + kv_bytes
     cpu = None
     if not args.no_cpu:
-        threads = min(os.cpu_count() or 1, 16)
-        cpu = cpu_baseline(eng, threads)
+        threads = host_threads()[0]
+        cpu = cpu_baseline(eng, threads, keys=keys)
     out = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -1008,9 +1108,13 @@ def main():
         },
         "roofline": roof,
         "cpu_baseline": cpu,
-        "token_bytes": token_bytes,
-        "token_roofline_tok_s": round(HBM_PEAK_GBPS * 1e9 / token_bytes, 1),
-        "decode_effective_GBps": round(token_bytes / (ms * 1e-3) / 1e9, 1),
+        # a token's algorithmic bytes: Q4_K weights at 144 B / 256, the
+        # keys and values of the cache rows it reads, activations
+        "token_bytes": tok_bytes,
+        "token_roofline_tok_s": round(HBM_PEAK_GBPS * 1e9 / tok_bytes, 1),
+        "token_roofline_ratio": round(HBM_PEAK_GBPS * 1e9 / tok_bytes / tok_s, 3),
+        "decode_effective_GBps": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
+        "stored_layout_token_bytes": stored_bytes,
         "setup_s": round(t_prefill, 1),
     }
     print(json.dumps(out), flush=True)

@@ -934,6 +934,45 @@ void orc_attention_f64(const float *q, const uint16_t *kc, const uint16_t *vc, i
   free(scores);
 }
 
+/* The shaders' float32 form of the same attention (scores, attend:
+ * src/gpu/kernels.ts:2386-2579): scores q.k summed in float32, the max
+ * subtracted, exp and the weighted values summed in float32, divided by the
+ * total. Heads in parallel (OpenMP) with threads > 0: the CPU baseline's
+ * attention. out: float32 [heads * head_dim]. */
+void orc_attention_f32(const float *q, const uint16_t *kc, const uint16_t *vc, int heads,
+                       int kv_heads, int head_dim, int keys, int kv_stride, float *out,
+                       int threads) {
+  const float *half = htab();
+  int group = heads / kv_heads;
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+#endif
+  for (int h = 0; h < heads; h++) {
+    int kh = h / group;
+    float *scores = (float *)malloc(sizeof(float) * (keys > 0 ? keys : 1));
+    float mx = -INFINITY;
+    for (int j = 0; j < keys; j++) {
+      float s = 0.0f;
+      for (int d = 0; d < head_dim; d++)
+        s += q[h * head_dim + d] * half[kc[(size_t)j * kv_stride + kh * head_dim + d]];
+      scores[j] = s;
+      if (s > mx) mx = s;
+    }
+    float l = 0.0f;
+    float *o = out + (size_t)h * head_dim;
+    for (int d = 0; d < head_dim; d++) o[d] = 0.0f;
+    for (int j = 0; j < keys; j++) {
+      float e = expf(scores[j] - mx);
+      l += e;
+      for (int d = 0; d < head_dim; d++) o[d] += e * half[vc[(size_t)j * kv_stride + kh * head_dim + d]];
+    }
+    for (int d = 0; d < head_dim; d++) o[d] = l > 0.0f ? o[d] / l : 0.0f;
+    free(scores);
+  }
+  (void)threads;
+}
+
 /* ------------------------------------------------------- short conv */
 
 /* convFused / convPrefixes (src/gpu/kernels.ts:1447-1523) for M tokens of

@@ -112,6 +112,9 @@ void orc_head_prep(const float *x, const float *norm_w, const float *rope, int h
 void orc_attention_f64(const float *q, const uint16_t *kc, const uint16_t *vc, int heads,
                        int kv_heads, int head_dim, int keys, int kv_stride, double *out);
                                                                    /* attention-check.ts:48-92 */
+void orc_attention_f32(const float *q, const uint16_t *kc, const uint16_t *vc, int heads,
+                       int kv_heads, int head_dim, int keys, int kv_stride, float *out,
+                       int threads);                      /* kernels.ts:2386-2579, float32 */
 
 /* ---- short convolution (kernels.ts:1380-1523) ---- */
 void orc_short_conv(const float *bcx, int M, int D, int W, const float *taps, const float *state,

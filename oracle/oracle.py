@@ -77,6 +77,7 @@ _lib.orc_rope_table.argtypes = [C.c_double, _I, _I, _I, _I, _P]
 _lib.orc_rope_rows.argtypes = [_I]
 _lib.orc_head_prep.argtypes = [_P, _P, _P, _I, _I, _I, C.c_float, C.c_float, _I, _P]
 _lib.orc_attention_f64.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _P]
+_lib.orc_attention_f32.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _P, _I]
 _lib.orc_short_conv.argtypes = [_P, _I, _I, _I, _P, _P, _P, _P, _P]
 _lib.orc_pick_candidates.argtypes = [_P, _I, _I, _P, _P, _I, _I, C.c_float, C.c_float, _P, _I,
                                      _I, _I, _P, _P]
@@ -370,6 +371,17 @@ def attention_f64(q, kc, vc, heads, kv_heads, head_dim, keys, kv_stride) -> np.n
     out = np.empty(heads * head_dim, dtype=np.float64)
     _lib.orc_attention_f64(_ptr(q), _ptr(kc), _ptr(vc), heads, kv_heads, head_dim, keys,
                            kv_stride, _ptr(out))
+    return out
+
+
+def attention_f32(q, kc, vc, heads, kv_heads, head_dim, keys, kv_stride, threads=0):
+    """The shaders' float32 attention (heads in parallel with threads > 0)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    kc = np.ascontiguousarray(kc, dtype=np.uint16)
+    vc = np.ascontiguousarray(vc, dtype=np.uint16)
+    out = np.empty(heads * head_dim, dtype=np.float32)
+    _lib.orc_attention_f32(_ptr(q), _ptr(kc), _ptr(vc), heads, kv_heads, head_dim, keys,
+                           kv_stride, _ptr(out), threads)
     return out
 
 

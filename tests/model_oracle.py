@@ -61,16 +61,23 @@ def h16(x):
 
 
 class OracleModel:
-    def __init__(self, weights, ctx):
+    """The whole-model decoder. `layers` (indices) limits which layers get
+    float64 weight copies (an 8B-shape layer is 1.7 GB of them); `head`
+    False leaves the embedding out (only layer_rows can run then)."""
+
+    def __init__(self, weights, ctx, layers=None, head=True):
         s = self.s = weights.shape
         self.ctx = ctx
         # float64 copies of the dequantized weights, made once
-        self.emb = dense_of(weights.embedding).astype(np.float64)
+        self.emb = dense_of(weights.embedding).astype(np.float64) if head else None
         self.final = _np(weights.final_norm)
+        keep = range(s.layers) if layers is None else set(layers)
         self.layers = []
         for i, lw in enumerate(weights.layers):
-            d = {k: (dense_of(v).astype(np.float64) if hasattr(v, "desc") else _np(v))
-                 for k, v in lw.items()}
+            d = None
+            if i in keep:
+                d = {k: (dense_of(v).astype(np.float64) if hasattr(v, "desc") else _np(v))
+                     for k, v in lw.items()}
             self.layers.append(d)
         self.rope = O.rope_table(s.rope_theta, s.head_dim, s.head_dim, ctx)
         self.reset()
@@ -98,67 +105,84 @@ class OracleModel:
         r = 32.0 / np.sqrt(ms + self.s.eps)
         return ((x16.astype(np.float64) @ w.T) * r).astype(np.float32)
 
-    def forward_rows(self, ids):
-        """One batch; returns (logits [M, V], picks [M])."""
-        s = self.s
-        M = len(ids)
-        pos0 = self.position
+    def layer_rows(self, i, h, pos0):
+        """Layer i over rows h [M, D] (float32) at positions pos0 ..: writes
+        the rows' keys and values (or advances the conv state) and returns
+        the new h."""
+        s, lw = self.s, self.layers[i]
+        M = h.shape[0]
         hd = s.head_dim
-        h = self.emb[np.asarray(ids)].astype(np.float32)
-        for i, lw in enumerate(self.layers):
-            if s.layer_type(i) == "conv":
-                bcx = self._normed_mm(h, lw["op_norm"], lw["in_proj"])
-                out, st = O.short_conv(bcx, s.hidden, s.conv_kernel, lw["taps"], self.state[i])
-                self.state[i] = st
-                h = h + self._mm(h16(out), lw["out_proj"])
-            else:
-                qkv = self._normed_mm(h, lw["op_norm"], lw["qkv"])
-                att = np.zeros((M, s.heads * hd), np.float32)
-                qd = s.heads * hd
-                kvd = s.kv_heads * hd
-                for m in range(M):
-                    pos = pos0 + m
-                    q = np.concatenate([
-                        O.head_prep(qkv[m, h_ * hd:(h_ + 1) * hd], lw.get("q_norm"), self.rope, hd,
-                                    hd, pos, s.eps, 1 / math.sqrt(hd), s.qk_norm)
-                        for h_ in range(s.heads)])
-                    for kh in range(s.kv_heads):
-                        kx = qkv[m, qd + kh * hd:qd + (kh + 1) * hd]
-                        self.k[i][pos, kh * hd:(kh + 1) * hd] = O.f32_to_h2(
-                            O.head_prep(kx, lw.get("k_norm"), self.rope, hd, hd, pos, s.eps, 1.0,
-                                        s.qk_norm))
-                        vx = qkv[m, qd + kvd + kh * hd:qd + kvd + (kh + 1) * hd]
-                        self.v[i][pos, kh * hd:(kh + 1) * hd] = O.f32_to_h2(vx)
-                    a = O.attention_f64(q, self.k[i], self.v[i], s.heads, s.kv_heads, hd,
-                                        pos + 1, kvd)
-                    att[m] = h16(a)
-                h = h + self._mm(att, lw["o"])
-            gu = self._normed_mm(h, lw["ffn_norm"], lw["gate_up"])
-            h = h + self._mm(h16(O.swiglu(gu)), lw["down"])
+        if s.layer_type(i) == "conv":
+            bcx = self._normed_mm(h, lw["op_norm"], lw["in_proj"])
+            out, st = O.short_conv(bcx, s.hidden, s.conv_kernel, lw["taps"], self.state[i])
+            self.state[i] = st
+            h = h + self._mm(h16(out), lw["out_proj"])
+        else:
+            qkv = self._normed_mm(h, lw["op_norm"], lw["qkv"])
+            att = np.zeros((M, s.heads * hd), np.float32)
+            qd = s.heads * hd
+            kvd = s.kv_heads * hd
+            for m in range(M):
+                pos = pos0 + m
+                q = np.concatenate([
+                    O.head_prep(qkv[m, h_ * hd:(h_ + 1) * hd], lw.get("q_norm"), self.rope, hd,
+                                hd, pos, s.eps, 1 / math.sqrt(hd), s.qk_norm)
+                    for h_ in range(s.heads)])
+                for kh in range(s.kv_heads):
+                    kx = qkv[m, qd + kh * hd:qd + (kh + 1) * hd]
+                    self.k[i][pos, kh * hd:(kh + 1) * hd] = O.f32_to_h2(
+                        O.head_prep(kx, lw.get("k_norm"), self.rope, hd, hd, pos, s.eps, 1.0,
+                                    s.qk_norm))
+                    vx = qkv[m, qd + kvd + kh * hd:qd + kvd + (kh + 1) * hd]
+                    self.v[i][pos, kh * hd:(kh + 1) * hd] = O.f32_to_h2(vx)
+                a = O.attention_f64(q, self.k[i], self.v[i], s.heads, s.kv_heads, hd,
+                                    pos + 1, kvd)
+                att[m] = h16(a)
+            h = h + self._mm(att, lw["o"])
+        gu = self._normed_mm(h, lw["ffn_norm"], lw["gate_up"])
+        return h + self._mm(h16(O.swiglu(gu)), lw["down"])
+
+    def head_rows(self, h):
+        """(logits [M, V], greedy picks) of rows h."""
         logits = self._normed_mm(h, self.final, self.emb)
-        picks = [O.argmax(logits[m])[0] for m in range(M)]
-        self.position += M
-        return logits, picks
+        return logits, [O.argmax(logits[m])[0] for m in range(h.shape[0])]
+
+    def forward_rows(self, ids, head=True):
+        """One batch; returns (logits [M, V], picks [M]), or (None, None)
+        when `head` is False."""
+        pos0 = self.position
+        h = self.emb[np.asarray(ids)].astype(np.float32)
+        for i in range(len(self.layers)):
+            h = self.layer_rows(i, h, pos0)
+        self.position += len(ids)
+        return self.head_rows(h) if head else (None, None)
 
     # the quantized matrices of a layer (the rest are vectors and conv taps)
     MATRICES = ("qkv", "o", "gate_up", "down", "in_proj", "out_proj")
 
-    def forward(self, tokens, f16_weights=False):
-        """A prompt, 8 rows a batch; returns the last batch's (logits, picks).
-        With f16_weights the layers' matmuls use the dequantized weights
-        rounded to halves, as the reference's prompt plan computes them
-        (dequant to an f16 texture, then matmulF16: src/gpu/kernels.ts:
-        436-735, Engine.f16Plan, src/engine.ts:980-995); the head keeps
-        exact weights. The engine takes that path for prompts longer than a
-        verify batch when every layer matrix is a 4- or 8-bit row-group one."""
+    def forward(self, tokens, f16_weights=False, batch=8):
+        """A prompt; returns the (logits, picks) of its last batch of 8 rows
+        (len mod 8 rows, or 8), as the engine returns them. The rows before
+        run `batch` at a time with no head: every row's result is the same
+        for any batching (rows are independent but for the cache and conv
+        state, which advance row by row). With f16_weights the layers'
+        matmuls use the dequantized weights rounded to halves, as the
+        reference's prompt plan computes them (dequant to an f16 texture,
+        then matmulF16: src/gpu/kernels.ts:436-735, Engine.f16Plan,
+        src/engine.ts:980-995); the head keeps exact weights. The engine
+        takes that path for prompts longer than a verify batch when every
+        layer matrix is a 4- or 8-bit row-group one."""
         layers = self.layers
         if f16_weights:
-            self.layers = [{k: (h16(v).astype(np.float64) if k in self.MATRICES else v)
+            self.layers = [None if lw is None else
+                           {k: (h16(v).astype(np.float64) if k in self.MATRICES else v)
                             for k, v in lw.items()} for lw in layers]
         try:
-            logits = picks = None
-            for b0 in range(0, len(tokens), 8):
-                logits, picks = self.forward_rows(tokens[b0:b0 + 8])
+            tokens = list(tokens)
+            last = len(tokens) - (len(tokens) % 8 or 8)
+            for b0 in range(0, last, batch):
+                self.forward_rows(tokens[b0:min(last, b0 + batch)], head=False)
+            logits, picks = self.forward_rows(tokens[last:])
         finally:
             self.layers = layers
         return logits, picks

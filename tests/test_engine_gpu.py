@@ -258,21 +258,25 @@ def test_capture_leaves_the_cache_alone(hip):
     assert eng.decode(first, 12) == orc.decode(first, 12)
 
 
-@pytest.mark.parametrize("family", ["llama-q4_k", "lfm2-q4_0", "gguf-q4_k-q6_k-head"])
-def test_sampled_generate_with_penalties(hip, family):
+@pytest.mark.parametrize("family,freq", [("llama-q4_k", 0.0), ("lfm2-q4_0", 0.0),
+                                         ("gguf-q4_k-q6_k-head", 0.0), ("llama-q4_k", 0.4),
+                                         ("lfm2-q4_0", 0.25)])
+def test_sampled_generate_with_penalties(hip, family, freq):
     """Sampled decoding through the GPU's candidate pick and the host
-    sampler: at temperature 0 with repetition and presence penalties it
-    writes the oracle decoder's penalized greedy tokens (the host sampler
-    over the oracle's full logits); at temperature 0.8 two seeded runs
-    write the same tokens."""
+    sampler (or, with a frequency penalty, the whole row read back and
+    penalized on the host): at temperature 0 with repetition, presence and
+    frequency penalties it writes the oracle decoder's penalized greedy
+    tokens (the host sampler over the oracle's full logits); at temperature
+    0.8 two seeded runs write the same tokens."""
     import random as pyrandom
     from webgllm_amd.sampler import Sampler
     eng, orc = _pair(family, seed=2)
     rng = np.random.default_rng(11)
     prompt = _prompt(rng, 13, eng.shape.vocab)
+    # a small vocabulary repeats tokens, so the frequency counts matter
     got = eng.generate(prompt, 12, Sampler(0, 40, repetition_penalty=1.3,
-                                           presence_penalty=0.2))
-    s = Sampler(0, 40, repetition_penalty=1.3, presence_penalty=0.2)
+                                           presence_penalty=0.2, frequency_penalty=freq))
+    s = Sampler(0, 40, repetition_penalty=1.3, presence_penalty=0.2, frequency_penalty=freq)
     s.see(prompt)
     want, tokens = [], prompt
     for _ in range(12):
@@ -289,3 +293,27 @@ def test_sampled_generate_with_penalties(hip, family):
         runs.append(e2.generate(prompt, 10, Sampler(0.8, 50, top_p=0.95,
                                                     repetition_penalty=1.1), r.random))
     assert runs[0] == runs[1] and all(0 <= t < eng.shape.vocab for t in runs[0])
+
+
+def test_sampled_generate_without_top_k_reads_the_row(hip):
+    """top_k 0 at temperature 0.7: the GPU's 64 chunks could not hold the
+    whole distribution, so the row is read back; two seeded runs write
+    the same tokens, and a top-k of 40 (the GPU's candidates) with the
+    same seed writes what the host path (fewer chunks kept than top-k)
+    writes."""
+    import random as pyrandom
+    from webgllm_amd.sampler import Sampler
+    eng, _ = _pair("llama-q4_k", seed=4)
+    rng = np.random.default_rng(12)
+    prompt = _prompt(rng, 11, eng.shape.vocab)
+    runs = []
+    for top_k in (0, 0, 40):
+        e2, _ = _pair("llama-q4_k", seed=4)
+        runs.append(e2.generate(prompt, 8, Sampler(0.7, top_k, repetition_penalty=1.1),
+                                pyrandom.Random(9).random))
+    assert runs[0] == runs[1]
+    # 8 chunks kept cannot hold a top-40: the row goes to the host
+    e3, _ = _pair("llama-q4_k", seed=4)
+    host = e3.generate(prompt, 8, Sampler(0.7, 40, repetition_penalty=1.1),
+                       pyrandom.Random(9).random, count=8)
+    assert host == runs[2]

@@ -218,6 +218,31 @@ def test_reader_errors(tmp_path):
         OnnxFile(tmp_path / "missing.onnx")
 
 
+def test_external_data_stays_in_the_model_folder(tmp_path):
+    """An external data location must name a file inside the model's folder:
+    absolute paths, .. parts and a symbolic link leading out are refused
+    before anything is mapped; a plain name (or a subfolder) is read."""
+    from webgllm_amd.onnx import OnnxFile
+    outside = tmp_path / "secret.bin"
+    outside.write_bytes(bytes(range(64)))
+    model_dir = tmp_path / "model"
+    (model_dir / "sub").mkdir(parents=True)
+    (model_dir / "w.bin").write_bytes(bytes(range(32)) * 2)
+    (model_dir / "sub" / "v.bin").write_bytes(bytes(range(16)) * 4)
+    (model_dir / "link.bin").symlink_to(outside)
+    locations = {"abs": str(outside), "up": "../secret.bin", "deep": "sub/../../secret.bin",
+                 "link": "link.bin", "ok": "w.bin", "sub": "sub/v.bin"}
+    inits = [W.tensor(k, (8,), W.UINT8, external=(v, 8, 8)) for k, v in locations.items()]
+    path = model_dir / "m.onnx"
+    path.write_bytes(W.model(W.graph("g", [], inits)))
+    with OnnxFile(path) as f:
+        for name in ("abs", "up", "deep", "link"):
+            with pytest.raises(ValueError, match="external data location"):
+                f.data(f.initializers[name])
+        assert bytes(f.data(f.initializers["ok"])) == bytes(range(8, 16))
+        assert bytes(f.data(f.initializers["sub"])) == bytes(range(8, 16))
+
+
 def _nbits_model(tmp_path, **kw):
     from webgllm_amd.onnx import OnnxFile, OnnxModel
     N, K = kw.pop("N", 8), kw.pop("K", 64)

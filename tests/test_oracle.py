@@ -348,6 +348,39 @@ def test_attention_closed_forms():
     assert np.allclose(full[:hd], wts @ vf[:, :hd], rtol=1e-12, atol=1e-12)
 
 
+def test_attention_f32_closed_forms_and_f64():
+    """The float32 attention (the CPU baseline's): one key gives v exactly,
+    q = 0 the mean of V, causal keys unread, and 4096 keys of 8 heads
+    within 1e-5 of the float64 form, single- and multi-threaded alike."""
+    rng = np.random.default_rng(16)
+    hd, heads, kvh = 128, 8, 2
+    stride = kvh * hd
+    q = (rng.standard_normal(heads * hd) / np.sqrt(hd)).astype(np.float32)
+    kc = O.f32_to_h2(rng.standard_normal((4096, stride)).astype(np.float32))
+    vc = O.f32_to_h2(rng.standard_normal((4096, stride)).astype(np.float32))
+    vf = O.halves_to_f32(vc).astype(np.float64)
+    one = O.attention_f32(q, kc, vc, heads, kvh, hd, 1, stride)
+    for h in range(heads):
+        kh = h // (heads // kvh)
+        assert np.array_equal(one[h * hd:(h + 1) * hd],
+                              O.halves_to_f32(vc[0, kh * hd:(kh + 1) * hd]))
+    mean = O.attention_f32(np.zeros_like(q), kc, vc, heads, kvh, hd, 7, stride)
+    assert np.allclose(mean[:hd], vf[:7, :hd].mean(0), rtol=1e-6, atol=1e-6)
+    kc3, vc3 = kc.copy(), vc.copy()
+    kc3[9:] = O.f32_to_h2(np.full((4096 - 9, stride), 50.0, np.float32))
+    vc3[9:] = O.f32_to_h2(np.full((4096 - 9, stride), -7.0, np.float32))
+    assert np.array_equal(O.attention_f32(q, kc, vc, heads, kvh, hd, 9, stride),
+                          O.attention_f32(q, kc3, vc3, heads, kvh, hd, 9, stride))
+    want = O.attention_f64(q, kc, vc, heads, kvh, hd, 4096, stride)
+    a1 = O.attention_f32(q, kc, vc, heads, kvh, hd, 4096, stride, threads=1)
+    a4 = O.attention_f32(q, kc, vc, heads, kvh, hd, 4096, stride, threads=4)
+    assert np.array_equal(a1, a4)
+    assert np.linalg.norm(a1 - want) / np.linalg.norm(want) <= 1e-5
+    # a dropped max subtraction or a wrong GQA head map would fail here
+    wrong = O.attention_f32(q, kc[:, ::-1].copy(), vc, heads, kvh, hd, 4096, stride)
+    assert np.linalg.norm(wrong - want) / np.linalg.norm(want) > 1e-2
+
+
 def test_rope_and_norm_closed_forms():
     hd, R = 64, 64
     rope = O.rope_table(1e6, hd, R, 4096)

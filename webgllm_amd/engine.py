@@ -183,12 +183,8 @@ class Weights:
             blk[:, 0:2] = d.half().view(torch.uint8).view(-1, 2)
             m = ops.Q4Matrix.from_q4_0(src, N, K, src_rows=src_rows)
         elif fmt == "nbits":
-            quant = torch.empty(N * (K // 32) * 16, dtype=torch.uint8, device=dev)
-            quant.random_(0, 256, generator=g)
-            sc = torch.empty(N * (K // 32), device=dev).uniform_(0.002, 0.006, generator=g)
-            zp = torch.empty(N * ((K // 32 + 1) // 2), dtype=torch.uint8, device=dev)
-            zp.random_(0, 256, generator=g)
-            m = ops.Q4Matrix.from_nbits(quant, sc.half().view(torch.uint8), zp, N, K,
+            quant, sc, zp = _nbits_from_normal(N, K, g, dev)
+            m = ops.Q4Matrix.from_nbits(quant, sc.view(torch.uint8), zp, N, K,
                                         src_rows=src_rows)
         elif fmt == "q8_0":
             src = torch.empty(N * (K // 32) * 34, dtype=torch.uint8, device=dev)
@@ -347,49 +343,63 @@ class Engine:
         """Enqueue one batch of M rows (ids[:M] at positions pos..pos+M-1);
         the greedy picks into next_ids unless `pick` is False (the caller
         picks)."""
+        self._embed_rows(M)
+        if M == 1 and self.plan is not None:
+            self.plan.run()
+        else:
+            for i in range(len(self.w.layers)):
+                self._layer_rows(i, M, keep_prefixes)
+        self._head_rows(M, pick)
+
+    def _embed_rows(self, M: int) -> None:
+        """h = the rows' embeddings; the first norm's prescaled input and
+        sums of squares."""
         s, w = self.shape, self.w
-        D, F = s.hidden, s.intermediate
-        h = self.h[:M]
-        x16 = self.x16[:M]
+        D = s.hidden
         first_norm = w.layers[0]["op_norm"] if w.layers else w.final_norm
-        ops.embed(w.embedding, self.ids[:M], out=h,
+        ops.embed(w.embedding, self.ids[:M], out=self.h[:M],
                   epilogue=L.Epilogue(mode=L.EPI_STORE, out16=self.x16.data_ptr(), ld_out16=D,
                                       out16_w=first_norm.data_ptr(), norm_mult_out=PRESCALE,
                                       parts_out=self.parts.data_ptr(), ld_parts_out=D // 4))
-        persistent = M == 1 and self.plan is not None
-        if persistent:
-            self.plan.run()
-        for i, lw in enumerate(() if persistent else w.layers):
-            if s.layer_type(i) == "conv":
-                bcx = self.bcx[:M]
-                ops.gemv(lw["in_proj"], x16, out=bcx,
-                         epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
-                c16 = self.c16[:M]
-                ops.short_conv(bcx, D, s.conv_kernel, lw["taps"], self.state[i],
-                               prefixes=self.prefixes[i][:M] if keep_prefixes else None,
-                               out=c16)
-                ops.gemv(lw["out_proj"], c16, out=h,
-                         epilogue=self._residual_out(M, lw["ffn_norm"]))
+
+    def _layer_rows(self, i: int, M: int, keep_prefixes: bool) -> None:
+        """Layer i over the batch: h += operator(norm(h)); h += FFN(norm(h));
+        the next norm's prescaled input and sums of squares."""
+        s, lw = self.shape, self.w.layers[i]
+        D, F = s.hidden, s.intermediate
+        h, x16 = self.h[:M], self.x16[:M]
+        if s.layer_type(i) == "conv":
+            bcx = self.bcx[:M]
+            ops.gemv(lw["in_proj"], x16, out=bcx,
+                     epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
+            c16 = self.c16[:M]
+            ops.short_conv(bcx, D, s.conv_kernel, lw["taps"], self.state[i],
+                           prefixes=self.prefixes[i][:M] if keep_prefixes else None, out=c16)
+            ops.gemv(lw["out_proj"], c16, out=h, epilogue=self._residual_out(M, lw["ffn_norm"]))
+        else:
+            if s.rope_in_epilogue:
+                ops.gemv(lw["qkv"], x16, epilogue=self._qkv_epilogue(i))
             else:
-                if s.rope_in_epilogue:
-                    ops.gemv(lw["qkv"], x16, epilogue=self._qkv_epilogue(i))
-                else:
-                    qkv = self.qkv[:M]
-                    ops.gemv(lw["qkv"], x16, out=qkv,
-                             epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
-                    ops.head_prep(qkv, self.attn, self.rope, self.pos, self.k_cache[i],
-                                  self.v_cache[i], lw.get("q_norm"), lw.get("k_norm"),
-                                  q_out=self.q[:M])
-                ops.attn_decode(self.q[:M], self.attn, self.k_cache[i], self.v_cache[i],
-                                self.pos, scratch=self.attn_scratch, out=self.att16[:M])
-                ops.gemv(lw["o"], self.att16[:M], out=h,
-                         epilogue=self._residual_out(M, lw["ffn_norm"]))
-            ops.gemv(lw["gate_up"], x16,
-                     epilogue=self._norm_in(L.Epilogue(mode=L.EPI_SWIGLU,
-                                                       out16=self.ff16.data_ptr(), ld_out16=F)))
-            ops.gemv(lw["down"], self.ff16[:M], out=h,
-                     epilogue=self._residual_out(M, self._next_norm(i)))
-        ops.gemv(w.embedding, x16, out=self.logits[:M],
+                qkv = self.qkv[:M]
+                ops.gemv(lw["qkv"], x16, out=qkv,
+                         epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
+                ops.head_prep(qkv, self.attn, self.rope, self.pos, self.k_cache[i],
+                              self.v_cache[i], lw.get("q_norm"), lw.get("k_norm"),
+                              q_out=self.q[:M])
+            ops.attn_decode(self.q[:M], self.attn, self.k_cache[i], self.v_cache[i],
+                            self.pos, scratch=self.attn_scratch, out=self.att16[:M])
+            ops.gemv(lw["o"], self.att16[:M], out=h,
+                     epilogue=self._residual_out(M, lw["ffn_norm"]))
+        ops.gemv(lw["gate_up"], x16,
+                 epilogue=self._norm_in(L.Epilogue(mode=L.EPI_SWIGLU,
+                                                   out16=self.ff16.data_ptr(), ld_out16=F)))
+        ops.gemv(lw["down"], self.ff16[:M], out=h,
+                 epilogue=self._residual_out(M, self._next_norm(i)))
+
+    def _head_rows(self, M: int, pick: bool = True) -> None:
+        """Logits of the batch's rows over the tied embedding; the greedy
+        picks into next_ids when `pick`."""
+        ops.gemv(self.w.embedding, self.x16[:M], out=self.logits[:M],
                  epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
         if pick:
             ops.argmax_rows(self.logits[:M], ids=self.next_ids[:M], tops=self.tops[:M],
@@ -615,20 +625,60 @@ class Engine:
         wg_pick_candidates (the penalties of the sampler's window on the
         device, the best `count` chunks read back) and the sampler draws
         the token from them. The window sees the prompt, then each token
-        written. Returns the `steps` tokens drawn."""
+        written. Returns the `steps` tokens drawn.
+
+        As the reference decides (src/handler.ts:1429-1437), the whole row
+        is read back and penalized and sampled on the host instead when the
+        GPU's candidates cannot hold the distribution: a frequency penalty
+        (the device's mask knows whether a token is in the window, not how
+        often), or top-k off or above the `count` chunks kept."""
         from . import sampler as S
-        pick = S.GpuPick(self.shape.vocab, count, device=self.device)
-        pick.see(sampler.see(prompt))
+        st = sampler.settings
+        greedy = st.temperature <= 0 or st.top_k == 1
+        on_gpu = sampler.frequency_penalty == 0 and (greedy or 0 < st.top_k <= count)
+        pick = S.GpuPick(self.shape.vocab, count, device=self.device) if on_gpu else None
+        changes = sampler.see(prompt)
+        if pick is not None:
+            pick.see(changes)
         out = []
         tokens = list(prompt)
         for _ in range(steps):
             self.forward(tokens)
             row = (len(tokens) - 1) % 8
-            t = S.draw(pick(self.logits[row], sampler), random)
+            if pick is not None:
+                d = pick(self.logits[row], sampler)
+            else:
+                d = sampler.distribution(self.logits[row].cpu().numpy().copy(), penalize=True)
+            t = S.draw(d, random)
             out.append(t)
-            pick.see(sampler.see([t], True))
+            changes = sampler.see([t], True)
+            if pick is not None:
+                pick.see(changes)
             tokens = [t]
         return out
+
+
+def _nbits_from_normal(N: int, K: int, g: torch.Generator, dev):
+    """A MatMulNBits q4 matrix's file arrays quantized from weights ~ N(0,
+    0.02): per block of 32, a zero point ~ U{0..15}, the half scale
+    absmax / max(zp, 15 - zp) and q = clamp(round(w / scale) + zp, 0, 15).
+    Returns (quant [N][K/32][16] bytes, element 2i in byte i's low nibble;
+    half scales [N][K/32]; zero points [N][ceil(K/64)], low nibble first),
+    the layouts src/load-onnx.ts:450-501 reads."""
+    B = K // 32
+    w = torch.randn((N, B, 32), generator=g, device=dev) * 0.02
+    zpv = torch.randint(0, 16, (N, B), generator=g, device=dev)
+    am = w.abs().amax(2).clamp_min(1e-8)
+    sc = (am / torch.maximum(zpv, 15 - zpv).float()).half()
+    q = torch.clamp(torch.round(w / sc.float()[..., None]) + zpv[..., None], 0, 15)
+    q = q.to(torch.uint8)
+    quant = (q[..., 0::2] | (q[..., 1::2] << 4)).contiguous().view(-1)
+    zp8 = zpv.to(torch.uint8)
+    if B % 2:
+        zp8 = torch.cat([zp8, torch.zeros((N, 1), dtype=torch.uint8, device=dev)], 1)
+    zp = (zp8[:, 0::2] | (zp8[:, 1::2] << 4)).contiguous().view(-1)
+    del w, q
+    return quant, sc.contiguous().view(-1), zp
 
 
 def _rope_table(theta: float, head_dim: int, ctx: int) -> torch.Tensor:

@@ -132,12 +132,27 @@ class OnnxFile:
             length = tensor_bytes(t)
         maps = self.__dict__.setdefault("_maps", {})
         if location not in maps:  # each data file mapped once, read-only
-            maps[location] = np.memmap(os.path.join(os.path.dirname(self.path), location),
-                                       dtype=np.uint8, mode="r")
+            maps[location] = np.memmap(self._data_path(t.name, location), dtype=np.uint8,
+                                       mode="r")
         m = maps[location]
         if offset < 0 or offset + length > m.size:
             raise ValueError(f"ONNX: {t.name}: {location} ends before byte {offset + length}")
         return m[offset:offset + length]
+
+    def _data_path(self, name: str, location: str) -> str:
+        """An external data file's path: a relative name inside the model's
+        folder. An absolute location, or one whose real path leaves the
+        folder (.. parts, a symbolic link out), is refused: a model file
+        must not name other files for the reader to map."""
+        folder = os.path.realpath(os.path.dirname(os.path.abspath(self.path)))
+        if not location or os.path.isabs(location) or "\0" in location:
+            raise ValueError(f"ONNX: {name}: external data location {location!r} is not a "
+                             f"relative file name")
+        path = os.path.realpath(os.path.join(folder, location))
+        if os.path.commonpath([folder, path]) != folder or path == folder:
+            raise ValueError(f"ONNX: {name}: external data location {location!r} is outside "
+                             f"the model's folder")
+        return path
 
     def close(self):
         self.__dict__.pop("_maps", None)

@@ -11,6 +11,7 @@ the speculative verify are here.
 from __future__ import annotations
 
 import ctypes as C
+from collections import Counter, deque
 from dataclasses import dataclass
 
 import numpy as np
@@ -51,110 +52,124 @@ class Distribution:
 
 
 class PenaltyWindow:
-    """The last `size` tokens read or written (llama.cpp's repeat_last_n),
-    each penalized once (src/penalty-window.ts:26-141): 0 penalizes none, a
-    negative size every token. States: 1 in the window from the prompt only,
-    3 written in this reply, 0 out of it."""
+    """The tokens the repetition and presence penalties apply to: the last
+    `size` tokens read or written (llama.cpp's repeat_last_n), each counted
+    however often it appears (src/penalty-window.ts:26-141 states the
+    contract). 0 penalizes none, a negative size every token seen. A token's
+    state is 1 while it is in the window from the prompt only, 3 once a
+    written copy is in it, 0 out of it.
+
+    The window is a bounded deque of (token, written) entries with two
+    counters: copies in the window and written copies in it."""
 
     def __init__(self, size: int = DEFAULT_REPEAT_LAST_N):
         self.size = size
-        self.ring: list[tuple[int, bool]] = []
-        self.start = 0
-        self.counts: dict[int, list[int]] = {}  # token -> [all, generated]
+        self._entries: deque = deque(maxlen=size if size > 0 else None)
+        self._seen: Counter = Counter()
+        self._written: Counter = Counter()
 
-    def _state(self, token: int) -> int:
-        c = self.counts.get(token)
-        return 0 if not c else (3 if c[1] > 0 else 1)
+    @staticmethod
+    def _state_of(seen: int, written: int) -> int:
+        return 0 if seen <= 0 else (3 if written > 0 else 1)
+
+    def state(self, token: int) -> int:
+        return self._state_of(self._seen[token], self._written[token])
+
+    def _leaving(self, incoming: list) -> list:
+        """The entries that leave when `incoming` entries join, oldest first
+        (some of `incoming` itself when it is longer than the window)."""
+        if self.size < 0:
+            return []
+        over = len(self._entries) + len(incoming) - self.size
+        if over <= 0:
+            return []
+        old = len(self._entries)
+        return [self._entries[k] if k < old else incoming[k - old] for k in range(over)]
 
     def push(self, tokens, generated: bool = False) -> list:
-        """Takes tokens in order; returns [(token, state)] of those whose state changed."""
+        """Takes tokens in order (the prompt's, then each one written);
+        returns [(token, state)] of the tokens whose state changed: the
+        tokens taken first, then those that left, each once."""
         if self.size == 0:
             return []
-        before: dict[int, int] = {}
-
-        def note(t):
-            if t not in before:
-                before[t] = self._state(t)
-        for t in tokens:
-            t = int(t)
-            note(t)
-            self.ring.append((t, generated))
-            c = self.counts.setdefault(t, [0, 0])
-            c[0] += 1
-            if generated:
-                c[1] += 1
-            if self.size > 0 and len(self.ring) - self.start > self.size:
-                old, gen = self.ring[self.start]
-                self.start += 1
-                note(old)
-                c = self.counts[old]
-                c[0] -= 1
-                if gen:
-                    c[1] -= 1
-                if c[0] == 0:
-                    del self.counts[old]
-        if self.start > 4096:
-            del self.ring[:self.start]
-            self.start = 0
-        return [(t, self._state(t)) for t, was in before.items() if self._state(t) != was]
+        incoming = [(int(t), bool(generated)) for t in tokens]
+        leaving = self._leaving(incoming)
+        touched = list(dict.fromkeys([t for t, _ in incoming] + [t for t, _ in leaving]))
+        before = [self.state(t) for t in touched]
+        for t, g in incoming:
+            self._seen[t] += 1
+            self._written[t] += g
+        for t, g in leaving:
+            self._seen[t] -= 1
+            self._written[t] -= g
+            if self._seen[t] == 0:
+                del self._seen[t]
+                self._written.pop(t, None)
+        self._entries.extend(incoming)
+        return [(t, self.state(t)) for t, b in zip(touched, before) if self.state(t) != b]
 
     def ahead(self, drafts) -> list:
-        """The SeenRows [token, state, first row, end row] of a batch whose
-        inputs after the first are `drafts` (src/penalty-window.ts:81-130)."""
-        if self.size == 0 or len(drafts) == 0:
+        """The window's states at each row of a batch whose inputs after the
+        first are `drafts` (row r has read drafts 0..r-1 as written), as
+        SeenRows [token, state, first row, end row): the runs of rows where
+        a token's state differs from its state now, ordered by first row,
+        a row's draft before the token it pushed out. Nothing changes.
+
+        The drafts are replayed on copies of the touched tokens' counts
+        (the drafts and the entries they push out, known up front), giving
+        a token x row table of states; each token's row is then cut into
+        runs."""
+        drafts = [int(d) for d in drafts]
+        if self.size == 0 or not drafts:
             return []
         rows = len(drafts) + 1
-        changed: dict[int, list[int]] = {}
-
-        def count(t):
-            c = changed.get(t)
-            if c is None:
-                now = self.counts.get(t)
-                c = [now[0], now[1]] if now else [0, 0]
-                changed[t] = c
-            return c
-        live = len(self.ring) - self.start
-        out = 0
-        open_: dict[int, list] = {}
-        segments: list = []
-        for i, d in enumerate(drafts):
-            d = int(d)
-            row = i + 1
-            touched = [d]
-            c = count(d)
-            c[0] += 1
-            c[1] += 1
-            if self.size > 0 and live + i + 1 - out > self.size:
-                if out < live:
-                    old, gen = self.ring[self.start + out]
-                else:
-                    old, gen = int(drafts[out - live]), True
-                out += 1
-                o = count(old)
-                o[0] -= 1
-                if gen:
-                    o[1] -= 1
-                touched.append(old)
+        incoming = [(d, True) for d in drafts]
+        leaving = self._leaving(incoming)
+        # the entry that leaves at row r (1-based), if any
+        first_out = len(drafts) - len(leaving) + 1
+        out_at = {first_out + k: e for k, e in enumerate(leaving)}
+        touched = list(dict.fromkeys(drafts + [t for t, _ in leaving]))
+        seen = {t: self._seen[t] for t in touched}
+        written = {t: self._written[t] for t in touched}
+        base = {t: self._state_of(seen[t], written[t]) for t in touched}
+        table = {t: [base[t]] for t in touched}  # state at rows 0 .. rows - 1
+        rank = {}  # (token, row) -> 0 for the row's draft, 1 for what it pushed out
+        for r in range(1, rows):
+            d = drafts[r - 1]
+            seen[d] += 1
+            written[d] += 1
+            rank.setdefault((d, r), 0)
+            if r in out_at:
+                t, g = out_at[r]
+                seen[t] -= 1
+                written[t] -= g
+                rank.setdefault((t, r), 1)
             for t in touched:
-                c = count(t)
-                state = 0 if c[0] == 0 else (3 if c[1] > 0 else 1)
-                seg = open_.get(t)
-                if state == (seg[1] if seg else self._state(t)):
+                table[t].append(self._state_of(seen[t], written[t]))
+        segments = []
+        for t in touched:
+            states = table[t]
+            r = 1
+            while r < rows:
+                if states[r] == base[t]:
+                    r += 1
                     continue
-                if seg:
-                    seg[3] = row
-                    del open_[t]
-                if state != self._state(t):
-                    nxt = [t, state, row, rows]
-                    segments.append(nxt)
-                    open_[t] = nxt
-        return segments
+                end = r + 1
+                while end < rows and states[end] == states[r]:
+                    end += 1
+                segments.append((r, rank.get((t, r), 0), [t, states[r], r, end]))
+                r = end
+        segments.sort(key=lambda s: (s[0], s[1]))
+        return [seg for _, _, seg in segments]
 
     def entries(self) -> list:
-        return [(t, self._state(t)) for t in self.counts]
+        """The tokens in the window, each once, with its state."""
+        return [(t, self.state(t)) for t in self._seen]
 
     def counted(self) -> list:
-        return [(t, c[0]) for t, c in self.counts.items()]
+        """Each token in the window and its copies there (the frequency
+        penalty's count)."""
+        return list(self._seen.items())
 
 
 class Sampler:
@@ -273,22 +288,25 @@ def draw_at(d: Distribution, u: float) -> int:
 
 
 def verify(d: Distribution, drafted: int, random=None):
-    """Speculative sampling's step for a drafted token (src/sampler.ts:
-    209-223): (True, drafted) when kept, else (False, a token drawn from d
-    without it). The uniform draws are taken in the reference's order."""
+    """Speculative sampling's accept-or-resample step for a drafted token
+    (src/sampler.ts:209-223 states it): the draft survives with the
+    probability d gives it, else the token comes from the residual, d with
+    the draft's mass taken out and the rest renormalized (float32 stores of
+    p / (1 - p_draft)). Returns (kept, token). One uniform decides the keep
+    (only when 0 < p_draft < 1) and the draw takes the next, the order that
+    makes a seeded reply reproduce the reference's tokens."""
     rnd = _random(random)
-    hit = np.nonzero(d.ids == drafted)[0]
-    j = int(hit[-1]) if hit.size else -1
-    pd = 0.0 if j < 0 else float(d.p[j])
-    if pd >= 1 or (pd > 0 and rnd() < pd):
+    where = np.flatnonzero(d.ids == drafted)
+    j = int(where[-1]) if where.size else None
+    p_draft = 0.0 if j is None else float(d.p[j])
+    keep = p_draft >= 1.0 or (p_draft > 0.0 and rnd() < p_draft)
+    if keep:
         return True, drafted
-    if j < 0:
+    if j is None:
         return False, draw(d, rnd)
-    rest = d.p.copy()
-    rest[j] = 0
-    total = 1 - pd
-    rest = (rest.astype(np.float64) / total).astype(np.float32)
-    return False, draw(Distribution(d.ids, rest), rnd)
+    residual = (d.p.astype(np.float64) / (1.0 - p_draft)).astype(np.float32)
+    residual[j] = 0.0
+    return False, draw(Distribution(d.ids, residual), rnd)
 
 
 def verify_at(d: Distribution, drafted: int, u: float):
