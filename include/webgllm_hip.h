@@ -67,7 +67,12 @@ typedef struct {
 } wg_limits;
 
 /* new Gpu(canvas) / dispose (gl.ts:316-331): a context on `device`, with
- * its own stream. Destroy frees every buffer it still holds. */
+ * its own stream and a pool of pinned host staging slots for writes and
+ * reads. Destroy waits for the stream, frees every buffer it still holds
+ * and cancels its outstanding reads. Every handle of a deleted buffer, a
+ * finished or cancelled read or a destroyed context makes later calls
+ * return WG_ERR_DISPOSED (the reference's lost-context GpuError, gl.ts:502).
+ * A context is used from one thread at a time, as the reference's Gpu is. */
 int wg_ctx_create(int device, wg_ctx **out);
 int wg_ctx_destroy(wg_ctx *ctx);
 /* Gpu.limits (gl.ts:131-140). */
@@ -77,11 +82,15 @@ void *wg_ctx_stream(wg_ctx *ctx);
 
 /* Gpu.texture (gl.ts:263-305): a device buffer, optionally initialised. */
 int wg_buf_create(wg_ctx *ctx, size_t bytes, const void *init, wg_buf **out);
-/* Gpu.write (gl.ts:354-374): bytes into [offset, offset + bytes). */
+/* Gpu.write (gl.ts:354-374): bytes into [offset, offset + bytes), queued on
+ * the context's stream; `src` is copied into pinned staging before the
+ * call returns (the caller may reuse it at once) and nothing waits. */
 int wg_buf_write(wg_ctx *ctx, wg_buf *buf, size_t offset, const void *src, size_t bytes);
 /* Gpu.zero (gl.ts:710-726). */
 int wg_buf_zero(wg_ctx *ctx, wg_buf *buf);
-/* Gpu.delete (gl.ts:448-461). */
+/* Gpu.delete (gl.ts:448-461): the handle dies at once (and leaves
+ * wg_bytes_live); the memory is freed once the work queued before the
+ * delete has finished. */
 int wg_buf_delete(wg_ctx *ctx, wg_buf *buf);
 void *wg_buf_ptr(wg_buf *buf);
 size_t wg_buf_size(wg_buf *buf);
@@ -101,6 +110,11 @@ int wg_read_now(wg_ctx *ctx, wg_buf *buf, size_t offset, size_t bytes, void *dst
 /* Gpu.flush (gl.ts:729-732) and PacedGpu.finish. */
 int wg_flush(wg_ctx *ctx);
 int wg_finish(wg_ctx *ctx);
+/* The context's pinned staging pool: slots and their bytes (slots are
+ * reused; the pool grows only while more copies are in flight than it
+ * holds, to at most 16 uploads in flight). No reference counterpart: it
+ * accounts for the host memory the readbacks and writes above use. */
+int wg_ctx_staging(wg_ctx *ctx, int32_t *slots, size_t *bytes);
 
 /* ------------------------------------------------ 2. quantized matrices */
 

@@ -296,24 +296,34 @@ def test_sampled_generate_with_penalties(hip, family, freq):
 
 
 def test_sampled_generate_without_top_k_reads_the_row(hip):
-    """top_k 0 at temperature 0.7: the GPU's 64 chunks could not hold the
-    whole distribution, so the row is read back; two seeded runs write
-    the same tokens, and a top-k of 40 (the GPU's candidates) with the
-    same seed writes what the host path (fewer chunks kept than top-k)
-    writes."""
+    """top_k 0 at temperature 0.7: the GPU's chunks could not hold the
+    whole distribution, so the row is read back and sampled on the host;
+    two seeded runs write the same tokens. And the two paths' distributions
+    for one row are the same set of (token, probability), bit for bit: the
+    GPU's candidates of a top-40 pick and the host's whole penalized row.
+    (Their draws may differ: a draw walks the distribution in its heap
+    order, which depends on the order the candidates come in.)"""
     import random as pyrandom
-    from webgllm_amd.sampler import Sampler
+    from webgllm_amd.sampler import GpuPick, Sampler
     eng, _ = _pair("llama-q4_k", seed=4)
     rng = np.random.default_rng(12)
     prompt = _prompt(rng, 11, eng.shape.vocab)
     runs = []
-    for top_k in (0, 0, 40):
+    for _ in range(2):
         e2, _ = _pair("llama-q4_k", seed=4)
-        runs.append(e2.generate(prompt, 8, Sampler(0.7, top_k, repetition_penalty=1.1),
+        runs.append(e2.generate(prompt, 8, Sampler(0.7, 0, repetition_penalty=1.1),
                                 pyrandom.Random(9).random))
-    assert runs[0] == runs[1]
-    # 8 chunks kept cannot hold a top-40: the row goes to the host
-    e3, _ = _pair("llama-q4_k", seed=4)
-    host = e3.generate(prompt, 8, Sampler(0.7, 40, repetition_penalty=1.1),
-                       pyrandom.Random(9).random, count=8)
-    assert host == runs[2]
+    assert runs[0] == runs[1] and all(0 <= t < eng.shape.vocab for t in runs[0])
+    eng.forward(prompt)
+    row = eng.logits[(len(prompt) - 1) % 8]
+    s_gpu = Sampler(0.7, 40, repetition_penalty=1.1, presence_penalty=0.3)
+    s_host = Sampler(0.7, 40, repetition_penalty=1.1, presence_penalty=0.3)
+    pick = GpuPick(eng.shape.vocab, 64)
+    pick.see(s_gpu.see(prompt))
+    s_host.see(prompt)
+    d_gpu = pick(row, s_gpu)
+    d_host = s_host.distribution(row.cpu().numpy().copy(), penalize=True)
+    a, b = np.argsort(d_gpu.ids), np.argsort(d_host.ids)
+    assert d_gpu.ids.size == d_host.ids.size == 40
+    assert np.array_equal(d_gpu.ids[a], d_host.ids[b])
+    assert np.array_equal(d_gpu.p[a], d_host.p[b])

@@ -6,9 +6,12 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <unordered_set>
+#include <utility>
+#include <vector>
 
 #include "common.h"
 #include "dot.h"
@@ -62,7 +65,8 @@ int check_matrix(const wg_q4_matrix *m, const char *who) {
 // src/engine.ts:147-625): read by the launchers, set through wg_tuning_set.
 struct Knob {
   const char *name;
-  int value, lo, hi;
+  std::atomic<int> value;
+  int lo, hi;
 };
 static Knob g_knobs[] = {
     {"gemv_wg_per_cu", 2, 1, 16},        // persistent row-group GEMV workgroups per CU
@@ -80,7 +84,7 @@ static Knob g_knobs[] = {
 
 int tuning(const char *name) {
   for (auto &k : g_knobs)
-    if (!strcmp(k.name, name)) return k.value;
+    if (!strcmp(k.name, name)) return k.value.load(std::memory_order_relaxed);
   return 0;
 }
 
@@ -118,9 +122,62 @@ int persistent_grid(int work_groups, int per_cu) {
 
 using namespace wg;
 
+// ------------------------------------------------------------ backend objects
+//
+// Pinned host staging: each context keeps a pool of page-locked slots, each
+// with its own event. A write copies the caller's bytes into a slot and
+// queues the upload from it (the caller's buffer is free at once, as after
+// gl.texSubImage2D, and nothing waits); a read queues the download into a
+// slot that its fence holds until finished or cancelled. A slot whose copy
+// may still be in flight is reused only after its event has completed.
+namespace {
+
+enum SlotState { SLOT_FREE, SLOT_INFLIGHT, SLOT_FENCED };
+
+struct Slot {
+  void *host = nullptr;
+  size_t cap = 0;
+  hipEvent_t done = nullptr;
+  SlotState state = SLOT_FREE;
+};
+
+constexpr size_t SLOT_MIN = 64 << 10;  // smallest slot: 64 KiB
+constexpr int INFLIGHT_MAX = 16;       // uploads in flight before a write waits for the oldest
+
+// Live handles, so that a call on a deleted buffer, a finished fence or a
+// destroyed context reports WG_ERR_DISPOSED instead of touching freed memory.
+struct Registry {
+  std::mutex mu;
+  std::unordered_set<const void *> live;
+};
+Registry &registry() {
+  static Registry *r = new Registry();  // never destroyed: handles may outlive static teardown
+  return *r;
+}
+void reg_add(const void *h) {
+  std::lock_guard<std::mutex> g(registry().mu);
+  registry().live.insert(h);
+}
+void reg_del(const void *h) {
+  std::lock_guard<std::mutex> g(registry().mu);
+  registry().live.erase(h);
+}
+bool reg_has(const void *h) {
+  std::lock_guard<std::mutex> g(registry().mu);
+  return h && registry().live.count(h);
+}
+
+}  // namespace
+
 struct wg_buf {
   wg_ctx *ctx;
   void *ptr;
+  size_t bytes;
+};
+
+struct wg_fence {
+  wg_ctx *ctx;
+  Slot *slot;
   size_t bytes;
 };
 
@@ -129,15 +186,103 @@ struct wg_ctx {
   hipStream_t stream;
   std::mutex lock;
   std::unordered_set<wg_buf *> live;
+  std::unordered_set<wg_fence *> fences;
+  std::vector<Slot *> pool;
+  // deleted buffers' memory, freed once the work queued before the delete is done
+  std::vector<std::pair<void *, hipEvent_t>> graveyard;
   size_t bytes = 0;
 };
 
-struct wg_fence {
-  wg_ctx *ctx;
-  hipEvent_t done;
-  void *host;  // pinned staging
-  size_t bytes;
-};
+namespace {
+
+// Frees the graveyard entries whose events have completed (all with `wait`).
+// Caller holds c->lock.
+void reap(wg_ctx *c, bool wait) {
+  auto &gy = c->graveyard;
+  for (size_t k = 0; k < gy.size();) {
+    hipError_t e = wait ? hipEventSynchronize(gy[k].second) : hipEventQuery(gy[k].second);
+    if (e == hipErrorNotReady) {
+      k++;
+      continue;
+    }
+    (void)hipFree(gy[k].first);
+    (void)hipEventDestroy(gy[k].second);
+    gy[k] = gy.back();
+    gy.pop_back();
+  }
+}
+
+// A slot of at least `bytes` for the caller (marked `state`). Caller holds c->lock.
+int take_slot(wg_ctx *c, size_t bytes, SlotState state, Slot **out, const char *who) {
+  Slot *best = nullptr;
+  int inflight = 0;
+  for (Slot *s : c->pool) {
+    if (s->state == SLOT_INFLIGHT) {
+      if (hipEventQuery(s->done) == hipErrorNotReady) {
+        inflight++;
+        continue;
+      }
+      s->state = SLOT_FREE;
+    }
+    if (s->state != SLOT_FREE) continue;
+    if (s->cap >= bytes && (!best || best->cap < bytes || s->cap < best->cap)) best = s;
+    else if (!best) best = s;  // a free slot to grow if none is large enough
+  }
+  if (!best && inflight >= INFLIGHT_MAX) {  // bounded pool: wait for an upload to land
+    for (Slot *s : c->pool)
+      if (s->state == SLOT_INFLIGHT) {
+        WG_HIP(hipEventSynchronize(s->done));
+        s->state = SLOT_FREE;
+        best = s;
+        break;
+      }
+  }
+  if (!best) {
+    best = new Slot();
+    hipError_t e = hipEventCreateWithFlags(&best->done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      delete best;
+      return fail(WG_ERR_DEVICE, "%s: event: %s", who, hipGetErrorString(e));
+    }
+    c->pool.push_back(best);
+  }
+  if (best->cap < bytes) {
+    size_t cap = bytes > SLOT_MIN ? bytes : SLOT_MIN;
+    void *h = nullptr;
+    hipError_t e = hipHostMalloc(&h, cap, hipHostMallocDefault);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(WG_ERR_OOM, "%s: %zu bytes of pinned staging: %s", who, cap,
+                  hipGetErrorString(e));
+    }
+    if (best->host) (void)hipHostFree(best->host);
+    best->host = h;
+    best->cap = cap;
+  }
+  best->state = state;
+  *out = best;
+  return WG_OK;
+}
+
+// The context and buffer are live and the buffer belongs to the context.
+int owned(wg_ctx *c, wg_buf *b, const char *who) {
+  WG_REQUIRE(c && b, "%s: null argument", who);
+  if (!reg_has(c)) return fail(WG_ERR_DISPOSED, "%s: the context was destroyed", who);
+  if (!reg_has(b)) return fail(WG_ERR_DISPOSED, "%s: buffer was deleted", who);
+  WG_REQUIRE(b->ctx == c, "%s: the buffer belongs to another context", who);
+  return WG_OK;
+}
+
+void fence_release(wg_fence *f, bool copied) {
+  // a fence's copy that was never waited for may still be landing: its slot
+  // is reused only after its event
+  f->slot->state = copied ? SLOT_FREE : SLOT_INFLIGHT;
+  f->ctx->fences.erase(f);
+  reg_del(f);
+  delete f;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -147,7 +292,7 @@ int wg_tuning_set(const char *name, int32_t value) {
     if (!strcmp(k.name, name)) {
       WG_REQUIRE(value >= k.lo && value <= k.hi, "wg_tuning_set: %s = %d is outside [%d, %d]",
                  name, value, k.lo, k.hi);
-      k.value = value;
+      k.value.store(value, std::memory_order_relaxed);
       return WG_OK;
     }
   return fail(WG_ERR_INVALID, "wg_tuning_set: no knob named %s", name);
@@ -157,14 +302,14 @@ int wg_tuning_get(const char *name, int32_t *value) {
   WG_REQUIRE(name && value, "wg_tuning_get: null argument");
   for (auto &k : g_knobs)
     if (!strcmp(k.name, name)) {
-      *value = k.value;
+      *value = k.value.load(std::memory_order_relaxed);
       return WG_OK;
     }
   return fail(WG_ERR_INVALID, "wg_tuning_get: no knob named %s", name);
 }
 
 const char *wg_last_error(void) { return g_error; }
-const char *wg_version(void) { return "webgllm_hip 0.1 gfx950"; }
+const char *wg_version(void) { return "webgllm_hip 0.2 gfx950"; }
 
 int wg_ctx_create(int device, wg_ctx **out) {
   WG_REQUIRE(out, "wg_ctx_create: no output");
@@ -177,26 +322,49 @@ int wg_ctx_create(int device, wg_ctx **out) {
   wg_ctx *c = new wg_ctx();
   c->device = device;
   c->stream = s;
+  reg_add(c);
   *out = c;
   return WG_OK;
 }
 
 int wg_ctx_destroy(wg_ctx *c) {
   WG_REQUIRE(c, "wg_ctx_destroy: no context");
+  if (!reg_has(c)) return fail(WG_ERR_DISPOSED, "wg_ctx_destroy: the context was destroyed");
+  reg_del(c);
   WG_HIP(hipSetDevice(c->device));
-  WG_HIP(hipStreamSynchronize(c->stream));
-  for (wg_buf *b : c->live) {
-    (void)hipFree(b->ptr);
-    delete b;
+  hipError_t sync = hipStreamSynchronize(c->stream);
+  {
+    std::lock_guard<std::mutex> g(c->lock);
+    // outstanding reads are cancelled: their handles report WG_ERR_DISPOSED
+    for (wg_fence *f : c->fences) {
+      reg_del(f);
+      delete f;
+    }
+    c->fences.clear();
+    for (wg_buf *b : c->live) {
+      reg_del(b);
+      (void)hipFree(b->ptr);
+      delete b;
+    }
+    c->live.clear();
+    reap(c, true);
+    for (Slot *s : c->pool) {
+      (void)hipEventDestroy(s->done);
+      if (s->host) (void)hipHostFree(s->host);
+      delete s;
+    }
+    c->pool.clear();
   }
-  c->live.clear();
   (void)hipStreamDestroy(c->stream);
   delete c;
+  if (sync != hipSuccess)
+    return fail(WG_ERR_DEVICE, "wg_ctx_destroy: %s", hipGetErrorString(sync));
   return WG_OK;
 }
 
 int wg_ctx_limits(wg_ctx *c, wg_limits *out) {
   WG_REQUIRE(c && out, "wg_ctx_limits: null argument");
+  if (!reg_has(c)) return fail(WG_ERR_DISPOSED, "wg_ctx_limits: the context was destroyed");
   hipDeviceProp_t p;
   WG_HIP(hipGetDeviceProperties(&p, c->device));
   out->device = c->device;
@@ -208,38 +376,40 @@ int wg_ctx_limits(wg_ctx *c, wg_limits *out) {
   return WG_OK;
 }
 
-void *wg_ctx_stream(wg_ctx *c) { return c ? (void *)c->stream : nullptr; }
+void *wg_ctx_stream(wg_ctx *c) { return reg_has(c) ? (void *)c->stream : nullptr; }
 
 int wg_buf_create(wg_ctx *c, size_t bytes, const void *init, wg_buf **out) {
   WG_REQUIRE(c && out, "wg_buf_create: null argument");
+  if (!reg_has(c)) return fail(WG_ERR_DISPOSED, "wg_buf_create: the context was destroyed");
   WG_REQUIRE(bytes > 0, "wg_buf_create: empty buffer");
   WG_HIP(hipSetDevice(c->device));
+  {
+    std::lock_guard<std::mutex> g(c->lock);
+    reap(c, false);
+  }
   void *p = nullptr;
   hipError_t e = hipMalloc(&p, bytes);
   if (e != hipSuccess) {
     (void)hipGetLastError();
     return fail(WG_ERR_OOM, "wg_buf_create: %zu bytes: %s", bytes, hipGetErrorString(e));
   }
+  wg_buf *b = new wg_buf{c, p, bytes};
+  {
+    std::lock_guard<std::mutex> g(c->lock);
+    c->live.insert(b);
+    c->bytes += bytes;
+  }
+  reg_add(b);
   if (init) {
-    e = hipMemcpyAsync(p, init, bytes, hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (e != hipSuccess) {
-      (void)hipFree(p);
-      return fail(WG_ERR_DEVICE, "wg_buf_create: upload: %s", hipGetErrorString(e));
+    int rc = wg_buf_write(c, b, 0, init, bytes);
+    if (rc) {
+      char msg[512];
+      snprintf(msg, sizeof msg, "%s", wg_last_error());
+      (void)wg_buf_delete(c, b);
+      return fail(rc, "wg_buf_create: %s", msg);
     }
   }
-  wg_buf *b = new wg_buf{c, p, bytes};
-  std::lock_guard<std::mutex> g(c->lock);
-  c->live.insert(b);
-  c->bytes += bytes;
   *out = b;
-  return WG_OK;
-}
-
-static int owned(wg_ctx *c, wg_buf *b, const char *who) {
-  WG_REQUIRE(c && b, "%s: null argument", who);
-  std::lock_guard<std::mutex> g(c->lock);
-  if (!c->live.count(b)) return fail(WG_ERR_DISPOSED, "%s: buffer was deleted", who);
   return WG_OK;
 }
 
@@ -250,14 +420,29 @@ int wg_buf_write(wg_ctx *c, wg_buf *b, size_t offset, const void *src, size_t by
   WG_REQUIRE(offset <= b->bytes && bytes <= b->bytes - offset,
              "wg_buf_write: [%zu, %zu) is outside the %zu-byte buffer", offset, offset + bytes,
              b->bytes);
-  WG_HIP(hipMemcpyAsync((char *)b->ptr + offset, src, bytes, hipMemcpyHostToDevice, c->stream));
-  WG_HIP(hipStreamSynchronize(c->stream));
+  if (!bytes) return WG_OK;
+  WG_HIP(hipSetDevice(c->device));
+  std::lock_guard<std::mutex> g(c->lock);
+  Slot *s = nullptr;
+  rc = take_slot(c, bytes, SLOT_INFLIGHT, &s, "wg_buf_write");
+  if (rc) return rc;
+  memcpy(s->host, src, bytes);
+  hipError_t e =
+      hipMemcpyAsync((char *)b->ptr + offset, s->host, bytes, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipEventRecord(s->done, c->stream);
+  if (e != hipSuccess) {
+    // the copy may or may not have been queued: wait for the stream before the slot is reused
+    (void)hipStreamSynchronize(c->stream);
+    s->state = SLOT_FREE;
+    return fail(WG_ERR_DEVICE, "wg_buf_write: %s", hipGetErrorString(e));
+  }
   return WG_OK;
 }
 
 int wg_buf_zero(wg_ctx *c, wg_buf *b) {
   int rc = owned(c, b, "wg_buf_zero");
   if (rc) return rc;
+  WG_HIP(hipSetDevice(c->device));
   WG_HIP(hipMemsetAsync(b->ptr, 0, b->bytes, c->stream));
   return WG_OK;
 }
@@ -265,23 +450,32 @@ int wg_buf_zero(wg_ctx *c, wg_buf *b) {
 int wg_buf_delete(wg_ctx *c, wg_buf *b) {
   int rc = owned(c, b, "wg_buf_delete");
   if (rc) return rc;
-  // The stream may still read it.
-  WG_HIP(hipStreamSynchronize(c->stream));
-  {
-    std::lock_guard<std::mutex> g(c->lock);
-    c->live.erase(b);
-    c->bytes -= b->bytes;
+  WG_HIP(hipSetDevice(c->device));
+  reg_del(b);
+  std::lock_guard<std::mutex> g(c->lock);
+  c->live.erase(b);
+  c->bytes -= b->bytes;
+  // the stream may still read it: freed once the work queued so far is done
+  hipEvent_t ev = nullptr;
+  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(ev, c->stream);
+  if (e == hipSuccess) {
+    c->graveyard.emplace_back(b->ptr, ev);
+  } else {
+    if (ev) (void)hipEventDestroy(ev);
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(b->ptr);
   }
-  WG_HIP(hipFree(b->ptr));
   delete b;
+  reap(c, false);
   return WG_OK;
 }
 
-void *wg_buf_ptr(wg_buf *b) { return b ? b->ptr : nullptr; }
-size_t wg_buf_size(wg_buf *b) { return b ? b->bytes : 0; }
+void *wg_buf_ptr(wg_buf *b) { return reg_has(b) ? b->ptr : nullptr; }
+size_t wg_buf_size(wg_buf *b) { return reg_has(b) ? b->bytes : 0; }
 
 size_t wg_bytes_live(wg_ctx *c) {
-  if (!c) return 0;
+  if (!reg_has(c)) return 0;
   std::lock_guard<std::mutex> g(c->lock);
   return c->bytes;
 }
@@ -293,51 +487,54 @@ int wg_read_start(wg_ctx *c, wg_buf *b, size_t offset, size_t bytes, wg_fence **
   WG_REQUIRE(offset <= b->bytes && bytes <= b->bytes - offset && bytes > 0,
              "wg_read_start: [%zu, %zu) is outside the %zu-byte buffer", offset, offset + bytes,
              b->bytes);
-  void *host = nullptr;
-  WG_HIP(hipHostMalloc(&host, bytes, hipHostMallocDefault));
-  hipEvent_t ev;
-  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(host, (char *)b->ptr + offset, bytes, hipMemcpyDeviceToHost, c->stream);
-  if (e == hipSuccess) e = hipEventRecord(ev, c->stream);
+  WG_HIP(hipSetDevice(c->device));
+  std::lock_guard<std::mutex> g(c->lock);
+  Slot *s = nullptr;
+  rc = take_slot(c, bytes, SLOT_FENCED, &s, "wg_read_start");
+  if (rc) return rc;
+  hipError_t e =
+      hipMemcpyAsync(s->host, (char *)b->ptr + offset, bytes, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipEventRecord(s->done, c->stream);
   if (e != hipSuccess) {
-    (void)hipHostFree(host);
+    (void)hipStreamSynchronize(c->stream);
+    s->state = SLOT_FREE;
     return fail(WG_ERR_DEVICE, "wg_read_start: %s", hipGetErrorString(e));
   }
-  *out = new wg_fence{c, ev, host, bytes};
+  wg_fence *f = new wg_fence{c, s, bytes};
+  c->fences.insert(f);
+  reg_add(f);
+  *out = f;
   return WG_OK;
 }
 
 int wg_fence_ready(wg_fence *f) {
   WG_REQUIRE(f, "wg_fence_ready: no fence");
-  hipError_t e = hipEventQuery(f->done);
+  if (!reg_has(f)) return fail(WG_ERR_DISPOSED, "wg_fence_ready: the read was finished or cancelled");
+  hipError_t e = hipEventQuery(f->slot->done);
   if (e == hipSuccess) return 1;
   if (e == hipErrorNotReady) return 0;
   return fail(WG_ERR_DEVICE, "wg_fence_ready: %s", hipGetErrorString(e));
 }
 
-static void fence_free(wg_fence *f) {
-  (void)hipEventDestroy(f->done);
-  (void)hipHostFree(f->host);
-  delete f;
-}
-
 int wg_read_finish(wg_fence *f, void *dst) {
   WG_REQUIRE(f, "wg_read_finish: no fence");
-  hipError_t e = hipEventSynchronize(f->done);
-  if (e != hipSuccess) {
-    fence_free(f);
-    return fail(WG_ERR_DEVICE, "wg_read_finish: %s", hipGetErrorString(e));
-  }
-  if (dst) memcpy(dst, f->host, f->bytes);
-  fence_free(f);
+  if (!reg_has(f))
+    return fail(WG_ERR_DISPOSED, "wg_read_finish: the read was finished or cancelled");
+  wg_ctx *c = f->ctx;
+  hipError_t e = hipEventSynchronize(f->slot->done);
+  std::lock_guard<std::mutex> g(c->lock);
+  if (e == hipSuccess && dst) memcpy(dst, f->slot->host, f->bytes);
+  fence_release(f, e == hipSuccess);
+  if (e != hipSuccess) return fail(WG_ERR_DEVICE, "wg_read_finish: %s", hipGetErrorString(e));
   return WG_OK;
 }
 
 int wg_read_cancel(wg_fence *f) {
   WG_REQUIRE(f, "wg_read_cancel: no fence");
-  (void)hipEventSynchronize(f->done);
-  fence_free(f);
+  if (!reg_has(f))
+    return fail(WG_ERR_DISPOSED, "wg_read_cancel: the read was finished or cancelled");
+  std::lock_guard<std::mutex> g(f->ctx->lock);
+  fence_release(f, false);  // no wait: the slot is reused after its copy lands
   return WG_OK;
 }
 
@@ -350,12 +547,28 @@ int wg_read_now(wg_ctx *c, wg_buf *b, size_t offset, size_t bytes, void *dst) {
 
 int wg_flush(wg_ctx *c) {
   WG_REQUIRE(c, "wg_flush: no context");
+  if (!reg_has(c)) return fail(WG_ERR_DISPOSED, "wg_flush: the context was destroyed");
   return WG_OK;  // HIP submits as it goes; nothing is held back.
 }
 
 int wg_finish(wg_ctx *c) {
   WG_REQUIRE(c, "wg_finish: no context");
+  if (!reg_has(c)) return fail(WG_ERR_DISPOSED, "wg_finish: the context was destroyed");
+  WG_HIP(hipSetDevice(c->device));
   WG_HIP(hipStreamSynchronize(c->stream));
+  std::lock_guard<std::mutex> g(c->lock);
+  reap(c, false);
+  return WG_OK;
+}
+
+int wg_ctx_staging(wg_ctx *c, int32_t *slots, size_t *bytes) {
+  WG_REQUIRE(c, "wg_ctx_staging: no context");
+  if (!reg_has(c)) return fail(WG_ERR_DISPOSED, "wg_ctx_staging: the context was destroyed");
+  std::lock_guard<std::mutex> g(c->lock);
+  size_t total = 0;
+  for (Slot *s : c->pool) total += s->cap;
+  if (slots) *slots = (int32_t)c->pool.size();
+  if (bytes) *bytes = total;
   return WG_OK;
 }
 

@@ -165,6 +165,7 @@ def load():
         "wg_read_now": (C.c_int, [P, P, SZ, SZ, P]),
         "wg_flush": (C.c_int, [P]),
         "wg_finish": (C.c_int, [P]),
+        "wg_ctx_staging": (C.c_int, [P, C.POINTER(I32), C.POINTER(SZ)]),
         "wg_q4_sizes": (C.c_int, [I32, I32, I32, I32, C.POINTER(SZ), C.POINTER(SZ),
                                   C.POINTER(SZ)]),
         "wg_repack_q4_0": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),
