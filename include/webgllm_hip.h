@@ -545,6 +545,20 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
                    const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0,
                    int32_t max_keys, uint16_t *out, int32_t ldo, void *scratch,
                    size_t scratch_bytes, void *stream);
+/* wg_attn_decode with no scratch argument and no allocation of any kind:
+ * no counterpart in the reference. It is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The partial results go to a 16 MiB
+ * array built into the library, one per GPU, held until the process ends;
+ * a request needing more (wg_attn_scratch_bytes(M, heads, head_dim,
+ * max_keys) > 16 MiB, e.g. 8 rows of 32 heads of 128 past 8,064 keys) is
+ * rejected with WG_ERR_INVALID before anything runs. Every call on a GPU
+ * shares that array: calls that overlap on one GPU (other streams, other
+ * threads) race. Same results as wg_attn_decode, bit for bit. */
+int wg_attn_decode_noalloc(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *shape,
+                           const uint16_t *k_cache, const uint16_t *v_cache,
+                           const int32_t *pos0, int32_t max_keys, uint16_t *out, int32_t ldo,
+                           void *stream);
 
 /* ------------------------------------------------ short convolution */
 

@@ -16,6 +16,8 @@
 // running max (attendPanelCombine's online softmax) into half outputs.
 // The position comes from device memory so a captured graph replays at any
 // position; chunks past the last key leave at once.
+#include <mutex>
+
 #include "attn_core.h"
 #include "common.h"
 #include "dot.h"
@@ -653,6 +655,35 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_mfma_kernel(
 }
 
 }  // namespace
+
+// The no-allocation entry point's scratch (the chunks' partial results):
+// one array per GPU, held while the process lives. Every call on a GPU
+// shares it, so calls that overlap on one GPU race.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+// The device address of `scratch` on the current device, looked up once per
+// device (each GPU holds its own copy at its own address; the array's name
+// is no device address in host code).
+static int noalloc_scratch(void **out) {
+  static std::mutex mu;
+  static void *ptrs[64];
+  int dev = 0;
+  WG_HIP(hipGetDevice(&dev));
+  WG_REQUIRE(dev >= 0 && dev < 64, "no-allocation scratch: device %d", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(WG_ERR_DEVICE, "no-allocation scratch on device %d: %s", dev,
+                  hipGetErrorString(e));
+    ptrs[dev] = p;
+  }
+  *out = ptrs[dev];
+  return WG_OK;
+}
+
 }  // namespace wg
 
 using namespace wg;
@@ -788,6 +819,26 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
     attn_combine_kernel<128><<<cgrid, 256, 0, s>>>(partial, M, H, chunks, pos0, max_keys, out,
                                                    ldo);
   return launched("wg_attn_decode (combine)");
+}
+
+int wg_attn_decode_noalloc(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *sh,
+                           const uint16_t *k_cache, const uint16_t *v_cache,
+                           const int32_t *pos0, int32_t max_keys, uint16_t *out, int32_t ldo,
+                           void *stream) {
+  WG_REQUIRE(sh, "wg_attn_decode_noalloc: null argument");
+  WG_REQUIRE(M >= 1 && max_keys >= 1 && sh->heads >= 1 && sh->head_dim >= 1,
+             "wg_attn_decode_noalloc: %d rows, %d heads of %d, %d keys", M, sh->heads,
+             sh->head_dim, max_keys);
+  const size_t need = wg_attn_scratch_bytes(M, sh->heads, sh->head_dim, max_keys);
+  WG_REQUIRE(need <= NOALLOC_SCRATCH_BYTES,
+             "wg_attn_decode_noalloc: %d rows x %d heads of %d over %d keys need %zu bytes of "
+             "scratch; the built-in scratch holds %zu",
+             M, sh->heads, sh->head_dim, max_keys, need, NOALLOC_SCRATCH_BYTES);
+  void *p = nullptr;
+  int rc = noalloc_scratch(&p);
+  if (rc) return rc;
+  return wg_attn_decode(q, M, ldq, sh, k_cache, v_cache, pos0, max_keys, out, ldo, p,
+                        NOALLOC_SCRATCH_BYTES, stream);
 }
 
 }  // extern "C"

@@ -192,6 +192,8 @@ def load():
         "wg_attn_prefill": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32, P, I32, P]),
         "wg_attn_decode": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32, P, I32,
                                      P, SZ, P]),
+        "wg_attn_decode_noalloc": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32,
+                                             P, I32, P]),
         "wg_short_conv": (C.c_int, [P, I32, I32, I32, I32, P, P, P, P, P, I32, P]),
         "wg_conv_accept": (C.c_int, [P, I32, I32, I32, I32, P, P]),
         "wg_argmax_scratch_bytes": (SZ, [I32, I32]),
