@@ -534,12 +534,16 @@ int wg_attn_prefill(const float *q, int32_t M, int32_t ldq, const wg_attn_shape 
 /* Decode / verify attention (scores, attend, attendPanel + attendPanelCombine,
  * kernels.ts:2386-2579, :2803-3027): row m's query at position *pos0 + m
  * attends keys 0..*pos0 + m (causal) of its KV head; half output. max_keys
- * is how many rows the caches hold (the position is clamped to it);
- * (at most 16384); scratch holds wg_attn_scratch_bytes(M, heads, head_dim,
- * max_keys) bytes of per-chunk partial results; calls that share a scratch
- * must not overlap. Two launches: the chunks of 64 keys (a wave per query
- * when heads / kv_heads * M <= 8, else an LDS-staged workgroup per chunk),
- * then the online-softmax combine. */
+ * is how many rows the caches hold (the position is clamped to it).
+ * scratch holds wg_attn_scratch_bytes(M, heads, head_dim, max_keys) bytes:
+ * 256 bytes of counters, then per-chunk partial results. The counters must
+ * be zero before the first call (a zeroed allocation); every call leaves
+ * them zero. Calls that share a scratch must not overlap.
+ * With heads / kv_heads * M <= 8 (and kv_heads <= 64) it is one launch: a
+ * workgroup per (KV head, split of 64, 128 or 256 keys), a wave per query,
+ * the last workgroup of a KV head to finish combining its splits (max_keys
+ * up to 2^20). Otherwise two launches, up to 16384 keys: an LDS-staged
+ * workgroup per 64-key chunk, then the online-softmax combine. */
 size_t wg_attn_scratch_bytes(int32_t M, int32_t heads, int32_t head_dim, int32_t max_keys);
 int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *shape,
                    const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0,

@@ -116,10 +116,25 @@ def test_head_prep(hip, H, KV, hd, R, norm, pos0):
     assert not np.any(kcn[pos0 + M:])
 
 
+@pytest.fixture(params=["one-launch", "one-launch-1", "one-launch-2", "one-launch-4",
+                        "two-launch"])
+def decode_path(request):
+    """wg_attn_decode's forms: one launch (chunks a workgroup chosen, or
+    1, 2, 4), or chunks then a combine."""
+    from webgllm_amd import lib as L
+    old = (L.tuning_get("attn_fused"), L.tuning_get("attn_split_chunks"))
+    name = request.param
+    L.tuning_set("attn_fused", 0 if name == "two-launch" else 2)
+    L.tuning_set("attn_split_chunks", int(name[-1]) if name[-1].isdigit() else 0)
+    yield name
+    L.tuning_set("attn_fused", old[0])
+    L.tuning_set("attn_split_chunks", old[1])
+
+
 @pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (32, 8, 128), (32, 8, 64)])
 @pytest.mark.parametrize("M,pos0", [(1, 0), (1, 63), (1, 64), (1, 127), (1, 128), (1, 4095),
                                     (2, 129), (2, 4000), (5, 200), (5, 1500)])
-def test_attn_decode(hip, H, KV, hd, M, pos0):
+def test_attn_decode(hip, decode_path, H, KV, hd, M, pos0):
     from webgllm_amd import ops
     rng = np.random.default_rng(H + hd + M + pos0)
     ctx = 4096 + 8
@@ -142,10 +157,10 @@ def test_attn_decode(hip, H, KV, hd, M, pos0):
 
 
 @pytest.mark.parametrize("H,KV,hd,M", [(32, 8, 128, 1), (14, 2, 64, 1), (32, 8, 64, 5)])
-def test_attn_decode_ignores_rows_past_the_position(hip, H, KV, hd, M):
+def test_attn_decode_ignores_rows_past_the_position(hip, decode_path, H, KV, hd, M):
     """Cache rows past the position and a scratch that hold NaN bits (the
     kernels load them before they know the position) never reach the
-    output."""
+    output; only the counters at the scratch's start are zero."""
     from webgllm_amd import ops
     rng = np.random.default_rng(H + M)
     ctx, pos0 = 1024, 300
@@ -158,6 +173,7 @@ def test_attn_decode_ignores_rows_past_the_position(hip, H, KV, hd, M):
     q = (rng.standard_normal((M, H * hd)) / math.sqrt(hd) * 2).astype(np.float32)
     scratch = ops.attn_scratch(M, shape, ctx)
     scratch.fill_(0xff)
+    scratch[:256].zero_()
     got = _h(ops.attn_decode(_t(q), shape, _t(k.view(np.int16)), _t(v.view(np.int16)),
                              _t(np.array([pos0], np.int32)), scratch=scratch))
     assert np.isfinite(got).all()
@@ -166,9 +182,10 @@ def test_attn_decode_ignores_rows_past_the_position(hip, H, KV, hd, M):
         assert rel_l2(got[m], want) <= 1e-3
 
 
-def test_attn_decode_reuses_its_scratch(hip):
+def test_attn_decode_reuses_its_scratch(hip, decode_path):
     """One scratch across calls at changing positions and row counts (both
-    chunk kernels and the combine): every call matches the oracle."""
+    chunk kernels and the combine, or the one-launch form whose counters
+    each call leaves at zero): every call matches the oracle."""
     from webgllm_amd import ops
     H, KV, hd, ctx = 32, 8, 128, 2048
     shape = ops.attn_shape(H, KV, hd)
@@ -178,13 +195,38 @@ def test_attn_decode_reuses_its_scratch(hip):
     v = O.f32_to_h2(rng.standard_normal((ctx, kd)).astype(np.float32))
     kc, vc = _t(k.view(np.int16)), _t(v.view(np.int16))
     scratch = ops.attn_scratch(8, shape, ctx)
-    for pos0, M in [(5, 1), (700, 2), (129, 1), (2000, 5), (1500, 1), (31, 2)]:
+    for pos0, M in [(5, 1), (700, 2), (129, 1), (2000, 5), (1500, 1), (31, 2), (2040, 8),
+                    (64, 1)]:
         q = (rng.standard_normal((M, H * hd)) / math.sqrt(hd) * 2).astype(np.float32)
         got = _h(ops.attn_decode(_t(q), shape, kc, vc, _t(np.array([pos0], np.int32)),
                                  scratch=scratch))
         for m in range(M):
             want = O.attention_f64(q[m], k, v, H, KV, hd, pos0 + m + 1, kd)
             assert rel_l2(got[m], want) <= 1e-3, (pos0, M, m)
+
+
+@pytest.mark.parametrize("keys,M", [(32768, 1), (20000, 2), (65536, 1)])
+def test_attn_decode_long_context(hip, keys, M):
+    """Past the two-launch form's 16,384 keys: 8B-shape heads (32 over 8 of
+    128) over 20,000 to 65,536 cached keys in one launch, against the
+    float64 oracle; a second call at a smaller position with the same
+    scratch agrees too."""
+    from webgllm_amd import ops
+    H, KV, hd = 32, 8, 128
+    shape = ops.attn_shape(H, KV, hd)
+    rng = np.random.default_rng(keys + M)
+    kd = KV * hd
+    k = O.f32_to_h2(rng.standard_normal((keys, kd)).astype(np.float32))
+    v = O.f32_to_h2(rng.standard_normal((keys, kd)).astype(np.float32))
+    kc, vc = _t(k.view(np.int16)), _t(v.view(np.int16))
+    scratch = ops.attn_scratch(M, shape, keys)
+    for pos0 in (keys - M, keys // 3):
+        q = (rng.standard_normal((M, H * hd)) / math.sqrt(hd) * 2).astype(np.float32)
+        got = _h(ops.attn_decode(_t(q), shape, kc, vc, _t(np.array([pos0], np.int32)),
+                                 scratch=scratch))
+        for m in range(M):
+            want = O.attention_f64(q[m], k, v, H, KV, hd, pos0 + m + 1, kd)
+            assert rel_l2(got[m], want) <= 1e-3, (pos0, m)
 
 
 def test_attn_decode_single_key_and_uniform(hip):

@@ -236,6 +236,255 @@ __global__ __launch_bounds__(FGM * 64) void attn_tile_kernel(
   }
 }
 
+// Decode attention in one launch, for GM = G * M <= 8 queries per KV head.
+// Workgroup = (KV head kh, split s of 64 * NCH keys), one wave per query.
+// All of the split's K and V tiles go to LDS by direct loads issued at the
+// start (as in attn_tile_kernel); each wave then runs the online softmax
+// over the NCH chunks (attendPanel's running max and sum) and publishes its
+// (max, sum of weights, weighted values) with coherent stores (sc1: they
+// reach the point where every compute unit sees them, with no write-back of
+// the L2). Once those stores are done, one relaxed atomic per workgroup
+// counts the KV head's live splits in; the workgroup that completes the
+// count resets the counter to zero for the next call and does
+// attendPanelCombine for the KV head's queries, reading every partial at
+// once with coherent vector loads. No workgroup waits on another, so the
+// launch always drains.
+constexpr int MAX_KV_COUNTERS = 64;       // counters at the scratch's start
+constexpr int COUNTER_BYTES = MAX_KV_COUNTERS * 4;
+constexpr int MAX_FUSED_KEYS = 1 << 20;   // keys the one-launch form takes
+
+// A split's partial for one query: max, sum, 2 floats of padding, then the
+// HD weighted values, so that the values start 16-byte aligned.
+__host__ __device__ constexpr int split_row(int hd) { return hd + 4; }
+
+// Coherent (sc1) 16-byte store and loads; a loaded value is ready after
+// wait_vm and settle().
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef float f2v __attribute__((ext_vector_type(2)));
+__device__ inline void store_sc1(float *p, f4v v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ inline f4v load_sc1(const float *p) {
+  f4v v;
+  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ inline f2v load2_sc1(const float *p) {
+  f2v v;
+  asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+// Ties a value loaded by inline assembly to a wait issued before: its uses
+// come after this point.
+template <typename T>
+__device__ inline void settle(T &v) {
+  asm volatile("" : "+v"(v));
+}
+
+template <int HD, int NCH>
+__global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
+    const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
+    const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int splits,
+    int *counters, uint16_t *out, int ldo) {
+  constexpr int KP = HD / 8;       // 16-byte pieces of a row
+  constexpr int ROWB = HD * 2;     // bytes of a row
+  constexpr int TILE = WK * ROWB;  // bytes of a chunk's K (or V) tile
+  constexpr int RPI = 64 / KP;     // rows one 1 KB load instruction covers
+  constexpr int NI = WK / RPI;     // load instructions a tile
+  constexpr int QOFF = 2 * NCH * TILE;
+  constexpr int SPLIT = WK * NCH;  // keys a workgroup takes
+  constexpr int SR = split_row(HD);
+  static_assert(HD * 4 <= 1024, "a query fits one load instruction");
+  auto swz = [](int r) { return KP == 16 ? (r & 15) : ((r ^ (r >> 3)) & (KP - 1)); };
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int last;
+  const int kh = blockIdx.x % KV, s = blockIdx.x / KV;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;  // = G * M
+  const int G = H / KV, g = wave % G, m = wave / G;
+  const int j0 = s * SPLIT;  // < max_keys: s < splits
+  const int kvd = KV * HD;
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  if (lane < HD / 4)
+    dma16(q + (int64_t)m * ldq + (int64_t)(kh * G + g) * HD + lane * 4,
+          __builtin_amdgcn_readfirstlane(sbase + QOFF + wave * HD * 4));
+  // rows at or past max_keys do not exist: their lanes load row j0 again,
+  // and they are masked below like rows past the position
+  for (int i = wave; i < 2 * NI * NCH; i += nw) {
+    const int c = i / (2 * NI), ic = i % (2 * NI);
+    const bool is_v = ic >= NI;
+    const int ii = is_v ? ic - NI : ic;
+    const int r = ii * RPI + lane / KP;
+    const int slot = lane % KP;
+    const int piece = is_v ? slot : (slot ^ swz(r));
+    const int row = j0 + c * WK + r;
+    const int rr = row < max_keys ? row : j0;
+    dma16((is_v ? v_cache : k_cache) + (int64_t)rr * kvd + kh * HD + piece * 8,
+          __builtin_amdgcn_readfirstlane(sbase + c * 2 * TILE + (is_v ? TILE : 0) + ii * 1024));
+  }
+  const int pos0 = *pos0_dev;
+  const int n_keys = min(pos0 + M, max_keys);
+  // every load has landed before any wave leaves
+  wait_vm<0>();
+  if (n_keys <= 0) {  // no position in the cache: the output is zero
+    if (s == 0) {
+      uint16_t *o = out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD;
+      for (int d = lane; d < HD; d += 64) o[d] = 0;
+    }
+    return;
+  }
+  const int live = (n_keys + SPLIT - 1) / SPLIT;  // splits holding a visible key
+  if (s >= live) return;
+  barrier();
+
+  const float4 *ql = reinterpret_cast<const float4 *>(smem + QOFF + wave * HD * 4);
+  const int d0 = (lane % KP) * 8;
+  float mrun = -INFINITY, lrun = 0.0f;
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < NCH; c++) {
+    const int jc = j0 + c * WK;
+    if (jc >= n_keys) break;
+    const int nk = min(WK, n_keys - jc);
+    const unsigned char *kt = smem + c * 2 * TILE;
+    const unsigned char *krow = kt + lane * ROWB;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KP; i++) {
+      const uint4 kr = *reinterpret_cast<const uint4 *>(krow + ((i ^ swz(lane)) * 16));
+      const half2v a = as_h2(kr.x), b = as_h2(kr.y), cc = as_h2(kr.z), dd = as_h2(kr.w);
+      const float4 qa = ql[2 * i], qb = ql[2 * i + 1];
+      s0 = __builtin_fmaf(qa.x, (float)a.x, s0);
+      s1 = __builtin_fmaf(qa.y, (float)a.y, s1);
+      s2 = __builtin_fmaf(qa.z, (float)b.x, s2);
+      s3 = __builtin_fmaf(qa.w, (float)b.y, s3);
+      s0 = __builtin_fmaf(qb.x, (float)cc.x, s0);
+      s1 = __builtin_fmaf(qb.y, (float)cc.y, s1);
+      s2 = __builtin_fmaf(qb.z, (float)dd.x, s2);
+      s3 = __builtin_fmaf(qb.w, (float)dd.y, s3);
+    }
+    const bool vis = lane < nk && jc + lane <= pos0 + m;  // causal
+    const float sc = vis ? (s0 + s1) + (s2 + s3) : -INFINITY;
+    float cmax = sc;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) cmax = fmaxf(cmax, __shfl_xor(cmax, off, 64));
+    const float mnew = fmaxf(mrun, cmax);
+    if (mnew == -INFINITY) continue;  // nothing visible to this row yet
+    const float alpha = mrun == -INFINITY ? 0.0f : __expf(mrun - mnew);
+    const float e = vis ? __expf(sc - mnew) : 0.0f;
+    lrun = lrun * alpha + wave_sum(e);
+#pragma unroll
+    for (int t = 0; t < 8; t++) acc[t] *= alpha;
+    // weighted values: lane holds dims d0..d0+7 of rows lane / KP + RPI i;
+    // rows past the position may hold any bits: read as zero
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const int r = lane / KP + RPI * i;
+      uint4 vr = *reinterpret_cast<const uint4 *>(kt + TILE + r * ROWB + (lane % KP) * 16);
+      if (r >= nk) vr = make_uint4(0u, 0u, 0u, 0u);
+      const float w = __shfl(e, r, 64);
+      const uint32_t w4[4] = {vr.x, vr.y, vr.z, vr.w};
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const half2v hv = as_h2(w4[t]);
+        acc[2 * t] = __builtin_fmaf(w, (float)hv.x, acc[2 * t]);
+        acc[2 * t + 1] = __builtin_fmaf(w, (float)hv.y, acc[2 * t + 1]);
+      }
+    }
+    mrun = mnew;
+  }
+#pragma unroll
+  for (int off = KP; off < 64; off <<= 1)
+#pragma unroll
+    for (int t = 0; t < 8; t++) acc[t] += __shfl_xor(acc[t], off, 64);
+  const int qrow = m * H + kh * G + g;
+  float *po = partial + ((int64_t)qrow * splits + s) * SR;
+  if (lane < KP) {
+    store_sc1(po + 4 + d0, f4v{acc[0], acc[1], acc[2], acc[3]});
+    store_sc1(po + 8 + d0, f4v{acc[4], acc[5], acc[6], acc[7]});
+  } else if (lane == KP) {
+    store_sc1(po, f4v{mrun, lrun, 0.0f, 0.0f});
+  }
+  wait_vm<0>();  // this wave's coherent stores are done
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(counters + kh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           live - 1;
+  __syncthreads();
+  if (!last) return;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(counters + kh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // attendPanelCombine for this wave's query, BT splits at a time: lane
+  // (t, h) with t = lane / LPS and h = lane % LPS holds dims 4h..4h+3 of
+  // split t + TS i; lane t < BT holds split t's max and sum. Every load of
+  // a batch is issued before the wait.
+  constexpr int LPS = HD / 4;      // lanes a split's values take
+  constexpr int TS = 64 / LPS;     // splits one load instruction covers
+  constexpr int BT = 4096 / HD;    // splits a batch (16 value loads a lane)
+  constexpr int NL = BT / TS;      // value loads a lane issues a batch
+  const float *pr = partial + (int64_t)qrow * splits * SR;
+  const int th = lane / LPS, dh = (lane % LPS) * 4;
+  float gmax = -INFINITY, ltot = 0.0f;
+  f4v o = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t0 = 0; t0 < live; t0 += BT) {
+    const int n = min(BT, live - t0);
+    f4v v[NL];
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int t = t0 + min(th + TS * i, n - 1);
+      v[i] = load_sc1(pr + (int64_t)t * SR + 4 + dh);
+    }
+    f2v ml = load2_sc1(pr + (int64_t)(t0 + min(lane, n - 1)) * SR);
+    wait_vm<0>();
+    settle(ml);
+#pragma unroll
+    for (int i = 0; i < NL; i++) settle(v[i]);
+    const float mt = lane < n ? ml.x : -INFINITY;
+    float bmax = mt;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) bmax = fmaxf(bmax, __shfl_xor(bmax, off, 64));
+    const float nmax = fmaxf(gmax, bmax);
+    if (nmax == -INFINITY) continue;  // nothing visible yet
+    const float alpha = gmax == -INFINITY ? 0.0f : __expf(gmax - nmax);
+    const float w = mt == -INFINITY ? 0.0f : __expf(mt - nmax);
+    ltot = ltot * alpha + wave_sum(w * (lane < n ? ml.y : 0.0f));
+    o.x *= alpha;
+    o.y *= alpha;
+    o.z *= alpha;
+    o.w *= alpha;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int t = th + TS * i;  // < 64
+      // every lane takes part in the shuffle: a lane whose split is past
+      // the batch must not leave its source lanes inactive
+      const float ws = __shfl(w, t, 64);
+      const float wt = t < n ? ws : 0.0f;
+      o.x = __builtin_fmaf(wt, v[i].x, o.x);
+      o.y = __builtin_fmaf(wt, v[i].y, o.y);
+      o.z = __builtin_fmaf(wt, v[i].z, o.z);
+      o.w = __builtin_fmaf(wt, v[i].w, o.w);
+    }
+    gmax = nmax;
+  }
+  // lanes holding the same dims (different splits) add up
+#pragma unroll
+  for (int off = LPS; off < 64; off <<= 1) {
+    o.x += __shfl_xor(o.x, off, 64);
+    o.y += __shfl_xor(o.y, off, 64);
+    o.z += __shfl_xor(o.z, off, 64);
+    o.w += __shfl_xor(o.w, off, 64);
+  }
+  const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+  if (lane < LPS) {
+    uint16_t *op = out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD + dh;
+    const uint32_t lo = (uint32_t)half_bits(o.x * inv) | ((uint32_t)half_bits(o.y * inv) << 16);
+    const uint32_t hi = (uint32_t)half_bits(o.z * inv) | ((uint32_t)half_bits(o.w * inv) << 16);
+    *reinterpret_cast<uint2 *>(op) = make_uint2(lo, hi);
+  }
+}
+
 // The chunks' online-softmax combine (attendPanelCombine): one wave per
 // (query head h, row m, slice of 16 dims), 4 per workgroup, lane = chunk
 // (c, c + 64, ... up to 256 chunks). A lane loads its chunks' max, sum and
@@ -662,10 +911,18 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_mfma_kernel(
 constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)16 << 20;
 static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
 
+__global__ void clear_ints_kernel(int *p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
 // The device address of `scratch` on the current device, looked up once per
 // device (each GPU holds its own copy at its own address; the array's name
-// is no device address in host code).
-static int noalloc_scratch(void **out) {
+// is no device address in host code). The first lookup on a device also
+// clears the one-launch attention's counters at the array's start (static
+// storage starts zeroed; the clear, a kernel on the caller's stream, makes
+// sure of it without a memset).
+static int noalloc_scratch(void **out, hipStream_t stream) {
   static std::mutex mu;
   static void *ptrs[64];
   int dev = 0;
@@ -678,6 +935,9 @@ static int noalloc_scratch(void **out) {
     if (e != hipSuccess || !p)
       return fail(WG_ERR_DEVICE, "no-allocation scratch on device %d: %s", dev,
                   hipGetErrorString(e));
+    clear_ints_kernel<<<1, MAX_KV_COUNTERS, 0, stream>>>((int *)p, MAX_KV_COUNTERS);
+    int rc = launched("no-allocation scratch (counters)");
+    if (rc) return rc;
     ptrs[dev] = p;
   }
   *out = ptrs[dev];
@@ -719,7 +979,8 @@ int wg_head_prep(const float *qkv, int32_t M, int32_t ldq, const wg_attn_shape *
 
 size_t wg_attn_scratch_bytes(int32_t M, int32_t heads, int32_t head_dim, int32_t max_keys) {
   int64_t chunks = (max_keys + CHUNK - 1) / CHUNK;
-  return (size_t)M * heads * chunks * (head_dim + 2) * sizeof(float);
+  // rows of split_row(head_dim) floats hold either form's partials
+  return COUNTER_BYTES + (size_t)M * heads * chunks * split_row(head_dim) * sizeof(float);
 }
 
 int wg_attn_prefill(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *sh,
@@ -778,8 +1039,20 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
   WG_REQUIRE(M >= 1 && (H / KV) * M <= 64,
              "wg_attn_decode: %d rows x %d heads per KV head (at most 64)", M, H / KV);
   WG_REQUIRE(hd == 64 || hd == 128, "wg_attn_decode: head_dim %d (64 or 128)", hd);
-  WG_REQUIRE(max_keys >= M && max_keys <= MAX_CH * CHUNK,
-             "wg_attn_decode: max_keys %d (rows %d; at most %d)", max_keys, M, MAX_CH * CHUNK);
+  // The one-launch form's last-arriver combine costs about as much as the
+  // second launch it saves at 2048 cached keys, more past that (measured at
+  // 4096 keys: 14.3 us against 8.4 + 4.7), less below: it is taken up to
+  // 1024 keys and past the two-launch form's 16384 (attn_fused 2 always
+  // takes it, 0 never).
+  const int fused_knob = tuning("attn_fused");
+  const bool fits = (H / KV) * M <= FGM && KV <= MAX_KV_COUNTERS;
+  const bool fused = fits && (fused_knob == 2 ||
+                              (fused_knob == 1 && (max_keys <= 1024 || max_keys > MAX_CH * CHUNK)));
+  // the one-launch form combines any number of splits; the two-launch
+  // combine holds MAX_CH chunks
+  const int key_cap = fused ? MAX_FUSED_KEYS : MAX_CH * CHUNK;
+  WG_REQUIRE(max_keys >= M && max_keys <= key_cap,
+             "wg_attn_decode: max_keys %d (rows %d; at most %d)", max_keys, M, key_cap);
   WG_REQUIRE(ldq >= H * hd && ldo >= H * hd, "wg_attn_decode: strides too small");
   WG_REQUIRE(((uintptr_t)out & 15) == 0 && ldo % 8 == 0,
              "wg_attn_decode: the output must be 16-byte aligned with a stride of 8k halves");
@@ -787,8 +1060,42 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
              "wg_attn_decode: scratch of %zu bytes, %zu needed", scratch_bytes,
              wg_attn_scratch_bytes(M, H, hd, max_keys));
   hipStream_t s = as_stream(stream);
-  float *partial = (float *)scratch;
+  int *counters = (int *)scratch;
+  float *partial = (float *)((char *)scratch + COUNTER_BYTES);
   const int chunks = (max_keys + CHUNK - 1) / CHUNK;
+  if (fused) {
+    // one launch: 64 * nch keys a workgroup, the smallest nch (1, 2, 4) that
+    // keeps the grid to about one workgroup a compute unit
+    int nch = tuning("attn_split_chunks");
+    if (nch == 3) nch = 4;
+    if (!nch) {
+      const int cus = persistent_grid(1 << 30, 1);
+      nch = KV * chunks <= cus ? 1 : KV * ((chunks + 1) / 2) <= cus ? 2 : 4;
+    }
+    const int splits = (chunks + nch - 1) / nch;
+    const size_t lds = (size_t)2 * nch * WK * hd * 2 + (size_t)FGM * hd * 4;
+    dim3 grid((unsigned)(KV * splits));
+    const unsigned threads = 64 * (H / KV) * M;
+#define WG_SPLIT_LAUNCH(HDV, NCHV)                                                              \
+  do {                                                                                          \
+    int rc_ = raise_lds((const void *)attn_split_kernel<HDV, NCHV>, (int)lds);                   \
+    if (rc_) return rc_;                                                                        \
+    attn_split_kernel<HDV, NCHV><<<grid, threads, lds, s>>>(q, ldq, M, H, KV, k_cache, v_cache,  \
+                                                           pos0, max_keys, partial, splits,     \
+                                                           counters, out, ldo);                 \
+  } while (0)
+    if (hd == 64) {
+      if (nch == 1) WG_SPLIT_LAUNCH(64, 1);
+      else if (nch == 2) WG_SPLIT_LAUNCH(64, 2);
+      else WG_SPLIT_LAUNCH(64, 4);
+    } else {
+      if (nch == 1) WG_SPLIT_LAUNCH(128, 1);
+      else if (nch == 2) WG_SPLIT_LAUNCH(128, 2);
+      else WG_SPLIT_LAUNCH(128, 4);
+    }
+#undef WG_SPLIT_LAUNCH
+    return launched("wg_attn_decode");
+  }
   if ((H / KV) * M <= FGM) {
     dim3 grid((unsigned)(KV * chunks));
     if (hd == 64)
@@ -835,7 +1142,7 @@ int wg_attn_decode_noalloc(const float *q, int32_t M, int32_t ldq, const wg_attn
              "scratch; the built-in scratch holds %zu",
              M, sh->heads, sh->head_dim, max_keys, need, NOALLOC_SCRATCH_BYTES);
   void *p = nullptr;
-  int rc = noalloc_scratch(&p);
+  int rc = noalloc_scratch(&p, as_stream(stream));
   if (rc) return rc;
   return wg_attn_decode(q, M, ldq, sh, k_cache, v_cache, pos0, max_keys, out, ldo, p,
                         NOALLOC_SCRATCH_BYTES, stream);
