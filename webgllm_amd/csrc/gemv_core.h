@@ -151,4 +151,106 @@ __device__ inline void accumulate_unit(const Unit<ZK, NB> &u, const uint4 (&a)[M
   }
 }
 
+// The unit of row group g at blocks bj[j] (every index in range: the caller
+// clamps), loaded with no branches.
+template <int ZK, int NB>
+__device__ inline void load_unit_at(Unit<ZK, NB> &u, const uint4 *__restrict__ quants,
+                                    const uint16_t *__restrict__ scales,
+                                    const void *__restrict__ zeros, int g, int B,
+                                    const int (&bj)[NB]) {
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const int64_t si = ((int64_t)g * B + bj[j]) * 4;
+    const uint4 *qp = quants + si;
+    u.q[j][0] = qp[0];
+    u.q[j][1] = qp[1];
+    u.q[j][2] = qp[2];
+    u.q[j][3] = qp[3];
+    u.sc[j] = *reinterpret_cast<const uint2 *>(scales + si);
+    if constexpr (ZK == WG_ZERO_U8)
+      u.zr[j].x = *reinterpret_cast<const uint32_t *>((const uint8_t *)zeros + si);
+    if constexpr (ZK == WG_ZERO_F16)
+      u.zr[j] = *reinterpret_cast<const uint2 *>((const uint16_t *)zeros + si);
+  }
+}
+
+// A block's 32 activations paired as the nibbles are unpacked below: for
+// each of its halves (elements 0..15, then 16..31) and dword i < 4, even
+// (a_4i, a_4i+2) and odd (a_4i+1, a_4i+3).
+struct PairedActs {
+  uint32_t e[2][4], o[2][4];
+};
+
+__device__ inline void pair_acts(const uint4 (&a)[4], PairedActs &p) {
+  const uint32_t d[16] = {a[0].x, a[0].y, a[0].z, a[0].w, a[1].x, a[1].y, a[1].z, a[1].w,
+                          a[2].x, a[2].y, a[2].z, a[2].w, a[3].x, a[3].y, a[3].z, a[3].w};
+#pragma unroll
+  for (int h = 0; h < 2; h++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      p.e[h][i] = __builtin_amdgcn_perm(d[8 * h + 2 * i + 1], d[8 * h + 2 * i], 0x05040100u);
+      p.o[h][i] = __builtin_amdgcn_perm(d[8 * h + 2 * i + 1], d[8 * h + 2 * i], 0x07060302u);
+    }
+}
+
+// v_perm_b32 selector: bytes 1 and 3 into the low byte of each half.
+constexpr uint32_t SEL13 = 0x0c030c01u;
+
+// sum q a over a block (times 2^-24) from one 16-byte block row: nibble
+// dword i holds weights 4i..4i+3 low and 16+4i.. high; the pairs (q_4i,
+// q_4i+2) take one mask, (q_4i+1, q_4i+3) a permute and a mask, and meet
+// the activations paired by pair_acts.
+__device__ inline float block_dot_paired(const uint4 &q, const PairedActs &p) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t t = __builtin_amdgcn_perm(0u, w[i], SEL13);
+    lo = dot2(w[i] & LO4, p.e[0][i], lo);
+    hi = dot2(w[i] & HI4, p.e[1][i], hi);
+    lo = dot2(t & LO4, p.o[0][i], lo);
+    hi = dot2(t & HI4, p.o[1][i], hi);
+  }
+  return __builtin_fmaf(hi, 0.0625f, lo);
+}
+
+// acc[r][m] += the unit's 4 rows times token m's paired activations (units
+// of 2^-24), blocks whose lane has no block (live[j] false) adding zero.
+template <int M, int ZK, int NB>
+__device__ inline void accumulate_unit_paired(const Unit<ZK, NB> &u,
+                                              const PairedActs (&a)[M][NB],
+                                              const float (&sa)[M][NB], const bool (&live)[NB],
+                                              float (&acc)[4][M]) {
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    float d[4] = {(float)as_h2(u.sc[j].x).x, (float)as_h2(u.sc[j].x).y,
+                  (float)as_h2(u.sc[j].y).x, (float)as_h2(u.sc[j].y).y};
+#pragma unroll
+    for (int r = 0; r < 4; r++) d[r] = live[j] ? d[r] : 0.0f;
+    float z[4];
+    if constexpr (ZK == WG_ZERO_8) {
+      z[0] = z[1] = z[2] = z[3] = 8.0f;
+    } else if constexpr (ZK == WG_ZERO_U8) {
+      uint32_t v = u.zr[j].x;
+      z[0] = (float)(v & 0xffu);
+      z[1] = (float)((v >> 8) & 0xffu);
+      z[2] = (float)((v >> 16) & 0xffu);
+      z[3] = (float)(v >> 24);
+    } else {
+      z[0] = (float)as_h2(u.zr[j].x).x;
+      z[1] = (float)as_h2(u.zr[j].x).y;
+      z[2] = (float)as_h2(u.zr[j].y).x;
+      z[3] = (float)as_h2(u.zr[j].y).y;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+      for (int m = 0; m < M; m++) {
+        float v = block_dot_paired(u.q[j][r], a[m][j]);
+        v = __builtin_fmaf(-z[r], sa[m][j], v);
+        acc[r][m] = __builtin_fmaf(d[r], v, acc[r][m]);
+      }
+  }
+}
+
 }  // namespace wg

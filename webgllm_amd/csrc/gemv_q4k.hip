@@ -364,6 +364,222 @@ int launch_kstream_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y
                  : launch_kstream<M, 2, 4>(w, x, ldx, y, ldy, ep, s);
 }
 
+// ---------------------------------------------------------------------------
+// Streaming kernel with every lane on all 4 rows of a row group, for 1 or 2
+// tokens and K of 16 to 64 super-blocks (K split into KS parts of at most
+// 16): lane = (super-block sl of 16, 32-byte chunk c of 4), so a lane takes
+// chunk c (the low nibbles of sub-block 2c, the high nibbles of 2c + 1) of
+// one super-block of the part for the group's 4 rows. Its activations and
+// their sums are loaded once; row groups are streamed through two register
+// sets (the loop unrolled by 2, so the prefetched records are never
+// copied). Scales are rebuilt per row and sub-block without branches, and a
+// dword of nibble bytes becomes its 4 pairs in 5 instructions: pairs
+// (w_l, w_l+2) with one mask, (w_l+1, w_l+3) with one permute and a mask,
+// the lane's activations paired to match once.
+struct Q4kRows {
+  uint4 h[4];     // the 4 rows' headers: d | dmin, 12 bytes of 6-bit scales and mins
+  uint4 q[4][2];  // the 4 rows' 32 nibble bytes of chunk c
+};
+
+__device__ inline void load_q4k_rows(Q4kRows &u, const uint8_t *__restrict__ quants, int g,
+                                     int S, int s, int c) {
+  const uint8_t *rec = quants + ((int64_t)g * S + s) * 4 * 144;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const uint8_t *p = rec + r * 144;
+    u.h[r] = *reinterpret_cast<const uint4 *>(p);
+    u.q[r][0] = *reinterpret_cast<const uint4 *>(p + 16 + 32 * c);
+    u.q[r][1] = *reinterpret_cast<const uint4 *>(p + 32 + 32 * c);
+  }
+}
+
+// d' and d' z' of sub-blocks 2c and 2c + 1 of one row (packQ4_K's rounding,
+// src/repack.ts:127-163; z' through v_rcp_f32 as sub_scale above), without
+// branches: the 6-bit fields are picked by selects, the constant sub-block
+// (d' = 0) by a select.
+__device__ inline SubScales decode_rows(const uint4 &h, int c) {
+  const float d = (float)as_h2(h.x).x, dmin = (float)as_h2(h.x).y;
+  const int sh = (c & 1) * 16;
+  const uint32_t y2 = h.y >> sh, z2 = h.z >> sh, w2 = h.w >> sh;
+  const bool hi = c >= 2;
+  // sub-blocks 0..3: scale = sc[j] & 63, min = sc[j + 4] & 63; 4..7: the low
+  // (scale) or high (min) nibble of sc[j + 4] under the top 2 bits of sc[j - 4]
+  // (scale) or sc[j] (min)
+  const uint32_t slo = hi ? w2 : y2, mlo = hi ? (w2 >> 4) : z2;
+  const uint32_t top = hi ? 0xfu : 0x3fu;
+  const uint32_t s0 = (slo & top) | (hi ? ((y2 >> 2) & 0x30u) : 0u);
+  const uint32_t s1 = ((slo >> 8) & top) | (hi ? ((y2 >> 10) & 0x30u) : 0u);
+  const uint32_t m0 = (mlo & top) | (hi ? ((z2 >> 2) & 0x30u) : 0u);
+  const uint32_t m1 = ((mlo >> 8) & top) | (hi ? ((z2 >> 10) & 0x30u) : 0u);
+  SubScales o;
+  const float sc[2] = {(float)s0, (float)s1}, mn[2] = {(float)m0, (float)m1};
+  float dq[2], dz[2];
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    dq[k] = (float)(_Float16)(d * sc[k]);  // exact product, rounded once
+    const float mins = dmin * mn[k];       // exact
+    const float z = (float)(_Float16)(mins * __builtin_amdgcn_rcpf(dq[k]));
+    const float cz = -15.0f * (float)(_Float16)(-mins * (1.0f / 15.0f));
+    dz[k] = dq[k] != 0.0f ? dq[k] * z : cz;
+  }
+  o.d0 = dq[0];
+  o.dz0 = dz[0];
+  o.d1 = dq[1];
+  o.dz1 = dz[1];
+  return o;
+}
+
+// v_perm_b32 selector: bytes 1 and 3 into the low byte of each half.
+constexpr uint32_t SEL13 = 0x0c030c01u;
+
+template <int M, int KS, int MODE>
+__global__ __launch_bounds__(256) void gemv_q4k_rows_kernel(
+    const uint8_t *__restrict__ quants, const uint16_t *__restrict__ x, int ldx,
+    float *__restrict__ y, int ldy, const wg_epilogue e, int G, int S) {
+  constexpr int RGW = 4 / KS;  // row groups a workgroup takes at a time
+  __shared__ float red[2][4][4 * M];
+  __shared__ float nred[4 * M];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int part = wave % KS, slot = wave / KS;
+  const int c = lane & 3, sl = lane >> 2;
+  const int SP = (S + KS - 1) / KS;
+  const int s_raw = part * SP + sl;
+  const bool s_live = sl < SP && s_raw < S;
+  const int s = s_live ? s_raw : 0;  // idle lanes read super-block 0 and add zeros
+  const int stride = gridDim.x * RGW;
+  const int g_first = blockIdx.x * RGW + slot;
+
+  Q4kRows A, B;
+  load_q4k_rows(A, quants, min(g_first, G - 1), S, s, c);
+  const int pos0 = epi_pos0<MODE>(e);
+  EpiPre pnext = {};
+  if (part == 0) epi_prefetch<M, MODE>(e, g_first, G, pos0, pnext);
+
+  // This lane's 64 activations (sub-block 2c, then 2c + 1) paired as the
+  // nibbles come: even (a_4i, a_4i+2) and odd (a_4i+1, a_4i+3); their sums.
+  uint32_t ae[M][2][8], ao[M][2][8];
+  float sa[M][2];
+#pragma unroll
+  for (int m = 0; m < M; m++) {
+    const uint4 *xp = reinterpret_cast<const uint4 *>(x + (int64_t)m * ldx + s * 256 + 64 * c);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      uint4 a4[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        a4[i] = s_live ? xp[4 * k + i] : make_uint4(0u, 0u, 0u, 0u);
+      const uint32_t dw[16] = {a4[0].x, a4[0].y, a4[0].z, a4[0].w, a4[1].x, a4[1].y,
+                               a4[1].z, a4[1].w, a4[2].x, a4[2].y, a4[2].z, a4[2].w,
+                               a4[3].x, a4[3].y, a4[3].z, a4[3].w};
+      float t = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        ae[m][k][i] = __builtin_amdgcn_perm(dw[2 * i + 1], dw[2 * i], 0x05040100u);
+        ao[m][k][i] = __builtin_amdgcn_perm(dw[2 * i + 1], dw[2 * i], 0x07060302u);
+        t = dot2(dw[2 * i], ONES, t);
+        t = dot2(dw[2 * i + 1], ONES, t);
+      }
+      sa[m][k] = t * 0x1p-24f;
+    }
+  }
+  float scale[M];
+  input_scales_wg<M, 4>(e, scale, nred);
+
+  // one row group: the 4 rows' sums for each token, then the epilogue
+  auto step = [&](const Q4kRows &u, int g, int it, const EpiPre &pe) {
+    float acc[4][M];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const SubScales sc = decode_rows(u.h[r], c);
+      const uint32_t w[8] = {u.q[r][0].x, u.q[r][0].y, u.q[r][0].z, u.q[r][0].w,
+                             u.q[r][1].x, u.q[r][1].y, u.q[r][1].z, u.q[r][1].w};
+      uint32_t le[8], lo[8], he[8], ho[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t p = __builtin_amdgcn_perm(0u, w[i], SEL13);
+        le[i] = w[i] & LO4;
+        he[i] = w[i] & HI4;
+        lo[i] = p & LO4;
+        ho[i] = p & HI4;
+      }
+#pragma unroll
+      for (int m = 0; m < M; m++) {
+        float l = 0.0f, h = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          l = dot2(le[i], ae[m][0][i], l);
+          h = dot2(he[i], ae[m][1][i], h);
+          l = dot2(lo[i], ao[m][0][i], l);
+          h = dot2(ho[i], ao[m][1][i], h);
+        }
+        float v = sc.d0 * l;
+        v = __builtin_fmaf(-sc.dz0, sa[m][0], v);
+        v = __builtin_fmaf(sc.d1 * 0.0625f, h, v);
+        v = __builtin_fmaf(-sc.dz1, sa[m][1], v);
+        acc[r][m] = v;
+      }
+    }
+    const int row = wave_sum4_row();
+    float tot[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) tot[m] = wave_sum4(acc[0][m], acc[1][m], acc[2][m], acc[3][m]);
+    if constexpr (KS > 1) {
+      if ((lane & 15) == 0 && part > 0)
+#pragma unroll
+        for (int m = 0; m < M; m++) red[it][wave][row * M + m] = tot[m];
+      __syncthreads();
+      if (part == 0)
+#pragma unroll
+        for (int m = 0; m < M; m++)
+#pragma unroll
+          for (int p = 1; p < KS; p++) tot[m] += red[it][wave + p][row * M + m];
+    }
+    if (part == 0) finish<M, MODE>(e, g, G, tot, scale, y, ldy, pe, pos0);
+  };
+
+  // g0 is the same for every wave of the workgroup, so all of them run the
+  // same iterations (the reductions' barriers); g >= G is an idle slot
+  for (int g0 = blockIdx.x * RGW, g = g_first; g0 < G; g0 += 2 * stride, g += 2 * stride) {
+    load_q4k_rows(B, quants, min(g + stride, G - 1), S, s, c);
+    EpiPre pe = pnext;
+    if (part == 0) epi_prefetch<M, MODE>(e, g + stride, G, pos0, pnext);
+    step(A, g, 0, pe);
+    if (g0 + stride >= G) break;
+    load_q4k_rows(A, quants, min(g + 2 * stride, G - 1), S, s, c);
+    pe = pnext;
+    if (part == 0) epi_prefetch<M, MODE>(e, g + 2 * stride, G, pos0, pnext);
+    step(B, g + stride, 1, pe);
+  }
+}
+
+template <int M, int KS>
+int launch_rows(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
+                const wg_epilogue &e, hipStream_t s) {
+  const int G = w->N / 4, S = w->K / 256;
+  constexpr int RGW = 4 / KS;
+  const int grid = persistent_grid((G + RGW - 1) / RGW, tuning("q4k_wg_per_cu"));
+  auto q = (const uint8_t *)w->quants;
+  if (e.mode == WG_EPI_SWIGLU)
+    gemv_q4k_rows_kernel<M, KS, WG_EPI_SWIGLU><<<grid, 256, 0, s>>>(q, x, ldx, y, ldy, e, G, S);
+  else if (e.mode == WG_EPI_ROPE_KV)
+    gemv_q4k_rows_kernel<M, KS, WG_EPI_ROPE_KV><<<grid, 256, 0, s>>>(q, x, ldx, y, ldy, e, G, S);
+  else
+    gemv_q4k_rows_kernel<M, KS, WG_EPI_STORE><<<grid, 256, 0, s>>>(q, x, ldx, y, ldy, e, G, S);
+  return launched("wg_q4_gemv (Q4_K)");
+}
+
+// K of 16 to 64 super-blocks in parts of at most 16; -1 for other shapes.
+template <int M>
+int launch_rows_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
+                  const wg_epilogue &ep, hipStream_t s) {
+  const int S = w->K / 256;
+  if (S < 16 || S > 64) return -1;
+  const int ks = S <= 16 ? 1 : S <= 32 ? 2 : 4;
+  if (ks == 1) return launch_rows<M, 1>(w, x, ldx, y, ldy, ep, s);
+  if (ks == 2) return launch_rows<M, 2>(w, x, ldx, y, ldy, ep, s);
+  return launch_rows<M, 4>(w, x, ldx, y, ldy, ep, s);
+}
+
 template <int M>
 int launch_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ldy,
              const wg_epilogue &e, hipStream_t s) {
@@ -382,6 +598,11 @@ int launch_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, int ld
 
 int launch_gemv_q4k(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y, int ldy,
                     const wg_epilogue &ep, hipStream_t s) {
+  if (M <= 2 && tuning("q4k_rows")) {
+    int rc = M == 1 ? launch_rows_m<1>(w, x, ldx, y, ldy, ep, s)
+                    : launch_rows_m<2>(w, x, ldx, y, ldy, ep, s);
+    if (rc != -1) return rc;
+  }
   if (M <= 2) {
     int rc = M == 1 ? launch_kstream_m<1>(w, x, ldx, y, ldy, ep, s)
                     : launch_kstream_m<2>(w, x, ldx, y, ldy, ep, s);

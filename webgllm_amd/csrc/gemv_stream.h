@@ -15,10 +15,14 @@ namespace {
 // Streaming variant (decode, and verify batches of up to 8 tokens): persistent
 // workgroups of 4 waves. The K range is split into KS parts (a wave per
 // part, KS waves per row group, reduced through LDS); lane l of a part
-// takes its blocks l and l + 64 (NB of them), whose activations and block
-// sums it loads once into registers: they are the same for every row
-// group. Row groups are streamed: the next row group's nibbles, scales and
-// zero points are loaded before the current one is computed.
+// takes its blocks l and l + 64 (NB of them), whose activations (paired as
+// the nibbles unpack, see pair_acts) and block sums it loads once into
+// registers: they are the same for every row group. Row groups are
+// streamed through two register sets, the loop unrolled by 2, so the next
+// row group's nibbles, scales and zero points are in flight while the
+// current one is computed and are never copied. Loads past the matrix
+// read an in-range row group or block (a clamped index): a row group past
+// the end is not stored, a block past the part adds zero.
 template <int M, int ZK, int NB, int KS, int MODE>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(
     const uint4 *__restrict__ quants, const uint16_t *__restrict__ scales,
@@ -32,56 +36,57 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
   const int BP = (B + KS - 1) / KS;
   const int b0 = part * BP + lane;
   const int b_end = min(B, (part + 1) * BP);
+  int bj[NB];
+  bool live[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    live[j] = b0 + 64 * j < b_end;
+    bj[j] = live[j] ? b0 + 64 * j : 0;
+  }
 
   // The first row group's weights go out first: they need no input, and
   // everything after them (activations, sums, the norm's parts) overlaps
   // their flight.
   const int stride = gridDim.x * RGW;
-  int g = blockIdx.x * RGW + slot;
-  Unit<ZK, NB> next;
-  load_unit<ZK, NB>(next, quants, scales, zeros, g, B, b0, b_end, g < G);
+  const int g_first = blockIdx.x * RGW + slot;
+  Unit<ZK, NB> U0, U1;
+  load_unit_at<ZK, NB>(U0, quants, scales, zeros, min(g_first, G - 1), B, bj);
   // and the first row group's epilogue operands (the waves that finish)
   const int pos0 = epi_pos0<MODE>(e);
   EpiPre pnext = {};
-  if (part == 0) epi_prefetch<M, MODE>(e, g, G, pos0, pnext);
+  if (part == 0) epi_prefetch<M, MODE>(e, g_first, G, pos0, pnext);
 
-  // This lane's activations and their block sums (times 2^-24), once.
-  uint4 a[M][NB][4];
+  // This lane's activations, paired, and their block sums (times 2^-24), once.
+  PairedActs a[M][NB];
   float sa[M][NB];
 #pragma unroll
   for (int m = 0; m < M; m++)
 #pragma unroll
     for (int j = 0; j < NB; j++) {
-      int b = b0 + 64 * j;
-      if (b < b_end) {
-        const uint4 *xp = reinterpret_cast<const uint4 *>(x + (int64_t)m * ldx + b * 32);
-        a[m][j][0] = xp[0];
-        a[m][j][1] = xp[1];
-        a[m][j][2] = xp[2];
-        a[m][j][3] = xp[3];
+      uint4 raw[4];
+      if (live[j]) {
+        const uint4 *xp = reinterpret_cast<const uint4 *>(x + (int64_t)m * ldx + bj[j] * 32);
+        raw[0] = xp[0];
+        raw[1] = xp[1];
+        raw[2] = xp[2];
+        raw[3] = xp[3];
       } else {
-        a[m][j][0] = a[m][j][1] = a[m][j][2] = a[m][j][3] = make_uint4(0u, 0u, 0u, 0u);
+        raw[0] = raw[1] = raw[2] = raw[3] = make_uint4(0u, 0u, 0u, 0u);
       }
+      sa[m][j] = block_sum(raw) * 0x1p-24f;
+      pair_acts(raw, a[m][j]);
     }
   float scale[M];
   input_scales_wg<M, 4>(e, scale, nred);
-#pragma unroll
-  for (int m = 0; m < M; m++)
-#pragma unroll
-    for (int j = 0; j < NB; j++) sa[m][j] = block_sum(a[m][j]) * 0x1p-24f;
 
-  int it = 0;
-  for (int g0 = blockIdx.x * RGW; g0 < G; g0 += stride, g += stride, it ^= 1) {
-    Unit<ZK, NB> u = next;
-    load_unit<ZK, NB>(next, quants, scales, zeros, g + stride, B, b0, b_end, g + stride < G);
-    const EpiPre pe = pnext;
-    if (part == 0) epi_prefetch<M, MODE>(e, g + stride, G, pos0, pnext);
+  // one row group: the 4 rows' sums for each token, reduced, then the epilogue
+  auto step = [&](const Unit<ZK, NB> &u, int g, int it, const EpiPre &pe) {
     float acc[4][M];
 #pragma unroll
     for (int r = 0; r < 4; r++)
 #pragma unroll
       for (int m = 0; m < M; m++) acc[r][m] = 0.0f;
-    accumulate_unit<M, ZK, NB>(u, a, sa, acc);
+    accumulate_unit_paired<M, ZK, NB>(u, a, sa, live, acc);
     const int row = wave_sum4_row();
     float tot[M];
 #pragma unroll
@@ -100,6 +105,20 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
           for (int p = 1; p < KS; p++) tot[m] += red[it][wave + p][row * M + m];
     }
     if (part == 0) finish<M, MODE>(e, g, G, tot, scale, y, ldy, pe, pos0);
+  };
+
+  // g0 is the same for every wave of the workgroup, so all of them run the
+  // same iterations (the reductions' barriers); g >= G is an idle slot
+  for (int g0 = blockIdx.x * RGW, g = g_first; g0 < G; g0 += 2 * stride, g += 2 * stride) {
+    load_unit_at<ZK, NB>(U1, quants, scales, zeros, min(g + stride, G - 1), B, bj);
+    EpiPre pe = pnext;
+    if (part == 0) epi_prefetch<M, MODE>(e, g + stride, G, pos0, pnext);
+    step(U0, g, 0, pe);
+    if (g0 + stride >= G) break;
+    load_unit_at<ZK, NB>(U0, quants, scales, zeros, min(g + 2 * stride, G - 1), B, bj);
+    pe = pnext;
+    if (part == 0) epi_prefetch<M, MODE>(e, g + 2 * stride, G, pos0, pnext);
+    step(U1, g + stride, 1, pe);
   }
 }
 

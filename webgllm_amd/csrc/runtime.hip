@@ -71,7 +71,8 @@ struct Knob {
 static Knob g_knobs[] = {
     {"gemv_wg_per_cu", 2, 1, 16},        // persistent row-group GEMV workgroups per CU
     {"gemv_wg_per_cu_wide", 8, 1, 16},   // the same for matrices of 16384+ row groups
-    {"q4k_wg_per_cu", 2, 1, 16},         // persistent Q4_K GEMV workgroups per CU
+    {"q4k_wg_per_cu", 3, 1, 16},         // persistent Q4_K GEMV workgroups per CU
+    {"q4k_rows", 1, 0, 1},               // Q4_K GEMV: every lane on a row group's 4 rows (0: 2 rows)
     {"wide_wg_per_cu", 2, 1, 16},        // the same for 8-bit and Q6_K GEMVs
     {"gemv_min_waves", 8192, 0, 1 << 20},  // split K within a workgroup below this
     {"gemv_few_stream", 1, 0, 1},        // 3 to 8 tokens on the streaming kernel (0: row groups)
