@@ -580,6 +580,42 @@ int wg_short_conv(const float *bcx, int32_t M, int32_t D, int32_t ldb, int32_t W
 int wg_conv_accept(const float *prefixes, int32_t kept, int32_t rows, int32_t D, int32_t W,
                    float *state, void *stream);
 
+/* ---------------------------------------------- speculative verify on the device
+ * The reference's verify loop (src/handler.ts:1811-1887) reads each batch's
+ * picks back and decides on the host; these two calls take the decision on
+ * the device, so that a verify step (drafts in, forward of the batch,
+ * greedy picks, accept, rollback) replays as one captured graph. */
+
+/* A conv layer's rollback operands: prefixes [rows][width - 1][dim] (the
+ * state after each prefix of the batch, wg_short_conv) and its state
+ * [width - 1][dim]. */
+typedef struct {
+  float *prefixes;
+  float *state;
+  int32_t dim;
+  int32_t width;
+} wg_conv_state;
+
+/* Engine.accept after a verify batch (engine.ts:8063-8086) with the
+ * handler's rule for what to keep (handler.ts:1811-1887): the batch's
+ * inputs are ids[0 .. rows) (ids[1 ..] the drafts) and picks[0 .. rows)
+ * its greedy picks; kept = 1 + the longest prefix i with picks[i] ==
+ * ids[i + 1]. Then every conv layer's state := its prefix kept - 1 (convs:
+ * a device array of n_conv wg_conv_state, each (width - 1) * dim <=
+ * max_state floats), hist[*pos + 1 + i] = picks[i] for i < kept (within
+ * hist_len), kept_log[*cursor] = kept (within log_len), *cursor += 1,
+ * *pos += kept, ids[0] = picks[kept - 1]. One launch. */
+int wg_verify_accept(const int32_t *picks, int32_t rows, const wg_conv_state *convs,
+                     int32_t n_conv, int32_t max_state, int32_t *pos, int32_t *ids,
+                     int32_t *hist, int32_t hist_len, int32_t *kept_log, int32_t log_len,
+                     int32_t *cursor, void *stream);
+/* The drafts of a verify step from a device table (the reference's draft
+ * lookup, src/draft.ts:15-45, runs on the host; a table lets a whole run
+ * of steps replay without it): ids[1 .. rows) := table row *cursor of
+ * rows - 1 ids (the last row once the cursor is past n_steps). */
+int wg_verify_drafts(int32_t *ids, int32_t rows, const int32_t *table, int32_t n_steps,
+                     const int32_t *cursor, void *stream);
+
 /* ------------------------------------------------- Gated DeltaNet */
 
 /* A Gated DeltaNet layer's shape (Qwen3.5's linear attention,

@@ -327,3 +327,55 @@ def test_sampled_generate_without_top_k_reads_the_row(hip):
     assert d_gpu.ids.size == d_host.ids.size == 40
     assert np.array_equal(d_gpu.ids[a], d_host.ids[b])
     assert np.array_equal(d_gpu.p[a], d_host.p[b])
+
+
+def _host_verify_recording(eng, token, truth, rng, steps):
+    """The host verify loop (forward(draft=True) + accept) for `steps`
+    steps, drafts partly the true continuation: (tokens written, kept
+    counts, the drafts fed)."""
+    written, kept_log, fed = [], [], []
+    for s in range(steps):
+        k = s % 3
+        nxt = truth[len(written):len(written) + 4]
+        drafts = nxt[:k] + [int(x) for x in rng.integers(0, eng.shape.vocab, 4 - len(nxt[:k]))]
+        fed.append(drafts)
+        rows = eng.forward([token] + drafts, draft=True).cpu().numpy()
+        kept = 1
+        for i in range(4):
+            if rows[i] != drafts[i]:
+                break
+            kept += 1
+        eng.accept(kept)
+        kept_log.append(kept)
+        written += [int(x) for x in rows[:kept]]
+        token = written[-1]
+    return written, kept_log, fed
+
+
+@pytest.mark.parametrize("family,table", [("lfm2-q4_0", 1024), ("lfm2-q4_0", 3),
+                                          ("llama-q4_k", 1024)])
+def test_graph_verify_equals_host_verify(hip, family, table, monkeypatch):
+    """Verify steps replayed as one captured graph each (drafts from a
+    device table, picks, accept and conv rollback on the device) write the
+    host loop's tokens and keep its counts, step for step; with a table of
+    3 rows the run is split and read back between parts."""
+    from webgllm_amd import engine as E
+    eng, orc = _pair(family, seed=3)
+    rng = np.random.default_rng(5)
+    prompt = _prompt(rng, 10, eng.shape.vocab)
+    token = int(eng.forward(prompt).cpu()[-1])
+    orc.forward(prompt)
+    truth = orc.decode(token, 64)  # 12 steps keep at most 3 each here
+    written, kept, fed = _host_verify_recording(eng, token, truth, rng, 12)
+    assert written == truth[:len(written)]
+    eng2, _ = _pair(family, seed=3)
+    monkeypatch.setattr(E.Engine, "VERIFY_TABLE", table)
+    eng2.forward(prompt)
+    p0 = eng2.position
+    tokens, kept2 = eng2.verify_drafts(token, fed)
+    assert kept2 == kept
+    assert tokens == written
+    assert eng2.position == p0 + sum(kept)
+    # and it goes on from there as sequential decoding does
+    assert eng2.decode(tokens[-1], 4) == truth[len(written):len(written) + 4]
+

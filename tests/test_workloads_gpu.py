@@ -231,6 +231,35 @@ def test_lfm2_12b_verify_with_rollback_against_oracle(hip):
     assert written[:24] == truth
 
 
+def test_lfm2_12b_graph_verify_equals_oracle(hip):
+    """All 16 layers at full width, every verify step one graph on the
+    device (4 drafts from a table, mostly random, some the true
+    continuation; accept and the 10 conv states' rollback on the device):
+    the tokens written are the oracle's sequential greedy tokens."""
+    from webgllm_amd import engine as E
+    s = E.LFM2_12B
+    w = E.Weights(s, seed=17)
+    eng = E.Engine(w, 512)
+    orc = OracleModel(w, 512)
+    rng = np.random.default_rng(23)
+    prompt = _prompt(rng, 40, s.vocab)
+    first = int(eng.forward(prompt).cpu()[-1])
+    orc.forward(prompt, f16_weights=eng._prefill_ok(), batch=40)
+    truth = orc.decode(first, 40)
+    # drafts: step s agrees for s % 3 tokens where the truth is known ahead
+    # (assuming one token kept a step before), random after; 12 steps keep
+    # at most 3 tokens each, within the 40 known
+    drafts = []
+    for st in range(12):
+        k = st % 3
+        nxt = truth[st:st + 4]
+        drafts.append(nxt[:k] + _prompt(rng, 4 - len(nxt[:k]), s.vocab))
+    tokens, kept = eng.verify_drafts(first, drafts)
+    assert len(kept) == 12 and all(1 <= k <= 5 for k in kept)
+    assert tokens == truth[:len(tokens)]
+    assert eng.position == 40 + sum(kept)
+
+
 def test_lfm2_12b_graph_decode_equals_verify_batches(hip):
     """The full model, no oracle: 30 tokens by graph replay from the
     prompt's state, then the same 30 from the same state (position and conv

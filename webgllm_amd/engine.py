@@ -617,6 +617,98 @@ class Engine:
         self.check_plan()
         return toks
 
+    # --- speculative verify on the device, graph-captured --------------------
+    VERIFY_TABLE = 1024  # draft rows the device table holds (steps a replay run takes)
+
+    def _verify_buffers(self, rows: int) -> dict:
+        v = getattr(self, "_verify", None)
+        if v is None or v["rows"] != rows:
+            dev, i32 = self.device, torch.int32
+            layers = [(self.prefixes[i], self.state[i]) for i in sorted(self.state)]
+            v = {"rows": rows, "convs": ops.conv_states(layers, dev),
+                 "table": torch.zeros((self.VERIFY_TABLE, rows - 1), dtype=i32, device=dev),
+                 "cursor": torch.zeros(1, dtype=i32, device=dev),
+                 "kept": torch.zeros(self.VERIFY_TABLE, dtype=i32, device=dev), "graph": None}
+            self._verify = v
+        return v
+
+    def _verify_body(self, v: dict) -> None:
+        """One verify step on the device: drafts from the table into ids[1:],
+        the batch's forward and greedy picks, then the accept (the kept
+        prefix's picks into hist, the conv states rolled back, pos and
+        ids[0] moved on: wg_verify_accept)."""
+        rows = v["rows"]
+        ops.verify_drafts(self.ids, rows, v["table"], v["cursor"])
+        self._forward_rows(rows, keep_prefixes=True)
+        ops.verify_accept(self.next_ids[:rows], rows, v["convs"], self.pos, self.ids, self.hist,
+                          v["kept"], v["cursor"])
+
+    def capture_verify(self, rows: int = 5) -> None:
+        """Captures one verify step of `rows` rows (a token and rows - 1
+        drafts) as a HIP graph. The capture first runs the step once
+        eagerly; the ids, position, conv states and cursor it changes are
+        put back (the cache rows it writes are written again by the first
+        replay)."""
+        if not 2 <= rows <= MAX_ROWS:
+            raise ValueError(f"A verify batch holds 2 to {MAX_ROWS} rows.")
+        v = self._verify_buffers(rows)
+        self.pos.fill_(self.position)
+        stream = torch.cuda.Stream(device=self.device)
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            saved = self._save()
+            cursor = v["cursor"].clone()
+            self._verify_body(v)
+            self._restore(saved)
+            v["cursor"].copy_(cursor)
+            torch.cuda.current_stream().synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                self._verify_body(v)
+        torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        self._restore(saved)
+        v["cursor"].copy_(cursor)
+        v["graph"] = g
+
+    def verify_drafts(self, first_token: int, drafts) -> tuple[list[int], list[int]]:
+        """Greedy speculative decoding with given drafts, every step on the
+        device: step s runs [the last accepted token] + drafts[s] (rows - 1
+        ids) as one batch and keeps its agreeing prefix + 1 (the reference's
+        verify loop, src/handler.ts:1811-1887, with Engine.accept,
+        src/engine.ts:8063-8086). Steps replay back to back with no host
+        decision; the tokens and each step's kept count are read back once
+        per run of up to VERIFY_TABLE steps. Returns (the tokens written,
+        the kept counts)."""
+        table = torch.as_tensor(drafts, dtype=torch.int32)
+        if table.dim() != 2 or table.shape[1] < 1:
+            raise ValueError("drafts must be [steps, rows - 1]")
+        steps, rows = table.shape[0], table.shape[1] + 1
+        v = self._verify_buffers(rows)
+        if v["graph"] is None:
+            self.capture_verify(rows)
+        p0 = self.position
+        self.ids[0] = first_token
+        self.pos.fill_(p0)
+        kept_all: list[int] = []
+        done = 0
+        while done < steps:
+            # every step of a run must fit the cache even if it keeps every row
+            n = min(steps - done, self.VERIFY_TABLE, (self.ctx - self.position) // rows)
+            if n <= 0:
+                raise ValueError(f"The cache holds {self.ctx} tokens; verify batches of {rows} "
+                                 f"from position {self.position} would pass it.")
+            v["table"][:n].copy_(table[done:done + n])
+            v["cursor"].zero_()
+            for _ in range(n):
+                v["graph"].replay()
+            kept = v["kept"][:n].tolist()
+            kept_all += kept
+            self.position += sum(kept)
+            done += n
+        tokens = self.hist[p0 + 1:self.position + 1].tolist()
+        return tokens, kept_all
+
     # --- sampled decoding -------------------------------------------------
     def generate(self, prompt: list[int], steps: int, sampler, random=None,
                  count: int = 64) -> list[int]:

@@ -39,6 +39,12 @@ class Q4MatrixDesc(C.Structure):
 EPI_STORE, EPI_SWIGLU, EPI_ROPE_KV = 0, 1, 2
 
 
+class ConvState(C.Structure):
+    """wg_conv_state (include/webgllm_hip.h): a conv layer's rollback operands."""
+    _fields_ = [("prefixes", C.c_void_p), ("state", C.c_void_p), ("dim", C.c_int32),
+                ("width", C.c_int32)]
+
+
 class Epilogue(C.Structure):
     """wg_epilogue (include/webgllm_hip.h)."""
     _fields_ = [("mode", C.c_int32),
@@ -194,6 +200,8 @@ def load():
                                      P, SZ, P]),
         "wg_attn_decode_noalloc": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32,
                                              P, I32, P]),
+        "wg_verify_accept": (C.c_int, [P, I32, P, I32, I32, P, P, P, I32, P, I32, P, P]),
+        "wg_verify_drafts": (C.c_int, [P, I32, P, I32, P, P]),
         "wg_short_conv": (C.c_int, [P, I32, I32, I32, I32, P, P, P, P, P, I32, P]),
         "wg_conv_accept": (C.c_int, [P, I32, I32, I32, I32, P, P]),
         "wg_argmax_scratch_bytes": (SZ, [I32, I32]),

@@ -400,6 +400,42 @@ def conv_accept(prefixes, kept, rows, D, W, state):
     L.check(L.load().wg_conv_accept(_p(prefixes), kept, rows, D, W, _p(state), _stream()))
 
 
+def conv_states(layers, device="cuda"):
+    """A device array of wg_conv_state for [(prefixes [R][W-1][D], state
+    [W-1][D])]: (the array, its count, the largest state in floats)."""
+    arr = (L.ConvState * max(1, len(layers)))()
+    big = 0
+    for i, (pre, st) in enumerate(layers):
+        W1, D = st.shape
+        arr[i] = L.ConvState(_p(_dev(pre, torch.float32)), _p(_dev(st, torch.float32)), D, W1 + 1)
+        big = max(big, W1 * D)
+    raw = np.frombuffer(bytes(arr), dtype=np.uint8).copy()
+    return torch.from_numpy(raw).to(device), len(layers), big
+
+
+def verify_accept(picks, rows, convs, pos, ids, hist, kept_log, cursor):
+    """wg_verify_accept: keep the batch's agreeing prefix + 1, roll the conv
+    states back, move the position and ids[0] on (all on the device).
+    convs is conv_states()'s triple."""
+    arr, n, big = convs
+    for t, name in ((picks, "picks"), (pos, "pos"), (ids, "ids"), (hist, "hist"),
+                    (kept_log, "kept_log"), (cursor, "cursor")):
+        if t.dtype != torch.int32 or not t.is_cuda:
+            raise ValueError(f"{name} must be an int32 device tensor")
+    L.check(L.load().wg_verify_accept(_p(picks), rows, _p(arr), n, big, _p(pos), _p(ids),
+                                      _p(hist), hist.numel(), _p(kept_log), kept_log.numel(),
+                                      _p(cursor), _stream()))
+
+
+def verify_drafts(ids, rows, table, cursor):
+    """wg_verify_drafts: ids[1:rows] = table[*cursor] (int32 [steps, rows - 1])."""
+    table = _dev(table, torch.int32)
+    if table.dim() != 2 or table.shape[1] != rows - 1:
+        raise ValueError(f"the draft table must be [steps, {rows - 1}]")
+    L.check(L.load().wg_verify_drafts(_p(ids), rows, _p(table), table.shape[0], _p(cursor),
+                                      _stream()))
+
+
 def argmax_rows(logits: torch.Tensor, V: int | None = None, ids=None, tops=None, scratch=None):
     logits = _dev(logits, torch.float32)
     M = logits.shape[0]
