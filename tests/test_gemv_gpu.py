@@ -120,3 +120,37 @@ def test_gemv_closed_forms(hip):
     y = ops.gemv(z, x)
     bound = 8 * x.float().abs().sum(1, keepdim=True) * 2 ** -20
     assert torch.all(y.abs() <= bound)
+
+
+@pytest.fixture(params=["mfma", "vector"])
+def few_path(request):
+    """The few-token GEMV on MFMA for every row count (knob 2), or on the
+    vector kernels only (knob 0)."""
+    from webgllm_amd import lib as L
+    old = L.tuning_get("gemv_mfma")
+    L.tuning_set("gemv_mfma", 2 if request.param == "mfma" else 0)
+    yield request.param
+    L.tuning_set("gemv_mfma", old)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k"])
+@pytest.mark.parametrize("N,K", [(2048, 2048), (36, 96), (100, 4096), (4864, 896), (512, 32),
+                                 (264, 1568), (2048, 8192)])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
+def test_gemv_paths_match_oracle(hip, few_path, fmt, N, K, M):
+    """Both few-token paths within rel-L2 1e-5 of the float64 oracle:
+    partial last tiles (N = 36, 100, 264: row groups that are not a
+    multiple of 4), an odd block count (K = 96, 1568), a single block,
+    K split over 8 waves (4096), and K = 8192, which the MFMA kernel leaves
+    to the vector one."""
+    from webgllm_amd import ops
+    if fmt == "q4_k" and K % 256:
+        pytest.skip("Q4_K rows are super-blocks of 256")
+    rng = np.random.default_rng(N * 7 + K * 3 + M)
+    m, want_m = MAKERS[fmt](rng, N, K)
+    h, xf = _x16(rng, M, K)
+    y = ops.gemv(m, torch.from_numpy(h.view(np.int16)).cuda())
+    torch.cuda.synchronize()
+    err = rel_l2(y.cpu().numpy(), O.gemv_f64(want_m, xf))
+    print(f"{few_path} {fmt} N={N} K={K} M={M} rel-L2 {err:.2e}")
+    assert err <= 1e-4

@@ -197,8 +197,7 @@ __global__ __launch_bounds__(FGM * 64) void attn_tile_kernel(
   const bool vis = lane < nk && j0 + lane <= pos0 + m;  // causal
   const float sc = vis ? (s0 + s1) + (s2 + s3) : -INFINITY;
   float mx = sc;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  mx = wave_max(mx);
   const float e = (mx == -INFINITY || !vis) ? 0.0f : __expf(sc - mx);
   const float lsum = wave_sum(e);
 
@@ -222,9 +221,7 @@ __global__ __launch_bounds__(FGM * 64) void attn_tile_kernel(
     }
   }
 #pragma unroll
-  for (int off = KP; off < 64; off <<= 1)
-#pragma unroll
-    for (int t = 0; t < 8; t++) acc[t] += __shfl_xor(acc[t], off, 64);
+  for (int t = 0; t < 8; t++) acc[t] = group_reduce<KP>(acc[t], Plus());
   PartialLayout pl{HD, chunks};
   float *po = partial + pl.base(m * H + kh * G + g, c);
   if (lane < KP)
@@ -367,8 +364,7 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
     const bool vis = lane < nk && jc + lane <= pos0 + m;  // causal
     const float sc = vis ? (s0 + s1) + (s2 + s3) : -INFINITY;
     float cmax = sc;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) cmax = fmaxf(cmax, __shfl_xor(cmax, off, 64));
+    cmax = wave_max(cmax);
     const float mnew = fmaxf(mrun, cmax);
     if (mnew == -INFINITY) continue;  // nothing visible to this row yet
     const float alpha = mrun == -INFINITY ? 0.0f : __expf(mrun - mnew);
@@ -395,9 +391,7 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
     mrun = mnew;
   }
 #pragma unroll
-  for (int off = KP; off < 64; off <<= 1)
-#pragma unroll
-    for (int t = 0; t < 8; t++) acc[t] += __shfl_xor(acc[t], off, 64);
+  for (int t = 0; t < 8; t++) acc[t] = group_reduce<KP>(acc[t], Plus());
   const int qrow = m * H + kh * G + g;
   float *po = partial + ((int64_t)qrow * splits + s) * SR;
   if (lane < KP) {
@@ -443,8 +437,7 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
     for (int i = 0; i < NL; i++) settle(v[i]);
     const float mt = lane < n ? ml.x : -INFINITY;
     float bmax = mt;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) bmax = fmaxf(bmax, __shfl_xor(bmax, off, 64));
+    bmax = wave_max(bmax);
     const float nmax = fmaxf(gmax, bmax);
     if (nmax == -INFINITY) continue;  // nothing visible yet
     const float alpha = gmax == -INFINITY ? 0.0f : __expf(gmax - nmax);
@@ -469,13 +462,10 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
     gmax = nmax;
   }
   // lanes holding the same dims (different splits) add up
-#pragma unroll
-  for (int off = LPS; off < 64; off <<= 1) {
-    o.x += __shfl_xor(o.x, off, 64);
-    o.y += __shfl_xor(o.y, off, 64);
-    o.z += __shfl_xor(o.z, off, 64);
-    o.w += __shfl_xor(o.w, off, 64);
-  }
+  o.x = group_reduce<LPS>(o.x, Plus());
+  o.y = group_reduce<LPS>(o.y, Plus());
+  o.z = group_reduce<LPS>(o.z, Plus());
+  o.w = group_reduce<LPS>(o.w, Plus());
   const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
   if (lane < LPS) {
     uint16_t *op = out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD + dh;
@@ -535,8 +525,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *partial,
 #pragma unroll
   for (int t = 0; t < MAX_CH / 64; t++)
     if (lane + 64 * t < used) gmax = fmaxf(gmax, cm[t]);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) gmax = fmaxf(gmax, __shfl_xor(gmax, off, 64));
+  gmax = wave_max(gmax);
   float ltot = 0.0f, acc[CSL];
 #pragma unroll
   for (int d = 0; d < CSL; d++) acc[d] = 0.0f;
@@ -850,7 +839,7 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_mfma_kernel(
         p[j] = vis ? st[j] : -INFINITY;
         tmax = fmaxf(tmax, p[j]);
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      tmax = fmaxf(tmax, xor32(tmax));
       const float m_new = fmaxf(m_run, tmax);
       const float corr = m_new == -INFINITY ? 1.0f : __expf(m_run - m_new);
       float psum = 0.0f;
@@ -859,7 +848,7 @@ __global__ __launch_bounds__(NW * 64) void attn_prefill_mfma_kernel(
         p[j] = p[j] == -INFINITY ? 0.0f : __expf(p[j] - m_new);
         psum += p[j];
       }
-      psum += __shfl_xor(psum, 32, 64);
+      psum += xor32(psum);
       l_run = l_run * corr + psum;
       m_run = m_new;
 #pragma unroll

@@ -95,8 +95,7 @@ __device__ inline void attn_chunk_item(const float *q, int ldq, int M, int H, in
   for (int qi = wave; qi < GM; qi += NT / 64) {
     float v = lane < CHUNK ? sc[qi * CHUNK + lane] : -INFINITY;
     float m_ = v;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m_ = fmaxf(m_, __shfl_xor(m_, off, 64));
+    m_ = wave_max(m_);
     float e = (m_ == -INFINITY || v == -INFINITY) ? 0.0f : __expf(v - m_);
     if (lane < CHUNK) sc[qi * CHUNK + lane] = e;
     float l = wave_sum(e);
@@ -158,8 +157,7 @@ __device__ inline void attn_combine_group(const float *partial, int chunks, int 
     float *w = wts + qi * used_all;
     float mx = -INFINITY;
     for (int c = lane; c < used; c += 64) mx = fmaxf(mx, w[c]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    mx = wave_max(mx);
     float l = 0.0f;
     for (int c = lane; c < used_all; c += 64) {
       float v = w[c];

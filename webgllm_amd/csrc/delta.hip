@@ -40,11 +40,6 @@ struct DeltaArgs {
   int ldo;
 };
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
 
 // A workgroup barrier that waits for this wave's LDS operations only: the
 // next row's global loads, issued before it, stay in flight across it.
@@ -127,10 +122,9 @@ __global__ __launch_bounds__(64 * DW) void delta_rule_kernel(DeltaArgs a) {
       pk = fmaf(s[r], kn[p][i0 + r], pk);
       pq = fmaf(s[r], qn[p][i0 + r], pq);
     }
-#pragma unroll
-    for (int off = CB; off < 64; off <<= 1) {  // the wave's row groups of this column
-      pk += __shfl_xor(pk, off, 64);
-      pq += __shfl_xor(pq, off, 64);
+    if constexpr (CB < 64) {  // the wave's row groups of this column
+      pk = group_reduce<CB>(pk, Plus());
+      pq = group_reduce<CB>(pq, Plus());
     }
     if (lane < CB) {
       redk[p][w][c] = pk * invk;
@@ -337,10 +331,8 @@ __global__ __launch_bounds__(256) void delta_chunk_prep_kernel(ChunkArgs a) {
       ssq = fmaf(sq[r * RS + i], sq[r * RS + i], ssq);
       ssk = fmaf(sk[r * RS + i], sk[r * RS + i], ssk);
     }
-    ssq += __shfl_xor(ssq, 1, 64);
-    ssq += __shfl_xor(ssq, 2, 64);
-    ssk += __shfl_xor(ssk, 1, 64);
-    ssk += __shfl_xor(ssk, 2, 64);
+    ssq = quad_sum(ssq);
+    ssk = quad_sum(ssk);
     const float invq = 1.0f / sqrtf((float)dk) / sqrtf(ssq + 1e-6f);
     const float invk = 1.0f / sqrtf(ssk + 1e-6f);
     for (int i = part; i < dk; i += 4) {

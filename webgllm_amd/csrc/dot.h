@@ -47,11 +47,59 @@ __device__ inline float sum8(const uint4 &a, float acc) {
   return dot2(a.w, ONES, acc);
 }
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+// Cross-lane moves without an LDS round trip (a shuffle is a ds_bpermute,
+// whose latency a chain of reductions pays at every step): the value of
+// lane l ^ 32 (v_permlane32_swap: the wave's halves trade places), of lane
+// l ^ 16 (v_permlane16_swap: rows 0 and 1, 2 and 3 trade), and DPP
+// rotations within 16-lane rows.
+__device__ inline float xor32(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
 }
+__device__ inline float xor16(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+}
+// lane (l - N) mod 16 of the same row (row_ror:N)
+template <int N>
+__device__ inline float row_ror(float v) {
+  static_assert(N >= 1 && N < 16, "rotation");
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x120 + N, 0xf, 0xf, false));
+}
+
+// op over the lanes of the wave that share lane % P (P a power of two,
+// 1 to 32), on every one of them. Each step combines a lane with the lane
+// P 2^k away in the same group (a rotation within 16-lane rows, then the
+// row and half swaps); both lanes of a pair combine the same two values,
+// so with a commutative op every lane of a group ends with the same bits.
+template <int P, typename Op>
+__device__ inline float group_reduce(float v, Op op) {
+  static_assert(P >= 1 && P <= 32 && (P & (P - 1)) == 0, "group stride");
+  if constexpr (P <= 1) v = op(v, row_ror<1>(v));
+  if constexpr (P <= 2) v = op(v, row_ror<2>(v));
+  if constexpr (P <= 4) v = op(v, row_ror<4>(v));
+  if constexpr (P <= 8) v = op(v, row_ror<8>(v));
+  if constexpr (P <= 16) v = op(v, xor16(v));
+  return op(v, xor32(v));
+}
+struct Plus {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct Max {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+// The sum over each group of 4 consecutive lanes, on each of them (DPP
+// quad permutes [1 0 3 2], then [2 3 0 1]).
+__device__ inline float quad_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));
+}
+// The wave's sum / max on every lane.
+__device__ inline float wave_sum(float v) { return group_reduce<1>(v, Plus()); }
+__device__ inline float wave_max(float v) { return group_reduce<1>(v, Max()); }
 
 // Wave64 reductions through DPP (no LDS round trip): within quads, half
 // rows and rows, then rows into lane 63 by the row broadcasts; the result is
@@ -80,23 +128,23 @@ __device__ inline float wave_sum_u(float v) {
   return wave_reduce_dpp(v, 0.0f, [](float a, float b) { return a + b; });
 }
 
-// Reduce-scatter of 4 per-lane values over the 64 lanes in 7 shuffles:
-// afterwards lanes 16 r .. 16 r + 15 all hold the wave's sum of v[r].
+// Reduce-scatter of 4 per-lane values over the 64 lanes (two lane swaps,
+// then a sum within 16-lane rows): afterwards lanes 16 r .. 16 r + 15 all
+// hold the wave's sum of v[r].
 __device__ inline float wave_sum4(float v0, float v1, float v2, float v3) {
   const int lane = threadIdx.x & 63;
   const bool hi = lane & 32;
   float s0 = hi ? v0 : v2, s1 = hi ? v1 : v3;
   float k0 = hi ? v2 : v0, k1 = hi ? v3 : v1;
-  k0 += __shfl_xor(s0, 32, 64);
-  k1 += __shfl_xor(s1, 32, 64);
+  k0 += xor32(s0);
+  k1 += xor32(s1);
   const bool hi2 = lane & 16;
   float k = hi2 ? k1 : k0;
-  k += __shfl_xor(hi2 ? k0 : k1, 16, 64);
-  k += __shfl_xor(k, 8, 64);
-  k += __shfl_xor(k, 4, 64);
-  k += __shfl_xor(k, 2, 64);
-  k += __shfl_xor(k, 1, 64);
-  return k;
+  k += xor16(hi2 ? k0 : k1);
+  k += row_ror<8>(k);
+  k += row_ror<4>(k);
+  k += row_ror<2>(k);
+  return k + row_ror<1>(k);
 }
 
 // The row a lane holds after wave_sum4.

@@ -62,7 +62,7 @@ __device__ inline void input_scales(const wg_epilogue &e, float s[M]) {
 // the kernel's start). Every thread of the workgroup calls it: it holds a
 // barrier.
 template <int M, int NW>
-__device__ inline void input_scales_wg(const wg_epilogue &e, float s[M], float *lds) {
+__device__ inline void input_scales_wg(const wg_epilogue &e, float s[M], float *lds, int mr = M) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (e.norm_parts) {
     // The M tokens' loads go out together (a token at a time, each waited
@@ -77,7 +77,8 @@ __device__ inline void input_scales_wg(const wg_epilogue &e, float s[M], float *
         float4 t[M];
 #pragma unroll
         for (int m = 0; m < M; m++)
-          t[m] = reinterpret_cast<const float4 *>(p + (int64_t)m * e.ld_parts_in)[i];
+          t[m] = m < mr ? reinterpret_cast<const float4 *>(p + (int64_t)m * e.ld_parts_in)[i]
+                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int m = 0; m < M; m++) a[m] += (t[m].x + t[m].y) + (t[m].z + t[m].w);
       }
@@ -85,7 +86,7 @@ __device__ inline void input_scales_wg(const wg_epilogue &e, float s[M], float *
       for (int i = wave * 64 + lane; i < e.n_parts; i += NW * 64) {
         float t[M];
 #pragma unroll
-        for (int m = 0; m < M; m++) t[m] = p[(int64_t)m * e.ld_parts_in + i];
+        for (int m = 0; m < M; m++) t[m] = m < mr ? p[(int64_t)m * e.ld_parts_in + i] : 0.0f;
 #pragma unroll
         for (int m = 0; m < M; m++) a[m] += t[m];
       }
@@ -106,7 +107,7 @@ __device__ inline void input_scales_wg(const wg_epilogue &e, float s[M], float *
       for (int w = 0; w < NW; w++) a += lds[w * M + m];
       v = e.norm_mult / sqrtf(a / (float)e.norm_count + e.eps);
     }
-    if (e.row_scale) v *= e.row_scale[m];
+    if (e.row_scale) v *= e.row_scale[m < mr ? m : 0];
     s[m] = v;
   }
 }
@@ -130,10 +131,11 @@ __device__ inline int epi_pos0(const wg_epilogue &e) {
 // Row (4 g + r, r = lane / 16 % 4) for token m = lane % 16 (m < M): the
 // operands finish<M, MODE> needs. g >= G loads nothing.
 template <int M, int MODE>
-__device__ inline void epi_prefetch(const wg_epilogue &e, int g, int G, int pos0, EpiPre &p) {
+__device__ inline void epi_prefetch(const wg_epilogue &e, int g, int G, int pos0, EpiPre &p,
+                                    int mr = M) {
   const int lane = threadIdx.x & 63;
   const int r = (lane >> 4) & 3, m = lane & 15;
-  const bool live = g < G && m < M;
+  const bool live = g < G && m < mr;
   const int n = 4 * g + r;
   p.res = p.w16 = p.c1 = p.s1 = p.c2 = p.s2 = 0.0f;
   if constexpr (MODE == WG_EPI_STORE) {
@@ -175,15 +177,28 @@ __device__ inline float pick(const float (&tot)[M], int m) {
 // Row group g's four rows for tokens 0..M-1, with the operands
 // epi_prefetch<M, MODE> loaded for g. Called by every lane of the wave (the
 // shuffles need all of them), with g >= G for idle waves.
+template <int MODE>
+__device__ inline void finish_value(const wg_epilogue &e, int g, float v, bool live, float *y,
+                                    int ldy, const EpiPre &pre, int pos0);
+
 template <int M, int MODE>
 __device__ inline void finish(const wg_epilogue &e, int g, int G, const float (&tot)[M],
                               const float (&scale)[M], float *y, int ldy, const EpiPre &pre,
                               int pos0) {
+  const int m = threadIdx.x & 15;
+  const int mm = m < M ? m : 0;
+  const float v = pick<M>(tot, mm) * 0x1p24f * pick<M>(scale, mm);  // (an index would put scale in LDS)
+  finish_value<MODE>(e, g, v, g < G && m < M, y, ldy, pre, pos0);
+}
+
+// Row 4 g + r (r = lane / 16 % 4) of token m = lane % 16 is v (final, before
+// the epilogue's own operation); `live`: the row and token exist. Called by
+// every lane of the wave.
+template <int MODE>
+__device__ inline void finish_value(const wg_epilogue &e, int g, float v, bool live, float *y,
+                                    int ldy, const EpiPre &pre, int pos0) {
   const int lane = threadIdx.x & 63;
   const int r = (lane >> 4) & 3, m = lane & 15;
-  const bool live = g < G && m < M;
-  const int mm = m < M ? m : 0;
-  float v = pick<M>(tot, mm) * 0x1p24f * pick<M>(scale, mm);  // (an index would put scale in LDS)
   const int n = 4 * g + r;
   if constexpr (MODE == WG_EPI_STORE) {
     if (live && e.residual) v += pre.res;
@@ -192,13 +207,13 @@ __device__ inline void finish(const wg_epilogue &e, int g, int G, const float (&
       e.out16[(int64_t)m * e.ld_out16 + n] = half_bits(v * pre.w16 / e.norm_mult_out);
     if (e.parts_out) {
       float sq = live ? v * v : 0.0f;
-      sq += __shfl_xor(sq, 16, 64);
-      sq += __shfl_xor(sq, 32, 64);
+      sq += xor16(sq);
+      sq += xor32(sq);
       if (live && r == 0) e.parts_out[(int64_t)m * e.ld_parts_out + g] = sq;
     }
   } else if constexpr (MODE == WG_EPI_SWIGLU) {
     // rows (gate 2i, gate 2i + 1, up 2i, up 2i + 1): row r < 2 meets row r + 2
-    float up = __shfl_xor(v, 32, 64);
+    float up = xor32(v);
     if (live && r < 2) {
       float gate = v;
       float o = gate / (1.0f + __expf(-gate)) * up;
@@ -207,7 +222,7 @@ __device__ inline void finish(const wg_epilogue &e, int g, int G, const float (&
   } else {  // WG_EPI_ROPE_KV
     const int hd = e.head_dim, P = hd / 2;
     const int qd = e.heads * hd, kd = e.kv_heads * hd;
-    float partner = __shfl_xor(v, 16, 64);  // rows 0 <-> 1 and 2 <-> 3
+    float partner = xor16(v);  // rows 0 <-> 1 and 2 <-> 3
     const int row = 4 * g;
     int pos = live ? pos0 + m : -1;
     bool in_cache = pos >= 0 && pos < e.ctx && 1024 + (pos >> 10) < e.rope_rows;

@@ -225,6 +225,7 @@ int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx,
   if (w->layout == WG_LAYOUT_Q4K) return launch_gemv_q4k(w, x, M, ldx, y, ldy, e, s);
   if (w->layout == WG_LAYOUT_Q8 || w->layout == WG_LAYOUT_Q6K)
     return launch_gemv_wide(w, x, M, ldx, y, ldy, e, s);
+  if ((rc = launch_gemv_mfma(w, x, M, ldx, y, ldy, e, s)) != -1) return rc;
   if (M <= 2 && w->K <= 512 * 32) {
     rc = M == 1 ? launch_stream_m<1>(w, x, ldx, y, ldy, e, s)
                 : launch_stream_m<2>(w, x, ldx, y, ldy, e, s);

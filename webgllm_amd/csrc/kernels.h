@@ -17,6 +17,10 @@ int launch_gemv_q4k(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, fl
 // row-group kernel.
 int launch_gemv_few(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y,
                     int ldy, const wg_epilogue &e, hipStream_t s);
+// 4-bit row-group GEMV of 1 to 8 tokens on MFMA, or -1 when the knob or
+// the shape (more than 128 blocks a row) leaves it to the other kernels.
+int launch_gemv_mfma(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y,
+                     int ldy, const wg_epilogue &e, hipStream_t s);
 int launch_gemv_wide(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y, int ldy,
                      const wg_epilogue &e, hipStream_t s);
 

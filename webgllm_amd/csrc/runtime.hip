@@ -77,6 +77,9 @@ static Knob g_knobs[] = {
     {"gemv_min_waves", 8192, 0, 1 << 20},  // split K within a workgroup below this
     {"gemv_few_stream", 1, 0, 1},        // 3 to 8 tokens on the streaming kernel (0: row groups)
     {"gemv_few_wg_per_cu", 1, 1, 16},    // its persistent workgroups per CU
+    {"gemv_mfma", 1, 0, 2},              // row-group GEMV on MFMA: 1 for 3 to 8 tokens, 2 also 1 and 2, 0 never
+    {"gemv_mfma_wg_per_cu", 2, 1, 16},   // its persistent workgroups per CU
+    {"gemv_mfma_pairs", 8, 2, 8},        // its block pairs a wave (2, 4, 8)
     {"decode_wg_per_cu", 1, 1, 4},       // persistent decode workgroups (8 waves) per CU
     {"attn_prefill_mfma", 4, 0, 4},      // prompt attention: MFMA waves a workgroup (1, 2, 4), 0 VALU
     {"attn_fused", 1, 0, 2},             // decode attention in one launch: 1 where it is faster, 2 always, 0 never

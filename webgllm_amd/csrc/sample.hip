@@ -14,6 +14,7 @@
 // `count`. Stage 3 (`chunk_gather_kernel`): a workgroup per kept chunk
 // writes its penalized logits.
 #include "common.h"
+#include "dot.h"
 
 namespace wg {
 namespace {
@@ -74,8 +75,7 @@ __global__ __launch_bounds__(256) void chunk_max_kernel(const float *logits, int
 #pragma unroll
   for (int i = 0; i < 4; i++)
     mx = fmaxf(mx, penalized(v[i], c * CHUNK + 4 * lane + i, r + p.row0, p, V, m[i]));
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  mx = wave_max(mx);
   if (lane == 0) maxima[w] = mx;
 }
 
