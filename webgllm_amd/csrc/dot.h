@@ -97,6 +97,23 @@ __device__ inline float quad_sum(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
   return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));
 }
+// Reduce-scatter of 8 per-lane values: afterwards lanes 8 t .. 8 t + 7 all
+// hold the wave's sum of v[t] (halves, rows and 8-lane halves of rows
+// trade the values they keep, then each 8 lanes add up by quad permutes
+// and a half-row mirror).
+__device__ inline float wave_sum8(const float (&v)[8]) {
+  const int lane = threadIdx.x & 63;
+  const bool h32 = lane & 32, h16 = lane & 16, h8 = lane & 8;
+  float a[4], b[2];
+#pragma unroll
+  for (int t = 0; t < 4; t++) a[t] = (h32 ? v[t + 4] : v[t]) + xor32(h32 ? v[t] : v[t + 4]);
+#pragma unroll
+  for (int u = 0; u < 2; u++) b[u] = (h16 ? a[u + 2] : a[u]) + xor16(h16 ? a[u] : a[u + 2]);
+  float c = (h8 ? b[1] : b[0]) + row_ror<8>(h8 ? b[0] : b[1]);
+  c += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, c), 0xb1, 0xf, 0xf, false));
+  c += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, c), 0x4e, 0xf, 0xf, false));
+  return c + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, c), 0x141, 0xf, 0xf, false));
+}
 // The wave's sum / max on every lane.
 __device__ inline float wave_sum(float v) { return group_reduce<1>(v, Plus()); }
 __device__ inline float wave_max(float v) { return group_reduce<1>(v, Max()); }

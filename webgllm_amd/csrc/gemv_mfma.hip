@@ -332,26 +332,23 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
     }
     // The round's sums are in LDS: finish its 4 rn row groups (wave w
     // takes w, w + KS, ...), their epilogue operands loaded together first.
-    if (deferred && r0 == 0) {
+    if (deferred && r0 == 0) {  // token t's sum on lanes 8 t .. 8 t + 7
+      float v[8];
 #pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const float sum = wave_sum((pt[t].x + pt[t].y) + (pt[t].z + pt[t].w));
-        if (lane == 0) nred[wave * 8 + t] = sum;
-      }
+      for (int t = 0; t < 8; t++) v[t] = (pt[t].x + pt[t].y) + (pt[t].z + pt[t].w);
+      const float sum = wave_sum8(v);
+      if ((lane & 7) == 0) nred[wave * 8 + (lane >> 3)] = sum;
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes done
     barrier();
-    if (deferred && r0 == 0) {
+    if (deferred && r0 == 0) {  // this lane's token only
+      const int t = m < M ? m : 0;
+      float a = 0.0f;
 #pragma unroll
-      for (int t = 0; t < 8; t++) {
-        float a = 0.0f;
-#pragma unroll
-        for (int w = 0; w < KS; w++) a += nred[w * 8 + t];
-        float v = e.norm_mult / sqrtf(a / (float)e.norm_count + e.eps);
-        if (e.row_scale) v *= e.row_scale[t < M ? t : 0];
-        scale[t] = v;
-      }
-      my_scale = pick<8>(scale, m < 8 ? m : 0) * (SUB ? 0x1p24f : 1.0f);
+      for (int w = 0; w < KS; w++) a += nred[w * 8 + t];
+      float v = e.norm_mult / sqrtf(a / (float)e.norm_count + e.eps);
+      if (e.row_scale) v *= e.row_scale[t];
+      my_scale = v * (SUB ? 0x1p24f : 1.0f);
     }
     EpiPre pe[RGF];
 #pragma unroll
