@@ -115,10 +115,14 @@ struct Slot {
   static constexpr int LOADS = NQ + NS + NZ;     // load instructions a wave-tile
 };
 
-// Tiles whose K-slice sums wait in LDS before a round of epilogues.
-template <int KS>
+// Tiles whose K-slice sums wait in LDS before a round of epilogues: up to
+// 8, as many as the LDS left by the ring holds (512 bytes a wave a tile).
+template <int ZK, int NP, int KS, int S>
 constexpr int mfma_round() {
-  return KS >= 16 ? 4 : 8;
+  constexpr int ring = S * KS * Slot<ZK, NP>::BYTES, spare = 160 * 1024 - ring - KS * 32;
+  constexpr int r = spare / (KS * 512);
+  static_assert(r >= 1, "LDS");
+  return r < 8 ? r : 8;
 }
 
 template <int ZK, int NP, int KS, int S, int MODE>
@@ -128,9 +132,9 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
     float *__restrict__ y, int ldy, const wg_epilogue e, int G, int B) {
   using SL = Slot<ZK, NP>;
   constexpr bool SUB = ZK == WG_ZERO_F16;  // subnormal nibbles, zero point in C
-  constexpr int R = mfma_round<KS>();       // tiles a round (their sums wait in LDS)
+  constexpr int R = mfma_round<ZK, NP, KS, S>();  // tiles a round (their sums wait in LDS)
   constexpr int RGF = (4 * R + KS - 1) / KS;  // row groups a wave finishes a round
-  static_assert(NP % 2 == 0 && (S - 1) * SL::LOADS < 64, "ring shape");
+  static_assert(NP % 2 == 0 && S >= 1 && (S - 1) * SL::LOADS < 64, "ring shape");
   extern __shared__ __align__(16) unsigned char smem[];
   float *red = reinterpret_cast<float *>(smem + S * KS * SL::BYTES);  // [R][KS][128]
   __shared__ float nred[KS * 8];
@@ -219,10 +223,11 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
       rb[j] = xp[2];
     }
   }
-  // The norm's parts: this lane's piece of each token's, summed at the
-  // first round's barrier, so nothing waits for them (or for the other
-  // waves) before the first tile is computed. Parts that a workgroup cannot
-  // take in one piece a lane are summed here, behind a barrier.
+  // The norm's parts: this lane's piece of each token's, loaded with A and
+  // summed with it (waiting for A waits for every load so far), the waves'
+  // sums left in LDS for the first round's barrier; no wave waits for
+  // another before the first tile. Parts that a workgroup cannot take in
+  // one piece a lane are summed here, behind a barrier.
   float scale[8];
   float4 pt[8];
   const int ip = wave * 64 + lane;
@@ -241,6 +246,13 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
   }
   const int pos0 = epi_pos0<MODE>(e);
 
+  if (deferred) {  // token t's sum on lanes 8 t .. 8 t + 7
+    float v[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) v[t] = (pt[t].x + pt[t].y) + (pt[t].z + pt[t].w);
+    const float sum = wave_sum8(v);
+    if ((lane & 7) == 0) nred[wave * 8 + (lane >> 3)] = sum;
+  }
   u4v alo[NP], ahi[NP];
   float sa[NP];
 #pragma unroll
@@ -286,6 +298,16 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
   if (!deferred) my_scale = pick<8>(scale, m < 8 ? m : 0) * (SUB ? 0x1p24f : 1.0f);
   for (int r0 = 0; r0 < ntiles; r0 += R) {
     const int rn = min(R, ntiles - r0);
+    // the round's epilogue operands, in flight under its tiles (waves w,
+    // w + KS, ... of its 4 rn row groups)
+    EpiPre pe[RGF];
+#pragma unroll
+    for (int f = 0; f < RGF; f++) {
+      const int qg = wave + f * KS;
+      if (qg < 4 * rn)
+        epi_prefetch<8, MODE>(e, 4 * ((int)blockIdx.x + (r0 + qg / 4) * (int)gridDim.x) + (qg & 3),
+                              G, pos0, pe[f], M);
+    }
     for (int i = r0; i < r0 + rn; i++) {
       // tile i's loads are done once at most the later tiles' are in flight
       const int later = min(S - 1, ntiles - 1 - i);
@@ -330,15 +352,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
       for (int k = 0; k < 4; k++) acc[k] += xor32(acc[k]);
       if (lane < 32) *reinterpret_cast<f4v *>(red + ((i - r0) * KS + wave) * 128 + lane * 4) = acc;
     }
-    // The round's sums are in LDS: finish its 4 rn row groups (wave w
-    // takes w, w + KS, ...), their epilogue operands loaded together first.
-    if (deferred && r0 == 0) {  // token t's sum on lanes 8 t .. 8 t + 7
-      float v[8];
-#pragma unroll
-      for (int t = 0; t < 8; t++) v[t] = (pt[t].x + pt[t].y) + (pt[t].z + pt[t].w);
-      const float sum = wave_sum8(v);
-      if ((lane & 7) == 0) nred[wave * 8 + (lane >> 3)] = sum;
-    }
+    // The round's sums are in LDS: finish its 4 rn row groups.
     __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes done
     barrier();
     if (deferred && r0 == 0) {  // this lane's token only
@@ -349,14 +363,6 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
       float v = e.norm_mult / sqrtf(a / (float)e.norm_count + e.eps);
       if (e.row_scale) v *= e.row_scale[t];
       my_scale = v * (SUB ? 0x1p24f : 1.0f);
-    }
-    EpiPre pe[RGF];
-#pragma unroll
-    for (int f = 0; f < RGF; f++) {
-      const int qg = wave + f * KS;
-      if (qg < 4 * rn)
-        epi_prefetch<8, MODE>(e, 4 * ((int)blockIdx.x + (r0 + qg / 4) * (int)gridDim.x) + (qg & 3),
-                              G, pos0, pe[f], M);
     }
 #pragma unroll
     for (int f = 0; f < RGF; f++) {
@@ -381,7 +387,8 @@ template <int ZK, int NP, int KS, int S>
 int launch_mfma(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y, int ldy,
                 const wg_epilogue &e, hipStream_t s) {
   const int G = w->N / 4, B = w->K / 32, NT = (G + 3) / 4;
-  constexpr size_t LDS = (size_t)S * KS * Slot<ZK, NP>::BYTES + mfma_round<KS>() * KS * 128 * 4;
+  constexpr size_t LDS =
+      (size_t)S * KS * Slot<ZK, NP>::BYTES + mfma_round<ZK, NP, KS, S>() * KS * 128 * 4;
   static_assert(LDS + KS * 32 <= 160 * 1024, "LDS");
   const int grid = persistent_grid(NT, tuning("gemv_mfma_wg_per_cu"));
   auto q = (const uint8_t *)w->quants;
@@ -416,6 +423,11 @@ int launch_mfma_k(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, floa
                               : launch_mfma<ZK, 8, 4, 3>(w, x, M, ldx, y, ldy, e, s);
   if (P <= 64) return np <= 4 ? launch_mfma<ZK, 4, 16, 3>(w, x, M, ldx, y, ldy, e, s)
                               : launch_mfma<ZK, 8, 8, 3>(w, x, M, ldx, y, ldy, e, s);
+  // 16 waves of 8 pairs: a tile's 16 rows fill most of the LDS, so the ring
+  // holds two (one with zero-point bytes); half zero points' C terms do not
+  // fit the registers a wave of 16 has
+  if constexpr (ZK != WG_ZERO_F16)
+    if (P <= 128) return launch_mfma<ZK, 8, 16, ZK == WG_ZERO_8 ? 2 : 1>(w, x, M, ldx, y, ldy, e, s);
   return -1;
 }
 
