@@ -116,19 +116,23 @@ def test_head_prep(hip, H, KV, hd, R, norm, pos0):
     assert not np.any(kcn[pos0 + M:])
 
 
-@pytest.fixture(params=["one-launch", "one-launch-1", "one-launch-2", "one-launch-4",
+@pytest.fixture(params=["mfma", "one-launch", "one-launch-1", "one-launch-2", "one-launch-4",
                         "two-launch"])
 def decode_path(request):
-    """wg_attn_decode's forms: one launch (chunks a workgroup chosen, or
-    1, 2, 4), or chunks then a combine."""
+    """wg_attn_decode's forms: one launch on MFMA, one launch on vector
+    units (chunks a workgroup chosen, or 1, 2, 4), or chunks then a
+    combine."""
     from webgllm_amd import lib as L
-    old = (L.tuning_get("attn_fused"), L.tuning_get("attn_split_chunks"))
+    old = (L.tuning_get("attn_mfma"), L.tuning_get("attn_fused"),
+           L.tuning_get("attn_split_chunks"))
     name = request.param
+    L.tuning_set("attn_mfma", 2 if name == "mfma" else 0)
     L.tuning_set("attn_fused", 0 if name == "two-launch" else 2)
     L.tuning_set("attn_split_chunks", int(name[-1]) if name[-1].isdigit() else 0)
     yield name
-    L.tuning_set("attn_fused", old[0])
-    L.tuning_set("attn_split_chunks", old[1])
+    L.tuning_set("attn_mfma", old[0])
+    L.tuning_set("attn_fused", old[1])
+    L.tuning_set("attn_split_chunks", old[2])
 
 
 @pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (32, 8, 128), (32, 8, 64)])

@@ -278,6 +278,78 @@ __device__ inline void settle(T &v) {
   asm volatile("" : "+v"(v));
 }
 
+// attendPanelCombine of one query's `live` split partials (rows of
+// split_row(HD) floats from pr, written with coherent stores) into its HD
+// output halves at op: the wave's lanes, every load of a batch issued
+// before the wait.
+template <int HD>
+__device__ inline void combine_splits(const float *pr, int live, uint16_t *op) {
+  constexpr int SR = split_row(HD);
+  const int lane = threadIdx.x & 63;
+  // BT splits at a time: lane
+  // (t, h) with t = lane / LPS and h = lane % LPS holds dims 4h..4h+3 of
+  // split t + TS i; lane t < BT holds split t's max and sum. Every load of
+  // a batch is issued before the wait.
+  constexpr int LPS = HD / 4;      // lanes a split's values take
+  constexpr int TS = 64 / LPS;     // splits one load instruction covers
+  constexpr int BT = 4096 / HD;    // splits a batch (16 value loads a lane)
+  constexpr int NL = BT / TS;      // value loads a lane issues a batch
+  const int th = lane / LPS, dh = (lane % LPS) * 4;
+  float gmax = -INFINITY, ltot = 0.0f;
+  f4v o = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t0 = 0; t0 < live; t0 += BT) {
+    const int n = min(BT, live - t0);
+    f4v v[NL];
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int t = t0 + min(th + TS * i, n - 1);
+      v[i] = load_sc1(pr + (int64_t)t * SR + 4 + dh);
+    }
+    f2v ml = load2_sc1(pr + (int64_t)(t0 + min(lane, n - 1)) * SR);
+    wait_vm<0>();
+    settle(ml);
+#pragma unroll
+    for (int i = 0; i < NL; i++) settle(v[i]);
+    const float mt = lane < n ? ml.x : -INFINITY;
+    float bmax = mt;
+    bmax = wave_max(bmax);
+    const float nmax = fmaxf(gmax, bmax);
+    if (nmax == -INFINITY) continue;  // nothing visible yet
+    const float alpha = gmax == -INFINITY ? 0.0f : __expf(gmax - nmax);
+    const float w = mt == -INFINITY ? 0.0f : __expf(mt - nmax);
+    ltot = ltot * alpha + wave_sum(w * (lane < n ? ml.y : 0.0f));
+    o.x *= alpha;
+    o.y *= alpha;
+    o.z *= alpha;
+    o.w *= alpha;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const int t = th + TS * i;  // < 64
+      // every lane takes part in the shuffle: a lane whose split is past
+      // the batch must not leave its source lanes inactive
+      const float ws = __shfl(w, t, 64);
+      const float wt = t < n ? ws : 0.0f;
+      o.x = __builtin_fmaf(wt, v[i].x, o.x);
+      o.y = __builtin_fmaf(wt, v[i].y, o.y);
+      o.z = __builtin_fmaf(wt, v[i].z, o.z);
+      o.w = __builtin_fmaf(wt, v[i].w, o.w);
+    }
+    gmax = nmax;
+  }
+  // lanes holding the same dims (different splits) add up
+  o.x = group_reduce<LPS>(o.x, Plus());
+  o.y = group_reduce<LPS>(o.y, Plus());
+  o.z = group_reduce<LPS>(o.z, Plus());
+  o.w = group_reduce<LPS>(o.w, Plus());
+  const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+  if (lane < LPS) {
+    op += dh;
+    const uint32_t lo = (uint32_t)half_bits(o.x * inv) | ((uint32_t)half_bits(o.y * inv) << 16);
+    const uint32_t hi = (uint32_t)half_bits(o.z * inv) | ((uint32_t)half_bits(o.w * inv) << 16);
+    *reinterpret_cast<uint2 *>(op) = make_uint2(lo, hi);
+  }
+}
+
 template <int HD, int NCH>
 __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
     const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
@@ -410,68 +482,305 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   if (threadIdx.x == 0)
     __hip_atomic_store(counters + kh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  // attendPanelCombine for this wave's query, BT splits at a time: lane
-  // (t, h) with t = lane / LPS and h = lane % LPS holds dims 4h..4h+3 of
-  // split t + TS i; lane t < BT holds split t's max and sum. Every load of
-  // a batch is issued before the wait.
-  constexpr int LPS = HD / 4;      // lanes a split's values take
-  constexpr int TS = 64 / LPS;     // splits one load instruction covers
-  constexpr int BT = 4096 / HD;    // splits a batch (16 value loads a lane)
-  constexpr int NL = BT / TS;      // value loads a lane issues a batch
-  const float *pr = partial + (int64_t)qrow * splits * SR;
-  const int th = lane / LPS, dh = (lane % LPS) * 4;
-  float gmax = -INFINITY, ltot = 0.0f;
-  f4v o = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int t0 = 0; t0 < live; t0 += BT) {
-    const int n = min(BT, live - t0);
-    f4v v[NL];
+  combine_splits<HD>(partial + (int64_t)qrow * splits * SR, live,
+                    out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD);
+}
+
+// Decode attention in one launch on MFMA, for any number of queries per KV
+// head (G M: a decode step's G heads, or a verify batch's G M). Workgroup
+// = (KV head kh, group qg of 16 of its queries, split s of AW CPW chunks of
+// 32 keys); its AW waves each take CPW consecutive chunks and run
+// attendPanel's online softmax over them alone:
+//  - a chunk's K and V tiles go to the wave's own LDS by direct loads (16-byte
+//    pieces of row r at slot piece ^ swz(r), for both), the lane offsets
+//    computed once, the chunk's row in a scalar base;
+//  - scores as S^T = K Q^T (v_mfma_f32_16x16x32_f16): A = 16 key rows of the
+//    K tile, B = the group's 16 queries, each split into hi = half(q) and lo
+//    = half(q - hi) (two MFMAs: the scores keep ~22 bits). Lane l then holds
+//    keys 4 (l / 16) .. + 3 of a 16-key tile for query l % 16, so a query's
+//    max and sum are in-lane plus two lane swaps;
+//  - weighted values as O^T = V^T P^T: A = V^T, 16 dims by 32 keys, read by
+//    two transposing LDS loads (ds_read_b64_tr_b16: lane i of each 16 gets
+//    element i % 4 of the 8 bytes lane 4 j + i / 4 addresses, as its element
+//    j), B = the weights split hi / lo, through a small per-wave LDS buffer;
+//  - the waves' (max, sum, values) merge in LDS; the workgroup publishes the
+//    split's partial with coherent stores, one relaxed atomic counts it in,
+//    and the workgroup that completes the count combines the group's
+//    queries, a wave each (combine_splits), as attn_split_kernel does.
+// K rows past the cache read the chunk's first row; V rows at or past the
+// last position are zeroed in LDS (a zero weight times a NaN is NaN); the
+// keys past a query's position are masked.
+constexpr int AW = 4;    // waves a workgroup
+constexpr int AWK = 32;  // keys a wave's chunk
+
+template <int HD>
+__host__ __device__ constexpr int amfma_wave_bytes() {
+  return 2 * AWK * HD * 2 + 16 * 36 * 4;  // K and V tiles, the weights (16 x 36 floats)
+}
+
+template <int HD>
+__global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
+    const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
+    const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int splits,
+    int cpw, int *counters, uint16_t *out, int ldo) {
+  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+  typedef short short4v __attribute__((ext_vector_type(4)));
+  constexpr int KP = HD / 8, ROWB = HD * 2, TILE = AWK * ROWB, RPI = 64 / KP, NI = AWK / RPI;
+  constexpr int QS = HD / 32;  // 32-dim steps of the scores
+  constexpr int DT = HD / 16;  // 16-dim tiles of the values
+  constexpr int SR = split_row(HD);
+  constexpr int WB = amfma_wave_bytes<HD>();
+  constexpr int PS = 36;  // weights row stride (floats)
+  auto swz = [](int r) { return KP == 16 ? (r & 15) : ((r ^ (r >> 3)) & (KP - 1)); };
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int last;
+  const int G = H / KV, GM = G * M;
+  const int QG = (GM + 15) / 16;
+  const int u = blockIdx.x % (KV * QG), s = blockIdx.x / (KV * QG);
+  const int kh = u % KV, qg = u / KV;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n16 = lane & 15, c4 = lane >> 4;
+  const int kvd = KV * HD;
+  unsigned char *wbase = smem + wave * WB;
+  unsigned char *kt = wbase, *vt = wbase + TILE;
+  float *pbuf = reinterpret_cast<float *>(wbase + 2 * TILE);
+  const uint32_t wlds = (uint32_t)(uintptr_t)wbase;
+  const int SPLIT = AW * cpw * AWK;  // keys a workgroup takes
+  const int j0w = s * SPLIT + wave * cpw * AWK;
+
+  // This lane's byte offset, from a chunk's first row, of its piece of each
+  // load instruction (K and V alike): row ii RPI + lane / KP, piece
+  // (lane % KP) ^ swz(row).
+  uint32_t loff[NI];
 #pragma unroll
-    for (int i = 0; i < NL; i++) {
-      const int t = t0 + min(th + TS * i, n - 1);
-      v[i] = load_sc1(pr + (int64_t)t * SR + 4 + dh);
-    }
-    f2v ml = load2_sc1(pr + (int64_t)(t0 + min(lane, n - 1)) * SR);
-    wait_vm<0>();
-    settle(ml);
-#pragma unroll
-    for (int i = 0; i < NL; i++) settle(v[i]);
-    const float mt = lane < n ? ml.x : -INFINITY;
-    float bmax = mt;
-    bmax = wave_max(bmax);
-    const float nmax = fmaxf(gmax, bmax);
-    if (nmax == -INFINITY) continue;  // nothing visible yet
-    const float alpha = gmax == -INFINITY ? 0.0f : __expf(gmax - nmax);
-    const float w = mt == -INFINITY ? 0.0f : __expf(mt - nmax);
-    ltot = ltot * alpha + wave_sum(w * (lane < n ? ml.y : 0.0f));
-    o.x *= alpha;
-    o.y *= alpha;
-    o.z *= alpha;
-    o.w *= alpha;
-#pragma unroll
-    for (int i = 0; i < NL; i++) {
-      const int t = th + TS * i;  // < 64
-      // every lane takes part in the shuffle: a lane whose split is past
-      // the batch must not leave its source lanes inactive
-      const float ws = __shfl(w, t, 64);
-      const float wt = t < n ? ws : 0.0f;
-      o.x = __builtin_fmaf(wt, v[i].x, o.x);
-      o.y = __builtin_fmaf(wt, v[i].y, o.y);
-      o.z = __builtin_fmaf(wt, v[i].z, o.z);
-      o.w = __builtin_fmaf(wt, v[i].w, o.w);
-    }
-    gmax = nmax;
+  for (int ii = 0; ii < NI; ii++) {
+    const int r = ii * RPI + lane / KP;
+    loff[ii] = (uint32_t)(r * kvd + ((lane % KP) ^ swz(r)) * 8) * 2u;
   }
-  // lanes holding the same dims (different splits) add up
-  o.x = group_reduce<LPS>(o.x, Plus());
-  o.y = group_reduce<LPS>(o.y, Plus());
-  o.z = group_reduce<LPS>(o.z, Plus());
-  o.w = group_reduce<LPS>(o.w, Plus());
-  const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
-  if (lane < LPS) {
-    uint16_t *op = out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD + dh;
-    const uint32_t lo = (uint32_t)half_bits(o.x * inv) | ((uint32_t)half_bits(o.y * inv) << 16);
-    const uint32_t hi = (uint32_t)half_bits(o.z * inv) | ((uint32_t)half_bits(o.w * inv) << 16);
-    *reinterpret_cast<uint2 *>(op) = make_uint2(lo, hi);
+  auto issue = [&](int j0) {  // chunk j0's K and V tiles, 2 NI instructions
+    if (j0 + AWK <= max_keys) {
+      const uint16_t *kb = k_cache + (int64_t)j0 * kvd + kh * HD;
+      const uint16_t *vb = v_cache + (int64_t)j0 * kvd + kh * HD;
+#pragma unroll
+      for (int ii = 0; ii < NI; ii++) dma16(kb, loff[ii], wlds + ii * 1024);
+#pragma unroll
+      for (int ii = 0; ii < NI; ii++) dma16(vb, loff[ii], wlds + TILE + ii * 1024);
+    } else {  // the cache's last, partial chunk: rows past it read row j0
+#pragma unroll
+      for (int i = 0; i < 2 * NI; i++) {
+        const bool is_v = i >= NI;
+        const int ii = is_v ? i - NI : i;
+        const int r = ii * RPI + lane / KP;
+        const int piece = (lane % KP) ^ swz(r);
+        const int row = j0 + r < max_keys ? j0 + r : j0;
+        dma16((is_v ? v_cache : k_cache) + (int64_t)row * kvd + kh * HD + piece * 8,
+              wlds + (is_v ? TILE : 0) + ii * 1024);
+      }
+    }
+  };
+  // this lane's query (column n16 of every tile)
+  const int qi = qg * 16 + n16;
+  const bool qvalid = qi < GM;
+  const int qm = qvalid ? qi / G : 0, qh = qvalid ? qi % G : 0;
+  // the wave's first chunk goes out before the position is read; every
+  // exit below waits for it (LDS still being written must not pass to the
+  // next workgroup)
+  if (j0w < max_keys) issue(j0w);
+  const int pos0 = *pos0_dev;
+  const int n_keys = min(pos0 + M, max_keys);
+  const int live = n_keys <= 0 ? 0 : (n_keys + SPLIT - 1) / SPLIT;  // splits with a visible key
+  if (n_keys <= 0) {  // no position in the cache: the output is zero
+    wait_vm<0>();
+    if (s == 0 && qvalid && c4 == 0) {
+      uint16_t *o = out + (int64_t)qm * ldo + (int64_t)(kh * G + qh) * HD;
+      for (int d = 0; d < HD; d++) o[d] = 0;
+    }
+    return;
+  }
+  if (s >= live) {
+    wait_vm<0>();
+    return;
+  }
+  const int nch = max(0, min(cpw, (n_keys - j0w + AWK - 1) / AWK));  // this wave's chunks
+
+  // the queries as B operands, hi and lo halves: dims 32 t + 8 c4 .. + 7
+  half8 qhi[QS], qlo[QS];
+  {
+    const float *qp = q + (int64_t)qm * ldq + (int64_t)(kh * G + qh) * HD + 8 * c4;
+#pragma unroll
+    for (int t = 0; t < QS; t++) {
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+      if (qvalid) {
+        a = *reinterpret_cast<const float4 *>(qp + 32 * t);
+        b = *reinterpret_cast<const float4 *>(qp + 32 * t + 4);
+      }
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const _Float16 hi = (_Float16)v[e];
+        qhi[t][e] = hi;
+        qlo[t][e] = (_Float16)(v[e] - (float)hi);
+      }
+    }
+  }
+  const int q_last = pos0 + qm;  // the last key this query sees
+  float m_run = -INFINITY, l_run = 0.0f;
+  f4v o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; dt++) o[dt] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int ci = 0; ci < nch; ci++) {
+    const int j0 = j0w + ci * AWK;
+    wait_vm<0>();
+    asm volatile("" ::: "memory");
+    if (j0 + AWK > n_keys) {  // V rows at or past the last position read as zero
+      const int nv = n_keys - j0;
+      for (int idx = nv * KP + lane; idx < AWK * KP; idx += 64)
+        *reinterpret_cast<uint4 *>(vt + idx * 16) = make_uint4(0u, 0u, 0u, 0u);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      asm volatile("" ::: "memory");
+    }
+    float sc[2][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; kt2++) {
+      f4v st = {0.0f, 0.0f, 0.0f, 0.0f};
+      const int r = 16 * kt2 + n16;
+#pragma unroll
+      for (int t = 0; t < QS; t++) {
+        const half8 ka =
+            *reinterpret_cast<const half8 *>(kt + r * ROWB + (((4 * t + c4) ^ swz(r)) * 16));
+        st = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi[t], st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo[t], st, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int key = j0 + 16 * kt2 + 4 * c4 + i;
+        const bool vis = qvalid && key <= q_last && key < max_keys;
+        sc[kt2][i] = vis ? st[i] : -INFINITY;
+        tmax = fmaxf(tmax, sc[kt2][i]);
+      }
+    }
+    tmax = fmaxf(tmax, xor16(tmax));
+    tmax = fmaxf(tmax, xor32(tmax));
+    const float m_new = fmaxf(m_run, tmax);
+    float psum = 0.0f;
+    const float corr = m_run == -INFINITY ? 0.0f : __expf(m_run - m_new);
+#pragma unroll
+    for (int kt2 = 0; kt2 < 2; kt2++) {
+      f4v pv;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        pv[i] = sc[kt2][i] == -INFINITY ? 0.0f : __expf(sc[kt2][i] - m_new);
+        psum += pv[i];
+      }
+      *reinterpret_cast<f4v *>(pbuf + n16 * PS + 16 * kt2 + 4 * c4) = pv;
+    }
+    psum += xor16(psum);
+    psum += xor32(psum);
+    if (m_new != -INFINITY) {
+      l_run = l_run * corr + psum;
+#pragma unroll
+      for (int dt = 0; dt < DT; dt++) o[dt] *= corr;
+    }
+    m_run = m_new;
+    // every lane's weights are in LDS before any lane reads another's
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("" ::: "memory");
+    {
+      const f4v pa = *reinterpret_cast<const f4v *>(pbuf + n16 * PS + 8 * c4);
+      const f4v pb = *reinterpret_cast<const f4v *>(pbuf + n16 * PS + 8 * c4 + 4);
+      half8 phi, plo;
+      const float pw[8] = {pa[0], pa[1], pa[2], pa[3], pb[0], pb[1], pb[2], pb[3]};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const _Float16 hi = (_Float16)pw[e];
+        phi[e] = hi;
+        plo[e] = (_Float16)(pw[e] - (float)hi);
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; dt++) {
+        half8 va;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+          // source lane n16 of this 16: row 8 c4 + 4 hh + n16 / 4, dims
+          // 16 dt + 4 (n16 % 4) .. + 3
+          const int r = 8 * c4 + 4 * hh + (n16 >> 2);
+          const int col = 16 * dt + 4 * (n16 & 3);
+          const unsigned char *a = vt + r * ROWB + (((col >> 3) ^ swz(r)) * 16) + (col & 7) * 2;
+          const short4v t4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) short4v *)(uint32_t)(uintptr_t)a);
+          const half4 h4 = __builtin_bit_cast(half4, t4);
+#pragma unroll
+          for (int e = 0; e < 4; e++) va[4 * hh + e] = h4[e];
+        }
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, phi, o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, plo, o[dt], 0, 0, 0);
+      }
+    }
+    // the next chunk's loads may overwrite the tiles: every read of them is done
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("" ::: "memory");
+    if (ci + 1 < nch) issue(j0 + AWK);
+  }
+
+  // The waves' partials merge in LDS (the tiles are free): wave w > 0 leaves
+  // its lane's (max, sum) and DT value quads; wave 0 merges them.
+  constexpr int MW = 64 * (4 * DT + 2);  // floats a wave leaves
+  static_assert((AW - 1) * MW * 4 <= WB * AW, "merge area");
+  float *mrg = reinterpret_cast<float *>(smem);
+  wait_vm<0>();  // a first chunk past the position was loaded and not read
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  barrier();
+  if (wave > 0) {
+    float *mw = mrg + (wave - 1) * MW;
+    mw[lane] = m_run;
+    mw[64 + lane] = l_run;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+      *reinterpret_cast<f4v *>(mw + 128 + (dt * 64 + lane) * 4) = o[dt];
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  barrier();
+  float *po = partial + ((int64_t)(qm * H + kh * G + qh) * splits + s) * SR;
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 1; w < AW; w++) {
+      const float *mw = mrg + (w - 1) * MW;
+      const float m2 = mw[lane], l2 = mw[64 + lane];
+      const float mx = fmaxf(m_run, m2);
+      const float a1 = m_run == -INFINITY ? 0.0f : __expf(m_run - mx);
+      const float a2 = m2 == -INFINITY ? 0.0f : __expf(m2 - mx);
+      l_run = l_run * a1 + l2 * a2;
+#pragma unroll
+      for (int dt = 0; dt < DT; dt++)
+        o[dt] = o[dt] * a1 + *reinterpret_cast<const f4v *>(mw + 128 + (dt * 64 + lane) * 4) * a2;
+      m_run = mx;
+    }
+    if (qvalid) {  // lane (query, c4) holds dims 16 dt + 4 c4 .. + 3
+#pragma unroll
+      for (int dt = 0; dt < DT; dt++) store_sc1(po + 4 + 16 * dt + 4 * c4, o[dt]);
+      if (c4 == 0) store_sc1(po, f4v{m_run, l_run, 0.0f, 0.0f});
+    }
+    wait_vm<0>();  // this wave's coherent stores are done
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(counters + u, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           live - 1;
+  __syncthreads();
+  if (!last) return;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(counters + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the group's queries, a wave each in turn
+  for (int k = wave; k < 16; k += AW) {
+    const int qk = qg * 16 + k;
+    if (qk >= GM) break;
+    const int mk = qk / G, gk = qk % G;
+    combine_splits<HD>(partial + (int64_t)(mk * H + kh * G + gk) * splits * SR, live,
+                       out + (int64_t)mk * ldo + (int64_t)(kh * G + gk) * HD);
   }
 }
 
@@ -1039,7 +1348,16 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
                               (fused_knob == 1 && (max_keys <= 1024 || max_keys > MAX_CH * CHUNK)));
   // the one-launch form combines any number of splits; the two-launch
   // combine holds MAX_CH chunks
-  const int key_cap = fused ? MAX_FUSED_KEYS : MAX_CH * CHUNK;
+  // The MFMA form is taken for more than FGM queries a KV head (a verify
+  // batch; measured 3% faster there at 1024 cached keys than the chunk and
+  // combine kernels); for a decode step's few queries its serial tail
+  // (coherent stores, the count, the last workgroup's combine) costs more
+  // than the second launch it saves (13.4 us against 7.2 + 4.1 at 4096 keys,
+  // 32 heads of 128 over 8). attn_mfma 2 always takes it, 0 never.
+  const int mfma_knob = tuning("attn_mfma");
+  const bool amfma = KV * (((H / KV) * M + 15) / 16) <= MAX_KV_COUNTERS &&
+                     (mfma_knob == 2 || (mfma_knob == 1 && (H / KV) * M > FGM));
+  const int key_cap = fused || amfma ? MAX_FUSED_KEYS : MAX_CH * CHUNK;
   WG_REQUIRE(max_keys >= M && max_keys <= key_cap,
              "wg_attn_decode: max_keys %d (rows %d; at most %d)", max_keys, M, key_cap);
   WG_REQUIRE(ldq >= H * hd && ldo >= H * hd, "wg_attn_decode: strides too small");
@@ -1052,6 +1370,31 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
   int *counters = (int *)scratch;
   float *partial = (float *)((char *)scratch + COUNTER_BYTES);
   const int chunks = (max_keys + CHUNK - 1) / CHUNK;
+  const int QG = ((H / KV) * M + 15) / 16;  // groups of 16 queries a KV head
+  if (amfma) {
+    // one launch on MFMA: cpw chunks a wave, as few as keep about one
+    // workgroup a compute unit
+    const int cus = persistent_grid(1 << 30, 1);
+    const int units = KV * QG;
+    const int wchunks = (max_keys + AWK - 1) / AWK;  // 32-key chunks
+    int cpw = (int)(((int64_t)wchunks * units + (int64_t)AW * cus - 1) / ((int64_t)AW * cus));
+    cpw = cpw < 1 ? 1 : cpw;
+    const int splits = (wchunks + AW * cpw - 1) / (AW * cpw);
+    const size_t lds = (size_t)AW * (hd == 64 ? amfma_wave_bytes<64>() : amfma_wave_bytes<128>());
+    const dim3 grid((unsigned)(units * splits));
+#define WG_AMFMA_LAUNCH(HDV)                                                                    \
+  do {                                                                                          \
+    int rc_ = raise_lds((const void *)attn_mfma_kernel<HDV>, (int)lds);                           \
+    if (rc_) return rc_;                                                                        \
+    attn_mfma_kernel<HDV><<<grid, AW * 64, lds, s>>>(q, ldq, M, H, KV, k_cache, v_cache, pos0,    \
+                                                    max_keys, partial, splits, cpw, counters,    \
+                                                    out, ldo);                                   \
+  } while (0)
+    if (hd == 64) WG_AMFMA_LAUNCH(64);
+    else WG_AMFMA_LAUNCH(128);
+#undef WG_AMFMA_LAUNCH
+    return launched("wg_attn_decode");
+  }
   if (fused) {
     // one launch: 64 * nch keys a workgroup, the smallest nch (1, 2, 4) that
     // keeps the grid to about one workgroup a compute unit
