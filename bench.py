@@ -418,6 +418,8 @@ def decode_engine_run(shape, ctx, prompt_len, steps, warmup, persistent=False):
     prompt = torch.randint(0, shape.vocab, (prompt_len,),
                            generator=torch.Generator().manual_seed(1)).tolist()
     first = int(eng.forward(prompt)[-1])
+    # the timed replays run past what decode() reserves: room for all of them
+    eng.reserve(min(ctx, eng.position + warmup + steps + 1))
     eng.capture_step(first)
     eng.decode(first, warmup)
     p0 = eng.position
@@ -497,6 +499,7 @@ def workload_lfm2_verify(args):
     # the device loop: every step one graph replay (drafts from a device
     # table; the picks, accept and conv-state rollback on the device), the
     # kept counts read back once after the timed steps
+    eng.reserve(min(ctx, eng.position + 5 * (args.warmup + steps)))
     eng.capture_verify(5)
     v = eng._verify
     eng.ids[0] = token
@@ -1073,6 +1076,8 @@ def main():
     rng = torch.Generator().manual_seed(1)
     prompt = torch.randint(0, shape.vocab, (prompt_len,), generator=rng).tolist()
     picks = eng.forward(prompt)
+    # the timed replays run past what decode() reserves: room for all of them
+    eng.reserve(args.ctx)
     torch.cuda.synchronize()
     t_prefill = time.time() - t0
     first = int(picks[-1])

@@ -379,3 +379,63 @@ def test_graph_verify_equals_host_verify(hip, family, table, monkeypatch):
     # and it goes on from there as sequential decoding does
     assert eng2.decode(tokens[-1], 4) == truth[len(written):len(written) + 4]
 
+
+
+def test_cache_grows_on_demand(hip):
+    """The attention caches start at KV_START positions and grow as the
+    prompt and the decode need them (whole KV_STEP steps, at least doubling):
+    the rows already written are kept, the decode graph captured over the
+    smaller caches is captured again, and the tokens are the oracle
+    decoder's across the growth; reset shrinks the caches back."""
+    from webgllm_amd import engine as E
+    eng, orc = _pair("lfm2-q4_0", seed=2, ctx=3000)
+    assert eng.kv_positions == E.KV_START == 1024
+    rng = np.random.default_rng(9)
+    prompt = _prompt(rng, 1016, eng.shape.vocab)
+    picks = eng.forward(prompt).cpu().numpy()
+    assert eng.kv_positions == 1024
+    _, picks_o = orc.forward(prompt, f16_weights=eng._prefill_ok(), batch=128)
+    assert list(picks) == list(picks_o)
+    first = int(picks[-1])
+    toks = eng.decode(first, 4)
+    assert eng.kv_positions == 1024
+    layer = next(iter(eng.k_cache))
+    kept_k = eng.k_cache[layer][:1020].clone()
+    kept_v = eng.v_cache[layer][:1020].clone()
+    graph = eng.graph
+    toks += eng.decode(toks[-1], 12)  # positions 1020 .. 1031: 2048 positions
+    assert eng.kv_positions == 2048 and eng.graph is not graph
+    assert torch.equal(eng.k_cache[layer][:1020], kept_k)
+    assert torch.equal(eng.v_cache[layer][:1020], kept_v)
+    assert toks == orc.decode(first, 16)
+    with pytest.raises(ValueError, match="holds 3000 tokens"):
+        eng.reserve(3001)
+    eng.reset()
+    orc.reset()
+    assert eng.kv_positions == 1024
+    short = _prompt(rng, 12, eng.shape.vocab)
+    first = int(eng.forward(short).cpu()[-1])
+    orc.forward(short)
+    assert eng.decode(first, 6) == orc.decode(first, 6)
+
+
+@pytest.mark.parametrize("family", ["lfm2-q4_0", "llama-q4_k"])
+def test_verify_grows_the_cache(hip, family):
+    """Verify steps whose run passes the caches' size: the run reserves its
+    room first (the verify graph captured again over the new caches) and
+    writes the host loop's tokens, which are the oracle decoder's."""
+    eng, orc = _pair(family, seed=4, ctx=2048)
+    rng = np.random.default_rng(6)
+    prompt = _prompt(rng, 1018, eng.shape.vocab)
+    token = int(eng.forward(prompt).cpu()[-1])
+    orc.forward(prompt, f16_weights=eng._prefill_ok(), batch=128)
+    truth = orc.decode(token, 64)
+    written, kept, fed = _host_verify_recording(eng, token, truth, rng, 12)
+    assert written == truth[:len(written)]
+    eng2, _ = _pair(family, seed=4, ctx=2048)
+    eng2.forward(prompt)
+    eng2.capture_verify(5)  # over the 1024-position caches
+    assert eng2.kv_positions == 1024
+    tokens, kept2 = eng2.verify_drafts(token, fed)
+    assert eng2.kv_positions == 2048
+    assert kept2 == kept and tokens == written

@@ -30,6 +30,11 @@ from . import ops
 MAX_ROWS = 8
 PREFILL_ROWS = 2048  # prompt rows a GEMM batch takes
 PRESCALE = 32.0  # the reference's PRESCALE (src/gpu/kernels.ts:89)
+# The attention caches start at KV_START positions (the reference's
+# KV_START, src/engine.ts:911) and grow in whole KV_STEP steps (TUNING.kvStep,
+# :614) as tokens need them.
+KV_START = 1024
+KV_STEP = 512
 
 
 def qkv_row_order(shape) -> list:
@@ -248,20 +253,21 @@ class Engine:
         self.argmax_scratch = torch.empty(L.load().wg_argmax_scratch_bytes(R, s.vocab),
                                           dtype=torch.uint8, device=dev)
         self.attn = ops.attn_shape(s.heads, s.kv_heads, s.head_dim, s.head_dim, s.eps, s.qk_norm)
-        self.attn_scratch = ops.attn_scratch(R, self.attn, ctx, dev)
         self.rope = _rope_table(s.rope_theta, s.head_dim, ctx).to(dev)
         self.k_cache, self.v_cache, self.state, self.prefixes = {}, {}, {}, {}
         for i in range(s.layers):
             if s.layer_type(i) == "conv":
                 self.state[i] = torch.zeros((s.conv_kernel - 1, D), dtype=f32, device=dev)
                 self.prefixes[i] = torch.zeros((R, s.conv_kernel - 1, D), dtype=f32, device=dev)
-            else:
-                kvd = s.kv_heads * s.head_dim
-                self.k_cache[i] = torch.zeros((ctx, kvd), dtype=f16, device=dev)
-                self.v_cache[i] = torch.zeros((ctx, kvd), dtype=f16, device=dev)
+        # the attention caches ([kv_positions][kv_heads * head_dim] halves a
+        # layer) and the attention scratch for that many keys: grown by reserve
+        self.kv_positions = 0
+        self.graph = None
+        self.plan = None
+        self._verify = None
+        self._resize_caches(min(ctx, KV_START), keep=0)
         self.position = 0
         self.draft = None
-        self.graph = None
         self._pre = None  # prefill buffers, made on the first prompt batch
         self._cols = {}   # device row orders of the matrices (GEMM column maps)
         # persistent=True: single-row forwards of attention-only models run as
@@ -269,7 +275,46 @@ class Engine:
         # default, take the per-op path. On MI355X a grid barrier costs about
         # as much as a kernel boundary (~4 us), so the per-op path is the
         # faster one at the Llama-3-8B shape.
+        self.persistent = persistent
         self.plan = self._build_plan() if persistent else None
+
+    # --- the attention caches, grown on demand ------------------------------
+    def reserve(self, end: int) -> None:
+        """Makes room in the attention caches for positions up to `end`
+        (Engine.reserve, src/engine.ts:1635-1696): new caches of whole
+        KV_STEP steps, at least twice the positions they replace (the copies
+        then add up to at most the final size: a 128K-token context is not
+        copied 250 times over), at most the context, holding the old rows.
+        The captured decode and verify graphs and the persistent plan hold
+        the old caches' addresses: they are dropped (captured again when
+        next used) or rebuilt."""
+        if end > self.ctx:
+            raise ValueError(f"The cache holds {self.ctx} tokens; this would need {end}.")
+        if end <= self.kv_positions:
+            return
+        n = min(self.ctx, max(-(-end // KV_STEP) * KV_STEP, 2 * self.kv_positions))
+        self._resize_caches(n, keep=self.kv_positions)
+
+    def _resize_caches(self, n: int, keep: int) -> None:
+        """Caches of n positions holding the first `keep` rows of the old
+        ones (the rest zero), and attention scratch for n keys."""
+        s, dev = self.shape, self.device
+        kvd = s.kv_heads * s.head_dim
+        for cache in (self.k_cache, self.v_cache):
+            for i in range(s.layers):
+                if s.layer_type(i) == "conv":
+                    continue
+                new = torch.zeros((n, kvd), dtype=torch.float16, device=dev)
+                if keep:
+                    new[:keep].copy_(cache[i][:keep])
+                cache[i] = new
+        self.attn_scratch = ops.attn_scratch(MAX_ROWS, self.attn, n, dev)
+        self.kv_positions = n
+        self.graph = None
+        if self._verify is not None:
+            self._verify["graph"] = None
+        if self.plan is not None:
+            self.plan = self._build_plan()
 
     # --- the batch ------------------------------------------------------------
     def _norm_in(self, ep: "L.Epilogue") -> "L.Epilogue":
@@ -296,7 +341,7 @@ class Engine:
         s = self.shape
         return self._norm_in(L.Epilogue(
             mode=L.EPI_ROPE_KV, heads=s.heads, kv_heads=s.kv_heads,
-            head_dim=s.head_dim, ctx=self.ctx, rope_rows=self.rope.shape[0],
+            head_dim=s.head_dim, ctx=self.kv_positions, rope_rows=self.rope.shape[0],
             rope=self.rope.data_ptr(), pos0=self.pos.data_ptr(),
             q_out=self.q.data_ptr(), ld_q_out=s.heads * s.head_dim,
             k_cache=self.k_cache[i].data_ptr(), v_cache=self.v_cache[i].data_ptr()))
@@ -491,11 +536,16 @@ class Engine:
 
     # --- the reference's Engine API -------------------------------------------
     def reset(self) -> None:
+        """A new sequence: position 0, conv states cleared, the caches back
+        to their starting size (shrink, src/engine.ts:1709-1719)."""
         self.position = 0
         self.pos.zero_()
         for st in self.state.values():
             st.zero_()
         self.draft = None
+        start = min(self.ctx, KV_START)
+        if self.kv_positions > start:
+            self._resize_caches(start, keep=0)
 
     def forward(self, tokens, draft: bool = False) -> torch.Tensor:
         """Runs tokens (a prompt in batches of 8, or a token and its drafts)
@@ -508,6 +558,8 @@ class Engine:
                              f"{self.position + len(tokens)}.")
         if draft and len(tokens) > MAX_ROWS:
             raise ValueError(f"A draft batch holds {MAX_ROWS} tokens at most.")
+        # the whole prompt's room at once (preparePrompt, src/engine.ts:1699-1704)
+        self.reserve(self.position + len(tokens))
         out = None
         # a prompt's leading rows in GEMM batches; its last (up to 8) rows, whose
         # picks are returned, through the few-token path
@@ -566,6 +618,7 @@ class Engine:
         ids[0] = token at pos = position (the token the first replay will
         run): that run writes this position's K and V, which the first replay
         writes again, and everything else it changes is put back."""
+        self.reserve(self.position + 1)
         self.ids[0] = token
         self.pos.fill_(self.position)
         stream = torch.cuda.Stream(device=self.device)
@@ -605,6 +658,7 @@ class Engine:
         """Greedy decode `steps` tokens after `first_token` by graph replay."""
         if self.position + steps > self.ctx:
             raise ValueError("decode would run past the cache")
+        self.reserve(self.position + steps)
         if self.graph is None:
             self.capture_step(first_token)
         p0 = self.position
@@ -621,7 +675,7 @@ class Engine:
     VERIFY_TABLE = 1024  # draft rows the device table holds (steps a replay run takes)
 
     def _verify_buffers(self, rows: int) -> dict:
-        v = getattr(self, "_verify", None)
+        v = self._verify
         if v is None or v["rows"] != rows:
             dev, i32 = self.device, torch.int32
             layers = [(self.prefixes[i], self.state[i]) for i in sorted(self.state)]
@@ -651,6 +705,7 @@ class Engine:
         replay)."""
         if not 2 <= rows <= MAX_ROWS:
             raise ValueError(f"A verify batch holds 2 to {MAX_ROWS} rows.")
+        self.reserve(self.position + rows)
         v = self._verify_buffers(rows)
         self.pos.fill_(self.position)
         stream = torch.cuda.Stream(device=self.device)
@@ -685,8 +740,6 @@ class Engine:
             raise ValueError("drafts must be [steps, rows - 1]")
         steps, rows = table.shape[0], table.shape[1] + 1
         v = self._verify_buffers(rows)
-        if v["graph"] is None:
-            self.capture_verify(rows)
         p0 = self.position
         self.ids[0] = first_token
         self.pos.fill_(p0)
@@ -698,6 +751,10 @@ class Engine:
             if n <= 0:
                 raise ValueError(f"The cache holds {self.ctx} tokens; verify batches of {rows} "
                                  f"from position {self.position} would pass it.")
+            # room for the run (which drops a graph that held smaller caches)
+            self.reserve(self.position + n * rows)
+            if v["graph"] is None:
+                self.capture_verify(rows)
             v["table"][:n].copy_(table[done:done + n])
             v["cursor"].zero_()
             for _ in range(n):
