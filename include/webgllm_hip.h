@@ -536,14 +536,19 @@ int wg_attn_prefill(const float *q, int32_t M, int32_t ldq, const wg_attn_shape 
  * attends keys 0..*pos0 + m (causal) of its KV head; half output. max_keys
  * is how many rows the caches hold (the position is clamped to it).
  * scratch holds wg_attn_scratch_bytes(M, heads, head_dim, max_keys) bytes:
- * 256 bytes of counters, then per-chunk partial results. The counters must
- * be zero before the first call (a zeroed allocation); every call leaves
- * them zero. Calls that share a scratch must not overlap.
- * With heads / kv_heads * M <= 8 (and kv_heads <= 64) it is one launch: a
- * workgroup per (KV head, split of 64, 128 or 256 keys), a wave per query,
- * the last workgroup of a KV head to finish combining its splits (max_keys
- * up to 2^20). Otherwise two launches, up to 16384 keys: an LDS-staged
- * workgroup per 64-key chunk, then the online-softmax combine. */
+ * counters (wg_attn_scratch_bytes(0, heads, head_dim, 0) bytes), then
+ * per-chunk partial results. The counters must be zero before the first
+ * call (a zeroed allocation); every call leaves them zero. Calls that share
+ * a scratch must not overlap.
+ * With heads / kv_heads * M <= 8 and kv_heads a multiple of 8 it is one
+ * launch (max_keys up to 2^20): a workgroup per (KV head, split of 64, 128
+ * or 256 keys), a wave per query; each of the 8 XCDs takes the KV heads
+ * congruent to its id mod 8, and its last workgroup to finish combines
+ * them from the XCD's L2. Other shapes of up to 8 queries a KV head: one
+ * launch whose last workgroup of a KV head combines its splits (up to 1024
+ * keys and past 16384), else two launches (an LDS-staged workgroup per
+ * 64-key chunk, then the online-softmax combine). More queries a KV head:
+ * one launch on MFMA. */
 size_t wg_attn_scratch_bytes(int32_t M, int32_t heads, int32_t head_dim, int32_t max_keys);
 int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *shape,
                    const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0,
@@ -555,7 +560,7 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
  * harnesses that forbid hipMalloc). The partial results go to a 16 MiB
  * array built into the library, one per GPU, held until the process ends;
  * a request needing more (wg_attn_scratch_bytes(M, heads, head_dim,
- * max_keys) > 16 MiB, e.g. 8 rows of 32 heads of 128 past 8,064 keys) is
+ * max_keys) > 16 MiB, e.g. 8 rows of 32 heads of 128 past 7,936 keys) is
  * rejected with WG_ERR_INVALID before anything runs. Every call on a GPU
  * shares that array: calls that overlap on one GPU (other streams, other
  * threads) race. Same results as wg_attn_decode, bit for bit. */

@@ -116,23 +116,24 @@ def test_head_prep(hip, H, KV, hd, R, norm, pos0):
     assert not np.any(kcn[pos0 + M:])
 
 
-@pytest.fixture(params=["mfma", "one-launch", "one-launch-1", "one-launch-2", "one-launch-4",
-                        "two-launch"])
+@pytest.fixture(params=["mfma", "xcd", "xcd-1", "xcd-4", "one-launch", "one-launch-1",
+                        "one-launch-2", "one-launch-4", "two-launch"])
 def decode_path(request):
-    """wg_attn_decode's forms: one launch on MFMA, one launch on vector
-    units (chunks a workgroup chosen, or 1, 2, 4), or chunks then a
-    combine."""
+    """wg_attn_decode's forms: one launch on MFMA; one launch combined
+    within each XCD (KV heads a multiple of 8; elsewhere the default form);
+    one launch on vector units (chunks a workgroup chosen, or 1, 2, 4); or
+    chunks then a combine."""
     from webgllm_amd import lib as L
-    old = (L.tuning_get("attn_mfma"), L.tuning_get("attn_fused"),
-           L.tuning_get("attn_split_chunks"))
+    knobs = ("attn_mfma", "attn_fused", "attn_split_chunks", "attn_xcd")
+    old = [L.tuning_get(k) for k in knobs]
     name = request.param
     L.tuning_set("attn_mfma", 2 if name == "mfma" else 0)
+    L.tuning_set("attn_xcd", 2 if name.startswith("xcd") else 0)
     L.tuning_set("attn_fused", 0 if name == "two-launch" else 2)
     L.tuning_set("attn_split_chunks", int(name[-1]) if name[-1].isdigit() else 0)
     yield name
-    L.tuning_set("attn_mfma", old[0])
-    L.tuning_set("attn_fused", old[1])
-    L.tuning_set("attn_split_chunks", old[2])
+    for k, v in zip(knobs, old):
+        L.tuning_set(k, v)
 
 
 @pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (32, 8, 128), (32, 8, 64)])
@@ -177,7 +178,9 @@ def test_attn_decode_ignores_rows_past_the_position(hip, decode_path, H, KV, hd,
     q = (rng.standard_normal((M, H * hd)) / math.sqrt(hd) * 2).astype(np.float32)
     scratch = ops.attn_scratch(M, shape, ctx)
     scratch.fill_(0xff)
-    scratch[:256].zero_()
+    # the counters: the scratch of no rows and no keys
+    from webgllm_amd import lib as L
+    scratch[:L.load().wg_attn_scratch_bytes(0, H, hd, 0)].zero_()
     got = _h(ops.attn_decode(_t(q), shape, _t(k.view(np.int16)), _t(v.view(np.int16)),
                              _t(np.array([pos0], np.int32)), scratch=scratch))
     assert np.isfinite(got).all()

@@ -246,8 +246,25 @@ __global__ __launch_bounds__(FGM * 64) void attn_tile_kernel(
 // attendPanelCombine for the KV head's queries, reading every partial at
 // once with coherent vector loads. No workgroup waits on another, so the
 // launch always drains.
+//
+// The XCD-local form (XL) keeps all of that inside one XCD, whose compute
+// units share an L2: KV head kh belongs to XCD kh mod 8 (KV a multiple of
+// 8), and the workgroup with blockIdx b, on XCD x (its hardware XCC id),
+// takes split (b / 8) mod splits of head x + 8 (b / 8 / splits). Workgroups
+// are handed to the XCDs round-robin, so the 8 with the same b / 8 run one
+// on each XCD and every XCD holds grid / 8 of them. The partials are plain
+// stores, which reach the XCD's L2 once the wave's stores are done; one
+// counter per XCD (on its own 256-byte line) counts its workgroups in, and
+// the last one resets it and combines every query of the XCD's heads,
+// reading the partials from that L2 (sc0 loads, past the compute unit's
+// L1). Nothing is written back to memory between the splits and the combine.
 constexpr int MAX_KV_COUNTERS = 64;       // counters at the scratch's start
-constexpr int COUNTER_BYTES = MAX_KV_COUNTERS * 4;
+// then one 256-byte line of counters per XCD (the XCD-local form's), so no
+// two XCDs' L2s ever hold the same counter line
+constexpr int XCDS = 8;
+constexpr int XCD_LINE = 64;              // ints: 256 bytes
+constexpr int COUNTER_INTS = MAX_KV_COUNTERS + XCDS * XCD_LINE;
+constexpr int COUNTER_BYTES = COUNTER_INTS * 4;
 constexpr int MAX_FUSED_KEYS = 1 << 20;   // keys the one-launch form takes
 
 // A split's partial for one query: max, sum, 2 floats of padding, then the
@@ -255,21 +272,36 @@ constexpr int MAX_FUSED_KEYS = 1 << 20;   // keys the one-launch form takes
 __host__ __device__ constexpr int split_row(int hd) { return hd + 4; }
 
 // Coherent (sc1) 16-byte store and loads; a loaded value is ready after
-// wait_vm and settle().
+// wait_vm and settle(). With LOCAL the loads are sc0 ones instead: they miss
+// the compute unit's L1 and are served by the XCD's L2, which holds what
+// the XCD's other compute units stored.
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef float f2v __attribute__((ext_vector_type(2)));
 __device__ inline void store_sc1(float *p, f4v v) {
   asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
+template <bool LOCAL = false>
 __device__ inline f4v load_sc1(const float *p) {
   f4v v;
-  asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
+  if constexpr (LOCAL)
+    asm volatile("global_load_dwordx4 %0, %1, off sc0" : "=v"(v) : "v"(p) : "memory");
+  else
+    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
   return v;
 }
+template <bool LOCAL = false>
 __device__ inline f2v load2_sc1(const float *p) {
   f2v v;
-  asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
+  if constexpr (LOCAL)
+    asm volatile("global_load_dwordx2 %0, %1, off sc0" : "=v"(v) : "v"(p) : "memory");
+  else
+    asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
   return v;
+}
+
+// The XCD this workgroup runs on (hardware register XCC_ID, bits 3:0).
+__device__ inline int xcd_id() {
+  return (int)(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);
 }
 // Ties a value loaded by inline assembly to a wait issued before: its uses
 // come after this point.
@@ -279,10 +311,10 @@ __device__ inline void settle(T &v) {
 }
 
 // attendPanelCombine of one query's `live` split partials (rows of
-// split_row(HD) floats from pr, written with coherent stores) into its HD
-// output halves at op: the wave's lanes, every load of a batch issued
-// before the wait.
-template <int HD>
+// split_row(HD) floats from pr, written with coherent stores, or by the
+// same XCD with LOCAL) into its HD output halves at op: the wave's lanes,
+// every load of a batch issued before the wait.
+template <int HD, bool LOCAL = false>
 __device__ inline void combine_splits(const float *pr, int live, uint16_t *op) {
   constexpr int SR = split_row(HD);
   const int lane = threadIdx.x & 63;
@@ -303,9 +335,9 @@ __device__ inline void combine_splits(const float *pr, int live, uint16_t *op) {
 #pragma unroll
     for (int i = 0; i < NL; i++) {
       const int t = t0 + min(th + TS * i, n - 1);
-      v[i] = load_sc1(pr + (int64_t)t * SR + 4 + dh);
+      v[i] = load_sc1<LOCAL>(pr + (int64_t)t * SR + 4 + dh);
     }
-    f2v ml = load2_sc1(pr + (int64_t)(t0 + min(lane, n - 1)) * SR);
+    f2v ml = load2_sc1<LOCAL>(pr + (int64_t)(t0 + min(lane, n - 1)) * SR);
     wait_vm<0>();
     settle(ml);
 #pragma unroll
@@ -350,7 +382,7 @@ __device__ inline void combine_splits(const float *pr, int live, uint16_t *op) {
   }
 }
 
-template <int HD, int NCH>
+template <int HD, int NCH, bool XL = false>
 __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
     const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
     const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int splits,
@@ -367,7 +399,13 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   auto swz = [](int r) { return KP == 16 ? (r & 15) : ((r ^ (r >> 3)) & (KP - 1)); };
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int last;
-  const int kh = blockIdx.x % KV, s = blockIdx.x / KV;
+  int kh = blockIdx.x % KV, s = blockIdx.x / KV, xcd = 0;
+  if constexpr (XL) {
+    xcd = xcd_id() & (XCDS - 1);  // (0..7 on an 8-XCD part)
+    const int rank = blockIdx.x / XCDS;  // < KV / 8 * splits: the grid is KV * splits
+    kh = xcd + XCDS * (rank / splits);
+    s = rank % splits;
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;  // = G * M
@@ -375,12 +413,15 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   const int j0 = s * SPLIT;  // < max_keys: s < splits
   const int kvd = KV * HD;
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
-  if (lane < HD / 4)
+  // (an XCC id past 7 would name a head past the last: such a workgroup
+  // loads nothing and computes nothing, and its XCD's count never completes)
+  const bool here = !XL || kh < KV;
+  if (here && lane < HD / 4)
     dma16(q + (int64_t)m * ldq + (int64_t)(kh * G + g) * HD + lane * 4,
           __builtin_amdgcn_readfirstlane(sbase + QOFF + wave * HD * 4));
   // rows at or past max_keys do not exist: their lanes load row j0 again,
   // and they are masked below like rows past the position
-  for (int i = wave; i < 2 * NI * NCH; i += nw) {
+  for (int i = wave; here && i < 2 * NI * NCH; i += nw) {
     const int c = i / (2 * NI), ic = i % (2 * NI);
     const bool is_v = ic >= NI;
     const int ii = is_v ? ic - NI : ic;
@@ -396,16 +437,20 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   const int n_keys = min(pos0 + M, max_keys);
   // every load has landed before any wave leaves
   wait_vm<0>();
-  if (n_keys <= 0) {  // no position in the cache: the output is zero
-    if (s == 0) {
-      uint16_t *o = out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD;
-      for (int d = lane; d < HD; d += 64) o[d] = 0;
+  if constexpr (!XL) {
+    if (n_keys <= 0) {  // no position in the cache: the output is zero
+      if (s == 0) {
+        uint16_t *o = out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD;
+        for (int d = lane; d < HD; d += 64) o[d] = 0;
+      }
+      return;
     }
-    return;
   }
-  const int live = (n_keys + SPLIT - 1) / SPLIT;  // splits holding a visible key
-  if (s >= live) return;
+  // splits holding a visible key (none: the combine writes zeros)
+  const int live = n_keys > 0 ? (n_keys + SPLIT - 1) / SPLIT : 0;
+  if (!XL && s >= live) return;
   barrier();
+  if (!XL || (here && s < live)) {
 
   const float4 *ql = reinterpret_cast<const float4 *>(smem + QOFF + wave * HD * 4);
   const int d0 = (lane % KP) * 8;
@@ -466,24 +511,47 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   for (int t = 0; t < 8; t++) acc[t] = group_reduce<KP>(acc[t], Plus());
   const int qrow = m * H + kh * G + g;
   float *po = partial + ((int64_t)qrow * splits + s) * SR;
-  if (lane < KP) {
-    store_sc1(po + 4 + d0, f4v{acc[0], acc[1], acc[2], acc[3]});
-    store_sc1(po + 8 + d0, f4v{acc[4], acc[5], acc[6], acc[7]});
-  } else if (lane == KP) {
-    store_sc1(po, f4v{mrun, lrun, 0.0f, 0.0f});
+  if constexpr (XL) {
+    if (lane < KP) {
+      *reinterpret_cast<f4v *>(po + 4 + d0) = f4v{acc[0], acc[1], acc[2], acc[3]};
+      *reinterpret_cast<f4v *>(po + 8 + d0) = f4v{acc[4], acc[5], acc[6], acc[7]};
+    } else if (lane == KP) {
+      *reinterpret_cast<f4v *>(po) = f4v{mrun, lrun, 0.0f, 0.0f};
+    }
+  } else {
+    if (lane < KP) {
+      store_sc1(po + 4 + d0, f4v{acc[0], acc[1], acc[2], acc[3]});
+      store_sc1(po + 8 + d0, f4v{acc[4], acc[5], acc[6], acc[7]});
+    } else if (lane == KP) {
+      store_sc1(po, f4v{mrun, lrun, 0.0f, 0.0f});
+    }
   }
-  wait_vm<0>();  // this wave's coherent stores are done
+  }  // the split's work
+  wait_vm<0>();  // this wave's stores are done
   __syncthreads();
+  int *count = XL ? counters + MAX_KV_COUNTERS + xcd * XCD_LINE : counters + kh;
+  // XL: every workgroup of the XCD; else the head's live splits
+  const int expect = XL ? (int)(gridDim.x / XCDS) : live;
   if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(counters + kh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           live - 1;
+    last = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           expect - 1;
   __syncthreads();
   if (!last) return;
   if (threadIdx.x == 0)
-    __hip_atomic_store(counters + kh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  combine_splits<HD>(partial + (int64_t)qrow * splits * SR, live,
-                    out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD);
+  if constexpr (XL) {
+    // every query of the XCD's heads, a wave each
+    const int GM = G * M;
+    for (int j = wave; j < (KV / XCDS) * GM; j += nw) {
+      const int kj = xcd + XCDS * (j / GM), gj = j % GM % G, mj = j % GM / G;
+      combine_splits<HD, true>(partial + (int64_t)(mj * H + kj * G + gj) * splits * SR, live,
+                               out + (int64_t)mj * ldo + (int64_t)(kj * G + gj) * HD);
+    }
+  } else {
+    combine_splits<HD>(partial + (int64_t)(m * H + kh * G + g) * splits * SR, live,
+                      out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD);
+  }
 }
 
 // Decode attention in one launch on MFMA, for any number of queries per KV
@@ -1233,7 +1301,7 @@ static int noalloc_scratch(void **out, hipStream_t stream) {
     if (e != hipSuccess || !p)
       return fail(WG_ERR_DEVICE, "no-allocation scratch on device %d: %s", dev,
                   hipGetErrorString(e));
-    clear_ints_kernel<<<1, MAX_KV_COUNTERS, 0, stream>>>((int *)p, MAX_KV_COUNTERS);
+    clear_ints_kernel<<<1, COUNTER_INTS, 0, stream>>>((int *)p, COUNTER_INTS);
     int rc = launched("no-allocation scratch (counters)");
     if (rc) return rc;
     ptrs[dev] = p;
@@ -1348,16 +1416,28 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
                               (fused_knob == 1 && (max_keys <= 1024 || max_keys > MAX_CH * CHUNK)));
   // the one-launch form combines any number of splits; the two-launch
   // combine holds MAX_CH chunks
-  // The MFMA form is taken for more than FGM queries a KV head (a verify
-  // batch; measured 3% faster there at 1024 cached keys than the chunk and
-  // combine kernels); for a decode step's few queries its serial tail
-  // (coherent stores, the count, the last workgroup's combine) costs more
-  // than the second launch it saves (13.4 us against 7.2 + 4.1 at 4096 keys,
-  // 32 heads of 128 over 8). attn_mfma 2 always takes it, 0 never.
+  // Which form, from layer-by-layer timings in captured graphs (32 heads
+  // over 8, one query row; us a layer, head_dim 128 / 64):
+  //   keys          2048         4096          8192          32768
+  //   XCD-local   8.2 / 6.9   11.8 / 8.5   20.7 / 12.5   71.8 / 30.4
+  //   two-launch  9.7 / 8.2   11.6 / 9.0   15.1 / 11.6      -
+  //   MFMA       10.7 / 8.9   13.5 / 10.9  17.3 / 13.0   33.1 / 23.8
+  // The MFMA form streams a wave's chunks through its own LDS ring, so it
+  // scales with the keys; the others load every key of a workgroup before
+  // any compute. So: MFMA past 8 queries a KV head (a verify batch) and
+  // from 16384 keys on; the XCD-local form below 4096 keys (KV heads a
+  // multiple of 8); otherwise the chunk and combine kernels, or the
+  // cross-XCD one-launch form where they do not reach. attn_mfma 2 always
+  // takes the MFMA form, 0 never; attn_xcd 2 always takes the XCD-local
+  // form where it applies, 0 never.
   const int mfma_knob = tuning("attn_mfma");
   const bool amfma = KV * (((H / KV) * M + 15) / 16) <= MAX_KV_COUNTERS &&
-                     (mfma_knob == 2 || (mfma_knob == 1 && (H / KV) * M > FGM));
-  const int key_cap = fused || amfma ? MAX_FUSED_KEYS : MAX_CH * CHUNK;
+                     (mfma_knob == 2 ||
+                      (mfma_knob == 1 && ((H / KV) * M > FGM || max_keys >= 16384)));
+  const int xcd_knob = tuning("attn_xcd");
+  const bool xl = !amfma && (H / KV) * M <= FGM && KV % XCDS == 0 &&
+                  (xcd_knob == 2 || (xcd_knob == 1 && max_keys < 4096));
+  const int key_cap = fused || amfma || xl ? MAX_FUSED_KEYS : MAX_CH * CHUNK;
   WG_REQUIRE(max_keys >= M && max_keys <= key_cap,
              "wg_attn_decode: max_keys %d (rows %d; at most %d)", max_keys, M, key_cap);
   WG_REQUIRE(ldq >= H * hd && ldo >= H * hd, "wg_attn_decode: strides too small");
@@ -1395,7 +1475,7 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
 #undef WG_AMFMA_LAUNCH
     return launched("wg_attn_decode");
   }
-  if (fused) {
+  if (fused || xl) {
     // one launch: 64 * nch keys a workgroup, the smallest nch (1, 2, 4) that
     // keeps the grid to about one workgroup a compute unit
     int nch = tuning("attn_split_chunks");
@@ -1408,13 +1488,18 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
     const size_t lds = (size_t)2 * nch * WK * hd * 2 + (size_t)FGM * hd * 4;
     dim3 grid((unsigned)(KV * splits));
     const unsigned threads = 64 * (H / KV) * M;
+#define WG_SPLIT_LAUNCH1(HDV, NCHV, XLV)                                                        \
+  do {                                                                                          \
+    int rc_ = raise_lds((const void *)attn_split_kernel<HDV, NCHV, XLV>, (int)lds);              \
+    if (rc_) return rc_;                                                                        \
+    attn_split_kernel<HDV, NCHV, XLV><<<grid, threads, lds, s>>>(                               \
+        q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, partial, splits, counters, out,    \
+        ldo);                                                                                   \
+  } while (0)
 #define WG_SPLIT_LAUNCH(HDV, NCHV)                                                              \
   do {                                                                                          \
-    int rc_ = raise_lds((const void *)attn_split_kernel<HDV, NCHV>, (int)lds);                   \
-    if (rc_) return rc_;                                                                        \
-    attn_split_kernel<HDV, NCHV><<<grid, threads, lds, s>>>(q, ldq, M, H, KV, k_cache, v_cache,  \
-                                                           pos0, max_keys, partial, splits,     \
-                                                           counters, out, ldo);                 \
+    if (xl) WG_SPLIT_LAUNCH1(HDV, NCHV, true);                                                  \
+    else WG_SPLIT_LAUNCH1(HDV, NCHV, false);                                                    \
   } while (0)
     if (hd == 64) {
       if (nch == 1) WG_SPLIT_LAUNCH(64, 1);
@@ -1426,6 +1511,7 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
       else WG_SPLIT_LAUNCH(128, 4);
     }
 #undef WG_SPLIT_LAUNCH
+#undef WG_SPLIT_LAUNCH1
     return launched("wg_attn_decode");
   }
   if ((H / KV) * M <= FGM) {

@@ -84,6 +84,7 @@ static Knob g_knobs[] = {
     {"attn_prefill_mfma", 4, 0, 4},      // prompt attention: MFMA waves a workgroup (1, 2, 4), 0 VALU
     {"attn_mfma", 1, 0, 2},              // decode attention in one launch on MFMA: 1 past 8 queries a KV head, 2 always, 0 never
     {"attn_fused", 1, 0, 2},             // decode attention in one launch: 1 where it is faster, 2 always, 0 never
+    {"attn_xcd", 1, 0, 2},               // decode attention in one launch combined within each XCD (KV heads a multiple of 8): 1 below 4096 keys, 2 always, 0 never
     {"attn_split_chunks", 0, 0, 4},      // its 64-key chunks a workgroup (1, 2, 4; 0 chooses)
     {"gemm_tile", 0, 0, 3},              // prefill GEMM tile: 0 chooses; 1 64x128, 2 128x128, 3 128x256
     {"delta_narrow_rows", 16, 0, 1 << 20},  // Gated DeltaNet batches up to this: 16-column workgroups
