@@ -380,12 +380,14 @@ typedef struct {
 /* Decode / few-token GEMV (matmulSplitRgba4 and the split matmul,
  * src/gpu/kernels.ts:744-895, :163-296, dispatched by Engine.splitPartials,
  * engine.ts:5241-5377): y[m][n] = sum_k W[n][k] x[m][k] for M <= 8 rows of
- * half activations x ([M][ldx], natural order), fp32 out. No MFMA: 128-bit
- * loads of nibbles, dequant in registers, wavefront reductions. Every
- * layout: 8-bit matrices as the 8-bit split matmul sums them (per block
- * acc += d * sum q a, kernels.ts:219-246), Q6_K as the Q6_K head does (per
- * super-block acc += d * sum_sub sc * sum (q - 32) a, kernels.ts:3593-3686),
- * with every epilogue. */
+ * half activations x ([M][ldx], natural order), fp32 out. One or two
+ * tokens stream on the vector units (128-bit loads of nibbles, dequant in
+ * registers, wavefront reductions); 3 to 8 tokens of a 4-bit row-group
+ * matrix run on MFMA (16x16x32 f16, nibbles unpacked to exact halves,
+ * f32 sums). Every layout: 8-bit matrices as the 8-bit split matmul sums
+ * them (per block acc += d * sum q a, kernels.ts:219-246), Q6_K as the Q6_K
+ * head does (per super-block acc += d * sum_sub sc * sum (q - 32) a,
+ * kernels.ts:3593-3686), with every epilogue. */
 int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx, float *y,
                int32_t ldy, const wg_epilogue *ep, void *stream);
 

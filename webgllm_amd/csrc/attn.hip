@@ -247,19 +247,19 @@ __global__ __launch_bounds__(FGM * 64) void attn_tile_kernel(
 // once with coherent vector loads. No workgroup waits on another, so the
 // launch always drains.
 //
-// The XCD-local form (XL) keeps all of that inside one XCD, whose compute
-// units share an L2: KV head kh belongs to XCD kh mod 8 (KV a multiple of
-// 8), and the workgroup with blockIdx b, on XCD x (its hardware XCC id),
-// takes split (b / 8) mod splits of head x + 8 (b / 8 / splits). Workgroups
-// are handed to the XCDs round-robin, so the 8 with the same b / 8 run one
-// on each XCD and every XCD holds grid / 8 of them. The partials are plain
-// stores, which reach the XCD's L2 once the wave's stores are done; one
-// counter per XCD (on its own 256-byte line) counts its workgroups in, and
-// the last one resets it and combines every query of the XCD's heads,
-// reading the partials from that L2 (sc0 loads, past the compute unit's
-// L1). Nothing is written back to memory between the splits and the combine.
+// The XCD-grouped form (XL) gives each XCD whole KV heads: KV head kh
+// belongs to XCD kh mod 8 (KV a multiple of 8), and the workgroup with
+// blockIdx b, on XCD x (its hardware XCC id), takes split (b / 8) mod
+// splits of head x + 8 (b / 8 / splits). Workgroups are handed to the XCDs
+// round-robin, so the 8 with the same b / 8 run one on each XCD and every
+// XCD holds grid / 8 of them. One counter per XCD (on its own 256-byte
+// line) counts its workgroups in, and the last one resets it and combines
+// every query of the XCD's heads: one serial combine an XCD instead of one
+// a KV head. The partials cross workgroups as coherent stores and loads,
+// as in the other form (plain stores read back through the XCD's L2 were
+// measured to miss now and then).
 constexpr int MAX_KV_COUNTERS = 64;       // counters at the scratch's start
-// then one 256-byte line of counters per XCD (the XCD-local form's), so no
+// then one 256-byte line of counters per XCD (the XCD-grouped form's), so no
 // two XCDs' L2s ever hold the same counter line
 constexpr int XCDS = 8;
 constexpr int XCD_LINE = 64;              // ints: 256 bytes
@@ -271,50 +271,37 @@ constexpr int MAX_FUSED_KEYS = 1 << 20;   // keys the one-launch form takes
 // HD weighted values, so that the values start 16-byte aligned.
 __host__ __device__ constexpr int split_row(int hd) { return hd + 4; }
 
-// Coherent (sc1) 16-byte store and loads; a loaded value is ready after
-// wait_vm and settle(). With LOCAL the loads are sc0 ones instead: they miss
-// the compute unit's L1 and are served by the XCD's L2, which holds what
-// the XCD's other compute units stored.
+// Coherent (sc1) 16-byte store; and coherent (sc1) loads, as buffer loads
+// whose cache-policy bits the compiler sees, so that it places the waits
+// for their results itself: they read, past the L2s, what any XCD's sc1
+// stores wrote.
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef float f2v __attribute__((ext_vector_type(2)));
 __device__ inline void store_sc1(float *p, f4v v) {
   asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
-template <bool LOCAL = false>
-__device__ inline f4v load_sc1(const float *p) {
-  f4v v;
-  if constexpr (LOCAL)
-    asm volatile("global_load_dwordx4 %0, %1, off sc0" : "=v"(v) : "v"(p) : "memory");
-  else
-    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
-  return v;
+// A buffer resource over [base, base + 2^31) (raw 32-bit loads).
+__device__ inline __amdgpu_buffer_rsrc_t rsrc_of(const float *base) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
 }
-template <bool LOCAL = false>
-__device__ inline f2v load2_sc1(const float *p) {
-  f2v v;
-  if constexpr (LOCAL)
-    asm volatile("global_load_dwordx2 %0, %1, off sc0" : "=v"(v) : "v"(p) : "memory");
-  else
-    asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
-  return v;
+constexpr int SC1 = 16;  // the sc1 bit of a buffer load's cache policy
+__device__ inline f4v load_sc1(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, SC1));
+}
+__device__ inline f2v load2_sc1(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(f2v, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, SC1));
 }
 
 // The XCD this workgroup runs on (hardware register XCC_ID, bits 3:0).
 __device__ inline int xcd_id() {
   return (int)(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);
 }
-// Ties a value loaded by inline assembly to a wait issued before: its uses
-// come after this point.
-template <typename T>
-__device__ inline void settle(T &v) {
-  asm volatile("" : "+v"(v));
-}
 
 // attendPanelCombine of one query's `live` split partials (rows of
-// split_row(HD) floats from pr, written with coherent stores, or by the
-// same XCD with LOCAL) into its HD output halves at op: the wave's lanes,
-// every load of a batch issued before the wait.
-template <int HD, bool LOCAL = false>
+// split_row(HD) floats from pr, written with coherent stores) into its HD
+// output halves at op: the wave's lanes, every load of a batch issued
+// before the first use.
+template <int HD>
 __device__ inline void combine_splits(const float *pr, int live, uint16_t *op) {
   constexpr int SR = split_row(HD);
   const int lane = threadIdx.x & 63;
@@ -329,19 +316,16 @@ __device__ inline void combine_splits(const float *pr, int live, uint16_t *op) {
   const int th = lane / LPS, dh = (lane % LPS) * 4;
   float gmax = -INFINITY, ltot = 0.0f;
   f4v o = {0.0f, 0.0f, 0.0f, 0.0f};
+  const __amdgpu_buffer_rsrc_t rs = rsrc_of(pr);
   for (int t0 = 0; t0 < live; t0 += BT) {
     const int n = min(BT, live - t0);
     f4v v[NL];
 #pragma unroll
     for (int i = 0; i < NL; i++) {
       const int t = t0 + min(th + TS * i, n - 1);
-      v[i] = load_sc1<LOCAL>(pr + (int64_t)t * SR + 4 + dh);
+      v[i] = load_sc1(rs, (t * SR + 4 + dh) * 4);
     }
-    f2v ml = load2_sc1<LOCAL>(pr + (int64_t)(t0 + min(lane, n - 1)) * SR);
-    wait_vm<0>();
-    settle(ml);
-#pragma unroll
-    for (int i = 0; i < NL; i++) settle(v[i]);
+    const f2v ml = load2_sc1(rs, (t0 + min(lane, n - 1)) * SR * 4);
     const float mt = lane < n ? ml.x : -INFINITY;
     float bmax = mt;
     bmax = wave_max(bmax);
@@ -511,22 +495,14 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   for (int t = 0; t < 8; t++) acc[t] = group_reduce<KP>(acc[t], Plus());
   const int qrow = m * H + kh * G + g;
   float *po = partial + ((int64_t)qrow * splits + s) * SR;
-  if constexpr (XL) {
-    if (lane < KP) {
-      *reinterpret_cast<f4v *>(po + 4 + d0) = f4v{acc[0], acc[1], acc[2], acc[3]};
-      *reinterpret_cast<f4v *>(po + 8 + d0) = f4v{acc[4], acc[5], acc[6], acc[7]};
-    } else if (lane == KP) {
-      *reinterpret_cast<f4v *>(po) = f4v{mrun, lrun, 0.0f, 0.0f};
-    }
-  } else {
-    if (lane < KP) {
-      store_sc1(po + 4 + d0, f4v{acc[0], acc[1], acc[2], acc[3]});
-      store_sc1(po + 8 + d0, f4v{acc[4], acc[5], acc[6], acc[7]});
-    } else if (lane == KP) {
-      store_sc1(po, f4v{mrun, lrun, 0.0f, 0.0f});
-    }
+  if (lane < KP) {
+    store_sc1(po + 4 + d0, f4v{acc[0], acc[1], acc[2], acc[3]});
+    store_sc1(po + 8 + d0, f4v{acc[4], acc[5], acc[6], acc[7]});
+  } else if (lane == KP) {
+    store_sc1(po, f4v{mrun, lrun, 0.0f, 0.0f});
   }
   }  // the split's work
+  asm volatile("" ::: "memory");
   wait_vm<0>();  // this wave's stores are done
   __syncthreads();
   int *count = XL ? counters + MAX_KV_COUNTERS + xcd * XCD_LINE : counters + kh;
@@ -545,8 +521,8 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
     const int GM = G * M;
     for (int j = wave; j < (KV / XCDS) * GM; j += nw) {
       const int kj = xcd + XCDS * (j / GM), gj = j % GM % G, mj = j % GM / G;
-      combine_splits<HD, true>(partial + (int64_t)(mj * H + kj * G + gj) * splits * SR, live,
-                               out + (int64_t)mj * ldo + (int64_t)(kj * G + gj) * HD);
+      combine_splits<HD>(partial + (int64_t)(mj * H + kj * G + gj) * splits * SR, live,
+                         out + (int64_t)mj * ldo + (int64_t)(kj * G + gj) * HD);
     }
   } else {
     combine_splits<HD>(partial + (int64_t)(m * H + kh * G + g) * splits * SR, live,
@@ -1419,16 +1395,16 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
   // Which form, from layer-by-layer timings in captured graphs (32 heads
   // over 8, one query row; us a layer, head_dim 128 / 64):
   //   keys          2048         4096          8192          32768
-  //   XCD-local   8.2 / 6.9   11.8 / 8.5   20.7 / 12.5   71.8 / 30.4
+  //   XCD-grouped 8.2 / 6.9   11.8 / 8.5   20.7 / 12.5   71.8 / 30.4
   //   two-launch  9.7 / 8.2   11.6 / 9.0   15.1 / 11.6      -
   //   MFMA       10.7 / 8.9   13.5 / 10.9  17.3 / 13.0   33.1 / 23.8
   // The MFMA form streams a wave's chunks through its own LDS ring, so it
   // scales with the keys; the others load every key of a workgroup before
   // any compute. So: MFMA past 8 queries a KV head (a verify batch) and
-  // from 16384 keys on; the XCD-local form below 4096 keys (KV heads a
+  // from 16384 keys on; the XCD-grouped form below 4096 keys (KV heads a
   // multiple of 8); otherwise the chunk and combine kernels, or the
   // cross-XCD one-launch form where they do not reach. attn_mfma 2 always
-  // takes the MFMA form, 0 never; attn_xcd 2 always takes the XCD-local
+  // takes the MFMA form, 0 never; attn_xcd 2 always takes the XCD-grouped
   // form where it applies, 0 never.
   const int mfma_knob = tuning("attn_mfma");
   const bool amfma = KV * (((H / KV) * M + 15) / 16) <= MAX_KV_COUNTERS &&

@@ -78,13 +78,13 @@ static Knob g_knobs[] = {
     {"gemv_few_stream", 1, 0, 1},        // 3 to 8 tokens on the streaming kernel (0: row groups)
     {"gemv_few_wg_per_cu", 1, 1, 16},    // its persistent workgroups per CU
     {"gemv_mfma", 1, 0, 2},              // row-group GEMV on MFMA: 1 for 3 to 8 tokens, 2 also 1 and 2, 0 never
-    {"gemv_mfma_wg_per_cu", 2, 1, 16},   // its persistent workgroups per CU
-    {"gemv_mfma_pairs", 8, 2, 8},        // its block pairs a wave (2, 4, 8)
+    {"gemv_mfma_wg_per_cu", 1, 1, 16},   // its persistent workgroups per CU
+    {"gemv_mfma_pairs", 4, 2, 8},        // its block pairs a wave (2, 4, 8)
     {"decode_wg_per_cu", 1, 1, 4},       // persistent decode workgroups (8 waves) per CU
     {"attn_prefill_mfma", 4, 0, 4},      // prompt attention: MFMA waves a workgroup (1, 2, 4), 0 VALU
-    {"attn_mfma", 1, 0, 2},              // decode attention in one launch on MFMA: 1 past 8 queries a KV head, 2 always, 0 never
+    {"attn_mfma", 1, 0, 2},              // decode attention in one launch on MFMA: 1 past 8 queries a KV head or from 16384 keys, 2 always, 0 never
     {"attn_fused", 1, 0, 2},             // decode attention in one launch: 1 where it is faster, 2 always, 0 never
-    {"attn_xcd", 1, 0, 2},               // decode attention in one launch combined within each XCD (KV heads a multiple of 8): 1 below 4096 keys, 2 always, 0 never
+    {"attn_xcd", 1, 0, 2},               // decode attention in one launch, each XCD combining its own KV heads (a multiple of 8): 1 below 4096 keys, 2 always, 0 never
     {"attn_split_chunks", 0, 0, 4},      // its 64-key chunks a workgroup (1, 2, 4; 0 chooses)
     {"gemm_tile", 0, 0, 3},              // prefill GEMM tile: 0 chooses; 1 64x128, 2 128x128, 3 128x256
     {"delta_narrow_rows", 16, 0, 1 << 20},  // Gated DeltaNet batches up to this: 16-column workgroups
