@@ -89,15 +89,22 @@ def gemv_roofline(mats, x, parts, out16, eps, reps=6, fmt="q4_k"):
     ep = L.Epilogue(mode=L.EPI_SWIGLU, out16=out16.data_ptr(), ld_out16=F,
                     norm_parts=parts.data_ptr(), n_parts=D // 4, ld_parts_in=D // 4,
                     norm_count=D, eps=eps, norm_mult=32.0)
+    # one pass over the matrices captured as a graph and replayed `reps`
+    # times: launch to launch on the GPU, with no host time between launches
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         for mm in mats[:4]:
             ops.gemv(mm, x, epilogue=ep)
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for mm in mats:
+                ops.gemv(mm, x, epilogue=ep)
+        g.replay()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(reps):
-            for mm in mats:
-                ops.gemv(mm, x, epilogue=ep)
+            g.replay()
         e1.record(stream)
     stream.synchronize()
     launches = reps * len(mats)
