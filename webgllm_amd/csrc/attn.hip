@@ -366,6 +366,61 @@ __device__ inline void combine_splits(const float *pr, int live, uint16_t *op) {
   }
 }
 
+// The same combine for several queries at once, when they have few splits:
+// lane (query slot lane / (HD / 4), dims 4 h .. 4 h + 3 with h = lane % (HD
+// / 4)) walks its own query's splits (CU at a time, every load of a batch
+// issued before the first use), so a wave takes 64 / (HD / 4) queries in
+// one memory round trip and needs no cross-lane reduction. qrow: the lane's
+// query row of the partials (rows of `splits` partials from `partial`);
+// op: its output, written when `valid`.
+constexpr int CU = 8;  // splits a lane loads at once
+template <int HD>
+__device__ inline void combine_lanes(const float *partial, int qrow, int splits, int live,
+                                     uint16_t *op, bool valid) {
+  constexpr int SR = split_row(HD);
+  const int dh = ((threadIdx.x & 63) % (HD / 4)) * 4;
+  const __amdgpu_buffer_rsrc_t rs = rsrc_of(partial);
+  const int row0 = (valid ? qrow : 0) * splits;
+  float gmax = -INFINITY, ltot = 0.0f;
+  f4v o = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t0 = 0; t0 < live; t0 += CU) {
+    f4v v[CU];
+    f2v ml[CU];
+#pragma unroll
+    for (int i = 0; i < CU; i++) {
+      const int t = row0 + min(t0 + i, live - 1);
+      v[i] = load_sc1(rs, (t * SR + 4 + dh) * 4);
+      ml[i] = load2_sc1(rs, t * SR * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < CU; i++) {
+      const float mt = t0 + i < live ? ml[i].x : -INFINITY;
+      const float nmax = fmaxf(gmax, mt);
+      const float a = gmax == -INFINITY ? (nmax == -INFINITY ? 1.0f : 0.0f) : __expf(gmax - nmax);
+      const float w = mt == -INFINITY ? 0.0f : __expf(mt - nmax);
+      ltot = ltot * a + w * ml[i].y;
+      o = o * a + v[i] * w;
+      gmax = nmax;
+    }
+  }
+  const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+  if (valid) {
+    const uint32_t lo = (uint32_t)half_bits(o.x * inv) | ((uint32_t)half_bits(o.y * inv) << 16);
+    const uint32_t hi = (uint32_t)half_bits(o.z * inv) | ((uint32_t)half_bits(o.w * inv) << 16);
+    *reinterpret_cast<uint2 *>(op + dh) = make_uint2(lo, hi);
+  }
+}
+
+// Whether combine_lanes takes nq queries of `live` splits in fewer memory
+// round trips than combine_splits, nw waves sharing them either way.
+template <int HD>
+__device__ inline bool lanes_combine_pays(int nq, int nw, int live) {
+  const int per = 64 / (HD / 4);  // queries a wave takes at once
+  const int lanes_trips = (nq + nw * per - 1) / (nw * per) * ((live + CU - 1) / CU);
+  const int split_trips = (nq + nw - 1) / nw * ((live + 4096 / HD - 1) / (4096 / HD));
+  return lanes_trips < split_trips;
+}
+
 template <int HD, int NCH, bool XL = false>
 __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
     const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
@@ -818,10 +873,22 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
   if (!last) return;
   if (threadIdx.x == 0)
     __hip_atomic_store(counters + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // the group's queries, a wave each in turn
-  for (int k = wave; k < 16; k += AW) {
+  const int nq = min(16, GM - qg * 16);  // the group's queries
+  if (lanes_combine_pays<HD>(nq, AW, live)) {
+    // several queries a wave at once, a lane group each
+    constexpr int PER = 64 / (HD / 4);
+    for (int k0 = wave * PER; k0 < nq; k0 += AW * PER) {
+      const int k = k0 + lane / (HD / 4);
+      const int qk = qg * 16 + min(k, nq - 1);
+      const int mk = qk / G, gk = qk % G;
+      combine_lanes<HD>(partial, mk * H + kh * G + gk, splits, live,
+                        out + (int64_t)mk * ldo + (int64_t)(kh * G + gk) * HD, k < nq);
+    }
+    return;
+  }
+  // a wave each in turn
+  for (int k = wave; k < nq; k += AW) {
     const int qk = qg * 16 + k;
-    if (qk >= GM) break;
     const int mk = qk / G, gk = qk % G;
     combine_splits<HD>(partial + (int64_t)(mk * H + kh * G + gk) * splits * SR, live,
                        out + (int64_t)mk * ldo + (int64_t)(kh * G + gk) * HD);
