@@ -116,19 +116,20 @@ def test_head_prep(hip, H, KV, hd, R, norm, pos0):
     assert not np.any(kcn[pos0 + M:])
 
 
-@pytest.fixture(params=["mfma", "xcd", "xcd-1", "xcd-4", "one-launch", "one-launch-1",
-                        "one-launch-2", "one-launch-4", "two-launch"])
+@pytest.fixture(params=["mfma", "mfma-xcd", "xcd", "xcd-1", "xcd-4", "one-launch",
+                        "one-launch-1", "one-launch-2", "one-launch-4", "two-launch"])
 def decode_path(request):
-    """wg_attn_decode's forms: one launch on MFMA; one launch combined
-    within each XCD (KV heads a multiple of 8; elsewhere the default form);
-    one launch on vector units (chunks a workgroup chosen, or 1, 2, 4); or
-    chunks then a combine."""
+    """wg_attn_decode's forms: one launch on MFMA, its splits exchanged
+    through memory or (KV heads x query groups a multiple of 8) within each
+    XCD; one launch combined within each XCD (KV heads a multiple of 8;
+    elsewhere the default form); one launch on vector units (chunks a
+    workgroup chosen, or 1, 2, 4); or chunks then a combine."""
     from webgllm_amd import lib as L
     knobs = ("attn_mfma", "attn_fused", "attn_split_chunks", "attn_xcd")
     old = [L.tuning_get(k) for k in knobs]
     name = request.param
-    L.tuning_set("attn_mfma", 2 if name == "mfma" else 0)
-    L.tuning_set("attn_xcd", 2 if name.startswith("xcd") else 0)
+    L.tuning_set("attn_mfma", 2 if name.startswith("mfma") else 0)
+    L.tuning_set("attn_xcd", 2 if name.startswith("xcd") else 1 if name == "mfma-xcd" else 0)
     L.tuning_set("attn_fused", 0 if name == "two-launch" else 2)
     L.tuning_set("attn_split_chunks", int(name[-1]) if name[-1].isdigit() else 0)
     yield name
@@ -210,6 +211,68 @@ def test_attn_decode_reuses_its_scratch(hip, decode_path):
         for m in range(M):
             want = O.attention_f64(q[m], k, v, H, KV, hd, pos0 + m + 1, kd)
             assert rel_l2(got[m], want) <= 1e-3, (pos0, M, m)
+
+
+@pytest.mark.parametrize("form,H,KV,hd,M,keys", [("xcd", 32, 8, 128, 1, 4096),
+                                                 ("xcd", 32, 8, 64, 2, 2048),
+                                                 ("mfma-xcd", 32, 8, 64, 5, 1024),
+                                                 ("mfma-xcd", 32, 8, 128, 3, 8192)])
+def test_attn_decode_xcd_exchange_over_many_launches(hip, form, H, KV, hd, M, keys):
+    """The forms whose partials, count and combine stay in one XCD's L2,
+    over 160 launches of changing queries and positions back to back in a
+    graph (4 layers' caches, one scratch), replayed 3 times: every launch
+    agrees with the two-launch form run eagerly on the same inputs (a stale
+    partial, from the launch before, would be off by far more)."""
+    from webgllm_amd import lib as L
+    from webgllm_amd import ops
+    knobs = ("attn_mfma", "attn_fused", "attn_split_chunks", "attn_xcd")
+    old = [L.tuning_get(k) for k in knobs]
+    g = torch.Generator(device="cuda").manual_seed(hd + M)
+    shape = ops.attn_shape(H, KV, hd)
+    caches = [(torch.randn((keys, KV * hd), device="cuda", generator=g).half(),
+               torch.randn((keys, KV * hd), device="cuda", generator=g).half()) for _ in range(4)]
+    qs = [torch.randn((M, H * hd), device="cuda", generator=g) / math.sqrt(hd) * 2
+          for _ in range(5)]
+    q = torch.empty_like(qs[0])
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    scratch = ops.attn_scratch(M, shape, keys)
+    iters = 40
+    positions = [keys - M - (i * 37) % (keys // 2) for i in range(iters)]
+    out = torch.zeros((iters, 4, M, H * hd), dtype=torch.float16, device="cuda")
+    want = torch.zeros_like(out)
+
+    def run(dst):
+        for i in range(iters):
+            q.copy_(qs[i % 5])
+            pos.fill_(positions[i])
+            for layer, (kc, vc) in enumerate(caches):
+                ops.attn_decode(q, shape, kc, vc, pos, scratch=scratch, out=dst[i, layer])
+    try:
+        for k, v in zip(knobs, (0, 0, 0, 0)):
+            L.tuning_set(k, v)
+        run(want)
+        L.tuning_set("attn_mfma", 2 if form == "mfma-xcd" else 0)
+        L.tuning_set("attn_fused", 1)
+        L.tuning_set("attn_xcd", 1 if form == "mfma-xcd" else 2)
+        run(out)  # the first-call set-up outside the capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                run(out)
+        torch.cuda.current_stream().wait_stream(stream)
+        for replay in range(3):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            d = (out.float() - want.float()).flatten(2)
+            err = d.norm(dim=2) / want.float().flatten(2).norm(dim=2)
+            assert float(err.max()) <= 1e-3, (replay, float(err.max()))
+    finally:
+        for k, v in zip(knobs, old):
+            L.tuning_set(k, v)
 
 
 @pytest.mark.parametrize("keys,M", [(32768, 1), (20000, 2), (65536, 1)])

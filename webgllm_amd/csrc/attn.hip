@@ -255,9 +255,11 @@ __global__ __launch_bounds__(FGM * 64) void attn_tile_kernel(
 // XCD holds grid / 8 of them. One counter per XCD (on its own 256-byte
 // line) counts its workgroups in, and the last one resets it and combines
 // every query of the XCD's heads: one serial combine an XCD instead of one
-// a KV head. The partials cross workgroups as coherent stores and loads,
-// as in the other form (plain stores read back through the XCD's L2 were
-// measured to miss now and then).
+// a KV head. Since every workgroup of the exchange shares the XCD's L2, the
+// partials, the count and the combine's loads stay in it (store_part and
+// load_part with LOCAL; checked bit for bit against the coherent exchange
+// over thousands of launches of changing queries and positions, eager and
+// in graphs).
 constexpr int MAX_KV_COUNTERS = 64;       // counters at the scratch's start
 // then one 256-byte line of counters per XCD (the XCD-grouped form's), so no
 // two XCDs' L2s ever hold the same counter line
@@ -271,25 +273,57 @@ constexpr int MAX_FUSED_KEYS = 1 << 20;   // keys the one-launch form takes
 // HD weighted values, so that the values start 16-byte aligned.
 __host__ __device__ constexpr int split_row(int hd) { return hd + 4; }
 
-// Coherent (sc1) 16-byte store; and coherent (sc1) loads, as buffer loads
-// whose cache-policy bits the compiler sees, so that it places the waits
-// for their results itself: they read, past the L2s, what any XCD's sc1
-// stores wrote.
+// How split partials pass from the workgroups that write them to the one
+// that combines them. Across XCDs (LOCAL false): 16-byte stores with sc1,
+// loads with sc1 (past the L2s, which are not coherent with each other)
+// and the count at agent scope. Within one XCD (LOCAL true: every
+// workgroup of the exchange runs on it): plain stores, which the vector L1
+// writes through to the XCD's L2, loads with sc0, which miss the L1 and
+// read that L2, and the count as an L2 atomic (workgroup scope). The loads
+// are buffer loads whose cache-policy bits the compiler sees, so that it
+// places the waits for their results itself.
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef float f2v __attribute__((ext_vector_type(2)));
-__device__ inline void store_sc1(float *p, f4v v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+template <bool LOCAL>
+__device__ inline void store_part(float *p, f4v v) {
+  if constexpr (LOCAL)
+    asm volatile("global_store_dwordx4 %0, %1, off" ::"v"(p), "v"(v) : "memory");
+  else
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
 // A buffer resource over [base, base + 2^31) (raw 32-bit loads).
 __device__ inline __amdgpu_buffer_rsrc_t rsrc_of(const float *base) {
   return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
 }
-constexpr int SC1 = 16;  // the sc1 bit of a buffer load's cache policy
-__device__ inline f4v load_sc1(__amdgpu_buffer_rsrc_t r, int byte_off) {
-  return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, SC1));
+// a buffer load's cache policy: sc0 (bit 0) or sc1 (bit 4)
+template <bool LOCAL>
+constexpr int part_policy() { return LOCAL ? 1 : 16; }
+template <bool LOCAL>
+__device__ inline f4v load_part(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(
+      f4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, part_policy<LOCAL>()));
 }
-__device__ inline f2v load2_sc1(__amdgpu_buffer_rsrc_t r, int byte_off) {
-  return __builtin_bit_cast(f2v, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, SC1));
+template <bool LOCAL>
+__device__ inline f2v load2_part(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(
+      f2v, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, part_policy<LOCAL>()));
+}
+// Counts a workgroup's partials in; true for the one that completes the
+// count (`expect` arrivals), which also puts the counter back to zero.
+template <bool LOCAL>
+__device__ inline bool count_in(int *count, int expect) {
+  if constexpr (LOCAL) {
+    if (__hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) !=
+        expect - 1)
+      return false;
+    __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  } else {
+    if (__hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
+        expect - 1)
+      return false;
+    __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return true;
 }
 
 // The XCD this workgroup runs on (hardware register XCC_ID, bits 3:0).
@@ -301,7 +335,7 @@ __device__ inline int xcd_id() {
 // split_row(HD) floats from pr, written with coherent stores) into its HD
 // output halves at op: the wave's lanes, every load of a batch issued
 // before the first use.
-template <int HD>
+template <int HD, bool LOCAL>
 __device__ inline void combine_splits(const float *pr, int live, uint16_t *op) {
   constexpr int SR = split_row(HD);
   const int lane = threadIdx.x & 63;
@@ -323,9 +357,9 @@ __device__ inline void combine_splits(const float *pr, int live, uint16_t *op) {
 #pragma unroll
     for (int i = 0; i < NL; i++) {
       const int t = t0 + min(th + TS * i, n - 1);
-      v[i] = load_sc1(rs, (t * SR + 4 + dh) * 4);
+      v[i] = load_part<LOCAL>(rs, (t * SR + 4 + dh) * 4);
     }
-    const f2v ml = load2_sc1(rs, (t0 + min(lane, n - 1)) * SR * 4);
+    const f2v ml = load2_part<LOCAL>(rs, (t0 + min(lane, n - 1)) * SR * 4);
     const float mt = lane < n ? ml.x : -INFINITY;
     float bmax = mt;
     bmax = wave_max(bmax);
@@ -374,7 +408,7 @@ __device__ inline void combine_splits(const float *pr, int live, uint16_t *op) {
 // query row of the partials (rows of `splits` partials from `partial`);
 // op: its output, written when `valid`.
 constexpr int CU = 8;  // splits a lane loads at once
-template <int HD>
+template <int HD, bool LOCAL>
 __device__ inline void combine_lanes(const float *partial, int qrow, int splits, int live,
                                      uint16_t *op, bool valid) {
   constexpr int SR = split_row(HD);
@@ -389,8 +423,8 @@ __device__ inline void combine_lanes(const float *partial, int qrow, int splits,
 #pragma unroll
     for (int i = 0; i < CU; i++) {
       const int t = row0 + min(t0 + i, live - 1);
-      v[i] = load_sc1(rs, (t * SR + 4 + dh) * 4);
-      ml[i] = load2_sc1(rs, t * SR * 4);
+      v[i] = load_part<LOCAL>(rs, (t * SR + 4 + dh) * 4);
+      ml[i] = load2_part<LOCAL>(rs, t * SR * 4);
     }
 #pragma unroll
     for (int i = 0; i < CU; i++) {
@@ -551,10 +585,10 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   const int qrow = m * H + kh * G + g;
   float *po = partial + ((int64_t)qrow * splits + s) * SR;
   if (lane < KP) {
-    store_sc1(po + 4 + d0, f4v{acc[0], acc[1], acc[2], acc[3]});
-    store_sc1(po + 8 + d0, f4v{acc[4], acc[5], acc[6], acc[7]});
+    store_part<XL>(po + 4 + d0, f4v{acc[0], acc[1], acc[2], acc[3]});
+    store_part<XL>(po + 8 + d0, f4v{acc[4], acc[5], acc[6], acc[7]});
   } else if (lane == KP) {
-    store_sc1(po, f4v{mrun, lrun, 0.0f, 0.0f});
+    store_part<XL>(po, f4v{mrun, lrun, 0.0f, 0.0f});
   }
   }  // the split's work
   asm volatile("" ::: "memory");
@@ -563,25 +597,33 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   int *count = XL ? counters + MAX_KV_COUNTERS + xcd * XCD_LINE : counters + kh;
   // XL: every workgroup of the XCD; else the head's live splits
   const int expect = XL ? (int)(gridDim.x / XCDS) : live;
-  if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           expect - 1;
+  if (threadIdx.x == 0) last = count_in<XL>(count, expect);
   __syncthreads();
   if (!last) return;
-  if (threadIdx.x == 0)
-    __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   if constexpr (XL) {
-    // every query of the XCD's heads, a wave each
-    const int GM = G * M;
-    for (int j = wave; j < (KV / XCDS) * GM; j += nw) {
-      const int kj = xcd + XCDS * (j / GM), gj = j % GM % G, mj = j % GM / G;
-      combine_splits<HD>(partial + (int64_t)(mj * H + kj * G + gj) * splits * SR, live,
-                         out + (int64_t)mj * ldo + (int64_t)(kj * G + gj) * HD);
+    // every query of the XCD's heads: several a wave at once when that
+    // takes fewer memory round trips, else a wave each
+    const int GM = G * M, nq = (KV / XCDS) * GM;
+    if (lanes_combine_pays<HD>(nq, nw, live)) {
+      constexpr int PER = 64 / (HD / 4);
+      for (int j0 = wave * PER; j0 < nq; j0 += nw * PER) {
+        const int j = min(j0 + lane / (HD / 4), nq - 1);
+        const int kj = xcd + XCDS * (j / GM), gj = j % GM % G, mj = j % GM / G;
+        combine_lanes<HD, true>(partial, mj * H + kj * G + gj, splits, live,
+                                out + (int64_t)mj * ldo + (int64_t)(kj * G + gj) * HD,
+                                j0 + lane / (HD / 4) < nq);
+      }
+    } else {
+      for (int j = wave; j < nq; j += nw) {
+        const int kj = xcd + XCDS * (j / GM), gj = j % GM % G, mj = j % GM / G;
+        combine_splits<HD, true>(partial + (int64_t)(mj * H + kj * G + gj) * splits * SR, live,
+                                 out + (int64_t)mj * ldo + (int64_t)(kj * G + gj) * HD);
+      }
     }
   } else {
-    combine_splits<HD>(partial + (int64_t)(m * H + kh * G + g) * splits * SR, live,
-                      out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD);
+    combine_splits<HD, false>(partial + (int64_t)(m * H + kh * G + g) * splits * SR, live,
+                              out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD);
   }
 }
 
@@ -603,9 +645,13 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
 //    element i % 4 of the 8 bytes lane 4 j + i / 4 addresses, as its element
 //    j), B = the weights split hi / lo, through a small per-wave LDS buffer;
 //  - the waves' (max, sum, values) merge in LDS; the workgroup publishes the
-//    split's partial with coherent stores, one relaxed atomic counts it in,
-//    and the workgroup that completes the count combines the group's
-//    queries, a wave each (combine_splits), as attn_split_kernel does.
+//    split's partial, one relaxed atomic counts it in, and the workgroup
+//    that completes the count combines the group's queries, several a wave
+//    at once (combine_lanes) when the splits are few, else a wave each
+//    (combine_splits), as attn_split_kernel does;
+//  - XG (KV * QG a multiple of 8): unit u's workgroups all run on XCD u mod
+//    8 (ranked as the XCD-grouped split form ranks them), and the exchange
+//    stays in that XCD's L2 (LOCAL).
 // K rows past the cache read the chunk's first row; V rows at or past the
 // last position are zeroed in LDS (a zero weight times a NaN is NaN); the
 // keys past a query's position are masked.
@@ -617,7 +663,7 @@ __host__ __device__ constexpr int amfma_wave_bytes() {
   return 2 * AWK * HD * 2 + 16 * 36 * 4;  // K and V tiles, the weights (16 x 36 floats)
 }
 
-template <int HD>
+template <int HD, bool XG>
 __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
     const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
     const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int splits,
@@ -636,7 +682,13 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
   __shared__ int last;
   const int G = H / KV, GM = G * M;
   const int QG = (GM + 15) / 16;
-  const int u = blockIdx.x % (KV * QG), s = blockIdx.x / (KV * QG);
+  // XG: the units (KV * QG, a multiple of 8) go to XCDs by unit % 8, each
+  // XCD's workgroups (ranked by blockIdx / 8: workgroups are dispatched to
+  // the XCDs in turn) taking its units' splits, so that a unit's partials
+  // meet in one L2
+  const int u = XG ? (xcd_id() & (XCDS - 1)) + XCDS * ((int)(blockIdx.x / XCDS) / splits)
+                   : (int)(blockIdx.x % (KV * QG));
+  const int s = XG ? (int)(blockIdx.x / XCDS) % splits : (int)(blockIdx.x / (KV * QG));
   const int kh = u % KV, qg = u / KV;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -860,19 +912,15 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
     }
     if (qvalid) {  // lane (query, c4) holds dims 16 dt + 4 c4 .. + 3
 #pragma unroll
-      for (int dt = 0; dt < DT; dt++) store_sc1(po + 4 + 16 * dt + 4 * c4, o[dt]);
-      if (c4 == 0) store_sc1(po, f4v{m_run, l_run, 0.0f, 0.0f});
+      for (int dt = 0; dt < DT; dt++) store_part<XG>(po + 4 + 16 * dt + 4 * c4, o[dt]);
+      if (c4 == 0) store_part<XG>(po, f4v{m_run, l_run, 0.0f, 0.0f});
     }
     wait_vm<0>();  // this wave's coherent stores are done
   }
   __syncthreads();
-  if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(counters + u, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           live - 1;
+  if (threadIdx.x == 0) last = count_in<XG>(counters + u, live);
   __syncthreads();
   if (!last) return;
-  if (threadIdx.x == 0)
-    __hip_atomic_store(counters + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int nq = min(16, GM - qg * 16);  // the group's queries
   if (lanes_combine_pays<HD>(nq, AW, live)) {
     // several queries a wave at once, a lane group each
@@ -881,7 +929,7 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
       const int k = k0 + lane / (HD / 4);
       const int qk = qg * 16 + min(k, nq - 1);
       const int mk = qk / G, gk = qk % G;
-      combine_lanes<HD>(partial, mk * H + kh * G + gk, splits, live,
+      combine_lanes<HD, XG>(partial, mk * H + kh * G + gk, splits, live,
                         out + (int64_t)mk * ldo + (int64_t)(kh * G + gk) * HD, k < nq);
     }
     return;
@@ -890,7 +938,7 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
   for (int k = wave; k < nq; k += AW) {
     const int qk = qg * 16 + k;
     const int mk = qk / G, gk = qk % G;
-    combine_splits<HD>(partial + (int64_t)(mk * H + kh * G + gk) * splits * SR, live,
+    combine_splits<HD, XG>(partial + (int64_t)(mk * H + kh * G + gk) * splits * SR, live,
                        out + (int64_t)mk * ldo + (int64_t)(kh * G + gk) * HD);
   }
 }
@@ -1505,16 +1553,23 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
     const int splits = (wchunks + AW * cpw - 1) / (AW * cpw);
     const size_t lds = (size_t)AW * (hd == 64 ? amfma_wave_bytes<64>() : amfma_wave_bytes<128>());
     const dim3 grid((unsigned)(units * splits));
-#define WG_AMFMA_LAUNCH(HDV)                                                                    \
+    // units a multiple of 8: grouped by XCD (attn_xcd 0: never)
+    const bool xg = units % XCDS == 0 && xcd_knob != 0;
+#define WG_AMFMA_LAUNCH(HDV, XGV)                                                               \
   do {                                                                                          \
-    int rc_ = raise_lds((const void *)attn_mfma_kernel<HDV>, (int)lds);                           \
+    int rc_ = raise_lds((const void *)attn_mfma_kernel<HDV, XGV>, (int)lds);                    \
     if (rc_) return rc_;                                                                        \
-    attn_mfma_kernel<HDV><<<grid, AW * 64, lds, s>>>(q, ldq, M, H, KV, k_cache, v_cache, pos0,    \
-                                                    max_keys, partial, splits, cpw, counters,    \
-                                                    out, ldo);                                   \
+    attn_mfma_kernel<HDV, XGV><<<grid, AW * 64, lds, s>>>(q, ldq, M, H, KV, k_cache, v_cache,   \
+                                                         pos0, max_keys, partial, splits, cpw,  \
+                                                         counters, out, ldo);                   \
   } while (0)
-    if (hd == 64) WG_AMFMA_LAUNCH(64);
-    else WG_AMFMA_LAUNCH(128);
+    if (hd == 64) {
+      if (xg) WG_AMFMA_LAUNCH(64, true);
+      else WG_AMFMA_LAUNCH(64, false);
+    } else {
+      if (xg) WG_AMFMA_LAUNCH(128, true);
+      else WG_AMFMA_LAUNCH(128, false);
+    }
 #undef WG_AMFMA_LAUNCH
     return launched("wg_attn_decode");
   }
