@@ -268,6 +268,9 @@ constexpr int XCD_LINE = 64;              // ints: 256 bytes
 constexpr int COUNTER_INTS = MAX_KV_COUNTERS + XCDS * XCD_LINE;
 constexpr int COUNTER_BYTES = COUNTER_INTS * 4;
 constexpr int MAX_FUSED_KEYS = 1 << 20;   // keys the one-launch form takes
+// partition partials a split workgroup merges in LDS: G M (P - 1) <= 12
+// with G M P <= 16 and P <= 4
+constexpr int MERGE_ROWS = 12;
 
 // A split's partial for one query: max, sum, 2 floats of padding, then the
 // HD weighted values, so that the values start 16-byte aligned.
@@ -403,12 +406,11 @@ __device__ inline void combine_splits(const float *pr, int live, uint16_t *op) {
 // The same combine for several queries at once, when they have few splits:
 // lane (query slot lane / (HD / 4), dims 4 h .. 4 h + 3 with h = lane % (HD
 // / 4)) walks its own query's splits (CU at a time, every load of a batch
-// issued before the first use), so a wave takes 64 / (HD / 4) queries in
-// one memory round trip and needs no cross-lane reduction. qrow: the lane's
-// query row of the partials (rows of `splits` partials from `partial`);
-// op: its output, written when `valid`.
-constexpr int CU = 8;  // splits a lane loads at once
-template <int HD, bool LOCAL>
+// issued before the first use: 6 CU registers), so a wave takes 64 / (HD /
+// 4) queries in one memory round trip and needs no cross-lane reduction.
+// qrow: the lane's query row of the partials (rows of `splits` partials
+// from `partial`); op: its output, written when `valid`.
+template <int HD, bool LOCAL, int CU>
 __device__ inline void combine_lanes(const float *partial, int qrow, int splits, int live,
                                      uint16_t *op, bool valid) {
   constexpr int SR = split_row(HD);
@@ -445,9 +447,9 @@ __device__ inline void combine_lanes(const float *partial, int qrow, int splits,
   }
 }
 
-// Whether combine_lanes takes nq queries of `live` splits in fewer memory
-// round trips than combine_splits, nw waves sharing them either way.
-template <int HD>
+// Whether combine_lanes<CU> takes nq queries of `live` splits in fewer
+// memory round trips than combine_splits, nw waves sharing them either way.
+template <int HD, int CU>
 __device__ inline bool lanes_combine_pays(int nq, int nw, int live) {
   const int per = 64 / (HD / 4);  // queries a wave takes at once
   const int lanes_trips = (nq + nw * per - 1) / (nw * per) * ((live + CU - 1) / CU);
@@ -456,7 +458,7 @@ __device__ inline bool lanes_combine_pays(int nq, int nw, int live) {
 }
 
 template <int HD, int NCH, bool XL = false>
-__global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
+__global__ __launch_bounds__(1024) void attn_split_kernel(
     const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
     const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int splits,
     int *counters, uint16_t *out, int ldo) {
@@ -481,17 +483,20 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = blockDim.x >> 6;  // = G * M
-  const int G = H / KV, g = wave % G, m = wave / G;
+  // G M queries, each taken by P waves (chunks p, p + P, ... of the split)
+  const int nw = blockDim.x >> 6;  // = G * M * P
+  const int G = H / KV, GM = G * M, P = nw / GM;
+  const int qi = wave % GM, p = wave / GM;
+  const int g = qi % G, m = qi / G;
   const int j0 = s * SPLIT;  // < max_keys: s < splits
   const int kvd = KV * HD;
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
   // (an XCC id past 7 would name a head past the last: such a workgroup
   // loads nothing and computes nothing, and its XCD's count never completes)
   const bool here = !XL || kh < KV;
-  if (here && lane < HD / 4)
+  if (here && p == 0 && lane < HD / 4)
     dma16(q + (int64_t)m * ldq + (int64_t)(kh * G + g) * HD + lane * 4,
-          __builtin_amdgcn_readfirstlane(sbase + QOFF + wave * HD * 4));
+          __builtin_amdgcn_readfirstlane(sbase + QOFF + qi * HD * 4));
   // rows at or past max_keys do not exist: their lanes load row j0 again,
   // and they are masked below like rows past the position
   for (int i = wave; here && i < 2 * NI * NCH; i += nw) {
@@ -512,7 +517,7 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   wait_vm<0>();
   if constexpr (!XL) {
     if (n_keys <= 0) {  // no position in the cache: the output is zero
-      if (s == 0) {
+      if (s == 0 && p == 0) {
         uint16_t *o = out + (int64_t)m * ldo + (int64_t)(kh * G + g) * HD;
         for (int d = lane; d < HD; d += 64) o[d] = 0;
       }
@@ -525,12 +530,11 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   barrier();
   if (!XL || (here && s < live)) {
 
-  const float4 *ql = reinterpret_cast<const float4 *>(smem + QOFF + wave * HD * 4);
+  const float4 *ql = reinterpret_cast<const float4 *>(smem + QOFF + qi * HD * 4);
   const int d0 = (lane % KP) * 8;
   float mrun = -INFINITY, lrun = 0.0f;
   float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int c = 0; c < NCH; c++) {
+  for (int c = p; c < NCH; c += P) {
     const int jc = j0 + c * WK;
     if (jc >= n_keys) break;
     const int nk = min(WK, n_keys - jc);
@@ -582,12 +586,42 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
   }
 #pragma unroll
   for (int t = 0; t < 8; t++) acc[t] = group_reduce<KP>(acc[t], Plus());
+  if (P > 1) {
+    // the query's P partitions meet in LDS (past the tiles and queries):
+    // partitions p > 0 leave (max, sum, values), partition 0 merges them
+    float *mg = reinterpret_cast<float *>(smem + QOFF + FGM * HD * 4);
+    if (p > 0) {
+      float *e = mg + (qi * (P - 1) + p - 1) * SR;
+      if (lane < KP) {
+        *reinterpret_cast<f4v *>(e + 4 + d0) = f4v{acc[0], acc[1], acc[2], acc[3]};
+        *reinterpret_cast<f4v *>(e + 8 + d0) = f4v{acc[4], acc[5], acc[6], acc[7]};
+      } else if (lane == KP) {
+        e[0] = mrun;
+        e[1] = lrun;
+      }
+    }
+    __syncthreads();
+    if (p == 0) {
+      for (int j = 1; j < P; j++) {
+        const float *e = mg + (qi * (P - 1) + j - 1) * SR;
+        const float m2 = e[0], l2 = e[1];
+        const float mx = fmaxf(mrun, m2);
+        const float a1 = mrun == -INFINITY ? 0.0f : __expf(mrun - mx);
+        const float a2 = m2 == -INFINITY ? 0.0f : __expf(m2 - mx);
+        lrun = lrun * a1 + l2 * a2;
+        if (lane < KP)
+#pragma unroll
+          for (int t = 0; t < 8; t++) acc[t] = acc[t] * a1 + e[4 + d0 + t] * a2;
+        mrun = mx;
+      }
+    }
+  }
   const int qrow = m * H + kh * G + g;
   float *po = partial + ((int64_t)qrow * splits + s) * SR;
-  if (lane < KP) {
+  if (p == 0 && lane < KP) {
     store_part<XL>(po + 4 + d0, f4v{acc[0], acc[1], acc[2], acc[3]});
     store_part<XL>(po + 8 + d0, f4v{acc[4], acc[5], acc[6], acc[7]});
-  } else if (lane == KP) {
+  } else if (p == 0 && lane == KP) {
     store_part<XL>(po, f4v{mrun, lrun, 0.0f, 0.0f});
   }
   }  // the split's work
@@ -605,12 +639,12 @@ __global__ __launch_bounds__(FGM * 64) void attn_split_kernel(
     // every query of the XCD's heads: several a wave at once when that
     // takes fewer memory round trips, else a wave each
     const int GM = G * M, nq = (KV / XCDS) * GM;
-    if (lanes_combine_pays<HD>(nq, nw, live)) {
+    if (lanes_combine_pays<HD, 8>(nq, nw, live)) {
       constexpr int PER = 64 / (HD / 4);
       for (int j0 = wave * PER; j0 < nq; j0 += nw * PER) {
         const int j = min(j0 + lane / (HD / 4), nq - 1);
         const int kj = xcd + XCDS * (j / GM), gj = j % GM % G, mj = j % GM / G;
-        combine_lanes<HD, true>(partial, mj * H + kj * G + gj, splits, live,
+        combine_lanes<HD, true, 8>(partial, mj * H + kj * G + gj, splits, live,
                                 out + (int64_t)mj * ldo + (int64_t)(kj * G + gj) * HD,
                                 j0 + lane / (HD / 4) < nq);
       }
@@ -739,6 +773,19 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
   // exit below waits for it (LDS still being written must not pass to the
   // next workgroup)
   if (j0w < max_keys) issue(j0w);
+  // the query's loads go out with the chunk's, ahead of the position
+  float4 qraw[QS][2];
+  {
+    const float *qp = q + (int64_t)qm * ldq + (int64_t)(kh * G + qh) * HD + 8 * c4;
+#pragma unroll
+    for (int t = 0; t < QS; t++) {
+      qraw[t][0] = qraw[t][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (qvalid) {
+        qraw[t][0] = *reinterpret_cast<const float4 *>(qp + 32 * t);
+        qraw[t][1] = *reinterpret_cast<const float4 *>(qp + 32 * t + 4);
+      }
+    }
+  }
   const int pos0 = *pos0_dev;
   const int n_keys = min(pos0 + M, max_keys);
   const int live = n_keys <= 0 ? 0 : (n_keys + SPLIT - 1) / SPLIT;  // splits with a visible key
@@ -759,14 +806,9 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
   // the queries as B operands, hi and lo halves: dims 32 t + 8 c4 .. + 7
   half8 qhi[QS], qlo[QS];
   {
-    const float *qp = q + (int64_t)qm * ldq + (int64_t)(kh * G + qh) * HD + 8 * c4;
 #pragma unroll
     for (int t = 0; t < QS; t++) {
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-      if (qvalid) {
-        a = *reinterpret_cast<const float4 *>(qp + 32 * t);
-        b = *reinterpret_cast<const float4 *>(qp + 32 * t + 4);
-      }
+      const float4 a = qraw[t][0], b = qraw[t][1];
       const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
       for (int e = 0; e < 8; e++) {
@@ -918,19 +960,27 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
     wait_vm<0>();  // this wave's coherent stores are done
   }
   __syncthreads();
-  if (threadIdx.x == 0) last = count_in<XG>(counters + u, live);
+  // XG: the counter on its XCD's own line (after the split form's)
+  int *count = XG ? counters + MAX_KV_COUNTERS + (u % XCDS) * XCD_LINE + 1 + u / XCDS
+                  : counters + u;
+  if (threadIdx.x == 0) last = count_in<XG>(count, live);
   __syncthreads();
   if (!last) return;
   const int nq = min(16, GM - qg * 16);  // the group's queries
-  if (lanes_combine_pays<HD>(nq, AW, live)) {
-    // several queries a wave at once, a lane group each
+  // several queries a wave at once, a lane group each, 8 or 16 splits a
+  // batch (the smaller when it holds them all)
+  const bool by8 = live <= 8 && lanes_combine_pays<HD, 8>(nq, AW, live);
+  if (by8 || lanes_combine_pays<HD, 16>(nq, AW, live)) {
     constexpr int PER = 64 / (HD / 4);
     for (int k0 = wave * PER; k0 < nq; k0 += AW * PER) {
       const int k = k0 + lane / (HD / 4);
       const int qk = qg * 16 + min(k, nq - 1);
       const int mk = qk / G, gk = qk % G;
-      combine_lanes<HD, XG>(partial, mk * H + kh * G + gk, splits, live,
-                        out + (int64_t)mk * ldo + (int64_t)(kh * G + gk) * HD, k < nq);
+      uint16_t *op = out + (int64_t)mk * ldo + (int64_t)(kh * G + gk) * HD;
+      if (by8)
+        combine_lanes<HD, XG, 8>(partial, mk * H + kh * G + gk, splits, live, op, k < nq);
+      else
+        combine_lanes<HD, XG, 16>(partial, mk * H + kh * G + gk, splits, live, op, k < nq);
     }
     return;
   }
@@ -1505,28 +1555,37 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
   const bool fits = (H / KV) * M <= FGM && KV <= MAX_KV_COUNTERS;
   const bool fused = fits && (fused_knob == 2 ||
                               (fused_knob == 1 && (max_keys <= 1024 || max_keys > MAX_CH * CHUNK)));
-  // the one-launch form combines any number of splits; the two-launch
+  // the one-launch forms combine any number of splits; the two-launch
   // combine holds MAX_CH chunks
-  // Which form, from layer-by-layer timings in captured graphs (32 heads
-  // over 8, one query row; us a layer, head_dim 128 / 64):
-  //   keys          2048         4096          8192          32768
-  //   XCD-grouped 8.2 / 6.9   11.8 / 8.5   20.7 / 12.5   71.8 / 30.4
-  //   two-launch  9.7 / 8.2   11.6 / 9.0   15.1 / 11.6      -
-  //   MFMA       10.7 / 8.9   13.5 / 10.9  17.3 / 13.0   33.1 / 23.8
-  // The MFMA form streams a wave's chunks through its own LDS ring, so it
-  // scales with the keys; the others load every key of a workgroup before
-  // any compute. So: MFMA past 8 queries a KV head (a verify batch) and
-  // from 16384 keys on; the XCD-grouped form below 4096 keys (KV heads a
-  // multiple of 8); otherwise the chunk and combine kernels, or the
-  // cross-XCD one-launch form where they do not reach. attn_mfma 2 always
-  // takes the MFMA form, 0 never; attn_xcd 2 always takes the XCD-grouped
-  // form where it applies, 0 never.
+  // Which form, from layer-by-layer timings in captured graphs (us a layer;
+  // 32 query heads over 8 of 128 dims / of 64 dims):
+  //   rows keys       XCD-grouped    MFMA          two-launch
+  //   1    1024       8.3 / 6.7      8.6 / 7.2     9.3 / 8.1
+  //   1    2048       8.6 / 7.2      9.0 / 7.5     9.8 / 8.3
+  //   1    4096      10.8 / 8.4     10.2 / 8.2    11.6 / 9.1
+  //   1    8192      16.9 / 11.2    14.7 / 10.2   15.2 / 11.2
+  //   2    1024       9.0 / 7.6      8.3 / 6.7     9.7 / 8.5
+  //   2    4096      13.4 / 10.3    11.8 / 9.7    13.6 / 10.4
+  // and with 14 query heads over 2 (not a multiple of 8, no XCD grouping;
+  // 64 dims, one row): MFMA 7.2 at 1024 and 2048 keys against 7.7 / 7.8
+  // two-launch, 9.6 / 11.1 at 4096 / 8192 against 8.4 / 8.9. So, by
+  // default: MFMA past 8 queries a KV head (a verify batch), from 16384
+  // keys on, and, with KV heads a multiple of 8, everywhere but the
+  // XCD-grouped form's range (up to 4 queries a KV head below 4096 keys),
+  // otherwise up to 2048 keys; the chunk and combine kernels in between.
+  // attn_mfma 2 always takes the MFMA form, 0 never; attn_xcd 2 always
+  // takes the XCD-grouped form where it applies, 0 never (nor groups the
+  // MFMA form by XCD).
+  const int GMq = (H / KV) * M;
+  const bool groupable = KV % XCDS == 0;
   const int mfma_knob = tuning("attn_mfma");
-  const bool amfma = KV * (((H / KV) * M + 15) / 16) <= MAX_KV_COUNTERS &&
-                     (mfma_knob == 2 ||
-                      (mfma_knob == 1 && ((H / KV) * M > FGM || max_keys >= 16384)));
   const int xcd_knob = tuning("attn_xcd");
-  const bool xl = !amfma && (H / KV) * M <= FGM && KV % XCDS == 0 &&
+  const bool xl_range = groupable && GMq <= 4 && max_keys < 4096 && xcd_knob != 0;
+  const bool amfma = KV * ((GMq + 15) / 16) <= MAX_KV_COUNTERS &&
+                     (mfma_knob == 2 ||
+                      (mfma_knob == 1 && (GMq > FGM || max_keys >= 16384 ||
+                                          (groupable ? !xl_range : max_keys <= 2048))));
+  const bool xl = !amfma && GMq <= FGM && groupable &&
                   (xcd_knob == 2 || (xcd_knob == 1 && max_keys < 4096));
   const int key_cap = fused || amfma || xl ? MAX_FUSED_KEYS : MAX_CH * CHUNK;
   WG_REQUIRE(max_keys >= M && max_keys <= key_cap,
@@ -1583,9 +1642,15 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
       nch = KV * chunks <= cus ? 1 : KV * ((chunks + 1) / 2) <= cus ? 2 : 4;
     }
     const int splits = (chunks + nch - 1) / nch;
-    const size_t lds = (size_t)2 * nch * WK * hd * 2 + (size_t)FGM * hd * 4;
+    // P waves a query, each taking every P-th chunk of the split (up to 16
+    // waves), their partials merged in LDS (MERGE_ROWS rows past the queries)
+    const int GMq = (H / KV) * M;
+    int P = nch < 16 / GMq ? nch : 16 / GMq;
+    if (tuning("attn_split_waves") == 0) P = 1;
+    const size_t lds = (size_t)2 * nch * WK * hd * 2 + (size_t)FGM * hd * 4 +
+                       (P > 1 ? (size_t)MERGE_ROWS * split_row(hd) * 4 : 0);
     dim3 grid((unsigned)(KV * splits));
-    const unsigned threads = 64 * (H / KV) * M;
+    const unsigned threads = 64 * GMq * P;
 #define WG_SPLIT_LAUNCH1(HDV, NCHV, XLV)                                                        \
   do {                                                                                          \
     int rc_ = raise_lds((const void *)attn_split_kernel<HDV, NCHV, XLV>, (int)lds);              \

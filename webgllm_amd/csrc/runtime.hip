@@ -82,10 +82,11 @@ static Knob g_knobs[] = {
     {"gemv_mfma_pairs", 4, 2, 8},        // its block pairs a wave (2, 4, 8)
     {"decode_wg_per_cu", 1, 1, 4},       // persistent decode workgroups (8 waves) per CU
     {"attn_prefill_mfma", 4, 0, 4},      // prompt attention: MFMA waves a workgroup (1, 2, 4), 0 VALU
-    {"attn_mfma", 1, 0, 2},              // decode attention in one launch on MFMA: 1 past 8 queries a KV head or from 16384 keys, 2 always, 0 never
+    {"attn_mfma", 1, 0, 2},              // decode attention in one launch on MFMA: 1 where it is faster (past 8 queries a KV head, from 16384 keys, outside the XCD-grouped split form's range with KV heads a multiple of 8, else up to 2048 keys), 2 always, 0 never
     {"attn_fused", 1, 0, 2},             // decode attention in one launch: 1 where it is faster, 2 always, 0 never
-    {"attn_xcd", 1, 0, 2},               // decode attention in one launch, each XCD combining its own KV heads (a multiple of 8): 1 below 4096 keys, 2 always, 0 never
+    {"attn_xcd", 1, 0, 2},               // decode attention with each XCD combining its own KV heads (a multiple of 8): 1 the split form up to 4 queries a KV head below 4096 keys and the MFMA form grouped, 2 the split form always, 0 never
     {"attn_split_chunks", 0, 0, 4},      // its 64-key chunks a workgroup (1, 2, 4; 0 chooses)
+    {"attn_split_waves", 1, 0, 1},       // its chunks spread over up to 16 waves (1), or a wave a query (0)
     {"gemm_tile", 0, 0, 3},              // prefill GEMM tile: 0 chooses; 1 64x128, 2 128x128, 3 128x256
     {"delta_narrow_rows", 16, 0, 1 << 20},  // Gated DeltaNet batches up to this: 16-column workgroups
 };
