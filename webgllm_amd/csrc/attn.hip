@@ -459,8 +459,8 @@ __device__ inline bool lanes_combine_pays(int nq, int nw, int live) {
 
 template <int HD, int NCH, bool XL = false>
 __global__ __launch_bounds__(1024) void attn_split_kernel(
-    const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
-    const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int splits,
+    const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0_dev, const float *q,
+    int max_keys, int splits, int M, int H, int KV, int nw, int ldq, float *partial,
     int *counters, uint16_t *out, int ldo) {
   constexpr int KP = HD / 8;       // 16-byte pieces of a row
   constexpr int ROWB = HD * 2;     // bytes of a row
@@ -483,8 +483,8 @@ __global__ __launch_bounds__(1024) void attn_split_kernel(
   }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // G M queries, each taken by P waves (chunks p, p + P, ... of the split)
-  const int nw = blockDim.x >> 6;  // = G * M * P
+  // G M queries, each taken by P waves (chunks p, p + P, ... of the split);
+  // nw = blockDim.x / 64 = G M P, passed among the preloaded arguments
   const int G = H / KV, GM = G * M, P = nw / GM;
   const int qi = wave % GM, p = wave / GM;
   const int g = qi % G, m = qi / G;
@@ -494,9 +494,6 @@ __global__ __launch_bounds__(1024) void attn_split_kernel(
   // (an XCC id past 7 would name a head past the last: such a workgroup
   // loads nothing and computes nothing, and its XCD's count never completes)
   const bool here = !XL || kh < KV;
-  if (here && p == 0 && lane < HD / 4)
-    dma16(q + (int64_t)m * ldq + (int64_t)(kh * G + g) * HD + lane * 4,
-          __builtin_amdgcn_readfirstlane(sbase + QOFF + qi * HD * 4));
   // rows at or past max_keys do not exist: their lanes load row j0 again,
   // and they are masked below like rows past the position
   for (int i = wave; here && i < 2 * NI * NCH; i += nw) {
@@ -511,6 +508,11 @@ __global__ __launch_bounds__(1024) void attn_split_kernel(
     dma16((is_v ? v_cache : k_cache) + (int64_t)rr * kvd + kh * HD + piece * 8,
           __builtin_amdgcn_readfirstlane(sbase + c * 2 * TILE + (is_v ? TILE : 0) + ii * 1024));
   }
+  // the query after the keys and values (ldq is not among the preloaded
+  // arguments: its fetch then delays no key load)
+  if (here && p == 0 && lane < HD / 4)
+    dma16(q + (int64_t)m * ldq + (int64_t)(kh * G + g) * HD + lane * 4,
+          __builtin_amdgcn_readfirstlane(sbase + QOFF + qi * HD * 4));
   const int pos0 = *pos0_dev;
   const int n_keys = min(pos0 + M, max_keys);
   // every load has landed before any wave leaves
@@ -689,6 +691,10 @@ __global__ __launch_bounds__(1024) void attn_split_kernel(
 // K rows past the cache read the chunk's first row; V rows at or past the
 // last position are zeroed in LDS (a zero weight times a NaN is NaN); the
 // keys past a query's position are masked.
+// The arguments that place the workgroup and address its first chunk (the
+// caches, the position, the query, the key count, the split shape) lead the
+// list, within the 14 dwords that arrive preloaded in scalar registers; the
+// split kernel's list is ordered the same way.
 constexpr int AW = 4;    // waves a workgroup
 constexpr int AWK = 32;  // keys a wave's chunk
 
@@ -699,9 +705,9 @@ __host__ __device__ constexpr int amfma_wave_bytes() {
 
 template <int HD, bool XG>
 __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
-    const float *q, int ldq, int M, int H, int KV, const uint16_t *k_cache,
-    const uint16_t *v_cache, const int32_t *pos0_dev, int max_keys, float *partial, int splits,
-    int cpw, int *counters, uint16_t *out, int ldo) {
+    const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0_dev, const float *q,
+    int max_keys, int splits, int cpw, int M, int H, int KV, int ldq, float *partial,
+    int *counters, uint16_t *out, int ldo) {
   typedef _Float16 half8 __attribute__((ext_vector_type(8)));
   typedef _Float16 half4 __attribute__((ext_vector_type(4)));
   typedef short short4v __attribute__((ext_vector_type(4)));
@@ -1618,8 +1624,8 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
   do {                                                                                          \
     int rc_ = raise_lds((const void *)attn_mfma_kernel<HDV, XGV>, (int)lds);                    \
     if (rc_) return rc_;                                                                        \
-    attn_mfma_kernel<HDV, XGV><<<grid, AW * 64, lds, s>>>(q, ldq, M, H, KV, k_cache, v_cache,   \
-                                                         pos0, max_keys, partial, splits, cpw,  \
+    attn_mfma_kernel<HDV, XGV><<<grid, AW * 64, lds, s>>>(k_cache, v_cache, pos0, q, max_keys, \
+                                                         splits, cpw, M, H, KV, ldq, partial,   \
                                                          counters, out, ldo);                   \
   } while (0)
     if (hd == 64) {
@@ -1656,8 +1662,8 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
     int rc_ = raise_lds((const void *)attn_split_kernel<HDV, NCHV, XLV>, (int)lds);              \
     if (rc_) return rc_;                                                                        \
     attn_split_kernel<HDV, NCHV, XLV><<<grid, threads, lds, s>>>(                               \
-        q, ldq, M, H, KV, k_cache, v_cache, pos0, max_keys, partial, splits, counters, out,    \
-        ldo);                                                                                   \
+        k_cache, v_cache, pos0, q, max_keys, splits, M, H, KV, (int)(threads / 64), ldq,       \
+        partial, counters, out, ldo);                                                           \
   } while (0)
 #define WG_SPLIT_LAUNCH(HDV, NCHV)                                                              \
   do {                                                                                          \

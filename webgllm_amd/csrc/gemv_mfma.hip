@@ -125,11 +125,14 @@ constexpr int mfma_round() {
   return r < 8 ? r : 8;
 }
 
+// The matrix, its shape and the activations lead the arguments, within the
+// 14 dwords that arrive preloaded in scalar registers, so the first ring
+// loads wait for no argument fetch.
 template <int ZK, int NP, int KS, int S, int MODE>
 __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
     const uint8_t *__restrict__ quants, const uint16_t *__restrict__ scales,
-    const void *__restrict__ zeros, const uint16_t *__restrict__ x, int ldx, int M,
-    float *__restrict__ y, int ldy, const wg_epilogue e, int G, int B) {
+    const void *__restrict__ zeros, const uint16_t *__restrict__ x, int G, int B, int ldx, int M,
+    float *__restrict__ y, int ldy, const wg_epilogue e) {
   using SL = Slot<ZK, NP>;
   constexpr bool SUB = ZK == WG_ZERO_F16;  // subnormal nibbles, zero point in C
   constexpr int R = mfma_round<ZK, NP, KS, S>();  // tiles a round (their sums wait in LDS)
@@ -400,7 +403,7 @@ int launch_mfma(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float 
       if (rc) return rc;                                                                       \
     }                                                                                          \
     gemv_mfma_kernel<ZK, NP, KS, S, MODE>                                                      \
-        <<<grid, KS * 64, LDS, s>>>(q, sc, w->zeros, x, ldx, M, y, ldy, e, G, B);              \
+        <<<grid, KS * 64, LDS, s>>>(q, sc, w->zeros, x, G, B, ldx, M, y, ldy, e);              \
   } while (0)
   if (e.mode == WG_EPI_SWIGLU) WG_MFMA_LAUNCH(WG_EPI_SWIGLU);
   else if (e.mode == WG_EPI_ROPE_KV) WG_MFMA_LAUNCH(WG_EPI_ROPE_KV);

@@ -23,11 +23,15 @@ namespace {
 // current one is computed and are never copied. Loads past the matrix
 // read an in-range row group or block (a clamped index): a row group past
 // the end is not stored, a block past the part adds zero.
+// The arguments the first loads need (the matrix, its shape, the
+// activations) lead the list: the first 14 dwords of the arguments arrive
+// in scalar registers with the wave, so the first loads wait for no
+// argument fetch.
 template <int M, int ZK, int NB, int KS, int MODE>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(
     const uint4 *__restrict__ quants, const uint16_t *__restrict__ scales,
-    const void *__restrict__ zeros, const uint16_t *__restrict__ x, int ldx,
-    float *__restrict__ y, int ldy, const wg_epilogue e, int G, int B) {
+    const void *__restrict__ zeros, const uint16_t *__restrict__ x, int G, int B, int ldx,
+    float *__restrict__ y, int ldy, const wg_epilogue e) {
   constexpr int RGW = 4 / KS;  // row groups a workgroup takes at a time
   __shared__ float red[2][4][4 * M];
   __shared__ float nred[4 * M];
@@ -135,14 +139,14 @@ int launch_stream(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, i
   auto q = (const uint4 *)w->quants;
   auto sc = (const uint16_t *)w->scales;
   if (e.mode == WG_EPI_SWIGLU)
-    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_SWIGLU><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, ldx,
-                                                                         y, ldy, e, G, B);
+    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_SWIGLU><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, G, B, ldx,
+                                                                         y, ldy, e);
   else if (e.mode == WG_EPI_ROPE_KV)
-    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_ROPE_KV><<<grid, 256, 0, s>>>(q, sc, w->zeros, x,
-                                                                          ldx, y, ldy, e, G, B);
+    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_ROPE_KV><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, G, B,
+                                                                          ldx, y, ldy, e);
   else
-    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_STORE><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, ldx,
-                                                                        y, ldy, e, G, B);
+    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_STORE><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, G, B, ldx,
+                                                                        y, ldy, e);
   return launched("wg_q4_gemv");
 }
 
