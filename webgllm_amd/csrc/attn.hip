@@ -34,15 +34,38 @@ __device__ inline uint16_t to_h(float v) {
 }
 
 // One wave per (row m, head slot): slots [0, H) queries, [H, H + KV) keys,
-// [H + KV, H + 2 KV) values.
+// [H + KV, H + 2 KV) values. The row's elements and norm weights (the
+// rotation partners' too: lane + 64 i, i < 4, as head_dim <= MAX_HD) load
+// with the position, only the rope table and the stores wait for it; the
+// arguments those loads need lead the list (the first 14 dwords arrive
+// preloaded in scalar registers).
 __global__ __launch_bounds__(64) void head_prep_kernel(
-    const float *qkv, int ldq, int H, int KV, int hd, int R, float eps, int use_norm,
-    const float *q_norm, const float *k_norm, const float *rope, int rope_rows,
-    const int32_t *pos0_dev, float *q_out, int ldqo, uint16_t *k_cache, uint16_t *v_cache,
-    int ctx) {
+    const float *qkv, const int32_t *pos0_dev, const float *q_norm, const float *k_norm, int ldq,
+    int H, int KV, int hd, int use_norm, int R, float eps, const float *rope, int rope_rows,
+    float *q_out, int ldqo, uint16_t *k_cache, uint16_t *v_cache, int ctx) {
+  static_assert(MAX_HD <= 4 * 64, "four elements a lane");
   const int slot = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
-  const int pos = *pos0_dev + m;
   const float *x = qkv + (int64_t)m * ldq + (int64_t)slot * hd;
+  const bool is_q = slot < H, is_v = slot >= H + KV;
+  const float *nw = is_q ? q_norm : k_norm;
+  const int P = R / 2;
+  const int pos = *pos0_dev + m;
+  float xv[4], wv[4], xp[4], wp[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int t = lane + 64 * i;
+    xv[i] = xp[i] = 0.0f;
+    wv[i] = wp[i] = 1.0f;
+    if (t < hd) {
+      xv[i] = x[t];
+      if (!is_v && use_norm) wv[i] = nw[t];
+      if (!is_v && t < 2 * P) {
+        const int tp = t < P ? t + P : t - P;  // the rotation partner
+        xp[i] = x[tp];
+        if (use_norm) wp[i] = nw[tp];
+      }
+    }
+  }
   const int kvd = KV * hd;
   if (pos < 0 || pos >= ctx || 1024 + (pos >> 10) >= rope_rows) {
     // A row past the cache has no position: its query is zero, nothing is stored.
@@ -50,34 +73,37 @@ __global__ __launch_bounds__(64) void head_prep_kernel(
       for (int t = lane; t < hd; t += 64) q_out[(int64_t)m * ldqo + (int64_t)slot * hd + t] = 0.0f;
     return;
   }
-  if (slot >= H + KV) {  // values: into the cache as they are
+  if (is_v) {  // values: into the cache as they are
     uint16_t *vo = v_cache + (int64_t)pos * kvd + (int64_t)(slot - H - KV) * hd;
-    for (int t = lane; t < hd; t += 64) vo[t] = to_h(x[t]);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      if (lane + 64 * i < hd) vo[lane + 64 * i] = to_h(xv[i]);
     return;
   }
-  const bool is_q = slot < H;
-  const float *nw = is_q ? q_norm : k_norm;
   float inv = 1.0f;
   if (use_norm) {
     float s = 0.0f;
-    for (int t = lane; t < hd; t += 64) s += x[t] * x[t];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      if (lane + 64 * i < hd) s += xv[i] * xv[i];
     s = wave_sum(s);
     inv = 1.0f / sqrtf(s / (float)hd + eps);
   }
-  const int P = R / 2;
   const int lo = pos & 1023, hi = 1024 + (pos >> 10);
   const float *r_lo = rope + (int64_t)lo * hd, *r_hi = rope + (int64_t)hi * hd;
   const float scale = is_q ? 1.0f / sqrtf((float)hd) : 1.0f;
-  for (int t = lane; t < hd; t += 64) {
-    float v = x[t] * (use_norm ? inv * nw[t] : 1.0f);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int t = lane + 64 * i;
+    if (t >= hd) break;
+    float v = xv[i] * (use_norm ? inv * wv[i] : 1.0f);
     float r = v;
     if (t < 2 * P) {
-      bool first = t < P;
-      int tp = first ? t + P : t - P;
-      int f = first ? t : tp;
-      float p = x[tp] * (use_norm ? inv * nw[tp] : 1.0f);
-      float c1 = r_lo[f], s1 = r_lo[hd / 2 + f], c2 = r_hi[f], s2 = r_hi[hd / 2 + f];
-      float cs = c1 * c2 - s1 * s2, sn = s1 * c2 + c1 * s2;
+      const bool first = t < P;
+      const int f = first ? t : t - P;
+      const float p = xp[i] * (use_norm ? inv * wp[i] : 1.0f);
+      const float c1 = r_lo[f], s1 = r_lo[hd / 2 + f], c2 = r_hi[f], s2 = r_hi[hd / 2 + f];
+      const float cs = c1 * c2 - s1 * s2, sn = s1 * c2 + c1 * s2;
       r = first ? v * cs - p * sn : v * cs + p * sn;
     }
     if (is_q) {
@@ -1485,8 +1511,8 @@ int wg_head_prep(const float *qkv, int32_t M, int32_t ldq, const wg_attn_shape *
   WG_REQUIRE(ldq >= slots * sh->head_dim && ldqo >= sh->heads * sh->head_dim,
              "wg_head_prep: strides too small");
   head_prep_kernel<<<dim3(slots, M), 64, 0, as_stream(stream)>>>(
-      qkv, ldq, sh->heads, sh->kv_heads, sh->head_dim, sh->rotated_dims, sh->eps, sh->use_norm,
-      q_norm, k_norm, rope, rope_rows, pos0, q_out, ldqo, k_cache, v_cache, ctx);
+      qkv, pos0, q_norm, k_norm, ldq, sh->heads, sh->kv_heads, sh->head_dim, sh->use_norm,
+      sh->rotated_dims, sh->eps, rope, rope_rows, q_out, ldqo, k_cache, v_cache, ctx);
   return launched("wg_head_prep");
 }
 

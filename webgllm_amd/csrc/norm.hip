@@ -105,12 +105,13 @@ __device__ inline void embed_extras(const wg_epilogue &e, int m, int c0, const f
   }
 }
 
-// Embedding rows of a ROWGROUP matrix: thread = (token m, block b).
-__global__ void embed_rowgroup_kernel(const uint32_t *quants, const uint16_t *scales,
-                                      const void *zeros, int zero_kind, const int32_t *ids,
-                                      int M, int blocks, int N, float *h, int ldh,
-                                      const wg_epilogue e) {
-  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// Embedding rows of a ROWGROUP matrix: thread = (token m, block b), 256
+// threads a workgroup (a constant: the workgroup size is not read from the
+// dispatch's arguments before the first load).
+__global__ __launch_bounds__(256) void embed_rowgroup_kernel(
+    const uint32_t *quants, const uint16_t *scales, const void *zeros, int zero_kind,
+    const int32_t *ids, int M, int blocks, int N, float *h, int ldh, const wg_epilogue e) {
+  int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= (int64_t)M * blocks) return;
   int m = (int)(t / blocks), b = (int)(t % blocks);
   int n = ids[m];
@@ -141,9 +142,11 @@ __global__ void embed_rowgroup_kernel(const uint32_t *quants, const uint16_t *sc
 
 // Embedding rows of a Q4_K matrix: thread = (token m, super-block s,
 // sub-block j), with packQ4_K's (d', z') chain (src/repack.ts:100-168).
-__global__ void embed_q4k_kernel(const uint8_t *quants, const int32_t *ids, int M, int supers,
-                                 int N, float *h, int ldh, const wg_epilogue e) {
-  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void embed_q4k_kernel(const uint8_t *quants,
+                                                        const int32_t *ids, int M, int supers,
+                                                        int N, float *h, int ldh,
+                                                        const wg_epilogue e) {
+  int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= (int64_t)M * supers * 8) return;
   int j = (int)(t & 7);
   int64_t ms = t >> 3;
