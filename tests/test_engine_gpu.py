@@ -295,6 +295,38 @@ def test_sampled_generate_with_penalties(hip, family, freq):
     assert runs[0] == runs[1] and all(0 <= t < eng.shape.vocab for t in runs[0])
 
 
+@pytest.mark.parametrize("family", ["llama-q4_k", "lfm2-q4_0"])
+def test_sampled_generate_guess_changes_no_token(hip, family):
+    """The guessed forward (the row's greedy pick run ahead while the host
+    draws, src/engine.ts:8095-8150) changes no token: seeded runs with and
+    without it write the same tokens, at temperatures where guesses both
+    hit and miss (LFM2's conv states put back after a miss), and leave the
+    engine at the same position with the same state: the next forward's
+    logits are equal bit for bit."""
+    import random as pyrandom
+    from webgllm_amd.sampler import Sampler
+    rng = np.random.default_rng(21)
+    hits = misses = 0
+    for temp, steps in ((0.9, 16), (0.05, 16)):
+        runs, ends = [], []
+        for guess in (False, True):
+            e, _ = _pair(family, seed=3)
+            prompt = _prompt(np.random.default_rng(31), 9, e.shape.vocab)
+            toks = e.generate(prompt, steps, Sampler(temp, 40, repetition_penalty=1.1),
+                              pyrandom.Random(7).random, guess=guess)
+            runs.append(toks)
+            if guess:
+                hits += e.guess_hits
+                misses += e.guess_misses
+                assert e.guess_hits + e.guess_misses == steps - 1
+            e.forward([toks[-1]])
+            ends.append((e.position, e.logits[:1].clone()))
+        assert runs[0] == runs[1]
+        assert ends[0][0] == ends[1][0] == 9 + steps
+        assert torch.equal(ends[0][1], ends[1][1])
+    assert hits > 0 and misses > 0, (hits, misses)
+
+
 def test_sampled_generate_without_top_k_reads_the_row(hip):
     """top_k 0 at temperature 0.7: the GPU's chunks could not hold the
     whole distribution, so the row is read back and sampled on the host;

@@ -768,7 +768,7 @@ class Engine:
 
     # --- sampled decoding -------------------------------------------------
     def generate(self, prompt: list[int], steps: int, sampler, random=None,
-                 count: int = 64) -> list[int]:
+                 count: int = 64, guess: bool = False) -> list[int]:
         """Sampled decoding (Engine.pick + the host sampler, src/engine.ts:
         8352-8473, src/sampler.ts): each step's last logits row goes through
         wg_pick_candidates (the penalties of the sampler's window on the
@@ -780,7 +780,21 @@ class Engine:
         is read back and penalized and sampled on the host instead when the
         GPU's candidates cannot hold the distribution: a frequency penalty
         (the device's mask knows whether a token is in the window, not how
-        often), or top-k off or above the `count` chunks kept."""
+        often), or top-k off or above the `count` chunks kept.
+
+        Each drawn token runs as one replay of the captured decode step
+        (capture_step), not as a host loop of launches. With `guess` (and
+        the GPU's candidates) the GPU does not wait for the host's draw
+        either (forwardGuess / keepGuess / dropGuess, src/engine.ts:
+        8095-8150): once a row's pick and read-back are enqueued, the row's
+        greedy pick runs as the next token (conv states saved first) while
+        the host draws. If the draw is that token, its forward is already
+        done; if not, the conv states are put back and the drawn token runs
+        (its K and V rows overwrite the guess's). The tokens are the same
+        either way; guess_hits and guess_misses count the two. On this GPU
+        a step's host gap (pick read-back and draw) is ~0.14 ms against a
+        ~1.6 ms replay of the 8B shape, so a guess pays only above a ~91%
+        hit rate: off by default."""
         from . import sampler as S
         st = sampler.settings
         greedy = st.temperature <= 0 or st.top_k == 1
@@ -789,13 +803,29 @@ class Engine:
         changes = sampler.see(prompt)
         if pick is not None:
             pick.see(changes)
+        guess = guess and pick is not None
+        guessed = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        saved = {i: torch.empty_like(s) for i, s in self.state.items()}
+        self.guess_hits = self.guess_misses = 0
+        end = self.position + len(prompt) + steps - 1  # the last token drawn is not run
+        if end > self.ctx:
+            raise ValueError(f"The cache holds {self.ctx} tokens; this would need {end}.")
+        # the whole run's room first: growing the caches would drop the graph
+        self.reserve(end)
         out = []
-        tokens = list(prompt)
-        for _ in range(steps):
-            self.forward(tokens)
-            row = (len(tokens) - 1) % 8
+        self.forward(prompt)
+        row = (len(prompt) - 1) % 8
+        greedy_pick = self.next_ids[row:row + 1]  # the last row's greedy pick
+        for step in range(steps):
+            last = step + 1 == steps
+            ahead = guess and not last
             if pick is not None:
-                d = pick(self.logits[row], sampler)
+                pick.start(self.logits[row], sampler, also=[(guessed, greedy_pick)] if ahead else ())
+                if ahead:
+                    for i, s in self.state.items():
+                        saved[i].copy_(s)
+                    self._replay_step(greedy_pick)
+                d = pick.finish(sampler)
             else:
                 d = sampler.distribution(self.logits[row].cpu().numpy().copy(), penalize=True)
             t = S.draw(d, random)
@@ -803,8 +833,34 @@ class Engine:
             changes = sampler.see([t], True)
             if pick is not None:
                 pick.see(changes)
-            tokens = [t]
+            if last:
+                break
+            if ahead and t == int(guessed[0]):
+                self.guess_hits += 1
+            else:
+                if ahead:
+                    for i, s in self.state.items():
+                        s.copy_(saved[i])
+                    self.guess_misses += 1
+                self._replay_step(t)
+            self.position += 1
+            self.check_plan()
+            row, greedy_pick = 0, self.ids[:1]  # the step's pick went to ids[0]
         return out
+
+    def _replay_step(self, token) -> None:
+        """One decode step of `token` (an int, or a 1-element device tensor)
+        at self.position by the captured graph (captured on first use):
+        logits into row 0, the greedy pick into ids[0]. self.position is
+        left to the caller."""
+        if self.graph is None:
+            self.capture_step(token if isinstance(token, int) else int(token[0]))
+        if isinstance(token, int):
+            self.ids[0] = token
+        elif token.data_ptr() != self.ids.data_ptr():
+            self.ids[:1].copy_(token)
+        self.pos.fill_(self.position)
+        self.graph.replay()
 
 
 def _nbits_from_normal(N: int, K: int, g: torch.Generator, dev):

@@ -232,6 +232,8 @@ class GpuPick:
     window's changes in one write), wg_pick_candidates into preallocated
     outputs, and one read-back into pinned host memory."""
 
+    STAGE = 64  # mask changes a see() stages without blocking
+
     def __init__(self, vocab: int, count: int = 64, device="cuda"):
         import torch
         from . import ops
@@ -246,16 +248,43 @@ class GpuPick:
         self.host = torch.empty(self.count + n, dtype=torch.float32, pin_memory=True)
         self.offsets = np.arange(256, dtype=np.int64)
         self._ops = ops
+        self.tok_host = torch.empty(self.STAGE, dtype=torch.int64, pin_memory=True)
+        self.val_host = torch.empty(self.STAGE, dtype=torch.uint8, pin_memory=True)
+        self.tok_dev = torch.empty(self.STAGE, dtype=torch.int64, device=device)
+        self.val_dev = torch.empty(self.STAGE, dtype=torch.uint8, device=device)
 
     def see(self, changes) -> None:
-        """The window's state changes [(token, state)] into the device mask."""
+        """The window's state changes [(token, state)] into the device mask.
+        Up to STAGE changes (a decode step's) go through pinned buffers kept
+        for it and copies that do not wait for the device, so a step's
+        update does not stall the host behind work already queued; the
+        buffers are written again only after finish() has waited for an
+        event recorded behind the last copies. More (a prompt's) are
+        written with blocking copies."""
         import torch
-        if changes:
+        if not changes:
+            return
+        n = len(changes)
+        if n > self.STAGE:
             t = torch.tensor([c[0] for c in changes], dtype=torch.int64)
             v = torch.tensor([c[1] for c in changes], dtype=torch.uint8)
             self.mask[t.to(self.mask.device)] = v.to(self.mask.device)
+            return
+        th, vh = self.tok_host.numpy(), self.val_host.numpy()
+        for j, (tok, state) in enumerate(changes):
+            th[j], vh[j] = tok, state
+        self.tok_dev[:n].copy_(self.tok_host[:n], non_blocking=True)
+        self.val_dev[:n].copy_(self.val_host[:n], non_blocking=True)
+        self.mask.index_put_((self.tok_dev[:n],), self.val_dev[:n])
 
     def __call__(self, logits_row, sampler: "Sampler") -> Distribution:
+        self.start(logits_row, sampler)
+        return self.finish(sampler)
+
+    def start(self, logits_row, sampler: "Sampler", also=()) -> None:
+        """Enqueues the pick and its read-back (and the copies in `also`,
+        (pinned host, device) pairs) and records an event after them: work
+        enqueued later runs on while finish() waits for this alone."""
         import torch
         lib = L.load()
         chunks = self.dev[:self.count].view(torch.int32)
@@ -265,7 +294,14 @@ class GpuPick:
             self.count, chunks.data_ptr(), self.dev[self.count:].data_ptr(),
             self.scratch.data_ptr(), self.scratch.numel(), self._ops._stream()))
         self.host.copy_(self.dev, non_blocking=True)
-        torch.cuda.current_stream().synchronize()
+        for host, dev in also:
+            host.copy_(dev, non_blocking=True)
+        self.done = torch.cuda.Event()
+        self.done.record()
+
+    def finish(self, sampler: "Sampler") -> Distribution:
+        """The distribution over the candidates start() read back."""
+        self.done.synchronize()
         h = self.host.numpy()
         ch = h[:self.count].view(np.int32).astype(np.int64)
         ids = (ch[:, None] * 256 + self.offsets[None, :]).astype(np.int32).reshape(-1)
