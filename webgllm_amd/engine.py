@@ -807,6 +807,8 @@ class Engine:
         guessed = torch.empty(1, dtype=torch.int32, pin_memory=True)
         saved = {i: torch.empty_like(s) for i, s in self.state.items()}
         self.guess_hits = self.guess_misses = 0
+        if steps <= 0:
+            return []
         end = self.position + len(prompt) + steps - 1  # the last token drawn is not run
         if end > self.ctx:
             raise ValueError(f"The cache holds {self.ctx} tokens; this would need {end}.")
