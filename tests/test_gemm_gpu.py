@@ -172,3 +172,96 @@ def test_gemm_swiglu_rejects(hip):
     lib = L.load()
     rc = lib.wg_q4_gemm_swiglu(C.byref(m.desc), 0x10000, 4, 64, 0x20000, 32, None, None)
     assert rc == -1 and "N / 2" in L.last_error()
+
+
+@pytest.mark.parametrize("tile,ks", [(1, 2), (1, 4), (1, 8), (2, 2), (2, 4), (3, 2), (3, 4), (3, 8)])
+@pytest.mark.parametrize("fmt", ["nbits", "q4_k_rowgroup", "q8"])
+def test_gemm_split_k(hip, fmt, tile, ks):
+    """K split 2, 4 or 8 ways (forced through gemm_splits) on each tile shape
+    and ragged rows: within float32 summation of the half-rounded weights,
+    the same bits on every repeat (the pairwise tree does not depend on
+    which split ends last), and a residual added in place."""
+    from webgllm_amd import lib as L, ops
+    m = _matrix(fmt, 512, 2048, seed=ks + tile)
+    L.tuning_set("gemm_tile", tile)
+    L.tuning_set("gemm_splits", ks)
+    try:
+        e, e16 = _check(m, 200, seed=ks)
+        er, er16 = _check(m, 77, seed=ks + 1, residual=True)
+        rng = np.random.default_rng(ks)
+        a = _t(O.f32_to_h2(rng.standard_normal((130, m.K)).astype(np.float32)).view(np.int16))
+        first = ops.gemm(m, a)
+        repeats = [ops.gemm(m, a) for _ in range(20)]
+    finally:
+        L.tuning_set("gemm_tile", 0)
+        L.tuning_set("gemm_splits", 0)
+    assert e <= 1e-3 and er <= 1e-3
+    assert e16 <= 1e-5 and er16 <= 1e-5
+    for r in repeats:
+        assert torch.equal(r, first)
+
+
+def test_gemm_split_k_first_launches(hip):
+    """Every launch right after the split layout changes (tile shape, split
+    count) equals the launch after it, bit for bit, and the unsplit result
+    to float32 rounding: the first launch of a layout reads no partial of
+    an earlier one."""
+    from webgllm_amd import lib as L, ops
+    m = _matrix("nbits", 4096, 4096, seed=6)
+    rng = np.random.default_rng(6)
+    a = _t(O.f32_to_h2(rng.standard_normal((512, 4096)).astype(np.float32)).view(np.int16))
+    L.tuning_set("gemm_splits", 1)
+    try:
+        unsplit = ops.gemm(m, a)
+        for tile, ks in [(2, 4), (1, 2), (2, 4), (2, 2), (1, 4), (2, 8), (1, 8), (3, 2), (3, 4),
+                         (2, 4)]:
+            L.tuning_set("gemm_tile", tile)
+            L.tuning_set("gemm_splits", ks)
+            c1 = ops.gemm(m, a)
+            c2 = ops.gemm(m, a)
+            assert torch.equal(c1, c2), (tile, ks)
+            assert rel_l2(c1.cpu().numpy(), unsplit.cpu().numpy()) <= 1e-6, (tile, ks)
+    finally:
+        L.tuning_set("gemm_tile", 0)
+        L.tuning_set("gemm_splits", 0)
+
+
+def test_gemm_split_k_prefill_shape_in_graph(hip):
+    """The 512 x 4096 -> 4096 prefill GEMM (split by default) captured in a
+    graph and replayed with eager launches between the replays: every
+    replay equals the eager result bit for bit, so the counters are back at
+    zero after each launch. A first capture on a stream with no workspace
+    yet runs unsplit (no allocation while capturing)."""
+    from webgllm_amd import lib as L, ops
+    m = _matrix("nbits", 4096, 4096, seed=5)
+    rng = np.random.default_rng(5)
+    a = _t(O.f32_to_h2(rng.standard_normal((512, 4096)).astype(np.float32)).view(np.int16))
+    s = torch.cuda.Stream()
+    out = torch.empty((512, 4096), device="cuda")
+    g0 = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g0, stream=s):
+            ops.gemm(m, a, out=out)
+    L.tuning_set("gemm_splits", 1)
+    try:
+        unsplit = ops.gemm(m, a)
+    finally:
+        L.tuning_set("gemm_splits", 0)
+    g0.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, unsplit)
+    with torch.cuda.stream(s):
+        eager = ops.gemm(m, a)  # allocates this stream's workspace
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        out2 = torch.empty_like(out)
+        with torch.cuda.graph(g, stream=s):
+            ops.gemm(m, a, out=out2)
+        for i in range(5):
+            out2.fill_(float("nan"))
+            g.replay()
+            other = ops.gemm(m, a)
+            torch.cuda.synchronize()
+            assert torch.equal(out2, eager), i
+            assert torch.equal(other, eager), i
+    assert rel_l2(eager.cpu().numpy(), unsplit.cpu().numpy()) <= 1e-6

@@ -39,7 +39,17 @@
 //    on both operands;
 //  - workgroups on one XCD (ids equal mod 8, as the dispatcher deals them
 //    round-robin) take the M tiles of one weight tile one after another, so
-//    it is read from HBM once into that XCD's L2.
+//    it is read from HBM once into that XCD's L2;
+//  - when the tiles are fewer than the compute units (M = 512 at N = 4096
+//    gives 128 tiles of 128 x 128), K is split KS ways (2 or 4): each
+//    workgroup runs one K range of one tile; the splits' float32 sums meet
+//    in a fixed pairwise tree (coherent stores and loads, counters put back
+//    to zero by their last arriver), and the tile's last workgroup runs the
+//    epilogue. The result does not depend on which split ends last.
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
 #include "common.h"
 #include "dot.h"
 #include "lds_load.h"
@@ -148,6 +158,31 @@ __device__ inline uint16_t half_clamped(float v) {
   return __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
+// How split-K partials pass between the workgroups of one tile, which may
+// run on different XCDs (whose L2s are not coherent with each other):
+// 16-byte stores with sc1, which reach the point every compute unit sees,
+// loads with sc1, which read past the L2, and the count at agent scope.
+typedef float f4v __attribute__((ext_vector_type(4)));
+__device__ inline void store_part(float *p, f4v v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+// a buffer resource over [base, base + 2^31) (raw 32-bit loads)
+__device__ inline __amdgpu_buffer_rsrc_t rsrc_over(const float *base) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ inline f4v load_part(__amdgpu_buffer_rsrc_t r, size_t floats) {
+  return __builtin_bit_cast(
+      f4v, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(floats * 4), 0, 16 /* sc1 */));
+}
+// Counts a group in; true for the one that completes the count, which puts
+// the counter back to zero for the next launch.
+__device__ inline bool count_in(int *count, int expect) {
+  if (__hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != expect - 1)
+    return false;
+  __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
 // BM x BN tiles, S stages of BK = 64, a WGM x WGN grid of waves. With SW the
 // matrix's rows come in groups of 4 as (gate 2i, gate 2i + 1, up 2i, up 2i
 // + 1) and C is a half output [M][ldc] of N / 2 columns: half(silu(gate) *
@@ -163,7 +198,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
                                                       const float *residual, int ldr,
                                                       const float *row_scale,
                                                       const int32_t *col_of, int M, int N,
-                                                      int K) {
+                                                      int K, int ks, float *part, int *count) {
   constexpr int NWV = WGM * WGN;  // waves
   constexpr int WM = BM / WGM, WN = BN / WGN, MT = WM / 32, NT = WN / 32;
   static_assert(MT >= 1 && NT >= 1 && WM % 32 == 0 && WN % 32 == 0, "32 x 32 MFMA tiles");
@@ -184,8 +219,13 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
   const int wm = wave / WGN, wn = wave % WGN, h = lane >> 5;
   // Tile order: ids equal mod 8 (one XCD) run the M tiles of one weight
   // tile in turn, so it is read from HBM once into that XCD's L2.
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = N / BN;
-  int id = blockIdx.x, tm, tn;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = N / BN, tiles = tiles_m * tiles_n;
+  int id = blockIdx.x, tm, tn, split = 0;
+  if (ks > 1) {  // workgroup id = split * tiles + tile
+    split = id / tiles;
+    id -= split * tiles;
+  }
+  const int tile = id;
   if (tiles_n % 8 == 0) {
     const int x = id % 8, j = id / 8;
     tm = j % tiles_m;
@@ -195,7 +235,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
     tn = id / tiles_m;
   }
   const int m0 = tm * BM, n0 = tn * BN, g0 = n0 / 4;
-  const int B = K / 32, KT = K / 64;
+  // this workgroup's K steps of 64: KT of them from step kb
+  const int B = K / 32, KT = K / 64 / ks, kb = split * KT;
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
 
   // This wave's loads of a step: per-lane byte offsets fixed for the whole
@@ -230,6 +271,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
   const unsigned char *s_base =
       s_is_zero ? (const unsigned char *)zeros : (const unsigned char *)scales;
   auto issue = [&](int kt, int st) {
+    kt += kb;
     const uint32_t base = sbase + st * STAGE;
 #pragma unroll
     for (int i = 0; i < IA; i++)
@@ -337,6 +379,60 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
   }
   }
 
+  if (ks > 1) {
+    // The splits' sums meet in a fixed pairwise tree: at level l, group g
+    // (the 2^l splits from g 2^l) publishes its sum in slot 2 ks - 2 ks /
+    // 2^l + g, and the last of each pair of groups adds its partner's. An
+    // addition of two values does not depend on their order, so neither
+    // does the result on which workgroup arrives last. Every slot is
+    // written once a launch, before anything reads it.
+    // A slot holds a tile's sums as fragments: fragment (wave, t, u) is 16
+    // floats a lane, stored as four 16-byte pieces a lane (1 KB a store).
+    constexpr int FRAG = 16 * 64;  // floats a fragment
+    const size_t tile_floats = (size_t)BM * BN;
+    auto at = [&](int slot, int t, int u, int j4) {
+      return (size_t)(slot * tiles + tile) * tile_floats +
+             (size_t)((wave * MT + t) * NT + u) * FRAG + (j4 * 64 + lane) * 4;
+    };
+    const __amdgpu_buffer_rsrc_t rs = rsrc_over(part);
+    __shared__ int last;
+    for (int l = 0; (1 << l) < ks; l++) {
+      const int g = split >> l;                    // this workgroup's group at level l
+      const int level = 2 * ks - ((2 * ks) >> l);  // the level's first slot
+#pragma unroll
+      for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int u = 0; u < NT; u++)
+#pragma unroll
+          for (int j4 = 0; j4 < 4; j4++) {
+            const f4v v = {acc[t][u][4 * j4], acc[t][u][4 * j4 + 1], acc[t][u][4 * j4 + 2],
+                           acc[t][u][4 * j4 + 3]};
+            store_part(part + at(level + g, t, u, j4), v);
+          }
+      wait_vm<0>();     // this wave's stores are done
+      __syncthreads();  // every wave's are
+      if (tid == 0) last = count_in(count + tile * 8 + (ks - (ks >> l)) + (g >> 1), 2);
+      // (a full __syncthreads: it waits for the LDS write of `last` before
+      // the barrier, which a bare s_barrier does not, and the other waves
+      // would read the flag stale)
+      __syncthreads();
+      if (!last) return;
+      const int partner = level + (g ^ 1);
+#pragma unroll
+      for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int u = 0; u < NT; u++) {
+          f4v got[4];
+#pragma unroll
+          for (int j4 = 0; j4 < 4; j4++) got[j4] = load_part(rs, at(partner, t, u, j4));
+#pragma unroll
+          for (int j4 = 0; j4 < 4; j4++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[t][u][4 * j4 + e] += got[j4][e];
+        }
+    }
+  }
+
   // D[j] of lane i: row 8 (j / 4) + 4 (i / 32) + j % 4, column i % 32.
   if constexpr (SW) {
     // Column i % 32's row in its group is i % 4: the gate rows' lanes (0, 1)
@@ -382,6 +478,82 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
   }
 }
 
+// Puts the split-K counters to zero by the atomic stores the counting uses.
+__global__ void split_zero_kernel(int *count, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    __hip_atomic_store(count + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A split-K workspace per device and stream (launches on one stream run in
+// turn; other streams get their own): the partial slots and the tree's
+// counters, grown on demand and kept until the process ends. The counters
+// start at zero and every launch leaves them so.
+struct SplitSpace {
+  int dev;
+  hipStream_t stream;
+  float *part;
+  size_t floats;
+  int *count;
+  int counters;
+};
+
+// The workspace for `floats` partial floats and `counters` counters on
+// stream s; part stays null when it would have to grow while s is being
+// captured into a graph (no allocation there: the launch runs unsplit).
+int split_space(hipStream_t s, size_t floats, int counters, float **part, int **count) {
+  static std::mutex mu;
+  static std::vector<SplitSpace *> spaces;
+  *part = nullptr;
+  *count = nullptr;
+  int dev = 0;
+  WG_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  SplitSpace *sp = nullptr;
+  for (SplitSpace *x : spaces)
+    if (x->dev == dev && x->stream == s) sp = x;
+  if (!sp || sp->floats < floats || sp->counters < counters) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+      (void)hipGetLastError();
+      return WG_OK;
+    }
+    if (cs != hipStreamCaptureStatusNone) return WG_OK;
+    if (!sp) {
+      sp = new SplitSpace{dev, s, nullptr, 0, nullptr, 0};
+      spaces.push_back(sp);
+    }
+    const size_t want = std::max(floats, sp->floats);
+    const int want_counters = std::max(counters, sp->counters);
+    if (sp->part) {  // launches queued on s may still use the old buffers
+      WG_HIP(hipStreamSynchronize(s));
+      WG_HIP(hipFree(sp->part));
+      WG_HIP(hipFree(sp->count));
+      sp->part = nullptr;
+      sp->count = nullptr;
+      sp->floats = 0;
+      sp->counters = 0;
+    }
+    const size_t round = (want + (1 << 20) - 1) & ~(size_t)((1 << 20) - 1);
+    float *p = nullptr;
+    int *c = nullptr;
+    if (hipMalloc(&p, round * sizeof(float)) != hipSuccess ||
+        hipMalloc(&c, (size_t)want_counters * sizeof(int)) != hipSuccess) {
+      (void)hipGetLastError();
+      if (p) (void)hipFree(p);
+      return fail(WG_ERR_OOM, "prefill GEMM: split-K workspace of %zu floats not allocated", round);
+    }
+    split_zero_kernel<<<(want_counters + 255) / 256, 256, 0, s>>>(c, want_counters);
+    WG_HIP(hipGetLastError());
+    sp->part = p;
+    sp->floats = round;
+    sp->count = c;
+    sp->counters = want_counters;
+  }
+  *part = sp->part;
+  *count = sp->count;
+  return WG_OK;
+}
+
 template <int ZK, int BM, int BN, int S, int WGM = 2, int WGN = 2, bool SW = false>
 int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
                  const float *residual, int ldr, const float *row_scale, const int32_t *col_of,
@@ -392,10 +564,33 @@ int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float
     const int rc = raise_lds((const void *)gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW>, (int)LDS);
     if (rc) return rc;
   }
-  const int grid = ((M + BM - 1) / BM) * (w->N / BN);
-  gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW><<<grid, WGM * WGN * 64, LDS, s>>>(
+  const int tiles = ((M + BM - 1) / BM) * (w->N / BN), steps = w->K / 64;
+  // K splits: the knob gemm_splits forces 1, 2, 4 or 8; 0 doubles them (up
+  // to 4) while the workgroups stay within two a compute unit (one for the
+  // 8-wave tile) and every split keeps at least S steps.
+  int ks = tuning("gemm_splits");
+  if (ks == 0) {
+    const int64_t room = (int64_t)persistent_grid(1 << 30, 1) * (WGM * WGN > 4 ? 1 : 2);
+    ks = 1;
+    while (ks < 4 && (int64_t)tiles * ks * 2 <= room && steps % (2 * ks) == 0 &&
+           steps / (2 * ks) >= S)
+      ks *= 2;
+  }
+  // (the slots are read by 32-bit buffer offsets: under 2 GiB of them)
+  if ((ks & (ks - 1)) || ks > 8 || steps % ks ||
+      (int64_t)(2 * ks - 2) * tiles * BM * BN * 4 >= ((int64_t)1 << 31))
+    ks = 1;
+  float *part = nullptr;
+  int *count = nullptr;
+  if (ks > 1) {
+    const int rc =
+        split_space(s, (size_t)(2 * ks - 2) * tiles * BM * BN, tiles * 8, &part, &count);
+    if (rc) return rc;
+    if (!part) ks = 1;
+  }
+  gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW><<<tiles * ks, WGM * WGN * 64, LDS, s>>>(
       (const uint8_t *)w->quants, (const uint16_t *)w->scales, w->zeros, A, lda, C, ldc,
-      residual, ldr, row_scale, col_of, M, w->N, w->K);
+      residual, ldr, row_scale, col_of, M, w->N, w->K, ks, part, count);
   return launched(SW ? "wg_q4_gemm_swiglu" : "wg_q4_gemm");
 }
 
@@ -403,16 +598,16 @@ template <int ZK, bool SW = false>
 int launch(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
            const float *residual, int ldr, const float *row_scale, const int32_t *col_of,
            hipStream_t s) {
-  // The largest tile whose count still covers most compute units: each
-  // weight is dequantized once per tile, so taller tiles (more rows a
-  // wave) spend fewer vector instructions per MFMA. The knob gemm_tile
-  // forces one (1: 64 x 128, 2: 128 x 128, 3: 128 x 256).
+  // Each weight is dequantized once per tile, so taller tiles (more rows a
+  // wave) spend fewer vector instructions per MFMA: 128 x 256 where its
+  // tiles cover most compute units, else 128 x 128 from 512 rows, else 64 x
+  // 128; splitting K makes up the workgroups that few tiles leave short.
+  // The knob gemm_tile forces one (1: 64 x 128, 2: 128 x 128, 3: 128 x 256).
   const int cus = persistent_grid(1 << 30, 1);
-  const int64_t tm128 = (M + 127) / 128;
   int t = tuning("gemm_tile");
   if (t == 0) {
-    if (w->N % 256 == 0 && tm128 * (w->N / 256) * 4 >= (int64_t)cus * 3) t = 3;
-    else if (w->N % 128 == 0 && tm128 * (w->N / 128) * 4 >= (int64_t)cus * 3) t = 2;
+    if (w->N % 256 == 0 && (int64_t)((M + 127) / 128) * (w->N / 256) * 4 >= (int64_t)cus * 3) t = 3;
+    else if (M >= 512 && w->N % 128 == 0) t = 2;
     else if (w->N % 128 == 0) t = 1;
   }
   if (t == 3 && w->N % 256 == 0)
