@@ -414,14 +414,14 @@ def workload_nbits_gemm(args, fmt="nbits"):
                 per_shape_tflops={str(N): round(r[1], 1) for N, r in res.items()})
 
 
-def decode_engine_run(shape, ctx, prompt_len, steps, warmup, persistent=False):
+def decode_engine_run(shape, ctx, prompt_len, steps, warmup):
     """Prefill random ids, capture the token step, warm up, then time
     `steps` graph replays. Returns (engine, weights, ms a token, first
     timed position)."""
     import torch
     from webgllm_amd import engine as E
     w = E.Weights(shape, seed=0)
-    eng = E.Engine(w, ctx, persistent=persistent)
+    eng = E.Engine(w, ctx)
     prompt = torch.randint(0, shape.vocab, (prompt_len,),
                            generator=torch.Generator().manual_seed(1)).tolist()
     first = int(eng.forward(prompt)[-1])
@@ -434,7 +434,6 @@ def decode_engine_run(shape, ctx, prompt_len, steps, warmup, persistent=False):
     eng.pos.fill_(p0)
     ms = timed(eng.graph.replay, steps)
     eng.position += steps
-    eng.check_plan()
     return eng, w, ms, p0
 
 
@@ -444,7 +443,7 @@ def workload_qwen2_decode(args):
     from webgllm_amd import engine as E
     shape = E.QWEN2_05B
     steps = 1024 - 512 - args.warmup - 1
-    eng, w, ms, p0 = decode_engine_run(shape, 1024, 512, steps, args.warmup, args.persistent)
+    eng, w, ms, p0 = decode_engine_run(shape, 1024, 512, steps, args.warmup)
     keys = p0 + (steps + 1) // 2
     tok_bytes = token_bytes(shape, keys)
     cpu = cpu_baseline(eng, host_threads()[0], 10.0, keys=keys) if not args.no_cpu else None
@@ -457,8 +456,7 @@ def workload_qwen2_decode(args):
     cfg = {"workload": f"Qwen2-0.5B-shape greedy decode, positions {p0}..{p0 + steps - 1}",
            "model": shape.name, "layers": shape.layers, "hidden": shape.hidden,
            "vocab": shape.vocab, "weights": "random MatMulNBits q4 (u8 zero points)",
-           "global_batch": 1, "seq_len": 1024, "parallelism": "none",
-           "decode_path": "persistent" if eng.plan is not None else "per-op kernels"}
+           "global_batch": 1, "seq_len": 1024, "parallelism": "none"}
     return line("decode tok/s, Qwen2-0.5B-shape MatMulNBits batch 1", round(1000.0 / ms, 2),
                 "tok/s", steps, args.warmup, ms, cfg, roof, cpu)
 
@@ -1043,8 +1041,6 @@ def main():
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the gate|up GEMV launches and a copy (for counter runs)")
     ap.add_argument("--reps", type=int, default=6, help=argparse.SUPPRESS)
-    ap.add_argument("--persistent", action="store_true",
-                    help="decode every layer in one persistent launch (wg_decode_run)")
     ap.add_argument("--workload", default="llama8b-decode",
                     choices=["llama8b-decode"] + sorted(WORKLOADS),
                     help="the headline Llama-3-8B-shape decode (default) or another "
@@ -1078,7 +1074,7 @@ def main():
         shape = dataclasses.replace(shape, layers=args.layers)
     t0 = time.time()
     w = E.Weights(shape, seed=0)
-    eng = E.Engine(w, args.ctx, persistent=args.persistent)
+    eng = E.Engine(w, args.ctx)
     prompt_len = args.ctx - args.warmup - args.steps - 1
     rng = torch.Generator().manual_seed(1)
     prompt = torch.randint(0, shape.vocab, (prompt_len,), generator=rng).tolist()
@@ -1141,7 +1137,6 @@ def main():
                        "reference's 32-blocks (packQ4_K)",
             "activations": "f16", "accumulate": "f32",
             "global_batch": 1, "seq_len": args.ctx, "parallelism": "none",
-            "decode_path": "persistent" if eng.plan is not None else "per-op kernels",
         },
         "roofline": roof,
         "cpu_baseline": cpu,

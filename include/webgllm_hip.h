@@ -45,9 +45,8 @@ const char *wg_version(void);
  * "q4k_wg_per_cu", "wide_wg_per_cu" (8-bit and Q6_K matrices: persistent
  * GEMV workgroups per compute unit) and
  * "gemv_min_waves" (below this many waves a GEMV splits K inside a
- * workgroup), "decode_wg_per_cu" (persistent decode workgroups per
- * compute unit, read at plan creation) and "gemm_tile" (prefill GEMM tile:
- * 1 64 x 128, 2 128 x 128, 3 128 x 256, or 0 to choose by shape).
+ * workgroup) and "gemm_tile" (prefill GEMM tile: 1 64 x 128, 2 128 x 128,
+ * 3 128 x 256, or 0 to choose by shape).
  * Process-wide; results never depend on them. */
 int wg_tuning_set(const char *name, int32_t value);
 int wg_tuning_get(const char *name, int32_t *value);
@@ -404,7 +403,14 @@ int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx,
  * 32 / RMS, see wg_norm_to_h2). col_of (or NULL for n -> n) maps the
  * matrix's stored row n to its output column: a matrix uploaded with a row
  * order (the loaders' srcRows, stored row n = logical row col_of[n]) then
- * comes out in logical order; entries outside 0..N-1 are not written. */
+ * comes out in logical order; entries outside 0..N-1 are not written.
+ * Where tiles are fewer than the compute units, K is split 2 or 4 ways and
+ * the partial sums are added in a fixed pairwise order (bits independent of
+ * which split ends last), in a workspace the library keeps per stream and
+ * grows on demand; launches on one stream run in turn. A launch made while
+ * its stream is being captured into a graph runs unsplit (the graph holds
+ * no workspace, so it may replay on any stream and beside eager GEMMs), and
+ * so its sums may differ in the last bits from an eager launch's. */
 int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda, float *C,
                int32_t ldc, const float *residual, int32_t ldr, const float *row_scale,
                const int32_t *col_of, void *stream);
@@ -422,53 +428,6 @@ int wg_q4_gemm_swiglu(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32
 
 /* float32 -> half activations, clamped to +-65504 (packH2, kernels.ts:32-36). */
 int wg_f32_to_f16(const float *x, uint16_t *out, int64_t n, void *stream);
-
-/* ---------------------------------------------- persistent batch-1 decode
- * The attention layers of one token's forward (Engine.forwardBatch at one
- * row, src/engine.ts:8875-9303: per layer the qkv matmul with RoPE and the
- * KV write, attention over the cache, o + residual + norm, gate|up +
- * SwiGLU, down + residual + the next norm) in ONE launch: a persistent
- * workgroup per compute-unit slot runs the phases in order, with a grid
- * barrier between them, and loads its first weights of the next phase
- * before it waits at a barrier, so weight streaming continues across phase
- * boundaries. Each layer is given as the four wg_q4_gemv calls (M = 1) the
- * per-op path makes:
- *  - qkv: WG_EPI_ROPE_KV (q_out, the caches, pos0 and ctx define the
- *    attention too);
- *  - o: WG_EPI_STORE, x = the attention output (heads * head_dim halves);
- *  - gate_up: WG_EPI_SWIGLU, its out16 = down's x;
- *  - down: WG_EPI_STORE.
- * All matrices ROWGROUP with one zero kind; head_dim 64 or 128; at most 8
- * query heads per KV head and 64 KV heads; ctx <= 16384. Unsupported
- * shapes return WG_ERR_UNSUPPORTED at plan creation. The plan copies the
- * calls to device memory and owns its attention partials and barrier
- * state; wg_decode_run launches one kernel (capturable in a graph: it
- * allocates nothing and sets no memory). Runs of one plan must not
- * overlap. A barrier wait that runs past its poll limit ends the kernel
- * early with its results undefined and is reported by wg_decode_status. */
-typedef struct {
-  wg_q4_matrix w;
-  const uint16_t *x;
-  int32_t ldx;
-  float *y;
-  int32_t ldy;
-  wg_epilogue ep;
-} wg_gemv_call;
-
-typedef struct {
-  wg_gemv_call qkv, o, gate_up, down;
-} wg_decode_layer;
-
-typedef struct wg_decode_plan wg_decode_plan;
-
-int wg_decode_plan_create(const wg_decode_layer *layers, int32_t n_layers, wg_decode_plan **out);
-int wg_decode_run(wg_decode_plan *plan, void *stream);
-/* After the stream has finished: WG_OK, or WG_ERR_DEVICE if a barrier wait
- * ran past its limit (the plan's barrier state is then reset). */
-int wg_decode_status(wg_decode_plan *plan);
-/* The polls a barrier wait makes before it gives up (default 1 << 20). */
-int wg_decode_set_spin_limit(wg_decode_plan *plan, int32_t polls);
-int wg_decode_plan_destroy(wg_decode_plan *plan);
 
 /* ---------------------------------------------- residual-stream glue */
 

@@ -111,31 +111,6 @@ def test_tuning_knobs():
         L.tuning_set("nope", 1)
 
 
-def _call(N, K, mode, y=0x40000, **ep):
-    return L.GemvCall(w=_desc(N=N, K=K), x=0x10000, ldx=K, y=y, ldy=N,
-                      ep=L.Epilogue(mode=mode, **ep))
-
-
-def test_decode_plan_rejects_before_any_device_work():
-    lib = L.load()
-    h = C.c_void_p()
-    assert lib.wg_decode_plan_create(None, 0, C.byref(h)) == -1
-    assert "no layers" in L.last_error()
-    # qkv given as a plain store: the plan needs its RoPE + KV epilogue
-    layer = L.DecodeLayer(qkv=_call(64, 64, L.EPI_STORE), o=_call(64, 64, L.EPI_STORE),
-                          gate_up=_call(64, 64, L.EPI_STORE), down=_call(64, 64, L.EPI_STORE))
-    arr = (L.DecodeLayer * 1)(layer)
-    assert lib.wg_decode_plan_create(arr, 1, C.byref(h)) == -1
-    assert "epilogue mode" in L.last_error()
-    # native Q4_K matrices are not streamed by the persistent kernel
-    layer.qkv.w = _desc(N=64, K=256, layout=L.LAYOUT_Q4K)
-    layer.qkv.ldx = 256
-    arr = (L.DecodeLayer * 1)(layer)
-    assert lib.wg_decode_plan_create(arr, 1, C.byref(h)) == -6  # unsupported
-    assert "row-group" in L.last_error()
-    assert not h.value
-
-
 def test_argmax_advance_rejects_before_any_device_work():
     lib = L.load()
     f = 0x1000  # fake device addresses: validation fails before a launch

@@ -147,79 +147,6 @@ def test_full_width_shapes(hip, name, layers):
     assert eng.decode(first, 4) == orc.decode(first, 4)
 
 
-@pytest.mark.parametrize("family", ["q4_k-rowgroup", "qwen-nbits"])
-def test_persistent_decode_matches_per_op_path(hip, family):
-    """The one-launch decode (wg_decode_run) against the per-op path on the
-    same weights: identical tokens, logits within the 1e-3 bar (the paths
-    sum in different orders, and a flipped half rounding of an activation
-    moves the logits by ~1e-4)."""
-    from webgllm_amd.engine import Engine, Weights
-    args = dict(FAMILIES[family])
-    w = Weights(_shape(**args, layers=4), seed=13)
-    fast, ref = Engine(w, 256, persistent=True), Engine(w, 256)
-    assert fast.plan is not None and ref.plan is None
-    rng = np.random.default_rng(4)
-    prompt = _prompt(rng, 17, fast.shape.vocab)
-    t1 = int(fast.forward(prompt).cpu()[-1])
-    t2 = int(ref.forward(prompt).cpu()[-1])
-    assert t1 == t2
-    for _ in range(6):  # eager single-row steps through both paths
-        a = int(fast.forward([t1]).cpu()[0])
-        b = int(ref.forward([t2]).cpu()[0])
-        assert rel_l2(fast.logits[:1].cpu().numpy(), ref.logits[:1].cpu().numpy()) <= 1e-3
-        assert a == b
-        t1, t2 = a, b
-    assert fast.decode(t1, 10) == ref.decode(t2, 10)
-
-
-def test_persistent_decode_long_context(hip):
-    """Llama-like heads (head_dim 128, 4 query heads per KV head) past 1024
-    keys, where attention spans 18 chunks and RoPE angles use the table's
-    second rows: persistent and per-op paths agree token for token."""
-    from webgllm_amd.engine import Engine, Weights
-    w = Weights(_shape("q4_k_rowgroup", layers=2, hidden=512, heads=8, kv=2, hd=128,
-                       inter=1024), seed=19)
-    fast, ref = Engine(w, 1536, persistent=True), Engine(w, 1536)
-    assert fast.plan is not None
-    rng = np.random.default_rng(8)
-    prompt = _prompt(rng, 1100, w.shape.vocab)
-    t1 = int(fast.forward(prompt).cpu()[-1])
-    t2 = int(ref.forward(prompt).cpu()[-1])
-    assert t1 == t2
-    for _ in range(4):
-        a = int(fast.forward([t1]).cpu()[0])
-        b = int(ref.forward([t2]).cpu()[0])
-        assert rel_l2(fast.logits[:1].cpu().numpy(), ref.logits[:1].cpu().numpy()) <= 1e-3
-        assert a == b
-        t1, t2 = a, b
-    assert fast.decode(t1, 8) == ref.decode(t2, 8)
-
-
-def test_persistent_decode_reports_a_barrier_timeout(hip):
-    """A poll limit of 1 makes every grid-barrier wait give up at once (the
-    kernel still drains); the status call reports it and resets the barrier
-    state, after which decoding is exact again."""
-    from webgllm_amd import lib as L
-    from webgllm_amd.engine import Engine
-    eng, orc = _pair("q4_k-rowgroup", seed=21)
-    eng = Engine(eng.w, eng.ctx, persistent=True)
-    rng = np.random.default_rng(3)
-    prompt = _prompt(rng, 9, eng.shape.vocab)
-    first = int(eng.forward(prompt).cpu()[-1])
-    saved_pos = eng.position
-    eng.plan.set_spin_limit(1)
-    eng.pos.fill_(eng.position)
-    eng.ids[0] = first
-    eng._forward_rows(1, keep_prefixes=False)
-    with pytest.raises(L.WgError, match="barrier"):
-        eng.check_plan()
-    eng.check_plan()  # reset: no error left behind
-    eng.plan.set_spin_limit(1 << 20)
-    eng.position = saved_pos
-    orc.forward(prompt)
-    assert eng.decode(first, 6) == orc.decode(first, 6)
-
-
 @pytest.mark.parametrize("family", ["q4_k-rowgroup", "lfm2-q4_0", "qwen-nbits"])
 def test_long_prompt_through_gemm_batches(hip, family, monkeypatch):
     """A 600-token prompt: rows 0..591 in GEMM batches of 512 and 80 (MFMA

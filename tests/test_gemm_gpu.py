@@ -227,41 +227,46 @@ def test_gemm_split_k_first_launches(hip):
 
 
 def test_gemm_split_k_prefill_shape_in_graph(hip):
-    """The 512 x 4096 -> 4096 prefill GEMM (split by default) captured in a
-    graph and replayed with eager launches between the replays: every
-    replay equals the eager result bit for bit, so the counters are back at
-    zero after each launch. A first capture on a stream with no workspace
-    yet runs unsplit (no allocation while capturing)."""
+    """The 512 x 4096 -> 4096 prefill GEMM (split by default when eager)
+    captured in a graph runs unsplit: every replay equals the unsplit result
+    bit for bit, also with eager split launches on the capture stream
+    between replays and after the stream's workspace has grown, and when
+    replayed on another stream; the eager launches equal one another."""
     from webgllm_amd import lib as L, ops
     m = _matrix("nbits", 4096, 4096, seed=5)
     rng = np.random.default_rng(5)
     a = _t(O.f32_to_h2(rng.standard_normal((512, 4096)).astype(np.float32)).view(np.int16))
-    s = torch.cuda.Stream()
-    out = torch.empty((512, 4096), device="cuda")
-    g0 = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(g0, stream=s):
-            ops.gemm(m, a, out=out)
     L.tuning_set("gemm_splits", 1)
     try:
         unsplit = ops.gemm(m, a)
     finally:
         L.tuning_set("gemm_splits", 0)
-    g0.replay()
-    torch.cuda.synchronize()
-    assert torch.equal(out, unsplit)
+    s = torch.cuda.Stream()
+    out = torch.empty((512, 4096), device="cuda")
     with torch.cuda.stream(s):
-        eager = ops.gemm(m, a)  # allocates this stream's workspace
+        eager = ops.gemm(m, a)  # this stream's workspace
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        out2 = torch.empty_like(out)
         with torch.cuda.graph(g, stream=s):
-            ops.gemm(m, a, out=out2)
-        for i in range(5):
-            out2.fill_(float("nan"))
+            ops.gemm(m, a, out=out)
+        for i in range(4):
+            out.fill_(float("nan"))
             g.replay()
             other = ops.gemm(m, a)
             torch.cuda.synchronize()
-            assert torch.equal(out2, eager), i
+            assert torch.equal(out, unsplit), i
             assert torch.equal(other, eager), i
+        # a 4-way split needs more room: the workspace grows (is freed and
+        # allocated again)
+        L.tuning_set("gemm_splits", 4)
+        try:
+            four = ops.gemm(m, a)
+        finally:
+            L.tuning_set("gemm_splits", 0)
+        torch.cuda.synchronize()
+        assert rel_l2(four.cpu().numpy(), unsplit.cpu().numpy()) <= 1e-6
+    out.fill_(float("nan"))
+    g.replay()  # on the current stream, not the capture stream
+    torch.cuda.synchronize()
+    assert torch.equal(out, unsplit)
     assert rel_l2(eager.cpu().numpy(), unsplit.cpu().numpy()) <= 1e-6

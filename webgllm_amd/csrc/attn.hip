@@ -1483,6 +1483,73 @@ static int noalloc_scratch(void **out, hipStream_t stream) {
   return WG_OK;
 }
 
+// The XCD-grouped forms take for granted that the dispatcher deals
+// workgroups to 8 XCDs round-robin: the 8 workgroups b = 8r .. 8r + 7 run
+// one on each XCD (the whole MI355X in its single-partition mode). On a
+// partitioned device, one with another XCD count, or under a CU mask, a
+// workgroup would take a (KV head, split) pair another one also takes and
+// leave one untaken, so the grouped forms run only where the device says it
+// has 8 XCDs and a probe launch has seen every such group of 8 land on 8
+// distinct XCDs.
+constexpr int PROBE_BLOCKS = 8 * 256;
+static __device__ int xcd_probe_ids[PROBE_BLOCKS];
+
+__global__ void xcd_probe_kernel(int *ids) {
+  if (threadIdx.x == 0) ids[blockIdx.x] = xcd_id();
+}
+
+// Whether the XCD-grouped forms may run on the current device: decided once
+// a device, by the first call not made while the stream is being captured
+// (the probe waits for its own launch); a call under capture before then
+// takes the ungrouped forms.
+static bool xcd_grouping(hipStream_t stream) {
+  static std::mutex mu;
+  static signed char known[64];  // 0 unknown, 1 grouped forms allowed, -1 not
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  std::lock_guard<std::mutex> lock(mu);
+  if (known[dev]) return known[dev] > 0;
+  int xccs = 0;
+  if (hipDeviceGetAttribute(&xccs, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess ||
+      xccs != XCDS) {
+    (void)hipGetLastError();
+    known[dev] = -1;
+    return false;
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return false;
+  }
+  void *d = nullptr;
+  if (hipGetSymbolAddress(&d, HIP_SYMBOL(xcd_probe_ids)) != hipSuccess || !d) {
+    (void)hipGetLastError();
+    known[dev] = -1;
+    return false;
+  }
+  static int ids[PROBE_BLOCKS];
+  xcd_probe_kernel<<<PROBE_BLOCKS, 64, 0, stream>>>((int *)d);
+  if (hipGetLastError() != hipSuccess ||
+      hipMemcpyAsync(ids, d, sizeof ids, hipMemcpyDeviceToHost, stream) != hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess) {
+    (void)hipGetLastError();
+    known[dev] = -1;
+    return false;
+  }
+  bool ok = true;
+  for (int g = 0; ok && g < PROBE_BLOCKS / XCDS; g++) {
+    int seen = 0;
+    for (int j = 0; j < XCDS; j++) {
+      const int x = ids[g * XCDS + j];
+      if (x < 0 || x >= XCDS) ok = false;
+      else seen |= 1 << x;
+    }
+    ok = ok && seen == (1 << XCDS) - 1;
+  }
+  known[dev] = ok ? 1 : -1;
+  return ok;
+}
+
 }  // namespace wg
 
 using namespace wg;
@@ -1609,9 +1676,11 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
   // takes the XCD-grouped form where it applies, 0 never (nor groups the
   // MFMA form by XCD).
   const int GMq = (H / KV) * M;
-  const bool groupable = KV % XCDS == 0;
-  const int mfma_knob = tuning("attn_mfma");
+  hipStream_t s = as_stream(stream);
   const int xcd_knob = tuning("attn_xcd");
+  // (the XCD-grouped forms only where the dispatch they assume is checked)
+  const bool groupable = KV % XCDS == 0 && xcd_grouping(s);
+  const int mfma_knob = tuning("attn_mfma");
   const bool xl_range = groupable && GMq <= 4 && max_keys < 4096 && xcd_knob != 0;
   const bool amfma = KV * ((GMq + 15) / 16) <= MAX_KV_COUNTERS &&
                      (mfma_knob == 2 ||
@@ -1628,7 +1697,6 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
   WG_REQUIRE(scratch_bytes >= wg_attn_scratch_bytes(M, H, hd, max_keys),
              "wg_attn_decode: scratch of %zu bytes, %zu needed", scratch_bytes,
              wg_attn_scratch_bytes(M, H, hd, max_keys));
-  hipStream_t s = as_stream(stream);
   int *counters = (int *)scratch;
   float *partial = (float *)((char *)scratch + COUNTER_BYTES);
   const int chunks = (max_keys + CHUNK - 1) / CHUNK;
@@ -1645,7 +1713,7 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
     const size_t lds = (size_t)AW * (hd == 64 ? amfma_wave_bytes<64>() : amfma_wave_bytes<128>());
     const dim3 grid((unsigned)(units * splits));
     // units a multiple of 8: grouped by XCD (attn_xcd 0: never)
-    const bool xg = units % XCDS == 0 && xcd_knob != 0;
+    const bool xg = units % XCDS == 0 && xcd_knob != 0 && xcd_grouping(s);
 #define WG_AMFMA_LAUNCH(HDV, XGV)                                                               \
   do {                                                                                          \
     int rc_ = raise_lds((const void *)attn_mfma_kernel<HDV, XGV>, (int)lds);                    \

@@ -486,8 +486,11 @@ __global__ void split_zero_kernel(int *count, int n) {
 
 // A split-K workspace per device and stream (launches on one stream run in
 // turn; other streams get their own): the partial slots and the tree's
-// counters, grown on demand and kept until the process ends. The counters
-// start at zero and every launch leaves them so.
+// counters, grown on demand. The counters start at zero and every launch
+// leaves them so. A launch recorded into a graph never takes it: a graph
+// may replay on another stream, beside eager launches on this one, and
+// must not outlive a workspace that grows (is freed and allocated again)
+// after the capture; captured GEMMs run unsplit.
 struct SplitSpace {
   int dev;
   hipStream_t stream;
@@ -498,13 +501,19 @@ struct SplitSpace {
 };
 
 // The workspace for `floats` partial floats and `counters` counters on
-// stream s; part stays null when it would have to grow while s is being
-// captured into a graph (no allocation there: the launch runs unsplit).
+// stream s; part stays null while s is being captured into a graph (the
+// launch runs unsplit).
 int split_space(hipStream_t s, size_t floats, int counters, float **part, int **count) {
   static std::mutex mu;
   static std::vector<SplitSpace *> spaces;
   *part = nullptr;
   *count = nullptr;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return WG_OK;
+  }
+  if (cs != hipStreamCaptureStatusNone) return WG_OK;
   int dev = 0;
   WG_HIP(hipGetDevice(&dev));
   std::lock_guard<std::mutex> lock(mu);
@@ -512,12 +521,6 @@ int split_space(hipStream_t s, size_t floats, int counters, float **part, int **
   for (SplitSpace *x : spaces)
     if (x->dev == dev && x->stream == s) sp = x;
   if (!sp || sp->floats < floats || sp->counters < counters) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
-      (void)hipGetLastError();
-      return WG_OK;
-    }
-    if (cs != hipStreamCaptureStatusNone) return WG_OK;
     if (!sp) {
       sp = new SplitSpace{dev, s, nullptr, 0, nullptr, 0};
       spaces.push_back(sp);

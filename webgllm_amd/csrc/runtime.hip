@@ -80,7 +80,6 @@ static Knob g_knobs[] = {
     {"gemv_mfma", 1, 0, 2},              // row-group GEMV on MFMA: 1 for 3 to 8 tokens, 2 also 1 and 2, 0 never
     {"gemv_mfma_wg_per_cu", 1, 1, 16},   // its persistent workgroups per CU
     {"gemv_mfma_pairs", 4, 2, 8},        // its block pairs a wave (2, 4, 8)
-    {"decode_wg_per_cu", 1, 1, 4},       // persistent decode workgroups (8 waves) per CU
     {"attn_prefill_mfma", 4, 0, 4},      // prompt attention: MFMA waves a workgroup (1, 2, 4), 0 VALU
     {"attn_mfma", 1, 0, 2},              // decode attention in one launch on MFMA: 1 where it is faster (past 8 queries a KV head, from 16384 keys, outside the XCD-grouped split form's range with KV heads a multiple of 8, else up to 2048 keys), 2 always, 0 never
     {"attn_fused", 1, 0, 2},             // decode attention in one launch: 1 where it is faster, 2 always, 0 never
@@ -178,6 +177,17 @@ bool reg_has(const void *h) {
 }
 
 }  // namespace
+
+// Zeroes `bytes` bytes at p (256-byte aligned): 16 bytes a lane, the tail
+// by the first lanes.
+__global__ void zero_bytes_kernel(uint8_t *p, size_t bytes) {
+  const size_t n16 = bytes / 16;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16;
+       i += (size_t)gridDim.x * blockDim.x)
+    reinterpret_cast<uint4 *>(p)[i] = make_uint4(0, 0, 0, 0);
+  const size_t tail = n16 * 16 + blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (blockIdx.x == 0 && tail < bytes) p[tail] = 0;
+}
 
 struct wg_buf {
   wg_ctx *ctx;
@@ -453,8 +463,12 @@ int wg_buf_zero(wg_ctx *c, wg_buf *b) {
   int rc = owned(c, b, "wg_buf_zero");
   if (rc) return rc;
   WG_HIP(hipSetDevice(c->device));
-  WG_HIP(hipMemsetAsync(b->ptr, 0, b->bytes, c->stream));
-  return WG_OK;
+  // a kernel, not a memset node: a caller may capture the context's stream
+  const size_t n16 = b->bytes / 16;
+  const size_t blocks = (n16 + 255) / 256;
+  zero_bytes_kernel<<<(unsigned)(blocks < 1024 ? (blocks ? blocks : 1) : 1024), 256, 0,
+                      c->stream>>>((uint8_t *)b->ptr, b->bytes);
+  return launched("wg_buf_zero");
 }
 
 int wg_buf_delete(wg_ctx *c, wg_buf *b) {

@@ -226,7 +226,7 @@ class Weights:
 class Engine:
     """Forward, greedy pick and accept over device-resident weights."""
 
-    def __init__(self, weights: Weights, ctx: int, persistent: bool = False):
+    def __init__(self, weights: Weights, ctx: int):
         s = self.shape = weights.shape
         self.w = weights
         self.ctx = ctx
@@ -263,20 +263,12 @@ class Engine:
         # layer) and the attention scratch for that many keys: grown by reserve
         self.kv_positions = 0
         self.graph = None
-        self.plan = None
         self._verify = None
         self._resize_caches(min(ctx, KV_START), keep=0)
         self.position = 0
         self.draft = None
         self._pre = None  # prefill buffers, made on the first prompt batch
         self._cols = {}   # device row orders of the matrices (GEMM column maps)
-        # persistent=True: single-row forwards of attention-only models run as
-        # one persistent launch (wg_decode_run); other shapes, and the
-        # default, take the per-op path. On MI355X a grid barrier costs about
-        # as much as a kernel boundary (~4 us), so the per-op path is the
-        # faster one at the Llama-3-8B shape.
-        self.persistent = persistent
-        self.plan = self._build_plan() if persistent else None
 
     # --- the attention caches, grown on demand ------------------------------
     def reserve(self, end: int) -> None:
@@ -285,9 +277,8 @@ class Engine:
         KV_STEP steps, at least twice the positions they replace (the copies
         then add up to at most the final size: a 128K-token context is not
         copied 250 times over), at most the context, holding the old rows.
-        The captured decode and verify graphs and the persistent plan hold
-        the old caches' addresses: they are dropped (captured again when
-        next used) or rebuilt."""
+        The captured decode and verify graphs hold the old caches'
+        addresses: they are dropped (captured again when next used)."""
         if end > self.ctx:
             raise ValueError(f"The cache holds {self.ctx} tokens; this would need {end}.")
         if end <= self.kv_positions:
@@ -313,8 +304,6 @@ class Engine:
         self.graph = None
         if self._verify is not None:
             self._verify["graph"] = None
-        if self.plan is not None:
-            self.plan = self._build_plan()
 
     # --- the batch ------------------------------------------------------------
     def _norm_in(self, ep: "L.Epilogue") -> "L.Epilogue":
@@ -350,50 +339,13 @@ class Engine:
         w = self.w
         return w.layers[i + 1]["op_norm"] if i + 1 < len(w.layers) else w.final_norm
 
-    def _build_plan(self):
-        """The persistent decode plan of every layer at one row, or None when
-        a layer is not attention with RoPE in the qkv epilogue, or the
-        library does not support the shape (e.g. native Q4_K matrices)."""
-        s, w = self.shape, self.w
-        if not s.rope_in_epilogue or not w.layers or \
-                any(s.layer_type(i) == "conv" for i in range(s.layers)):
-            return None
-        F = s.intermediate
-        x16, h = self.x16[:1], self.h[:1]
-        layers = []
-        for i, lw in enumerate(w.layers):
-            layers.append(L.DecodeLayer(
-                qkv=ops.gemv_call(lw["qkv"], x16, epilogue=self._qkv_epilogue(i)),
-                o=ops.gemv_call(lw["o"], self.att16[:1], out=h,
-                                epilogue=self._residual_out(1, lw["ffn_norm"])),
-                gate_up=ops.gemv_call(lw["gate_up"], x16, epilogue=self._norm_in(
-                    L.Epilogue(mode=L.EPI_SWIGLU, out16=self.ff16.data_ptr(), ld_out16=F))),
-                down=ops.gemv_call(lw["down"], self.ff16[:1], out=h,
-                                   epilogue=self._residual_out(1, self._next_norm(i)))))
-        try:
-            return ops.DecodePlan(layers)
-        except L.WgError as e:
-            if e.kind == "unsupported":
-                return None
-            raise
-
-    def check_plan(self) -> None:
-        """Raises if a persistent launch's barrier wait gave up (waits for
-        the current stream first)."""
-        if self.plan is not None:
-            torch.cuda.current_stream().synchronize()
-            self.plan.status()
-
     def _forward_rows(self, M: int, keep_prefixes: bool, pick: bool = True) -> None:
         """Enqueue one batch of M rows (ids[:M] at positions pos..pos+M-1);
         the greedy picks into next_ids unless `pick` is False (the caller
         picks)."""
         self._embed_rows(M)
-        if M == 1 and self.plan is not None:
-            self.plan.run()
-        else:
-            for i in range(len(self.w.layers)):
-                self._layer_rows(i, M, keep_prefixes)
+        for i in range(len(self.w.layers)):
+            self._layer_rows(i, M, keep_prefixes)
         self._head_rows(M, pick)
 
     def _embed_rows(self, M: int) -> None:
@@ -590,10 +542,7 @@ class Engine:
             out = self.next_ids[:M]
         if draft:
             self.draft = (self.position - len(tokens), len(tokens))
-        out = out.clone()
-        if len(tokens) % MAX_ROWS == 1:
-            self.check_plan()
-        return out
+        return out.clone()
 
     def accept(self, count: int) -> None:
         """Keeps the first `count` tokens of the last draft batch
@@ -667,9 +616,7 @@ class Engine:
         for _ in range(steps):
             self.graph.replay()
         self.position += steps
-        toks = self.hist[p0 + 1:p0 + steps + 1].tolist()
-        self.check_plan()
-        return toks
+        return self.hist[p0 + 1:p0 + steps + 1].tolist()
 
     # --- speculative verify on the device, graph-captured --------------------
     VERIFY_TABLE = 1024  # draft rows the device table holds (steps a replay run takes)
@@ -846,7 +793,6 @@ class Engine:
                     self.guess_misses += 1
                 self._replay_step(t)
             self.position += 1
-            self.check_plan()
             row, greedy_pick = 0, self.ids[:1]  # the step's pick went to ids[0]
         return out
 

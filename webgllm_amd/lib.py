@@ -62,16 +62,6 @@ class Epilogue(C.Structure):
                 ("k_cache", C.c_void_p), ("v_cache", C.c_void_p)]
 
 
-class GemvCall(C.Structure):
-    """wg_gemv_call: one wg_q4_gemv call (M = 1) of a persistent decode layer."""
-    _fields_ = [("w", Q4MatrixDesc), ("x", C.c_void_p), ("ldx", C.c_int32),
-                ("y", C.c_void_p), ("ldy", C.c_int32), ("ep", Epilogue)]
-
-
-class DecodeLayer(C.Structure):
-    _fields_ = [("qkv", GemvCall), ("o", GemvCall), ("gate_up", GemvCall), ("down", GemvCall)]
-
-
 class AttnShape(C.Structure):
     _fields_ = [("heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
                 ("rotated_dims", C.c_int32), ("eps", C.c_float), ("use_norm", C.c_int32)]
@@ -242,11 +232,6 @@ def load():
         "wg_delta_conv": (C.c_int, [P, I32, I32, I32, I32, P, P, P, P, I32, P]),
         "wg_delta_norm": (C.c_int, [P, I32, I32, C.POINTER(DeltaShape), P, I32, P, C.c_float, P,
                                     I32, P]),
-        "wg_decode_plan_create": (C.c_int, [C.POINTER(DecodeLayer), I32, C.POINTER(P)]),
-        "wg_decode_run": (C.c_int, [P, P]),
-        "wg_decode_status": (C.c_int, [P]),
-        "wg_decode_set_spin_limit": (C.c_int, [P, I32]),
-        "wg_decode_plan_destroy": (C.c_int, [P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

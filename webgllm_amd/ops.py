@@ -185,55 +185,6 @@ def gemv(m: Q4Matrix, x16: torch.Tensor, out: torch.Tensor | None = None,
     return out
 
 
-def gemv_call(m: Q4Matrix, x16: torch.Tensor, out: torch.Tensor | None = None,
-              epilogue: "L.Epilogue | None" = None) -> "L.GemvCall":
-    """The arguments of one single-row gemv() as a wg_gemv_call (for a
-    DecodePlan); nothing runs."""
-    if x16.dtype not in (torch.float16, torch.int16):
-        raise ValueError("activations must be halves")
-    _dev(x16)
-    if out is not None:
-        _dev(out, torch.float32)
-    return L.GemvCall(w=m.desc, x=_p(x16), ldx=x16.shape[-1], y=_p(out),
-                      ldy=out.shape[-1] if out is not None else 0,
-                      ep=epilogue if epilogue is not None else L.Epilogue(mode=L.EPI_STORE))
-
-
-class DecodePlan:
-    """wg_decode_plan: the attention layers of a batch-1 token in one
-    persistent launch. `layers` are L.DecodeLayer of four gemv_call()s each;
-    `keep` holds the tensors their pointers refer to."""
-
-    def __init__(self, layers, keep=()):
-        arr = (L.DecodeLayer * len(layers))(*layers)
-        handle = C.c_void_p()
-        L.check(L.load().wg_decode_plan_create(arr, len(layers), C.byref(handle)))
-        self.handle = handle
-        self._keep = keep
-
-    def run(self) -> None:
-        L.check(L.load().wg_decode_run(self.handle, _stream()))
-
-    def status(self) -> None:
-        """Raises WgError if a barrier wait of an earlier run gave up (call
-        after the stream has finished)."""
-        L.check(L.load().wg_decode_status(self.handle))
-
-    def set_spin_limit(self, polls: int) -> None:
-        L.check(L.load().wg_decode_set_spin_limit(self.handle, polls))
-
-    def close(self) -> None:
-        if self.handle:
-            L.load().wg_decode_plan_destroy(self.handle)
-            self.handle = None
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
-
-
 def gemm(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
          residual: torch.Tensor | None = None, col_of: torch.Tensor | None = None,
          row_scale: torch.Tensor | None = None) -> torch.Tensor:
