@@ -101,6 +101,14 @@ size_t wg_bytes_live(wg_ctx *ctx);
  * waits, copies into dst and frees the fence, wg_read_cancel frees it
  * unread (PendingRead.cancel). */
 int wg_read_start(wg_ctx *ctx, wg_buf *buf, size_t offset, size_t bytes, wg_fence **out);
+/* PacedGpu.fence (src/gpu/paced.ts:11-22): a fence behind the work queued
+ * on the context's stream so far, with no read; wg_fence_ready polls it,
+ * wg_read_finish waits for it (dst ignored) and releases it, wg_read_cancel
+ * releases it without waiting (deleteFence). */
+int wg_fence_record(wg_ctx *ctx, wg_fence **out);
+/* The bytes a fence's read copies into wg_read_finish's dst (0 for a plain
+ * fence or a released handle). */
+size_t wg_fence_bytes(wg_fence *f);
 int wg_fence_ready(wg_fence *f); /* 1 ready, 0 pending, < 0 error */
 int wg_read_finish(wg_fence *f, void *dst);
 int wg_read_cancel(wg_fence *f);

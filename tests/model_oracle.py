@@ -82,6 +82,21 @@ class OracleModel:
         self.rope = O.rope_table(s.rope_theta, s.head_dim, s.head_dim, ctx)
         self.reset()
 
+    @classmethod
+    def from_dense(cls, shape, emb, final_norm, layers, ctx):
+        """The decoder over weights given as arrays: emb [V, D] and each
+        layer's matrices as float32/float64 [N, K] in logical row order,
+        vectors and conv taps as they are."""
+        self = cls.__new__(cls)
+        self.s, self.ctx = shape, ctx
+        self.emb = np.asarray(emb, np.float64)
+        self.final = np.asarray(final_norm, np.float32)
+        self.layers = [{k: (np.asarray(v, np.float64) if k in cls.MATRICES else np.asarray(v))
+                        for k, v in lw.items()} for lw in layers]
+        self.rope = O.rope_table(shape.rope_theta, shape.head_dim, shape.head_dim, ctx)
+        self.reset()
+        return self
+
     def reset(self):
         s = self.s
         kvd = s.kv_heads * s.head_dim

@@ -2,7 +2,8 @@
 /*
  * The N-API addon and HipGpu, run by Node (CommonJS, Node 12). Usage:
  *   node addon_test.js cpu <gguf path> <onnx path>   (no GPU: sizes, errors, readers)
- *   node addon_test.js gpu <folder>                   (textures, reads, a Q4_0 GEMV)
+ *   node addon_test.js gpu <folder>                   (textures, reads, fences, a Q4_0 GEMV,
+ *                                                      operands refused by size)
  * Assertions fail the process; a JSON summary of what was read goes to
  * stdout for the Python side to compare with its own readers.
  */
@@ -115,6 +116,37 @@ async function gpu (dir) {
   fs.writeFileSync(path.join(dir, 'dequant.bin'), Buffer.from(gpu.readNow(dq).buffer))
   // bad shapes are refused before any launch
   throwsGpu(() => gpu.ops.gemv(Object.assign({}, w, { K: K + 1 }), tx, M, ty), 'WG_ERR_INVALID')
+  // operands smaller than their shapes imply are refused before any launch
+  // (the device would otherwise read or write past them)
+  const small = gpu.texture(GL.R32F, 4, 1)
+  throwsGpu(() => gpu.ops.gemv(w, tx, M, small), 'WG_ERR_INVALID', 'y: ')
+  throwsGpu(() => gpu.ops.gemv(w, small, M, ty), 'WG_ERR_INVALID', 'x: ')
+  throwsGpu(() => gpu.ops.gemv(w, tx, M, ty, { mode: hip.constants.EPI_STORE, residual: small, ldResidual: N }), 'WG_ERR_INVALID', 'residual')
+  throwsGpu(() => gpu.ops.gemv(Object.assign({}, w, { quants: small }), tx, M, ty), 'WG_ERR_INVALID', 'quants')
+  throwsGpu(() => gpu.ops.gemv(w, gpu.view(tx, x16.length - 16), M, ty), 'WG_ERR_INVALID', 'offset')
+  throwsGpu(() => gpu.ops.repack('q4_0', w, 0, N, small), 'WG_ERR_INVALID', 'src')
+  throwsGpu(() => gpu.ops.repack('q4_0', w, 0, 4, tsrc, Int32Array.from([0, 1, 2, N])), 'WG_ERR_INVALID', 'srcRows[3]')
+  throwsGpu(() => gpu.ops.argmax(ty, M, N, ids, small), 'WG_ERR_INVALID', 'scratch')
+  throwsGpu(() => gpu.ops.dequant(w, 0, 4, small), 'WG_ERR_INVALID', 'out')
+  const shape = { heads: 4, kvHeads: 2, headDim: 64 }
+  throwsGpu(() => gpu.ops.attnDecode(small, 1, shape, small, small, small, 16, small, small), 'WG_ERR_INVALID')
+  throwsGpu(() => gpu.ops.shortConv(small, 1, 64, 3, small, small, small, null, small), 'WG_ERR_INVALID', 'bcx')
+  // a read's bytes are the fence's own: another count is refused before the copy
+  const rf = hip.addon.readStart(gpu.ctx, ty.tex, 0, 64)
+  throwsGpu(() => hip.addon.readFinish(rf, 4096), 'WG_ERR_INVALID', 'holds 64 bytes')
+  assert.strictEqual(hip.addon.readFinish(rf).byteLength, 64)
+  // plain fences (PacedGpu.fence / fenceReady / wait / deleteFence)
+  const f1 = gpu.fence()
+  await gpu.wait(f1)
+  const f2 = gpu.fence()
+  gpu.deleteFence(f2)
+  throwsGpu(() => hip.addon.fenceReady(f2), 'WG_ERR_DISPOSED')
+  assert.strictEqual(gpu.readBack(), true)
+  // the device still works after the refusals: the same GEMV again
+  gpu.ops.gemv(w, tx, M, ty)
+  const y2 = await gpu.read(ty)
+  assert.deepStrictEqual(Array.from(y2), Array.from(y))
+  assert.ok(gpu.limits.maxTextureSize >= 1 << 20 && gpu.limits.maxTextureUnits >= 16)
   const staging = hip.addon.staging(gpu.ctx)
   gpu.dispose()
   assert.strictEqual(hip.addon.bytesLive(gpu.ctx), 0)

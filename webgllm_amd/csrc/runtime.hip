@@ -195,10 +195,13 @@ struct wg_buf {
   size_t bytes;
 };
 
+// A fence: a read's (its staging slot's event) or a plain one (its own
+// event, no slot, no bytes).
 struct wg_fence {
   wg_ctx *ctx;
   Slot *slot;
   size_t bytes;
+  hipEvent_t ev;
 };
 
 struct wg_ctx {
@@ -293,10 +296,13 @@ int owned(wg_ctx *c, wg_buf *b, const char *who) {
   return WG_OK;
 }
 
+hipEvent_t fence_event(const wg_fence *f) { return f->slot ? f->slot->done : f->ev; }
+
 void fence_release(wg_fence *f, bool copied) {
   // a fence's copy that was never waited for may still be landing: its slot
   // is reused only after its event
-  f->slot->state = copied ? SLOT_FREE : SLOT_INFLIGHT;
+  if (f->slot) f->slot->state = copied ? SLOT_FREE : SLOT_INFLIGHT;
+  if (f->ev) (void)hipEventDestroy(f->ev);
   f->ctx->fences.erase(f);
   reg_del(f);
   delete f;
@@ -358,6 +364,7 @@ int wg_ctx_destroy(wg_ctx *c) {
     // outstanding reads are cancelled: their handles report WG_ERR_DISPOSED
     for (wg_fence *f : c->fences) {
       reg_del(f);
+      if (f->ev) (void)hipEventDestroy(f->ev);
       delete f;
     }
     c->fences.clear();
@@ -524,17 +531,40 @@ int wg_read_start(wg_ctx *c, wg_buf *b, size_t offset, size_t bytes, wg_fence **
     s->state = SLOT_FREE;
     return fail(WG_ERR_DEVICE, "wg_read_start: %s", hipGetErrorString(e));
   }
-  wg_fence *f = new wg_fence{c, s, bytes};
+  wg_fence *f = new wg_fence{c, s, bytes, nullptr};
   c->fences.insert(f);
   reg_add(f);
   *out = f;
   return WG_OK;
 }
 
+int wg_fence_record(wg_ctx *c, wg_fence **out) {
+  WG_REQUIRE(c && out, "wg_fence_record: null argument");
+  if (!reg_has(c)) return fail(WG_ERR_DISPOSED, "wg_fence_record: the context was destroyed");
+  WG_HIP(hipSetDevice(c->device));
+  hipEvent_t ev = nullptr;
+  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(ev, c->stream);
+  if (e != hipSuccess) {
+    if (ev) (void)hipEventDestroy(ev);
+    return fail(WG_ERR_DEVICE, "wg_fence_record: %s", hipGetErrorString(e));
+  }
+  wg_fence *f = new wg_fence{c, nullptr, 0, ev};
+  {
+    std::lock_guard<std::mutex> g(c->lock);
+    c->fences.insert(f);
+  }
+  reg_add(f);
+  *out = f;
+  return WG_OK;
+}
+
+size_t wg_fence_bytes(wg_fence *f) { return reg_has(f) ? f->bytes : 0; }
+
 int wg_fence_ready(wg_fence *f) {
   WG_REQUIRE(f, "wg_fence_ready: no fence");
   if (!reg_has(f)) return fail(WG_ERR_DISPOSED, "wg_fence_ready: the read was finished or cancelled");
-  hipError_t e = hipEventQuery(f->slot->done);
+  hipError_t e = hipEventQuery(fence_event(f));
   if (e == hipSuccess) return 1;
   if (e == hipErrorNotReady) return 0;
   return fail(WG_ERR_DEVICE, "wg_fence_ready: %s", hipGetErrorString(e));
@@ -545,9 +575,9 @@ int wg_read_finish(wg_fence *f, void *dst) {
   if (!reg_has(f))
     return fail(WG_ERR_DISPOSED, "wg_read_finish: the read was finished or cancelled");
   wg_ctx *c = f->ctx;
-  hipError_t e = hipEventSynchronize(f->slot->done);
+  hipError_t e = hipEventSynchronize(fence_event(f));
   std::lock_guard<std::mutex> g(c->lock);
-  if (e == hipSuccess && dst) memcpy(dst, f->slot->host, f->bytes);
+  if (e == hipSuccess && dst && f->slot) memcpy(dst, f->slot->host, f->bytes);
   fence_release(f, e == hipSuccess);
   if (e != hipSuccess) return fail(WG_ERR_DEVICE, "wg_read_finish: %s", hipGetErrorString(e));
   return WG_OK;

@@ -16,6 +16,8 @@
  *
  * Paths cited are relative to packages/webgllm/ of the reference.
  */
+#include <stdarg.h>
+#include <stddef.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -356,16 +358,46 @@ static napi_value js_fence_ready(napi_env env, napi_callback_info info) {
   return v;
 }
 
-/* readFinish(fence, bytes): waits, returns an ArrayBuffer of `bytes`. */
+/* readFinish(fence, bytes?): waits, returns an ArrayBuffer of the fence's
+ * bytes (a `bytes` other than the read's is refused before anything is
+ * copied); a plain fence returns an empty one. */
 static napi_value js_read_finish(napi_env env, napi_callback_info info) {
   ARGS(2);
   HANDLE_ARG(0, wg_fence, f, H_FENCE, "fence");
-  INT64_ARG(1, bytes);
+  const size_t have = wg_fence_bytes(f);
+  if (!is_nullish(env, argv[1])) {
+    INT64_ARG(1, bytes);
+    if ((uint64_t)bytes != (uint64_t)have) {
+      char text[128];
+      snprintf(text, sizeof text, "readFinish: the read holds %zu bytes, not %lld", have,
+               (long long)bytes);
+      napi_value msg, code, err, name;
+      napi_create_string_utf8(env, text, NAPI_AUTO_LENGTH, &msg);
+      napi_create_string_utf8(env, "WG_ERR_INVALID", NAPI_AUTO_LENGTH, &code);
+      napi_create_error(env, code, msg, &err);
+      napi_create_string_utf8(env, "GpuError", NAPI_AUTO_LENGTH, &name);
+      napi_set_named_property(env, err, "name", name);
+      napi_throw(env, err);
+      return NULL;
+    }
+  }
   void *data = NULL;
   napi_value ab;
-  NAPI_OK(napi_create_arraybuffer(env, (size_t)bytes, &data, &ab));
-  int rc = wg_read_finish(f, data);
+  NAPI_OK(napi_create_arraybuffer(env, have, &data, &ab));
+  int rc = wg_read_finish(f, have ? data : NULL);
   return rc ? throw_wg(env, rc) : ab;
+}
+
+/* fence(ctx): PacedGpu.fence (src/gpu/paced.ts:11-22), a fence behind the
+ * work queued so far; fenceReady polls it, readCancel deletes it
+ * (deleteFence), readFinish waits for it. */
+static napi_value js_fence_record(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  wg_fence *f = NULL;
+  int rc = wg_fence_record(c, &f);
+  if (rc) return throw_wg(env, rc);
+  return wrap(env, H_FENCE, f);
 }
 
 static napi_value js_read_cancel(napi_env env, napi_callback_info info) {
@@ -403,58 +435,290 @@ static napi_value js_finish(napi_env env, napi_callback_info info) {
   return rc ? throw_wg(env, rc) : NULL;
 }
 
-/* ------------------------------------------------------------ typed ops */
+/* ------------------------------------------------------------ typed ops
+ *
+ * Every device operand is a buffer handle, or [handle, byteOffset] for a
+ * view into one. Before any launch the addon checks that each operand
+ * holds what the shapes imply from its offset on (rows of a [M][ld] array:
+ * (M - 1) ld + width elements), and throws a GpuError WG_ERR_INVALID
+ * otherwise, as the reference's backend throws for a texture over its
+ * limits (src/gpu/gl.ts:271-275); the library then checks the shapes
+ * themselves. */
 
-/* A matrix object {N, K, layout, zero, quants: buf, scales?: buf,
- * zeros?: buf} as the C descriptor. */
-static int read_matrix(napi_env env, napi_value o, wg_q4_matrix *m) {
-  napi_value v;
-  memset(m, 0, sizeof *m);
-  int32_t *ints[4] = {&m->N, &m->K, &m->layout, &m->zero};
-  const char *names[4] = {"N", "K", "layout", "zero"};
-  for (int k = 0; k < 4; k++) {
-    if (napi_get_named_property(env, o, names[k], &v) != napi_ok || !get_i32(env, v, ints[k])) {
+static napi_value throw_limits(napi_env env, const char *fmt, ...) {
+  char text[256];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(text, sizeof text, fmt, ap);
+  va_end(ap);
+  napi_value msg, code, err, name, status;
+  napi_create_string_utf8(env, text, NAPI_AUTO_LENGTH, &msg);
+  napi_create_string_utf8(env, "WG_ERR_INVALID", NAPI_AUTO_LENGTH, &code);
+  napi_create_error(env, code, msg, &err);
+  napi_create_string_utf8(env, "GpuError", NAPI_AUTO_LENGTH, &name);
+  napi_set_named_property(env, err, "name", name);
+  napi_create_int32(env, WG_ERR_INVALID, &status);
+  napi_set_named_property(env, err, "status", status);
+  napi_throw(env, err);
+  return NULL;
+}
+
+/* Elements a [rows][ld] array of rows `width` wide spans (0 for no rows). */
+static uint64_t span(int64_t rows, int64_t ld, int64_t width) {
+  if (rows <= 0 || width <= 0) return 0;
+  return (uint64_t)(rows - 1) * (uint64_t)(ld > width ? ld : width) + (uint64_t)width;
+}
+
+/* A device operand: the pointer `need` bytes of which must lie in its
+ * buffer from its offset on. Optional operands may be null or undefined
+ * (NULL out). Returns 0 after throwing. */
+static int operand(napi_env env, napi_value v, uint64_t need, int optional, const char *what,
+                   void **out) {
+  *out = NULL;
+  if (is_nullish(env, v)) {
+    if (optional) return 1;
+    char msg[96];
+    snprintf(msg, sizeof msg, "%s: a buffer is required", what);
+    napi_throw_type_error(env, "EARG", msg);
+    return 0;
+  }
+  napi_value h = v;
+  int64_t offset = 0;
+  bool is_array = false;
+  if (napi_is_array(env, v, &is_array) == napi_ok && is_array) {
+    uint32_t n = 0;
+    napi_value off;
+    if (napi_get_array_length(env, v, &n) != napi_ok || n != 2 ||
+        napi_get_element(env, v, 0, &h) != napi_ok || napi_get_element(env, v, 1, &off) != napi_ok ||
+        !get_i64(env, off, &offset) || offset < 0) {
       char msg[96];
-      snprintf(msg, sizeof msg, "matrix.%s must be an integer", names[k]);
+      snprintf(msg, sizeof msg, "%s: a view is [buffer, byteOffset >= 0]", what);
       napi_throw_type_error(env, "EARG", msg);
       return 0;
     }
   }
-  const char *arrays[3] = {"quants", "scales", "zeros"};
-  void **ptrs[3] = {(void **)&m->quants, (void **)&m->scales, (void **)&m->zeros};
-  for (int k = 0; k < 3; k++) {
-    if (napi_get_named_property(env, o, arrays[k], &v) != napi_ok) return 0;
-    if (is_nullish(env, v)) continue;
-    wg_buf *b = (wg_buf *)unwrap(env, v, H_BUF, "buffer");
-    if (!b) return 0;
-    *ptrs[k] = wg_buf_ptr(b);
-    if (!*ptrs[k]) {
-      napi_throw_error(env, "WG_ERR_DISPOSED", "a matrix buffer was deleted");
-      return 0;
-    }
+  char kind[96];
+  snprintf(kind, sizeof kind, "buffer for %s", what);
+  wg_buf *b = (wg_buf *)unwrap(env, h, H_BUF, kind);
+  if (!b) return 0;
+  char *p = (char *)wg_buf_ptr(b);
+  if (!p) {
+    char msg[96];
+    snprintf(msg, sizeof msg, "%s: the buffer was deleted", what);
+    napi_value m, c, err;
+    napi_create_string_utf8(env, msg, NAPI_AUTO_LENGTH, &m);
+    napi_create_string_utf8(env, "WG_ERR_DISPOSED", NAPI_AUTO_LENGTH, &c);
+    napi_create_error(env, c, m, &err);
+    napi_value name;
+    napi_create_string_utf8(env, "GpuError", NAPI_AUTO_LENGTH, &name);
+    napi_set_named_property(env, err, "name", name);
+    napi_throw(env, err);
+    return 0;
+  }
+  const uint64_t size = wg_buf_size(b);
+  if ((uint64_t)offset > size || need > size - (uint64_t)offset) {
+    throw_limits(env, "%s: %llu bytes needed at offset %lld of a %llu-byte buffer", what,
+                 (unsigned long long)need, (long long)offset, (unsigned long long)size);
+    return 0;
+  }
+  *out = p + offset;
+  return 1;
+}
+
+#define OPERAND(i, type, var, need, optional, what)                              \
+  type *var;                                                                      \
+  do {                                                                            \
+    void *p_;                                                                     \
+    if (!operand(env, argv[i], (uint64_t)(need), optional, what, &p_)) return NULL; \
+    var = (type *)p_;                                                             \
+  } while (0)
+
+static int get_f64(napi_env env, napi_value v, double *out) {
+  napi_valuetype t;
+  return napi_typeof(env, v, &t) == napi_ok && t == napi_number &&
+         napi_get_value_double(env, v, out) == napi_ok;
+}
+
+#define FLOAT_ARG(i, var)                                                        \
+  float var;                                                                     \
+  do {                                                                           \
+    double d_;                                                                   \
+    if (!get_f64(env, argv[i], &d_)) return type_error(env, #var " must be a number"); \
+    var = (float)d_;                                                             \
+  } while (0)
+
+static int prop(napi_env env, napi_value o, const char *key, napi_value *v) {
+  bool has = false;
+  if (napi_has_named_property(env, o, key, &has) != napi_ok || !has) {
+    napi_get_undefined(env, v);
+    return 1;
+  }
+  return napi_get_named_property(env, o, key, v) == napi_ok;
+}
+
+/* An integer property (0 when absent). */
+static int prop_i32(napi_env env, napi_value o, const char *key, int32_t *out) {
+  napi_value v;
+  *out = 0;
+  if (!prop(env, o, key, &v)) return 0;
+  if (is_nullish(env, v)) return 1;
+  if (!get_i32(env, v, out)) {
+    char msg[96];
+    snprintf(msg, sizeof msg, "%s must be an integer", key);
+    napi_throw_type_error(env, "EARG", msg);
+    return 0;
   }
   return 1;
 }
 
-static void *buf_ptr_arg(napi_env env, napi_value v, int optional, int *ok) {
-  *ok = 1;
-  if (optional && is_nullish(env, v)) return NULL;
-  wg_buf *b = (wg_buf *)unwrap(env, v, H_BUF, "buffer");
-  if (!b) {
-    *ok = 0;
-    return NULL;
+static int prop_f32(napi_env env, napi_value o, const char *key, float *out) {
+  napi_value v;
+  double d = 0;
+  *out = 0.0f;
+  if (!prop(env, o, key, &v)) return 0;
+  if (is_nullish(env, v)) return 1;
+  if (!get_f64(env, v, &d)) {
+    char msg[96];
+    snprintf(msg, sizeof msg, "%s must be a number", key);
+    napi_throw_type_error(env, "EARG", msg);
+    return 0;
   }
-  void *p = wg_buf_ptr(b);
-  if (!p) {
-    *ok = 0;
-    napi_throw_error(env, "WG_ERR_DISPOSED", "the buffer was deleted");
-  }
-  return p;
+  *out = (float)d;
+  return 1;
 }
 
+static int prop_operand(napi_env env, napi_value o, const char *key, uint64_t need, int optional,
+                        void **out) {
+  napi_value v;
+  if (!prop(env, o, key, &v)) return 0;
+  return operand(env, v, need, optional, key, out);
+}
+
+/* A matrix object {N, K, layout, zero, quants, scales?, zeros?} (the
+ * QuantMatrix arrays, src/weights.ts:1-31) as the C descriptor, each array
+ * holding what wg_q4_sizes says its shape needs. */
+static int read_matrix(napi_env env, napi_value o, wg_q4_matrix *m) {
+  memset(m, 0, sizeof *m);
+  napi_valuetype t;
+  if (napi_typeof(env, o, &t) != napi_ok || t != napi_object) {
+    napi_throw_type_error(env, "EARG", "matrix must be an object");
+    return 0;
+  }
+  if (!prop_i32(env, o, "N", &m->N) || !prop_i32(env, o, "K", &m->K) ||
+      !prop_i32(env, o, "layout", &m->layout) || !prop_i32(env, o, "zero", &m->zero))
+    return 0;
+  size_t q = 0, s = 0, z = 0;
+  int rc = wg_q4_sizes(m->N, m->K, m->layout, m->zero, &q, &s, &z);
+  if (rc) {
+    throw_wg(env, rc);
+    return 0;
+  }
+  void *p;
+  if (!prop_operand(env, o, "quants", q, 0, &p)) return 0;
+  m->quants = p;
+  if (!prop_operand(env, o, "scales", s, s == 0, &p)) return 0;
+  m->scales = p;
+  if (!prop_operand(env, o, "zeros", z, z == 0, &p)) return 0;
+  m->zeros = p;
+  return 1;
+}
+
+#define MATRIX_ARG(i, var) \
+  wg_q4_matrix var;        \
+  if (!read_matrix(env, argv[i], &var)) return NULL
+
+/* An attention shape {heads, kvHeads, headDim, rotatedDims?, eps?, useNorm?}. */
+static int read_attn_shape(napi_env env, napi_value o, wg_attn_shape *sh) {
+  memset(sh, 0, sizeof *sh);
+  napi_valuetype t;
+  if (napi_typeof(env, o, &t) != napi_ok || t != napi_object) {
+    napi_throw_type_error(env, "EARG", "shape must be an object");
+    return 0;
+  }
+  if (!prop_i32(env, o, "heads", &sh->heads) || !prop_i32(env, o, "kvHeads", &sh->kv_heads) ||
+      !prop_i32(env, o, "headDim", &sh->head_dim) ||
+      !prop_i32(env, o, "rotatedDims", &sh->rotated_dims) || !prop_f32(env, o, "eps", &sh->eps) ||
+      !prop_i32(env, o, "useNorm", &sh->use_norm))
+    return 0;
+  if (!sh->rotated_dims) sh->rotated_dims = sh->head_dim;
+  if (sh->heads <= 0 || sh->kv_heads <= 0 || sh->head_dim <= 0) {
+    throw_limits(env, "attention shape: %d heads over %d KV heads of %d", sh->heads, sh->kv_heads,
+                 sh->head_dim);
+    return 0;
+  }
+  return 1;
+}
+
+#define SHAPE_ARG(i, var) \
+  wg_attn_shape var;      \
+  if (!read_attn_shape(env, argv[i], &var)) return NULL
+
+/* An epilogue object (wg_epilogue with camelCase names) for M rows of an
+ * N-row matrix; absent fields are zero or null. */
+static int read_epilogue(napi_env env, napi_value o, int32_t M, int32_t N, wg_epilogue *e) {
+  memset(e, 0, sizeof *e);
+  napi_valuetype t;
+  if (napi_typeof(env, o, &t) != napi_ok || t != napi_object) {
+    napi_throw_type_error(env, "EARG", "epilogue must be an object");
+    return 0;
+  }
+  static const struct {
+    const char *key;
+    size_t at;
+  } ints[] = {
+      {"mode", offsetof(wg_epilogue, mode)},
+      {"nParts", offsetof(wg_epilogue, n_parts)},
+      {"ldPartsIn", offsetof(wg_epilogue, ld_parts_in)},
+      {"normCount", offsetof(wg_epilogue, norm_count)},
+      {"ldResidual", offsetof(wg_epilogue, ld_residual)},
+      {"ldOut16", offsetof(wg_epilogue, ld_out16)},
+      {"ldPartsOut", offsetof(wg_epilogue, ld_parts_out)},
+      {"heads", offsetof(wg_epilogue, heads)},
+      {"kvHeads", offsetof(wg_epilogue, kv_heads)},
+      {"headDim", offsetof(wg_epilogue, head_dim)},
+      {"ctx", offsetof(wg_epilogue, ctx)},
+      {"ropeRows", offsetof(wg_epilogue, rope_rows)},
+      {"ldQOut", offsetof(wg_epilogue, ld_q_out)},
+  };
+  for (size_t k = 0; k < sizeof ints / sizeof ints[0]; k++)
+    if (!prop_i32(env, o, ints[k].key, (int32_t *)((char *)e + ints[k].at))) return 0;
+  if (!prop_f32(env, o, "eps", &e->eps) || !prop_f32(env, o, "normMult", &e->norm_mult) ||
+      !prop_f32(env, o, "normMultOut", &e->norm_mult_out))
+    return 0;
+  const int64_t hd = e->head_dim;
+  const uint64_t out16_width = e->mode == WG_EPI_SWIGLU ? (uint64_t)N / 2 : (uint64_t)N;
+  const uint64_t cache = (uint64_t)(e->ctx > 0 ? e->ctx : 0) * (uint64_t)(e->kv_heads > 0 ? e->kv_heads : 0) *
+                         (uint64_t)(hd > 0 ? hd : 0) * 2;
+  const struct {
+    const char *key;
+    void **at;
+    uint64_t need;
+  } ptrs[] = {
+      {"normParts", (void **)&e->norm_parts, span(M, e->ld_parts_in, e->n_parts) * 4},
+      {"rowScale", (void **)&e->row_scale, (uint64_t)M * 4},
+      {"residual", (void **)&e->residual, span(M, e->ld_residual, N) * 4},
+      {"out16", (void **)&e->out16, span(M, e->ld_out16, (int64_t)out16_width) * 2},
+      {"out16W", (void **)&e->out16_w, (uint64_t)N * 4},
+      {"partsOut", (void **)&e->parts_out, span(M, e->ld_parts_out, N / 4) * 4},
+      {"rope", (void **)&e->rope, (uint64_t)(e->rope_rows > 0 ? e->rope_rows : 0) * (uint64_t)(hd > 0 ? hd : 0) * 4},
+      {"pos0", (void **)&e->pos0, 4},
+      {"qOut", (void **)&e->q_out, span(M, e->ld_q_out, (int64_t)e->heads * hd) * 4},
+      {"kCache", (void **)&e->k_cache, cache},
+      {"vCache", (void **)&e->v_cache, cache},
+  };
+  for (size_t k = 0; k < sizeof ptrs / sizeof ptrs[0]; k++)
+    if (!prop_operand(env, o, ptrs[k].key, ptrs[k].need, 1, ptrs[k].at)) return 0;
+  return 1;
+}
+
+static void *ctx_stream(wg_ctx *c) { return wg_ctx_stream(c); }
+
+#define DONE(rc) return (rc) ? throw_wg(env, (rc)) : NULL
+
 /* repack(ctx, kind, matrix, row0, rows, src, srcRows?): the loaders'
- * packers on the GPU (packQ4_0, packQ4_K, repack.ts:60-168); kind
- * "q4_0" | "q4_k" | "q4_k_native" | "q8_0" | "q6_k". */
+ * packers on the GPU (packQ4_0, packQ4_K, repack.ts:60-168); kind "q4_0" |
+ * "q4_k" | "q4_k_native" | "q8_0" | "q6_k"; src holds `rows` rows of the
+ * file's blocks, srcRows (or null) the logical row of each stored row. */
 static napi_value js_repack(napi_env env, napi_callback_info info) {
   ARGS(7);
   HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
@@ -462,56 +726,391 @@ static napi_value js_repack(napi_env env, napi_callback_info info) {
   size_t n = 0;
   if (napi_get_value_string_utf8(env, argv[1], kind, sizeof kind, &n) != napi_ok)
     return type_error(env, "kind must be a string");
-  wg_q4_matrix m;
-  if (!read_matrix(env, argv[2], &m)) return NULL;
+  MATRIX_ARG(2, m);
   INT32_ARG(3, row0);
   INT32_ARG(4, rows);
-  int ok;
-  const void *src = buf_ptr_arg(env, argv[5], 0, &ok);
-  if (!ok) return NULL;
-  const int32_t *src_rows = (const int32_t *)buf_ptr_arg(env, argv[6], 1, &ok);
-  if (!ok) return NULL;
-  void *s = wg_ctx_stream(c);
+  if (row0 < 0 || rows < 1 || row0 > m.N - rows)
+    return throw_limits(env, "repack: rows [%d, %d) of a %d-row matrix", row0, row0 + rows, m.N);
+  uint64_t per_row = 0; /* a row's bytes in the file */
+  if (!strcmp(kind, "q4_0")) per_row = (uint64_t)(m.K / 32) * 18;
+  else if (!strcmp(kind, "q4_k") || !strcmp(kind, "q4_k_native")) per_row = (uint64_t)(m.K / 256) * 144;
+  else if (!strcmp(kind, "q8_0")) per_row = (uint64_t)(m.K / 32) * 34;
+  else if (!strcmp(kind, "q6_k")) per_row = (uint64_t)(m.K / 256) * 210;
+  else return type_error(env, "kind must be q4_0, q4_k, q4_k_native, q8_0 or q6_k");
+  /* srcRows: host int32 of `rows` source rows, each checked against the
+   * rows src holds, then copied to the device for the launch */
+  wg_buf *rows_buf = NULL;
+  const int32_t *src_rows = NULL;
+  void *src_v;
+  if (is_nullish(env, argv[6])) {
+    if (!operand(env, argv[5], per_row * (uint64_t)rows, 0, "src", &src_v)) return NULL;
+  } else {
+    napi_typedarray_type type;
+    size_t n_rows = 0, off = 0;
+    void *data = NULL;
+    napi_value ab;
+    bool is = false;
+    if (napi_is_typedarray(env, argv[6], &is) != napi_ok || !is ||
+        napi_get_typedarray_info(env, argv[6], &type, &n_rows, &data, &ab, &off) != napi_ok ||
+        type != napi_int32_array)
+      return type_error(env, "srcRows must be an Int32Array");
+    if (n_rows != (size_t)rows) return throw_limits(env, "repack: %zu srcRows for %d rows", n_rows, rows);
+    if (!operand(env, argv[5], per_row, 0, "src", &src_v)) return NULL;
+    /* the rows src holds from its offset on */
+    napi_value h = argv[5];
+    int64_t src_off = 0;
+    bool arr = false;
+    if (napi_is_array(env, h, &arr) == napi_ok && arr) {
+      napi_value o;
+      napi_get_element(env, argv[5], 1, &o);
+      get_i64(env, o, &src_off);
+      napi_get_element(env, argv[5], 0, &h);
+    }
+    const uint64_t have = (wg_buf_size((wg_buf *)unwrap(env, h, H_BUF, "buffer")) - (uint64_t)src_off) / per_row;
+    const int32_t *r = (const int32_t *)data;
+    for (int32_t i = 0; i < rows; i++)
+      if (r[i] < 0 || (uint64_t)r[i] >= have)
+        return throw_limits(env, "repack: srcRows[%d] = %d; src holds %llu rows", i, r[i],
+                            (unsigned long long)have);
+    int rc = wg_buf_create(c, (size_t)rows * 4, data, &rows_buf);
+    if (rc) return throw_wg(env, rc);
+    src_rows = (const int32_t *)wg_buf_ptr(rows_buf);
+  }
+  const void *src = src_v;
+  void *s = ctx_stream(c);
   int rc;
   if (!strcmp(kind, "q4_0")) rc = wg_repack_q4_0(&m, row0, rows, src, src_rows, s);
   else if (!strcmp(kind, "q4_k")) rc = wg_repack_q4_k(&m, row0, rows, src, src_rows, s);
   else if (!strcmp(kind, "q4_k_native")) rc = wg_repack_q4_k_native(&m, row0, rows, src, src_rows, s);
   else if (!strcmp(kind, "q8_0")) rc = wg_repack_q8_0(&m, row0, rows, src, src_rows, s);
-  else if (!strcmp(kind, "q6_k")) rc = wg_repack_q6_k(&m, row0, rows, src, src_rows, s);
-  else return type_error(env, "kind must be q4_0, q4_k, q4_k_native, q8_0 or q6_k");
-  return rc ? throw_wg(env, rc) : NULL;
+  else rc = wg_repack_q6_k(&m, row0, rows, src, src_rows, s);
+  if (rows_buf) (void)wg_buf_delete(c, rows_buf); /* freed once the launch is done */
+  DONE(rc);
 }
 
-/* dequant(ctx, matrix, row0, rows, out): matrixRow (repack.ts:865-891). */
+/* dequant(ctx, matrix, row0, rows, out): matrixRow (repack.ts:865-891),
+ * rows x K floats. */
 static napi_value js_dequant(napi_env env, napi_callback_info info) {
   ARGS(5);
   HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
-  wg_q4_matrix m;
-  if (!read_matrix(env, argv[1], &m)) return NULL;
+  MATRIX_ARG(1, m);
   INT32_ARG(2, row0);
   INT32_ARG(3, rows);
-  int ok;
-  float *out = (float *)buf_ptr_arg(env, argv[4], 0, &ok);
-  if (!ok) return NULL;
-  int rc = wg_q4_dequant(&m, row0, rows, out, wg_ctx_stream(c));
-  return rc ? throw_wg(env, rc) : NULL;
+  if (rows < 1) return throw_limits(env, "dequant: %d rows", rows);
+  OPERAND(4, float, out, (uint64_t)rows * (uint64_t)m.K * 4, 0, "out");
+  DONE(wg_q4_dequant(&m, row0, rows, out, ctx_stream(c)));
 }
 
-/* gemv(ctx, matrix, x, M, y): splitPartials + pf (engine.ts:5241-5377;
- * kernels.ts:744-895, :69-79): y [M][N] f32 = x [M][K] halves times W^T. */
+/* gemv(ctx, matrix, x, M, y, epilogue?, ldx?, ldy?): splitPartials + pf and
+ * the passes folded into it (engine.ts:5241-5377; kernels.ts:744-895,
+ * :1169-1361): y [M][ldy] f32 = x [M][ldx] halves times W^T, with the
+ * epilogue's norm, residual, SwiGLU or RoPE + KV write. */
 static napi_value js_gemv(napi_env env, napi_callback_info info) {
-  ARGS(5);
+  ARGS(8);
   HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
-  wg_q4_matrix m;
-  if (!read_matrix(env, argv[1], &m)) return NULL;
-  int ok;
-  const uint16_t *x = (const uint16_t *)buf_ptr_arg(env, argv[2], 0, &ok);
-  if (!ok) return NULL;
+  MATRIX_ARG(1, m);
   INT32_ARG(3, M);
-  float *y = (float *)buf_ptr_arg(env, argv[4], 0, &ok);
-  if (!ok) return NULL;
-  int rc = wg_q4_gemv(&m, x, M, m.K, y, m.N, NULL, wg_ctx_stream(c));
-  return rc ? throw_wg(env, rc) : NULL;
+  int32_t ldx = m.K, ldy = m.N;
+  if (!is_nullish(env, argv[6]) && !get_i32(env, argv[6], &ldx)) return type_error(env, "ldx must be an integer");
+  if (!is_nullish(env, argv[7]) && !get_i32(env, argv[7], &ldy)) return type_error(env, "ldy must be an integer");
+  if (M < 1 || M > 8) return throw_limits(env, "gemv: %d rows (1 to 8)", M);
+  OPERAND(2, const uint16_t, x, span(M, ldx, m.K) * 2, 0, "x");
+  wg_epilogue ep;
+  const int has_ep = !is_nullish(env, argv[5]);
+  if (has_ep && !read_epilogue(env, argv[5], M, m.N, &ep)) return NULL;
+  const int needs_y = !has_ep || ep.mode == WG_EPI_STORE;
+  OPERAND(4, float, y, needs_y ? span(M, ldy, m.N) * 4 : 0, !needs_y, "y");
+  DONE(wg_q4_gemv(&m, x, M, ldx, y, ldy, has_ep ? &ep : NULL, ctx_stream(c)));
+}
+
+/* gemm(ctx, matrix, A, M, C, {lda?, ldc?, residual?, ldr?, rowScale?,
+ * colOf?}): Engine.matmul for a prompt batch (engine.ts:4969-5234) on
+ * MFMA: C [M][ldc] f32 = (residual) + row_scale * A [M][lda] halves W^T. */
+static napi_value js_gemm(napi_env env, napi_callback_info info) {
+  ARGS(6);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  MATRIX_ARG(1, m);
+  INT32_ARG(3, M);
+  if (M < 1) return throw_limits(env, "gemm: %d rows", M);
+  int32_t lda = m.K, ldc = m.N, ldr = m.N;
+  void *residual = NULL, *row_scale = NULL, *col_of = NULL;
+  if (!is_nullish(env, argv[5])) {
+    napi_value o = argv[5];
+    int32_t v;
+    if (!prop_i32(env, o, "lda", &v)) return NULL;
+    if (v) lda = v;
+    if (!prop_i32(env, o, "ldc", &v)) return NULL;
+    if (v) ldc = v;
+    if (!prop_i32(env, o, "ldr", &v)) return NULL;
+    if (v) ldr = v;
+    if (!prop_operand(env, o, "residual", span(M, ldr, m.N) * 4, 1, &residual) ||
+        !prop_operand(env, o, "rowScale", (uint64_t)M * 4, 1, &row_scale) ||
+        !prop_operand(env, o, "colOf", (uint64_t)m.N * 4, 1, &col_of))
+      return NULL;
+  }
+  OPERAND(2, const uint16_t, A, span(M, lda, m.K) * 2, 0, "A");
+  OPERAND(4, float, C, span(M, ldc, m.N) * 4, 0, "C");
+  DONE(wg_q4_gemm(&m, A, M, lda, C, ldc, (const float *)residual, ldr, (const float *)row_scale,
+                  (const int32_t *)col_of, ctx_stream(c)));
+}
+
+/* gemmSwiglu(ctx, matrix, A, M, out16, rowScale?, lda?, ldo?): the gate|up
+ * GEMM with SwiGLU folded in (src/gpu/native.ts:33; kernels.ts:1066-1077):
+ * out16 [M][ldo] halves, N / 2 columns. */
+static napi_value js_gemm_swiglu(napi_env env, napi_callback_info info) {
+  ARGS(8);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  MATRIX_ARG(1, m);
+  INT32_ARG(3, M);
+  if (M < 1) return throw_limits(env, "gemmSwiglu: %d rows", M);
+  int32_t lda = m.K, ldo = m.N / 2;
+  if (!is_nullish(env, argv[6]) && !get_i32(env, argv[6], &lda)) return type_error(env, "lda must be an integer");
+  if (!is_nullish(env, argv[7]) && !get_i32(env, argv[7], &ldo)) return type_error(env, "ldo must be an integer");
+  OPERAND(2, const uint16_t, A, span(M, lda, m.K) * 2, 0, "A");
+  OPERAND(4, uint16_t, out16, span(M, ldo, m.N / 2) * 2, 0, "out16");
+  OPERAND(5, const float, row_scale, (uint64_t)M * 4, 1, "rowScale");
+  DONE(wg_q4_gemm_swiglu(&m, A, M, lda, out16, ldo, row_scale, ctx_stream(c)));
+}
+
+/* embed(ctx, matrix, ids, M, h, epilogue?, ldh?): embed / embedFold
+ * (kernels.ts:1092-1149, :985-1041): h [M][ldh] = the ids' dequantized
+ * rows, with the epilogue's prescaled half input and sums of squares. */
+static napi_value js_embed(napi_env env, napi_callback_info info) {
+  ARGS(7);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  MATRIX_ARG(1, m);
+  INT32_ARG(3, M);
+  if (M < 1) return throw_limits(env, "embed: %d rows", M);
+  int32_t ldh = m.K;
+  if (!is_nullish(env, argv[6]) && !get_i32(env, argv[6], &ldh)) return type_error(env, "ldh must be an integer");
+  OPERAND(2, const int32_t, ids, (uint64_t)M * 4, 0, "ids");
+  OPERAND(4, float, h, span(M, ldh, m.K) * 4, 0, "h");
+  wg_epilogue ep;
+  const int has_ep = !is_nullish(env, argv[5]);
+  if (has_ep && !read_epilogue(env, argv[5], M, m.K, &ep)) return NULL;
+  DONE(wg_embed(&m, ids, M, h, ldh, has_ep ? &ep : NULL, ctx_stream(c)));
+}
+
+/* normToH2(ctx, x, M, D, w, eps, out, rowScale, ldx?, ldo?): NORM_TO_H2
+ * with PRESCALE 32 (kernels.ts:89, :1195-1242). */
+static napi_value js_norm_to_h2(napi_env env, napi_callback_info info) {
+  ARGS(10);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, M);
+  INT32_ARG(3, D);
+  FLOAT_ARG(5, eps);
+  if (M < 1 || D < 1) return throw_limits(env, "normToH2: %d rows of %d", M, D);
+  int32_t ldx = D, ldo = D;
+  if (!is_nullish(env, argv[8]) && !get_i32(env, argv[8], &ldx)) return type_error(env, "ldx must be an integer");
+  if (!is_nullish(env, argv[9]) && !get_i32(env, argv[9], &ldo)) return type_error(env, "ldo must be an integer");
+  OPERAND(1, const float, x, span(M, ldx, D) * 4, 0, "x");
+  OPERAND(4, const float, w, (uint64_t)D * 4, 0, "w");
+  OPERAND(6, uint16_t, out, span(M, ldo, D) * 2, 0, "out");
+  OPERAND(7, float, row_scale, (uint64_t)M * 4, 0, "rowScale");
+  DONE(wg_norm_to_h2(x, M, D, ldx, w, eps, out, ldo, row_scale, ctx_stream(c)));
+}
+
+/* headPrep(ctx, qkv, M, shape, qNorm?, kNorm?, rope, ropeRows, pos0, qOut,
+ * kCache, vCache, ctxRows, ldq?, ldqo?): headPrep + values
+ * (kernels.ts:2196-2322, :3030-3045). */
+static napi_value js_head_prep(napi_env env, napi_callback_info info) {
+  ARGS(15);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, M);
+  SHAPE_ARG(3, sh);
+  INT32_ARG(7, rope_rows);
+  INT32_ARG(12, ctx_rows);
+  const int64_t hd = sh.head_dim, qd = (int64_t)sh.heads * hd, kvd = (int64_t)sh.kv_heads * hd;
+  int32_t ldq = (int32_t)(qd + 2 * kvd), ldqo = (int32_t)qd;
+  if (!is_nullish(env, argv[13]) && !get_i32(env, argv[13], &ldq)) return type_error(env, "ldq must be an integer");
+  if (!is_nullish(env, argv[14]) && !get_i32(env, argv[14], &ldqo)) return type_error(env, "ldqo must be an integer");
+  if (M < 1 || rope_rows < 1 || ctx_rows < 1)
+    return throw_limits(env, "headPrep: %d rows, %d rope rows, %d cache rows", M, rope_rows, ctx_rows);
+  OPERAND(1, const float, qkv, span(M, ldq, qd + 2 * kvd) * 4, 0, "qkv");
+  OPERAND(4, const float, q_norm, (uint64_t)hd * 4, 1, "qNorm");
+  OPERAND(5, const float, k_norm, (uint64_t)hd * 4, 1, "kNorm");
+  OPERAND(6, const float, rope, (uint64_t)rope_rows * (uint64_t)hd * 4, 0, "rope");
+  OPERAND(8, const int32_t, pos0, 4, 0, "pos0");
+  OPERAND(9, float, q_out, span(M, ldqo, qd) * 4, 0, "qOut");
+  OPERAND(10, uint16_t, k_cache, (uint64_t)ctx_rows * (uint64_t)kvd * 2, 0, "kCache");
+  OPERAND(11, uint16_t, v_cache, (uint64_t)ctx_rows * (uint64_t)kvd * 2, 0, "vCache");
+  DONE(wg_head_prep(qkv, M, ldq, &sh, q_norm, k_norm, rope, rope_rows, pos0, q_out, ldqo, k_cache,
+                    v_cache, ctx_rows, ctx_stream(c)));
+}
+
+static napi_value js_attn_scratch_bytes(napi_env env, napi_callback_info info) {
+  ARGS(4);
+  INT32_ARG(0, M);
+  INT32_ARG(1, heads);
+  INT32_ARG(2, head_dim);
+  INT32_ARG(3, max_keys);
+  return num(env, (double)wg_attn_scratch_bytes(M, heads, head_dim, max_keys));
+}
+
+/* attnDecode(ctx, q, M, shape, kCache, vCache, pos0, maxKeys, out, scratch,
+ * ldq?, ldo?): scores, attend, attendPanel + attendPanelCombine
+ * (kernels.ts:2386-2579, :2803-3027) for up to a few query rows.
+ * attnPrefill(ctx, q, M, shape, kCache, vCache, pos0, maxKeys, out, ldq?,
+ * ldo?): the prompt plan (engine.ts:6359-6630). */
+static napi_value attn_common(napi_env env, napi_callback_info info, int prefill) {
+  ARGS(12);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, M);
+  SHAPE_ARG(3, sh);
+  INT32_ARG(7, max_keys);
+  const int extra = prefill ? 9 : 10;
+  const int64_t qd = (int64_t)sh.heads * sh.head_dim, kvd = (int64_t)sh.kv_heads * sh.head_dim;
+  int32_t ldq = (int32_t)qd, ldo = (int32_t)qd;
+  if (!is_nullish(env, argv[extra]) && !get_i32(env, argv[extra], &ldq)) return type_error(env, "ldq must be an integer");
+  if (!is_nullish(env, argv[extra + 1]) && !get_i32(env, argv[extra + 1], &ldo)) return type_error(env, "ldo must be an integer");
+  if (M < 1 || max_keys < 1) return throw_limits(env, "attention: %d rows over %d keys", M, max_keys);
+  OPERAND(1, const float, q, span(M, ldq, qd) * 4, 0, "q");
+  OPERAND(4, const uint16_t, k_cache, (uint64_t)max_keys * (uint64_t)kvd * 2, 0, "kCache");
+  OPERAND(5, const uint16_t, v_cache, (uint64_t)max_keys * (uint64_t)kvd * 2, 0, "vCache");
+  OPERAND(6, const int32_t, pos0, 4, 0, "pos0");
+  OPERAND(8, uint16_t, out, span(M, ldo, qd) * 2, 0, "out");
+  if (prefill)
+    DONE(wg_attn_prefill(q, M, ldq, &sh, k_cache, v_cache, pos0, max_keys, out, ldo, ctx_stream(c)));
+  const size_t need = wg_attn_scratch_bytes(M, sh.heads, sh.head_dim, max_keys);
+  OPERAND(9, void, scratch, need, 0, "scratch");
+  DONE(wg_attn_decode(q, M, ldq, &sh, k_cache, v_cache, pos0, max_keys, out, ldo, scratch, need,
+                      ctx_stream(c)));
+}
+
+static napi_value js_attn_decode(napi_env env, napi_callback_info info) {
+  return attn_common(env, info, 0);
+}
+
+static napi_value js_attn_prefill(napi_env env, napi_callback_info info) {
+  return attn_common(env, info, 1);
+}
+
+/* shortConv(ctx, bcx, M, D, W, taps, state, stateOut, prefixes?, out, ldb?,
+ * ldo?): convFused + convPrefixes (kernels.ts:1447-1523; Engine.convolve,
+ * engine.ts:5806-5899). */
+static napi_value js_short_conv(napi_env env, napi_callback_info info) {
+  ARGS(12);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, M);
+  INT32_ARG(3, D);
+  INT32_ARG(4, W);
+  if (M < 1 || D < 1 || W < 2) return throw_limits(env, "shortConv: %d rows of %d, width %d", M, D, W);
+  int32_t ldb = 3 * D, ldo = D;
+  if (!is_nullish(env, argv[10]) && !get_i32(env, argv[10], &ldb)) return type_error(env, "ldb must be an integer");
+  if (!is_nullish(env, argv[11]) && !get_i32(env, argv[11], &ldo)) return type_error(env, "ldo must be an integer");
+  const uint64_t st = (uint64_t)(W - 1) * (uint64_t)D * 4;
+  OPERAND(1, const float, bcx, span(M, ldb, 3 * (int64_t)D) * 4, 0, "bcx");
+  OPERAND(5, const float, taps, (uint64_t)D * (uint64_t)W * 4, 0, "taps");
+  OPERAND(6, const float, state, st, 0, "state");
+  OPERAND(7, float, state_out, st, 0, "stateOut");
+  OPERAND(8, float, prefixes, (uint64_t)M * st, 1, "prefixes");
+  OPERAND(9, uint16_t, out, span(M, ldo, D) * 2, 0, "out");
+  DONE(wg_short_conv(bcx, M, D, ldb, W, taps, state, state_out, prefixes, out, ldo, ctx_stream(c)));
+}
+
+/* convAccept(ctx, prefixes, kept, rows, D, W, state): Engine.accept's
+ * rollback (engine.ts:8063-8086, COPY_ROWS kernels.ts:2177-2183). */
+static napi_value js_conv_accept(napi_env env, napi_callback_info info) {
+  ARGS(7);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, kept);
+  INT32_ARG(3, rows);
+  INT32_ARG(4, D);
+  INT32_ARG(5, W);
+  if (rows < 1 || D < 1 || W < 2) return throw_limits(env, "convAccept: %d rows of %d, width %d", rows, D, W);
+  const uint64_t st = (uint64_t)(W - 1) * (uint64_t)D * 4;
+  OPERAND(1, const float, prefixes, (uint64_t)rows * st, 0, "prefixes");
+  OPERAND(6, float, state, st, 0, "state");
+  DONE(wg_conv_accept(prefixes, kept, rows, D, W, state, ctx_stream(c)));
+}
+
+/* convStates(ctx, [{prefixes, state, dim, width}]): a device array of
+ * wg_conv_state for verifyAccept, in a new buffer (its size checked
+ * against each layer's, `rows` prefixes each). */
+static napi_value js_conv_states(napi_env env, napi_callback_info info) {
+  ARGS(3);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, rows);
+  bool is = false;
+  uint32_t n = 0;
+  if (napi_is_array(env, argv[1], &is) != napi_ok || !is ||
+      napi_get_array_length(env, argv[1], &n) != napi_ok || n == 0 || n > 4096)
+    return type_error(env, "convStates takes a non-empty array of layers");
+  if (rows < 1 || rows > 64) return throw_limits(env, "convStates: %d rows", rows);
+  wg_conv_state *arr = (wg_conv_state *)calloc(n, sizeof *arr);
+  if (!arr) {
+    napi_throw_error(env, "EADDON", "out of host memory");
+    return NULL;
+  }
+  for (uint32_t i = 0; i < n; i++) {
+    napi_value o;
+    void *p;
+    if (napi_get_element(env, argv[1], i, &o) != napi_ok || !prop_i32(env, o, "dim", &arr[i].dim) ||
+        !prop_i32(env, o, "width", &arr[i].width)) {
+      free(arr);
+      return NULL;
+    }
+    if (arr[i].dim < 1 || arr[i].width < 2) {
+      free(arr);
+      return throw_limits(env, "convStates: layer %u is %d wide with %d taps", i, arr[i].dim, arr[i].width);
+    }
+    const uint64_t st = (uint64_t)(arr[i].width - 1) * (uint64_t)arr[i].dim * 4;
+    if (!prop_operand(env, o, "prefixes", (uint64_t)rows * st, 0, &p)) {
+      free(arr);
+      return NULL;
+    }
+    arr[i].prefixes = (float *)p;
+    if (!prop_operand(env, o, "state", st, 0, &p)) {
+      free(arr);
+      return NULL;
+    }
+    arr[i].state = (float *)p;
+  }
+  wg_buf *b = NULL;
+  int rc = wg_buf_create(c, (size_t)n * sizeof *arr, arr, &b);
+  free(arr);
+  if (rc) return throw_wg(env, rc);
+  return wrap(env, H_BUF, b);
+}
+
+/* verifyAccept(ctx, picks, rows, convs, nConv, maxState, pos, ids, hist,
+ * histLen, keptLog, logLen, cursor): Engine.accept after a verify batch with
+ * the handler's keep rule (engine.ts:8063-8086, handler.ts:1811-1887), on
+ * the device. */
+static napi_value js_verify_accept(napi_env env, napi_callback_info info) {
+  ARGS(13);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, rows);
+  INT32_ARG(4, n_conv);
+  INT32_ARG(5, max_state);
+  INT32_ARG(9, hist_len);
+  INT32_ARG(11, log_len);
+  if (rows < 1 || n_conv < 0 || hist_len < 0 || log_len < 0)
+    return throw_limits(env, "verifyAccept: %d rows, %d conv layers", rows, n_conv);
+  OPERAND(1, const int32_t, picks, (uint64_t)rows * 4, 0, "picks");
+  OPERAND(3, const wg_conv_state, convs, (uint64_t)n_conv * sizeof(wg_conv_state), n_conv == 0, "convs");
+  OPERAND(6, int32_t, pos, 4, 0, "pos");
+  OPERAND(7, int32_t, ids, (uint64_t)rows * 4, 0, "ids");
+  OPERAND(8, int32_t, hist, (uint64_t)hist_len * 4, hist_len == 0, "hist");
+  OPERAND(10, int32_t, kept_log, (uint64_t)log_len * 4, log_len == 0, "keptLog");
+  OPERAND(12, int32_t, cursor, 4, 0, "cursor");
+  DONE(wg_verify_accept(picks, rows, convs, n_conv, max_state, pos, ids, hist, hist_len, kept_log,
+                        log_len, cursor, ctx_stream(c)));
+}
+
+/* verifyDrafts(ctx, ids, rows, table, nSteps, cursor): a verify step's
+ * drafts from a device table (the reference's lookupDraft runs on the
+ * host, src/draft.ts:15-45). */
+static napi_value js_verify_drafts(napi_env env, napi_callback_info info) {
+  ARGS(6);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, rows);
+  INT32_ARG(4, n_steps);
+  if (rows < 2 || n_steps < 1) return throw_limits(env, "verifyDrafts: %d rows, %d steps", rows, n_steps);
+  OPERAND(1, int32_t, ids, (uint64_t)rows * 4, 0, "ids");
+  OPERAND(3, const int32_t, table, (uint64_t)n_steps * (uint64_t)(rows - 1) * 4, 0, "table");
+  OPERAND(5, const int32_t, cursor, 4, 0, "cursor");
+  DONE(wg_verify_drafts(ids, rows, table, n_steps, cursor, ctx_stream(c)));
 }
 
 static napi_value js_argmax_scratch_bytes(napi_env env, napi_callback_info info) {
@@ -521,21 +1120,93 @@ static napi_value js_argmax_scratch_bytes(napi_env env, napi_callback_info info)
   return num(env, (double)wg_argmax_scratch_bytes(M, V));
 }
 
-/* argmax(ctx, logits, M, V, ids, scratch): Engine.argmax (engine.ts:8271-8336). */
+/* argmax(ctx, logits, M, V, ids, scratch, tops?, ld?): Engine.argmax
+ * (engine.ts:8271-8336; CHUNK_MAX_AT + CHUNK_ARGMAX_ROWS,
+ * kernels.ts:3169-3246). */
 static napi_value js_argmax(napi_env env, napi_callback_info info) {
-  ARGS(6);
+  ARGS(8);
   HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
-  int ok;
-  const float *logits = (const float *)buf_ptr_arg(env, argv[1], 0, &ok);
-  if (!ok) return NULL;
   INT32_ARG(2, M);
   INT32_ARG(3, V);
-  int32_t *ids = (int32_t *)buf_ptr_arg(env, argv[4], 0, &ok);
-  if (!ok) return NULL;
-  HANDLE_ARG(5, wg_buf, scratch, H_BUF, "buffer");
-  void *sp = wg_buf_ptr(scratch);
-  int rc = wg_argmax_rows(logits, M, V, V, ids, NULL, sp, wg_buf_size(scratch), wg_ctx_stream(c));
-  return rc ? throw_wg(env, rc) : NULL;
+  int32_t ld = V;
+  if (!is_nullish(env, argv[7]) && !get_i32(env, argv[7], &ld)) return type_error(env, "ld must be an integer");
+  if (M < 1 || V < 1) return throw_limits(env, "argmax: %d rows of %d", M, V);
+  const size_t need = wg_argmax_scratch_bytes(M, V);
+  OPERAND(1, const float, logits, span(M, ld, V) * 4, 0, "logits");
+  OPERAND(4, int32_t, ids, (uint64_t)M * 4, 0, "ids");
+  OPERAND(5, void, scratch, need, 0, "scratch");
+  OPERAND(6, float, tops, (uint64_t)M * 4, 1, "tops");
+  DONE(wg_argmax_rows(logits, M, V, ld, ids, tops, scratch, need, ctx_stream(c)));
+}
+
+/* argmaxAdvance(ctx, logits, V, ids, pos, hist?, histLen, scratch, tops?):
+ * one greedy decode step's pick and advance on the device (the guessed
+ * forward's pick, engine.ts:8095-8110, :8318-8336). */
+static napi_value js_argmax_advance(napi_env env, napi_callback_info info) {
+  ARGS(9);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, V);
+  INT32_ARG(6, hist_len);
+  if (V < 1 || hist_len < 0) return throw_limits(env, "argmaxAdvance: %d logits", V);
+  const size_t need = wg_argmax_scratch_bytes(1, V);
+  OPERAND(1, const float, logits, (uint64_t)V * 4, 0, "logits");
+  OPERAND(3, int32_t, ids, 4, 0, "ids");
+  OPERAND(4, int32_t, pos, 4, 0, "pos");
+  OPERAND(5, int32_t, hist, (uint64_t)hist_len * 4, hist_len == 0, "hist");
+  OPERAND(7, void, scratch, need, 0, "scratch");
+  OPERAND(8, float, tops, 4, 1, "tops");
+  DONE(wg_argmax_advance(logits, V, ids, pos, hist, hist_len, tops, scratch, need, ctx_stream(c)));
+}
+
+static napi_value js_pick_scratch_bytes(napi_env env, napi_callback_info info) {
+  ARGS(2);
+  INT32_ARG(0, M);
+  INT32_ARG(1, V);
+  return num(env, (double)wg_pick_scratch_bytes(M, V));
+}
+
+/* pickCandidates(ctx, logits, M, V, count, chunksOut, candidates, scratch,
+ * {ld?, mask?, seenRows?, nSeen?, row0?, penalty?, presencePenalty?,
+ * allowed?, allowedRows?, ldAllowed?}): Engine.pick's penalized chunk
+ * candidates (engine.ts:8352-8473; kernels.ts:3085-3163, :3265-3323). */
+static napi_value js_pick_candidates(napi_env env, napi_callback_info info) {
+  ARGS(9);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, M);
+  INT32_ARG(3, V);
+  INT32_ARG(4, count);
+  if (M < 1 || V < 1 || count < 1 || count > 64)
+    return throw_limits(env, "pickCandidates: %d rows of %d, %d chunks", M, V, count);
+  int32_t ld = V, n_seen = 0, row0 = 0, allowed_rows = 0, ld_allowed = 0;
+  float penalty = 1.0f, presence = 0.0f;
+  void *mask = NULL, *seen = NULL, *allowed = NULL;
+  if (!is_nullish(env, argv[8])) {
+    napi_value o = argv[8];
+    int32_t v;
+    if (!prop_i32(env, o, "ld", &v)) return NULL;
+    if (v) ld = v;
+    if (!prop_i32(env, o, "nSeen", &n_seen) || !prop_i32(env, o, "row0", &row0) ||
+        !prop_i32(env, o, "allowedRows", &allowed_rows) || !prop_i32(env, o, "ldAllowed", &ld_allowed))
+      return NULL;
+    napi_value pv;
+    if (!prop(env, o, "penalty", &pv)) return NULL;
+    if (!is_nullish(env, pv) && !prop_f32(env, o, "penalty", &penalty)) return NULL;
+    if (!prop_f32(env, o, "presencePenalty", &presence)) return NULL;
+    if (n_seen < 0 || allowed_rows < 0 || ld_allowed < 0)
+      return throw_limits(env, "pickCandidates: negative counts");
+    if (!prop_operand(env, o, "mask", (uint64_t)V, 1, &mask) ||
+        !prop_operand(env, o, "seenRows", (uint64_t)n_seen * 16, n_seen == 0, &seen) ||
+        !prop_operand(env, o, "allowed", span(allowed_rows, ld_allowed, ld_allowed) * 4, 1, &allowed))
+      return NULL;
+  }
+  const size_t need = wg_pick_scratch_bytes(M, V);
+  OPERAND(1, const float, logits, span(M, ld, V) * 4, 0, "logits");
+  OPERAND(5, int32_t, chunks_out, (uint64_t)M * (uint64_t)count * 4, 0, "chunksOut");
+  OPERAND(6, float, candidates, (uint64_t)M * (uint64_t)count * 256 * 4, 0, "candidates");
+  OPERAND(7, void, scratch, need, 0, "scratch");
+  DONE(wg_pick_candidates(logits, M, V, ld, (const uint8_t *)mask, (const int32_t *)seen, n_seen,
+                          row0, penalty, presence, (const uint32_t *)allowed, allowed_rows,
+                          ld_allowed, count, chunks_out, candidates, scratch, need, ctx_stream(c)));
 }
 
 /* ---------------------------------------------------------- file readers */
@@ -715,11 +1386,28 @@ static napi_value init(napi_env env, napi_value exports) {
       {"readNow", js_read_now},
       {"flush", js_flush},
       {"finish", js_finish},
+      {"fence", js_fence_record},
       {"repack", js_repack},
       {"dequant", js_dequant},
       {"gemv", js_gemv},
+      {"gemm", js_gemm},
+      {"gemmSwiglu", js_gemm_swiglu},
+      {"embed", js_embed},
+      {"normToH2", js_norm_to_h2},
+      {"headPrep", js_head_prep},
+      {"attnScratchBytes", js_attn_scratch_bytes},
+      {"attnDecode", js_attn_decode},
+      {"attnPrefill", js_attn_prefill},
+      {"shortConv", js_short_conv},
+      {"convAccept", js_conv_accept},
+      {"convStates", js_conv_states},
+      {"verifyAccept", js_verify_accept},
+      {"verifyDrafts", js_verify_drafts},
       {"argmaxScratchBytes", js_argmax_scratch_bytes},
       {"argmax", js_argmax},
+      {"argmaxAdvance", js_argmax_advance},
+      {"pickScratchBytes", js_pick_scratch_bytes},
+      {"pickCandidates", js_pick_candidates},
       {"ggufHeader", js_gguf_header},
       {"onnxGraph", js_onnx_graph},
   };
@@ -740,6 +1428,10 @@ static napi_value init(napi_env env, napi_value exports) {
   set(env, consts, "ZERO_8", num(env, WG_ZERO_8));
   set(env, consts, "ZERO_U8", num(env, WG_ZERO_U8));
   set(env, consts, "ZERO_F16", num(env, WG_ZERO_F16));
+  set(env, consts, "EPI_STORE", num(env, WG_EPI_STORE));
+  set(env, consts, "EPI_SWIGLU", num(env, WG_EPI_SWIGLU));
+  set(env, consts, "EPI_ROPE_KV", num(env, WG_EPI_ROPE_KV));
+  set(env, consts, "CONV_STATE_BYTES", num(env, (double)sizeof(wg_conv_state)));
   set(env, exports, "constants", consts);
   return exports;
 }
