@@ -96,10 +96,11 @@ def test_lfm2_config_from_metadata(tmp_path):
     assert (s.hidden, s.heads, s.kv_heads, s.head_dim, s.intermediate, s.vocab) == \
         (256, 4, 2, 64, 512, 1024)
     assert s.eps == 1e-5 and s.rope_theta == 1e6 and s.conv_kernel == 3 and s.qk_norm
-    for kw, msg in ((dict(arch="lfm3"), "unsupported architecture lfm3"),
+    for kw, msg in ((dict(arch="lfm3"), "architecture lfm3 is not one this engine runs"),
                     (dict(sliding=4), "sliding-window"),
-                    (dict(output_head=True), "separate output head"),
-                    (dict(kv=[0, 2, 1]), "different KV head counts")):
+                    (dict(output_head=True), "its own output.weight"),
+                    (dict(kv=[0, 2, 1]), r"differ in KV heads \(\[1, 2\]\)"),
+                    (dict(kv=[0, 0, 0]), "no attention layer")):
         p = lfm2_file(tmp_path / "bad.gguf", layers=3, **{"kv": [0, 2, 0], **kw})
         with G.GgufFile(p) as f, pytest.raises(ValueError, match=msg):
             LG.gguf_shape(f)

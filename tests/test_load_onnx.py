@@ -171,12 +171,12 @@ def test_an_embedding_whose_rows_are_not_a_multiple_of_4_is_refused(graph):
                                      for t in c["layer_types"]]), "sliding_attention layers"),
     (lambda c: c.update(rope_parameters={"rope_theta": 1e6, "partial_rotary_factor": 0.5}),
      "partial RoPE"),
-    (lambda c: c.update(rope_parameters={"rope_type": "yarn", "rope_theta": 1e6}), "rope type"),
+    (lambda c: c.update(rope_parameters={"rope_type": "yarn", "rope_theta": 1e6}), "yarn RoPE"),
     (lambda c: c.update(intermediate_size=1000, block_auto_adjust_ff_dim=False),
      "intermediate_size 1000"),
     (lambda c: c.update(vocab_size=1000), "vocab_size 1000"),
-    (lambda c: c.pop("layer_types"), "no layer_types"),
-    (lambda c: c.update(num_hidden_layers=15), "doesn't match num_hidden_layers"),
+    (lambda c: c.pop("layer_types"), "neither layer_types"),
+    (lambda c: c.update(num_hidden_layers=15), "16 layer types for 15 layers"),
 ])
 def test_configs_off_the_engines_path_are_refused(graph, edit, match):
     g, cfg = graph("lfm2-350m")
@@ -196,7 +196,7 @@ def test_interleaved_or_partial_rotary_graphs_are_refused(graph):
     gqa.attributes["rotary_interleaved"] = a
     cos = g.initializers["cos_cache"]
     g.initializers["cos_cache"] = _with(cos, dims=(cos.dims[0], 16))
-    with pytest.raises(ValueError, match="rotates 32 dims per head, expected 64"):
+    with pytest.raises(ValueError, match="rotates 32 of each head's 64 dims"):
         _check(g, cfg)
 
 

@@ -37,77 +37,129 @@ _EIGHT_BIT = (G.F32, G.F16, G.Q8_0, G.Q4_1, G.Q4_K, G.Q5_K, G.Q6_K)
 
 
 def _f32_decimal(v: float) -> float:
-    """A float32 metadata value as the decimal it was written from
-    (f32Decimal, src/load-gguf.ts:594-597: 1e-5, not 9.9999997e-6)."""
+    """A float32 metadata value as the decimal it was written from (7
+    significant digits: 1e-5, not 9.9999997e-6), as the reference reads
+    them (src/load-gguf.ts:594-597)."""
     return float(f"{v:.7g}")
 
 
-def gguf_shape(f: G.GgufFile, name: str | None = None) -> E.ModelShape:
-    """ggufConfig (src/load-gguf.ts:600-752) for the architectures the
-    engine runs: LFM2 (short-conv and full-attention layers, q/k norms, a
-    tied output head)."""
+# The LFM2 metadata the engine's shape is made of: (field, key under the
+# architecture's prefix, how to read it, default). A key is looked up bare
+# first, then under "<arch>." (the format lets writers put either). A
+# default of _NEEDED makes the key required. Which keys exist is the
+# format (llama.cpp's GGUF writer for LFM2); the table is this loader's.
+_NEEDED = object()
+_SCHEMA = (
+    ("layers", "block_count", "int", _NEEDED),
+    ("hidden", "embedding_length", "int", _NEEDED),
+    ("heads", "attention.head_count", "int", _NEEDED),
+    ("kv", "attention.head_count_kv", "per-layer", None),
+    ("head_dim", "attention.key_length", "int", None),
+    ("rope_dims", "rope.dimension_count", "int", None),
+    ("theta", "rope.freq_base", "decimal", _NEEDED),
+    ("eps", "attention.layer_norm_rms_epsilon", "decimal", _NEEDED),
+    ("conv_kernel", "shortconv.l_cache", "int", _NEEDED),
+    ("context", "context_length", "int", 8192),
+    ("window", "attention.sliding_window", "int", 0),
+    ("window_pattern", "attention.sliding_window_pattern", "any", None),
+    ("ffn", "feed_forward_length", "int", None),
+)
+
+
+def _read_schema(meta: dict, arch: str) -> dict:
+    """The schema's fields from the metadata, each converted by its kind."""
+    out = {}
+    for field_, key, kind, default in _SCHEMA:
+        value = meta.get(key, meta.get(f"{arch}.{key}"))
+        if value is None:
+            if default is _NEEDED:
+                raise ValueError(f"GGUF metadata lacks {arch}.{key}, which the engine needs")
+            out[field_] = default
+            continue
+        if kind == "any":
+            out[field_] = value
+        elif kind == "per-layer":
+            out[field_] = [int(x) for x in value] if isinstance(value, list) else int(value)
+        elif isinstance(value, bool) or not isinstance(value, (int, float)):
+            raise ValueError(f"GGUF metadata {arch}.{key} holds {type(value).__name__} "
+                             f"{value!r} where a number belongs")
+        else:
+            out[field_] = _f32_decimal(value) if kind == "decimal" else int(value)
+    return out
+
+
+def _lfm2_fields(f: G.GgufFile) -> dict:
+    """The schema's fields of an LFM2 file, with the derived ones: kv per
+    layer, head_dim, intermediate (from the first gate matrix when the
+    metadata has no feed_forward_length) and vocab (the embedding's
+    rows)."""
     meta = f.metadata
     arch = meta.get("general.architecture")
     if not isinstance(arch, str):
-        raise ValueError("GGUF: no general.architecture")
+        raise ValueError("GGUF metadata names no general.architecture")
     if arch != "lfm2":
-        raise ValueError(f"GGUF: unsupported architecture {arch}"
-                         + (" (its attention gate, sandwich norms or Gated DeltaNet are not "
-                            "on this engine's path)" if arch in ("lfm3", "qwen35") else ""))
-    if "output.weight" in f.tensors:
-        raise ValueError("GGUF: LFM2 models with a separate output head are not supported.")
-
-    def num(key, fallback=None):
-        v = meta.get(key, meta.get(f"{arch}.{key}"))
-        if v is None:
-            if fallback is not None:
-                return fallback
-            raise ValueError(f"GGUF: missing metadata {arch}.{key}")
-        if isinstance(v, bool) or not isinstance(v, (int, float)):
-            raise ValueError(f"GGUF: {key} is not a number")
-        return v
-
-    layers = int(num("block_count"))
-    hidden = int(num("embedding_length"))
-    heads = int(num("attention.head_count"))
-    kv_value = meta.get(f"{arch}.attention.head_count_kv")
-    if isinstance(kv_value, list):
-        kv = [int(x) for x in kv_value]
-    else:
-        kv = [int(kv_value if kv_value is not None else heads)] * layers
-    if len(kv) != layers:
-        raise ValueError("GGUF: head_count_kv doesn't have one entry per layer")
-    if num("attention.sliding_window", 0) > 0 or \
-            isinstance(meta.get(f"{arch}.attention.sliding_window_pattern"), list):
-        raise ValueError("GGUF: sliding-window attention is not supported by this engine")
-    kv_heads = max(kv)
-    if any(k not in (0, kv_heads) for k in kv):
-        raise ValueError("GGUF: attention layers with different KV head counts are not "
-                         "supported")
-    if kv_heads == 0:
-        raise ValueError("GGUF: no attention layer")
-    head_dim = int(num("attention.key_length", hidden // heads))
-    if int(num("rope.dimension_count", head_dim)) != head_dim or "rope_freqs.weight" in f.tensors:
-        raise ValueError("GGUF: partial RoPE is not supported by this engine")
+        why = {"lfm3": "gated attention and sandwich norms",
+               "qwen35": "Gated DeltaNet layers"}.get(arch)
+        raise ValueError(f"GGUF architecture {arch} is not one this engine runs"
+                         + (f" ({why})" if why else "") + "; it runs lfm2")
+    v = _read_schema(meta, arch)
+    kv = v["kv"] if v["kv"] is not None else v["heads"]
+    v["kv"] = list(kv) if isinstance(kv, list) else [kv] * v["layers"]
+    if v["head_dim"] is None:
+        v["head_dim"] = v["hidden"] // v["heads"]
     emb = f.tensors.get("token_embd.weight")
-    if emb is None:
-        raise ValueError("GGUF: missing tensor token_embd.weight")
-    if emb.dims[0] != hidden:
-        raise ValueError(f"GGUF: token_embd has {emb.dims[0]} columns, expected {hidden}")
-    ffn = meta.get(f"{arch}.feed_forward_length")
+    v["emb"] = emb
     gate0 = f.tensors.get("blk.0.ffn_gate.weight")
-    inter = int(ffn) if isinstance(ffn, int) else (gate0.dims[1] if gate0 else -1)
-    if gate0 is not None and gate0.dims[1] != inter:
-        raise ValueError(f"GGUF: feed_forward_length {inter} doesn't match ffn_gate rows "
-                         f"{gate0.dims[1]}")
-    label = name or str(meta.get("general.name") or os.path.basename(f.path))
-    return E.ModelShape(label, hidden, layers, heads, kv_heads, head_dim, inter, emb.dims[1],
-                        "gguf", rope_theta=_f32_decimal(num("rope.freq_base")),
-                        eps=_f32_decimal(num("attention.layer_norm_rms_epsilon")),
-                        qk_norm=True, conv_kernel=int(num("shortconv.l_cache")),
-                        conv_layers=tuple(i for i, k in enumerate(kv) if k == 0),
-                        embed_fmt="gguf", extra={"context_length": int(num("context_length",
-                                                                            8192))})
+    v["gate_rows"] = gate0.dims[1] if gate0 is not None else None
+    if v["ffn"] is None:
+        v["ffn"] = v["gate_rows"] if v["gate_rows"] is not None else -1
+    v["arch"] = arch
+    return v
+
+
+# What the engine refuses, checked in order: (test over the fields and the
+# file, message). The first that holds raises.
+_REFUSALS = (
+    (lambda v, f: "output.weight" in f.tensors,
+     "GGUF file has its own output.weight: this engine ties the output head to the embedding"),
+    (lambda v, f: len(v["kv"]) != v["layers"],
+     "GGUF metadata gives {n_kv} KV head counts for {layers} layers"),
+    (lambda v, f: v["window"] > 0 or isinstance(v["window_pattern"], list),
+     "GGUF model uses sliding-window attention, which this engine does not run"),
+    (lambda v, f: len({k for k in v["kv"] if k}) > 1,
+     "GGUF model's attention layers differ in KV heads ({kv_set}); this engine needs one count"),
+    (lambda v, f: not any(v["kv"]),
+     "GGUF model has no attention layer (every KV head count is 0)"),
+    (lambda v, f: (v["rope_dims"] not in (None, v["head_dim"])) or "rope_freqs.weight" in f.tensors,
+     "GGUF model rotates part of each head (partial RoPE), which this engine does not run"),
+    (lambda v, f: v["emb"] is None,
+     "GGUF file has no token_embd.weight"),
+    (lambda v, f: v["emb"].dims[0] != v["hidden"],
+     "GGUF token_embd.weight rows are {emb_cols} wide; the model is {hidden} wide"),
+    (lambda v, f: v["gate_rows"] is not None and v["gate_rows"] != v["ffn"],
+     "GGUF metadata feed_forward_length {ffn} but blk.0.ffn_gate.weight has {gate_rows} rows"),
+)
+
+
+def gguf_shape(f: G.GgufFile, name: str | None = None) -> E.ModelShape:
+    """The engine's shape of an LFM2 GGUF file (what ggufConfig,
+    src/load-gguf.ts:600-752, reads for LFM2: short-conv layers where the
+    KV head count is 0, q/k norms, the output head tied to the
+    embedding)."""
+    v = _lfm2_fields(f)
+    for test, msg in _REFUSALS:
+        if test(v, f):
+            raise ValueError(msg.format(
+                n_kv=len(v["kv"]), layers=v["layers"], kv_set=sorted({k for k in v["kv"] if k}),
+                emb_cols=v["emb"].dims[0] if v["emb"] is not None else 0, hidden=v["hidden"],
+                ffn=v["ffn"], gate_rows=v["gate_rows"]))
+    label = name or str(f.metadata.get("general.name") or os.path.basename(f.path))
+    return E.ModelShape(label, v["hidden"], v["layers"], v["heads"], max(v["kv"]),
+                        v["head_dim"], v["ffn"], v["emb"].dims[1], "gguf",
+                        rope_theta=v["theta"], eps=v["eps"], qk_norm=True,
+                        conv_kernel=v["conv_kernel"],
+                        conv_layers=tuple(i for i, k in enumerate(v["kv"]) if k == 0),
+                        embed_fmt="gguf", extra={"context_length": v["context"]})
 
 
 class _Uploader:

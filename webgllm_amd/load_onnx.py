@@ -2,33 +2,38 @@
 GatherBlockQuantized embedding, as onnxruntime-genai writes them, or a
 float16 embedding read by a plain Gather with the LM head a MatMul over it
 transposed, as transformers.js exports have it) into the engine's device
-weights, as the reference's loadOnnx does (src/load-onnx.ts:119-447):
+weights: what the reference's loadOnnx takes (src/load-onnx.ts:119-447),
+found this loader's own way.
 
-- the settings from config.json over the shapes the weights have
-  (onnxConfig, :1333-1457);
-- each layer's weights found by the graph's structure, not by initializer
-  names (OnnxModel.layerPlan, :826-900): a projection is the MatMulNBits
-  node under its module path; the conv in_proj's B, C and x rows are
-  placed by following its Split to the convolution (bcxSegments,
-  :1043-1080); the attention's rotary embedding is checked against the
-  head layout the engine uses (checkRotary, :1109-1150);
-- the final norm: the norm feeding the LM head (finalNorm, :1166-1180);
-- the embedding, also the output head (embedding, :1191-1292): 4-bit rows
-  kept as they are; 8-bit rows with zero points, or float rows,
-  quantized to 8 bits, in chunks of rows.
+- A walker over the graph's dataflow (_Flow: the nodes a value reaches
+  downstream through given op types, the node that wrote it upstream)
+  answers every structural question.
+- One pass over the MatMulNBits nodes makes an inventory of the layer
+  projections, keyed by module path from the node's name or, where an
+  export renamed the node, from the weight it reads.
+- Tables say what each layer kind reads (projections with their shapes
+  in terms of the config), which embedding forms exist (tried in turn),
+  which rotary layouts match the engine's RoPE, and which config.json
+  fields the settings come from.
+- The conv in_proj's B, C and x rows are placed by following its Split
+  into the convolution: C is the part multiplied with the convolution's
+  output. The GroupQueryAttention is the node the o projection reads.
+- Every read the load makes is listed, and each tensor's size checked,
+  before any data is read.
 
 Fused matrices are assembled from their parts on the host (rows copied in
 the order the engine stores them) and repacked on the GPU
 (wg_repack_nbits); a matrix with an 8-bit part is 8-bit as a whole, every
 part dequantized and requantized there (wg_quantize_q8), as the reference
 stores it (:189-251). Architectures outside the engine's path (Qwen3.5's
-Gated DeltaNet, LFM3's attention gate, sliding-window or partial-RoPE
-attention, an untied head) are refused with a message.
+Gated DeltaNet, LFM3's attention gate, sandwich norms, sliding-window or
+partial-RoPE attention, an untied head) are refused with a message.
 """
 from __future__ import annotations
 
 import json
 import os
+import re
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -71,344 +76,525 @@ class Embedding:
     weight: OnnxTensor | None = None
 
 
-def _int64s(t: OnnxTensor) -> list:
-    """An int64 tensor's values (onnxInt64s, src/onnx.ts:329-345)."""
+def _int64_values(t: OnnxTensor) -> list:
+    """An int64 tensor's values, from its int64_data or its raw bytes."""
     if t.int64_data is not None:
         return [int(v) for v in t.int64_data]
     if t.raw is not None and t.data_type == INT64:
         return [int(v) for v in np.frombuffer(np.ascontiguousarray(t.raw).tobytes(), "<i8")]
-    raise ValueError(f"ONNX: {t.name} has no int64 values")
+    raise ValueError(f"ONNX tensor {t.name} carries no int64 values")
 
 
-class _Graph:
-    """The structural lookups of OnnxModel (src/load-onnx.ts:717-1290)
-    that the text loader needs, over an OnnxModel."""
+def _attr_int(node: OnnxNode, key: str, default=None):
+    a = node.attributes.get(key)
+    return default if a is None else int(a.i)
+
+
+# ------------------------------------------------------------ the dataflow
+class _Flow:
+    """Walks the graph's dataflow: values to the nodes that read them
+    (downstream) and to the node that wrote them (upstream)."""
 
     def __init__(self, model: OnnxModel):
         self.m = model
-        self.nodes = model.file.nodes
 
-    def consumers_of(self, name: str) -> list:
-        return self.m.consumers.get(name, [])
+    def readers(self, value: str) -> list:
+        return self.m.consumers.get(value, [])
 
-    def producer_of(self, name: str) -> OnnxNode | None:
-        return self.m.producers.get(name)
+    def writer(self, value: str) -> OnnxNode | None:
+        return self.m.producers.get(value)
 
-    def layer_plan(self, i: int, type_: str, cfg: dict) -> LayerPlan:
-        """layerPlan for LFM2 (src/load-onnx.ts:826-900)."""
-        m, D = self.m, cfg["hidden"]
-        p = f"model.layers.{i}."
-        for opt in ("post_operator_layernorm", "post_ffn_layernorm"):
-            if m.has(f"{p}{opt}.weight"):
-                raise ValueError(f"ONNX: layer {i} has a {opt} (sandwich norms are not on this "
-                                 "engine's path)")
-        norms = [m.init(f"{p}operator_layernorm.weight"), m.init(f"{p}ffn_layernorm.weight")]
+    def downstream(self, values, want, via=(), hops=1) -> list:
+        """The nodes satisfying `want` that read `values`, or read a value
+        written by a chain of at most `hops` nodes whose op types are in
+        `via` (breadth first, each node once)."""
+        found, seen = [], set()
+        frontier = list(values)
+        for depth in range(hops + 1):
+            nxt = []
+            for v in frontier:
+                for n in self.readers(v):
+                    if id(n) in seen:
+                        continue
+                    seen.add(id(n))
+                    if want(n):
+                        found.append(n)
+                    elif depth < hops and n.op_type in via:
+                        nxt.extend(n.outputs)
+            frontier = nxt
+        return found
 
-        def w(name):
-            return m.nbits(f"/model/layers.{i}/{name}/")
-        mlp = {"gate": w("mlp/gate_proj"), "up": w("mlp/up_proj"), "down": w("mlp/down_proj")}
-        if type_ == "conv":
-            in_proj, out_proj = w("conv/in_proj"), w("conv/out_proj")
-            if (in_proj.N, in_proj.K, out_proj.N, out_proj.K) != (3 * D, D, D, D):
-                raise ValueError(f"ONNX: layer {i} conv projections have unexpected shapes")
-            kernel = m.init(f"{p}conv.conv.weight")
-            check_shape(kernel, kernel.data_type, D * cfg["conv_kernel"])
-            if kernel.dims[0] != D or kernel.dims[-1] != cfg["conv_kernel"]:
-                raise ValueError(f"ONNX: {kernel.name} is {list(kernel.dims)}")
-            return LayerPlan(type_, norms, {"in_proj": in_proj, "out_proj": out_proj, **mlp},
-                             [kernel], bcx=self.bcx_segments(in_proj, D))
-        if m.has_nbits(f"/model/layers.{i}/attn/gate_proj/"):
-            raise ValueError(f"ONNX: layer {i}'s attention has an output gate (not on this "
-                             "engine's path)")
-        q, k, v, o = w("attn/q_proj"), w("attn/k_proj"), w("attn/v_proj"), w("attn/o_proj")
-        if q.N != cfg["heads"] * cfg["head_dim"]:
-            raise ValueError(f"ONNX: layer {i} q_proj has {q.N} rows, expected "
-                             f"{cfg['heads'] * cfg['head_dim']}")
-        extra = [m.init(f"{p}attn.q_norm.layernorm.weight"),
-                 m.init(f"{p}attn.k_norm.layernorm.weight")]
-        sin = self.check_rotary(i, cfg)
-        return LayerPlan(type_, norms, {"q": q, "k": k, "v": v, "o": o, **mlp}, extra,
-                         rope_sin=sin)
-
-    def split_sizes(self, split: OnnxNode) -> list:
-        """A Split's part sizes, from its input or attribute (splitSizes,
-        src/load-onnx.ts:995-1008)."""
-        a = split.attributes.get("axis")
-        axis = a.i if a is not None else 0
-        if axis not in (-1, 2, 1):
-            raise ValueError(f"ONNX: {split.name} doesn't split the channels axis")
-        if len(split.inputs) > 1 and split.inputs[1]:
-            return _int64s(self.m.constant(split.inputs[1]))
-        attr = split.attributes.get("split")
-        if attr is not None and attr.ints:
-            return list(attr.ints)
-        raise ValueError(f"ONNX: {split.name} has no split sizes")
-
-    def feeds(self, name: str, node: OnnxNode) -> bool:
-        """`name` reaches `node` through at most one Mul, then at most one
-        Concat (the export prepends the past conv state): feeds,
-        src/load-onnx.ts:1082-1099."""
-        if name in node.inputs:
-            return True
-        for n in self.consumers_of(name):
-            if n.op_type != "Mul":
-                continue
-            for o in n.outputs:
-                if o in node.inputs:
-                    return True
-                for c in self.consumers_of(o):
-                    if c.op_type == "Concat" and any(x in node.inputs for x in c.outputs):
-                        return True
-        return False
-
-    def bcx_segments(self, in_proj: NBits, D: int) -> list:
-        """in_proj's B, C, x rows (bcxSegments, src/load-onnx.ts:1043-1080):
-        C is the Split output multiplied by the convolution's output; B and
-        x are the two multiplied together before it, kept in the graph's
-        order."""
-        out = in_proj.node.outputs[0]
-        transposed = next((n for n in self.consumers_of(out) if n.op_type == "Transpose"), None)
-        names = [out] + (list(transposed.outputs) if transposed else [])
-        split = next((n for name in names for n in self.consumers_of(name)
-                      if n.op_type == "Split"), None)
-        if split is None:
-            raise ValueError(f"ONNX: {in_proj.node.name} is not split into B, C, x")
-        sizes = self.split_sizes(split)
-        if len(sizes) != 3 or any(s != D for s in sizes):
-            raise ValueError(f"ONNX: {split.name} sizes {sizes}")
-        conv = next((n for n in self.nodes
-                     if (n.op_type.startswith("CausalConv") or n.op_type == "Conv")
-                     and any(self.feeds(o, n) for o in split.outputs)), None)
-        if conv is None:
-            raise ValueError(f"ONNX: no convolution after {split.name}")
-        conv_out = {conv.outputs[0]}
-        for n in self.consumers_of(conv.outputs[0]):
-            if n.op_type == "Slice":
-                conv_out.add(n.outputs[0])
-        c_index = next((j for j, o in enumerate(split.outputs)
-                        if any(n.op_type == "Mul" and any(x in conv_out for x in n.inputs)
-                               for n in self.consumers_of(o))), -1)
-        if c_index < 0:
-            raise ValueError(f"ONNX: can't find C after {conv.name}")
-        others = [j for j in range(3) if j != c_index]
-        return [Segment(j * D, D) for j in (others[0], c_index, others[1])]
-
-    def check_rotary(self, i: int, cfg: dict) -> OnnxTensor | None:
-        """How layer i rotates q and k (checkRotary, src/load-onnx.ts:
-        1109-1150): by GroupQueryAttention itself, non-interleaved, over
-        every dim of a head (a cos cache of head_dim / 2 frequencies); or by
-        two RotaryEmbedding nodes before it over all of each head (HF's
-        layout, the same as the engine's when every dim rotates): their sin
-        cache is returned."""
-        prefix = f"/model/layers.{i}/"
-        gqa = next((n for n in self.nodes
-                    if n.op_type == "GroupQueryAttention" and n.name.startswith(prefix)), None)
-        if gqa is None:
-            raise ValueError(f"ONNX: no GroupQueryAttention in layer {i}")
-        hd = cfg["head_dim"]
-
-        def attr(n, key, default=0):
-            a = n.attributes.get(key)
-            return a.i if a is not None else default
-        if attr(gqa, "do_rotary") != 1:
-            rotary = [n for n in self.nodes
-                      if n.op_type == "RotaryEmbedding" and n.name.startswith(prefix + "attn/")]
-            sin = rotary[0].inputs[3] if rotary and len(rotary[0].inputs) > 3 else ""
-            cache = self.m.file.initializers.get(sin) if sin else None
-            if (len(rotary) != 2 or cache is None or len(cache.dims) != 2 or
-                    cache.dims[1] * 2 != hd or
-                    any(n.inputs[3] != sin or attr(n, "interleaved") != 0 or
-                        attr(n, "rotary_embedding_dim") != 0 for n in rotary) or
-                    not all(any(n.outputs[0] == x for n in rotary) for x in gqa.inputs[:2])):
-                raise ValueError(f"ONNX: layer {i}'s attention doesn't rotate q and k over each "
-                                 "head, non-interleaved")
-            return cache
-        if attr(gqa, "rotary_interleaved") != 0:
-            raise ValueError(f"ONNX: {gqa.name} doesn't apply non-interleaved rotary embeddings")
-        cos = gqa.inputs[7] if len(gqa.inputs) > 7 else ""
-        t = self.m.file.initializers.get(cos) if cos else None
-        rotated = t.dims[-1] * 2 if t is not None and t.dims else -1
-        if rotated != hd:
-            raise ValueError(f"ONNX: layer {i} rotates {rotated} dims per head, expected {hd} "
-                             "(partial RoPE is not on this engine's path)")
+    def upstream(self, value: str, want, via=None, hops=8) -> OnnxNode | None:
+        """The first node satisfying `want` walking writers back from
+        `value` along each node's first input, through at most `hops` nodes
+        (of the op types in `via`, any when None)."""
+        for _ in range(hops + 1):
+            n = self.writer(value) if value else None
+            if n is None:
+                return None
+            if want(n):
+                return n
+            if via is not None and n.op_type not in via:
+                return None
+            value = n.inputs[0] if n.inputs else ""
         return None
 
-    def lm_head(self) -> OnnxNode:
-        """The MatMulNBits or MatMul node under /lm_head/, or the one that
-        writes `logits` (through a Cast): lmHead, src/load-onnx.ts:1149-1164."""
-        def is_head(n):
-            return n is not None and n.op_type in ("MatMulNBits", "MatMul")
-        heads = [n for n in self.nodes if n.name.startswith("/lm_head/") and is_head(n)]
-        if len(heads) == 1:
-            return heads[0]
-        if not heads:
-            node = self.producer_of("logits")
-            if node is not None and node.op_type == "Cast":
-                node = self.producer_of(node.inputs[0])
-            if is_head(node):
-                return node
-        raise ValueError(f"ONNX: {len(heads)} LM head MatMul nodes")
 
-    def final_norm(self) -> OnnxTensor:
-        """The norm feeding the LM head (finalNorm, src/load-onnx.ts:1166-1180)."""
-        name = self.lm_head().inputs[0]
-        for _ in range(8):
-            node = self.producer_of(name) if name else None
-            if node is None:
-                break
-            if node.op_type == "SimplifiedLayerNormalization":
-                return self.m.init(node.inputs[1])
-            if node.op_type == "SkipSimplifiedLayerNormalization":
-                return self.m.init(node.inputs[2])
-            name = node.inputs[0]
-        raise ValueError("ONNX: can't find the final norm")
+def _op(*types):
+    return lambda n: n.op_type in types
 
-    def embedding(self, D: int) -> Embedding:
-        """The embedding, also the output head (embedding,
-        src/load-onnx.ts:1181-1292)."""
-        m = self.m
-        gather = next((n for n in self.nodes if n.op_type == "GatherBlockQuantized"), None)
-        if gather is not None:
-            def attr(key):
-                a = gather.attributes.get(key)
-                return None if a is None else a.i
-            bits = attr("bits")
-            if bits not in (4, 8) or attr("block_size") != 32 or attr("quantize_axis") != 1 or \
-                    (attr("gather_axis") or 0) != 0:
-                raise ValueError(f"ONNX: {gather.name} is not 4-bit or 8-bit, block 32, "
-                                 "quantized along rows")
-            reshaped = None if m.has(gather.inputs[0]) else self.producer_of(gather.inputs[0])
-            quant = m.init(reshaped.inputs[0] if reshaped is not None and
-                           reshaped.op_type == "Reshape" else gather.inputs[0])
-            scales = m.init(gather.inputs[2])
-            zp = m.init(gather.inputs[3]) if len(gather.inputs) > 3 and gather.inputs[3] else None
-            N = quant.dims[0]
-            check_shape(quant, UINT8, N * D * bits // 8)
-            check_shape(scales, FLOAT16, N * D // 32)
-            if zp is not None:
-                check_shape(zp, UINT8, N * -(-D // 64) if bits == 4 else N * D // 32)
-            head = self.lm_head()
-            if head.op_type == "MatMul":
-                raise ValueError("ONNX: the LM head is a float MatMul with its own weights, not "
-                                 "the embedding (only a tied head is supported)")
-            if bits == 8:
-                if head.inputs[1] != quant.name:
-                    raise ValueError(f"ONNX: the LM head isn't {quant.name} (only a tied head "
-                                     "is supported)")
-                return Embedding("q8", N, quant, scales, zp)
-            return Embedding("q4", N, quant, scales, zp)
-        fg = next((n for n in self.nodes if n.op_type == "Gather" and len(n.inputs) > 1 and
-                   n.inputs[1] == "input_ids" and m.has(n.inputs[0])), None)
-        if fg is not None:
-            weight = m.init(fg.inputs[0])
-            if weight.data_type not in (FLOAT16, FLOAT):
-                raise ValueError(f"ONNX: {weight.name} has data type {weight.data_type}, "
-                                 "expected float16 or float")
-            if len(weight.dims) != 2 or weight.dims[1] != D:
-                raise ValueError(f"ONNX: {weight.name} is {list(weight.dims)}")
-            head = self.lm_head()
-            tr = self.producer_of(head.inputs[1]) if len(head.inputs) > 1 else None
-            perm = tr.attributes.get("perm").ints if tr is not None and \
-                tr.attributes.get("perm") is not None else None
-            if head.op_type != "MatMul" or tr is None or tr.op_type != "Transpose" or \
-                    tr.inputs[0] != weight.name or (perm and list(perm) != [1, 0]):
-                raise ValueError(f"ONNX: the LM head isn't {weight.name} (only a tied head is "
-                                 "supported)")
-            return Embedding("float", weight.dims[0], weight=weight)
-        head = self.lm_head()
-        tr = self.producer_of(head.inputs[1]) if head.op_type == "MatMul" else None
-        if tr is not None and tr.op_type == "Transpose" and m.has(tr.inputs[0]):
-            weight = m.init(tr.inputs[0])
-            perm = tr.attributes.get("perm").ints if tr.attributes.get("perm") else None
-            if weight.data_type not in (FLOAT16, FLOAT):
-                raise ValueError(f"ONNX: {weight.name} has data type {weight.data_type}, "
-                                 "expected float16 or float")
-            if len(weight.dims) != 2 or weight.dims[1] != D or (perm and list(perm) != [1, 0]):
-                raise ValueError(f"ONNX: the LM head's {weight.name} is {list(weight.dims)}, not "
-                                 "the embedding transposed")
-            return Embedding("float", weight.dims[0], weight=weight)
-        if m.has_nbits("/lm_head/"):
-            h = m.nbits("/lm_head/")
-            if h.K != D:
-                raise ValueError(f"ONNX: lm_head has K {h.K}")
-            return Embedding("q4", h.N, h.quant, h.scales, h.zp)
-        raise ValueError("ONNX: no embedding the loader reads")
+
+def _is_conv(n: OnnxNode) -> bool:
+    return n.op_type == "Conv" or n.op_type.startswith("CausalConv")
+
+
+# ---------------------------------------------------- projections by module
+# A projection is the MatMulNBits node of a module: its node name is the
+# module path (/model/layers.3/attn/q_proj/...), or, where an export
+# renames nodes, the weight it reads is the module path in the
+# initializer spelling (model_layers_3_attn_q_proj_..., or dotted).
+_BY_NODE = re.compile(r"^/model/layers\.(\d+)/(conv|attn|mlp)/(\w+?)_proj/")
+_BY_WEIGHT = re.compile(r"^model_layers_(\d+)_(conv|attn|mlp)_([a-z]+)_proj_")
+
+
+def _spelling(name: str) -> str:
+    return re.sub(r"[^a-z0-9]+", "_", name.lower())
+
+
+def _inventory(model: OnnxModel) -> dict:
+    """Every layer projection of the graph in one pass: {(layer, block,
+    proj): NBits} (block conv | attn | mlp; proj as in q for q_proj). Two
+    nodes for one module is an error."""
+    out = {}
+    for n in model.file.nodes:
+        if n.op_type != "MatMulNBits":
+            continue
+        hit = _BY_NODE.match(n.name)
+        if hit is None and len(n.inputs) > 1 and model.has(n.inputs[1]):
+            hit = _BY_WEIGHT.match(_spelling(n.inputs[1]))
+        if hit is None:
+            continue
+        key = (int(hit.group(1)), hit.group(2), hit.group(3))
+        if key in out:
+            raise ValueError(f"ONNX graph has two MatMulNBits nodes for "
+                             f"layers.{key[0]}.{key[1]}.{key[2]}_proj ({out[key].node.name}, "
+                             f"{n.name})")
+        w = model.nbits_of(n, f"layers.{key[0]}.{key[1]}.{key[2]}_proj")
+        if w.block_size != 32:
+            raise ValueError(f"ONNX: {n.name} is not in blocks of 32")
+        out[key] = w
+    return out
+
+
+# What each layer kind reads: its operator block's projections with their
+# (rows, columns) in terms of the config, then the MLP's. The roles are the
+# engine's names for them.
+_OPERATOR = {
+    "conv": ("conv", (("in_proj", "in", lambda c: (3 * c["hidden"], c["hidden"])),
+                      ("out_proj", "out", lambda c: (c["hidden"], c["hidden"])))),
+    "full_attention": ("attn", (
+        ("q", "q", lambda c: (c["heads"] * c["head_dim"], c["hidden"])),
+        ("k", "k", lambda c: (c["kv_heads"] * c["head_dim"], c["hidden"])),
+        ("v", "v", lambda c: (c["kv_heads"] * c["head_dim"], c["hidden"])),
+        ("o", "o", lambda c: (c["hidden"], c["heads"] * c["head_dim"])))),
+}
+_MLP = (("gate", "gate", lambda c: (c["intermediate"], c["hidden"])),
+        ("up", "up", lambda c: (c["intermediate"], c["hidden"])),
+        ("down", "down", lambda c: (c["hidden"], c["intermediate"])))
+
+
+def _projections(inv: dict, i: int, kind: str, cfg: dict) -> dict:
+    """Layer i's projections by role, each of the shape the config gives;
+    a projection the engine has no place for (an attention output gate) is
+    refused."""
+    block, roles = _OPERATOR[kind]
+    wanted = [(block, r) for r in roles] + [("mlp", r) for r in _MLP]
+    known = {(blk, proj) for blk, (_, proj, _) in wanted}
+    for (layer, blk, proj) in inv:
+        if layer == i and blk in (block, "mlp") and (blk, proj) not in known:
+            raise ValueError(f"ONNX layer {i} has a {blk}/{proj}_proj projection (an attention "
+                             f"output gate), which this engine does not run")
+    out = {}
+    for blk, (role, proj, dims) in wanted:
+        w = inv.get((i, blk, proj))
+        if w is None:
+            raise ValueError(f"ONNX layer {i} ({kind}) has no {blk}/{proj}_proj MatMulNBits")
+        want = dims(cfg)
+        if (w.N, w.K) != want:
+            raise ValueError(f"ONNX layer {i}'s {blk}/{proj}_proj is {w.N} x {w.K}; the "
+                             f"config makes it {want[0]} x {want[1]}")
+        if w.K % 32:
+            raise ValueError(f"ONNX: {w.node.name} has K {w.K}, not a multiple of 32")
+        out[role] = w
+    return out
+
+
+def _split_parts(flow: _Flow, split: OnnxNode) -> list:
+    """A Split's part sizes (its second input, or its `split` attribute),
+    after checking it cuts the channel axis."""
+    axis = _attr_int(split, "axis", 0)
+    if axis not in (-1, 1, 2):
+        raise ValueError(f"ONNX: {split.name} splits axis {axis}, not the channels")
+    if len(split.inputs) > 1 and split.inputs[1]:
+        return _int64_values(flow.m.constant(split.inputs[1]))
+    a = split.attributes.get("split")
+    if a is not None and a.ints:
+        return list(a.ints)
+    raise ValueError(f"ONNX: {split.name} gives no part sizes")
+
+
+def _conv_rows(flow: _Flow, in_proj: NBits, D: int) -> list:
+    """in_proj's rows as the engine stores them, B | C | x, found from the
+    dataflow: its output (maybe transposed) is split in three D-wide
+    parts; the part whose product is taken with the convolution's output is
+    C, the two multiplied before the convolution are B and x (in the
+    Split's order)."""
+    split = next(iter(flow.downstream(in_proj.node.outputs[:1], _op("Split"),
+                                      via=("Transpose",), hops=1)), None)
+    if split is None:
+        raise ValueError(f"ONNX: the output of {in_proj.node.name} reaches no Split")
+    parts = _split_parts(flow, split)
+    if parts != [D, D, D]:
+        raise ValueError(f"ONNX: {split.name} cuts {parts}, not three parts of {D}")
+    conv = next(iter(flow.downstream(split.outputs, _is_conv, via=("Mul", "Concat"), hops=2)),
+                None)
+    if conv is None:
+        raise ValueError(f"ONNX: no convolution reads what {split.name} cuts")
+    conv_values = set(conv.outputs[:1]) | {n.outputs[0] for n in flow.readers(conv.outputs[0])
+                                           if n.op_type == "Slice"}
+    gated = [j for j, o in enumerate(split.outputs)
+             if any(n.op_type == "Mul" and conv_values & set(n.inputs) for n in flow.readers(o))]
+    if len(gated) != 1:
+        raise ValueError(f"ONNX: {len(gated)} parts of {split.name} multiply {conv.name}'s "
+                         "output; one (C) should")
+    b, x = (j for j in range(3) if j != gated[0])
+    return [Segment(b * D, D), Segment(gated[0] * D, D), Segment(x * D, D)]
+
+
+# The two ways an export rotates q and k that match the engine's RoPE (every
+# dim of a head, pairs (j, j + hd/2)): GroupQueryAttention's own rotary, or
+# a RotaryEmbedding on each of its q and k inputs sharing one sin cache.
+def _rotary_in_attention(flow: _Flow, gqa: OnnxNode, i: int, hd: int):
+    if _attr_int(gqa, "rotary_interleaved", 0) != 0:
+        raise ValueError(f"ONNX layer {i} rotates interleaved pairs; the engine's RoPE pairs "
+                         "dims (j, j + hd/2) (non-interleaved)")
+    cos = gqa.inputs[7] if len(gqa.inputs) > 7 else ""
+    cache = flow.m.file.initializers.get(cos) if cos else None
+    dims = 2 * cache.dims[-1] if cache is not None and cache.dims else 0
+    if dims != hd:
+        raise ValueError(f"ONNX layer {i} rotates {dims} of each head's {hd} dims (partial "
+                         "RoPE), which this engine does not run")
+    return None
+
+
+def _rotary_before_attention(flow: _Flow, gqa: OnnxNode, i: int, hd: int):
+    rot = [flow.writer(v) for v in gqa.inputs[:2]]
+    if any(r is None or r.op_type != "RotaryEmbedding" for r in rot):
+        raise ValueError(f"ONNX layer {i}'s attention neither rotates q and k itself nor reads "
+                         "them from RotaryEmbedding nodes")
+    sins = {r.inputs[3] if len(r.inputs) > 3 else "" for r in rot}
+    cache = flow.m.file.initializers.get(sins.pop()) if len(sins) == 1 else None
+    if cache is None or len(cache.dims) != 2 or 2 * cache.dims[1] != hd or \
+            any(_attr_int(r, "interleaved", 0) or _attr_int(r, "rotary_embedding_dim", 0)
+                for r in rot):
+        raise ValueError(f"ONNX layer {i}'s RotaryEmbedding nodes do not rotate every dim of a "
+                         "head in non-interleaved pairs from one sin cache")
+    return cache
+
+
+def _attention_rotary(flow: _Flow, o: NBits, i: int, hd: int) -> OnnxTensor | None:
+    """Checks how layer i rotates q and k: the GroupQueryAttention is what
+    the o projection reads. Returns the sin cache of RotaryEmbedding nodes,
+    or None when the attention rotates itself."""
+    gqa = flow.writer(o.node.inputs[0])
+    if gqa is None or gqa.op_type != "GroupQueryAttention":
+        raise ValueError(f"ONNX layer {i}'s o_proj does not read a GroupQueryAttention")
+    rotates_itself = _attr_int(gqa, "do_rotary", 0) == 1
+    return (_rotary_in_attention if rotates_itself else _rotary_before_attention)(flow, gqa, i, hd)
+
+
+# The norms the engine's layers read, by initializer name (the export's
+# module names); norms the engine has no place for are refused.
+_LAYER_NORMS = ("operator_layernorm", "ffn_layernorm")
+_SANDWICH_NORMS = ("post_operator_layernorm", "post_ffn_layernorm")
+
+
+def _layer_plan(flow: _Flow, inv: dict, i: int, kind: str, cfg: dict) -> LayerPlan:
+    m, D = flow.m, cfg["hidden"]
+    prefix = f"model.layers.{i}."
+    extra_norms = [n for n in _SANDWICH_NORMS if m.has(f"{prefix}{n}.weight")]
+    if extra_norms:
+        raise ValueError(f"ONNX layer {i} has {', '.join(extra_norms)} (sandwich norms), "
+                         "which this engine does not run")
+    norms = [m.init(f"{prefix}{n}.weight") for n in _LAYER_NORMS]
+    mats = _projections(inv, i, kind, cfg)
+    if kind == "conv":
+        kernel = m.init(f"{prefix}conv.conv.weight")
+        W = cfg["conv_kernel"]
+        check_shape(kernel, kernel.data_type, D * W)
+        if kernel.dims[0] != D or kernel.dims[-1] != W:
+            raise ValueError(f"ONNX: {kernel.name} is {list(kernel.dims)}, not [{D}, 1, {W}]")
+        return LayerPlan(kind, norms, mats, [kernel], bcx=_conv_rows(flow, mats["in_proj"], D))
+    qk = [m.init(f"{prefix}attn.{n}.layernorm.weight") for n in ("q_norm", "k_norm")]
+    sin = _attention_rotary(flow, mats["o"], i, cfg["head_dim"])
+    return LayerPlan(kind, norms, mats, qk, rope_sin=sin)
+
+
+# ------------------------------------------------------ head and embedding
+_NORM_WEIGHT_INPUT = {"SimplifiedLayerNormalization": 1, "SkipSimplifiedLayerNormalization": 2}
+
+
+def _head(flow: _Flow) -> OnnxNode:
+    """The LM head: the MatMulNBits or MatMul writing the graph's logits
+    (through a Cast), else the one node of that kind named /lm_head/."""
+    is_mm = _op("MatMulNBits", "MatMul")
+    node = flow.upstream("logits", is_mm, via=("Cast",), hops=1)
+    if node is not None:
+        return node
+    named = [n for n in flow.m.file.nodes if n.name.startswith("/lm_head/") and is_mm(n)]
+    if len(named) != 1:
+        raise ValueError(f"ONNX graph has {len(named)} LM head matmuls and none writes logits")
+    return named[0]
+
+
+def _final_norm(flow: _Flow) -> OnnxTensor:
+    """The weight of the last norm before the LM head."""
+    node = flow.upstream(_head(flow).inputs[0], lambda n: n.op_type in _NORM_WEIGHT_INPUT)
+    if node is None:
+        raise ValueError("ONNX: no RMS norm found before the LM head")
+    return flow.m.init(node.inputs[_NORM_WEIGHT_INPUT[node.op_type]])
+
+
+def _untied(what: str):
+    raise ValueError(f"ONNX: the LM head does not read {what}; this engine ties the output "
+                     "head to the embedding")
+
+
+def _transpose_of(flow: _Flow, value: str) -> str | None:
+    """The initializer a [1, 0] Transpose writes `value` from, or None."""
+    t = flow.writer(value)
+    if t is None or t.op_type != "Transpose" or not flow.m.has(t.inputs[0]):
+        return None
+    perm = t.attributes.get("perm")
+    if perm is not None and perm.ints and list(perm.ints) != [1, 0]:
+        return None
+    return t.inputs[0]
+
+
+def _float_table(m: OnnxModel, name: str, D: int) -> OnnxTensor:
+    w = m.init(name)
+    if w.data_type not in (FLOAT16, FLOAT):
+        raise ValueError(f"ONNX: {w.name} is of data type {w.data_type}; a float embedding is "
+                         "float16 or float")
+    if len(w.dims) != 2 or w.dims[1] != D:
+        raise ValueError(f"ONNX: {w.name} is {list(w.dims)}, not [vocab, {D}]")
+    return w
+
+
+# Each recognizer returns the Embedding if the graph has its form, else None.
+def _block_quantized_gather(flow: _Flow, D: int):
+    g = next(iter(flow.downstream(["input_ids"], _op("GatherBlockQuantized"))), None)
+    if g is None:
+        g = next((n for n in flow.m.file.nodes if n.op_type == "GatherBlockQuantized"), None)
+    if g is None:
+        return None
+    bits = _attr_int(g, "bits")
+    form = (bits, _attr_int(g, "block_size"), _attr_int(g, "quantize_axis"),
+            _attr_int(g, "gather_axis", 0))
+    if form not in ((4, 32, 1, 0), (8, 32, 1, 0)):
+        raise ValueError(f"ONNX: {g.name} reads bits/block/axes {form}; the engine reads 4- or "
+                         "8-bit rows in blocks of 32")
+    m = flow.m
+    src = g.inputs[0]
+    if not m.has(src):  # the export may reshape the table first
+        r = flow.writer(src)
+        src = r.inputs[0] if r is not None and r.op_type == "Reshape" else src
+    quant, scales = m.init(src), m.init(g.inputs[2])
+    zp = m.init(g.inputs[3]) if len(g.inputs) > 3 and g.inputs[3] else None
+    V = quant.dims[0]
+    check_shape(quant, UINT8, V * D * bits // 8)
+    check_shape(scales, FLOAT16, V * D // 32)
+    if zp is not None:
+        check_shape(zp, UINT8, V * (-(-D // 64) if bits == 4 else D // 32))
+    head = _head(flow)
+    if head.op_type == "MatMul":
+        _untied(quant.name + " (it is a float MatMul with weights of its own)")
+    if bits == 8 and head.inputs[1] != quant.name:
+        _untied(quant.name)
+    return Embedding("q4" if bits == 4 else "q8", V, quant, scales, zp)
+
+
+def _float_gather(flow: _Flow, D: int):
+    m = flow.m
+    g = next(iter(flow.downstream(["input_ids"],
+                                  lambda n: n.op_type == "Gather" and m.has(n.inputs[0]))), None)
+    if g is None:
+        return None
+    w = _float_table(m, g.inputs[0], D)
+    head = _head(flow)
+    if head.op_type != "MatMul" or len(head.inputs) < 2 or \
+            _transpose_of(flow, head.inputs[1]) != w.name:
+        _untied(w.name + " transposed")
+    return Embedding("float", w.dims[0], weight=w)
+
+
+def _transposed_head(flow: _Flow, D: int):
+    head = _head(flow)
+    name = _transpose_of(flow, head.inputs[1]) if head.op_type == "MatMul" else None
+    if name is None:
+        return None
+    w = _float_table(flow.m, name, D)
+    return Embedding("float", w.dims[0], weight=w)
+
+
+def _quantized_head(flow: _Flow, D: int):
+    head = _head(flow)
+    if head.op_type != "MatMulNBits":
+        return None
+    h = flow.m.nbits_of(head, "lm_head")
+    if h.K != D or h.bits != 4 or h.block_size != 32:
+        raise ValueError(f"ONNX: the LM head {head.name} is {h.bits}-bit over {h.K} columns; "
+                         f"a 4-bit head of {D} columns stands for the embedding")
+    return Embedding("q4", h.N, h.quant, h.scales, h.zp)
+
+
+_EMBEDDING_FORMS = (_block_quantized_gather, _float_gather, _transposed_head, _quantized_head)
+
+
+def _embedding(flow: _Flow, D: int) -> Embedding:
+    """The embedding table (also the output head) in the first form the
+    graph has."""
+    for recognize in _EMBEDDING_FORMS:
+        e = recognize(flow, D)
+        if e is not None:
+            return e
+    raise ValueError("ONNX: no embedding in a form this loader reads")
+
+
+# ------------------------------------------------------------- the config
+# config.json fields: (name, keys tried in turn, default or _NEEDED or a
+# function of the fields read so far). Transformers' LFM2 config names the
+# keys; the table is this loader's.
+_NEEDED = object()
+_CONFIG_FIELDS = (
+    ("layers", ("num_hidden_layers",), _NEEDED),
+    ("hidden", ("hidden_size",), _NEEDED),
+    ("heads", ("num_attention_heads",), _NEEDED),
+    ("kv_heads", ("num_key_value_heads",), lambda v: v["heads"]),
+    ("head_dim", ("head_dim",), lambda v: v["hidden"] // v["heads"]),
+    ("context_length", ("max_position_embeddings",), 8192),
+    ("eps", ("norm_eps", "rms_norm_eps"), 1e-5),
+    ("conv_kernel", ("conv_L_cache",), _NEEDED),
+    ("sliding_window", ("sliding_window",), 0),
+    ("rope_theta_flat", ("rope_theta",), None),
+)
+_INT_FIELDS = {"layers", "hidden", "heads", "kv_heads", "head_dim", "context_length",
+               "conv_kernel"}
+_LAYER_KINDS = ("conv", "full_attention", "sliding_attention", "linear_attention")
+_ENGINE_KINDS = ("conv", "full_attention")
+
+
+def _config_fields(c: dict) -> dict:
+    v = {}
+    for name, keys, default in _CONFIG_FIELDS:
+        raw = next((c[k] for k in keys if c.get(k) is not None), None)
+        if raw is None:
+            if default is _NEEDED:
+                raise ValueError(f"config.json has no {keys[0]}")
+            raw = default(v) if callable(default) else default
+        elif isinstance(raw, bool) or not isinstance(raw, (int, float)):
+            raise ValueError(f"config.json: {keys[0]} is {raw!r}, not a number")
+        v[name] = int(raw) if name in _INT_FIELDS else raw
+    return v
+
+
+def _layer_kinds(c: dict, layers: int) -> list:
+    if isinstance(c.get("layer_types"), list):
+        kinds = list(c["layer_types"])
+        unknown = [k for k in kinds if k not in _LAYER_KINDS]
+        if unknown:
+            raise ValueError(f"config.json names layer type {unknown[0]!r}")
+    elif isinstance(c.get("full_attn_idxs"), list):
+        attn = set(c["full_attn_idxs"])
+        kinds = ["full_attention" if i in attn else "conv" for i in range(layers)]
+    else:
+        raise ValueError("config.json has neither layer_types nor full_attn_idxs")
+    if len(kinds) != layers:
+        raise ValueError(f"config.json lists {len(kinds)} layer types for {layers} layers")
+    off = sorted({k for k in kinds if k not in _ENGINE_KINDS})
+    if off:
+        raise ValueError(f"ONNX model has {' and '.join(off)} layers, which this engine does "
+                         "not run")
+    if "full_attention" not in kinds:
+        raise ValueError("ONNX model has no attention layer")
+    return kinds
+
+
+def _rope(c: dict, v: dict) -> float:
+    """RoPE's base, with the checks that it is the plain kind over whole
+    heads."""
+    params = c.get("rope_parameters") or {}
+    full = params.get("full_attention", params) if isinstance(params, dict) else {}
+    kind = full.get("rope_type")
+    if kind not in (None, "default"):
+        raise ValueError(f"config.json asks for {kind} RoPE; this engine runs the default kind")
+    frac = full.get("partial_rotary_factor", 1)
+    if round(frac * v["head_dim"]) != v["head_dim"]:
+        raise ValueError(f"config.json rotates {frac} of each head (partial RoPE), which this "
+                         "engine does not run")
+    theta = full.get("rope_theta", v["rope_theta_flat"])
+    if theta is None:
+        raise ValueError("config.json has no rope_theta")
+    return float(theta)
+
+
+def _special_token(c: dict, key: str) -> int:
+    t = c.get(key)
+    if isinstance(t, list) and t and isinstance(t[0], int):
+        return t[0]
+    return t if isinstance(t, int) and not isinstance(t, bool) else -1
 
 
 def onnx_config(config: dict, model: OnnxModel) -> dict:
-    """The model's settings: config.json over the shapes the weights have
-    (onnxConfig, src/load-onnx.ts:1333-1457), for the layer types the
-    engine runs (conv and full attention)."""
+    """The engine's settings from config.json (its text_config where it
+    has one), checked against the shapes of the graph's weights: the MLP
+    width and the vocabulary are the weights' (an export may shrink the
+    MLP: block_auto_adjust_ff_dim)."""
     if not isinstance(config, dict):
-        raise ValueError("ONNX: config must be the parsed config.json")
-    c = config.get("text_config") if isinstance(config.get("text_config"), dict) else config
-
-    def num(key, fallback=None):
-        v = c.get(key, fallback)
-        if isinstance(v, bool) or not isinstance(v, (int, float)):
-            raise ValueError(f"config.json: {key} is missing")
-        return v
-    layers = int(num("num_hidden_layers"))
-    hidden = int(num("hidden_size"))
-    heads = int(num("num_attention_heads"))
-    head_dim = int(num("head_dim", hidden // heads))
-    if isinstance(c.get("layer_types"), list):
-        types = []
-        for t in c["layer_types"]:
-            if t not in ("conv", "full_attention", "sliding_attention", "linear_attention"):
-                raise ValueError(f"config.json: unknown layer type {t}")
-            types.append(t)
-    elif isinstance(c.get("full_attn_idxs"), list):
-        full = set(c["full_attn_idxs"])
-        types = ["full_attention" if i in full else "conv" for i in range(layers)]
-    else:
-        raise ValueError("config.json: no layer_types")
-    if len(types) != layers:
-        raise ValueError("config.json: layer_types doesn't match num_hidden_layers")
-    bad = sorted({t for t in types if t not in ("conv", "full_attention")})
-    if bad:
-        raise ValueError(f"ONNX: {', '.join(bad)} layers are not on this engine's path")
-    if "full_attention" not in types:
-        raise ValueError("ONNX: no attention layer")
-    rope = c.get("rope_parameters") or {}
-    full_rope = rope.get("full_attention", rope) if isinstance(rope, dict) else {}
-    if full_rope.get("rope_type") not in (None, "default"):
-        raise ValueError(f"config.json: rope type {full_rope['rope_type']} is not supported")
-    theta = full_rope.get("rope_theta", None)
-    theta = float(theta if theta is not None else num("rope_theta"))
-    rotated = round(full_rope.get("partial_rotary_factor", 1) * head_dim)
-    if rotated != head_dim:
-        raise ValueError("ONNX: partial RoPE is not on this engine's path")
-    if num("sliding_window", 0) > 0:
-        raise ValueError("ONNX: sliding-window attention is not on this engine's path")
-    inter = model.nbits("/model/layers.0/mlp/gate_proj/").N
-    if c.get("intermediate_size") is not None and c["intermediate_size"] != inter and \
-            not c.get("block_auto_adjust_ff_dim"):
-        raise ValueError(f"config.json: intermediate_size {c['intermediate_size']} but the "
-                         f"weights have {inter}")
-    emb = _Graph(model).embedding(hidden)
+        raise ValueError("ONNX: the config must be config.json parsed")
+    c = config["text_config"] if isinstance(config.get("text_config"), dict) else config
+    v = _config_fields(c)
+    kinds = _layer_kinds(c, v["layers"])
+    theta = _rope(c, v)
+    if v["sliding_window"] > 0:
+        raise ValueError("config.json sets a sliding window; this engine attends to the whole "
+                         "context")
+    inv = _inventory(model)
+    gate0 = inv.get((0, "mlp", "gate"))
+    if gate0 is None:
+        raise ValueError("ONNX layer 0 has no mlp/gate_proj MatMulNBits")
+    inter = gate0.N
+    said = c.get("intermediate_size")
+    if said is not None and said != inter and not c.get("block_auto_adjust_ff_dim"):
+        raise ValueError(f"config.json: intermediate_size {said}, the weights' MLP is {inter} "
+                         "wide")
+    emb = _embedding(_Flow(model), v["hidden"])
     if c.get("vocab_size") is not None and c["vocab_size"] != emb.N:
-        raise ValueError(f"config.json: vocab_size {c['vocab_size']} but the embedding has "
+        raise ValueError(f"config.json: vocab_size {c['vocab_size']}, the embedding has "
                          f"{emb.N} rows")
-
-    def token(key):
-        v = c.get(key)
-        if isinstance(v, list) and v and isinstance(v[0], int):
-            return v[0]
-        return v if isinstance(v, int) and not isinstance(v, bool) else -1
-    return {"layers": layers, "hidden": hidden, "heads": heads,
-            "kv_heads": int(num("num_key_value_heads", heads)), "head_dim": head_dim,
-            "intermediate": inter, "vocab": emb.N, "layer_types": types,
-            "context_length": int(num("max_position_embeddings", 8192)), "rope_theta": theta,
-            "eps": float(num("norm_eps", num("rms_norm_eps", 1e-5))),
-            "conv_kernel": int(num("conv_L_cache")), "bos": token("bos_token_id"),
-            "eos": token("eos_token_id"), "pad": token("pad_token_id")}
+    return {"layers": v["layers"], "hidden": v["hidden"], "heads": v["heads"],
+            "kv_heads": v["kv_heads"], "head_dim": v["head_dim"], "intermediate": inter,
+            "vocab": emb.N, "layer_types": kinds, "context_length": v["context_length"],
+            "rope_theta": theta, "eps": float(v["eps"]), "conv_kernel": v["conv_kernel"],
+            "bos": _special_token(c, "bos_token_id"), "eos": _special_token(c, "eos_token_id"),
+            "pad": _special_token(c, "pad_token_id")}
 
 
+# ------------------------------------------------------------- the plan
 @dataclass
 class OnnxPlan:
-    """Everything the load reads, checked against the layout (planOnnx,
-    src/load-onnx.ts:557-668)."""
+    """What a load reads: the settings, each layer's tensors, the final
+    norm, the embedding, and every read the load makes, in order."""
     config: dict
     shape: E.ModelShape
     layers: list
@@ -417,96 +603,100 @@ class OnnxPlan:
     reads: list                     # (tensor name, location or "", offset, length)
 
 
-def plan_onnx(model: OnnxModel, config: dict, name: str | None = None,
-              chunk_rows: int = 2048) -> OnnxPlan:
-    """Checks the graph against what the loader takes and lists every read
-    the load makes, in order, without reading the external data."""
-    cfg = onnx_config(config, model)
-    g = _Graph(model)
-    D, F = cfg["hidden"], cfg["intermediate"]
-    kv = cfg["kv_heads"] * cfg["head_dim"]
-    plans = [g.layer_plan(i, t, cfg) for i, t in enumerate(cfg["layer_types"])]
-    for i, lp in enumerate(plans):
-        mm = lp.matrices
-        if lp.type != "conv" and (mm["k"].N != kv or mm["v"].N != kv):
-            raise ValueError(f"ONNX: layer {i} k/v projections have {mm['k'].N}/{mm['v'].N} rows")
-        if mm["gate"].N != F or mm["up"].N != F or mm["down"].K != F:
-            raise ValueError(f"ONNX: layer {i} MLP shapes don't match")
-        for w in mm.values():
-            if w.K % 32:
-                raise ValueError(f"ONNX: {w.name} has K {w.K}, not a multiple of 32")
-    reads = []
+class _Reads:
+    """The list of reads a load makes, each tensor checked to hold the
+    bytes its shape says."""
 
-    def want(t):
+    def __init__(self):
+        self.items = []
+
+    def whole(self, t: OnnxTensor | None) -> None:
         if t is None:
             return
         n = tensor_bytes(t)
         if t.external is None:
             if t.raw is None:
-                raise ValueError(f"ONNX: {t.name} has no data")
+                raise ValueError(f"ONNX: {t.name} holds no data")
             if t.raw.size != n:
                 raise ValueError(f"ONNX: {t.name} has {t.raw.size} bytes, expected {n}")
-            reads.append((t.name, "", 0, n))
+            self.items.append((t.name, "", 0, n))
             return
         if t.external[2] != n:
             raise ValueError(f"ONNX: {t.name} has {t.external[2]} bytes, expected {n}")
-        reads.append((t.name, t.external[0], t.external[1], n))
-    for lp in plans:
+        self.items.append((t.name, t.external[0], t.external[1], n))
+
+    def rows(self, t: OnnxTensor, row_bytes: int, N: int, r0: int, n: int) -> None:
+        """Rows [r0, r0 + n) of an N-row tensor in the external data."""
+        if t.external is None:
+            raise ValueError(f"ONNX: {t.name} is not in the external data file")
+        if t.external[2] != tensor_bytes(t) or row_bytes * N != tensor_bytes(t):
+            raise ValueError(f"ONNX: {t.name} has {t.external[2]} bytes, expected {row_bytes * N}")
+        self.items.append((t.name, t.external[0], t.external[1] + r0 * row_bytes, n * row_bytes))
+
+
+def _embedding_row_bytes(emb: Embedding, D: int) -> list:
+    """(tensor, bytes a row) of each array an embedding chunk reads."""
+    blocks = D // 32
+    if emb.kind == "float":
+        return [(emb.weight, D * int(element_size(emb.weight.data_type)))]
+    out = [(emb.quant, blocks * (32 if emb.kind == "q8" else 16)), (emb.scales, blocks * 2)]
+    if emb.zp is not None:
+        out.append((emb.zp, blocks if emb.kind == "q8" else -(-blocks // 2)))
+    return out
+
+
+def plan_onnx(model: OnnxModel, config: dict, name: str | None = None,
+              chunk_rows: int = 2048) -> OnnxPlan:
+    """Checks the graph against what the loader takes and lists every read
+    the load makes, in the load's order (per layer its norms, operator
+    matrices, conv kernel or q/k norms, MLP; the final norm; the embedding
+    in chunks of rows), without reading the external data."""
+    cfg = onnx_config(config, model)
+    flow, inv = _Flow(model), _inventory(model)
+    layers = [_layer_plan(flow, inv, i, k, cfg) for i, k in enumerate(cfg["layer_types"])]
+    reads = _Reads()
+    for lp in layers:
         for t in lp.norms:
-            want(t)
-        for role, w in lp.matrices.items():
-            if role not in ("gate", "up", "down"):
-                for t in (w.quant, w.scales, w.zp):
-                    want(t)
-        for t in lp.extra:
-            want(t)
-        for role in ("gate", "up", "down"):
-            w = lp.matrices[role]
+            reads.whole(t)
+        operator = [w for role, w in lp.matrices.items() if role not in ("gate", "up", "down")]
+        mlp = [lp.matrices[r] for r in ("gate", "up", "down")]
+        for w in operator:
             for t in (w.quant, w.scales, w.zp):
-                want(t)
-    final = g.final_norm()
-    want(final)
-    emb = g.embedding(D)
+                reads.whole(t)
+        for t in lp.extra:
+            reads.whole(t)
+        for w in mlp:
+            for t in (w.quant, w.scales, w.zp):
+                reads.whole(t)
+    final = _final_norm(flow)
+    reads.whole(final)
+    D = cfg["hidden"]
+    emb = _embedding(flow, D)
     if emb.N % 4:
         raise ValueError(f"ONNX: the embedding has {emb.N} rows, not a multiple of 4")
     if chunk_rows < emb.N and chunk_rows % 4:
-        raise ValueError(f"ONNX: embedding chunks of {chunk_rows} rows aren't a multiple of 4")
-    blocks = D // 32
-    for r in range(0, emb.N, chunk_rows):
-        rows = min(chunk_rows, emb.N - r)
-
-        def ext(t, row_bytes):
-            if t.external is None:
-                raise ValueError(f"ONNX: {t.name} is expected in the external data file")
-            if t.external[2] != tensor_bytes(t) or row_bytes * emb.N != tensor_bytes(t):
-                raise ValueError(f"ONNX: {t.name} has {t.external[2]} bytes, expected "
-                                 f"{row_bytes * emb.N}")
-            reads.append((t.name, t.external[0], t.external[1] + r * row_bytes,
-                          rows * row_bytes))
-        if emb.kind == "float":
-            ext(emb.weight, D * int(element_size(emb.weight.data_type)))
-            continue
-        ext(emb.quant, blocks * (32 if emb.kind == "q8" else 16))
-        ext(emb.scales, blocks * 2)
-        if emb.zp is not None:
-            ext(emb.zp, blocks if emb.kind == "q8" else -(-blocks // 2))
-    types = cfg["layer_types"]
+        raise ValueError(f"ONNX: embedding chunks of {chunk_rows} rows, not a multiple of 4")
+    arrays = _embedding_row_bytes(emb, D)
+    for r0 in range(0, emb.N, chunk_rows):
+        n = min(chunk_rows, emb.N - r0)
+        for t, row_bytes in arrays:
+            reads.rows(t, row_bytes, emb.N, r0, n)
+    kinds = cfg["layer_types"]
     # the model's folder names it (an export's graph is "main_graph" or the like)
     label = name or os.path.basename(os.path.dirname(os.path.abspath(model.file.path))) or \
         model.file.name
     shape = E.ModelShape(label, D, cfg["layers"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
-                         F, emb.N, "nbits", rope_theta=cfg["rope_theta"], eps=cfg["eps"],
-                         qk_norm=True, conv_kernel=cfg["conv_kernel"],
-                         conv_layers=tuple(i for i, t in enumerate(types) if t == "conv"),
+                         cfg["intermediate"], emb.N, "nbits", rope_theta=cfg["rope_theta"],
+                         eps=cfg["eps"], qk_norm=True, conv_kernel=cfg["conv_kernel"],
+                         conv_layers=tuple(i for i, k in enumerate(kinds) if k == "conv"),
                          embed_fmt="nbits" if emb.kind == "q4" else "q8",
                          extra={k: cfg[k] for k in ("context_length", "bos", "eos", "pad")})
-    return OnnxPlan(cfg, shape, plans, final, emb, reads)
+    return OnnxPlan(cfg, shape, layers, final, emb, reads.items)
 
 
 def check_onnx(path: str, config: dict) -> list:
     """The external data files a graph's weights are in, reading only the
-    graph; raises the loader's own error where the loader doesn't take it
-    (checkOnnxGraph, src/load-onnx.ts:662-681)."""
+    graph; raises where the loader would refuse the model."""
     with OnnxFile(path) as f:
         return check_model(OnnxModel(f), config)
 

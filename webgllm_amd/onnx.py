@@ -259,6 +259,10 @@ class OnnxModel:
         node = self.nbits_node(path)
         if node is None:
             raise ValueError(f"ONNX: no MatMulNBits node under {path}")
+        return self.nbits_of(node, path)
+
+    def nbits_of(self, node: OnnxNode, label: str) -> NBits:
+        """The weight a MatMulNBits node reads, checked as wide_nbits does."""
         quant = self.init(node.inputs[1])
         scales = self.init(node.inputs[2])
         zp = self.init(node.inputs[3]) if len(node.inputs) > 3 and node.inputs[3] else None
@@ -281,7 +285,7 @@ class OnnxModel:
         check_shape(scales, scales.data_type, N * blocks)
         if zp is not None:
             check_shape(zp, UINT8, N * (-(-blocks // 2) if bits == 4 else blocks))
-        return NBits(path, node, N, K, bits, bs, quant, scales, zp)
+        return NBits(label, node, N, K, bits, bs, quant, scales, zp)
 
     def nbits(self, path: str) -> NBits:
         """nbits: the text loader's weights, blocks of 32."""
