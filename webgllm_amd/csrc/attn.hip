@@ -303,14 +303,18 @@ constexpr int MERGE_ROWS = 12;
 __host__ __device__ constexpr int split_row(int hd) { return hd + 4; }
 
 // How split partials pass from the workgroups that write them to the one
-// that combines them. Across XCDs (LOCAL false): 16-byte stores with sc1,
-// loads with sc1 (past the L2s, which are not coherent with each other)
-// and the count at agent scope. Within one XCD (LOCAL true: every
-// workgroup of the exchange runs on it): plain stores, which the vector L1
-// writes through to the XCD's L2, loads with sc0, which miss the L1 and
-// read that L2, and the count as an L2 atomic (workgroup scope). The loads
-// are buffer loads whose cache-policy bits the compiler sees, so that it
-// places the waits for their results itself.
+// that combines them. Across XCDs (LOCAL false): 16-byte stores with sc1
+// (through to memory: the XCDs' L2s are not coherent with each other) and
+// the count at agent scope. Within one XCD (LOCAL true: every workgroup of
+// the exchange runs on it): plain stores, which the vector L1 writes
+// through to the XCD's L2, and the count as an L2 atomic (workgroup
+// scope). Loads with sc1 either way: they pass the L1 and take the line
+// from the XCD's L2 when it has it (measured on the MI355X: a plain or sc0
+// load keeps returning a line the CU's L1 holds, even after a workgroup on
+// the same XCD has stored to it and counted itself in; an sc1 load sees
+// the store every time, and takes a line the L2 holds in the L2 hit's
+// time). The loads are buffer loads whose cache-policy bits the compiler
+// sees, so that it places the waits for their results itself.
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef float f2v __attribute__((ext_vector_type(2)));
 template <bool LOCAL>
@@ -324,9 +328,9 @@ __device__ inline void store_part(float *p, f4v v) {
 __device__ inline __amdgpu_buffer_rsrc_t rsrc_of(const float *base) {
   return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
 }
-// a buffer load's cache policy: sc0 (bit 0) or sc1 (bit 4)
+// a buffer load's cache policy: sc1 (bit 4)
 template <bool LOCAL>
-constexpr int part_policy() { return LOCAL ? 1 : 16; }
+constexpr int part_policy() { return 16; }
 template <bool LOCAL>
 __device__ inline f4v load_part(__amdgpu_buffer_rsrc_t r, int byte_off) {
   return __builtin_bit_cast(
