@@ -269,6 +269,11 @@ class Engine:
         self.draft = None
         self._pre = None  # prefill buffers, made on the first prompt batch
         self._cols = {}   # device row orders of the matrices (GEMM column maps)
+        # probe(layer, name, rows), called as the forward enqueues (not under
+        # graph capture): ("embedding", h rows) after the lookup, ("attention",
+        # (q rows, output rows)) after each attention, ("output", h rows)
+        # after the last layer; the self-check reads them back
+        self.probe = None
 
     # --- the attention caches, grown on demand ------------------------------
     def reserve(self, end: int) -> None:
@@ -344,8 +349,12 @@ class Engine:
         the greedy picks into next_ids unless `pick` is False (the caller
         picks)."""
         self._embed_rows(M)
+        if self.probe:
+            self.probe(-1, "embedding", self.h[:M])
         for i in range(len(self.w.layers)):
             self._layer_rows(i, M, keep_prefixes)
+        if self.probe:
+            self.probe(len(self.w.layers) - 1, "output", self.h[:M])
         self._head_rows(M, pick)
 
     def _embed_rows(self, M: int) -> None:
@@ -385,6 +394,8 @@ class Engine:
                               q_out=self.q[:M])
             ops.attn_decode(self.q[:M], self.attn, self.k_cache[i], self.v_cache[i],
                             self.pos, scratch=self.attn_scratch, out=self.att16[:M])
+            if self.probe:
+                self.probe(i, "attention", (self.q[:M], self.att16[:M]))
             ops.gemv(lw["o"], self.att16[:M], out=h,
                      epilogue=self._residual_out(M, lw["ffn_norm"]))
         ops.gemv(lw["gate_up"], x16,
@@ -471,6 +482,8 @@ class Engine:
                               q_out=b["q"][:M])
                 ops.attn_prefill(b["q"][:M], self.attn, self.k_cache[i], self.v_cache[i],
                                  self.pos, out=b["att16"][:M])
+                if self.probe:
+                    self.probe(i, "attention", (b["q"][:M], b["att16"][:M]))
                 ops.gemm(lw["o"], b["att16"][:M], out=h, residual=h)
             ops.norm_to_h2(h, lw["ffn_norm"], s.eps, x16, rs)
             ops.gemm_swiglu(lw["gate_up"], x16, out=b["ff16"][:M], row_scale=rs)
