@@ -353,10 +353,24 @@ int wg_q4_dequant(const wg_q4_matrix *m, int32_t row0, int32_t rows, float *out,
  *  WG_EPI_ROPE_KV: the matrix is a q|k|v projection whose q and k rows come
  *    in groups of 4 as (j, j + hd/2, j + 1, j + 1 + hd/2) of a head (all dims
  *    rotated); q goes to q_out (rotated, times 1/sqrt(hd)), k (rotated) and
- *    v to the caches as halves at row *pos0 + m (see wg_head_prep). */
+ *    v to the caches as halves at row *pos0 + m (see wg_head_prep).
+ *  WG_EPI_SHORT_CONV: the matrix is a short-conv in_proj of N = 3 D rows,
+ *    B | C | x (D a multiple of 16); the GEMV's float32 outputs go straight
+ *    into wg_short_conv's computation (same results, bit for bit, as
+ *    wg_q4_gemv with WG_EPI_STORE then wg_short_conv over those rows):
+ *    out16[m][c] = half(C_m[c] * sum_k conv_taps[c][k] y[m - (W-1) + k])
+ *    with y_t = B_t[c] x_t[c] (earlier tokens' y from conv_state, W - 1
+ *    rows of D, oldest first), the state after the M tokens to
+ *    conv_state_out (may equal conv_state), and with conv_prefixes the
+ *    state after each prefix ([M][W - 1][D]). W = conv_width, 2 to 4; y
+ *    is not written. Taken by the streaming and the MFMA GEMVs on 4-bit
+ *    row-group matrices (one to eight tokens); elsewhere the
+ *    call returns WG_ERR_UNSUPPORTED and the caller makes the two calls
+ *    (LFM2's convolve: src/engine.ts:5806-5899, src/gpu/kernels.ts:1447-1523). */
 #define WG_EPI_STORE 0
 #define WG_EPI_SWIGLU 1
 #define WG_EPI_ROPE_KV 2
+#define WG_EPI_SHORT_CONV 3
 
 typedef struct {
   int32_t mode;
@@ -382,6 +396,12 @@ typedef struct {
   float *q_out;
   int32_t ld_q_out;
   uint16_t *k_cache, *v_cache;
+  /* WG_EPI_SHORT_CONV */
+  const float *conv_taps;
+  const float *conv_state;
+  float *conv_state_out;
+  float *conv_prefixes;
+  int32_t conv_width;
 } wg_epilogue;
 
 /* Decode / few-token GEMV (matmulSplitRgba4 and the split matmul,

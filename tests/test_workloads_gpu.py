@@ -298,6 +298,7 @@ def test_lfm2_width_verify_layerwise_and_rollback(hip):
     s = dataclasses.replace(E.LFM2_12B, layers=4, conv_layers=(0, 1, 3))
     w = E.Weights(s, seed=43)
     eng, orc = E.Engine(w, 256), OracleModel(w, 256, head=False)
+    eng.fuse_conv = False  # (the B | C | x rows stay in eng.bcx)
     rng = np.random.default_rng(47)
     prompt = _prompt(rng, 9, s.vocab)
     token = int(eng.forward(prompt).cpu()[-1])
@@ -336,3 +337,48 @@ def test_lfm2_width_verify_layerwise_and_rollback(hip):
                                          before[i])
             assert np.array_equal(st.cpu().numpy(), want_state), (rnd, i, kept)
         token = int(rows[kept - 1])
+
+
+def test_lfm2_conv_epilogue_equals_gemv_then_conv(hip):
+    """The short convs in in_proj's epilogue against in_proj into the
+    B | C | x rows then the conv kernel (which the layerwise test above
+    checks against the oracle): the same logits, conv states and prefixes,
+    bit for bit, over a prompt, verify batches with rollback and decode
+    steps at LFM2-1.2B width."""
+    from webgllm_amd import engine as E
+    s = dataclasses.replace(E.LFM2_12B, layers=4, conv_layers=(0, 1, 3))
+    w = E.Weights(s, seed=5)
+    fused, plain = E.Engine(w, 256), E.Engine(w, 256)
+    plain.fuse_conv = False
+    rng = np.random.default_rng(9)
+    prompt = _prompt(rng, 11, s.vocab)
+
+    def same(step):
+        assert torch.equal(fused.logits[:5].view(torch.int32),
+                           plain.logits[:5].view(torch.int32)), step
+        for i in fused.state:
+            assert torch.equal(fused.state[i].view(torch.int32),
+                               plain.state[i].view(torch.int32)), (step, i)
+
+    ta, tb = fused.forward(prompt).cpu(), plain.forward(prompt).cpu()
+    assert torch.equal(ta, tb)
+    same("prompt")
+    token = int(ta[-1])
+    for step, kept in enumerate((1, 4, 2, 5, 3)):
+        drafts = _prompt(rng, 4, s.vocab)
+        ra = fused.forward([token] + drafts, draft=True).cpu()
+        rb = plain.forward([token] + drafts, draft=True).cpu()
+        assert torch.equal(ra, rb)
+        for i in fused.prefixes:
+            assert torch.equal(fused.prefixes[i][:5].view(torch.int32),
+                               plain.prefixes[i][:5].view(torch.int32)), (step, i)
+        same(step)
+        fused.accept(kept)
+        plain.accept(kept)
+        same((step, kept))
+        token = int(ra[kept - 1])
+    for step in range(3):
+        ta, tb = fused.forward([token]).cpu(), plain.forward([token]).cpu()
+        assert torch.equal(ta, tb)
+        same(("decode", step))
+        token = int(ta[-1])

@@ -115,11 +115,74 @@ __device__ inline void input_scales_wg(const wg_epilogue &e, float s[M], float *
 // The epilogue's operands of one row group that do not depend on its sums,
 // loaded ahead (with the row group's weights) so the epilogue does not wait
 // for memory: the residual and the next norm's weight (STORE), the rope
-// table entries of the lane's dim at its position (ROPE_KV).
+// table entries of the lane's dim at its position (ROPE_KV), the lane's
+// channel's taps and state (SHORT_CONV).
+constexpr int CONV_MAX_W = 4;
 struct EpiPre {
   float res, w16;
   float c1, s1, c2, s2;
+  float tp[CONV_MAX_W], st[CONV_MAX_W - 1];
 };
+
+// (SHORT_CONV) channel c's taps and state, for the lane's row r of a row
+// group of x rows.
+__device__ inline void conv_prefetch(const wg_epilogue &e, int c, int D, bool live, EpiPre &p) {
+  const int W = e.conv_width;
+#pragma unroll
+  for (int k = 0; k < CONV_MAX_W; k++) p.tp[k] = live && k < W ? e.conv_taps[(int64_t)c * W + k] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < CONV_MAX_W - 1; i++)
+    p.st[i] = live && i < W - 1 ? e.conv_state[(int64_t)i * D + c] : 0.0f;
+}
+
+// (SHORT_CONV) channel c's outputs for the lane's token m = lane % 16, from
+// its B, C and x sums (bv, cv, xv, final): y = B x, the window of the last W
+// y's from the lanes of the earlier tokens (lane - d) and the state, then
+// what short_conv_kernel computes, in its order. Every lane of the wave
+// takes part (the window's shuffles); `live`: the channel and token exist.
+__device__ inline void conv_finish(const wg_epilogue &e, int c, int D, int M, float bv, float cv,
+                                   float xv, bool live, const EpiPre &p) {
+  const int lane = threadIdx.x & 63, m = lane & 15;
+  const int W = e.conv_width;
+  const float y = bv * xv;
+  // y of token m - d, d < CONV_MAX_W, from the lane d lanes down (its own
+  // 16-lane group when m >= d)
+  float sh[CONV_MAX_W];
+  sh[0] = y;
+#pragma unroll
+  for (int d = 1; d < CONV_MAX_W; d++) sh[d] = __shfl(y, (lane - d) & 63, 64);
+  // the window: yw[k] = y of token t = m - (W - 1) + k; before the batch
+  // (t < 0) state row W - 1 + t = m + k, oldest first
+  float yw[CONV_MAX_W];
+#pragma unroll
+  for (int k = 0; k < CONV_MAX_W; k++) {
+    const int d = W - 1 - k;
+    float v = 0.0f;
+#pragma unroll
+    for (int dd = 0; dd < CONV_MAX_W; dd++)
+      if (dd == d) v = sh[dd];
+    if (m < d) {
+#pragma unroll
+      for (int i = 0; i < CONV_MAX_W - 1; i++)
+        if (i == m + k) v = p.st[i];
+    }
+    yw[k] = v;
+  }
+  float a = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CONV_MAX_W; k++)
+    if (k < W) a += p.tp[k] * yw[k];
+  if (!live) return;
+  e.out16[(int64_t)m * e.ld_out16 + c] = half_bits(cv * a);
+  if (e.conv_prefixes)  // the state after the first m + 1 tokens
+#pragma unroll
+    for (int i = 0; i < CONV_MAX_W - 1; i++)
+      if (i < W - 1) e.conv_prefixes[((int64_t)m * (W - 1) + i) * D + c] = yw[i + 1];
+  if (m == M - 1)
+#pragma unroll
+    for (int i = 0; i < CONV_MAX_W - 1; i++)
+      if (i < W - 1) e.conv_state_out[(int64_t)i * D + c] = yw[i + 1];
+}
 
 // The position the epilogue uses (ROPE_KV), read once per kernel.
 template <int MODE>

@@ -157,7 +157,8 @@ __global__ void f32_to_f16_kernel(const float *x, uint16_t *out, int64_t n) {
 int check_epilogue(const wg_q4_matrix *w, int M, const float *y, int ldy,
                           const wg_epilogue &e) {
   const int N = w->N, G = N / 4;
-  WG_REQUIRE(e.mode == WG_EPI_STORE || e.mode == WG_EPI_SWIGLU || e.mode == WG_EPI_ROPE_KV,
+  WG_REQUIRE(e.mode == WG_EPI_STORE || e.mode == WG_EPI_SWIGLU || e.mode == WG_EPI_ROPE_KV ||
+                 e.mode == WG_EPI_SHORT_CONV,
              "wg_q4_gemv: unknown epilogue mode %d", e.mode);
   if (e.norm_parts) {
     WG_REQUIRE(e.n_parts >= 1 && e.norm_count >= 1 && e.ld_parts_in >= e.n_parts &&
@@ -181,6 +182,19 @@ int check_epilogue(const wg_q4_matrix *w, int M, const float *y, int ldy,
     if (e.parts_out) WG_REQUIRE(e.ld_parts_out >= G, "wg_q4_gemv: parts stride too small");
   } else if (e.mode == WG_EPI_SWIGLU) {
     WG_REQUIRE(e.out16 && e.ld_out16 >= N / 2, "wg_q4_gemv: SwiGLU needs a half output of N/2");
+  } else if (e.mode == WG_EPI_SHORT_CONV) {
+    const int D = N / 3, W = e.conv_width;
+    WG_REQUIRE(N % 48 == 0, "wg_q4_gemv: short-conv epilogue: %d rows are not B | C | x of a "
+               "multiple of 16 channels", N);
+    WG_REQUIRE(W >= 2 && W <= 4, "wg_q4_gemv: short-conv epilogue: width %d (2 to 4)", W);
+    WG_REQUIRE(e.conv_taps && e.conv_state && e.conv_state_out && e.out16,
+               "wg_q4_gemv: short-conv epilogue: null pointer");
+    WG_REQUIRE(e.ld_out16 >= D, "wg_q4_gemv: short-conv epilogue: ld_out16 %d < %d channels",
+               e.ld_out16, D);
+    WG_REQUIRE(e.conv_state == e.conv_state_out ||
+                   !overlaps(e.conv_state, (size_t)(W - 1) * D * 4, e.conv_state_out,
+                             (size_t)(W - 1) * D * 4),
+               "wg_q4_gemv: short-conv epilogue: state and new state partly overlap");
   } else {
     const int hd = e.head_dim;
     WG_REQUIRE(e.kv_heads > 0 && e.heads % e.kv_heads == 0 && hd >= 4 && hd % 4 == 0,
@@ -222,6 +236,19 @@ int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx,
     WG_REQUIRE(!overlaps(x, (size_t)M * ldx * 2, e.out16, (size_t)M * e.ld_out16 * 2),
                "wg_q4_gemv: activations and half output overlap");
   hipStream_t s = as_stream(stream);
+  if (e.mode == WG_EPI_SHORT_CONV) {
+    // the kernels that take it: the MFMA and the streaming GEMVs
+    if (w->layout != WG_LAYOUT_ROWGROUP)
+      return fail(WG_ERR_UNSUPPORTED, "wg_q4_gemv: short-conv epilogue: 4-bit row groups only");
+    if ((rc = launch_gemv_mfma(w, x, M, ldx, y, ldy, e, s)) != -1) return rc;
+    if (M <= 2 && w->K <= 512 * 32) {
+      rc = M == 1 ? launch_stream_m<1>(w, x, ldx, y, ldy, e, s)
+                  : launch_stream_m<2>(w, x, ldx, y, ldy, e, s);
+      if (rc != -1) return rc;
+    }
+    if (M >= 3 && (rc = launch_gemv_few(w, x, M, ldx, y, ldy, e, s)) != -1) return rc;
+    return fail(WG_ERR_UNSUPPORTED, "wg_q4_gemv: short-conv epilogue: not for this shape");
+  }
   if (w->layout == WG_LAYOUT_Q4K) return launch_gemv_q4k(w, x, M, ldx, y, ldy, e, s);
   if (w->layout == WG_LAYOUT_Q8 || w->layout == WG_LAYOUT_Q6K)
     return launch_gemv_wide(w, x, M, ldx, y, ldy, e, s);

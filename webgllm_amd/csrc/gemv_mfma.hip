@@ -146,8 +146,19 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
   const int n = lane & 15, c = lane >> 4;
   const int bsel = c >> 1, h = c & 1;
   const int b0w = 2 * wave * NP;  // this wave's first block
-  const int NT = (G + 3) >> 2;
+  // SHORT_CONV: tile t holds the B, C and x row groups of channels 4 t ..
+  // 4 t + 3 (row groups t, t + G / 3, t + 2 G / 3) in its first 3 row
+  // groups; its 4th repeats the x row group's bytes (L2 hits, its sums
+  // unread). G / 3 tiles, each finished on its own: 4 times as many work
+  // units as tiles of whole row groups of one part would give.
+  constexpr bool CONV = MODE == WG_EPI_SHORT_CONV;
+  const int NT = CONV ? G / 3 : (G + 3) >> 2;
   const int ntiles = (NT - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  auto tile_of = [&](int i) { return (int)blockIdx.x + i * (int)gridDim.x; };
+  // row group q (0..3) of tile T
+  auto rg_of = [&](int T, int q) {
+    return CONV ? (uint32_t)(min(q, 2) * NT + T) : (uint32_t)min(4 * T + q, G - 1);
+  };
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
 
   // This lane's piece of each load: row group and byte offset within the
@@ -183,24 +194,24 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
   // past the last tile: a wait for an epilogue operand (the compiler's,
   // which does not see these loads and waits for all) would wait for it.
   auto issue = [&](int i) {
-    const int T = (int)blockIdx.x + i * (int)gridDim.x;
+    const int T = tile_of(i);
     const uint32_t live = ~0u;
     const uint32_t slot = sbase + (uint32_t)(((i % S) * KS + wave) * SL::BYTES);
 #pragma unroll
     for (int k = 0; k < SL::NQ; k++) {
-      const uint32_t g = (uint32_t)min(4 * T + qrg[k], G - 1);
+      const uint32_t g = rg_of(T, qrg[k]);
       dma16(quants, (g * (uint32_t)B * 64u + qoff[k]) & live, slot + k * 1024);
     }
 #pragma unroll
     for (int k = 0; k < SL::NS; k++) {
-      const uint32_t g = (uint32_t)min(4 * T + srg[k], G - 1);
+      const uint32_t g = rg_of(T, srg[k]);
       if (slive[k]) dma4(scales, (g * (uint32_t)B * 8u + soff[k]) & live, slot + SL::QB + k * 256);
     }
     if constexpr (SL::NZ > 0) {
       constexpr uint32_t ZPB = ZK == WG_ZERO_U8 ? 4 : 8;
 #pragma unroll
       for (int k = 0; k < SL::NZ; k++) {
-        const uint32_t g = (uint32_t)min(4 * T + zrg[k], G - 1);
+        const uint32_t g = rg_of(T, zrg[k]);
         if (zlive[k])
           dma4(zeros, (g * (uint32_t)B * ZPB + zoff[k]) & live, slot + SL::QB + SL::SB + k * 256);
       }
@@ -299,17 +310,23 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
   const int m = lane & 15;
   float my_scale = 0.0f;
   if (!deferred) my_scale = pick<8>(scale, m < 8 ? m : 0) * (SUB ? 0x1p24f : 1.0f);
+  const int D = 4 * NT;  // (SHORT_CONV) channels: 4 a tile
   for (int r0 = 0; r0 < ntiles; r0 += R) {
     const int rn = min(R, ntiles - r0);
+    // row groups to finish: every one, or a tile's channels (SHORT_CONV)
+    const int nfin = CONV ? rn : 4 * rn;
     // the round's epilogue operands, in flight under its tiles (waves w,
-    // w + KS, ... of its 4 rn row groups)
+    // w + KS, ... of its row groups to finish)
     EpiPre pe[RGF];
 #pragma unroll
     for (int f = 0; f < RGF; f++) {
       const int qg = wave + f * KS;
-      if (qg < 4 * rn)
-        epi_prefetch<8, MODE>(e, 4 * ((int)blockIdx.x + (r0 + qg / 4) * (int)gridDim.x) + (qg & 3),
-                              G, pos0, pe[f], M);
+      if constexpr (CONV) {
+        if (qg < nfin)
+          conv_prefetch(e, 4 * tile_of(r0 + qg) + ((lane >> 4) & 3), D, m < M, pe[f]);
+      } else if (qg < nfin) {
+        epi_prefetch<8, MODE>(e, 4 * tile_of(r0 + qg / 4) + (qg & 3), G, pos0, pe[f], M);
+      }
     }
     for (int i = r0; i < r0 + rn; i++) {
       // tile i's loads are done once at most the later tiles' are in flight
@@ -370,16 +387,25 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
 #pragma unroll
     for (int f = 0; f < RGF; f++) {
       const int qg = wave + f * KS;
-      if (qg < 4 * rn) {
-        const int t = qg / 4, jr = qg & 3;
-        // row 4 jr + r of token m sits at lane (4 jr + r) + 16 (m / 4), slot m % 4
+      if (qg < nfin) {
         const int r = (lane >> 4) & 3;
-        const int src = ((4 * jr + r) + 16 * ((m >> 2) & 1)) * 4 + (m & 3);
-        float v = 0.0f;
+        // row 4 jr + r of the round's tile t for token m: at lane (4 jr + r)
+        // + 16 (m / 4), slot m % 4
+        auto sum_of = [&](int t, int jr) {
+          const int src = ((4 * jr + r) + 16 * ((m >> 2) & 1)) * 4 + (m & 3);
+          float v = 0.0f;
 #pragma unroll
-        for (int w = 0; w < KS; w++) v += red[(t * KS + w) * 128 + src];
-        const int g = 4 * ((int)blockIdx.x + (r0 + t) * (int)gridDim.x) + jr;
-        finish_value<MODE>(e, g, v * my_scale, g < G && m < M, y, ldy, pe[f], pos0);
+          for (int w = 0; w < KS; w++) v += red[(t * KS + w) * 128 + src];
+          return v * my_scale;
+        };
+        if constexpr (CONV) {
+          conv_finish(e, 4 * tile_of(r0 + qg) + r, D, M, sum_of(qg, 0), sum_of(qg, 1),
+                      sum_of(qg, 2), m < M, pe[f]);
+        } else {
+          const int t = qg / 4, jr = qg & 3;
+          const int g = 4 * tile_of(r0 + t) + jr;
+          finish_value<MODE>(e, g, sum_of(t, jr), g < G && m < M, y, ldy, pe[f], pos0);
+        }
       }
     }
     barrier();  // the sums are read before the next round writes them
@@ -393,7 +419,9 @@ int launch_mfma(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float 
   constexpr size_t LDS =
       (size_t)S * KS * Slot<ZK, NP>::BYTES + mfma_round<ZK, NP, KS, S>() * KS * 128 * 4;
   static_assert(LDS + KS * 32 <= 160 * 1024, "LDS");
-  const int grid = persistent_grid(NT, tuning("gemv_mfma_wg_per_cu"));
+  // (SHORT_CONV: a tile a channel quad)
+  const int grid = persistent_grid(e.mode == WG_EPI_SHORT_CONV ? G / 3 : NT,
+                                   tuning("gemv_mfma_wg_per_cu"));
   auto q = (const uint8_t *)w->quants;
   auto sc = (const uint16_t *)w->scales;
 #define WG_MFMA_LAUNCH(MODE)                                                                    \
@@ -405,7 +433,8 @@ int launch_mfma(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float 
     gemv_mfma_kernel<ZK, NP, KS, S, MODE>                                                      \
         <<<grid, KS * 64, LDS, s>>>(q, sc, w->zeros, x, G, B, ldx, M, y, ldy, e);              \
   } while (0)
-  if (e.mode == WG_EPI_SWIGLU) WG_MFMA_LAUNCH(WG_EPI_SWIGLU);
+  if (e.mode == WG_EPI_SHORT_CONV) WG_MFMA_LAUNCH(WG_EPI_SHORT_CONV);
+  else if (e.mode == WG_EPI_SWIGLU) WG_MFMA_LAUNCH(WG_EPI_SWIGLU);
   else if (e.mode == WG_EPI_ROPE_KV) WG_MFMA_LAUNCH(WG_EPI_ROPE_KV);
   else WG_MFMA_LAUNCH(WG_EPI_STORE);
 #undef WG_MFMA_LAUNCH

@@ -83,8 +83,9 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
   float scale[M];
   input_scales_wg<M, 4>(e, scale, nred);
 
-  // one row group: the 4 rows' sums for each token, reduced, then the epilogue
-  auto step = [&](const Unit<ZK, NB> &u, int g, int it, const EpiPre &pe) {
+  // one row group: the 4 rows' sums for each token, reduced (into part 0's
+  // lanes' tot)
+  auto sums = [&](const Unit<ZK, NB> &u, int it, float (&tot)[M]) {
     float acc[4][M];
 #pragma unroll
     for (int r = 0; r < 4; r++)
@@ -92,7 +93,6 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
       for (int m = 0; m < M; m++) acc[r][m] = 0.0f;
     accumulate_unit_paired<M, ZK, NB>(u, a, sa, live, acc);
     const int row = wave_sum4_row();
-    float tot[M];
 #pragma unroll
     for (int m = 0; m < M; m++) tot[m] = wave_sum4(acc[0][m], acc[1][m], acc[2][m], acc[3][m]);
     if constexpr (KS > 1) {
@@ -108,6 +108,54 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
 #pragma unroll
           for (int p = 1; p < KS; p++) tot[m] += red[it][wave + p][row * M + m];
     }
+  };
+
+  if constexpr (MODE == WG_EPI_SHORT_CONV) {
+    // The slot's steps walk triples of row groups, the B, C and x rows of
+    // the same 4 channels (part k % 3 of triple t = blockIdx RGW + slot +
+    // (k / 3) stride, a row group of each part holding 4 channels): the B
+    // and C sums wait in registers for the x step, which convolves.
+    const int T = G / 3, D = 4 * T;
+    auto rg = [&](int k) {
+      const int t = (int)blockIdx.x * RGW + slot + (k / 3) * stride;
+      return t < T ? (k % 3) * T + t : G;
+    };
+    auto base = [&](int k) { return (int)blockIdx.x * RGW + (k / 3) * stride; };  // uniform
+    const int r = (lane >> 4) & 3, m = lane & 15, mm = m < M ? m : 0;
+    float bv = 0.0f, cv = 0.0f;
+    EpiPre cp = {};
+    auto conv_step = [&](const Unit<ZK, NB> &u, int k, int it) {
+      float tot[M];
+      sums(u, it, tot);
+      if (part == 0) {
+        const float v = pick<M>(tot, mm) * 0x1p24f * pick<M>(scale, mm);
+        const int g = rg(k);
+        const int c = 4 * (g - (k % 3) * T) + r;  // the lane's channel (g < G)
+        const bool live = g < G && m < M;
+        if (k % 3 == 0) {
+          bv = v;
+          conv_prefetch(e, c, D, live, cp);
+        } else if (k % 3 == 1) {
+          cv = v;
+        } else {
+          conv_finish(e, c, D, M, bv, cv, v, live, cp);
+        }
+      }
+    };
+    // U0 holds step 0's row group (g_first)
+    for (int k = 0; base(k) < T; k += 2) {
+      load_unit_at<ZK, NB>(U1, quants, scales, zeros, min(rg(k + 1), G - 1), B, bj);
+      conv_step(U0, k, 0);
+      if (base(k + 1) >= T) break;
+      load_unit_at<ZK, NB>(U0, quants, scales, zeros, min(rg(k + 2), G - 1), B, bj);
+      conv_step(U1, k + 1, 1);
+    }
+    return;
+  }
+
+  auto step = [&](const Unit<ZK, NB> &u, int g, int it, const EpiPre &pe) {
+    float tot[M];
+    sums(u, it, tot);
     if (part == 0) finish<M, MODE>(e, g, G, tot, scale, y, ldy, pe, pos0);
   };
 
@@ -138,7 +186,12 @@ int launch_stream(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, i
   int grid = persistent_grid((G + RGW - 1) / RGW, tuning(knob));
   auto q = (const uint4 *)w->quants;
   auto sc = (const uint16_t *)w->scales;
-  if (e.mode == WG_EPI_SWIGLU)
+  if (e.mode == WG_EPI_SHORT_CONV) {
+    // a slot takes triples of row groups: G / 3 of them
+    grid = persistent_grid((G / 3 + RGW - 1) / RGW, tuning(knob));
+    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_SHORT_CONV><<<grid, 256, 0, s>>>(
+        q, sc, w->zeros, x, G, B, ldx, y, ldy, e);
+  } else if (e.mode == WG_EPI_SWIGLU)
     gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_SWIGLU><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, G, B, ldx,
                                                                          y, ldy, e);
   else if (e.mode == WG_EPI_ROPE_KV)

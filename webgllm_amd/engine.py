@@ -274,6 +274,8 @@ class Engine:
         # (q rows, output rows)) after each attention, ("output", h rows)
         # after the last layer; the self-check reads them back
         self.probe = None
+        # short convs in in_proj's epilogue (False: in_proj, then the conv)
+        self.fuse_conv = True
 
     # --- the attention caches, grown on demand ------------------------------
     def reserve(self, end: int) -> None:
@@ -375,12 +377,22 @@ class Engine:
         D, F = s.hidden, s.intermediate
         h, x16 = self.h[:M], self.x16[:M]
         if s.layer_type(i) == "conv":
-            bcx = self.bcx[:M]
-            ops.gemv(lw["in_proj"], x16, out=bcx,
-                     epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
             c16 = self.c16[:M]
-            ops.short_conv(bcx, D, s.conv_kernel, lw["taps"], self.state[i],
-                           prefixes=self.prefixes[i][:M] if keep_prefixes else None, out=c16)
+            prefixes = self.prefixes[i][:M] if keep_prefixes else None
+            # the convolution in in_proj's epilogue where the library takes
+            # it, else in_proj into the B | C | x rows, then the conv
+            fused = self.fuse_conv and ops.gemv_short_conv(lw["in_proj"], x16, self._norm_in(
+                L.Epilogue(mode=L.EPI_SHORT_CONV, out16=c16.data_ptr(), ld_out16=D,
+                           conv_taps=lw["taps"].data_ptr(), conv_state=self.state[i].data_ptr(),
+                           conv_state_out=self.state[i].data_ptr(),
+                           conv_prefixes=prefixes.data_ptr() if prefixes is not None else None,
+                           conv_width=s.conv_kernel)))
+            if not fused:
+                bcx = self.bcx[:M]
+                ops.gemv(lw["in_proj"], x16, out=bcx,
+                         epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
+                ops.short_conv(bcx, D, s.conv_kernel, lw["taps"], self.state[i],
+                               prefixes=prefixes, out=c16)
             ops.gemv(lw["out_proj"], c16, out=h, epilogue=self._residual_out(M, lw["ffn_norm"]))
         else:
             if s.rope_in_epilogue:

@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libwebgllm_hip.so")
 HEADER = os.path.join(os.path.dirname(_HERE), "include", "webgllm_hip.h")
 
 WG_OK = 0
+ERR_UNSUPPORTED = -6
 STATUS = {-1: "invalid", -2: "out-of-memory", -3: "device", -4: "aliased", -5: "disposed",
           -6: "unsupported"}
 
@@ -36,7 +37,7 @@ class Q4MatrixDesc(C.Structure):
                 ("quants", C.c_void_p), ("scales", C.c_void_p), ("zeros", C.c_void_p)]
 
 
-EPI_STORE, EPI_SWIGLU, EPI_ROPE_KV = 0, 1, 2
+EPI_STORE, EPI_SWIGLU, EPI_ROPE_KV, EPI_SHORT_CONV = 0, 1, 2, 3
 
 
 class ConvState(C.Structure):
@@ -59,7 +60,10 @@ class Epilogue(C.Structure):
                 ("ctx", C.c_int32), ("rope_rows", C.c_int32),
                 ("rope", C.c_void_p), ("pos0", C.c_void_p),
                 ("q_out", C.c_void_p), ("ld_q_out", C.c_int32),
-                ("k_cache", C.c_void_p), ("v_cache", C.c_void_p)]
+                ("k_cache", C.c_void_p), ("v_cache", C.c_void_p),
+                ("conv_taps", C.c_void_p), ("conv_state", C.c_void_p),
+                ("conv_state_out", C.c_void_p), ("conv_prefixes", C.c_void_p),
+                ("conv_width", C.c_int32)]
 
 
 class AttnShape(C.Structure):

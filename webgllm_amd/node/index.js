@@ -283,7 +283,11 @@ class HipGpu {
       /**
        * splitPartials + pf and the passes folded into it (src/engine.ts:5241-5377,
        * src/gpu/kernels.ts:744-895, :1169-1361): y = x W^T for M <= 8 rows of
-       * halves, with an epilogue (mode EPI_STORE | EPI_SWIGLU | EPI_ROPE_KV).
+       * halves, with an epilogue (mode EPI_STORE | EPI_SWIGLU | EPI_ROPE_KV |
+       * EPI_SHORT_CONV: the short conv of convFused over the B | C | x rows,
+       * src/gpu/kernels.ts:1447-1523, into out16, convState(Out) and
+       * convPrefixes; it throws WG_ERR_UNSUPPORTED for a layout or shape its
+       * kernels do not take, where gemv with EPI_STORE and shortConv follow).
        */
       gemv: (w, x, M, y, epilogue = null, ldx = null, ldy = null) =>
         call(addon.gemv, ctx, matrix(w), o(x), M, o(y), operands(epilogue), ldx, ldy),

@@ -679,6 +679,7 @@ static int read_epilogue(napi_env env, napi_value o, int32_t M, int32_t N, wg_ep
       {"ctx", offsetof(wg_epilogue, ctx)},
       {"ropeRows", offsetof(wg_epilogue, rope_rows)},
       {"ldQOut", offsetof(wg_epilogue, ld_q_out)},
+      {"convWidth", offsetof(wg_epilogue, conv_width)},
   };
   for (size_t k = 0; k < sizeof ints / sizeof ints[0]; k++)
     if (!prop_i32(env, o, ints[k].key, (int32_t *)((char *)e + ints[k].at))) return 0;
@@ -686,7 +687,11 @@ static int read_epilogue(napi_env env, napi_value o, int32_t M, int32_t N, wg_ep
       !prop_f32(env, o, "normMultOut", &e->norm_mult_out))
     return 0;
   const int64_t hd = e->head_dim;
-  const uint64_t out16_width = e->mode == WG_EPI_SWIGLU ? (uint64_t)N / 2 : (uint64_t)N;
+  const uint64_t out16_width = e->mode == WG_EPI_SWIGLU      ? (uint64_t)N / 2
+                               : e->mode == WG_EPI_SHORT_CONV ? (uint64_t)N / 3
+                                                              : (uint64_t)N;
+  /* (short conv) channels and width */
+  const uint64_t cd = (uint64_t)N / 3, cw = (uint64_t)(e->conv_width > 1 ? e->conv_width : 1);
   const uint64_t cache = (uint64_t)(e->ctx > 0 ? e->ctx : 0) * (uint64_t)(e->kv_heads > 0 ? e->kv_heads : 0) *
                          (uint64_t)(hd > 0 ? hd : 0) * 2;
   const struct {
@@ -705,6 +710,10 @@ static int read_epilogue(napi_env env, napi_value o, int32_t M, int32_t N, wg_ep
       {"qOut", (void **)&e->q_out, span(M, e->ld_q_out, (int64_t)e->heads * hd) * 4},
       {"kCache", (void **)&e->k_cache, cache},
       {"vCache", (void **)&e->v_cache, cache},
+      {"convTaps", (void **)&e->conv_taps, cd * cw * 4},
+      {"convState", (void **)&e->conv_state, cd * (cw - 1) * 4},
+      {"convStateOut", (void **)&e->conv_state_out, cd * (cw - 1) * 4},
+      {"convPrefixes", (void **)&e->conv_prefixes, (uint64_t)M * (cw - 1) * cd * 4},
   };
   for (size_t k = 0; k < sizeof ptrs / sizeof ptrs[0]; k++)
     if (!prop_operand(env, o, ptrs[k].key, ptrs[k].need, 1, ptrs[k].at)) return 0;
@@ -1431,6 +1440,7 @@ static napi_value init(napi_env env, napi_value exports) {
   set(env, consts, "EPI_STORE", num(env, WG_EPI_STORE));
   set(env, consts, "EPI_SWIGLU", num(env, WG_EPI_SWIGLU));
   set(env, consts, "EPI_ROPE_KV", num(env, WG_EPI_ROPE_KV));
+  set(env, consts, "EPI_SHORT_CONV", num(env, WG_EPI_SHORT_CONV));
   set(env, consts, "CONV_STATE_BYTES", num(env, (double)sizeof(wg_conv_state)));
   set(env, exports, "constants", consts);
   return exports;

@@ -185,6 +185,23 @@ def gemv(m: Q4Matrix, x16: torch.Tensor, out: torch.Tensor | None = None,
     return out
 
 
+def gemv_short_conv(m: Q4Matrix, x16: torch.Tensor, epilogue: "L.Epilogue") -> bool:
+    """The in_proj GEMV of a short conv with the convolution in its epilogue
+    (epilogue.mode = EPI_SHORT_CONV). Returns False, having launched
+    nothing, where the library's kernels do not take the shape (the caller
+    then runs gemv() into the B | C | x rows and short_conv())."""
+    if x16.dtype not in (torch.float16, torch.int16):
+        raise ValueError("activations must be halves")
+    x16 = _dev(x16)
+    M = x16.shape[0] if x16.dim() == 2 else 1
+    rc = L.load().wg_q4_gemv(C.byref(m.desc), _p(x16), M, x16.shape[-1], None, 0,
+                             C.byref(epilogue), _stream())
+    if rc == L.ERR_UNSUPPORTED:
+        return False
+    L.check(rc)
+    return True
+
+
 def gemm(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
          residual: torch.Tensor | None = None, col_of: torch.Tensor | None = None,
          row_scale: torch.Tensor | None = None) -> torch.Tensor:
