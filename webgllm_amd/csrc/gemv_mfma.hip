@@ -451,7 +451,9 @@ int launch_mfma_k(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, floa
   if (P <= 8) return launch_mfma<ZK, 2, 4, 4>(w, x, M, ldx, y, ldy, e, s);
   if (P <= 16) return np <= 2 ? launch_mfma<ZK, 2, 8, 4>(w, x, M, ldx, y, ldy, e, s)
                               : launch_mfma<ZK, 4, 4, 4>(w, x, M, ldx, y, ldy, e, s);
-  if (P <= 32) return np <= 4 ? launch_mfma<ZK, 4, 8, 3>(w, x, M, ldx, y, ldy, e, s)
+  // (8 waves of 4 pairs: a 2-stage ring, measured faster than 3 to 6 stages
+  // on every 2048-deep matrix from 2048 to 65536 rows at 3, 5 and 8 tokens)
+  if (P <= 32) return np <= 4 ? launch_mfma<ZK, 4, 8, 2>(w, x, M, ldx, y, ldy, e, s)
                               : launch_mfma<ZK, 8, 4, 3>(w, x, M, ldx, y, ldy, e, s);
   if (P <= 64) return np <= 4 ? launch_mfma<ZK, 4, 16, 3>(w, x, M, ldx, y, ldy, e, s)
                               : launch_mfma<ZK, 8, 8, 3>(w, x, M, ldx, y, ldy, e, s);
