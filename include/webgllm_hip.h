@@ -367,6 +367,15 @@ int wg_q4_dequant(const wg_q4_matrix *m, int32_t row0, int32_t rows, float *out,
  *    row-group matrices (one to eight tokens); elsewhere the
  *    call returns WG_ERR_UNSUPPORTED and the caller makes the two calls
  *    (LFM2's convolve: src/engine.ts:5806-5899, src/gpu/kernels.ts:1447-1523). */
+/* With pick_parts (WG_EPI_STORE, no residual; the head GEMV), the GEMV also
+ * runs CHUNK_MAX_AT's reduction (src/gpu/kernels.ts:3169-3205) over the
+ * values it stores: each workgroup's (largest value, lowest row holding it)
+ * of every row m (strict > from -3e38, so NaN never enters), into
+ * pick_parts (wg_pick_parts_bytes(M), 16-byte aligned); wg_argmax_parts then
+ * finishes the pick from them, reading no logit again. The 4-bit row-group
+ * GEMVs (MFMA and streaming) take it; elsewhere the call returns
+ * WG_ERR_UNSUPPORTED having launched nothing (then wg_q4_gemv without it
+ * and wg_argmax_rows over y). */
 #define WG_EPI_STORE 0
 #define WG_EPI_SWIGLU 1
 #define WG_EPI_ROPE_KV 2
@@ -402,6 +411,8 @@ typedef struct {
   float *conv_state_out;
   float *conv_prefixes;
   int32_t conv_width;
+  /* WG_EPI_STORE without residual: the greedy pick's first stage */
+  void *pick_parts;
 } wg_epilogue;
 
 /* Decode / few-token GEMV (matmulSplitRgba4 and the split matmul,
@@ -683,6 +694,16 @@ int wg_argmax_rows(const float *logits, int32_t M, int32_t V, int32_t ld, int32_
 int wg_argmax_advance(const float *logits, int32_t V, int32_t *ids, int32_t *pos, int32_t *hist,
                       int32_t hist_len, float *tops, void *scratch, size_t scratch_bytes,
                       void *stream);
+
+/* The pick finished from a head GEMV's pick_parts (see wg_epilogue): ids[m]
+ * and tops[m] (or NULL) as wg_argmax_rows gives them over the GEMV's y,
+ * bit for bit. With pos (M = 1), the advance of wg_argmax_advance as well.
+ * One launch; for one decode step the GEMV's own reduction replaces
+ * wg_argmax_advance's first. */
+#define WG_PICK_SLOTS 4096 /* workgroups a GEMV may write parts for */
+size_t wg_pick_parts_bytes(int32_t M);
+int wg_argmax_parts(const void *pick_parts, int32_t M, int32_t *ids, float *tops, int32_t *pos,
+                    int32_t *hist, int32_t hist_len, void *stream);
 
 /* -------------------------------------------------- sampling candidates */
 

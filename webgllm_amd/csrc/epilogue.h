@@ -5,6 +5,7 @@
 
 #include "common.h"
 #include "dot.h"
+#include "pick_core.h"
 
 namespace wg {
 
@@ -314,6 +315,33 @@ __device__ inline void finish_value(const wg_epilogue &e, int g, float v, bool l
       e.v_cache[(int64_t)pos * kd + dv] = half_bits(v);
     }
   }
+}
+
+// (pick_parts) Row n's stored value v of the lane's token into the lane's
+// running best: only values above the scan's floor enter (NaN never does).
+__device__ inline void pick_take(PickBest &b, float v, int n, bool live) {
+  if (live && v > PICK_FLOOR) b = pick_better(b, PickBest{v, n});
+}
+
+// (pick_parts) The workgroup's best of every token into its slot: the lanes
+// of a token (lane % 16, rows lane / 16 % 4) merged by swaps, then the W
+// waves through LDS. Every thread of the workgroup calls it.
+template <int W>
+__device__ inline void pick_flush(const wg_epilogue &e, PickBest b, int M,
+                                  PickBest (&lds)[W][16]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  b = pick_xor(b, 16);
+  b = pick_xor(b, 32);
+  if (lane < 16) lds[wave][lane] = b;
+  __syncthreads();
+  if (wave == 0 && lane < M) {
+    PickBest t = lds[0][lane];
+#pragma unroll
+    for (int w = 1; w < W; w++) t = pick_better(t, lds[w][lane]);
+    auto *parts = reinterpret_cast<PickBest *>(static_cast<char *>(e.pick_parts) + PICK_HEADER);
+    parts[(int64_t)lane * WG_PICK_SLOTS + blockIdx.x] = t;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) *static_cast<int *>(e.pick_parts) = (int)gridDim.x;
 }
 
 }  // namespace wg

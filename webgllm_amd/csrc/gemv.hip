@@ -165,6 +165,12 @@ int check_epilogue(const wg_q4_matrix *w, int M, const float *y, int ldy,
                    e.norm_mult != 0.0f,
                "wg_q4_gemv: input norm needs parts, their count and a prescale");
   }
+  if (e.pick_parts) {
+    WG_REQUIRE(e.mode == WG_EPI_STORE && !e.residual,
+               "wg_q4_gemv: the pick's parts come from a plain store (no residual)");
+    WG_REQUIRE(((uintptr_t)e.pick_parts & 15) == 0,
+               "wg_q4_gemv: the pick's parts must be 16-byte aligned");
+  }
   if (e.mode == WG_EPI_STORE) {
     WG_REQUIRE(y, "wg_q4_gemv: no output");
     WG_REQUIRE(ldy >= N, "wg_q4_gemv: ldy %d < N %d", ldy, N);
@@ -249,6 +255,9 @@ int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx,
     if (M >= 3 && (rc = launch_gemv_few(w, x, M, ldx, y, ldy, e, s)) != -1) return rc;
     return fail(WG_ERR_UNSUPPORTED, "wg_q4_gemv: short-conv epilogue: not for this shape");
   }
+  // (the pick's first stage: the MFMA and the streaming GEMVs)
+  if (e.pick_parts && w->layout != WG_LAYOUT_ROWGROUP)
+    return fail(WG_ERR_UNSUPPORTED, "wg_q4_gemv: the pick's parts: 4-bit row groups only");
   if (w->layout == WG_LAYOUT_Q4K) return launch_gemv_q4k(w, x, M, ldx, y, ldy, e, s);
   if (w->layout == WG_LAYOUT_Q8 || w->layout == WG_LAYOUT_Q6K)
     return launch_gemv_wide(w, x, M, ldx, y, ldy, e, s);
@@ -262,6 +271,8 @@ int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx,
     rc = launch_gemv_few(w, x, M, ldx, y, ldy, e, s);
     if (rc != -1) return rc;
   }
+  if (e.pick_parts)
+    return fail(WG_ERR_UNSUPPORTED, "wg_q4_gemv: the pick's parts: not for this shape");
   switch (M) {
     case 1: return launch_gemv_m<1>(w, x, ldx, y, ldy, e, s);
     case 2: return launch_gemv_m<2>(w, x, ldx, y, ldy, e, s);

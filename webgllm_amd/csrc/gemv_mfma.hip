@@ -119,7 +119,8 @@ struct Slot {
 // 8, as many as the LDS left by the ring holds (512 bytes a wave a tile).
 template <int ZK, int NP, int KS, int S>
 constexpr int mfma_round() {
-  constexpr int ring = S * KS * Slot<ZK, NP>::BYTES, spare = 160 * 1024 - ring - KS * 32;
+  // (KS * 32: the norm's sums; KS * 128: the pick's parts)
+  constexpr int ring = S * KS * Slot<ZK, NP>::BYTES, spare = 160 * 1024 - ring - KS * 160;
   constexpr int r = spare / (KS * 512);
   static_assert(r >= 1, "LDS");
   return r < 8 ? r : 8;
@@ -141,6 +142,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
   extern __shared__ __align__(16) unsigned char smem[];
   float *red = reinterpret_cast<float *>(smem + S * KS * SL::BYTES);  // [R][KS][128]
   __shared__ float nred[KS * 8];
+  __shared__ PickBest pick_lds[MODE == WG_EPI_STORE ? KS : 1][16];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, c = lane >> 4;
@@ -311,6 +313,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
   float my_scale = 0.0f;
   if (!deferred) my_scale = pick<8>(scale, m < 8 ? m : 0) * (SUB ? 0x1p24f : 1.0f);
   const int D = 4 * NT;  // (SHORT_CONV) channels: 4 a tile
+  PickBest pbest{PICK_FLOOR, PICK_NONE};  // (pick_parts) this lane's token's best row
   for (int r0 = 0; r0 < ntiles; r0 += R) {
     const int rn = min(R, ntiles - r0);
     // row groups to finish: every one, or a tile's channels (SHORT_CONV)
@@ -404,12 +407,17 @@ __global__ __launch_bounds__(KS * 64) void gemv_mfma_kernel(
         } else {
           const int t = qg / 4, jr = qg & 3;
           const int g = 4 * tile_of(r0 + t) + jr;
-          finish_value<MODE>(e, g, sum_of(t, jr), g < G && m < M, y, ldy, pe[f], pos0);
+          const float val = sum_of(t, jr);
+          finish_value<MODE>(e, g, val, g < G && m < M, y, ldy, pe[f], pos0);
+          if constexpr (MODE == WG_EPI_STORE)
+            if (e.pick_parts) pick_take(pbest, val, 4 * g + r, g < G && m < M);
         }
       }
     }
     barrier();  // the sums are read before the next round writes them
   }
+  if constexpr (MODE == WG_EPI_STORE)
+    if (e.pick_parts) pick_flush<KS>(e, pbest, M, pick_lds);
 }
 
 template <int ZK, int NP, int KS, int S>
@@ -418,10 +426,12 @@ int launch_mfma(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float 
   const int G = w->N / 4, B = w->K / 32, NT = (G + 3) / 4;
   constexpr size_t LDS =
       (size_t)S * KS * Slot<ZK, NP>::BYTES + mfma_round<ZK, NP, KS, S>() * KS * 128 * 4;
-  static_assert(LDS + KS * 32 <= 160 * 1024, "LDS");
+  static_assert(LDS + KS * 160 <= 160 * 1024, "LDS");
   // (SHORT_CONV: a tile a channel quad)
   const int grid = persistent_grid(e.mode == WG_EPI_SHORT_CONV ? G / 3 : NT,
                                    tuning("gemv_mfma_wg_per_cu"));
+  if (e.pick_parts && grid > WG_PICK_SLOTS)
+    return fail(WG_ERR_UNSUPPORTED, "wg_q4_gemv: %d workgroups for the pick's parts", grid);
   auto q = (const uint8_t *)w->quants;
   auto sc = (const uint16_t *)w->scales;
 #define WG_MFMA_LAUNCH(MODE)                                                                    \

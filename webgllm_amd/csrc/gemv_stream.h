@@ -35,6 +35,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
   constexpr int RGW = 4 / KS;  // row groups a workgroup takes at a time
   __shared__ float red[2][4][4 * M];
   __shared__ float nred[4 * M];
+  __shared__ PickBest pick_lds[MODE == WG_EPI_STORE ? 4 : 1][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int part = wave % KS, slot = wave / KS;
   const int BP = (B + KS - 1) / KS;
@@ -153,10 +154,19 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
     return;
   }
 
+  PickBest pbest{PICK_FLOOR, PICK_NONE};  // (pick_parts) this lane's token's best row
   auto step = [&](const Unit<ZK, NB> &u, int g, int it, const EpiPre &pe) {
     float tot[M];
     sums(u, it, tot);
-    if (part == 0) finish<M, MODE>(e, g, G, tot, scale, y, ldy, pe, pos0);
+    if (part == 0) {
+      finish<M, MODE>(e, g, G, tot, scale, y, ldy, pe, pos0);
+      if constexpr (MODE == WG_EPI_STORE)
+        if (e.pick_parts) {  // the value finish stored (no residual)
+          const int m = lane & 15, mm = m < M ? m : 0;
+          const float v = pick<M>(tot, mm) * 0x1p24f * pick<M>(scale, mm);
+          pick_take(pbest, v, 4 * g + ((lane >> 4) & 3), g < G && m < M);
+        }
+    }
   };
 
   // g0 is the same for every wave of the workgroup, so all of them run the
@@ -172,6 +182,8 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
     if (part == 0) epi_prefetch<M, MODE>(e, g + 2 * stride, G, pos0, pnext);
     step(U1, g + stride, 1, pe);
   }
+  if constexpr (MODE == WG_EPI_STORE)
+    if (e.pick_parts) pick_flush<4>(e, pbest, M, pick_lds);
 }
 
 template <int M, int ZK, int NB, int KS>
@@ -186,6 +198,8 @@ int launch_stream(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, i
   int grid = persistent_grid((G + RGW - 1) / RGW, tuning(knob));
   auto q = (const uint4 *)w->quants;
   auto sc = (const uint16_t *)w->scales;
+  if (e.pick_parts && grid > WG_PICK_SLOTS)
+    return fail(WG_ERR_UNSUPPORTED, "wg_q4_gemv: %d workgroups for the pick's parts", grid);
   if (e.mode == WG_EPI_SHORT_CONV) {
     // a slot takes triples of row groups: G / 3 of them
     grid = persistent_grid((G / 3 + RGW - 1) / RGW, tuning(knob));

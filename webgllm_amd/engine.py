@@ -252,6 +252,10 @@ class Engine:
         self.tops = torch.zeros(R, dtype=f32, device=dev)
         self.argmax_scratch = torch.empty(L.load().wg_argmax_scratch_bytes(R, s.vocab),
                                           dtype=torch.uint8, device=dev)
+        # the head GEMV's share of the greedy pick (False: the GEMV, then the
+        # two-stage pick over the logits)
+        self.pick_parts = ops.pick_parts(R, device=dev)
+        self.fuse_pick = True
         self.attn = ops.attn_shape(s.heads, s.kv_heads, s.head_dim, s.head_dim, s.eps, s.qk_norm)
         self.rope = _rope_table(s.rope_theta, s.head_dim, ctx).to(dev)
         self.k_cache, self.v_cache, self.state, self.prefixes = {}, {}, {}, {}
@@ -346,10 +350,10 @@ class Engine:
         w = self.w
         return w.layers[i + 1]["op_norm"] if i + 1 < len(w.layers) else w.final_norm
 
-    def _forward_rows(self, M: int, keep_prefixes: bool, pick: bool = True) -> None:
+    def _forward_rows(self, M: int, keep_prefixes: bool, pick=True) -> None:
         """Enqueue one batch of M rows (ids[:M] at positions pos..pos+M-1);
         the greedy picks into next_ids unless `pick` is False (the caller
-        picks)."""
+        picks), or "advance" (see _head_rows)."""
         self._embed_rows(M)
         if self.probe:
             self.probe(-1, "embedding", self.h[:M])
@@ -416,13 +420,25 @@ class Engine:
         ops.gemv(lw["down"], self.ff16[:M], out=h,
                  epilogue=self._residual_out(M, self._next_norm(i)))
 
-    def _head_rows(self, M: int, pick: bool = True) -> None:
+    def _head_rows(self, M: int, pick=True) -> None:
         """Logits of the batch's rows over the tied embedding; the greedy
-        picks into next_ids when `pick`."""
-        ops.gemv(self.w.embedding, self.x16[:M], out=self.logits[:M],
-                 epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
-        if pick:
-            ops.argmax_rows(self.logits[:M], ids=self.next_ids[:M], tops=self.tops[:M],
+        picks into next_ids when `pick`, or (pick "advance", one row) the
+        decode step's pick and advance (ids[0], hist, pos)."""
+        emb, x16, logits = self.w.embedding, self.x16[:M], self.logits[:M]
+        if pick and self.fuse_pick and ops.gemv_pick(
+                emb, x16, logits, self.pick_parts, self._norm_in(L.Epilogue(mode=L.EPI_STORE))):
+            if pick == "advance":
+                ops.argmax_parts(self.pick_parts, 1, self.ids, tops=self.tops[:1],
+                                 pos=self.pos, hist=self.hist)
+            else:
+                ops.argmax_parts(self.pick_parts, M, self.next_ids[:M], tops=self.tops[:M])
+            return
+        ops.gemv(emb, x16, out=logits, epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
+        if pick == "advance":
+            ops.argmax_advance(self.logits[0], self.ids, self.pos, hist=self.hist,
+                               tops=self.tops[:1], scratch=self.argmax_scratch)
+        elif pick:
+            ops.argmax_rows(logits, ids=self.next_ids[:M], tops=self.tops[:M],
                             scratch=self.argmax_scratch)
 
     # --- prompt batches on MFMA ----------------------------------------------
@@ -614,9 +630,7 @@ class Engine:
     def _step_body(self) -> None:
         # the pick goes to ids[0] and hist[pos + 1], then pos += 1: the next
         # replay runs the picked token at the next position
-        self._forward_rows(1, keep_prefixes=False, pick=False)
-        ops.argmax_advance(self.logits[0], self.ids, self.pos, hist=self.hist,
-                           tops=self.tops[:1], scratch=self.argmax_scratch)
+        self._forward_rows(1, keep_prefixes=False, pick="advance")
 
     def _save(self):
         return (self.ids.clone(), self.pos.clone(), {i: s.clone() for i, s in self.state.items()})

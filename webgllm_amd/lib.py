@@ -63,7 +63,7 @@ class Epilogue(C.Structure):
                 ("k_cache", C.c_void_p), ("v_cache", C.c_void_p),
                 ("conv_taps", C.c_void_p), ("conv_state", C.c_void_p),
                 ("conv_state_out", C.c_void_p), ("conv_prefixes", C.c_void_p),
-                ("conv_width", C.c_int32)]
+                ("conv_width", C.c_int32), ("pick_parts", C.c_void_p)]
 
 
 class AttnShape(C.Structure):
@@ -201,6 +201,8 @@ def load():
         "wg_argmax_scratch_bytes": (SZ, [I32, I32]),
         "wg_argmax_rows": (C.c_int, [P, I32, I32, I32, P, P, P, SZ, P]),
         "wg_argmax_advance": (C.c_int, [P, I32, P, P, P, I32, P, P, SZ, P]),
+        "wg_pick_parts_bytes": (SZ, [I32]),
+        "wg_argmax_parts": (C.c_int, [P, I32, P, P, P, P, I32, P]),
         "wg_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
         "wg_gguf_close": (C.c_int, [P]),
         "wg_gguf_version": (I32, [P]),

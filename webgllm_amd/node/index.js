@@ -339,6 +339,15 @@ class HipGpu {
       /** One decode step's pick and advance on the device (src/engine.ts:8095-8110, :8318-8336). */
       argmaxAdvance: (logits, V, ids, pos, hist, histLen, scratch, tops = null) =>
         call(addon.argmaxAdvance, ctx, o(logits), V, o(ids), o(pos), o(hist), histLen, o(scratch), o(tops)),
+      /**
+       * The picks from a head gemv's epilogue.pickParts (its workgroups'
+       * share of CHUNK_MAX_AT, src/gpu/kernels.ts:3169-3246): as argmaxRows
+       * over its logits, bit for bit; with pos (M = 1) argmaxAdvance's
+       * advance. pickPartsBytes(M) sizes the parts buffer.
+       */
+      argmaxParts: (parts, M, ids, tops = null, pos = null, hist = null, histLen = 0) =>
+        call(addon.argmaxParts, ctx, o(parts), M, o(ids), o(tops), o(pos), o(hist), histLen),
+      pickPartsBytes: (M) => addon.pickPartsBytes(M),
       pickScratchBytes: (M, V) => addon.pickScratchBytes(M, V),
       /** Engine.pick's penalized chunk candidates (src/engine.ts:8352-8473). */
       pickCandidates: (logits, M, V, count, chunksOut, candidates, scratch, opts = null) =>

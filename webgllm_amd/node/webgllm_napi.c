@@ -714,6 +714,7 @@ static int read_epilogue(napi_env env, napi_value o, int32_t M, int32_t N, wg_ep
       {"convState", (void **)&e->conv_state, cd * (cw - 1) * 4},
       {"convStateOut", (void **)&e->conv_state_out, cd * (cw - 1) * 4},
       {"convPrefixes", (void **)&e->conv_prefixes, (uint64_t)M * (cw - 1) * cd * 4},
+      {"pickParts", &e->pick_parts, (uint64_t)wg_pick_parts_bytes(M)},
   };
   for (size_t k = 0; k < sizeof ptrs / sizeof ptrs[0]; k++)
     if (!prop_operand(env, o, ptrs[k].key, ptrs[k].need, 1, ptrs[k].at)) return 0;
@@ -1167,6 +1168,30 @@ static napi_value js_argmax_advance(napi_env env, napi_callback_info info) {
   DONE(wg_argmax_advance(logits, V, ids, pos, hist, hist_len, tops, scratch, need, ctx_stream(c)));
 }
 
+static napi_value js_pick_parts_bytes(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  INT32_ARG(0, M);
+  return num(env, (double)wg_pick_parts_bytes(M));
+}
+
+/* argmaxParts(ctx, parts, M, ids, tops?, pos?, hist?, histLen): the greedy
+ * picks from a head GEMV's pickParts (the epilogue's first stage of
+ * CHUNK_ARGMAX_ROWS, kernels.ts:3169-3246); with pos (M = 1) the decode
+ * step's advance as argmaxAdvance. */
+static napi_value js_argmax_parts(napi_env env, napi_callback_info info) {
+  ARGS(8);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, M);
+  INT32_ARG(7, hist_len);
+  if (M < 1 || M > 8 || hist_len < 0) return throw_limits(env, "argmaxParts: %d rows", M);
+  OPERAND(1, const void, parts, (uint64_t)wg_pick_parts_bytes(M), 0, "parts");
+  OPERAND(3, int32_t, ids, (uint64_t)M * 4, 0, "ids");
+  OPERAND(4, float, tops, (uint64_t)M * 4, 1, "tops");
+  OPERAND(5, int32_t, pos, 4, 1, "pos");
+  OPERAND(6, int32_t, hist, (uint64_t)hist_len * 4, 1, "hist");
+  DONE(wg_argmax_parts(parts, M, ids, tops, pos, hist, hist_len, ctx_stream(c)));
+}
+
 static napi_value js_pick_scratch_bytes(napi_env env, napi_callback_info info) {
   ARGS(2);
   INT32_ARG(0, M);
@@ -1415,6 +1440,8 @@ static napi_value init(napi_env env, napi_value exports) {
       {"argmaxScratchBytes", js_argmax_scratch_bytes},
       {"argmax", js_argmax},
       {"argmaxAdvance", js_argmax_advance},
+      {"argmaxParts", js_argmax_parts},
+      {"pickPartsBytes", js_pick_parts_bytes},
       {"pickScratchBytes", js_pick_scratch_bytes},
       {"pickCandidates", js_pick_candidates},
       {"ggufHeader", js_gguf_header},

@@ -418,6 +418,43 @@ def argmax_rows(logits: torch.Tensor, V: int | None = None, ids=None, tops=None,
     return ids
 
 
+def pick_parts(M: int, device="cuda") -> torch.Tensor:
+    """A buffer for a head GEMV's pick parts (wg_pick_parts_bytes, 16-byte
+    aligned as torch allocates)."""
+    return torch.empty(L.load().wg_pick_parts_bytes(M), dtype=torch.uint8, device=device)
+
+
+def gemv_pick(m: Q4Matrix, x16: torch.Tensor, out: torch.Tensor, parts: torch.Tensor,
+              epilogue: "L.Epilogue | None" = None) -> bool:
+    """The head GEMV storing the logits into `out` and running the greedy
+    pick's first stage into `parts` (a plain store, no residual). Returns
+    False, having launched nothing, where the library's kernels do not take
+    it (then gemv() and argmax_rows())."""
+    ep = epilogue if epilogue is not None else L.Epilogue(mode=L.EPI_STORE)
+    ep.pick_parts = parts.data_ptr()
+    x16 = _dev(x16)
+    M = x16.shape[0] if x16.dim() == 2 else 1
+    rc = L.load().wg_q4_gemv(C.byref(m.desc), _p(x16), M, x16.shape[-1], _p(out),
+                             out.shape[-1], C.byref(ep), _stream())
+    if rc == L.ERR_UNSUPPORTED:
+        return False
+    L.check(rc)
+    return True
+
+
+def argmax_parts(parts: torch.Tensor, M: int, ids: torch.Tensor, tops=None, pos=None,
+                 hist=None) -> torch.Tensor:
+    """The greedy picks from a head GEMV's parts (gemv_pick), bit for bit
+    argmax_rows' over its logits; with pos (one row) the decode advance of
+    argmax_advance as well."""
+    for t, name in ((ids, "ids"), (pos, "pos"), (hist, "hist")):
+        if t is not None and (t.dtype != torch.int32 or not t.is_cuda):
+            raise ValueError(f"{name} must be an int32 device tensor")
+    L.check(L.load().wg_argmax_parts(_p(parts), M, _p(ids), _p(tops), _p(pos), _p(hist),
+                                     0 if hist is None else hist.numel(), _stream()))
+    return ids
+
+
 def argmax_advance(logits: torch.Tensor, ids: torch.Tensor, pos: torch.Tensor,
                    hist: torch.Tensor | None = None, tops=None, scratch=None) -> None:
     """A decode step's greedy pick and advance on the device: ids[0] = the
