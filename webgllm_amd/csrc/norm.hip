@@ -105,39 +105,53 @@ __device__ inline void embed_extras(const wg_epilogue &e, int m, int c0, const f
   }
 }
 
-// Embedding rows of a ROWGROUP matrix: thread = (token m, block b), 256
-// threads a workgroup (a constant: the workgroup size is not read from the
-// dispatch's arguments before the first load).
+// Embedding rows of a ROWGROUP matrix: thread = (token m, 4 values of a
+// block), 256 threads a workgroup (a constant: the workgroup size is not
+// read from the dispatch's arguments before the first load). Values 4j ..
+// 4j + 3 of a block are the low (j < 4) or high nibbles of its bytes
+// 4 (j % 4) .. + 3: one 32-bit load a thread; its 4 outputs, prescaled
+// halves and one sum of squares are the thread's own. The next norm's
+// weights load ahead of the token id they do not depend on.
 __global__ __launch_bounds__(256) void embed_rowgroup_kernel(
     const uint32_t *quants, const uint16_t *scales, const void *zeros, int zero_kind,
     const int32_t *ids, int M, int blocks, int N, float *h, int ldh, const wg_epilogue e) {
-  int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t >= (int64_t)M * blocks) return;
-  int m = (int)(t / blocks), b = (int)(t % blocks);
-  int n = ids[m];
-  float *o = h + (int64_t)m * ldh + b * 32;
-  if (n < 0 || n >= N) {  // an id outside the vocabulary embeds as zeros
-    float z[32] = {};
-    for (int j = 0; j < 32; j++) o[j] = 0.0f;
-    embed_extras(e, m, b * 32, z);
-    return;
-  }
-  int64_t si = ((int64_t)(n >> 2) * blocks + b) * 4 + (n & 3);
-  double d = half_to_float(scales[si]);
-  double z = zero_kind == WG_ZERO_U8    ? (double)((const uint8_t *)zeros)[si]
-             : zero_kind == WG_ZERO_F16 ? (double)half_to_float(((const uint16_t *)zeros)[si])
-                                        : 8.0;
-  uint4 q = reinterpret_cast<const uint4 *>(quants)[si];
-  uint32_t w[4] = {q.x, q.y, q.z, q.w};
-  float v[32];
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int quads = blocks * 8;
+  if (t >= (int64_t)M * quads) return;
+  const int m = (int)(t / quads), qd = (int)(t % quads);
+  const int b = qd >> 3, j = qd & 7;
+  const int c0 = b * 32 + 4 * j;  // the thread's first value
+  float w16[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (e.out16)
 #pragma unroll
-  for (int j = 0; j < 16; j++) {
-    uint32_t byte = (w[j >> 2] >> (8 * (j & 3))) & 0xffu;
-    v[j] = (float)(d * ((double)(byte & 15u) - z));
-    v[j + 16] = (float)(d * ((double)(byte >> 4) - z));
+    for (int i = 0; i < 4; i++) w16[i] = e.out16_w[c0 + i];
+  const int n = ids[m];
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (n >= 0 && n < N) {  // an id outside the vocabulary embeds as zeros
+    const int64_t si = ((int64_t)(n >> 2) * blocks + b) * 4 + (n & 3);
+    const double d = half_to_float(scales[si]);
+    const double z = zero_kind == WG_ZERO_U8    ? (double)((const uint8_t *)zeros)[si]
+                     : zero_kind == WG_ZERO_F16 ? (double)half_to_float(((const uint16_t *)zeros)[si])
+                                                : 8.0;
+    const uint32_t word = quants[si * 4 + (j & 3)];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t byte = (word >> (8 * i)) & 0xffu;
+      const uint32_t nib = j < 4 ? (byte & 15u) : (byte >> 4);
+      v[i] = (float)(d * ((double)nib - z));
+    }
   }
-  for (int j = 0; j < 32; j++) o[j] = v[j];
-  embed_extras(e, m, b * 32, v);
+  float *o = h + (int64_t)m * ldh + c0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) o[i] = v[i];
+  if (e.out16) {
+    uint16_t *o16 = e.out16 + (int64_t)m * e.ld_out16 + c0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) o16[i] = half_bits(v[i] * w16[i] / e.norm_mult_out);
+  }
+  if (e.parts_out)
+    e.parts_out[(int64_t)m * e.ld_parts_out + c0 / 4] =
+        v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
 }
 
 // Embedding rows of a Q4_K matrix: thread = (token m, super-block s,
@@ -263,7 +277,7 @@ int wg_embed(const wg_q4_matrix *emb, const int32_t *ids, int32_t M, float *h, i
   hipStream_t s = as_stream(stream);
   if (emb->layout == WG_LAYOUT_ROWGROUP) {
     int blocks = emb->K / 32;
-    int64_t n = (int64_t)M * blocks;
+    int64_t n = (int64_t)M * blocks * 8;
     embed_rowgroup_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
         (const uint32_t *)emb->quants, (const uint16_t *)emb->scales, emb->zeros, emb->zero, ids,
         M, blocks, emb->N, h, ldh, e);
