@@ -554,6 +554,25 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
                    const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0,
                    int32_t max_keys, uint16_t *out, int32_t ldo, void *scratch,
                    size_t scratch_bytes, void *stream);
+/* wg_head_prep then wg_attn_decode in one launch, the heads prepared in the
+ * attention kernel (headPrep + attention, kernels.ts:2196-2322, :2803-3027):
+ * qkv [M][ldqkv] f32 rows q | k | v as wg_head_prep takes them; each
+ * workgroup makes its queries (norm, rotation at *pos0 + m, 1/sqrt(hd)),
+ * and the batch's new keys and values (rows *pos0 + m, k normed and
+ * rotated) go into the K and V tiles of the workgroups that read them and,
+ * from one workgroup a KV head, into the caches (ctx rows; rows outside
+ * [0, ctx) or the rope table store nothing, their queries are zero, as
+ * wg_head_prep does). q_out (or NULL) receives the queries as wg_head_prep
+ * writes them. The same bits as wg_head_prep then wg_attn_decode on the
+ * MFMA form (attn_mfma 2). Every dim rotated, up to 16 rows: other shapes
+ * return WG_ERR_UNSUPPORTED before any launch (then the two calls).
+ * qkv, rope and the caches 16-byte aligned; max_keys <= ctx. */
+int wg_attn_decode_prep(const float *qkv, int32_t M, int32_t ldqkv, const wg_attn_shape *shape,
+                        const float *q_norm, const float *k_norm, const float *rope,
+                        int32_t rope_rows, int32_t ctx, uint16_t *k_cache, uint16_t *v_cache,
+                        const int32_t *pos0, int32_t max_keys, float *q_out, int32_t ld_q_out,
+                        uint16_t *out, int32_t ldo, void *scratch, size_t scratch_bytes,
+                        void *stream);
 /* wg_attn_decode with no scratch argument and no allocation of any kind:
  * no counterpart in the reference. It is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,

@@ -82,12 +82,24 @@ __global__ __launch_bounds__(64) void head_prep_kernel(
   }
   float inv = 1.0f;
   if (use_norm) {
-    float s = 0.0f;
+    // the sum of squares in head_norm_inv's order: lane c < 4 walks dims
+    // 32 t + 8 c + e (held by lane (32 t + 8 c + e) % 64, element t / 2)
+    const int c = lane & 3;
+    float part = 0.0f;
+    for (int t = 0; 32 * t < hd; t++) {
+      float xs = xv[0];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      if (lane + 64 * i < hd) s += xv[i] * xv[i];
-    s = wave_sum(s);
-    inv = 1.0f / sqrtf(s / (float)hd + eps);
+      for (int i = 1; i < 4; i++)
+        if (i == (t >> 1)) xs = xv[i];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float x = __shfl(xs, (32 * t + 8 * c + e) & 63, 64);
+        part = __builtin_fmaf(x, x, part);
+      }
+    }
+    const float total = (__shfl(part, 0, 64) + __shfl(part, 1, 64)) +
+                        (__shfl(part, 2, 64) + __shfl(part, 3, 64));
+    inv = head_norm_inv(total, hd, eps);
   }
   const int lo = pos & 1023, hi = 1024 + (pos >> 10);
   const float *r_lo = rope + (int64_t)lo * hd, *r_hi = rope + (int64_t)hi * hd;
@@ -102,9 +114,7 @@ __global__ __launch_bounds__(64) void head_prep_kernel(
       const bool first = t < P;
       const int f = first ? t : t - P;
       const float p = xp[i] * (use_norm ? inv * wp[i] : 1.0f);
-      const float c1 = r_lo[f], s1 = r_lo[hd / 2 + f], c2 = r_hi[f], s2 = r_hi[hd / 2 + f];
-      const float cs = c1 * c2 - s1 * s2, sn = s1 * c2 + c1 * s2;
-      r = first ? v * cs - p * sn : v * cs + p * sn;
+      r = rope_rotate(v, p, first, r_lo[f], r_lo[hd / 2 + f], r_hi[f], r_hi[hd / 2 + f]);
     }
     if (is_q) {
       q_out[(int64_t)m * ldqo + (int64_t)slot * hd + t] = r * scale;
@@ -733,11 +743,95 @@ __host__ __device__ constexpr int amfma_wave_bytes() {
   return 2 * AWK * HD * 2 + 16 * 36 * 4;  // K and V tiles, the weights (16 x 36 floats)
 }
 
-template <int HD, bool XG>
+// (PREP) What head_prep_kernel takes besides the rows: the attention then
+// prepares its own heads from the q|k|v rows.
+struct AttnPrep {
+  const float *q_norm, *k_norm;  // (use_norm) the heads' norm weights
+  const float *rope;             // rope_rows rows of hd floats
+  uint16_t *k_cache, *v_cache;   // the new rows' destination (the caches read)
+  float *q_out;                  // (or null) the prepared queries, as head_prep writes them
+  int ld_q_out;
+  float eps;
+  int use_norm, rope_rows, ctx;
+};
+
+// (PREP) A lane's rope values for the position of its row: cos and sin of
+// the low (c1, s1) and high (c2, s2) table rows at the lane's frequencies
+// 32 t + 8 c4 + e (t < HD / 64, c4 = lane / 16 % 4). Returns whether the
+// position has rows (in the cache and the table); where it has not, the
+// values are row 0's and unused, as head_prep_kernel stores nothing there.
+template <int HD>
+struct RopeLane {
+  float c1[HD / 64][8], s1[HD / 64][8], c2[HD / 64][8], s2[HD / 64][8];
+};
+
+template <int HD>
+__device__ inline bool rope_lane_load(const AttnPrep &pp, int pos, RopeLane<HD> &r) {
+  const bool in = pos >= 0 && pos < pp.ctx && 1024 + (pos >> 10) < pp.rope_rows;
+  const int p = in ? pos : 0;
+  const int c4 = (threadIdx.x >> 4) & 3;
+  const float *r_lo = pp.rope + (int64_t)(p & 1023) * HD;
+  const float *r_hi = pp.rope + (int64_t)(1024 + (p >> 10)) * HD;
+#pragma unroll
+  for (int t = 0; t < HD / 64; t++) {
+    const int f = 32 * t + 8 * c4;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      *reinterpret_cast<float4 *>(r.c1[t] + 4 * h) = *reinterpret_cast<const float4 *>(r_lo + f + 4 * h);
+      *reinterpret_cast<float4 *>(r.s1[t] + 4 * h) =
+          *reinterpret_cast<const float4 *>(r_lo + HD / 2 + f + 4 * h);
+      *reinterpret_cast<float4 *>(r.c2[t] + 4 * h) = *reinterpret_cast<const float4 *>(r_hi + f + 4 * h);
+      *reinterpret_cast<float4 *>(r.s2[t] + 4 * h) =
+          *reinterpret_cast<const float4 *>(r_hi + HD / 2 + f + 4 * h);
+    }
+  }
+  return in;
+}
+
+// (PREP) One head row as head_prep_kernel makes it, for a lane holding
+// dims 32 t + 8 c4 + e (the 4 lanes of a row are lane % 16 + 16 c4): x the
+// raw values, w their norm weights, r the rope values of the row's
+// position (`in`: it has rows); every dim rotated (its partner, dim +- hd /
+// 2, is in the same lane at t ^ QS / 2). The norm's sum runs in
+// head_norm_inv's order (the lane's dims, then the lanes as (S0 + S1) +
+// (S2 + S3)). Every lane of the wave calls it; out is written where `in`.
+template <int HD>
+__device__ inline void prep_head_lane(const float (&x)[HD / 32][8], const float (&w)[HD / 32][8],
+                                      bool in, const RopeLane<HD> &r, const AttnPrep &pp,
+                                      float scale, float (&out)[HD / 32][8]) {
+  constexpr int QS = HD / 32, HQ = QS / 2;
+  float inv = 1.0f;
+  if (pp.use_norm) {
+    float part = 0.0f;
+#pragma unroll
+    for (int t = 0; t < QS; t++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) part = __builtin_fmaf(x[t][e], x[t][e], part);
+    part = part + xor16(part);
+    part = part + xor32(part);
+    inv = head_norm_inv(part, HD, pp.eps);
+  }
+  if (!in) return;
+  float v[QS][8];
+#pragma unroll
+  for (int t = 0; t < QS; t++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[t][e] = x[t][e] * (pp.use_norm ? inv * w[t][e] : 1.0f);
+#pragma unroll
+  for (int t = 0; t < HQ; t++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float c1 = r.c1[t][e], s1 = r.s1[t][e], c2 = r.c2[t][e], s2 = r.s2[t][e];
+      out[t][e] = rope_rotate(v[t][e], v[t + HQ][e], true, c1, s1, c2, s2) * scale;
+      out[t + HQ][e] = rope_rotate(v[t + HQ][e], v[t][e], false, c1, s1, c2, s2) * scale;
+    }
+}
+
+template <int HD, bool XG, bool PREP = false>
 __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
     const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0_dev, const float *q,
     int max_keys, int splits, int cpw, int M, int H, int KV, int ldq, float *partial,
-    int *counters, uint16_t *out, int ldo) {
+    int *counters, uint16_t *out, int ldo, const AttnPrep pp) {
   typedef _Float16 half8 __attribute__((ext_vector_type(8)));
   typedef _Float16 half4 __attribute__((ext_vector_type(4)));
   typedef short short4v __attribute__((ext_vector_type(4)));
@@ -810,7 +904,9 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
   // next workgroup)
   if (j0w < max_keys) issue(j0w);
   // the query's loads go out with the chunk's, ahead of the position
+  // (PREP: the raw query of the q|k|v row, and its norm weights)
   float4 qraw[QS][2];
+  float qw[PREP ? QS : 1][8];
   {
     const float *qp = q + (int64_t)qm * ldq + (int64_t)(kh * G + qh) * HD + 8 * c4;
 #pragma unroll
@@ -821,7 +917,32 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
         qraw[t][1] = *reinterpret_cast<const float4 *>(qp + 32 * t + 4);
       }
     }
+    if constexpr (PREP)
+#pragma unroll
+      for (int t = 0; t < QS; t++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) qw[t][e] = pp.use_norm ? pp.q_norm[32 * t + 8 * c4 + e] : 1.0f;
   }
+  // (PREP) the lane's new row j = n16 of the batch: its raw key and the key
+  // norm's weights go out with the query's (64 dims: before the position
+  // is read; 128: with the rope values, to spare registers)
+  constexpr bool EARLY = PREP && HD == 64;
+  float xk[PREP ? QS : 1][8], wk[PREP ? QS : 1][8];
+  auto load_key = [&]() {
+    const float *kp = q + (int64_t)(n16 < M ? n16 : 0) * ldq + (int64_t)(H + kh) * HD + 8 * c4;
+#pragma unroll
+    for (int t = 0; t < QS; t++) {
+      const float4 k0 = *reinterpret_cast<const float4 *>(kp + 32 * t);
+      const float4 k1 = *reinterpret_cast<const float4 *>(kp + 32 * t + 4);
+      const float ka[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        xk[t][e] = ka[e];
+        wk[t][e] = pp.use_norm ? pp.k_norm[32 * t + 8 * c4 + e] : 1.0f;
+      }
+    }
+  };
+  if constexpr (EARLY) load_key();
   const int pos0 = *pos0_dev;
   const int n_keys = min(pos0 + M, max_keys);
   const int live = n_keys <= 0 ? 0 : (n_keys + SPLIT - 1) / SPLIT;  // splits with a visible key
@@ -838,6 +959,93 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
     return;
   }
   const int nch = max(0, min(cpw, (n_keys - j0w + AWK - 1) / AWK));  // this wave's chunks
+
+  // PREP: the batch's new keys and values (rows j < M of the q|k|v rows, at
+  // positions pos0 + j) are made here as head_prep_kernel makes them, by
+  // the waves whose chunks hold them (into their K and V tiles after each
+  // load) and by one wave of the head's first query group and split (into
+  // the caches): lane (j = lane % 16, c4) holds row j's dims 32 t + 8 c4 ..
+  // + 7 as halves.
+  const bool patch = PREP && j0w < n_keys && j0w + nch * AWK > pos0;
+  bool knew = false;
+  uint4 kh4[PREP ? QS : 1], vh4[PREP ? QS : 1];
+  if constexpr (PREP) {
+    const bool writer = qg == 0 && s == 0 && wave == 0;
+    const bool keys = writer || patch;  // (uniform in the wave)
+    // the rope values of the query's position and of the new row's, and
+    // the new row's raw value (and key where not loaded yet), all at once
+    RopeLane<HD> rq, rk;
+    const bool qin = rope_lane_load<HD>(pp, pos0 + qm, rq);
+    bool kin = false;
+    float xv[QS][8];
+    if (keys) {
+      kin = rope_lane_load<HD>(pp, pos0 + n16, rk);
+      if constexpr (!EARLY) load_key();
+      const float *vp =
+          q + (int64_t)(n16 < M ? n16 : 0) * ldq + (int64_t)(H + KV + kh) * HD + 8 * c4;
+#pragma unroll
+      for (int t = 0; t < QS; t++) {
+        const float4 v0 = *reinterpret_cast<const float4 *>(vp + 32 * t);
+        const float4 v1 = *reinterpret_cast<const float4 *>(vp + 32 * t + 4);
+        const float va[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) xv[t][e] = va[e];
+      }
+    }
+    if (keys) {
+      float kr[QS][8];
+      prep_head_lane<HD>(xk, wk, kin, rk, pp, 1.0f, kr);
+      knew = kin && n16 < M;
+      if (knew) {
+#pragma unroll
+        for (int t = 0; t < QS; t++) {
+          uint32_t kw[4], vw[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            kw[e] = (uint32_t)to_h(kr[t][2 * e]) | ((uint32_t)to_h(kr[t][2 * e + 1]) << 16);
+            vw[e] = (uint32_t)to_h(xv[t][2 * e]) | ((uint32_t)to_h(xv[t][2 * e + 1]) << 16);
+          }
+          kh4[t] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+          vh4[t] = make_uint4(vw[0], vw[1], vw[2], vw[3]);
+        }
+        if (writer) {
+          const int64_t row = (int64_t)(pos0 + n16) * kvd + (int64_t)kh * HD + 8 * c4;
+#pragma unroll
+          for (int t = 0; t < QS; t++) {
+            *reinterpret_cast<uint4 *>(pp.k_cache + row + 32 * t) = kh4[t];
+            *reinterpret_cast<uint4 *>(pp.v_cache + row + 32 * t) = vh4[t];
+          }
+        }
+      }
+    }
+    // the query as head_prep_kernel makes it (zero where its position has
+    // no row)
+    float xq[QS][8], oq[QS][8];
+#pragma unroll
+    for (int t = 0; t < QS; t++) {
+      const float4 a = qraw[t][0], b = qraw[t][1];
+      const float qa[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) xq[t][e] = qa[e];
+    }
+    prep_head_lane<HD>(xq, qw, qin, rq, pp, 1.0f / sqrtf((float)HD), oq);
+#pragma unroll
+    for (int t = 0; t < QS; t++) {
+      qraw[t][0] = qraw[t][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (qvalid && qin) {
+        qraw[t][0] = make_float4(oq[t][0], oq[t][1], oq[t][2], oq[t][3]);
+        qraw[t][1] = make_float4(oq[t][4], oq[t][5], oq[t][6], oq[t][7]);
+      }
+    }
+    if (pp.q_out && s == 0 && qvalid) {  // each query once: its group's first split
+      float *qo = pp.q_out + (int64_t)qm * pp.ld_q_out + (int64_t)(kh * G + qh) * HD + 8 * c4;
+#pragma unroll
+      for (int t = 0; t < QS; t++) {
+        *reinterpret_cast<float4 *>(qo + 32 * t) = qraw[t][0];
+        *reinterpret_cast<float4 *>(qo + 32 * t + 4) = qraw[t][1];
+      }
+    }
+  }
 
   // the queries as B operands, hi and lo halves: dims 32 t + 8 c4 .. + 7
   half8 qhi[QS], qlo[QS];
@@ -870,6 +1078,21 @@ __global__ __launch_bounds__(AW * 64) void attn_mfma_kernel(
         *reinterpret_cast<uint4 *>(vt + idx * 16) = make_uint4(0u, 0u, 0u, 0u);
       __builtin_amdgcn_s_waitcnt(0xc07f);
       asm volatile("" ::: "memory");
+    }
+    if constexpr (PREP) {
+      if (patch) {  // the new rows in this chunk: their pieces over the loaded ones
+        const int r = pos0 + n16 - j0;
+        if (knew && r >= 0 && r < AWK && pos0 + n16 < n_keys) {
+#pragma unroll
+          for (int t = 0; t < QS; t++) {
+            const int at = r * ROWB + (((4 * t + c4) ^ swz(r)) * 16);
+            *reinterpret_cast<uint4 *>(kt + at) = kh4[t];
+            *reinterpret_cast<uint4 *>(vt + at) = vh4[t];
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        asm volatile("" ::: "memory");
+      }
     }
     float sc[2][4];
     float tmax = -INFINITY;
@@ -1554,6 +1777,43 @@ static bool xcd_grouping(hipStream_t stream) {
   return ok;
 }
 
+// The MFMA decode attention's launch: cpw chunks a wave, as few as keep
+// about one workgroup a compute unit; grouped by XCD where the units are a
+// multiple of 8 and `group`. PREP: the heads prepared in the kernel.
+template <bool PREP>
+static int launch_amfma(const float *q, int M, int ldq, int H, int KV, int hd,
+                        const uint16_t *k_cache, const uint16_t *v_cache, const int32_t *pos0,
+                        int max_keys, uint16_t *out, int ldo, float *partial, int *counters,
+                        const AttnPrep &pp, bool group, hipStream_t s) {
+  const int QG = ((H / KV) * M + 15) / 16;  // groups of 16 queries a KV head
+  const int cus = persistent_grid(1 << 30, 1);
+  const int units = KV * QG;
+  const int wchunks = (max_keys + AWK - 1) / AWK;  // 32-key chunks
+  int cpw = (int)(((int64_t)wchunks * units + (int64_t)AW * cus - 1) / ((int64_t)AW * cus));
+  cpw = cpw < 1 ? 1 : cpw;
+  const int splits = (wchunks + AW * cpw - 1) / (AW * cpw);
+  const size_t lds = (size_t)AW * (hd == 64 ? amfma_wave_bytes<64>() : amfma_wave_bytes<128>());
+  const dim3 grid((unsigned)(units * splits));
+  const bool xg = units % XCDS == 0 && group && xcd_grouping(s);
+#define WG_AMFMA_LAUNCH(HDV, XGV)                                                                \
+  do {                                                                                           \
+    int rc_ = raise_lds((const void *)attn_mfma_kernel<HDV, XGV, PREP>, (int)lds);               \
+    if (rc_) return rc_;                                                                         \
+    attn_mfma_kernel<HDV, XGV, PREP><<<grid, AW * 64, lds, s>>>(                                 \
+        k_cache, v_cache, pos0, q, max_keys, splits, cpw, M, H, KV, ldq, partial, counters, out, \
+        ldo, pp);                                                                                \
+  } while (0)
+  if (hd == 64) {
+    if (xg) WG_AMFMA_LAUNCH(64, true);
+    else WG_AMFMA_LAUNCH(64, false);
+  } else {
+    if (xg) WG_AMFMA_LAUNCH(128, true);
+    else WG_AMFMA_LAUNCH(128, false);
+  }
+#undef WG_AMFMA_LAUNCH
+  return launched("wg_attn_decode");
+}
+
 }  // namespace wg
 
 using namespace wg;
@@ -1705,37 +1965,9 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
   float *partial = (float *)((char *)scratch + COUNTER_BYTES);
   const int chunks = (max_keys + CHUNK - 1) / CHUNK;
   const int QG = ((H / KV) * M + 15) / 16;  // groups of 16 queries a KV head
-  if (amfma) {
-    // one launch on MFMA: cpw chunks a wave, as few as keep about one
-    // workgroup a compute unit
-    const int cus = persistent_grid(1 << 30, 1);
-    const int units = KV * QG;
-    const int wchunks = (max_keys + AWK - 1) / AWK;  // 32-key chunks
-    int cpw = (int)(((int64_t)wchunks * units + (int64_t)AW * cus - 1) / ((int64_t)AW * cus));
-    cpw = cpw < 1 ? 1 : cpw;
-    const int splits = (wchunks + AW * cpw - 1) / (AW * cpw);
-    const size_t lds = (size_t)AW * (hd == 64 ? amfma_wave_bytes<64>() : amfma_wave_bytes<128>());
-    const dim3 grid((unsigned)(units * splits));
-    // units a multiple of 8: grouped by XCD (attn_xcd 0: never)
-    const bool xg = units % XCDS == 0 && xcd_knob != 0 && xcd_grouping(s);
-#define WG_AMFMA_LAUNCH(HDV, XGV)                                                               \
-  do {                                                                                          \
-    int rc_ = raise_lds((const void *)attn_mfma_kernel<HDV, XGV>, (int)lds);                    \
-    if (rc_) return rc_;                                                                        \
-    attn_mfma_kernel<HDV, XGV><<<grid, AW * 64, lds, s>>>(k_cache, v_cache, pos0, q, max_keys, \
-                                                         splits, cpw, M, H, KV, ldq, partial,   \
-                                                         counters, out, ldo);                   \
-  } while (0)
-    if (hd == 64) {
-      if (xg) WG_AMFMA_LAUNCH(64, true);
-      else WG_AMFMA_LAUNCH(64, false);
-    } else {
-      if (xg) WG_AMFMA_LAUNCH(128, true);
-      else WG_AMFMA_LAUNCH(128, false);
-    }
-#undef WG_AMFMA_LAUNCH
-    return launched("wg_attn_decode");
-  }
+  if (amfma)  // (attn_xcd 0: never grouped by XCD)
+    return launch_amfma<false>(q, M, ldq, H, KV, hd, k_cache, v_cache, pos0, max_keys, out, ldo,
+                               partial, counters, AttnPrep{}, xcd_knob != 0, s);
   if (fused || xl) {
     // one launch: 64 * nch keys a workgroup, the smallest nch (1, 2, 4) that
     // keeps the grid to about one workgroup a compute unit
@@ -1811,6 +2043,53 @@ int wg_attn_decode(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *
     attn_combine_kernel<128><<<cgrid, 256, 0, s>>>(partial, M, H, chunks, pos0, max_keys, out,
                                                    ldo);
   return launched("wg_attn_decode (combine)");
+}
+
+int wg_attn_decode_prep(const float *qkv, int32_t M, int32_t ldqkv, const wg_attn_shape *sh,
+                        const float *q_norm, const float *k_norm, const float *rope,
+                        int32_t rope_rows, int32_t ctx, uint16_t *k_cache, uint16_t *v_cache,
+                        const int32_t *pos0, int32_t max_keys, float *q_out, int32_t ld_q_out,
+                        uint16_t *out, int32_t ldo, void *scratch, size_t scratch_bytes,
+                        void *stream) {
+  WG_REQUIRE(sh && qkv && rope && k_cache && v_cache && pos0 && out && scratch,
+             "wg_attn_decode_prep: null argument");
+  const int H = sh->heads, KV = sh->kv_heads, hd = sh->head_dim;
+  WG_REQUIRE(KV > 0 && H % KV == 0, "wg_attn_decode_prep: %d query heads over %d KV heads", H,
+             KV);
+  WG_REQUIRE(hd == 64 || hd == 128, "wg_attn_decode_prep: head_dim %d (64 or 128)", hd);
+  WG_REQUIRE(M >= 1 && (H / KV) * M <= 64,
+             "wg_attn_decode_prep: %d rows x %d heads per KV head (at most 64)", M, H / KV);
+  WG_REQUIRE(!sh->use_norm || (q_norm && k_norm), "wg_attn_decode_prep: norm weights missing");
+  WG_REQUIRE(ctx >= 1 && rope_rows >= 1024 + (ctx + 1023) / 1024,
+             "wg_attn_decode_prep: a rope table of %d rows for a %d-position cache", rope_rows,
+             ctx);
+  WG_REQUIRE(max_keys >= M && max_keys <= ctx && max_keys <= MAX_FUSED_KEYS,
+             "wg_attn_decode_prep: max_keys %d (rows %d, cache %d)", max_keys, M, ctx);
+  WG_REQUIRE(ldqkv >= (H + 2 * KV) * hd && ldqkv % 4 == 0 && ((uintptr_t)qkv & 15) == 0 &&
+                 ((uintptr_t)rope & 15) == 0 && ((uintptr_t)k_cache & 15) == 0 &&
+                 ((uintptr_t)v_cache & 15) == 0,
+             "wg_attn_decode_prep: the q|k|v rows, rope table and caches must be 16-byte "
+             "aligned (row stride a multiple of 4 floats, at least the heads' width)");
+  WG_REQUIRE(!q_out || (ld_q_out >= H * hd && ld_q_out % 4 == 0 && ((uintptr_t)q_out & 15) == 0),
+             "wg_attn_decode_prep: q_out stride or alignment");
+  WG_REQUIRE(ldo >= H * hd && ((uintptr_t)out & 15) == 0 && ldo % 8 == 0,
+             "wg_attn_decode_prep: the output must be 16-byte aligned with a stride of 8k halves");
+  WG_REQUIRE(scratch_bytes >= wg_attn_scratch_bytes(M, H, hd, max_keys),
+             "wg_attn_decode_prep: scratch of %zu bytes, %zu needed", scratch_bytes,
+             wg_attn_scratch_bytes(M, H, hd, max_keys));
+  // the form that prepares its heads: the MFMA one, every dim rotated, up
+  // to 16 rows (a lane group's new key each)
+  const int QG = ((H / KV) * M + 15) / 16;
+  if (sh->rotated_dims != hd || M > 16 || KV * QG > MAX_KV_COUNTERS)
+    return fail(WG_ERR_UNSUPPORTED,
+                "wg_attn_decode_prep: %d rows, %d of %d dims rotated: not for this shape", M,
+                sh->rotated_dims, hd);
+  int *counters = (int *)scratch;
+  float *partial = (float *)((char *)scratch + COUNTER_BYTES);
+  AttnPrep pp{q_norm, k_norm, rope, k_cache, v_cache, q_out, ld_q_out,
+              sh->eps, sh->use_norm, rope_rows, ctx};
+  return launch_amfma<true>(qkv, M, ldqkv, H, KV, hd, k_cache, v_cache, pos0, max_keys, out, ldo,
+                            partial, counters, pp, tuning("attn_xcd") != 0, as_stream(stream));
 }
 
 int wg_attn_decode_noalloc(const float *q, int32_t M, int32_t ldq, const wg_attn_shape *sh,

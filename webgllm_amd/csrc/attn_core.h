@@ -13,6 +13,23 @@ namespace wg {
 
 constexpr int CHUNK = 64;  // keys an item takes
 
+// Head preparation's arithmetic (the reference's headPrep,
+// src/gpu/kernels.ts:2196-2322), shared by head_prep_kernel and the decode
+// attention that prepares its own heads, so that both give the same bits.
+// The norm's sum of squares runs in one fixed order: per c = 0..3 the
+// dims 32 t + 8 c + e (e = 0..7 fastest, then t), as fmas from zero, then
+// (S0 + S1) + (S2 + S3).
+__device__ inline float head_norm_inv(float total, int hd, float eps) {
+  return 1.0f / sqrtf(total / (float)hd + eps);
+}
+// The rotation of v by its partner p: cos and sin of the position's low
+// (c1, s1) and high (c2, s2) table rows combined by angle addition.
+__device__ inline float rope_rotate(float v, float p, bool first, float c1, float s1, float c2,
+                                    float s2) {
+  const float cs = __builtin_fmaf(c1, c2, -(s1 * s2)), sn = __builtin_fmaf(s1, c2, c1 * s2);
+  return first ? __builtin_fmaf(v, cs, -(p * sn)) : __builtin_fmaf(v, cs, p * sn);
+}
+
 // LDS bytes attn_chunk_item needs for GM queries of head_dim hd.
 __host__ __device__ constexpr size_t attn_lds_bytes(int GM, int hd) {
   return (size_t)2 * CHUNK * (hd + 2) * 2 + (size_t)GM * hd * 4 + (size_t)GM * CHUNK * 4 +

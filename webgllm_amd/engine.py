@@ -280,6 +280,9 @@ class Engine:
         self.probe = None
         # short convs in in_proj's epilogue (False: in_proj, then the conv)
         self.fuse_conv = True
+        # heads prepared inside the decode attention (False: head_prep, then
+        # the attention)
+        self.fuse_prep = True
 
     # --- the attention caches, grown on demand ------------------------------
     def reserve(self, end: int) -> None:
@@ -405,11 +408,18 @@ class Engine:
                 qkv = self.qkv[:M]
                 ops.gemv(lw["qkv"], x16, out=qkv,
                          epilogue=self._norm_in(L.Epilogue(mode=L.EPI_STORE)))
-                ops.head_prep(qkv, self.attn, self.rope, self.pos, self.k_cache[i],
-                              self.v_cache[i], lw.get("q_norm"), lw.get("k_norm"),
-                              q_out=self.q[:M])
-            ops.attn_decode(self.q[:M], self.attn, self.k_cache[i], self.v_cache[i],
-                            self.pos, scratch=self.attn_scratch, out=self.att16[:M])
+            # the heads prepared inside the attention kernel where it takes
+            # the shape, else head preparation, then the attention
+            if s.rope_in_epilogue or not self.fuse_prep or ops.attn_decode_prep(
+                    self.qkv[:M], self.attn, self.rope, self.pos, self.k_cache[i],
+                    self.v_cache[i], lw.get("q_norm"), lw.get("k_norm"),
+                    scratch=self.attn_scratch, out=self.att16[:M], q_out=self.q[:M]) is None:
+                if not s.rope_in_epilogue:
+                    ops.head_prep(self.qkv[:M], self.attn, self.rope, self.pos, self.k_cache[i],
+                                  self.v_cache[i], lw.get("q_norm"), lw.get("k_norm"),
+                                  q_out=self.q[:M])
+                ops.attn_decode(self.q[:M], self.attn, self.k_cache[i], self.v_cache[i],
+                                self.pos, scratch=self.attn_scratch, out=self.att16[:M])
             if self.probe:
                 self.probe(i, "attention", (self.q[:M], self.att16[:M]))
             ops.gemv(lw["o"], self.att16[:M], out=h,

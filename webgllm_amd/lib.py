@@ -192,6 +192,8 @@ def load():
         "wg_attn_prefill": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32, P, I32, P]),
         "wg_attn_decode": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32, P, I32,
                                      P, SZ, P]),
+        "wg_attn_decode_prep": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32, I32,
+                                          P, P, P, I32, P, I32, P, I32, P, SZ, P]),
         "wg_attn_decode_noalloc": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32,
                                              P, I32, P]),
         "wg_verify_accept": (C.c_int, [P, I32, P, I32, I32, P, P, P, I32, P, I32, P, P]),

@@ -309,6 +309,15 @@ class HipGpu {
       /** scores / attend / attendPanel + combine (src/gpu/kernels.ts:2386-2579, :2803-3027). */
       attnDecode: (q, M, shape, kCache, vCache, pos0, maxKeys, out, scratch, ldq = null, ldo = null) =>
         call(addon.attnDecode, ctx, o(q), M, shape, o(kCache), o(vCache), o(pos0), maxKeys, o(out), o(scratch), ldq, ldo),
+      /**
+       * headPrep + attnDecode in one launch, the heads prepared inside the
+       * attention (the same bits); throws WG_ERR_UNSUPPORTED where the
+       * kernel does not take the shape (then the two calls).
+       */
+      attnDecodePrep: (qkv, M, shape, qNorm, kNorm, rope, ropeRows, pos0, kCache, vCache, ctxRows, out, scratch,
+                       qOut = null, ldqkv = null, ldo = null) =>
+        call(addon.attnDecodePrep, ctx, o(qkv), M, shape, o(qNorm), o(kNorm), o(rope), ropeRows, o(pos0),
+             o(kCache), o(vCache), ctxRows, o(out), o(scratch), o(qOut), ldqkv, ldo),
       /** The prompt's attention plan (src/engine.ts:6359-6630). */
       attnPrefill: (q, M, shape, kCache, vCache, pos0, maxKeys, out, ldq = null, ldo = null) =>
         call(addon.attnPrefill, ctx, o(q), M, shape, o(kCache), o(vCache), o(pos0), maxKeys, o(out), ldq, ldo),

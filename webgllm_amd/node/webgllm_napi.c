@@ -995,6 +995,40 @@ static napi_value js_attn_prefill(napi_env env, napi_callback_info info) {
   return attn_common(env, info, 1);
 }
 
+/* attnDecodePrep(ctx, qkv, M, shape, qNorm?, kNorm?, rope, ropeRows, pos0,
+ * kCache, vCache, ctxRows, out, scratch, qOut?, ldqkv?, ldo?): headPrep +
+ * values and the decode attention in one launch (kernels.ts:2196-2322,
+ * :2803-3027); throws WG_ERR_UNSUPPORTED for a shape the kernel does not
+ * take (then headPrep and attnDecode). */
+static napi_value js_attn_decode_prep(napi_env env, napi_callback_info info) {
+  ARGS(17);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(2, M);
+  SHAPE_ARG(3, sh);
+  INT32_ARG(7, rope_rows);
+  INT32_ARG(11, ctx_rows);
+  const int64_t hd = sh.head_dim, qd = (int64_t)sh.heads * hd, kvd = (int64_t)sh.kv_heads * hd;
+  int32_t ldqkv = (int32_t)(qd + 2 * kvd), ldo = (int32_t)qd;
+  if (!is_nullish(env, argv[15]) && !get_i32(env, argv[15], &ldqkv)) return type_error(env, "ldqkv must be an integer");
+  if (!is_nullish(env, argv[16]) && !get_i32(env, argv[16], &ldo)) return type_error(env, "ldo must be an integer");
+  if (M < 1 || ctx_rows < 1 || rope_rows < 1)
+    return throw_limits(env, "attnDecodePrep: %d rows, a cache of %d", M, ctx_rows);
+  OPERAND(1, const float, qkv, span(M, ldqkv, qd + 2 * kvd) * 4, 0, "qkv");
+  OPERAND(4, const float, q_norm, (uint64_t)hd * 4, 1, "qNorm");
+  OPERAND(5, const float, k_norm, (uint64_t)hd * 4, 1, "kNorm");
+  OPERAND(6, const float, rope, (uint64_t)rope_rows * (uint64_t)hd * 4, 0, "rope");
+  OPERAND(8, const int32_t, pos0, 4, 0, "pos0");
+  OPERAND(9, uint16_t, k_cache, (uint64_t)ctx_rows * (uint64_t)kvd * 2, 0, "kCache");
+  OPERAND(10, uint16_t, v_cache, (uint64_t)ctx_rows * (uint64_t)kvd * 2, 0, "vCache");
+  OPERAND(12, uint16_t, out, span(M, ldo, qd) * 2, 0, "out");
+  const size_t need = wg_attn_scratch_bytes(M, sh.heads, sh.head_dim, ctx_rows);
+  OPERAND(13, void, scratch, need, 0, "scratch");
+  OPERAND(14, float, q_out, span(M, (int32_t)qd, qd) * 4, 1, "qOut");
+  DONE(wg_attn_decode_prep(qkv, M, ldqkv, &sh, q_norm, k_norm, rope, rope_rows, ctx_rows, k_cache,
+                           v_cache, pos0, ctx_rows, q_out, (int32_t)qd, out, ldo, scratch, need,
+                           ctx_stream(c)));
+}
+
 /* shortConv(ctx, bcx, M, D, W, taps, state, stateOut, prefixes?, out, ldb?,
  * ldo?): convFused + convPrefixes (kernels.ts:1447-1523; Engine.convolve,
  * engine.ts:5806-5899). */
@@ -1432,6 +1466,7 @@ static napi_value init(napi_env env, napi_value exports) {
       {"attnScratchBytes", js_attn_scratch_bytes},
       {"attnDecode", js_attn_decode},
       {"attnPrefill", js_attn_prefill},
+      {"attnDecodePrep", js_attn_decode_prep},
       {"shortConv", js_short_conv},
       {"convAccept", js_conv_accept},
       {"convStates", js_conv_states},

@@ -336,6 +336,32 @@ def attn_decode(q: torch.Tensor, shape, k_cache, v_cache, pos0: torch.Tensor,
     return out
 
 
+def attn_decode_prep(qkv: torch.Tensor, shape, rope: torch.Tensor, pos0: torch.Tensor,
+                     k_cache, v_cache, q_norm=None, k_norm=None, scratch=None, out=None,
+                     q_out: torch.Tensor | None = None):
+    """head_prep then attn_decode in one launch (the heads prepared inside
+    the attention kernel), the same bits. Returns the half output, or None,
+    having launched nothing, where the kernel does not take the shape (then
+    head_prep() and attn_decode())."""
+    qkv = _dev(qkv, torch.float32)
+    M = qkv.shape[0]
+    max_keys = k_cache.shape[0]
+    if scratch is None:
+        scratch = attn_scratch(M, shape, max_keys, qkv.device)
+    if out is None:
+        out = torch.empty((M, shape.heads * shape.head_dim), dtype=torch.float16,
+                          device=qkv.device)
+    rc = L.load().wg_attn_decode_prep(
+        _p(qkv), M, qkv.shape[1], C.byref(shape), _p(q_norm), _p(k_norm),
+        _p(_dev(rope, torch.float32)), rope.shape[0], k_cache.shape[0], _p(k_cache), _p(v_cache),
+        _p(_dev(pos0, torch.int32)), max_keys, _p(q_out), q_out.shape[1] if q_out is not None else 0,
+        _p(out), out.shape[1], _p(scratch), scratch.numel(), _stream())
+    if rc == L.ERR_UNSUPPORTED:
+        return None
+    L.check(rc)
+    return out
+
+
 def attn_prefill(q: torch.Tensor, shape, k_cache, v_cache, pos0: torch.Tensor,
                  out: torch.Tensor | None = None):
     """Causal attention of a prompt batch (rows at pos0, pos0 + 1, ...)
