@@ -496,6 +496,12 @@ int wg_swiglu(const float *gu, int32_t M, int32_t F, int32_t ldg, uint16_t *out,
  * input and the sums of squares of each 4 values, as embedFold draws them. */
 int wg_embed(const wg_q4_matrix *emb, const int32_t *ids, int32_t M, float *h, int32_t ldh,
              const wg_epilogue *ep, void *stream);
+/* wg_verify_drafts and wg_embed in one launch: row 0 embeds ids[0], row
+ * m >= 1 entry m - 1 of table row *cursor (the last row once the cursor is
+ * past n_steps), which it also writes to ids[m] for the accept. */
+int wg_embed_drafts(const wg_q4_matrix *emb, int32_t *ids, int32_t rows, const int32_t *table,
+                    int32_t n_steps, const int32_t *cursor, float *h, int32_t ldh,
+                    const wg_epilogue *ep, void *stream);
 
 /* -------------------------------------------------------- attention */
 
@@ -639,6 +645,13 @@ int wg_verify_accept(const int32_t *picks, int32_t rows, const wg_conv_state *co
  * rows - 1 ids (the last row once the cursor is past n_steps). */
 int wg_verify_drafts(int32_t *ids, int32_t rows, const int32_t *table, int32_t n_steps,
                      const int32_t *cursor, void *stream);
+/* wg_argmax_parts and wg_verify_accept in one launch: the batch's picks
+ * finished from a head GEMV's pick_parts (the same ids wg_argmax_parts
+ * gives), written to picks_out, then the accept as wg_verify_accept. */
+int wg_verify_accept_parts(const void *pick_parts, int32_t *picks_out, int32_t rows,
+                           const wg_conv_state *convs, int32_t n_conv, int32_t max_state,
+                           int32_t *pos, int32_t *ids, int32_t *hist, int32_t hist_len,
+                           int32_t *kept_log, int32_t log_len, int32_t *cursor, void *stream);
 
 /* ------------------------------------------------- Gated DeltaNet */
 

@@ -90,6 +90,26 @@ __global__ void swiglu_kernel(const float *gu, int M, int F, int ldg, uint16_t *
   out[(int64_t)m * ldo + i] = to_h(g / (1.0f + __expf(-g)) * u);
 }
 
+// The rows' token ids: ids[m], or (a verify step's drafts from a device
+// table) ids[0] and, for rows m >= 1, entry m - 1 of table row *cursor
+// (the last row once the cursor is past it), which the row's first thread
+// also writes to ids[m] for the accept that follows.
+struct EmbedIds {
+  int32_t *ids;
+  const int32_t *table;  // (or null)
+  int n_steps;
+  const int32_t *cursor;
+};
+
+__device__ inline int embed_id(const EmbedIds &s, int M, int m, bool first) {
+  if (!s.table || m == 0) return s.ids[m];
+  int step = *s.cursor;
+  step = step < 0 ? 0 : (step >= s.n_steps ? s.n_steps - 1 : step);
+  const int n = s.table[(int64_t)step * (M - 1) + m - 1];
+  if (first) s.ids[m] = n;
+  return n;
+}
+
 // The embedding's extras (a GEMV epilogue's STORE outputs): the next
 // norm's prescaled half input and the sums of squares of each 4 values.
 __device__ inline void embed_extras(const wg_epilogue &e, int m, int c0, const float *v) {
@@ -114,7 +134,7 @@ __device__ inline void embed_extras(const wg_epilogue &e, int m, int c0, const f
 // weights load ahead of the token id they do not depend on.
 __global__ __launch_bounds__(256) void embed_rowgroup_kernel(
     const uint32_t *quants, const uint16_t *scales, const void *zeros, int zero_kind,
-    const int32_t *ids, int M, int blocks, int N, float *h, int ldh, const wg_epilogue e) {
+    const EmbedIds ids, int M, int blocks, int N, float *h, int ldh, const wg_epilogue e) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int quads = blocks * 8;
   if (t >= (int64_t)M * quads) return;
@@ -125,7 +145,7 @@ __global__ __launch_bounds__(256) void embed_rowgroup_kernel(
   if (e.out16)
 #pragma unroll
     for (int i = 0; i < 4; i++) w16[i] = e.out16_w[c0 + i];
-  const int n = ids[m];
+  const int n = embed_id(ids, M, m, qd == 0);
   float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (n >= 0 && n < N) {  // an id outside the vocabulary embeds as zeros
     const int64_t si = ((int64_t)(n >> 2) * blocks + b) * 4 + (n & 3);
@@ -157,7 +177,7 @@ __global__ __launch_bounds__(256) void embed_rowgroup_kernel(
 // Embedding rows of a Q4_K matrix: thread = (token m, super-block s,
 // sub-block j), with packQ4_K's (d', z') chain (src/repack.ts:100-168).
 __global__ __launch_bounds__(256) void embed_q4k_kernel(const uint8_t *quants,
-                                                        const int32_t *ids, int M, int supers,
+                                                        const EmbedIds ids, int M, int supers,
                                                         int N, float *h, int ldh,
                                                         const wg_epilogue e) {
   int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -165,7 +185,7 @@ __global__ __launch_bounds__(256) void embed_q4k_kernel(const uint8_t *quants,
   int j = (int)(t & 7);
   int64_t ms = t >> 3;
   int m = (int)(ms / supers), s = (int)(ms % supers);
-  int n = ids[m];
+  int n = embed_id(ids, M, m, s == 0 && j == 0);
   float *o = h + (int64_t)m * ldh + s * 256 + j * 32;
   if (n < 0 || n >= N) {
     float zr[32] = {};
@@ -197,13 +217,13 @@ __global__ __launch_bounds__(256) void embed_q4k_kernel(const uint8_t *quants,
 // piece c), each piece dequantized as wg_q4_dequant does.
 template <int LAYOUT>
 __global__ void embed_wide_kernel(const uint8_t *quants, const uint16_t *scales,
-                                  const int32_t *ids, int M, int K, int N, float *h, int ldh,
+                                  const EmbedIds ids, int M, int K, int N, float *h, int ldh,
                                   const wg_epilogue e) {
   const int pieces = K / 32;
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (int64_t)M * pieces) return;
   int m = (int)(t / pieces), c = (int)(t % pieces);
-  int n = ids[m];
+  int n = embed_id(ids, M, m, c == 0);
   float v[32];
   if (n < 0 || n >= N) {
     for (int j = 0; j < 32; j++) v[j] = 0.0f;
@@ -223,6 +243,41 @@ __global__ void embed_wide_kernel(const uint8_t *quants, const uint16_t *scales,
 }  // namespace wg
 
 using namespace wg;
+
+static int embed_rows(const wg_q4_matrix *emb, const EmbedIds &ids, int32_t M, float *h,
+                      int32_t ldh, const wg_epilogue *ep, void *stream) {
+  int rc = check_matrix(emb, "wg_embed");
+  if (rc) return rc;
+  WG_REQUIRE(ids.ids && h && M >= 1 && ldh >= emb->K, "wg_embed: bad arguments");
+  wg_epilogue e = {};
+  if (ep) e = *ep;
+  if (e.out16)
+    WG_REQUIRE(e.out16_w && e.ld_out16 >= emb->K && e.norm_mult_out != 0.0f,
+               "wg_embed: the prescaled half output needs weights, a stride and a prescale");
+  if (e.parts_out)
+    WG_REQUIRE(e.ld_parts_out >= emb->K / 4, "wg_embed: parts stride too small");
+  hipStream_t s = as_stream(stream);
+  if (emb->layout == WG_LAYOUT_ROWGROUP) {
+    int blocks = emb->K / 32;
+    int64_t n = (int64_t)M * blocks * 8;
+    embed_rowgroup_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+        (const uint32_t *)emb->quants, (const uint16_t *)emb->scales, emb->zeros, emb->zero, ids,
+        M, blocks, emb->N, h, ldh, e);
+  } else if (emb->layout == WG_LAYOUT_Q8 || emb->layout == WG_LAYOUT_Q6K) {
+    int64_t n = (int64_t)M * (emb->K / 32);
+    auto kernel = emb->layout == WG_LAYOUT_Q8 ? embed_wide_kernel<WG_LAYOUT_Q8>
+                                              : embed_wide_kernel<WG_LAYOUT_Q6K>;
+    kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>((const uint8_t *)emb->quants,
+                                                       (const uint16_t *)emb->scales, ids, M,
+                                                       emb->K, emb->N, h, ldh, e);
+  } else {
+    int supers = emb->K / 256;
+    int64_t n = (int64_t)M * supers * 8;
+    embed_q4k_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+        (const uint8_t *)emb->quants, ids, M, supers, emb->N, h, ldh, e);
+  }
+  return launched("wg_embed");
+}
 
 extern "C" {
 
@@ -262,39 +317,20 @@ int wg_swiglu(const float *gu, int32_t M, int32_t F, int32_t ldg, uint16_t *out,
   return launched("wg_swiglu");
 }
 
+
 int wg_embed(const wg_q4_matrix *emb, const int32_t *ids, int32_t M, float *h, int32_t ldh,
              const wg_epilogue *ep, void *stream) {
-  int rc = check_matrix(emb, "wg_embed");
-  if (rc) return rc;
-  WG_REQUIRE(ids && h && M >= 1 && ldh >= emb->K, "wg_embed: bad arguments");
-  wg_epilogue e = {};
-  if (ep) e = *ep;
-  if (e.out16)
-    WG_REQUIRE(e.out16_w && e.ld_out16 >= emb->K && e.norm_mult_out != 0.0f,
-               "wg_embed: the prescaled half output needs weights, a stride and a prescale");
-  if (e.parts_out)
-    WG_REQUIRE(e.ld_parts_out >= emb->K / 4, "wg_embed: parts stride too small");
-  hipStream_t s = as_stream(stream);
-  if (emb->layout == WG_LAYOUT_ROWGROUP) {
-    int blocks = emb->K / 32;
-    int64_t n = (int64_t)M * blocks * 8;
-    embed_rowgroup_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
-        (const uint32_t *)emb->quants, (const uint16_t *)emb->scales, emb->zeros, emb->zero, ids,
-        M, blocks, emb->N, h, ldh, e);
-  } else if (emb->layout == WG_LAYOUT_Q8 || emb->layout == WG_LAYOUT_Q6K) {
-    int64_t n = (int64_t)M * (emb->K / 32);
-    auto kernel = emb->layout == WG_LAYOUT_Q8 ? embed_wide_kernel<WG_LAYOUT_Q8>
-                                              : embed_wide_kernel<WG_LAYOUT_Q6K>;
-    kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>((const uint8_t *)emb->quants,
-                                                       (const uint16_t *)emb->scales, ids, M,
-                                                       emb->K, emb->N, h, ldh, e);
-  } else {
-    int supers = emb->K / 256;
-    int64_t n = (int64_t)M * supers * 8;
-    embed_q4k_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
-        (const uint8_t *)emb->quants, ids, M, supers, emb->N, h, ldh, e);
-  }
-  return launched("wg_embed");
+  // (ids are only read without a table)
+  return embed_rows(emb, EmbedIds{const_cast<int32_t *>(ids), nullptr, 0, nullptr}, M, h, ldh,
+                    ep, stream);
+}
+
+int wg_embed_drafts(const wg_q4_matrix *emb, int32_t *ids, int32_t rows, const int32_t *table,
+                    int32_t n_steps, const int32_t *cursor, float *h, int32_t ldh,
+                    const wg_epilogue *ep, void *stream) {
+  WG_REQUIRE(ids && table && cursor, "wg_embed_drafts: null argument");
+  WG_REQUIRE(rows >= 2 && n_steps >= 1, "wg_embed_drafts: %d rows, %d table rows", rows, n_steps);
+  return embed_rows(emb, EmbedIds{ids, table, n_steps, cursor}, rows, h, ldh, ep, stream);
 }
 
 }  // extern "C"

@@ -10,6 +10,7 @@
 // src/gpu/kernels.ts:1499-1523). Here those decisions read the picks and
 // drafts from device memory.
 #include "common.h"
+#include "pick_core.h"
 
 namespace wg {
 namespace {
@@ -28,16 +29,48 @@ __device__ inline int kept_of(const int32_t *ids, const int32_t *picks, int rows
 // ((W - 1) x D floats). Workgroup 0 also moves the step on: the accepted
 // picks into hist after the position, the last of them into ids[0], the
 // position by kept, kept into the log at the cursor, and the cursor on.
+// PARTS: the picks are finished here from a head GEMV's pick parts (as
+// wg_argmax_parts finishes them; wave w takes rows w and w + 4, its lanes
+// every part at once), and workgroup 0 writes them to picks_out.
+template <bool PARTS>
 __global__ __launch_bounds__(256) void verify_accept_kernel(
     const int32_t *ids_in, const int32_t *picks, int rows, const wg_conv_state *convs,
     int n_conv, int32_t *pos, int32_t *ids, int32_t *hist, int32_t hist_len, int32_t *kept_log,
-    int32_t log_len, int32_t *cursor) {
+    int32_t log_len, int32_t *cursor, const char *pick_parts, int32_t *picks_out) {
   __shared__ int32_t p[MAX_VERIFY_ROWS], d[MAX_VERIFY_ROWS];
-  if (threadIdx.x < rows) {
-    p[threadIdx.x] = picks[threadIdx.x];
-    d[threadIdx.x] = ids_in[threadIdx.x];
+  if constexpr (PARTS) {
+    constexpr int PER = WG_PICK_SLOTS / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int parts = min(*reinterpret_cast<const int *>(pick_parts), WG_PICK_SLOTS);
+    for (int i = wave; i < rows; i += 4) {
+      const uint2 *row =
+          reinterpret_cast<const uint2 *>(pick_parts + PICK_HEADER) + (int64_t)i * WG_PICK_SLOTS;
+      PickBest b{PICK_FLOOR, PICK_NONE};
+      for (int k0 = 0; k0 < PER && 64 * k0 < parts; k0 += 16) {
+        uint2 raw[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+          const int at = lane + 64 * (k0 + k);
+          raw[k] = at < parts ? row[at]
+                              : make_uint2(__float_as_uint(PICK_FLOOR), (uint32_t)PICK_NONE);
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+          b = pick_better(b, PickBest{__uint_as_float(raw[k].x), (int)raw[k].y});
+      }
+      b = pick_wave_best(b);
+      if (lane == 0) p[i] = b.id == PICK_NONE ? 0 : b.id;
+    }
+    if (threadIdx.x < rows) d[threadIdx.x] = ids_in[threadIdx.x];
+    __syncthreads();
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < rows) picks_out[threadIdx.x] = p[threadIdx.x];
+  } else {
+    if (threadIdx.x < rows) {
+      p[threadIdx.x] = picks[threadIdx.x];
+      d[threadIdx.x] = ids_in[threadIdx.x];
+    }
+    __syncthreads();
   }
-  __syncthreads();
   const int kept = kept_of(d, p, rows);
   const int l = blockIdx.y;
   if (l < n_conv) {
@@ -99,10 +132,35 @@ int wg_verify_accept(const int32_t *picks, int32_t rows, const wg_conv_state *co
   // ids is read (the drafts) and written (ids[0]) by the same launch: the
   // kernel reads the drafts into LDS before workgroup 0 writes ids[0]; the
   // other workgroups read ids[1 ..] only
-  verify_accept_kernel<<<grid, 256, 0, as_stream(stream)>>>(ids, picks, rows, convs, n_conv, pos,
-                                                           ids, hist, hist_len, kept_log,
-                                                           log_len, cursor);
+  verify_accept_kernel<false><<<grid, 256, 0, as_stream(stream)>>>(
+      ids, picks, rows, convs, n_conv, pos, ids, hist, hist_len, kept_log, log_len, cursor,
+      nullptr, nullptr);
   return launched("wg_verify_accept");
+}
+
+int wg_verify_accept_parts(const void *pick_parts, int32_t *picks_out, int32_t rows,
+                           const wg_conv_state *convs, int32_t n_conv, int32_t max_state,
+                           int32_t *pos, int32_t *ids, int32_t *hist, int32_t hist_len,
+                           int32_t *kept_log, int32_t log_len, int32_t *cursor, void *stream) {
+  WG_REQUIRE(pick_parts && picks_out && pos && ids && cursor,
+             "wg_verify_accept_parts: null argument");
+  WG_REQUIRE(((uintptr_t)pick_parts & 15) == 0, "wg_verify_accept_parts: parts not 16-byte aligned");
+  WG_REQUIRE(rows >= 1 && rows <= MAX_VERIFY_ROWS, "wg_verify_accept_parts: %d rows (1 to %d)",
+             rows, MAX_VERIFY_ROWS);
+  WG_REQUIRE(n_conv >= 0 && (n_conv == 0 || convs), "wg_verify_accept_parts: %d conv layers",
+             n_conv);
+  WG_REQUIRE(max_state >= 0, "wg_verify_accept_parts: state of %d floats", max_state);
+  WG_REQUIRE(!overlaps(picks_out, rows * 4, ids, rows * 4),
+             "wg_verify_accept_parts: the picks and the batch's ids overlap");
+  WG_REQUIRE(hist_len >= 0 && (hist || !hist_len) && log_len >= 0 && (kept_log || !log_len),
+             "wg_verify_accept_parts: bad history or log");
+  const int per = 256 * 8;
+  const unsigned gx = (unsigned)(max_state > 0 ? (max_state + per - 1) / per : 1);
+  dim3 grid(gx, (unsigned)(n_conv > 0 ? n_conv : 1));
+  verify_accept_kernel<true><<<grid, 256, 0, as_stream(stream)>>>(
+      ids, nullptr, rows, convs, n_conv, pos, ids, hist, hist_len, kept_log, log_len, cursor,
+      (const char *)pick_parts, picks_out);
+  return launched("wg_verify_accept_parts");
 }
 
 int wg_verify_drafts(int32_t *ids, int32_t rows, const int32_t *table, int32_t n_steps,

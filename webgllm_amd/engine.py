@@ -283,6 +283,10 @@ class Engine:
         # heads prepared inside the decode attention (False: head_prep, then
         # the attention)
         self.fuse_prep = True
+        # a device verify step's drafts read by the embedding and its picks
+        # finished by the accept (False: drafts, pick and accept launches)
+        self.fuse_verify = True
+        self._drafts = None
 
     # --- the attention caches, grown on demand ------------------------------
     def reserve(self, end: int) -> None:
@@ -364,7 +368,7 @@ class Engine:
             self._layer_rows(i, M, keep_prefixes)
         if self.probe:
             self.probe(len(self.w.layers) - 1, "output", self.h[:M])
-        self._head_rows(M, pick)
+        return self._head_rows(M, pick)
 
     def _embed_rows(self, M: int) -> None:
         """h = the rows' embeddings; the first norm's prescaled input and
@@ -372,10 +376,14 @@ class Engine:
         s, w = self.shape, self.w
         D = s.hidden
         first_norm = w.layers[0]["op_norm"] if w.layers else w.final_norm
-        ops.embed(w.embedding, self.ids[:M], out=self.h[:M],
-                  epilogue=L.Epilogue(mode=L.EPI_STORE, out16=self.x16.data_ptr(), ld_out16=D,
-                                      out16_w=first_norm.data_ptr(), norm_mult_out=PRESCALE,
-                                      parts_out=self.parts.data_ptr(), ld_parts_out=D // 4))
+        ep = L.Epilogue(mode=L.EPI_STORE, out16=self.x16.data_ptr(), ld_out16=D,
+                        out16_w=first_norm.data_ptr(), norm_mult_out=PRESCALE,
+                        parts_out=self.parts.data_ptr(), ld_parts_out=D // 4)
+        if self._drafts is not None:  # a verify step's drafts from the device table
+            table, cursor = self._drafts
+            ops.embed_drafts(w.embedding, self.ids, M, table, cursor, out=self.h[:M], epilogue=ep)
+        else:
+            ops.embed(w.embedding, self.ids[:M], out=self.h[:M], epilogue=ep)
 
     def _layer_rows(self, i: int, M: int, keep_prefixes: bool) -> None:
         """Layer i over the batch: h += operator(norm(h)); h += FFN(norm(h));
@@ -437,6 +445,8 @@ class Engine:
         emb, x16, logits = self.w.embedding, self.x16[:M], self.logits[:M]
         if pick and self.fuse_pick and ops.gemv_pick(
                 emb, x16, logits, self.pick_parts, self._norm_in(L.Epilogue(mode=L.EPI_STORE))):
+            if pick == "parts":  # the caller finishes the picks from the parts
+                return True
             if pick == "advance":
                 ops.argmax_parts(self.pick_parts, 1, self.ids, tops=self.tops[:1],
                                  pos=self.pos, hist=self.hist)
@@ -450,6 +460,7 @@ class Engine:
         elif pick:
             ops.argmax_rows(logits, ids=self.next_ids[:M], tops=self.tops[:M],
                             scratch=self.argmax_scratch)
+        return False
 
     # --- prompt batches on MFMA ----------------------------------------------
     def _prefill_ok(self) -> bool:
@@ -688,10 +699,24 @@ class Engine:
         prefix's picks into hist, the conv states rolled back, pos and
         ids[0] moved on: wg_verify_accept)."""
         rows = v["rows"]
-        ops.verify_drafts(self.ids, rows, v["table"], v["cursor"])
-        self._forward_rows(rows, keep_prefixes=True)
-        ops.verify_accept(self.next_ids[:rows], rows, v["convs"], self.pos, self.ids, self.hist,
-                          v["kept"], v["cursor"])
+        if not self.fuse_verify:
+            ops.verify_drafts(self.ids, rows, v["table"], v["cursor"])
+            self._forward_rows(rows, keep_prefixes=True)
+            ops.verify_accept(self.next_ids[:rows], rows, v["convs"], self.pos, self.ids,
+                              self.hist, v["kept"], v["cursor"])
+            return
+        # the drafts read by the embedding, the picks finished by the accept
+        self._drafts = (v["table"], v["cursor"])
+        try:
+            parts = self._forward_rows(rows, keep_prefixes=True, pick="parts")
+        finally:
+            self._drafts = None
+        if parts:
+            ops.verify_accept_parts(self.pick_parts, self.next_ids[:rows], rows, v["convs"],
+                                    self.pos, self.ids, self.hist, v["kept"], v["cursor"])
+        else:
+            ops.verify_accept(self.next_ids[:rows], rows, v["convs"], self.pos, self.ids,
+                              self.hist, v["kept"], v["cursor"])
 
     def capture_verify(self, rows: int = 5) -> None:
         """Captures one verify step of `rows` rows (a token and rows - 1

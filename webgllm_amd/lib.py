@@ -197,6 +197,9 @@ def load():
         "wg_attn_decode_noalloc": (C.c_int, [P, I32, I32, C.POINTER(AttnShape), P, P, P, I32,
                                              P, I32, P]),
         "wg_verify_accept": (C.c_int, [P, I32, P, I32, I32, P, P, P, I32, P, I32, P, P]),
+        "wg_verify_accept_parts": (C.c_int, [P, P, I32, P, I32, I32, P, P, P, I32, P, I32, P, P]),
+        "wg_embed_drafts": (C.c_int, [C.POINTER(Q4MatrixDesc), P, I32, P, I32, P, P, I32,
+                                      C.POINTER(Epilogue), P]),
         "wg_verify_drafts": (C.c_int, [P, I32, P, I32, P, P]),
         "wg_short_conv": (C.c_int, [P, I32, I32, I32, I32, P, P, P, P, P, I32, P]),
         "wg_conv_accept": (C.c_int, [P, I32, I32, I32, I32, P, P]),

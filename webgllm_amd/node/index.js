@@ -338,6 +338,13 @@ class HipGpu {
       /** Engine.accept after a verify batch with the handler's keep rule (src/handler.ts:1811-1887), on the device. */
       verifyAccept: (picks, rows, convs, nConv, maxState, pos, ids, hist, histLen, keptLog, logLen, cursor) =>
         call(addon.verifyAccept, ctx, o(picks), rows, o(convs), nConv, maxState, o(pos), o(ids), o(hist), histLen, o(keptLog), logLen, o(cursor)),
+      /** argmaxParts + verifyAccept in one launch (the picks also to picksOut). */
+      verifyAcceptParts: (parts, picksOut, rows, convs, nConv, maxState, pos, ids, hist, histLen, keptLog, logLen, cursor) =>
+        call(addon.verifyAcceptParts, ctx, o(parts), o(picksOut), rows, o(convs), nConv, maxState, o(pos), o(ids), o(hist),
+             histLen, o(keptLog), logLen, o(cursor)),
+      /** verifyDrafts + embed in one launch (rows 1.. from the table's row *cursor, also into ids). */
+      embedDrafts: (w, ids, rows, table, nSteps, cursor, h, epilogue = null, ldh = null) =>
+        call(addon.embedDrafts, ctx, matrix(w), o(ids), rows, o(table), nSteps, o(cursor), o(h), operands(epilogue), ldh),
       /** A verify step's drafts from a device table (src/draft.ts:15-45 runs on the host). */
       verifyDrafts: (ids, rows, table, nSteps, cursor) =>
         call(addon.verifyDrafts, ctx, o(ids), rows, o(table), nSteps, o(cursor)),

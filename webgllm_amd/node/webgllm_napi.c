@@ -901,6 +901,28 @@ static napi_value js_embed(napi_env env, napi_callback_info info) {
   DONE(wg_embed(&m, ids, M, h, ldh, has_ep ? &ep : NULL, ctx_stream(c)));
 }
 
+/* embedDrafts(ctx, matrix, ids, rows, table, nSteps, cursor, h, epilogue?,
+ * ldh?): verifyDrafts and embed in one launch (row 0 embeds ids[0], rows
+ * 1 .. rows - 1 the table's row *cursor, also written to ids). */
+static napi_value js_embed_drafts(napi_env env, napi_callback_info info) {
+  ARGS(10);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  MATRIX_ARG(1, m);
+  INT32_ARG(3, rows);
+  INT32_ARG(5, n_steps);
+  if (rows < 2 || n_steps < 1) return throw_limits(env, "embedDrafts: %d rows, %d table rows", rows, n_steps);
+  int32_t ldh = m.K;
+  if (!is_nullish(env, argv[9]) && !get_i32(env, argv[9], &ldh)) return type_error(env, "ldh must be an integer");
+  OPERAND(2, int32_t, ids, (uint64_t)rows * 4, 0, "ids");
+  OPERAND(4, const int32_t, table, (uint64_t)n_steps * (uint64_t)(rows - 1) * 4, 0, "table");
+  OPERAND(6, const int32_t, cursor, 4, 0, "cursor");
+  OPERAND(7, float, h, span(rows, ldh, m.K) * 4, 0, "h");
+  wg_epilogue ep;
+  const int has_ep = !is_nullish(env, argv[8]);
+  if (has_ep && !read_epilogue(env, argv[8], rows, m.K, &ep)) return NULL;
+  DONE(wg_embed_drafts(&m, ids, rows, table, n_steps, cursor, h, ldh, has_ep ? &ep : NULL, ctx_stream(c)));
+}
+
 /* normToH2(ctx, x, M, D, w, eps, out, rowScale, ldx?, ldo?): NORM_TO_H2
  * with PRESCALE 32 (kernels.ts:89, :1195-1242). */
 static napi_value js_norm_to_h2(napi_env env, napi_callback_info info) {
@@ -1140,6 +1162,31 @@ static napi_value js_verify_accept(napi_env env, napi_callback_info info) {
   OPERAND(12, int32_t, cursor, 4, 0, "cursor");
   DONE(wg_verify_accept(picks, rows, convs, n_conv, max_state, pos, ids, hist, hist_len, kept_log,
                         log_len, cursor, ctx_stream(c)));
+}
+
+/* verifyAcceptParts(ctx, parts, picksOut, rows, convs, nConv, maxState, pos,
+ * ids, hist, histLen, keptLog, logLen, cursor): argmaxParts and
+ * verifyAccept in one launch (the picks also to picksOut). */
+static napi_value js_verify_accept_parts(napi_env env, napi_callback_info info) {
+  ARGS(14);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  INT32_ARG(3, rows);
+  INT32_ARG(5, n_conv);
+  INT32_ARG(6, max_state);
+  INT32_ARG(10, hist_len);
+  INT32_ARG(12, log_len);
+  if (rows < 1 || rows > 8 || n_conv < 0 || hist_len < 0 || log_len < 0)
+    return throw_limits(env, "verifyAcceptParts: %d rows, %d conv layers", rows, n_conv);
+  OPERAND(1, const void, parts, (uint64_t)wg_pick_parts_bytes(rows), 0, "parts");
+  OPERAND(2, int32_t, picks_out, (uint64_t)rows * 4, 0, "picksOut");
+  OPERAND(4, const wg_conv_state, convs, (uint64_t)n_conv * sizeof(wg_conv_state), n_conv == 0, "convs");
+  OPERAND(7, int32_t, pos, 4, 0, "pos");
+  OPERAND(8, int32_t, ids, (uint64_t)rows * 4, 0, "ids");
+  OPERAND(9, int32_t, hist, (uint64_t)hist_len * 4, hist_len == 0, "hist");
+  OPERAND(11, int32_t, kept_log, (uint64_t)log_len * 4, log_len == 0, "keptLog");
+  OPERAND(13, int32_t, cursor, 4, 0, "cursor");
+  DONE(wg_verify_accept_parts(parts, picks_out, rows, convs, n_conv, max_state, pos, ids, hist,
+                              hist_len, kept_log, log_len, cursor, ctx_stream(c)));
 }
 
 /* verifyDrafts(ctx, ids, rows, table, nSteps, cursor): a verify step's
@@ -1472,6 +1519,8 @@ static napi_value init(napi_env env, napi_value exports) {
       {"convStates", js_conv_states},
       {"verifyAccept", js_verify_accept},
       {"verifyDrafts", js_verify_drafts},
+      {"verifyAcceptParts", js_verify_accept_parts},
+      {"embedDrafts", js_embed_drafts},
       {"argmaxScratchBytes", js_argmax_scratch_bytes},
       {"argmax", js_argmax},
       {"argmaxAdvance", js_argmax_advance},

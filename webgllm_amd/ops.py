@@ -421,6 +421,36 @@ def verify_accept(picks, rows, convs, pos, ids, hist, kept_log, cursor):
                                       _p(cursor), _stream()))
 
 
+def verify_accept_parts(parts, picks_out, rows, convs, pos, ids, hist, kept_log, cursor):
+    """wg_verify_accept_parts: the batch's picks finished from a head GEMV's
+    pick parts into picks_out, then verify_accept's keep, rollback and
+    advance, in one launch."""
+    arr, n, big = convs
+    for t, name in ((picks_out, "picks_out"), (pos, "pos"), (ids, "ids"), (hist, "hist"),
+                    (kept_log, "kept_log"), (cursor, "cursor")):
+        if t.dtype != torch.int32 or not t.is_cuda:
+            raise ValueError(f"{name} must be an int32 device tensor")
+    L.check(L.load().wg_verify_accept_parts(_p(parts), _p(picks_out), rows, _p(arr), n, big,
+                                            _p(pos), _p(ids), _p(hist), hist.numel(),
+                                            _p(kept_log), kept_log.numel(), _p(cursor),
+                                            _stream()))
+
+
+def embed_drafts(m: Q4Matrix, ids: torch.Tensor, rows: int, table: torch.Tensor, cursor,
+                 out: torch.Tensor, epilogue: "L.Epilogue | None" = None) -> torch.Tensor:
+    """verify_drafts then embed in one launch: row 0 embeds ids[0], rows
+    1 .. rows - 1 the draft table's row *cursor (also written to ids)."""
+    table = _dev(table, torch.int32)
+    if table.dim() != 2 or table.shape[1] != rows - 1:
+        raise ValueError(f"the draft table must be [steps, {rows - 1}]")
+    _dev(out, torch.float32)
+    L.check(L.load().wg_embed_drafts(C.byref(m.desc), _p(ids), rows, _p(table), table.shape[0],
+                                     _p(cursor), _p(out), out.shape[-1],
+                                     C.byref(epilogue) if epilogue is not None else None,
+                                     _stream()))
+    return out
+
+
 def verify_drafts(ids, rows, table, cursor):
     """wg_verify_drafts: ids[1:rows] = table[*cursor] (int32 [steps, rows - 1])."""
     table = _dev(table, torch.int32)
