@@ -427,9 +427,15 @@ int launch_mfma(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float 
   constexpr size_t LDS =
       (size_t)S * KS * Slot<ZK, NP>::BYTES + mfma_round<ZK, NP, KS, S>() * KS * 128 * 4;
   static_assert(LDS + KS * 160 <= 160 * 1024, "LDS");
-  // (SHORT_CONV: a tile a channel quad)
-  const int grid = persistent_grid(e.mode == WG_EPI_SHORT_CONV ? G / 3 : NT,
-                                   tuning("gemv_mfma_wg_per_cu"));
+  // (SHORT_CONV: a tile a channel quad.) Workgroups a CU: the knob, or by
+  // default 1, and 2 where each still takes 8 tiles or more and two fit the
+  // LDS (a 65536-row head at 5 tokens: the verify step 1897 -> 1902 steps/s;
+  // with 4 tiles a workgroup, 16384 x 2048, the step was slower)
+  const int units = e.mode == WG_EPI_SHORT_CONV ? G / 3 : NT;
+  int per_cu = tuning("gemv_mfma_wg_per_cu");
+  if (!per_cu)
+    per_cu = 2 * (LDS + KS * 160) <= 160 * 1024 && units >= 16 * persistent_grid(1 << 30, 1) ? 2 : 1;
+  const int grid = persistent_grid(units, per_cu);
   if (e.pick_parts && grid > WG_PICK_SLOTS)
     return fail(WG_ERR_UNSUPPORTED, "wg_q4_gemv: %d workgroups for the pick's parts", grid);
   auto q = (const uint8_t *)w->quants;

@@ -78,7 +78,7 @@ static Knob g_knobs[] = {
     {"gemv_few_stream", 1, 0, 1},        // 3 to 8 tokens on the streaming kernel (0: row groups)
     {"gemv_few_wg_per_cu", 1, 1, 16},    // its persistent workgroups per CU
     {"gemv_mfma", 1, 0, 2},              // row-group GEMV on MFMA: 1 for 3 to 8 tokens, 2 also 1 and 2, 0 never
-    {"gemv_mfma_wg_per_cu", 1, 1, 16},   // its persistent workgroups per CU
+    {"gemv_mfma_wg_per_cu", 0, 0, 16},   // its persistent workgroups per CU (0: by shape)
     {"gemv_mfma_pairs", 4, 2, 8},        // its block pairs a wave (2, 4, 8)
     {"attn_prefill_mfma", 4, 0, 4},      // prompt attention: MFMA waves a workgroup (1, 2, 4), 0 VALU
     {"attn_mfma", 1, 0, 2},              // decode attention in one launch on MFMA: 1 where it is faster (past 8 queries a KV head, from 16384 keys, outside the XCD-grouped split form's range with KV heads a multiple of 8, else up to 2048 keys), 2 always, 0 never
