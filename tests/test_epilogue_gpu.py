@@ -91,12 +91,13 @@ def test_swiglu_epilogue(hip, fmt, M):
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "q8"])
-@pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (32, 8, 128)])
+# K = 4096 at 32/8 heads: more row groups than the grid's waves, where the
+# rotation's table rows are fetched after the activations
+@pytest.mark.parametrize("H,KV,hd,K", [(14, 2, 64, 1024), (32, 8, 128, 1024), (32, 8, 128, 4096)])
 @pytest.mark.parametrize("M,pos0", [(1, 0), (1, 1500), (4, 1022)])
-def test_rope_kv_epilogue(hip, fmt, H, KV, hd, M, pos0):
+def test_rope_kv_epilogue(hip, fmt, H, KV, hd, K, M, pos0):
     from webgllm_amd import engine as E, lib as L, ops
-    shape = E.ModelShape("t", 1024, 1, H, KV, hd, 4, 4, fmt)
-    K = 1024
+    shape = E.ModelShape("t", K, 1, H, KV, hd, 4, 4, fmt)
     N = shape.qkv_rows
     rng = np.random.default_rng(H + M + pos0)
     m = _matrix(fmt, N, K, seed=5, row_order=E.qkv_row_order(shape))

@@ -27,7 +27,7 @@ namespace {
 // activations) lead the list: the first 14 dwords of the arguments arrive
 // in scalar registers with the wave, so the first loads wait for no
 // argument fetch.
-template <int M, int ZK, int NB, int KS, int MODE>
+template <int M, int ZK, int NB, int KS, int MODE, bool LATE = false>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(
     const uint4 *__restrict__ quants, const uint16_t *__restrict__ scales,
     const void *__restrict__ zeros, const uint16_t *__restrict__ x, int G, int B, int ldx,
@@ -56,10 +56,15 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
   const int g_first = blockIdx.x * RGW + slot;
   Unit<ZK, NB> U0, U1;
   load_unit_at<ZK, NB>(U0, quants, scales, zeros, min(g_first, G - 1), B, bj);
-  // and the first row group's epilogue operands (the waves that finish)
+  // and the first row group's epilogue operands (the waves that finish).
+  // LATE (the rotation, where waves have later row groups to hide them
+  // behind): the table rows hang on the position, a pointer chase, so they
+  // go out after the activations and the norm's parts, whose waits would
+  // otherwise take in that chase too. Where every wave has one row group,
+  // nothing is left to hide them behind, and they go out first.
   const int pos0 = epi_pos0<MODE>(e);
   EpiPre pnext = {};
-  if (part == 0) epi_prefetch<M, MODE>(e, g_first, G, pos0, pnext);
+  if (!LATE && part == 0) epi_prefetch<M, MODE>(e, g_first, G, pos0, pnext);
 
   // This lane's activations, paired, and their block sums (times 2^-24), once.
   PairedActs a[M][NB];
@@ -83,6 +88,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
     }
   float scale[M];
   input_scales_wg<M, 4>(e, scale, nred);
+  if (LATE && part == 0) epi_prefetch<M, MODE>(e, g_first, G, pos0, pnext);
 
   // one row group: the 4 rows' sums for each token, reduced (into part 0's
   // lanes' tot)
@@ -208,6 +214,9 @@ int launch_stream(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, i
   } else if (e.mode == WG_EPI_SWIGLU)
     gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_SWIGLU><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, G, B, ldx,
                                                                          y, ldy, e);
+  else if (e.mode == WG_EPI_ROPE_KV && G > grid * RGW)
+    gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_ROPE_KV, true><<<grid, 256, 0, s>>>(
+        q, sc, w->zeros, x, G, B, ldx, y, ldy, e);
   else if (e.mode == WG_EPI_ROPE_KV)
     gemv_stream_kernel<M, ZK, NB, KS, WG_EPI_ROPE_KV><<<grid, 256, 0, s>>>(q, sc, w->zeros, x, G, B,
                                                                           ldx, y, ldy, e);
