@@ -1,7 +1,8 @@
 """Headline benchmark: batch-1 Q4 decode of the Llama-3-8B-shaped model
 (hidden 4096, 32 layers, 32/8 heads of 128, intermediate 14336, vocab
-128256, GGUF Q4_K weights repacked at load as the reference does, fp16 KV
-cache of 4096) on one MI355X.
+128256, GGUF Q4_K weights repacked at load into the reference's 32-blocks
+with Q4_K's own scales kept beside them, fp16 KV cache of 4096) on one
+MI355X.
 
 A step is one greedy decode token (one replay of the captured token graph:
 32 layers of Q4_K GEMVs, attention over the cache, the head and the pick).
@@ -33,7 +34,8 @@ HBM_PEAK_GBPS = 8000.0
 # read at least, whatever layout the device keeps (GGUF Q4_0 18 B / 32,
 # Q4_K 144 B / 256, MatMulNBits q4 16 B of nibbles + a half scale + half a
 # byte of zero point / 32, Q8_0 34 B / 32, Q6_K 210 B / 256).
-BPW = {"q4_0": 18 / 32, "q4_k": 144 / 256, "q4_k_rowgroup": 144 / 256, "nbits": 18.5 / 32,
+BPW = {"q4_0": 18 / 32, "q4_k": 144 / 256, "q4_k_rowgroup": 144 / 256,
+       "q4_k_records": 144 / 256, "nbits": 18.5 / 32,
        "q8_0": 34 / 32, "q8": 34 / 32, "q6_k": 210 / 256}
 
 
@@ -111,9 +113,13 @@ def gemv_roofline(mats, x, parts, out16, eps, reps=6, fmt="q4_k"):
     us = e0.elapsed_time(e1) * 1e3 / launches
     algo = gemv_bytes(m.N, m.K, 1, fmt)
     achieved = algo / (us * 1e-6) / 1e9
-    # the device layout's bytes: nibbles, half scales, half zero points, x
-    # (halves), the norm's parts and the half SwiGLU output
+    # the device layout's bytes: nibbles and scales (Q4_K records, or half
+    # scales and zero points), x (halves), the norm's parts and the half
+    # SwiGLU output
     stored = m.nbytes + D * 2 + (D // 4) * 4 + F * 2
+    scales = ("Q4_K scale records (d, dmin, 6-bit scales and mins: 0.5625 bytes a weight "
+              "with the nibbles)" if m.zero == L.ZERO_Q4K else "half scale + half zero per 32 "
+              "weights")
     stored_gbps = stored / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
@@ -125,8 +131,8 @@ def gemv_roofline(mats, x, parts, out16, eps, reps=6, fmt="q4_k"):
             "avg_launch_us": round(us, 3), "launches": launches,
             "stored_layout": {"bytes_per_launch": stored, "achieved": round(stored_gbps, 1),
                               "frac": round(stored_gbps / HBM_PEAK_GBPS, 4),
-                              "what": "the device's layout: 4-bit + half scale + half zero "
-                                      "per 32 weights, x, norm parts, half SwiGLU out"}}
+                              "what": f"the device's layout: 4-bit + {scales}, x, norm "
+                                      "parts, half SwiGLU out"}}
 
 
 def measured_traffic():
@@ -180,6 +186,12 @@ def oracle_matrix(m):
         src = np.ascontiguousarray(rec.transpose(0, 2, 1, 3)).reshape(-1)
         qm = O.QuantMatrix(m.N, m.K, "halves")
         O.pack_q4_k(qm, 0, src, m.N)
+        return qm
+    if m.zero == L.ZERO_Q4K:  # the super-blocks behind the records, packed as the reference does
+        src = O.q4k_from_records(m.quants.cpu().numpy(), m.scales.cpu().numpy().view(np.uint8),
+                                 m.N, m.K)
+        qm = O.QuantMatrix(m.N, m.K, "halves")
+        O.pack_q4_k(qm, 0, src.reshape(-1), m.N)
         return qm
     qm = O.QuantMatrix(m.N, m.K, {L.ZERO_8: False, L.ZERO_U8: True, L.ZERO_F16: "halves"}[m.zero])
     qm.quants[:] = m.quants.cpu().numpy().view(np.uint32)
@@ -601,8 +613,9 @@ def workload_llama8b_prefill(args):
     tf = flop / (gms * 1e-3) / 1e12
     roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
             "frac": round(tf / 2500.0, 4), "traffic": None,
-            "kernel": f"gemm_q4_kernel gate|up 512 x {2 * F} x {D} (Q4_K repacked, f16 zero "
-                      f"points), column map to gate | up", "flops_per_launch": flop,
+            "kernel": f"gemm_q4_kernel gate|up 512 x {2 * F} x {D} (Q4_K repacked; f16 zero "
+                      f"points, rebuilt from the Q4_K records by one launch before it), column "
+                      f"map to gate | up", "flops_per_launch": flop,
             "avg_launch_us": round(gms * 1e3, 2), "launches": 60}
     cpu = None
     if not args.no_cpu:
@@ -1134,7 +1147,8 @@ def main():
             "model": shape.name, "layers": shape.layers, "hidden": shape.hidden,
             "vocab": shape.vocab,
             "weights": "random GGUF Q4_K super-blocks, repacked on the GPU to the "
-                       "reference's 32-blocks (packQ4_K)",
+                       "reference's 32-blocks (packQ4_K's quants) with Q4_K's own scales and "
+                       "mins kept in 64-byte records a row group (0.5625 bytes a weight)",
             "activations": "f16", "accumulate": "f32",
             "global_batch": 1, "seq_len": args.ctx, "parallelism": "none",
         },

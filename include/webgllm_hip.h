@@ -152,21 +152,36 @@ int wg_ctx_staging(wg_ctx *ctx, int32_t *slots, size_t *bytes);
 #define WG_LAYOUT_Q6K 3
 
 /* Zero points of WG_LAYOUT_ROWGROUP: none (8, Q4_0), one u8 a block
- * (MatMulNBits), or one half a block (Q4_K repacked: QuantMatrix.zeroHalves). */
+ * (MatMulNBits), or one half a block (Q4_K repacked: QuantMatrix.zeroHalves).
+ * WG_ZERO_Q4K keeps Q4_K's own scales instead of per-block halves, at the
+ * file's 0.5625 bytes a weight: quants as above (a block whose d' below is
+ * 0 holds 15s, as packQ4_K writes it), no zeros array, and in `scales` one
+ * 64-byte record a row group and super-block of 256 columns, at byte (g *
+ * K / 256 + s) * 64: bytes 0-15 the 4 rows' (half d, half dmin), bytes
+ * 16-63 the 8 blocks' 6-bit scales and mins (get_scale_min_k4), blocks 2i
+ * and 2i + 1 in the 96 bits of dwords 4 + 3i .. 6 + 3i (block 2i in bits
+ * 0-47), a block's row r at bits 12r (scale) and 12r + 6 (min). Dequant
+ * rebuilds packQ4_K's (d', z') bit for bit (d' = half(d sc), z' =
+ * half(dmin m / d'), src/repack.ts:100-168); the GEMVs weigh a block as d'
+ * q - dmin m (the zero term without z's half rounding: within 2^-11 of
+ * it); the prefill GEMM takes (d', z') rebuilt into a workspace. K a
+ * multiple of 256. */
 #define WG_ZERO_8 0
 #define WG_ZERO_U8 1
 #define WG_ZERO_F16 2
+#define WG_ZERO_Q4K 3
 
 /* A quantized matrix of any layout above (the name is historical: 8- and
  * 6-bit layouts use the same descriptor). */
 typedef struct {
   int32_t N;      /* output rows, a multiple of 4 */
-  int32_t K;      /* inputs per row, a multiple of 32 (256 for WG_LAYOUT_Q4K, Q6K) */
+  int32_t K;      /* inputs per row, a multiple of 32 (256 for WG_LAYOUT_Q4K, Q6K, WG_ZERO_Q4K) */
   int32_t layout; /* WG_LAYOUT_* */
   int32_t zero;   /* WG_ZERO_* (WG_LAYOUT_ROWGROUP only) */
   const void *quants; /* ROWGROUP: N*K/2 bytes; Q4K: N*K/256*144; Q8: N*K; Q6K: N*K/256*208 */
-  const void *scales; /* ROWGROUP, Q8: N*K/32 halves; Q6K: N*K/256 halves; Q4K: unused */
-  const void *zeros;  /* ROWGROUP: N*K/32 u8 or halves, or NULL for WG_ZERO_8 */
+  const void *scales; /* ROWGROUP, Q8: N*K/32 halves (WG_ZERO_Q4K: N*K/256*16 bytes of
+                         records); Q6K: N*K/256 halves; Q4K: unused */
+  const void *zeros;  /* ROWGROUP: N*K/32 u8 or halves, or NULL for WG_ZERO_8, WG_ZERO_Q4K */
 } wg_q4_matrix;
 
 /* Bytes of device memory each array of a matrix needs. */
@@ -182,7 +197,9 @@ int wg_q4_sizes(int32_t N, int32_t K, int32_t layout, int32_t zero, size_t *quan
 int wg_repack_q4_0(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *src,
                    const int32_t *src_rows, void *stream);
 /* packQ4_K (src/repack.ts:100-168): Q4_K super-blocks -> ROWGROUP, WG_ZERO_F16,
- * bit-exact to the reference's (d', z') chain. */
+ * bit-exact to the reference's (d', z') chain; or, into a WG_ZERO_Q4K
+ * matrix, the same quants with the file's d, dmin and 6-bit scales and mins
+ * regrouped into its records. */
 int wg_repack_q4_k(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *src,
                    const int32_t *src_rows, void *stream);
 /* Q4_K super-blocks -> WG_LAYOUT_Q4K (a regrouping copy). */
@@ -449,7 +466,12 @@ int wg_q4_gemv(const wg_q4_matrix *w, const uint16_t *x, int32_t M, int32_t ldx,
  * grows on demand; launches on one stream run in turn. A launch made while
  * its stream is being captured into a graph runs unsplit (the graph holds
  * no workspace, so it may replay on any stream and beside eager GEMMs), and
- * so its sums may differ in the last bits from an eager launch's. */
+ * so its sums may differ in the last bits from an eager launch's.
+ * A WG_ZERO_Q4K matrix's (d', z') halves are rebuilt first, bit for bit as
+ * packQ4_K makes them, into a second workspace of the same kind (one more
+ * launch; N*K/8 bytes), so its results are a WG_ZERO_F16 matrix's; such a
+ * call made while the stream is being captured returns WG_ERR_UNSUPPORTED
+ * before any launch. */
 int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda, float *C,
                int32_t ldc, const float *residual, int32_t ldr, const float *row_scale,
                const int32_t *col_of, void *stream);

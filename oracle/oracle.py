@@ -251,6 +251,53 @@ def pack_q4_k(m: QuantMatrix, row0: int, src: np.ndarray, rows: int, src_rows=No
         raise ValueError(f"packQ4_K failed ({rc})")
 
 
+def q4k_from_records(quants: np.ndarray, recs: np.ndarray, N: int, K: int) -> np.ndarray:
+    """The GGUF Q4_K super-blocks ([N][K/256][144] bytes, rows in stored
+    order) behind a backend matrix of Q4_K records (WG_ZERO_Q4K): the
+    inverse of its layout, for the checks. quants: the row-group nibble rows
+    (byte k of a block row: weight k low, weight k + 16 high); recs: a
+    64-byte record a row group and super-block (the 4 rows' d and dmin, then
+    block pair i's 96 bits at byte 16 + 12 i, row r of a block at bits 12 r
+    (scale) and 12 r + 6 (min)). The 12 scale bytes are get_scale_min_k4's
+    encoding (src/repack.ts:127-140). A block packQ4_K makes constant comes
+    back with 15s, which packQ4_K reads as the file's own nibbles."""
+    G, S = N // 4, K // 256
+    q = np.asarray(quants, dtype=np.uint8).reshape(G, S, 8, 4, 16)  # g, s, block, row, byte
+    rec = np.asarray(recs, dtype=np.uint8).reshape(G, S, 64)
+    out = np.zeros((G, 4, S, 144), np.uint8)
+    out[..., 0:4] = rec[:, :, 0:16].reshape(G, S, 4, 4).transpose(0, 2, 1, 3)
+    bits = rec[:, :, 16:64].reshape(G, S, 4, 12)  # block pair i's 96 bits
+    lo = bits[..., 0:8].copy().view("<u8")[..., 0]
+    hi = bits[..., 8:12].copy().view("<u4")[..., 0].astype(np.uint64)
+    sc = np.zeros((G, S, 8, 4), np.uint8)
+    mn = np.zeros((G, S, 8, 4), np.uint8)
+    for j in range(8):
+        for r in range(4):
+            for which, dst in ((0, sc), (1, mn)):
+                bit = 48 * (j & 1) + 12 * r + 6 * which
+                pair_lo, pair_hi = lo[:, :, j >> 1], hi[:, :, j >> 1]
+                if bit + 6 <= 64:
+                    v = (pair_lo >> np.uint64(bit)) & np.uint64(63)
+                elif bit >= 64:
+                    v = (pair_hi >> np.uint64(bit - 64)) & np.uint64(63)
+                else:
+                    v = ((pair_lo >> np.uint64(bit)) | (pair_hi << np.uint64(64 - bit))) & np.uint64(63)
+                dst[:, :, j, r] = v.astype(np.uint8)
+    scb = np.zeros((G, S, 4, 12), np.uint8)  # g, s, row, byte
+    s_, m_ = sc.transpose(0, 1, 3, 2), mn.transpose(0, 1, 3, 2)  # g, s, row, block
+    scb[..., 0:4] = (s_[..., 0:4] & 63) | ((s_[..., 4:8] >> 4) << 6)
+    scb[..., 4:8] = (m_[..., 0:4] & 63) | ((m_[..., 4:8] >> 4) << 6)
+    scb[..., 8:12] = (s_[..., 4:8] & 15) | ((m_[..., 4:8] & 15) << 4)
+    out[..., 4:16] = scb.transpose(0, 2, 1, 3)
+    qe = q[:, :, 0::2].transpose(0, 3, 1, 2, 4)  # g, row, s, pair, byte: blocks 2i
+    qo = q[:, :, 1::2].transpose(0, 3, 1, 2, 4)  # blocks 2i + 1
+    chunk = np.zeros(qe.shape[:-1] + (32,), np.uint8)
+    chunk[..., 0:16] = (qe & 15) | ((qo & 15) << 4)
+    chunk[..., 16:32] = (qe >> 4) | (qo & 0xF0)
+    out[..., 16:144] = chunk.reshape(G, 4, S, 128)
+    return out.reshape(N, S * 144)
+
+
 def pack_nbits(m: QuantMatrix, row0: int, quant, scale_bytes, zp, rows: int, src_rows=None):
     quant = np.ascontiguousarray(quant, dtype=np.uint8)
     scale_bytes = np.ascontiguousarray(scale_bytes).view(np.uint8)

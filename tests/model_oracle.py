@@ -45,6 +45,11 @@ def _dense_stored(m, threads=0) -> np.ndarray:
         qm = O.QuantMatrix(N, K, "halves")
         O.pack_q4_k(qm, 0, src, N)
         return qm.dense(threads)
+    if m.zero == L.ZERO_Q4K:  # the super-blocks behind the records, through packQ4_K
+        src = O.q4k_from_records(_np(m.quants), _np(m.scales).view(np.uint8), N, K)
+        qm = O.QuantMatrix(N, K, "halves")
+        O.pack_q4_k(qm, 0, src.reshape(-1), N)
+        return qm.dense(threads)
     qm = O.QuantMatrix(N, K, {L.ZERO_8: False, L.ZERO_U8: True, L.ZERO_F16: "halves"}[m.zero])
     qm.quants[:] = _np(m.quants).view(np.uint32)
     qm.scales[:] = _np(m.scales).view(np.uint16)

@@ -32,6 +32,14 @@ def test_sizes():
     assert z.value == 4096 * 128
     L.check(lib.wg_q4_sizes(4096, 4096, L.LAYOUT_Q4K, 0, C.byref(q), C.byref(s), C.byref(z)))
     assert q.value == 4096 * 16 * 144
+    # Q4_K records: the file's 144 bytes a super-block row, as 128 nibble
+    # bytes and a 64-byte record a row group (16 a row), no zeros array
+    L.check(lib.wg_q4_sizes(4096, 4096, L.LAYOUT_ROWGROUP, L.ZERO_Q4K, C.byref(q), C.byref(s),
+                            C.byref(z)))
+    assert (q.value, s.value, z.value) == (4096 * 16 * 128, 4096 * 16 * 16, 0)
+    assert q.value + s.value == 4096 * 16 * 144
+    with pytest.raises(L.WgError, match="multiple of 256"):
+        L.check(lib.wg_q4_sizes(4, 32, L.LAYOUT_ROWGROUP, L.ZERO_Q4K, None, None, None))
     with pytest.raises(L.WgError, match="multiple of 4"):
         L.check(lib.wg_q4_sizes(6, 32, 0, 0, None, None, None))
     with pytest.raises(L.WgError, match="multiple of 256"):
@@ -91,7 +99,7 @@ def test_repack_rejects_mismatched_layouts():
     assert "without zero points" in L.last_error()
     d = _desc(zero=L.ZERO_8)
     assert lib.wg_repack_q4_k(C.byref(d), 0, 8, 0x1000, None, None) == -1
-    assert "fractional zero points" in L.last_error()
+    assert "half zero points or Q4_K records" in L.last_error()
     assert lib.wg_repack_q4_0(C.byref(d), 4, 8, 0x1000, None, None) == -1
     assert "outside the matrix" in L.last_error()
     d = _desc(zero=L.ZERO_8)

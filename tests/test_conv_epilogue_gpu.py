@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 
 # the kernel forms: streaming GEMVs for every row count, MFMA for every one
 FORMS = {"stream": {"gemv_mfma": 0, "gemv_few_stream": 1}, "mfma": {"gemv_mfma": 2}}
-ROWGROUP_FMTS = ["q4_0", "nbits", "q4_k_rowgroup"]
+ROWGROUP_FMTS = ["q4_0", "nbits", "q4_k_rowgroup", "q4_k_records"]
 
 
 def _t(a):

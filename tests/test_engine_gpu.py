@@ -23,6 +23,7 @@ FAMILIES = {
     "qwen-nbits": dict(fmt="nbits", heads=7, kv=1),
     "lfm2-q4_0": dict(fmt="q4_0", conv_layers=(0, 2), qk_norm=True),
     "q4_k-rowgroup": dict(fmt="q4_k_rowgroup"),
+    "q4_k-records": dict(fmt="q4_k_records"),
     # as real GGUF files: a Q6_K embedding and output head; Q8_0 tensors; and
     # tensors the loader requantizes to 8 bits (Q4_K_M's Q6_K/Q5_K ones)
     "gguf-q4_k-q6_k-head": dict(fmt="q4_k_rowgroup", embed_fmt="q6_k"),

@@ -33,7 +33,14 @@ def _matrix(fmt, N, K, seed, row_order=None):
     return w.matrix(N, K, row_order)
 
 
-FMTS = ["q4_0", "nbits", "q4_k", "q4_k_rowgroup", "q8_0", "q6_k"]
+FMTS = ["q4_0", "nbits", "q4_k", "q4_k_rowgroup", "q4_k_records", "q8_0", "q6_k"]
+
+
+def _tol(fmt, tight):
+    # Q4_K records weigh a block's zero term as dmin m, not packQ4_K's d'
+    # half(dmin m / d') that the oracle computes: the north star's 1e-3
+    # then, rather than the float32 sums' tighter margin
+    return 1e-3 if fmt == "q4_k_records" else tight
 
 
 @pytest.mark.parametrize("fmt", FMTS)
@@ -65,7 +72,7 @@ def test_store_normed_residual_prescaled_out(hip, fmt, M, N, K):
     want = res + (O.halves_to_f32(x16).astype(np.float64) @ W.T) * r
     got = y.cpu().numpy()
     # float32 sums (products exact): well inside the 1e-3 bar
-    assert rel_l2(got, want) <= 1e-4
+    assert rel_l2(got, want) <= _tol(fmt, 1e-4)
     assert rel_l2(_h(out16), got * w_next / 32) <= 1e-3
     want_parts = (got.astype(np.float64).reshape(M, N // 4, 4) ** 2).sum(-1)
     assert rel_l2(parts_out.cpu().numpy(), want_parts) <= 1e-4
@@ -90,7 +97,7 @@ def test_swiglu_epilogue(hip, fmt, M):
     assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -9 + 1e-3 * np.abs(want).max())
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "q8"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_k", "q4_k_records", "q8"])
 # K = 4096 at 32/8 heads: more row groups than the grid's waves, where the
 # rotation's table rows are fetched after the activations
 @pytest.mark.parametrize("H,KV,hd,K", [(14, 2, 64, 1024), (32, 8, 128, 1024), (32, 8, 128, 4096)])
@@ -126,7 +133,7 @@ def test_rope_kv_epilogue(hip, fmt, H, KV, hd, K, M, pos0):
             want = O.head_prep(qkv[t, h * hd:(h + 1) * hd], None, rope, hd, hd, p, 0.0,
                                1 / math.sqrt(hd), False)
             got = qg[t, h * hd:(h + 1) * hd]
-            assert rel_l2(got, want) <= 1e-4
+            assert rel_l2(got, want) <= _tol(fmt, 1e-4)
             assert np.all(np.abs(got - want) <= 1e-3 * np.abs(want).max())
         for h in range(KV):
             want = O.f32_to_h2(O.head_prep(qkv[t, qd + h * hd:qd + (h + 1) * hd], None, rope, hd,
@@ -134,11 +141,11 @@ def test_rope_kv_epilogue(hip, fmt, H, KV, hd, K, M, pos0):
             got = O.halves_to_f32(kg[p, h * hd:(h + 1) * hd])
             wf = O.halves_to_f32(want)
             # halves of float32 results that agree to ~1e-5 of the vector
-            assert np.all(np.abs(got - wf) <= np.abs(wf) * 2 ** -10 + 1e-4 * np.abs(wf).max())
+            assert np.all(np.abs(got - wf) <= np.abs(wf) * 2 ** -10 + _tol(fmt, 1e-4) * np.abs(wf).max())
             vw = O.halves_to_f32(O.f32_to_h2(qkv[t, qd + KV * hd + h * hd:
                                                  qd + KV * hd + (h + 1) * hd]))
             vgot = O.halves_to_f32(vg[p, h * hd:(h + 1) * hd])
-            assert np.all(np.abs(vgot - vw) <= np.abs(vw) * 2 ** -10 + 1e-4 * np.abs(vw).max())
+            assert np.all(np.abs(vgot - vw) <= np.abs(vw) * 2 ** -10 + _tol(fmt, 1e-4) * np.abs(vw).max())
     assert not np.any(kg[pos0 + M:])
 
 

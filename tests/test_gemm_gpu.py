@@ -60,7 +60,8 @@ def test_c2_matmulnbits_prefill(hip, N):
     assert e16 <= 1e-5
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup", "q8_0", "q8"])
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup", "q4_k_records", "q8_0",
+                                 "q8"])
 @pytest.mark.parametrize("M,N,K", [(1, 64, 64), (37, 192, 128), (200, 512, 1024),
                                    (128, 1024, 2048)])
 def test_gemm_shapes_and_formats(hip, fmt, M, N, K):
@@ -101,7 +102,7 @@ def test_gemm_8bit_c2_shape(hip):
 
 
 @pytest.mark.parametrize("tile", [1, 2, 3])
-@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup", "q8_0"])
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup", "q4_k_records", "q8_0"])
 def test_gemm_every_tile(hip, fmt, tile):
     """Each tile shape (64 x 128, 128 x 128, 128 x 256), forced through the
     gemm_tile knob, on ragged rows (M = 200 leaves a partial 128-row tile)."""

@@ -235,7 +235,7 @@ def test_loaded_matrices_are_the_files(hip, tmp_path, mix, emb):
     assert np.array_equal(dense_of(w.embedding), want)
     if mix == "q4_k_m":  # the storage the rules pick
         assert w.layers[1]["qkv"].layout == L.LAYOUT_Q8          # Q4_K q, k + Q6_K v
-        assert w.layers[1]["o"].zero == L.ZERO_F16               # Q4_K alone: 4 bits
+        assert w.layers[1]["o"].zero == L.ZERO_Q4K               # Q4_K alone: 4 bits
         assert w.layers[0]["down"].layout == L.LAYOUT_Q8         # Q6_K
 
 

@@ -67,7 +67,7 @@ def _both(m, x16, N):
 
 
 @pytest.mark.parametrize("form", sorted(FORMS))
-@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup"])
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup", "q4_k_records"])
 @pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
 @pytest.mark.parametrize("N,K", [(65536, 2048), (4004, 1024)])
 def test_pick_parts_match_the_pick_over_the_logits(hip, form, fmt, M, N, K):

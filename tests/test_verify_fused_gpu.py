@@ -21,7 +21,8 @@ def _matrix(fmt, N, K, seed):
     return w.matrix(N, K)
 
 
-@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup", "q4_k", "q8_0", "q6_k"])
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup", "q4_k_records", "q4_k",
+                                 "q8_0", "q6_k"])
 @pytest.mark.parametrize("cursor", [0, 2, 7, -3])
 def test_embed_drafts_equals_drafts_then_embed(hip, fmt, cursor):
     from webgllm_amd import lib as L, ops

@@ -99,4 +99,57 @@ __host__ __device__ inline void q4k_scale_min(const uint8_t *sc, int j, int *s, 
   }
 }
 
+// packQ4_K's per-block halves from a Q4_K scale and min (src/repack.ts:100-168):
+// d' = toHalf(d sc); z' = toHalf(dmin m / d') with the quotient in doubles;
+// where d' is 0 the block is constant: d' = toHalf(-dmin m / 15), z' = 0,
+// and its quants are 15. Returns whether the block is constant.
+__host__ __device__ inline bool q4k_block_dz(double d, double dmin, int sc, int mn, uint16_t *dq,
+                                             uint16_t *zq) {
+  const double mins = dmin * mn;
+  const uint16_t h = double_to_half_ref(d * sc);
+  const float hv = half_to_float(h);
+  if (hv != 0.0f) {
+    *dq = h;
+    *zq = double_to_half_ref(mins / (double)hv);
+    return false;
+  }
+  *dq = double_to_half_ref(-mins / 15.0);
+  *zq = 0;
+  return true;
+}
+
+// A WG_ZERO_Q4K record (64 bytes a row group and super-block): the rows'
+// (half d, half dmin) in bytes 0-15, then block pair i's 96 bits at byte 16
+// + 12 i (block 2i in bits 0-47, 2i + 1 in 48-95), a block's row r at bits
+// 12 r (scale) and 12 r + 6 (min), 6 bits each.
+constexpr int Q4K_REC = 64;
+__host__ __device__ inline int q4k_rec_field(const uint8_t *rec, int j, int r, int which) {
+  const int bit = 48 * (j & 1) + 12 * r + 6 * which;
+  const uint8_t *p = rec + 16 + 12 * (j >> 1) + (bit >> 3);
+  // (the second byte only where the field crosses into it: never past the record)
+  const uint32_t v = (uint32_t)p[0] | ((bit & 7) > 2 ? (uint32_t)p[1] << 8 : 0u);
+  return (int)((v >> (bit & 7)) & 63u);
+}
+__host__ __device__ inline void q4k_rec_put(uint8_t *rec, int j, int r, int sc, int mn) {
+  for (int which = 0; which < 2; which++) {
+    const int bit = 48 * (j & 1) + 12 * r + 6 * which;
+    const uint32_t v = (uint32_t)(which ? mn : sc) & 63u;
+    uint8_t *p = rec + 16 + 12 * (j >> 1) + (bit >> 3);
+    const bool two = (bit & 7) > 2;
+    const uint32_t word =
+        ((uint32_t)p[0] | (two ? (uint32_t)p[1] << 8 : 0u)) & ~(63u << (bit & 7));
+    const uint32_t out = word | (v << (bit & 7));
+    p[0] = (uint8_t)out;
+    if (two) p[1] = (uint8_t)(out >> 8);
+  }
+}
+// packQ4_K's (d', z') of row r, block j (0..7) of a record.
+__host__ __device__ inline bool q4k_rec_dz(const uint8_t *rec, int j, int r, uint16_t *dq,
+                                           uint16_t *zq) {
+  const uint16_t db = (uint16_t)(rec[4 * r] | (rec[4 * r + 1] << 8));
+  const uint16_t mb = (uint16_t)(rec[4 * r + 2] | (rec[4 * r + 3] << 8));
+  return q4k_block_dz(half_to_float(db), half_to_float(mb), q4k_rec_field(rec, j, r, 0),
+                      q4k_rec_field(rec, j, r, 1), dq, zq);
+}
+
 }  // namespace wg

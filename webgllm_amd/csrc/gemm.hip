@@ -52,6 +52,7 @@
 
 #include "common.h"
 #include "dot.h"
+#include "kernels.h"
 #include "lds_load.h"
 
 namespace wg {
@@ -557,6 +558,57 @@ int split_space(hipStream_t s, size_t floats, int counters, float **part, int **
   return WG_OK;
 }
 
+// The halves a WG_ZERO_Q4K matrix's (d', z') are rebuilt into before its
+// GEMM, per device and stream as the split-K workspace, grown on demand,
+// and never taken by a launch being captured (a graph would keep pointing
+// at it after it grows, and may replay beside eager launches).
+struct ExpandSpace {
+  int dev;
+  hipStream_t stream;
+  uint16_t *halves;
+  size_t count;
+};
+
+// `count` halves on stream s, or null while s is being captured.
+int expand_space(hipStream_t s, size_t count, uint16_t **out) {
+  static std::mutex mu;
+  static std::vector<ExpandSpace *> spaces;
+  *out = nullptr;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return WG_OK;
+  }
+  if (cs != hipStreamCaptureStatusNone) return WG_OK;
+  int dev = 0;
+  WG_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  ExpandSpace *sp = nullptr;
+  for (ExpandSpace *x : spaces)
+    if (x->dev == dev && x->stream == s) sp = x;
+  if (!sp) {
+    sp = new ExpandSpace{dev, s, nullptr, 0};
+    spaces.push_back(sp);
+  }
+  if (sp->count < count) {
+    if (sp->halves) {  // launches queued on s may still read the old halves
+      WG_HIP(hipStreamSynchronize(s));
+      WG_HIP(hipFree(sp->halves));
+      sp->halves = nullptr;
+      sp->count = 0;
+    }
+    uint16_t *p = nullptr;
+    if (hipMalloc(&p, count * sizeof(uint16_t)) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(WG_ERR_OOM, "prefill GEMM: %zu halves for Q4_K scales not allocated", count);
+    }
+    sp->halves = p;
+    sp->count = count;
+  }
+  *out = sp->halves;
+  return WG_OK;
+}
+
 template <int ZK, int BM, int BN, int S, int WGM = 2, int WGN = 2, bool SW = false>
 int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
                  const float *residual, int ldr, const float *row_scale, const int32_t *col_of,
@@ -649,6 +701,23 @@ static int dispatch(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, fl
                     const int32_t *col_of, hipStream_t s) {
   if (w->layout == WG_LAYOUT_Q8)
     return launch<Q8, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+  if (w->zero == WG_ZERO_Q4K) {
+    // packQ4_K's halves rebuilt from the records, then the half-zero-point
+    // GEMM over the same quants: the bits of a WG_ZERO_F16 matrix's GEMM
+    const size_t blocks = (size_t)w->N * (w->K / 32);
+    uint16_t *halves = nullptr;
+    int rc = expand_space(s, 2 * blocks, &halves);
+    if (rc) return rc;
+    if (!halves)
+      return fail(WG_ERR_UNSUPPORTED, "%s: a Q4_K-record matrix is not taken under capture",
+                  SW ? "wg_q4_gemm_swiglu" : "wg_q4_gemm");
+    wg_q4_matrix f = *w;
+    f.zero = WG_ZERO_F16;
+    f.scales = halves;
+    f.zeros = halves + blocks;
+    if ((rc = launch_q4k_expand(w, halves, halves + blocks, s))) return rc;
+    return launch<WG_ZERO_F16, SW>(&f, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+  }
   switch (w->zero) {
     case WG_ZERO_8: return launch<WG_ZERO_8, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
     case WG_ZERO_U8: return launch<WG_ZERO_U8, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
@@ -692,14 +761,8 @@ int wg_q4_gemm(const wg_q4_matrix *w, const uint16_t *A, int32_t M, int32_t lda,
     WG_REQUIRE(residual == C || !overlaps(residual, (size_t)M * ldr * 4, C, (size_t)M * ldc * 4),
                "wg_q4_gemm: residual overlaps the output");
   }
-  hipStream_t s = as_stream(stream);
-  if (w->layout == WG_LAYOUT_Q8)
-    return launch<Q8>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
-  switch (w->zero) {
-    case WG_ZERO_8: return launch<WG_ZERO_8>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
-    case WG_ZERO_U8: return launch<WG_ZERO_U8>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
-    default: return launch<WG_ZERO_F16>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
-  }
+  return dispatch<false>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of,
+                         as_stream(stream));
 }
 
 }  // extern "C"

@@ -52,11 +52,22 @@ __global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
   for (int b = lane; b < B; b += 64) {
     const uint4 *qp = qg + (int64_t)b * 4;
     uint4 q[4] = {qp[0], qp[1], qp[2], qp[3]};
-    uint2 sc = *reinterpret_cast<const uint2 *>(sg + (int64_t)b * 4);
-    float z[4];
-    load_zeros<ZK>(zeros, ((int64_t)g * B + b) * 4, z);
-    float d[4] = {(float)as_h2(sc.x).x, (float)as_h2(sc.x).y, (float)as_h2(sc.y).x,
-                  (float)as_h2(sc.y).y};
+    // per row, d (b - z sa), or for Q4_K records d' b - c sa (z := c / d')
+    float z[4], d[4], c[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (ZK == WG_ZERO_Q4K) {
+      uint4 dd;
+      uint2 bits;
+      q4k_load(scales, g, B, b, dd, bits);
+      q4k_dc(dd, bits, d, c);
+      z[0] = z[1] = z[2] = z[3] = 0.0f;
+    } else {
+      uint2 sc = *reinterpret_cast<const uint2 *>(sg + (int64_t)b * 4);
+      load_zeros<ZK>(zeros, ((int64_t)g * B + b) * 4, z);
+      d[0] = (float)as_h2(sc.x).x;
+      d[1] = (float)as_h2(sc.x).y;
+      d[2] = (float)as_h2(sc.y).x;
+      d[3] = (float)as_h2(sc.y).y;
+    }
     uint4 a[M][4];
 #pragma unroll
     for (int m = 0; m < M; m++) {
@@ -76,8 +87,13 @@ __global__ __launch_bounds__(256) void gemv_rowgroup_kernel(
 #pragma unroll
       for (int m = 0; m < M; m++) {
         float v = block_dot(n, a[m]);
-        v = __builtin_fmaf(-z[r], sa[m], v);
-        acc[r][m] = __builtin_fmaf(d[r], v, acc[r][m]);
+        if constexpr (ZK == WG_ZERO_Q4K) {
+          acc[r][m] = __builtin_fmaf(d[r], v, acc[r][m]);
+          acc[r][m] = __builtin_fmaf(-c[r], sa[m], acc[r][m]);
+        } else {
+          v = __builtin_fmaf(-z[r], sa[m], v);
+          acc[r][m] = __builtin_fmaf(d[r], v, acc[r][m]);
+        }
       }
     }
   }
@@ -113,6 +129,7 @@ int launch_stream_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y,
   switch (w->zero) {
     case WG_ZERO_8: return launch_stream_k<M, WG_ZERO_8>(w, x, ldx, y, ldy, ep, s);
     case WG_ZERO_U8: return launch_stream_k<M, WG_ZERO_U8>(w, x, ldx, y, ldy, ep, s);
+    case WG_ZERO_Q4K: return launch_stream_k<M, WG_ZERO_Q4K>(w, x, ldx, y, ldy, ep, s);
     default: return launch_stream_k<M, WG_ZERO_F16>(w, x, ldx, y, ldy, ep, s);
   }
 }
@@ -139,6 +156,7 @@ int launch_gemv_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, i
   switch (w->zero) {
     case WG_ZERO_8: launch_rowgroup_mode<M, WG_ZERO_8>(w, x, ldx, y, ldy, e, s); break;
     case WG_ZERO_U8: launch_rowgroup_mode<M, WG_ZERO_U8>(w, x, ldx, y, ldy, e, s); break;
+    case WG_ZERO_Q4K: launch_rowgroup_mode<M, WG_ZERO_Q4K>(w, x, ldx, y, ldy, e, s); break;
     default: launch_rowgroup_mode<M, WG_ZERO_F16>(w, x, ldx, y, ldy, e, s); break;
   }
   return launched("wg_q4_gemv");

@@ -75,13 +75,49 @@ __device__ inline void load_zeros(const void *zeros, int64_t si, float z[4]) {
 }
 
 
+// WG_ZERO_Q4K: the record's (d, dmin) words of row group g's super-block
+// holding block b (every lane of the super-block loads the same 16 bytes),
+// and the block's 48 bits of 6-bit scales and mins (block 2i at dword 3i,
+// 2i + 1 at dword 3i + 1, 16 bits in) as lo (bits 0-31) and hi (32-47).
+__device__ inline void q4k_load(const void *scales, int64_t g, int B, int b, uint4 &dd,
+                                uint2 &bits) {
+  const uint8_t *rec =
+      reinterpret_cast<const uint8_t *>(scales) + (g * (B / 8) + (b >> 3)) * Q4K_REC;
+  const int jb = b & 7;
+  dd = *reinterpret_cast<const uint4 *>(rec);
+  const uint2 w2 = *reinterpret_cast<const uint2 *>(rec + 16 + 4 * (3 * (jb >> 1) + (jb & 1)));
+  const uint32_t sh = (uint32_t)(jb & 1) * 16u;
+  bits.x = __builtin_amdgcn_alignbit(w2.y, w2.x, sh);
+  bits.y = w2.y >> sh;
+}
+// The 4 rows' d' = half(d sc), exactly as packQ4_K rounds it, and zero terms
+// c = dmin m (their products exact in float32), from q4k_load's words: a
+// block weighs d' q - c, where packQ4_K's d' half(dmin m / d') rounds c to
+// a half's precision.
+__device__ inline void q4k_dc(const uint4 &dd, const uint2 &bits, float (&d)[4], float (&c)[4]) {
+  const uint32_t lo = bits.x, hi = bits.y;
+  const uint32_t sc[4] = {lo & 63u, (lo >> 12) & 63u, (lo >> 24) & 63u, (hi >> 4) & 63u};
+  const uint32_t mn[4] = {(lo >> 6) & 63u, (lo >> 18) & 63u,
+                          __builtin_amdgcn_alignbit(hi, lo, 30) & 63u, (hi >> 10) & 63u};
+  const uint32_t dw[4] = {dd.x, dd.y, dd.z, dd.w};
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const float dr = (float)as_h2(dw[r]).x, mr = (float)as_h2(dw[r]).y;
+    d[r] = (float)(_Float16)(dr * (float)sc[r]);
+    c[r] = mr * (float)mn[r];
+  }
+}
+
 // The streamed unit of one row group for one lane: NB blocks (b0, b0 + 64,
-// ...) of the group's 4 rows, their half scales and zero points.
+// ...) of the group's 4 rows, their half scales and zero points; or, for
+// WG_ZERO_Q4K, the 4 rows' (d, dmin) of the block's super-block and the
+// block's 48 bits of 6-bit scales and mins.
 template <int ZK, int NB>
 struct Unit {
   uint4 q[NB][4];
   uint2 sc[NB];
-  uint2 zr[NB];  // u8: .x holds 4 zero points; f16: 4 halves
+  uint2 zr[NB];  // u8: .x holds 4 zero points; f16: 4 halves; Q4K: the 48 bits
+  uint4 dd[ZK == WG_ZERO_Q4K ? NB : 1];
 };
 
 template <int ZK, int NB>
@@ -166,7 +202,11 @@ __device__ inline void load_unit_at(Unit<ZK, NB> &u, const uint4 *__restrict__ q
     u.q[j][1] = qp[1];
     u.q[j][2] = qp[2];
     u.q[j][3] = qp[3];
-    u.sc[j] = *reinterpret_cast<const uint2 *>(scales + si);
+    if constexpr (ZK == WG_ZERO_Q4K) {
+      q4k_load(scales, g, B, bj[j], u.dd[j], u.zr[j]);
+    } else {
+      u.sc[j] = *reinterpret_cast<const uint2 *>(scales + si);
+    }
     if constexpr (ZK == WG_ZERO_U8)
       u.zr[j].x = *reinterpret_cast<const uint32_t *>((const uint8_t *)zeros + si);
     if constexpr (ZK == WG_ZERO_F16)
@@ -223,6 +263,24 @@ __device__ inline void accumulate_unit_paired(const Unit<ZK, NB> &u,
                                               float (&acc)[4][M]) {
 #pragma unroll
   for (int j = 0; j < NB; j++) {
+    if constexpr (ZK == WG_ZERO_Q4K) {
+      float d[4], c[4];
+      q4k_dc(u.dd[j], u.zr[j], d, c);
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        d[r] = live[j] ? d[r] : 0.0f;
+        c[r] = live[j] ? c[r] : 0.0f;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          const float v = block_dot_paired(u.q[j][r], a[m][j]);
+          acc[r][m] = __builtin_fmaf(d[r], v, acc[r][m]);
+          acc[r][m] = __builtin_fmaf(-c[r], sa[m][j], acc[r][m]);
+        }
+      continue;
+    }
     float d[4] = {(float)as_h2(u.sc[j].x).x, (float)as_h2(u.sc[j].x).y,
                   (float)as_h2(u.sc[j].y).x, (float)as_h2(u.sc[j].y).y};
 #pragma unroll

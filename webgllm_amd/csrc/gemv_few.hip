@@ -30,6 +30,7 @@ int launch_few_m(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, in
   switch (w->zero) {
     case WG_ZERO_8: return launch_few_k<M, WG_ZERO_8>(w, x, ldx, y, ldy, e, s);
     case WG_ZERO_U8: return launch_few_k<M, WG_ZERO_U8>(w, x, ldx, y, ldy, e, s);
+    case WG_ZERO_Q4K: return launch_few_k<M, WG_ZERO_Q4K>(w, x, ldx, y, ldy, e, s);
     default: return launch_few_k<M, WG_ZERO_F16>(w, x, ldx, y, ldy, e, s);
   }
 }

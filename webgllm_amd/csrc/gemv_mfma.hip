@@ -487,6 +487,7 @@ int launch_gemv_mfma(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, f
                      int ldy, const wg_epilogue &e, hipStream_t s) {
   const int mode = tuning("gemv_mfma");
   if (!mode || M < 1 || M > 8 || (M <= 2 && mode < 2)) return -1;
+  if (w->zero == WG_ZERO_Q4K) return -1;  // (Q4_K records: the streaming kernels)
   switch (w->zero) {
     case WG_ZERO_8: return launch_mfma_k<WG_ZERO_8>(w, x, M, ldx, y, ldy, e, s);
     case WG_ZERO_U8: return launch_mfma_k<WG_ZERO_U8>(w, x, M, ldx, y, ldy, e, s);

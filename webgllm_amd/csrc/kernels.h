@@ -23,5 +23,8 @@ int launch_gemv_mfma(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, f
                      int ldy, const wg_epilogue &e, hipStream_t s);
 int launch_gemv_wide(const wg_q4_matrix *w, const uint16_t *x, int M, int ldx, float *y, int ldy,
                      const wg_epilogue &e, hipStream_t s);
+// A WG_ZERO_Q4K matrix's packQ4_K (d', z') halves into scales and zeros
+// (N * K / 32 halves each, the WG_ZERO_F16 arrays of the same quants).
+int launch_q4k_expand(const wg_q4_matrix *w, uint16_t *scales, uint16_t *zeros, hipStream_t s);
 
 }  // namespace wg

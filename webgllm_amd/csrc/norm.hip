@@ -149,10 +149,19 @@ __global__ __launch_bounds__(256) void embed_rowgroup_kernel(
   float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (n >= 0 && n < N) {  // an id outside the vocabulary embeds as zeros
     const int64_t si = ((int64_t)(n >> 2) * blocks + b) * 4 + (n & 3);
-    const double d = half_to_float(scales[si]);
-    const double z = zero_kind == WG_ZERO_U8    ? (double)((const uint8_t *)zeros)[si]
-                     : zero_kind == WG_ZERO_F16 ? (double)half_to_float(((const uint16_t *)zeros)[si])
-                                                : 8.0;
+    double d, z;
+    if (zero_kind == WG_ZERO_Q4K) {  // packQ4_K's halves rebuilt from the record
+      uint16_t dq, zq;
+      q4k_rec_dz((const uint8_t *)scales + ((int64_t)(n >> 2) * (blocks / 8) + b / 8) * Q4K_REC,
+                 b & 7, n & 3, &dq, &zq);
+      d = half_to_float(dq);
+      z = half_to_float(zq);
+    } else {
+      d = half_to_float(scales[si]);
+      z = zero_kind == WG_ZERO_U8    ? (double)((const uint8_t *)zeros)[si]
+          : zero_kind == WG_ZERO_F16 ? (double)half_to_float(((const uint16_t *)zeros)[si])
+                                     : 8.0;
+    }
     const uint32_t word = quants[si * 4 + (j & 3)];
 #pragma unroll
     for (int i = 0; i < 4; i++) {

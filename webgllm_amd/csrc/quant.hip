@@ -4,6 +4,7 @@
 // device once and rearranged there, one thread per row block.
 #include "common.h"
 #include "wide.h"
+#include "kernels.h"
 
 namespace wg {
 namespace {
@@ -120,6 +121,72 @@ __global__ void repack_q4_k_kernel(uint32_t *quants, uint16_t *scales, uint16_t 
   }
 }
 
+// packQ4_K's quants with Q4_K's own scales kept (WG_ZERO_Q4K): thread =
+// (row group gi of the range, super-block s). The group's 4 rows' nibbles go
+// out as repack_q4_k_kernel writes them (15s for a constant block), and its
+// record gets the rows' d and dmin and the 8 blocks' 6-bit scales and mins.
+__global__ void repack_q4_k_rec_kernel(uint32_t *quants, uint8_t *recs, const uint8_t *src,
+                                       const int32_t *src_rows, int row0, int rows, int supers) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)(rows / 4) * supers) return;
+  const int gi = (int)(t / supers), s = (int)(t % supers);
+  const int g = row0 / 4 + gi, blocks = supers * 8;
+  uint8_t rec[Q4K_REC];
+  for (int k = 0; k < Q4K_REC; k++) rec[k] = 0;
+  uint4 *qv = reinterpret_cast<uint4 *>(quants);
+  const uint32_t LOW = 0x0f0f0f0fu;
+  for (int r = 0; r < 4; r++) {
+    const int i = 4 * gi + r;
+    const int sr = src_rows ? src_rows[i] : i;
+    const uint8_t *p = src + ((int64_t)sr * supers + s) * 144;
+    for (int k = 0; k < 4; k++) rec[4 * r + k] = p[k];
+    const double d = half_to_float(ld16_unaligned(p));
+    const double dmin = half_to_float(ld16_unaligned(p + 2));
+    for (int pair = 0; pair < 4; pair++) {
+      const uint8_t *at = p + 16 + pair * 32;
+      uint32_t lo[4], hi[4];
+      for (int w = 0; w < 4; w++) {
+        uint32_t a = ld32_unaligned(at + 4 * w), b = ld32_unaligned(at + 16 + 4 * w);
+        lo[w] = (a & LOW) | ((b & LOW) << 4);
+        hi[w] = ((a >> 4) & LOW) | (b & ~LOW);
+      }
+      for (int j2 = 0; j2 < 2; j2++) {
+        const int j = 2 * pair + j2;
+        int sc, mn;
+        q4k_scale_min(p + 4, j, &sc, &mn);
+        q4k_rec_put(rec, j, r, sc, mn);
+        uint16_t dq, zq;
+        const bool constant = q4k_block_dz(d, dmin, sc, mn, &dq, &zq);
+        const uint32_t *w = j2 ? hi : lo;
+        qv[((int64_t)g * blocks + s * 8 + j) * 4 + r] =
+            constant ? make_uint4(0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu)
+                     : make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+  }
+  uint4 *o = reinterpret_cast<uint4 *>(recs + ((int64_t)g * supers + s) * Q4K_REC);
+  for (int k = 0; k < Q4K_REC / 16; k++) {
+    uint32_t v[4];
+    for (int w = 0; w < 4; w++) v[w] = ld32_unaligned(rec + 16 * k + 4 * w);
+    o[k] = make_uint4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+// WG_ZERO_Q4K records -> packQ4_K's per-block (d', z') halves at the
+// WG_ZERO_F16 indices (the prefill GEMM's operands): thread = (row n, block b).
+__global__ void q4k_rec_expand_kernel(const uint8_t *recs, uint16_t *scales, uint16_t *zeros,
+                                      int N, int blocks) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)N * blocks) return;
+  const int n = (int)(t / blocks), b = (int)(t % blocks);
+  const uint8_t *rec = recs + ((int64_t)(n >> 2) * (blocks / 8) + b / 8) * Q4K_REC;
+  uint16_t dq, zq;
+  q4k_rec_dz(rec, b & 7, n & 3, &dq, &zq);
+  const int64_t si = ((int64_t)(n >> 2) * blocks + b) * 4 + (n & 3);
+  scales[si] = dq;
+  zeros[si] = zq;
+}
+
 // Q4_K super-blocks regrouped by rows of 4 (record (g * supers + s) * 4 + r):
 // thread = one 16-byte piece of one record.
 __global__ void repack_q4_k_native_kernel(uint8_t *dst, const uint8_t *src,
@@ -149,10 +216,19 @@ __global__ void dequant_rowgroup_kernel(const uint32_t *quants, const uint16_t *
   int i = (int)(t / blocks), b = (int)(t % blocks);
   int n = row0 + i;
   int64_t si = ((int64_t)(n >> 2) * blocks + b) * 4 + (n & 3);
-  double d = half_to_float(scales[si]);
-  double z = zero_kind == WG_ZERO_U8    ? (double)((const uint8_t *)zeros)[si]
-             : zero_kind == WG_ZERO_F16 ? (double)half_to_float(((const uint16_t *)zeros)[si])
-                                        : 8.0;
+  double d, z;
+  if (zero_kind == WG_ZERO_Q4K) {  // packQ4_K's halves rebuilt from the record
+    uint16_t dq, zq;
+    q4k_rec_dz((const uint8_t *)scales + ((int64_t)(n >> 2) * (blocks / 8) + b / 8) * Q4K_REC,
+               b & 7, n & 3, &dq, &zq);
+    d = half_to_float(dq);
+    z = half_to_float(zq);
+  } else {
+    d = half_to_float(scales[si]);
+    z = zero_kind == WG_ZERO_U8    ? (double)((const uint8_t *)zeros)[si]
+        : zero_kind == WG_ZERO_F16 ? (double)half_to_float(((const uint16_t *)zeros)[si])
+                                   : 8.0;
+  }
   uint4 q = reinterpret_cast<const uint4 *>(quants)[si];
   uint32_t w[4] = {q.x, q.y, q.z, q.w};
   float *o = out + (int64_t)i * blocks * 32 + b * 32;
@@ -349,6 +425,14 @@ __global__ void rows_to_floats_kernel(int type, const uint8_t *src, int64_t piec
 inline unsigned grid_for(int64_t threads, int per) { return (unsigned)((threads + per - 1) / per); }
 
 }  // namespace
+
+int launch_q4k_expand(const wg_q4_matrix *w, uint16_t *scales, uint16_t *zeros, hipStream_t s) {
+  const int blocks = w->K / 32;
+  q4k_rec_expand_kernel<<<grid_for((int64_t)w->N * blocks, 256), 256, 0, s>>>(
+      (const uint8_t *)w->scales, scales, zeros, w->N, blocks);
+  return launched("Q4_K record expansion");
+}
+
 }  // namespace wg
 
 using namespace wg;
@@ -403,12 +487,22 @@ int wg_repack_q4_k(const wg_q4_matrix *m, int32_t row0, int32_t rows, const void
   int rc = check_matrix(m, "wg_repack_q4_k");
   if (rc) return rc;
   if ((rc = check_rows(m, row0, rows, "wg_repack_q4_k"))) return rc;
-  WG_REQUIRE(m->layout == WG_LAYOUT_ROWGROUP && m->zero == WG_ZERO_F16,
-             "wg_repack_q4_k: Q4_K rows go into a matrix with fractional zero points");
+  WG_REQUIRE(m->layout == WG_LAYOUT_ROWGROUP && (m->zero == WG_ZERO_F16 || m->zero == WG_ZERO_Q4K),
+             "wg_repack_q4_k: Q4_K rows go into a row-group matrix with half zero points or "
+             "Q4_K records");
   WG_REQUIRE(m->K % 256 == 0, "wg_repack_q4_k: columns (%d) must be a multiple of 256", m->K);
   WG_REQUIRE(src, "wg_repack_q4_k: no source");
   if (!rows) return WG_OK;
   int supers = m->K / 256;
+  if (m->zero == WG_ZERO_Q4K) {
+    WG_REQUIRE(row0 % 4 == 0 && rows % 4 == 0,
+               "wg_repack_q4_k: rows must start and end on a row group");
+    const int64_t n = (int64_t)(rows / 4) * supers;
+    repack_q4_k_rec_kernel<<<grid_for(n, 64), 64, 0, as_stream(stream)>>>(
+        (uint32_t *)m->quants, (uint8_t *)m->scales, (const uint8_t *)src, src_rows, row0, rows,
+        supers);
+    return launched("wg_repack_q4_k");
+  }
   int64_t n = (int64_t)rows * supers * 4;
   repack_q4_k_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(
       (uint32_t *)m->quants, (uint16_t *)m->scales, (uint16_t *)m->zeros, (const uint8_t *)src,

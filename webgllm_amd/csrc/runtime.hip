@@ -43,9 +43,13 @@ int check_matrix(const wg_q4_matrix *m, const char *who) {
     WG_REQUIRE(m->K > 0 && m->K % 32 == 0,
                "%s: matrix columns (%d) must be a positive multiple of 32", who, m->K);
     WG_REQUIRE(m->scales, "%s: matrix has no scales", who);
-    WG_REQUIRE(m->zero == WG_ZERO_8 || m->zero == WG_ZERO_U8 || m->zero == WG_ZERO_F16,
+    WG_REQUIRE(m->zero == WG_ZERO_8 || m->zero == WG_ZERO_U8 || m->zero == WG_ZERO_F16 ||
+                   m->zero == WG_ZERO_Q4K,
                "%s: unknown zero-point kind %d", who, m->zero);
-    WG_REQUIRE(m->zero == WG_ZERO_8 || m->zeros, "%s: matrix has no zero points", who);
+    WG_REQUIRE(m->zero == WG_ZERO_8 || m->zero == WG_ZERO_Q4K || m->zeros,
+               "%s: matrix has no zero points", who);
+    WG_REQUIRE(m->zero != WG_ZERO_Q4K || m->K % 256 == 0,
+               "%s: Q4_K row-group columns (%d) must be a multiple of 256", who, m->K);
   } else if (m->layout == WG_LAYOUT_Q4K) {
     WG_REQUIRE(m->K > 0 && m->K % 256 == 0,
                "%s: Q4_K matrix columns (%d) must be a positive multiple of 256", who, m->K);
@@ -636,6 +640,11 @@ int wg_q4_sizes(int32_t N, int32_t K, int32_t layout, int32_t zero, size_t *qb, 
     q = blocks * 16;
     s = blocks * 2;
     z = zero == WG_ZERO_U8 ? blocks : zero == WG_ZERO_F16 ? blocks * 2 : 0;
+    if (zero == WG_ZERO_Q4K) {
+      WG_REQUIRE(K % 256 == 0, "wg_q4_sizes: Q4_K row-group columns (%d) must be a multiple of 256",
+                 K);
+      s = (size_t)N * (K / 256) * 16;  // a 64-byte record a row group and super-block
+    }
   } else if (layout == WG_LAYOUT_Q4K) {
     WG_REQUIRE(K > 0 && K % 256 == 0, "wg_q4_sizes: Q4_K columns (%d) must be a multiple of 256",
                K);

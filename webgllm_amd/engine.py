@@ -73,6 +73,7 @@ class ModelShape:
     intermediate: int
     vocab: int
     # "q4_0" | "nbits" | "q4_k" (native super-blocks) | "q4_k_rowgroup" |
+    # "q4_k_records" (packQ4_K's quants with Q4_K's own scales) |
     # "q8_0" (GGUF Q8_0) | "q8" (floats requantized to 8 bits) | "q6_k"
     fmt: str
     rope_theta: float = 1e6
@@ -103,12 +104,14 @@ class ModelShape:
 # The workloads' shapes.
 QWEN2_05B = ModelShape("qwen2-0.5b-shape", 896, 24, 14, 2, 64, 4864, 151936, "nbits",
                        rope_theta=1e6, eps=1e-6)
-# GGUF Q4_K weights, repacked at load into the reference's 32-blocks with half
-# scale and zero point (packQ4_K, src/repack.ts:100-168): measured faster than
-# streaming the super-blocks as they are, whose per-sub-block (d', z')
-# rebuild makes that GEMV VALU-bound.
+# GGUF Q4_K weights, repacked at load into the reference's 32-blocks
+# (packQ4_K, src/repack.ts:100-168) with Q4_K's own scales and mins kept
+# beside them, at the file's 0.5625 bytes a weight (the half scale and zero
+# point a block take 0.625): measured faster than both the half-zero-point
+# form and streaming the super-blocks as they are, whose nibble order and
+# per-sub-block (d', z') rebuild make that GEMV VALU-bound.
 LLAMA3_8B = ModelShape("llama3-8b-shape", 4096, 32, 32, 8, 128, 14336, 128256,
-                       "q4_k_rowgroup", rope_theta=5e5, eps=1e-5)
+                       "q4_k_records", rope_theta=5e5, eps=1e-5)
 LFM2_12B = ModelShape("lfm2-1.2b-shape", 2048, 16, 32, 8, 64, 8192, 65536, "q4_0",
                       rope_theta=1e6, eps=1e-5, qk_norm=True, conv_kernel=3,
                       conv_layers=(0, 1, 3, 4, 6, 7, 9, 11, 13, 15))
@@ -170,7 +173,7 @@ class Weights:
         g, dev = self.g, self.device
         src_rows = None if row_order is None else \
             torch.tensor(row_order, dtype=torch.int32, device=dev)
-        if fmt in ("q4_k", "q4_k_rowgroup"):
+        if fmt in ("q4_k", "q4_k_rowgroup", "q4_k_records"):
             src = torch.empty(N * (K // 256) * 144, dtype=torch.uint8, device=dev)
             src.random_(0, 256, generator=g)
             rec = src.view(-1, 144)
@@ -179,7 +182,8 @@ class Weights:
             hdr[:, 0].uniform_(1.0e-4, 2.0e-4, generator=g)
             hdr[:, 1].uniform_(4.0e-4, 8.0e-4, generator=g)
             rec[:, 0:4] = hdr.half().view(torch.uint8)
-            m = ops.Q4Matrix.from_q4_k(src, N, K, native=fmt == "q4_k", src_rows=src_rows)
+            m = ops.Q4Matrix.from_q4_k(src, N, K, native=fmt == "q4_k", src_rows=src_rows,
+                                       records=fmt == "q4_k_records")
         elif fmt == "q4_0":
             src = torch.empty(N * (K // 32) * 18, dtype=torch.uint8, device=dev)
             src.random_(0, 256, generator=g)

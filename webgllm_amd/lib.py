@@ -20,7 +20,7 @@ STATUS = {-1: "invalid", -2: "out-of-memory", -3: "device", -4: "aliased", -5: "
           -6: "unsupported"}
 
 LAYOUT_ROWGROUP, LAYOUT_Q4K, LAYOUT_Q8, LAYOUT_Q6K = 0, 1, 2, 3
-ZERO_8, ZERO_U8, ZERO_F16 = 0, 1, 2
+ZERO_8, ZERO_U8, ZERO_F16, ZERO_Q4K = 0, 1, 2, 3
 
 
 class WgError(RuntimeError):

@@ -207,7 +207,9 @@ class _Uploader:
         src_rows = None if row_order is None else \
             torch.tensor(row_order, dtype=torch.int32, device=self.device)
         if types == {G.Q4_K} and K % 256 == 0:
-            m = ops.Q4Matrix(N, K, L.LAYOUT_ROWGROUP, L.ZERO_F16, device=self.device)
+            # packQ4_K's quants with Q4_K's own scales and mins kept (0.5625
+            # bytes a weight; dequant rebuilds packQ4_K's halves bit for bit)
+            m = ops.Q4Matrix(N, K, L.LAYOUT_ROWGROUP, L.ZERO_Q4K, device=self.device)
             m.repack_q4_k(0, N, self._cat(parts), src_rows)
         elif G.Q4_0 in types:
             if types != {G.Q4_0}:

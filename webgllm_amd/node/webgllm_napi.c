@@ -1548,6 +1548,7 @@ static napi_value init(napi_env env, napi_value exports) {
   set(env, consts, "ZERO_8", num(env, WG_ZERO_8));
   set(env, consts, "ZERO_U8", num(env, WG_ZERO_U8));
   set(env, consts, "ZERO_F16", num(env, WG_ZERO_F16));
+  set(env, consts, "ZERO_Q4K", num(env, WG_ZERO_Q4K));
   set(env, consts, "EPI_STORE", num(env, WG_EPI_STORE));
   set(env, consts, "EPI_SWIGLU", num(env, WG_EPI_SWIGLU));
   set(env, consts, "EPI_ROPE_KV", num(env, WG_EPI_ROPE_KV));

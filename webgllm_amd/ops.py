@@ -85,12 +85,16 @@ class Q4Matrix:
 
     @classmethod
     def from_q4_k(cls, src: torch.Tensor, N: int, K: int, native: bool = True,
-                  src_rows=None) -> "Q4Matrix":
+                  src_rows=None, records: bool = False) -> "Q4Matrix":
+        """A matrix from GGUF Q4_K rows: the super-blocks as they are
+        (native), packQ4_K's row groups with half zero points, or (records)
+        the same quants with Q4_K's own scales kept (ZERO_Q4K)."""
         if native:
             m = cls(N, K, L.LAYOUT_Q4K, L.ZERO_8, device=src.device)
             m.repack_q4_k_native(0, N, src, src_rows)
         else:
-            m = cls(N, K, L.LAYOUT_ROWGROUP, L.ZERO_F16, device=src.device)
+            m = cls(N, K, L.LAYOUT_ROWGROUP, L.ZERO_Q4K if records else L.ZERO_F16,
+                    device=src.device)
             m.repack_q4_k(0, N, src, src_rows)
         return m
 
