@@ -41,7 +41,8 @@ const char *wg_last_error(void);
 const char *wg_version(void);
 
 /* Launch-shape knobs, as the reference's TUNING table (src/engine.ts:147-625):
- * "gemv_wg_per_cu", "gemv_wg_per_cu_wide" (matrices of 16384+ row groups),
+ * "gemv_wg_per_cu", "gemv_wg_per_cu_small" (1024 row groups or fewer),
+ * "gemv_wg_per_cu_deep" (4096 to 16383), "gemv_wg_per_cu_wide" (16384+),
  * "q4k_wg_per_cu", "wide_wg_per_cu" (8-bit and Q6_K matrices: persistent
  * GEMV workgroups per compute unit) and
  * "gemv_min_waves" (below this many waves a GEMV splits K inside a

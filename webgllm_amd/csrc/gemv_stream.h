@@ -198,9 +198,17 @@ int launch_stream(const wg_q4_matrix *w, const uint16_t *x, int ldx, float *y, i
   int G = w->N / 4, B = w->K / 32;
   constexpr int RGW = 4 / KS;
   // 3 tokens and more: one workgroup a CU (each wave then takes more row
-  // groups for the activations it holds)
-  const char *knob = M >= 3 ? "gemv_few_wg_per_cu"
-                            : G >= 16384 ? "gemv_wg_per_cu_wide" : "gemv_wg_per_cu";
+  // groups for the activations it holds). One or two tokens, by the row
+  // groups (8B-shape matrices, µs a launch over 12 distinct ones at 1 / 2 /
+  // 3 / 4 a CU): 1024 or fewer, one a CU (4096 x 4096: 4.56 / 4.86 / 4.80 /
+  // 4.77; 4096 x 14336 10.66 / 10.62 / 11.27 / 11.56); from 4096, three
+  // (28672 x 4096: 21.4 / 14.58 / 13.88 / 14.72); from 16384 (the head),
+  // eight; two between (6144 x 4096: 5.95 / 5.40 / 5.68 / 5.65)
+  const char *knob = M >= 3        ? "gemv_few_wg_per_cu"
+                     : G >= 16384  ? "gemv_wg_per_cu_wide"
+                     : G >= 4096   ? "gemv_wg_per_cu_deep"
+                     : G <= 1024   ? "gemv_wg_per_cu_small"
+                                   : "gemv_wg_per_cu";
   int grid = persistent_grid((G + RGW - 1) / RGW, tuning(knob));
   auto q = (const uint4 *)w->quants;
   auto sc = (const uint16_t *)w->scales;

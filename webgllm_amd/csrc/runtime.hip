@@ -74,6 +74,8 @@ struct Knob {
 };
 static Knob g_knobs[] = {
     {"gemv_wg_per_cu", 2, 1, 16},        // persistent row-group GEMV workgroups per CU
+    {"gemv_wg_per_cu_small", 1, 1, 16},  // the same for matrices of 1024 row groups or fewer
+    {"gemv_wg_per_cu_deep", 3, 1, 16},   // the same for 4096 to 16383 row groups
     {"gemv_wg_per_cu_wide", 8, 1, 16},   // the same for matrices of 16384+ row groups
     {"q4k_wg_per_cu", 3, 1, 16},         // persistent Q4_K GEMV workgroups per CU
     {"q4k_rows", 1, 0, 1},               // Q4_K GEMV: every lane on a row group's 4 rows (0: 2 rows)
