@@ -203,6 +203,13 @@ int wg_repack_q4_0(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const vo
  * regrouped into its records. */
 int wg_repack_q4_k(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *src,
                    const int32_t *src_rows, void *stream);
+/* packQ4_K's half scales and zero points of a WG_ZERO_Q4K matrix (N*K/32
+ * halves each, at the WG_ZERO_F16 indices), bit for bit what
+ * wg_repack_q4_k writes into a WG_ZERO_F16 matrix of the same rows: with
+ * the same quants they make that matrix, which the prefill GEMM reads
+ * without rebuilding them each call. No reference counterpart (a caller
+ * keeping Q4_K records for decode and halves for prompts). */
+int wg_q4k_record_halves(const wg_q4_matrix *m, uint16_t *scales, uint16_t *zeros, void *stream);
 /* Q4_K super-blocks -> WG_LAYOUT_Q4K (a regrouping copy). */
 int wg_repack_q4_k_native(const wg_q4_matrix *dst, int32_t row0, int32_t rows, const void *src,
                           const int32_t *src_rows, void *stream);

@@ -86,13 +86,20 @@ def test_gemm_equals_the_half_zero_form(hip, N, K, M):
     a = torch.from_numpy(O.f32_to_h2(rng.standard_normal((M, K)).astype(np.float32))
                          .view(np.int16)).cuda()
     ya = ops.gemm(f16, a)
-    yb = ops.gemm(rec, a)
+    yb = ops.gemm(rec, a, kept=False)  # the library's rebuild each call
+    yc = ops.gemm(rec, a)              # the kept halves (wg_q4k_record_halves)
     torch.cuda.synchronize()
     assert torch.equal(ya.view(torch.int32), yb.view(torch.int32))
+    assert torch.equal(ya.view(torch.int32), yc.view(torch.int32))
     sa = ops.gemm_swiglu(f16, a)
-    sb = ops.gemm_swiglu(rec, a)
+    sb = ops.gemm_swiglu(rec, a, kept=False)
+    sc = ops.gemm_swiglu(rec, a)
     torch.cuda.synchronize()
     assert torch.equal(sa.view(torch.int16), sb.view(torch.int16))
+    assert torch.equal(sa.view(torch.int16), sc.view(torch.int16))
+    # the kept halves are the half-zero-point repack's arrays
+    rec.prompt_desc()
+    assert torch.equal(rec._halves[0], f16.scales) and torch.equal(rec._halves[1], f16.zeros)
 
 
 def test_gemm_refuses_capture(hip):
@@ -107,7 +114,7 @@ def test_gemm_refuses_capture(hip):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=st):
             try:
-                ops.gemm(rec, a, out=out)
+                ops.gemm(rec, a, out=out, kept=False)
             except Exception as e:  # refused before any launch: nothing captured
                 raised = e
     torch.cuda.synchronize()

@@ -510,6 +510,21 @@ int wg_repack_q4_k(const wg_q4_matrix *m, int32_t row0, int32_t rows, const void
   return launched("wg_repack_q4_k");
 }
 
+int wg_q4k_record_halves(const wg_q4_matrix *m, uint16_t *scales, uint16_t *zeros,
+                         void *stream) {
+  int rc = check_matrix(m, "wg_q4k_record_halves");
+  if (rc) return rc;
+  WG_REQUIRE(m->layout == WG_LAYOUT_ROWGROUP && m->zero == WG_ZERO_Q4K,
+             "wg_q4k_record_halves: the matrix holds no Q4_K records");
+  WG_REQUIRE(scales && zeros, "wg_q4k_record_halves: null output");
+  // (bytes: N K / 32 halves each; the records are N K / 16 bytes too)
+  const size_t n = (size_t)m->N * (m->K / 32) * 2;
+  WG_REQUIRE(!overlaps(scales, n, zeros, n) && !overlaps(scales, n, m->scales, n) &&
+                 !overlaps(zeros, n, m->scales, n),
+             "wg_q4k_record_halves: outputs overlap each other or the records");
+  return launch_q4k_expand(m, scales, zeros, as_stream(stream));
+}
+
 int wg_repack_q4_k_native(const wg_q4_matrix *m, int32_t row0, int32_t rows, const void *src,
                           const int32_t *src_rows, void *stream) {
   int rc = check_matrix(m, "wg_repack_q4_k_native");

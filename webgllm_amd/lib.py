@@ -170,6 +170,7 @@ def load():
                                   C.POINTER(SZ)]),
         "wg_repack_q4_0": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),
         "wg_repack_q4_k": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),
+        "wg_q4k_record_halves": (C.c_int, [C.POINTER(Q4MatrixDesc), P, P, P]),
         "wg_repack_q4_k_native": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),
         "wg_repack_nbits": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P, P, P]),
         "wg_repack_q8_0": (C.c_int, [C.POINTER(Q4MatrixDesc), I32, I32, P, P, P]),

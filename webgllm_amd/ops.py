@@ -156,6 +156,22 @@ class Q4Matrix:
         L.check(L.load().wg_repack_q6_k(C.byref(self.desc), row0, rows, _p(_dev(src)),
                                         _p(src_rows), _stream()))
 
+    def prompt_desc(self):
+        """The descriptor the prefill GEMM takes: for Q4_K records, the same
+        quants with packQ4_K's half scales and zero points, made once
+        (wg_q4k_record_halves) and kept beside the records (0.125 bytes a
+        weight, never read by the GEMVs); else the matrix itself."""
+        if self.zero != L.ZERO_Q4K:
+            return self.desc
+        if getattr(self, "_halves", None) is None:
+            n = self.N * (self.K // 32)
+            sc = torch.empty(n, dtype=torch.int16, device=self.quants.device)
+            zr = torch.empty(n, dtype=torch.int16, device=self.quants.device)
+            L.check(L.load().wg_q4k_record_halves(C.byref(self.desc), _p(sc), _p(zr), _stream()))
+            self._halves = (sc, zr, L.Q4MatrixDesc(self.N, self.K, L.LAYOUT_ROWGROUP, L.ZERO_F16,
+                                                   _p(self.quants), _p(sc), _p(zr)))
+        return self._halves[2]
+
     def dequant(self, row0: int = 0, rows: int | None = None) -> torch.Tensor:
         rows = self.N - row0 if rows is None else rows
         out = torch.empty((rows, self.K), dtype=torch.float32, device=self.quants.device)
@@ -208,10 +224,12 @@ def gemv_short_conv(m: Q4Matrix, x16: torch.Tensor, epilogue: "L.Epilogue") -> b
 
 def gemm(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
          residual: torch.Tensor | None = None, col_of: torch.Tensor | None = None,
-         row_scale: torch.Tensor | None = None) -> torch.Tensor:
+         row_scale: torch.Tensor | None = None, kept: bool = True) -> torch.Tensor:
     """C = A W^T on MFMA for M tokens of half activations A [M, K]; col_of
     (int32 [N], optional) sends stored row n to output column col_of[n];
-    row_scale (float32 [M], optional) multiplies row m's sums."""
+    row_scale (float32 [M], optional) multiplies row m's sums. Q4_K records
+    go through their kept halves (prompt_desc), or with kept=False through
+    the library's rebuild each call: the same bits."""
     if a16.dtype not in (torch.float16, torch.int16):
         raise ValueError("activations must be halves")
     a16 = _dev(a16)
@@ -219,7 +237,8 @@ def gemm(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
     if out is None:
         out = torch.empty((M, m.N), dtype=torch.float32, device=a16.device)
     _dev(out, torch.float32)
-    L.check(L.load().wg_q4_gemm(C.byref(m.desc), _p(a16), M, a16.shape[1], _p(out), out.shape[1],
+    desc = m.prompt_desc() if kept else m.desc
+    L.check(L.load().wg_q4_gemm(C.byref(desc), _p(a16), M, a16.shape[1], _p(out), out.shape[1],
                                 _p(residual), residual.shape[1] if residual is not None else 0,
                                 _p(None if row_scale is None else _dev(row_scale, torch.float32)),
                                 _p(None if col_of is None else _dev(col_of, torch.int32)),
@@ -228,7 +247,7 @@ def gemm(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
 
 
 def gemm_swiglu(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
-                row_scale: torch.Tensor | None = None) -> torch.Tensor:
+                row_scale: torch.Tensor | None = None, kept: bool = True) -> torch.Tensor:
     """half(silu(gate) * up) [M, N / 2] of A W^T on MFMA, for a gate|up
     matrix stored in the SwiGLU row order (gate 2i, gate 2i + 1, up 2i,
     up 2i + 1 per row group)."""
@@ -239,7 +258,8 @@ def gemm_swiglu(m: Q4Matrix, a16: torch.Tensor, out: torch.Tensor | None = None,
     if out is None:
         out = torch.empty((M, m.N // 2), dtype=torch.float16, device=a16.device)
     _dev(out)
-    L.check(L.load().wg_q4_gemm_swiglu(C.byref(m.desc), _p(a16), M, a16.shape[1], _p(out),
+    desc = m.prompt_desc() if kept else m.desc
+    L.check(L.load().wg_q4_gemm_swiglu(C.byref(desc), _p(a16), M, a16.shape[1], _p(out),
                                        out.shape[1],
                                        _p(None if row_scale is None else
                                           _dev(row_scale, torch.float32)), _stream()))
