@@ -16,6 +16,7 @@ namespace wg {
 namespace {
 
 constexpr int MAX_VERIFY_ROWS = 8;
+constexpr int CPT = 8;  // state floats a thread copies (the grid covers max_state with them)
 
 // Rows kept of a batch whose inputs are ids[0..rows) (ids[1..] the drafts)
 // and whose greedy picks are picks[0..rows): 1 + the agreeing prefix.
@@ -74,12 +75,21 @@ __global__ __launch_bounds__(256) void verify_accept_kernel(
   const int kept = kept_of(d, p, rows);
   const int l = blockIdx.y;
   if (l < n_conv) {
+    // CPT floats a thread, every load issued before the first store (the
+    // state and the prefixes are separate arrays, but a loop of single
+    // copies had waited for each load in turn)
     const wg_conv_state c = convs[l];
     const int64_t n = (int64_t)(c.width - 1) * c.dim;
     const float *src = c.prefixes + (int64_t)(kept - 1) * n;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (int64_t)gridDim.x * blockDim.x)
-      c.state[i] = src[i];
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < n; i0 += CPT * step) {
+      float v[CPT];
+#pragma unroll
+      for (int k = 0; k < CPT; k++) v[k] = i0 + k * step < n ? src[i0 + k * step] : 0.0f;
+#pragma unroll
+      for (int k = 0; k < CPT; k++)
+        if (i0 + k * step < n) c.state[i0 + k * step] = v[k];
+    }
   }
   if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
     const int p0 = *pos;
@@ -126,7 +136,7 @@ int wg_verify_accept(const int32_t *picks, int32_t rows, const wg_conv_state *co
   WG_REQUIRE(hist_len >= 0 && (hist || !hist_len) && log_len >= 0 && (kept_log || !log_len),
              "wg_verify_accept: bad history or log");
   // every conv state (W - 1) x D floats is at most max_state: the grid covers it
-  const int per = 256 * 8;
+  const int per = 256 * CPT;
   const unsigned gx = (unsigned)(max_state > 0 ? (max_state + per - 1) / per : 1);
   dim3 grid(gx, (unsigned)(n_conv > 0 ? n_conv : 1));
   // ids is read (the drafts) and written (ids[0]) by the same launch: the
@@ -154,7 +164,7 @@ int wg_verify_accept_parts(const void *pick_parts, int32_t *picks_out, int32_t r
              "wg_verify_accept_parts: the picks and the batch's ids overlap");
   WG_REQUIRE(hist_len >= 0 && (hist || !hist_len) && log_len >= 0 && (kept_log || !log_len),
              "wg_verify_accept_parts: bad history or log");
-  const int per = 256 * 8;
+  const int per = 256 * CPT;
   const unsigned gx = (unsigned)(max_state > 0 ? (max_state + per - 1) / per : 1);
   dim3 grid(gx, (unsigned)(n_conv > 0 ? n_conv : 1));
   verify_accept_kernel<true><<<grid, 256, 0, as_stream(stream)>>>(
