@@ -31,10 +31,13 @@ __device__ inline int kept_of(const int32_t *ids, const int32_t *picks, int rows
 // picks into hist after the position, the last of them into ids[0], the
 // position by kept, kept into the log at the cursor, and the cursor on.
 // PARTS: the picks are finished here from a head GEMV's pick parts (as
-// wg_argmax_parts finishes them; wave w takes rows w and w + 4, its lanes
-// every part at once), and workgroup 0 writes them to picks_out.
+// wg_argmax_parts finishes them; wave w takes row w, its lanes every part
+// at once, the first 1024 loaded with the parts' count, not after it: the
+// slots past the count are in the array and left out once it arrives),
+// and workgroup 0 writes them to picks_out.
+constexpr int ACCEPT_THREADS = 64 * MAX_VERIFY_ROWS;
 template <bool PARTS>
-__global__ __launch_bounds__(256) void verify_accept_kernel(
+__global__ __launch_bounds__(ACCEPT_THREADS) void verify_accept_kernel(
     const int32_t *ids_in, const int32_t *picks, int rows, const wg_conv_state *convs,
     int n_conv, int32_t *pos, int32_t *ids, int32_t *hist, int32_t hist_len, int32_t *kept_log,
     int32_t log_len, int32_t *cursor, const char *pick_parts, int32_t *picks_out) {
@@ -42,26 +45,30 @@ __global__ __launch_bounds__(256) void verify_accept_kernel(
   if constexpr (PARTS) {
     constexpr int PER = WG_PICK_SLOTS / 64;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int i = wave;  // (a wave a row: MAX_VERIFY_ROWS waves)
+    const uint2 *row =
+        reinterpret_cast<const uint2 *>(pick_parts + PICK_HEADER) + (int64_t)min(i, rows - 1) * WG_PICK_SLOTS;
+    uint2 raw[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) raw[k] = row[lane + 64 * k];
     const int parts = min(*reinterpret_cast<const int *>(pick_parts), WG_PICK_SLOTS);
-    for (int i = wave; i < rows; i += 4) {
-      const uint2 *row =
-          reinterpret_cast<const uint2 *>(pick_parts + PICK_HEADER) + (int64_t)i * WG_PICK_SLOTS;
-      PickBest b{PICK_FLOOR, PICK_NONE};
-      for (int k0 = 0; k0 < PER && 64 * k0 < parts; k0 += 16) {
-        uint2 raw[16];
+    PickBest b{PICK_FLOOR, PICK_NONE};
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-          const int at = lane + 64 * (k0 + k);
-          raw[k] = at < parts ? row[at]
-                              : make_uint2(__float_as_uint(PICK_FLOOR), (uint32_t)PICK_NONE);
-        }
+    for (int k = 0; k < 16; k++)
+      if (lane + 64 * k < parts) b = pick_better(b, PickBest{__uint_as_float(raw[k].x), (int)raw[k].y});
+    for (int k0 = 16; k0 < PER && 64 * k0 < parts; k0 += 16) {
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-          b = pick_better(b, PickBest{__uint_as_float(raw[k].x), (int)raw[k].y});
+      for (int k = 0; k < 16; k++) {
+        const int at = lane + 64 * (k0 + k);
+        raw[k] = at < parts ? row[at]
+                            : make_uint2(__float_as_uint(PICK_FLOOR), (uint32_t)PICK_NONE);
       }
-      b = pick_wave_best(b);
-      if (lane == 0) p[i] = b.id == PICK_NONE ? 0 : b.id;
+#pragma unroll
+      for (int k = 0; k < 16; k++)
+        b = pick_better(b, PickBest{__uint_as_float(raw[k].x), (int)raw[k].y});
     }
+    b = pick_wave_best(b);
+    if (lane == 0 && i < rows) p[i] = b.id == PICK_NONE ? 0 : b.id;
     if (threadIdx.x < rows) d[threadIdx.x] = ids_in[threadIdx.x];
     __syncthreads();
     if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < rows) picks_out[threadIdx.x] = p[threadIdx.x];
@@ -136,13 +143,13 @@ int wg_verify_accept(const int32_t *picks, int32_t rows, const wg_conv_state *co
   WG_REQUIRE(hist_len >= 0 && (hist || !hist_len) && log_len >= 0 && (kept_log || !log_len),
              "wg_verify_accept: bad history or log");
   // every conv state (W - 1) x D floats is at most max_state: the grid covers it
-  const int per = 256 * CPT;
+  const int per = ACCEPT_THREADS * CPT;
   const unsigned gx = (unsigned)(max_state > 0 ? (max_state + per - 1) / per : 1);
   dim3 grid(gx, (unsigned)(n_conv > 0 ? n_conv : 1));
   // ids is read (the drafts) and written (ids[0]) by the same launch: the
   // kernel reads the drafts into LDS before workgroup 0 writes ids[0]; the
   // other workgroups read ids[1 ..] only
-  verify_accept_kernel<false><<<grid, 256, 0, as_stream(stream)>>>(
+  verify_accept_kernel<false><<<grid, ACCEPT_THREADS, 0, as_stream(stream)>>>(
       ids, picks, rows, convs, n_conv, pos, ids, hist, hist_len, kept_log, log_len, cursor,
       nullptr, nullptr);
   return launched("wg_verify_accept");
@@ -164,10 +171,10 @@ int wg_verify_accept_parts(const void *pick_parts, int32_t *picks_out, int32_t r
              "wg_verify_accept_parts: the picks and the batch's ids overlap");
   WG_REQUIRE(hist_len >= 0 && (hist || !hist_len) && log_len >= 0 && (kept_log || !log_len),
              "wg_verify_accept_parts: bad history or log");
-  const int per = 256 * CPT;
+  const int per = ACCEPT_THREADS * CPT;
   const unsigned gx = (unsigned)(max_state > 0 ? (max_state + per - 1) / per : 1);
   dim3 grid(gx, (unsigned)(n_conv > 0 ? n_conv : 1));
-  verify_accept_kernel<true><<<grid, 256, 0, as_stream(stream)>>>(
+  verify_accept_kernel<true><<<grid, ACCEPT_THREADS, 0, as_stream(stream)>>>(
       ids, nullptr, rows, convs, n_conv, pos, ids, hist, hist_len, kept_log, log_len, cursor,
       (const char *)pick_parts, picks_out);
   return launched("wg_verify_accept_parts");
