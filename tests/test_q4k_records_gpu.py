@@ -97,9 +97,16 @@ def test_gemm_equals_the_half_zero_form(hip, N, K, M):
     torch.cuda.synchronize()
     assert torch.equal(sa.view(torch.int16), sb.view(torch.int16))
     assert torch.equal(sa.view(torch.int16), sc.view(torch.int16))
-    # the kept halves are the half-zero-point repack's arrays
+    # the kept halves are the half-zero-point repack's arrays, made again
+    # after the rows are repacked
     rec.prompt_desc()
     assert torch.equal(rec._halves[0], f16.scales) and torch.equal(rec._halves[1], f16.zeros)
+    rec.repack_q4_k(0, 4, ops.to_device_bytes(np.zeros(K // 256 * 144 * 4, np.uint8)))
+    assert rec._halves is None
+    rec.prompt_desc()
+    torch.cuda.synchronize()
+    # (all-zero super-blocks: constant blocks of scale -0)
+    assert not (rec._halves[0][:K // 32 * 4] & 0x7FFF).any()
 
 
 def test_gemm_refuses_capture(hip):
@@ -117,6 +124,7 @@ def test_gemm_refuses_capture(hip):
                 ops.gemm(rec, a, out=out, kept=False)
             except Exception as e:  # refused before any launch: nothing captured
                 raised = e
+            out.zero_()  # (a graph of one fill, not an empty one)
     torch.cuda.synchronize()
     assert raised is not None and "under capture" in str(raised)
 

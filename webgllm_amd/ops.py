@@ -133,6 +133,7 @@ class Q4Matrix:
                                         _p(src_rows), _stream()))
 
     def repack_q4_k(self, row0, rows, src, src_rows=None):
+        self._halves = None  # (prompt_desc's halves are made again from the new rows)
         L.check(L.load().wg_repack_q4_k(C.byref(self.desc), row0, rows, _p(_dev(src)),
                                         _p(src_rows), _stream()))
 
