@@ -114,6 +114,27 @@ async function gpu (dir) {
   const dq = gpu.texture(GL.R32F, K, 4)
   gpu.ops.dequant(w, 8, 4, dq)
   fs.writeFileSync(path.join(dir, 'dequant.bin'), Buffer.from(gpu.readNow(dq).buffer))
+  // a Q4_K-records matrix: repacked from Q4_K blocks, its prompt halves kept
+  const src4 = fs.readFileSync(path.join(dir, 'q4_k.bin'))
+  const N4 = 64
+  const s4 = hip.quantSizes(N4, K, hip.constants.LAYOUT_ROWGROUP, hip.constants.ZERO_Q4K)
+  assert.strictEqual(s4.zeros, 0)
+  assert.strictEqual(s4.quants + s4.scales, N4 * K / 256 * 144)
+  const t4 = gpu.texture(GL.R8UI, src4.length, 1, { format: 0, type: 0, pixels: src4 })
+  const w4 = {
+    N: N4, K, layout: hip.constants.LAYOUT_ROWGROUP, zero: hip.constants.ZERO_Q4K,
+    quants: gpu.texture(GL.RGBA32UI, s4.quants / 16, 1),
+    scales: gpu.texture(GL.R8UI, s4.scales, 1)
+  }
+  gpu.ops.repack('q4_k', w4, 0, N4, t4)
+  const halves = gpu.texture(GL.R8UI, N4 * K / 32 * 4, 1)
+  gpu.ops.q4kRecordHalves(w4, halves, gpu.view(halves, N4 * K / 32 * 2))
+  fs.writeFileSync(path.join(dir, 'q4k_halves.bin'), Buffer.from(gpu.readNow(halves).buffer))
+  const dq4 = gpu.texture(GL.R32F, K, 4)
+  gpu.ops.dequant(w4, 4, 4, dq4)
+  fs.writeFileSync(path.join(dir, 'q4k_dequant.bin'), Buffer.from(gpu.readNow(dq4).buffer))
+  throwsGpu(() => gpu.ops.q4kRecordHalves(w4, gpu.texture(GL.R8UI, 16, 1), halves), 'WG_ERR_INVALID', 'scales')
+  throwsGpu(() => gpu.ops.q4kRecordHalves(w, halves, halves), 'WG_ERR_INVALID')
   // bad shapes are refused before any launch
   throwsGpu(() => gpu.ops.gemv(Object.assign({}, w, { K: K + 1 }), tx, M, ty), 'WG_ERR_INVALID')
   // operands smaller than their shapes imply are refused before any launch

@@ -89,6 +89,11 @@ def test_addon_textures_and_q4_0_gemv(hip, tmp_path):
     (tmp_path / "q4_0.bin").write_bytes(np.ascontiguousarray(src).tobytes())
     (tmp_path / "x16.bin").write_bytes(np.ascontiguousarray(x16).tobytes())
     (tmp_path / "gemv.json").write_text(json.dumps({"N": N, "K": K, "M": M}))
+    # Q4_K blocks for a Q4_K-records matrix (N4 x K, zero scales in some)
+    from tests.helpers import random_q4_k_bytes
+    N4 = 64
+    src4 = random_q4_k_bytes(rng, N4, K, zero_scale_every=3)
+    (tmp_path / "q4_k.bin").write_bytes(np.ascontiguousarray(src4).tobytes())
     out = _run(["gpu", str(tmp_path)])
     qm = O.QuantMatrix(N, K, False)
     O.pack_q4_0(qm, 0, src, N)
@@ -98,4 +103,12 @@ def test_addon_textures_and_q4_0_gemv(hip, tmp_path):
     assert out["picks"] == [O.argmax(y[m])[0] for m in range(M)]
     dq = np.frombuffer((tmp_path / "dequant.bin").read_bytes(), np.float32).reshape(4, K)
     assert np.array_equal(dq.view(np.uint32), qm.dense()[8:12].view(np.uint32))
+    # the records matrix's kept halves are packQ4_K's, its dequant packQ4_K's rows
+    q4 = O.QuantMatrix(N4, K, "halves")
+    O.pack_q4_k(q4, 0, src4, N4)
+    halves = np.frombuffer((tmp_path / "q4k_halves.bin").read_bytes(), np.uint16)
+    assert np.array_equal(halves[:q4.scales.size], q4.scales)
+    assert np.array_equal(halves[q4.scales.size:], q4.zero_halves)
+    dq4 = np.frombuffer((tmp_path / "q4k_dequant.bin").read_bytes(), np.float32).reshape(4, K)
+    assert np.array_equal(dq4.view(np.uint32), q4.dense()[4:8].view(np.uint32))
     assert 1 <= out["staging"]["slots"] <= 18

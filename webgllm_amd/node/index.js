@@ -280,6 +280,10 @@ class HipGpu {
         call(addon.repack, ctx, kind, matrix(w), row0, rows, o(src), srcRows || null),
       /** matrixRow (src/repack.ts:865-891) into an R32F texture. */
       dequant: (w, row0, rows, out) => call(addon.dequant, ctx, matrix(w), row0, rows, o(out)),
+      /** packQ4_K's half scales and zero points of a Q4_K-records matrix (N K / 32 halves each),
+       *  kept for the prompt GEMMs: with its quants they form the half-zero-point matrix. */
+      q4kRecordHalves: (w, scales, zeros) =>
+        call(addon.q4kRecordHalves, ctx, matrix(w), o(scales), o(zeros)),
       /**
        * splitPartials + pf and the passes folded into it (src/engine.ts:5241-5377,
        * src/gpu/kernels.ts:744-895, :1169-1361): y = x W^T for M <= 8 rows of

@@ -811,6 +811,19 @@ static napi_value js_dequant(napi_env env, napi_callback_info info) {
   DONE(wg_q4_dequant(&m, row0, rows, out, ctx_stream(c)));
 }
 
+/* q4kRecordHalves(ctx, matrix, scales, zeros): packQ4_K's half scales and
+ * zero points of a Q4_K-records matrix (N K / 32 halves each), kept for
+ * the prompt GEMMs (no reference counterpart; packQ4_K's own arrays). */
+static napi_value js_q4k_record_halves(napi_env env, napi_callback_info info) {
+  ARGS(4);
+  HANDLE_ARG(0, wg_ctx, c, H_CTX, "context");
+  MATRIX_ARG(1, m);
+  const uint64_t n = (uint64_t)m.N * (uint64_t)(m.K / 32) * 2;
+  OPERAND(2, uint16_t, scales, n, 0, "scales");
+  OPERAND(3, uint16_t, zeros, n, 0, "zeros");
+  DONE(wg_q4k_record_halves(&m, scales, zeros, ctx_stream(c)));
+}
+
 /* gemv(ctx, matrix, x, M, y, epilogue?, ldx?, ldy?): splitPartials + pf and
  * the passes folded into it (engine.ts:5241-5377; kernels.ts:744-895,
  * :1169-1361): y [M][ldy] f32 = x [M][ldx] halves times W^T, with the
@@ -1504,6 +1517,7 @@ static napi_value init(napi_env env, napi_value exports) {
       {"fence", js_fence_record},
       {"repack", js_repack},
       {"dequant", js_dequant},
+      {"q4kRecordHalves", js_q4k_record_halves},
       {"gemv", js_gemv},
       {"gemm", js_gemm},
       {"gemmSwiglu", js_gemm_swiglu},
