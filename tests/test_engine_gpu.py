@@ -1,6 +1,6 @@
 """End-to-end decode and speculative verify through the HIP kernels against
 the CPU decoder over the oracle: identical greedy tokens, logits within
-rel-L2 1e-3 (the north star's bar)."""
+rel-L2 1e-3 (the parity bar)."""
 import numpy as np
 import pytest
 import torch

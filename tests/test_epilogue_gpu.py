@@ -38,7 +38,7 @@ FMTS = ["q4_0", "nbits", "q4_k", "q4_k_rowgroup", "q4_k_records", "q8_0", "q6_k"
 
 def _tol(fmt, tight):
     # Q4_K records weigh a block's zero term as dmin m, not packQ4_K's d'
-    # half(dmin m / d') that the oracle computes: the north star's 1e-3
+    # half(dmin m / d') that the oracle computes: the 1e-3 rel-L2 parity bar
     # then, rather than the float32 sums' tighter margin
     return 1e-3 if fmt == "q4_k_records" else tight
 

@@ -1,5 +1,5 @@
 """Prefill GEMM on MFMA against the oracle. Two references: the exact
-dequantized weights in float64 (the north star's rel-L2 <= 1e-3 bar), and
+dequantized weights in float64 (the rel-L2 <= 1e-3 parity bar), and
 the weights rounded to halves the way the reference's dequantOut stores them
 (src/gpu/kernels.ts:436-597), which the GEMM must match to float32
 accumulation error."""

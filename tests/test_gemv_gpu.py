@@ -1,5 +1,5 @@
 """Decode / few-token GEMV against the oracle (fp64 over the reference's
-dequantized weights): rel-L2 <= 1e-3, the north star's bar (in practice
+dequantized weights): rel-L2 <= 1e-3, the parity bar (in practice
 ~1e-6: products are exact and sums float32)."""
 import numpy as np
 import pytest
