@@ -157,3 +157,23 @@ def test_gemv_close_to_the_half_zero_form(hip, few_path, N, K, M):
     err = rel_l2(_np(yb), _np(ya))
     print(f"{few_path} N={N} K={K} M={M} rel-L2 {err:.2e}")
     assert err <= 2e-4
+
+
+@pytest.mark.parametrize("N,K", [(2048, 4096), (6144, 2048), (4096, 14336)])
+def test_few_rows_take_the_kept_halves(hip, N, K):
+    """With its halves kept, a records matrix's 3-8-row GEMVs at K <= 4096
+    run on the half-zero-point form (the MFMA kernel): its bits; deeper
+    rows and 1-2 rows stay on the records."""
+    from webgllm_amd import ops
+    rng = np.random.default_rng(N + K)
+    _, f16, rec = _pair(rng, N, K, zero_every=5)
+    rec.prompt_desc()
+    for M in (1, 5, 8):
+        x = torch.from_numpy(O.f32_to_h2(rng.standard_normal((M, K)).astype(np.float32))
+                             .view(np.int16)).cuda()
+        ya, yb = ops.gemv(f16, x), ops.gemv(rec, x)
+        torch.cuda.synchronize()
+        if M >= 3 and K <= 4096:
+            assert torch.equal(ya.view(torch.int32), yb.view(torch.int32)), M
+        else:
+            assert rel_l2(_np(yb), _np(ya)) <= 2e-4, M

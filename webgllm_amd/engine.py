@@ -184,6 +184,8 @@ class Weights:
             rec[:, 0:4] = hdr.half().view(torch.uint8)
             m = ops.Q4Matrix.from_q4_k(src, N, K, native=fmt == "q4_k", src_rows=src_rows,
                                        records=fmt == "q4_k_records")
+            if fmt == "q4_k_records":
+                m.prompt_desc()  # the halves prompts and few-token batches read, made now
         elif fmt == "q4_0":
             src = torch.empty(N * (K // 32) * 18, dtype=torch.uint8, device=dev)
             src.random_(0, 256, generator=g)

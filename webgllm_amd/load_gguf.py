@@ -211,6 +211,7 @@ class _Uploader:
             # bytes a weight; dequant rebuilds packQ4_K's halves bit for bit)
             m = ops.Q4Matrix(N, K, L.LAYOUT_ROWGROUP, L.ZERO_Q4K, device=self.device)
             m.repack_q4_k(0, N, self._cat(parts), src_rows)
+            m.prompt_desc()  # packQ4_K's halves for prompts and few-token batches
         elif G.Q4_0 in types:
             if types != {G.Q4_0}:
                 raise ValueError(f"GGUF: {parts[0][0]} can't be combined with "

@@ -161,7 +161,8 @@ class Q4Matrix:
         """The descriptor the prefill GEMM takes: for Q4_K records, the same
         quants with packQ4_K's half scales and zero points, made once
         (wg_q4k_record_halves) and kept beside the records (0.125 bytes a
-        weight, never read by the GEMVs); else the matrix itself."""
+        weight, never read by one- and two-row GEMVs; gemv takes them for 3
+        to 8 rows where K <= 4096); else the matrix itself."""
         if self.zero != L.ZERO_Q4K:
             return self.desc
         if getattr(self, "_halves", None) is None:
@@ -200,7 +201,14 @@ def gemv(m: Q4Matrix, x16: torch.Tensor, out: torch.Tensor | None = None,
                             row_scale=_p(row_scale))
     if out is not None:
         _dev(out, torch.float32)
-    L.check(L.load().wg_q4_gemv(C.byref(m.desc), _p(x16), M, ldx, _p(out),
+    desc = m.desc
+    if M >= 3 and m.zero == L.ZERO_Q4K and m.K <= 4096 and \
+            getattr(m, "_halves", None) is not None:
+        # 3 to 8 rows of Q4_K records through their kept halves: the MFMA
+        # form takes half zero points, not records (at the 8B shape a
+        # 5-row gate|up took 35.1 us on the records' vector form, 18.2 here)
+        desc = m._halves[2]
+    L.check(L.load().wg_q4_gemv(C.byref(desc), _p(x16), M, ldx, _p(out),
                                 out.shape[-1] if out is not None else 0,
                                 C.byref(ep) if ep is not None else None, _stream()))
     return out
