@@ -181,6 +181,19 @@ class Q4Matrix:
         return out
 
 
+def _gemv_desc(m: Q4Matrix, M: int) -> "L.Q4MatrixDesc":
+    """The matrix a GEMV of M rows reads: 3 to 8 rows of Q4_K records at
+    K <= 4096 go through their kept halves (prompt_desc), since the MFMA
+    form takes half zero points, not records (at the 8B shape a 5-row
+    gate|up took 35.1 us on the records' vector form, 18.2 on the halves);
+    every GEMV entry routes alike, so the fused epilogues give the plain
+    GEMV's bits."""
+    if M >= 3 and m.zero == L.ZERO_Q4K and m.K <= 4096 and \
+            getattr(m, "_halves", None) is not None:
+        return m._halves[2]
+    return m.desc
+
+
 def gemv(m: Q4Matrix, x16: torch.Tensor, out: torch.Tensor | None = None,
          residual: torch.Tensor | None = None, row_scale: torch.Tensor | None = None,
          epilogue: "L.Epilogue | None" = None):
@@ -201,14 +214,7 @@ def gemv(m: Q4Matrix, x16: torch.Tensor, out: torch.Tensor | None = None,
                             row_scale=_p(row_scale))
     if out is not None:
         _dev(out, torch.float32)
-    desc = m.desc
-    if M >= 3 and m.zero == L.ZERO_Q4K and m.K <= 4096 and \
-            getattr(m, "_halves", None) is not None:
-        # 3 to 8 rows of Q4_K records through their kept halves: the MFMA
-        # form takes half zero points, not records (at the 8B shape a
-        # 5-row gate|up took 35.1 us on the records' vector form, 18.2 here)
-        desc = m._halves[2]
-    L.check(L.load().wg_q4_gemv(C.byref(desc), _p(x16), M, ldx, _p(out),
+    L.check(L.load().wg_q4_gemv(C.byref(_gemv_desc(m, M)), _p(x16), M, ldx, _p(out),
                                 out.shape[-1] if out is not None else 0,
                                 C.byref(ep) if ep is not None else None, _stream()))
     return out
@@ -223,7 +229,7 @@ def gemv_short_conv(m: Q4Matrix, x16: torch.Tensor, epilogue: "L.Epilogue") -> b
         raise ValueError("activations must be halves")
     x16 = _dev(x16)
     M = x16.shape[0] if x16.dim() == 2 else 1
-    rc = L.load().wg_q4_gemv(C.byref(m.desc), _p(x16), M, x16.shape[-1], None, 0,
+    rc = L.load().wg_q4_gemv(C.byref(_gemv_desc(m, M)), _p(x16), M, x16.shape[-1], None, 0,
                              C.byref(epilogue), _stream())
     if rc == L.ERR_UNSUPPORTED:
         return False
@@ -523,7 +529,7 @@ def gemv_pick(m: Q4Matrix, x16: torch.Tensor, out: torch.Tensor, parts: torch.Te
     ep.pick_parts = parts.data_ptr()
     x16 = _dev(x16)
     M = x16.shape[0] if x16.dim() == 2 else 1
-    rc = L.load().wg_q4_gemv(C.byref(m.desc), _p(x16), M, x16.shape[-1], _p(out),
+    rc = L.load().wg_q4_gemv(C.byref(_gemv_desc(m, M)), _p(x16), M, x16.shape[-1], _p(out),
                              out.shape[-1], C.byref(ep), _stream())
     if rc == L.ERR_UNSUPPORTED:
         return False
