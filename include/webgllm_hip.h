@@ -47,7 +47,9 @@ const char *wg_version(void);
  * GEMV workgroups per compute unit) and
  * "gemv_min_waves" (below this many waves a GEMV splits K inside a
  * workgroup) and "gemm_tile" (prefill GEMM tile: 1 64 x 128, 2 128 x 128,
- * 3 128 x 256, or 0 to choose by shape).
+ * 3 128 x 256, or 0 to choose by shape) and "gemm_pingpong" (its 128 x 256
+ * tiles with two wave groups half a K step apart, 1, or in lock-step, 0,
+ * the default: the lock-step form runs two workgroups a compute unit).
  * Process-wide; results never depend on them. */
 int wg_tuning_set(const char *name, int32_t value);
 int wg_tuning_get(const char *name, int32_t *value);

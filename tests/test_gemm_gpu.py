@@ -271,3 +271,37 @@ def test_gemm_split_k_prefill_shape_in_graph(hip):
     torch.cuda.synchronize()
     assert torch.equal(out, unsplit)
     assert rel_l2(eager.cpu().numpy(), unsplit.cpu().numpy()) <= 1e-6
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "nbits", "q4_k_rowgroup", "q8"])
+@pytest.mark.parametrize("K,ks", [(64, 1), (256, 2), (2048, 1), (2048, 4)])
+@pytest.mark.parametrize("M", [1, 200, 640])
+def test_gemm_pingpong_same_bits(hip, fmt, K, ks, M):
+    """The 128 x 256 tile's two schedules, the wave groups half a step apart
+    (gemm_pingpong 1) and in lock-step (0), add the same products in the
+    same order: the same bits, plain and fused with SwiGLU, at one K step,
+    fewer steps than the ring's stages, and split K (test_gemm_every_tile
+    holds the default, lock-step, form to the oracle)."""
+    from webgllm_amd import engine as E, lib as L, ops
+    if fmt == "q4_k_rowgroup" and K % 256:
+        pytest.skip("Q4_K rows are whole 256-weight super-blocks")
+    N = 512
+    shape = E.ModelShape("t", K, 1, 1, 1, 4, 4, 4, fmt)
+    w = E.Weights.blank(shape, seed=M + K)
+    m = w.matrix(N, K, E.gate_up_row_order(N // 2))
+    rng = np.random.default_rng(M + K + ks)
+    a = _t(O.f32_to_h2(rng.standard_normal((M, K)).astype(np.float32)).view(np.int16))
+    got = {}
+    L.tuning_set("gemm_tile", 3)
+    L.tuning_set("gemm_splits", ks)
+    try:
+        for pp in (1, 0):
+            L.tuning_set("gemm_pingpong", pp)
+            got[pp] = (ops.gemm(m, a), ops.gemm_swiglu(m, a))
+            torch.cuda.synchronize()
+    finally:
+        L.tuning_set("gemm_pingpong", 0)
+        L.tuning_set("gemm_tile", 0)
+        L.tuning_set("gemm_splits", 0)
+    assert torch.equal(got[1][0].view(torch.int32), got[0][0].view(torch.int32))
+    assert torch.equal(got[1][1].view(torch.int16), got[0][1].view(torch.int16))

@@ -189,7 +189,7 @@ __device__ inline bool count_in(int *count, int expect) {
 // + 1) and C is a half output [M][ldc] of N / 2 columns: half(silu(gate) *
 // up), as REDUCE_SWIGLU (src/gpu/kernels.ts:1066-1077) computes it from
 // the float32 sums.
-template <int ZK, int BM, int BN, int S, int WGM, int WGN, bool SW = false>
+template <int ZK, int BM, int BN, int S, int WGM, int WGN, bool SW = false, bool PP = false>
 __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
     1, gemm_waves_per_simd<ZK, BM, BN, S, WGM * WGN>()))) void gemm_q4_kernel(const uint8_t *__restrict__ quants,
                                                       const uint16_t *__restrict__ scales,
@@ -218,6 +218,9 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave % WGN, h = lane >> 5;
+  // the ping-pong group: waves 0-3 and 4-7 (wave w runs on SIMD w % 4)
+  static_assert(!PP || NWV == 8, "the ping-pong schedule pairs 8 waves");
+  [[maybe_unused]] const int group = wave >> 2;
   // Tile order: ids equal mod 8 (one XCD) run the M tiles of one weight
   // tile in turn, so it is read from HBM once into that XCD's L2.
   const int tiles_m = (M + BM - 1) / BM, tiles_n = N / BN, tiles = tiles_m * tiles_n;
@@ -301,26 +304,13 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int j = 0; j < 16; j++) acc[t][u][j] = 0.0f;
 
-  for (int s = 0; s < S - 1; s++)
-    if (s < KT) issue(s, s);
-  // Unrolled by S: a step's stage is a constant, so its LDS addresses are
-  // immediate offsets.
-  for (int k0 = 0; k0 < KT; k0 += S) {
-#pragma unroll
-  for (int ss = 0; ss < S; ss++) {
-    const int kt = k0 + ss;
-    if (kt >= KT) break;
-    // this wave's loads of step kt have landed (younger stages may fly on)
-    if (kt + S - 2 < KT) wait_vm<NW * (S - 2)>();
-    else wait_vm<0>();
-    barrier();  // every wave's have, and every wave is done with step kt - 1
-    if (kt + S - 1 < KT) issue(kt + S - 1, (ss + S - 1) % S);
-    const unsigned char *st = smem + ss * STAGE;
-    const uint16_t *As = reinterpret_cast<const uint16_t *>(st);
+  // A step's dequantized weights (its two blocks), kept in registers from
+  // their LDS reads to the step's MFMAs.
+  half8 blo[2][NT], bhi[2][NT];
+  // The step's weight, scale and zero-point reads from LDS and the dequant.
+  auto wreads = [&](const unsigned char *st) {
     const unsigned char *Wq = st + A_BYTES;
     const uint16_t *Ws = reinterpret_cast<const uint16_t *>(st + A_BYTES + WQ);
-    // Every LDS read of the step first (weights, scales, zeros, A chunks),
-    // so their latencies overlap; then the dequant and the MFMAs.
     uint2 wbytes[2][NT], wbytes2[2][NT];
     uint16_t wsc[2][NT];
     float wz[2][NT];
@@ -346,38 +336,87 @@ __global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(
           wz[j][u] = (float)__builtin_bit_cast(
               _Float16, reinterpret_cast<const uint16_t *>(st + A_BYTES + WQ + WS)[rg * 8 + j * 4 + r]);
       }
-    half8 av[2][2][MT];
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
-      for (int step = 0; step < 2; step++) {
-        const int c = 4 * j + 2 * step + h;  // 16-byte chunk of the A rows
+      for (int u = 0; u < NT; u++) {
+        if constexpr (ZK == Q8) dequant8_q8(wbytes[j][u], wbytes2[j][u], wsc[j][u], blo[j][u], bhi[j][u]);
+        else dequant8<ZK>(wbytes[j][u], wsc[j][u], wz[j][u], blo[j][u], bhi[j][u]);
+      }
+  };
+  // The step's A chunks from LDS and its MFMAs.
+  auto amfmas = [&](const unsigned char *st) {
+    const uint16_t *As = reinterpret_cast<const uint16_t *>(st);
+#pragma unroll
+    for (int j = 0; j < 2; j++)  // the two blocks of the step
+#pragma unroll
+      for (int step = 0; step < 2; step++) {  // low nibbles: K 0..15, high: 16..31
+        const int c = 4 * j + 2 * step + h;   // 16-byte chunk of the A rows
+        half8 av[MT];
 #pragma unroll
         for (int t = 0; t < MT; t++) {
           const int row = wm * WM + t * 32 + (lane & 31);
-          av[j][step][t] =
-              *reinterpret_cast<const half8 *>(As + row * 64 + (c ^ ((row >> 1) & 7)) * 8);
+          av[t] = *reinterpret_cast<const half8 *>(As + row * 64 + (c ^ ((row >> 1) & 7)) * 8);
         }
-      }
-#pragma unroll
-    for (int j = 0; j < 2; j++) {  // the two blocks of the step
-      half8 blo[NT], bhi[NT];
-#pragma unroll
-      for (int u = 0; u < NT; u++) {
-        if constexpr (ZK == Q8) dequant8_q8(wbytes[j][u], wbytes2[j][u], wsc[j][u], blo[u], bhi[u]);
-        else dequant8<ZK>(wbytes[j][u], wsc[j][u], wz[j][u], blo[u], bhi[u]);
-      }
-#pragma unroll
-      for (int step = 0; step < 2; step++)  // low nibbles: K 0..15, high: 16..31
 #pragma unroll
         for (int t = 0; t < MT; t++)
 #pragma unroll
           for (int u = 0; u < NT; u++)
-            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[j][step][t],
-                                                              step ? bhi[u] : blo[u], acc[t][u],
-                                                              0, 0, 0);
+            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[t], step ? bhi[j][u] : blo[j][u],
+                                                              acc[t][u], 0, 0, 0);
+      }
+  };
+  // (every LDS read of the wave has returned: a stage another wave fills
+  // next may follow the next barrier)
+  auto reads_done = []() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
+
+  for (int s = 0; s < S - 1; s++)
+    if (s < KT) issue(s, s);
+  // Unrolled by S: a step's stage is a constant, so its LDS addresses are
+  // immediate offsets.
+  for (int k0 = 0; k0 < KT; k0 += S) {
+#pragma unroll
+  for (int ss = 0; ss < S; ss++) {
+    const int kt = k0 + ss;
+    if (kt >= KT) break;
+    // this wave's loads of step kt have landed (younger stages may fly on)
+    if (kt + S - 2 < KT) wait_vm<NW * (S - 2)>();
+    else wait_vm<0>();
+    barrier();  // every wave's have, and every wave is done with step kt - 1
+    const unsigned char *st = smem + ss * STAGE;
+    if constexpr (PP) {
+      // Two wave groups half a step apart, one wave of each on every SIMD:
+      // between two barriers one group dequantizes while the other runs
+      // MFMAs. Group 1 runs step kt - 1's MFMAs, then step kt's dequant;
+      // every wave passes two barriers a step. Step kt + S - 1's loads go
+      // into step kt - 1's stage after the second, once group 1's MFMAs
+      // have read its A chunks. (Holding a step's weights across the
+      // barrier takes ~200 registers, one workgroup a compute unit: 13-30%
+      // slower than two lock-step workgroups at 512-2048 rows, K 4096.)
+      __builtin_amdgcn_sched_barrier(0);
+      if (group) {
+        if (kt > 0) amfmas(smem + ((ss + S - 1) % S) * STAGE);
+      } else {
+        wreads(st);
+      }
+      reads_done();
+      __builtin_amdgcn_sched_barrier(0);
+      barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + S - 1 < KT) issue(kt + S - 1, (ss + S - 1) % S);
+      if (group) wreads(st);
+      else amfmas(st);
+      reads_done();
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      if (kt + S - 1 < KT) issue(kt + S - 1, (ss + S - 1) % S);
+      wreads(st);
+      amfmas(st);
     }
   }
+  }
+  if constexpr (PP) {
+    if (group && KT > 0) amfmas(smem + ((KT - 1) % S) * STAGE);  // group 1's last step
   }
 
   if (ks > 1) {
@@ -609,14 +648,16 @@ int expand_space(hipStream_t s, size_t count, uint16_t **out) {
   return WG_OK;
 }
 
-template <int ZK, int BM, int BN, int S, int WGM = 2, int WGN = 2, bool SW = false>
+template <int ZK, int BM, int BN, int S, int WGM = 2, int WGN = 2, bool SW = false,
+          bool PP = false>
 int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, int ldc,
                  const float *residual, int ldr, const float *row_scale, const int32_t *col_of,
                  hipStream_t s) {
   constexpr int STAGE = BM * 128 + Stage<ZK, BN>::WQ + Stage<ZK, BN>::WS + Stage<ZK, BN>::WZ;
   constexpr size_t LDS = (size_t)S * STAGE;
   if (LDS > 64 * 1024) {  // more than 64 KiB of dynamic LDS
-    const int rc = raise_lds((const void *)gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW>, (int)LDS);
+    const int rc =
+        raise_lds((const void *)gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW, PP>, (int)LDS);
     if (rc) return rc;
   }
   const int tiles = ((M + BM - 1) / BM) * (w->N / BN), steps = w->K / 64;
@@ -643,7 +684,7 @@ int launch_tiles(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float
     if (rc) return rc;
     if (!part) ks = 1;
   }
-  gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW><<<tiles * ks, WGM * WGN * 64, LDS, s>>>(
+  gemm_q4_kernel<ZK, BM, BN, S, WGM, WGN, SW, PP><<<tiles * ks, WGM * WGN * 64, LDS, s>>>(
       (const uint8_t *)w->quants, (const uint16_t *)w->scales, w->zeros, A, lda, C, ldc,
       residual, ldr, row_scale, col_of, M, w->N, w->K, ks, part, count);
   return launched(SW ? "wg_q4_gemm_swiglu" : "wg_q4_gemm");
@@ -665,8 +706,12 @@ int launch(const wg_q4_matrix *w, const uint16_t *A, int M, int lda, float *C, i
     else if (M >= 512 && w->N % 128 == 0) t = 2;
     else if (w->N % 128 == 0) t = 1;
   }
-  if (t == 3 && w->N % 256 == 0)
+  if (t == 3 && w->N % 256 == 0) {
+    if (tuning("gemm_pingpong"))
+      return launch_tiles<ZK, 128, 256, 3, 1, 8, SW, true>(w, A, M, lda, C, ldc, residual, ldr,
+                                                           row_scale, col_of, s);
     return launch_tiles<ZK, 128, 256, 3, 1, 8, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
+  }
   if (t == 2 && w->N % 128 == 0)
     return launch_tiles<ZK, 128, 128, 3, 1, 4, SW>(w, A, M, lda, C, ldc, residual, ldr, row_scale, col_of, s);
   if (w->N % 128 == 0)

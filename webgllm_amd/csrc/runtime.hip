@@ -93,6 +93,7 @@ static Knob g_knobs[] = {
     {"attn_split_chunks", 0, 0, 4},      // its 64-key chunks a workgroup (1, 2, 4; 0 chooses)
     {"attn_split_waves", 1, 0, 1},       // its chunks spread over up to 16 waves (1), or a wave a query (0)
     {"gemm_tile", 0, 0, 3},              // prefill GEMM tile: 0 chooses; 1 64x128, 2 128x128, 3 128x256
+    {"gemm_pingpong", 0, 0, 1},          // 128 x 256 tiles: 1 two wave groups half a step apart, 0 in lock-step
     {"gemm_splits", 0, 0, 8},            // prefill GEMM K splits (1, 2, 4, 8): 0 chooses
     {"delta_narrow_rows", 16, 0, 1 << 20},  // Gated DeltaNet batches up to this: 16-column workgroups
 };
